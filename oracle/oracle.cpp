@@ -1,0 +1,1713 @@
+// oracle.cpp -- CPU restatement of the FerrisBoost CPU engine.
+//
+// TEST INFRASTRUCTURE ONLY. The test suite, the smoke check and the
+// benchmark's CPU-baseline leg load this library as the checker; the shipped
+// package never links, loads or calls it.
+//
+// Each function names the reference file:line it restates (reference crate
+// `ferrisboost` 0.1.1, Rust). The reference cannot be compiled here (no Rust
+// toolchain), so parity is pinned instead by:
+//   * end to end (quantizer + sketch + histogram + split + partition + leaf
+//     values + logistic / squared-error gradients + base margin + predict):
+//     the reference's XGBoost-3.4.1 golden margins, bit-exact, all 44 cases
+//     of tests/fixtures/{index,weighted_index,monotone_index}.json
+//     (unweighted, weighted and monotone-constrained);
+//   * histogram: brute-force per-row accumulation, order independence, the
+//     sibling identity parent = left + right, the 16-bit / 8-bit equivalence;
+//   * split: brute-force enumeration over every (bin, missing direction)
+//     partition of the rows (src/training/split.rs:806-898 restated in the
+//     Python tests), missing-direction closed forms;
+//   * partition: the stable-order closed form;
+//   * TreeSHAP: additivity (sum of contributions = margin), exact Shapley
+//     values by subset enumeration on small trees, the quadrature rule
+//     integrating polynomials of degree <= 15 exactly;
+//   * colsample: the reference's count and sortedness unit tests;
+//   * sketch: low-cardinality midpoint cuts (the fixtures) and the
+//     reference's sketch unit-test properties. High-cardinality cut values
+//     beyond those are parity unpinned.
+// Lossguide growth and categorical splits have no golden fixture in the
+// reference; they are pinned by brute-force split enumeration and by
+// invariants (leaf hessians sum to the root, max_leaves respected), so their
+// end-to-end tree shape is partially pinned only.
+//
+// Floating point: compiled with -ffp-contract=off and without fast-math so
+// every f32 / f64 operation rounds like the reference's (Rust does not
+// contract a*b+c). expf / logf come from the same glibc the reference links.
+
+#include "oracle.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <memory>
+#include <queue>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+namespace {
+
+using u8 = uint8_t;
+using u16 = uint16_t;
+using u32 = uint32_t;
+using u64 = uint64_t;
+using i64 = int64_t;
+
+constexpr float MIN_GAIN_EPS = 1e-6f;      // src/training/split.rs:15
+constexpr float K_RT_EPS = 1e-6f;          // src/training/objective.rs:18
+constexpr u32 SKETCH_RATIO = 16;           // src/data/sketch.rs:28
+
+// ------------------------------------------------------------ fixed point
+// GradPairFixed (src/types.rs:151-227): wrapping i64 pair.
+struct Fixed {
+    i64 g = 0, h = 0;
+};
+inline Fixed add(Fixed a, Fixed b) {
+    return {(i64)((u64)a.g + (u64)b.g), (i64)((u64)a.h + (u64)b.h)};
+}
+inline Fixed sub(Fixed a, Fixed b) {
+    return {(i64)((u64)a.g - (u64)b.g), (i64)((u64)a.h - (u64)b.h)};
+}
+inline bool eq(Fixed a, Fixed b) { return a.g == b.g && a.h == b.h; }
+
+// pow2_scale (src/types.rs:367-385).
+double pow2_scale(double max_abs, u64 n_rows) {
+    if (!(max_abs > 0.0) || !std::isfinite(max_abs)) return 1.0;
+    double budget = (double)(1ull << 62) / (double)std::max<u64>(n_rows, 1);
+    double raw = budget / max_abs;
+    if (!std::isfinite(raw) || raw <= 0.0) return 1.0;
+    double l = std::floor(std::log2(raw));
+    int e;
+    if (std::isnan(l)) e = 0;
+    else if (l > 2147483647.0) e = 2147483647;
+    else if (l < -2147483648.0) e = (int)-2147483648LL;
+    else e = (int)l;
+    e = std::max(-1000, std::min(1000, e));
+    return std::exp2((double)e);
+}
+
+// `as i64` in Rust saturates (NaN -> 0).
+inline i64 sat_i64(double x) {
+    if (std::isnan(x)) return 0;
+    if (x >= 9223372036854775808.0) return std::numeric_limits<i64>::max();
+    if (x < -9223372036854775808.0) return std::numeric_limits<i64>::min();
+    return (i64)x;
+}
+
+// GradQuantizer (src/types.rs:239-341).
+struct Quantizer {
+    double gs = 1, hs = 1, gi = 1, hi = 1;
+    static Quantizer from_bounds(double mg, double mh, u64 n) {
+        if (!(std::isfinite(mg) && std::isfinite(mh) && mg >= 0.0 && mh >= 0.0))
+            throw std::runtime_error(
+                "non-finite gradient or Hessian (or invalid bounds); reduce extreme labels, "
+                "weights, base_score or objective parameters");
+        Quantizer q;
+        q.gs = pow2_scale(mg, n);
+        q.hs = pow2_scale(mh, n);
+        q.gi = 1.0 / q.gs;
+        q.hi = 1.0 / q.hs;
+        return q;
+    }
+    Fixed to_fixed(float g, float h) const {
+        // quantize (src/types.rs:352-355): round half away from zero.
+        return {sat_i64(std::round((double)g * gs)), sat_i64(std::round((double)h * hs))};
+    }
+    void to_f64(Fixed f, double &g, double &h) const {
+        g = (double)f.g * gi;
+        h = (double)f.h * hi;
+    }
+};
+
+inline double finite_abs(float v) {  // src/types.rs:343-350
+    return std::isfinite(v) ? std::fabs((double)v) : INFINITY;
+}
+
+// ------------------------------------------------------------ sketch
+// src/data/sketch.rs:28-435.
+struct Entry {
+    float value, weight, rmin, rmax;
+    float rmid() const { return 0.5f * (rmin + rmax); }
+};
+
+std::vector<Entry> build_summary(std::vector<std::pair<float, float>> &pairs) {
+    std::sort(pairs.begin(), pairs.end(),
+              [](const std::pair<float, float> &a, const std::pair<float, float> &b) {
+                  return a.first < b.first;
+              });
+    std::vector<Entry> out;
+    out.reserve(pairs.size());
+    float acc = 0.0f;
+    size_t i = 0;
+    while (i < pairs.size()) {
+        float v = pairs[i].first;
+        float w = 0.0f;
+        while (i < pairs.size() && pairs[i].first == v) {
+            w += pairs[i].second;
+            i++;
+        }
+        out.push_back({v, w, acc, acc + w});
+        acc += w;
+    }
+    return out;
+}
+
+std::vector<Entry> dedup_same_value(const std::vector<Entry> &entries) {
+    std::vector<Entry> out;
+    out.reserve(entries.size());
+    for (const Entry &e : entries) {
+        if (!out.empty() && out.back().value == e.value) {
+            Entry &last = out.back();
+            last.weight += e.weight;
+            last.rmin = std::min(last.rmin, e.rmin);
+            last.rmax = std::max(last.rmax, e.rmax);
+        } else {
+            out.push_back(e);
+        }
+    }
+    return out;
+}
+
+std::vector<Entry> merge_entries(const std::vector<Entry> &a, const std::vector<Entry> &b) {
+    if (a.empty()) return b;
+    if (b.empty()) return a;
+    std::vector<Entry> out;
+    out.reserve(a.size() + b.size());
+    size_t i = 0, j = 0;
+    float pass_a = 0.0f, pass_b = 0.0f;
+    while (i < a.size() || j < b.size()) {
+        bool take_a;
+        if (i < a.size() && j < b.size()) take_a = a[i].value <= b[j].value;
+        else take_a = i < a.size();
+        if (take_a) {
+            Entry e = a[i];
+            out.push_back({e.value, e.weight, e.rmin + pass_b, e.rmax + pass_b});
+            pass_a = e.rmax;
+            i++;
+        } else {
+            Entry e = b[j];
+            out.push_back({e.value, e.weight, e.rmin + pass_a, e.rmax + pass_a});
+            pass_b = e.rmax;
+            j++;
+        }
+    }
+    return dedup_same_value(out);
+}
+
+std::vector<Entry> compress(const std::vector<Entry> &entries, size_t max_size) {
+    size_t n = entries.size();
+    if (n <= max_size) return entries;
+    float total = entries[n - 1].rmax;
+    size_t slots = max_size - 1;
+    std::vector<Entry> out;
+    out.reserve(max_size);
+    out.push_back(entries[0]);
+    size_t taken = 0;
+    for (size_t k = 1; k < slots; k++) {
+        float target = total * (float)k / (float)slots;
+        size_t j = taken + 1;
+        while (j < n - 1 && entries[j].rmid() < target) j++;
+        size_t ceiling = n - 1 - (slots - 1 - k);
+        j = std::min(std::max(j, taken + 1), ceiling);
+        if (j > taken) {
+            out.push_back(entries[j]);
+            taken = j;
+        }
+    }
+    if (taken < n - 1) out.push_back(entries[n - 1]);
+    return out;
+}
+
+float midpoint(float a, float b) {  // src/data/sketch.rs:290-302
+    float d = b - a;
+    float m = std::isfinite(d) ? a + d * 0.5f : a * 0.5f + b * 0.5f;
+    return m <= a ? b : m;
+}
+
+struct FeatureSketch {
+    std::vector<std::pair<float, float>> buffer;
+    std::vector<std::vector<Entry>> levels;
+    std::vector<bool> occupied;
+    size_t limit;
+    float total_weight = 0.0f;
+    bool cat = false;
+    int max_code = -1;
+    bool bad = false;
+    float bad_value = 0.0f;
+
+    explicit FeatureSketch(size_t max_bins, bool categorical) {
+        cat = categorical;
+        limit = categorical ? 0 : std::max<size_t>(max_bins * SKETCH_RATIO, 32);
+        if (!cat) buffer.reserve(limit);
+    }
+
+    void push(float value, float weight) {  // src/data/sketch.rs:128-149
+        if (cat) {
+            if (!std::isnan(value)) {
+                bool invalid = value < 0.0f || value > 65533.0f || value != std::trunc(value);
+                if (invalid) {
+                    if (!bad) {
+                        bad = true;
+                        bad_value = value;
+                    }
+                } else {
+                    max_code = std::max(max_code, (int)value);
+                }
+            }
+            return;
+        }
+        if (std::isnan(value) || weight <= 0.0f) return;
+        total_weight += weight;
+        buffer.push_back({value, weight});
+        if (buffer.size() >= limit) drain_buffer();
+    }
+
+    void drain_buffer() {
+        if (buffer.empty()) return;
+        std::vector<Entry> summary = compress(build_summary(buffer), limit);
+        buffer.clear();
+        insert_level(std::move(summary));
+    }
+
+    void insert_level(std::vector<Entry> cur) {
+        size_t lvl = 0;
+        for (;;) {
+            if (lvl == levels.size()) {
+                levels.push_back(std::move(cur));
+                occupied.push_back(true);
+                return;
+            }
+            if (!occupied[lvl]) {
+                levels[lvl] = std::move(cur);
+                occupied[lvl] = true;
+                return;
+            }
+            std::vector<Entry> existing = std::move(levels[lvl]);
+            occupied[lvl] = false;
+            levels[lvl].clear();
+            cur = compress(merge_entries(existing, cur), limit);
+            lvl++;
+        }
+    }
+
+    std::vector<Entry> collapse() {
+        drain_buffer();
+        std::vector<Entry> acc;
+        for (size_t i = 0; i < levels.size(); i++) {
+            if (!occupied[i]) continue;
+            acc = acc.empty() ? levels[i] : merge_entries(acc, levels[i]);
+        }
+        levels.clear();
+        occupied.clear();
+        if (!acc.empty()) {
+            levels.push_back(compress(acc, limit));
+            occupied.push_back(true);
+            return levels[0];
+        }
+        return {};
+    }
+
+    std::vector<float> cuts(size_t max_bins) {  // src/data/sketch.rs:236-275
+        std::vector<float> out;
+        if (cat) {
+            u32 mc = (u32)std::max(max_code, 0);
+            for (u32 c = 1; c <= mc; c++) out.push_back((float)c);
+            return out;
+        }
+        size_t n_cuts = max_bins > 0 ? max_bins - 1 : 0;
+        if (n_cuts == 0) return out;
+        std::vector<Entry> entries = collapse();
+        if (entries.empty()) return out;
+        if (entries.size() <= n_cuts) {
+            for (size_t i = 0; i + 1 < entries.size(); i++)
+                out.push_back(midpoint(entries[i].value, entries[i + 1].value));
+            return out;
+        }
+        float total = entries.back().rmax;
+        for (size_t k = 1; k <= n_cuts; k++) {
+            float target = total * (float)k / (float)max_bins;
+            size_t idx = 0;
+            {
+                size_t lo = 0, hi = entries.size();
+                while (lo < hi) {
+                    size_t mid = (lo + hi) / 2;
+                    if (entries[mid].rmid() < target) lo = mid + 1;
+                    else hi = mid;
+                }
+                idx = std::min(lo, entries.size() - 1);
+            }
+            float v = entries[idx].value;
+            if (out.empty() || v > out.back()) out.push_back(v);
+        }
+        return out;
+    }
+};
+
+// ------------------------------------------------------------ cuts / bins
+// BinWidth (src/data/bins.rs:17-76), BinCuts (src/data/columns.rs:50-360).
+struct Cuts {
+    std::vector<float> values;
+    std::vector<u32> offsets;
+    std::vector<u8> cat;
+    u32 n_feats() const { return (u32)offsets.size() - 1; }
+    u32 n_bins(u32 f) const { return offsets[f + 1] - offsets[f] + 1; }
+    bool is_cat(u32 f) const { return f < cat.size() && cat[f]; }
+    int width(u32 f) const {
+        u32 n = n_bins(f);
+        if (is_cat(f)) return n <= 254 ? 1 : 2;
+        return n <= 255 ? 1 : 2;
+    }
+    const float *cuts_for(u32 f) const { return values.data() + offsets[f]; }
+    u32 n_cuts(u32 f) const { return offsets[f + 1] - offsets[f]; }
+    u32 find_bin(u32 f, float v) const {  // columns.rs:335-341, categorical.rs code_to_bin
+        if (is_cat(f)) {
+            u32 nb = n_bins(f);
+            if (v >= 0.0f && v < (float)nb) return (u32)v;
+            return (nb <= 254 ? 255u : 65535u) - 1;
+        }
+        const float *c = cuts_for(f);
+        return (u32)(std::upper_bound(c, c + n_cuts(f), v, [](float a, float b) { return a < b; }) -
+                     c);
+    }
+};
+
+u32 missing_of(int width) { return width == 1 ? 0xFFu : 0xFFFFu; }
+
+struct Block {
+    std::vector<u32> feats;
+    int width;
+    u64 n_rows;
+    std::vector<u8> d8;
+    std::vector<u16> d16;
+    u32 bin(u32 local, u64 row) const {
+        return width == 1 ? d8[local * n_rows + row] : d16[local * n_rows + row];
+    }
+};
+
+// partition_features_by_width (src/data/columns.rs:446-463).
+std::vector<std::vector<u32>> partition_by_width(const std::vector<int> &widths, u32 cols) {
+    std::vector<std::vector<u32>> blocks;
+    for (int w : {1, 2}) {
+        std::vector<u32> feats;
+        for (u32 f = 0; f < widths.size(); f++)
+            if (widths[f] == w) feats.push_back(f);
+        u32 per = (cols + (u32)w - 1) / (u32)w;
+        for (size_t i = 0; i < feats.size(); i += per)
+            blocks.emplace_back(feats.begin() + i,
+                                feats.begin() + std::min(feats.size(), i + per));
+    }
+    std::sort(blocks.begin(), blocks.end(),
+              [](const std::vector<u32> &a, const std::vector<u32> &b) { return a[0] < b[0]; });
+    return blocks;
+}
+
+Cuts sketch_cuts(const float *x, u64 n, u32 nf, u32 max_bin, const float *w, const u8 *cat) {
+    Cuts c;
+    c.offsets.push_back(0);
+    for (u32 f = 0; f < nf; f++) {
+        bool is_cat = cat && cat[f];
+        FeatureSketch sk(max_bin, is_cat);
+        for (u64 r = 0; r < n; r++) sk.push(x[r * nf + f], w ? w[r] : 1.0f);
+        if (sk.bad) throw std::runtime_error("categorical feature contains an invalid code");
+        std::vector<float> cf = sk.cuts(max_bin);
+        c.values.insert(c.values.end(), cf.begin(), cf.end());
+        c.offsets.push_back((u32)c.values.size());
+        c.cat.push_back(is_cat ? 1 : 0);
+    }
+    return c;
+}
+
+std::vector<Block> bin_blocks(const float *x, u64 n, u32 nf, const Cuts &c, u32 cols) {
+    std::vector<int> widths(nf);
+    for (u32 f = 0; f < nf; f++) widths[f] = c.width(f);
+    std::vector<Block> blocks;
+    for (auto &feats : partition_by_width(widths, cols)) {
+        Block b;
+        b.feats = feats;
+        b.width = widths[feats[0]];
+        b.n_rows = n;
+        if (b.width == 1) b.d8.assign(feats.size() * n, 0);
+        else b.d16.assign(feats.size() * n, 0);
+        for (size_t l = 0; l < feats.size(); l++) {
+            u32 f = feats[l];
+            for (u64 r = 0; r < n; r++) {
+                float v = x[r * nf + f];
+                u32 bin = std::isnan(v) ? missing_of(b.width) : c.find_bin(f, v);
+                if (b.width == 1) b.d8[l * n + r] = (u8)bin;
+                else b.d16[l * n + r] = (u16)bin;
+            }
+        }
+        blocks.push_back(std::move(b));
+    }
+    return blocks;
+}
+
+// ------------------------------------------------------------ params
+struct Params {
+    orc_params p;
+    std::vector<int8_t> monotone;
+    int8_t monotone_of(u32 f) const { return f < monotone.size() ? monotone[f] : 0; }
+};
+
+// ------------------------------------------------------------ split math
+// src/training/split.rs:113-270.
+struct Bounds {
+    float lo = -std::numeric_limits<float>::max();
+    float hi = std::numeric_limits<float>::max();
+    float apply(float w) const {
+        if (w < lo) return lo;
+        if (w > hi) return hi;
+        return w;
+    }
+    void children(int8_t c, float wl, float wr, Bounds &l, Bounds &r) const {
+        float mid = (wl + wr) / 2.0f;
+        l = *this;
+        r = *this;
+        if (c < 0) {
+            l.lo = mid;
+            r.hi = mid;
+        } else if (c > 0) {
+            l.hi = mid;
+            r.lo = mid;
+        }
+    }
+};
+
+double threshold_l1(double g, float alpha) {
+    double a = (double)alpha;
+    if (g > a) return g - a;
+    if (g < -a) return g + a;
+    return 0.0;
+}
+
+float xgb_weight(double g, double h, const orc_params &p) {
+    if (h <= 0.0) return 0.0f;
+    double dw = -threshold_l1(g, p.alpha) / (h + (double)p.lambda_);
+    float mds = p.max_delta_step;
+    if (mds != 0.0f && std::fabs(dw) > (double)mds) dw = std::copysign((double)mds, dw);
+    return (float)dw;
+}
+
+float gain_given_weight(double g, double h, float w, const orc_params &p) {
+    if (h <= 0.0) return 0.0f;
+    double square = (double)(w * w);
+    double l1 = 2.0 * (double)p.alpha * (double)std::fabs(w);
+    return (float)(-((2.0 * g * (double)w + (h + (double)p.lambda_) * square) + l1));
+}
+
+float bounded_node_gain(double g, double h, const orc_params &p, Bounds b) {
+    float w = b.apply(xgb_weight(g, h, p));
+    return gain_given_weight(g, h, w, p);
+}
+
+bool bounded_split_gain(float parent, double lg, double lh, double rg, double rh, int8_t c,
+                        Bounds b, const orc_params &p, float &out) {
+    double mcw = (double)p.min_child_weight;
+    if (!(lh > 0.0 && rh > 0.0 && lh >= mcw && rh >= mcw)) return false;
+    float wl = b.apply(xgb_weight(lg, lh, p));
+    float wr = b.apply(xgb_weight(rg, rh, p));
+    if ((c > 0 && wl > wr) || (c < 0 && wl < wr)) return false;
+    float gain = gain_given_weight(lg, lh, wl, p) + gain_given_weight(rg, rh, wr, p);
+    float loss = gain - parent;
+    out = (float)((double)loss - (double)p.gamma);
+    return true;
+}
+
+double plain_gain(double g, double h, const orc_params &p) { return g * g / (h + (double)p.lambda_); }
+
+struct Cand {
+    bool found = false;
+    u32 feat = 0, bin = 0;
+    float gain = 0;
+    Fixed left, right;
+    bool missing_left = false;
+    std::vector<u64> cats;  // right-going set; empty = numeric
+    bool is_cat = false;
+};
+
+// update_best (src/training/split.rs:260-270).
+void update_best(Cand &best, const Cand &c) {
+    if (!(c.gain > MIN_GAIN_EPS)) return;
+    if (!best.found || c.gain > best.gain) best = c;
+}
+
+// reduce_best (src/training/split.rs:631-642).
+void reduce_into(Cand &best, const Cand &c) {
+    if (!c.found) return;
+    if (best.found && c.gain == best.gain && c.feat < best.feat && c.gain > MIN_GAIN_EPS) {
+        best = c;
+        return;
+    }
+    update_best(best, c);
+}
+
+struct SplitCtx {
+    const Quantizer *q;
+    const orc_params *p;
+    bool given_weight;
+    Bounds bounds;
+    const Params *params;  // monotone lookup (may be null)
+    const std::vector<int8_t> *mono;
+    float bounded_parent;
+    double parent_gain;
+    int8_t mono_of(u32 f) const { return (mono && f < mono->size()) ? (*mono)[f] : 0; }
+    bool gain(u32 feat, Fixed l, Fixed r, float &out) const {
+        double lg, lh, rg, rh;
+        q->to_f64(l, lg, lh);
+        q->to_f64(r, rg, rh);
+        if (given_weight)
+            return bounded_split_gain(bounded_parent, lg, lh, rg, rh, mono_of(feat), bounds, *p,
+                                      out);
+        double mcw = (double)p->min_child_weight;
+        if (lh < mcw || rh < mcw) return false;
+        double g = plain_gain(lg, lh, *p) + plain_gain(rg, rh, *p) - parent_gain - (double)p->gamma;
+        out = (float)g;
+        return true;
+    }
+};
+
+// enumerate_categorical (src/training/split.rs:484-617).
+void enumerate_categorical(u32 feat, const Fixed *bins, u32 n, Fixed node_sum, const SplitCtx &sc,
+                           Cand &best) {
+    struct Local {
+        bool found = false;
+        float gain = 0.0f;
+        Fixed l, r;
+        bool ml = false;
+        size_t at = 0;
+    };
+    Local local;
+    auto consider = [&](Local &loc, Fixed l, Fixed r, bool ml, size_t at) {
+        float g;
+        if (sc.gain(feat, l, r, g)) {
+            if (g > MIN_GAIN_EPS && (!loc.found || g > loc.gain)) {
+                loc.found = true;
+                loc.gain = g;
+                loc.l = l;
+                loc.r = r;
+                loc.ml = ml;
+                loc.at = at;
+            }
+        }
+    };
+    size_t nwords = n <= 256 ? 4 : (n + 63) / 64;
+    auto finish = [&](const Local &loc, const std::vector<u32> &set_members) {
+        if (!loc.found) return;
+        Cand c;
+        c.found = true;
+        c.feat = feat;
+        c.bin = 0;
+        c.gain = loc.gain;
+        c.left = loc.l;
+        c.right = loc.r;
+        c.missing_left = loc.ml;
+        c.is_cat = true;
+        c.cats.assign(nwords, 0);
+        for (u32 cat : set_members) c.cats[cat >> 6] |= 1ull << (cat & 63);
+        update_best(best, c);
+    };
+    if ((u64)n < (u64)sc.p->max_cat_to_onehot) {
+        Fixed fs;
+        for (u32 i = 0; i < n; i++) fs = add(fs, bins[i]);
+        Fixed missing = sub(node_sum, fs);
+        for (u32 i = 0; i < n; i++) {
+            consider(local, sub(node_sum, bins[i]), bins[i], true, i);
+            Fixed right = add(bins[i], missing);
+            consider(local, sub(node_sum, right), right, false, i);
+        }
+        if (local.found) finish(local, {(u32)local.at});
+        return;
+    }
+    std::vector<float> weights(n);
+    for (u32 i = 0; i < n; i++) {
+        double g, h;
+        sc.q->to_f64(bins[i], g, h);
+        weights[i] = xgb_weight(g, h, *sc.p);
+    }
+    std::vector<u32> order(n);
+    for (u32 i = 0; i < n; i++) order[i] = i;
+    std::stable_sort(order.begin(), order.end(),
+                     [&](u32 a, u32 b) { return weights[a] < weights[b]; });
+    size_t n_scan = std::min<size_t>(sc.p->max_cat_threshold, n);
+    if (n_scan < 2) return;
+    auto prefix = [&](size_t k) { return std::vector<u32>(order.begin(), order.begin() + k); };
+    Fixed right;
+    for (size_t k = 0; k + 1 < n_scan; k++) {
+        right = add(right, bins[order[k]]);
+        consider(local, sub(node_sum, right), right, true, k + 1);
+    }
+    if (local.found) finish(local, prefix(local.at));
+    local = Local();
+    Fixed left;
+    for (size_t j = n; j-- > n - (n_scan - 1);) {
+        left = add(left, bins[order[j]]);
+        consider(local, left, sub(node_sum, left), false, j);
+    }
+    if (local.found) finish(local, prefix(local.at));
+}
+
+// best_split_in_block_typed (src/training/split.rs:331-461).
+Cand best_split_in_block(const Fixed *hist, const std::vector<u32> &feat_ids,
+                         const std::vector<u32> &offsets, Fixed node_sum, const SplitCtx &sc0,
+                         const std::vector<u32> *sampled, const std::vector<u8> *categorical) {
+    SplitCtx sc = sc0;
+    double ng, nh;
+    sc.q->to_f64(node_sum, ng, nh);
+    sc.parent_gain = plain_gain(ng, nh, *sc.p);
+    sc.bounded_parent = sc.given_weight ? bounded_node_gain(ng, nh, *sc.p, sc.bounds) : 0.0f;
+    Cand best;
+    for (size_t local = 0; local < feat_ids.size(); local++) {
+        u32 feat = feat_ids[local];
+        if (sampled && !std::binary_search(sampled->begin(), sampled->end(), feat)) continue;
+        u32 lo = offsets[local], hi = offsets[local + 1];
+        const Fixed *bins = hist + lo;
+        u32 n = hi - lo;
+        if (categorical && feat < categorical->size() && (*categorical)[feat]) {
+            enumerate_categorical(feat, bins, n, node_sum, sc, best);
+            continue;
+        }
+        Fixed left;
+        for (u32 i = 0; i < n; i++) {
+            left = add(left, bins[i]);
+            Fixed right = sub(node_sum, left);
+            float g;
+            if (!sc.gain(feat, left, right, g)) continue;
+            Cand c;
+            c.found = true;
+            c.feat = feat;
+            c.bin = i + 1;
+            c.gain = g;
+            c.left = left;
+            c.right = right;
+            c.missing_left = false;
+            update_best(best, c);
+        }
+        if (eq(left, node_sum)) continue;
+        Fixed right;
+        for (u32 i = n; i-- > 0;) {
+            right = add(right, bins[i]);
+            Fixed l2 = sub(node_sum, right);
+            float g;
+            if (!sc.gain(feat, l2, right, g)) continue;
+            Cand c;
+            c.found = true;
+            c.feat = feat;
+            c.bin = i;
+            c.gain = g;
+            c.left = l2;
+            c.right = right;
+            c.missing_left = true;
+            update_best(best, c);
+        }
+    }
+    return best;
+}
+
+// ------------------------------------------------------------ histogram
+// hist::build_rows (src/training/hist.rs:148-176), column-sliced form.
+void hist_rows(const Block &b, const std::vector<u32> &locals, const std::vector<u32> &offsets,
+               const std::vector<Fixed> &gpair, const u32 *rows, size_t n_sel, Fixed *out) {
+    const u32 missing = missing_of(b.width);
+    const size_t tile = 4096;
+    for (size_t c0 = 0; c0 < n_sel; c0 += tile) {
+        size_t c1 = std::min(n_sel, c0 + tile);
+        for (size_t f = 0; f < locals.size(); f++) {
+            Fixed *h = out + offsets[f];
+            u32 l = locals[f];
+            if (b.width == 1) {
+                const u8 *col = b.d8.data() + (size_t)l * b.n_rows;
+                for (size_t i = c0; i < c1; i++) {
+                    u32 r = rows[i];
+                    u32 bin = col[r];
+                    if (bin == missing) continue;
+                    h[bin] = add(h[bin], gpair[r]);
+                }
+            } else {
+                const u16 *col = b.d16.data() + (size_t)l * b.n_rows;
+                for (size_t i = c0; i < c1; i++) {
+                    u32 r = rows[i];
+                    u32 bin = col[r];
+                    if (bin == missing) continue;
+                    h[bin] = add(h[bin], gpair[r]);
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------ colsample
+// src/data/colsample.rs:3-73.
+struct SplitMix64 {
+    u64 s;
+    u64 next() {
+        s += 0x9E3779B97F4A7C15ull;
+        u64 z = s;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    }
+    u64 below(u64 n) {
+        u64 zone = UINT64_MAX - (UINT64_MAX % n) - 1;
+        for (;;) {
+            u64 v = next();
+            if (v <= zone) return v % n;
+        }
+    }
+};
+
+inline u64 rotl(u64 x, int r) { return (x << r) | (x >> (64 - r)); }
+
+size_t sampled_count(size_t nf, float rate) {
+    if (nf == 0) return 0;
+    double n = std::floor((double)rate * (double)nf);
+    size_t k = (std::isfinite(n) && n >= 1.0) ? (size_t)n : 1;
+    return std::max<size_t>(std::min(k, nf), 1);
+}
+
+std::vector<u32> sample_features(u32 nf, float rate, u64 seed, u64 round) {
+    size_t take = sampled_count(nf, rate);
+    std::vector<u32> ids(nf);
+    for (u32 i = 0; i < nf; i++) ids[i] = i;
+    if (take >= nf) return ids;
+    SplitMix64 rng{seed ^ rotl(round * 0x9E3779B97F4A7C15ull, 17)};
+    for (size_t i = ids.size() - 1; i >= 1; i--) {
+        size_t j = (size_t)rng.below(i + 1);
+        std::swap(ids[i], ids[j]);
+    }
+    ids.resize(take);
+    std::sort(ids.begin(), ids.end());
+    return ids;
+}
+
+// subsample (src/data/subsample.rs).
+inline u64 mix64(u64 z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+u64 threshold_for(float rate) {
+    if (rate >= 1.0f) return UINT64_MAX;
+    if (!(rate > 0.0f)) return UINT64_MAX;
+    return (u64)((double)rate * (double)(1ull << 53));
+}
+bool row_selected(u64 row, u64 th, u64 seed, u64 tree) {
+    if (th == UINT64_MAX) return true;
+    u64 h = mix64(seed ^ rotl(tree * 0x9E3779B97F4A7C15ull, 23) ^ (row * 0xD6E8FEB86659FD93ull));
+    return (h >> 11) < th;
+}
+
+// ------------------------------------------------------------ objective
+float sigmoidf(float m) { return 1.0f / (1.0f + std::exp(-m)); }
+
+void gradient(u32 obj, float pred, float label, float &g, float &h) {
+    if (obj == 1) {  // binary:logistic (objective.rs:511-517)
+        float s = sigmoidf(pred);
+        g = s - label;
+        h = std::fmax(s * (1.0f - s), 1e-16f);
+    } else {  // reg:squarederror
+        g = pred - label;
+        h = 1.0f;
+    }
+}
+
+float base_margin_of(u32 obj, float bs) {  // objective.rs:363-398
+    if (obj == 1) {
+        float x = std::min(std::max(bs, K_RT_EPS), 1.0f - K_RT_EPS);
+        return -std::log(1.0f / x - 1.0f);
+    }
+    return bs;
+}
+
+float estimate_base_score(const float *y, const float *w, u64 n) {  // objective.rs:42-60
+    if (!w) {
+        double nn = (double)n, acc = 0.0;
+        for (u64 i = 0; i < n; i++) acc = acc + (double)y[i] / nn;
+        return (float)acc;
+    }
+    double sw = 0.0;
+    for (u64 i = 0; i < n; i++) sw = sw + (double)w[i];
+    if (sw <= 0.0) return 0.5f;
+    double acc = 0.0;
+    for (u64 i = 0; i < n; i++) acc = acc + (double)y[i] / sw * (double)w[i];
+    return (float)acc;
+}
+
+// ------------------------------------------------------------ tree
+struct Node {
+    u32 feat = 0;
+    float split_cond = 0;
+    int32_t left = -1, right = -1;
+    bool default_left = false;
+    float leaf_value = 0;
+    bool is_leaf = true;
+    float gain = 0;
+    float sum_hess = 0;
+    std::vector<u32> cats;  // u32 words, trailing zeros trimmed
+    bool is_cat = false;
+};
+
+struct Tree {
+    std::vector<Node> nodes;
+    size_t push_leaf(float v, float h) {
+        Node n;
+        n.leaf_value = v;
+        n.sum_hess = h;
+        nodes.push_back(n);
+        return nodes.size() - 1;
+    }
+    std::pair<size_t, size_t> split_leaf(size_t node, u32 feat, float cond, bool dl, float gain,
+                                         float lv, float lh, float rv, float rh) {
+        size_t l = push_leaf(lv, lh), r = push_leaf(rv, rh);
+        Node &n = nodes[node];
+        n.feat = feat;
+        n.split_cond = cond;
+        n.left = (int32_t)l;
+        n.right = (int32_t)r;
+        n.default_left = dl;
+        n.leaf_value = 0.0f;
+        n.is_leaf = false;
+        n.gain = gain;
+        return {l, r};
+    }
+    void set_categories(size_t node, const std::vector<u64> &bits) {
+        std::vector<u32> words;
+        for (size_t i = 0; i < 2 * bits.size(); i++) words.push_back((u32)(bits[i / 2] >> (32 * (i % 2))));
+        while (!words.empty() && words.back() == 0) words.pop_back();
+        nodes[node].cats = words;
+        nodes[node].is_cat = true;
+        float one;
+        u32 bitsone = 1;
+        std::memcpy(&one, &bitsone, 4);
+        nodes[node].split_cond = one;
+    }
+    // Node::goes_left (tree.rs:90-101) + categorical::goes_left
+    // (src/data/categorical.rs goes_left).
+    static bool goes_left(const Node &n, float v) {
+        if (std::isnan(v)) return n.default_left;
+        if (n.is_cat) {
+            if (v < 0.0f || v >= 16777216.0f) return true;
+            u32 cat = (u32)v;
+            u32 word = cat / 32;
+            if (word >= n.cats.size()) return true;
+            return ((n.cats[word] >> (cat % 32)) & 1) == 0;
+        }
+        return v < n.split_cond;
+    }
+    float leaf_value(const float *x) const {
+        if (nodes.empty()) return 0.0f;
+        size_t i = 0;
+        for (;;) {
+            const Node &n = nodes[i];
+            if (n.is_leaf) return n.leaf_value;
+            i = goes_left(n, x[n.feat]) ? (size_t)n.left : (size_t)n.right;
+        }
+    }
+};
+
+float split_threshold(const Cuts &c, u32 f, u32 bin) {  // tree.rs:991-1001
+    if (bin == 0) return -std::numeric_limits<float>::max();
+    if (bin > c.n_cuts(f)) return std::numeric_limits<float>::max();
+    return c.cuts_for(f)[bin - 1];
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ model
+struct orc_model {
+    std::vector<Tree> trees;
+    float base_score = 0.5f;
+    u32 objective = 1;
+    std::vector<float> train_margins;
+    double train_seconds = 0.0;
+};
+
+namespace {
+
+// ------------------------------------------------------------ training
+struct Plan {
+    u32 block;                 // physical block
+    std::vector<u32> feats;    // sampled global features of the block (ascending)
+    std::vector<u32> locals;   // their local column index in the block
+    std::vector<u32> offsets;  // compact histogram offsets
+};
+
+struct Trainer {
+    const Cuts &cuts;
+    const std::vector<Block> &blocks;
+    const Params &P;
+    const orc_params &p;
+    const Quantizer &q;
+    const std::vector<Fixed> &gpair;
+    std::vector<float> &pred;
+    std::vector<Plan> plans;
+    std::vector<u32> rows_cur, rows_next;
+    const std::vector<u32> *sampled;
+    unsigned nthread;
+
+    Trainer(const Cuts &c, const std::vector<Block> &b, const Params &P_, const Quantizer &q_,
+            const std::vector<Fixed> &g, std::vector<float> &pr, const std::vector<u32> *smp)
+        : cuts(c), blocks(b), P(P_), p(P_.p), q(q_), gpair(g), pred(pr), sampled(smp) {
+        nthread = std::max(1u, p.nthread);
+        for (u32 bi = 0; bi < blocks.size(); bi++) {
+            Plan pl;
+            pl.block = bi;
+            for (u32 l = 0; l < blocks[bi].feats.size(); l++) {
+                u32 f = blocks[bi].feats[l];
+                if (sampled && !std::binary_search(sampled->begin(), sampled->end(), f)) continue;
+                pl.feats.push_back(f);
+                pl.locals.push_back(l);
+            }
+            if (pl.feats.empty()) continue;
+            pl.offsets.push_back(0);
+            for (u32 f : pl.feats) pl.offsets.push_back(pl.offsets.back() + cuts.n_bins(f));
+            plans.push_back(std::move(pl));
+        }
+    }
+
+    SplitCtx ctx(Bounds b) const {
+        SplitCtx sc;
+        sc.q = &q;
+        sc.p = &p;
+        sc.given_weight = true;  // uses_given_weight() is always true (types.rs:637-639)
+        sc.bounds = b;
+        sc.params = &P;
+        sc.mono = &P.monotone;
+        return sc;
+    }
+
+    // Histogram of one node for every plan; hists[plan] sized offsets.back().
+    void build_hists(const u32 *rows, size_t n, std::vector<std::vector<Fixed>> &out) {
+        out.resize(plans.size());
+        auto work = [&](size_t pi) {
+            out[pi].assign(plans[pi].offsets.back(), Fixed());
+            hist_rows(blocks[plans[pi].block], plans[pi].locals, plans[pi].offsets, gpair, rows, n,
+                      out[pi].data());
+        };
+        if (nthread <= 1 || plans.size() <= 1) {
+            for (size_t pi = 0; pi < plans.size(); pi++) work(pi);
+        } else {
+            std::vector<std::thread> th;
+            for (unsigned t = 0; t < nthread; t++)
+                th.emplace_back([&, t] {
+                    for (size_t pi = t; pi < plans.size(); pi += nthread) work(pi);
+                });
+            for (auto &x : th) x.join();
+        }
+    }
+
+    Cand best_of(const std::vector<std::vector<Fixed>> &h, Fixed sum, Bounds b) {
+        SplitCtx sc = ctx(b);
+        Cand best;
+        for (size_t pi = 0; pi < plans.size(); pi++) {
+            Cand c = best_split_in_block(h[pi].data(), plans[pi].feats, plans[pi].offsets, sum, sc,
+                                         sampled, &cuts.cat);
+            reduce_into(best, c);
+        }
+        return best;
+    }
+
+    // Stable partition of rows[start, start+len) into out (same span).
+    size_t partition(const u32 *rows, size_t len, const Cand &c, u32 *out) {
+        int width = cuts.width(c.feat);
+        const Block *blk = nullptr;
+        u32 local = 0;
+        for (const Block &b : blocks)
+            for (u32 l = 0; l < b.feats.size(); l++)
+                if (b.feats[l] == c.feat) {
+                    blk = &b;
+                    local = l;
+                }
+        u32 missing = missing_of(width);
+        size_t nl = 0;
+        std::vector<u32> right;
+        right.reserve(len);
+        for (size_t i = 0; i < len; i++) {
+            u32 r = rows[i];
+            u32 bin = blk->bin(local, r);
+            bool gl;
+            if (bin == missing) gl = c.missing_left;
+            else if (c.is_cat) {
+                u32 w = bin >> 6;
+                bool in = w < c.cats.size() && ((c.cats[w] >> (bin & 63)) & 1);
+                gl = !in;
+            } else gl = bin < c.bin;
+            if (gl) out[nl++] = r;
+            else right.push_back(r);
+        }
+        std::copy(right.begin(), right.end(), out + nl);
+        return nl;
+    }
+
+    void child_leaves(const Cand &c, Bounds parent, float &lv, float &rv, Bounds &lb, Bounds &rb) {
+        double g, h;
+        q.to_f64(c.left, g, h);
+        float wl = parent.apply(xgb_weight(g, h, p));
+        q.to_f64(c.right, g, h);
+        float wr = parent.apply(xgb_weight(g, h, p));
+        parent.children(P.monotone_of(c.feat), wl, wr, lb, rb);
+        lv = wl * p.learning_rate;
+        rv = wr * p.learning_rate;
+    }
+
+    float hess_of(Fixed s) const {
+        double g, h;
+        q.to_f64(s, g, h);
+        return (float)h;
+    }
+
+    void apply_split(Tree &t, size_t node, const Cand &c, Bounds parent, size_t &l, size_t &r,
+                     Bounds &lb, Bounds &rb) {
+        float lv, rv;
+        child_leaves(c, parent, lv, rv, lb, rb);
+        float thr = c.is_cat ? 0.0f : split_threshold(cuts, c.feat, c.bin);
+        auto lr = t.split_leaf(node, c.feat, thr, c.missing_left, c.gain, lv, hess_of(c.left), rv,
+                               hess_of(c.right));
+        if (c.is_cat) t.set_categories(node, c.cats);
+        l = lr.first;
+        r = lr.second;
+    }
+
+    // Depthwise build_tree (src/training/mod.rs:3357-4565), CPU branch.
+    Tree depthwise(Fixed root_sum) {
+        Tree t;
+        double g, h;
+        q.to_f64(root_sum, g, h);
+        size_t root = t.push_leaf(xgb_weight(g, h, p) * p.learning_rate, (float)h);
+        u64 n = pred.size();
+        rows_cur.resize(n);
+        for (u64 i = 0; i < n; i++) rows_cur[i] = (u32)i;
+        rows_next.assign(n, 0);
+        struct LN {
+            size_t node, start, len;
+            Fixed sum;
+            int parent = -1, sibling = -1;  // Subtract source
+            Bounds bounds;
+        };
+        std::vector<LN> level{{root, 0, (size_t)n, root_sum, -1, -1, Bounds()}};
+        std::vector<std::vector<std::vector<Fixed>>> parent_hists;
+        u32 leaf_count = 1;
+        for (u32 depth = 0; depth < p.max_depth; depth++) {
+            if (level.empty() || (p.max_leaves != 0 && leaf_count >= p.max_leaves)) break;
+            std::vector<std::vector<std::vector<Fixed>>> hists(level.size());
+            for (size_t i = 0; i < level.size(); i++)
+                if (level[i].parent < 0)
+                    build_hists(rows_cur.data() + level[i].start, level[i].len, hists[i]);
+            for (size_t i = 0; i < level.size(); i++) {
+                if (level[i].parent < 0) continue;
+                auto &ph = parent_hists[level[i].parent];
+                hists[i] = ph;
+                for (size_t pi = 0; pi < plans.size(); pi++)
+                    for (size_t k = 0; k < hists[i][pi].size(); k++)
+                        hists[i][pi][k] = sub(ph[pi][k], hists[level[i].sibling][pi][k]);
+            }
+            std::vector<Cand> chosen(level.size());
+            for (size_t i = 0; i < level.size(); i++)
+                chosen[i] = best_of(hists[i], level[i].sum, level[i].bounds);
+            if (p.max_leaves != 0) {
+                u32 remaining = p.max_leaves > leaf_count ? p.max_leaves - leaf_count : 0;
+                for (Cand &c : chosen)
+                    if (c.found) {
+                        if (remaining == 0) c.found = false;
+                        else remaining--;
+                    }
+            }
+            std::vector<LN> next;
+            for (size_t i = 0; i < level.size(); i++) {
+                const LN &ln = level[i];
+                if (!chosen[i].found) {
+                    float v = t.nodes[ln.node].leaf_value;
+                    for (size_t k = 0; k < ln.len; k++) pred[rows_cur[ln.start + k]] += v;
+                    continue;
+                }
+                size_t nl = partition(rows_cur.data() + ln.start, ln.len, chosen[i],
+                                      rows_next.data() + ln.start);
+                leaf_count++;
+                size_t lnode, rnode;
+                Bounds lb, rb;
+                apply_split(t, ln.node, chosen[i], ln.bounds, lnode, rnode, lb, rb);
+                size_t slot = next.size();
+                LN L{lnode, ln.start, nl, chosen[i].left, -1, -1, lb};
+                LN R{rnode, ln.start + nl, ln.len - nl, chosen[i].right, -1, -1, rb};
+                bool left_small = L.len <= R.len;
+                if (left_small) {
+                    R.parent = (int)i;
+                    R.sibling = (int)slot;
+                } else {
+                    L.parent = (int)i;
+                    L.sibling = (int)slot + 1;
+                }
+                next.push_back(L);
+                next.push_back(R);
+            }
+            parent_hists = std::move(hists);
+            // Rows of nodes that did not split stay where they are; copy them.
+            for (size_t i = 0; i < level.size(); i++)
+                if (!chosen[i].found)
+                    std::copy(rows_cur.begin() + level[i].start,
+                              rows_cur.begin() + level[i].start + level[i].len,
+                              rows_next.begin() + level[i].start);
+            std::swap(rows_cur, rows_next);
+            level = std::move(next);
+        }
+        for (const LN &ln : level) {
+            float v = t.nodes[ln.node].leaf_value;
+            for (size_t k = 0; k < ln.len; k++) pred[rows_cur[ln.start + k]] += v;
+        }
+        return t;
+    }
+
+    // Lossguide grow (src/training/lossguide.rs:494-700), CPU branch.
+    Tree lossguide(Fixed root_sum) {
+        Tree t;
+        double g, h;
+        q.to_f64(root_sum, g, h);
+        size_t root = t.push_leaf(xgb_weight(g, h, p) * p.learning_rate, (float)h);
+        u64 n = pred.size();
+        rows_cur.resize(n);
+        for (u64 i = 0; i < n; i++) rows_cur[i] = (u32)i;
+        struct Leaf {
+            size_t id, start, len;
+            u32 depth;
+            Fixed sum;
+            Bounds bounds;
+        };
+        struct Pending {
+            Leaf leaf;
+            Cand split;
+            std::shared_ptr<std::vector<std::vector<Fixed>>> hist;
+        };
+        auto less = [](const Pending &a, const Pending &b) {
+            // BinaryHeap max by (gain, then lower leaf id first).
+            if (a.split.gain != b.split.gain) return a.split.gain < b.split.gain;
+            return a.leaf.id > b.leaf.id;
+        };
+        std::priority_queue<Pending, std::vector<Pending>, decltype(less)> heap(less);
+        auto finish_leaf = [&](const Leaf &l) {
+            float v = t.nodes[l.id].leaf_value;
+            for (size_t k = 0; k < l.len; k++) pred[rows_cur[l.start + k]] += v;
+        };
+        auto evaluate = [&](std::vector<Leaf> leaves,
+                            std::shared_ptr<std::vector<std::vector<Fixed>>> parent_hist) {
+            std::vector<std::shared_ptr<std::vector<std::vector<Fixed>>>> hs(leaves.size());
+            if (parent_hist && leaves.size() == 2) {
+                size_t small = leaves[0].len > leaves[1].len ? 1 : 0;
+                hs[small] = std::make_shared<std::vector<std::vector<Fixed>>>();
+                build_hists(rows_cur.data() + leaves[small].start, leaves[small].len, *hs[small]);
+                hs[1 - small] = std::make_shared<std::vector<std::vector<Fixed>>>(*parent_hist);
+                auto &big = *hs[1 - small];
+                for (size_t pi = 0; pi < plans.size(); pi++)
+                    for (size_t k = 0; k < big[pi].size(); k++)
+                        big[pi][k] = sub(big[pi][k], (*hs[small])[pi][k]);
+            } else {
+                for (size_t i = 0; i < leaves.size(); i++) {
+                    hs[i] = std::make_shared<std::vector<std::vector<Fixed>>>();
+                    build_hists(rows_cur.data() + leaves[i].start, leaves[i].len, *hs[i]);
+                }
+            }
+            for (size_t i = 0; i < leaves.size(); i++) {
+                Cand c = best_of(*hs[i], leaves[i].sum, leaves[i].bounds);
+                if (c.found) heap.push(Pending{leaves[i], c, hs[i]});
+                else finish_leaf(leaves[i]);
+            }
+        };
+        Leaf rootl{root, 0, (size_t)n, 0, root_sum, Bounds()};
+        if (p.max_depth == 0 || p.max_leaves == 1) finish_leaf(rootl);
+        else evaluate({rootl}, nullptr);
+        u32 leaf_count = 1;
+        std::vector<u32> buf;
+        while (p.max_leaves == 0 || leaf_count < p.max_leaves) {
+            if (heap.empty()) break;
+            Pending ps = heap.top();
+            heap.pop();
+            buf.resize(ps.leaf.len);
+            size_t nl = partition(rows_cur.data() + ps.leaf.start, ps.leaf.len, ps.split, buf.data());
+            std::copy(buf.begin(), buf.end(), rows_cur.begin() + ps.leaf.start);
+            size_t lnode, rnode;
+            Bounds lb, rb;
+            apply_split(t, ps.leaf.id, ps.split, ps.leaf.bounds, lnode, rnode, lb, rb);
+            leaf_count++;
+            u32 depth = ps.leaf.depth + 1;
+            std::vector<Leaf> children{
+                {lnode, ps.leaf.start, nl, depth, ps.split.left, lb},
+                {rnode, ps.leaf.start + nl, ps.leaf.len - nl, depth, ps.split.right, rb}};
+            if (depth == p.max_depth || leaf_count == p.max_leaves) {
+                for (auto &c : children) finish_leaf(c);
+            } else {
+                evaluate(children, ps.hist);
+            }
+        }
+        while (!heap.empty()) {
+            finish_leaf(heap.top().leaf);
+            heap.pop();
+        }
+        return t;
+    }
+};
+
+// QuadratureTreeSHAP (src/model/explain.rs:116-401).
+constexpr int POINTS = 8;
+constexpr float UNSEEN = -999.0f;
+struct Rule {
+    float nodes[POINTS], weights[POINTS];
+};
+
+double legendre(int n, double x) {
+    if (n == 0) return 1.0;
+    double p0 = 1.0, p1 = x;
+    for (int k = 2; k <= n; k++) {
+        double kf = (double)k;
+        double pk = ((2.0 * kf - 1.0) * x * p1 - (kf - 1.0) * p0) / kf;
+        p0 = p1;
+        p1 = pk;
+    }
+    return p1;
+}
+
+Rule make_rule() {
+    Rule r;
+    const int n = POINTS;
+    for (int i = 0; i < n; i++) {
+        double theta = M_PI * ((double)i + 0.75) / ((double)n + 0.5);
+        double x = std::cos(theta);
+        for (int it = 0; it < 64; it++) {
+            double pn = legendre(n, x);
+            double dpn = (double)n * (x * pn - legendre(n - 1, x)) / (x * x - 1.0);
+            double dx = pn / dpn;
+            x -= dx;
+            if (std::fabs(dx) < 1e-15) break;
+        }
+        double pn = legendre(n, x);
+        double dpn = (double)n * (x * pn - legendre(n - 1, x)) / (x * x - 1.0);
+        double w = 2.0 / ((1.0 - x * x) * dpn * dpn);
+        double s = 0.5 * (x + 1.0);
+        double ws = 0.5 * w;
+        int out = n - 1 - i;
+        r.nodes[out] = (float)(s * s);
+        r.weights[out] = (float)(2.0 * s * ws);
+    }
+    return r;
+}
+
+float branch_weight(float cover, float parent) {
+    if (parent <= 0.0f) return 0.5f;
+    float w = cover / parent;
+    return w < 1e-12f ? 1e-12f : w;
+}
+
+float extract_delta(const Rule &r, const float *h, float pe, float px) {
+    float acc = 0.0f;
+    if (pe != 1.0f) {
+        float a = pe - 1.0f;
+        for (int i = 0; i < POINTS; i++) acc += a * h[i] / (1.0f + a * r.nodes[i]);
+    }
+    if (px != 1.0f) {
+        float a = px - 1.0f;
+        for (int i = 0; i < POINTS; i++) acc -= a * h[i] / (1.0f + a * r.nodes[i]);
+    }
+    return acc;
+}
+
+struct ShapRunner {
+    const std::vector<Node> &nodes;
+    const float *feats;
+    const Rule &rule;
+    std::vector<float> &path_prob;
+    std::vector<float> &phi;
+
+    void visit(size_t split, size_t child, float cw, bool sat, const float *c, float wprod,
+               float *out_h) {
+        u32 feat = nodes[split].feat;
+        float p_old = path_prob[feat];
+        float pe = sat ? (p_old == UNSEEN ? 1.0f / cw : p_old / cw) : 0.0f;
+        float cc[POINTS];
+        std::memcpy(cc, c, sizeof(cc));
+        float ae = pe - 1.0f;
+        for (int i = 0; i < POINTS; i++) cc[i] *= 1.0f + ae * rule.nodes[i];
+        if (p_old != UNSEEN) {
+            float ao = p_old - 1.0f;
+            if (ao != 0.0f)
+                for (int i = 0; i < POINTS; i++) cc[i] /= 1.0f + ao * rule.nodes[i];
+        }
+        path_prob[feat] = pe;
+        run(child, cc, wprod * cw, out_h);
+        float px = p_old == UNSEEN ? 1.0f : p_old;
+        phi[feat] += extract_delta(rule, out_h, pe, px);
+        path_prob[feat] = p_old;
+    }
+    void run(size_t idx, const float *c, float wprod, float *out_h) {
+        const Node &n = nodes[idx];
+        if (n.is_leaf) {
+            float ls = wprod * n.leaf_value;
+            for (int i = 0; i < POINTS; i++) out_h[i] = c[i] * ls * rule.weights[i];
+            return;
+        }
+        size_t l = (size_t)n.left, r = (size_t)n.right;
+        float lw = branch_weight(nodes[l].sum_hess, n.sum_hess);
+        float rw = branch_weight(nodes[r].sum_hess, n.sum_hess);
+        bool gl = Tree::goes_left(n, feats[n.feat]);
+        float rh[POINTS] = {0};
+        visit(idx, l, lw, gl, c, wprod, out_h);
+        visit(idx, r, rw, !gl, c, wprod, rh);
+        for (int i = 0; i < POINTS; i++) out_h[i] += rh[i];
+    }
+};
+
+double root_mean(const std::vector<Node> &nodes, size_t idx) {
+    const Node &n = nodes[idx];
+    if (n.is_leaf) return (double)n.leaf_value;
+    size_t l = (size_t)n.left, r = (size_t)n.right;
+    double lm = root_mean(nodes, l), rm = root_mean(nodes, r);
+    if (n.sum_hess == 0.0f) return 0.5 * (lm + rm);
+    return (lm * (double)nodes[l].sum_hess + rm * (double)nodes[r].sum_hess) / (double)n.sum_hess;
+}
+
+thread_local std::string g_error;
+
+}  // namespace
+
+// ======================================================================== C ABI
+extern "C" {
+
+int orc_quantizer_from_bounds(double mg, double mh, uint64_t n, double out[2]) {
+    try {
+        Quantizer q = Quantizer::from_bounds(mg, mh, n);
+        out[0] = q.gs;
+        out[1] = q.hs;
+        return 0;
+    } catch (std::exception &e) {
+        g_error = e.what();
+        return 1;
+    }
+}
+
+void orc_quantize(const float *gp, uint64_t n, const double scale[2], int64_t *out,
+                  int64_t sum[2]) {
+    Quantizer q;
+    q.gs = scale[0];
+    q.hs = scale[1];
+    Fixed s;
+    for (u64 i = 0; i < n; i++) {
+        Fixed f = q.to_fixed(gp[2 * i], gp[2 * i + 1]);
+        out[2 * i] = f.g;
+        out[2 * i + 1] = f.h;
+        s = add(s, f);
+    }
+    sum[0] = s.g;
+    sum[1] = s.h;
+}
+
+void orc_to_f64(const int64_t *fx, uint64_t n, const double scale[2], double *out) {
+    Quantizer q;
+    q.gi = 1.0 / scale[0];
+    q.hi = 1.0 / scale[1];
+    for (u64 i = 0; i < n; i++) q.to_f64({fx[2 * i], fx[2 * i + 1]}, out[2 * i], out[2 * i + 1]);
+}
+
+int orc_sketch_cuts(const float *x, uint64_t n, uint32_t nf, uint32_t max_bin, const float *w,
+                    const uint8_t *cat, float *cv, uint32_t *co) {
+    try {
+        Cuts c = sketch_cuts(x, n, nf, max_bin, w, cat);
+        std::copy(c.values.begin(), c.values.end(), cv);
+        std::copy(c.offsets.begin(), c.offsets.end(), co);
+        return 0;
+    } catch (std::exception &e) {
+        g_error = e.what();
+        return 1;
+    }
+}
+
+uint32_t orc_find_bin(const float *cv, const uint32_t *co, uint32_t f, uint8_t cat, float v) {
+    Cuts c;
+    c.values.assign(cv, cv + co[f + 1]);
+    c.offsets.assign(co, co + f + 2);
+    c.cat.assign(f + 1, 0);
+    c.cat[f] = cat;
+    int w = c.width(f);
+    if (std::isnan(v)) return missing_of(w);
+    return c.find_bin(f, v);
+}
+
+void orc_hist_build(const void *bins, uint32_t width, uint64_t n_rows, uint32_t n_feats,
+                    const uint32_t *offsets, const int64_t *gp, const uint32_t *rows,
+                    uint64_t n_sel, int64_t *out) {
+    u32 missing = missing_of((int)width);
+    Fixed *o = reinterpret_cast<Fixed *>(out);
+    const Fixed *g = reinterpret_cast<const Fixed *>(gp);
+    u64 n = rows ? n_sel : n_rows;
+    for (u32 f = 0; f < n_feats; f++) {
+        Fixed *h = o + offsets[f];
+        for (u64 i = 0; i < n; i++) {
+            u64 r = rows ? rows[i] : i;
+            u32 b = width == 1 ? ((const u8 *)bins)[(u64)f * n_rows + r]
+                               : ((const u16 *)bins)[(u64)f * n_rows + r];
+            if (b == missing) continue;
+            h[b] = add(h[b], g[r]);
+        }
+    }
+}
+
+void orc_node_sum(const int64_t *gp, const uint32_t *rows, uint64_t n_sel, uint64_t n_rows,
+                  int64_t out[2]) {
+    const Fixed *g = reinterpret_cast<const Fixed *>(gp);
+    Fixed s;
+    u64 n = rows ? n_sel : n_rows;
+    for (u64 i = 0; i < n; i++) s = add(s, g[rows ? rows[i] : i]);
+    out[0] = s.g;
+    out[1] = s.h;
+}
+
+void orc_best_split(const int64_t *hist, uint32_t n_feats, const uint32_t *feat_ids,
+                    const uint32_t *offsets, const int64_t node_sum[2], const double scale[2],
+                    const orc_params *p, const uint32_t *sampled, uint32_t n_sampled,
+                    uint32_t given_weight, float lo, float hi, const int8_t *monotone,
+                    uint32_t n_monotone, const uint8_t *categorical, uint32_t n_categorical,
+                    orc_split *out) {
+    Quantizer q;
+    q.gs = scale[0];
+    q.hs = scale[1];
+    q.gi = 1.0 / q.gs;
+    q.hi = 1.0 / q.hs;
+    std::vector<int8_t> mono(monotone, monotone + n_monotone);
+    SplitCtx sc;
+    sc.q = &q;
+    sc.p = p;
+    sc.given_weight = given_weight != 0;
+    sc.bounds.lo = lo;
+    sc.bounds.hi = hi;
+    sc.params = nullptr;
+    sc.mono = &mono;
+    std::vector<u32> ids(feat_ids, feat_ids + n_feats);
+    std::vector<u32> offs(offsets, offsets + n_feats + 1);
+    std::vector<u32> smp;
+    if (sampled) smp.assign(sampled, sampled + n_sampled);
+    std::vector<u8> cat;
+    if (categorical) cat.assign(categorical, categorical + n_categorical);
+    Cand c = best_split_in_block(reinterpret_cast<const Fixed *>(hist), ids, offs,
+                                 {node_sum[0], node_sum[1]}, sc, sampled ? &smp : nullptr,
+                                 categorical ? &cat : nullptr);
+    std::memset(out, 0, sizeof(*out));
+    out->found = c.found;
+    if (!c.found) return;
+    out->feat = c.feat;
+    out->bin = c.bin;
+    out->gain = c.gain;
+    out->left[0] = c.left.g;
+    out->left[1] = c.left.h;
+    out->right[0] = c.right.g;
+    out->right[1] = c.right.h;
+    out->missing_left = c.missing_left;
+    out->n_cat_words = (u32)std::min<size_t>(c.cats.size(), 1024);
+    for (u32 i = 0; i < out->n_cat_words; i++) out->cats[i] = c.cats[i];
+}
+
+uint64_t orc_partition(const uint32_t *rows, uint64_t n, const void *col, uint32_t width,
+                       uint32_t split_bin, uint32_t missing_left, const uint64_t *cats,
+                       uint32_t n_cat_words, uint32_t *out) {
+    u32 missing = missing_of((int)width);
+    u64 nl = 0;
+    std::vector<u32> right;
+    for (u64 i = 0; i < n; i++) {
+        u32 r = rows[i];
+        u32 b = width == 1 ? ((const u8 *)col)[r] : ((const u16 *)col)[r];
+        bool gl;
+        if (b == missing) gl = missing_left != 0;
+        else if (cats) {
+            u32 w = b >> 6;
+            gl = !(w < n_cat_words && ((cats[w] >> (b & 63)) & 1));
+        } else gl = b < split_bin;
+        if (gl) out[nl++] = r;
+        else right.push_back(r);
+    }
+    std::copy(right.begin(), right.end(), out + nl);
+    return nl;
+}
+
+int orc_train(const float *x, uint64_t n, uint32_t nf, const float *labels, const float *weights,
+              const uint8_t *categorical, const int8_t *monotone, uint32_t n_monotone,
+              const orc_params *pp, orc_model **out) {
+    try {
+        Params P;
+        P.p = *pp;
+        if (monotone) P.monotone.assign(monotone, monotone + n_monotone);
+        const orc_params &p = P.p;
+        if (n == 0 || nf == 0) throw std::runtime_error("training data must be non-empty");
+        if (p.max_depth > 14) throw std::runtime_error("max_depth must be in 0..=14");
+        Cuts cuts = sketch_cuts(x, n, nf, p.max_bin, weights, categorical);
+        std::vector<Block> blocks = bin_blocks(x, n, nf, cuts, p.cols_per_block);
+        auto m = std::make_unique<orc_model>();
+        m->objective = p.objective;
+        m->base_score = p.has_base_score ? p.base_score : estimate_base_score(labels, weights, n);
+        float margin = base_margin_of(p.objective, m->base_score);
+        std::vector<float> pred(n, margin);
+        std::vector<Fixed> gpair(n);
+        std::vector<float> gf(2 * n);
+        auto t0 = std::chrono::steady_clock::now();
+        for (u32 round = 0; round < p.n_rounds; round++) {
+            double mg = 0, mh = 0;
+            u64 th = threshold_for(p.subsample);
+            for (u64 i = 0; i < n; i++) {
+                float g, h;
+                gradient(p.objective, pred[i], labels[i], g, h);
+                if (weights) {
+                    g = g * weights[i];
+                    h = h * weights[i];
+                }
+                if (!row_selected(i, th, p.seed, round)) g = h = 0.0f;
+                gf[2 * i] = g;
+                gf[2 * i + 1] = h;
+                mg = std::fmax(mg, finite_abs(g));
+                mh = std::fmax(mh, finite_abs(h));
+            }
+            Quantizer q = Quantizer::from_bounds(mg, mh, n);
+            Fixed root;
+            for (u64 i = 0; i < n; i++) {
+                gpair[i] = q.to_fixed(gf[2 * i], gf[2 * i + 1]);
+                root = add(root, gpair[i]);
+            }
+            std::vector<u32> smp;
+            bool use_smp = p.colsample_bytree < 1.0f;
+            if (use_smp) smp = sample_features(nf, p.colsample_bytree, p.seed, round);
+            Trainer tr(cuts, blocks, P, q, gpair, pred, use_smp ? &smp : nullptr);
+            m->trees.push_back(p.grow_policy == 1 ? tr.lossguide(root) : tr.depthwise(root));
+        }
+        m->train_seconds =
+            std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        m->train_margins = std::move(pred);
+        *out = m.release();
+        return 0;
+    } catch (std::exception &e) {
+        g_error = e.what();
+        return 1;
+    }
+}
+
+void orc_model_free(orc_model *m) { delete m; }
+uint32_t orc_model_n_trees(const orc_model *m) { return (u32)m->trees.size(); }
+uint32_t orc_model_tree_len(const orc_model *m, uint32_t t) { return (u32)m->trees[t].nodes.size(); }
+
+void orc_model_tree_nodes(const orc_model *m, uint32_t t, orc_node *out) {
+    u32 cat_base = 0;
+    for (u32 k = 0; k < t; k++)
+        for (const Node &n : m->trees[k].nodes) cat_base += (u32)n.cats.size();
+    for (size_t i = 0; i < m->trees[t].nodes.size(); i++) {
+        const Node &n = m->trees[t].nodes[i];
+        orc_node o;
+        std::memset(&o, 0, sizeof(o));
+        o.feat = n.feat;
+        o.split_cond = n.split_cond;
+        o.left = n.left;
+        o.right = n.right;
+        o.default_left = n.default_left;
+        o.is_leaf = n.is_leaf;
+        o.leaf_value = n.leaf_value;
+        o.gain = n.gain;
+        o.sum_hess = n.sum_hess;
+        o.cat_begin = cat_base;
+        o.cat_len = (u32)n.cats.size();
+        cat_base += o.cat_len;
+        out[i] = o;
+    }
+}
+
+uint32_t orc_model_n_cat_words(const orc_model *m) {
+    u32 s = 0;
+    for (const Tree &t : m->trees)
+        for (const Node &n : t.nodes) s += (u32)n.cats.size();
+    return s;
+}
+
+void orc_model_cat_words(const orc_model *m, uint32_t *out) {
+    for (const Tree &t : m->trees)
+        for (const Node &n : t.nodes)
+            for (u32 w : n.cats) *out++ = w;
+}
+
+float orc_model_base_score(const orc_model *m) { return m->base_score; }
+float orc_model_base_margin(const orc_model *m) { return base_margin_of(m->objective, m->base_score); }
+double orc_model_train_seconds(const orc_model *m) { return m->train_seconds; }
+
+void orc_predict_margin(const orc_model *m, const float *x, uint64_t n, uint32_t nf, float *out) {
+    float bm = base_margin_of(m->objective, m->base_score);
+    for (u64 r = 0; r < n; r++) {
+        float acc = bm;
+        for (const Tree &t : m->trees) acc += t.leaf_value(x + r * nf);
+        out[r] = acc;
+    }
+}
+
+void orc_model_train_margins(const orc_model *m, float *out) {
+    std::copy(m->train_margins.begin(), m->train_margins.end(), out);
+}
+
+void orc_quadrature_rule(float nodes[8], float weights[8]) {
+    Rule r = make_rule();
+    std::memcpy(nodes, r.nodes, sizeof(r.nodes));
+    std::memcpy(weights, r.weights, sizeof(r.weights));
+}
+
+// Explainer::shap_row (src/model/explain.rs:704-728), single output group.
+int orc_shap(const orc_model *m, const float *x, uint64_t n, uint32_t nf, float *out) {
+    Rule rule = make_rule();
+    double sum = 0.0;
+    for (const Tree &t : m->trees) {
+        if (t.nodes.empty()) {
+            g_error = "tree has no nodes";
+            return 1;
+        }
+        sum += root_mean(t.nodes, 0);
+    }
+    float root_mean_f = (float)sum;
+    float bias = base_margin_of(m->objective, m->base_score);
+    std::vector<float> path_prob(nf, UNSEEN), contribs(nf + 1);
+    for (u64 r = 0; r < n; r++) {
+        float *p = out + r * (nf + 1);
+        std::fill(p, p + nf + 1, 0.0f);
+        for (const Tree &t : m->trees) {
+            std::fill(contribs.begin(), contribs.end(), 0.0f);
+            if (!t.nodes[0].is_leaf) {
+                ShapRunner runner{t.nodes, x + r * nf, rule, path_prob, contribs};
+                float ones[POINTS], h[POINTS] = {0};
+                for (int i = 0; i < POINTS; i++) ones[i] = 1.0f;
+                runner.run(0, ones, 1.0f, h);
+            }
+            for (u32 c = 0; c < nf; c++) p[c] += contribs[c];
+        }
+        p[nf] += root_mean_f;
+        p[nf] += bias;
+    }
+    return 0;
+}
+
+uint32_t orc_sample_features(uint32_t nf, float rate, uint64_t seed, uint64_t round,
+                             uint32_t *out) {
+    std::vector<u32> s = sample_features(nf, rate, seed, round);
+    std::copy(s.begin(), s.end(), out);
+    return (u32)s.size();
+}
+
+void orc_gradients(const float *pred, const float *labels, const float *w, uint64_t n, uint32_t obj,
+                   float *out) {
+    for (u64 i = 0; i < n; i++) {
+        float g, h;
+        gradient(obj, pred[i], labels[i], g, h);
+        if (w) {
+            g *= w[i];
+            h *= w[i];
+        }
+        out[2 * i] = g;
+        out[2 * i + 1] = h;
+    }
+}
+
+float orc_base_margin(uint32_t obj, float bs) { return base_margin_of(obj, bs); }
+float orc_estimate_base_score(const float *y, const float *w, uint64_t n) {
+    return estimate_base_score(y, w, n);
+}
+
+const char *orc_last_error() { return g_error.c_str(); }
+
+}  // extern "C"

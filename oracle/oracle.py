@@ -1,0 +1,377 @@
+"""ctypes binding of the CPU oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by the test suite, the smoke check and the
+CPU-baseline leg of bench.py, always as the checker. The shipped package
+(ferrisboost_amd) never imports this module.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+
+def build(force: bool = False) -> str:
+    """Compile oracle.cpp with g++ (no fast-math, no FMA contraction)."""
+    src = os.path.join(HERE, "oracle.cpp")
+    if force or not os.path.exists(LIB_PATH) or os.path.getmtime(LIB_PATH) < max(
+        os.path.getmtime(src), os.path.getmtime(os.path.join(HERE, "oracle.h"))
+    ):
+        tmp = LIB_PATH + ".tmp"
+        subprocess.check_call(
+            ["g++", "-std=c++17", "-O2", "-ffp-contract=off", "-fPIC", "-shared", "-o", tmp, src,
+             "-lpthread"]
+        )
+        os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+class Params(C.Structure):
+    _fields_ = [
+        ("n_rounds", C.c_uint32),
+        ("max_depth", C.c_uint32),
+        ("max_leaves", C.c_uint32),
+        ("max_bin", C.c_uint32),
+        ("learning_rate", C.c_float),
+        ("lambda_", C.c_float),
+        ("gamma", C.c_float),
+        ("min_child_weight", C.c_float),
+        ("alpha", C.c_float),
+        ("max_delta_step", C.c_float),
+        ("scale_pos_weight", C.c_float),
+        ("subsample", C.c_float),
+        ("colsample_bytree", C.c_float),
+        ("cols_per_block", C.c_uint32),
+        ("seed", C.c_uint64),
+        ("objective", C.c_uint32),
+        ("grow_policy", C.c_uint32),
+        ("max_cat_to_onehot", C.c_uint32),
+        ("max_cat_threshold", C.c_uint32),
+        ("base_score", C.c_float),
+        ("has_base_score", C.c_uint32),
+        ("nthread", C.c_uint32),
+        ("reserved", C.c_uint32),
+    ]
+
+
+class Node(C.Structure):
+    _fields_ = [
+        ("feat", C.c_uint32),
+        ("split_cond", C.c_float),
+        ("left", C.c_int32),
+        ("right", C.c_int32),
+        ("default_left", C.c_uint8),
+        ("is_leaf", C.c_uint8),
+        ("pad", C.c_uint16),
+        ("leaf_value", C.c_float),
+        ("gain", C.c_float),
+        ("sum_hess", C.c_float),
+        ("cat_begin", C.c_uint32),
+        ("cat_len", C.c_uint32),
+    ]
+
+
+NODE_DTYPE = np.dtype(
+    [
+        ("feat", "<u4"),
+        ("split_cond", "<f4"),
+        ("left", "<i4"),
+        ("right", "<i4"),
+        ("default_left", "u1"),
+        ("is_leaf", "u1"),
+        ("pad", "<u2"),
+        ("leaf_value", "<f4"),
+        ("gain", "<f4"),
+        ("sum_hess", "<f4"),
+        ("cat_begin", "<u4"),
+        ("cat_len", "<u4"),
+    ]
+)
+assert NODE_DTYPE.itemsize == C.sizeof(Node) == 40
+
+
+class Split(C.Structure):
+    _fields_ = [
+        ("found", C.c_uint32),
+        ("feat", C.c_uint32),
+        ("bin", C.c_uint32),
+        ("gain", C.c_float),
+        ("left", C.c_int64 * 2),
+        ("right", C.c_int64 * 2),
+        ("missing_left", C.c_uint32),
+        ("n_cat_words", C.c_uint32),
+        ("cats", C.c_uint64 * 1024),
+    ]
+
+
+OBJECTIVES = {"reg:squarederror": 0, "binary:logistic": 1}
+GROW = {"depthwise": 0, "lossguide": 1}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        P = C.c_void_p
+        L.orc_quantizer_from_bounds.argtypes = [C.c_double, C.c_double, C.c_uint64, P]
+        L.orc_quantize.argtypes = [P, C.c_uint64, P, P, P]
+        L.orc_quantize.restype = None
+        L.orc_to_f64.argtypes = [P, C.c_uint64, P, P]
+        L.orc_to_f64.restype = None
+        L.orc_sketch_cuts.argtypes = [P, C.c_uint64, C.c_uint32, C.c_uint32, P, P, P, P]
+        L.orc_find_bin.argtypes = [P, P, C.c_uint32, C.c_uint8, C.c_float]
+        L.orc_find_bin.restype = C.c_uint32
+        L.orc_hist_build.argtypes = [P, C.c_uint32, C.c_uint64, C.c_uint32, P, P, P, C.c_uint64, P]
+        L.orc_hist_build.restype = None
+        L.orc_node_sum.argtypes = [P, P, C.c_uint64, C.c_uint64, P]
+        L.orc_node_sum.restype = None
+        L.orc_best_split.argtypes = [
+            P, C.c_uint32, P, P, P, P, C.POINTER(Params), P, C.c_uint32, C.c_uint32, C.c_float,
+            C.c_float, P, C.c_uint32, P, C.c_uint32, C.POINTER(Split),
+        ]
+        L.orc_best_split.restype = None
+        L.orc_partition.argtypes = [P, C.c_uint64, P, C.c_uint32, C.c_uint32, C.c_uint32, P,
+                                    C.c_uint32, P]
+        L.orc_partition.restype = C.c_uint64
+        L.orc_train.argtypes = [P, C.c_uint64, C.c_uint32, P, P, P, P, C.c_uint32,
+                                C.POINTER(Params), C.POINTER(C.c_void_p)]
+        L.orc_model_free.argtypes = [P]
+        L.orc_model_free.restype = None
+        L.orc_model_n_trees.argtypes = [P]
+        L.orc_model_n_trees.restype = C.c_uint32
+        L.orc_model_tree_len.argtypes = [P, C.c_uint32]
+        L.orc_model_tree_len.restype = C.c_uint32
+        L.orc_model_tree_nodes.argtypes = [P, C.c_uint32, P]
+        L.orc_model_tree_nodes.restype = None
+        L.orc_model_n_cat_words.argtypes = [P]
+        L.orc_model_n_cat_words.restype = C.c_uint32
+        L.orc_model_cat_words.argtypes = [P, P]
+        L.orc_model_cat_words.restype = None
+        L.orc_model_base_score.argtypes = [P]
+        L.orc_model_base_score.restype = C.c_float
+        L.orc_model_base_margin.argtypes = [P]
+        L.orc_model_base_margin.restype = C.c_float
+        L.orc_model_train_seconds.argtypes = [P]
+        L.orc_model_train_seconds.restype = C.c_double
+        L.orc_predict_margin.argtypes = [P, P, C.c_uint64, C.c_uint32, P]
+        L.orc_predict_margin.restype = None
+        L.orc_model_train_margins.argtypes = [P, P]
+        L.orc_model_train_margins.restype = None
+        L.orc_shap.argtypes = [P, P, C.c_uint64, C.c_uint32, P]
+        L.orc_quadrature_rule.argtypes = [P, P]
+        L.orc_quadrature_rule.restype = None
+        L.orc_sample_features.argtypes = [C.c_uint32, C.c_float, C.c_uint64, C.c_uint64, P]
+        L.orc_sample_features.restype = C.c_uint32
+        L.orc_gradients.argtypes = [P, P, P, C.c_uint64, C.c_uint32, P]
+        L.orc_gradients.restype = None
+        L.orc_base_margin.argtypes = [C.c_uint32, C.c_float]
+        L.orc_base_margin.restype = C.c_float
+        L.orc_estimate_base_score.argtypes = [P, P, C.c_uint64]
+        L.orc_estimate_base_score.restype = C.c_float
+        L.orc_last_error.restype = C.c_char_p
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def make_params(**kw) -> Params:
+    """Params from XGBoost-style keyword names (defaults follow
+    python/ferrisboost/__init__.py:_DEFAULTS)."""
+    p = Params()
+    p.n_rounds = kw.get("n_rounds", 10)
+    p.max_depth = kw.get("max_depth", 6)
+    p.max_leaves = kw.get("max_leaves", 0)
+    p.max_bin = kw.get("max_bin", 255)
+    p.learning_rate = kw.get("eta", 0.3)
+    p.lambda_ = kw.get("lambda", 1.0)
+    p.gamma = kw.get("gamma", 0.0)
+    p.min_child_weight = kw.get("min_child_weight", 1.0)
+    p.alpha = kw.get("alpha", 0.0)
+    p.max_delta_step = kw.get("max_delta_step", 0.0)
+    p.scale_pos_weight = kw.get("scale_pos_weight", 1.0)
+    p.subsample = kw.get("subsample", 1.0)
+    p.colsample_bytree = kw.get("colsample_bytree", 1.0)
+    p.cols_per_block = kw.get("cols_per_block", 64)
+    p.seed = kw.get("seed", 0)
+    p.objective = OBJECTIVES[kw.get("objective", "binary:logistic")]
+    p.grow_policy = GROW[kw.get("grow_policy", "depthwise")]
+    p.max_cat_to_onehot = kw.get("max_cat_to_onehot", 4)
+    p.max_cat_threshold = kw.get("max_cat_threshold", 64)
+    if kw.get("base_score") is not None:
+        p.base_score = kw["base_score"]
+        p.has_base_score = 1
+    p.nthread = kw.get("nthread", 1)
+    return p
+
+
+class Model:
+    def __init__(self, handle):
+        self.h = handle
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_model_free(self.h)
+            self.h = None
+
+    @property
+    def n_trees(self) -> int:
+        return lib().orc_model_n_trees(self.h)
+
+    def tree(self, t: int) -> np.ndarray:
+        n = lib().orc_model_tree_len(self.h, t)
+        out = np.zeros(n, NODE_DTYPE)
+        lib().orc_model_tree_nodes(self.h, t, _p(out))
+        return out
+
+    def trees(self):
+        return [self.tree(t) for t in range(self.n_trees)]
+
+    def cat_words(self) -> np.ndarray:
+        n = lib().orc_model_n_cat_words(self.h)
+        out = np.zeros(n, np.uint32)
+        if n:
+            lib().orc_model_cat_words(self.h, _p(out))
+        return out
+
+    @property
+    def base_score(self) -> float:
+        return lib().orc_model_base_score(self.h)
+
+    @property
+    def base_margin(self) -> float:
+        return lib().orc_model_base_margin(self.h)
+
+    @property
+    def train_seconds(self) -> float:
+        return lib().orc_model_train_seconds(self.h)
+
+    def predict_margin(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(x.shape[0], np.float32)
+        lib().orc_predict_margin(self.h, _p(x), x.shape[0], x.shape[1], _p(out))
+        return out
+
+    def train_margins(self, n: int) -> np.ndarray:
+        out = np.zeros(n, np.float32)
+        lib().orc_model_train_margins(self.h, _p(out))
+        return out
+
+    def shap(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros((x.shape[0], x.shape[1] + 1), np.float32)
+        rc = lib().orc_shap(self.h, _p(x), x.shape[0], x.shape[1], _p(out))
+        if rc:
+            raise RuntimeError(lib().orc_last_error().decode())
+        return out
+
+
+def train(x, y, params: Params, weights=None, categorical=None, monotone=None) -> Model:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.ascontiguousarray(y, np.float32)
+    w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+    cat = None if categorical is None else np.ascontiguousarray(categorical, np.uint8)
+    mono = None if monotone is None else np.ascontiguousarray(monotone, np.int8)
+    h = C.c_void_p()
+    rc = lib().orc_train(_p(x), x.shape[0], x.shape[1], _p(y), _p(w), _p(cat), _p(mono),
+                         0 if mono is None else len(mono), C.byref(params), C.byref(h))
+    if rc:
+        raise RuntimeError(lib().orc_last_error().decode())
+    return Model(h)
+
+
+def sketch_cuts(x, max_bin, weights=None, categorical=None):
+    x = np.ascontiguousarray(x, np.float32)
+    n, nf = x.shape
+    vals = np.zeros(nf * max(max_bin, 2) + 1, np.float32)
+    offs = np.zeros(nf + 1, np.uint32)
+    w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+    cat = None if categorical is None else np.ascontiguousarray(categorical, np.uint8)
+    rc = lib().orc_sketch_cuts(_p(x), n, nf, max_bin, _p(w), _p(cat), _p(vals), _p(offs))
+    if rc:
+        raise RuntimeError(lib().orc_last_error().decode())
+    return vals[: offs[-1]].copy(), offs
+
+
+def quantizer_scales(max_grad, max_hess, n_rows):
+    out = np.zeros(2, np.float64)
+    rc = lib().orc_quantizer_from_bounds(max_grad, max_hess, n_rows, _p(out))
+    if rc:
+        raise RuntimeError(lib().orc_last_error().decode())
+    return out
+
+
+def quantize(gpair2n: np.ndarray, scales: np.ndarray):
+    gpair2n = np.ascontiguousarray(gpair2n, np.float32)
+    n = gpair2n.size // 2
+    out = np.zeros(2 * n, np.int64)
+    s = np.zeros(2, np.int64)
+    lib().orc_quantize(_p(gpair2n), n, _p(np.ascontiguousarray(scales, np.float64)), _p(out), _p(s))
+    return out, s
+
+
+def hist_build(bins, offsets, gpair_fixed, rows=None):
+    """bins: column-major [n_feats, n_rows] uint8/uint16."""
+    bins = np.ascontiguousarray(bins)
+    width = bins.dtype.itemsize
+    nf, n = bins.shape
+    offsets = np.ascontiguousarray(offsets, np.uint32)
+    out = np.zeros(2 * int(offsets[-1]), np.int64)
+    r = None if rows is None else np.ascontiguousarray(rows, np.uint32)
+    lib().orc_hist_build(_p(bins), width, n, nf, _p(offsets),
+                         _p(np.ascontiguousarray(gpair_fixed, np.int64)), _p(r),
+                         0 if r is None else r.size, _p(out))
+    return out
+
+
+def best_split(hist, feat_ids, offsets, node_sum, scales, params, sampled=None, given_weight=True,
+               bounds=(-3.4028234663852886e38, 3.4028234663852886e38), monotone=None,
+               categorical=None) -> Split:
+    out = Split()
+    feat_ids = np.ascontiguousarray(feat_ids, np.uint32)
+    offsets = np.ascontiguousarray(offsets, np.uint32)
+    smp = None if sampled is None else np.ascontiguousarray(sampled, np.uint32)
+    mono = None if monotone is None else np.ascontiguousarray(monotone, np.int8)
+    cat = None if categorical is None else np.ascontiguousarray(categorical, np.uint8)
+    lib().orc_best_split(
+        _p(np.ascontiguousarray(hist, np.int64)), feat_ids.size, _p(feat_ids), _p(offsets),
+        _p(np.ascontiguousarray(node_sum, np.int64)), _p(np.ascontiguousarray(scales, np.float64)),
+        C.byref(params), _p(smp), 0 if smp is None else smp.size, 1 if given_weight else 0,
+        bounds[0], bounds[1], _p(mono), 0 if mono is None else mono.size, _p(cat),
+        0 if cat is None else cat.size, C.byref(out))
+    return out
+
+
+def partition(rows, col, split_bin, missing_left, cats=None):
+    rows = np.ascontiguousarray(rows, np.uint32)
+    col = np.ascontiguousarray(col)
+    out = np.zeros_like(rows)
+    c = None if cats is None else np.ascontiguousarray(cats, np.uint64)
+    nl = lib().orc_partition(_p(rows), rows.size, _p(col), col.dtype.itemsize, split_bin,
+                             1 if missing_left else 0, _p(c), 0 if c is None else c.size, _p(out))
+    return out, int(nl)
+
+
+def quadrature_rule():
+    n = np.zeros(8, np.float32)
+    w = np.zeros(8, np.float32)
+    lib().orc_quadrature_rule(_p(n), _p(w))
+    return n, w
+
+
+def sample_features(n_features, rate, seed, round_):
+    out = np.zeros(max(n_features, 1), np.uint32)
+    k = lib().orc_sample_features(n_features, rate, seed, round_, _p(out))
+    return out[:k].copy()
