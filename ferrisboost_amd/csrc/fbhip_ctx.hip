@@ -1,0 +1,1087 @@
+// fbhip_ctx.hip -- the training context behind the fbh_* C ABI (include/fbhip.h).
+//
+// A context owns every device buffer of one training run, allocated once at
+// creation (GpuTrainCtx::new_with_shape, src/backend/cuda/train_ctx.rs:728):
+//   tiles      the training matrix as LDS-sized tiles of row records
+//   gpair      i64 [n_rows][2] fixed-point gradient pairs (+ f32 staging)
+//   rows       u32 [n_rows] row arena (+ temporary arena and u8 flags)
+//   delta      f32 [n_rows] per-row leaf value of the current tree
+//   hist       i64 [slots][width][2] node histograms kept on the device
+// All work runs in order on one HIP stream; the host blocks only where a
+// result must come back (scales, root sum, split packets, left counts).
+
+#include "fbhip_internal.h"
+#include "../../include/fbhip.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+using namespace fbh;
+
+namespace {
+
+thread_local std::string g_err;
+
+struct InputError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+struct RuntimeError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+void check(hipError_t e, const char *what) {
+    if (e != hipSuccess)
+        throw RuntimeError(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+template <class F>
+int guard(F &&f) {
+    try {
+        f();
+        return FBH_OK;
+    } catch (const InputError &e) {
+        g_err = e.what();
+        return FBH_INPUT_ERROR;
+    } catch (const std::exception &e) {
+        g_err = e.what();
+        return FBH_RUNTIME_ERROR;
+    } catch (...) {
+        g_err = "unknown error";
+        return FBH_RUNTIME_ERROR;
+    }
+}
+
+uint64_t env_u64(const char *name, uint64_t dflt) {
+    const char *v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    char *end = nullptr;
+    unsigned long long x = std::strtoull(v, &end, 10);
+    return (end && *end == 0) ? (uint64_t)x : dflt;
+}
+
+// Record sizes the histogram kernel is instantiated for.
+uint32_t round_stride(uint32_t bytes) {
+    static const uint32_t allowed[] = {4, 8, 12, 16, 32, 48, 64};
+    for (uint32_t a : allowed)
+        if (bytes <= a) return a;
+    return 0;
+}
+
+constexpr uint32_t MAX_RECORD_BYTES = 64;
+constexpr uint32_t MAX_NODES = 16384;      // nodes of one eval / partition call
+constexpr uint32_t DEFAULT_TILE_BYTES = 64 * 1024;
+constexpr uint32_t DEFAULT_CHUNK_ROWS = 4096;
+
+struct DeviceBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+};
+
+struct PinnedBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+};
+
+}  // namespace
+
+namespace fbh {
+void set_last_error(const char *msg) { g_err = msg; }
+const char *last_error() { return g_err.c_str(); }
+}  // namespace fbh
+
+struct fbh_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    uint64_t n_rows = 0;
+    uint32_t n_features = 0;
+    std::vector<uint8_t> width, cat;
+    std::vector<uint32_t> n_bins;
+    uint32_t tile_bytes = DEFAULT_TILE_BYTES;
+    uint32_t chunk_rows = DEFAULT_CHUNK_ROWS;
+    uint32_t n_slots = 0;
+    uint32_t max_cat_words = 0;
+    uint64_t width_max = 0;  // sum of all features' bins
+    uint64_t device_bytes = 0;
+    std::vector<DeviceBuf> allocs;
+
+    struct Tile {
+        uint32_t width, stride;
+        std::vector<uint32_t> feats;  // ascending global ids
+        uint8_t *data;
+        bool global;  // one feature too wide for LDS: global-memory atomics
+    };
+    std::vector<Tile> tiles;
+    std::vector<int32_t> feat_tile, feat_pos;
+    std::vector<uint8_t> uploaded;
+
+    float *gpair_f32 = nullptr;
+    int64_t *gpair = nullptr;
+    uint32_t *rows = nullptr, *tmp = nullptr;
+    uint8_t *flags = nullptr;
+    float *delta = nullptr;
+    int64_t *hist = nullptr;
+    uint8_t *col_stage = nullptr;
+    double *red_f64 = nullptr;
+    int64_t *red_i64 = nullptr;
+    uint32_t n_red_blocks = 1024;
+
+    // launch tables (device) and their pinned staging
+    TileDev *d_tiles = nullptr;
+    TileFeatDev *d_tilefeats = nullptr;
+    HistNodeDev *d_hnodes = nullptr;
+    uint32_t *d_u32a = nullptr;  // zero-slot list / subtract triples
+    uint32_t *d_u32b = nullptr;
+    SplitNodeDev *d_snodes = nullptr;
+    SplitFeatDev *d_sfeats = nullptr;
+    uint8_t *d_enabled = nullptr;
+    FeatCandDev *d_cands = nullptr;
+    uint64_t *d_cat_scratch = nullptr;
+    SplitPacketDev *d_packets = nullptr;
+    uint64_t *d_cat_out = nullptr;
+    PartReqDev *d_preqs = nullptr;
+    uint64_t *d_cat_in = nullptr;
+    uint32_t *d_counts = nullptr, *d_excl = nullptr, *d_totals = nullptr;
+    LeafDev *d_leaves = nullptr;
+    uint64_t max_chunks = 0;    // capacity of the partition chunk arrays
+    uint64_t cat_in_words = 0;  // capacity of the partition category words
+
+    PinnedBuf pin_small;   // launch tables, reused by blocking calls
+    PinnedBuf pin_leaves;  // leaf tables (asynchronous call)
+    PinnedBuf pin_out;     // results coming back
+    hipEvent_t leaves_done = nullptr;
+    bool leaves_pending = false;
+
+    // per tree
+    std::vector<uint32_t> tree_feats;
+    std::vector<int64_t> hist_off;  // global feature -> compact offset, -1 if not built
+    uint64_t hist_width = 0;
+    std::vector<int8_t> monotone;
+    struct Group {
+        int width, rd;
+        uint32_t tile_begin, n_tiles;
+        uint32_t lds_max;
+        uint32_t bytes_per_row;  // active feature bytes of the group's tiles
+        bool global;
+    };
+    std::vector<Group> groups;
+    bool has_global = false;  // this tree builds a feature with global atomics
+    uint32_t cat_words_per_node = 0;
+    bool tree_begun = false;
+    double scales[2] = {1.0, 1.0};
+
+    // timing
+    bool timing = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> ev_pool;
+    size_t ev_used = 0;
+    double hist_ms = 0.0;
+    uint64_t hist_launches = 0, hist_bytes = 0;
+
+    ~fbh_ctx() { release(); }
+
+    void release() {
+        if (device >= 0) (void)hipSetDevice(device);
+        if (stream) (void)hipStreamSynchronize(stream);
+        for (auto &a : allocs)
+            if (a.p) (void)hipFree(a.p);
+        allocs.clear();
+        if (pin_small.p) (void)hipHostFree(pin_small.p);
+        if (pin_leaves.p) (void)hipHostFree(pin_leaves.p);
+        if (pin_out.p) (void)hipHostFree(pin_out.p);
+        pin_small.p = pin_leaves.p = pin_out.p = nullptr;
+        for (auto &e : ev_pool) {
+            (void)hipEventDestroy(e.first);
+            (void)hipEventDestroy(e.second);
+        }
+        ev_pool.clear();
+        if (leaves_done) (void)hipEventDestroy(leaves_done);
+        leaves_done = nullptr;
+        if (stream) (void)hipStreamDestroy(stream);
+        stream = nullptr;
+    }
+
+    template <class T>
+    T *alloc(size_t count, const char *what) {
+        size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+        void *p = nullptr;
+        hipError_t e = hipMalloc(&p, bytes);
+        if (e != hipSuccess)
+            throw RuntimeError(std::string("device allocation of ") + what + " (" +
+                               std::to_string(bytes) + " bytes) failed: " + hipGetErrorString(e));
+        allocs.push_back({p, bytes});
+        device_bytes += bytes;
+        return static_cast<T *>(p);
+    }
+
+    void pinned(PinnedBuf &b, size_t bytes) {
+        check(hipHostMalloc(&b.p, bytes, hipHostMallocDefault), "pinned host allocation");
+        b.bytes = bytes;
+    }
+
+    void sync() { check(hipStreamSynchronize(stream), "stream synchronize"); }
+
+    void collect_timing() {
+        for (size_t i = 0; i < ev_used; i++) {
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, ev_pool[i].first, ev_pool[i].second) == hipSuccess)
+                hist_ms += ms;
+        }
+        ev_used = 0;
+    }
+};
+
+namespace {
+
+void plan_tiles(fbh_ctx &c) {
+    c.feat_tile.assign(c.n_features, -1);
+    c.feat_pos.assign(c.n_features, -1);
+    for (uint32_t w : {1u, 2u}) {
+        fbh_ctx::Tile cur{w, 0, {}, nullptr, false};
+        uint64_t lds = 0;
+        auto flush = [&]() {
+            if (cur.feats.empty()) return;
+            cur.stride = round_stride((uint32_t)cur.feats.size() * w);
+            const uint32_t t = (uint32_t)c.tiles.size();
+            for (size_t k = 0; k < cur.feats.size(); k++) {
+                c.feat_tile[cur.feats[k]] = (int32_t)t;
+                c.feat_pos[cur.feats[k]] = (int32_t)k;
+            }
+            c.tiles.push_back(cur);
+            cur.feats.clear();
+            cur.global = false;
+            lds = 0;
+        };
+        for (uint32_t f = 0; f < c.n_features; f++) {
+            if (c.width[f] != w) continue;
+            const uint64_t fb = (uint64_t)c.n_bins[f] * 16u;
+            if (fb > c.tile_bytes) {
+                // Too wide for LDS: a tile of its own, accumulated in global memory.
+                flush();
+                cur.feats.push_back(f);
+                cur.global = true;
+                flush();
+                continue;
+            }
+            const uint32_t rec = (uint32_t)(cur.feats.size() + 1) * w;
+            if (!cur.feats.empty() && (lds + fb > c.tile_bytes || rec > MAX_RECORD_BYTES)) flush();
+            cur.feats.push_back(f);
+            lds += fb;
+        }
+        flush();
+    }
+}
+
+uint32_t div_up(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+void ensure_tree(const fbh_ctx *c) {
+    if (!c->tree_begun) throw InputError("fbh_begin_tree must be called before this operation");
+}
+
+}  // namespace
+
+// ====================================================================== API
+extern "C" {
+
+size_t fbh_last_error(char *buf, size_t len) {
+    if (buf && len) {
+        size_t n = std::min(len - 1, g_err.size());
+        std::memcpy(buf, g_err.data(), n);
+        buf[n] = 0;
+    }
+    return g_err.size();
+}
+
+int fbh_device_available(int device) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return 0;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return 0;
+    return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fbh_config *cfg,
+                   fbh_ctx **out) {
+    return guard([&] {
+        if (!out) throw InputError("out must not be null");
+        *out = nullptr;
+        if (!shape || shape->n_features == 0) throw InputError("shape has no features");
+        if (n_rows == 0) throw InputError("training data must have at least one row");
+        if (n_rows > 0xFFFFFFFFull)
+            throw InputError("training data has " + std::to_string(n_rows) +
+                             " rows, above the supported limit 4294967295");
+        int n_dev = 0;
+        if (hipGetDeviceCount(&n_dev) != hipSuccess || n_dev == 0)
+            throw RuntimeError("no HIP device is available");
+        if (device < 0 || device >= n_dev)
+            throw InputError("device " + std::to_string(device) + " does not exist");
+        auto c = std::make_unique<fbh_ctx>();
+        c->device = device;
+        check(hipSetDevice(device), "hipSetDevice");
+        check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "stream creation");
+        c->n_rows = n_rows;
+        c->n_features = shape->n_features;
+        c->width.assign(shape->width, shape->width + shape->n_features);
+        c->n_bins.assign(shape->n_bins, shape->n_bins + shape->n_features);
+        c->cat.assign(shape->n_features, 0);
+        if (shape->categorical)
+            c->cat.assign(shape->categorical, shape->categorical + shape->n_features);
+        for (uint32_t f = 0; f < c->n_features; f++) {
+            if (c->width[f] != 1 && c->width[f] != 2)
+                throw InputError("feature " + std::to_string(f) + " has bin width " +
+                                 std::to_string(c->width[f]) + "; only 1 and 2 are supported");
+            const uint32_t lim = c->width[f] == 1 ? 255u : 65535u;
+            if (c->n_bins[f] == 0 || c->n_bins[f] > lim)
+                throw InputError("feature " + std::to_string(f) + " has " +
+                                 std::to_string(c->n_bins[f]) + " bins, not storable at width " +
+                                 std::to_string(c->width[f]));
+            if (c->cat[f] && c->n_bins[f] > MAX_DEVICE_CATS)
+                throw InputError("categorical feature " + std::to_string(f) + " has " +
+                                 std::to_string(c->n_bins[f]) +
+                                 " categories; the device split scan supports at most " +
+                                 std::to_string(MAX_DEVICE_CATS));
+            c->width_max += c->n_bins[f];
+            if (c->cat[f]) c->max_cat_words += (c->n_bins[f] + 63) / 64;
+        }
+        fbh_config conf{};
+        if (cfg) conf = *cfg;
+        c->tile_bytes = (uint32_t)env_u64("FB_HIP_TILE_BYTES",
+                                          conf.tile_bytes ? conf.tile_bytes : DEFAULT_TILE_BYTES);
+        c->chunk_rows = (uint32_t)env_u64(
+            "FB_HIP_CHUNK_ROWS", conf.rows_per_block ? conf.rows_per_block : DEFAULT_CHUNK_ROWS);
+        if (c->tile_bytes < 4096 || c->tile_bytes > 160 * 1024)
+            throw InputError("tile_bytes must be in 4096..=163840");
+        if (c->chunk_rows < 256 || c->chunk_rows % 256)
+            throw InputError("rows_per_block must be a positive multiple of 256");
+        c->n_slots = conf.hist_slots ? conf.hist_slots : 64;
+        if (c->n_slots > MAX_NODES)
+            throw InputError("hist_slots must be at most " + std::to_string(MAX_NODES));
+        plan_tiles(*c);
+
+        // ---- allocation, once ----
+        for (auto &t : c->tiles) t.data = c->alloc<uint8_t>(n_rows * t.stride, "tile records");
+        c->uploaded.assign(c->n_features, 0);
+        c->gpair_f32 = c->alloc<float>(2 * n_rows, "f32 gradient pairs");
+        c->gpair = c->alloc<int64_t>(2 * n_rows, "fixed-point gradient pairs");
+        c->rows = c->alloc<uint32_t>(n_rows, "row arena");
+        c->tmp = c->alloc<uint32_t>(n_rows, "partition arena");
+        c->flags = c->alloc<uint8_t>(n_rows, "partition flags");
+        c->delta = c->alloc<float>(n_rows, "prediction delta");
+        c->hist = c->alloc<int64_t>((size_t)c->n_slots * c->width_max * 2, "histogram slots");
+        c->col_stage = c->alloc<uint8_t>(n_rows * 2, "column staging");
+        c->red_f64 = c->alloc<double>(2 * c->n_red_blocks + 2, "reduction scratch");
+        c->red_i64 = c->alloc<int64_t>(2 * c->n_red_blocks + 2, "reduction scratch");
+        c->d_tiles = c->alloc<TileDev>(c->tiles.size(), "tile table");
+        c->d_tilefeats = c->alloc<TileFeatDev>(c->n_features, "tile feature table");
+        c->d_hnodes = c->alloc<HistNodeDev>(MAX_NODES, "histogram node table");
+        c->d_u32a = c->alloc<uint32_t>(3 * MAX_NODES, "slot lists");
+        c->d_u32b = c->alloc<uint32_t>(3 * MAX_NODES, "slot lists");
+        c->d_snodes = c->alloc<SplitNodeDev>(MAX_NODES, "split node table");
+        c->d_sfeats = c->alloc<SplitFeatDev>(c->n_features, "split feature table");
+        c->d_cands = c->alloc<FeatCandDev>((size_t)c->n_slots * c->n_features,
+                                           "split candidates");
+        c->d_enabled = c->alloc<uint8_t>((size_t)c->n_slots * c->n_features, "feature masks");
+        c->d_cat_scratch =
+            c->alloc<uint64_t>((size_t)c->n_slots * std::max(1u, c->max_cat_words), "category sets");
+        c->d_packets = c->alloc<SplitPacketDev>(MAX_NODES, "split packets");
+        c->d_cat_out =
+            c->alloc<uint64_t>((size_t)c->n_slots * std::max(1u, c->max_cat_words), "category sets");
+        c->d_preqs = c->alloc<PartReqDev>(MAX_NODES, "partition requests");
+        c->cat_in_words = (uint64_t)c->n_slots * std::max(1u, c->max_cat_words);
+        c->d_cat_in = c->alloc<uint64_t>(c->cat_in_words, "partition category sets");
+        c->max_chunks = n_rows / PART_CHUNK + MAX_NODES + 1;
+        c->d_counts = c->alloc<uint32_t>(c->max_chunks, "partition counts");
+        c->d_excl = c->alloc<uint32_t>(c->max_chunks + 1, "partition offsets");
+        c->d_totals = c->alloc<uint32_t>(MAX_NODES, "partition totals");
+        c->d_leaves = c->alloc<LeafDev>(MAX_NODES, "leaf table");
+        // Staging of the launch tables of one blocking call (each table 256-aligned).
+        const size_t eval_tables = sizeof(HistNodeDev) * MAX_NODES + 4 * MAX_NODES +
+                                   12 * MAX_NODES + sizeof(SplitNodeDev) * MAX_NODES +
+                                   (size_t)c->n_slots * c->n_features + 8 * 256;
+        const size_t small = std::max<size_t>(
+            {eval_tables,
+             sizeof(PartReqDev) * MAX_NODES + 8 * c->cat_in_words + 2 * 256,
+             sizeof(TileDev) * c->tiles.size() + sizeof(TileFeatDev) * c->n_features +
+                 sizeof(SplitFeatDev) * c->n_features + 256});
+        c->pinned(c->pin_small, small);
+        c->pinned(c->pin_leaves, sizeof(LeafDev) * MAX_NODES);
+        c->pinned(c->pin_out, std::max<size_t>({sizeof(SplitPacketDev) * MAX_NODES +
+                                                    8 * (size_t)c->n_slots *
+                                                        std::max(1u, c->max_cat_words),
+                                                4 * (size_t)MAX_NODES, 64}));
+        check(hipEventCreateWithFlags(&c->leaves_done, hipEventDisableTiming), "event");
+        // Zero the tile padding once.
+        for (auto &t : c->tiles)
+            check(hipMemsetAsync(t.data, 0, n_rows * t.stride, c->stream), "tile clear");
+        c->sync();
+        *out = c.release();
+    });
+}
+
+int fbh_ctx_destroy(fbh_ctx *ctx) {
+    return guard([&] { delete ctx; });
+}
+
+uint64_t fbh_ctx_device_bytes(const fbh_ctx *ctx) { return ctx ? ctx->device_bytes : 0; }
+
+int fbh_upload_block(fbh_ctx *c, const uint32_t *feat_ids, uint32_t n_feats, uint32_t width,
+                     const void *bins) {
+    return guard([&] {
+        if (!c || !feat_ids || !bins) throw InputError("null argument");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        for (uint32_t l = 0; l < n_feats; l++) {
+            const uint32_t f = feat_ids[l];
+            if (f >= c->n_features) throw InputError("feature id out of range");
+            if (c->width[f] != width)
+                throw InputError("feature " + std::to_string(f) +
+                                 " does not have the block's bin width");
+        }
+        for (uint32_t l = 0; l < n_feats; l++) {
+            const uint32_t f = feat_ids[l];
+            const fbh_ctx::Tile &t = c->tiles[c->feat_tile[f]];
+            const uint8_t *src = static_cast<const uint8_t *>(bins) + (uint64_t)l * c->n_rows * width;
+            check(hipMemcpyAsync(c->col_stage, src, c->n_rows * width, hipMemcpyHostToDevice,
+                                 c->stream),
+                  "block upload");
+            // One feature column into its record position.
+            check(launch_pack_feature(c->col_stage, c->n_rows, width, t.data, t.stride,
+                                      (uint32_t)c->feat_pos[f] * width, c->stream),
+                  "tile packing");
+            c->uploaded[f] = 1;
+        }
+        c->sync();
+    });
+}
+
+int fbh_upload_quantize_gpair(fbh_ctx *c, const float *g2n, uint64_t th, uint64_t seed,
+                              uint64_t tree, double scales_out[2], int64_t root_out[2]) {
+    return guard([&] {
+        if (!c || !g2n) throw InputError("null argument");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        check(hipMemcpyAsync(c->gpair_f32, g2n, c->n_rows * 8, hipMemcpyHostToDevice, c->stream),
+              "gradient upload");
+        check(launch_gpair_maxabs(c->gpair_f32, c->n_rows, th, seed, tree, c->red_f64,
+                                  c->n_red_blocks, c->red_f64 + 2 * c->n_red_blocks, c->stream),
+              "gradient bounds");
+        double mx[2];
+        check(hipMemcpyAsync(c->pin_out.p, c->red_f64 + 2 * c->n_red_blocks, 16,
+                             hipMemcpyDeviceToHost, c->stream),
+              "bounds download");
+        c->sync();
+        std::memcpy(mx, c->pin_out.p, 16);
+        // GradQuantizer::try_from_bounds (src/types.rs:288-303, 367-385).
+        if (!(std::isfinite(mx[0]) && std::isfinite(mx[1]) && mx[0] >= 0.0 && mx[1] >= 0.0))
+            throw InputError(
+                "non-finite gradient or Hessian (or invalid bounds); reduce extreme labels, "
+                "weights, base_score or objective parameters");
+        for (int k = 0; k < 2; k++) {
+            double s = 1.0;
+            const double m = mx[k];
+            if (m > 0.0 && std::isfinite(m)) {
+                const double budget = (double)(1ull << 62) / (double)std::max<uint64_t>(c->n_rows, 1);
+                const double raw = budget / m;
+                if (std::isfinite(raw) && raw > 0.0) {
+                    double l = std::floor(std::log2(raw));
+                    int e = std::isnan(l) ? 0 : (l > 1000.0 ? 1000 : (l < -1000.0 ? -1000 : (int)l));
+                    s = std::exp2((double)e);
+                }
+            }
+            c->scales[k] = s;
+        }
+        check(launch_gpair_quantize(c->gpair_f32, c->n_rows, c->scales[0], c->scales[1], c->gpair,
+                                    c->red_i64, c->n_red_blocks, c->red_i64 + 2 * c->n_red_blocks,
+                                    c->stream),
+              "gradient quantisation");
+        check(hipMemcpyAsync(c->pin_out.p, c->red_i64 + 2 * c->n_red_blocks, 16,
+                             hipMemcpyDeviceToHost, c->stream),
+              "root sum download");
+        c->sync();
+        std::memcpy(root_out, c->pin_out.p, 16);
+        scales_out[0] = c->scales[0];
+        scales_out[1] = c->scales[1];
+    });
+}
+
+int fbh_upload_gpair_fixed(fbh_ctx *c, const int64_t *g2n, const double scales[2]) {
+    return guard([&] {
+        if (!c || !g2n || !scales) throw InputError("null argument");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        check(hipMemcpyAsync(c->gpair, g2n, c->n_rows * 16, hipMemcpyHostToDevice, c->stream),
+              "gradient upload");
+        c->scales[0] = scales[0];
+        c->scales[1] = scales[1];
+        c->sync();
+    });
+}
+
+int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const int8_t *monotone,
+                   uint32_t n_monotone, fbh_span *root) {
+    return guard([&] {
+        if (!c || !root) throw InputError("null argument");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        c->tree_feats.clear();
+        if (features) {
+            for (uint32_t i = 0; i < n_sel; i++) {
+                if (features[i] >= c->n_features) throw InputError("feature id out of range");
+                if (i && features[i] <= features[i - 1])
+                    throw InputError("tree features must be strictly ascending");
+                c->tree_feats.push_back(features[i]);
+            }
+        } else {
+            for (uint32_t f = 0; f < c->n_features; f++) c->tree_feats.push_back(f);
+        }
+        if (c->tree_feats.empty()) throw InputError("a tree needs at least one feature");
+        for (uint32_t f : c->tree_feats)
+            if (!c->uploaded[f])
+                throw InputError("feature " + std::to_string(f) + " was never uploaded");
+        c->monotone.assign(c->n_features, 0);
+        if (monotone)
+            for (uint32_t i = 0; i < std::min(n_monotone, c->n_features); i++)
+                c->monotone[i] = monotone[i];
+        // compact histogram layout of this tree
+        c->hist_off.assign(c->n_features, -1);
+        uint64_t off = 0;
+        for (uint32_t f : c->tree_feats) {
+            c->hist_off[f] = (int64_t)off;
+            off += c->n_bins[f];
+        }
+        c->hist_width = off;
+        // tiles with active features, grouped by (width, record dwords)
+        std::vector<TileDev> td;
+        std::vector<TileFeatDev> tf;
+        c->groups.clear();
+        c->has_global = false;
+        for (int glob = 0; glob < 2; glob++)
+        for (uint32_t w : {1u, 2u}) {
+            for (uint32_t stride : {4u, 8u, 12u, 16u, 32u, 48u, 64u}) {
+                fbh_ctx::Group g{(int)w, (int)stride / 4, (uint32_t)td.size(), 0, 0, 0, glob == 1};
+                for (const auto &t : c->tiles) {
+                    if (t.width != w || t.stride != stride || (int)t.global != glob) continue;
+                    TileDev d{};
+                    d.data = t.data;
+                    d.stride = t.stride;
+                    d.width = t.width;
+                    d.n_feat = (uint32_t)t.feats.size();
+                    d.feat_base = (uint32_t)tf.size();
+                    uint32_t lds = 0, active_bytes = 0;
+                    for (uint32_t f : t.feats) {
+                        TileFeatDev e{};
+                        if (c->hist_off[f] >= 0) {
+                            e.n_bins = c->n_bins[f];
+                            e.lds_off = lds;
+                            e.hist_off = (uint32_t)c->hist_off[f];
+                            lds += c->n_bins[f];
+                            active_bytes += w;
+                        }
+                        tf.push_back(e);
+                    }
+                    if (lds == 0) {
+                        tf.resize(d.feat_base);
+                        continue;
+                    }
+                    d.lds_slots = t.global ? 0 : lds;
+                    td.push_back(d);
+                    g.n_tiles++;
+                    if (!t.global) g.lds_max = std::max(g.lds_max, lds);
+                    g.bytes_per_row += active_bytes;
+                }
+                if (g.n_tiles) {
+                    c->groups.push_back(g);
+                    c->has_global = c->has_global || g.global;
+                }
+            }
+        }
+        // split feature table
+        std::vector<SplitFeatDev> sf;
+        uint32_t cat_base = 0;
+        for (uint32_t f : c->tree_feats) {
+            SplitFeatDev s{};
+            s.feat = f;
+            s.hist_off = (uint32_t)c->hist_off[f];
+            s.n_bins = c->n_bins[f];
+            s.monotone = c->monotone[f];
+            s.categorical = c->cat[f];
+            if (c->cat[f]) {
+                s.cat_words = (c->n_bins[f] + 63) / 64;
+                s.cat_base = cat_base;
+                cat_base += s.cat_words;
+            }
+            sf.push_back(s);
+        }
+        c->cat_words_per_node = cat_base;
+        uint8_t *st = static_cast<uint8_t *>(c->pin_small.p);
+        const size_t b1 = sizeof(TileDev) * td.size(), b2 = sizeof(TileFeatDev) * tf.size(),
+                     b3 = sizeof(SplitFeatDev) * sf.size();
+        std::memcpy(st, td.data(), b1);
+        std::memcpy(st + b1, tf.data(), b2);
+        std::memcpy(st + b1 + b2, sf.data(), b3);
+        check(hipMemcpyAsync(c->d_tiles, st, b1, hipMemcpyHostToDevice, c->stream), "tree tables");
+        check(hipMemcpyAsync(c->d_tilefeats, st + b1, b2, hipMemcpyHostToDevice, c->stream),
+              "tree tables");
+        check(hipMemcpyAsync(c->d_sfeats, st + b1 + b2, b3, hipMemcpyHostToDevice, c->stream),
+              "tree tables");
+        check(launch_init_rows(c->rows, c->delta, c->n_rows, c->stream), "row arena reset");
+        c->sync();
+        c->tree_begun = true;
+        root->offset = 0;
+        root->len = (uint32_t)c->n_rows;
+    });
+}
+
+int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_split_params *sp,
+                   const uint8_t *enabled, fbh_split *out, uint64_t *cat_words,
+                   uint32_t cat_capacity) {
+    return guard([&] {
+        if (!c || (!nodes && n) || !sp || (!out && n)) throw InputError("null argument");
+        ensure_tree(c);
+        if (n == 0) return;
+        if (n > c->n_slots) throw InputError("more nodes than histogram slots");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        for (uint32_t i = 0; i < n; i++) {
+            const fbh_node &nd = nodes[i];
+            if (nd.slot >= c->n_slots) throw InputError("histogram slot out of range");
+            if ((uint64_t)nd.rows.offset + nd.rows.len > c->n_rows)
+                throw InputError("row span out of range");
+            if (nd.subtract_parent >= 0) {
+                if ((uint32_t)nd.subtract_parent >= c->n_slots)
+                    throw InputError("parent slot out of range");
+                if (nd.subtract_sibling < 0 || (uint32_t)nd.subtract_sibling >= n ||
+                    nodes[nd.subtract_sibling].subtract_parent >= 0)
+                    throw InputError("subtract sibling must be an accumulated node of the call");
+            }
+        }
+        uint8_t *st = static_cast<uint8_t *>(c->pin_small.p);
+        // ---- histograms of accumulated nodes ----
+        std::vector<HistNodeDev> hn;
+        std::vector<uint32_t> zero_slots;
+        uint32_t chunks = 0;
+        uint64_t acc_rows = 0;
+        for (uint32_t i = 0; i < n; i++) {
+            const fbh_node &nd = nodes[i];
+            if (nd.subtract_parent >= 0) continue;
+            const uint32_t nc = div_up(nd.rows.len, c->chunk_rows);
+            // Single-chunk nodes are written by plain stores, except that a
+            // globally accumulated feature needs a zeroed slot.
+            if (nc != 1 || c->has_global) zero_slots.push_back(nd.slot);
+            if (nc == 0) continue;
+            HistNodeDev h{};
+            h.row_off = nd.rows.offset;
+            h.row_len = nd.rows.len;
+            h.chunk_begin = chunks;
+            h.slot = nd.slot;
+            h.n_chunks = nc;
+            hn.push_back(h);
+            chunks += nc;
+            acc_rows += nd.rows.len;
+        }
+        std::vector<uint32_t> triples;
+        for (uint32_t i = 0; i < n; i++) {
+            const fbh_node &nd = nodes[i];
+            if (nd.subtract_parent < 0) continue;
+            triples.push_back(nd.slot);
+            triples.push_back((uint32_t)nd.subtract_parent);
+            triples.push_back(nodes[nd.subtract_sibling].slot);
+        }
+        size_t o = 0;
+        const size_t bh = sizeof(HistNodeDev) * hn.size();
+        std::memcpy(st + o, hn.data(), bh);
+        check(hipMemcpyAsync(c->d_hnodes, st + o, bh, hipMemcpyHostToDevice, c->stream), "tables");
+        o += (bh + 255) & ~size_t(255);
+        std::memcpy(st + o, zero_slots.data(), 4 * zero_slots.size());
+        check(hipMemcpyAsync(c->d_u32a, st + o, 4 * zero_slots.size(), hipMemcpyHostToDevice,
+                             c->stream),
+              "tables");
+        o += (4 * zero_slots.size() + 255) & ~size_t(255);
+        std::memcpy(st + o, triples.data(), 4 * triples.size());
+        check(hipMemcpyAsync(c->d_u32b, st + o, 4 * triples.size(), hipMemcpyHostToDevice,
+                             c->stream),
+              "tables");
+        o += (4 * triples.size() + 255) & ~size_t(255);
+        check(launch_zero_slots(c->hist, c->hist_width, c->d_u32a, (uint32_t)zero_slots.size(),
+                                c->stream),
+              "histogram clear");
+        if (!hn.empty()) {
+            size_t ev = c->ev_used;
+            if (c->timing) {
+                if (c->ev_pool.size() <= ev) {
+                    hipEvent_t a, b;
+                    check(hipEventCreate(&a), "event");
+                    check(hipEventCreate(&b), "event");
+                    c->ev_pool.push_back({a, b});
+                }
+                check(hipEventRecord(c->ev_pool[ev].first, c->stream), "event");
+            }
+            uint64_t bins_active = 0;
+            for (const auto &g : c->groups) {
+                HistLaunch L{};
+                L.tiles = c->d_tiles + g.tile_begin;
+                L.feats = c->d_tilefeats;
+                L.n_tiles = g.n_tiles;
+                L.nodes = c->d_hnodes;
+                L.n_nodes = (uint32_t)hn.size();
+                L.n_chunks = chunks;
+                L.chunk_rows = c->chunk_rows;
+                L.chunk_groups = div_up(chunks, XCDS);
+                L.rows = c->rows;
+                L.gpair = c->gpair;
+                L.hist = c->hist;
+                L.hist_width = c->hist_width;
+                if (g.global)
+                    check(launch_hist_global(L, g.width, c->stream), "histogram launch");
+                else
+                    check(launch_hist(L, g.width, g.rd, (size_t)g.lds_max * 16, c->stream),
+                          "histogram launch");
+                c->hist_bytes += acc_rows * g.bytes_per_row;
+            }
+            for (uint32_t f : c->tree_feats) bins_active += c->n_bins[f];
+            // Algorithmic bytes: cells + gpair (16) + row id (4) per row and
+            // feature set, and the written histogram (2 x 16 per bin).
+            c->hist_bytes += acc_rows * 20 + (uint64_t)hn.size() * 32 * bins_active;
+            c->hist_launches++;
+            if (c->timing) {
+                check(hipEventRecord(c->ev_pool[ev].second, c->stream), "event");
+                c->ev_used++;
+            }
+        }
+        check(launch_subtract(c->hist, c->hist_width, c->d_u32b, (uint32_t)(triples.size() / 3),
+                              c->stream),
+              "sibling subtraction");
+        // ---- split scan ----
+        std::vector<SplitNodeDev> sn(n);
+        for (uint32_t i = 0; i < n; i++) {
+            sn[i].sum_g = nodes[i].sum[0];
+            sn[i].sum_h = nodes[i].sum[1];
+            sn[i].lower = nodes[i].lower;
+            sn[i].upper = nodes[i].upper;
+            sn[i].slot = nodes[i].slot;
+        }
+        const size_t bs = sizeof(SplitNodeDev) * n;
+        std::memcpy(st + o, sn.data(), bs);
+        check(hipMemcpyAsync(c->d_snodes, st + o, bs, hipMemcpyHostToDevice, c->stream), "tables");
+        o += (bs + 255) & ~size_t(255);
+        const uint32_t nf = (uint32_t)c->tree_feats.size();
+        const uint8_t *d_en = nullptr;
+        if (enabled) {
+            std::memcpy(st + o, enabled, (size_t)n * nf);
+            check(hipMemcpyAsync(c->d_enabled, st + o, (size_t)n * nf, hipMemcpyHostToDevice,
+                                 c->stream),
+                  "tables");
+            d_en = c->d_enabled;
+        }
+        SplitParamsDev P{};
+        P.inv_g = 1.0 / c->scales[0];
+        P.inv_h = 1.0 / c->scales[1];
+        P.lambda_ = sp->lambda_;
+        P.gamma = sp->gamma;
+        P.mcw = sp->min_child_weight;
+        P.alpha = sp->alpha;
+        P.mds = sp->max_delta_step;
+        P.max_cat_to_onehot = sp->max_cat_to_onehot;
+        P.max_cat_threshold = sp->max_cat_threshold;
+        P.n_feats = nf;
+        P.cat_words_per_node = c->cat_words_per_node;
+        check(launch_split_feats(c->hist, c->hist_width, c->d_snodes, n, c->d_sfeats, d_en, P,
+                                 c->d_cands, c->d_cat_scratch, c->stream),
+              "split scan");
+        const uint32_t cw = std::max(1u, c->cat_words_per_node);
+        check(launch_split_nodes(c->d_cands, c->d_sfeats, n, P, c->d_snodes, c->d_cat_scratch,
+                                 c->d_packets, c->d_cat_out, cw, c->stream),
+              "split argmax");
+        uint8_t *po = static_cast<uint8_t *>(c->pin_out.p);
+        check(hipMemcpyAsync(po, c->d_packets, sizeof(SplitPacketDev) * n, hipMemcpyDeviceToHost,
+                             c->stream),
+              "packet download");
+        const bool any_cat = c->cat_words_per_node > 0;
+        if (any_cat)
+            check(hipMemcpyAsync(po + sizeof(SplitPacketDev) * n, c->d_cat_out,
+                                 8 * (size_t)n * cw, hipMemcpyDeviceToHost, c->stream),
+                  "category download");
+        c->sync();
+        if (c->timing) c->collect_timing();
+        static_assert(sizeof(SplitPacketDev) == sizeof(fbh_split), "packet layout");
+        std::memcpy(out, po, sizeof(fbh_split) * n);
+        if (any_cat) {
+            const uint64_t *words = reinterpret_cast<const uint64_t *>(po + sizeof(SplitPacketDev) * n);
+            for (uint32_t i = 0; i < n; i++) {
+                if (!out[i].found || !out[i].is_cat) continue;
+                if (!cat_words || (uint64_t)out[i].cat_offset + out[i].n_cat_words > cat_capacity)
+                    throw InputError("cat_words capacity is too small for the category sets");
+                std::memcpy(cat_words + out[i].cat_offset, words + (size_t)i * cw,
+                            8 * out[i].n_cat_words);
+            }
+        }
+    });
+}
+
+int fbh_download_histogram(fbh_ctx *c, uint32_t slot, int64_t *out, uint64_t *width_out) {
+    return guard([&] {
+        if (!c) throw InputError("null argument");
+        ensure_tree(c);
+        if (width_out) *width_out = c->hist_width;
+        if (!out) return;
+        if (slot >= c->n_slots) throw InputError("histogram slot out of range");
+        check(hipMemcpyAsync(out, c->hist + (uint64_t)slot * c->hist_width * 2,
+                             c->hist_width * 16, hipMemcpyDeviceToHost, c->stream),
+              "histogram download");
+        c->sync();
+    });
+}
+
+int fbh_partition(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n, const uint64_t *cat_words,
+                  uint32_t n_cat_words, fbh_span *children) {
+    return guard([&] {
+        if (!c || (!reqs && n) || (!children && n)) throw InputError("null argument");
+        ensure_tree(c);
+        if (n == 0) return;
+        if (n > MAX_NODES) throw InputError("too many partition requests");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        std::vector<PartReqDev> pr;
+        std::vector<uint32_t> which;
+        uint32_t chunks = 0;
+        for (uint32_t i = 0; i < n; i++) {
+            const fbh_part_req &r = reqs[i];
+            if ((uint64_t)r.rows.offset + r.rows.len > c->n_rows)
+                throw InputError("row span out of range");
+            if (r.feat >= c->n_features) throw InputError("feature id out of range");
+            if (r.n_cat_words && (uint64_t)r.cat_offset + r.n_cat_words > n_cat_words)
+                throw InputError("category set out of range");
+            if (r.rows.len == 0) continue;
+            const auto &t = c->tiles[c->feat_tile[r.feat]];
+            PartReqDev d{};
+            d.row_off = r.rows.offset;
+            d.row_len = r.rows.len;
+            d.chunk_begin = chunks;
+            d.n_chunks = div_up(r.rows.len, PART_CHUNK);
+            d.data = t.data;
+            d.stride = t.stride;
+            d.byte_off = (uint32_t)c->feat_pos[r.feat] * t.width;
+            d.width = t.width;
+            d.bin = r.bin;
+            d.missing_left = r.missing_left;
+            d.cat_off = r.cat_offset;
+            d.n_cat_words = r.n_cat_words;
+            pr.push_back(d);
+            which.push_back(i);
+            chunks += d.n_chunks;
+        }
+        for (uint32_t i = 0; i < n; i++) {
+            children[2 * i] = {reqs[i].rows.offset, 0};
+            children[2 * i + 1] = {reqs[i].rows.offset, 0};
+        }
+        if (pr.empty()) return;
+        if (chunks > c->max_chunks)
+            throw InputError("partition spans overlap or exceed the row arena");
+        if (n_cat_words > c->cat_in_words)
+            throw InputError("too many category words for one partition call");
+        uint8_t *st = static_cast<uint8_t *>(c->pin_small.p);
+        const size_t bp = sizeof(PartReqDev) * pr.size();
+        std::memcpy(st, pr.data(), bp);
+        check(hipMemcpyAsync(c->d_preqs, st, bp, hipMemcpyHostToDevice, c->stream), "tables");
+        if (n_cat_words) {
+            const size_t off = (bp + 255) & ~size_t(255);
+            std::memcpy(st + off, cat_words, 8 * (size_t)n_cat_words);
+            check(hipMemcpyAsync(c->d_cat_in, st + off, 8 * (size_t)n_cat_words,
+                                 hipMemcpyHostToDevice, c->stream),
+                  "tables");
+        }
+        check(launch_partition(c->d_preqs, (uint32_t)pr.size(), chunks, c->rows, c->tmp, c->flags,
+                               c->d_counts, c->d_excl, c->d_totals, c->d_cat_in, c->stream),
+              "partition");
+        check(hipMemcpyAsync(c->pin_out.p, c->d_totals, 4 * pr.size(), hipMemcpyDeviceToHost,
+                             c->stream),
+              "partition totals");
+        c->sync();
+        const uint32_t *tot = static_cast<const uint32_t *>(c->pin_out.p);
+        for (size_t k = 0; k < pr.size(); k++) {
+            const uint32_t i = which[k];
+            const uint32_t nl = tot[k];
+            children[2 * i] = {reqs[i].rows.offset, nl};
+            children[2 * i + 1] = {reqs[i].rows.offset + nl, reqs[i].rows.len - nl};
+        }
+    });
+}
+
+int fbh_assign_leaves(fbh_ctx *c, const fbh_span *spans, const float *values, uint32_t n) {
+    return guard([&] {
+        if (!c || (n && (!spans || !values))) throw InputError("null argument");
+        ensure_tree(c);
+        if (n == 0) return;
+        if (n > MAX_NODES) throw InputError("too many leaves");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        if (c->leaves_pending) {
+            check(hipEventSynchronize(c->leaves_done), "leaf table reuse");
+            c->leaves_pending = false;
+        }
+        LeafDev *ld = static_cast<LeafDev *>(c->pin_leaves.p);
+        uint32_t m = 0, chunks = 0;
+        for (uint32_t i = 0; i < n; i++) {
+            if ((uint64_t)spans[i].offset + spans[i].len > c->n_rows)
+                throw InputError("row span out of range");
+            if (spans[i].len == 0) continue;
+            ld[m].row_off = spans[i].offset;
+            ld[m].row_len = spans[i].len;
+            ld[m].chunk_begin = chunks;
+            ld[m].value = values[i];
+            chunks += div_up(spans[i].len, PART_CHUNK);
+            m++;
+        }
+        if (m == 0) return;
+        check(hipMemcpyAsync(c->d_leaves, ld, sizeof(LeafDev) * m, hipMemcpyHostToDevice,
+                             c->stream),
+              "leaf table");
+        check(hipEventRecord(c->leaves_done, c->stream), "event");
+        c->leaves_pending = true;
+        check(launch_assign_leaves(c->d_leaves, m, chunks, c->rows, c->delta, c->stream),
+              "leaf assignment");
+    });
+}
+
+int fbh_download_delta(fbh_ctx *c, float *out) {
+    return guard([&] {
+        if (!c || !out) throw InputError("null argument");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        check(hipMemcpyAsync(out, c->delta, c->n_rows * 4, hipMemcpyDeviceToHost, c->stream),
+              "delta download");
+        c->sync();
+    });
+}
+
+int fbh_download_rows(fbh_ctx *c, uint32_t *out) {
+    return guard([&] {
+        if (!c || !out) throw InputError("null argument");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        check(hipMemcpyAsync(out, c->rows, c->n_rows * 4, hipMemcpyDeviceToHost, c->stream),
+              "row download");
+        c->sync();
+    });
+}
+
+int fbh_set_timing(fbh_ctx *c, int enabled) {
+    return guard([&] {
+        if (!c) throw InputError("null argument");
+        c->timing = enabled != 0;
+    });
+}
+
+int fbh_hist_timing(fbh_ctx *c, double *ms, uint64_t *launches, uint64_t *bytes, int reset) {
+    return guard([&] {
+        if (!c) throw InputError("null argument");
+        c->sync();
+        c->collect_timing();
+        if (ms) *ms = c->hist_ms;
+        if (launches) *launches = c->hist_launches;
+        if (bytes) *bytes = c->hist_bytes;
+        if (reset) {
+            c->hist_ms = 0.0;
+            c->hist_launches = 0;
+            c->hist_bytes = 0;
+        }
+    });
+}
+
+// ------------------------------------------------------------- standalone
+int fbh_build_histogram(int device, const void *bins, uint32_t width, uint64_t n_rows,
+                        uint32_t n_feats, const uint32_t *offsets, const int64_t *gpair2n,
+                        const uint32_t *rows, uint64_t n_sel, int64_t *out) {
+    return guard([&] {
+        if (!bins || !offsets || !gpair2n || !out) throw InputError("null argument");
+        if (width != 1 && width != 2) throw InputError("width must be 1 or 2");
+        std::vector<uint8_t> wv(n_feats, (uint8_t)width);
+        std::vector<uint32_t> nb(n_feats);
+        for (uint32_t f = 0; f < n_feats; f++) {
+            if (offsets[f + 1] < offsets[f]) throw InputError("offsets must be non-decreasing");
+            nb[f] = offsets[f + 1] - offsets[f];
+            if (nb[f] == 0) throw InputError("every feature needs at least one bin");
+        }
+        fbh_shape sh{n_feats, wv.data(), nb.data(), nullptr};
+        fbh_config cf{};
+        cf.hist_slots = 1;
+        fbh_ctx *c = nullptr;
+        int rc = fbh_ctx_create(device, n_rows, &sh, &cf, &c);
+        if (rc) throw RuntimeError(g_err);
+        std::unique_ptr<fbh_ctx> own(c);
+        std::vector<uint32_t> ids(n_feats);
+        for (uint32_t f = 0; f < n_feats; f++) ids[f] = f;
+        if (fbh_upload_block(c, ids.data(), n_feats, width, bins)) throw RuntimeError(g_err);
+        const double one[2] = {1.0, 1.0};
+        if (fbh_upload_gpair_fixed(c, gpair2n, one)) throw RuntimeError(g_err);
+        fbh_span root;
+        if (fbh_begin_tree(c, nullptr, 0, nullptr, 0, &root)) throw RuntimeError(g_err);
+        uint64_t n_use = rows ? n_sel : n_rows;
+        if (rows) {
+            for (uint64_t i = 0; i < n_sel; i++)
+                if (rows[i] >= n_rows) throw InputError("row index out of range");
+            if (n_sel > n_rows) throw InputError("more selected rows than rows");
+            check(hipMemcpyAsync(c->rows, rows, 4 * n_sel, hipMemcpyHostToDevice, c->stream),
+                  "row upload");
+        }
+        fbh_node nd{};
+        nd.rows = {0, (uint32_t)n_use};
+        nd.slot = 0;
+        nd.subtract_parent = -1;
+        nd.subtract_sibling = -1;
+        nd.lower = -3.4028234663852886e38f;
+        nd.upper = 3.4028234663852886e38f;
+        fbh_split_params sp{};
+        sp.lambda_ = 1.0f;
+        sp.max_cat_to_onehot = 4;
+        sp.max_cat_threshold = 64;
+        fbh_split pk;
+        if (fbh_eval_nodes(c, &nd, 1, &sp, nullptr, &pk, nullptr, 0)) throw RuntimeError(g_err);
+        if (fbh_download_histogram(c, 0, out, nullptr)) throw RuntimeError(g_err);
+    });
+}
+
+int fbh_partition_rows(int device, const void *col, uint32_t width, uint64_t n_rows,
+                       const uint32_t *rows, uint64_t n, uint32_t split_bin, uint32_t missing_left,
+                       const uint64_t *cat_words, uint32_t n_cat_words, uint32_t *out,
+                       uint64_t *n_left) {
+    return guard([&] {
+        if (!col || !rows || !out || !n_left) throw InputError("null argument");
+        if (width != 1 && width != 2) throw InputError("width must be 1 or 2");
+        if (n > n_rows) throw InputError("more rows than the column holds");
+        for (uint64_t i = 0; i < n; i++)
+            if (rows[i] >= n_rows) throw InputError("row index out of range");
+        uint8_t w8 = (uint8_t)width;
+        // Only the bin width matters to a partition; a categorical column
+        // needs category-set capacity for n_cat_words words.
+        uint32_t nb = 1;
+        uint8_t catf = n_cat_words ? 1 : 0;
+        if (catf) {
+            if ((uint64_t)n_cat_words * 64 > MAX_DEVICE_CATS)
+                throw InputError("category sets wider than " + std::to_string(MAX_DEVICE_CATS) +
+                                 " codes are not supported on the device");
+            nb = std::min<uint32_t>(n_cat_words * 64, width == 1 ? 254u : MAX_DEVICE_CATS);
+        }
+        fbh_shape sh{1, &w8, &nb, &catf};
+        fbh_config cf{};
+        cf.hist_slots = 1;
+        fbh_ctx *c = nullptr;
+        if (fbh_ctx_create(device, n_rows, &sh, &cf, &c)) throw RuntimeError(g_err);
+        std::unique_ptr<fbh_ctx> own(c);
+        const uint32_t f0 = 0;
+        if (fbh_upload_block(c, &f0, 1, width, col)) throw RuntimeError(g_err);
+        fbh_span root;
+        if (fbh_begin_tree(c, nullptr, 0, nullptr, 0, &root)) throw RuntimeError(g_err);
+        check(hipMemcpyAsync(c->rows, rows, 4 * n, hipMemcpyHostToDevice, c->stream), "row upload");
+        fbh_part_req r{};
+        r.rows = {0, (uint32_t)n};
+        r.feat = 0;
+        r.bin = split_bin;
+        r.missing_left = missing_left;
+        r.cat_offset = 0;
+        r.n_cat_words = n_cat_words;
+        fbh_span ch[2];
+        if (fbh_partition(c, &r, 1, cat_words, n_cat_words, ch)) throw RuntimeError(g_err);
+        check(hipMemcpyAsync(out, c->rows, 4 * n, hipMemcpyDeviceToHost, c->stream), "download");
+        c->sync();
+        *n_left = ch[0].len;
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,184 @@
+// fbhip_internal.h -- device-side structures shared by the kernels
+// (fbhip_kernels.hip) and the context that launches them (fbhip_ctx.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fbh {
+
+constexpr int HIST_TPB = 256;      // threads of one histogram workgroup
+constexpr int SPLIT_TPB = 256;     // threads of one split-scan workgroup
+constexpr int PART_TPB = 256;      // threads of one partition workgroup
+constexpr int PART_CHUNK = 2048;   // rows of one partition chunk (8 per thread)
+constexpr int XCDS = 8;            // MI355X accelerator complex dies
+constexpr uint32_t NO_SLOT = 0xFFFFFFFFu;
+
+// One histogram tile: a group of features of one width stored as row
+// records, record i at data + i * stride, feature k of the tile at byte
+// k * width of the record. A tile's histogram fits the LDS tile budget.
+struct TileDev {
+    const uint8_t *data;
+    uint32_t stride;     // bytes per record (multiple of 4)
+    uint32_t width;      // 1 or 2
+    uint32_t n_feat;     // features in the record
+    uint32_t feat_base;  // first entry of this tile in the TileFeatDev table
+    uint32_t lds_slots;  // LDS histogram slots of the tile's active features
+    uint32_t pad;
+};
+
+// Per-feature entry of a tile for one tree.
+struct TileFeatDev {
+    uint32_t n_bins;    // 0 when the feature is not built this tree
+    uint32_t lds_off;   // first LDS slot of the feature
+    uint32_t hist_off;  // first slot of the feature in a node histogram
+    uint32_t pad;
+};
+
+// One node of a histogram batch.
+struct HistNodeDev {
+    uint32_t row_off;
+    uint32_t row_len;
+    uint32_t chunk_begin;  // first chunk of the node in the launch
+    uint32_t slot;         // output histogram slot
+    uint32_t n_chunks;
+    uint32_t pad[3];
+};
+
+struct HistLaunch {
+    const TileDev *tiles;      // tiles of this launch (same width / record size)
+    const TileFeatDev *feats;
+    uint32_t n_tiles;
+    const HistNodeDev *nodes;
+    uint32_t n_nodes;
+    uint32_t n_chunks;
+    uint32_t chunk_rows;
+    uint32_t chunk_groups;     // ceil(n_chunks / XCDS)
+    const uint32_t *rows;      // row arena
+    const int64_t *gpair;      // [n_rows][2]
+    int64_t *hist;             // [slots][hist_width][2]
+    uint64_t hist_width;
+};
+
+// Per-tree feature table of the split scan (compact histogram order).
+struct SplitFeatDev {
+    uint32_t feat;       // global feature id
+    uint32_t hist_off;
+    uint32_t n_bins;
+    int32_t monotone;
+    uint32_t categorical;
+    uint32_t cat_words;  // 64-bit words of the feature's category set
+    uint32_t cat_base;   // word offset of the feature's set within a node's set scratch
+    uint32_t pad;
+};
+
+struct SplitNodeDev {
+    int64_t sum_g, sum_h;
+    float lower, upper;
+    uint32_t slot;
+    uint32_t pad;
+};
+
+struct SplitParamsDev {
+    double inv_g, inv_h;  // inverse quantizer scales
+    float lambda_, gamma, mcw, alpha, mds;
+    uint32_t max_cat_to_onehot, max_cat_threshold;
+    uint32_t n_feats;     // features of the tree
+    uint32_t cat_words_per_node;
+    uint32_t pad;
+};
+
+// Best candidate of one (node, feature).
+struct FeatCandDev {
+    float gain;
+    uint32_t found;
+    uint32_t bin;
+    uint32_t missing_left;
+    int64_t left_g, left_h;
+};
+
+// Packet of one node (layout of fbh_split).
+struct SplitPacketDev {
+    uint32_t found, feat, bin, missing_left;
+    float gain;
+    uint32_t is_cat, cat_offset, n_cat_words;
+    int64_t left[2];
+    int64_t right[2];
+};
+
+struct PartReqDev {
+    uint32_t row_off, row_len;
+    uint32_t chunk_begin, n_chunks;
+    const uint8_t *data;   // tile records of the split feature
+    uint32_t stride, byte_off, width;
+    uint32_t bin, missing_left;
+    uint32_t cat_off, n_cat_words;
+    uint32_t pad;
+};
+
+struct LeafDev {
+    uint32_t row_off, row_len, chunk_begin;
+    float value;
+};
+
+// Flattened ensemble for TreeSHAP.
+struct ShapNodeDev {
+    uint32_t feat;
+    float split_cond;
+    int32_t left, right;   // global node ids, -1 for leaves
+    float leaf_value;
+    float left_weight, right_weight;  // branch_weight of each child
+    uint32_t flags;        // bit 0 leaf, bit 1 default_left, bit 2 categorical
+    uint32_t cat_offset, cat_len;
+    uint32_t uslot;        // slot of the node's feature in its tree's unique list
+    uint32_t pad;
+};
+
+// Last-error message shared by every fbh_* entry point (thread local).
+void set_last_error(const char *msg);
+const char *last_error();
+
+// ---------------------------------------------------------------- launchers
+hipError_t launch_hist(const HistLaunch &L, int width, int rec_dwords, size_t lds_bytes,
+                       hipStream_t s);
+hipError_t launch_hist_global(const HistLaunch &L, int width, hipStream_t s);
+hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slots, uint32_t n,
+                             hipStream_t s);
+hipError_t launch_subtract(int64_t *hist, uint64_t width, const uint32_t *triples, uint32_t n,
+                           hipStream_t s);
+hipError_t launch_split_feats(const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
+                              uint32_t n_nodes, const SplitFeatDev *feats, const uint8_t *enabled,
+                              SplitParamsDev P, FeatCandDev *cands, uint64_t *cat_scratch,
+                              hipStream_t s);
+hipError_t launch_split_nodes(const FeatCandDev *cands, const SplitFeatDev *feats,
+                              uint32_t n_nodes, SplitParamsDev P, const SplitNodeDev *nodes,
+                              const uint64_t *cat_scratch, SplitPacketDev *out,
+                              uint64_t *cat_out, uint32_t cat_out_words, hipStream_t s);
+hipError_t launch_partition(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
+                            uint32_t *rows, uint32_t *tmp, uint8_t *flags, uint32_t *chunk_counts,
+                            uint32_t *chunk_offsets, uint32_t *totals, const uint64_t *cat_words,
+                            hipStream_t s);
+hipError_t launch_assign_leaves(const LeafDev *leaves, uint32_t n_leaves, uint32_t n_chunks,
+                                const uint32_t *rows, float *delta, hipStream_t s);
+hipError_t launch_init_rows(uint32_t *rows, float *delta, uint64_t n, hipStream_t s);
+hipError_t launch_gpair_maxabs(float *g2n, uint64_t n, uint64_t threshold, uint64_t seed,
+                               uint64_t tree, double *block_max, uint32_t n_blocks,
+                               double *out_max, hipStream_t s);
+hipError_t launch_gpair_quantize(const float *g2n, uint64_t n, double scale_g, double scale_h,
+                                 int64_t *out, int64_t *block_sum, uint32_t n_blocks,
+                                 int64_t *out_sum, hipStream_t s);
+hipError_t launch_pack_feature(const uint8_t *col, uint64_t n_rows, uint32_t width, uint8_t *tile,
+                               uint32_t stride, uint32_t byte_off, hipStream_t s);
+
+// Categories the device split scan sorts in LDS (weights + order, 32 KiB).
+constexpr uint32_t MAX_DEVICE_CATS = 4096;
+// Distinct split features of one tree the TreeSHAP kernel accepts.
+constexpr uint32_t MAX_SHAP_UNIQUE = 1024;
+hipError_t launch_shap(const ShapNodeDev *nodes, const uint32_t *tree_roots, uint32_t n_trees,
+                       const uint32_t *tree_ufeat_off, const uint32_t *ufeats,
+                       const uint32_t *cat_words, const float *rule, const float *rows,
+                       uint64_t n_rows, uint32_t n_features, const float *margin, float bias,
+                       float root_mean, float *out, uint32_t max_unique, uint32_t max_depth,
+                       hipStream_t s);
+
+}  // namespace fbh

@@ -1,0 +1,1258 @@
+// fbhip_kernels.hip -- CDNA4 (gfx950) kernels of the training and explanation
+// backend. Built with -ffp-contract=off and correctly rounded f32 division so
+// every floating-point step rounds exactly like the host engine.
+//
+// Kernels:
+//   hist_kernel          fixed-point gradient histograms, LDS-privatised per
+//                        tile, batched over the nodes of a level
+//                        (reference: histogram.cu:1685-1852)
+//   subtract_kernel      sibling subtraction (hist.rs:391-400)
+//   split_feat_kernel    split-gain scan of one (node, feature)
+//                        (split.rs:331-617, histogram.cu:250-510)
+//   split_node_kernel    per-node argmax over features (split.rs:631-642)
+//   part_*_kernel        stable row partition (mod.rs:5169-5430,
+//                        histogram.cu:2029-2395)
+//   leaf_kernel          leaf value scatter into the prediction delta
+//                        (histogram.cu:2397-2441)
+//   gpair_*_kernel       device quantisation (histogram.cu:1079-1177)
+//   shap_kernel          QuadratureTreeSHAP (explain.rs:303-401, 704-728)
+
+#include "fbhip_internal.h"
+
+#include <math.h>
+
+#include <algorithm>
+
+namespace fbh {
+
+// ======================================================================
+// histogram
+// ======================================================================
+
+template <int RD>
+__device__ __forceinline__ void load_record(const uint8_t *p, uint32_t (&r)[RD]) {
+    if constexpr (RD % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < RD / 4; q++) {
+            uint4 v = reinterpret_cast<const uint4 *>(p)[q];
+            r[4 * q + 0] = v.x;
+            r[4 * q + 1] = v.y;
+            r[4 * q + 2] = v.z;
+            r[4 * q + 3] = v.w;
+        }
+    } else if constexpr (RD % 2 == 0) {
+#pragma unroll
+        for (int q = 0; q < RD / 2; q++) {
+            uint2 v = reinterpret_cast<const uint2 *>(p)[q];
+            r[2 * q + 0] = v.x;
+            r[2 * q + 1] = v.y;
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < RD; q++) r[q] = reinterpret_cast<const uint32_t *>(p)[q];
+    }
+}
+
+__device__ __forceinline__ void lds_add_u64(unsigned long long *p, unsigned long long v) {
+    __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void global_add_u64(unsigned long long *p, unsigned long long v) {
+    __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One workgroup accumulates one chunk of one node's rows into the LDS
+// histogram of one tile, then merges it into the node's histogram slot:
+// a plain store when the node has a single chunk, 64-bit global atomics
+// otherwise. Fixed-point addition is exact and order independent, so the
+// result equals the host engine's bit for bit.
+//
+// Workgroup -> (chunk, tile) is XCD aware: workgroups are dispatched
+// round-robin over the 8 XCDs, and every tile of chunk c runs on XCD c % 8,
+// so the chunk's row ids and gradient pairs are fetched from HBM once into
+// that XCD's L2 and re-read from there by the other tiles.
+template <int W, int RD, int UNROLL>
+__global__ __launch_bounds__(HIST_TPB) void hist_kernel(const HistLaunch L) {
+    extern __shared__ unsigned long long lds[];
+    constexpr int FPD = 4 / W;
+    constexpr int NF = RD * FPD;
+    constexpr uint32_t MASK = W == 1 ? 0xFFu : 0xFFFFu;
+
+    const uint32_t b = blockIdx.x;
+    const uint32_t xcd = b % XCDS;
+    const uint32_t k = b / XCDS;
+    const uint32_t tile_i = k % L.n_tiles;
+    const uint32_t chunk = (k / L.n_tiles) * XCDS + xcd;
+    if (chunk >= L.n_chunks) return;
+    const TileDev T = L.tiles[tile_i];
+
+    uint32_t lo = 0, hi = L.n_nodes;
+    while (hi - lo > 1) {
+        uint32_t mid = (lo + hi) >> 1;
+        if (L.nodes[mid].chunk_begin <= chunk) lo = mid;
+        else hi = mid;
+    }
+    const HistNodeDev N = L.nodes[lo];
+    const uint32_t r0 = (chunk - N.chunk_begin) * L.chunk_rows;
+    const uint32_t r1 = min(r0 + L.chunk_rows, N.row_len);
+
+    uint32_t nb[NF], loff[NF];
+#pragma unroll
+    for (int fi = 0; fi < NF; fi++) {
+        if (fi < (int)T.n_feat) {
+            const TileFeatDev F = L.feats[T.feat_base + fi];
+            nb[fi] = F.n_bins;
+            loff[fi] = F.lds_off;
+        } else {
+            nb[fi] = 0;
+            loff[fi] = 0;
+        }
+    }
+
+    const uint32_t tid = threadIdx.x;
+    for (uint32_t i = tid; i < 2 * T.lds_slots; i += HIST_TPB) lds[i] = 0ull;
+    __syncthreads();
+
+    const uint32_t *rows = L.rows + N.row_off;
+    const longlong2 *gp = reinterpret_cast<const longlong2 *>(L.gpair);
+    for (uint32_t i = r0 + tid; i < r1; i += HIST_TPB * UNROLL) {
+        uint32_t row[UNROLL];
+        bool ok[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; u++) {
+            const uint32_t idx = i + u * HIST_TPB;
+            ok[u] = idx < r1;
+            row[u] = ok[u] ? rows[idx] : 0u;
+        }
+        longlong2 g[UNROLL];
+        uint32_t rec[UNROLL][RD];
+#pragma unroll
+        for (int u = 0; u < UNROLL; u++) {
+            if (ok[u]) {
+                g[u] = gp[row[u]];
+                load_record<RD>(T.data + (size_t)row[u] * T.stride, rec[u]);
+            } else {
+                g[u] = make_longlong2(0, 0);
+#pragma unroll
+                for (int d = 0; d < RD; d++) rec[u][d] = 0u;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; u++) {
+            // Rows whose pair is zero (sampled out, zero weight) add nothing.
+            if ((g[u].x | g[u].y) == 0) continue;
+            const unsigned long long gg = (unsigned long long)g[u].x;
+            const unsigned long long hh = (unsigned long long)g[u].y;
+#pragma unroll
+            for (int d = 0; d < RD; d++) {
+#pragma unroll
+                for (int q = 0; q < FPD; q++) {
+                    const int fi = d * FPD + q;
+                    const uint32_t bin = (rec[u][d] >> (q * 8 * W)) & MASK;
+                    // Missing (all ones) and unseen-category codes are >= n_bins,
+                    // and features not built this tree have n_bins == 0.
+                    if (bin < nb[fi]) {
+                        unsigned long long *slot = lds + 2u * (loff[fi] + bin);
+                        lds_add_u64(slot, gg);
+                        lds_add_u64(slot + 1, hh);
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    int64_t *out = L.hist + (uint64_t)N.slot * L.hist_width * 2u;
+    const bool single = N.n_chunks == 1;
+    for (uint32_t fi = 0; fi < T.n_feat; fi++) {
+        const TileFeatDev F = L.feats[T.feat_base + fi];
+        for (uint32_t bin = tid; bin < F.n_bins; bin += HIST_TPB) {
+            const unsigned long long gg = lds[2u * (F.lds_off + bin)];
+            const unsigned long long hh = lds[2u * (F.lds_off + bin) + 1];
+            unsigned long long *dst =
+                reinterpret_cast<unsigned long long *>(out + 2u * (F.hist_off + bin));
+            if (single) {
+                dst[0] = gg;
+                dst[1] = hh;
+            } else if ((gg | hh) != 0ull) {
+                global_add_u64(dst, gg);
+                global_add_u64(dst + 1, hh);
+            }
+        }
+    }
+}
+
+// A feature whose histogram does not fit an LDS tile (wide 16-bit bins)
+// accumulates straight into the node's zeroed histogram with 64-bit global
+// atomics; each tile of this kind holds one feature.
+template <int W>
+__global__ __launch_bounds__(HIST_TPB) void hist_global_kernel(const HistLaunch L) {
+    const uint32_t b = blockIdx.x;
+    const uint32_t xcd = b % XCDS;
+    const uint32_t k = b / XCDS;
+    const uint32_t tile_i = k % L.n_tiles;
+    const uint32_t chunk = (k / L.n_tiles) * XCDS + xcd;
+    if (chunk >= L.n_chunks) return;
+    const TileDev T = L.tiles[tile_i];
+    const TileFeatDev F = L.feats[T.feat_base];
+    if (F.n_bins == 0) return;
+    uint32_t lo = 0, hi = L.n_nodes;
+    while (hi - lo > 1) {
+        uint32_t mid = (lo + hi) >> 1;
+        if (L.nodes[mid].chunk_begin <= chunk) lo = mid;
+        else hi = mid;
+    }
+    const HistNodeDev N = L.nodes[lo];
+    const uint32_t r0 = (chunk - N.chunk_begin) * L.chunk_rows;
+    const uint32_t r1 = min(r0 + L.chunk_rows, N.row_len);
+    unsigned long long *out = reinterpret_cast<unsigned long long *>(
+        L.hist + ((uint64_t)N.slot * L.hist_width + F.hist_off) * 2u);
+    const uint32_t *rows = L.rows + N.row_off;
+    const longlong2 *gp = reinterpret_cast<const longlong2 *>(L.gpair);
+    for (uint32_t i = r0 + threadIdx.x; i < r1; i += HIST_TPB) {
+        const uint32_t row = rows[i];
+        const longlong2 g = gp[row];
+        if ((g.x | g.y) == 0) continue;
+        const uint8_t *p = T.data + (size_t)row * T.stride;
+        const uint32_t bin = W == 1 ? (uint32_t)p[0] : (uint32_t)*reinterpret_cast<const uint16_t *>(p);
+        if (bin < F.n_bins) {
+            global_add_u64(out + 2u * bin, (unsigned long long)g.x);
+            global_add_u64(out + 2u * bin + 1, (unsigned long long)g.y);
+        }
+    }
+}
+
+hipError_t launch_hist_global(const HistLaunch &L, int width, hipStream_t s) {
+    const uint32_t blocks = L.chunk_groups * XCDS * L.n_tiles;
+    if (blocks == 0) return hipSuccess;
+    if (width == 1)
+        hipLaunchKernelGGL(hist_global_kernel<1>, dim3(blocks), dim3(HIST_TPB), 0, s, L);
+    else
+        hipLaunchKernelGGL(hist_global_kernel<2>, dim3(blocks), dim3(HIST_TPB), 0, s, L);
+    return hipGetLastError();
+}
+
+template <int W, int RD>
+static hipError_t launch_hist_t(const HistLaunch &L, size_t lds, hipStream_t s) {
+    const uint32_t blocks = L.chunk_groups * XCDS * L.n_tiles;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL((hist_kernel<W, RD, 4>), dim3(blocks), dim3(HIST_TPB), lds, s, L);
+    return hipGetLastError();
+}
+
+hipError_t launch_hist(const HistLaunch &L, int width, int rd, size_t lds, hipStream_t s) {
+#define FBH_HIST_CASE(WW, R) \
+    if (width == WW && rd == R) return launch_hist_t<WW, R>(L, lds, s);
+    FBH_HIST_CASE(1, 1) FBH_HIST_CASE(1, 2) FBH_HIST_CASE(1, 3) FBH_HIST_CASE(1, 4)
+    FBH_HIST_CASE(1, 8) FBH_HIST_CASE(1, 12) FBH_HIST_CASE(1, 16)
+    FBH_HIST_CASE(2, 1) FBH_HIST_CASE(2, 2) FBH_HIST_CASE(2, 3) FBH_HIST_CASE(2, 4)
+    FBH_HIST_CASE(2, 8) FBH_HIST_CASE(2, 12) FBH_HIST_CASE(2, 16)
+#undef FBH_HIST_CASE
+    return hipErrorInvalidValue;
+}
+
+// Zero whole histogram slots before atomic accumulation.
+__global__ void zero_slots_kernel(int64_t *hist, uint64_t width, const uint32_t *slots) {
+    int64_t *base = hist + (uint64_t)slots[blockIdx.y] * width * 2u;
+    const uint64_t n = width * 2u;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        base[i] = 0;
+}
+
+hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slots, uint32_t n,
+                             hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    uint32_t bx = (uint32_t)std::min<uint64_t>((width * 2 + 255) / 256, 1024);
+    hipLaunchKernelGGL(zero_slots_kernel, dim3(bx, n), dim3(256), 0, s, hist, width, slots);
+    return hipGetLastError();
+}
+
+// dst = parent - sibling, elementwise wrapping i64 (triples: dst, parent, sibling).
+__global__ void subtract_kernel(int64_t *hist, uint64_t width, const uint32_t *triples) {
+    const uint32_t *t = triples + 3u * blockIdx.y;
+    uint64_t *dst = reinterpret_cast<uint64_t *>(hist + (uint64_t)t[0] * width * 2u);
+    const uint64_t *par = reinterpret_cast<const uint64_t *>(hist + (uint64_t)t[1] * width * 2u);
+    const uint64_t *sib = reinterpret_cast<const uint64_t *>(hist + (uint64_t)t[2] * width * 2u);
+    const uint64_t n = width * 2u;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        dst[i] = par[i] - sib[i];
+}
+
+hipError_t launch_subtract(int64_t *hist, uint64_t width, const uint32_t *triples, uint32_t n,
+                           hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    uint32_t bx = (uint32_t)std::min<uint64_t>((width * 2 + 255) / 256, 1024);
+    hipLaunchKernelGGL(subtract_kernel, dim3(bx, n), dim3(256), 0, s, hist, width, triples);
+    return hipGetLastError();
+}
+
+// ======================================================================
+// split scan
+// ======================================================================
+
+constexpr float MIN_GAIN_EPS = 1e-6f;
+
+__device__ __forceinline__ double threshold_l1(double g, float alpha) {
+    const double a = (double)alpha;
+    if (g > a) return g - a;
+    if (g < -a) return g + a;
+    return 0.0;
+}
+
+// XGBoost CalcWeight, as split.rs:182-192.
+__device__ __forceinline__ float xgb_weight(double g, double h, const SplitParamsDev &P) {
+    if (h <= 0.0) return 0.0f;
+    double dw = -threshold_l1(g, P.alpha) / (h + (double)P.lambda_);
+    if (P.mds != 0.0f && fabs(dw) > (double)P.mds) dw = copysign((double)P.mds, dw);
+    return (float)dw;
+}
+
+__device__ __forceinline__ float apply_bounds(float w, float lo, float hi) {
+    if (w < lo) return lo;
+    if (w > hi) return hi;
+    return w;
+}
+
+// CalcGainGivenWeight, as split.rs:210-218.
+__device__ __forceinline__ float gain_given_weight(double g, double h, float w,
+                                                   const SplitParamsDev &P) {
+    if (h <= 0.0) return 0.0f;
+    const float w2 = w * w;
+    const double square = (double)w2;
+    const double l1 = 2.0 * (double)P.alpha * (double)fabsf(w);
+    const double a = 2.0 * g * (double)w;
+    const double b = (h + (double)P.lambda_) * square;
+    return (float)(-((a + b) + l1));
+}
+
+// bounded_split_gain (split.rs:226-252). Returns false when invalid.
+__device__ __forceinline__ bool candidate_gain(int64_t lg_i, int64_t lh_i, int64_t rg_i,
+                                               int64_t rh_i, float parent, int mono, float lo,
+                                               float hi, const SplitParamsDev &P, float &out) {
+    const double lg = (double)lg_i * P.inv_g, lh = (double)lh_i * P.inv_h;
+    const double rg = (double)rg_i * P.inv_g, rh = (double)rh_i * P.inv_h;
+    const double mcw = (double)P.mcw;
+    if (!(lh > 0.0 && rh > 0.0 && lh >= mcw && rh >= mcw)) return false;
+    const float wl = apply_bounds(xgb_weight(lg, lh, P), lo, hi);
+    const float wr = apply_bounds(xgb_weight(rg, rh, P), lo, hi);
+    if ((mono > 0 && wl > wr) || (mono < 0 && wl < wr)) return false;
+    const float gain = gain_given_weight(lg, lh, wl, P) + gain_given_weight(rg, rh, wr, P);
+    const float loss = gain - parent;
+    out = (float)((double)loss - (double)P.gamma);
+    return true;
+}
+
+struct Best {
+    float gain;
+    uint32_t ord;
+    uint32_t found;
+    int64_t lg, lh;
+};
+
+__device__ __forceinline__ bool better(const Best &a, const Best &b) {
+    if (!a.found) return false;
+    if (!b.found) return true;
+    if (a.gain > b.gain) return true;
+    return a.gain == b.gain && a.ord < b.ord;
+}
+
+__device__ __forceinline__ void offer(Best &best, float gain, uint32_t ord, int64_t lg,
+                                      int64_t lh) {
+    // update_best: strict greater than the eps floor and the current best.
+    if (!(gain > MIN_GAIN_EPS)) return;
+    if (!best.found || gain > best.gain || (gain == best.gain && ord < best.ord)) {
+        best.found = 1;
+        best.gain = gain;
+        best.ord = ord;
+        best.lg = lg;
+        best.lh = lh;
+    }
+}
+
+__device__ Best block_best(Best mine, Best *sh) {
+    const uint32_t tid = threadIdx.x;
+    sh[tid] = mine;
+    __syncthreads();
+    for (uint32_t s = SPLIT_TPB / 2; s > 0; s >>= 1) {
+        if (tid < s && better(sh[tid + s], sh[tid])) sh[tid] = sh[tid + s];
+        __syncthreads();
+    }
+    Best r = sh[0];
+    __syncthreads();
+    return r;
+}
+
+// Inclusive block scan of (g, h) pairs; returns the exclusive prefix of this
+// thread and the block total.
+__device__ void block_scan_pairs(int64_t g, int64_t h, int64_t *sg, int64_t *shh, int64_t &eg,
+                                 int64_t &eh, int64_t &tg, int64_t &th) {
+    const uint32_t tid = threadIdx.x;
+    sg[tid] = g;
+    shh[tid] = h;
+    __syncthreads();
+    for (uint32_t off = 1; off < SPLIT_TPB; off <<= 1) {
+        int64_t ag = 0, ah = 0;
+        if (tid >= off) {
+            ag = sg[tid - off];
+            ah = shh[tid - off];
+        }
+        __syncthreads();
+        sg[tid] = (int64_t)((uint64_t)sg[tid] + (uint64_t)ag);
+        shh[tid] = (int64_t)((uint64_t)shh[tid] + (uint64_t)ah);
+        __syncthreads();
+    }
+    eg = (int64_t)((uint64_t)sg[tid] - (uint64_t)g);
+    eh = (int64_t)((uint64_t)shh[tid] - (uint64_t)h);
+    tg = sg[SPLIT_TPB - 1];
+    th = shh[SPLIT_TPB - 1];
+    __syncthreads();
+}
+
+__device__ __forceinline__ int64_t wadd(int64_t a, int64_t b) {
+    return (int64_t)((uint64_t)a + (uint64_t)b);
+}
+__device__ __forceinline__ int64_t wsub(int64_t a, int64_t b) {
+    return (int64_t)((uint64_t)a - (uint64_t)b);
+}
+
+// Categorical enumeration of one (node, feature): enumerate_categorical
+// (split.rs:484-617). One-hot below max_cat_to_onehot, otherwise a stable
+// sort of the categories by weight and prefix scans of at most
+// max_cat_threshold - 1 categories per direction.
+__device__ void split_categorical(const int64_t *h, uint32_t n, const SplitNodeDev &N,
+                                  float parent, int mono, const SplitParamsDev &P, Best *shb,
+                                  int64_t *sg, int64_t *shh, float *wts, uint32_t *order,
+                                  uint64_t *set_out, uint32_t set_words, FeatCandDev *outc) {
+    const uint32_t tid = threadIdx.x;
+    int64_t tg = 0, th = 0;
+    for (uint32_t i = tid; i < n; i += SPLIT_TPB) {
+        tg = wadd(tg, h[2 * i]);
+        th = wadd(th, h[2 * i + 1]);
+    }
+    int64_t eg, eh, totg, toth;
+    block_scan_pairs(tg, th, sg, shh, eg, eh, totg, toth);
+    const int64_t mg = wsub(N.sum_g, totg), mh = wsub(N.sum_h, toth);  // missing rows
+
+    for (uint32_t w = tid; w < set_words; w += SPLIT_TPB) set_out[w] = 0ull;
+    Best best{0.0f, 0u, 0u, 0, 0};
+    uint32_t at = 0;
+    uint32_t ml = 0;
+    if ((uint64_t)n < (uint64_t)P.max_cat_to_onehot) {
+        for (uint32_t i = tid; i < n; i += SPLIT_TPB) {
+            const int64_t bg = h[2 * i], bh = h[2 * i + 1];
+            float gain;
+            // Missing rows with the other categories.
+            if (candidate_gain(wsub(N.sum_g, bg), wsub(N.sum_h, bh), bg, bh, parent, mono,
+                               N.lower, N.upper, P, gain))
+                offer(best, gain, 2 * i, wsub(N.sum_g, bg), wsub(N.sum_h, bh));
+            // Missing rows with the chosen category.
+            const int64_t rg = wadd(bg, mg), rh = wadd(bh, mh);
+            if (candidate_gain(wsub(N.sum_g, rg), wsub(N.sum_h, rh), rg, rh, parent, mono,
+                               N.lower, N.upper, P, gain))
+                offer(best, gain, 2 * i + 1, wsub(N.sum_g, rg), wsub(N.sum_h, rh));
+        }
+        best = block_best(best, shb);
+        if (best.found) {
+            at = best.ord >> 1;
+            ml = (best.ord & 1) ? 0u : 1u;
+        }
+        __syncthreads();
+        if (tid == 0 && best.found) set_out[at >> 6] |= 1ull << (at & 63);
+    } else {
+        for (uint32_t i = tid; i < n; i += SPLIT_TPB) {
+            const double g = (double)h[2 * i] * P.inv_g, hh = (double)h[2 * i + 1] * P.inv_h;
+            wts[i] = xgb_weight(g, hh, P);
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < n; i += SPLIT_TPB) order[i] = i;
+        __syncthreads();
+        // Stable ascending rank by `<` (std::stable_sort / sort_by partial_cmp).
+        for (uint32_t i = tid; i < n; i += SPLIT_TPB) {
+            const float wi = wts[i];
+            uint32_t r = 0;
+            for (uint32_t j = 0; j < n; j++) {
+                const float wj = wts[j];
+                r += (wj < wi) || (j < i && !(wi < wj) && !(wj < wi));
+            }
+            if (r < n) order[r] = i;
+        }
+        __syncthreads();
+        const uint32_t n_scan = min(P.max_cat_threshold, n);
+        if (tid == 0 && n_scan >= 2) {
+            Best fwd{0.0f, 0u, 0u, 0, 0}, bwd{0.0f, 0u, 0u, 0, 0};
+            int64_t rg = 0, rh = 0;
+            for (uint32_t kk = 0; kk + 1 < n_scan; kk++) {
+                rg = wadd(rg, h[2 * order[kk]]);
+                rh = wadd(rh, h[2 * order[kk] + 1]);
+                float gain;
+                const int64_t lg = wsub(N.sum_g, rg), lh = wsub(N.sum_h, rh);
+                if (candidate_gain(lg, lh, rg, rh, parent, mono, N.lower, N.upper, P, gain))
+                    if (gain > MIN_GAIN_EPS && (!fwd.found || gain > fwd.gain))
+                        fwd = Best{gain, kk + 1, 1u, lg, lh};
+            }
+            int64_t lg = 0, lh = 0;
+            for (uint32_t j = n; j-- > n - (n_scan - 1);) {
+                lg = wadd(lg, h[2 * order[j]]);
+                lh = wadd(lh, h[2 * order[j] + 1]);
+                float gain;
+                const int64_t rg2 = wsub(N.sum_g, lg), rh2 = wsub(N.sum_h, lh);
+                if (candidate_gain(lg, lh, rg2, rh2, parent, mono, N.lower, N.upper, P, gain))
+                    if (gain > MIN_GAIN_EPS && (!bwd.found || gain > bwd.gain))
+                        bwd = Best{gain, j, 1u, lg, lh};
+            }
+            Best win = fwd;
+            uint32_t win_ml = 1;
+            if (bwd.found && (!win.found || bwd.gain > win.gain)) {
+                win = bwd;
+                win_ml = 0;
+            }
+            shb[0] = win;
+            sg[0] = win_ml;
+        }
+        __syncthreads();
+        best = shb[0];
+        ml = (uint32_t)sg[0];
+        at = best.ord;
+        __syncthreads();
+        if (best.found && tid == 0)
+            for (uint32_t kk = 0; kk < at; kk++) set_out[order[kk] >> 6] |= 1ull << (order[kk] & 63);
+    }
+    if (tid == 0) {
+        outc->found = best.found;
+        outc->gain = best.gain;
+        outc->bin = 0;
+        outc->missing_left = ml;
+        outc->left_g = best.lg;
+        outc->left_h = best.lh;
+    }
+}
+
+// One workgroup per (feature, node): prefix sums of the feature's bins, the
+// forward (missing right) and reverse (missing left, only when the node has
+// missing mass) candidates, and the first best by the reference's rules.
+__global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
+    const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
+    const SplitFeatDev *feats, const uint8_t *enabled, SplitParamsDev P, FeatCandDev *cands,
+    uint64_t *cat_scratch) {
+    __shared__ Best shb[SPLIT_TPB];
+    __shared__ int64_t sg[SPLIT_TPB], shh[SPLIT_TPB];
+    extern __shared__ unsigned char dyn[];
+
+    const uint32_t j = blockIdx.x, ni = blockIdx.y, tid = threadIdx.x;
+    const SplitFeatDev F = feats[j];
+    const SplitNodeDev N = nodes[ni];
+    FeatCandDev *outc = cands + (size_t)ni * P.n_feats + j;
+    if (enabled && !enabled[(size_t)ni * P.n_feats + j]) {
+        if (tid == 0) outc->found = 0;
+        return;
+    }
+    const int64_t *h = hist + ((uint64_t)N.slot * hist_width + F.hist_off) * 2u;
+    const double ng = (double)N.sum_g * P.inv_g, nh = (double)N.sum_h * P.inv_h;
+    const float parent = gain_given_weight(ng, nh, apply_bounds(xgb_weight(ng, nh, P), N.lower,
+                                                                N.upper), P);
+    const uint32_t n = F.n_bins;
+
+    if (F.categorical) {
+        float *wts = reinterpret_cast<float *>(dyn);
+        uint32_t *order = reinterpret_cast<uint32_t *>(dyn + sizeof(float) * MAX_DEVICE_CATS);
+        uint64_t *set = cat_scratch + (size_t)ni * P.cat_words_per_node + F.cat_base;
+        split_categorical(h, n, N, parent, F.monotone, P, shb, sg, shh, wts, order, set,
+                          F.cat_words, outc);
+        return;
+    }
+
+    const uint32_t per = (n + SPLIT_TPB - 1) / SPLIT_TPB;
+    const uint32_t b0 = min(tid * per, n), b1 = min(b0 + per, n);
+    int64_t tg = 0, th = 0;
+    for (uint32_t bb = b0; bb < b1; bb++) {
+        tg = wadd(tg, h[2 * bb]);
+        th = wadd(th, h[2 * bb + 1]);
+    }
+    int64_t eg, eh, totg, toth;
+    block_scan_pairs(tg, th, sg, shh, eg, eh, totg, toth);
+
+    Best best{0.0f, 0u, 0u, 0, 0};
+    const int mono = F.monotone;
+    // Forward: missing rows go right.
+    int64_t lg = eg, lh = eh;
+    for (uint32_t bb = b0; bb < b1; bb++) {
+        lg = wadd(lg, h[2 * bb]);
+        lh = wadd(lh, h[2 * bb + 1]);
+        float gain;
+        if (candidate_gain(lg, lh, wsub(N.sum_g, lg), wsub(N.sum_h, lh), parent, mono, N.lower,
+                           N.upper, P, gain))
+            offer(best, gain, bb, lg, lh);
+    }
+    // Reverse: missing rows go left; skipped when the bins hold the whole node.
+    if (!(totg == N.sum_g && toth == N.sum_h)) {
+        // Sum of the bins after this thread's range.
+        int64_t rg = wsub(wsub(totg, eg), tg), rh = wsub(wsub(toth, eh), th);
+        for (uint32_t bb = b1; bb-- > b0;) {
+            rg = wadd(rg, h[2 * bb]);
+            rh = wadd(rh, h[2 * bb + 1]);
+            const int64_t l2g = wsub(N.sum_g, rg), l2h = wsub(N.sum_h, rh);
+            float gain;
+            if (candidate_gain(l2g, l2h, rg, rh, parent, mono, N.lower, N.upper, P, gain))
+                offer(best, gain, n + (n - 1 - bb), l2g, l2h);
+        }
+    }
+    best = block_best(best, shb);
+    if (tid == 0) {
+        outc->found = best.found;
+        outc->gain = best.gain;
+        if (best.ord < n) {
+            outc->bin = best.ord + 1;
+            outc->missing_left = 0;
+        } else {
+            outc->bin = n - 1 - (best.ord - n);
+            outc->missing_left = 1;
+        }
+        outc->left_g = best.lg;
+        outc->left_h = best.lh;
+    }
+}
+
+hipError_t launch_split_feats(const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
+                              uint32_t n_nodes, const SplitFeatDev *feats, const uint8_t *enabled,
+                              SplitParamsDev P, FeatCandDev *cands, uint64_t *cat_scratch,
+                              hipStream_t s) {
+    if (n_nodes == 0 || P.n_feats == 0) return hipSuccess;
+    const size_t dyn = P.cat_words_per_node ? (sizeof(float) + sizeof(uint32_t)) * MAX_DEVICE_CATS
+                                            : 0;
+    hipLaunchKernelGGL(split_feat_kernel, dim3(P.n_feats, n_nodes), dim3(SPLIT_TPB), dyn, s, hist,
+                       hist_width, nodes, feats, enabled, P, cands, cat_scratch);
+    return hipGetLastError();
+}
+
+// Per node: the best feature by gain, ties to the lowest feature id
+// (features are in ascending global order), as reduce_best / update_best.
+__global__ __launch_bounds__(SPLIT_TPB) void split_node_kernel(
+    const FeatCandDev *cands, const SplitFeatDev *feats, SplitParamsDev P,
+    const SplitNodeDev *nodes, const uint64_t *cat_scratch, SplitPacketDev *out,
+    uint64_t *cat_out, uint32_t cat_out_words) {
+    __shared__ Best shb[SPLIT_TPB];
+    const uint32_t ni = blockIdx.x, tid = threadIdx.x;
+    const FeatCandDev *c = cands + (size_t)ni * P.n_feats;
+    Best best{0.0f, 0u, 0u, 0, 0};
+    for (uint32_t j = tid; j < P.n_feats; j += SPLIT_TPB) {
+        const FeatCandDev cj = c[j];
+        if (cj.found && (!best.found || cj.gain > best.gain)) {
+            best.found = 1;
+            best.gain = cj.gain;
+            best.ord = j;
+        }
+    }
+    best = block_best(best, shb);
+    if (tid == 0) {
+        SplitPacketDev pk;
+        pk.found = best.found;
+        pk.feat = 0;
+        pk.bin = 0;
+        pk.missing_left = 0;
+        pk.gain = 0.0f;
+        pk.is_cat = 0;
+        pk.cat_offset = ni * cat_out_words;
+        pk.n_cat_words = 0;
+        pk.left[0] = pk.left[1] = pk.right[0] = pk.right[1] = 0;
+        if (best.found) {
+            const FeatCandDev w = c[best.ord];
+            const SplitFeatDev F = feats[best.ord];
+            const SplitNodeDev N = nodes[ni];
+            pk.feat = F.feat;
+            pk.bin = w.bin;
+            pk.missing_left = w.missing_left;
+            pk.gain = w.gain;
+            pk.left[0] = w.left_g;
+            pk.left[1] = w.left_h;
+            pk.right[0] = wsub(N.sum_g, w.left_g);
+            pk.right[1] = wsub(N.sum_h, w.left_h);
+            if (F.categorical) {
+                pk.is_cat = 1;
+                pk.n_cat_words = F.cat_words;
+                const uint64_t *src = cat_scratch + (size_t)ni * P.cat_words_per_node + F.cat_base;
+                for (uint32_t k = 0; k < F.cat_words && k < cat_out_words; k++)
+                    cat_out[(size_t)ni * cat_out_words + k] = src[k];
+            }
+        }
+        out[ni] = pk;
+    }
+}
+
+hipError_t launch_split_nodes(const FeatCandDev *cands, const SplitFeatDev *feats,
+                              uint32_t n_nodes, SplitParamsDev P, const SplitNodeDev *nodes,
+                              const uint64_t *cat_scratch, SplitPacketDev *out,
+                              uint64_t *cat_out, uint32_t cat_out_words, hipStream_t s) {
+    if (n_nodes == 0) return hipSuccess;
+    hipLaunchKernelGGL(split_node_kernel, dim3(n_nodes), dim3(SPLIT_TPB), 0, s, cands, feats, P,
+                       nodes, cat_scratch, out, cat_out, cat_out_words);
+    return hipGetLastError();
+}
+
+// ======================================================================
+// stable partition
+// ======================================================================
+
+__device__ __forceinline__ uint32_t find_req(const PartReqDev *reqs, uint32_t n, uint32_t chunk) {
+    uint32_t lo = 0, hi = n;
+    while (hi - lo > 1) {
+        uint32_t mid = (lo + hi) >> 1;
+        if (reqs[mid].chunk_begin <= chunk) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+__device__ __forceinline__ bool goes_left(const PartReqDev &R, uint32_t row,
+                                          const uint64_t *cat_words) {
+    const uint8_t *p = R.data + (size_t)row * R.stride + R.byte_off;
+    const uint32_t bin = R.width == 1 ? (uint32_t)p[0] : (uint32_t) * reinterpret_cast<const uint16_t *>(p);
+    const uint32_t missing = R.width == 1 ? 0xFFu : 0xFFFFu;
+    if (bin == missing) return R.missing_left != 0;
+    if (R.n_cat_words) {
+        const uint32_t w = bin >> 6;
+        const bool in = w < R.n_cat_words && ((cat_words[R.cat_off + w] >> (bin & 63)) & 1ull);
+        return !in;
+    }
+    return bin < R.bin;
+}
+
+// Pass 1: direction flag per row and the left count of every chunk.
+__global__ __launch_bounds__(PART_TPB) void part_count_kernel(const PartReqDev *reqs,
+                                                              uint32_t n_reqs,
+                                                              const uint32_t *rows,
+                                                              uint8_t *flags, uint32_t *counts,
+                                                              const uint64_t *cat_words) {
+    __shared__ uint32_t wave_sum[PART_TPB / 64];
+    const uint32_t chunk = blockIdx.x;
+    const PartReqDev R = reqs[find_req(reqs, n_reqs, chunk)];
+    const uint32_t c0 = (chunk - R.chunk_begin) * PART_CHUNK;
+    const uint32_t c1 = min(c0 + PART_CHUNK, R.row_len);
+    uint32_t cnt = 0;
+    for (uint32_t i = c0 + threadIdx.x; i < c1; i += PART_TPB) {
+        const uint32_t pos = R.row_off + i;
+        const bool gl = goes_left(R, rows[pos], cat_words);
+        flags[pos] = gl ? 1 : 0;
+        cnt += gl;
+    }
+    // wave reduction
+    for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+    if ((threadIdx.x & 63) == 0) wave_sum[threadIdx.x >> 6] = cnt;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t t = 0;
+        for (int w = 0; w < PART_TPB / 64; w++) t += wave_sum[w];
+        counts[chunk] = t;
+    }
+}
+
+// Pass 2: exclusive scan of the chunk counts (one workgroup) and the left
+// total of every request.
+__global__ __launch_bounds__(1024) void part_scan_kernel(const uint32_t *counts, uint32_t n_chunks,
+                                                         uint32_t *excl, const PartReqDev *reqs,
+                                                         uint32_t n_reqs, uint32_t *totals) {
+    __shared__ uint32_t buf[1024];
+    __shared__ uint32_t carry;
+    if (threadIdx.x == 0) carry = 0;
+    __syncthreads();
+    for (uint32_t base = 0; base < n_chunks; base += 1024) {
+        const uint32_t i = base + threadIdx.x;
+        const uint32_t v = i < n_chunks ? counts[i] : 0;
+        buf[threadIdx.x] = v;
+        __syncthreads();
+        for (uint32_t off = 1; off < 1024; off <<= 1) {
+            uint32_t a = threadIdx.x >= off ? buf[threadIdx.x - off] : 0;
+            __syncthreads();
+            buf[threadIdx.x] += a;
+            __syncthreads();
+        }
+        if (i < n_chunks) excl[i] = carry + buf[threadIdx.x] - v;
+        __syncthreads();
+        if (threadIdx.x == 0) carry += buf[1023];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) excl[n_chunks] = carry;
+    __syncthreads();
+    for (uint32_t r = threadIdx.x; r < n_reqs; r += 1024)
+        totals[r] = excl[reqs[r].chunk_begin + reqs[r].n_chunks] - excl[reqs[r].chunk_begin];
+}
+
+// Pass 3: stable scatter into the temporary arena. Rows of a chunk are taken
+// in order, 256 at a time; a wave's lanes rank their rows with a ballot.
+__global__ __launch_bounds__(PART_TPB) void part_scatter_kernel(const PartReqDev *reqs,
+                                                                uint32_t n_reqs,
+                                                                const uint32_t *rows,
+                                                                const uint8_t *flags,
+                                                                const uint32_t *excl,
+                                                                const uint32_t *totals,
+                                                                uint32_t *tmp) {
+    __shared__ uint32_t wave_left[PART_TPB / 64];
+    const uint32_t chunk = blockIdx.x;
+    const uint32_t ri = find_req(reqs, n_reqs, chunk);
+    const PartReqDev R = reqs[ri];
+    const uint32_t c0 = (chunk - R.chunk_begin) * PART_CHUNK;
+    const uint32_t c1 = min(c0 + PART_CHUNK, R.row_len);
+    const uint32_t left_base = excl[chunk] - excl[R.chunk_begin];
+    const uint32_t total_left = totals[ri];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t done_left = 0;  // lefts of earlier rounds in this chunk
+    for (uint32_t base = c0; base < c1; base += PART_TPB) {
+        const uint32_t i = base + threadIdx.x;
+        const bool valid = i < c1;
+        const bool gl = valid && flags[R.row_off + i];
+        const uint64_t ball = __ballot(gl);
+        const uint32_t below = __popcll(ball & ((1ull << lane) - 1ull));
+        if (lane == 0) wave_left[wave] = __popcll(ball);
+        __syncthreads();
+        uint32_t before = 0, round_left = 0;
+        for (uint32_t w = 0; w < PART_TPB / 64; w++) {
+            if (w < wave) before += wave_left[w];
+            round_left += wave_left[w];
+        }
+        if (valid) {
+            const uint32_t row = rows[R.row_off + i];
+            const uint32_t lrank = done_left + before + below;
+            const uint32_t idx_in_chunk = i - c0;
+            uint32_t dst;
+            if (gl) dst = R.row_off + left_base + lrank;
+            else dst = R.row_off + total_left + (c0 - left_base) + (idx_in_chunk - lrank);
+            tmp[dst] = row;
+        }
+        done_left += round_left;
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(PART_TPB) void part_copy_kernel(const PartReqDev *reqs,
+                                                             uint32_t n_reqs, const uint32_t *tmp,
+                                                             uint32_t *rows) {
+    const uint32_t chunk = blockIdx.x;
+    const PartReqDev R = reqs[find_req(reqs, n_reqs, chunk)];
+    const uint32_t c0 = (chunk - R.chunk_begin) * PART_CHUNK;
+    const uint32_t c1 = min(c0 + PART_CHUNK, R.row_len);
+    for (uint32_t i = c0 + threadIdx.x; i < c1; i += PART_TPB)
+        rows[R.row_off + i] = tmp[R.row_off + i];
+}
+
+hipError_t launch_partition(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
+                            uint32_t *rows, uint32_t *tmp, uint8_t *flags, uint32_t *counts,
+                            uint32_t *excl, uint32_t *totals, const uint64_t *cat_words,
+                            hipStream_t s) {
+    if (n_chunks == 0) return hipSuccess;
+    hipLaunchKernelGGL(part_count_kernel, dim3(n_chunks), dim3(PART_TPB), 0, s, reqs, n_reqs, rows,
+                       flags, counts, cat_words);
+    hipLaunchKernelGGL(part_scan_kernel, dim3(1), dim3(1024), 0, s, counts, n_chunks, excl, reqs,
+                       n_reqs, totals);
+    hipLaunchKernelGGL(part_scatter_kernel, dim3(n_chunks), dim3(PART_TPB), 0, s, reqs, n_reqs,
+                       rows, flags, excl, totals, tmp);
+    hipLaunchKernelGGL(part_copy_kernel, dim3(n_chunks), dim3(PART_TPB), 0, s, reqs, n_reqs, tmp,
+                       rows);
+    return hipGetLastError();
+}
+
+// ======================================================================
+// leaves, row arena, quantisation, tile packing
+// ======================================================================
+
+__global__ __launch_bounds__(PART_TPB) void leaf_kernel(const LeafDev *leaves, uint32_t n,
+                                                        const uint32_t *rows, float *delta) {
+    const uint32_t chunk = blockIdx.x;
+    uint32_t lo = 0, hi = n;
+    while (hi - lo > 1) {
+        uint32_t mid = (lo + hi) >> 1;
+        if (leaves[mid].chunk_begin <= chunk) lo = mid;
+        else hi = mid;
+    }
+    const LeafDev L = leaves[lo];
+    const uint32_t c0 = (chunk - L.chunk_begin) * PART_CHUNK;
+    const uint32_t c1 = min(c0 + PART_CHUNK, L.row_len);
+    for (uint32_t i = c0 + threadIdx.x; i < c1; i += PART_TPB) delta[rows[L.row_off + i]] = L.value;
+}
+
+hipError_t launch_assign_leaves(const LeafDev *leaves, uint32_t n_leaves, uint32_t n_chunks,
+                                const uint32_t *rows, float *delta, hipStream_t s) {
+    if (n_chunks == 0) return hipSuccess;
+    hipLaunchKernelGGL(leaf_kernel, dim3(n_chunks), dim3(PART_TPB), 0, s, leaves, n_leaves, rows,
+                       delta);
+    return hipGetLastError();
+}
+
+__global__ void init_rows_kernel(uint32_t *rows, float *delta, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        rows[i] = (uint32_t)i;
+        delta[i] = 0.0f;
+    }
+}
+
+hipError_t launch_init_rows(uint32_t *rows, float *delta, uint64_t n, hipStream_t s) {
+    uint32_t blocks = (uint32_t)std::min<uint64_t>((n + 255) / 256, 4096);
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(init_rows_kernel, dim3(blocks), dim3(256), 0, s, rows, delta, n);
+    return hipGetLastError();
+}
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ uint64_t rotl64(uint64_t x, int r) { return (x << r) | (x >> (64 - r)); }
+
+// subsample::row_selected (src/data/subsample.rs).
+__device__ __forceinline__ bool row_selected(uint64_t row, uint64_t th, uint64_t seed,
+                                             uint64_t tree) {
+    if (th == ~0ull) return true;
+    const uint64_t hsh = mix64(seed ^ rotl64(tree * 0x9E3779B97F4A7C15ull, 23) ^
+                               (row * 0xD6E8FEB86659FD93ull));
+    return (hsh >> 11) < th;
+}
+
+__device__ __forceinline__ double finite_abs(float v) {
+    return isfinite(v) ? fabs((double)v) : (double)INFINITY;
+}
+
+// Masks sampled-out rows (in place) and reduces max |g|, max |h| per block.
+__global__ __launch_bounds__(256) void gpair_maxabs_kernel(float *g2n, uint64_t n, uint64_t th,
+                                                           uint64_t seed, uint64_t tree,
+                                                           double *block_max) {
+    __shared__ double sm[2][256];
+    double mg = 0.0, mh = 0.0;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        float2 v = reinterpret_cast<float2 *>(g2n)[i];
+        if (!row_selected(i, th, seed, tree)) {
+            v = make_float2(0.0f, 0.0f);
+            reinterpret_cast<float2 *>(g2n)[i] = v;
+        }
+        mg = fmax(mg, finite_abs(v.x));
+        mh = fmax(mh, finite_abs(v.y));
+    }
+    sm[0][threadIdx.x] = mg;
+    sm[1][threadIdx.x] = mh;
+    __syncthreads();
+    for (uint32_t s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            sm[0][threadIdx.x] = fmax(sm[0][threadIdx.x], sm[0][threadIdx.x + s]);
+            sm[1][threadIdx.x] = fmax(sm[1][threadIdx.x], sm[1][threadIdx.x + s]);
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        block_max[2 * blockIdx.x] = sm[0][0];
+        block_max[2 * blockIdx.x + 1] = sm[1][0];
+    }
+}
+
+__global__ void reduce_max_kernel(const double *block_max, uint32_t n, double *out) {
+    __shared__ double sm[2][256];
+    double mg = 0.0, mh = 0.0;
+    for (uint32_t i = threadIdx.x; i < n; i += 256) {
+        mg = fmax(mg, block_max[2 * i]);
+        mh = fmax(mh, block_max[2 * i + 1]);
+    }
+    sm[0][threadIdx.x] = mg;
+    sm[1][threadIdx.x] = mh;
+    __syncthreads();
+    for (uint32_t s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            sm[0][threadIdx.x] = fmax(sm[0][threadIdx.x], sm[0][threadIdx.x + s]);
+            sm[1][threadIdx.x] = fmax(sm[1][threadIdx.x], sm[1][threadIdx.x + s]);
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        out[0] = sm[0][0];
+        out[1] = sm[1][0];
+    }
+}
+
+hipError_t launch_gpair_maxabs(float *g2n, uint64_t n, uint64_t th, uint64_t seed, uint64_t tree,
+                               double *block_max, uint32_t n_blocks, double *out_max,
+                               hipStream_t s) {
+    hipLaunchKernelGGL(gpair_maxabs_kernel, dim3(n_blocks), dim3(256), 0, s, g2n, n, th, seed,
+                       tree, block_max);
+    hipLaunchKernelGGL(reduce_max_kernel, dim3(1), dim3(256), 0, s, block_max, n_blocks, out_max);
+    return hipGetLastError();
+}
+
+// `as i64` of Rust: saturating, NaN -> 0.
+__device__ __forceinline__ int64_t sat_i64(double x) {
+    if (isnan(x)) return 0;
+    if (x >= 9223372036854775808.0) return (int64_t)0x7FFFFFFFFFFFFFFFll;
+    if (x < -9223372036854775808.0) return (int64_t)0x8000000000000000ull;
+    return (int64_t)x;
+}
+
+// GradQuantizer::to_fixed: round half away from zero of v * 2^k.
+__global__ __launch_bounds__(256) void gpair_quantize_kernel(const float *g2n, uint64_t n,
+                                                             double sg, double sh, int64_t *out,
+                                                             int64_t *block_sum) {
+    __shared__ int64_t sm[2][256];
+    uint64_t ag = 0, ah = 0;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const float2 v = reinterpret_cast<const float2 *>(g2n)[i];
+        const int64_t qg = sat_i64(round((double)v.x * sg));
+        const int64_t qh = sat_i64(round((double)v.y * sh));
+        reinterpret_cast<longlong2 *>(out)[i] = make_longlong2(qg, qh);
+        ag += (uint64_t)qg;
+        ah += (uint64_t)qh;
+    }
+    sm[0][threadIdx.x] = (int64_t)ag;
+    sm[1][threadIdx.x] = (int64_t)ah;
+    __syncthreads();
+    for (uint32_t s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            sm[0][threadIdx.x] = wadd(sm[0][threadIdx.x], sm[0][threadIdx.x + s]);
+            sm[1][threadIdx.x] = wadd(sm[1][threadIdx.x], sm[1][threadIdx.x + s]);
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        block_sum[2 * blockIdx.x] = sm[0][0];
+        block_sum[2 * blockIdx.x + 1] = sm[1][0];
+    }
+}
+
+__global__ void reduce_sum_kernel(const int64_t *block_sum, uint32_t n, int64_t *out) {
+    __shared__ int64_t sm[2][256];
+    uint64_t ag = 0, ah = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += 256) {
+        ag += (uint64_t)block_sum[2 * i];
+        ah += (uint64_t)block_sum[2 * i + 1];
+    }
+    sm[0][threadIdx.x] = (int64_t)ag;
+    sm[1][threadIdx.x] = (int64_t)ah;
+    __syncthreads();
+    for (uint32_t s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            sm[0][threadIdx.x] = wadd(sm[0][threadIdx.x], sm[0][threadIdx.x + s]);
+            sm[1][threadIdx.x] = wadd(sm[1][threadIdx.x], sm[1][threadIdx.x + s]);
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        out[0] = sm[0][0];
+        out[1] = sm[1][0];
+    }
+}
+
+hipError_t launch_gpair_quantize(const float *g2n, uint64_t n, double sg, double sh, int64_t *out,
+                                 int64_t *block_sum, uint32_t n_blocks, int64_t *out_sum,
+                                 hipStream_t s) {
+    hipLaunchKernelGGL(gpair_quantize_kernel, dim3(n_blocks), dim3(256), 0, s, g2n, n, sg, sh, out,
+                       block_sum);
+    hipLaunchKernelGGL(reduce_sum_kernel, dim3(1), dim3(256), 0, s, block_sum, n_blocks, out_sum);
+    return hipGetLastError();
+}
+
+// One column-major feature column [n_rows] of `width`-byte cells into its
+// position (byte_off) of every row record of a tile.
+__global__ void pack_feature_kernel(const uint8_t *col, uint64_t n_rows, uint32_t width,
+                                    uint8_t *tile, uint32_t stride, uint32_t byte_off) {
+    for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n_rows;
+         r += (uint64_t)gridDim.x * blockDim.x) {
+        uint8_t *dst = tile + r * stride + byte_off;
+        if (width == 1) dst[0] = col[r];
+        else *reinterpret_cast<uint16_t *>(dst) = reinterpret_cast<const uint16_t *>(col)[r];
+    }
+}
+
+hipError_t launch_pack_feature(const uint8_t *col, uint64_t n_rows, uint32_t width, uint8_t *tile,
+                               uint32_t stride, uint32_t byte_off, hipStream_t s) {
+    uint32_t blocks = (uint32_t)std::min<uint64_t>((n_rows + 255) / 256, 8192);
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(pack_feature_kernel, dim3(blocks), dim3(256), 0, s, col, n_rows, width,
+                       tile, stride, byte_off);
+    return hipGetLastError();
+}
+
+// ======================================================================
+// QuadratureTreeSHAP
+// ======================================================================
+
+constexpr int QP = 8;          // quadrature points
+constexpr float UNSEEN = -999.0f;
+constexpr int SHAP_MAXD = 16;  // path frames (max_depth <= 14)
+constexpr int SHAP_TPB = 128;
+
+__device__ __forceinline__ bool shap_goes_left(const ShapNodeDev &n, float v,
+                                               const uint32_t *cat_words) {
+    if (isnan(v)) return (n.flags & 2u) != 0;
+    if (n.flags & 4u) {
+        if (v < 0.0f || v >= 16777216.0f) return true;
+        const uint32_t cat = (uint32_t)v;
+        const uint32_t word = cat / 32;
+        if (word >= n.cat_len) return true;
+        return ((cat_words[n.cat_offset + word] >> (cat % 32)) & 1u) == 0;
+    }
+    return v < n.split_cond;
+}
+
+// One thread per row: every tree's QuadratureTreeSHAP with the recursion of
+// Runner::run_node / visit_child unrolled onto an explicit path stack, in
+// the host's exact float32 operation order.
+template <int MAXU>
+__global__ __launch_bounds__(SHAP_TPB) void shap_kernel(
+    const ShapNodeDev *nodes, const uint32_t *tree_roots, uint32_t n_trees,
+    const uint32_t *tree_ufeat_off, const uint32_t *ufeats, const uint32_t *cat_words,
+    const float *rule, const float *rows, uint64_t n_rows, uint32_t n_features,
+    const float *margin, float bias, float root_mean, float *out) {
+    const uint64_t row = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= n_rows) return;
+    float rn[QP], rw[QP];
+#pragma unroll
+    for (int i = 0; i < QP; i++) {
+        rn[i] = rule[i];
+        rw[i] = rule[QP + i];
+    }
+    const float *x = rows + row * n_features;
+    float *p = out + row * (uint64_t)(n_features + 1);
+    for (uint32_t f = 0; f <= n_features; f++) p[f] = 0.0f;
+
+    float tc[MAXU];
+    float c[SHAP_MAXD][QP];
+    float hl[SHAP_MAXD][QP];
+    float wprod[SHAP_MAXD];
+    float pe[SHAP_MAXD], pold[SHAP_MAXD];
+    uint32_t nid[SHAP_MAXD], pfeat[SHAP_MAXD];
+    uint8_t stage[SHAP_MAXD], gl[SHAP_MAXD];
+
+    for (uint32_t t = 0; t < n_trees; t++) {
+        const uint32_t root = tree_roots[t];
+        const uint32_t u0 = tree_ufeat_off[t], nu = tree_ufeat_off[t + 1] - u0;
+        if (nodes[root].flags & 1u) continue;  // a leaf-only tree contributes nothing
+        for (uint32_t u = 0; u < nu; u++) tc[u] = 0.0f;
+        int d = 0;
+        nid[0] = root;
+        wprod[0] = 1.0f;
+#pragma unroll
+        for (int i = 0; i < QP; i++) c[0][i] = 1.0f;
+        stage[0] = 0;
+        {
+            const ShapNodeDev &n0 = nodes[root];
+            gl[0] = shap_goes_left(n0, x[n0.feat], cat_words);
+        }
+        float ret[QP];
+        for (;;) {
+            const ShapNodeDev &n = nodes[nid[d]];
+            // Begin the visit of the next child of frame d.
+            const bool right = stage[d] != 0;
+            const uint32_t child = (uint32_t)(right ? n.right : n.left);
+            const float cw = right ? n.right_weight : n.left_weight;
+            const bool sat = right ? !gl[d] : (gl[d] != 0);
+            const uint32_t feat = n.feat;
+            float p_old = UNSEEN;
+            for (int k = d - 1; k >= 0; k--)
+                if (pfeat[k] == feat) {
+                    p_old = pe[k];
+                    break;
+                }
+            const float p_e = sat ? (p_old == UNSEEN ? 1.0f / cw : p_old / cw) : 0.0f;
+            float cc[QP];
+            const float ae = p_e - 1.0f;
+#pragma unroll
+            for (int i = 0; i < QP; i++) {
+                const float m = 1.0f + ae * rn[i];
+                cc[i] = c[d][i] * m;
+            }
+            if (p_old != UNSEEN) {
+                const float ao = p_old - 1.0f;
+                if (ao != 0.0f) {
+#pragma unroll
+                    for (int i = 0; i < QP; i++) cc[i] /= 1.0f + ao * rn[i];
+                }
+            }
+            pfeat[d] = feat;
+            pe[d] = p_e;
+            pold[d] = p_old;
+            const float wchild = wprod[d] * cw;
+            const ShapNodeDev &cn = nodes[child];
+            if (!(cn.flags & 1u)) {
+                // descend
+                d++;
+                nid[d] = child;
+                wprod[d] = wchild;
+#pragma unroll
+                for (int i = 0; i < QP; i++) c[d][i] = cc[i];
+                stage[d] = 0;
+                gl[d] = shap_goes_left(cn, x[cn.feat], cat_words);
+                continue;
+            }
+            const float ls = wchild * cn.leaf_value;
+#pragma unroll
+            for (int i = 0; i < QP; i++) {
+                const float a = cc[i] * ls;
+                ret[i] = a * rw[i];
+            }
+            // Finish visits upward while frames complete.
+            for (;;) {
+                // extract_delta (explain.rs:225-240) for the visit of frame d.
+                const float pen = pe[d];
+                const float px = pold[d] == UNSEEN ? 1.0f : pold[d];
+                float acc = 0.0f;
+                if (pen != 1.0f) {
+                    const float a = pen - 1.0f;
+#pragma unroll
+                    for (int i = 0; i < QP; i++) {
+                        const float num = a * ret[i];
+                        const float den = 1.0f + a * rn[i];
+                        acc += num / den;
+                    }
+                }
+                if (px != 1.0f) {
+                    const float a = px - 1.0f;
+#pragma unroll
+                    for (int i = 0; i < QP; i++) {
+                        const float num = a * ret[i];
+                        const float den = 1.0f + a * rn[i];
+                        acc -= num / den;
+                    }
+                }
+                const uint32_t us = nodes[nid[d]].uslot;
+                tc[us] += acc;
+                if (stage[d] == 0) {
+#pragma unroll
+                    for (int i = 0; i < QP; i++) hl[d][i] = ret[i];
+                    stage[d] = 1;
+                    break;  // begin the right visit of frame d
+                }
+#pragma unroll
+                for (int i = 0; i < QP; i++) ret[i] = hl[d][i] + ret[i];
+                if (d == 0) goto tree_done;
+                d--;
+            }
+        }
+    tree_done:
+        for (uint32_t u = 0; u < nu; u++) p[ufeats[u0 + u]] += tc[u];
+    }
+    p[n_features] += root_mean;
+    p[n_features] += margin ? margin[row] : bias;
+}
+
+hipError_t launch_shap(const ShapNodeDev *nodes, const uint32_t *tree_roots, uint32_t n_trees,
+                       const uint32_t *tree_ufeat_off, const uint32_t *ufeats,
+                       const uint32_t *cat_words, const float *rule, const float *rows,
+                       uint64_t n_rows, uint32_t n_features, const float *margin, float bias,
+                       float root_mean, float *out, uint32_t max_unique, uint32_t max_depth,
+                       hipStream_t s) {
+    if (n_rows == 0) return hipSuccess;
+    if (max_depth > SHAP_MAXD) return hipErrorInvalidValue;
+    const uint32_t blocks = (uint32_t)((n_rows + SHAP_TPB - 1) / SHAP_TPB);
+#define FBH_SHAP_CASE(U)                                                                         \
+    if (max_unique <= U) {                                                                       \
+        hipLaunchKernelGGL(shap_kernel<U>, dim3(blocks), dim3(SHAP_TPB), 0, s, nodes,           \
+                           tree_roots, n_trees, tree_ufeat_off, ufeats, cat_words, rule, rows,  \
+                           n_rows, n_features, margin, bias, root_mean, out);                    \
+        return hipGetLastError();                                                               \
+    }
+    FBH_SHAP_CASE(32) FBH_SHAP_CASE(64) FBH_SHAP_CASE(128) FBH_SHAP_CASE(256)
+    FBH_SHAP_CASE(1024)
+#undef FBH_SHAP_CASE
+    return hipErrorInvalidValue;
+}
+
+}  // namespace fbh

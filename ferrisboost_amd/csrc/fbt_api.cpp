@@ -1,0 +1,215 @@
+// fbt_api.cpp -- C ABI of the round driver (include/fbtrain.h).
+
+#include <cstring>
+#include <memory>
+#include <string>
+
+#include "fbhip.h"
+#include "fbt_internal.h"
+
+namespace fbt {
+Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float *w,
+            const uint8_t *cat, const int8_t *mono, uint32_t n_mono, const fbt_params &p);
+fbt_stats last_stats();
+}  // namespace fbt
+
+struct fbt_model {
+    fbt::Model m;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+template <class F>
+int guard(F &&f) {
+    try {
+        f();
+        return FBH_OK;
+    } catch (const fbt::InputError &e) {
+        g_err = e.what();
+        return FBH_INPUT_ERROR;
+    } catch (const std::exception &e) {
+        g_err = e.what();
+        return FBH_RUNTIME_ERROR;
+    } catch (...) {
+        g_err = "unknown error";
+        return FBH_RUNTIME_ERROR;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t fbt_last_error(char *buf, size_t len) {
+    if (buf && len) {
+        const size_t n = std::min(len - 1, g_err.size());
+        std::memcpy(buf, g_err.data(), n);
+        buf[n] = 0;
+    }
+    return g_err.size();
+}
+
+int fbt_train(const float *x, uint64_t n_rows, uint32_t n_features, const float *labels,
+              const float *weights, const uint8_t *categorical, const int8_t *monotone,
+              uint32_t n_monotone, const fbt_params *params, fbt_model **out) {
+    return guard([&] {
+        if (!x || !labels || !params || !out) throw fbt::InputError("null argument");
+        *out = nullptr;
+        auto m = std::make_unique<fbt_model>();
+        m->m = fbt::train(x, n_rows, n_features, labels, weights, categorical, monotone, n_monotone,
+                          *params);
+        *out = m.release();
+    });
+}
+
+int fbt_last_stats(fbt_stats *out) {
+    return guard([&] {
+        if (!out) throw fbt::InputError("null argument");
+        *out = fbt::last_stats();
+    });
+}
+
+void fbt_model_free(fbt_model *m) { delete m; }
+uint32_t fbt_model_n_trees(const fbt_model *m) { return (uint32_t)m->m.trees.size(); }
+uint32_t fbt_model_tree_len(const fbt_model *m, uint32_t t) {
+    return (uint32_t)m->m.trees[t].nodes.size();
+}
+
+void fbt_model_tree_nodes(const fbt_model *m, uint32_t t, fbt_node *out) {
+    uint32_t base = 0;
+    for (uint32_t k = 0; k < t; k++)
+        for (const auto &n : m->m.trees[k].nodes) base += (uint32_t)n.cats.size();
+    const auto &nodes = m->m.trees[t].nodes;
+    for (size_t i = 0; i < nodes.size(); i++) {
+        const auto &n = nodes[i];
+        fbt_node o;
+        std::memset(&o, 0, sizeof(o));
+        o.feat = n.feat;
+        o.split_cond = n.split_cond;
+        o.left = n.left;
+        o.right = n.right;
+        o.default_left = n.default_left;
+        o.is_leaf = n.is_leaf;
+        o.leaf_value = n.leaf_value;
+        o.gain = n.gain;
+        o.sum_hess = n.sum_hess;
+        o.cat_begin = base;
+        o.cat_len = (uint32_t)n.cats.size();
+        base += o.cat_len;
+        out[i] = o;
+    }
+}
+
+uint32_t fbt_model_n_cat_words(const fbt_model *m) {
+    uint32_t s = 0;
+    for (const auto &t : m->m.trees)
+        for (const auto &n : t.nodes) s += (uint32_t)n.cats.size();
+    return s;
+}
+
+void fbt_model_cat_words(const fbt_model *m, uint32_t *out) {
+    for (const auto &t : m->m.trees)
+        for (const auto &n : t.nodes)
+            for (uint32_t w : n.cats) *out++ = w;
+}
+
+float fbt_model_base_score(const fbt_model *m) { return m->m.base_score; }
+float fbt_model_base_margin(const fbt_model *m) { return m->m.base_margin(); }
+uint32_t fbt_model_n_features(const fbt_model *m) { return m->m.n_features; }
+
+int fbt_model_train_margins(const fbt_model *m, float *out, uint64_t n) {
+    return guard([&] {
+        if (!m || !out) throw fbt::InputError("null argument");
+        if (n != m->m.train_margins.size()) throw fbt::InputError("row count mismatch");
+        std::memcpy(out, m->m.train_margins.data(), 4 * n);
+    });
+}
+
+uint32_t fbt_model_n_cuts(const fbt_model *m) { return (uint32_t)m->m.cuts.values.size(); }
+
+void fbt_model_cuts(const fbt_model *m, float *values, uint32_t *offsets) {
+    std::copy(m->m.cuts.values.begin(), m->m.cuts.values.end(), values);
+    std::copy(m->m.cuts.offsets.begin(), m->m.cuts.offsets.end(), offsets);
+}
+
+void fbt_predict_margin(const fbt_model *m, const float *x, uint64_t n, uint32_t nf, float *out) {
+    const float bm = m->m.base_margin();
+    for (uint64_t r = 0; r < n; r++) {
+        float acc = bm;
+        for (const auto &t : m->m.trees) acc += t.leaf_value(x + r * nf);
+        out[r] = acc;
+    }
+}
+
+size_t fbt_model_to_json(const fbt_model *m, char *buf, size_t len) {
+    const std::string s = fbt::model_to_json(m->m);
+    if (buf && len) {
+        const size_t n = std::min(len - 1, s.size());
+        std::memcpy(buf, s.data(), n);
+        buf[n] = 0;
+    }
+    return s.size();
+}
+
+int fbt_shap(const fbt_model *mm, const float *x, uint64_t n_rows, uint32_t n_features,
+             int device, float *out) {
+    return guard([&] {
+        if (!mm || !x || !out) throw fbt::InputError("null argument");
+        const fbt::Model &m = mm->m;
+        if (n_features != m.n_features)
+            throw fbt::InputError("expected " + std::to_string(m.n_features) + " features, got " +
+                                  std::to_string(n_features));
+        std::vector<uint32_t> offs{0}, feat, cat_off, cat_len, words;
+        std::vector<float> cond, leaf, hess;
+        std::vector<int32_t> left, right;
+        std::vector<uint8_t> dl, is_leaf;
+        for (const auto &t : m.trees) {
+            for (const auto &n : t.nodes) {
+                feat.push_back(n.feat);
+                cond.push_back(n.split_cond);
+                left.push_back(n.left);
+                right.push_back(n.right);
+                dl.push_back(n.default_left);
+                is_leaf.push_back(n.is_leaf);
+                leaf.push_back(n.leaf_value);
+                hess.push_back(n.sum_hess);
+                cat_off.push_back((uint32_t)words.size());
+                cat_len.push_back((uint32_t)n.cats.size());
+                words.insert(words.end(), n.cats.begin(), n.cats.end());
+            }
+            offs.push_back((uint32_t)feat.size());
+        }
+        fbh_shap_model *sm = nullptr;
+        char buf[1024];
+        int rc = fbh_shap_model_create(device, (uint32_t)m.trees.size(), offs.data(), feat.data(),
+                                       cond.data(), left.data(), right.data(), dl.data(),
+                                       is_leaf.data(), leaf.data(), hess.data(), cat_off.data(),
+                                       cat_len.data(), words.data(), (uint32_t)words.size(),
+                                       n_features, m.base_margin(), &sm);
+        if (rc) {
+            fbh_last_error(buf, sizeof(buf));
+            if (rc == FBH_INPUT_ERROR) throw fbt::InputError(buf);
+            throw fbt::RuntimeError(buf);
+        }
+        std::unique_ptr<fbh_shap_model, int (*)(fbh_shap_model *)> own(sm, fbh_shap_model_destroy);
+        rc = fbh_shap_contribs(sm, x, n_rows, nullptr, out);
+        if (rc) {
+            fbh_last_error(buf, sizeof(buf));
+            throw fbt::RuntimeError(buf);
+        }
+    });
+}
+
+int fbt_sketch_cuts(const float *x, uint64_t n, uint32_t nf, uint32_t max_bin, const float *w,
+                    const uint8_t *cat, float *values, uint32_t *offsets) {
+    return guard([&] {
+        if (!x || !values || !offsets) throw fbt::InputError("null argument");
+        fbt::Cuts c = fbt::sketch_matrix(x, n, nf, max_bin, w, cat, 0);
+        std::copy(c.values.begin(), c.values.end(), values);
+        std::copy(c.offsets.begin(), c.offsets.end(), offsets);
+    });
+}
+
+}  // extern "C"

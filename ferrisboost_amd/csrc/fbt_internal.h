@@ -1,0 +1,86 @@
+// fbt_internal.h -- host-side types of the round driver (libfbtrain.so).
+#pragma once
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "fbtrain.h"
+
+namespace fbt {
+
+struct InputError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+struct RuntimeError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+// BinCuts (src/data/columns.rs:50-360): per-feature upper-bound cuts.
+struct Cuts {
+    std::vector<float> values;
+    std::vector<uint32_t> offsets;  // n_features + 1
+    std::vector<uint8_t> categorical;
+
+    uint32_t n_features() const { return (uint32_t)offsets.size() - 1; }
+    uint32_t n_cuts(uint32_t f) const { return offsets[f + 1] - offsets[f]; }
+    uint32_t n_bins(uint32_t f) const { return n_cuts(f) + 1; }
+    bool is_cat(uint32_t f) const { return categorical[f] != 0; }
+    // BinWidth::for_feature (src/data/bins.rs:55-66).
+    uint32_t width(uint32_t f) const {
+        return n_bins(f) <= (is_cat(f) ? 254u : 255u) ? 1u : 2u;
+    }
+    uint32_t bin_of(uint32_t f, float v) const;
+};
+
+// Sketch every feature of a row-major matrix (DenseSource binning pass).
+Cuts sketch_matrix(const float *x, uint64_t n_rows, uint32_t n_features, uint32_t max_bin,
+                   const float *weights, const uint8_t *categorical, unsigned threads);
+
+// Column-major bins of `feats` (one width) for upload.
+void bin_columns(const float *x, uint64_t n_rows, uint32_t n_features, const Cuts &cuts,
+                 const std::vector<uint32_t> &feats, uint32_t width, void *out, unsigned threads);
+
+// partition_features_by_width (src/data/columns.rs:446-463).
+std::vector<std::vector<uint32_t>> blocks_by_width(const Cuts &cuts, uint32_t cols_per_block);
+
+struct Node {
+    uint32_t feat = 0;
+    float split_cond = 0.0f;
+    int32_t left = -1, right = -1;
+    bool default_left = false;
+    bool is_leaf = true;
+    float leaf_value = 0.0f;
+    float gain = 0.0f;
+    float sum_hess = 0.0f;
+    std::vector<uint32_t> cats;  // right-going set, u32 words, trailing zeros trimmed
+};
+
+struct Tree {
+    std::vector<Node> nodes;
+    uint32_t push_leaf(float value, float hess);
+    // Tree::split_leaf (src/model/tree.rs:140-170).
+    std::pair<uint32_t, uint32_t> split_leaf(uint32_t node, uint32_t feat, float cond,
+                                             bool default_left, float gain, float lv, float lh,
+                                             float rv, float rh);
+    // Tree::set_categories: set words from 64-bit CatBits words.
+    void set_categories(uint32_t node, const uint64_t *words64, uint32_t n_words64);
+    float leaf_value(const float *x) const;
+};
+
+struct Model {
+    std::vector<Tree> trees;
+    float base_score = 0.5f;
+    uint32_t objective = 1;
+    uint32_t n_features = 0;
+    float scale_pos_weight = 1.0f;
+    Cuts cuts;
+    std::vector<float> train_margins;
+    float base_margin() const;
+};
+
+float base_margin_of(uint32_t objective, float base_score);
+std::string model_to_json(const Model &m);
+
+}  // namespace fbt

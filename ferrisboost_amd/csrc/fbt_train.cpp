@@ -1,0 +1,688 @@
+// fbt_train.cpp -- the round driver of the device path.
+//
+// Restates train_with_backend (src/training/mod.rs:1299-2376) for the
+// single-output logistic and squared-error objectives with gpu_math="exact":
+// the raw margins live on the host, every round downloads the previous
+// tree's per-row delta, applies it and computes the f32 gradient pairs with
+// the host's libm (so exp() rounds like the CPU engine), uploads them, and
+// the device quantises them to i64 fixed point. Trees are grown depthwise
+// (build_tree, src/training/mod.rs:3357-4565) or loss-guided
+// (src/training/lossguide.rs:494-700); histograms, split scans, partitions
+// and leaf scatters all run through the fbh_* backend.
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <condition_variable>
+#include <cstring>
+#include <functional>
+#include <limits>
+#include <memory>
+#include <mutex>
+#include <queue>
+#include <thread>
+
+#include "fbhip.h"
+#include "fbt_internal.h"
+
+namespace fbt {
+namespace {
+
+using Clock = std::chrono::steady_clock;
+
+std::string backend_error() {
+    char buf[1024];
+    fbh_last_error(buf, sizeof(buf));
+    return buf;
+}
+
+void call(int rc) {
+    if (rc == FBH_INPUT_ERROR) throw InputError(backend_error());
+    if (rc != FBH_OK) throw RuntimeError(backend_error());
+}
+
+// A fixed pool of host threads for the per-row passes.
+class Pool {
+  public:
+    explicit Pool(unsigned n) : n_(std::max(1u, n)) {
+        for (unsigned t = 1; t < n_; t++) workers_.emplace_back([this, t] { loop(t); });
+    }
+    ~Pool() {
+        {
+            std::lock_guard<std::mutex> g(m_);
+            stop_ = true;
+            gen_++;
+        }
+        cv_.notify_all();
+        for (auto &w : workers_) w.join();
+    }
+    unsigned size() const { return n_; }
+    // Runs f(t) on every thread t in [0, n) and waits.
+    void run(const std::function<void(unsigned)> &f) {
+        if (n_ == 1) {
+            f(0);
+            return;
+        }
+        {
+            std::lock_guard<std::mutex> g(m_);
+            job_ = &f;
+            pending_ = n_ - 1;
+            gen_++;
+        }
+        cv_.notify_all();
+        f(0);
+        std::unique_lock<std::mutex> lk(m_);
+        done_.wait(lk, [this] { return pending_ == 0; });
+        job_ = nullptr;
+    }
+
+  private:
+    void loop(unsigned t) {
+        uint64_t seen = 0;
+        for (;;) {
+            const std::function<void(unsigned)> *job;
+            {
+                std::unique_lock<std::mutex> lk(m_);
+                cv_.wait(lk, [&] { return gen_ != seen; });
+                seen = gen_;
+                if (stop_) return;
+                job = job_;
+            }
+            (*job)(t);
+            {
+                std::lock_guard<std::mutex> g(m_);
+                if (--pending_ == 0) done_.notify_one();
+            }
+        }
+    }
+    unsigned n_;
+    std::vector<std::thread> workers_;
+    std::mutex m_;
+    std::condition_variable cv_, done_;
+    const std::function<void(unsigned)> *job_ = nullptr;
+    unsigned pending_ = 0;
+    uint64_t gen_ = 0;
+    bool stop_ = false;
+};
+
+// ---------------------------------------------------------------- host math
+// The leaf-value arithmetic of split.rs:113-218, in f64 then f32.
+struct LeafMath {
+    float lambda_, alpha, mds, lr;
+    double inv_g, inv_h;
+    void to_f64(const int64_t s[2], double &g, double &h) const {
+        g = (double)s[0] * inv_g;
+        h = (double)s[1] * inv_h;
+    }
+    float weight(double g, double h) const {  // xgb_weight
+        if (h <= 0.0) return 0.0f;
+        const double a = (double)alpha;
+        const double t = g > a ? g - a : (g < -a ? g + a : 0.0);
+        double dw = -t / (h + (double)lambda_);
+        if (mds != 0.0f && std::fabs(dw) > (double)mds) dw = std::copysign((double)mds, dw);
+        return (float)dw;
+    }
+    float hess(const int64_t s[2]) const {
+        double g, h;
+        to_f64(s, g, h);
+        return (float)h;
+    }
+};
+
+struct Bounds {  // NodeBounds (split.rs:120-160)
+    float lo = -std::numeric_limits<float>::max();
+    float hi = std::numeric_limits<float>::max();
+    float apply(float w) const { return w < lo ? lo : (w > hi ? hi : w); }
+};
+
+// colsample::sample_features (src/data/colsample.rs:57-73): SplitMix64
+// Fisher-Yates keyed by (seed, round), first `count` ids, sorted.
+std::vector<uint32_t> sample_columns(uint32_t nf, float rate, uint64_t seed, uint64_t round) {
+    std::vector<uint32_t> ids(nf);
+    for (uint32_t i = 0; i < nf; i++) ids[i] = i;
+    const double c = std::floor((double)rate * (double)nf);
+    size_t take = (std::isfinite(c) && c >= 1.0) ? (size_t)c : 1;
+    take = std::max<size_t>(std::min<size_t>(take, nf), 1);
+    if (take >= nf) return ids;
+    const uint64_t r = round * 0x9E3779B97F4A7C15ull;
+    uint64_t state = seed ^ ((r << 17) | (r >> 47));
+    auto next = [&state] {
+        state += 0x9E3779B97F4A7C15ull;
+        uint64_t z = state;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    };
+    for (size_t i = nf - 1; i >= 1; i--) {
+        const uint64_t n = i + 1;
+        const uint64_t zone = UINT64_MAX - (UINT64_MAX % n) - 1;
+        uint64_t v;
+        do v = next();
+        while (v > zone);
+        std::swap(ids[i], ids[v % n]);
+    }
+    ids.resize(take);
+    std::sort(ids.begin(), ids.end());
+    return ids;
+}
+
+uint64_t sample_threshold(float rate) {  // subsample::threshold_for
+    if (rate >= 1.0f || !(rate > 0.0f)) return UINT64_MAX;
+    return (uint64_t)((double)rate * (double)(1ull << 53));
+}
+
+// ---------------------------------------------------------------- growers
+class Grower {
+  public:
+    Grower(fbh_ctx *ctx, const fbt_params &p, const Cuts &cuts, const std::vector<int8_t> &mono,
+           uint32_t n_slots)
+        : ctx_(ctx), p_(p), cuts_(cuts), mono_(mono) {
+        sp_.lambda_ = p.lambda_;
+        sp_.gamma = p.gamma;
+        sp_.min_child_weight = p.min_child_weight;
+        sp_.alpha = p.alpha;
+        sp_.max_delta_step = p.max_delta_step;
+        sp_.max_cat_to_onehot = p.max_cat_to_onehot;
+        sp_.max_cat_threshold = p.max_cat_threshold;
+        for (uint32_t s = n_slots; s-- > 0;) free_.push_back(s);
+        // Category words of one node: every categorical feature's set.
+        uint32_t words = 0;
+        for (uint32_t f = 0; f < cuts.n_features(); f++)
+            if (cuts.is_cat(f)) words += (cuts.n_bins(f) + 63) / 64;
+        cat_cap_ = words;
+    }
+
+    Tree grow(const double scales[2], const int64_t root_sum[2]) {
+        lm_ = {p_.lambda_, p_.alpha, p_.max_delta_step, p_.learning_rate, 1.0 / scales[0],
+               1.0 / scales[1]};
+        leaves_spans_.clear();
+        leaves_values_.clear();
+        Tree t;
+        double g, h;
+        lm_.to_f64(root_sum, g, h);
+        t.push_leaf(lm_.weight(g, h) * p_.learning_rate, (float)h);
+        fbh_span root;
+        root.offset = 0;
+        root.len = n_rows_;
+        if (p_.grow_policy == 1) lossguide(t, root, root_sum);
+        else depthwise(t, root, root_sum);
+        if (!leaves_spans_.empty())
+            call(fbh_assign_leaves(ctx_, leaves_spans_.data(), leaves_values_.data(),
+                                   (uint32_t)leaves_spans_.size()));
+        return t;
+    }
+    uint32_t n_rows_ = 0;
+
+  private:
+    struct Pending {
+        uint32_t node;
+        fbh_span rows;
+        int64_t sum[2];
+        Bounds b;
+        uint32_t slot;
+        int32_t parent_slot;  // -1: accumulate
+        int32_t sibling;      // index of the accumulated sibling in the batch
+        uint32_t depth;
+    };
+
+    uint32_t take_slot() {
+        if (free_.empty())
+            throw RuntimeError("histogram slots exhausted; raise the slot budget");
+        const uint32_t s = free_.back();
+        free_.pop_back();
+        return s;
+    }
+    void give_slot(uint32_t s) { free_.push_back(s); }
+
+    void finish_leaf(const Tree &t, uint32_t node, fbh_span rows) {
+        if (rows.len == 0) return;
+        leaves_spans_.push_back(rows);
+        leaves_values_.push_back(t.nodes[node].leaf_value);
+    }
+
+    // Split scans of a batch of nodes; returns packets.
+    std::vector<fbh_split> eval(const std::vector<Pending> &batch) {
+        std::vector<fbh_node> nodes(batch.size());
+        for (size_t i = 0; i < batch.size(); i++) {
+            const Pending &b = batch[i];
+            fbh_node &n = nodes[i];
+            n.rows = b.rows;
+            n.sum[0] = b.sum[0];
+            n.sum[1] = b.sum[1];
+            n.lower = b.b.lo;
+            n.upper = b.b.hi;
+            n.slot = b.slot;
+            n.subtract_parent = b.parent_slot;
+            n.subtract_sibling = b.sibling;
+            n.reserved = 0;
+        }
+        std::vector<fbh_split> out(batch.size());
+        cat_words_.assign((size_t)std::max<uint32_t>(1, cat_cap_) * batch.size(), 0);
+        call(fbh_eval_nodes(ctx_, nodes.data(), (uint32_t)nodes.size(), &sp_, nullptr, out.data(),
+                            cat_words_.data(), (uint32_t)cat_words_.size()));
+        return out;
+    }
+
+    // Tree::split_leaf with child_leaves (src/training/mod.rs:5069-5094).
+    void apply(Tree &t, uint32_t node, const fbh_split &s, const uint64_t *cats, Bounds parent,
+               uint32_t &l, uint32_t &r, Bounds &lb, Bounds &rb) {
+        double g, h;
+        lm_.to_f64(s.left, g, h);
+        const float wl = parent.apply(lm_.weight(g, h));
+        lm_.to_f64(s.right, g, h);
+        const float wr = parent.apply(lm_.weight(g, h));
+        const int8_t c = s.feat < mono_.size() ? mono_[s.feat] : 0;
+        const float mid = (wl + wr) / 2.0f;
+        lb = parent;
+        rb = parent;
+        if (c < 0) {
+            lb.lo = mid;
+            rb.hi = mid;
+        } else if (c > 0) {
+            lb.hi = mid;
+            rb.lo = mid;
+        }
+        float cond = 0.0f;
+        if (!s.is_cat) {  // split_threshold (tree.rs:991-1001)
+            const uint32_t nc = cuts_.n_cuts(s.feat);
+            if (s.bin == 0) cond = -std::numeric_limits<float>::max();
+            else if (s.bin > nc) cond = std::numeric_limits<float>::max();
+            else cond = cuts_.values[cuts_.offsets[s.feat] + s.bin - 1];
+        }
+        auto lr = t.split_leaf(node, s.feat, cond, s.missing_left != 0, s.gain,
+                               wl * p_.learning_rate, lm_.hess(s.left), wr * p_.learning_rate,
+                               lm_.hess(s.right));
+        if (s.is_cat) t.set_categories(node, cats, s.n_cat_words);
+        l = lr.first;
+        r = lr.second;
+    }
+
+    fbh_part_req part_req(const Pending &nd, const fbh_split &s, uint32_t cat_off) {
+        fbh_part_req q{};
+        q.rows = nd.rows;
+        q.feat = s.feat;
+        q.bin = s.bin;
+        q.missing_left = s.missing_left;
+        q.cat_offset = cat_off;
+        q.n_cat_words = s.is_cat ? s.n_cat_words : 0;
+        return q;
+    }
+
+    void depthwise(Tree &t, fbh_span root_rows, const int64_t root_sum[2]) {
+        std::vector<Pending> level(1);
+        level[0] = {0, root_rows, {root_sum[0], root_sum[1]}, Bounds(), take_slot(), -1, -1, 0};
+        uint32_t leaf_count = 1;
+        for (uint32_t depth = 0; depth < p_.max_depth; depth++) {
+            if (level.empty() || (p_.max_leaves != 0 && leaf_count >= p_.max_leaves)) break;
+            std::vector<fbh_split> chosen = eval(level);
+            const std::vector<uint64_t> cats = cat_words_;
+            if (p_.max_leaves != 0) {
+                uint32_t remaining = p_.max_leaves > leaf_count ? p_.max_leaves - leaf_count : 0;
+                for (auto &c : chosen)
+                    if (c.found) {
+                        if (remaining == 0) c.found = 0;
+                        else remaining--;
+                    }
+            }
+            std::vector<fbh_part_req> reqs;
+            std::vector<uint32_t> req_of(level.size(), UINT32_MAX);
+            for (size_t i = 0; i < level.size(); i++)
+                if (chosen[i].found) {
+                    req_of[i] = (uint32_t)reqs.size();
+                    reqs.push_back(part_req(level[i], chosen[i], chosen[i].cat_offset));
+                }
+            std::vector<fbh_span> children(2 * reqs.size());
+            if (!reqs.empty())
+                call(fbh_partition(ctx_, reqs.data(), (uint32_t)reqs.size(), cats.data(),
+                                   (uint32_t)cats.size(), children.data()));
+            std::vector<Pending> next;
+            for (size_t i = 0; i < level.size(); i++) {
+                const Pending &ln = level[i];
+                if (!chosen[i].found) {
+                    finish_leaf(t, ln.node, ln.rows);
+                    give_slot(ln.slot);
+                    continue;
+                }
+                leaf_count++;
+                uint32_t l, r;
+                Bounds lb, rb;
+                apply(t, ln.node, chosen[i], cats.data() + chosen[i].cat_offset, ln.b, l, r, lb,
+                      rb);
+                const fbh_span ls = children[2 * req_of[i]], rs = children[2 * req_of[i] + 1];
+                Pending L{l, ls, {chosen[i].left[0], chosen[i].left[1]}, lb, 0, -1, -1, depth + 1};
+                Pending R{r, rs, {chosen[i].right[0], chosen[i].right[1]}, rb, 0, -1, -1,
+                          depth + 1};
+                // The smaller child is accumulated; the other takes over the
+                // parent's histogram slot: parent - sibling, in place.
+                const bool left_small = ls.len <= rs.len;
+                Pending &small = left_small ? L : R;
+                Pending &big = left_small ? R : L;
+                const uint32_t at = (uint32_t)next.size();
+                big.slot = ln.slot;
+                big.parent_slot = (int32_t)ln.slot;
+                big.sibling = (int32_t)(at + (left_small ? 0 : 1));
+                small.slot = UINT32_MAX;  // assigned below, after freed slots return
+                next.push_back(L);
+                next.push_back(R);
+            }
+            // Children that will be evaluated need a slot for the smaller one.
+            const bool evaluated = depth + 1 < p_.max_depth &&
+                                   !(p_.max_leaves != 0 && leaf_count >= p_.max_leaves);
+            for (auto &nd : next) {
+                if (nd.slot != UINT32_MAX) continue;
+                if (evaluated) nd.slot = take_slot();
+            }
+            if (!evaluated) {
+                for (auto &nd : next) {
+                    finish_leaf(t, nd.node, nd.rows);
+                    if (nd.parent_slot >= 0) give_slot(nd.slot);
+                }
+                return;
+            }
+            level = std::move(next);
+        }
+        for (auto &nd : level) {
+            finish_leaf(t, nd.node, nd.rows);
+            give_slot(nd.slot);
+        }
+    }
+
+    void lossguide(Tree &t, fbh_span root_rows, const int64_t root_sum[2]) {
+        struct Cand {
+            Pending leaf;
+            fbh_split split;
+            std::vector<uint64_t> cats;
+        };
+        auto less = [](const Cand &a, const Cand &b) {
+            if (a.split.gain != b.split.gain) return a.split.gain < b.split.gain;
+            return a.leaf.node > b.leaf.node;
+        };
+        std::priority_queue<Cand, std::vector<Cand>, decltype(less)> heap(less);
+        auto evaluate = [&](std::vector<Pending> batch) {
+            std::vector<fbh_split> res = eval(batch);
+            for (size_t i = 0; i < batch.size(); i++) {
+                if (res[i].found) {
+                    Cand c{batch[i], res[i], {}};
+                    if (res[i].is_cat)
+                        c.cats.assign(cat_words_.begin() + res[i].cat_offset,
+                                      cat_words_.begin() + res[i].cat_offset + res[i].n_cat_words);
+                    c.leaf.parent_slot = -1;
+                    c.leaf.sibling = -1;
+                    heap.push(std::move(c));
+                } else {
+                    finish_leaf(t, batch[i].node, batch[i].rows);
+                    give_slot(batch[i].slot);
+                }
+            }
+        };
+        Pending root{0, root_rows, {root_sum[0], root_sum[1]}, Bounds(), 0, -1, -1, 0};
+        if (p_.max_depth == 0 || p_.max_leaves == 1) {
+            finish_leaf(t, 0, root_rows);
+        } else {
+            root.slot = take_slot();
+            evaluate({root});
+        }
+        uint32_t leaf_count = 1;
+        while (p_.max_leaves == 0 || leaf_count < p_.max_leaves) {
+            if (heap.empty()) break;
+            Cand c = heap.top();
+            heap.pop();
+            fbh_part_req q = part_req(c.leaf, c.split, 0);
+            fbh_span ch[2];
+            call(fbh_partition(ctx_, &q, 1, c.cats.data(), (uint32_t)c.cats.size(), ch));
+            uint32_t l, r;
+            Bounds lb, rb;
+            apply(t, c.leaf.node, c.split, c.cats.data(), c.leaf.b, l, r, lb, rb);
+            leaf_count++;
+            const uint32_t depth = c.leaf.depth + 1;
+            Pending L{l, ch[0], {c.split.left[0], c.split.left[1]}, lb, 0, -1, -1, depth};
+            Pending R{r, ch[1], {c.split.right[0], c.split.right[1]}, rb, 0, -1, -1, depth};
+            if (depth == p_.max_depth || leaf_count == p_.max_leaves) {
+                finish_leaf(t, l, ch[0]);
+                finish_leaf(t, r, ch[1]);
+                give_slot(c.leaf.slot);
+                continue;
+            }
+            // lossguide.rs evaluate: the smaller child (left on ties) is
+            // accumulated, the other derived from the parent's histogram.
+            const bool left_small = !(ch[0].len > ch[1].len);
+            Pending &small = left_small ? L : R;
+            Pending &big = left_small ? R : L;
+            big.slot = c.leaf.slot;
+            big.parent_slot = (int32_t)c.leaf.slot;
+            big.sibling = 0;
+            small.slot = take_slot();
+            evaluate({small, big});
+        }
+        while (!heap.empty()) {
+            finish_leaf(t, heap.top().leaf.node, heap.top().leaf.rows);
+            give_slot(heap.top().leaf.slot);
+            heap.pop();
+        }
+    }
+
+    fbh_ctx *ctx_;
+    const fbt_params &p_;
+    const Cuts &cuts_;
+    const std::vector<int8_t> &mono_;
+    fbh_split_params sp_{};
+    LeafMath lm_{};
+    std::vector<uint32_t> free_;
+    std::vector<fbh_span> leaves_spans_;
+    std::vector<float> leaves_values_;
+    std::vector<uint64_t> cat_words_;
+    uint32_t cat_cap_ = 0;
+};
+
+void validate(const fbt_params &p, uint64_t n, uint32_t nf, const float *y) {
+    if (n == 0) throw InputError("training data must have at least one row");
+    if (n > 0xFFFFFFFFull)
+        throw InputError("training data has " + std::to_string(n) +
+                         " rows, above the supported limit 4294967295");
+    if (nf == 0) throw InputError("training data must have at least one feature");
+    if (p.objective > 1) throw InputError("objective must be reg:squarederror or binary:logistic");
+    if (p.grow_policy > 1) throw InputError("grow_policy must be depthwise or lossguide");
+    if (p.gpu_math != 0)
+        throw InputError("gpu_math=\"fast\" is not available in this build; use \"exact\"");
+    if (p.max_bin < 1 || p.max_bin > 65535)
+        throw InputError("max_bin must be in 1..=65535, got " + std::to_string(p.max_bin));
+    if (p.max_depth > 14)
+        throw InputError("max_depth must be in 0..=14, got " + std::to_string(p.max_depth) +
+                         "; 0 means a root-only tree");
+    auto nonneg = [](float v, const char *name) {
+        if (!(std::isfinite(v) && v >= 0.0f))
+            throw InputError(std::string(name) + " must be finite and non-negative");
+    };
+    nonneg(p.learning_rate, "learning_rate");
+    nonneg(p.lambda_, "lambda");
+    nonneg(p.gamma, "gamma");
+    nonneg(p.min_child_weight, "min_child_weight");
+    nonneg(p.alpha, "alpha");
+    nonneg(p.max_delta_step, "max_delta_step");
+    nonneg(p.scale_pos_weight, "scale_pos_weight");
+    if (!(p.subsample > 0.0f && p.subsample <= 1.0f))
+        throw InputError("subsample must be in (0, 1]");
+    if (!(p.colsample_bytree > 0.0f && p.colsample_bytree <= 1.0f))
+        throw InputError("colsample_bytree must be in (0, 1]");
+    if (p.cols_per_block == 0) throw InputError("cols_per_block must be > 0");
+    for (uint64_t i = 0; i < n; i++) {
+        if (!std::isfinite(y[i])) throw InputError("labels must all be finite");
+        if (p.objective == 1 && !(y[i] >= 0.0f && y[i] <= 1.0f))
+            throw InputError("training set: binary:logistic labels must be in [0, 1]");
+    }
+}
+
+fbt_stats g_stats{};
+
+}  // namespace
+
+fbt_stats last_stats() { return g_stats; }
+
+Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float *w,
+            const uint8_t *cat, const int8_t *mono_in, uint32_t n_mono, const fbt_params &p) {
+    const auto t_setup = Clock::now();
+    validate(p, n, nf, y);
+    if (n_mono > nf) throw InputError("monotone_constraints has more entries than features");
+    std::vector<int8_t> mono(nf, 0);
+    for (uint32_t i = 0; i < n_mono; i++) {
+        if (mono_in[i] < -1 || mono_in[i] > 1)
+            throw InputError("monotone_constraints accepts only -1 / 0 / 1");
+        mono[i] = mono_in[i];
+    }
+    if (w)
+        for (uint64_t i = 0; i < n; i++)
+            if (!(std::isfinite(w[i]) && w[i] >= 0.0f))
+                throw InputError("sample weights must be finite and non-negative");
+    if (!fbh_device_available(p.device))
+        throw RuntimeError("device cuda:" + std::to_string(p.device) +
+                           " is not an available gfx950 GPU; the device path has no CPU fallback");
+    const unsigned threads = p.nthread ? p.nthread : std::min(16u, std::max(1u, std::thread::hardware_concurrency()));
+    Pool pool(threads);
+
+    Model m;
+    m.objective = p.objective;
+    m.n_features = nf;
+    m.scale_pos_weight = p.scale_pos_weight;
+    m.cuts = sketch_matrix(x, n, nf, p.max_bin, w, cat, threads);
+    // Base score: explicit, else the (weighted) label mean
+    // (Objective::estimate_base_score, src/training/objective.rs:42-60, 452-470).
+    if (p.has_base_score) {
+        m.base_score = p.base_score;
+    } else {
+        if (p.scale_pos_weight != 1.0f)
+            throw InputError("scale_pos_weight != 1 requires an explicit base_score in this build");
+        double acc = 0.0;
+        if (!w) {
+            const double nn = (double)n;
+            for (uint64_t i = 0; i < n; i++) acc = acc + (double)y[i] / nn;
+            m.base_score = (float)acc;
+        } else {
+            double sw = 0.0;
+            for (uint64_t i = 0; i < n; i++) sw = sw + (double)w[i];
+            if (sw <= 0.0) {
+                m.base_score = 0.5f;
+            } else {
+                for (uint64_t i = 0; i < n; i++) acc = acc + (double)y[i] / sw * (double)w[i];
+                m.base_score = (float)acc;
+            }
+        }
+    }
+    if (p.objective == 1 && !(m.base_score >= 0.0f && m.base_score <= 1.0f))
+        throw InputError("logistic base_score is a probability and must be in [0, 1]");
+    const float margin = m.base_margin();
+
+    // scale_pos_weight folded into the gradient weights (mod.rs:5470-5496).
+    std::vector<float> gw;
+    const float *grad_w = w;
+    if (p.scale_pos_weight != 1.0f) {
+        gw.resize(n);
+        for (uint64_t i = 0; i < n; i++) {
+            const float wi = w ? w[i] : 1.0f;
+            gw[i] = y[i] == 1.0f ? wi * p.scale_pos_weight : wi;
+        }
+        grad_w = gw.data();
+    }
+
+    // ---- device context (allocates everything once) ----
+    std::vector<uint8_t> widths(nf);
+    std::vector<uint32_t> nbins(nf);
+    for (uint32_t f = 0; f < nf; f++) {
+        widths[f] = (uint8_t)m.cuts.width(f);
+        nbins[f] = m.cuts.n_bins(f);
+    }
+    fbh_shape shape{nf, widths.data(), nbins.data(), m.cuts.categorical.data()};
+    fbh_config cfg{};
+    cfg.memory_budget = p.gpu_memory_budget;
+    cfg.tile_bytes = p.tile_bytes;
+    cfg.rows_per_block = p.rows_per_block;
+    uint32_t slots;
+    if (p.grow_policy == 1) {
+        const uint64_t leaves = p.max_leaves ? p.max_leaves : (1ull << std::min(p.max_depth, 14u));
+        slots = (uint32_t)std::min<uint64_t>(leaves + 2, 16384);
+    } else {
+        slots = 1u << (p.max_depth > 0 ? p.max_depth - 1 : 0);
+        if (p.max_leaves) slots = std::min(slots, p.max_leaves + 1);
+        slots = std::max(slots, 2u);
+    }
+    cfg.hist_slots = slots;
+    fbh_ctx *raw = nullptr;
+    call(fbh_ctx_create(p.device, n, &shape, &cfg, &raw));
+    std::unique_ptr<fbh_ctx, int (*)(fbh_ctx *)> ctx(raw, fbh_ctx_destroy);
+    call(fbh_set_timing(ctx.get(), p.profile ? 1 : 0));
+    for (const auto &feats : blocks_by_width(m.cuts, p.cols_per_block)) {
+        const uint32_t wdt = m.cuts.width(feats[0]);
+        std::vector<uint8_t> buf((size_t)feats.size() * n * wdt);
+        bin_columns(x, n, nf, m.cuts, feats, wdt, buf.data(), threads);
+        call(fbh_upload_block(ctx.get(), feats.data(), (uint32_t)feats.size(), wdt, buf.data()));
+    }
+    g_stats = fbt_stats{};
+    g_stats.device_bytes = (double)fbh_ctx_device_bytes(ctx.get());
+    g_stats.setup_seconds = std::chrono::duration<double>(Clock::now() - t_setup).count();
+
+    // ---- round loop ----
+    const auto t_train = Clock::now();
+    std::vector<float> pred(n, margin), delta(n), g2(2 * n);
+    Grower grower(ctx.get(), p, m.cuts, mono, slots);
+    grower.n_rows_ = (uint32_t)n;
+    const uint32_t obj = p.objective;
+    double grad_s = 0.0;
+    for (uint32_t round = 0; round < p.n_rounds; round++) {
+        const auto tg = Clock::now();
+        if (round > 0) call(fbh_download_delta(ctx.get(), delta.data()));
+        const bool apply_delta = round > 0;
+        pool.run([&](unsigned t) {
+            const uint64_t lo = n * t / pool.size(), hi = n * (t + 1) / pool.size();
+            for (uint64_t i = lo; i < hi; i++) {
+                if (apply_delta) pred[i] += delta[i];
+                const float pi = pred[i];
+                float g, h;
+                if (obj == 1) {  // Objective::gradient, binary:logistic
+                    const float s = 1.0f / (1.0f + std::exp(-pi));
+                    g = s - y[i];
+                    h = std::fmax(s * (1.0f - s), 1e-16f);
+                } else {
+                    g = pi - y[i];
+                    h = 1.0f;
+                }
+                if (grad_w) {
+                    g = g * grad_w[i];
+                    h = h * grad_w[i];
+                }
+                g2[2 * i] = g;
+                g2[2 * i + 1] = h;
+            }
+        });
+        grad_s += std::chrono::duration<double>(Clock::now() - tg).count();
+        double scales[2];
+        int64_t root_sum[2];
+        call(fbh_upload_quantize_gpair(ctx.get(), g2.data(), sample_threshold(p.subsample), p.seed,
+                                       round, scales, root_sum));
+        std::vector<uint32_t> feats;
+        if (p.colsample_bytree < 1.0f) feats = sample_columns(nf, p.colsample_bytree, p.seed, round);
+        fbh_span root;
+        call(fbh_begin_tree(ctx.get(), feats.empty() ? nullptr : feats.data(),
+                            (uint32_t)feats.size(), mono.data(), nf, &root));
+        m.trees.push_back(grower.grow(scales, root_sum));
+    }
+    if (p.n_rounds > 0) {
+        call(fbh_download_delta(ctx.get(), delta.data()));
+        pool.run([&](unsigned t) {
+            const uint64_t lo = n * t / pool.size(), hi = n * (t + 1) / pool.size();
+            for (uint64_t i = lo; i < hi; i++) pred[i] += delta[i];
+        });
+    }
+    g_stats.train_seconds = std::chrono::duration<double>(Clock::now() - t_train).count();
+    g_stats.host_gradient_seconds = grad_s;
+    g_stats.rounds = p.n_rounds;
+    double ms = 0.0;
+    uint64_t launches = 0, bytes = 0;
+    call(fbh_hist_timing(ctx.get(), &ms, &launches, &bytes, 0));
+    g_stats.hist_kernel_ms = ms;
+    g_stats.hist_launches = launches;
+    g_stats.hist_bytes = bytes;
+    m.train_margins = std::move(pred);
+    return m;
+}
+
+}  // namespace fbt

@@ -1,0 +1,263 @@
+/* fbhip.h -- C ABI of the MI355X (gfx950) training and explanation backend.
+ *
+ * This is the drop-in boundary for FerrisBoost's device="cuda" path. The
+ * reference binds its device backend through the Rust API of
+ * src/backend/cuda/{train_ctx.rs,split_ctx.rs,explain.rs,mod.rs}; every
+ * entry point below names the reference function it replaces. Signatures
+ * carry plain pointers and sizes only: host buffers are borrowed for the
+ * duration of the call, device memory is owned by the context and allocated
+ * once at creation (worst case, like GpuTrainCtx::new_with_shape).
+ *
+ * Status codes: FBH_OK (0), FBH_INPUT_ERROR (1, the reference's InputError,
+ * ValueError in Python, src/error.rs:1-68) and FBH_RUNTIME_ERROR (2).
+ * fbh_last_error() returns the message of the last failure on the calling
+ * thread. No call panics, aborts or throws across the boundary.
+ *
+ * Threading: one context is used by one host thread at a time; all device
+ * work of a context runs in order on the context's single HIP stream.
+ */
+#ifndef FBHIP_H
+#define FBHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { FBH_OK = 0, FBH_INPUT_ERROR = 1, FBH_RUNTIME_ERROR = 2 };
+
+typedef struct fbh_ctx fbh_ctx;
+
+/* A contiguous run of the device row arena: GpuRowSpan
+ * (src/backend/cuda/train_ctx.rs, used by src/training/mod.rs:3253-3281). */
+typedef struct {
+    uint32_t offset;
+    uint32_t len;
+} fbh_span;
+
+/* Feature shape of the training matrix: GpuBlockShape
+ * (src/training/gpu_mem_plan.rs:95-144) flattened per feature. width[f] is
+ * the stored bin width in bytes (1 = u8, 2 = u16), n_bins[f] the histogram
+ * bins of feature f (cuts + 1), categorical[f] != 0 marks a categorical
+ * feature (may be NULL). */
+typedef struct {
+    uint32_t n_features;
+    const uint8_t *width;
+    const uint32_t *n_bins;
+    const uint8_t *categorical;
+} fbh_shape;
+
+/* Context options: SharedHistogramConfig (src/backend/cuda/mod.rs:84-208)
+ * re-derived for MI355X. Zero selects the default of each field. */
+typedef struct {
+    uint64_t memory_budget;  /* bytes the context may allocate; 0 = free HBM
+                                minus the safety reserve (gpu_memory_budget) */
+    uint32_t hist_slots;     /* node histograms kept on the device at once */
+    uint32_t tile_bytes;     /* LDS bytes of one histogram tile (<= 160 KiB) */
+    uint32_t rows_per_block; /* rows one histogram workgroup accumulates */
+    uint32_t max_cat_words;  /* 64-bit words of the widest category set */
+    uint32_t reserved[6];
+} fbh_config;
+
+/* Split-scan parameters: the TrainParams fields split.rs reads
+ * (src/training/split.rs:113-270, src/types.rs:432-660). */
+typedef struct {
+    float lambda_;
+    float gamma;
+    float min_child_weight;
+    float alpha;
+    float max_delta_step;
+    uint32_t max_cat_to_onehot;
+    uint32_t max_cat_threshold;
+    uint32_t reserved;
+} fbh_split_params;
+
+/* One node handed to the split scan: a LevelNode (src/training/mod.rs:3239)
+ * plus its histogram source (HistFrom, src/training/mod.rs:3283-3291).
+ * subtract_parent < 0: accumulate the node's rows into `slot`; otherwise
+ * slot = histogram(subtract_parent) - histogram(subtract_sibling), where the
+ * sibling is accumulated by an earlier entry of the same call. */
+typedef struct {
+    fbh_span rows;
+    int64_t sum[2];  /* fixed-point node sum, missing rows included */
+    float lower;     /* NodeBounds (src/training/split.rs:120-160) */
+    float upper;
+    uint32_t slot;
+    int32_t subtract_parent;
+    int32_t subtract_sibling;
+    uint32_t reserved;
+} fbh_node;
+
+/* The chosen split of one node: SplitCandidate
+ * (src/training/split.rs:17-52), 64 bytes like the reference's packet
+ * (src/backend/cuda/histogram.cu:6-11). Categorical sets are returned in a
+ * separate word array at cat_offset (64-bit words, bit c of word c/64 set =
+ * category c goes right). */
+typedef struct {
+    uint32_t found;
+    uint32_t feat;
+    uint32_t bin;
+    uint32_t missing_left;
+    float gain;
+    uint32_t is_cat;
+    uint32_t cat_offset;
+    uint32_t n_cat_words;
+    int64_t left[2];
+    int64_t right[2];
+} fbh_split;
+
+/* One stable partition request (GpuPartitionSession::partition /
+ * partition_categorical, src/backend/cuda/train_ctx.rs:4849-5500). */
+typedef struct {
+    fbh_span rows;
+    uint32_t feat;
+    uint32_t bin;          /* rows with bin < this go left (numeric) */
+    uint32_t missing_left;
+    uint32_t cat_offset;   /* into the category words passed alongside */
+    uint32_t n_cat_words;  /* 0 = numeric split */
+    uint32_t reserved;
+} fbh_part_req;
+
+/* ---------------------------------------------------------------- errors */
+/* Copies the last error message of this thread (NUL-terminated). Returns its
+ * full length. */
+size_t fbh_last_error(char *buf, size_t len);
+/* 1 when a usable gfx950 device is present, 0 otherwise (never errors). */
+int fbh_device_available(int device);
+
+/* ------------------------------------------------------------ lifecycle */
+/* GpuTrainCtx::new_with_shape (src/backend/cuda/train_ctx.rs:728-1769):
+ * allocates every device buffer of the run once. */
+int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fbh_config *cfg,
+                   fbh_ctx **out);
+/* Drop of GpuTrainCtx. */
+int fbh_ctx_destroy(fbh_ctx *ctx);
+/* GpuTrainCtx::budget (src/backend/cuda/train_ctx.rs:103-242): bytes the
+ * context holds on the device. */
+uint64_t fbh_ctx_device_bytes(const fbh_ctx *ctx);
+
+/* --------------------------------------------------------------- blocks */
+/* GpuTrainCtx::block_session_bins / resident block upload
+ * (src/backend/cuda/train_ctx.rs:3507-4052): one ColumnBlock
+ * (src/data/columns.rs:9-46), column-major data[local * n_rows + row] of
+ * `width` bytes per cell, features feat_ids[0..n_feats). The device re-lays
+ * it into LDS-sized tiles of row records. */
+int fbh_upload_block(fbh_ctx *ctx, const uint32_t *feat_ids, uint32_t n_feats, uint32_t width,
+                     const void *bins);
+
+/* ------------------------------------------------------------ gradients */
+/* GpuTrainCtx::upload_and_quantize_gpair_sampled
+ * (src/backend/cuda/train_ctx.rs:2345-2391, 3182-3343): uploads interleaved
+ * f32 [grad, hess] per row, masks rows the sampler drops
+ * (threshold from subsample::threshold_for; UINT64_MAX keeps all), picks the
+ * power-of-two scales (GradQuantizer::try_from_bounds) and writes the i64
+ * fixed-point pairs. Returns the scales and the fixed-point root sum. */
+int fbh_upload_quantize_gpair(fbh_ctx *ctx, const float *gpair2n, uint64_t sample_threshold,
+                              uint64_t seed, uint64_t tree, double scales_out[2],
+                              int64_t root_sum_out[2]);
+/* GpuTrainCtx::upload_gpair: fixed-point pairs quantized on the host. */
+int fbh_upload_gpair_fixed(fbh_ctx *ctx, const int64_t *gpair2n, const double scales[2]);
+
+/* ------------------------------------------------------------------ tree */
+/* GpuTrainCtx::begin_tree_rows (src/backend/cuda/train_ctx.rs:1971-1993) plus
+ * the tree's column plan (BlockPlan, src/training/mod.rs:3302-3463): resets
+ * the row arena to 0..n_rows, zeroes the prediction delta and selects the
+ * features whose histograms this tree builds (ascending global ids; NULL =
+ * all features). Returns the root span. */
+int fbh_begin_tree(fbh_ctx *ctx, const uint32_t *features, uint32_t n_features,
+                   const int8_t *monotone, uint32_t n_monotone, fbh_span *root);
+
+/* GpuBlockSession::split_cached_submit / split_cached_finish
+ * (src/backend/cuda/split_ctx.rs:387-960) over every selected feature:
+ * builds the histograms of the accumulate nodes in one batched launch
+ * (hist_build_shared_planar32_batched, histogram.cu:1685-1852), derives the
+ * subtract nodes (sibling subtraction), runs the split scan per
+ * (node, feature) and the per-node argmax with the reference's tie rules
+ * (split.rs:260-270, 631-642). enabled[i*n_features_tree + j] (may be NULL)
+ * masks feature j of the tree for node i. Category sets of categorical
+ * winners are copied to cat_words (capacity cat_capacity 64-bit words). */
+int fbh_eval_nodes(fbh_ctx *ctx, const fbh_node *nodes, uint32_t n_nodes,
+                   const fbh_split_params *params, const uint8_t *enabled, fbh_split *out,
+                   uint64_t *cat_words, uint32_t cat_capacity);
+
+/* Copies the histogram of a slot to the host (download_histograms,
+ * src/backend/cuda/train_ctx.rs:4770-4817): 2 * width int64, in the tree's
+ * compact feature order. Returns the width through width_out when out is
+ * NULL. */
+int fbh_download_histogram(fbh_ctx *ctx, uint32_t slot, int64_t *out, uint64_t *width_out);
+
+/* GpuPartitionSession::partition_resident_multi + resolve_partitions
+ * (src/backend/cuda/train_ctx.rs:4893-5196, 2007-2055): stable partition of
+ * every requested span (left rows keep their order, then right rows keep
+ * theirs) in place, one blocking copy of the left counts. children receives
+ * (left, right) per request. */
+int fbh_partition(fbh_ctx *ctx, const fbh_part_req *reqs, uint32_t n_reqs,
+                  const uint64_t *cat_words, uint32_t n_cat_words, fbh_span *children);
+
+/* GpuTrainCtx::assign_leaf_values (src/backend/cuda/train_ctx.rs:2128-2252):
+ * delta[row] = value for every row of each span. */
+int fbh_assign_leaves(fbh_ctx *ctx, const fbh_span *spans, const float *values, uint32_t n);
+
+/* GpuTrainCtx::download_prediction_delta (src/backend/cuda/train_ctx.rs:2215-2236). */
+int fbh_download_delta(fbh_ctx *ctx, float *out);
+/* The current row arena (tests and diagnostics). */
+int fbh_download_rows(fbh_ctx *ctx, uint32_t *out);
+
+/* Device time of the histogram kernels since creation or the last reset, in
+ * milliseconds, and their launch count (HIP events on the context stream). */
+int fbh_hist_timing(fbh_ctx *ctx, double *ms_out, uint64_t *launches_out, uint64_t *bytes_out,
+                    int reset);
+/* Enables HIP-event timing of histogram launches (off by default). */
+int fbh_set_timing(fbh_ctx *ctx, int enabled);
+
+/* ---------------------------------------------- standalone characterization */
+/* build_histogram (src/backend/cuda/mod.rs:241-497): one histogram over a
+ * column-major block and a row subset (rows == NULL: all rows), on host
+ * buffers. out must hold 2 * offsets[n_feats] int64. */
+int fbh_build_histogram(int device, const void *bins, uint32_t width, uint64_t n_rows,
+                        uint32_t n_feats, const uint32_t *offsets, const int64_t *gpair2n,
+                        const uint32_t *rows, uint64_t n_sel, int64_t *out);
+/* partition_rows_gpu (src/backend/cuda/mod.rs:848-892): stable partition of
+ * rows by one column, on host buffers. Returns the left count. */
+int fbh_partition_rows(int device, const void *col, uint32_t width, uint64_t n_rows,
+                       const uint32_t *rows, uint64_t n, uint32_t split_bin,
+                       uint32_t missing_left, const uint64_t *cat_words, uint32_t n_cat_words,
+                       uint32_t *out, uint64_t *n_left);
+
+/* ------------------------------------------------------------ TreeSHAP */
+typedef struct fbh_shap_model fbh_shap_model;
+
+/* GpuExplainModel::new (src/backend/cuda/explain.rs:186-490): flattened
+ * single-output ensemble. Node arrays are indexed by the global node id;
+ * tree_offsets[t] is the first node of tree t (n_trees + 1 entries).
+ * left/right are tree-local child ids (-1 for leaves), cat_offset/cat_len
+ * index cat_words (32-bit words; cat_len 0 = numeric). bias is the model's
+ * margin-space base score. */
+int fbh_shap_model_create(int device, uint32_t n_trees, const uint32_t *tree_offsets,
+                          const uint32_t *feat, const float *split_cond, const int32_t *left,
+                          const int32_t *right, const uint8_t *default_left,
+                          const uint8_t *is_leaf, const float *leaf_value,
+                          const float *sum_hess, const uint32_t *cat_offset,
+                          const uint32_t *cat_len, const uint32_t *cat_words,
+                          uint32_t n_cat_words, uint32_t n_features, float bias,
+                          fbh_shap_model **out);
+int fbh_shap_model_destroy(fbh_shap_model *m);
+/* GpuExplainModel::compute (src/backend/cuda/explain.rs:491-843) for
+ * pred_contribs: rows row-major [n_rows][n_features], optional per-row
+ * margin replacing the bias, out [n_rows][n_features + 1]. */
+int fbh_shap_contribs(fbh_shap_model *m, const float *rows, uint64_t n_rows,
+                      const float *margin, float *out);
+/* Same on device-resident buffers (no host copies): d_rows and d_out are
+ * device pointers; the call is asynchronous on the model's stream when
+ * sync == 0. */
+int fbh_shap_contribs_device(fbh_shap_model *m, const float *d_rows, uint64_t n_rows,
+                             const float *d_margin, float *d_out, int sync);
+/* Milliseconds of the last fbh_shap_contribs_device kernel (HIP events). */
+double fbh_shap_last_ms(const fbh_shap_model *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FBHIP_H */

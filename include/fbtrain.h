@@ -1,0 +1,136 @@
+/* fbtrain.h -- C ABI of the host round driver (libfbtrain.so).
+ *
+ * The driver is the restated training state machine of FerrisBoost's
+ * device="cuda" path: train_with_backend (src/training/mod.rs:1299-2376),
+ * build_tree (src/training/mod.rs:3357-4565) and lossguide::grow
+ * (src/training/lossguide.rs:494-700). It prepares the data exactly like
+ * DenseSource (sketch -> cuts -> u8/u16 column blocks,
+ * src/source/dense.rs:99-290), computes exact-mode gradients on the host
+ * (gpu_math="exact", src/training/mod.rs:2033-2087) and runs every
+ * histogram, split scan, partition and leaf scatter through the fbh_*
+ * backend (fbhip.h). It never falls back to a CPU histogram or split path:
+ * without a usable device, fbt_train fails with FBH_RUNTIME_ERROR.
+ *
+ * Status codes as fbhip.h (0 ok, 1 input error, 2 runtime error).
+ */
+#ifndef FBTRAIN_H
+#define FBTRAIN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Training parameters: TrainParams (src/types.rs:432-660) and the Python
+ * parameter surface (python/ferrisboost/__init__.py:46-200). */
+typedef struct {
+    uint32_t n_rounds;
+    uint32_t max_depth;
+    uint32_t max_leaves;
+    uint32_t max_bin;
+    float learning_rate;
+    float lambda_;
+    float gamma;
+    float min_child_weight;
+    float alpha;
+    float max_delta_step;
+    float scale_pos_weight;
+    float subsample;
+    float colsample_bytree;
+    uint32_t cols_per_block;
+    uint64_t seed;
+    uint32_t objective;        /* 0 = reg:squarederror, 1 = binary:logistic */
+    uint32_t grow_policy;      /* 0 = depthwise, 1 = lossguide */
+    uint32_t max_cat_to_onehot;
+    uint32_t max_cat_threshold;
+    float base_score;          /* used when has_base_score != 0 */
+    uint32_t has_base_score;
+    uint32_t nthread;          /* host threads (0 = up to 16) */
+    uint32_t reserved;
+    /* device-path knobs */
+    int32_t device;            /* "cuda:N" */
+    uint32_t gpu_math;         /* 0 = exact (only mode of this build) */
+    uint64_t gpu_memory_budget;/* bytes, 0 = automatic */
+    uint32_t tile_bytes;       /* LDS histogram tile (0 = default) */
+    uint32_t rows_per_block;   /* histogram rows per workgroup (0 = default) */
+    uint32_t profile;          /* 1: time histogram kernels with HIP events */
+    uint32_t reserved2[3];
+} fbt_params;
+
+/* One tree node: Node (src/model/tree.rs:52-111). */
+typedef struct {
+    uint32_t feat;
+    float split_cond;
+    int32_t left;
+    int32_t right;
+    uint8_t default_left;
+    uint8_t is_leaf;
+    uint16_t pad;
+    float leaf_value;
+    float gain;
+    float sum_hess;
+    uint32_t cat_begin;
+    uint32_t cat_len;
+} fbt_node;
+
+/* Timing of the last training call. */
+typedef struct {
+    double train_seconds;     /* the round loop (gradients .. leaf deltas) */
+    double setup_seconds;     /* sketch, binning, context, upload */
+    double hist_kernel_ms;    /* histogram kernels (HIP events; profile=1) */
+    uint64_t hist_launches;
+    uint64_t hist_bytes;      /* algorithmic bytes of the histogram launches */
+    double host_gradient_seconds;
+    double device_bytes;      /* bytes the backend context holds */
+    uint32_t rounds;
+    uint32_t reserved;
+} fbt_stats;
+
+typedef struct fbt_model fbt_model;
+
+size_t fbt_last_error(char *buf, size_t len);
+
+/* fb.train(params, X, label, weight) on the device path. x is row-major
+ * [n_rows][n_features] f32 (NaN = missing), categorical[f] != 0 marks
+ * categorical features, monotone holds per-feature -1/0/1 constraints. */
+int fbt_train(const float *x, uint64_t n_rows, uint32_t n_features, const float *labels,
+              const float *weights, const uint8_t *categorical, const int8_t *monotone,
+              uint32_t n_monotone, const fbt_params *params, fbt_model **out);
+int fbt_last_stats(fbt_stats *out);
+
+void fbt_model_free(fbt_model *m);
+uint32_t fbt_model_n_trees(const fbt_model *m);
+uint32_t fbt_model_tree_len(const fbt_model *m, uint32_t tree);
+void fbt_model_tree_nodes(const fbt_model *m, uint32_t tree, fbt_node *out);
+uint32_t fbt_model_n_cat_words(const fbt_model *m);
+void fbt_model_cat_words(const fbt_model *m, uint32_t *out);
+float fbt_model_base_score(const fbt_model *m);
+float fbt_model_base_margin(const fbt_model *m);
+uint32_t fbt_model_n_features(const fbt_model *m);
+/* Training-set margins the round loop accumulated (n_rows floats). */
+int fbt_model_train_margins(const fbt_model *m, float *out, uint64_t n_rows);
+/* Cuts the model was trained with (values, offsets n_features + 1). */
+uint32_t fbt_model_n_cuts(const fbt_model *m);
+void fbt_model_cuts(const fbt_model *m, float *values, uint32_t *offsets);
+/* Model::predict_margin (src/model/tree.rs:486-510) on row-major rows. */
+void fbt_predict_margin(const fbt_model *m, const float *x, uint64_t n_rows, uint32_t n_features,
+                        float *out);
+/* XGBoost-schema JSON (Model::to_xgboost_json, src/model/tree.rs:600-760).
+ * Returns the length; writes at most len bytes (NUL-terminated) when buf. */
+size_t fbt_model_to_json(const fbt_model *m, char *buf, size_t len);
+/* pred_contribs on the device (GpuExplainModel): out [n_rows][n_features+1]. */
+int fbt_shap(const fbt_model *m, const float *x, uint64_t n_rows, uint32_t n_features,
+             int device, float *out);
+
+/* Sketch cuts and bins exactly as training does (tests / diagnostics).
+ * cut_values holds n_features * max(max_bin, 2) floats. */
+int fbt_sketch_cuts(const float *x, uint64_t n_rows, uint32_t n_features, uint32_t max_bin,
+                    const float *weights, const uint8_t *categorical, float *cut_values,
+                    uint32_t *cut_offsets);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FBTRAIN_H */

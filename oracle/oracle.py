@@ -295,7 +295,10 @@ def train(x, y, params: Params, weights=None, categorical=None, monotone=None) -
 def sketch_cuts(x, max_bin, weights=None, categorical=None):
     x = np.ascontiguousarray(x, np.float32)
     n, nf = x.shape
-    vals = np.zeros(nf * max(max_bin, 2) + 1, np.float32)
+    # numeric features emit < max_bin cuts; categorical ones one per code
+    cap = sum(65534 if (categorical is not None and categorical[f]) else max(max_bin, 2)
+              for f in range(nf))
+    vals = np.zeros(cap + 1, np.float32)
     offs = np.zeros(nf + 1, np.uint32)
     w = None if weights is None else np.ascontiguousarray(weights, np.float32)
     cat = None if categorical is None else np.ascontiguousarray(categorical, np.uint8)

@@ -1,0 +1,229 @@
+"""GPU parity: the HIP path against the CPU oracle, through the C ABI.
+
+Integer work (histograms, partitions, node sums, split packets, trees) must
+be bit-identical; margins are compared bit for bit with the oracle and with
+the reference's XGBoost-3.4.1 golden margins.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from helpers import (assert_same_models, case_params, golden_cases, load_case,
+                     product_params)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def fb():
+    import ferrisboost_amd as fb
+    from ferrisboost_amd import _native as N
+
+    if not N.device_available(0):
+        pytest.fail("no gfx950 device: the GPU suite needs an MI355X")
+    return fb
+
+
+@pytest.fixture(scope="module")
+def N(fb):
+    from ferrisboost_amd import _native as N
+
+    return N
+
+
+def _device_hist(N, bins, offsets, gpair, rows=None):
+    bins = np.ascontiguousarray(bins)
+    nf, n = bins.shape
+    out = np.zeros(2 * int(offsets[-1]), np.int64)
+    r = None if rows is None else np.ascontiguousarray(rows, np.uint32)
+    N.check_hip(N.hip().fbh_build_histogram(
+        0, N.ptr(bins), bins.dtype.itemsize, n, nf, N.ptr(np.ascontiguousarray(offsets, np.uint32)),
+        N.ptr(np.ascontiguousarray(gpair, np.int64)), N.ptr(r), 0 if r is None else r.size,
+        N.ptr(out)))
+    return out
+
+
+@pytest.mark.parametrize("width", [1, 2])
+@pytest.mark.parametrize("n_feats", [1, 3, 7, 28, 63])
+def test_histogram_matches_oracle(N, oracle, width, n_feats):
+    rng = np.random.default_rng(100 + n_feats * 3 + width)
+    n = 4203
+    n_bins = rng.integers(1, 255 if width == 1 else 1200, size=n_feats)
+    offsets = np.concatenate([[0], np.cumsum(n_bins)]).astype(np.uint32)
+    dtype = np.uint8 if width == 1 else np.uint16
+    miss = 0xFF if width == 1 else 0xFFFF
+    bins = np.empty((n_feats, n), dtype)
+    for f in range(n_feats):
+        b = rng.integers(0, n_bins[f], size=n)
+        b[rng.random(n) < 0.1] = miss
+        bins[f] = b
+    big = 1 << 42
+    g = rng.integers(-big, big, size=n)
+    h = rng.integers(0, big, size=n)
+    gpair = np.stack([g, h], axis=1).reshape(-1).astype(np.int64)
+    for rows in (None, np.sort(rng.choice(n, size=n // 7, replace=False)),
+                 np.array([0, 4202, 0, 2048, 2048, 17], np.uint32), np.array([2047], np.uint32)):
+        got = _device_hist(N, bins, offsets, gpair, rows)
+        want = oracle.hist_build(bins, offsets, gpair, rows)
+        assert np.array_equal(got, want)
+
+
+def test_histogram_wide_features_use_global_path(N, oracle):
+    # 16-bit features whose histogram exceeds an LDS tile, mixed with small ones.
+    rng = np.random.default_rng(55)
+    n = 20_000
+    n_bins = np.array([5000, 7, 60000, 300], np.int64)
+    offsets = np.concatenate([[0], np.cumsum(n_bins)]).astype(np.uint32)
+    bins = np.empty((4, n), np.uint16)
+    for f in range(4):
+        b = rng.integers(0, n_bins[f], size=n)
+        b[rng.random(n) < 0.05] = 0xFFFF
+        bins[f] = b
+    gpair = rng.integers(-(1 << 40), 1 << 40, size=2 * n).astype(np.int64)
+    for rows in (None, np.sort(rng.choice(n, 3000, replace=False)).astype(np.uint32)):
+        got = _device_hist(N, bins, offsets, gpair, rows)
+        assert np.array_equal(got, oracle.hist_build(bins, offsets, gpair, rows))
+
+
+def test_histogram_low_word_carry(N, oracle):
+    # Values whose low 32 bits overflow when summed: exact 64-bit wrapping sums.
+    n = 9000
+    bins = np.zeros((1, n), np.uint8)
+    bins[0] = np.arange(n) % 3
+    v = np.full(n, (1 << 32) - 1, np.int64)
+    gpair = np.stack([v, v // 3], axis=1).reshape(-1)
+    offsets = np.array([0, 3], np.uint32)
+    got = _device_hist(N, bins, offsets, gpair)
+    assert np.array_equal(got, oracle.hist_build(bins, offsets, gpair))
+    # wrapping: near i64 limits
+    v2 = np.full(n, (1 << 62), np.int64)
+    gpair2 = np.stack([v2, -v2], axis=1).reshape(-1)
+    got2 = _device_hist(N, bins, offsets, gpair2)
+    assert np.array_equal(got2, oracle.hist_build(bins, offsets, gpair2))
+
+
+@pytest.mark.parametrize("width", [1, 2])
+def test_partition_matches_oracle(N, oracle, width):
+    rng = np.random.default_rng(7 + width)
+    n = 10_037
+    nb = 200 if width == 1 else 3000
+    dtype = np.uint8 if width == 1 else np.uint16
+    miss = 0xFF if width == 1 else 0xFFFF
+    col = rng.integers(0, nb, size=n).astype(dtype)
+    col[rng.random(n) < 0.15] = miss
+    for rows in (np.arange(n, dtype=np.uint32), np.sort(rng.choice(n, 5000, replace=False)).astype(np.uint32)):
+        for split_bin, ml in ((0, True), (nb // 3, False), (nb // 3, True), (nb, False)):
+            out = np.zeros_like(rows)
+            nl = C.c_uint64()
+            N.check_hip(N.hip().fbh_partition_rows(0, N.ptr(col), width, n, N.ptr(rows), rows.size,
+                                                   split_bin, int(ml), None, 0, N.ptr(out),
+                                                   C.byref(nl)))
+            want, wl = oracle.partition(rows, col, split_bin, ml)
+            assert nl.value == wl
+            assert np.array_equal(out, want)
+        # categorical set
+        cats = np.zeros((nb + 63) // 64, np.uint64)
+        for c in rng.choice(nb, nb // 4, replace=False):
+            cats[c >> 6] |= np.uint64(1) << np.uint64(c & 63)
+        out = np.zeros_like(rows)
+        nl = C.c_uint64()
+        N.check_hip(N.hip().fbh_partition_rows(0, N.ptr(col), width, n, N.ptr(rows), rows.size, 0,
+                                               1, N.ptr(cats), cats.size, N.ptr(out), C.byref(nl)))
+        want, wl = oracle.partition(rows, col, 0, True, cats)
+        assert nl.value == wl and np.array_equal(out, want)
+
+
+CASES = golden_cases()
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c["name"] for c in CASES])
+def test_golden_training_is_bit_exact(fb, oracle, case):
+    x, y, w, want = load_case(case)
+    p = case_params(case)
+    mono = case.get("monotone_constraints")
+    om = oracle.train(x, y, oracle.make_params(**p), weights=w, monotone=mono)
+    pp = product_params(p)
+    if mono:
+        pp["monotone_constraints"] = mono
+    pm = fb.train(pp, x, y, weight=w, num_boost_round=p["n_rounds"])
+    assert_same_models(om, pm)
+    got = pm.predict(x, output_margin=True)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(pm.train_margins(x.shape[0]).view(np.uint32),
+                          om.train_margins(x.shape[0]).view(np.uint32))
+
+
+def _synthetic(kind, n):
+    from ferrisboost_amd import datasets
+
+    return getattr(datasets, kind)(n)
+
+
+@pytest.mark.parametrize("max_bin", [255, 256])
+def test_plumbing_config_matches_oracle(fb, oracle, max_bin):
+    X, y, params, _ = _synthetic("plumbing", 30_000)
+    params = dict(params, max_bin=max_bin)
+    rounds = 12
+    om = oracle.train(X, y, oracle.make_params(n_rounds=rounds, **params))
+    pm = fb.train(params, X, y, num_boost_round=rounds)
+    assert_same_models(om, pm)
+    assert np.array_equal(pm.train_margins(X.shape[0]), om.train_margins(X.shape[0]))
+
+
+def test_wide_colsample_matches_oracle(fb, oracle):
+    from ferrisboost_amd import datasets
+
+    X, y, params, _ = datasets.wide_binary(6_000, n_features=300)
+    rounds = 6
+    params = dict(params, max_depth=6)
+    om = oracle.train(X, y, oracle.make_params(n_rounds=rounds, **params))
+    pm = fb.train(params, X, y, num_boost_round=rounds)
+    assert_same_models(om, pm)
+
+
+def test_lossguide_categorical_matches_oracle(fb, oracle):
+    from ferrisboost_amd import datasets
+
+    X, y, params, _ = datasets.widebin_cat(20_000, n_num=12, n_cat=4, n_codes=500)
+    # one low-cardinality categorical column takes the one-hot path
+    X[:, -1] = np.floor(X[:, -1]) % 3
+    rounds = 5
+    params = dict(params, max_leaves=31, max_bin=300)
+    cat = [1 if t == "c" else 0 for t in params["feature_types"]]
+    op = {k: v for k, v in params.items() if k != "feature_types"}
+    om = oracle.train(X, y, oracle.make_params(n_rounds=rounds, **op), categorical=cat)
+    pm = fb.train(params, X, y, num_boost_round=rounds)
+    assert_same_models(om, pm)
+    assert np.array_equal(pm.train_margins(X.shape[0]), om.train_margins(X.shape[0]))
+
+
+def test_depthwise_categorical_partition_path(fb, oracle):
+    from ferrisboost_amd import datasets
+
+    X, y, params, _ = datasets.widebin_cat(15_000, n_num=6, n_cat=3, n_codes=40)
+    params = dict(params, grow_policy="depthwise", max_depth=5, max_leaves=0, max_bin=64,
+                  max_cat_threshold=8)
+    cat = [1 if t == "c" else 0 for t in params["feature_types"]]
+    op = {k: v for k, v in params.items() if k != "feature_types"}
+    om = oracle.train(X, y, oracle.make_params(n_rounds=4, **op), categorical=cat)
+    pm = fb.train(params, X, y, num_boost_round=4)
+    assert_same_models(om, pm)
+
+
+def test_shap_matches_oracle_and_is_additive(fb, oracle):
+    X, y, params, _ = _synthetic("plumbing", 8_000)
+    X[::7, 3] = np.nan
+    rounds = 8
+    om = oracle.train(X, y, oracle.make_params(n_rounds=rounds, **params))
+    pm = fb.train(params, X, y, num_boost_round=rounds)
+    assert_same_models(om, pm)
+    rows = X[:2000]
+    got = pm.predict(rows, pred_contribs=True)
+    want = om.shap(rows)
+    assert np.max(np.abs(got - want)) <= 1e-5
+    margin = pm.predict(rows, output_margin=True).astype(np.float64)
+    assert np.max(np.abs(got.astype(np.float64).sum(axis=1) - margin)) <= 1e-4
