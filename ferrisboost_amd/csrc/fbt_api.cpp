@@ -11,6 +11,7 @@ namespace fbt {
 Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float *w,
             const uint8_t *cat, const int8_t *mono, uint32_t n_mono, const fbt_params &p);
 fbt_stats last_stats();
+uint32_t last_round_stats(double *wall, double *ms, uint64_t *bytes, uint32_t cap);
 }  // namespace fbt
 
 struct fbt_model {
@@ -69,6 +70,11 @@ int fbt_last_stats(fbt_stats *out) {
         if (!out) throw fbt::InputError("null argument");
         *out = fbt::last_stats();
     });
+}
+
+uint32_t fbt_last_round_stats(double *wall_s, double *hist_ms, uint64_t *hist_bytes,
+                              uint32_t capacity) {
+    return fbt::last_round_stats(wall_s, hist_ms, hist_bytes, capacity);
 }
 
 void fbt_model_free(fbt_model *m) { delete m; }

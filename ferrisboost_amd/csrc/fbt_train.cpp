@@ -514,10 +514,22 @@ void validate(const fbt_params &p, uint64_t n, uint32_t nf, const float *y) {
 }
 
 fbt_stats g_stats{};
+std::vector<double> g_round_wall, g_round_hist_ms;
+std::vector<uint64_t> g_round_hist_bytes;
 
 }  // namespace
 
 fbt_stats last_stats() { return g_stats; }
+
+uint32_t last_round_stats(double *wall, double *ms, uint64_t *bytes, uint32_t cap) {
+    const uint32_t n = (uint32_t)g_round_wall.size();
+    for (uint32_t i = 0; i < std::min(n, cap); i++) {
+        if (wall) wall[i] = g_round_wall[i];
+        if (ms) ms[i] = g_round_hist_ms[i];
+        if (bytes) bytes[i] = g_round_hist_bytes[i];
+    }
+    return n;
+}
 
 Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float *w,
             const uint8_t *cat, const int8_t *mono_in, uint32_t n_mono, const fbt_params &p) {
@@ -627,9 +639,32 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     grower.n_rows_ = (uint32_t)n;
     const uint32_t obj = p.objective;
     double grad_s = 0.0;
+    g_round_wall.assign(p.n_rounds, 0.0);
+    g_round_hist_ms.assign(p.n_rounds, 0.0);
+    g_round_hist_bytes.assign(p.n_rounds, 0);
+    auto t_round = Clock::now();
+    double ms_seen = 0.0;
+    uint64_t bytes_seen = 0;
+    auto close_round = [&](uint32_t r) {
+        const auto now = Clock::now();
+        g_round_wall[r] = std::chrono::duration<double>(now - t_round).count();
+        t_round = now;
+        if (p.profile) {
+            double ms = 0.0;
+            uint64_t launches = 0, bytes = 0;
+            call(fbh_hist_timing(ctx.get(), &ms, &launches, &bytes, 0));
+            g_round_hist_ms[r] = ms - ms_seen;
+            g_round_hist_bytes[r] = bytes - bytes_seen;
+            ms_seen = ms;
+            bytes_seen = bytes;
+        }
+    };
     for (uint32_t round = 0; round < p.n_rounds; round++) {
         const auto tg = Clock::now();
-        if (round > 0) call(fbh_download_delta(ctx.get(), delta.data()));
+        if (round > 0) {
+            call(fbh_download_delta(ctx.get(), delta.data()));
+            close_round(round - 1);
+        }
         const bool apply_delta = round > 0;
         pool.run([&](unsigned t) {
             const uint64_t lo = n * t / pool.size(), hi = n * (t + 1) / pool.size();
@@ -667,6 +702,7 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     }
     if (p.n_rounds > 0) {
         call(fbh_download_delta(ctx.get(), delta.data()));
+        close_round(p.n_rounds - 1);
         pool.run([&](unsigned t) {
             const uint64_t lo = n * t / pool.size(), hi = n * (t + 1) / pool.size();
             for (uint64_t i = lo; i < hi; i++) pred[i] += delta[i];

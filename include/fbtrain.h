@@ -99,6 +99,12 @@ int fbt_train(const float *x, uint64_t n_rows, uint32_t n_features, const float 
               const float *weights, const uint8_t *categorical, const int8_t *monotone,
               uint32_t n_monotone, const fbt_params *params, fbt_model **out);
 int fbt_last_stats(fbt_stats *out);
+/* Per-round timing of the last training call: wall seconds of round r (from
+ * its start to the start of round r+1, delta download and gradient pass
+ * included), histogram kernel milliseconds and algorithmic bytes (the
+ * latter two need params.profile = 1). Returns the number of rounds. */
+uint32_t fbt_last_round_stats(double *wall_s, double *hist_ms, uint64_t *hist_bytes,
+                              uint32_t capacity);
 
 void fbt_model_free(fbt_model *m);
 uint32_t fbt_model_n_trees(const fbt_model *m);

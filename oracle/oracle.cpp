@@ -405,18 +405,33 @@ std::vector<std::vector<u32>> partition_by_width(const std::vector<int> &widths,
     return blocks;
 }
 
-Cuts sketch_cuts(const float *x, u64 n, u32 nf, u32 max_bin, const float *w, const u8 *cat) {
+// DenseSource binning pass (src/source/dense.rs:145-190): one sketch per
+// feature, built start to finish by one thread, never merged across threads,
+// so the cuts do not depend on the thread count.
+Cuts sketch_cuts(const float *x, u64 n, u32 nf, u32 max_bin, const float *w, const u8 *cat,
+                 unsigned threads = 0) {
+    if (threads == 0) threads = std::min(16u, std::max(1u, std::thread::hardware_concurrency()));
+    std::vector<std::vector<float>> per(nf);
+    std::vector<int> bad(nf, 0);
+    auto one = [&](u32 f) {
+        FeatureSketch sk(max_bin, cat && cat[f]);
+        for (u64 r = 0; r < n; r++) sk.push(x[r * nf + f], w ? w[r] : 1.0f);
+        bad[f] = sk.bad;
+        per[f] = sk.cuts(max_bin);
+    };
+    std::vector<std::thread> pool;
+    for (unsigned t = 0; t < std::min<unsigned>(threads, nf); t++)
+        pool.emplace_back([&, t] {
+            for (u32 f = t; f < nf; f += std::min<unsigned>(threads, nf)) one(f);
+        });
+    for (auto &th : pool) th.join();
     Cuts c;
     c.offsets.push_back(0);
     for (u32 f = 0; f < nf; f++) {
-        bool is_cat = cat && cat[f];
-        FeatureSketch sk(max_bin, is_cat);
-        for (u64 r = 0; r < n; r++) sk.push(x[r * nf + f], w ? w[r] : 1.0f);
-        if (sk.bad) throw std::runtime_error("categorical feature contains an invalid code");
-        std::vector<float> cf = sk.cuts(max_bin);
-        c.values.insert(c.values.end(), cf.begin(), cf.end());
+        if (bad[f]) throw std::runtime_error("categorical feature contains an invalid code");
+        c.values.insert(c.values.end(), per[f].begin(), per[f].end());
         c.offsets.push_back((u32)c.values.size());
-        c.cat.push_back(is_cat ? 1 : 0);
+        c.cat.push_back(cat && cat[f] ? 1 : 0);
     }
     return c;
 }
