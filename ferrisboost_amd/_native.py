@@ -160,7 +160,8 @@ HIP_SYMBOLS = [
     "fbh_last_error", "fbh_device_available", "fbh_ctx_create", "fbh_ctx_destroy",
     "fbh_ctx_device_bytes", "fbh_upload_block", "fbh_upload_quantize_gpair",
     "fbh_upload_gpair_fixed", "fbh_begin_tree", "fbh_eval_nodes", "fbh_download_histogram",
-    "fbh_partition", "fbh_assign_leaves", "fbh_download_delta", "fbh_download_rows",
+    "fbh_partition", "fbh_assign_leaves", "fbh_download_delta", "fbh_host_alloc",
+    "fbh_host_free", "fbh_download_rows",
     "fbh_hist_timing", "fbh_set_timing", "fbh_build_histogram", "fbh_partition_rows",
     "fbh_shap_model_create", "fbh_shap_model_destroy", "fbh_shap_contribs",
     "fbh_shap_contribs_device", "fbh_shap_last_ms",

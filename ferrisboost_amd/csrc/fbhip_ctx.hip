@@ -259,8 +259,10 @@ void plan_tiles(fbh_ctx &c) {
         };
         for (uint32_t f = 0; f < c.n_features; f++) {
             if (c.width[f] != w) continue;
+            // The tile's LDS also holds 64 per-lane dummy slots (1 KiB).
+            const uint64_t budget = c.tile_bytes - 1024u;
             const uint64_t fb = (uint64_t)c.n_bins[f] * 16u;
-            if (fb > c.tile_bytes) {
+            if (fb > budget) {
                 // Too wide for LDS: a tile of its own, accumulated in global memory.
                 flush();
                 cur.feats.push_back(f);
@@ -269,7 +271,7 @@ void plan_tiles(fbh_ctx &c) {
                 continue;
             }
             const uint32_t rec = (uint32_t)(cur.feats.size() + 1) * w;
-            if (!cur.feats.empty() && (lds + fb > c.tile_bytes || rec > MAX_RECORD_BYTES)) flush();
+            if (!cur.feats.empty() && (lds + fb > budget || rec > MAX_RECORD_BYTES)) flush();
             cur.feats.push_back(f);
             lds += fb;
         }
@@ -734,7 +736,7 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
                 if (g.global)
                     check(launch_hist_global(L, g.width, c->stream), "histogram launch");
                 else
-                    check(launch_hist(L, g.width, g.rd, (size_t)g.lds_max * 16, c->stream),
+                    check(launch_hist(L, g.width, g.rd, (size_t)(g.lds_max + 64) * 16, c->stream),
                           "histogram launch");
                 c->hist_bytes += acc_rows * g.bytes_per_row;
             }
@@ -948,6 +950,21 @@ int fbh_download_delta(fbh_ctx *c, float *out) {
         check(hipMemcpyAsync(out, c->delta, c->n_rows * 4, hipMemcpyDeviceToHost, c->stream),
               "delta download");
         c->sync();
+    });
+}
+
+int fbh_host_alloc(size_t bytes, void **out) {
+    return guard([&] {
+        if (!out) throw InputError("null argument");
+        *out = nullptr;
+        check(hipHostMalloc(out, std::max<size_t>(bytes, 64), hipHostMallocDefault),
+              "pinned host allocation");
+    });
+}
+
+int fbh_host_free(void *p) {
+    return guard([&] {
+        if (p) check(hipHostFree(p), "pinned host free");
     });
 }
 

@@ -71,6 +71,11 @@ __device__ __forceinline__ void global_add_u64(unsigned long long *p, unsigned l
 // round-robin over the 8 XCDs, and every tile of chunk c runs on XCD c % 8,
 // so the chunk's row ids and gradient pairs are fetched from HBM once into
 // that XCD's L2 and re-read from there by the other tiles.
+//
+// LDS layout is planar: slots [0, S) hold gradient sums, [S, 2S) Hessian
+// sums (S = tile slots + 64). The last 64 slots of each plane are one dummy
+// slot per lane: a missing / unseen / unselected cell adds zero there instead
+// of branching, so the atomic stream has no divergent control flow.
 template <int W, int RD, int UNROLL>
 __global__ __launch_bounds__(HIST_TPB) void hist_kernel(const HistLaunch L) {
     extern __shared__ unsigned long long lds[];
@@ -110,8 +115,12 @@ __global__ __launch_bounds__(HIST_TPB) void hist_kernel(const HistLaunch L) {
     }
 
     const uint32_t tid = threadIdx.x;
-    for (uint32_t i = tid; i < 2 * T.lds_slots; i += HIST_TPB) lds[i] = 0ull;
+    const uint32_t S = T.lds_slots + 64u;  // plane size incl. the per-lane dummies
+    for (uint32_t i = tid; i < 2 * S; i += HIST_TPB) lds[i] = 0ull;
     __syncthreads();
+    const uint32_t dummy = T.lds_slots + (tid & 63u);
+    unsigned long long *gplane = lds;
+    unsigned long long *hplane = lds + S;
 
     const uint32_t *rows = L.rows + N.row_off;
     const longlong2 *gp = reinterpret_cast<const longlong2 *>(L.gpair);
@@ -139,8 +148,6 @@ __global__ __launch_bounds__(HIST_TPB) void hist_kernel(const HistLaunch L) {
         }
 #pragma unroll
         for (int u = 0; u < UNROLL; u++) {
-            // Rows whose pair is zero (sampled out, zero weight) add nothing.
-            if ((g[u].x | g[u].y) == 0) continue;
             const unsigned long long gg = (unsigned long long)g[u].x;
             const unsigned long long hh = (unsigned long long)g[u].y;
 #pragma unroll
@@ -148,14 +155,14 @@ __global__ __launch_bounds__(HIST_TPB) void hist_kernel(const HistLaunch L) {
 #pragma unroll
                 for (int q = 0; q < FPD; q++) {
                     const int fi = d * FPD + q;
+                    if (fi >= (int)T.n_feat) continue;  // uniform
                     const uint32_t bin = (rec[u][d] >> (q * 8 * W)) & MASK;
                     // Missing (all ones) and unseen-category codes are >= n_bins,
-                    // and features not built this tree have n_bins == 0.
-                    if (bin < nb[fi]) {
-                        unsigned long long *slot = lds + 2u * (loff[fi] + bin);
-                        lds_add_u64(slot, gg);
-                        lds_add_u64(slot + 1, hh);
-                    }
+                    // and features not built this tree have n_bins == 0; out-of-
+                    // range rows (ok false) carry a zero pair.
+                    const uint32_t s = bin < nb[fi] ? loff[fi] + bin : dummy;
+                    lds_add_u64(gplane + s, gg);
+                    lds_add_u64(hplane + s, hh);
                 }
             }
         }
@@ -167,8 +174,8 @@ __global__ __launch_bounds__(HIST_TPB) void hist_kernel(const HistLaunch L) {
     for (uint32_t fi = 0; fi < T.n_feat; fi++) {
         const TileFeatDev F = L.feats[T.feat_base + fi];
         for (uint32_t bin = tid; bin < F.n_bins; bin += HIST_TPB) {
-            const unsigned long long gg = lds[2u * (F.lds_off + bin)];
-            const unsigned long long hh = lds[2u * (F.lds_off + bin) + 1];
+            const unsigned long long gg = gplane[F.lds_off + bin];
+            const unsigned long long hh = hplane[F.lds_off + bin];
             unsigned long long *dst =
                 reinterpret_cast<unsigned long long *>(out + 2u * (F.hist_off + bin));
             if (single) {
@@ -236,6 +243,14 @@ template <int W, int RD>
 static hipError_t launch_hist_t(const HistLaunch &L, size_t lds, hipStream_t s) {
     const uint32_t blocks = L.chunk_groups * XCDS * L.n_tiles;
     if (blocks == 0) return hipSuccess;
+    // gfx950 has 160 KiB of LDS per workgroup; opt in beyond the 64 KiB default.
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&hist_kernel<W, RD, 4>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
     hipLaunchKernelGGL((hist_kernel<W, RD, 4>), dim3(blocks), dim3(HIST_TPB), lds, s, L);
     return hipGetLastError();
 }

@@ -167,6 +167,26 @@ std::vector<uint32_t> sample_columns(uint32_t nf, float rate, uint64_t seed, uin
     return ids;
 }
 
+// Page-locked host array from the backend.
+template <class T>
+class PinnedArray {
+  public:
+    explicit PinnedArray(size_t n) {
+        void *p = nullptr;
+        call(fbh_host_alloc(n * sizeof(T), &p));
+        p_ = static_cast<T *>(p);
+    }
+    ~PinnedArray() { fbh_host_free(p_); }
+    PinnedArray(const PinnedArray &) = delete;
+    PinnedArray &operator=(const PinnedArray &) = delete;
+    T &operator[](size_t i) { return p_[i]; }
+    const T &operator[](size_t i) const { return p_[i]; }
+    T *data() { return p_; }
+
+  private:
+    T *p_ = nullptr;
+};
+
 uint64_t sample_threshold(float rate) {  // subsample::threshold_for
     if (rate >= 1.0f || !(rate > 0.0f)) return UINT64_MAX;
     return (uint64_t)((double)rate * (double)(1ull << 53));
@@ -634,7 +654,9 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
 
     // ---- round loop ----
     const auto t_train = Clock::now();
-    std::vector<float> pred(n, margin), delta(n), g2(2 * n);
+    std::vector<float> pred(n, margin);
+    // Pinned staging for the per-round delta download and gradient upload.
+    PinnedArray<float> delta(n), g2(2 * n);
     Grower grower(ctx.get(), p, m.cuts, mono, slots);
     grower.n_rows_ = (uint32_t)n;
     const uint32_t obj = p.objective;

@@ -202,6 +202,12 @@ int fbh_assign_leaves(fbh_ctx *ctx, const fbh_span *spans, const float *values, 
 
 /* GpuTrainCtx::download_prediction_delta (src/backend/cuda/train_ctx.rs:2215-2236). */
 int fbh_download_delta(fbh_ctx *ctx, float *out);
+
+/* Page-locked host memory (the reference's pinned staging windows,
+ * FB_CUDA_PINNED, src/backend/cuda/train_ctx.rs:1129-1204): the per-round
+ * delta download and gradient upload run at full link speed from it. */
+int fbh_host_alloc(size_t bytes, void **out);
+int fbh_host_free(void *p);
 /* The current row arena (tests and diagnostics). */
 int fbh_download_rows(fbh_ctx *ctx, uint32_t *out);
 
