@@ -1,0 +1,202 @@
+"""CPU tests of the boundary and the host logic (no GPU needed).
+
+* both C-ABI libraries load and export every function include/*.h declares;
+* the Python package mirrors the reference's parameter surface and error
+  classes (python/ferrisboost/__init__.py, src/error.rs:1-68): bad input is a
+  ValueError before any device work, and with no device every training call
+  is a RuntimeError -- the package has no CPU fallback;
+* the product's quantile sketch (the setup step that feeds both engines)
+  produces the oracle's cuts bit for bit;
+* bench.py refuses more than one GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, gpu_ready
+
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("fbhip.h", "fbtrain.h")]
+
+
+def _declared(path: str, prefix: str) -> list[str]:
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(" + prefix + r"_\w+)\s*\(", text)))
+
+
+def test_headers_declare_the_boundary():
+    hip = _declared(HEADERS[0], "fbh")
+    train = _declared(HEADERS[1], "fbt")
+    assert {"fbh_ctx_create", "fbh_eval_nodes", "fbh_partition", "fbh_build_histogram",
+            "fbh_shap_contribs", "fbh_last_error"} <= set(hip)
+    assert {"fbt_train", "fbt_shap", "fbt_model_to_json"} <= set(train)
+
+
+def test_libraries_export_every_declared_symbol():
+    from ferrisboost_amd import _native as N
+
+    L = N.hip()
+    T = N.train_lib()
+    for name in _declared(HEADERS[0], "fbh"):
+        assert hasattr(L, name), f"libfbhip.so does not export {name}"
+    for name in _declared(HEADERS[1], "fbt"):
+        assert hasattr(T, name), f"libfbtrain.so does not export {name}"
+    # the Python binding knows every symbol, too
+    assert set(_declared(HEADERS[0], "fbh")) == set(N.HIP_SYMBOLS)
+    assert set(_declared(HEADERS[1], "fbt")) == set(N.TRAIN_SYMBOLS)
+
+
+def test_libraries_are_gfx950_code_objects():
+    """The HIP library carries a gfx950 code object (and no other target)."""
+    from ferrisboost_amd import _native as N
+
+    data = open(N.LIB_HIP, "rb").read()
+    assert b"gfx950" in data
+    assert b"sm_" + b"80" not in data
+
+
+def test_oracle_is_not_linked_by_the_product():
+    """The shipped libraries and package never reference the oracle."""
+    from ferrisboost_amd import _native as N
+
+    for lib in (N.LIB_HIP, N.LIB_TRAIN):
+        out = subprocess.run(["ldd", lib], capture_output=True, text=True).stdout
+        assert "oracle" not in out
+        assert b"orc_" not in open(lib, "rb").read()
+    pkg = os.path.join(ROOT, "ferrisboost_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".cpp", ".hip", ".h")):
+                src = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in src.lower(), f
+
+
+def test_error_classes_map_to_python():
+    from ferrisboost_amd import _native as N
+
+    assert issubclass(N.InputError, ValueError)
+    assert issubclass(N.BackendError, RuntimeError)
+
+
+def _tiny():
+    rng = np.random.default_rng(0)
+    x = rng.normal(size=(64, 3)).astype(np.float32)
+    y = (x[:, 0] > 0).astype(np.float32)
+    return x, y
+
+
+@pytest.mark.parametrize("params, msg", [
+    ({"device": "cpu"}, "device"),
+    ({"device": "tpu"}, "device"),
+    ({"objective": "multi:softprob"}, "objective"),
+    ({"grow_policy": "levelwise"}, "grow_policy"),
+    ({"max_bin": 0}, "max_bin"),
+    ({"max_bin": 70000}, "max_bin"),
+    ({"gpu_math": "fast"}, "gpu_math"),
+    ({"gpu_math": "sloppy"}, "gpu_math"),
+    ({"colsample_bylevel": 0.5}, "colsample_bylevel"),
+    ({"colsample_bynode": 0.5}, "colsample_bynode"),
+    ({"tree_method": "exact"}, "tree_method"),
+    ({"no_such_param": 1}, "unknown parameter"),
+    ({"interaction_constraints": [[0, 1]]}, "interaction"),
+])
+def test_bad_params_are_value_errors(params, msg):
+    import ferrisboost_amd as fb
+
+    x, y = _tiny()
+    with pytest.raises(ValueError, match=msg):
+        fb.train(params, x, label=y, num_boost_round=2)
+
+
+def test_bad_shapes_are_value_errors():
+    import ferrisboost_amd as fb
+
+    x, y = _tiny()
+    with pytest.raises(ValueError):
+        fb.train({}, x, label=y[:10], num_boost_round=2)
+    with pytest.raises(ValueError):
+        fb.train({}, x[:, 0], label=y, num_boost_round=2)
+    with pytest.raises(ValueError):
+        fb.train({}, x, label=y, weight=np.ones(3, np.float32), num_boost_round=2)
+    with pytest.raises(ValueError):
+        fb.train({}, x, label=y, num_boost_round=0)
+
+
+@pytest.mark.parametrize("params, msg", [
+    ({"max_depth": 15}, "max_depth"),
+    ({"eta": -1.0}, "learning_rate"),
+    ({"subsample": 0.0}, "subsample"),
+    ({"colsample_bytree": 1.5}, "colsample_bytree"),
+])
+def test_driver_validation_is_input_error(params, msg):
+    """The C++ driver validates before any device call (src/types.rs:432-660,
+    src/training/mod.rs:1487-1493): FBH_INPUT_ERROR -> ValueError."""
+    import ferrisboost_amd as fb
+
+    x, y = _tiny()
+    with pytest.raises(ValueError, match=msg):
+        fb.train(params, x, label=y, num_boost_round=2)
+
+
+@pytest.mark.skipif(gpu_ready(), reason="checks the no-device error path")
+def test_no_device_is_a_runtime_error_not_a_fallback():
+    import ferrisboost_amd as fb
+
+    x, y = _tiny()
+    assert not fb.device_available(0)
+    with pytest.raises(RuntimeError):
+        fb.train({"max_depth": 3}, x, label=y, num_boost_round=2)
+
+
+def _product_cuts(x, max_bin, weights=None, categorical=None):
+    from ferrisboost_amd import _native as N
+
+    x = np.ascontiguousarray(x, np.float32)
+    n, nf = x.shape
+    cap = sum(65534 if (categorical is not None and categorical[f]) else max(max_bin, 2)
+              for f in range(nf))
+    vals = np.zeros(cap + 1, np.float32)
+    offs = np.zeros(nf + 1, np.uint32)
+    w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+    cat = None if categorical is None else np.ascontiguousarray(categorical, np.uint8)
+    N.check_train(N.train_lib().fbt_sketch_cuts(N.ptr(x), n, nf, max_bin, N.ptr(w), N.ptr(cat),
+                                                N.ptr(vals), N.ptr(offs)))
+    return vals[: offs[-1]].copy(), offs
+
+
+@pytest.mark.parametrize("max_bin", [16, 255, 256, 1024])
+def test_product_sketch_equals_oracle(oracle, max_bin):
+    rng = np.random.default_rng(max_bin)
+    n = 60_000
+    x = np.stack([
+        rng.normal(size=n),
+        np.abs(rng.normal(size=n)),
+        np.exp(rng.normal(size=n)),
+        rng.integers(0, 7, size=n),
+        rng.uniform(size=n),
+        np.full(n, 3.0),
+        rng.integers(0, 300, size=n),
+    ], 1).astype(np.float32)
+    x[rng.random(x.shape) < 0.07] = np.nan
+    w = rng.uniform(0.5, 2.0, size=n).astype(np.float32)
+    cat = np.array([0, 0, 0, 0, 0, 0, 1], np.uint8)
+    for weights in (None, w):
+        a = _product_cuts(x, max_bin, weights, cat)
+        b = oracle.sketch_cuts(x, max_bin, weights, cat)
+        assert np.array_equal(a[1], b[1])
+        assert np.array_equal(a[0].view(np.uint32), b[0].view(np.uint32))
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)
