@@ -37,11 +37,35 @@ def log(msg: str) -> None:
 
 
 def load_traffic(path: str):
+    """`key = value` lines of a committed rocprofv3 counter summary."""
+    out = {}
     try:
         with open(path) as f:
-            return json.load(f)
-    except (OSError, ValueError):
+            for line in f:
+                if "=" in line and not line.lstrip().startswith("#"):
+                    k, v = line.split("=", 1)
+                    try:
+                        out[k.strip()] = float(v.split()[0])
+                    except (ValueError, IndexError):
+                        pass
+    except OSError:
         return None
+    return out or None
+
+
+def copy_probe(mib: int) -> int:
+    """Run a plain device copy of known size (the calibration kernel of the
+    FETCH_SIZE / WRITE_SIZE counters)."""
+    import torch
+
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": n, "launches": 3}), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -53,11 +77,15 @@ def main() -> int:
     ap.add_argument("--max-bin", type=int, default=255)
     ap.add_argument("--cpu-rounds", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a device copy of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported "
-              "(the path is single-device; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(the training path is single-device)", file=sys.stderr)
         return 2
+    if args.copy_probe:
+        return copy_probe(args.copy_probe)
 
     import ferrisboost_amd as fb
     from ferrisboost_amd import _native as N
@@ -87,14 +115,18 @@ def main() -> int:
     b_hist = float(hbytes[timed].astype(np.float64).sum())
     rounds_per_sec = args.steps / t_wall
     hist_gbps = b_hist / (t_hist_ms * 1e-3) / 1e9 if t_hist_ms > 0 else 0.0
-    traffic = load_traffic(os.path.join(ROOT, "profiles", "hist_traffic_narrow.json"))
+    launches = int(model.stats["hist_launches"])
+    bytes_per_launch = float(model.stats["hist_bytes"]) / launches if launches else 0.0
+    traffic = load_traffic(os.path.join(ROOT, "profiles",
+                                        f"hist_traffic_narrow_{'u8' if args.max_bin <= 255 else 'u16'}.txt"))
     roofline = {
         "bound": "hbm",
         "achieved": round(hist_gbps, 1),
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
         "frac": round(hist_gbps / HBM_PEAK_GBPS, 4),
-        "traffic": traffic.get("bytes_per_launch") if traffic else None,
+        "traffic": traffic.get("hbm_bytes_per_launch") if traffic else None,
+        "algorithmic_bytes_per_launch": round(bytes_per_launch),
     }
 
     cpu = None
@@ -148,6 +180,7 @@ def main() -> int:
         },
         "hist_gbps": round(hist_gbps, 1),
         "hist_ms_per_round": round(t_hist_ms / args.steps, 3),
+        "hist_launches_per_round": round(launches / rounds, 2),
         "host_gradient_ms_per_round": round(1e3 * model.stats["host_gradient_seconds"] / rounds, 3),
         "roofline": roofline,
         "cpu_baseline": cpu,
