@@ -77,7 +77,11 @@ uint32_t round_stride(uint32_t bytes) {
 constexpr uint32_t MAX_RECORD_BYTES = 64;
 constexpr uint32_t MAX_NODES = 16384;      // nodes of one eval / partition call
 constexpr uint32_t DEFAULT_TILE_BYTES = 64 * 1024;
-constexpr uint32_t DEFAULT_CHUNK_ROWS = 4096;
+// Rows per histogram workgroup: chosen per launch so that the launch makes
+// one full wave of workgroups (HIST_WAVES), never fewer than MIN_CHUNK_ROWS
+// rows: each workgroup then flushes its LDS histogram once per launch.
+constexpr uint32_t MIN_CHUNK_ROWS = 4096;
+constexpr uint32_t HIST_WAVES = 1;
 
 struct DeviceBuf {
     void *p = nullptr;
@@ -104,7 +108,10 @@ struct fbh_ctx {
     std::vector<uint8_t> width, cat;
     std::vector<uint32_t> n_bins;
     uint32_t tile_bytes = DEFAULT_TILE_BYTES;
-    uint32_t chunk_rows = DEFAULT_CHUNK_ROWS;
+    uint32_t fixed_chunk_rows = 0;  // nonzero: rows per workgroup forced by the caller
+    uint32_t hist_tpb = 256;        // histogram threads per workgroup
+    uint32_t hist_waves = HIST_WAVES;
+    uint32_t n_cus = 256;
     uint32_t n_slots = 0;
     uint32_t max_cat_words = 0;
     uint64_t width_max = 0;  // sum of all features' bins
@@ -225,6 +232,27 @@ struct fbh_ctx {
     }
 
     void sync() { check(hipStreamSynchronize(stream), "stream synchronize"); }
+
+    // Rows per histogram workgroup for a launch accumulating acc_rows rows:
+    // enough chunks for hist_waves full waves of workgroups over all tiles
+    // (occupancy bounded by LDS and by 2048 threads per CU), so that each
+    // workgroup flushes its LDS histogram once per many rows.
+    uint32_t chunk_rows_for(uint64_t acc_rows) const {
+        if (fixed_chunk_rows) return fixed_chunk_rows;
+        uint64_t n_tiles = 0, lds_max = 0;
+        for (const auto &g : groups) {
+            n_tiles += g.n_tiles;
+            if (!g.global) lds_max = std::max<uint64_t>(lds_max, (uint64_t)(g.lds_max + 64) * 16);
+        }
+        if (n_tiles == 0) return MIN_CHUNK_ROWS;
+        uint64_t per_cu = lds_max ? (160u * 1024u) / lds_max : 8;
+        per_cu = std::max<uint64_t>(1, std::min<uint64_t>(per_cu, 2048 / hist_tpb));
+        const uint64_t wgs = (uint64_t)n_cus * per_cu * hist_waves;
+        const uint64_t want_chunks = std::max<uint64_t>(1, wgs / n_tiles);
+        uint64_t r = (acc_rows + want_chunks - 1) / want_chunks;
+        r = (r + 1023) & ~uint64_t(1023);
+        return (uint32_t)std::min<uint64_t>(std::max<uint64_t>(r, MIN_CHUNK_ROWS), 1u << 24);
+    }
 
     void collect_timing() {
         for (size_t i = 0; i < ev_used; i++) {
@@ -354,12 +382,20 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
         if (cfg) conf = *cfg;
         c->tile_bytes = (uint32_t)env_u64("FB_HIP_TILE_BYTES",
                                           conf.tile_bytes ? conf.tile_bytes : DEFAULT_TILE_BYTES);
-        c->chunk_rows = (uint32_t)env_u64(
-            "FB_HIP_CHUNK_ROWS", conf.rows_per_block ? conf.rows_per_block : DEFAULT_CHUNK_ROWS);
+        c->fixed_chunk_rows = (uint32_t)env_u64("FB_HIP_CHUNK_ROWS", conf.rows_per_block);
+        c->hist_tpb = (uint32_t)env_u64("FB_HIP_HIST_TPB", 256);
+        c->hist_waves = (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HIST_WAVES", HIST_WAVES));
         if (c->tile_bytes < 4096 || c->tile_bytes > 160 * 1024)
             throw InputError("tile_bytes must be in 4096..=163840");
-        if (c->chunk_rows < 256 || c->chunk_rows % 256)
+        if (c->fixed_chunk_rows && (c->fixed_chunk_rows < 256 || c->fixed_chunk_rows % 256))
             throw InputError("rows_per_block must be a positive multiple of 256");
+        if (c->hist_tpb != 256 && c->hist_tpb != 512 && c->hist_tpb != 1024)
+            throw InputError("histogram threads per workgroup must be 256, 512 or 1024");
+        {
+            hipDeviceProp_t prop;
+            check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+            c->n_cus = (uint32_t)std::max(1, prop.multiProcessorCount);
+        }
         c->n_slots = conf.hist_slots ? conf.hist_slots : 64;
         if (c->n_slots > MAX_NODES)
             throw InputError("hist_slots must be at most " + std::to_string(MAX_NODES));
@@ -663,10 +699,14 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
         std::vector<uint32_t> zero_slots;
         uint32_t chunks = 0;
         uint64_t acc_rows = 0;
+        for (uint32_t i = 0; i < n; i++)
+            if (nodes[i].subtract_parent < 0) acc_rows += nodes[i].rows.len;
+        const uint32_t chunk_rows = c->chunk_rows_for(acc_rows);
+        acc_rows = 0;
         for (uint32_t i = 0; i < n; i++) {
             const fbh_node &nd = nodes[i];
             if (nd.subtract_parent >= 0) continue;
-            const uint32_t nc = div_up(nd.rows.len, c->chunk_rows);
+            const uint32_t nc = div_up(nd.rows.len, chunk_rows);
             // Single-chunk nodes are written by plain stores, except that a
             // globally accumulated feature needs a zeroed slot.
             if (nc != 1 || c->has_global) zero_slots.push_back(nd.slot);
@@ -727,7 +767,7 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
                 L.nodes = c->d_hnodes;
                 L.n_nodes = (uint32_t)hn.size();
                 L.n_chunks = chunks;
-                L.chunk_rows = c->chunk_rows;
+                L.chunk_rows = chunk_rows;
                 L.chunk_groups = div_up(chunks, XCDS);
                 L.rows = c->rows;
                 L.gpair = c->gpair;
@@ -736,7 +776,8 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
                 if (g.global)
                     check(launch_hist_global(L, g.width, c->stream), "histogram launch");
                 else
-                    check(launch_hist(L, g.width, g.rd, (size_t)(g.lds_max + 64) * 16, c->stream),
+                    check(launch_hist(L, g.width, g.rd, (int)c->hist_tpb, (size_t)(g.lds_max + 64) * 16,
+                                      c->stream),
                           "histogram launch");
                 c->hist_bytes += acc_rows * g.bytes_per_row;
             }

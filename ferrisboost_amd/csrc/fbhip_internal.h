@@ -139,8 +139,9 @@ void set_last_error(const char *msg);
 const char *last_error();
 
 // ---------------------------------------------------------------- launchers
-hipError_t launch_hist(const HistLaunch &L, int width, int rec_dwords, size_t lds_bytes,
-                       hipStream_t s);
+// threads_per_block is 256, 512 or 1024.
+hipError_t launch_hist(const HistLaunch &L, int width, int rec_dwords, int threads_per_block,
+                       size_t lds_bytes, hipStream_t s);
 hipError_t launch_hist_global(const HistLaunch &L, int width, hipStream_t s);
 hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slots, uint32_t n,
                              hipStream_t s);

@@ -76,8 +76,8 @@ __device__ __forceinline__ void global_add_u64(unsigned long long *p, unsigned l
 // sums (S = tile slots + 64). The last 64 slots of each plane are one dummy
 // slot per lane: a missing / unseen / unselected cell adds zero there instead
 // of branching, so the atomic stream has no divergent control flow.
-template <int W, int RD, int UNROLL>
-__global__ __launch_bounds__(HIST_TPB) void hist_kernel(const HistLaunch L) {
+template <int W, int RD, int UNROLL, int TPB>
+__global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
     extern __shared__ unsigned long long lds[];
     constexpr int FPD = 4 / W;
     constexpr int NF = RD * FPD;
@@ -116,7 +116,7 @@ __global__ __launch_bounds__(HIST_TPB) void hist_kernel(const HistLaunch L) {
 
     const uint32_t tid = threadIdx.x;
     const uint32_t S = T.lds_slots + 64u;  // plane size incl. the per-lane dummies
-    for (uint32_t i = tid; i < 2 * S; i += HIST_TPB) lds[i] = 0ull;
+    for (uint32_t i = tid; i < 2 * S; i += TPB) lds[i] = 0ull;
     __syncthreads();
     const uint32_t dummy = T.lds_slots + (tid & 63u);
     unsigned long long *gplane = lds;
@@ -124,12 +124,12 @@ __global__ __launch_bounds__(HIST_TPB) void hist_kernel(const HistLaunch L) {
 
     const uint32_t *rows = L.rows + N.row_off;
     const longlong2 *gp = reinterpret_cast<const longlong2 *>(L.gpair);
-    for (uint32_t i = r0 + tid; i < r1; i += HIST_TPB * UNROLL) {
+    for (uint32_t i = r0 + tid; i < r1; i += TPB * UNROLL) {
         uint32_t row[UNROLL];
         bool ok[UNROLL];
 #pragma unroll
         for (int u = 0; u < UNROLL; u++) {
-            const uint32_t idx = i + u * HIST_TPB;
+            const uint32_t idx = i + u * TPB;
             ok[u] = idx < r1;
             row[u] = ok[u] ? rows[idx] : 0u;
         }
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(HIST_TPB) void hist_kernel(const HistLaunch L) {
     const bool single = N.n_chunks == 1;
     for (uint32_t fi = 0; fi < T.n_feat; fi++) {
         const TileFeatDev F = L.feats[T.feat_base + fi];
-        for (uint32_t bin = tid; bin < F.n_bins; bin += HIST_TPB) {
+        for (uint32_t bin = tid; bin < F.n_bins; bin += TPB) {
             const unsigned long long gg = gplane[F.lds_off + bin];
             const unsigned long long hh = hplane[F.lds_off + bin];
             unsigned long long *dst =
@@ -239,30 +239,39 @@ hipError_t launch_hist_global(const HistLaunch &L, int width, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int W, int RD>
+template <int W, int RD, int TPB>
 static hipError_t launch_hist_t(const HistLaunch &L, size_t lds, hipStream_t s) {
     const uint32_t blocks = L.chunk_groups * XCDS * L.n_tiles;
     if (blocks == 0) return hipSuccess;
-    // gfx950 has 160 KiB of LDS per workgroup; opt in beyond the 64 KiB default.
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&hist_kernel<W, RD, 4>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    // gfx950 has 160 KiB of LDS per workgroup; opt in beyond the 64 KiB
+    // default (a per-function attribute, set once per device).
+    static uint64_t attr_done = 0;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 64 && !(attr_done >> dev & 1)) {
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&hist_kernel<W, RD, 4, TPB>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
-        attr = true;
+        attr_done |= 1ull << dev;
     }
-    hipLaunchKernelGGL((hist_kernel<W, RD, 4>), dim3(blocks), dim3(HIST_TPB), lds, s, L);
+    hipLaunchKernelGGL((hist_kernel<W, RD, 4, TPB>), dim3(blocks), dim3(TPB), lds, s, L);
     return hipGetLastError();
 }
 
-hipError_t launch_hist(const HistLaunch &L, int width, int rd, size_t lds, hipStream_t s) {
-#define FBH_HIST_CASE(WW, R) \
-    if (width == WW && rd == R) return launch_hist_t<WW, R>(L, lds, s);
-    FBH_HIST_CASE(1, 1) FBH_HIST_CASE(1, 2) FBH_HIST_CASE(1, 3) FBH_HIST_CASE(1, 4)
-    FBH_HIST_CASE(1, 8) FBH_HIST_CASE(1, 12) FBH_HIST_CASE(1, 16)
-    FBH_HIST_CASE(2, 1) FBH_HIST_CASE(2, 2) FBH_HIST_CASE(2, 3) FBH_HIST_CASE(2, 4)
-    FBH_HIST_CASE(2, 8) FBH_HIST_CASE(2, 12) FBH_HIST_CASE(2, 16)
-#undef FBH_HIST_CASE
+hipError_t launch_hist(const HistLaunch &L, int width, int rd, int tpb, size_t lds, hipStream_t s) {
+#define FBH_HIST_TPB(WW, R)                                                  \
+    if (width == WW && rd == R) {                                            \
+        if (tpb == 1024) return launch_hist_t<WW, R, 1024>(L, lds, s);       \
+        if (tpb == 512) return launch_hist_t<WW, R, 512>(L, lds, s);         \
+        if (tpb == 256) return launch_hist_t<WW, R, 256>(L, lds, s);         \
+        return hipErrorInvalidValue;                                         \
+    }
+    FBH_HIST_TPB(1, 1) FBH_HIST_TPB(1, 2) FBH_HIST_TPB(1, 3) FBH_HIST_TPB(1, 4)
+    FBH_HIST_TPB(1, 8) FBH_HIST_TPB(1, 12) FBH_HIST_TPB(1, 16)
+    FBH_HIST_TPB(2, 1) FBH_HIST_TPB(2, 2) FBH_HIST_TPB(2, 3) FBH_HIST_TPB(2, 4)
+    FBH_HIST_TPB(2, 8) FBH_HIST_TPB(2, 12) FBH_HIST_TPB(2, 16)
+#undef FBH_HIST_TPB
     return hipErrorInvalidValue;
 }
 
