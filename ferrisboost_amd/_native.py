@@ -159,7 +159,8 @@ NODE_DTYPE = np.dtype(
 HIP_SYMBOLS = [
     "fbh_last_error", "fbh_device_available", "fbh_ctx_create", "fbh_ctx_destroy",
     "fbh_ctx_device_bytes", "fbh_upload_block", "fbh_upload_quantize_gpair",
-    "fbh_upload_gpair_fixed", "fbh_begin_tree", "fbh_eval_nodes", "fbh_download_histogram",
+    "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_gradient_exchange",
+    "fbh_download_margin", "fbh_begin_tree", "fbh_eval_nodes", "fbh_download_histogram",
     "fbh_partition", "fbh_assign_leaves", "fbh_download_delta", "fbh_host_alloc",
     "fbh_host_free", "fbh_download_rows",
     "fbh_hist_timing", "fbh_set_timing", "fbh_build_histogram", "fbh_partition_rows",
@@ -210,6 +211,9 @@ def hip() -> C.CDLL:
         L.fbh_upload_block.argtypes = [P, P, C.c_uint32, C.c_uint32, P]
         L.fbh_upload_quantize_gpair.argtypes = [P, P, C.c_uint64, C.c_uint64, C.c_uint64, P, P]
         L.fbh_upload_gpair_fixed.argtypes = [P, P, P]
+        L.fbh_set_objective.argtypes = [P, C.c_uint32, P, P, C.c_float]
+        L.fbh_gradient_exchange.argtypes = [P, P, P, C.c_uint64, C.c_uint64, C.c_uint64, P, P]
+        L.fbh_download_margin.argtypes = [P, P]
         L.fbh_begin_tree.argtypes = [P, P, C.c_uint32, P, C.c_uint32, C.POINTER(Span)]
         L.fbh_eval_nodes.argtypes = [P, P, C.c_uint32, C.POINTER(SplitParams), P, P, P,
                                      C.c_uint32]

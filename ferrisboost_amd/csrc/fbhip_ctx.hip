@@ -81,6 +81,9 @@ constexpr uint32_t DEFAULT_TILE_BYTES = 64 * 1024;
 // one full wave of workgroups (HIST_WAVES), never fewer than MIN_CHUNK_ROWS
 // rows: each workgroup then flushes its LDS histogram once per launch.
 constexpr uint32_t MIN_CHUNK_ROWS = 4096;
+// Row chunks of the per-round gradient exchange (download, host work and
+// upload of different chunks overlap).
+constexpr int EXCHANGE_CHUNKS = 8;
 constexpr uint32_t HIST_WAVES = 1;
 
 struct DeviceBuf {
@@ -183,6 +186,19 @@ struct fbh_ctx {
     bool tree_begun = false;
     double scales[2] = {1.0, 1.0};
 
+    // objective state on the device (fbh_set_objective)
+    int objective = -1;                 // -1 none, 0 squared error, 1 logistic
+    float *labels = nullptr, *gweights = nullptr, *margin = nullptr;
+    void *leaf_ids = nullptr;           // per-row leaf position of the last tree
+    int leaf_id_bytes = 0;              // 1 or 2 for the last assigned tree
+    bool ids_fresh = false;             // leaf ids not yet handed to the host
+    bool has_weights = false;
+    float *sig = nullptr;               // the host's per-row sigmoids (logistic)
+    PinnedBuf pin_ids, pin_src;         // leaf-id download / sigmoid upload staging
+    hipStream_t up_stream = nullptr;    // host-to-device copies of the exchange
+    std::vector<hipEvent_t> chunk_ev;   // one per exchange chunk
+    hipEvent_t up_done = nullptr;
+
     // timing
     bool timing = false;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> ev_pool;
@@ -201,7 +217,16 @@ struct fbh_ctx {
         if (pin_small.p) (void)hipHostFree(pin_small.p);
         if (pin_leaves.p) (void)hipHostFree(pin_leaves.p);
         if (pin_out.p) (void)hipHostFree(pin_out.p);
-        pin_small.p = pin_leaves.p = pin_out.p = nullptr;
+        if (pin_ids.p) (void)hipHostFree(pin_ids.p);
+        if (pin_src.p) (void)hipHostFree(pin_src.p);
+        pin_small.p = pin_leaves.p = pin_out.p = pin_ids.p = pin_src.p = nullptr;
+        if (up_stream) (void)hipStreamSynchronize(up_stream);
+        for (auto e : chunk_ev) (void)hipEventDestroy(e);
+        chunk_ev.clear();
+        if (up_done) (void)hipEventDestroy(up_done);
+        up_done = nullptr;
+        if (up_stream) (void)hipStreamDestroy(up_stream);
+        up_stream = nullptr;
         for (auto &e : ev_pool) {
             (void)hipEventDestroy(e.first);
             (void)hipEventDestroy(e.second);
@@ -496,52 +521,164 @@ int fbh_upload_block(fbh_ctx *c, const uint32_t *feat_ids, uint32_t n_feats, uin
     });
 }
 
+namespace {
+
+// Bounds, power-of-two scales and fixed-point pairs of the f32 pairs in
+// gpair_f32 (GradQuantizer::try_from_bounds, src/types.rs:288-303, 367-385;
+// device passes src/backend/cuda/histogram.cu:1079-1177).
+void quantize_device_pairs(fbh_ctx *c, uint64_t th, uint64_t seed, uint64_t tree,
+                           double scales_out[2], int64_t root_out[2]) {
+    check(launch_gpair_maxabs(c->gpair_f32, c->n_rows, th, seed, tree, c->red_f64,
+                              c->n_red_blocks, c->red_f64 + 2 * c->n_red_blocks, c->stream),
+          "gradient bounds");
+    double mx[2];
+    check(hipMemcpyAsync(c->pin_out.p, c->red_f64 + 2 * c->n_red_blocks, 16,
+                         hipMemcpyDeviceToHost, c->stream),
+          "bounds download");
+    c->sync();
+    std::memcpy(mx, c->pin_out.p, 16);
+    if (!(std::isfinite(mx[0]) && std::isfinite(mx[1]) && mx[0] >= 0.0 && mx[1] >= 0.0))
+        throw InputError(
+            "non-finite gradient or Hessian (or invalid bounds); reduce extreme labels, "
+            "weights, base_score or objective parameters");
+    for (int k = 0; k < 2; k++) {
+        double s = 1.0;
+        const double m = mx[k];
+        if (m > 0.0 && std::isfinite(m)) {
+            const double budget = (double)(1ull << 62) / (double)std::max<uint64_t>(c->n_rows, 1);
+            const double raw = budget / m;
+            if (std::isfinite(raw) && raw > 0.0) {
+                double l = std::floor(std::log2(raw));
+                int e = std::isnan(l) ? 0 : (l > 1000.0 ? 1000 : (l < -1000.0 ? -1000 : (int)l));
+                s = std::exp2((double)e);
+            }
+        }
+        c->scales[k] = s;
+    }
+    check(launch_gpair_quantize(c->gpair_f32, c->n_rows, c->scales[0], c->scales[1], c->gpair,
+                                c->red_i64, c->n_red_blocks, c->red_i64 + 2 * c->n_red_blocks,
+                                c->stream),
+          "gradient quantisation");
+    check(hipMemcpyAsync(c->pin_out.p, c->red_i64 + 2 * c->n_red_blocks, 16,
+                         hipMemcpyDeviceToHost, c->stream),
+          "root sum download");
+    c->sync();
+    std::memcpy(root_out, c->pin_out.p, 16);
+    scales_out[0] = c->scales[0];
+    scales_out[1] = c->scales[1];
+}
+
+}  // namespace
+
 int fbh_upload_quantize_gpair(fbh_ctx *c, const float *g2n, uint64_t th, uint64_t seed,
                               uint64_t tree, double scales_out[2], int64_t root_out[2]) {
     return guard([&] {
-        if (!c || !g2n) throw InputError("null argument");
+        if (!c || !g2n || !scales_out || !root_out) throw InputError("null argument");
         check(hipSetDevice(c->device), "hipSetDevice");
         check(hipMemcpyAsync(c->gpair_f32, g2n, c->n_rows * 8, hipMemcpyHostToDevice, c->stream),
               "gradient upload");
-        check(launch_gpair_maxabs(c->gpair_f32, c->n_rows, th, seed, tree, c->red_f64,
-                                  c->n_red_blocks, c->red_f64 + 2 * c->n_red_blocks, c->stream),
-              "gradient bounds");
-        double mx[2];
-        check(hipMemcpyAsync(c->pin_out.p, c->red_f64 + 2 * c->n_red_blocks, 16,
-                             hipMemcpyDeviceToHost, c->stream),
-              "bounds download");
-        c->sync();
-        std::memcpy(mx, c->pin_out.p, 16);
-        // GradQuantizer::try_from_bounds (src/types.rs:288-303, 367-385).
-        if (!(std::isfinite(mx[0]) && std::isfinite(mx[1]) && mx[0] >= 0.0 && mx[1] >= 0.0))
-            throw InputError(
-                "non-finite gradient or Hessian (or invalid bounds); reduce extreme labels, "
-                "weights, base_score or objective parameters");
-        for (int k = 0; k < 2; k++) {
-            double s = 1.0;
-            const double m = mx[k];
-            if (m > 0.0 && std::isfinite(m)) {
-                const double budget = (double)(1ull << 62) / (double)std::max<uint64_t>(c->n_rows, 1);
-                const double raw = budget / m;
-                if (std::isfinite(raw) && raw > 0.0) {
-                    double l = std::floor(std::log2(raw));
-                    int e = std::isnan(l) ? 0 : (l > 1000.0 ? 1000 : (l < -1000.0 ? -1000 : (int)l));
-                    s = std::exp2((double)e);
-                }
-            }
-            c->scales[k] = s;
+        quantize_device_pairs(c, th, seed, tree, scales_out, root_out);
+    });
+}
+
+int fbh_set_objective(fbh_ctx *c, uint32_t objective, const float *labels,
+                      const float *grad_weights, float base_margin) {
+    return guard([&] {
+        if (!c || !labels) throw InputError("null argument");
+        if (objective > 1) throw InputError("objective must be 0 (squared error) or 1 (logistic)");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        if (c->objective < 0) {
+            c->labels = c->alloc<float>(c->n_rows, "labels");
+            c->margin = c->alloc<float>(c->n_rows, "margins");
+            c->leaf_ids = c->alloc<uint16_t>(c->n_rows, "leaf ids");
         }
-        check(launch_gpair_quantize(c->gpair_f32, c->n_rows, c->scales[0], c->scales[1], c->gpair,
-                                    c->red_i64, c->n_red_blocks, c->red_i64 + 2 * c->n_red_blocks,
-                                    c->stream),
-              "gradient quantisation");
-        check(hipMemcpyAsync(c->pin_out.p, c->red_i64 + 2 * c->n_red_blocks, 16,
-                             hipMemcpyDeviceToHost, c->stream),
-              "root sum download");
+        if (grad_weights && !c->gweights) c->gweights = c->alloc<float>(c->n_rows, "row weights");
+        if (objective == 1 && !c->pin_ids.p) {
+            c->sig = c->alloc<float>(c->n_rows, "sigmoids");
+            c->pinned(c->pin_ids, std::max<uint64_t>(2 * c->n_rows, 64));
+            c->pinned(c->pin_src, std::max<uint64_t>(4 * c->n_rows, 64));
+            check(hipStreamCreateWithFlags(&c->up_stream, hipStreamNonBlocking), "stream");
+            check(hipEventCreateWithFlags(&c->up_done, hipEventDisableTiming), "event");
+            for (int k = 0; k < EXCHANGE_CHUNKS; k++) {
+                hipEvent_t e;
+                check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "event");
+                c->chunk_ev.push_back(e);
+            }
+        }
         c->sync();
-        std::memcpy(root_out, c->pin_out.p, 16);
-        scales_out[0] = c->scales[0];
-        scales_out[1] = c->scales[1];
+        check(hipMemcpy(c->labels, labels, 4 * c->n_rows, hipMemcpyHostToDevice), "label upload");
+        c->has_weights = grad_weights != nullptr;
+        if (grad_weights)
+            check(hipMemcpy(c->gweights, grad_weights, 4 * c->n_rows, hipMemcpyHostToDevice),
+                  "weight upload");
+        check(launch_fill_f32(c->margin, base_margin, c->n_rows, c->stream), "margin init");
+        c->sync();
+        c->objective = (int)objective;
+        c->ids_fresh = false;
+    });
+}
+
+int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th, uint64_t seed,
+                          uint64_t tree, double scales_out[2], int64_t root_out[2]) {
+    return guard([&] {
+        if (!c || !scales_out || !root_out) throw InputError("null argument");
+        if (c->objective < 0) throw InputError("fbh_set_objective has not been called");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        if (c->leaves_pending) {
+            check(hipEventSynchronize(c->leaves_done), "leaf table reuse");
+            c->leaves_pending = false;
+        }
+        const float *w = c->has_weights ? c->gweights : nullptr;
+        if (c->objective == 0) {
+            check(launch_gradient(c->margin, c->labels, w, c->n_rows, 0, c->gpair_f32, c->stream),
+                  "device gradient");
+        } else {
+            if (!fn) throw InputError("the logistic objective needs a sigmoid callback");
+            const uint64_t n = c->n_rows;
+            const int idb = c->ids_fresh ? c->leaf_id_bytes : 0;
+            uint8_t *ids = static_cast<uint8_t *>(c->pin_ids.p);
+            float *src = static_cast<float *>(c->pin_src.p);
+            const uint64_t step = ((n + EXCHANGE_CHUNKS - 1) / EXCHANGE_CHUNKS + 255) & ~uint64_t(255);
+            // Leaf ids of every chunk go down at once, each chunk signalling
+            // its own event; the host works on chunk k while later chunks are
+            // still in flight and chunk k's sigmoids go up on the copy stream.
+            if (idb)
+                for (int k = 0; k < EXCHANGE_CHUNKS; k++) {
+                    const uint64_t b = std::min<uint64_t>(n, k * step), e = std::min<uint64_t>(n, b + step);
+                    if (e > b)
+                        check(hipMemcpyAsync(ids + b * idb,
+                                             static_cast<uint8_t *>(c->leaf_ids) + b * idb,
+                                             (e - b) * idb, hipMemcpyDeviceToHost, c->stream),
+                              "leaf id download");
+                    check(hipEventRecord(c->chunk_ev[k], c->stream), "event");
+                }
+            for (int k = 0; k < EXCHANGE_CHUNKS; k++) {
+                const uint64_t b = std::min<uint64_t>(n, k * step), e = std::min<uint64_t>(n, b + step);
+                if (idb) check(hipEventSynchronize(c->chunk_ev[k]), "leaf id download");
+                if (e <= b) continue;
+                fn(user, b, e - b, idb ? ids + b * idb : nullptr, (uint32_t)idb, src + b);
+                check(hipMemcpyAsync(c->sig + b, src + b, 4 * (e - b),
+                                     hipMemcpyHostToDevice, c->up_stream),
+                      "sigmoid upload");
+            }
+            check(hipEventRecord(c->up_done, c->up_stream), "event");
+            check(hipStreamWaitEvent(c->stream, c->up_done, 0), "stream wait");
+            check(launch_gradient(c->sig, c->labels, w, n, 1, c->gpair_f32, c->stream),
+                  "device gradient");
+        }
+        c->ids_fresh = false;
+        quantize_device_pairs(c, th, seed, tree, scales_out, root_out);
+    });
+}
+
+int fbh_download_margin(fbh_ctx *c, float *out) {
+    return guard([&] {
+        if (!c || !out) throw InputError("null argument");
+        if (c->objective < 0) throw InputError("fbh_set_objective has not been called");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        check(hipMemcpyAsync(out, c->margin, c->n_rows * 4, hipMemcpyDeviceToHost, c->stream),
+              "margin download");
+        c->sync();
     });
 }
 
@@ -970,6 +1107,7 @@ int fbh_assign_leaves(fbh_ctx *c, const fbh_span *spans, const float *values, ui
             ld[m].row_len = spans[i].len;
             ld[m].chunk_begin = chunks;
             ld[m].value = values[i];
+            ld[m].id = i;
             chunks += div_up(spans[i].len, PART_CHUNK);
             m++;
         }
@@ -979,8 +1117,13 @@ int fbh_assign_leaves(fbh_ctx *c, const fbh_span *spans, const float *values, ui
               "leaf table");
         check(hipEventRecord(c->leaves_done, c->stream), "event");
         c->leaves_pending = true;
-        check(launch_assign_leaves(c->d_leaves, m, chunks, c->rows, c->delta, c->stream),
+        const int idb = c->objective >= 0 ? (n <= 256 ? 1 : 2) : 0;
+        if (idb && n > 65536) throw InputError("too many leaves for 16-bit leaf ids");
+        check(launch_assign_leaves(c->d_leaves, m, chunks, c->rows, c->delta, c->margin,
+                                   c->leaf_ids, idb, c->stream),
               "leaf assignment");
+        c->leaf_id_bytes = idb;
+        c->ids_fresh = idb != 0;
     });
 }
 

@@ -879,8 +879,10 @@ hipError_t launch_partition(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_
 // leaves, row arena, quantisation, tile packing
 // ======================================================================
 
+template <int IDB>
 __global__ __launch_bounds__(PART_TPB) void leaf_kernel(const LeafDev *leaves, uint32_t n,
-                                                        const uint32_t *rows, float *delta) {
+                                                        const uint32_t *rows, float *delta,
+                                                        float *margin, void *ids) {
     const uint32_t chunk = blockIdx.x;
     uint32_t lo = 0, hi = n;
     while (hi - lo > 1) {
@@ -891,14 +893,70 @@ __global__ __launch_bounds__(PART_TPB) void leaf_kernel(const LeafDev *leaves, u
     const LeafDev L = leaves[lo];
     const uint32_t c0 = (chunk - L.chunk_begin) * PART_CHUNK;
     const uint32_t c1 = min(c0 + PART_CHUNK, L.row_len);
-    for (uint32_t i = c0 + threadIdx.x; i < c1; i += PART_TPB) delta[rows[L.row_off + i]] = L.value;
+    for (uint32_t i = c0 + threadIdx.x; i < c1; i += PART_TPB) {
+        const uint32_t r = rows[L.row_off + i];
+        delta[r] = L.value;
+        // The same f32 addition as the host's pred += delta.
+        if (margin) margin[r] = margin[r] + L.value;
+        if (IDB == 1) static_cast<uint8_t *>(ids)[r] = (uint8_t)L.id;
+        if (IDB == 2) static_cast<uint16_t *>(ids)[r] = (uint16_t)L.id;
+    }
 }
 
 hipError_t launch_assign_leaves(const LeafDev *leaves, uint32_t n_leaves, uint32_t n_chunks,
-                                const uint32_t *rows, float *delta, hipStream_t s) {
+                                const uint32_t *rows, float *delta, float *margin, void *ids,
+                                int id_bytes, hipStream_t s) {
     if (n_chunks == 0) return hipSuccess;
-    hipLaunchKernelGGL(leaf_kernel, dim3(n_chunks), dim3(PART_TPB), 0, s, leaves, n_leaves, rows,
-                       delta);
+    if (id_bytes == 1)
+        hipLaunchKernelGGL(leaf_kernel<1>, dim3(n_chunks), dim3(PART_TPB), 0, s, leaves, n_leaves,
+                           rows, delta, margin, ids);
+    else if (id_bytes == 2)
+        hipLaunchKernelGGL(leaf_kernel<2>, dim3(n_chunks), dim3(PART_TPB), 0, s, leaves, n_leaves,
+                           rows, delta, margin, ids);
+    else
+        hipLaunchKernelGGL(leaf_kernel<0>, dim3(n_chunks), dim3(PART_TPB), 0, s, leaves, n_leaves,
+                           rows, delta, margin, ids);
+    return hipGetLastError();
+}
+
+// Objective::gradient (src/training/objective.rs:499-530), restated in f32
+// with the host's operation order; compiled without FMA contraction, so the
+// pairs equal the host's bit for bit.
+__global__ __launch_bounds__(256) void gradient_kernel(const float *src, const float *y,
+                                                       const float *w, uint64_t n, int logistic,
+                                                       float *g2n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const float v = src[i];
+        float g = v - y[i];
+        float h = logistic ? fmaxf(v * (1.0f - v), 1e-16f) : 1.0f;
+        if (w) {
+            g = g * w[i];
+            h = h * w[i];
+        }
+        reinterpret_cast<float2 *>(g2n)[i] = make_float2(g, h);
+    }
+}
+
+hipError_t launch_gradient(const float *src, const float *y, const float *w, uint64_t n,
+                           int logistic, float *g2n, hipStream_t s) {
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((n + 255) / 256, 8192);
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(gradient_kernel, dim3(blocks), dim3(256), 0, s, src, y, w, n, logistic,
+                       g2n);
+    return hipGetLastError();
+}
+
+__global__ void fill_f32_kernel(float *p, float v, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+hipError_t launch_fill_f32(float *p, float v, uint64_t n, hipStream_t s) {
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((n + 255) / 256, 4096);
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_f32_kernel, dim3(blocks), dim3(256), 0, s, p, v, n);
     return hipGetLastError();
 }
 

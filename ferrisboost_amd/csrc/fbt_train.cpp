@@ -1,11 +1,14 @@
 // fbt_train.cpp -- the round driver of the device path.
 //
 // Restates train_with_backend (src/training/mod.rs:1299-2376) for the
-// single-output logistic and squared-error objectives with gpu_math="exact":
-// the raw margins live on the host, every round downloads the previous
-// tree's per-row delta, applies it and computes the f32 gradient pairs with
-// the host's libm (so exp() rounds like the CPU engine), uploads them, and
-// the device quantises them to i64 fixed point. Trees are grown depthwise
+// single-output logistic and squared-error objectives with gpu_math="exact".
+// The device keeps labels, weights and margins; squared-error gradients are
+// computed there. For logistic, every round downloads the previous tree's
+// per-row leaf id (one byte at depth <= 8), the host applies the leaf value
+// to its margins and computes the sigmoid with its libm (so exp() rounds like
+// the CPU engine), in chunks overlapped with the copies, and uploads it; the
+// device forms the f32 gradient pairs with the host's operations and
+// quantises them to i64 fixed point. Trees are grown depthwise
 // (build_tree, src/training/mod.rs:3357-4565) or loss-guided
 // (src/training/lossguide.rs:494-700); histograms, split scans, partitions
 // and leaf scatters all run through the fbh_* backend.
@@ -106,6 +109,43 @@ class Pool {
     bool stop_ = false;
 };
 
+// Host half of the exact logistic gradient, one chunk of rows at a time:
+// pred += the previous tree's leaf value, then s = 1 / (1 + expf(-pred))
+// (Objective::gradient, src/training/objective.rs:37-39, 499-530).
+struct SigmoidJob {
+    Pool *pool;
+    float *pred;
+    const std::vector<float> *values;  // leaf values of the previous tree
+};
+
+void sigmoid_chunk(void *user, uint64_t begin, uint64_t n, const void *ids, uint32_t id_bytes,
+                   float *out) {
+    SigmoidJob &J = *static_cast<SigmoidJob *>(user);
+    const float *vals = J.values->data();
+    const uint32_t n_vals = (uint32_t)J.values->size();
+    std::atomic<bool> bad{false};
+    J.pool->run([&](unsigned t) {
+        const uint64_t lo = n * t / J.pool->size(), hi = n * (t + 1) / J.pool->size();
+        float *pred = J.pred + begin;
+        for (uint64_t i = lo; i < hi; i++) {
+            if (ids) {
+                const uint32_t id = id_bytes == 1 ? static_cast<const uint8_t *>(ids)[i]
+                                                  : static_cast<const uint16_t *>(ids)[i];
+                if (id >= n_vals) {
+                    bad = true;
+                    continue;
+                }
+                pred[i] += vals[id];
+            }
+            out[i] = 1.0f / (1.0f + std::exp(-pred[i]));
+        }
+    });
+    // The callback cannot throw across the C ABI; a bad id poisons the
+    // sigmoids so the device bounds check rejects the round.
+    if (bad)
+        for (uint64_t i = 0; i < n; i++) out[i] = std::numeric_limits<float>::quiet_NaN();
+}
+
 // ---------------------------------------------------------------- host math
 // The leaf-value arithmetic of split.rs:113-218, in f64 then f32.
 struct LeafMath {
@@ -167,26 +207,6 @@ std::vector<uint32_t> sample_columns(uint32_t nf, float rate, uint64_t seed, uin
     return ids;
 }
 
-// Page-locked host array from the backend.
-template <class T>
-class PinnedArray {
-  public:
-    explicit PinnedArray(size_t n) {
-        void *p = nullptr;
-        call(fbh_host_alloc(n * sizeof(T), &p));
-        p_ = static_cast<T *>(p);
-    }
-    ~PinnedArray() { fbh_host_free(p_); }
-    PinnedArray(const PinnedArray &) = delete;
-    PinnedArray &operator=(const PinnedArray &) = delete;
-    T &operator[](size_t i) { return p_[i]; }
-    const T &operator[](size_t i) const { return p_[i]; }
-    T *data() { return p_; }
-
-  private:
-    T *p_ = nullptr;
-};
-
 uint64_t sample_threshold(float rate) {  // subsample::threshold_for
     if (rate >= 1.0f || !(rate > 0.0f)) return UINT64_MAX;
     return (uint64_t)((double)rate * (double)(1ull << 53));
@@ -227,11 +247,18 @@ class Grower {
         root.len = n_rows_;
         if (p_.grow_policy == 1) lossguide(t, root, root_sum);
         else depthwise(t, root, root_sum);
+        uint64_t covered = 0;
+        for (const auto &sp : leaves_spans_) covered += sp.len;
+        if (covered != n_rows_)
+            throw RuntimeError("leaf spans cover " + std::to_string(covered) + " of " +
+                               std::to_string(n_rows_) + " rows");
         if (!leaves_spans_.empty())
             call(fbh_assign_leaves(ctx_, leaves_spans_.data(), leaves_values_.data(),
                                    (uint32_t)leaves_spans_.size()));
         return t;
     }
+    // Leaf values of the last grown tree, by leaf position.
+    const std::vector<float> &leaf_values() const { return leaves_values_; }
     uint32_t n_rows_ = 0;
 
   private:
@@ -577,13 +604,13 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     m.n_features = nf;
     m.scale_pos_weight = p.scale_pos_weight;
     m.cuts = sketch_matrix(x, n, nf, p.max_bin, w, cat, threads);
-    // Base score: explicit, else the (weighted) label mean
-    // (Objective::estimate_base_score, src/training/objective.rs:42-60, 452-470).
+    // Base score: explicit, else the label mean weighted by the sample weights
+    // only (Objective::estimate_base_score, src/training/objective.rs:42-60,
+    // 452-470; scale_pos_weight enters the gradient weights alone,
+    // src/training/mod.rs:1450-1468).
     if (p.has_base_score) {
         m.base_score = p.base_score;
     } else {
-        if (p.scale_pos_weight != 1.0f)
-            throw InputError("scale_pos_weight != 1 requires an explicit base_score in this build");
         double acc = 0.0;
         if (!w) {
             const double nn = (double)n;
@@ -654,12 +681,14 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
 
     // ---- round loop ----
     const auto t_train = Clock::now();
+    // Host margins feed the logistic sigmoid; the device keeps its own copy
+    // (the same f32 additions), which squared error uses directly.
     std::vector<float> pred(n, margin);
-    // Pinned staging for the per-round delta download and gradient upload.
-    PinnedArray<float> delta(n), g2(2 * n);
     Grower grower(ctx.get(), p, m.cuts, mono, slots);
     grower.n_rows_ = (uint32_t)n;
     const uint32_t obj = p.objective;
+    call(fbh_set_objective(ctx.get(), obj, y, grad_w, margin));
+    SigmoidJob job{&pool, pred.data(), &grower.leaf_values()};
     double grad_s = 0.0;
     g_round_wall.assign(p.n_rounds, 0.0);
     g_round_hist_ms.assign(p.n_rounds, 0.0);
@@ -682,39 +711,14 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
         }
     };
     for (uint32_t round = 0; round < p.n_rounds; round++) {
+        if (round > 0) close_round(round - 1);
         const auto tg = Clock::now();
-        if (round > 0) {
-            call(fbh_download_delta(ctx.get(), delta.data()));
-            close_round(round - 1);
-        }
-        const bool apply_delta = round > 0;
-        pool.run([&](unsigned t) {
-            const uint64_t lo = n * t / pool.size(), hi = n * (t + 1) / pool.size();
-            for (uint64_t i = lo; i < hi; i++) {
-                if (apply_delta) pred[i] += delta[i];
-                const float pi = pred[i];
-                float g, h;
-                if (obj == 1) {  // Objective::gradient, binary:logistic
-                    const float s = 1.0f / (1.0f + std::exp(-pi));
-                    g = s - y[i];
-                    h = std::fmax(s * (1.0f - s), 1e-16f);
-                } else {
-                    g = pi - y[i];
-                    h = 1.0f;
-                }
-                if (grad_w) {
-                    g = g * grad_w[i];
-                    h = h * grad_w[i];
-                }
-                g2[2 * i] = g;
-                g2[2 * i + 1] = h;
-            }
-        });
-        grad_s += std::chrono::duration<double>(Clock::now() - tg).count();
         double scales[2];
         int64_t root_sum[2];
-        call(fbh_upload_quantize_gpair(ctx.get(), g2.data(), sample_threshold(p.subsample), p.seed,
-                                       round, scales, root_sum));
+        call(fbh_gradient_exchange(ctx.get(), obj == 1 ? sigmoid_chunk : nullptr, &job,
+                                   sample_threshold(p.subsample), p.seed, round, scales,
+                                   root_sum));
+        grad_s += std::chrono::duration<double>(Clock::now() - tg).count();
         std::vector<uint32_t> feats;
         if (p.colsample_bytree < 1.0f) feats = sample_columns(nf, p.colsample_bytree, p.seed, round);
         fbh_span root;
@@ -722,14 +726,8 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
                             (uint32_t)feats.size(), mono.data(), nf, &root));
         m.trees.push_back(grower.grow(scales, root_sum));
     }
-    if (p.n_rounds > 0) {
-        call(fbh_download_delta(ctx.get(), delta.data()));
-        close_round(p.n_rounds - 1);
-        pool.run([&](unsigned t) {
-            const uint64_t lo = n * t / pool.size(), hi = n * (t + 1) / pool.size();
-            for (uint64_t i = lo; i < hi; i++) pred[i] += delta[i];
-        });
-    }
+    call(fbh_download_margin(ctx.get(), pred.data()));
+    if (p.n_rounds > 0) close_round(p.n_rounds - 1);
     g_stats.train_seconds = std::chrono::duration<double>(Clock::now() - t_train).count();
     g_stats.host_gradient_seconds = grad_s;
     g_stats.rounds = p.n_rounds;

@@ -160,6 +160,39 @@ int fbh_upload_quantize_gpair(fbh_ctx *ctx, const float *gpair2n, uint64_t sampl
 /* GpuTrainCtx::upload_gpair: fixed-point pairs quantized on the host. */
 int fbh_upload_gpair_fixed(fbh_ctx *ctx, const int64_t *gpair2n, const double scales[2]);
 
+/* Resident labels, gradient weights and margins (GpuTrainCtx::init_fast_math,
+ * src/backend/cuda/train_ctx.rs:2964-3060): objective 0 = reg:squarederror,
+ * 1 = binary:logistic; grad_weights (may be NULL) are the row weights with
+ * scale_pos_weight folded in; every margin starts at base_margin. From then
+ * on fbh_assign_leaves also adds each row's leaf value to its margin (the
+ * same f32 addition as the host's pred += delta) and records the row's leaf
+ * position (u8 when the tree has at most 256 leaves, else u16). */
+int fbh_set_objective(fbh_ctx *ctx, uint32_t objective, const float *labels,
+                      const float *grad_weights, float base_margin);
+
+/* Host half of the exact-mode logistic gradient: for rows
+ * [row_begin, row_begin + n) apply the last tree's leaf values (leaf_ids is
+ * NULL before the first tree) to the host margins and write
+ * s = 1 / (1 + expf(-margin)) per row to sigmoid_out. */
+typedef void (*fbh_sigmoid_fn)(void *user, uint64_t row_begin, uint64_t n, const void *leaf_ids,
+                               uint32_t id_bytes, float *sigmoid_out);
+
+/* One round's gradient pairs, the exact-mode round of train_with_backend
+ * (src/training/mod.rs:2010-2110: with_prediction_delta, gradient_of
+ * :5449-5459, upload_and_quantize_gpair_sampled) with the per-row traffic cut
+ * to one leaf id down and one f32 up: squared error is computed from the
+ * device margins (no host work); logistic downloads the last tree's leaf ids
+ * in chunks, calls fn per chunk while later chunks are in flight, uploads the
+ * sigmoids and derives g = s - y, h = max(s(1 - s), 1e-16) (times the weight)
+ * on the device with the host's f32 operations. Then masks, scales and
+ * quantizes as fbh_upload_quantize_gpair. */
+int fbh_gradient_exchange(fbh_ctx *ctx, fbh_sigmoid_fn fn, void *user, uint64_t sample_threshold,
+                          uint64_t seed, uint64_t tree, double scales_out[2],
+                          int64_t root_sum_out[2]);
+
+/* The device margins (the training margins after the assigned trees). */
+int fbh_download_margin(fbh_ctx *ctx, float *out);
+
 /* ------------------------------------------------------------------ tree */
 /* GpuTrainCtx::begin_tree_rows (src/backend/cuda/train_ctx.rs:1971-1993) plus
  * the tree's column plan (BlockPlan, src/training/mod.rs:3302-3463): resets

@@ -1560,6 +1560,19 @@ int orc_train(const float *x, uint64_t n, uint32_t nf, const float *labels, cons
         std::vector<float> pred(n, margin);
         std::vector<Fixed> gpair(n);
         std::vector<float> gf(2 * n);
+        // gradient_weights (src/training/mod.rs:5466-5490): scale_pos_weight
+        // multiplies the sample weight (1 when absent) of rows labelled 1;
+        // logistic and squared error both use it (objective.rs:346-356).
+        std::vector<float> spw_w;
+        const float *gw = weights;
+        if (p.scale_pos_weight != 1.0f) {
+            spw_w.resize(n);
+            for (u64 i = 0; i < n; i++) {
+                const float w = weights ? weights[i] : 1.0f;
+                spw_w[i] = labels[i] == 1.0f ? w * p.scale_pos_weight : w;
+            }
+            gw = spw_w.data();
+        }
         auto t0 = std::chrono::steady_clock::now();
         for (u32 round = 0; round < p.n_rounds; round++) {
             double mg = 0, mh = 0;
@@ -1567,9 +1580,9 @@ int orc_train(const float *x, uint64_t n, uint32_t nf, const float *labels, cons
             for (u64 i = 0; i < n; i++) {
                 float g, h;
                 gradient(p.objective, pred[i], labels[i], g, h);
-                if (weights) {
-                    g = g * weights[i];
-                    h = h * weights[i];
+                if (gw) {
+                    g = g * gw[i];
+                    h = h * gw[i];
                 }
                 if (!row_selected(i, th, p.seed, round)) g = h = 0.0f;
                 gf[2 * i] = g;
@@ -1702,6 +1715,12 @@ uint32_t orc_sample_features(uint32_t nf, float rate, uint64_t seed, uint64_t ro
     std::vector<u32> s = sample_features(nf, rate, seed, round);
     std::copy(s.begin(), s.end(), out);
     return (u32)s.size();
+}
+
+uint64_t orc_threshold_for(float rate) { return threshold_for(rate); }
+
+int orc_row_selected(uint64_t row, uint64_t th, uint64_t seed, uint64_t tree) {
+    return row_selected(row, th, seed, tree) ? 1 : 0;
 }
 
 void orc_gradients(const float *pred, const float *labels, const float *w, uint64_t n, uint32_t obj,

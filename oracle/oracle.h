@@ -153,6 +153,10 @@ void orc_quadrature_rule(float nodes[8], float weights[8]);
 uint32_t orc_sample_features(uint32_t n_features, float rate, uint64_t seed, uint64_t round,
                              uint32_t *out);
 
+/* ---- row subsample (src/data/subsample.rs:1-104) ---- */
+uint64_t orc_threshold_for(float rate);
+int orc_row_selected(uint64_t row, uint64_t threshold, uint64_t seed, uint64_t tree);
+
 /* ---- objective (src/training/objective.rs:37-39, 363-530) ---- */
 void orc_gradients(const float *pred, const float *labels, const float *weights, uint64_t n,
                    uint32_t objective, float *out2n);

@@ -163,6 +163,34 @@ def _synthetic(kind, n):
     return getattr(datasets, kind)(n)
 
 
+@pytest.mark.parametrize("objective, depth", [("binary:logistic", 6), ("reg:squarederror", 6),
+                                              ("binary:logistic", 10)])
+def test_sampled_weighted_rounds_match_oracle(fb, oracle, objective, depth):
+    """Device margins, leaf ids (u8 up to 256 leaves, u16 beyond), the chunked
+    sigmoid exchange and on-device gradient pairs reproduce the host round
+    (subsample, row weights, scale_pos_weight, missing values)."""
+    rng = np.random.default_rng(depth * 7 + len(objective))
+    n, nf = 40_037, 7
+    x = rng.normal(size=(n, nf)).astype(np.float32)
+    x[rng.random((n, nf)) < 0.05] = np.nan
+    z = np.nan_to_num(x[:, 0]) - 0.7 * np.nan_to_num(x[:, 1]) * np.nan_to_num(x[:, 2])
+    if objective == "binary:logistic":
+        y = (z + 0.3 * rng.normal(size=n) > 0).astype(np.float32)
+    else:
+        y = (z + 0.1 * rng.normal(size=n)).astype(np.float32)
+    w = rng.uniform(0.2, 3.0, size=n).astype(np.float32)
+    p = {"n_rounds": 7, "max_depth": depth, "eta": 0.3, "subsample": 0.7, "seed": 11,
+         "max_bin": 64, "objective": objective, "min_child_weight": 0.5}
+    if objective == "binary:logistic":
+        p.update(scale_pos_weight=2.5, base_score=0.4)
+    om = oracle.train(x, y, oracle.make_params(**p), weights=w)
+    pm = fb.train(product_params(p), x, y, weight=w, num_boost_round=p["n_rounds"])
+    assert_same_models(om, pm)
+    if depth > 8:
+        assert max(int(t["is_leaf"].sum()) for t in pm.trees()) > 256
+    assert np.array_equal(pm.train_margins(n).view(np.uint32), om.train_margins(n).view(np.uint32))
+
+
 @pytest.mark.parametrize("max_bin", [255, 256])
 def test_plumbing_config_matches_oracle(fb, oracle, max_bin):
     X, y, params, _ = _synthetic("plumbing", 30_000)

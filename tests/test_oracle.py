@@ -632,3 +632,69 @@ def test_shap_categorical_matches_brute_force(oracle):
     for r in range(rows.shape[0]):
         assert np.max(np.abs(got[r] - _brute_shap(m, rows[r], nf))) < 2e-5, r
     assert np.max(np.abs(got.sum(axis=1) - m.predict_margin(rows))) < 1e-4
+
+
+# ---------------------------------------------------------------- row subsample
+
+def _selected(oracle, n, rate, seed, tree):
+    L = oracle.lib()
+    th = L.orc_threshold_for(rate)
+    return np.array([L.orc_row_selected(r, th, seed, tree) for r in range(n)], bool)
+
+
+def test_subsample_threshold_closed_form(oracle):
+    """threshold_for = floor(rate * 2^53), all rows at rate >= 1 or <= 0
+    (src/data/subsample.rs:19-29)."""
+    L = oracle.lib()
+    for rate in (0.1, 0.25, 0.5, 0.7, 0.9, 0.999):
+        assert L.orc_threshold_for(rate) == int(Fraction(float(np.float32(rate))) * 2**53)
+    for rate in (1.0, 1.5, 0.0, -1.0, float("nan")):
+        assert L.orc_threshold_for(rate) == 2**64 - 1
+
+
+def test_subsample_properties(oracle):
+    """src/data/subsample.rs:121-185: reproducible, keyed by seed and tree,
+    Bernoulli per row (counts vary by tree, near the rate)."""
+    a = _selected(oracle, 500, 0.5, 11, 2)
+    assert np.array_equal(a, _selected(oracle, 500, 0.5, 11, 2))
+    assert not np.array_equal(a, _selected(oracle, 500, 0.5, 11, 3))
+    assert not np.array_equal(a, _selected(oracle, 500, 0.5, 12, 2))
+    counts = [int(_selected(oracle, 10_000, 0.5, 1, t).sum()) for t in range(8)]
+    assert len(set(counts)) > 1 and all(4700 <= c < 5300 for c in counts)
+    for rate in (0.1, 0.25, 0.9):
+        frac = _selected(oracle, 100_000, rate, 3, 0).mean()
+        assert abs(frac - rate) < 0.01, rate
+
+
+def test_subsample_one_is_identity_and_sampling_changes_trees(oracle):
+    rng = np.random.default_rng(41)
+    x = rng.normal(size=(3000, 4)).astype(np.float32)
+    y = (x[:, 0] + 0.5 * rng.normal(size=3000) > 0).astype(np.float32)
+    base = oracle.train(x, y, oracle.make_params(n_rounds=4, max_depth=4))
+    one = oracle.train(x, y, oracle.make_params(n_rounds=4, max_depth=4, subsample=1.0))
+    half = oracle.train(x, y, oracle.make_params(n_rounds=4, max_depth=4, subsample=0.5, seed=3))
+    same = oracle.train(x, y, oracle.make_params(n_rounds=4, max_depth=4, subsample=0.5, seed=3))
+    assert all(np.array_equal(a, b) for a, b in zip(base.trees(), one.trees()))
+    assert not all(a.size == b.size and np.array_equal(a, b) for a, b in zip(base.trees(), half.trees()))
+    assert all(np.array_equal(a, b) for a, b in zip(half.trees(), same.trees()))
+
+
+@pytest.mark.parametrize("objective", ["binary:logistic", "reg:squarederror"])
+def test_scale_pos_weight_is_folded_weight(oracle, objective):
+    """gradient_weights (src/training/mod.rs:5466-5490): at a fixed base
+    score, scale_pos_weight k trains the same model as sample weights
+    w * k on rows labelled 1 (and w elsewhere). Sample weights also weight
+    the quantile sketch, so the features have few distinct values (lossless
+    cuts whatever the weights)."""
+    rng = np.random.default_rng(42)
+    n = 4000
+    x = np.clip(np.round(rng.normal(size=(n, 5)) * 3), -8, 8).astype(np.float32)
+    y = (x[:, 0] - x[:, 1] + 0.4 * rng.normal(size=n) > 0.5).astype(np.float32)
+    w = rng.uniform(0.5, 2.0, size=n).astype(np.float32)
+    k = np.float32(3.25)
+    kw = dict(n_rounds=5, max_depth=5, objective=objective, base_score=0.3)
+    a = oracle.train(x, y, oracle.make_params(scale_pos_weight=float(k), **kw), weights=w)
+    b = oracle.train(x, y, oracle.make_params(**kw), weights=np.where(y == 1.0, w * k, w).astype(np.float32))
+    c = oracle.train(x, y, oracle.make_params(**kw), weights=w)
+    assert all(np.array_equal(s, t) for s, t in zip(a.trees(), b.trees()))
+    assert not all(s.size == t.size and np.array_equal(s, t) for s, t in zip(a.trees(), c.trees()))
