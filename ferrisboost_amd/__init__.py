@@ -73,6 +73,7 @@ _DEFAULTS: dict[str, Any] = {
     "hip_tile_bytes": 0,
     "hip_rows_per_block": 0,
     "hip_profile": False,
+    "hip_host_sigmoid": False,
 }
 
 _ALIASES = {
@@ -188,6 +189,7 @@ def _params_struct(p: dict[str, Any], n_features: int) -> N.TrainParams:
     s.tile_bytes = int(p["hip_tile_bytes"])
     s.rows_per_block = int(p["hip_rows_per_block"])
     s.profile = 1 if p["hip_profile"] else 0
+    s.host_sigmoid = 1 if p["hip_host_sigmoid"] else 0
     return s
 
 

@@ -120,7 +120,8 @@ class TrainParams(C.Structure):
         ("tile_bytes", C.c_uint32),
         ("rows_per_block", C.c_uint32),
         ("profile", C.c_uint32),
-        ("reserved2", C.c_uint32 * 3),
+        ("host_sigmoid", C.c_uint32),
+        ("reserved2", C.c_uint32 * 2),
     ]
 
 
@@ -134,7 +135,7 @@ class Stats(C.Structure):
         ("host_gradient_seconds", C.c_double),
         ("device_bytes", C.c_double),
         ("rounds", C.c_uint32),
-        ("reserved", C.c_uint32),
+        ("device_sigmoid", C.c_uint32),
     ]
 
 
@@ -160,7 +161,8 @@ HIP_SYMBOLS = [
     "fbh_last_error", "fbh_device_available", "fbh_ctx_create", "fbh_ctx_destroy",
     "fbh_ctx_device_bytes", "fbh_upload_block", "fbh_upload_quantize_gpair",
     "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_gradient_exchange",
-    "fbh_download_margin", "fbh_begin_tree", "fbh_eval_nodes", "fbh_download_histogram",
+    "fbh_download_margin", "fbh_sigmoid_host", "fbh_sigmoid_device", "fbh_sigmoid_checksum",
+    "fbh_begin_tree", "fbh_eval_nodes", "fbh_download_histogram",
     "fbh_partition", "fbh_assign_leaves", "fbh_download_delta", "fbh_host_alloc",
     "fbh_host_free", "fbh_download_rows",
     "fbh_hist_timing", "fbh_set_timing", "fbh_build_histogram", "fbh_partition_rows",
@@ -214,6 +216,9 @@ def hip() -> C.CDLL:
         L.fbh_set_objective.argtypes = [P, C.c_uint32, P, P, C.c_float]
         L.fbh_gradient_exchange.argtypes = [P, P, P, C.c_uint64, C.c_uint64, C.c_uint64, P, P]
         L.fbh_download_margin.argtypes = [P, P]
+        L.fbh_sigmoid_host.argtypes = [P, C.c_uint64, P]
+        L.fbh_sigmoid_device.argtypes = [C.c_int, P, C.c_uint64, P]
+        L.fbh_sigmoid_checksum.argtypes = [C.c_int, C.c_uint64, C.c_uint64, P]
         L.fbh_begin_tree.argtypes = [P, P, C.c_uint32, P, C.c_uint32, C.POINTER(Span)]
         L.fbh_eval_nodes.argtypes = [P, P, C.c_uint32, C.POINTER(SplitParams), P, P, P,
                                      C.c_uint32]

@@ -10,6 +10,7 @@
 // All work runs in order on one HIP stream; the host blocks only where a
 // result must come back (scales, root sum, split packets, left counts).
 
+#include "fb_expf.h"
 #include "fbhip_internal.h"
 #include "../../include/fbhip.h"
 
@@ -159,6 +160,7 @@ struct fbh_ctx {
     uint64_t *d_cat_in = nullptr;
     uint32_t *d_counts = nullptr, *d_excl = nullptr, *d_totals = nullptr;
     LeafDev *d_leaves = nullptr;
+    float *d_leaf_vals = nullptr;
     uint64_t max_chunks = 0;    // capacity of the partition chunk arrays
     uint64_t cat_in_words = 0;  // capacity of the partition category words
 
@@ -462,6 +464,7 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
         c->d_excl = c->alloc<uint32_t>(c->max_chunks + 1, "partition offsets");
         c->d_totals = c->alloc<uint32_t>(MAX_NODES, "partition totals");
         c->d_leaves = c->alloc<LeafDev>(MAX_NODES, "leaf table");
+        c->d_leaf_vals = c->alloc<float>(MAX_NODES, "leaf values");
         // Staging of the launch tables of one blocking call (each table 256-aligned).
         const size_t eval_tables = sizeof(HistNodeDev) * MAX_NODES + 4 * MAX_NODES +
                                    12 * MAX_NODES + sizeof(SplitNodeDev) * MAX_NODES +
@@ -472,7 +475,7 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
              sizeof(TileDev) * c->tiles.size() + sizeof(TileFeatDev) * c->n_features +
                  sizeof(SplitFeatDev) * c->n_features + 256});
         c->pinned(c->pin_small, small);
-        c->pinned(c->pin_leaves, sizeof(LeafDev) * MAX_NODES);
+        c->pinned(c->pin_leaves, (sizeof(LeafDev) + 4) * MAX_NODES);
         c->pinned(c->pin_out, std::max<size_t>({sizeof(SplitPacketDev) * MAX_NODES +
                                                     8 * (size_t)c->n_slots *
                                                         std::max(1u, c->max_cat_words),
@@ -629,11 +632,12 @@ int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th
             c->leaves_pending = false;
         }
         const float *w = c->has_weights ? c->gweights : nullptr;
-        if (c->objective == 0) {
-            check(launch_gradient(c->margin, c->labels, w, c->n_rows, 0, c->gpair_f32, c->stream),
+        if (c->objective == 0 || !fn) {
+            // Squared error, or logistic with the device sigmoid.
+            check(launch_gradient(c->margin, c->labels, w, c->n_rows, c->objective == 0 ? 0 : 2,
+                                  c->gpair_f32, c->stream),
                   "device gradient");
         } else {
-            if (!fn) throw InputError("the logistic objective needs a sigmoid callback");
             const uint64_t n = c->n_rows;
             const int idb = c->ids_fresh ? c->leaf_id_bytes : 0;
             uint8_t *ids = static_cast<uint8_t *>(c->pin_ids.p);
@@ -1115,13 +1119,24 @@ int fbh_assign_leaves(fbh_ctx *c, const fbh_span *spans, const float *values, ui
         check(hipMemcpyAsync(c->d_leaves, ld, sizeof(LeafDev) * m, hipMemcpyHostToDevice,
                              c->stream),
               "leaf table");
+        const int idb = c->objective >= 0 ? (n <= 256 ? 1 : 2) : 0;
+        if (idb) {
+            // Leaf values by position, staged behind the leaf table.
+            float *pv = reinterpret_cast<float *>(ld + m);
+            std::memcpy(pv, values, 4 * (size_t)n);
+            check(hipMemcpyAsync(c->d_leaf_vals, pv, 4 * (size_t)n, hipMemcpyHostToDevice,
+                                 c->stream),
+                  "leaf values");
+        }
         check(hipEventRecord(c->leaves_done, c->stream), "event");
         c->leaves_pending = true;
-        const int idb = c->objective >= 0 ? (n <= 256 ? 1 : 2) : 0;
-        if (idb && n > 65536) throw InputError("too many leaves for 16-bit leaf ids");
-        check(launch_assign_leaves(c->d_leaves, m, chunks, c->rows, c->delta, c->margin,
-                                   c->leaf_ids, idb, c->stream),
+        check(launch_assign_leaves(c->d_leaves, m, chunks, c->rows, c->delta, c->leaf_ids, idb,
+                                   c->stream),
               "leaf assignment");
+        if (idb)
+            check(launch_apply_leaves(c->leaf_ids, idb, c->d_leaf_vals, c->n_rows, c->margin,
+                                      c->stream),
+                  "margin update");
         c->leaf_id_bytes = idb;
         c->ids_fresh = idb != 0;
     });
@@ -1130,6 +1145,9 @@ int fbh_assign_leaves(fbh_ctx *c, const fbh_span *spans, const float *values, ui
 int fbh_download_delta(fbh_ctx *c, float *out) {
     return guard([&] {
         if (!c || !out) throw InputError("null argument");
+        if (c->objective >= 0)
+            throw InputError("this context keeps the margins (fbh_set_objective); use "
+                             "fbh_download_margin");
         check(hipSetDevice(c->device), "hipSetDevice");
         check(hipMemcpyAsync(out, c->delta, c->n_rows * 4, hipMemcpyDeviceToHost, c->stream),
               "delta download");
@@ -1186,6 +1204,44 @@ int fbh_hist_timing(fbh_ctx *c, double *ms, uint64_t *launches, uint64_t *bytes,
 }
 
 // ------------------------------------------------------------- standalone
+int fbh_sigmoid_host(const float *in, uint64_t n, float *out) {
+    return guard([&] {
+        if ((!in || !out) && n) throw InputError("null argument");
+        for (uint64_t i = 0; i < n; i++) out[i] = fb_sigmoid(in[i]);
+    });
+}
+
+int fbh_sigmoid_device(int device, const float *in, uint64_t n, float *out) {
+    return guard([&] {
+        if ((!in || !out) && n) throw InputError("null argument");
+        if (n == 0) return;
+        check(hipSetDevice(device), "hipSetDevice");
+        float *d = nullptr;
+        check(hipMalloc(&d, 8 * n), "device allocation");
+        std::unique_ptr<float, hipError_t (*)(void *)> own(d, hipFree);
+        check(hipMemcpy(d, in, 4 * n, hipMemcpyHostToDevice), "input upload");
+        check(launch_sigmoid(d, n, d + n, nullptr), "sigmoid");
+        check(hipMemcpy(out, d + n, 4 * n, hipMemcpyDeviceToHost), "output download");
+    });
+}
+
+int fbh_sigmoid_checksum(int device, uint64_t begin, uint64_t end, uint64_t *out) {
+    return guard([&] {
+        if (!out) throw InputError("null argument");
+        if (end > (1ull << 32) || begin > end) throw InputError("range must lie in [0, 2^32]");
+        check(hipSetDevice(device), "hipSetDevice");
+        unsigned long long *d = nullptr;
+        check(hipMalloc(&d, 8), "device allocation");
+        std::unique_ptr<unsigned long long, hipError_t (*)(void *)> own(d, hipFree);
+        const unsigned long long zero = 0;
+        check(hipMemcpy(d, &zero, 8, hipMemcpyHostToDevice), "clear");
+        check(launch_sigmoid_checksum(begin, end, d, nullptr), "sigmoid checksum");
+        unsigned long long v = 0;
+        check(hipMemcpy(&v, d, 8, hipMemcpyDeviceToHost), "checksum download");
+        *out = v;
+    });
+}
+
 int fbh_build_histogram(int device, const void *bins, uint32_t width, uint64_t n_rows,
                         uint32_t n_feats, const uint32_t *offsets, const int64_t *gpair2n,
                         const uint32_t *rows, uint64_t n_sel, int64_t *out) {

@@ -160,17 +160,24 @@ hipError_t launch_partition(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_
                             uint32_t *rows, uint32_t *tmp, uint8_t *flags, uint32_t *chunk_counts,
                             uint32_t *chunk_offsets, uint32_t *totals, const uint64_t *cat_words,
                             hipStream_t s);
-// delta[row] = value; margin[row] += value (if margin); ids[row] = leaf
-// position as id_bytes (0: none, 1: u8, 2: u16).
+// id_bytes 0: delta[row] = leaf value; 1 / 2: ids[row] = leaf position as
+// u8 / u16.
 hipError_t launch_assign_leaves(const LeafDev *leaves, uint32_t n_leaves, uint32_t n_chunks,
-                                const uint32_t *rows, float *delta, float *margin, void *ids,
-                                int id_bytes, hipStream_t s);
+                                const uint32_t *rows, float *delta, void *ids, int id_bytes,
+                                hipStream_t s);
+// margin[row] += values[ids[row]] over all rows (id_bytes 1 or 2).
+hipError_t launch_apply_leaves(const void *ids, int id_bytes, const float *values, uint64_t n,
+                               float *margin, hipStream_t s);
 // Objective gradient pairs (f32, interleaved) from a per-row source value:
-// logistic = 0: squared error from the margin (g = p - y, h = 1);
-// logistic = 1: from the host's sigmoid s (g = s - y, h = max(s(1 - s), 1e-16)).
-// Both are multiplied by the row weight when w is non-null.
+// mode 0: squared error from the margin (g = p - y, h = 1);
+// mode 1: from the host's sigmoid s (g = s - y, h = max(s(1 - s), 1e-16));
+// mode 2: as 1 with s computed on the device from the margin.
+// All are multiplied by the row weight when w is non-null.
 hipError_t launch_gradient(const float *src, const float *y, const float *w, uint64_t n,
-                           int logistic, float *g2n, hipStream_t s);
+                           int mode, float *g2n, hipStream_t s);
+hipError_t launch_sigmoid(const float *in, uint64_t n, float *out, hipStream_t s);
+hipError_t launch_sigmoid_checksum(uint64_t begin, uint64_t end, unsigned long long *out,
+                                   hipStream_t s);
 hipError_t launch_fill_f32(float *p, float v, uint64_t n, hipStream_t s);
 hipError_t launch_init_rows(uint32_t *rows, float *delta, uint64_t n, hipStream_t s);
 hipError_t launch_gpair_maxabs(float *g2n, uint64_t n, uint64_t threshold, uint64_t seed,

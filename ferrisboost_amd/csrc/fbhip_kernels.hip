@@ -17,6 +17,7 @@
 //   gpair_*_kernel       device quantisation (histogram.cu:1079-1177)
 //   shap_kernel          QuadratureTreeSHAP (explain.rs:303-401, 704-728)
 
+#include "fb_expf.h"
 #include "fbhip_internal.h"
 
 #include <math.h>
@@ -879,10 +880,21 @@ hipError_t launch_partition(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_
 // leaves, row arena, quantisation, tile packing
 // ======================================================================
 
+// SplitMix64 finaliser (subsample::mix, src/data/subsample.rs).
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ uint64_t rotl64(uint64_t x, int r) { return (x << r) | (x >> (64 - r)); }
+
+// IDB == 0: delta[row] = leaf value; IDB == 1 / 2: ids[row] = leaf position
+// as u8 / u16 (the margins are then updated in row order by apply_leaves).
 template <int IDB>
 __global__ __launch_bounds__(PART_TPB) void leaf_kernel(const LeafDev *leaves, uint32_t n,
                                                         const uint32_t *rows, float *delta,
-                                                        float *margin, void *ids) {
+                                                        void *ids) {
     const uint32_t chunk = blockIdx.x;
     uint32_t lo = 0, hi = n;
     while (hi - lo > 1) {
@@ -895,41 +907,67 @@ __global__ __launch_bounds__(PART_TPB) void leaf_kernel(const LeafDev *leaves, u
     const uint32_t c1 = min(c0 + PART_CHUNK, L.row_len);
     for (uint32_t i = c0 + threadIdx.x; i < c1; i += PART_TPB) {
         const uint32_t r = rows[L.row_off + i];
-        delta[r] = L.value;
-        // The same f32 addition as the host's pred += delta.
-        if (margin) margin[r] = margin[r] + L.value;
+        if (IDB == 0) delta[r] = L.value;
         if (IDB == 1) static_cast<uint8_t *>(ids)[r] = (uint8_t)L.id;
         if (IDB == 2) static_cast<uint16_t *>(ids)[r] = (uint16_t)L.id;
     }
 }
 
+// margin[row] += values[ids[row]] in row order: the same f32 addition as the
+// host's pred += delta.
+template <int IDB>
+__global__ __launch_bounds__(256) void apply_leaves_kernel(const void *ids, const float *values,
+                                                           uint64_t n, float *margin) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t id = IDB == 1 ? (uint32_t) static_cast<const uint8_t *>(ids)[i]
+                                     : (uint32_t) static_cast<const uint16_t *>(ids)[i];
+        margin[i] = margin[i] + values[id];
+    }
+}
+
 hipError_t launch_assign_leaves(const LeafDev *leaves, uint32_t n_leaves, uint32_t n_chunks,
-                                const uint32_t *rows, float *delta, float *margin, void *ids,
-                                int id_bytes, hipStream_t s) {
+                                const uint32_t *rows, float *delta, void *ids, int id_bytes,
+                                hipStream_t s) {
     if (n_chunks == 0) return hipSuccess;
     if (id_bytes == 1)
         hipLaunchKernelGGL(leaf_kernel<1>, dim3(n_chunks), dim3(PART_TPB), 0, s, leaves, n_leaves,
-                           rows, delta, margin, ids);
+                           rows, delta, ids);
     else if (id_bytes == 2)
         hipLaunchKernelGGL(leaf_kernel<2>, dim3(n_chunks), dim3(PART_TPB), 0, s, leaves, n_leaves,
-                           rows, delta, margin, ids);
+                           rows, delta, ids);
     else
         hipLaunchKernelGGL(leaf_kernel<0>, dim3(n_chunks), dim3(PART_TPB), 0, s, leaves, n_leaves,
-                           rows, delta, margin, ids);
+                           rows, delta, ids);
+    return hipGetLastError();
+}
+
+hipError_t launch_apply_leaves(const void *ids, int id_bytes, const float *values, uint64_t n,
+                               float *margin, hipStream_t s) {
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((n + 255) / 256, 8192);
+    if (blocks == 0) return hipSuccess;
+    if (id_bytes == 1)
+        hipLaunchKernelGGL(apply_leaves_kernel<1>, dim3(blocks), dim3(256), 0, s, ids, values, n,
+                           margin);
+    else
+        hipLaunchKernelGGL(apply_leaves_kernel<2>, dim3(blocks), dim3(256), 0, s, ids, values, n,
+                           margin);
     return hipGetLastError();
 }
 
 // Objective::gradient (src/training/objective.rs:499-530), restated in f32
 // with the host's operation order; compiled without FMA contraction, so the
-// pairs equal the host's bit for bit.
+// pairs equal the host's bit for bit. mode 0: squared error from the margin;
+// 1: logistic from the host's sigmoid in src; 2: logistic from the margin
+// with the device sigmoid (bit-identical to the host's libm).
 __global__ __launch_bounds__(256) void gradient_kernel(const float *src, const float *y,
-                                                       const float *w, uint64_t n, int logistic,
+                                                       const float *w, uint64_t n, int mode,
                                                        float *g2n) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * blockDim.x) {
-        const float v = src[i];
+        const float v = mode == 2 ? fb_sigmoid(src[i]) : src[i];
         float g = v - y[i];
-        float h = logistic ? fmaxf(v * (1.0f - v), 1e-16f) : 1.0f;
+        float h = mode != 0 ? fmaxf(v * (1.0f - v), 1e-16f) : 1.0f;
         if (w) {
             g = g * w[i];
             h = h * w[i];
@@ -938,12 +976,54 @@ __global__ __launch_bounds__(256) void gradient_kernel(const float *src, const f
     }
 }
 
-hipError_t launch_gradient(const float *src, const float *y, const float *w, uint64_t n,
-                           int logistic, float *g2n, hipStream_t s) {
+hipError_t launch_gradient(const float *src, const float *y, const float *w, uint64_t n, int mode,
+                           float *g2n, hipStream_t s) {
     const uint32_t blocks = (uint32_t)std::min<uint64_t>((n + 255) / 256, 8192);
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(gradient_kernel, dim3(blocks), dim3(256), 0, s, src, y, w, n, logistic,
-                       g2n);
+    hipLaunchKernelGGL(gradient_kernel, dim3(blocks), dim3(256), 0, s, src, y, w, n, mode, g2n);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void sigmoid_kernel(const float *in, uint64_t n, float *out) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        out[i] = fb_sigmoid(in[i]);
+}
+
+hipError_t launch_sigmoid(const float *in, uint64_t n, float *out, hipStream_t s) {
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((n + 255) / 256, 8192);
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(sigmoid_kernel, dim3(blocks), dim3(256), 0, s, in, n, out);
+    return hipGetLastError();
+}
+
+// Sum over bit patterns u in [begin, end) of mix64(u ^ bits(sigmoid(u)) << 32)
+// (NaN outputs canonicalised), wrapping: a fingerprint of the sigmoid over
+// every float input, compared with the host libm's.
+__global__ __launch_bounds__(256) void sigmoid_checksum_kernel(uint64_t begin, uint64_t end,
+                                                               unsigned long long *out) {
+    uint64_t acc = 0;
+    for (uint64_t u = begin + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; u < end;
+         u += (uint64_t)gridDim.x * blockDim.x) {
+        const float s = fb_sigmoid(__builtin_bit_cast(float, (uint32_t)u));
+        const uint32_t b = s != s ? 0x7fc00000u : __builtin_bit_cast(uint32_t, s);
+        acc += mix64(u ^ ((uint64_t)b << 32));
+    }
+    __shared__ uint64_t sm[256];
+    sm[threadIdx.x] = acc;
+    __syncthreads();
+    for (uint32_t k = 128; k > 0; k >>= 1) {
+        if (threadIdx.x < k) sm[threadIdx.x] += sm[threadIdx.x + k];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) global_add_u64(out, sm[0]);
+}
+
+hipError_t launch_sigmoid_checksum(uint64_t begin, uint64_t end, unsigned long long *out,
+                                   hipStream_t s) {
+    if (end <= begin) return hipSuccess;
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((end - begin + 255) / 256, 65536);
+    hipLaunchKernelGGL(sigmoid_checksum_kernel, dim3(blocks), dim3(256), 0, s, begin, end, out);
     return hipGetLastError();
 }
 
@@ -975,13 +1055,6 @@ hipError_t launch_init_rows(uint32_t *rows, float *delta, uint64_t n, hipStream_
     return hipGetLastError();
 }
 
-__device__ __forceinline__ uint64_t mix64(uint64_t z) {
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    return z ^ (z >> 31);
-}
-
-__device__ __forceinline__ uint64_t rotl64(uint64_t x, int r) { return (x << r) | (x >> (64 - r)); }
 
 // subsample::row_selected (src/data/subsample.rs).
 __device__ __forceinline__ bool row_selected(uint64_t row, uint64_t th, uint64_t seed,

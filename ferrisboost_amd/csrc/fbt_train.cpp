@@ -146,6 +146,32 @@ void sigmoid_chunk(void *user, uint64_t begin, uint64_t n, const void *ids, uint
         for (uint64_t i = 0; i < n; i++) out[i] = std::numeric_limits<float>::quiet_NaN();
 }
 
+// True when the device sigmoid equals the host libm's 1 / (1 + expf(-x)) on
+// probe inputs: a prime-stride sweep of all float bit patterns plus a dense
+// sweep of the margins training meets. A host whose libm rounds differently
+// keeps the host sigmoid, so exactness never rests on the device restatement.
+bool device_sigmoid_matches_host(int device) {
+    std::vector<float> in;
+    in.reserve(300000);
+    for (uint64_t u = 0; u < (1ull << 32); u += 65521) {
+        uint32_t b = (uint32_t)u;
+        float x;
+        std::memcpy(&x, &b, 4);
+        in.push_back(x);
+    }
+    for (float x = -104.0f; x <= 104.0f; x += 0.001953125f) in.push_back(x);
+    std::vector<float> dev(in.size());
+    if (fbh_sigmoid_device(device, in.data(), in.size(), dev.data()) != FBH_OK) return false;
+    for (size_t i = 0; i < in.size(); i++) {
+        const float h = 1.0f / (1.0f + std::exp(-in[i]));
+        uint32_t a, b;
+        std::memcpy(&a, &h, 4);
+        std::memcpy(&b, &dev[i], 4);
+        if (a != b && !(h != h && dev[i] != dev[i])) return false;
+    }
+    return true;
+}
+
 // ---------------------------------------------------------------- host math
 // The leaf-value arithmetic of split.rs:113-218, in f64 then f32.
 struct LeafMath {
@@ -689,6 +715,7 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     const uint32_t obj = p.objective;
     call(fbh_set_objective(ctx.get(), obj, y, grad_w, margin));
     SigmoidJob job{&pool, pred.data(), &grower.leaf_values()};
+    const bool dev_sigmoid = obj == 1 && !p.host_sigmoid && device_sigmoid_matches_host(p.device);
     double grad_s = 0.0;
     g_round_wall.assign(p.n_rounds, 0.0);
     g_round_hist_ms.assign(p.n_rounds, 0.0);
@@ -715,7 +742,7 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
         const auto tg = Clock::now();
         double scales[2];
         int64_t root_sum[2];
-        call(fbh_gradient_exchange(ctx.get(), obj == 1 ? sigmoid_chunk : nullptr, &job,
+        call(fbh_gradient_exchange(ctx.get(), obj == 1 && !dev_sigmoid ? sigmoid_chunk : nullptr, &job,
                                    sample_threshold(p.subsample), p.seed, round, scales,
                                    root_sum));
         grad_s += std::chrono::duration<double>(Clock::now() - tg).count();
@@ -731,6 +758,7 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     g_stats.train_seconds = std::chrono::duration<double>(Clock::now() - t_train).count();
     g_stats.host_gradient_seconds = grad_s;
     g_stats.rounds = p.n_rounds;
+    g_stats.device_sigmoid = dev_sigmoid ? 1 : 0;
     double ms = 0.0;
     uint64_t launches = 0, bytes = 0;
     call(fbh_hist_timing(ctx.get(), &ms, &launches, &bytes, 0));

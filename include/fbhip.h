@@ -179,19 +179,33 @@ typedef void (*fbh_sigmoid_fn)(void *user, uint64_t row_begin, uint64_t n, const
 
 /* One round's gradient pairs, the exact-mode round of train_with_backend
  * (src/training/mod.rs:2010-2110: with_prediction_delta, gradient_of
- * :5449-5459, upload_and_quantize_gpair_sampled) with the per-row traffic cut
- * to one leaf id down and one f32 up: squared error is computed from the
- * device margins (no host work); logistic downloads the last tree's leaf ids
- * in chunks, calls fn per chunk while later chunks are in flight, uploads the
- * sigmoids and derives g = s - y, h = max(s(1 - s), 1e-16) (times the weight)
- * on the device with the host's f32 operations. Then masks, scales and
- * quantizes as fbh_upload_quantize_gpair. */
+ * :5449-5459, upload_and_quantize_gpair_sampled). Squared error is computed
+ * from the device margins. Logistic with fn == NULL uses the device sigmoid
+ * (fbh_sigmoid_device, bit-identical to the host libm's 1 / (1 + expf(-x)))
+ * on the device margins: no host work, no per-row traffic. Logistic with a
+ * callback downloads the last tree's leaf ids in chunks, calls fn per chunk
+ * while later chunks are in flight and uploads the sigmoids. Either way the
+ * device derives g = s - y, h = max(s(1 - s), 1e-16) (times the weight) with
+ * the host's f32 operations, then masks, scales and quantizes as
+ * fbh_upload_quantize_gpair. */
 int fbh_gradient_exchange(fbh_ctx *ctx, fbh_sigmoid_fn fn, void *user, uint64_t sample_threshold,
                           uint64_t seed, uint64_t tree, double scales_out[2],
                           int64_t root_sum_out[2]);
 
 /* The device margins (the training margins after the assigned trees). */
 int fbh_download_margin(fbh_ctx *ctx, float *out);
+
+/* The logistic sigmoid 1 / (1 + expf(-x)) of Objective::gradient
+ * (src/training/objective.rs:37-39) with expf restated from glibc's
+ * table-driven method, computed by the host compile (fbh_sigmoid_host) or on
+ * the device (fbh_sigmoid_device). fbh_sigmoid_checksum fingerprints the
+ * device sigmoid over the float bit patterns [begin, end) (end <= 2^32):
+ * the wrapping sum of splitmix64(u ^ bits(s(u)) << 32), NaN outputs as
+ * 0x7fc00000. The round driver compares device and host sigmoids on probe
+ * inputs before it relies on the device. */
+int fbh_sigmoid_host(const float *in, uint64_t n, float *out);
+int fbh_sigmoid_device(int device, const float *in, uint64_t n, float *out);
+int fbh_sigmoid_checksum(int device, uint64_t begin, uint64_t end, uint64_t *out);
 
 /* ------------------------------------------------------------------ tree */
 /* GpuTrainCtx::begin_tree_rows (src/backend/cuda/train_ctx.rs:1971-1993) plus

@@ -56,7 +56,10 @@ typedef struct {
     uint32_t tile_bytes;       /* LDS histogram tile (0 = default) */
     uint32_t rows_per_block;   /* histogram rows per workgroup (0 = default) */
     uint32_t profile;          /* 1: time histogram kernels with HIP events */
-    uint32_t reserved2[3];
+    uint32_t host_sigmoid;     /* 1: logistic sigmoid on the host every round
+                                  (0: on the device once it matches the host
+                                  libm on the probe inputs) */
+    uint32_t reserved2[2];
 } fbt_params;
 
 /* One tree node: Node (src/model/tree.rs:52-111). */
@@ -82,10 +85,10 @@ typedef struct {
     double hist_kernel_ms;    /* histogram kernels (HIP events; profile=1) */
     uint64_t hist_launches;
     uint64_t hist_bytes;      /* algorithmic bytes of the histogram launches */
-    double host_gradient_seconds;
+    double host_gradient_seconds;  /* the per-round gradient step (host and device) */
     double device_bytes;      /* bytes the backend context holds */
     uint32_t rounds;
-    uint32_t reserved;
+    uint32_t device_sigmoid;  /* 1: logistic gradients used the device sigmoid */
 } fbt_stats;
 
 typedef struct fbt_model fbt_model;

@@ -1717,6 +1717,35 @@ uint32_t orc_sample_features(uint32_t nf, float rate, uint64_t seed, uint64_t ro
     return (u32)s.size();
 }
 
+void orc_sigmoid(const float *in, uint64_t n, float *out) {
+    for (uint64_t i = 0; i < n; i++) out[i] = sigmoidf(in[i]);
+}
+
+uint64_t orc_sigmoid_checksum(uint64_t begin, uint64_t end, uint32_t threads) {
+    if (threads == 0) threads = 1;
+    std::vector<u64> part(threads, 0);
+    std::vector<std::thread> pool;
+    for (u32 t = 0; t < threads; t++)
+        pool.emplace_back([&, t] {
+            u64 acc = 0;
+            for (u64 u = begin + t; u < end; u += threads) {
+                const u32 b = (u32)u;
+                float x;
+                std::memcpy(&x, &b, 4);
+                const float s = sigmoidf(x);
+                u32 sb;
+                std::memcpy(&sb, &s, 4);
+                if (s != s) sb = 0x7fc00000u;
+                acc += mix64(u ^ ((u64)sb << 32));
+            }
+            part[t] = acc;
+        });
+    for (auto &th : pool) th.join();
+    u64 acc = 0;
+    for (u64 v : part) acc += v;
+    return acc;
+}
+
 uint64_t orc_threshold_for(float rate) { return threshold_for(rate); }
 
 int orc_row_selected(uint64_t row, uint64_t th, uint64_t seed, uint64_t tree) {

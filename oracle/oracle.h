@@ -163,6 +163,12 @@ void orc_gradients(const float *pred, const float *labels, const float *weights,
 float orc_base_margin(uint32_t objective, float base_score);
 float orc_estimate_base_score(const float *labels, const float *weights, uint64_t n);
 
+/* Logistic sigmoid 1 / (1 + expf(-x)) with the host libm (objective.rs:37-39),
+ * elementwise, and its fingerprint over float bit patterns [begin, end):
+ * wrapping sum of splitmix64(u ^ bits(s(u)) << 32), NaN outputs as 0x7fc00000. */
+void orc_sigmoid(const float *in, uint64_t n, float *out);
+uint64_t orc_sigmoid_checksum(uint64_t begin, uint64_t end, uint32_t threads);
+
 /* Message of the last failing call on this thread. */
 const char *orc_last_error(void);
 

@@ -172,6 +172,10 @@ def lib() -> C.CDLL:
         L.orc_quadrature_rule.restype = None
         L.orc_sample_features.argtypes = [C.c_uint32, C.c_float, C.c_uint64, C.c_uint64, P]
         L.orc_sample_features.restype = C.c_uint32
+        L.orc_sigmoid.argtypes = [P, C.c_uint64, P]
+        L.orc_sigmoid.restype = None
+        L.orc_sigmoid_checksum.argtypes = [C.c_uint64, C.c_uint64, C.c_uint32]
+        L.orc_sigmoid_checksum.restype = C.c_uint64
         L.orc_threshold_for.argtypes = [C.c_float]
         L.orc_threshold_for.restype = C.c_uint64
         L.orc_row_selected.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64]

@@ -163,12 +163,37 @@ def _synthetic(kind, n):
     return getattr(datasets, kind)(n)
 
 
-@pytest.mark.parametrize("objective, depth", [("binary:logistic", 6), ("reg:squarederror", 6),
-                                              ("binary:logistic", 10)])
-def test_sampled_weighted_rounds_match_oracle(fb, oracle, objective, depth):
-    """Device margins, leaf ids (u8 up to 256 leaves, u16 beyond), the chunked
-    sigmoid exchange and on-device gradient pairs reproduce the host round
-    (subsample, row weights, scale_pos_weight, missing values)."""
+def test_device_sigmoid_equals_host_libm_on_every_float(N, oracle):
+    """The device sigmoid (expf restated from glibc's method) against the
+    host libm's 1 / (1 + expf(-x)) on all 2^32 float inputs, compared by
+    fingerprints of four 2^30-input ranges."""
+    import os
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    for k in range(4):
+        b, e = k << 30, (k + 1) << 30
+        dev = C.c_uint64()
+        N.check_hip(N.hip().fbh_sigmoid_checksum(0, b, e, C.byref(dev)))
+        host = oracle.lib().orc_sigmoid_checksum(b, e, threads)
+        assert dev.value == host, f"range {k}: device {dev.value:#x} host {host:#x}"
+    # denormal and saturated outputs element by element
+    x = np.array([-88.0, -87.5, -88.7, -89.0, -103.0, 0.0, -0.0, 1e-30, 20.0, 88.0, -20.0,
+                  np.inf, -np.inf], np.float32)
+    got = np.empty_like(x)
+    want = np.empty_like(x)
+    N.check_hip(N.hip().fbh_sigmoid_device(0, N.ptr(x), x.size, N.ptr(got)))
+    oracle.lib().orc_sigmoid(oracle._p(x), x.size, oracle._p(want))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("objective, depth, host_sigmoid", [
+    ("binary:logistic", 6, False), ("reg:squarederror", 6, False), ("binary:logistic", 10, False),
+    ("binary:logistic", 6, True), ("binary:logistic", 10, True)])
+def test_sampled_weighted_rounds_match_oracle(fb, oracle, objective, depth, host_sigmoid):
+    """Device margins, leaf ids (u8 up to 256 leaves, u16 beyond), the device
+    sigmoid or the chunked host-sigmoid exchange, and on-device gradient pairs
+    reproduce the host round (subsample, row weights, scale_pos_weight,
+    missing values)."""
     rng = np.random.default_rng(depth * 7 + len(objective))
     n, nf = 40_037, 7
     x = rng.normal(size=(n, nf)).astype(np.float32)
@@ -184,8 +209,11 @@ def test_sampled_weighted_rounds_match_oracle(fb, oracle, objective, depth):
     if objective == "binary:logistic":
         p.update(scale_pos_weight=2.5, base_score=0.4)
     om = oracle.train(x, y, oracle.make_params(**p), weights=w)
-    pm = fb.train(product_params(p), x, y, weight=w, num_boost_round=p["n_rounds"])
+    pm = fb.train(dict(product_params(p), hip_host_sigmoid=host_sigmoid), x, y, weight=w,
+                  num_boost_round=p["n_rounds"])
     assert_same_models(om, pm)
+    if objective == "binary:logistic":
+        assert pm.stats["device_sigmoid"] == (0 if host_sigmoid else 1)
     if depth > 8:
         assert max(int(t["is_leaf"].sum()) for t in pm.trees()) > 256
     assert np.array_equal(pm.train_margins(n).view(np.uint32), om.train_margins(n).view(np.uint32))

@@ -200,3 +200,27 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=120)
     assert r.returncode != 0
     assert "one GPU" in (r.stdout + r.stderr)
+
+
+def test_host_sigmoid_restatement_equals_libm(oracle):
+    """The restated expf (glibc's table-driven method) gives the host libm's
+    logistic sigmoid bit for bit: every 251st float bit pattern (17.1M
+    inputs, all exponents) plus a dense sweep of the margins training meets.
+    The device compile of the same code is checked on all 2^32 inputs by the
+    GPU suite."""
+    from ferrisboost_amd import _native as N
+
+    u = np.arange(0, 2**32, 251, dtype=np.uint64).astype(np.uint32)
+    x = np.concatenate([u.view(np.float32),
+                        np.arange(-105.0, 105.0, 2.0**-10, dtype=np.float64).astype(np.float32)])
+    got = np.empty_like(x)
+    want = np.empty_like(x)
+    N.check_hip(N.hip().fbh_sigmoid_host(N.ptr(x), x.size, N.ptr(got)))
+    oracle.lib().orc_sigmoid(oracle._p(x), x.size, oracle._p(want))
+    gb, wb = got.view(np.uint32).copy(), want.view(np.uint32).copy()
+    gb[np.isnan(got)] = 0x7FC00000
+    wb[np.isnan(want)] = 0x7FC00000
+    bad = np.nonzero(gb != wb)[0]
+    assert bad.size == 0, [(hex(int(x.view(np.uint32)[i])), got[i], want[i]) for i in bad[:5]]
+    # denormal outputs are produced and kept
+    assert np.any((want > 0) & (want < np.finfo(np.float32).tiny))
