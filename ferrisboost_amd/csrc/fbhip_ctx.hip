@@ -130,6 +130,9 @@ struct fbh_ctx {
     };
     std::vector<Tile> tiles;
     std::vector<int32_t> feat_tile, feat_pos;
+    // Column-major bins of every feature (the partition reads one cell per
+    // row: rows of the nodes splitting on one feature share cache lines).
+    std::vector<uint8_t *> cols;
     std::vector<uint8_t> uploaded;
 
     float *gpair_f32 = nullptr;
@@ -138,7 +141,6 @@ struct fbh_ctx {
     uint8_t *flags = nullptr;
     float *delta = nullptr;
     int64_t *hist = nullptr;
-    uint8_t *col_stage = nullptr;
     double *red_f64 = nullptr;
     int64_t *red_i64 = nullptr;
     uint32_t n_red_blocks = 1024;
@@ -430,6 +432,16 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
 
         // ---- allocation, once ----
         for (auto &t : c->tiles) t.data = c->alloc<uint8_t>(n_rows * t.stride, "tile records");
+        {
+            uint64_t col_bytes = 0;
+            for (uint32_t f = 0; f < c->n_features; f++) col_bytes += n_rows * c->width[f];
+            uint8_t *base = c->alloc<uint8_t>(col_bytes, "bin columns");
+            c->cols.resize(c->n_features);
+            for (uint32_t f = 0; f < c->n_features; f++) {
+                c->cols[f] = base;
+                base += n_rows * c->width[f];
+            }
+        }
         c->uploaded.assign(c->n_features, 0);
         c->gpair_f32 = c->alloc<float>(2 * n_rows, "f32 gradient pairs");
         c->gpair = c->alloc<int64_t>(2 * n_rows, "fixed-point gradient pairs");
@@ -438,7 +450,6 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
         c->flags = c->alloc<uint8_t>(n_rows, "partition flags");
         c->delta = c->alloc<float>(n_rows, "prediction delta");
         c->hist = c->alloc<int64_t>((size_t)c->n_slots * c->width_max * 2, "histogram slots");
-        c->col_stage = c->alloc<uint8_t>(n_rows * 2, "column staging");
         c->red_f64 = c->alloc<double>(2 * c->n_red_blocks + 2, "reduction scratch");
         c->red_i64 = c->alloc<int64_t>(2 * c->n_red_blocks + 2, "reduction scratch");
         c->d_tiles = c->alloc<TileDev>(c->tiles.size(), "tile table");
@@ -511,11 +522,11 @@ int fbh_upload_block(fbh_ctx *c, const uint32_t *feat_ids, uint32_t n_feats, uin
             const uint32_t f = feat_ids[l];
             const fbh_ctx::Tile &t = c->tiles[c->feat_tile[f]];
             const uint8_t *src = static_cast<const uint8_t *>(bins) + (uint64_t)l * c->n_rows * width;
-            check(hipMemcpyAsync(c->col_stage, src, c->n_rows * width, hipMemcpyHostToDevice,
+            check(hipMemcpyAsync(c->cols[f], src, c->n_rows * width, hipMemcpyHostToDevice,
                                  c->stream),
                   "block upload");
-            // One feature column into its record position.
-            check(launch_pack_feature(c->col_stage, c->n_rows, width, t.data, t.stride,
+            // The column into its record position.
+            check(launch_pack_feature(c->cols[f], c->n_rows, width, t.data, t.stride,
                                       (uint32_t)c->feat_pos[f] * width, c->stream),
                   "tile packing");
             c->uploaded[f] = 1;
@@ -1041,9 +1052,9 @@ int fbh_partition(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n, const uint64
             d.row_len = r.rows.len;
             d.chunk_begin = chunks;
             d.n_chunks = div_up(r.rows.len, PART_CHUNK);
-            d.data = t.data;
-            d.stride = t.stride;
-            d.byte_off = (uint32_t)c->feat_pos[r.feat] * t.width;
+            d.data = c->cols[r.feat];
+            d.stride = t.width;
+            d.byte_off = 0;
             d.width = t.width;
             d.bin = r.bin;
             d.missing_left = r.missing_left;
