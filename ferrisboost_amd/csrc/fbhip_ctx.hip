@@ -148,21 +148,14 @@ struct fbh_ctx {
     // launch tables (device) and their pinned staging
     TileDev *d_tiles = nullptr;
     TileFeatDev *d_tilefeats = nullptr;
-    HistNodeDev *d_hnodes = nullptr;
-    uint32_t *d_u32a = nullptr;  // zero-slot list / subtract triples
-    uint32_t *d_u32b = nullptr;
-    SplitNodeDev *d_snodes = nullptr;
     SplitFeatDev *d_sfeats = nullptr;
-    uint8_t *d_enabled = nullptr;
+    uint8_t *d_stage = nullptr;  // device copy of the pinned launch-table staging
     FeatCandDev *d_cands = nullptr;
     uint64_t *d_cat_scratch = nullptr;
     SplitPacketDev *d_packets = nullptr;
-    uint64_t *d_cat_out = nullptr;
-    PartReqDev *d_preqs = nullptr;
-    uint64_t *d_cat_in = nullptr;
     uint32_t *d_counts = nullptr, *d_excl = nullptr, *d_totals = nullptr;
     LeafDev *d_leaves = nullptr;
-    float *d_leaf_vals = nullptr;
+    size_t off_tilefeats = 0, off_sfeats = 0;  // offsets in the tree-table buffer
     uint64_t max_chunks = 0;    // capacity of the partition chunk arrays
     uint64_t cat_in_words = 0;  // capacity of the partition category words
 
@@ -452,30 +445,35 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
         c->hist = c->alloc<int64_t>((size_t)c->n_slots * c->width_max * 2, "histogram slots");
         c->red_f64 = c->alloc<double>(2 * c->n_red_blocks + 2, "reduction scratch");
         c->red_i64 = c->alloc<int64_t>(2 * c->n_red_blocks + 2, "reduction scratch");
-        c->d_tiles = c->alloc<TileDev>(c->tiles.size(), "tile table");
-        c->d_tilefeats = c->alloc<TileFeatDev>(c->n_features, "tile feature table");
-        c->d_hnodes = c->alloc<HistNodeDev>(MAX_NODES, "histogram node table");
-        c->d_u32a = c->alloc<uint32_t>(3 * MAX_NODES, "slot lists");
-        c->d_u32b = c->alloc<uint32_t>(3 * MAX_NODES, "slot lists");
-        c->d_snodes = c->alloc<SplitNodeDev>(MAX_NODES, "split node table");
-        c->d_sfeats = c->alloc<SplitFeatDev>(c->n_features, "split feature table");
+        // The per-tree tables (tiles, tile features, split features) share
+        // one buffer so that a tree's plan goes to the device in one copy.
+        {
+            auto al = [](size_t b) { return (b + 255) & ~size_t(255); };
+            c->off_tilefeats = al(sizeof(TileDev) * c->tiles.size());
+            c->off_sfeats = c->off_tilefeats + al(sizeof(TileFeatDev) * c->n_features);
+            uint8_t *tt = c->alloc<uint8_t>(c->off_sfeats + sizeof(SplitFeatDev) * c->n_features,
+                                            "tree tables");
+            c->d_tiles = reinterpret_cast<TileDev *>(tt);
+            c->d_tilefeats = reinterpret_cast<TileFeatDev *>(tt + c->off_tilefeats);
+            c->d_sfeats = reinterpret_cast<SplitFeatDev *>(tt + c->off_sfeats);
+        }
         c->d_cands = c->alloc<FeatCandDev>((size_t)c->n_slots * c->n_features,
                                            "split candidates");
-        c->d_enabled = c->alloc<uint8_t>((size_t)c->n_slots * c->n_features, "feature masks");
         c->d_cat_scratch =
             c->alloc<uint64_t>((size_t)c->n_slots * std::max(1u, c->max_cat_words), "category sets");
-        c->d_packets = c->alloc<SplitPacketDev>(MAX_NODES, "split packets");
-        c->d_cat_out =
-            c->alloc<uint64_t>((size_t)c->n_slots * std::max(1u, c->max_cat_words), "category sets");
-        c->d_preqs = c->alloc<PartReqDev>(MAX_NODES, "partition requests");
+        // Split packets, then (256-aligned) the category sets of the call.
+        c->d_packets = reinterpret_cast<SplitPacketDev *>(c->alloc<uint8_t>(
+            sizeof(SplitPacketDev) * MAX_NODES + 256 +
+                8 * (size_t)c->n_slots * std::max(1u, c->max_cat_words),
+            "split packets"));
         c->cat_in_words = (uint64_t)c->n_slots * std::max(1u, c->max_cat_words);
-        c->d_cat_in = c->alloc<uint64_t>(c->cat_in_words, "partition category sets");
         c->max_chunks = n_rows / PART_CHUNK + MAX_NODES + 1;
         c->d_counts = c->alloc<uint32_t>(c->max_chunks, "partition counts");
         c->d_excl = c->alloc<uint32_t>(c->max_chunks + 1, "partition offsets");
         c->d_totals = c->alloc<uint32_t>(MAX_NODES, "partition totals");
-        c->d_leaves = c->alloc<LeafDev>(MAX_NODES, "leaf table");
-        c->d_leaf_vals = c->alloc<float>(MAX_NODES, "leaf values");
+        // Leaf table followed by the leaf values of one call.
+        c->d_leaves = reinterpret_cast<LeafDev *>(
+            c->alloc<uint8_t>((sizeof(LeafDev) + 4) * MAX_NODES, "leaf table"));
         // Staging of the launch tables of one blocking call (each table 256-aligned).
         const size_t eval_tables = sizeof(HistNodeDev) * MAX_NODES + 4 * MAX_NODES +
                                    12 * MAX_NODES + sizeof(SplitNodeDev) * MAX_NODES +
@@ -483,11 +481,11 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
         const size_t small = std::max<size_t>(
             {eval_tables,
              sizeof(PartReqDev) * MAX_NODES + 8 * c->cat_in_words + 2 * 256,
-             sizeof(TileDev) * c->tiles.size() + sizeof(TileFeatDev) * c->n_features +
-                 sizeof(SplitFeatDev) * c->n_features + 256});
+             c->off_sfeats + sizeof(SplitFeatDev) * c->n_features});
         c->pinned(c->pin_small, small);
+        c->d_stage = c->alloc<uint8_t>(small, "launch tables");
         c->pinned(c->pin_leaves, (sizeof(LeafDev) + 4) * MAX_NODES);
-        c->pinned(c->pin_out, std::max<size_t>({sizeof(SplitPacketDev) * MAX_NODES +
+        c->pinned(c->pin_out, std::max<size_t>({sizeof(SplitPacketDev) * MAX_NODES + 256 +
                                                     8 * (size_t)c->n_slots *
                                                         std::max(1u, c->max_cat_words),
                                                 4 * (size_t)MAX_NODES, 64}));
@@ -805,17 +803,16 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
         }
         c->cat_words_per_node = cat_base;
         uint8_t *st = static_cast<uint8_t *>(c->pin_small.p);
-        const size_t b1 = sizeof(TileDev) * td.size(), b2 = sizeof(TileFeatDev) * tf.size(),
-                     b3 = sizeof(SplitFeatDev) * sf.size();
-        std::memcpy(st, td.data(), b1);
-        std::memcpy(st + b1, tf.data(), b2);
-        std::memcpy(st + b1 + b2, sf.data(), b3);
-        check(hipMemcpyAsync(c->d_tiles, st, b1, hipMemcpyHostToDevice, c->stream), "tree tables");
-        check(hipMemcpyAsync(c->d_tilefeats, st + b1, b2, hipMemcpyHostToDevice, c->stream),
+        std::memcpy(st, td.data(), sizeof(TileDev) * td.size());
+        std::memcpy(st + c->off_tilefeats, tf.data(), sizeof(TileFeatDev) * tf.size());
+        std::memcpy(st + c->off_sfeats, sf.data(), sizeof(SplitFeatDev) * sf.size());
+        check(hipMemcpyAsync(c->d_tiles, st, c->off_sfeats + sizeof(SplitFeatDev) * sf.size(),
+                             hipMemcpyHostToDevice, c->stream),
               "tree tables");
-        check(hipMemcpyAsync(c->d_sfeats, st + b1 + b2, b3, hipMemcpyHostToDevice, c->stream),
-              "tree tables");
-        check(launch_init_rows(c->rows, c->delta, c->n_rows, c->stream), "row arena reset");
+        // The delta is kept only for callers without a device objective.
+        check(launch_init_rows(c->rows, c->objective >= 0 ? nullptr : c->delta, c->n_rows,
+                               c->stream),
+              "row arena reset");
         c->sync();
         c->tree_begun = true;
         root->offset = 0;
@@ -881,22 +878,36 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
             triples.push_back((uint32_t)nd.subtract_parent);
             triples.push_back(nodes[nd.subtract_sibling].slot);
         }
+        // Every table of the call is laid out in the pinned staging and sent
+        // in one copy to the device staging at the same offsets.
+        uint8_t *ds = c->d_stage;
         size_t o = 0;
-        const size_t bh = sizeof(HistNodeDev) * hn.size();
-        std::memcpy(st + o, hn.data(), bh);
-        check(hipMemcpyAsync(c->d_hnodes, st + o, bh, hipMemcpyHostToDevice, c->stream), "tables");
-        o += (bh + 255) & ~size_t(255);
-        std::memcpy(st + o, zero_slots.data(), 4 * zero_slots.size());
-        check(hipMemcpyAsync(c->d_u32a, st + o, 4 * zero_slots.size(), hipMemcpyHostToDevice,
-                             c->stream),
-              "tables");
-        o += (4 * zero_slots.size() + 255) & ~size_t(255);
-        std::memcpy(st + o, triples.data(), 4 * triples.size());
-        check(hipMemcpyAsync(c->d_u32b, st + o, 4 * triples.size(), hipMemcpyHostToDevice,
-                             c->stream),
-              "tables");
-        o += (4 * triples.size() + 255) & ~size_t(255);
-        check(launch_zero_slots(c->hist, c->hist_width, c->d_u32a, (uint32_t)zero_slots.size(),
+        auto put = [&](const void *src, size_t bytes) {
+            const size_t at = o;
+            if (bytes) std::memcpy(st + at, src, bytes);
+            o += (bytes + 255) & ~size_t(255);
+            return at;
+        };
+        const size_t o_hn = put(hn.data(), sizeof(HistNodeDev) * hn.size());
+        const size_t o_zero = put(zero_slots.data(), 4 * zero_slots.size());
+        const size_t o_tri = put(triples.data(), 4 * triples.size());
+        std::vector<SplitNodeDev> sn(n);
+        for (uint32_t i = 0; i < n; i++) {
+            sn[i].sum_g = nodes[i].sum[0];
+            sn[i].sum_h = nodes[i].sum[1];
+            sn[i].lower = nodes[i].lower;
+            sn[i].upper = nodes[i].upper;
+            sn[i].slot = nodes[i].slot;
+        }
+        const size_t o_sn = put(sn.data(), sizeof(SplitNodeDev) * n);
+        const uint32_t nf = (uint32_t)c->tree_feats.size();
+        const size_t o_en = enabled ? put(enabled, (size_t)n * nf) : 0;
+        check(hipMemcpyAsync(ds, st, o, hipMemcpyHostToDevice, c->stream), "tables");
+        const HistNodeDev *d_hn = reinterpret_cast<const HistNodeDev *>(ds + o_hn);
+        const uint32_t *d_zero = reinterpret_cast<const uint32_t *>(ds + o_zero);
+        const uint32_t *d_tri = reinterpret_cast<const uint32_t *>(ds + o_tri);
+        const SplitNodeDev *d_sn = reinterpret_cast<const SplitNodeDev *>(ds + o_sn);
+        check(launch_zero_slots(c->hist, c->hist_width, d_zero, (uint32_t)zero_slots.size(),
                                 c->stream),
               "histogram clear");
         if (!hn.empty()) {
@@ -916,7 +927,7 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
                 L.tiles = c->d_tiles + g.tile_begin;
                 L.feats = c->d_tilefeats;
                 L.n_tiles = g.n_tiles;
-                L.nodes = c->d_hnodes;
+                L.nodes = d_hn;
                 L.n_nodes = (uint32_t)hn.size();
                 L.n_chunks = chunks;
                 L.chunk_rows = chunk_rows;
@@ -943,31 +954,11 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
                 c->ev_used++;
             }
         }
-        check(launch_subtract(c->hist, c->hist_width, c->d_u32b, (uint32_t)(triples.size() / 3),
+        check(launch_subtract(c->hist, c->hist_width, d_tri, (uint32_t)(triples.size() / 3),
                               c->stream),
               "sibling subtraction");
         // ---- split scan ----
-        std::vector<SplitNodeDev> sn(n);
-        for (uint32_t i = 0; i < n; i++) {
-            sn[i].sum_g = nodes[i].sum[0];
-            sn[i].sum_h = nodes[i].sum[1];
-            sn[i].lower = nodes[i].lower;
-            sn[i].upper = nodes[i].upper;
-            sn[i].slot = nodes[i].slot;
-        }
-        const size_t bs = sizeof(SplitNodeDev) * n;
-        std::memcpy(st + o, sn.data(), bs);
-        check(hipMemcpyAsync(c->d_snodes, st + o, bs, hipMemcpyHostToDevice, c->stream), "tables");
-        o += (bs + 255) & ~size_t(255);
-        const uint32_t nf = (uint32_t)c->tree_feats.size();
-        const uint8_t *d_en = nullptr;
-        if (enabled) {
-            std::memcpy(st + o, enabled, (size_t)n * nf);
-            check(hipMemcpyAsync(c->d_enabled, st + o, (size_t)n * nf, hipMemcpyHostToDevice,
-                                 c->stream),
-                  "tables");
-            d_en = c->d_enabled;
-        }
+        const uint8_t *d_en = enabled ? ds + o_en : nullptr;
         SplitParamsDev P{};
         P.inv_g = 1.0 / c->scales[0];
         P.inv_h = 1.0 / c->scales[1];
@@ -980,28 +971,30 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
         P.max_cat_threshold = sp->max_cat_threshold;
         P.n_feats = nf;
         P.cat_words_per_node = c->cat_words_per_node;
-        check(launch_split_feats(c->hist, c->hist_width, c->d_snodes, n, c->d_sfeats, d_en, P,
+        check(launch_split_feats(c->hist, c->hist_width, d_sn, n, c->d_sfeats, d_en, P,
                                  c->d_cands, c->d_cat_scratch, c->stream),
               "split scan");
         const uint32_t cw = std::max(1u, c->cat_words_per_node);
-        check(launch_split_nodes(c->d_cands, c->d_sfeats, n, P, c->d_snodes, c->d_cat_scratch,
-                                 c->d_packets, c->d_cat_out, cw, c->stream),
+        // Packets and category sets land back to back: one download.
+        const bool any_cat = c->cat_words_per_node > 0;
+        const size_t pk_bytes = sizeof(SplitPacketDev) * n;
+        uint8_t *d_out = reinterpret_cast<uint8_t *>(c->d_packets);
+        uint64_t *d_cats = reinterpret_cast<uint64_t *>(d_out + ((pk_bytes + 255) & ~size_t(255)));
+        check(launch_split_nodes(c->d_cands, c->d_sfeats, n, P, d_sn, c->d_cat_scratch,
+                                 c->d_packets, d_cats, cw, c->stream),
               "split argmax");
         uint8_t *po = static_cast<uint8_t *>(c->pin_out.p);
-        check(hipMemcpyAsync(po, c->d_packets, sizeof(SplitPacketDev) * n, hipMemcpyDeviceToHost,
-                             c->stream),
+        const size_t out_bytes =
+            any_cat ? ((pk_bytes + 255) & ~size_t(255)) + 8 * (size_t)n * cw : pk_bytes;
+        check(hipMemcpyAsync(po, d_out, out_bytes, hipMemcpyDeviceToHost, c->stream),
               "packet download");
-        const bool any_cat = c->cat_words_per_node > 0;
-        if (any_cat)
-            check(hipMemcpyAsync(po + sizeof(SplitPacketDev) * n, c->d_cat_out,
-                                 8 * (size_t)n * cw, hipMemcpyDeviceToHost, c->stream),
-                  "category download");
         c->sync();
         if (c->timing) c->collect_timing();
         static_assert(sizeof(SplitPacketDev) == sizeof(fbh_split), "packet layout");
         std::memcpy(out, po, sizeof(fbh_split) * n);
         if (any_cat) {
-            const uint64_t *words = reinterpret_cast<const uint64_t *>(po + sizeof(SplitPacketDev) * n);
+            const uint64_t *words =
+                reinterpret_cast<const uint64_t *>(po + ((pk_bytes + 255) & ~size_t(255)));
             for (uint32_t i = 0; i < n; i++) {
                 if (!out[i].found || !out[i].is_cat) continue;
                 if (!cat_words || (uint64_t)out[i].cat_offset + out[i].n_cat_words > cat_capacity)
@@ -1074,18 +1067,18 @@ int fbh_partition(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n, const uint64
         if (n_cat_words > c->cat_in_words)
             throw InputError("too many category words for one partition call");
         uint8_t *st = static_cast<uint8_t *>(c->pin_small.p);
+        // Requests and category words: one copy into the device staging.
         const size_t bp = sizeof(PartReqDev) * pr.size();
+        const size_t off = (bp + 255) & ~size_t(255);
         std::memcpy(st, pr.data(), bp);
-        check(hipMemcpyAsync(c->d_preqs, st, bp, hipMemcpyHostToDevice, c->stream), "tables");
-        if (n_cat_words) {
-            const size_t off = (bp + 255) & ~size_t(255);
-            std::memcpy(st + off, cat_words, 8 * (size_t)n_cat_words);
-            check(hipMemcpyAsync(c->d_cat_in, st + off, 8 * (size_t)n_cat_words,
-                                 hipMemcpyHostToDevice, c->stream),
-                  "tables");
-        }
-        check(launch_partition(c->d_preqs, (uint32_t)pr.size(), chunks, c->rows, c->tmp, c->flags,
-                               c->d_counts, c->d_excl, c->d_totals, c->d_cat_in, c->stream),
+        if (n_cat_words) std::memcpy(st + off, cat_words, 8 * (size_t)n_cat_words);
+        check(hipMemcpyAsync(c->d_stage, st, n_cat_words ? off + 8 * (size_t)n_cat_words : bp,
+                             hipMemcpyHostToDevice, c->stream),
+              "tables");
+        check(launch_partition(reinterpret_cast<const PartReqDev *>(c->d_stage),
+                               (uint32_t)pr.size(), chunks, c->rows, c->tmp, c->flags, c->d_counts,
+                               c->d_excl, c->d_totals,
+                               reinterpret_cast<const uint64_t *>(c->d_stage + off), c->stream),
               "partition");
         check(hipMemcpyAsync(c->pin_out.p, c->d_totals, 4 * pr.size(), hipMemcpyDeviceToHost,
                              c->stream),
@@ -1127,26 +1120,21 @@ int fbh_assign_leaves(fbh_ctx *c, const fbh_span *spans, const float *values, ui
             m++;
         }
         if (m == 0) return;
-        check(hipMemcpyAsync(c->d_leaves, ld, sizeof(LeafDev) * m, hipMemcpyHostToDevice,
-                             c->stream),
-              "leaf table");
         const int idb = c->objective >= 0 ? (n <= 256 ? 1 : 2) : 0;
-        if (idb) {
-            // Leaf values by position, staged behind the leaf table.
-            float *pv = reinterpret_cast<float *>(ld + m);
-            std::memcpy(pv, values, 4 * (size_t)n);
-            check(hipMemcpyAsync(c->d_leaf_vals, pv, 4 * (size_t)n, hipMemcpyHostToDevice,
-                                 c->stream),
-                  "leaf values");
-        }
+        // Leaf values by position follow the leaf table: one copy.
+        float *pv = reinterpret_cast<float *>(ld + m);
+        if (idb) std::memcpy(pv, values, 4 * (size_t)n);
+        check(hipMemcpyAsync(c->d_leaves, ld, sizeof(LeafDev) * m + (idb ? 4 * (size_t)n : 0),
+                             hipMemcpyHostToDevice, c->stream),
+              "leaf table");
+        const float *d_vals = reinterpret_cast<const float *>(c->d_leaves + m);
         check(hipEventRecord(c->leaves_done, c->stream), "event");
         c->leaves_pending = true;
         check(launch_assign_leaves(c->d_leaves, m, chunks, c->rows, c->delta, c->leaf_ids, idb,
                                    c->stream),
               "leaf assignment");
         if (idb)
-            check(launch_apply_leaves(c->leaf_ids, idb, c->d_leaf_vals, c->n_rows, c->margin,
-                                      c->stream),
+            check(launch_apply_leaves(c->leaf_ids, idb, d_vals, c->n_rows, c->margin, c->stream),
                   "margin update");
         c->leaf_id_bytes = idb;
         c->ids_fresh = idb != 0;

@@ -1044,7 +1044,7 @@ __global__ void init_rows_kernel(uint32_t *rows, float *delta, uint64_t n) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * blockDim.x) {
         rows[i] = (uint32_t)i;
-        delta[i] = 0.0f;
+        if (delta) delta[i] = 0.0f;
     }
 }
 
