@@ -1,18 +1,26 @@
 #!/usr/bin/env python3
 """Benchmark of the device training path on one MI355X.
 
-Workload (default): 10.5M x 28 HIGGS-like binary classification, max_bin=255
-(u8 bins), depth 8, eta 0.1, gpu_math="exact" (host gradients, byte-identical
-trees). One step = one boosting round. W warmup rounds, then K timed rounds,
-all resident in HBM; the round timer runs between blocking device syncs.
+Default workload (the headline): 10.5M x 28 HIGGS-like binary classification,
+max_bin=255 (u8 bins), depth 8, eta 0.1, gpu_math="exact" (byte-identical
+trees). One step = one boosting round with everything resident in HBM; W
+warmup rounds, then K timed rounds; the round timer runs between blocking
+device syncs. Other workloads (--workload):
+
+  wide      400k x 2000 L2-normalised rows, colsample_bytree 0.5, depth 8
+  widebin   2M x (80 numeric with 10% NaN + 20 categorical x 500 codes),
+            max_bin 1024 (u16), reg:squarederror, lossguide, 255 leaves
+  shap      GPU TreeSHAP of 1M rows x 200 features against a 100-tree,
+            depth-8 ensemble (trained first, untimed); one step = one pass
 
 Prints one JSON line:
-  value      boosting rounds per second over the K timed rounds
-  roofline   histogram kernels: algorithmic bytes (cells + 16 B gradient pair
-             + 4 B row id per accumulated row, + 32 B per written histogram
-             bin) over their HIP-event time, against 8 TB/s HBM
+  value         boosting rounds per second (shap: rows per second)
+  roofline      the dominant kernel: histogram algorithmic bytes (cells +
+                16 B gradient pair + 4 B row id per accumulated row, + 32 B
+                per written histogram bin) over their HIP-event time, against
+                8 TB/s HBM; traffic from the committed rocprofv3 summary
   cpu_baseline  the CPU oracle (C++ restatement of the reference CPU engine)
-             on the same data, first R rounds, host threads stated
+                on a bounded sample of the same workload, threads stated
 """
 
 from __future__ import annotations
@@ -68,42 +76,39 @@ def copy_probe(mib: int) -> int:
     return 0
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--rows", type=int, default=10_500_000)
-    ap.add_argument("--max-bin", type=int, default=255)
-    ap.add_argument("--cpu-rounds", type=int, default=2)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
-                    help="only run a device copy of MIB MiB (counter calibration) and exit")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported "
-              "(the training path is single-device)", file=sys.stderr)
-        return 2
-    if args.copy_probe:
-        return copy_probe(args.copy_probe)
+def cpu_threads() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
 
+
+def base_line(args, value, unit, ms_per_step, config, dtype="int64"):
+    return {
+        "metric": METRIC,
+        "value": value,
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic",
+        "config": config,
+    }
+
+
+def train_workload(args, X, y, params, desc: str, traffic_tag: str):
     import ferrisboost_amd as fb
     from ferrisboost_amd import _native as N
-    from ferrisboost_amd import datasets
 
-    if not fb.device_available(0):
-        print("no gfx950 device at cuda:0", file=sys.stderr)
-        return 1
-
-    t0 = time.time()
-    X, y, params, _ = datasets.narrow_binary(args.rows, max_bin=args.max_bin)
-    log(f"data {X.shape} generated in {time.time() - t0:.1f}s")
     rounds = args.warmup + args.steps
     gparams = dict(params, device="cuda:0", hip_profile=True)
     t0 = time.time()
     model = fb.train(gparams, X, y, num_boost_round=rounds)
     log(f"trained {rounds} rounds in {time.time() - t0:.1f}s "
-        f"(setup {model.stats['setup_seconds']:.1f}s)")
+        f"(setup {model.stats['setup_seconds']:.1f}s, device sigmoid "
+        f"{model.stats['device_sigmoid']})")
     wall = np.zeros(rounds)
     hms = np.zeros(rounds)
     hbytes = np.zeros(rounds, np.uint64)
@@ -113,12 +118,10 @@ def main() -> int:
     t_wall = float(wall[timed].sum())
     t_hist_ms = float(hms[timed].sum())
     b_hist = float(hbytes[timed].astype(np.float64).sum())
-    rounds_per_sec = args.steps / t_wall
     hist_gbps = b_hist / (t_hist_ms * 1e-3) / 1e9 if t_hist_ms > 0 else 0.0
     launches = int(model.stats["hist_launches"])
     bytes_per_launch = float(model.stats["hist_bytes"]) / launches if launches else 0.0
-    traffic = load_traffic(os.path.join(ROOT, "profiles",
-                                        f"hist_traffic_narrow_{'u8' if args.max_bin <= 255 else 'u16'}.txt"))
+    traffic = load_traffic(os.path.join(ROOT, "profiles", f"hist_traffic_{traffic_tag}.txt"))
     roofline = {
         "bound": "hbm",
         "achieved": round(hist_gbps, 1),
@@ -134,12 +137,15 @@ def main() -> int:
     if not args.no_cpu:
         from oracle import oracle as O
 
-        threads = min(16, os.cpu_count() or 1)
+        threads = cpu_threads()
         cols = max(1, -(-X.shape[1] // threads))
-        op = {k: v for k, v in params.items() if k != "device"}
+        op = {k: v for k, v in params.items() if k not in ("device", "feature_types")}
         op.update(n_rounds=args.cpu_rounds, cols_per_block=cols, nthread=threads)
+        cat = None
+        if "feature_types" in params:
+            cat = np.array([1 if t == "c" else 0 for t in params["feature_types"]], np.uint8)
         t0 = time.time()
-        om = O.train(X, y, O.make_params(**op))
+        om = O.train(X, y, O.make_params(**op), categorical=cat)
         cpu_s = om.train_seconds
         log(f"cpu oracle {args.cpu_rounds} rounds: {cpu_s:.1f}s train, {time.time() - t0:.1f}s total")
         blocks = -(-X.shape[1] // cols)
@@ -156,36 +162,132 @@ def main() -> int:
             np.array_equal(om.tree(t)[f], model.tree_nodes(t)[f])
             for t in range(args.cpu_rounds) for f in om.tree(t).dtype.names if f != "pad")
 
-    out = {
-        "metric": METRIC,
-        "value": round(rounds_per_sec, 3),
-        "unit": "rounds/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(1e3 * t_wall / args.steps, 3),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int64",
-        "data": "synthetic",
-        "config": {
-            "workload": f"narrow {X.shape[0]}x{X.shape[1]} HIGGS-like binary, max_bin={args.max_bin} "
-                        f"({'u8' if args.max_bin <= 255 else 'u16'} bins), depth 8, eta 0.1, "
-                        "gpu_math=exact, depthwise",
-            "rows": int(X.shape[0]),
-            "features": int(X.shape[1]),
-            "max_bin": args.max_bin,
-            "max_depth": 8,
-        },
+    config = {"workload": desc, "rows": int(X.shape[0]), "features": int(X.shape[1])}
+    config.update({k: params[k] for k in ("max_bin", "max_depth", "max_leaves", "grow_policy",
+                                          "colsample_bytree", "objective") if k in params})
+    out = base_line(args, round(args.steps / t_wall, 3), "rounds/s",
+                    round(1e3 * t_wall / args.steps, 3), config)
+    out.update({
         "hist_gbps": round(hist_gbps, 1),
         "hist_ms_per_round": round(t_hist_ms / args.steps, 3),
         "hist_launches_per_round": round(launches / rounds, 2),
-        "host_gradient_ms_per_round": round(1e3 * model.stats["host_gradient_seconds"] / rounds, 3),
+        "gradient_ms_per_round": round(1e3 * model.stats["host_gradient_seconds"] / rounds, 3),
         "roofline": roofline,
         "cpu_baseline": cpu,
         "parity_first_rounds_vs_cpu": parity,
-    }
+    })
+    return out
+
+
+def shap_workload(args):
+    import ferrisboost_amd as fb
+    from ferrisboost_amd import _native as N
+    from ferrisboost_amd import datasets
+
+    n_rows = args.rows or 1_000_000
+    X, y, params, _ = datasets.streaming(n_rows=n_rows, n_features=200)
+    t0 = time.time()
+    model = fb.train(dict(params, device="cuda:0"), X, y, num_boost_round=100)
+    log(f"trained 100 trees on {X.shape} in {time.time() - t0:.1f}s")
+    L = N.train_lib()
+    model.predict(X[:4096], pred_contribs=True)  # load the kernels
+    for _ in range(args.warmup):
+        model.predict(X, pred_contribs=True)
+    kernel_ms = 0.0
+    t0 = time.time()
+    for _ in range(args.steps):
+        phi = model.predict(X, pred_contribs=True)
+        kernel_ms += L.fbt_last_shap_ms()
+    wall = time.time() - t0
+    rows_per_s = args.steps * n_rows / (kernel_ms * 1e-3)
+    # bytes the kernel must move: the row in, its contributions out
+    per_row = 4 * X.shape[1] + 4 * (X.shape[1] + 1)
+    gbps = args.steps * n_rows * per_row / (kernel_ms * 1e-3) / 1e9
+    margin = model.predict(X[:20000], output_margin=True)
+    additivity = float(np.max(np.abs(phi[:20000].sum(axis=1) - margin)))
+
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+
+        k = 2000
+        om = O.model_from_nodes(model.trees(), model.cat_words(), model.objective,
+                                model.base_score)
+        t0 = time.time()
+        ref = om.shap(X[:k])
+        cpu_s = time.time() - t0
+        parity = float(np.max(np.abs(ref - phi[:k])))
+        cpu = {"value": round(k / cpu_s, 1), "unit": "rows/s", "cores": 1, "kind": "port",
+               "sample": f"the first {k} rows of the same explanation (same trees), one thread"}
+    config = {"workload": f"GPU TreeSHAP, {n_rows} rows x {X.shape[1]} features, "
+                          "100 trees depth 8 (QuadratureTreeSHAP)",
+              "rows": n_rows, "features": int(X.shape[1]), "trees": 100, "max_depth": 8}
+    out = base_line(args, round(rows_per_s, 1), "rows/s", round(kernel_ms / args.steps, 3),
+                    config, dtype="f32")
+    out.update({
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 5), "traffic": None},
+        "pcie_inclusive_rows_per_s": round(args.steps * n_rows / wall, 1),
+        "additivity_max_abs": additivity,
+        "cpu_baseline": cpu,
+        "max_abs_vs_cpu": parity,
+    })
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="narrow", choices=["narrow", "wide", "widebin", "shap"])
+    ap.add_argument("--rows", type=int, default=0, help="rows (0: the workload's own size)")
+    ap.add_argument("--max-bin", type=int, default=255, help="narrow workload: 255 (u8) or 256 (u16)")
+    ap.add_argument("--cpu-rounds", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a device copy of MIB MiB (counter calibration) and exit")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(the training path is single-device)", file=sys.stderr)
+        return 2
+    if args.copy_probe:
+        return copy_probe(args.copy_probe)
+
+    import ferrisboost_amd as fb
+    from ferrisboost_amd import datasets
+
+    if not fb.device_available(0):
+        print("no gfx950 device at cuda:0", file=sys.stderr)
+        return 1
+
+    t0 = time.time()
+    if args.workload == "shap":
+        out = shap_workload(args)
+    elif args.workload == "narrow":
+        X, y, params, _ = datasets.narrow_binary(args.rows or 10_500_000, max_bin=args.max_bin)
+        log(f"data {X.shape} generated in {time.time() - t0:.1f}s")
+        u = "u8" if args.max_bin <= 255 else "u16"
+        out = train_workload(
+            args, X, y, params,
+            f"narrow {X.shape[0]}x{X.shape[1]} HIGGS-like binary, max_bin={args.max_bin} "
+            f"({u} bins), depth 8, eta 0.1, gpu_math=exact, depthwise", f"narrow_{u}")
+    elif args.workload == "wide":
+        X, y, params, _ = datasets.wide_binary(args.rows or 400_000, n_features=2000)
+        log(f"data {X.shape} generated in {time.time() - t0:.1f}s")
+        out = train_workload(
+            args, X, y, params,
+            f"wide {X.shape[0]}x{X.shape[1]} L2-normalised binary, max_bin=256, depth 8, "
+            "colsample_bytree 0.5, gpu_math=exact", "wide")
+    else:
+        X, y, params, _ = datasets.widebin_cat(args.rows or 2_000_000)
+        log(f"data {X.shape} generated in {time.time() - t0:.1f}s")
+        out = train_workload(
+            args, X, y, params,
+            f"wide-bin {X.shape[0]}x{X.shape[1]} (80 numeric 10% NaN + 20 categorical x 500 "
+            "Zipf codes), max_bin=1024 (u16), reg:squarederror, lossguide 255 leaves", "widebin")
     print(json.dumps(out), flush=True)
     return 0
 

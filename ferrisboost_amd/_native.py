@@ -174,7 +174,7 @@ TRAIN_SYMBOLS = [
     "fbt_model_tree_len", "fbt_model_tree_nodes", "fbt_model_n_cat_words", "fbt_model_cat_words",
     "fbt_model_base_score", "fbt_model_base_margin", "fbt_model_n_features",
     "fbt_model_train_margins", "fbt_model_n_cuts", "fbt_model_cuts", "fbt_predict_margin",
-    "fbt_model_to_json", "fbt_shap", "fbt_sketch_cuts",
+    "fbt_model_to_json", "fbt_shap", "fbt_last_shap_ms", "fbt_sketch_cuts",
 ]
 
 _hip = None
@@ -284,6 +284,8 @@ def train_lib() -> C.CDLL:
         L.fbt_model_to_json.restype = C.c_size_t
         L.fbt_shap.argtypes = [P, P, C.c_uint64, C.c_uint32, C.c_int, P]
         L.fbt_sketch_cuts.argtypes = [P, C.c_uint64, C.c_uint32, C.c_uint32, P, P, P, P]
+        L.fbt_last_shap_ms.argtypes = []
+        L.fbt_last_shap_ms.restype = C.c_double
         _train = L
     return _train
 

@@ -286,6 +286,7 @@ int fbh_shap_contribs(fbh_shap_model *m, const float *rows, uint64_t n_rows, con
         std::unique_ptr<float, decltype(&hipFree)> f2(d_out, hipFree);
         if (margin) chk(hipMalloc(&d_margin, 4 * nb), "shap margin");
         std::unique_ptr<float, decltype(&hipFree)> f3(d_margin, hipFree);
+        double kernel_ms = 0.0;
         for (uint64_t r0 = 0; r0 < n_rows; r0 += nb) {
             const uint64_t k = std::min(nb, n_rows - r0);
             chk(hipMemcpyAsync(d_rows, rows + r0 * m->n_features, 4 * k * m->n_features,
@@ -300,7 +301,11 @@ int fbh_shap_contribs(fbh_shap_model *m, const float *rows, uint64_t n_rows, con
                                hipMemcpyDeviceToHost, m->stream),
                 "shap out");
             chk(hipStreamSynchronize(m->stream), "shap");
+            float ms = 0.0f;
+            chk(hipEventElapsedTime(&ms, m->e0, m->e1), "event");
+            kernel_ms += ms;
         }
+        m->last_ms = kernel_ms;
     });
 }
 

@@ -21,6 +21,7 @@ struct fbt_model {
 namespace {
 
 thread_local std::string g_err;
+thread_local double g_last_shap_ms = 0.0;
 
 template <class F>
 int guard(F &&f) {
@@ -205,8 +206,11 @@ int fbt_shap(const fbt_model *mm, const float *x, uint64_t n_rows, uint32_t n_fe
             fbh_last_error(buf, sizeof(buf));
             throw fbt::RuntimeError(buf);
         }
+        g_last_shap_ms = fbh_shap_last_ms(sm);
     });
 }
+
+double fbt_last_shap_ms(void) { return g_last_shap_ms; }
 
 int fbt_sketch_cuts(const float *x, uint64_t n, uint32_t nf, uint32_t max_bin, const float *w,
                     const uint8_t *cat, float *values, uint32_t *offsets) {

@@ -307,7 +307,8 @@ int fbh_shap_contribs(fbh_shap_model *m, const float *rows, uint64_t n_rows,
  * sync == 0. */
 int fbh_shap_contribs_device(fbh_shap_model *m, const float *d_rows, uint64_t n_rows,
                              const float *d_margin, float *d_out, int sync);
-/* Milliseconds of the last fbh_shap_contribs_device kernel (HIP events). */
+/* Milliseconds of the SHAP kernels of the last fbh_shap_contribs (all
+ * batches) or fbh_shap_contribs_device (sync != 0) call (HIP events). */
 double fbh_shap_last_ms(const fbh_shap_model *m);
 
 #ifdef __cplusplus

@@ -132,6 +132,8 @@ size_t fbt_model_to_json(const fbt_model *m, char *buf, size_t len);
 /* pred_contribs on the device (GpuExplainModel): out [n_rows][n_features+1]. */
 int fbt_shap(const fbt_model *m, const float *x, uint64_t n_rows, uint32_t n_features,
              int device, float *out);
+/* Device time of the SHAP kernels of this thread's last fbt_shap call (ms). */
+double fbt_last_shap_ms(void);
 
 /* Sketch cuts and bins exactly as training does (tests / diagnostics).
  * cut_values holds n_features * max(max_bin, 2) floats. */

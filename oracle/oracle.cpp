@@ -1678,6 +1678,45 @@ void orc_quadrature_rule(float nodes[8], float weights[8]) {
 }
 
 // Explainer::shap_row (src/model/explain.rs:704-728), single output group.
+int orc_model_from_nodes(const orc_node *nodes, const uint32_t *offs, uint32_t n_trees,
+                         const uint32_t *cat_words, uint32_t n_cat_words, uint32_t objective,
+                         float base_score, orc_model **out) {
+    try {
+        auto m = std::make_unique<orc_model>();
+        m->objective = objective;
+        m->base_score = base_score;
+        for (u32 t = 0; t < n_trees; t++) {
+            Tree tr;
+            for (u32 i = offs[t]; i < offs[t + 1]; i++) {
+                const orc_node &o = nodes[i];
+                Node n;
+                n.feat = o.feat;
+                n.split_cond = o.split_cond;
+                n.left = o.left;
+                n.right = o.right;
+                n.default_left = o.default_left != 0;
+                n.is_leaf = o.is_leaf != 0;
+                n.leaf_value = o.leaf_value;
+                n.gain = o.gain;
+                n.sum_hess = o.sum_hess;
+                if (o.cat_len) {
+                    if ((u64)o.cat_begin + o.cat_len > n_cat_words)
+                        throw std::runtime_error("category words out of range");
+                    n.cats.assign(cat_words + o.cat_begin, cat_words + o.cat_begin + o.cat_len);
+                    n.is_cat = true;
+                }
+                tr.nodes.push_back(n);
+            }
+            m->trees.push_back(std::move(tr));
+        }
+        *out = m.release();
+        return 0;
+    } catch (std::exception &e) {
+        g_error = e.what();
+        return 1;
+    }
+}
+
 int orc_shap(const orc_model *m, const float *x, uint64_t n, uint32_t nf, float *out) {
     Rule rule = make_rule();
     double sum = 0.0;

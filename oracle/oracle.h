@@ -128,6 +128,12 @@ int orc_train(const float *x, uint64_t n_rows, uint32_t n_features, const float 
               const float *weights, const uint8_t *categorical, const int8_t *monotone,
               uint32_t n_monotone, const orc_params *p, orc_model **out);
 void orc_model_free(orc_model *m);
+/* A model from node records (the layout of orc_node; cat_begin/cat_len index
+ * the u32 category words) -- e.g. a model trained elsewhere, to explain it
+ * on the CPU. tree_offsets has n_trees + 1 entries. */
+int orc_model_from_nodes(const orc_node *nodes, const uint32_t *tree_offsets, uint32_t n_trees,
+                         const uint32_t *cat_words, uint32_t n_cat_words, uint32_t objective,
+                         float base_score, orc_model **out);
 uint32_t orc_model_n_trees(const orc_model *m);
 uint32_t orc_model_tree_len(const orc_model *m, uint32_t tree);
 void orc_model_tree_nodes(const orc_model *m, uint32_t tree, orc_node *out);

@@ -145,6 +145,8 @@ def lib() -> C.CDLL:
         L.orc_partition.restype = C.c_uint64
         L.orc_train.argtypes = [P, C.c_uint64, C.c_uint32, P, P, P, P, C.c_uint32,
                                 C.POINTER(Params), C.POINTER(C.c_void_p)]
+        L.orc_model_from_nodes.argtypes = [P, P, C.c_uint32, P, C.c_uint32, C.c_uint32, C.c_float,
+                                           C.POINTER(C.c_void_p)]
         L.orc_model_free.argtypes = [P]
         L.orc_model_free.restype = None
         L.orc_model_n_trees.argtypes = [P]
@@ -295,6 +297,19 @@ def train(x, y, params: Params, weights=None, categorical=None, monotone=None) -
     h = C.c_void_p()
     rc = lib().orc_train(_p(x), x.shape[0], x.shape[1], _p(y), _p(w), _p(cat), _p(mono),
                          0 if mono is None else len(mono), C.byref(params), C.byref(h))
+    if rc:
+        raise RuntimeError(lib().orc_last_error().decode())
+    return Model(h)
+
+
+def model_from_nodes(trees, cat_words, objective: str, base_score: float) -> Model:
+    """An oracle model holding the given node records (NODE_DTYPE arrays)."""
+    nodes = np.ascontiguousarray(np.concatenate(trees)).astype(NODE_DTYPE)
+    offs = np.concatenate([[0], np.cumsum([t.size for t in trees])]).astype(np.uint32)
+    words = np.ascontiguousarray(cat_words, np.uint32)
+    h = C.c_void_p()
+    rc = lib().orc_model_from_nodes(_p(nodes), _p(offs), len(trees), _p(words), words.size,
+                                    OBJECTIVES[objective], base_score, C.byref(h))
     if rc:
         raise RuntimeError(lib().orc_last_error().decode())
     return Model(h)
