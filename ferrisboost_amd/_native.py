@@ -25,6 +25,24 @@ class Shape(C.Structure):
     _fields_ = [("n_features", C.c_uint32), ("width", P), ("n_bins", P), ("categorical", P)]
 
 
+class Plan(C.Structure):
+    """fbh_plan: the memory plan of a context."""
+
+    _fields_ = [
+        ("budget", C.c_uint64),
+        ("fixed_bytes", C.c_uint64),
+        ("resident_record_bytes", C.c_uint64),
+        ("column_bytes", C.c_uint64),
+        ("staging_bytes", C.c_uint64),
+        ("peak_bytes", C.c_uint64),
+        ("streamed_record_bytes", C.c_uint64),
+        ("n_tiles", C.c_uint32),
+        ("resident_tiles", C.c_uint32),
+        ("columns_resident", C.c_uint32),
+        ("window_rows", C.c_uint32),
+    ]
+
+
 class Config(C.Structure):
     _fields_ = [
         ("memory_budget", C.c_uint64),
@@ -136,6 +154,11 @@ class Stats(C.Structure):
         ("device_bytes", C.c_double),
         ("rounds", C.c_uint32),
         ("device_sigmoid", C.c_uint32),
+        ("n_tiles", C.c_uint32),
+        ("resident_tiles", C.c_uint32),
+        ("streamed_bytes", C.c_uint64),
+        ("planned_bytes", C.c_uint64),
+        ("budget_bytes", C.c_uint64),
     ]
 
 
@@ -159,6 +182,7 @@ NODE_DTYPE = np.dtype(
 # Every symbol the headers declare, per library.
 HIP_SYMBOLS = [
     "fbh_last_error", "fbh_device_available", "fbh_ctx_create", "fbh_ctx_destroy",
+    "fbh_plan_memory", "fbh_ctx_plan", "fbh_ctx_streamed_bytes",
     "fbh_ctx_device_bytes", "fbh_upload_block", "fbh_upload_quantize_gpair",
     "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_gradient_exchange",
     "fbh_download_margin", "fbh_sigmoid_host", "fbh_sigmoid_device", "fbh_sigmoid_checksum",
@@ -208,6 +232,11 @@ def hip() -> C.CDLL:
         L.fbh_ctx_create.argtypes = [C.c_int, C.c_uint64, C.POINTER(Shape), C.POINTER(Config),
                                      C.POINTER(P)]
         L.fbh_ctx_destroy.argtypes = [P]
+        L.fbh_plan_memory.argtypes = [C.c_uint64, C.POINTER(Shape), C.POINTER(Config), C.c_uint64,
+                                      C.POINTER(Plan)]
+        L.fbh_ctx_plan.argtypes = [P, C.POINTER(Plan)]
+        L.fbh_ctx_streamed_bytes.argtypes = [P]
+        L.fbh_ctx_streamed_bytes.restype = C.c_uint64
         L.fbh_ctx_device_bytes.argtypes = [P]
         L.fbh_ctx_device_bytes.restype = C.c_uint64
         L.fbh_upload_block.argtypes = [P, P, C.c_uint32, C.c_uint32, P]

@@ -21,6 +21,7 @@
 #include <cstring>
 #include <memory>
 #include <stdexcept>
+#include <thread>
 #include <string>
 #include <vector>
 
@@ -127,12 +128,25 @@ struct fbh_ctx {
         std::vector<uint32_t> feats;  // ascending global ids
         uint8_t *data;
         bool global;  // one feature too wide for LDS: global-memory atomics
+        bool resident = true;      // records in HBM; else streamed from host
+        uint8_t *host = nullptr;   // pinned host records of a streamed tile
     };
     std::vector<Tile> tiles;
     std::vector<int32_t> feat_tile, feat_pos;
-    // Column-major bins of every feature (the partition reads one cell per
-    // row: rows of the nodes splitting on one feature share cache lines).
+    // Column-major bins of every feature, when the plan keeps them (the
+    // partition reads one cell per row: rows of the nodes splitting on one
+    // feature share cache lines).
     std::vector<uint8_t *> cols;
+    fbh_plan plan{};
+    // Streaming (plan.staging_bytes > 0): pinned host columns of the features
+    // of streamed tiles, two device windows for records and two for columns,
+    // a copy stream and the events that hand the windows back and forth.
+    std::vector<uint8_t *> host_cols;
+    uint8_t *win_rec[2] = {nullptr, nullptr};
+    uint8_t *win_col[2] = {nullptr, nullptr};
+    hipStream_t copy_stream = nullptr;
+    hipEvent_t win_ready[4] = {}, win_free[4] = {};
+    std::vector<void *> host_allocs;
     std::vector<uint8_t> uploaded;
 
     float *gpair_f32 = nullptr;
@@ -156,6 +170,7 @@ struct fbh_ctx {
     uint32_t *d_counts = nullptr, *d_excl = nullptr, *d_totals = nullptr;
     LeafDev *d_leaves = nullptr;
     size_t off_tilefeats = 0, off_sfeats = 0;  // offsets in the tree-table buffer
+    size_t stage_bytes = 0;
     uint64_t max_chunks = 0;    // capacity of the partition chunk arrays
     uint64_t cat_in_words = 0;  // capacity of the partition category words
 
@@ -178,6 +193,16 @@ struct fbh_ctx {
         bool global;
     };
     std::vector<Group> groups;
+    struct Streamed {
+        uint32_t tile;         // index in tiles
+        uint32_t entry;        // index of its TileDev in the tree's table
+        uint32_t lds_slots;
+        uint32_t bytes_per_row;
+    };
+    std::vector<Streamed> streamed;  // streamed tiles with active features this tree
+    uint64_t win_flip = 0;           // alternates the two record windows
+    uint64_t col_flip = 0;           // alternates the two column windows
+    uint64_t streamed_bytes = 0;     // host-to-device bytes of streamed records and columns
     bool has_global = false;  // this tree builds a feature with global atomics
     uint32_t cat_words_per_node = 0;
     bool tree_begun = false;
@@ -217,6 +242,16 @@ struct fbh_ctx {
         if (pin_ids.p) (void)hipHostFree(pin_ids.p);
         if (pin_src.p) (void)hipHostFree(pin_src.p);
         pin_small.p = pin_leaves.p = pin_out.p = pin_ids.p = pin_src.p = nullptr;
+        if (copy_stream) (void)hipStreamSynchronize(copy_stream);
+        for (void *h : host_allocs) (void)hipHostFree(h);
+        host_allocs.clear();
+        for (int k = 0; k < 4; k++) {
+            if (win_ready[k]) (void)hipEventDestroy(win_ready[k]);
+            if (win_free[k]) (void)hipEventDestroy(win_free[k]);
+            win_ready[k] = win_free[k] = nullptr;
+        }
+        if (copy_stream) (void)hipStreamDestroy(copy_stream);
+        copy_stream = nullptr;
         if (up_stream) (void)hipStreamSynchronize(up_stream);
         for (auto e : chunk_ev) (void)hipEventDestroy(e);
         chunk_ev.clear();
@@ -251,6 +286,16 @@ struct fbh_ctx {
     void pinned(PinnedBuf &b, size_t bytes) {
         check(hipHostMalloc(&b.p, bytes, hipHostMallocDefault), "pinned host allocation");
         b.bytes = bytes;
+    }
+
+    uint8_t *host_alloc(size_t bytes, const char *what) {
+        void *p = nullptr;
+        hipError_t e = hipHostMalloc(&p, std::max<size_t>(bytes, 64), hipHostMallocDefault);
+        if (e != hipSuccess)
+            throw RuntimeError(std::string("pinned host allocation of ") + what + " (" +
+                               std::to_string(bytes) + " bytes) failed: " + hipGetErrorString(e));
+        host_allocs.push_back(p);
+        return static_cast<uint8_t *>(p);
     }
 
     void sync() { check(hipStreamSynchronize(stream), "stream synchronize"); }
@@ -331,8 +376,202 @@ void plan_tiles(fbh_ctx &c) {
 
 uint32_t div_up(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 
+// Per-row bytes of the arrays fbh_set_objective adds later: labels, margins,
+// leaf ids, row weights and host sigmoids (a context without objective keeps
+// a 4-byte delta instead, which this covers).
+constexpr uint64_t OBJECTIVE_ROW_BYTES = 4 + 4 + 2 + 4 + 4;
+constexpr uint64_t MAX_WINDOW_BYTES = 512ull << 20;  // one streamed record window
+constexpr uint64_t MIN_WINDOW_ROWS = 65536;
+
+uint64_t al256(uint64_t b) { return (b + 255) & ~uint64_t(255); }
+
+// Every allocation whose size does not depend on the residency plan, in one
+// place: the planner sums it (a returns nullptr), the context performs it.
+template <class A>
+void fixed_allocations(fbh_ctx &c, A &&a) {
+    const uint64_t n = c.n_rows;
+    c.gpair_f32 = static_cast<float *>(a(8 * n, "f32 gradient pairs"));
+    c.gpair = static_cast<int64_t *>(a(16 * n, "fixed-point gradient pairs"));
+    c.rows = static_cast<uint32_t *>(a(4 * n, "row arena"));
+    c.tmp = static_cast<uint32_t *>(a(4 * n, "partition arena"));
+    c.flags = static_cast<uint8_t *>(a(n, "partition flags"));
+    c.hist = static_cast<int64_t *>(a(16 * (uint64_t)c.n_slots * c.width_max, "histogram slots"));
+    c.red_f64 = static_cast<double *>(a(8 * (2 * (uint64_t)c.n_red_blocks + 2), "reduction scratch"));
+    c.red_i64 = static_cast<int64_t *>(a(8 * (2 * (uint64_t)c.n_red_blocks + 2), "reduction scratch"));
+    // The per-tree tables (tiles, tile features, split features) share one
+    // buffer so that a tree's plan goes to the device in one copy.
+    c.off_tilefeats = al256(sizeof(TileDev) * c.tiles.size());
+    c.off_sfeats = c.off_tilefeats + al256(sizeof(TileFeatDev) * c.n_features);
+    uint8_t *tt = static_cast<uint8_t *>(
+        a(c.off_sfeats + sizeof(SplitFeatDev) * c.n_features, "tree tables"));
+    c.d_tiles = reinterpret_cast<TileDev *>(tt);
+    c.d_tilefeats = reinterpret_cast<TileFeatDev *>(tt ? tt + c.off_tilefeats : nullptr);
+    c.d_sfeats = reinterpret_cast<SplitFeatDev *>(tt ? tt + c.off_sfeats : nullptr);
+    const uint64_t cw = std::max(1u, c.max_cat_words);
+    c.d_cands = static_cast<FeatCandDev *>(
+        a(sizeof(FeatCandDev) * (uint64_t)c.n_slots * c.n_features, "split candidates"));
+    c.d_cat_scratch = static_cast<uint64_t *>(a(8 * (uint64_t)c.n_slots * cw, "category sets"));
+    // Split packets, then (256-aligned) the category sets of the call.
+    c.d_packets = static_cast<SplitPacketDev *>(
+        a(sizeof(SplitPacketDev) * MAX_NODES + 256 + 8 * (uint64_t)c.n_slots * cw, "split packets"));
+    c.cat_in_words = (uint64_t)c.n_slots * cw;
+    c.max_chunks = n / PART_CHUNK + MAX_NODES + 1;
+    c.d_counts = static_cast<uint32_t *>(a(4 * c.max_chunks, "partition counts"));
+    c.d_excl = static_cast<uint32_t *>(a(4 * (c.max_chunks + 1), "partition offsets"));
+    c.d_totals = static_cast<uint32_t *>(a(4 * (uint64_t)MAX_NODES, "partition totals"));
+    // Leaf table followed by the leaf values of one call.
+    c.d_leaves = static_cast<LeafDev *>(a((sizeof(LeafDev) + 4) * MAX_NODES, "leaf table"));
+    // Staging of the launch tables of one blocking call (each table 256-aligned).
+    const size_t eval_tables = sizeof(HistNodeDev) * MAX_NODES + 4 * MAX_NODES +
+                               12 * MAX_NODES + sizeof(SplitNodeDev) * MAX_NODES +
+                               (size_t)c.n_slots * c.n_features + 8 * 256;
+    c.stage_bytes = std::max<size_t>(
+        {eval_tables, 2 * sizeof(PartReqDev) * MAX_NODES + 8 * c.cat_in_words + 4 * 256,
+         c.off_sfeats + sizeof(SplitFeatDev) * c.n_features});
+    c.d_stage = static_cast<uint8_t *>(a(c.stage_bytes, "launch tables"));
+}
+
+// StreamingMemModel + fill_residency (src/training/gpu_mem_plan.rs:279-600,
+// 855-880) for LDS tiles in HBM: everything resident when it fits; else the
+// columns go first, the streaming windows are reserved and tiles stay
+// resident in order while they fit (tiles of one too-wide feature always).
+fbh_plan plan_memory(fbh_ctx &c, uint64_t budget) {
+    fbh_plan P{};
+    P.budget = budget;
+    P.n_tiles = (uint32_t)c.tiles.size();
+    uint64_t fixed = 0;
+    fixed_allocations(c, [&](uint64_t b, const char *) -> void * {
+        fixed += std::max<uint64_t>(b, 256);
+        return nullptr;
+    });
+    const uint64_t n = c.n_rows;
+    fixed += OBJECTIVE_ROW_BYTES * n;
+    P.fixed_bytes = fixed;
+    if (fixed > budget)
+        throw InputError("gpu_memory_budget of " + std::to_string(budget) +
+                         " bytes cannot hold the per-row arrays and tables (" +
+                         std::to_string(fixed) + " bytes)");
+    const uint64_t avail = budget - fixed;
+    uint64_t rec_all = 0, col_all = 0;
+    for (const auto &t : c.tiles) rec_all += n * t.stride;
+    for (uint32_t f = 0; f < c.n_features; f++) col_all += n * c.width[f];
+    for (auto &t : c.tiles) t.resident = true;
+    if (rec_all + col_all <= avail) {
+        P.resident_record_bytes = rec_all;
+        P.column_bytes = col_all;
+        P.columns_resident = 1;
+        P.resident_tiles = P.n_tiles;
+    } else {
+        uint32_t max_stride = 4, max_w = 1;
+        for (const auto &t : c.tiles) max_stride = std::max(max_stride, t.stride);
+        for (uint32_t f = 0; f < c.n_features; f++) max_w = std::max<uint32_t>(max_w, c.width[f]);
+        // Two column windows (uploads, partitions of streamed features) and
+        // two record windows (histograms of streamed tiles).
+        const uint64_t col_win = 2 * n * max_w;
+        uint64_t w = std::min<uint64_t>(MAX_WINDOW_BYTES, avail / 8) / (2 * max_stride);
+        w = std::min<uint64_t>(n, std::max<uint64_t>(w, MIN_WINDOW_ROWS));
+        const uint64_t rec_win = 2 * w * max_stride;
+        if (col_win + rec_win > avail)
+            throw InputError("gpu_memory_budget of " + std::to_string(budget) +
+                             " bytes leaves " + std::to_string(avail) +
+                             " bytes after the per-row arrays; streaming needs " +
+                             std::to_string(col_win + rec_win));
+        uint64_t left = avail - col_win - rec_win;
+        for (auto &t : c.tiles) {
+            if (!t.global) continue;
+            if (n * t.stride > left)
+                throw InputError("gpu_memory_budget too small for the records of a feature "
+                                 "too wide for LDS, which must stay resident");
+            left -= n * t.stride;
+            P.resident_record_bytes += n * t.stride;
+            P.resident_tiles++;
+        }
+        bool any_streamed = false;
+        for (auto &t : c.tiles) {
+            if (t.global) continue;
+            if (n * t.stride <= left) {
+                left -= n * t.stride;
+                P.resident_record_bytes += n * t.stride;
+                P.resident_tiles++;
+            } else {
+                t.resident = false;
+                any_streamed = true;
+                P.streamed_record_bytes += n * t.stride;
+            }
+        }
+        P.columns_resident = 0;
+        P.window_rows = any_streamed ? (uint32_t)w : 0;
+        P.staging_bytes = col_win + (any_streamed ? rec_win : 0);
+    }
+    P.peak_bytes = P.fixed_bytes + P.resident_record_bytes + P.column_bytes + P.staging_bytes;
+    return P;
+}
+
+uint64_t budget_of(const fbh_config &conf, uint64_t free_bytes) {
+    if (conf.memory_budget) return conf.memory_budget;
+    const uint64_t reserve = std::max<uint64_t>(free_bytes / 100 * 15, 512ull << 20);
+    return free_bytes > reserve ? free_bytes - reserve : 0;
+}
+
 void ensure_tree(const fbh_ctx *c) {
     if (!c->tree_begun) throw InputError("fbh_begin_tree must be called before this operation");
+}
+
+}  // namespace
+
+namespace {
+
+// Shape and configuration of a context (no device work): shared by
+// fbh_ctx_create and fbh_plan_memory.
+fbh_config configure(fbh_ctx &c, uint64_t n_rows, const fbh_shape *shape, const fbh_config *cfg) {
+    if (!shape || shape->n_features == 0) throw InputError("shape has no features");
+    if (!shape->width || !shape->n_bins) throw InputError("shape needs widths and bin counts");
+    if (n_rows == 0) throw InputError("training data must have at least one row");
+    if (n_rows > 0xFFFFFFFFull)
+        throw InputError("training data has " + std::to_string(n_rows) +
+                         " rows, above the supported limit 4294967295");
+    c.n_rows = n_rows;
+    c.n_features = shape->n_features;
+    c.width.assign(shape->width, shape->width + shape->n_features);
+    c.n_bins.assign(shape->n_bins, shape->n_bins + shape->n_features);
+    c.cat.assign(shape->n_features, 0);
+    if (shape->categorical)
+        c.cat.assign(shape->categorical, shape->categorical + shape->n_features);
+    for (uint32_t f = 0; f < c.n_features; f++) {
+        if (c.width[f] != 1 && c.width[f] != 2)
+            throw InputError("feature " + std::to_string(f) + " has bin width " +
+                             std::to_string(c.width[f]) + "; only 1 and 2 are supported");
+        const uint32_t lim = c.width[f] == 1 ? 255u : 65535u;
+        if (c.n_bins[f] == 0 || c.n_bins[f] > lim)
+            throw InputError("feature " + std::to_string(f) + " has " +
+                             std::to_string(c.n_bins[f]) + " bins, not storable at width " +
+                             std::to_string(c.width[f]));
+        if (c.cat[f] && c.n_bins[f] > MAX_DEVICE_CATS)
+            throw InputError("categorical feature " + std::to_string(f) + " has " +
+                             std::to_string(c.n_bins[f]) +
+                             " categories; the device split scan supports at most " +
+                             std::to_string(MAX_DEVICE_CATS));
+        c.width_max += c.n_bins[f];
+        if (c.cat[f]) c.max_cat_words += (c.n_bins[f] + 63) / 64;
+    }
+    fbh_config conf{};
+    if (cfg) conf = *cfg;
+    c.tile_bytes = (uint32_t)env_u64("FB_HIP_TILE_BYTES",
+                                      conf.tile_bytes ? conf.tile_bytes : DEFAULT_TILE_BYTES);
+    c.fixed_chunk_rows = (uint32_t)env_u64("FB_HIP_CHUNK_ROWS", conf.rows_per_block);
+    c.hist_tpb = (uint32_t)env_u64("FB_HIP_HIST_TPB", 256);
+    c.hist_waves = (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HIST_WAVES", HIST_WAVES));
+    if (c.tile_bytes < 4096 || c.tile_bytes > 160 * 1024)
+        throw InputError("tile_bytes must be in 4096..=163840");
+    if (c.fixed_chunk_rows && (c.fixed_chunk_rows < 256 || c.fixed_chunk_rows % 256))
+        throw InputError("rows_per_block must be a positive multiple of 256");
+    if (c.hist_tpb != 256 && c.hist_tpb != 512 && c.hist_tpb != 1024)
+        throw InputError("histogram threads per workgroup must be 256, 512 or 1024");
+    c.n_slots = conf.hist_slots ? conf.hist_slots : 64;
+    if (c.n_slots > MAX_NODES)
+        throw InputError("hist_slots must be at most " + std::to_string(MAX_NODES));
+    plan_tiles(c);
+    return conf;
 }
 
 }  // namespace
@@ -362,128 +601,74 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
     return guard([&] {
         if (!out) throw InputError("out must not be null");
         *out = nullptr;
-        if (!shape || shape->n_features == 0) throw InputError("shape has no features");
-        if (n_rows == 0) throw InputError("training data must have at least one row");
-        if (n_rows > 0xFFFFFFFFull)
-            throw InputError("training data has " + std::to_string(n_rows) +
-                             " rows, above the supported limit 4294967295");
+        auto c = std::make_unique<fbh_ctx>();
+        c->device = -1;
+        const fbh_config conf = configure(*c, n_rows, shape, cfg);
         int n_dev = 0;
         if (hipGetDeviceCount(&n_dev) != hipSuccess || n_dev == 0)
             throw RuntimeError("no HIP device is available");
         if (device < 0 || device >= n_dev)
             throw InputError("device " + std::to_string(device) + " does not exist");
-        auto c = std::make_unique<fbh_ctx>();
         c->device = device;
         check(hipSetDevice(device), "hipSetDevice");
         check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "stream creation");
-        c->n_rows = n_rows;
-        c->n_features = shape->n_features;
-        c->width.assign(shape->width, shape->width + shape->n_features);
-        c->n_bins.assign(shape->n_bins, shape->n_bins + shape->n_features);
-        c->cat.assign(shape->n_features, 0);
-        if (shape->categorical)
-            c->cat.assign(shape->categorical, shape->categorical + shape->n_features);
-        for (uint32_t f = 0; f < c->n_features; f++) {
-            if (c->width[f] != 1 && c->width[f] != 2)
-                throw InputError("feature " + std::to_string(f) + " has bin width " +
-                                 std::to_string(c->width[f]) + "; only 1 and 2 are supported");
-            const uint32_t lim = c->width[f] == 1 ? 255u : 65535u;
-            if (c->n_bins[f] == 0 || c->n_bins[f] > lim)
-                throw InputError("feature " + std::to_string(f) + " has " +
-                                 std::to_string(c->n_bins[f]) + " bins, not storable at width " +
-                                 std::to_string(c->width[f]));
-            if (c->cat[f] && c->n_bins[f] > MAX_DEVICE_CATS)
-                throw InputError("categorical feature " + std::to_string(f) + " has " +
-                                 std::to_string(c->n_bins[f]) +
-                                 " categories; the device split scan supports at most " +
-                                 std::to_string(MAX_DEVICE_CATS));
-            c->width_max += c->n_bins[f];
-            if (c->cat[f]) c->max_cat_words += (c->n_bins[f] + 63) / 64;
-        }
-        fbh_config conf{};
-        if (cfg) conf = *cfg;
-        c->tile_bytes = (uint32_t)env_u64("FB_HIP_TILE_BYTES",
-                                          conf.tile_bytes ? conf.tile_bytes : DEFAULT_TILE_BYTES);
-        c->fixed_chunk_rows = (uint32_t)env_u64("FB_HIP_CHUNK_ROWS", conf.rows_per_block);
-        c->hist_tpb = (uint32_t)env_u64("FB_HIP_HIST_TPB", 256);
-        c->hist_waves = (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HIST_WAVES", HIST_WAVES));
-        if (c->tile_bytes < 4096 || c->tile_bytes > 160 * 1024)
-            throw InputError("tile_bytes must be in 4096..=163840");
-        if (c->fixed_chunk_rows && (c->fixed_chunk_rows < 256 || c->fixed_chunk_rows % 256))
-            throw InputError("rows_per_block must be a positive multiple of 256");
-        if (c->hist_tpb != 256 && c->hist_tpb != 512 && c->hist_tpb != 1024)
-            throw InputError("histogram threads per workgroup must be 256, 512 or 1024");
         {
             hipDeviceProp_t prop;
             check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
             c->n_cus = (uint32_t)std::max(1, prop.multiProcessorCount);
         }
-        c->n_slots = conf.hist_slots ? conf.hist_slots : 64;
-        if (c->n_slots > MAX_NODES)
-            throw InputError("hist_slots must be at most " + std::to_string(MAX_NODES));
-        plan_tiles(*c);
+        size_t free_b = 0, total_b = 0;
+        check(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
+        c->plan = plan_memory(*c, budget_of(conf, free_b));
+        const fbh_plan &P = c->plan;
 
-        // ---- allocation, once ----
-        for (auto &t : c->tiles) t.data = c->alloc<uint8_t>(n_rows * t.stride, "tile records");
-        {
+        // ---- allocation, once, as planned ----
+        for (auto &t : c->tiles) {
+            if (t.resident) {
+                t.data = c->alloc<uint8_t>(n_rows * t.stride, "tile records");
+            } else {
+                t.data = nullptr;
+                t.host = c->host_alloc(n_rows * t.stride, "streamed tile records");
+                std::memset(t.host, 0, n_rows * t.stride);
+            }
+        }
+        c->cols.assign(c->n_features, nullptr);
+        c->host_cols.assign(c->n_features, nullptr);
+        if (P.columns_resident) {
             uint64_t col_bytes = 0;
             for (uint32_t f = 0; f < c->n_features; f++) col_bytes += n_rows * c->width[f];
             uint8_t *base = c->alloc<uint8_t>(col_bytes, "bin columns");
-            c->cols.resize(c->n_features);
             for (uint32_t f = 0; f < c->n_features; f++) {
                 c->cols[f] = base;
                 base += n_rows * c->width[f];
             }
+        } else {
+            uint32_t max_stride = 4, max_w = 1;
+            for (const auto &t : c->tiles) max_stride = std::max(max_stride, t.stride);
+            for (uint32_t f = 0; f < c->n_features; f++)
+                max_w = std::max<uint32_t>(max_w, c->width[f]);
+            for (int k = 0; k < 2; k++)
+                c->win_col[k] = c->alloc<uint8_t>(n_rows * max_w, "column window");
+            if (P.window_rows)
+                for (int k = 0; k < 2; k++)
+                    c->win_rec[k] =
+                        c->alloc<uint8_t>((uint64_t)P.window_rows * max_stride, "record window");
+            for (const auto &t : c->tiles)
+                if (!t.resident)
+                    for (uint32_t f : t.feats)
+                        c->host_cols[f] = c->host_alloc(n_rows * c->width[f], "streamed column");
+            check(hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking), "stream creation");
+            for (int k = 0; k < 4; k++) {
+                check(hipEventCreateWithFlags(&c->win_ready[k], hipEventDisableTiming), "event");
+                check(hipEventCreateWithFlags(&c->win_free[k], hipEventDisableTiming), "event");
+                check(hipEventRecord(c->win_free[k], c->stream), "event");
+            }
         }
         c->uploaded.assign(c->n_features, 0);
-        c->gpair_f32 = c->alloc<float>(2 * n_rows, "f32 gradient pairs");
-        c->gpair = c->alloc<int64_t>(2 * n_rows, "fixed-point gradient pairs");
-        c->rows = c->alloc<uint32_t>(n_rows, "row arena");
-        c->tmp = c->alloc<uint32_t>(n_rows, "partition arena");
-        c->flags = c->alloc<uint8_t>(n_rows, "partition flags");
-        c->delta = c->alloc<float>(n_rows, "prediction delta");
-        c->hist = c->alloc<int64_t>((size_t)c->n_slots * c->width_max * 2, "histogram slots");
-        c->red_f64 = c->alloc<double>(2 * c->n_red_blocks + 2, "reduction scratch");
-        c->red_i64 = c->alloc<int64_t>(2 * c->n_red_blocks + 2, "reduction scratch");
-        // The per-tree tables (tiles, tile features, split features) share
-        // one buffer so that a tree's plan goes to the device in one copy.
-        {
-            auto al = [](size_t b) { return (b + 255) & ~size_t(255); };
-            c->off_tilefeats = al(sizeof(TileDev) * c->tiles.size());
-            c->off_sfeats = c->off_tilefeats + al(sizeof(TileFeatDev) * c->n_features);
-            uint8_t *tt = c->alloc<uint8_t>(c->off_sfeats + sizeof(SplitFeatDev) * c->n_features,
-                                            "tree tables");
-            c->d_tiles = reinterpret_cast<TileDev *>(tt);
-            c->d_tilefeats = reinterpret_cast<TileFeatDev *>(tt + c->off_tilefeats);
-            c->d_sfeats = reinterpret_cast<SplitFeatDev *>(tt + c->off_sfeats);
-        }
-        c->d_cands = c->alloc<FeatCandDev>((size_t)c->n_slots * c->n_features,
-                                           "split candidates");
-        c->d_cat_scratch =
-            c->alloc<uint64_t>((size_t)c->n_slots * std::max(1u, c->max_cat_words), "category sets");
-        // Split packets, then (256-aligned) the category sets of the call.
-        c->d_packets = reinterpret_cast<SplitPacketDev *>(c->alloc<uint8_t>(
-            sizeof(SplitPacketDev) * MAX_NODES + 256 +
-                8 * (size_t)c->n_slots * std::max(1u, c->max_cat_words),
-            "split packets"));
-        c->cat_in_words = (uint64_t)c->n_slots * std::max(1u, c->max_cat_words);
-        c->max_chunks = n_rows / PART_CHUNK + MAX_NODES + 1;
-        c->d_counts = c->alloc<uint32_t>(c->max_chunks, "partition counts");
-        c->d_excl = c->alloc<uint32_t>(c->max_chunks + 1, "partition offsets");
-        c->d_totals = c->alloc<uint32_t>(MAX_NODES, "partition totals");
-        // Leaf table followed by the leaf values of one call.
-        c->d_leaves = reinterpret_cast<LeafDev *>(
-            c->alloc<uint8_t>((sizeof(LeafDev) + 4) * MAX_NODES, "leaf table"));
-        // Staging of the launch tables of one blocking call (each table 256-aligned).
-        const size_t eval_tables = sizeof(HistNodeDev) * MAX_NODES + 4 * MAX_NODES +
-                                   12 * MAX_NODES + sizeof(SplitNodeDev) * MAX_NODES +
-                                   (size_t)c->n_slots * c->n_features + 8 * 256;
-        const size_t small = std::max<size_t>(
-            {eval_tables,
-             sizeof(PartReqDev) * MAX_NODES + 8 * c->cat_in_words + 2 * 256,
-             c->off_sfeats + sizeof(SplitFeatDev) * c->n_features});
-        c->pinned(c->pin_small, small);
-        c->d_stage = c->alloc<uint8_t>(small, "launch tables");
+        fixed_allocations(*c, [&](uint64_t b, const char *what) -> void * {
+            return c->alloc<uint8_t>(b, what);
+        });
+        c->pinned(c->pin_small, c->stage_bytes);
         c->pinned(c->pin_leaves, (sizeof(LeafDev) + 4) * MAX_NODES);
         c->pinned(c->pin_out, std::max<size_t>({sizeof(SplitPacketDev) * MAX_NODES + 256 +
                                                     8 * (size_t)c->n_slots *
@@ -492,9 +677,28 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
         check(hipEventCreateWithFlags(&c->leaves_done, hipEventDisableTiming), "event");
         // Zero the tile padding once.
         for (auto &t : c->tiles)
-            check(hipMemsetAsync(t.data, 0, n_rows * t.stride, c->stream), "tile clear");
+            if (t.resident)
+                check(hipMemsetAsync(t.data, 0, n_rows * t.stride, c->stream), "tile clear");
         c->sync();
         *out = c.release();
+    });
+}
+
+int fbh_plan_memory(uint64_t n_rows, const fbh_shape *shape, const fbh_config *cfg,
+                    uint64_t free_bytes, fbh_plan *out) {
+    return guard([&] {
+        if (!out) throw InputError("out must not be null");
+        fbh_ctx c;
+        c.device = -1;
+        const fbh_config conf = configure(c, n_rows, shape, cfg);
+        *out = plan_memory(c, budget_of(conf, free_bytes));
+    });
+}
+
+int fbh_ctx_plan(const fbh_ctx *c, fbh_plan *out) {
+    return guard([&] {
+        if (!c || !out) throw InputError("null argument");
+        *out = c->plan;
     });
 }
 
@@ -503,6 +707,8 @@ int fbh_ctx_destroy(fbh_ctx *ctx) {
 }
 
 uint64_t fbh_ctx_device_bytes(const fbh_ctx *ctx) { return ctx ? ctx->device_bytes : 0; }
+
+uint64_t fbh_ctx_streamed_bytes(const fbh_ctx *ctx) { return ctx ? ctx->streamed_bytes : 0; }
 
 int fbh_upload_block(fbh_ctx *c, const uint32_t *feat_ids, uint32_t n_feats, uint32_t width,
                      const void *bins) {
@@ -516,17 +722,37 @@ int fbh_upload_block(fbh_ctx *c, const uint32_t *feat_ids, uint32_t n_feats, uin
                 throw InputError("feature " + std::to_string(f) +
                                  " does not have the block's bin width");
         }
+        const uint64_t n = c->n_rows;
         for (uint32_t l = 0; l < n_feats; l++) {
             const uint32_t f = feat_ids[l];
             const fbh_ctx::Tile &t = c->tiles[c->feat_tile[f]];
-            const uint8_t *src = static_cast<const uint8_t *>(bins) + (uint64_t)l * c->n_rows * width;
-            check(hipMemcpyAsync(c->cols[f], src, c->n_rows * width, hipMemcpyHostToDevice,
-                                 c->stream),
-                  "block upload");
-            // The column into its record position.
-            check(launch_pack_feature(c->cols[f], c->n_rows, width, t.data, t.stride,
-                                      (uint32_t)c->feat_pos[f] * width, c->stream),
-                  "tile packing");
+            const uint32_t off = (uint32_t)c->feat_pos[f] * width;
+            const uint8_t *src = static_cast<const uint8_t *>(bins) + (uint64_t)l * n * width;
+            if (t.resident) {
+                // Through the resident column, or a column window, into the
+                // feature's record position.
+                uint8_t *col = c->plan.columns_resident ? c->cols[f] : c->win_col[0];
+                check(hipMemcpyAsync(col, src, n * width, hipMemcpyHostToDevice, c->stream),
+                      "block upload");
+                check(launch_pack_feature(col, n, width, t.data, t.stride, off, c->stream),
+                      "tile packing");
+                if (!c->plan.columns_resident) c->sync();  // the window is reused
+            } else {
+                // A streamed tile: records packed into pinned host memory, and
+                // the column kept for the partitions of this feature.
+                std::memcpy(c->host_cols[f], src, n * width);
+                uint8_t *rec = t.host + off;
+                const uint32_t stride = t.stride;
+                const unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+                std::vector<std::thread> pool;
+                for (unsigned k = 0; k < nt; k++)
+                    pool.emplace_back([&, k] {
+                        const uint64_t lo = n * k / nt, hi = n * (k + 1) / nt;
+                        for (uint64_t r = lo; r < hi; r++)
+                            std::memcpy(rec + r * stride, src + r * width, width);
+                    });
+                for (auto &th : pool) th.join();
+            }
             c->uploaded[f] = 1;
         }
         c->sync();
@@ -743,37 +969,47 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
         std::vector<TileDev> td;
         std::vector<TileFeatDev> tf;
         c->groups.clear();
+        c->streamed.clear();
         c->has_global = false;
+        // Appends tile t's entry (and its active features) when it has any;
+        // returns the LDS slots and active cell bytes per row.
+        auto add_tile = [&](const fbh_ctx::Tile &t, uint32_t &lds, uint32_t &active_bytes) {
+            TileDev d{};
+            d.data = t.data;
+            d.stride = t.stride;
+            d.width = t.width;
+            d.n_feat = (uint32_t)t.feats.size();
+            d.feat_base = (uint32_t)tf.size();
+            lds = 0;
+            active_bytes = 0;
+            for (uint32_t f : t.feats) {
+                TileFeatDev e{};
+                if (c->hist_off[f] >= 0) {
+                    e.n_bins = c->n_bins[f];
+                    e.lds_off = lds;
+                    e.hist_off = (uint32_t)c->hist_off[f];
+                    lds += c->n_bins[f];
+                    active_bytes += t.width;
+                }
+                tf.push_back(e);
+            }
+            if (lds == 0) {
+                tf.resize(d.feat_base);
+                return false;
+            }
+            d.lds_slots = t.global ? 0 : lds;
+            td.push_back(d);
+            return true;
+        };
         for (int glob = 0; glob < 2; glob++)
         for (uint32_t w : {1u, 2u}) {
             for (uint32_t stride : {4u, 8u, 12u, 16u, 32u, 48u, 64u}) {
                 fbh_ctx::Group g{(int)w, (int)stride / 4, (uint32_t)td.size(), 0, 0, 0, glob == 1};
                 for (const auto &t : c->tiles) {
                     if (t.width != w || t.stride != stride || (int)t.global != glob) continue;
-                    TileDev d{};
-                    d.data = t.data;
-                    d.stride = t.stride;
-                    d.width = t.width;
-                    d.n_feat = (uint32_t)t.feats.size();
-                    d.feat_base = (uint32_t)tf.size();
-                    uint32_t lds = 0, active_bytes = 0;
-                    for (uint32_t f : t.feats) {
-                        TileFeatDev e{};
-                        if (c->hist_off[f] >= 0) {
-                            e.n_bins = c->n_bins[f];
-                            e.lds_off = lds;
-                            e.hist_off = (uint32_t)c->hist_off[f];
-                            lds += c->n_bins[f];
-                            active_bytes += w;
-                        }
-                        tf.push_back(e);
-                    }
-                    if (lds == 0) {
-                        tf.resize(d.feat_base);
-                        continue;
-                    }
-                    d.lds_slots = t.global ? 0 : lds;
-                    td.push_back(d);
+                    if (!t.resident) continue;
+                    uint32_t lds, active_bytes;
+                    if (!add_tile(t, lds, active_bytes)) continue;
                     g.n_tiles++;
                     if (!t.global) g.lds_max = std::max(g.lds_max, lds);
                     g.bytes_per_row += active_bytes;
@@ -783,6 +1019,15 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
                     c->has_global = c->has_global || g.global;
                 }
             }
+        }
+        // Streamed tiles: entries after the resident groups, launched one
+        // window at a time.
+        for (const auto &t : c->tiles) {
+            if (t.resident) continue;
+            uint32_t lds, active_bytes;
+            const uint32_t k = (uint32_t)td.size();
+            if (!add_tile(t, lds, active_bytes)) continue;
+            c->streamed.push_back({(uint32_t)(&t - c->tiles.data()), k, lds, active_bytes});
         }
         // split feature table
         std::vector<SplitFeatDev> sf;
@@ -810,6 +1055,7 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
                              hipMemcpyHostToDevice, c->stream),
               "tree tables");
         // The delta is kept only for callers without a device objective.
+        if (c->objective < 0 && !c->delta) c->delta = c->alloc<float>(c->n_rows, "prediction delta");
         check(launch_init_rows(c->rows, c->objective >= 0 ? nullptr : c->delta, c->n_rows,
                                c->stream),
               "row arena reset");
@@ -858,7 +1104,7 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
             const uint32_t nc = div_up(nd.rows.len, chunk_rows);
             // Single-chunk nodes are written by plain stores, except that a
             // globally accumulated feature needs a zeroed slot.
-            if (nc != 1 || c->has_global) zero_slots.push_back(nd.slot);
+            if (nc != 1 || c->has_global || !c->streamed.empty()) zero_slots.push_back(nd.slot);
             if (nc == 0) continue;
             HistNodeDev h{};
             h.row_off = nd.rows.offset;
@@ -922,11 +1168,9 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
                 check(hipEventRecord(c->ev_pool[ev].first, c->stream), "event");
             }
             uint64_t bins_active = 0;
-            for (const auto &g : c->groups) {
+            auto launch_base = [&]() {
                 HistLaunch L{};
-                L.tiles = c->d_tiles + g.tile_begin;
                 L.feats = c->d_tilefeats;
-                L.n_tiles = g.n_tiles;
                 L.nodes = d_hn;
                 L.n_nodes = (uint32_t)hn.size();
                 L.n_chunks = chunks;
@@ -936,13 +1180,48 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
                 L.gpair = c->gpair;
                 L.hist = c->hist;
                 L.hist_width = c->hist_width;
+                return L;
+            };
+            for (const auto &g : c->groups) {
+                HistLaunch L = launch_base();
+                L.tiles = c->d_tiles + g.tile_begin;
+                L.n_tiles = g.n_tiles;
                 if (g.global)
                     check(launch_hist_global(L, g.width, c->stream), "histogram launch");
                 else
-                    check(launch_hist(L, g.width, g.rd, (int)c->hist_tpb, (size_t)(g.lds_max + 64) * 16,
-                                      c->stream),
+                    check(launch_hist(L, g.width, g.rd, (int)c->hist_tpb, false,
+                                      (size_t)(g.lds_max + 64) * 16, c->stream),
                           "histogram launch");
                 c->hist_bytes += acc_rows * g.bytes_per_row;
+            }
+            // Streamed tiles: row windows of their pinned host records go up
+            // on the copy stream, alternating between two device windows;
+            // each window's launch accumulates the rows it holds.
+            for (const auto &sd : c->streamed) {
+                const fbh_ctx::Tile &t = c->tiles[sd.tile];
+                const uint64_t W = c->plan.window_rows;
+                for (uint64_t lo = 0; lo < c->n_rows; lo += W) {
+                    const uint64_t hi = std::min<uint64_t>(c->n_rows, lo + W);
+                    const int b = (int)(c->win_flip++ & 1);
+                    check(hipStreamWaitEvent(c->copy_stream, c->win_free[b], 0), "stream wait");
+                    check(hipMemcpyAsync(c->win_rec[b], t.host + lo * t.stride, (hi - lo) * t.stride,
+                                         hipMemcpyHostToDevice, c->copy_stream),
+                          "record window upload");
+                    check(hipEventRecord(c->win_ready[b], c->copy_stream), "event");
+                    check(hipStreamWaitEvent(c->stream, c->win_ready[b], 0), "stream wait");
+                    HistLaunch L = launch_base();
+                    L.tiles = c->d_tiles + sd.entry;
+                    L.n_tiles = 1;
+                    L.stream_data = c->win_rec[b];
+                    L.row_lo = (uint32_t)lo;
+                    L.row_hi = (uint32_t)hi;
+                    check(launch_hist(L, (int)t.width, (int)(t.stride / 4), 256, true,
+                                      (size_t)(sd.lds_slots + 64) * 16, c->stream),
+                          "streamed histogram launch");
+                    check(hipEventRecord(c->win_free[b], c->stream), "event");
+                }
+                c->hist_bytes += acc_rows * sd.bytes_per_row;
+                c->streamed_bytes += c->n_rows * t.stride;
             }
             for (uint32_t f : c->tree_feats) bins_active += c->n_bins[f];
             // Algorithmic bytes: cells + gpair (16) + row id (4) per row and
@@ -1044,10 +1323,21 @@ int fbh_partition(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n, const uint64
             d.row_off = r.rows.offset;
             d.row_len = r.rows.len;
             d.chunk_begin = chunks;
+            d.count_base = chunks;
             d.n_chunks = div_up(r.rows.len, PART_CHUNK);
-            d.data = c->cols[r.feat];
-            d.stride = t.width;
-            d.byte_off = 0;
+            if (c->plan.columns_resident) {  // the resident column
+                d.data = c->cols[r.feat];
+                d.stride = t.width;
+                d.byte_off = 0;
+            } else if (t.resident) {  // the cell inside the resident records
+                d.data = t.data;
+                d.stride = t.stride;
+                d.byte_off = (uint32_t)c->feat_pos[r.feat] * t.width;
+            } else {  // a streamed column, set per feature group below
+                d.data = nullptr;
+                d.stride = t.width;
+                d.byte_off = 0;
+            }
             d.width = t.width;
             d.bin = r.bin;
             d.missing_left = r.missing_left;
@@ -1066,19 +1356,87 @@ int fbh_partition(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n, const uint64
             throw InputError("partition spans overlap or exceed the row arena");
         if (n_cat_words > c->cat_in_words)
             throw InputError("too many category words for one partition call");
+        // Count groups: the requests whose split cells are on the device, then
+        // one group per streamed feature (its column goes up into a column
+        // window first). A group numbers its own chunks; counts land at each
+        // request's place in the call's chunk arrays.
+        std::vector<PartReqDev> grp;
+        std::vector<std::pair<uint32_t, uint32_t>> groups;  // (first, count) in grp
+        std::vector<uint32_t> group_feat;                  // UINT32_MAX: on the device
+        {
+            std::vector<uint32_t> order(pr.size());
+            for (uint32_t k = 0; k < pr.size(); k++) order[k] = k;
+            auto feat_of = [&](uint32_t k) { return reqs[which[k]].feat; };
+            auto key = [&](uint32_t k) -> uint64_t {
+                return pr[k].data ? 0 : 1 + (uint64_t)feat_of(k);
+            };
+            std::stable_sort(order.begin(), order.end(),
+                             [&](uint32_t a, uint32_t b) { return key(a) < key(b); });
+            uint32_t local = 0;
+            for (size_t j = 0; j < order.size(); j++) {
+                const uint32_t k = order[j];
+                if (j == 0 || key(k) != key(order[j - 1])) {
+                    groups.push_back({(uint32_t)grp.size(), 0});
+                    group_feat.push_back(pr[k].data ? UINT32_MAX : feat_of(k));
+                    local = 0;
+                }
+                PartReqDev g = pr[k];
+                g.chunk_begin = local;
+                local += g.n_chunks;
+                grp.push_back(g);
+                groups.back().second++;
+            }
+        }
+        // Streamed groups alternate between the two column windows.
+        std::vector<int> group_win(groups.size(), -1);
+        for (size_t gi = 0; gi < groups.size(); gi++) {
+            if (group_feat[gi] == UINT32_MAX) continue;
+            group_win[gi] = (int)(c->col_flip++ & 1);
+            for (uint32_t k = groups[gi].first; k < groups[gi].first + groups[gi].second; k++)
+                grp[k].data = c->win_col[group_win[gi]];
+        }
         uint8_t *st = static_cast<uint8_t *>(c->pin_small.p);
-        // Requests and category words: one copy into the device staging.
+        // Requests, category words and count groups: one copy into the device staging.
         const size_t bp = sizeof(PartReqDev) * pr.size();
         const size_t off = (bp + 255) & ~size_t(255);
+        const size_t off_g = off + ((8 * (size_t)n_cat_words + 255) & ~size_t(255));
         std::memcpy(st, pr.data(), bp);
         if (n_cat_words) std::memcpy(st + off, cat_words, 8 * (size_t)n_cat_words);
-        check(hipMemcpyAsync(c->d_stage, st, n_cat_words ? off + 8 * (size_t)n_cat_words : bp,
+        std::memcpy(st + off_g, grp.data(), sizeof(PartReqDev) * grp.size());
+        check(hipMemcpyAsync(c->d_stage, st, off_g + sizeof(PartReqDev) * grp.size(),
                              hipMemcpyHostToDevice, c->stream),
               "tables");
-        check(launch_partition(reinterpret_cast<const PartReqDev *>(c->d_stage),
-                               (uint32_t)pr.size(), chunks, c->rows, c->tmp, c->flags, c->d_counts,
-                               c->d_excl, c->d_totals,
-                               reinterpret_cast<const uint64_t *>(c->d_stage + off), c->stream),
+        const uint64_t *d_cats = reinterpret_cast<const uint64_t *>(c->d_stage + off);
+        PartReqDev *d_grp = reinterpret_cast<PartReqDev *>(c->d_stage + off_g);
+        for (size_t gi = 0; gi < groups.size(); gi++) {
+            const uint32_t first = groups[gi].first, cnt = groups[gi].second;
+            uint32_t g_chunks = 0;
+            for (uint32_t k = first; k < first + cnt; k++) g_chunks += grp[k].n_chunks;
+            if (group_feat[gi] != UINT32_MAX) {
+                // A streamed feature: its column goes up into the group's window.
+                const uint32_t f = group_feat[gi];
+                const int b = group_win[gi];
+                const uint64_t bytes = c->n_rows * c->width[f];
+                check(hipStreamWaitEvent(c->copy_stream, c->win_free[2 + b], 0), "stream wait");
+                check(hipMemcpyAsync(c->win_col[b], c->host_cols[f], bytes, hipMemcpyHostToDevice,
+                                     c->copy_stream),
+                      "column window upload");
+                check(hipEventRecord(c->win_ready[2 + b], c->copy_stream), "event");
+                c->streamed_bytes += bytes;
+                check(hipStreamWaitEvent(c->stream, c->win_ready[2 + b], 0), "stream wait");
+                check(launch_partition_count(d_grp + first, cnt, g_chunks, c->rows, c->flags,
+                                             c->d_counts, d_cats, c->stream),
+                      "partition count");
+                check(hipEventRecord(c->win_free[2 + b], c->stream), "event");
+            } else {
+                check(launch_partition_count(d_grp + first, cnt, g_chunks, c->rows, c->flags,
+                                             c->d_counts, d_cats, c->stream),
+                      "partition count");
+            }
+        }
+        check(launch_partition_finish(reinterpret_cast<const PartReqDev *>(c->d_stage),
+                                      (uint32_t)pr.size(), chunks, c->rows, c->tmp, c->flags,
+                                      c->d_counts, c->d_excl, c->d_totals, c->stream),
               "partition");
         check(hipMemcpyAsync(c->pin_out.p, c->d_totals, 4 * pr.size(), hipMemcpyDeviceToHost,
                              c->stream),

@@ -58,6 +58,10 @@ struct HistLaunch {
     const int64_t *gpair;      // [n_rows][2]
     int64_t *hist;             // [slots][hist_width][2]
     uint64_t hist_width;
+    // Streamed tile: its records of rows [row_lo, row_hi) sit at
+    // stream_data + (row - row_lo) * stride; only those rows are accumulated.
+    const uint8_t *stream_data;
+    uint32_t row_lo, row_hi;
 };
 
 // Per-tree feature table of the split scan (compact histogram order).
@@ -113,7 +117,7 @@ struct PartReqDev {
     uint32_t stride, byte_off, width;
     uint32_t bin, missing_left;
     uint32_t cat_off, n_cat_words;
-    uint32_t pad;
+    uint32_t count_base;   // index of the request's first chunk in the chunk arrays
 };
 
 struct LeafDev {
@@ -141,8 +145,9 @@ const char *last_error();
 
 // ---------------------------------------------------------------- launchers
 // threads_per_block is 256, 512 or 1024.
+// stream: L describes one streamed tile window (see HistLaunch).
 hipError_t launch_hist(const HistLaunch &L, int width, int rec_dwords, int threads_per_block,
-                       size_t lds_bytes, hipStream_t s);
+                       bool stream, size_t lds_bytes, hipStream_t s);
 hipError_t launch_hist_global(const HistLaunch &L, int width, hipStream_t s);
 hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slots, uint32_t n,
                              hipStream_t s);
@@ -156,10 +161,16 @@ hipError_t launch_split_nodes(const FeatCandDev *cands, const SplitFeatDev *feat
                               uint32_t n_nodes, SplitParamsDev P, const SplitNodeDev *nodes,
                               const uint64_t *cat_scratch, SplitPacketDev *out,
                               uint64_t *cat_out, uint32_t cat_out_words, hipStream_t s);
-hipError_t launch_partition(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
-                            uint32_t *rows, uint32_t *tmp, uint8_t *flags, uint32_t *chunk_counts,
-                            uint32_t *chunk_offsets, uint32_t *totals, const uint64_t *cat_words,
-                            hipStream_t s);
+// Pass 1 (direction flags, left count per chunk) over a group of requests
+// whose chunk_begin numbers the group's own chunks; counts land at count_base.
+hipError_t launch_partition_count(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
+                                  const uint32_t *rows, uint8_t *flags, uint32_t *chunk_counts,
+                                  const uint64_t *cat_words, hipStream_t s);
+// Passes 2-4 (scan, stable scatter, copy back) over all requests of the call.
+hipError_t launch_partition_finish(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
+                                   uint32_t *rows, uint32_t *tmp, const uint8_t *flags,
+                                   const uint32_t *chunk_counts, uint32_t *chunk_offsets,
+                                   uint32_t *totals, hipStream_t s);
 // id_bytes 0: delta[row] = leaf value; 1 / 2: ids[row] = leaf position as
 // u8 / u16.
 hipError_t launch_assign_leaves(const LeafDev *leaves, uint32_t n_leaves, uint32_t n_chunks,

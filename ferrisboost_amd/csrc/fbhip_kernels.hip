@@ -77,7 +77,10 @@ __device__ __forceinline__ void global_add_u64(unsigned long long *p, unsigned l
 // sums (S = tile slots + 64). The last 64 slots of each plane are one dummy
 // slot per lane: a missing / unseen / unselected cell adds zero there instead
 // of branching, so the atomic stream has no divergent control flow.
-template <int W, int RD, int UNROLL, int TPB>
+// STREAM: the tile is streamed; the launch covers the rows of one window
+// [L.row_lo, L.row_hi), whose records are at L.stream_data, and every node's
+// histogram accumulates over several launches (global atomics only).
+template <int W, int RD, int UNROLL, int TPB, bool STREAM>
 __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
     extern __shared__ unsigned long long lds[];
     constexpr int FPD = 4 / W;
@@ -99,8 +102,28 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
         else hi = mid;
     }
     const HistNodeDev N = L.nodes[lo];
-    const uint32_t r0 = (chunk - N.chunk_begin) * L.chunk_rows;
-    const uint32_t r1 = min(r0 + L.chunk_rows, N.row_len);
+    uint32_t r0 = (chunk - N.chunk_begin) * L.chunk_rows;
+    uint32_t r1 = min(r0 + L.chunk_rows, N.row_len);
+    if (STREAM) {
+        // A node's row ids ascend (stable partitions of 0..n), so the rows of
+        // the window are one sub-range of the chunk: two lower bounds.
+        __shared__ uint32_t win[2];
+        if (threadIdx.x < 2) {
+            const uint32_t key = threadIdx.x == 0 ? L.row_lo : L.row_hi;
+            const uint32_t *rr = L.rows + N.row_off;
+            uint32_t a = r0, b = r1;
+            while (a < b) {
+                const uint32_t m = (a + b) >> 1;
+                if (rr[m] < key) a = m + 1;
+                else b = m;
+            }
+            win[threadIdx.x] = a;
+        }
+        __syncthreads();
+        r0 = win[0];
+        r1 = win[1];
+        if (r0 >= r1) return;  // uniform: no row of this chunk in the window
+    }
 
     uint32_t nb[NF], loff[NF];
 #pragma unroll
@@ -140,7 +163,10 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
         for (int u = 0; u < UNROLL; u++) {
             if (ok[u]) {
                 g[u] = gp[row[u]];
-                load_record<RD>(T.data + (size_t)row[u] * T.stride, rec[u]);
+                if (STREAM)
+                    load_record<RD>(L.stream_data + (size_t)(row[u] - L.row_lo) * T.stride, rec[u]);
+                else
+                    load_record<RD>(T.data + (size_t)row[u] * T.stride, rec[u]);
             } else {
                 g[u] = make_longlong2(0, 0);
 #pragma unroll
@@ -171,7 +197,7 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
     __syncthreads();
 
     int64_t *out = L.hist + (uint64_t)N.slot * L.hist_width * 2u;
-    const bool single = N.n_chunks == 1;
+    const bool single = !STREAM && N.n_chunks == 1;
     for (uint32_t fi = 0; fi < T.n_feat; fi++) {
         const TileFeatDev F = L.feats[T.feat_base + fi];
         for (uint32_t bin = tid; bin < F.n_bins; bin += TPB) {
@@ -240,7 +266,7 @@ hipError_t launch_hist_global(const HistLaunch &L, int width, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int W, int RD, int TPB>
+template <int W, int RD, int TPB, bool STREAM>
 static hipError_t launch_hist_t(const HistLaunch &L, size_t lds, hipStream_t s) {
     const uint32_t blocks = L.chunk_groups * XCDS * L.n_tiles;
     if (blocks == 0) return hipSuccess;
@@ -251,28 +277,39 @@ static hipError_t launch_hist_t(const HistLaunch &L, size_t lds, hipStream_t s) 
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     if (dev < 64 && !(attr_done >> dev & 1)) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&hist_kernel<W, RD, 4, TPB>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        // The dynamic share is what the kernel's static LDS leaves of 160 KiB.
+        const void *fn = reinterpret_cast<const void *>(&hist_kernel<W, RD, 4, TPB, STREAM>);
+        hipFuncAttributes fa{};
+        e = hipFuncGetAttributes(&fa, fn);
+        if (e != hipSuccess) return e;
+        e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)(160 * 1024 - fa.sharedSizeBytes));
         if (e != hipSuccess) return e;
         attr_done |= 1ull << dev;
     }
-    hipLaunchKernelGGL((hist_kernel<W, RD, 4, TPB>), dim3(blocks), dim3(TPB), lds, s, L);
+    hipLaunchKernelGGL((hist_kernel<W, RD, 4, TPB, STREAM>), dim3(blocks), dim3(TPB), lds, s, L);
     return hipGetLastError();
 }
 
-hipError_t launch_hist(const HistLaunch &L, int width, int rd, int tpb, size_t lds, hipStream_t s) {
-#define FBH_HIST_TPB(WW, R)                                                  \
-    if (width == WW && rd == R) {                                            \
-        if (tpb == 1024) return launch_hist_t<WW, R, 1024>(L, lds, s);       \
-        if (tpb == 512) return launch_hist_t<WW, R, 512>(L, lds, s);         \
-        if (tpb == 256) return launch_hist_t<WW, R, 256>(L, lds, s);         \
-        return hipErrorInvalidValue;                                         \
-    }
-    FBH_HIST_TPB(1, 1) FBH_HIST_TPB(1, 2) FBH_HIST_TPB(1, 3) FBH_HIST_TPB(1, 4)
-    FBH_HIST_TPB(1, 8) FBH_HIST_TPB(1, 12) FBH_HIST_TPB(1, 16)
-    FBH_HIST_TPB(2, 1) FBH_HIST_TPB(2, 2) FBH_HIST_TPB(2, 3) FBH_HIST_TPB(2, 4)
-    FBH_HIST_TPB(2, 8) FBH_HIST_TPB(2, 12) FBH_HIST_TPB(2, 16)
-#undef FBH_HIST_TPB
+template <int W, int RD>
+static hipError_t launch_hist_wr(const HistLaunch &L, int tpb, bool stream, size_t lds,
+                                 hipStream_t s) {
+    if (stream) return launch_hist_t<W, RD, 256, true>(L, lds, s);
+    if (tpb == 256) return launch_hist_t<W, RD, 256, false>(L, lds, s);
+    if (tpb == 512) return launch_hist_t<W, RD, 512, false>(L, lds, s);
+    if (tpb == 1024) return launch_hist_t<W, RD, 1024, false>(L, lds, s);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_hist(const HistLaunch &L, int width, int rd, int tpb, bool stream, size_t lds,
+                       hipStream_t s) {
+#define FBH_HIST_WR(WW, R) \
+    if (width == WW && rd == R) return launch_hist_wr<WW, R>(L, tpb, stream, lds, s);
+    FBH_HIST_WR(1, 1) FBH_HIST_WR(1, 2) FBH_HIST_WR(1, 3) FBH_HIST_WR(1, 4)
+    FBH_HIST_WR(1, 8) FBH_HIST_WR(1, 12) FBH_HIST_WR(1, 16)
+    FBH_HIST_WR(2, 1) FBH_HIST_WR(2, 2) FBH_HIST_WR(2, 3) FBH_HIST_WR(2, 4)
+    FBH_HIST_WR(2, 8) FBH_HIST_WR(2, 12) FBH_HIST_WR(2, 16)
+#undef FBH_HIST_WR
     return hipErrorInvalidValue;
 }
 
@@ -768,7 +805,7 @@ __global__ __launch_bounds__(PART_TPB) void part_count_kernel(const PartReqDev *
     if (threadIdx.x == 0) {
         uint32_t t = 0;
         for (int w = 0; w < PART_TPB / 64; w++) t += wave_sum[w];
-        counts[chunk] = t;
+        counts[R.count_base + (chunk - R.chunk_begin)] = t;
     }
 }
 
@@ -860,13 +897,20 @@ __global__ __launch_bounds__(PART_TPB) void part_copy_kernel(const PartReqDev *r
         rows[R.row_off + i] = tmp[R.row_off + i];
 }
 
-hipError_t launch_partition(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
-                            uint32_t *rows, uint32_t *tmp, uint8_t *flags, uint32_t *counts,
-                            uint32_t *excl, uint32_t *totals, const uint64_t *cat_words,
-                            hipStream_t s) {
+hipError_t launch_partition_count(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
+                                  const uint32_t *rows, uint8_t *flags, uint32_t *counts,
+                                  const uint64_t *cat_words, hipStream_t s) {
     if (n_chunks == 0) return hipSuccess;
     hipLaunchKernelGGL(part_count_kernel, dim3(n_chunks), dim3(PART_TPB), 0, s, reqs, n_reqs, rows,
                        flags, counts, cat_words);
+    return hipGetLastError();
+}
+
+hipError_t launch_partition_finish(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
+                                   uint32_t *rows, uint32_t *tmp, const uint8_t *flags,
+                                   const uint32_t *counts, uint32_t *excl, uint32_t *totals,
+                                   hipStream_t s) {
+    if (n_chunks == 0) return hipSuccess;
     hipLaunchKernelGGL(part_scan_kernel, dim3(1), dim3(1024), 0, s, counts, n_chunks, excl, reqs,
                        n_reqs, totals);
     hipLaunchKernelGGL(part_scatter_kernel, dim3(n_chunks), dim3(PART_TPB), 0, s, reqs, n_reqs,

@@ -759,6 +759,16 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     g_stats.host_gradient_seconds = grad_s;
     g_stats.rounds = p.n_rounds;
     g_stats.device_sigmoid = dev_sigmoid ? 1 : 0;
+    {
+        fbh_plan plan{};
+        call(fbh_ctx_plan(ctx.get(), &plan));
+        g_stats.n_tiles = plan.n_tiles;
+        g_stats.resident_tiles = plan.resident_tiles;
+        g_stats.planned_bytes = plan.peak_bytes;
+        g_stats.budget_bytes = plan.budget;
+        g_stats.streamed_bytes = fbh_ctx_streamed_bytes(ctx.get());
+        g_stats.device_bytes = (double)fbh_ctx_device_bytes(ctx.get());
+    }
     double ms = 0.0;
     uint64_t launches = 0, bytes = 0;
     call(fbh_hist_timing(ctx.get(), &ms, &launches, &bytes, 0));

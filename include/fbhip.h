@@ -134,6 +134,39 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
                    fbh_ctx **out);
 /* Drop of GpuTrainCtx. */
 int fbh_ctx_destroy(fbh_ctx *ctx);
+
+/* The memory plan of a context (StreamingMemModel + fill_residency,
+ * src/training/gpu_mem_plan.rs:279-600, 855-880, re-derived for HBM-resident
+ * LDS tiles). Everything is resident when it fits the budget; otherwise the
+ * column-major copies go first, then as many tiles as fit stay resident and
+ * the others stream from pinned host memory in row windows (histograms) and
+ * whole columns (partitions of their features). A budget that cannot hold
+ * the per-row arrays plus the streaming windows is an input error. */
+typedef struct {
+    uint64_t budget;                /* bytes the context may allocate */
+    uint64_t fixed_bytes;           /* per-row arrays, histogram slots, tables */
+    uint64_t resident_record_bytes; /* records of the resident tiles */
+    uint64_t column_bytes;          /* resident column-major bins (0: none) */
+    uint64_t staging_bytes;         /* streaming windows (0: nothing streams) */
+    uint64_t peak_bytes;            /* the sum: what the context allocates */
+    uint64_t streamed_record_bytes; /* host records streamed by one full pass */
+    uint32_t n_tiles;
+    uint32_t resident_tiles;
+    uint32_t columns_resident;      /* 1: the partition reads resident columns */
+    uint32_t window_rows;           /* rows of one streamed window */
+} fbh_plan;
+
+/* The plan fbh_ctx_create would make for this shape, configuration and free
+ * device memory (no device needed; free_bytes is used when
+ * cfg->memory_budget is 0, minus max(15 %, 512 MiB) of it as the reserve of
+ * default_safety_reserve, src/training/gpu_mem_plan.rs:957-959). */
+int fbh_plan_memory(uint64_t n_rows, const fbh_shape *shape, const fbh_config *cfg,
+                    uint64_t free_bytes, fbh_plan *out);
+/* The plan a context was created with. */
+int fbh_ctx_plan(const fbh_ctx *ctx, fbh_plan *out);
+/* Host-to-device bytes the context has streamed (records and columns of
+ * streamed tiles) since its creation. */
+uint64_t fbh_ctx_streamed_bytes(const fbh_ctx *ctx);
 /* GpuTrainCtx::budget (src/backend/cuda/train_ctx.rs:103-242): bytes the
  * context holds on the device. */
 uint64_t fbh_ctx_device_bytes(const fbh_ctx *ctx);

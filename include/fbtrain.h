@@ -89,6 +89,11 @@ typedef struct {
     double device_bytes;      /* bytes the backend context holds */
     uint32_t rounds;
     uint32_t device_sigmoid;  /* 1: logistic gradients used the device sigmoid */
+    uint32_t n_tiles;         /* LDS tiles of the memory plan (fbh_plan) */
+    uint32_t resident_tiles;  /* tiles kept in HBM; the others streamed */
+    uint64_t streamed_bytes;  /* host-to-device bytes of streamed records and columns */
+    uint64_t planned_bytes;   /* peak_bytes of the plan */
+    uint64_t budget_bytes;    /* the budget the plan honoured */
 } fbt_stats;
 
 typedef struct fbt_model fbt_model;

@@ -283,3 +283,84 @@ def test_shap_matches_oracle_and_is_additive(fb, oracle):
     assert np.max(np.abs(got - want)) <= 1e-5
     margin = pm.predict(rows, output_margin=True).astype(np.float64)
     assert np.max(np.abs(got.astype(np.float64).sum(axis=1) - margin)) <= 1e-4
+
+
+def _plan_for(N, model, n_rows, slots, budget, categorical=None):
+    """The plan the trainer makes for this model's shape under a budget."""
+    vals, offs = model.cuts()
+    nb = (np.diff(offs.astype(np.int64)) + 1).astype(np.uint32)
+    w = np.where(nb > 255, 2, 1).astype(np.uint8)
+    cat = None if categorical is None else np.ascontiguousarray(categorical, np.uint8)
+    shape = N.Shape(nb.size, N.ptr(w), N.ptr(nb), N.ptr(cat))
+    cfg = N.Config()
+    cfg.memory_budget = budget
+    cfg.hist_slots = slots
+    out = N.Plan()
+    N.check_hip(N.hip().fbh_plan_memory(n_rows, C.byref(shape), C.byref(cfg), 0, C.byref(out)))
+    return out
+
+
+def _streaming_budgets(N, model, n_rows, slots, categorical=None):
+    """A budget keeping some tiles resident and one keeping none."""
+    big = _plan_for(N, model, n_rows, slots, 1 << 40, categorical)
+    assert big.n_tiles >= 3, big.n_tiles
+    lo = big.fixed_bytes
+    some = none = None
+    for step in range(0, 4000):
+        b = lo + step * (1 << 18)
+        try:
+            p = _plan_for(N, model, n_rows, slots, b, categorical)
+        except ValueError:
+            continue
+        if p.resident_tiles == 0 and none is None:
+            none = b
+        if 0 < p.resident_tiles < p.n_tiles:
+            some = b
+            break
+    assert some and none, (some, none)
+    return some, none
+
+
+@pytest.mark.parametrize("kind", ["depthwise", "lossguide_categorical"])
+def test_streaming_matches_resident_and_oracle(fb, oracle, N, kind):
+    """gpu_memory_budget forces tiles to stream from pinned host memory
+    (record windows for histograms, columns for partitions): the models are
+    byte-identical to the all-resident run and to the CPU oracle, and the
+    context stays within the budget."""
+    rng = np.random.default_rng(61 if kind == "depthwise" else 62)
+    n = 120_007
+    if kind == "depthwise":
+        nf = 40
+        x = rng.normal(size=(n, nf)).astype(np.float32)
+        x[rng.random((n, nf)) < 0.04] = np.nan
+        y = (np.nan_to_num(x[:, 0]) - np.nan_to_num(x[:, 7]) * np.nan_to_num(x[:, 31])
+             + 0.3 * rng.normal(size=n) > 0).astype(np.float32)
+        p = {"n_rounds": 4, "max_depth": 6, "eta": 0.3, "max_bin": 255}
+        slots, cat = 32, None
+    else:
+        nf = 24
+        x = rng.random((n, nf)).astype(np.float32)
+        x[:, 18:] = rng.integers(0, 300, size=(n, 6))
+        x[rng.random((n, nf)) < 0.05] = np.nan
+        y = (np.nan_to_num(x[:, 0]) + (np.nan_to_num(x[:, 20]) % 7 == 3) + 0.1 * rng.normal(size=n)
+             ).astype(np.float32)
+        p = {"n_rounds": 3, "max_bin": 1024, "grow_policy": "lossguide", "max_leaves": 31,
+             "objective": "reg:squarederror", "eta": 0.3}
+        slots = 33
+        cat = np.array([0] * 18 + [1] * 6, np.uint8)
+    pp = product_params(p)
+    if cat is not None:
+        pp["feature_types"] = ["c" if c else "q" for c in cat]
+    ref = fb.train(pp, x, y, num_boost_round=p["n_rounds"])
+    assert ref.stats["resident_tiles"] == ref.stats["n_tiles"]
+    some, none = _streaming_budgets(N, ref, n, slots, cat)
+    om = oracle.train(x, y, oracle.make_params(**p), categorical=cat)
+    for budget in (some, none):
+        st = fb.train(dict(pp, gpu_memory_budget=budget), x, y, num_boost_round=p["n_rounds"])
+        assert st.stats["budget_bytes"] == budget
+        assert st.stats["resident_tiles"] < st.stats["n_tiles"]
+        assert st.stats["streamed_bytes"] > 0
+        assert st.stats["device_bytes"] <= budget
+        assert_same_models(ref, st)
+        assert_same_models(om, st)
+        assert np.array_equal(st.train_margins(n).view(np.uint32), ref.train_margins(n).view(np.uint32))

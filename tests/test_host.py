@@ -224,3 +224,70 @@ def test_host_sigmoid_restatement_equals_libm(oracle):
     assert bad.size == 0, [(hex(int(x.view(np.uint32)[i])), got[i], want[i]) for i in bad[:5]]
     # denormal outputs are produced and kept
     assert np.any((want > 0) & (want < np.finfo(np.float32).tiny))
+
+
+# ---------------------------------------------------------------- memory plan
+
+def _plan(n_rows, n_features, n_bins=256, width=1, budget=0, free=0, slots=128,
+          categorical=None):
+    from ferrisboost_amd import _native as N
+
+    w = np.full(n_features, width, np.uint8)
+    nb = np.full(n_features, n_bins - 1 if width == 1 and n_bins > 255 else n_bins, np.uint32)
+    cat = None if categorical is None else np.ascontiguousarray(categorical, np.uint8)
+    shape = N.Shape(n_features, N.ptr(w), N.ptr(nb), N.ptr(cat))
+    cfg = N.Config()
+    cfg.memory_budget = budget
+    cfg.hist_slots = slots
+    out = N.Plan()
+    N.check_hip(N.hip().fbh_plan_memory(n_rows, C.byref(shape), C.byref(cfg), free, C.byref(out)))
+    return out
+
+
+def test_plan_everything_resident_when_it_fits():
+    """288 GB of HBM: the narrow and wide configs are fully resident."""
+    for n, f in ((10_500_000, 28), (400_000, 2000)):
+        p = _plan(n, f, free=280 << 30)
+        assert p.resident_tiles == p.n_tiles and p.columns_resident == 1
+        assert p.staging_bytes == 0 and p.streamed_record_bytes == 0
+        assert p.peak_bytes == p.fixed_bytes + p.resident_record_bytes + p.column_bytes
+        assert p.peak_bytes <= p.budget
+        # the record tiles and the columns each hold every cell once (u8)
+        assert p.column_bytes == n * f and p.resident_record_bytes >= n * f
+
+
+def test_plan_streams_under_a_forced_budget():
+    """50M x 200 u8 under 4 GiB: columns leave HBM, the windows are reserved,
+    some tiles stay resident and the rest stream; the plan fits the budget."""
+    p = _plan(50_000_000, 200, budget=4 << 30)
+    assert p.budget == 4 << 30 and p.peak_bytes <= p.budget
+    assert p.columns_resident == 0 and p.column_bytes == 0
+    assert 0 < p.resident_tiles < p.n_tiles
+    assert p.staging_bytes > 0 and p.window_rows >= 65536
+    assert p.streamed_record_bytes > 0
+
+
+def test_plan_residency_grows_with_the_budget():
+    prev = -1
+    for gib in (3, 4, 6, 8, 12, 16, 24):
+        p = _plan(50_000_000, 200, budget=gib << 30)
+        assert p.peak_bytes <= p.budget
+        assert p.resident_tiles >= prev
+        prev = p.resident_tiles
+    assert prev == _plan(50_000_000, 200, budget=24 << 30).n_tiles
+
+
+def test_plan_rejects_a_budget_below_the_per_row_arrays():
+    """Planning failure is an error, never a silent fallback
+    (src/training/gpu_mem_plan.rs:764-800)."""
+    with pytest.raises(ValueError, match="gpu_memory_budget"):
+        _plan(50_000_000, 200, budget=1 << 30)
+
+
+def test_plan_default_reserve():
+    """Without a budget: free memory minus max(15 %, 512 MiB)
+    (default_safety_reserve, src/training/gpu_mem_plan.rs:957-959)."""
+    p = _plan(100_000, 28, free=100 << 30)
+    assert p.budget == (100 << 30) - (100 << 30) // 100 * 15
+    p = _plan(100_000, 28, free=2 << 30)
+    assert p.budget == (2 << 30) - (512 << 20)
