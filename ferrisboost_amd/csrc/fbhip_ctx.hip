@@ -124,14 +124,31 @@ struct fbh_ctx {
     std::vector<DeviceBuf> allocs;
 
     struct Tile {
-        uint32_t width, stride;
+        uint32_t width;
+        uint32_t rec;     // record bytes per row (the kernel's record size)
+        uint32_t stride;  // bytes from one row's record to the next
         std::vector<uint32_t> feats;  // ascending global ids
         uint8_t *data;
         bool global;  // one feature too wide for LDS: global-memory atomics
         bool resident = true;      // records in HBM; else streamed from host
         uint8_t *host = nullptr;   // pinned host records of a streamed tile
+        int32_t bundle = -1;       // row bundle holding the records, or -1
+        uint32_t bundle_off = 0;   // offset of the record in the bundle row
     };
     std::vector<Tile> tiles;
+    // Row bundles: consecutive tiles of one width and record size whose
+    // records fit in 64 bytes share one allocation, row r's records together
+    // at data + r * pitch. A histogram over a scattered node then fetches one
+    // cache line per row for the whole bundle instead of one per tile (the
+    // tiles of a bundle run side by side on one XCD). Used when every tile is
+    // resident. The gradient pairs stay a separate array: they are rewritten
+    // every round, and a partial-line write costs a full line.
+    struct Bundle {
+        uint32_t pitch;
+        uint8_t *data;
+    };
+    std::vector<Bundle> bundles;
+    bool bundled = false;
     std::vector<int32_t> feat_tile, feat_pos;
     // Column-major bins of every feature, when the plan keeps them (the
     // partition reads one cell per row: rows of the nodes splitting on one
@@ -337,11 +354,12 @@ void plan_tiles(fbh_ctx &c) {
     c.feat_tile.assign(c.n_features, -1);
     c.feat_pos.assign(c.n_features, -1);
     for (uint32_t w : {1u, 2u}) {
-        fbh_ctx::Tile cur{w, 0, {}, nullptr, false};
+        fbh_ctx::Tile cur{w, 0, 0, {}, nullptr, false};
         uint64_t lds = 0;
         auto flush = [&]() {
             if (cur.feats.empty()) return;
-            cur.stride = round_stride((uint32_t)cur.feats.size() * w);
+            cur.rec = round_stride((uint32_t)cur.feats.size() * w);
+            cur.stride = cur.rec;
             const uint32_t t = (uint32_t)c.tiles.size();
             for (size_t k = 0; k < cur.feats.size(); k++) {
                 c.feat_tile[cur.feats[k]] = (int32_t)t;
@@ -372,6 +390,42 @@ void plan_tiles(fbh_ctx &c) {
         }
         flush();
     }
+}
+
+// Row-bundle layout (see fbh_ctx::bundles): runs of consecutive tiles of one
+// width and record size, up to 64 bytes of records each; a record's offset
+// is a multiple of its size, so every load keeps its alignment. A run of one
+// tile stays on its own. Returns whether any bundle was formed.
+bool layout_bundles(fbh_ctx &c) {
+    c.bundles.clear();
+    for (auto &t : c.tiles) {
+        t.bundle = -1;
+        t.bundle_off = 0;
+    }
+    size_t i = 0;
+    while (i < c.tiles.size()) {
+        const fbh_ctx::Tile &a = c.tiles[i];
+        size_t j = i + 1;
+        uint32_t used = a.rec;
+        if (!a.global)
+            while (j < c.tiles.size() && !c.tiles[j].global && c.tiles[j].width == a.width &&
+                   c.tiles[j].rec == a.rec && used + a.rec <= 64) {
+                used += a.rec;
+                j++;
+            }
+        if (j - i >= 2) {
+            const int32_t b = (int32_t)c.bundles.size();
+            uint32_t pitch = 16;
+            while (pitch < used) pitch *= 2;
+            c.bundles.push_back({pitch, nullptr});
+            for (size_t k = i; k < j; k++) {
+                c.tiles[k].bundle = b;
+                c.tiles[k].bundle_off = (uint32_t)(k - i) * a.rec;
+            }
+        }
+        i = j;
+    }
+    return !c.bundles.empty();
 }
 
 uint32_t div_up(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
@@ -435,6 +489,28 @@ void fixed_allocations(fbh_ctx &c, A &&a) {
 // 855-880) for LDS tiles in HBM: everything resident when it fits; else the
 // columns go first, the streaming windows are reserved and tiles stay
 // resident in order while they fit (tiles of one too-wide feature always).
+fbh_plan plan_memory(fbh_ctx &c, uint64_t budget);
+
+// The plan with the row bundle when the bundle and the columns fit, else the
+// plan of separate tile records and pairs (which may stream).
+fbh_plan plan_layout(fbh_ctx &c, uint64_t budget) {
+    c.bundled = layout_bundles(c);
+    if (c.bundled) {
+        try {
+            const fbh_plan P = plan_memory(c, budget);
+            if (P.resident_tiles == P.n_tiles && P.columns_resident) return P;
+        } catch (const InputError &) {
+        }
+        c.bundled = false;
+        c.bundles.clear();
+        for (auto &t : c.tiles) {
+            t.bundle = -1;
+            t.bundle_off = 0;
+        }
+    }
+    return plan_memory(c, budget);
+}
+
 fbh_plan plan_memory(fbh_ctx &c, uint64_t budget) {
     fbh_plan P{};
     P.budget = budget;
@@ -453,7 +529,9 @@ fbh_plan plan_memory(fbh_ctx &c, uint64_t budget) {
                          std::to_string(fixed) + " bytes)");
     const uint64_t avail = budget - fixed;
     uint64_t rec_all = 0, col_all = 0;
-    for (const auto &t : c.tiles) rec_all += n * t.stride;
+    for (const auto &b : c.bundles) rec_all += n * b.pitch;
+    for (const auto &t : c.tiles)
+        if (t.bundle < 0) rec_all += n * t.rec;
     for (uint32_t f = 0; f < c.n_features; f++) col_all += n * c.width[f];
     for (auto &t : c.tiles) t.resident = true;
     if (rec_all + col_all <= avail) {
@@ -461,6 +539,8 @@ fbh_plan plan_memory(fbh_ctx &c, uint64_t budget) {
         P.column_bytes = col_all;
         P.columns_resident = 1;
         P.resident_tiles = P.n_tiles;
+    } else if (c.bundled) {
+        throw InputError("the row bundles do not fit the budget");
     } else {
         uint32_t max_stride = 4, max_w = 1;
         for (const auto &t : c.tiles) max_stride = std::max(max_stride, t.stride);
@@ -619,12 +699,16 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
         }
         size_t free_b = 0, total_b = 0;
         check(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
-        c->plan = plan_memory(*c, budget_of(conf, free_b));
+        c->plan = plan_layout(*c, budget_of(conf, free_b));
         const fbh_plan &P = c->plan;
 
         // ---- allocation, once, as planned ----
+        for (auto &b : c->bundles) b.data = c->alloc<uint8_t>(n_rows * b.pitch, "row bundle");
         for (auto &t : c->tiles) {
-            if (t.resident) {
+            if (t.bundle >= 0) {
+                t.data = c->bundles[t.bundle].data + t.bundle_off;
+                t.stride = c->bundles[t.bundle].pitch;
+            } else if (t.resident) {
                 t.data = c->alloc<uint8_t>(n_rows * t.stride, "tile records");
             } else {
                 t.data = nullptr;
@@ -675,9 +759,11 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
                                                         std::max(1u, c->max_cat_words),
                                                 4 * (size_t)MAX_NODES, 64}));
         check(hipEventCreateWithFlags(&c->leaves_done, hipEventDisableTiming), "event");
-        // Zero the tile padding once.
+        // Zero the record padding once.
+        for (const auto &b : c->bundles)
+            check(hipMemsetAsync(b.data, 0, n_rows * b.pitch, c->stream), "bundle clear");
         for (auto &t : c->tiles)
-            if (t.resident)
+            if (t.resident && t.bundle < 0)
                 check(hipMemsetAsync(t.data, 0, n_rows * t.stride, c->stream), "tile clear");
         c->sync();
         *out = c.release();
@@ -691,7 +777,7 @@ int fbh_plan_memory(uint64_t n_rows, const fbh_shape *shape, const fbh_config *c
         fbh_ctx c;
         c.device = -1;
         const fbh_config conf = configure(c, n_rows, shape, cfg);
-        *out = plan_memory(c, budget_of(conf, free_bytes));
+        *out = plan_layout(c, budget_of(conf, free_bytes));
     });
 }
 
@@ -1003,10 +1089,10 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
         };
         for (int glob = 0; glob < 2; glob++)
         for (uint32_t w : {1u, 2u}) {
-            for (uint32_t stride : {4u, 8u, 12u, 16u, 32u, 48u, 64u}) {
-                fbh_ctx::Group g{(int)w, (int)stride / 4, (uint32_t)td.size(), 0, 0, 0, glob == 1};
+            for (uint32_t rec : {4u, 8u, 12u, 16u, 32u, 48u, 64u}) {
+                fbh_ctx::Group g{(int)w, (int)rec / 4, (uint32_t)td.size(), 0, 0, 0, glob == 1};
                 for (const auto &t : c->tiles) {
-                    if (t.width != w || t.stride != stride || (int)t.global != glob) continue;
+                    if (t.width != w || t.rec != rec || (int)t.global != glob) continue;
                     if (!t.resident) continue;
                     uint32_t lds, active_bytes;
                     if (!add_tile(t, lds, active_bytes)) continue;
@@ -1215,7 +1301,7 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
                     L.stream_data = c->win_rec[b];
                     L.row_lo = (uint32_t)lo;
                     L.row_hi = (uint32_t)hi;
-                    check(launch_hist(L, (int)t.width, (int)(t.stride / 4), 256, true,
+                    check(launch_hist(L, (int)t.width, (int)(t.rec / 4), 256, true,
                                       (size_t)(sd.lds_slots + 64) * 16, c->stream),
                           "streamed histogram launch");
                     check(hipEventRecord(c->win_free[b], c->stream), "event");

@@ -17,9 +17,11 @@ constexpr uint32_t NO_SLOT = 0xFFFFFFFFu;
 // One histogram tile: a group of features of one width stored as row
 // records, record i at data + i * stride, feature k of the tile at byte
 // k * width of the record. A tile's histogram fits the LDS tile budget.
+// Tiles may share one row bundle (stride = bundle pitch, data = the tile's
+// offset in it), so a scattered row costs one cache line for all of them.
 struct TileDev {
     const uint8_t *data;
-    uint32_t stride;     // bytes per record (multiple of 4)
+    uint32_t stride;     // bytes from one row's record to the next (multiple of 4)
     uint32_t width;      // 1 or 2
     uint32_t n_feat;     // features in the record
     uint32_t feat_base;  // first entry of this tile in the TileFeatDev table
