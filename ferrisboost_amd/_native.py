@@ -107,6 +107,19 @@ class PartReq(C.Structure):
     ]
 
 
+class ChildPair(C.Structure):
+    _fields_ = [
+        ("parent_slot", C.c_uint32),
+        ("new_slot", C.c_uint32),
+        ("evaluate", C.c_uint32),
+        ("reserved", C.c_uint32),
+        ("lower", C.c_float * 2),
+        ("upper", C.c_float * 2),
+        ("left_sum", C.c_int64 * 2),
+        ("right_sum", C.c_int64 * 2),
+    ]
+
+
 class TrainParams(C.Structure):
     _fields_ = [
         ("n_rounds", C.c_uint32),
@@ -187,7 +200,7 @@ HIP_SYMBOLS = [
     "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_gradient_exchange",
     "fbh_download_margin", "fbh_sigmoid_host", "fbh_sigmoid_device", "fbh_sigmoid_checksum",
     "fbh_begin_tree", "fbh_eval_nodes", "fbh_download_histogram",
-    "fbh_partition", "fbh_assign_leaves", "fbh_download_delta", "fbh_host_alloc",
+    "fbh_partition", "fbh_partition_eval", "fbh_assign_leaves", "fbh_download_delta", "fbh_host_alloc",
     "fbh_host_free", "fbh_download_rows",
     "fbh_hist_timing", "fbh_set_timing", "fbh_build_histogram", "fbh_partition_rows",
     "fbh_shap_model_create", "fbh_shap_model_destroy", "fbh_shap_contribs",
@@ -253,6 +266,8 @@ def hip() -> C.CDLL:
                                      C.c_uint32]
         L.fbh_download_histogram.argtypes = [P, C.c_uint32, P, C.POINTER(C.c_uint64)]
         L.fbh_partition.argtypes = [P, P, C.c_uint32, P, C.c_uint32, P]
+        L.fbh_partition_eval.argtypes = [P, P, C.c_uint32, P, C.c_uint32, P, P, P, P, P, P,
+                                         C.c_uint32]
         L.fbh_assign_leaves.argtypes = [P, P, P, C.c_uint32]
         L.fbh_download_delta.argtypes = [P, P]
         L.fbh_download_rows.argtypes = [P, P]

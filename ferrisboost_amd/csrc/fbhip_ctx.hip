@@ -186,6 +186,11 @@ struct fbh_ctx {
     SplitPacketDev *d_packets = nullptr;
     uint32_t *d_counts = nullptr, *d_excl = nullptr, *d_totals = nullptr;
     LeafDev *d_leaves = nullptr;
+    // Tables a fused partition + evaluation step plans on the device.
+    HistNodeDev *d_lvl_hist = nullptr;
+    SplitNodeDev *d_lvl_split = nullptr;
+    uint32_t *d_lvl_out = nullptr;  // spans (4 per pair), then left slots (1 per pair)
+    uint32_t *d_lvl_rows = nullptr; // rows per chunk of the planned launch
     size_t off_tilefeats = 0, off_sfeats = 0;  // offsets in the tree-table buffer
     size_t stage_bytes = 0;
     uint64_t max_chunks = 0;    // capacity of the partition chunk arrays
@@ -194,6 +199,7 @@ struct fbh_ctx {
     PinnedBuf pin_small;   // launch tables, reused by blocking calls
     PinnedBuf pin_leaves;  // leaf tables (asynchronous call)
     PinnedBuf pin_out;     // results coming back
+    size_t pin_out_spans = 0;  // offset of a fused step's spans in pin_out
     hipEvent_t leaves_done = nullptr;
     bool leaves_pending = false;
 
@@ -221,6 +227,8 @@ struct fbh_ctx {
     uint64_t col_flip = 0;           // alternates the two column windows
     uint64_t streamed_bytes = 0;     // host-to-device bytes of streamed records and columns
     bool has_global = false;  // this tree builds a feature with global atomics
+    uint32_t hist_row_bytes = 0;  // active cell bytes per row over all built tiles
+    uint64_t bins_active = 0;     // bins of the tree's features
     uint32_t cat_words_per_node = 0;
     bool tree_begun = false;
     double scales[2] = {1.0, 1.0};
@@ -321,21 +329,26 @@ struct fbh_ctx {
     // enough chunks for hist_waves full waves of workgroups over all tiles
     // (occupancy bounded by LDS and by 2048 threads per CU), so that each
     // workgroup flushes its LDS histogram once per many rows.
-    uint32_t chunk_rows_for(uint64_t acc_rows) const {
-        if (fixed_chunk_rows) return fixed_chunk_rows;
+    ChunkRule chunk_rule() const {
+        ChunkRule R{fixed_chunk_rows, 1, MIN_CHUNK_ROWS, 1u << 24};
         uint64_t n_tiles = 0, lds_max = 0;
         for (const auto &g : groups) {
             n_tiles += g.n_tiles;
             if (!g.global) lds_max = std::max<uint64_t>(lds_max, (uint64_t)(g.lds_max + 64) * 16);
         }
-        if (n_tiles == 0) return MIN_CHUNK_ROWS;
+        if (n_tiles == 0) return R;
         uint64_t per_cu = lds_max ? (160u * 1024u) / lds_max : 8;
         per_cu = std::max<uint64_t>(1, std::min<uint64_t>(per_cu, 2048 / hist_tpb));
         const uint64_t wgs = (uint64_t)n_cus * per_cu * hist_waves;
-        const uint64_t want_chunks = std::max<uint64_t>(1, wgs / n_tiles);
-        uint64_t r = (acc_rows + want_chunks - 1) / want_chunks;
+        R.want_chunks = (uint32_t)std::max<uint64_t>(1, wgs / n_tiles);
+        return R;
+    }
+    uint32_t chunk_rows_for(uint64_t acc_rows) const {
+        const ChunkRule R = chunk_rule();
+        if (R.fixed) return R.fixed;
+        uint64_t r = (acc_rows + R.want_chunks - 1) / R.want_chunks;
         r = (r + 1023) & ~uint64_t(1023);
-        return (uint32_t)std::min<uint64_t>(std::max<uint64_t>(r, MIN_CHUNK_ROWS), 1u << 24);
+        return (uint32_t)std::min<uint64_t>(std::max<uint64_t>(r, R.min_rows), R.max_rows);
     }
 
     void collect_timing() {
@@ -475,12 +488,21 @@ void fixed_allocations(fbh_ctx &c, A &&a) {
     c.d_totals = static_cast<uint32_t *>(a(4 * (uint64_t)MAX_NODES, "partition totals"));
     // Leaf table followed by the leaf values of one call.
     c.d_leaves = static_cast<LeafDev *>(a((sizeof(LeafDev) + 4) * MAX_NODES, "leaf table"));
-    // Staging of the launch tables of one blocking call (each table 256-aligned).
+    // Device plan of a fused partition + evaluation step.
+    c.d_lvl_hist = static_cast<HistNodeDev *>(a(sizeof(HistNodeDev) * MAX_NODES, "level plan"));
+    c.d_lvl_split =
+        static_cast<SplitNodeDev *>(a(sizeof(SplitNodeDev) * MAX_NODES, "level plan"));
+    c.d_lvl_out = static_cast<uint32_t *>(a(20 * (uint64_t)MAX_NODES + 256, "level plan"));
+    c.d_lvl_rows = c.d_lvl_out ? c.d_lvl_out + 5 * MAX_NODES : nullptr;
+    // Staging of the launch tables of one blocking call (each table 256-aligned);
+    // a fused step stages a partition's and an evaluation's tables together.
     const size_t eval_tables = sizeof(HistNodeDev) * MAX_NODES + 4 * MAX_NODES +
                                12 * MAX_NODES + sizeof(SplitNodeDev) * MAX_NODES +
                                (size_t)c.n_slots * c.n_features + 8 * 256;
+    const size_t part_tables = 2 * sizeof(PartReqDev) * MAX_NODES + 8 * c.cat_in_words + 4 * 256;
+    const size_t pair_tables = sizeof(PairDev) * MAX_NODES + 256;
     c.stage_bytes = std::max<size_t>(
-        {eval_tables, 2 * sizeof(PartReqDev) * MAX_NODES + 8 * c.cat_in_words + 4 * 256,
+        {eval_tables + part_tables + pair_tables,
          c.off_sfeats + sizeof(SplitFeatDev) * c.n_features});
     c.d_stage = static_cast<uint8_t *>(a(c.stage_bytes, "launch tables"));
 }
@@ -754,10 +776,10 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
         });
         c->pinned(c->pin_small, c->stage_bytes);
         c->pinned(c->pin_leaves, (sizeof(LeafDev) + 4) * MAX_NODES);
-        c->pinned(c->pin_out, std::max<size_t>({sizeof(SplitPacketDev) * MAX_NODES + 256 +
-                                                    8 * (size_t)c->n_slots *
-                                                        std::max(1u, c->max_cat_words),
-                                                4 * (size_t)MAX_NODES, 64}));
+        // Results: packets, category sets, then a fused step's spans and slots.
+        c->pin_out_spans = al256(sizeof(SplitPacketDev) * MAX_NODES) +
+                           al256(8 * (size_t)c->n_slots * std::max(1u, c->max_cat_words));
+        c->pinned(c->pin_out, c->pin_out_spans + 20 * (size_t)MAX_NODES + 256);
         check(hipEventCreateWithFlags(&c->leaves_done, hipEventDisableTiming), "event");
         // Zero the record padding once.
         for (const auto &b : c->bundles)
@@ -1115,6 +1137,11 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
             if (!add_tile(t, lds, active_bytes)) continue;
             c->streamed.push_back({(uint32_t)(&t - c->tiles.data()), k, lds, active_bytes});
         }
+        c->hist_row_bytes = 0;
+        for (const auto &g : c->groups) c->hist_row_bytes += g.bytes_per_row;
+        for (const auto &sd : c->streamed) c->hist_row_bytes += sd.bytes_per_row;
+        c->bins_active = 0;
+        for (uint32_t f : c->tree_feats) c->bins_active += c->n_bins[f];
         // split feature table
         std::vector<SplitFeatDev> sf;
         uint32_t cat_base = 0;
@@ -1152,6 +1179,195 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
     });
 }
 
+}  // extern "C"
+
+namespace {
+
+// Launch tables of one blocking call, laid out in the pinned staging at
+// 256-byte aligned offsets and sent to the device staging at the same
+// offsets in one copy.
+struct Stager {
+    fbh_ctx *c;
+    size_t o = 0;
+    size_t put(const void *src, size_t bytes) {
+        const size_t at = o;
+        const size_t next = at + ((bytes + 255) & ~size_t(255));
+        if (next > c->stage_bytes) throw RuntimeError("launch tables exceed the staging buffer");
+        if (bytes) std::memcpy(static_cast<uint8_t *>(c->pin_small.p) + at, src, bytes);
+        o = next;
+        return at;
+    }
+    template <class T>
+    T *dev(size_t off) const {
+        return reinterpret_cast<T *>(c->d_stage + off);
+    }
+    void send() {
+        if (o)
+            check(hipMemcpyAsync(c->d_stage, c->pin_small.p, o, hipMemcpyHostToDevice, c->stream),
+                  "tables");
+    }
+};
+
+// Histograms, sibling subtraction and split scan of one batch of nodes. The
+// accumulated-node table is planned on the host (exact chunks) or on the
+// device (dev_chunk_rows set, grid_chunks an upper bound).
+struct EvalPlan {
+    const HistNodeDev *hn = nullptr;
+    uint32_t n_hn = 0;
+    uint32_t grid_chunks = 0;
+    uint32_t chunk_rows = 0;
+    const uint32_t *dev_chunk_rows = nullptr;
+    const uint32_t *zero_slots = nullptr;  // host plan: slots to clear
+    uint32_t n_zero = 0;
+    const uint32_t *triples = nullptr;     // (dst, parent, sibling) slots
+    uint32_t n_tri = 0;
+    const SplitNodeDev *sn = nullptr;
+    uint32_t n_nodes = 0;
+    const uint8_t *enabled = nullptr;
+};
+
+void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
+    if (E.dev_chunk_rows)
+        check(launch_zero_nodes(c->hist, c->hist_width, E.hn, E.n_hn,
+                                c->has_global || !c->streamed.empty(), c->stream),
+              "histogram clear");
+    else
+        check(launch_zero_slots(c->hist, c->hist_width, E.zero_slots, E.n_zero, c->stream),
+              "histogram clear");
+    if (E.n_hn && E.grid_chunks) {
+        const size_t ev = c->ev_used;
+        if (c->timing) {
+            if (c->ev_pool.size() <= ev) {
+                hipEvent_t a, b;
+                check(hipEventCreate(&a), "event");
+                check(hipEventCreate(&b), "event");
+                c->ev_pool.push_back({a, b});
+            }
+            check(hipEventRecord(c->ev_pool[ev].first, c->stream), "event");
+        }
+        auto launch_base = [&]() {
+            HistLaunch L{};
+            L.feats = c->d_tilefeats;
+            L.nodes = E.hn;
+            L.n_nodes = E.n_hn;
+            L.n_chunks = E.grid_chunks;
+            L.chunk_rows = E.chunk_rows;
+            L.dev_chunk_rows = E.dev_chunk_rows;
+            L.chunk_groups = div_up(E.grid_chunks, XCDS);
+            L.rows = c->rows;
+            L.gpair = c->gpair;
+            L.hist = c->hist;
+            L.hist_width = c->hist_width;
+            return L;
+        };
+        for (const auto &g : c->groups) {
+            HistLaunch L = launch_base();
+            L.tiles = c->d_tiles + g.tile_begin;
+            L.n_tiles = g.n_tiles;
+            if (g.global)
+                check(launch_hist_global(L, g.width, c->stream), "histogram launch");
+            else
+                check(launch_hist(L, g.width, g.rd, (int)c->hist_tpb, false,
+                                  (size_t)(g.lds_max + 64) * 16, c->stream),
+                      "histogram launch");
+        }
+        // Streamed tiles: row windows of their pinned host records go up
+        // on the copy stream, alternating between two device windows;
+        // each window's launch accumulates the rows it holds.
+        for (const auto &sd : c->streamed) {
+            const fbh_ctx::Tile &t = c->tiles[sd.tile];
+            const uint64_t W = c->plan.window_rows;
+            for (uint64_t lo = 0; lo < c->n_rows; lo += W) {
+                const uint64_t hi = std::min<uint64_t>(c->n_rows, lo + W);
+                const int b = (int)(c->win_flip++ & 1);
+                check(hipStreamWaitEvent(c->copy_stream, c->win_free[b], 0), "stream wait");
+                check(hipMemcpyAsync(c->win_rec[b], t.host + lo * t.stride, (hi - lo) * t.stride,
+                                     hipMemcpyHostToDevice, c->copy_stream),
+                      "record window upload");
+                check(hipEventRecord(c->win_ready[b], c->copy_stream), "event");
+                check(hipStreamWaitEvent(c->stream, c->win_ready[b], 0), "stream wait");
+                HistLaunch L = launch_base();
+                L.tiles = c->d_tiles + sd.entry;
+                L.n_tiles = 1;
+                L.stream_data = c->win_rec[b];
+                L.row_lo = (uint32_t)lo;
+                L.row_hi = (uint32_t)hi;
+                check(launch_hist(L, (int)t.width, (int)(t.rec / 4), 256, true,
+                                  (size_t)(sd.lds_slots + 64) * 16, c->stream),
+                      "streamed histogram launch");
+                check(hipEventRecord(c->win_free[b], c->stream), "event");
+            }
+            c->streamed_bytes += c->n_rows * t.stride;
+        }
+        c->hist_launches++;
+        if (c->timing) {
+            check(hipEventRecord(c->ev_pool[ev].second, c->stream), "event");
+            c->ev_used++;
+        }
+    }
+    check(launch_subtract(c->hist, c->hist_width, E.triples, E.n_tri, c->stream),
+          "sibling subtraction");
+    // ---- split scan ----
+    SplitParamsDev P{};
+    P.inv_g = 1.0 / c->scales[0];
+    P.inv_h = 1.0 / c->scales[1];
+    P.lambda_ = sp->lambda_;
+    P.gamma = sp->gamma;
+    P.mcw = sp->min_child_weight;
+    P.alpha = sp->alpha;
+    P.mds = sp->max_delta_step;
+    P.max_cat_to_onehot = sp->max_cat_to_onehot;
+    P.max_cat_threshold = sp->max_cat_threshold;
+    P.n_feats = (uint32_t)c->tree_feats.size();
+    P.cat_words_per_node = c->cat_words_per_node;
+    check(launch_split_feats(c->hist, c->hist_width, E.sn, E.n_nodes, c->d_sfeats, E.enabled, P,
+                             c->d_cands, c->d_cat_scratch, c->stream),
+          "split scan");
+    const uint32_t cw = std::max(1u, c->cat_words_per_node);
+    const size_t pk_bytes = sizeof(SplitPacketDev) * E.n_nodes;
+    uint8_t *d_out = reinterpret_cast<uint8_t *>(c->d_packets);
+    uint64_t *d_cats = reinterpret_cast<uint64_t *>(d_out + ((pk_bytes + 255) & ~size_t(255)));
+    check(launch_split_nodes(c->d_cands, c->d_sfeats, E.n_nodes, P, E.sn, c->d_cat_scratch,
+                             c->d_packets, d_cats, cw, c->stream),
+          "split argmax");
+    // Packets and category sets land back to back: one download.
+    const size_t out_bytes = c->cat_words_per_node > 0
+                                 ? ((pk_bytes + 255) & ~size_t(255)) + 8 * (size_t)E.n_nodes * cw
+                                 : pk_bytes;
+    check(hipMemcpyAsync(c->pin_out.p, d_out, out_bytes, hipMemcpyDeviceToHost, c->stream),
+          "packet download");
+}
+
+// Packets and category sets of n nodes out of the pinned results (after the
+// stream synchronised).
+void unpack_packets(fbh_ctx *c, uint32_t n, fbh_split *out, uint64_t *cat_words,
+                    uint32_t cat_capacity) {
+    static_assert(sizeof(SplitPacketDev) == sizeof(fbh_split), "packet layout");
+    const uint8_t *po = static_cast<const uint8_t *>(c->pin_out.p);
+    std::memcpy(out, po, sizeof(fbh_split) * n);
+    if (c->cat_words_per_node == 0) return;
+    const uint32_t cw = c->cat_words_per_node;
+    const size_t pk_bytes = sizeof(SplitPacketDev) * n;
+    const uint64_t *words = reinterpret_cast<const uint64_t *>(po + ((pk_bytes + 255) & ~size_t(255)));
+    for (uint32_t i = 0; i < n; i++) {
+        if (!out[i].found || !out[i].is_cat) continue;
+        if (!cat_words || (uint64_t)out[i].cat_offset + out[i].n_cat_words > cat_capacity)
+            throw InputError("cat_words capacity is too small for the category sets");
+        std::memcpy(cat_words + out[i].cat_offset, words + (size_t)i * cw, 8 * out[i].n_cat_words);
+    }
+}
+
+// Algorithmic bytes of one histogram launch: cells + gpair (16) + row id (4)
+// per accumulated row, and the written histogram (2 x 16 per bin) per node.
+void account_hist(fbh_ctx *c, uint64_t acc_rows, uint64_t nodes_with_rows) {
+    if (nodes_with_rows == 0) return;
+    c->hist_bytes += acc_rows * (c->hist_row_bytes + 20) + nodes_with_rows * 32 * c->bins_active;
+}
+
+}  // namespace
+
+extern "C" {
+
 int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_split_params *sp,
                    const uint8_t *enabled, fbh_split *out, uint64_t *cat_words,
                    uint32_t cat_capacity) {
@@ -1174,8 +1390,7 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
                     throw InputError("subtract sibling must be an accumulated node of the call");
             }
         }
-        uint8_t *st = static_cast<uint8_t *>(c->pin_small.p);
-        // ---- histograms of accumulated nodes ----
+        // ---- histograms of accumulated nodes, planned here ----
         std::vector<HistNodeDev> hn;
         std::vector<uint32_t> zero_slots;
         uint32_t chunks = 0;
@@ -1183,7 +1398,6 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
         for (uint32_t i = 0; i < n; i++)
             if (nodes[i].subtract_parent < 0) acc_rows += nodes[i].rows.len;
         const uint32_t chunk_rows = c->chunk_rows_for(acc_rows);
-        acc_rows = 0;
         for (uint32_t i = 0; i < n; i++) {
             const fbh_node &nd = nodes[i];
             if (nd.subtract_parent >= 0) continue;
@@ -1200,7 +1414,6 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
             h.n_chunks = nc;
             hn.push_back(h);
             chunks += nc;
-            acc_rows += nd.rows.len;
         }
         std::vector<uint32_t> triples;
         for (uint32_t i = 0; i < n; i++) {
@@ -1210,19 +1423,6 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
             triples.push_back((uint32_t)nd.subtract_parent);
             triples.push_back(nodes[nd.subtract_sibling].slot);
         }
-        // Every table of the call is laid out in the pinned staging and sent
-        // in one copy to the device staging at the same offsets.
-        uint8_t *ds = c->d_stage;
-        size_t o = 0;
-        auto put = [&](const void *src, size_t bytes) {
-            const size_t at = o;
-            if (bytes) std::memcpy(st + at, src, bytes);
-            o += (bytes + 255) & ~size_t(255);
-            return at;
-        };
-        const size_t o_hn = put(hn.data(), sizeof(HistNodeDev) * hn.size());
-        const size_t o_zero = put(zero_slots.data(), 4 * zero_slots.size());
-        const size_t o_tri = put(triples.data(), 4 * triples.size());
         std::vector<SplitNodeDev> sn(n);
         for (uint32_t i = 0; i < n; i++) {
             sn[i].sum_g = nodes[i].sum[0];
@@ -1231,143 +1431,26 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
             sn[i].upper = nodes[i].upper;
             sn[i].slot = nodes[i].slot;
         }
-        const size_t o_sn = put(sn.data(), sizeof(SplitNodeDev) * n);
-        const uint32_t nf = (uint32_t)c->tree_feats.size();
-        const size_t o_en = enabled ? put(enabled, (size_t)n * nf) : 0;
-        check(hipMemcpyAsync(ds, st, o, hipMemcpyHostToDevice, c->stream), "tables");
-        const HistNodeDev *d_hn = reinterpret_cast<const HistNodeDev *>(ds + o_hn);
-        const uint32_t *d_zero = reinterpret_cast<const uint32_t *>(ds + o_zero);
-        const uint32_t *d_tri = reinterpret_cast<const uint32_t *>(ds + o_tri);
-        const SplitNodeDev *d_sn = reinterpret_cast<const SplitNodeDev *>(ds + o_sn);
-        check(launch_zero_slots(c->hist, c->hist_width, d_zero, (uint32_t)zero_slots.size(),
-                                c->stream),
-              "histogram clear");
-        if (!hn.empty()) {
-            size_t ev = c->ev_used;
-            if (c->timing) {
-                if (c->ev_pool.size() <= ev) {
-                    hipEvent_t a, b;
-                    check(hipEventCreate(&a), "event");
-                    check(hipEventCreate(&b), "event");
-                    c->ev_pool.push_back({a, b});
-                }
-                check(hipEventRecord(c->ev_pool[ev].first, c->stream), "event");
-            }
-            uint64_t bins_active = 0;
-            auto launch_base = [&]() {
-                HistLaunch L{};
-                L.feats = c->d_tilefeats;
-                L.nodes = d_hn;
-                L.n_nodes = (uint32_t)hn.size();
-                L.n_chunks = chunks;
-                L.chunk_rows = chunk_rows;
-                L.chunk_groups = div_up(chunks, XCDS);
-                L.rows = c->rows;
-                L.gpair = c->gpair;
-                L.hist = c->hist;
-                L.hist_width = c->hist_width;
-                return L;
-            };
-            for (const auto &g : c->groups) {
-                HistLaunch L = launch_base();
-                L.tiles = c->d_tiles + g.tile_begin;
-                L.n_tiles = g.n_tiles;
-                if (g.global)
-                    check(launch_hist_global(L, g.width, c->stream), "histogram launch");
-                else
-                    check(launch_hist(L, g.width, g.rd, (int)c->hist_tpb, false,
-                                      (size_t)(g.lds_max + 64) * 16, c->stream),
-                          "histogram launch");
-                c->hist_bytes += acc_rows * g.bytes_per_row;
-            }
-            // Streamed tiles: row windows of their pinned host records go up
-            // on the copy stream, alternating between two device windows;
-            // each window's launch accumulates the rows it holds.
-            for (const auto &sd : c->streamed) {
-                const fbh_ctx::Tile &t = c->tiles[sd.tile];
-                const uint64_t W = c->plan.window_rows;
-                for (uint64_t lo = 0; lo < c->n_rows; lo += W) {
-                    const uint64_t hi = std::min<uint64_t>(c->n_rows, lo + W);
-                    const int b = (int)(c->win_flip++ & 1);
-                    check(hipStreamWaitEvent(c->copy_stream, c->win_free[b], 0), "stream wait");
-                    check(hipMemcpyAsync(c->win_rec[b], t.host + lo * t.stride, (hi - lo) * t.stride,
-                                         hipMemcpyHostToDevice, c->copy_stream),
-                          "record window upload");
-                    check(hipEventRecord(c->win_ready[b], c->copy_stream), "event");
-                    check(hipStreamWaitEvent(c->stream, c->win_ready[b], 0), "stream wait");
-                    HistLaunch L = launch_base();
-                    L.tiles = c->d_tiles + sd.entry;
-                    L.n_tiles = 1;
-                    L.stream_data = c->win_rec[b];
-                    L.row_lo = (uint32_t)lo;
-                    L.row_hi = (uint32_t)hi;
-                    check(launch_hist(L, (int)t.width, (int)(t.rec / 4), 256, true,
-                                      (size_t)(sd.lds_slots + 64) * 16, c->stream),
-                          "streamed histogram launch");
-                    check(hipEventRecord(c->win_free[b], c->stream), "event");
-                }
-                c->hist_bytes += acc_rows * sd.bytes_per_row;
-                c->streamed_bytes += c->n_rows * t.stride;
-            }
-            for (uint32_t f : c->tree_feats) bins_active += c->n_bins[f];
-            // Algorithmic bytes: cells + gpair (16) + row id (4) per row and
-            // feature set, and the written histogram (2 x 16 per bin).
-            c->hist_bytes += acc_rows * 20 + (uint64_t)hn.size() * 32 * bins_active;
-            c->hist_launches++;
-            if (c->timing) {
-                check(hipEventRecord(c->ev_pool[ev].second, c->stream), "event");
-                c->ev_used++;
-            }
-        }
-        check(launch_subtract(c->hist, c->hist_width, d_tri, (uint32_t)(triples.size() / 3),
-                              c->stream),
-              "sibling subtraction");
-        // ---- split scan ----
-        const uint8_t *d_en = enabled ? ds + o_en : nullptr;
-        SplitParamsDev P{};
-        P.inv_g = 1.0 / c->scales[0];
-        P.inv_h = 1.0 / c->scales[1];
-        P.lambda_ = sp->lambda_;
-        P.gamma = sp->gamma;
-        P.mcw = sp->min_child_weight;
-        P.alpha = sp->alpha;
-        P.mds = sp->max_delta_step;
-        P.max_cat_to_onehot = sp->max_cat_to_onehot;
-        P.max_cat_threshold = sp->max_cat_threshold;
-        P.n_feats = nf;
-        P.cat_words_per_node = c->cat_words_per_node;
-        check(launch_split_feats(c->hist, c->hist_width, d_sn, n, c->d_sfeats, d_en, P,
-                                 c->d_cands, c->d_cat_scratch, c->stream),
-              "split scan");
-        const uint32_t cw = std::max(1u, c->cat_words_per_node);
-        // Packets and category sets land back to back: one download.
-        const bool any_cat = c->cat_words_per_node > 0;
-        const size_t pk_bytes = sizeof(SplitPacketDev) * n;
-        uint8_t *d_out = reinterpret_cast<uint8_t *>(c->d_packets);
-        uint64_t *d_cats = reinterpret_cast<uint64_t *>(d_out + ((pk_bytes + 255) & ~size_t(255)));
-        check(launch_split_nodes(c->d_cands, c->d_sfeats, n, P, d_sn, c->d_cat_scratch,
-                                 c->d_packets, d_cats, cw, c->stream),
-              "split argmax");
-        uint8_t *po = static_cast<uint8_t *>(c->pin_out.p);
-        const size_t out_bytes =
-            any_cat ? ((pk_bytes + 255) & ~size_t(255)) + 8 * (size_t)n * cw : pk_bytes;
-        check(hipMemcpyAsync(po, d_out, out_bytes, hipMemcpyDeviceToHost, c->stream),
-              "packet download");
+        Stager S{c};
+        EvalPlan E;
+        E.hn = S.dev<HistNodeDev>(S.put(hn.data(), sizeof(HistNodeDev) * hn.size()));
+        E.n_hn = (uint32_t)hn.size();
+        E.grid_chunks = chunks;
+        E.chunk_rows = chunk_rows;
+        E.zero_slots = S.dev<uint32_t>(S.put(zero_slots.data(), 4 * zero_slots.size()));
+        E.n_zero = (uint32_t)zero_slots.size();
+        E.triples = S.dev<uint32_t>(S.put(triples.data(), 4 * triples.size()));
+        E.n_tri = (uint32_t)(triples.size() / 3);
+        E.sn = S.dev<SplitNodeDev>(S.put(sn.data(), sizeof(SplitNodeDev) * n));
+        E.n_nodes = n;
+        if (enabled)
+            E.enabled = S.dev<uint8_t>(S.put(enabled, (size_t)n * c->tree_feats.size()));
+        S.send();
+        enqueue_eval(c, E, sp);
         c->sync();
         if (c->timing) c->collect_timing();
-        static_assert(sizeof(SplitPacketDev) == sizeof(fbh_split), "packet layout");
-        std::memcpy(out, po, sizeof(fbh_split) * n);
-        if (any_cat) {
-            const uint64_t *words =
-                reinterpret_cast<const uint64_t *>(po + ((pk_bytes + 255) & ~size_t(255)));
-            for (uint32_t i = 0; i < n; i++) {
-                if (!out[i].found || !out[i].is_cat) continue;
-                if (!cat_words || (uint64_t)out[i].cat_offset + out[i].n_cat_words > cat_capacity)
-                    throw InputError("cat_words capacity is too small for the category sets");
-                std::memcpy(cat_words + out[i].cat_offset, words + (size_t)i * cw,
-                            8 * out[i].n_cat_words);
-            }
-        }
+        account_hist(c, acc_rows, hn.size());
+        unpack_packets(c, n, out, cat_words, cat_capacity);
     });
 }
 
@@ -1385,6 +1468,149 @@ int fbh_download_histogram(fbh_ctx *c, uint32_t slot, int64_t *out, uint64_t *wi
     });
 }
 
+}  // extern "C"
+
+namespace {
+
+// Partition tables of one call: the requests with rows (in call order),
+// their count groups (requests whose split cells are on the device, then one
+// group per streamed feature) and their places in the staging.
+struct PartStage {
+    std::vector<PartReqDev> pr;
+    std::vector<uint32_t> which;   // pr index -> request index
+    std::vector<uint32_t> req_of;  // request index -> pr index, NO_SLOT without rows
+    std::vector<PartReqDev> grp;
+    std::vector<std::pair<uint32_t, uint32_t>> groups;  // (first, count) in grp
+    std::vector<uint32_t> group_feat;                  // UINT32_MAX: on the device
+    std::vector<int> group_win;                        // column window of a streamed group
+    uint32_t chunks = 0;
+    size_t o_pr = 0, o_cats = 0, o_grp = 0;
+};
+
+PartStage stage_partition(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
+                          const uint64_t *cat_words, uint32_t n_cat_words, Stager &S) {
+    PartStage P;
+    P.req_of.assign(n, NO_SLOT);
+    for (uint32_t i = 0; i < n; i++) {
+        const fbh_part_req &r = reqs[i];
+        if ((uint64_t)r.rows.offset + r.rows.len > c->n_rows)
+            throw InputError("row span out of range");
+        if (r.feat >= c->n_features) throw InputError("feature id out of range");
+        if (r.n_cat_words && (uint64_t)r.cat_offset + r.n_cat_words > n_cat_words)
+            throw InputError("category set out of range");
+        if (r.rows.len == 0) continue;
+        const auto &t = c->tiles[c->feat_tile[r.feat]];
+        PartReqDev d{};
+        d.row_off = r.rows.offset;
+        d.row_len = r.rows.len;
+        d.chunk_begin = P.chunks;
+        d.count_base = P.chunks;
+        d.n_chunks = div_up(r.rows.len, PART_CHUNK);
+        if (c->plan.columns_resident) {  // the resident column
+            d.data = c->cols[r.feat];
+            d.stride = t.width;
+            d.byte_off = 0;
+        } else if (t.resident) {  // the cell inside the resident records
+            d.data = t.data;
+            d.stride = t.stride;
+            d.byte_off = (uint32_t)c->feat_pos[r.feat] * t.width;
+        } else {  // a streamed column, set per feature group below
+            d.data = nullptr;
+            d.stride = t.width;
+            d.byte_off = 0;
+        }
+        d.width = t.width;
+        d.bin = r.bin;
+        d.missing_left = r.missing_left;
+        d.cat_off = r.cat_offset;
+        d.n_cat_words = r.n_cat_words;
+        P.req_of[i] = (uint32_t)P.pr.size();
+        P.pr.push_back(d);
+        P.which.push_back(i);
+        P.chunks += d.n_chunks;
+    }
+    if (P.pr.empty()) return P;
+    if (P.chunks > c->max_chunks)
+        throw InputError("partition spans overlap or exceed the row arena");
+    if (n_cat_words > c->cat_in_words)
+        throw InputError("too many category words for one partition call");
+    // A group numbers its own chunks; counts land at each request's place in
+    // the call's chunk arrays.
+    std::vector<uint32_t> order(P.pr.size());
+    for (uint32_t k = 0; k < P.pr.size(); k++) order[k] = k;
+    auto feat_of = [&](uint32_t k) { return reqs[P.which[k]].feat; };
+    auto key = [&](uint32_t k) -> uint64_t { return P.pr[k].data ? 0 : 1 + (uint64_t)feat_of(k); };
+    std::stable_sort(order.begin(), order.end(),
+                     [&](uint32_t a, uint32_t b) { return key(a) < key(b); });
+    uint32_t local = 0;
+    for (size_t j = 0; j < order.size(); j++) {
+        const uint32_t k = order[j];
+        if (j == 0 || key(k) != key(order[j - 1])) {
+            P.groups.push_back({(uint32_t)P.grp.size(), 0});
+            P.group_feat.push_back(P.pr[k].data ? UINT32_MAX : feat_of(k));
+            local = 0;
+        }
+        PartReqDev g = P.pr[k];
+        g.chunk_begin = local;
+        local += g.n_chunks;
+        P.grp.push_back(g);
+        P.groups.back().second++;
+    }
+    // Streamed groups alternate between the two column windows.
+    P.group_win.assign(P.groups.size(), -1);
+    for (size_t gi = 0; gi < P.groups.size(); gi++) {
+        if (P.group_feat[gi] == UINT32_MAX) continue;
+        P.group_win[gi] = (int)(c->col_flip++ & 1);
+        for (uint32_t k = P.groups[gi].first; k < P.groups[gi].first + P.groups[gi].second; k++)
+            P.grp[k].data = c->win_col[P.group_win[gi]];
+    }
+    P.o_pr = S.put(P.pr.data(), sizeof(PartReqDev) * P.pr.size());
+    P.o_cats = S.put(cat_words, n_cat_words ? 8 * (size_t)n_cat_words : 0);
+    P.o_grp = S.put(P.grp.data(), sizeof(PartReqDev) * P.grp.size());
+    return P;
+}
+
+// Count passes (streamed features after their column's upload), then the
+// scan, stable scatter and copy back; left totals land in d_totals by pr index.
+void enqueue_partition(fbh_ctx *c, const PartStage &P, const Stager &S) {
+    const uint64_t *d_cats = S.dev<const uint64_t>(P.o_cats);
+    PartReqDev *d_grp = S.dev<PartReqDev>(P.o_grp);
+    for (size_t gi = 0; gi < P.groups.size(); gi++) {
+        const uint32_t first = P.groups[gi].first, cnt = P.groups[gi].second;
+        uint32_t g_chunks = 0;
+        for (uint32_t k = first; k < first + cnt; k++) g_chunks += P.grp[k].n_chunks;
+        if (P.group_feat[gi] != UINT32_MAX) {
+            // A streamed feature: its column goes up into the group's window.
+            const uint32_t f = P.group_feat[gi];
+            const int b = P.group_win[gi];
+            const uint64_t bytes = c->n_rows * c->width[f];
+            check(hipStreamWaitEvent(c->copy_stream, c->win_free[2 + b], 0), "stream wait");
+            check(hipMemcpyAsync(c->win_col[b], c->host_cols[f], bytes, hipMemcpyHostToDevice,
+                                 c->copy_stream),
+                  "column window upload");
+            check(hipEventRecord(c->win_ready[2 + b], c->copy_stream), "event");
+            c->streamed_bytes += bytes;
+            check(hipStreamWaitEvent(c->stream, c->win_ready[2 + b], 0), "stream wait");
+            check(launch_partition_count(d_grp + first, cnt, g_chunks, c->rows, c->flags,
+                                         c->d_counts, d_cats, c->stream),
+                  "partition count");
+            check(hipEventRecord(c->win_free[2 + b], c->stream), "event");
+        } else {
+            check(launch_partition_count(d_grp + first, cnt, g_chunks, c->rows, c->flags,
+                                         c->d_counts, d_cats, c->stream),
+                  "partition count");
+        }
+    }
+    check(launch_partition_finish(S.dev<const PartReqDev>(P.o_pr), (uint32_t)P.pr.size(),
+                                  P.chunks, c->rows, c->tmp, c->flags, c->d_counts, c->d_excl,
+                                  c->d_totals, c->stream),
+          "partition");
+}
+
+}  // namespace
+
+extern "C" {
+
 int fbh_partition(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n, const uint64_t *cat_words,
                   uint32_t n_cat_words, fbh_span *children) {
     return guard([&] {
@@ -1393,148 +1619,124 @@ int fbh_partition(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n, const uint64
         if (n == 0) return;
         if (n > MAX_NODES) throw InputError("too many partition requests");
         check(hipSetDevice(c->device), "hipSetDevice");
-        std::vector<PartReqDev> pr;
-        std::vector<uint32_t> which;
-        uint32_t chunks = 0;
-        for (uint32_t i = 0; i < n; i++) {
-            const fbh_part_req &r = reqs[i];
-            if ((uint64_t)r.rows.offset + r.rows.len > c->n_rows)
-                throw InputError("row span out of range");
-            if (r.feat >= c->n_features) throw InputError("feature id out of range");
-            if (r.n_cat_words && (uint64_t)r.cat_offset + r.n_cat_words > n_cat_words)
-                throw InputError("category set out of range");
-            if (r.rows.len == 0) continue;
-            const auto &t = c->tiles[c->feat_tile[r.feat]];
-            PartReqDev d{};
-            d.row_off = r.rows.offset;
-            d.row_len = r.rows.len;
-            d.chunk_begin = chunks;
-            d.count_base = chunks;
-            d.n_chunks = div_up(r.rows.len, PART_CHUNK);
-            if (c->plan.columns_resident) {  // the resident column
-                d.data = c->cols[r.feat];
-                d.stride = t.width;
-                d.byte_off = 0;
-            } else if (t.resident) {  // the cell inside the resident records
-                d.data = t.data;
-                d.stride = t.stride;
-                d.byte_off = (uint32_t)c->feat_pos[r.feat] * t.width;
-            } else {  // a streamed column, set per feature group below
-                d.data = nullptr;
-                d.stride = t.width;
-                d.byte_off = 0;
-            }
-            d.width = t.width;
-            d.bin = r.bin;
-            d.missing_left = r.missing_left;
-            d.cat_off = r.cat_offset;
-            d.n_cat_words = r.n_cat_words;
-            pr.push_back(d);
-            which.push_back(i);
-            chunks += d.n_chunks;
-        }
+        Stager S{c};
+        const PartStage P = stage_partition(c, reqs, n, cat_words, n_cat_words, S);
         for (uint32_t i = 0; i < n; i++) {
             children[2 * i] = {reqs[i].rows.offset, 0};
             children[2 * i + 1] = {reqs[i].rows.offset, 0};
         }
-        if (pr.empty()) return;
-        if (chunks > c->max_chunks)
-            throw InputError("partition spans overlap or exceed the row arena");
-        if (n_cat_words > c->cat_in_words)
-            throw InputError("too many category words for one partition call");
-        // Count groups: the requests whose split cells are on the device, then
-        // one group per streamed feature (its column goes up into a column
-        // window first). A group numbers its own chunks; counts land at each
-        // request's place in the call's chunk arrays.
-        std::vector<PartReqDev> grp;
-        std::vector<std::pair<uint32_t, uint32_t>> groups;  // (first, count) in grp
-        std::vector<uint32_t> group_feat;                  // UINT32_MAX: on the device
-        {
-            std::vector<uint32_t> order(pr.size());
-            for (uint32_t k = 0; k < pr.size(); k++) order[k] = k;
-            auto feat_of = [&](uint32_t k) { return reqs[which[k]].feat; };
-            auto key = [&](uint32_t k) -> uint64_t {
-                return pr[k].data ? 0 : 1 + (uint64_t)feat_of(k);
-            };
-            std::stable_sort(order.begin(), order.end(),
-                             [&](uint32_t a, uint32_t b) { return key(a) < key(b); });
-            uint32_t local = 0;
-            for (size_t j = 0; j < order.size(); j++) {
-                const uint32_t k = order[j];
-                if (j == 0 || key(k) != key(order[j - 1])) {
-                    groups.push_back({(uint32_t)grp.size(), 0});
-                    group_feat.push_back(pr[k].data ? UINT32_MAX : feat_of(k));
-                    local = 0;
-                }
-                PartReqDev g = pr[k];
-                g.chunk_begin = local;
-                local += g.n_chunks;
-                grp.push_back(g);
-                groups.back().second++;
-            }
-        }
-        // Streamed groups alternate between the two column windows.
-        std::vector<int> group_win(groups.size(), -1);
-        for (size_t gi = 0; gi < groups.size(); gi++) {
-            if (group_feat[gi] == UINT32_MAX) continue;
-            group_win[gi] = (int)(c->col_flip++ & 1);
-            for (uint32_t k = groups[gi].first; k < groups[gi].first + groups[gi].second; k++)
-                grp[k].data = c->win_col[group_win[gi]];
-        }
-        uint8_t *st = static_cast<uint8_t *>(c->pin_small.p);
-        // Requests, category words and count groups: one copy into the device staging.
-        const size_t bp = sizeof(PartReqDev) * pr.size();
-        const size_t off = (bp + 255) & ~size_t(255);
-        const size_t off_g = off + ((8 * (size_t)n_cat_words + 255) & ~size_t(255));
-        std::memcpy(st, pr.data(), bp);
-        if (n_cat_words) std::memcpy(st + off, cat_words, 8 * (size_t)n_cat_words);
-        std::memcpy(st + off_g, grp.data(), sizeof(PartReqDev) * grp.size());
-        check(hipMemcpyAsync(c->d_stage, st, off_g + sizeof(PartReqDev) * grp.size(),
-                             hipMemcpyHostToDevice, c->stream),
-              "tables");
-        const uint64_t *d_cats = reinterpret_cast<const uint64_t *>(c->d_stage + off);
-        PartReqDev *d_grp = reinterpret_cast<PartReqDev *>(c->d_stage + off_g);
-        for (size_t gi = 0; gi < groups.size(); gi++) {
-            const uint32_t first = groups[gi].first, cnt = groups[gi].second;
-            uint32_t g_chunks = 0;
-            for (uint32_t k = first; k < first + cnt; k++) g_chunks += grp[k].n_chunks;
-            if (group_feat[gi] != UINT32_MAX) {
-                // A streamed feature: its column goes up into the group's window.
-                const uint32_t f = group_feat[gi];
-                const int b = group_win[gi];
-                const uint64_t bytes = c->n_rows * c->width[f];
-                check(hipStreamWaitEvent(c->copy_stream, c->win_free[2 + b], 0), "stream wait");
-                check(hipMemcpyAsync(c->win_col[b], c->host_cols[f], bytes, hipMemcpyHostToDevice,
-                                     c->copy_stream),
-                      "column window upload");
-                check(hipEventRecord(c->win_ready[2 + b], c->copy_stream), "event");
-                c->streamed_bytes += bytes;
-                check(hipStreamWaitEvent(c->stream, c->win_ready[2 + b], 0), "stream wait");
-                check(launch_partition_count(d_grp + first, cnt, g_chunks, c->rows, c->flags,
-                                             c->d_counts, d_cats, c->stream),
-                      "partition count");
-                check(hipEventRecord(c->win_free[2 + b], c->stream), "event");
-            } else {
-                check(launch_partition_count(d_grp + first, cnt, g_chunks, c->rows, c->flags,
-                                             c->d_counts, d_cats, c->stream),
-                      "partition count");
-            }
-        }
-        check(launch_partition_finish(reinterpret_cast<const PartReqDev *>(c->d_stage),
-                                      (uint32_t)pr.size(), chunks, c->rows, c->tmp, c->flags,
-                                      c->d_counts, c->d_excl, c->d_totals, c->stream),
-              "partition");
-        check(hipMemcpyAsync(c->pin_out.p, c->d_totals, 4 * pr.size(), hipMemcpyDeviceToHost,
+        if (P.pr.empty()) return;
+        S.send();
+        enqueue_partition(c, P, S);
+        check(hipMemcpyAsync(c->pin_out.p, c->d_totals, 4 * P.pr.size(), hipMemcpyDeviceToHost,
                              c->stream),
               "partition totals");
         c->sync();
         const uint32_t *tot = static_cast<const uint32_t *>(c->pin_out.p);
-        for (size_t k = 0; k < pr.size(); k++) {
-            const uint32_t i = which[k];
+        for (size_t k = 0; k < P.pr.size(); k++) {
+            const uint32_t i = P.which[k];
             const uint32_t nl = tot[k];
             children[2 * i] = {reqs[i].rows.offset, nl};
             children[2 * i + 1] = {reqs[i].rows.offset + nl, reqs[i].rows.len - nl};
         }
+    });
+}
+
+int fbh_partition_eval(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
+                       const uint64_t *cat_words, uint32_t n_cat_words,
+                       const fbh_child_pair *pairs, const fbh_split_params *sp,
+                       fbh_span *children, uint32_t *left_slot, fbh_split *out,
+                       uint64_t *cat_out, uint32_t cat_capacity) {
+    return guard([&] {
+        if (!c || (n && (!reqs || !pairs || !children || !left_slot)) || !sp)
+            throw InputError("null argument");
+        ensure_tree(c);
+        if (n == 0) return;
+        if (n > MAX_NODES) throw InputError("too many partition requests");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        // Every slot of the evaluated pairs is used once: the larger child
+        // takes over the parent's slot, the smaller one accumulates into its own.
+        std::vector<uint8_t> used(c->n_slots, 0);
+        uint32_t n_eval = 0;
+        for (uint32_t i = 0; i < n; i++) {
+            if (!pairs[i].evaluate) continue;
+            const uint32_t a = pairs[i].parent_slot, b = pairs[i].new_slot;
+            if (a >= c->n_slots || b >= c->n_slots) throw InputError("histogram slot out of range");
+            if (a == b || used[a] || used[b])
+                throw InputError("each slot of the evaluated pairs must be used once");
+            used[a] = used[b] = 1;
+            n_eval++;
+        }
+        if (n_eval && !out) throw InputError("null argument");
+        Stager S{c};
+        const PartStage P = stage_partition(c, reqs, n, cat_words, n_cat_words, S);
+        std::vector<PairDev> pd(n);
+        std::vector<uint32_t> triples;
+        const ChunkRule rule = c->chunk_rule();
+        uint64_t bound_rule = (uint64_t)std::max<uint32_t>(rule.want_chunks, 256) + n_eval;
+        uint64_t bound_min = 0;  // the smaller child holds at most half its parent's rows
+        uint32_t e = 0;
+        for (uint32_t i = 0; i < n; i++) {
+            const fbh_child_pair &q = pairs[i];
+            PairDev &d = pd[i];
+            d.req = P.req_of[i];
+            d.row_off = reqs[i].rows.offset;
+            d.row_len = d.req == NO_SLOT ? 0 : reqs[i].rows.len;
+            d.parent_slot = q.parent_slot;
+            d.new_slot = q.new_slot;
+            d.eval_index = q.evaluate ? e++ : NO_SLOT;
+            for (int k = 0; k < 2; k++) {
+                d.lower[k] = q.lower[k];
+                d.upper[k] = q.upper[k];
+                d.left_sum[k] = q.left_sum[k];
+                d.right_sum[k] = q.right_sum[k];
+            }
+            if (!q.evaluate) continue;
+            triples.push_back(q.parent_slot);
+            triples.push_back(q.parent_slot);
+            triples.push_back(q.new_slot);
+            bound_min += div_up(d.row_len / 2, rule.fixed ? rule.fixed : rule.min_rows);
+        }
+        const size_t o_pairs = S.put(pd.data(), sizeof(PairDev) * n);
+        const size_t o_tri = S.put(triples.data(), 4 * triples.size());
+        S.send();
+        if (!P.pr.empty()) enqueue_partition(c, P, S);
+        check(launch_level_plan(S.dev<const PairDev>(o_pairs), n, c->d_totals, rule,
+                                c->d_lvl_hist, c->d_lvl_split, c->d_lvl_out,
+                                c->d_lvl_out + 4 * (size_t)n, c->d_lvl_rows, c->stream),
+              "level plan");
+        if (n_eval) {
+            EvalPlan E;
+            E.hn = c->d_lvl_hist;
+            E.n_hn = n_eval;
+            E.grid_chunks = (uint32_t)(rule.fixed ? bound_min : std::min(bound_rule, bound_min));
+            E.dev_chunk_rows = c->d_lvl_rows;
+            E.triples = S.dev<const uint32_t>(o_tri);
+            E.n_tri = n_eval;
+            E.sn = c->d_lvl_split;
+            E.n_nodes = 2 * n_eval;
+            enqueue_eval(c, E, sp);
+        }
+        uint8_t *po = static_cast<uint8_t *>(c->pin_out.p);
+        check(hipMemcpyAsync(po + c->pin_out_spans, c->d_lvl_out, 20 * (size_t)n,
+                             hipMemcpyDeviceToHost, c->stream),
+              "children download");
+        c->sync();
+        if (c->timing) c->collect_timing();
+        const uint32_t *sp4 = reinterpret_cast<const uint32_t *>(po + c->pin_out_spans);
+        uint64_t acc = 0, with_rows = 0;
+        for (uint32_t i = 0; i < n; i++) {
+            children[2 * i] = {sp4[4 * i], sp4[4 * i + 1]};
+            children[2 * i + 1] = {sp4[4 * i + 2], sp4[4 * i + 3]};
+            left_slot[i] = sp4[4 * (size_t)n + i];
+            if (pairs[i].evaluate) {
+                const uint32_t small = std::min(sp4[4 * i + 1], sp4[4 * i + 3]);
+                acc += small;
+                with_rows += small ? 1 : 0;
+            }
+        }
+        account_hist(c, acc, with_rows);
+        if (n_eval) unpack_packets(c, 2 * n_eval, out, cat_out, cat_capacity);
     });
 }
 

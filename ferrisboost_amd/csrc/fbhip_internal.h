@@ -53,8 +53,11 @@ struct HistLaunch {
     uint32_t n_tiles;
     const HistNodeDev *nodes;
     uint32_t n_nodes;
-    uint32_t n_chunks;
+    uint32_t n_chunks;         // chunks of the grid (a node may use fewer)
     uint32_t chunk_rows;
+    // Non-null: the launch was planned on the device and the rows per chunk
+    // are read from here (chunk_rows is then unused).
+    const uint32_t *dev_chunk_rows;
     uint32_t chunk_groups;     // ceil(n_chunks / XCDS)
     const uint32_t *rows;      // row arena
     const int64_t *gpair;      // [n_rows][2]
@@ -122,6 +125,25 @@ struct PartReqDev {
     uint32_t count_base;   // index of the request's first chunk in the chunk arrays
 };
 
+// One split node of a fused partition + evaluation step: its children's
+// spans come from the partition; the smaller child is accumulated into
+// new_slot and the larger derived in place from parent_slot.
+struct PairDev {
+    uint32_t req;          // index of the node's partition request, NO_SLOT when it has no rows
+    uint32_t row_off, row_len;
+    uint32_t parent_slot, new_slot;
+    uint32_t eval_index;   // position among evaluated pairs, NO_SLOT when not evaluated
+    float lower[2], upper[2];  // bounds of the left and right child
+    int64_t left_sum[2], right_sum[2];
+};
+
+// Rows per chunk of a device-planned histogram launch: fixed when nonzero,
+// else ceil(rows / want_chunks) rounded up to 1024 and clamped to
+// [min_rows, max_rows].
+struct ChunkRule {
+    uint32_t fixed, want_chunks, min_rows, max_rows;
+};
+
 struct LeafDev {
     uint32_t row_off, row_len, chunk_begin;
     float value;
@@ -155,6 +177,18 @@ hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slot
                              hipStream_t s);
 hipError_t launch_subtract(int64_t *hist, uint64_t width, const uint32_t *triples, uint32_t n,
                            hipStream_t s);
+// Zero the slots of accumulated nodes that need it: all when force, else
+// those not written by plain stores (n_chunks != 1).
+hipError_t launch_zero_nodes(int64_t *hist, uint64_t width, const HistNodeDev *nodes, uint32_t n,
+                             bool force, hipStream_t s);
+// Device plan of a fused step: children spans (2 per pair) and the left
+// child's slot per pair, the accumulated nodes (one per evaluated pair, in
+// pair order), the split-scan nodes (left, right per evaluated pair) and
+// the rows per chunk.
+hipError_t launch_level_plan(const PairDev *pairs, uint32_t n_pairs, const uint32_t *totals,
+                             ChunkRule rule, HistNodeDev *hist_nodes, SplitNodeDev *split_nodes,
+                             uint32_t *spans, uint32_t *left_slot, uint32_t *chunk_rows,
+                             hipStream_t s);
 hipError_t launch_split_feats(const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
                               uint32_t n_nodes, const SplitFeatDev *feats, const uint8_t *enabled,
                               SplitParamsDev P, FeatCandDev *cands, uint64_t *cat_scratch,

@@ -102,8 +102,12 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
         else hi = mid;
     }
     const HistNodeDev N = L.nodes[lo];
-    uint32_t r0 = (chunk - N.chunk_begin) * L.chunk_rows;
-    uint32_t r1 = min(r0 + L.chunk_rows, N.row_len);
+    // A device-planned grid is an upper bound: chunks past the last node's
+    // end have no rows.
+    if (chunk - N.chunk_begin >= N.n_chunks) return;
+    const uint32_t chunk_rows = L.dev_chunk_rows ? *L.dev_chunk_rows : L.chunk_rows;
+    uint32_t r0 = (chunk - N.chunk_begin) * chunk_rows;
+    uint32_t r1 = min(r0 + chunk_rows, N.row_len);
     if (STREAM) {
         // A node's row ids ascend (stable partitions of 0..n), so the rows of
         // the window are one sub-range of the chunk: two lower bounds.
@@ -237,8 +241,10 @@ __global__ __launch_bounds__(HIST_TPB) void hist_global_kernel(const HistLaunch 
         else hi = mid;
     }
     const HistNodeDev N = L.nodes[lo];
-    const uint32_t r0 = (chunk - N.chunk_begin) * L.chunk_rows;
-    const uint32_t r1 = min(r0 + L.chunk_rows, N.row_len);
+    if (chunk - N.chunk_begin >= N.n_chunks) return;
+    const uint32_t chunk_rows = L.dev_chunk_rows ? *L.dev_chunk_rows : L.chunk_rows;
+    const uint32_t r0 = (chunk - N.chunk_begin) * chunk_rows;
+    const uint32_t r1 = min(r0 + chunk_rows, N.row_len);
     unsigned long long *out = reinterpret_cast<unsigned long long *>(
         L.hist + ((uint64_t)N.slot * L.hist_width + F.hist_off) * 2u);
     const uint32_t *rows = L.rows + N.row_off;
@@ -347,6 +353,140 @@ hipError_t launch_subtract(int64_t *hist, uint64_t width, const uint32_t *triple
     if (n == 0) return hipSuccess;
     uint32_t bx = (uint32_t)std::min<uint64_t>((width * 2 + 255) / 256, 1024);
     hipLaunchKernelGGL(subtract_kernel, dim3(bx, n), dim3(256), 0, s, hist, width, triples);
+    return hipGetLastError();
+}
+
+__global__ void zero_nodes_kernel(int64_t *hist, uint64_t width, const HistNodeDev *nodes,
+                                  bool force) {
+    const HistNodeDev N = nodes[blockIdx.y];
+    if (!force && N.n_chunks == 1) return;  // written by plain stores
+    int64_t *base = hist + (uint64_t)N.slot * width * 2u;
+    const uint64_t n = width * 2u;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        base[i] = 0;
+}
+
+hipError_t launch_zero_nodes(int64_t *hist, uint64_t width, const HistNodeDev *nodes, uint32_t n,
+                             bool force, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    uint32_t bx = (uint32_t)std::min<uint64_t>((width * 2 + 255) / 256, 1024);
+    hipLaunchKernelGGL(zero_nodes_kernel, dim3(bx, n), dim3(256), 0, s, hist, width, nodes, force);
+    return hipGetLastError();
+}
+
+// Exclusive scan of v over the 1024 threads of the block (carry added by the
+// caller); returns this thread's prefix and sets total.
+__device__ uint32_t block_scan_1024(uint32_t v, uint32_t *buf, uint32_t &total) {
+    buf[threadIdx.x] = v;
+    __syncthreads();
+    for (uint32_t off = 1; off < 1024; off <<= 1) {
+        const uint32_t a = threadIdx.x >= off ? buf[threadIdx.x - off] : 0;
+        __syncthreads();
+        buf[threadIdx.x] += a;
+        __syncthreads();
+    }
+    const uint32_t incl = buf[threadIdx.x];
+    total = buf[1023];
+    __syncthreads();
+    return incl - v;
+}
+
+// One workgroup plans the children of a fused partition + evaluation step
+// from the partition's left counts (see launch_level_plan).
+__global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, uint32_t n,
+                                                          const uint32_t *totals, ChunkRule rule,
+                                                          HistNodeDev *hn, SplitNodeDev *sn,
+                                                          uint32_t *spans, uint32_t *left_slot,
+                                                          uint32_t *chunk_rows_out) {
+    __shared__ uint32_t buf[1024];
+    __shared__ unsigned long long acc_sh;
+    __shared__ uint32_t cr_sh;
+    if (threadIdx.x == 0) acc_sh = 0;
+    __syncthreads();
+    // Spans of every pair and the rows the evaluated pairs accumulate.
+    unsigned long long acc = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += 1024) {
+        const PairDev P = pairs[i];
+        const uint32_t nl = P.req == NO_SLOT ? 0u : totals[P.req];
+        const uint32_t nr = P.row_len - nl;
+        spans[4 * i + 0] = P.row_off;
+        spans[4 * i + 1] = nl;
+        spans[4 * i + 2] = P.row_off + nl;
+        spans[4 * i + 3] = nr;
+        if (P.eval_index != NO_SLOT) acc += min(nl, nr);
+    }
+    atomicAdd(&acc_sh, acc);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t r;
+        if (rule.fixed) {
+            r = rule.fixed;
+        } else {
+            r = (acc_sh + rule.want_chunks - 1) / rule.want_chunks;
+            r = (r + 1023) & ~uint64_t(1023);
+            r = r < rule.min_rows ? rule.min_rows : (r > rule.max_rows ? rule.max_rows : r);
+        }
+        cr_sh = (uint32_t)r;
+        *chunk_rows_out = (uint32_t)r;
+    }
+    __syncthreads();
+    const uint32_t cr = cr_sh;
+    uint32_t carry = 0;
+    for (uint32_t base = 0; base < n; base += 1024) {
+        const uint32_t i = base + threadIdx.x;
+        PairDev P{};
+        uint32_t nl = 0, nr = 0, nc = 0;
+        const bool ev = i < n && pairs[i].eval_index != NO_SLOT;
+        if (i < n) {
+            P = pairs[i];
+            nl = P.req == NO_SLOT ? 0u : totals[P.req];
+            nr = P.row_len - nl;
+            if (ev) nc = (min(nl, nr) + cr - 1) / cr;
+        }
+        uint32_t total;
+        const uint32_t before = carry + block_scan_1024(nc, buf, total);
+        if (i < n) {
+            // The smaller child (the left one on ties) is accumulated.
+            const bool left_small = nl <= nr;
+            if (ev) {
+                const uint32_t e = P.eval_index;
+                HistNodeDev h{};
+                h.row_off = left_small ? P.row_off : P.row_off + nl;
+                h.row_len = left_small ? nl : nr;
+                h.chunk_begin = before;
+                h.slot = P.new_slot;
+                h.n_chunks = nc;
+                hn[e] = h;
+                SplitNodeDev l{}, r{};
+                l.sum_g = P.left_sum[0];
+                l.sum_h = P.left_sum[1];
+                l.lower = P.lower[0];
+                l.upper = P.upper[0];
+                l.slot = left_small ? P.new_slot : P.parent_slot;
+                r.sum_g = P.right_sum[0];
+                r.sum_h = P.right_sum[1];
+                r.lower = P.lower[1];
+                r.upper = P.upper[1];
+                r.slot = left_small ? P.parent_slot : P.new_slot;
+                sn[2 * e] = l;
+                sn[2 * e + 1] = r;
+                left_slot[i] = l.slot;
+            } else {
+                left_slot[i] = NO_SLOT;
+            }
+        }
+        carry += total;
+    }
+}
+
+hipError_t launch_level_plan(const PairDev *pairs, uint32_t n_pairs, const uint32_t *totals,
+                             ChunkRule rule, HistNodeDev *hist_nodes, SplitNodeDev *split_nodes,
+                             uint32_t *spans, uint32_t *left_slot, uint32_t *chunk_rows,
+                             hipStream_t s) {
+    if (n_pairs == 0) return hipSuccess;
+    hipLaunchKernelGGL(level_plan_kernel, dim3(1), dim3(1024), 0, s, pairs, n_pairs, totals, rule,
+                       hist_nodes, split_nodes, spans, left_slot, chunk_rows);
     return hipGetLastError();
 }
 

@@ -382,14 +382,64 @@ class Grower {
         return q;
     }
 
+    // One fused backend step: partition the split nodes and, when the
+    // children are evaluated, build and scan their histograms. pairs carries
+    // each node's slot, a new slot for one child, the children's bounds and
+    // sums; on return next[2k], next[2k+1] hold the children's rows and
+    // slots and the packets are (left, right) per pair.
+    std::vector<fbh_split> step(const std::vector<fbh_part_req> &reqs,
+                                const std::vector<fbh_child_pair> &pairs,
+                                const std::vector<uint64_t> &cats, std::vector<Pending> &next) {
+        const size_t n = reqs.size();
+        std::vector<fbh_span> children(2 * n);
+        std::vector<uint32_t> left_slot(n);
+        std::vector<fbh_split> packets(2 * n);
+        cat_words_.assign((size_t)std::max<uint32_t>(1, cat_cap_) * 2 * n, 0);
+        call(fbh_partition_eval(ctx_, reqs.data(), (uint32_t)n, cats.data(), (uint32_t)cats.size(),
+                                pairs.data(), &sp_, children.data(), left_slot.data(),
+                                packets.data(), cat_words_.data(), (uint32_t)cat_words_.size()));
+        for (size_t k = 0; k < n; k++) {
+            next[2 * k].rows = children[2 * k];
+            next[2 * k + 1].rows = children[2 * k + 1];
+            next[2 * k].slot = left_slot[k];
+            next[2 * k + 1].slot =
+                left_slot[k] == pairs[k].parent_slot ? pairs[k].new_slot : pairs[k].parent_slot;
+        }
+        return packets;
+    }
+
+    fbh_child_pair pair_of(const Pending &nd, const fbh_split &s, const Bounds &lb,
+                           const Bounds &rb, bool evaluate) {
+        fbh_child_pair q{};
+        q.parent_slot = nd.slot;
+        q.new_slot = evaluate ? take_slot() : UINT32_MAX;
+        q.evaluate = evaluate ? 1u : 0u;
+        q.lower[0] = lb.lo;
+        q.lower[1] = rb.lo;
+        q.upper[0] = lb.hi;
+        q.upper[1] = rb.hi;
+        for (int k = 0; k < 2; k++) {
+            q.left_sum[k] = s.left[k];
+            q.right_sum[k] = s.right[k];
+        }
+        return q;
+    }
+
+    // Depthwise growth (build_tree, src/training/mod.rs:3357-4565): the root
+    // is evaluated alone, then each level is one fused step (partition of the
+    // split nodes, histograms and split scans of their children).
     void depthwise(Tree &t, fbh_span root_rows, const int64_t root_sum[2]) {
         std::vector<Pending> level(1);
         level[0] = {0, root_rows, {root_sum[0], root_sum[1]}, Bounds(), take_slot(), -1, -1, 0};
         uint32_t leaf_count = 1;
-        for (uint32_t depth = 0; depth < p_.max_depth; depth++) {
-            if (level.empty() || (p_.max_leaves != 0 && leaf_count >= p_.max_leaves)) break;
-            std::vector<fbh_split> chosen = eval(level);
-            const std::vector<uint64_t> cats = cat_words_;
+        if (p_.max_depth == 0 || (p_.max_leaves != 0 && leaf_count >= p_.max_leaves)) {
+            finish_leaf(t, 0, root_rows);
+            give_slot(level[0].slot);
+            return;
+        }
+        std::vector<fbh_split> chosen = eval(level);
+        std::vector<uint64_t> cats = cat_words_;
+        for (uint32_t depth = 0;; depth++) {
             if (p_.max_leaves != 0) {
                 uint32_t remaining = p_.max_leaves > leaf_count ? p_.max_leaves - leaf_count : 0;
                 for (auto &c : chosen)
@@ -398,69 +448,57 @@ class Grower {
                         else remaining--;
                     }
             }
-            std::vector<fbh_part_req> reqs;
-            std::vector<uint32_t> req_of(level.size(), UINT32_MAX);
-            for (size_t i = 0; i < level.size(); i++)
-                if (chosen[i].found) {
-                    req_of[i] = (uint32_t)reqs.size();
-                    reqs.push_back(part_req(level[i], chosen[i], chosen[i].cat_offset));
-                }
-            std::vector<fbh_span> children(2 * reqs.size());
-            if (!reqs.empty())
-                call(fbh_partition(ctx_, reqs.data(), (uint32_t)reqs.size(), cats.data(),
-                                   (uint32_t)cats.size(), children.data()));
-            std::vector<Pending> next;
+            // Nodes without a split become leaves and hand back their slots
+            // before the children take new ones.
+            std::vector<uint32_t> split_idx;
             for (size_t i = 0; i < level.size(); i++) {
-                const Pending &ln = level[i];
-                if (!chosen[i].found) {
-                    finish_leaf(t, ln.node, ln.rows);
-                    give_slot(ln.slot);
-                    continue;
+                if (chosen[i].found) {
+                    split_idx.push_back((uint32_t)i);
+                    leaf_count++;
+                } else {
+                    finish_leaf(t, level[i].node, level[i].rows);
+                    give_slot(level[i].slot);
                 }
-                leaf_count++;
+            }
+            if (split_idx.empty()) return;
+            const bool evaluated = depth + 1 < p_.max_depth &&
+                                   !(p_.max_leaves != 0 && leaf_count >= p_.max_leaves);
+            std::vector<fbh_part_req> reqs;
+            std::vector<fbh_child_pair> pairs;
+            std::vector<Pending> next;
+            for (uint32_t i : split_idx) {
+                const Pending &ln = level[i];
                 uint32_t l, r;
                 Bounds lb, rb;
                 apply(t, ln.node, chosen[i], cats.data() + chosen[i].cat_offset, ln.b, l, r, lb,
                       rb);
-                const fbh_span ls = children[2 * req_of[i]], rs = children[2 * req_of[i] + 1];
-                Pending L{l, ls, {chosen[i].left[0], chosen[i].left[1]}, lb, 0, -1, -1, depth + 1};
-                Pending R{r, rs, {chosen[i].right[0], chosen[i].right[1]}, rb, 0, -1, -1,
-                          depth + 1};
-                // The smaller child is accumulated; the other takes over the
-                // parent's histogram slot: parent - sibling, in place.
-                const bool left_small = ls.len <= rs.len;
-                Pending &small = left_small ? L : R;
-                Pending &big = left_small ? R : L;
-                const uint32_t at = (uint32_t)next.size();
-                big.slot = ln.slot;
-                big.parent_slot = (int32_t)ln.slot;
-                big.sibling = (int32_t)(at + (left_small ? 0 : 1));
-                small.slot = UINT32_MAX;  // assigned below, after freed slots return
-                next.push_back(L);
-                next.push_back(R);
+                reqs.push_back(part_req(ln, chosen[i], chosen[i].cat_offset));
+                pairs.push_back(pair_of(ln, chosen[i], lb, rb, evaluated));
+                next.push_back(
+                    {l, {}, {chosen[i].left[0], chosen[i].left[1]}, lb, 0, -1, -1, depth + 1});
+                next.push_back(
+                    {r, {}, {chosen[i].right[0], chosen[i].right[1]}, rb, 0, -1, -1, depth + 1});
             }
-            // Children that will be evaluated need a slot for the smaller one.
-            const bool evaluated = depth + 1 < p_.max_depth &&
-                                   !(p_.max_leaves != 0 && leaf_count >= p_.max_leaves);
-            for (auto &nd : next) {
-                if (nd.slot != UINT32_MAX) continue;
-                if (evaluated) nd.slot = take_slot();
-            }
-            if (!evaluated) {
-                for (auto &nd : next) {
-                    finish_leaf(t, nd.node, nd.rows);
-                    if (nd.parent_slot >= 0) give_slot(nd.slot);
+            if (!evaluated) {  // the children are leaves
+                std::vector<fbh_span> children(2 * reqs.size());
+                call(fbh_partition(ctx_, reqs.data(), (uint32_t)reqs.size(), cats.data(),
+                                   (uint32_t)cats.size(), children.data()));
+                for (size_t k = 0; k < reqs.size(); k++) {
+                    finish_leaf(t, next[2 * k].node, children[2 * k]);
+                    finish_leaf(t, next[2 * k + 1].node, children[2 * k + 1]);
+                    give_slot(pairs[k].parent_slot);
                 }
                 return;
             }
+            chosen = step(reqs, pairs, cats, next);
+            cats = cat_words_;
             level = std::move(next);
-        }
-        for (auto &nd : level) {
-            finish_leaf(t, nd.node, nd.rows);
-            give_slot(nd.slot);
         }
     }
 
+    // Lossguide growth (src/training/lossguide.rs): best-first expansion from
+    // a priority queue by gain (ties: the lower node id); each expansion is
+    // one fused step.
     void lossguide(Tree &t, fbh_span root_rows, const int64_t root_sum[2]) {
         struct Cand {
             Pending leaf;
@@ -472,14 +510,15 @@ class Grower {
             return a.leaf.node > b.leaf.node;
         };
         std::priority_queue<Cand, std::vector<Cand>, decltype(less)> heap(less);
-        auto evaluate = [&](std::vector<Pending> batch) {
-            std::vector<fbh_split> res = eval(batch);
+        // Candidates or leaves from evaluated nodes (packets in batch order).
+        auto take = [&](const std::vector<Pending> &batch, const std::vector<fbh_split> &res,
+                        const std::vector<uint64_t> &words) {
             for (size_t i = 0; i < batch.size(); i++) {
                 if (res[i].found) {
                     Cand c{batch[i], res[i], {}};
                     if (res[i].is_cat)
-                        c.cats.assign(cat_words_.begin() + res[i].cat_offset,
-                                      cat_words_.begin() + res[i].cat_offset + res[i].n_cat_words);
+                        c.cats.assign(words.begin() + res[i].cat_offset,
+                                      words.begin() + res[i].cat_offset + res[i].n_cat_words);
                     c.leaf.parent_slot = -1;
                     c.leaf.sibling = -1;
                     heap.push(std::move(c));
@@ -494,39 +533,40 @@ class Grower {
             finish_leaf(t, 0, root_rows);
         } else {
             root.slot = take_slot();
-            evaluate({root});
+            const std::vector<Pending> batch{root};
+            take(batch, eval(batch), cat_words_);
         }
         uint32_t leaf_count = 1;
         while (p_.max_leaves == 0 || leaf_count < p_.max_leaves) {
             if (heap.empty()) break;
             Cand c = heap.top();
             heap.pop();
-            fbh_part_req q = part_req(c.leaf, c.split, 0);
-            fbh_span ch[2];
-            call(fbh_partition(ctx_, &q, 1, c.cats.data(), (uint32_t)c.cats.size(), ch));
             uint32_t l, r;
             Bounds lb, rb;
             apply(t, c.leaf.node, c.split, c.cats.data(), c.leaf.b, l, r, lb, rb);
             leaf_count++;
             const uint32_t depth = c.leaf.depth + 1;
-            Pending L{l, ch[0], {c.split.left[0], c.split.left[1]}, lb, 0, -1, -1, depth};
-            Pending R{r, ch[1], {c.split.right[0], c.split.right[1]}, rb, 0, -1, -1, depth};
+            const std::vector<fbh_part_req> reqs{part_req(c.leaf, c.split, 0)};
+            std::vector<Pending> next{
+                {l, {}, {c.split.left[0], c.split.left[1]}, lb, 0, -1, -1, depth},
+                {r, {}, {c.split.right[0], c.split.right[1]}, rb, 0, -1, -1, depth}};
             if (depth == p_.max_depth || leaf_count == p_.max_leaves) {
+                fbh_span ch[2];
+                call(fbh_partition(ctx_, reqs.data(), 1, c.cats.data(), (uint32_t)c.cats.size(),
+                                   ch));
                 finish_leaf(t, l, ch[0]);
                 finish_leaf(t, r, ch[1]);
                 give_slot(c.leaf.slot);
                 continue;
             }
-            // lossguide.rs evaluate: the smaller child (left on ties) is
-            // accumulated, the other derived from the parent's histogram.
-            const bool left_small = !(ch[0].len > ch[1].len);
-            Pending &small = left_small ? L : R;
-            Pending &big = left_small ? R : L;
-            big.slot = c.leaf.slot;
-            big.parent_slot = (int32_t)c.leaf.slot;
-            big.sibling = 0;
-            small.slot = take_slot();
-            evaluate({small, big});
+            const std::vector<fbh_child_pair> pairs{pair_of(c.leaf, c.split, lb, rb, true)};
+            const std::vector<fbh_split> res = step(reqs, pairs, c.cats, next);
+            // lossguide.rs evaluate: the smaller child (left on ties) first.
+            const bool left_small = !(next[0].rows.len > next[1].rows.len);
+            if (left_small)
+                take(next, res, cat_words_);
+            else
+                take({next[1], next[0]}, {res[1], res[0]}, cat_words_);
         }
         while (!heap.empty()) {
             finish_leaf(t, heap.top().leaf.node, heap.top().leaf.rows);

@@ -276,6 +276,38 @@ int fbh_download_histogram(fbh_ctx *ctx, uint32_t slot, int64_t *out, uint64_t *
 int fbh_partition(fbh_ctx *ctx, const fbh_part_req *reqs, uint32_t n_reqs,
                   const uint64_t *cat_words, uint32_t n_cat_words, fbh_span *children);
 
+/* One split node of fbh_partition_eval. */
+typedef struct fbh_child_pair {
+    uint32_t parent_slot; /* histogram slot of the split node */
+    uint32_t new_slot;    /* a free slot for one child */
+    uint32_t evaluate;    /* nonzero: build and scan both children */
+    uint32_t reserved;
+    float lower[2];       /* monotone bounds of the left and right child */
+    float upper[2];
+    int64_t left_sum[2];  /* fixed-point sums of the children (the split's left, right) */
+    int64_t right_sum[2];
+} fbh_child_pair;
+
+/* One growth step with one host round trip: fbh_partition of the split
+ * nodes, then fbh_eval_nodes of the children of every pair marked
+ * `evaluate`, planned on the device from the partition's left counts.
+ * Replaces partition_resident_multi + resolve_partitions +
+ * finish_partition_level followed by histogram_device_batch +
+ * split_cached_submit/finish of the children (train_ctx.rs:4893, 2007, 2058,
+ * 4543; split_ctx.rs:387-960), as one depthwise level or one lossguide
+ * expansion (lossguide.rs:73, 416-463) drives them. Of an evaluated pair the
+ * smaller child (the left one on ties) accumulates into new_slot and the
+ * larger one is derived in place from parent_slot; left_slot[i] receives the
+ * slot the left child holds (UINT32_MAX when not evaluated). children gets
+ * (left, right) per request; out gets (left, right) packets per evaluated
+ * pair, in order, with their category sets in cat_out. Every slot of the
+ * evaluated pairs must be used once. */
+int fbh_partition_eval(fbh_ctx *ctx, const fbh_part_req *reqs, uint32_t n_reqs,
+                       const uint64_t *cat_words, uint32_t n_cat_words,
+                       const fbh_child_pair *pairs, const fbh_split_params *params,
+                       fbh_span *children, uint32_t *left_slot, fbh_split *out,
+                       uint64_t *cat_out, uint32_t cat_capacity);
+
 /* GpuTrainCtx::assign_leaf_values (src/backend/cuda/train_ctx.rs:2128-2252):
  * delta[row] = value for every row of each span. */
 int fbh_assign_leaves(fbh_ctx *ctx, const fbh_span *spans, const float *values, uint32_t n);
