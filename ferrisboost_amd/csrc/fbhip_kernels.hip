@@ -626,7 +626,8 @@ __device__ __forceinline__ int64_t wsub(int64_t a, int64_t b) {
 __device__ void split_categorical(const int64_t *h, uint32_t n, const SplitNodeDev &N,
                                   float parent, int mono, const SplitParamsDev &P, Best *shb,
                                   int64_t *sg, int64_t *shh, float *wts, uint32_t *order,
-                                  uint64_t *set_out, uint32_t set_words, FeatCandDev *outc) {
+                                  unsigned long long *set_lds, uint64_t *set_out,
+                                  uint32_t set_words, FeatCandDev *outc) {
     const uint32_t tid = threadIdx.x;
     int64_t tg = 0, th = 0;
     for (uint32_t i = tid; i < n; i += SPLIT_TPB) {
@@ -682,44 +683,59 @@ __device__ void split_categorical(const int64_t *h, uint32_t n, const SplitNodeD
         }
         __syncthreads();
         const uint32_t n_scan = min(P.max_cat_threshold, n);
-        if (tid == 0 && n_scan >= 2) {
-            Best fwd{0.0f, 0u, 0u, 0, 0}, bwd{0.0f, 0u, 0u, 0, 0};
-            int64_t rg = 0, rh = 0;
-            for (uint32_t kk = 0; kk + 1 < n_scan; kk++) {
-                rg = wadd(rg, h[2 * order[kk]]);
-                rh = wadd(rh, h[2 * order[kk] + 1]);
-                float gain;
-                const int64_t lg = wsub(N.sum_g, rg), lh = wsub(N.sum_h, rh);
-                if (candidate_gain(lg, lh, rg, rh, parent, mono, N.lower, N.upper, P, gain))
-                    if (gain > MIN_GAIN_EPS && (!fwd.found || gain > fwd.gain))
-                        fwd = Best{gain, kk + 1, 1u, lg, lh};
-            }
-            int64_t lg = 0, lh = 0;
-            for (uint32_t j = n; j-- > n - (n_scan - 1);) {
-                lg = wadd(lg, h[2 * order[j]]);
-                lh = wadd(lh, h[2 * order[j] + 1]);
-                float gain;
-                const int64_t rg2 = wsub(N.sum_g, lg), rh2 = wsub(N.sum_h, lh);
-                if (candidate_gain(lg, lh, rg2, rh2, parent, mono, N.lower, N.upper, P, gain))
-                    if (gain > MIN_GAIN_EPS && (!bwd.found || gain > bwd.gain))
-                        bwd = Best{gain, j, 1u, lg, lh};
-            }
-            Best win = fwd;
-            uint32_t win_ml = 1;
-            if (bwd.found && (!win.found || bwd.gain > win.gain)) {
-                win = bwd;
-                win_ml = 0;
-            }
-            shb[0] = win;
-            sg[0] = win_ml;
+        // Prefix sums of the categories in sorted order, each thread a run of
+        // them; then every prefix is a candidate in parallel. Forward: the
+        // first k+1 categories go right (missing left), ties to the shorter
+        // prefix. Backward: categories k..n-1 go left (missing right), ties
+        // to the larger k. Integer sums wrap, so T - prefix equals the
+        // reference's running suffix exactly.
+        const uint32_t per = (n + SPLIT_TPB - 1) / SPLIT_TPB;
+        const uint32_t k0 = min(tid * per, n), k1 = min(k0 + per, n);
+        int64_t sg_loc = 0, sh_loc = 0;
+        for (uint32_t k = k0; k < k1; k++) {
+            sg_loc = wadd(sg_loc, h[2 * order[k]]);
+            sh_loc = wadd(sh_loc, h[2 * order[k] + 1]);
         }
+        int64_t exg, exh, allg, allh;
+        block_scan_pairs(sg_loc, sh_loc, sg, shh, exg, exh, allg, allh);
+        Best fwd{0.0f, 0u, 0u, 0, 0}, bwd{0.0f, 0u, 0u, 0, 0};
+        if (n_scan >= 2) {
+            int64_t cg = exg, ch = exh;  // sum of the categories before k
+            for (uint32_t k = k0; k < k1; k++) {
+                float gain;
+                if (k >= n - (n_scan - 1)) {
+                    const int64_t lg = wsub(allg, cg), lh = wsub(allh, ch);
+                    const int64_t rg = wsub(N.sum_g, lg), rh = wsub(N.sum_h, lh);
+                    if (candidate_gain(lg, lh, rg, rh, parent, mono, N.lower, N.upper, P, gain))
+                        offer(bwd, gain, n - 1 - k, lg, lh);
+                }
+                cg = wadd(cg, h[2 * order[k]]);
+                ch = wadd(ch, h[2 * order[k] + 1]);
+                if (k + 1 < n_scan) {
+                    const int64_t lg = wsub(N.sum_g, cg), lh = wsub(N.sum_h, ch);
+                    if (candidate_gain(lg, lh, cg, ch, parent, mono, N.lower, N.upper, P, gain))
+                        offer(fwd, gain, k + 1, lg, lh);
+                }
+            }
+        }
+        fwd = block_best(fwd, shb);
+        bwd = block_best(bwd, shb);
+        best = fwd;
+        ml = 1;
+        at = fwd.ord;
+        if (bwd.found && (!fwd.found || bwd.gain > fwd.gain)) {
+            best = bwd;
+            ml = 0;
+            at = n - 1 - bwd.ord;
+        }
+        // The right-going set: the first `at` categories in sorted order.
+        for (uint32_t w = tid; w < set_words; w += SPLIT_TPB) set_lds[w] = 0ull;
         __syncthreads();
-        best = shb[0];
-        ml = (uint32_t)sg[0];
-        at = best.ord;
+        if (best.found)
+            for (uint32_t kk = tid; kk < at; kk += SPLIT_TPB)
+                atomicOr(&set_lds[order[kk] >> 6], 1ull << (order[kk] & 63));
         __syncthreads();
-        if (best.found && tid == 0)
-            for (uint32_t kk = 0; kk < at; kk++) set_out[order[kk] >> 6] |= 1ull << (order[kk] & 63);
+        for (uint32_t w = tid; w < set_words; w += SPLIT_TPB) set_out[w] = set_lds[w];
     }
     if (tid == 0) {
         outc->found = best.found;
@@ -760,7 +776,8 @@ __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
         float *wts = reinterpret_cast<float *>(dyn);
         uint32_t *order = reinterpret_cast<uint32_t *>(dyn + sizeof(float) * MAX_DEVICE_CATS);
         uint64_t *set = cat_scratch + (size_t)ni * P.cat_words_per_node + F.cat_base;
-        split_categorical(h, n, N, parent, F.monotone, P, shb, sg, shh, wts, order, set,
+        __shared__ unsigned long long set_lds[MAX_DEVICE_CATS / 64];
+        split_categorical(h, n, N, parent, F.monotone, P, shb, sg, shh, wts, order, set_lds, set,
                           F.cat_words, outc);
         return;
     }

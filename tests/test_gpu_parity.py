@@ -270,6 +270,33 @@ def test_depthwise_categorical_partition_path(fb, oracle):
     assert_same_models(om, pm)
 
 
+@pytest.mark.parametrize("threshold", [2, 64, 1000])
+def test_categorical_scan_directions_and_ties(fb, oracle, threshold):
+    """Sorted-category prefix scans in both directions, up to every category
+    (max_cat_threshold above the category count), with categories of equal
+    weight: each category code repeats one of a few label patterns exactly,
+    so weights and candidate gains tie."""
+    rng = np.random.default_rng(71 + threshold)
+    n, n_codes = 24_000, 300
+    codes = rng.integers(0, n_codes, n)
+    X = np.zeros((n, 3), np.float32)
+    X[:, 0] = codes
+    X[:, 1] = rng.standard_normal(n)
+    X[:, 2] = rng.integers(0, 7, n)
+    # four groups of categories by code % 4, two of them label-pure
+    y = ((codes % 4 == 1) | ((codes % 4 == 2) & (X[:, 1] > 0))).astype(np.float32)
+    X[rng.random(n) < 0.05, 0] = np.nan
+    params = dict(objective="binary:logistic", max_depth=5, learning_rate=0.3, max_bin=512,
+                  grow_policy="lossguide", max_leaves=24, max_cat_to_onehot=4,
+                  max_cat_threshold=threshold, feature_types=["c", "q", "c"])
+    cat = [1, 0, 1]
+    op = {k: v for k, v in params.items() if k != "feature_types"}
+    om = oracle.train(X, y, oracle.make_params(n_rounds=4, **op), categorical=cat)
+    pm = fb.train(params, X, y, num_boost_round=4)
+    assert_same_models(om, pm)
+    assert np.array_equal(pm.train_margins(n), om.train_margins(n))
+
+
 def test_shap_matches_oracle_and_is_additive(fb, oracle):
     X, y, params, _ = _synthetic("plumbing", 8_000)
     X[::7, 3] = np.nan
