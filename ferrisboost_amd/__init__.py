@@ -74,6 +74,7 @@ _DEFAULTS: dict[str, Any] = {
     "hip_rows_per_block": 0,
     "hip_profile": False,
     "hip_host_sigmoid": False,
+    "hip_host_levels": False,
 }
 
 _ALIASES = {
@@ -190,6 +191,7 @@ def _params_struct(p: dict[str, Any], n_features: int) -> N.TrainParams:
     s.rows_per_block = int(p["hip_rows_per_block"])
     s.profile = 1 if p["hip_profile"] else 0
     s.host_sigmoid = 1 if p["hip_host_sigmoid"] else 0
+    s.host_levels = 1 if p["hip_host_levels"] else 0
     return s
 
 

@@ -152,7 +152,8 @@ class TrainParams(C.Structure):
         ("rows_per_block", C.c_uint32),
         ("profile", C.c_uint32),
         ("host_sigmoid", C.c_uint32),
-        ("reserved2", C.c_uint32 * 2),
+        ("host_levels", C.c_uint32),
+        ("reserved2", C.c_uint32),
     ]
 
 
@@ -172,6 +173,8 @@ class Stats(C.Structure):
         ("streamed_bytes", C.c_uint64),
         ("planned_bytes", C.c_uint64),
         ("budget_bytes", C.c_uint64),
+        ("device_trees", C.c_uint32),
+        ("reserved", C.c_uint32),
     ]
 
 
@@ -200,7 +203,7 @@ HIP_SYMBOLS = [
     "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_gradient_exchange",
     "fbh_download_margin", "fbh_sigmoid_host", "fbh_sigmoid_device", "fbh_sigmoid_checksum",
     "fbh_begin_tree", "fbh_eval_nodes", "fbh_download_histogram",
-    "fbh_partition", "fbh_partition_eval", "fbh_assign_leaves", "fbh_download_delta", "fbh_host_alloc",
+    "fbh_partition", "fbh_partition_eval", "fbh_grow_depthwise", "fbh_assign_leaves", "fbh_download_delta", "fbh_host_alloc",
     "fbh_host_free", "fbh_download_rows",
     "fbh_hist_timing", "fbh_set_timing", "fbh_build_histogram", "fbh_partition_rows",
     "fbh_shap_model_create", "fbh_shap_model_destroy", "fbh_shap_contribs",

@@ -19,6 +19,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <limits>
 #include <memory>
 #include <stdexcept>
 #include <thread>
@@ -191,6 +192,23 @@ struct fbh_ctx {
     SplitNodeDev *d_lvl_split = nullptr;
     uint32_t *d_lvl_out = nullptr;  // spans (4 per pair), then left slots (1 per pair)
     uint32_t *d_lvl_rows = nullptr; // rows per chunk of the planned launch
+    // Device-grown depthwise trees (fbh_grow_depthwise): buffers sized for
+    // the deepest tree asked for so far, allocated on first use.
+    struct Grow {
+        uint32_t depth = 0;  // capacity: trees up to this depth
+        size_t level_cap = 0, tree_cap = 0, leaf_cap = 0, cat_cap = 0;
+        GrowState *st = nullptr;
+        LNodeDev *level[2] = {nullptr, nullptr};
+        TreeNodeDev *tree = nullptr;
+        uint64_t *tree_cats = nullptr;
+        PartReqDev *reqs = nullptr;
+        PairDev *pairs = nullptr;
+        uint32_t *triples = nullptr;
+        LeafDev *leaves = nullptr;
+        float *leaf_vals = nullptr;
+        DevColumn *cols = nullptr;
+        PinnedBuf out;  // state, tree, category words and leaf values coming back
+    } grow;
     size_t off_tilefeats = 0, off_sfeats = 0;  // offsets in the tree-table buffer
     size_t stage_bytes = 0;
     uint64_t max_chunks = 0;    // capacity of the partition chunk arrays
@@ -264,6 +282,8 @@ struct fbh_ctx {
         if (pin_small.p) (void)hipHostFree(pin_small.p);
         if (pin_leaves.p) (void)hipHostFree(pin_leaves.p);
         if (pin_out.p) (void)hipHostFree(pin_out.p);
+        if (grow.out.p) (void)hipHostFree(grow.out.p);
+        grow.out.p = nullptr;
         if (pin_ids.p) (void)hipHostFree(pin_ids.p);
         if (pin_src.p) (void)hipHostFree(pin_src.p);
         pin_small.p = pin_leaves.p = pin_out.p = pin_ids.p = pin_src.p = nullptr;
@@ -1224,11 +1244,15 @@ struct EvalPlan {
     const SplitNodeDev *sn = nullptr;
     uint32_t n_nodes = 0;
     const uint8_t *enabled = nullptr;
+    // Device-grown trees: counts read on the device (the host values above
+    // are then upper bounds that size the grids).
+    const uint32_t *dev_n_hn = nullptr, *dev_n_tri = nullptr, *dev_n_nodes = nullptr;
+    bool download = true;  // copy the packets back (a device-grown tree reads them in place)
 };
 
 void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
     if (E.dev_chunk_rows)
-        check(launch_zero_nodes(c->hist, c->hist_width, E.hn, E.n_hn,
+        check(launch_zero_nodes(c->hist, c->hist_width, E.hn, E.n_hn, E.dev_n_hn,
                                 c->has_global || !c->streamed.empty(), c->stream),
               "histogram clear");
     else
@@ -1250,6 +1274,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
             L.feats = c->d_tilefeats;
             L.nodes = E.hn;
             L.n_nodes = E.n_hn;
+            L.dev_n_nodes = E.dev_n_hn;
             L.n_chunks = E.grid_chunks;
             L.chunk_rows = E.chunk_rows;
             L.dev_chunk_rows = E.dev_chunk_rows;
@@ -1305,7 +1330,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
             c->ev_used++;
         }
     }
-    check(launch_subtract(c->hist, c->hist_width, E.triples, E.n_tri, c->stream),
+    check(launch_subtract(c->hist, c->hist_width, E.triples, E.n_tri, E.dev_n_tri, c->stream),
           "sibling subtraction");
     // ---- split scan ----
     SplitParamsDev P{};
@@ -1321,15 +1346,16 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
     P.n_feats = (uint32_t)c->tree_feats.size();
     P.cat_words_per_node = c->cat_words_per_node;
     check(launch_split_feats(c->hist, c->hist_width, E.sn, E.n_nodes, c->d_sfeats, E.enabled, P,
-                             c->d_cands, c->d_cat_scratch, c->stream),
+                             c->d_cands, c->d_cat_scratch, E.dev_n_nodes, c->stream),
           "split scan");
     const uint32_t cw = std::max(1u, c->cat_words_per_node);
     const size_t pk_bytes = sizeof(SplitPacketDev) * E.n_nodes;
     uint8_t *d_out = reinterpret_cast<uint8_t *>(c->d_packets);
     uint64_t *d_cats = reinterpret_cast<uint64_t *>(d_out + ((pk_bytes + 255) & ~size_t(255)));
     check(launch_split_nodes(c->d_cands, c->d_sfeats, E.n_nodes, P, E.sn, c->d_cat_scratch,
-                             c->d_packets, d_cats, cw, c->stream),
+                             c->d_packets, d_cats, cw, E.dev_n_nodes, c->stream),
           "split argmax");
+    if (!E.download) return;
     // Packets and category sets land back to back: one download.
     const size_t out_bytes = c->cat_words_per_node > 0
                                  ? ((pk_bytes + 255) & ~size_t(255)) + 8 * (size_t)E.n_nodes * cw
@@ -1368,15 +1394,16 @@ void account_hist(fbh_ctx *c, uint64_t acc_rows, uint64_t nodes_with_rows) {
 
 extern "C" {
 
-int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_split_params *sp,
-                   const uint8_t *enabled, fbh_split *out, uint64_t *cat_words,
-                   uint32_t cat_capacity) {
-    return guard([&] {
-        if (!c || (!nodes && n) || !sp || (!out && n)) throw InputError("null argument");
-        ensure_tree(c);
-        if (n == 0) return;
-        if (n > c->n_slots) throw InputError("more nodes than histogram slots");
-        check(hipSetDevice(c->device), "hipSetDevice");
+}  // extern "C"
+
+namespace {
+
+// Validates a batch of nodes and stages the tables of its evaluation as
+// planned on the host: exact chunks of the accumulated nodes, slots to
+// clear, subtraction triples and split-scan nodes. Returns the accumulated
+// rows and the accumulated nodes with rows (for the byte count).
+std::pair<uint64_t, uint64_t> stage_host_eval(fbh_ctx *c, const fbh_node *nodes, uint32_t n,
+                                              const uint8_t *enabled, Stager &S, EvalPlan &E) {
         for (uint32_t i = 0; i < n; i++) {
             const fbh_node &nd = nodes[i];
             if (nd.slot >= c->n_slots) throw InputError("histogram slot out of range");
@@ -1431,8 +1458,6 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
             sn[i].upper = nodes[i].upper;
             sn[i].slot = nodes[i].slot;
         }
-        Stager S{c};
-        EvalPlan E;
         E.hn = S.dev<HistNodeDev>(S.put(hn.data(), sizeof(HistNodeDev) * hn.size()));
         E.n_hn = (uint32_t)hn.size();
         E.grid_chunks = chunks;
@@ -1445,11 +1470,30 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
         E.n_nodes = n;
         if (enabled)
             E.enabled = S.dev<uint8_t>(S.put(enabled, (size_t)n * c->tree_feats.size()));
+        return {acc_rows, (uint64_t)hn.size()};
+}
+
+}  // namespace
+
+extern "C" {
+
+int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_split_params *sp,
+                   const uint8_t *enabled, fbh_split *out, uint64_t *cat_words,
+                   uint32_t cat_capacity) {
+    return guard([&] {
+        if (!c || (!nodes && n) || !sp || (!out && n)) throw InputError("null argument");
+        ensure_tree(c);
+        if (n == 0) return;
+        if (n > c->n_slots) throw InputError("more nodes than histogram slots");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        Stager S{c};
+        EvalPlan E;
+        const auto acc = stage_host_eval(c, nodes, n, enabled, S, E);
         S.send();
         enqueue_eval(c, E, sp);
         c->sync();
         if (c->timing) c->collect_timing();
-        account_hist(c, acc_rows, hn.size());
+        account_hist(c, acc.first, acc.second);
         unpack_packets(c, n, out, cat_words, cat_capacity);
     });
 }
@@ -1703,7 +1747,8 @@ int fbh_partition_eval(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
         if (!P.pr.empty()) enqueue_partition(c, P, S);
         check(launch_level_plan(S.dev<const PairDev>(o_pairs), n, c->d_totals, rule,
                                 c->d_lvl_hist, c->d_lvl_split, c->d_lvl_out,
-                                c->d_lvl_out + 4 * (size_t)n, c->d_lvl_rows, c->stream),
+                                c->d_lvl_out + 4 * (size_t)n, c->d_lvl_rows, GrowDevOut{},
+                                c->stream),
               "level plan");
         if (n_eval) {
             EvalPlan E;
@@ -1737,6 +1782,206 @@ int fbh_partition_eval(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
         }
         account_hist(c, acc, with_rows);
         if (n_eval) unpack_packets(c, 2 * n_eval, out, cat_out, cat_capacity);
+    });
+}
+
+}  // extern "C"
+
+namespace {
+
+constexpr uint32_t MAX_GROW_DEPTH = 14;
+
+// Buffers of device-grown trees up to depth D (grown, never shrunk).
+void ensure_grow(fbh_ctx *c, uint32_t D) {
+    auto &G = c->grow;
+    const uint32_t cw = std::max(1u, c->max_cat_words);
+    if (!G.cols) {
+        G.st = c->alloc<GrowState>(1, "grown tree state");
+        G.cols = c->alloc<DevColumn>(c->n_features, "grown tree columns");
+        std::vector<DevColumn> cols(c->n_features);
+        for (uint32_t f = 0; f < c->n_features; f++) cols[f] = {c->cols[f], c->width[f], 0};
+        check(hipMemcpy(G.cols, cols.data(), sizeof(DevColumn) * cols.size(),
+                        hipMemcpyHostToDevice),
+              "column table");
+    }
+    if (G.depth >= D) return;
+    G.depth = D;
+    G.level_cap = (size_t)1 << (D - 1);
+    G.tree_cap = ((size_t)2 << D) - 1;
+    G.leaf_cap = (size_t)1 << D;
+    G.cat_cap = G.leaf_cap * cw;
+    G.level[0] = c->alloc<LNodeDev>(G.level_cap, "grown tree level");
+    G.level[1] = c->alloc<LNodeDev>(G.level_cap, "grown tree level");
+    G.tree = c->alloc<TreeNodeDev>(G.tree_cap, "grown tree nodes");
+    G.tree_cats = c->alloc<uint64_t>(G.cat_cap, "grown tree categories");
+    G.reqs = c->alloc<PartReqDev>(G.level_cap, "grown tree requests");
+    G.pairs = c->alloc<PairDev>(G.level_cap, "grown tree pairs");
+    G.triples = c->alloc<uint32_t>(3 * G.level_cap, "grown tree triples");
+    G.leaves = c->alloc<LeafDev>(G.leaf_cap, "grown tree leaves");
+    G.leaf_vals = c->alloc<float>(G.leaf_cap, "grown tree leaf values");
+    if (G.out.p) (void)hipHostFree(G.out.p);
+    G.out.p = nullptr;
+    c->pinned(G.out, al256(sizeof(GrowState)) + al256(sizeof(TreeNodeDev) * G.tree_cap) +
+                         al256(8 * G.cat_cap) + al256(4 * G.leaf_cap));
+}
+
+}  // namespace
+
+extern "C" {
+
+int fbh_grow_depthwise(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params *sp,
+                       const int64_t root_sum[2], fbh_tree_node *nodes, uint32_t node_capacity,
+                       uint32_t *n_nodes, uint64_t *cat_words, uint32_t cat_capacity,
+                       float *leaf_values, uint32_t leaf_capacity, uint32_t *n_leaves) {
+    return guard([&] {
+        if (!c || !gp || !sp || !root_sum || !nodes || !n_nodes || !leaf_values || !n_leaves)
+            throw InputError("null argument");
+        ensure_tree(c);
+        const uint32_t D = gp->max_depth;
+        if (D == 0 || D > MAX_GROW_DEPTH)
+            throw InputError("a device-grown tree needs max_depth in 1..=" +
+                             std::to_string(MAX_GROW_DEPTH));
+        if (gp->max_leaves == 1) throw InputError("max_leaves 1 leaves nothing to grow");
+        if (!c->plan.columns_resident || !c->streamed.empty())
+            throw InputError("a device-grown tree needs every tile and column resident");
+        if (c->n_slots > MAX_GROW_SLOTS)
+            throw InputError("a device-grown tree supports at most " +
+                             std::to_string(MAX_GROW_SLOTS) + " histogram slots");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        ensure_grow(c, D);
+        auto &GB = c->grow;
+        const uint32_t n_rows = (uint32_t)c->n_rows;
+        const uint32_t n_slots = c->n_slots;
+        auto lvl_bound = [&](uint32_t d) { return std::min<uint32_t>(1u << d, n_slots); };
+
+        // The root is evaluated as fbh_eval_nodes plans it, without waiting.
+        Stager S{c};
+        fbh_node root{};
+        root.rows = {0, n_rows};
+        root.sum[0] = root_sum[0];
+        root.sum[1] = root_sum[1];
+        root.lower = -std::numeric_limits<float>::max();
+        root.upper = std::numeric_limits<float>::max();
+        root.slot = 0;
+        root.subtract_parent = -1;
+        root.subtract_sibling = -1;
+        EvalPlan E0;
+        const auto acc0 = stage_host_eval(c, &root, 1, nullptr, S, E0);
+        E0.download = false;
+        const int8_t *d_mono = S.dev<const int8_t>(S.put(c->monotone.data(), c->n_features));
+        S.send();
+
+        GrowParamsDev G{};
+        G.sp.inv_g = 1.0 / c->scales[0];
+        G.sp.inv_h = 1.0 / c->scales[1];
+        G.sp.lambda_ = sp->lambda_;
+        G.sp.gamma = sp->gamma;
+        G.sp.mcw = sp->min_child_weight;
+        G.sp.alpha = sp->alpha;
+        G.sp.mds = sp->max_delta_step;
+        G.sp.max_cat_to_onehot = sp->max_cat_to_onehot;
+        G.sp.max_cat_threshold = sp->max_cat_threshold;
+        G.sp.n_feats = (uint32_t)c->tree_feats.size();
+        G.sp.cat_words_per_node = c->cat_words_per_node;
+        G.learning_rate = gp->learning_rate;
+        G.max_depth = D;
+        G.max_leaves = gp->max_leaves;
+        G.n_slots = n_slots;
+        G.cw = std::max(1u, c->cat_words_per_node);
+        G.n_rows = n_rows;
+        check(launch_grow_init(G, root_sum[0], root_sum[1], 0, GB.level[0], GB.tree, GB.st,
+                               c->stream),
+              "tree init");
+        enqueue_eval(c, E0, sp);
+        account_hist(c, acc0.first, acc0.second);
+
+        const ChunkRule rule = c->chunk_rule();
+        uint8_t *pk_base = reinterpret_cast<uint8_t *>(c->d_packets);
+        for (uint32_t d = 0; d < D; d++) {
+            const uint32_t nb = lvl_bound(d);
+            const uint64_t *pk_cats =
+                reinterpret_cast<const uint64_t *>(pk_base + al256(sizeof(SplitPacketDev) * nb));
+            check(launch_grow_decide(G, d, c->d_packets, pk_cats, GB.level[d & 1], GB.tree,
+                                     GB.tree_cats, d_mono, GB.cols, GB.reqs, GB.pairs,
+                                     GB.triples, GB.leaves, GB.leaf_vals, GB.st, c->stream),
+                  "tree level decision");
+            check(launch_partition_dev(GB.reqs, &GB.st->n_split, n_rows / PART_CHUNK + nb + 1,
+                                       c->rows, c->tmp, c->flags, c->d_counts, c->d_excl,
+                                       c->d_totals, pk_cats, c->stream),
+                  "partition");
+            const GrowDevOut out{GB.st, GB.level[(d + 1) & 1], GB.tree, GB.leaves, GB.leaf_vals};
+            check(launch_level_plan(GB.pairs, nb, c->d_totals, rule, c->d_lvl_hist,
+                                    c->d_lvl_split, c->d_lvl_out, c->d_lvl_out + 4 * MAX_NODES,
+                                    c->d_lvl_rows, out, c->stream),
+                  "level plan");
+            if (d + 1 == D) break;
+            EvalPlan E;
+            E.hn = c->d_lvl_hist;
+            E.n_hn = nb;
+            E.dev_n_hn = &GB.st->n_eval;
+            E.grid_chunks = rule.fixed ? n_rows / rule.fixed + nb + 1
+                                       : std::max<uint32_t>(rule.want_chunks, 256) + nb;
+            E.dev_chunk_rows = c->d_lvl_rows;
+            E.triples = GB.triples;
+            E.n_tri = nb;
+            E.dev_n_tri = &GB.st->n_eval;
+            E.sn = c->d_lvl_split;
+            E.n_nodes = lvl_bound(d + 1);
+            E.dev_n_nodes = &GB.st->n_level;
+            E.download = false;
+            enqueue_eval(c, E, sp);
+        }
+        check(launch_leaf_plan(GB.leaves, GB.st, c->stream), "leaf plan");
+        uint64_t leaf_bound = (uint64_t)1 << D;
+        if (gp->max_leaves) leaf_bound = std::min<uint64_t>(leaf_bound, gp->max_leaves);
+        const int idb = c->objective >= 0 ? (leaf_bound <= 256 ? 1 : 2) : 0;
+        check(launch_assign_leaves(GB.leaves, 0, (uint32_t)(n_rows / PART_CHUNK + leaf_bound + 1),
+                                   c->rows, c->delta, c->leaf_ids, idb, &GB.st->n_leaves,
+                                   c->stream),
+              "leaf assignment");
+        if (idb)
+            check(launch_apply_leaves(c->leaf_ids, idb, GB.leaf_vals, c->n_rows, c->margin,
+                                      c->stream),
+                  "margin update");
+        c->leaf_id_bytes = idb;
+        c->ids_fresh = idb != 0;
+
+        uint8_t *po = static_cast<uint8_t *>(GB.out.p);
+        const size_t o_tree = al256(sizeof(GrowState));
+        const size_t o_cats = o_tree + al256(sizeof(TreeNodeDev) * GB.tree_cap);
+        const size_t o_vals = o_cats + al256(8 * GB.cat_cap);
+        check(hipMemcpyAsync(po, GB.st, sizeof(GrowState), hipMemcpyDeviceToHost, c->stream),
+              "tree download");
+        check(hipMemcpyAsync(po + o_tree, GB.tree, sizeof(TreeNodeDev) * GB.tree_cap,
+                             hipMemcpyDeviceToHost, c->stream),
+              "tree download");
+        if (c->cat_words_per_node)
+            check(hipMemcpyAsync(po + o_cats, GB.tree_cats, 8 * GB.cat_cap, hipMemcpyDeviceToHost,
+                                 c->stream),
+                  "tree download");
+        check(hipMemcpyAsync(po + o_vals, GB.leaf_vals, 4 * GB.leaf_cap, hipMemcpyDeviceToHost,
+                             c->stream),
+              "tree download");
+        c->sync();
+        if (c->timing) c->collect_timing();
+        GrowState st;
+        std::memcpy(&st, po, sizeof(st));
+        if (st.error)
+            throw RuntimeError("histogram slots exhausted; raise the slot budget");
+        account_hist(c, st.hist_rows, st.hist_nodes);
+        if (st.covered != c->n_rows)
+            throw RuntimeError("leaves cover " + std::to_string(st.covered) + " of " +
+                               std::to_string(c->n_rows) + " rows");
+        if (st.tree_size > node_capacity || st.n_leaves > leaf_capacity ||
+            (c->cat_words_per_node && st.tree_cat_words > cat_capacity))
+            throw InputError("output capacity too small for the grown tree");
+        static_assert(sizeof(TreeNodeDev) == sizeof(fbh_tree_node), "tree node layout");
+        std::memcpy(nodes, po + o_tree, sizeof(fbh_tree_node) * st.tree_size);
+        if (c->cat_words_per_node && cat_words)
+            std::memcpy(cat_words, po + o_cats, 8 * (size_t)st.tree_cat_words);
+        std::memcpy(leaf_values, po + o_vals, 4 * (size_t)st.n_leaves);
+        *n_nodes = st.tree_size;
+        *n_leaves = st.n_leaves;
     });
 }
 
@@ -1777,6 +2022,7 @@ int fbh_assign_leaves(fbh_ctx *c, const fbh_span *spans, const float *values, ui
         check(hipEventRecord(c->leaves_done, c->stream), "event");
         c->leaves_pending = true;
         check(launch_assign_leaves(c->d_leaves, m, chunks, c->rows, c->delta, c->leaf_ids, idb,
+                                   nullptr,
                                    c->stream),
               "leaf assignment");
         if (idb)

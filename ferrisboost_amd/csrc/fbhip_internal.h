@@ -13,6 +13,7 @@ constexpr int PART_TPB = 256;      // threads of one partition workgroup
 constexpr int PART_CHUNK = 2048;   // rows of one partition chunk (8 per thread)
 constexpr int XCDS = 8;            // MI355X accelerator complex dies
 constexpr uint32_t NO_SLOT = 0xFFFFFFFFu;
+constexpr uint32_t MAX_GROW_SLOTS = 16384;  // histogram slots a device-grown tree can use
 
 // One histogram tile: a group of features of one width stored as row
 // records, record i at data + i * stride, feature k of the tile at byte
@@ -53,6 +54,7 @@ struct HistLaunch {
     uint32_t n_tiles;
     const HistNodeDev *nodes;
     uint32_t n_nodes;
+    const uint32_t *dev_n_nodes;  // non-null: the node count, read on the device
     uint32_t n_chunks;         // chunks of the grid (a node may use fewer)
     uint32_t chunk_rows;
     // Non-null: the launch was planned on the device and the rows per chunk
@@ -135,6 +137,62 @@ struct PairDev {
     uint32_t eval_index;   // position among evaluated pairs, NO_SLOT when not evaluated
     float lower[2], upper[2];  // bounds of the left and right child
     int64_t left_sum[2], right_sum[2];
+    uint32_t left_id, right_id;  // tree node ids of the children (device-grown trees)
+};
+
+// ---- device-grown depthwise trees ----
+// Counters of one tree in device memory; kernels read the counts they run
+// over from here (pairs of fields are read as {count, chunks}).
+struct GrowState {
+    uint32_t n_level;       // evaluated nodes of the current level
+    uint32_t n_split;       // split nodes of the level (partition requests, pairs)
+    uint32_t part_chunks;   // partition chunks of the split nodes
+    uint32_t n_eval;        // pairs whose children are evaluated (n_split or 0)
+    uint32_t n_leaves;      // leaf table entries
+    uint32_t leaf_chunks;   // leaf-assignment chunks
+    uint32_t tree_size;     // tree nodes so far
+    uint32_t leaf_count;    // leaves as the host grower counts them (max_leaves)
+    uint32_t tree_cat_words;
+    uint32_t error;         // nonzero: histogram slots ran out
+    uint32_t hist_nodes;    // accumulated nodes with rows (all levels)
+    uint32_t pad;
+    uint64_t hist_rows;     // accumulated rows (all levels)
+    uint64_t covered;       // rows of all leaves
+};
+
+// Column of one feature for the partition of a device-grown tree.
+struct DevColumn {
+    const uint8_t *data;
+    uint32_t width, pad;
+};
+
+
+// One evaluated node of the current level.
+struct LNodeDev {
+    uint32_t tree_id, row_off, row_len, slot;
+    int64_t sum_g, sum_h;
+    float lower, upper;
+    uint32_t pad[2];
+};
+
+// One tree node as the device grows it (node ids in the host grower's order).
+struct TreeNodeDev {
+    uint32_t feat, bin;
+    int32_t left, right;
+    float leaf_value, sum_hess, gain;
+    uint32_t flags;  // bit 0 leaf, bit 1 default left, bit 2 categorical
+    uint32_t cat_off, n_cat_words;
+    uint32_t pad[2];
+};
+
+struct GrowParamsDev {
+    SplitParamsDev sp;     // lambda, alpha, max_delta_step, inverse scales
+    float learning_rate;
+    uint32_t max_depth, max_leaves;
+    uint32_t n_slots;
+    uint32_t cw;           // category words per node of the split outputs
+    uint32_t n_rows;
+    uint32_t pad[2];
 };
 
 // Rows per chunk of a device-planned histogram launch: fixed when nonzero,
@@ -163,6 +221,16 @@ struct ShapNodeDev {
     uint32_t pad;
 };
 
+// Outputs of the level plan that only a device-grown tree has (st null:
+// the host drives the tree).
+struct GrowDevOut {
+    GrowState *st;
+    LNodeDev *next;            // the next level's evaluated nodes
+    const TreeNodeDev *tree;
+    LeafDev *leaves;
+    float *leaf_vals;
+};
+
 // Last-error message shared by every fbh_* entry point (thread local).
 void set_last_error(const char *msg);
 const char *last_error();
@@ -175,12 +243,13 @@ hipError_t launch_hist(const HistLaunch &L, int width, int rec_dwords, int threa
 hipError_t launch_hist_global(const HistLaunch &L, int width, hipStream_t s);
 hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slots, uint32_t n,
                              hipStream_t s);
+// dev_n (nullable): the triple count read on the device, n its upper bound.
 hipError_t launch_subtract(int64_t *hist, uint64_t width, const uint32_t *triples, uint32_t n,
-                           hipStream_t s);
+                           const uint32_t *dev_n, hipStream_t s);
 // Zero the slots of accumulated nodes that need it: all when force, else
 // those not written by plain stores (n_chunks != 1).
 hipError_t launch_zero_nodes(int64_t *hist, uint64_t width, const HistNodeDev *nodes, uint32_t n,
-                             bool force, hipStream_t s);
+                             const uint32_t *dev_n, bool force, hipStream_t s);
 // Device plan of a fused step: children spans (2 per pair) and the left
 // child's slot per pair, the accumulated nodes (one per evaluated pair, in
 // pair order), the split-scan nodes (left, right per evaluated pair) and
@@ -188,20 +257,38 @@ hipError_t launch_zero_nodes(int64_t *hist, uint64_t width, const HistNodeDev *n
 hipError_t launch_level_plan(const PairDev *pairs, uint32_t n_pairs, const uint32_t *totals,
                              ChunkRule rule, HistNodeDev *hist_nodes, SplitNodeDev *split_nodes,
                              uint32_t *spans, uint32_t *left_slot, uint32_t *chunk_rows,
-                             hipStream_t s);
+                             const GrowDevOut &D, hipStream_t s);
+// Device-grown depthwise trees (one workgroup each): the root, the decision
+// of one level (see grow_decide_kernel) and the leaf table's chunks.
+hipError_t launch_grow_init(const GrowParamsDev &G, int64_t root_g, int64_t root_h,
+                            uint32_t root_slot, LNodeDev *level, TreeNodeDev *tree,
+                            GrowState *st, hipStream_t s);
+hipError_t launch_grow_decide(const GrowParamsDev &G, uint32_t depth, const SplitPacketDev *pk,
+                              const uint64_t *pk_cats, const LNodeDev *level, TreeNodeDev *tree,
+                              uint64_t *tree_cats, const int8_t *monotone, const DevColumn *cols,
+                              PartReqDev *reqs, PairDev *pairs, uint32_t *triples,
+                              LeafDev *leaves, float *leaf_vals, GrowState *st, hipStream_t s);
+hipError_t launch_leaf_plan(LeafDev *leaves, GrowState *st, hipStream_t s);
 hipError_t launch_split_feats(const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
                               uint32_t n_nodes, const SplitFeatDev *feats, const uint8_t *enabled,
                               SplitParamsDev P, FeatCandDev *cands, uint64_t *cat_scratch,
-                              hipStream_t s);
+                              const uint32_t *dev_n, hipStream_t s);
 hipError_t launch_split_nodes(const FeatCandDev *cands, const SplitFeatDev *feats,
                               uint32_t n_nodes, SplitParamsDev P, const SplitNodeDev *nodes,
                               const uint64_t *cat_scratch, SplitPacketDev *out,
-                              uint64_t *cat_out, uint32_t cat_out_words, hipStream_t s);
+                              uint64_t *cat_out, uint32_t cat_out_words, const uint32_t *dev_n,
+                              hipStream_t s);
 // Pass 1 (direction flags, left count per chunk) over a group of requests
 // whose chunk_begin numbers the group's own chunks; counts land at count_base.
 hipError_t launch_partition_count(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
                                   const uint32_t *rows, uint8_t *flags, uint32_t *chunk_counts,
                                   const uint64_t *cat_words, hipStream_t s);
+// All four passes over requests planned on the device: dev = {requests,
+// chunks}; grid_chunks is an upper bound of the chunks.
+hipError_t launch_partition_dev(const PartReqDev *reqs, const uint32_t *dev, uint32_t grid_chunks,
+                                uint32_t *rows, uint32_t *tmp, uint8_t *flags, uint32_t *counts,
+                                uint32_t *excl, uint32_t *totals, const uint64_t *cat_words,
+                                hipStream_t s);
 // Passes 2-4 (scan, stable scatter, copy back) over all requests of the call.
 hipError_t launch_partition_finish(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
                                    uint32_t *rows, uint32_t *tmp, const uint8_t *flags,
@@ -209,9 +296,11 @@ hipError_t launch_partition_finish(const PartReqDev *reqs, uint32_t n_reqs, uint
                                    uint32_t *totals, hipStream_t s);
 // id_bytes 0: delta[row] = leaf value; 1 / 2: ids[row] = leaf position as
 // u8 / u16.
+// dev (nullable): {leaf count, chunks} read on the device; n_chunks is then
+// the grid's upper bound.
 hipError_t launch_assign_leaves(const LeafDev *leaves, uint32_t n_leaves, uint32_t n_chunks,
                                 const uint32_t *rows, float *delta, void *ids, int id_bytes,
-                                hipStream_t s);
+                                const uint32_t *dev, hipStream_t s);
 // margin[row] += values[ids[row]] over all rows (id_bytes 1 or 2).
 hipError_t launch_apply_leaves(const void *ids, int id_bytes, const float *values, uint64_t n,
                                float *margin, hipStream_t s);

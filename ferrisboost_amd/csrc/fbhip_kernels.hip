@@ -94,8 +94,10 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
     const uint32_t chunk = (k / L.n_tiles) * XCDS + xcd;
     if (chunk >= L.n_chunks) return;
     const TileDev T = L.tiles[tile_i];
+    const uint32_t n_nodes = L.dev_n_nodes ? *L.dev_n_nodes : L.n_nodes;
+    if (n_nodes == 0) return;
 
-    uint32_t lo = 0, hi = L.n_nodes;
+    uint32_t lo = 0, hi = n_nodes;
     while (hi - lo > 1) {
         uint32_t mid = (lo + hi) >> 1;
         if (L.nodes[mid].chunk_begin <= chunk) lo = mid;
@@ -234,7 +236,9 @@ __global__ __launch_bounds__(HIST_TPB) void hist_global_kernel(const HistLaunch 
     const TileDev T = L.tiles[tile_i];
     const TileFeatDev F = L.feats[T.feat_base];
     if (F.n_bins == 0) return;
-    uint32_t lo = 0, hi = L.n_nodes;
+    const uint32_t n_nodes = L.dev_n_nodes ? *L.dev_n_nodes : L.n_nodes;
+    if (n_nodes == 0) return;
+    uint32_t lo = 0, hi = n_nodes;
     while (hi - lo > 1) {
         uint32_t mid = (lo + hi) >> 1;
         if (L.nodes[mid].chunk_begin <= chunk) lo = mid;
@@ -337,7 +341,9 @@ hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slot
 }
 
 // dst = parent - sibling, elementwise wrapping i64 (triples: dst, parent, sibling).
-__global__ void subtract_kernel(int64_t *hist, uint64_t width, const uint32_t *triples) {
+__global__ void subtract_kernel(int64_t *hist, uint64_t width, const uint32_t *triples,
+                                const uint32_t *dev_n) {
+    if (dev_n && blockIdx.y >= *dev_n) return;
     const uint32_t *t = triples + 3u * blockIdx.y;
     uint64_t *dst = reinterpret_cast<uint64_t *>(hist + (uint64_t)t[0] * width * 2u);
     const uint64_t *par = reinterpret_cast<const uint64_t *>(hist + (uint64_t)t[1] * width * 2u);
@@ -349,15 +355,16 @@ __global__ void subtract_kernel(int64_t *hist, uint64_t width, const uint32_t *t
 }
 
 hipError_t launch_subtract(int64_t *hist, uint64_t width, const uint32_t *triples, uint32_t n,
-                           hipStream_t s) {
+                           const uint32_t *dev_n, hipStream_t s) {
     if (n == 0) return hipSuccess;
     uint32_t bx = (uint32_t)std::min<uint64_t>((width * 2 + 255) / 256, 1024);
-    hipLaunchKernelGGL(subtract_kernel, dim3(bx, n), dim3(256), 0, s, hist, width, triples);
+    hipLaunchKernelGGL(subtract_kernel, dim3(bx, n), dim3(256), 0, s, hist, width, triples, dev_n);
     return hipGetLastError();
 }
 
 __global__ void zero_nodes_kernel(int64_t *hist, uint64_t width, const HistNodeDev *nodes,
-                                  bool force) {
+                                  const uint32_t *dev_n, bool force) {
+    if (dev_n && blockIdx.y >= *dev_n) return;
     const HistNodeDev N = nodes[blockIdx.y];
     if (!force && N.n_chunks == 1) return;  // written by plain stores
     int64_t *base = hist + (uint64_t)N.slot * width * 2u;
@@ -368,10 +375,11 @@ __global__ void zero_nodes_kernel(int64_t *hist, uint64_t width, const HistNodeD
 }
 
 hipError_t launch_zero_nodes(int64_t *hist, uint64_t width, const HistNodeDev *nodes, uint32_t n,
-                             bool force, hipStream_t s) {
+                             const uint32_t *dev_n, bool force, hipStream_t s) {
     if (n == 0) return hipSuccess;
     uint32_t bx = (uint32_t)std::min<uint64_t>((width * 2 + 255) / 256, 1024);
-    hipLaunchKernelGGL(zero_nodes_kernel, dim3(bx, n), dim3(256), 0, s, hist, width, nodes, force);
+    hipLaunchKernelGGL(zero_nodes_kernel, dim3(bx, n), dim3(256), 0, s, hist, width, nodes, dev_n,
+                       force);
     return hipGetLastError();
 }
 
@@ -398,11 +406,18 @@ __global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, 
                                                           const uint32_t *totals, ChunkRule rule,
                                                           HistNodeDev *hn, SplitNodeDev *sn,
                                                           uint32_t *spans, uint32_t *left_slot,
-                                                          uint32_t *chunk_rows_out) {
+                                                          uint32_t *chunk_rows_out, GrowDevOut D) {
     __shared__ uint32_t buf[1024];
-    __shared__ unsigned long long acc_sh;
+    __shared__ unsigned long long acc_sh, acc_nodes_sh;
     __shared__ uint32_t cr_sh;
-    if (threadIdx.x == 0) acc_sh = 0;
+    // A device-grown tree: the pair count and the leaf table base come from
+    // its state (read by every thread before thread 0 updates it).
+    uint32_t leaf_base = 0;
+    if (D.st) {
+        n = D.st->n_split;
+        leaf_base = D.st->n_leaves;
+    }
+    if (threadIdx.x == 0) acc_sh = acc_nodes_sh = 0;
     __syncthreads();
     // Spans of every pair and the rows the evaluated pairs accumulate.
     unsigned long long acc = 0;
@@ -418,6 +433,7 @@ __global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, 
     }
     atomicAdd(&acc_sh, acc);
     __syncthreads();
+    unsigned long long acc_nodes = 0;
     if (threadIdx.x == 0) {
         uint64_t r;
         if (rule.fixed) {
@@ -444,8 +460,13 @@ __global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, 
             nr = P.row_len - nl;
             if (ev) nc = (min(nl, nr) + cr - 1) / cr;
         }
-        uint32_t total;
+        uint32_t total, leaves_total = 0, leaf_before = 0;
         const uint32_t before = carry + block_scan_1024(nc, buf, total);
+        // Children of pairs that are not evaluated are leaves (those with rows).
+        if (D.st) {
+            const uint32_t nlv = (i < n && !ev) ? (nl > 0) + (nr > 0) : 0u;
+            leaf_before = leaf_base + block_scan_1024(nlv, buf, leaves_total);
+        }
         if (i < n) {
             // The smaller child (the left one on ties) is accumulated.
             const bool left_small = nl <= nr;
@@ -472,21 +493,72 @@ __global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, 
                 sn[2 * e] = l;
                 sn[2 * e + 1] = r;
                 left_slot[i] = l.slot;
+                if (D.st) {
+                    LNodeDev a{}, b{};
+                    a.tree_id = P.left_id;
+                    a.row_off = P.row_off;
+                    a.row_len = nl;
+                    a.slot = l.slot;
+                    a.sum_g = l.sum_g;
+                    a.sum_h = l.sum_h;
+                    a.lower = l.lower;
+                    a.upper = l.upper;
+                    b.tree_id = P.right_id;
+                    b.row_off = P.row_off + nl;
+                    b.row_len = nr;
+                    b.slot = r.slot;
+                    b.sum_g = r.sum_g;
+                    b.sum_h = r.sum_h;
+                    b.lower = r.lower;
+                    b.upper = r.upper;
+                    D.next[2 * e] = a;
+                    D.next[2 * e + 1] = b;
+                    acc_nodes += min(nl, nr) > 0;
+                }
             } else {
                 left_slot[i] = NO_SLOT;
+                if (D.st) {
+                    uint32_t k = leaf_before;
+                    const uint32_t ids[2] = {P.left_id, P.right_id};
+                    const uint32_t offs[2] = {P.row_off, P.row_off + nl};
+                    const uint32_t lens[2] = {nl, nr};
+                    for (int c = 0; c < 2; c++) {
+                        if (lens[c] == 0) continue;
+                        LeafDev lf{};
+                        lf.row_off = offs[c];
+                        lf.row_len = lens[c];
+                        lf.value = D.tree[ids[c]].leaf_value;
+                        lf.id = k;
+                        D.leaves[k] = lf;
+                        D.leaf_vals[k] = lf.value;
+                        k++;
+                    }
+                }
             }
         }
         carry += total;
+        leaf_base += leaves_total;
+    }
+    if (D.st) {
+        atomicAdd(&acc_nodes_sh, acc_nodes);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            GrowState *st = D.st;
+            st->n_level = 2 * st->n_eval;
+            st->n_leaves = leaf_base;
+            st->hist_rows += acc_sh;
+            st->hist_nodes += (uint32_t)acc_nodes_sh;
+        }
     }
 }
 
 hipError_t launch_level_plan(const PairDev *pairs, uint32_t n_pairs, const uint32_t *totals,
                              ChunkRule rule, HistNodeDev *hist_nodes, SplitNodeDev *split_nodes,
                              uint32_t *spans, uint32_t *left_slot, uint32_t *chunk_rows,
-                             hipStream_t s) {
-    if (n_pairs == 0) return hipSuccess;
+                             const GrowDevOut &D, hipStream_t s) {
+    if (n_pairs == 0 && !D.st) return hipSuccess;
     hipLaunchKernelGGL(level_plan_kernel, dim3(1), dim3(1024), 0, s, pairs, n_pairs, totals, rule,
-                       hist_nodes, split_nodes, spans, left_slot, chunk_rows);
+                       hist_nodes, split_nodes, spans, left_slot, chunk_rows, D);
     return hipGetLastError();
 }
 
@@ -753,12 +825,13 @@ __device__ void split_categorical(const int64_t *h, uint32_t n, const SplitNodeD
 __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
     const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
     const SplitFeatDev *feats, const uint8_t *enabled, SplitParamsDev P, FeatCandDev *cands,
-    uint64_t *cat_scratch) {
+    uint64_t *cat_scratch, const uint32_t *dev_n) {
     __shared__ Best shb[SPLIT_TPB];
     __shared__ int64_t sg[SPLIT_TPB], shh[SPLIT_TPB];
     extern __shared__ unsigned char dyn[];
 
     const uint32_t j = blockIdx.x, ni = blockIdx.y, tid = threadIdx.x;
+    if (dev_n && ni >= *dev_n) return;
     const SplitFeatDev F = feats[j];
     const SplitNodeDev N = nodes[ni];
     FeatCandDev *outc = cands + (size_t)ni * P.n_feats + j;
@@ -836,12 +909,12 @@ __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
 hipError_t launch_split_feats(const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
                               uint32_t n_nodes, const SplitFeatDev *feats, const uint8_t *enabled,
                               SplitParamsDev P, FeatCandDev *cands, uint64_t *cat_scratch,
-                              hipStream_t s) {
+                              const uint32_t *dev_n, hipStream_t s) {
     if (n_nodes == 0 || P.n_feats == 0) return hipSuccess;
     const size_t dyn = P.cat_words_per_node ? (sizeof(float) + sizeof(uint32_t)) * MAX_DEVICE_CATS
                                             : 0;
     hipLaunchKernelGGL(split_feat_kernel, dim3(P.n_feats, n_nodes), dim3(SPLIT_TPB), dyn, s, hist,
-                       hist_width, nodes, feats, enabled, P, cands, cat_scratch);
+                       hist_width, nodes, feats, enabled, P, cands, cat_scratch, dev_n);
     return hipGetLastError();
 }
 
@@ -850,9 +923,10 @@ hipError_t launch_split_feats(const int64_t *hist, uint64_t hist_width, const Sp
 __global__ __launch_bounds__(SPLIT_TPB) void split_node_kernel(
     const FeatCandDev *cands, const SplitFeatDev *feats, SplitParamsDev P,
     const SplitNodeDev *nodes, const uint64_t *cat_scratch, SplitPacketDev *out,
-    uint64_t *cat_out, uint32_t cat_out_words) {
+    uint64_t *cat_out, uint32_t cat_out_words, const uint32_t *dev_n) {
     __shared__ Best shb[SPLIT_TPB];
     const uint32_t ni = blockIdx.x, tid = threadIdx.x;
+    if (dev_n && ni >= *dev_n) return;
     const FeatCandDev *c = cands + (size_t)ni * P.n_feats;
     Best best{0.0f, 0u, 0u, 0, 0};
     for (uint32_t j = tid; j < P.n_feats; j += SPLIT_TPB) {
@@ -902,10 +976,11 @@ __global__ __launch_bounds__(SPLIT_TPB) void split_node_kernel(
 hipError_t launch_split_nodes(const FeatCandDev *cands, const SplitFeatDev *feats,
                               uint32_t n_nodes, SplitParamsDev P, const SplitNodeDev *nodes,
                               const uint64_t *cat_scratch, SplitPacketDev *out,
-                              uint64_t *cat_out, uint32_t cat_out_words, hipStream_t s) {
+                              uint64_t *cat_out, uint32_t cat_out_words, const uint32_t *dev_n,
+                              hipStream_t s) {
     if (n_nodes == 0) return hipSuccess;
     hipLaunchKernelGGL(split_node_kernel, dim3(n_nodes), dim3(SPLIT_TPB), 0, s, cands, feats, P,
-                       nodes, cat_scratch, out, cat_out, cat_out_words);
+                       nodes, cat_scratch, out, cat_out, cat_out_words, dev_n);
     return hipGetLastError();
 }
 
@@ -942,10 +1017,12 @@ __global__ __launch_bounds__(PART_TPB) void part_count_kernel(const PartReqDev *
                                                               uint32_t n_reqs,
                                                               const uint32_t *rows,
                                                               uint8_t *flags, uint32_t *counts,
-                                                              const uint64_t *cat_words) {
+                                                              const uint64_t *cat_words,
+                                                              const uint32_t *dev) {
     __shared__ uint32_t wave_sum[PART_TPB / 64];
     const uint32_t chunk = blockIdx.x;
-    const PartReqDev R = reqs[find_req(reqs, n_reqs, chunk)];
+    if (dev && chunk >= dev[1]) return;
+    const PartReqDev R = reqs[find_req(reqs, dev ? dev[0] : n_reqs, chunk)];
     const uint32_t c0 = (chunk - R.chunk_begin) * PART_CHUNK;
     const uint32_t c1 = min(c0 + PART_CHUNK, R.row_len);
     uint32_t cnt = 0;
@@ -970,9 +1047,14 @@ __global__ __launch_bounds__(PART_TPB) void part_count_kernel(const PartReqDev *
 // total of every request.
 __global__ __launch_bounds__(1024) void part_scan_kernel(const uint32_t *counts, uint32_t n_chunks,
                                                          uint32_t *excl, const PartReqDev *reqs,
-                                                         uint32_t n_reqs, uint32_t *totals) {
+                                                         uint32_t n_reqs, uint32_t *totals,
+                                                         const uint32_t *dev) {
     __shared__ uint32_t buf[1024];
     __shared__ uint32_t carry;
+    if (dev) {
+        n_reqs = dev[0];
+        n_chunks = dev[1];
+    }
     if (threadIdx.x == 0) carry = 0;
     __syncthreads();
     for (uint32_t base = 0; base < n_chunks; base += 1024) {
@@ -1005,10 +1087,12 @@ __global__ __launch_bounds__(PART_TPB) void part_scatter_kernel(const PartReqDev
                                                                 const uint8_t *flags,
                                                                 const uint32_t *excl,
                                                                 const uint32_t *totals,
-                                                                uint32_t *tmp) {
+                                                                uint32_t *tmp,
+                                                                const uint32_t *dev) {
     __shared__ uint32_t wave_left[PART_TPB / 64];
     const uint32_t chunk = blockIdx.x;
-    const uint32_t ri = find_req(reqs, n_reqs, chunk);
+    if (dev && chunk >= dev[1]) return;
+    const uint32_t ri = find_req(reqs, dev ? dev[0] : n_reqs, chunk);
     const PartReqDev R = reqs[ri];
     const uint32_t c0 = (chunk - R.chunk_begin) * PART_CHUNK;
     const uint32_t c1 = min(c0 + PART_CHUNK, R.row_len);
@@ -1045,9 +1129,10 @@ __global__ __launch_bounds__(PART_TPB) void part_scatter_kernel(const PartReqDev
 
 __global__ __launch_bounds__(PART_TPB) void part_copy_kernel(const PartReqDev *reqs,
                                                              uint32_t n_reqs, const uint32_t *tmp,
-                                                             uint32_t *rows) {
+                                                             uint32_t *rows, const uint32_t *dev) {
     const uint32_t chunk = blockIdx.x;
-    const PartReqDev R = reqs[find_req(reqs, n_reqs, chunk)];
+    if (dev && chunk >= dev[1]) return;
+    const PartReqDev R = reqs[find_req(reqs, dev ? dev[0] : n_reqs, chunk)];
     const uint32_t c0 = (chunk - R.chunk_begin) * PART_CHUNK;
     const uint32_t c1 = min(c0 + PART_CHUNK, R.row_len);
     for (uint32_t i = c0 + threadIdx.x; i < c1; i += PART_TPB)
@@ -1059,7 +1144,23 @@ hipError_t launch_partition_count(const PartReqDev *reqs, uint32_t n_reqs, uint3
                                   const uint64_t *cat_words, hipStream_t s) {
     if (n_chunks == 0) return hipSuccess;
     hipLaunchKernelGGL(part_count_kernel, dim3(n_chunks), dim3(PART_TPB), 0, s, reqs, n_reqs, rows,
-                       flags, counts, cat_words);
+                       flags, counts, cat_words, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_partition_dev(const PartReqDev *reqs, const uint32_t *dev, uint32_t grid_chunks,
+                                uint32_t *rows, uint32_t *tmp, uint8_t *flags, uint32_t *counts,
+                                uint32_t *excl, uint32_t *totals, const uint64_t *cat_words,
+                                hipStream_t s) {
+    if (grid_chunks == 0) return hipSuccess;
+    hipLaunchKernelGGL(part_count_kernel, dim3(grid_chunks), dim3(PART_TPB), 0, s, reqs, 0u, rows,
+                       flags, counts, cat_words, dev);
+    hipLaunchKernelGGL(part_scan_kernel, dim3(1), dim3(1024), 0, s, counts, 0u, excl, reqs, 0u,
+                       totals, dev);
+    hipLaunchKernelGGL(part_scatter_kernel, dim3(grid_chunks), dim3(PART_TPB), 0, s, reqs, 0u,
+                       rows, flags, excl, totals, tmp, dev);
+    hipLaunchKernelGGL(part_copy_kernel, dim3(grid_chunks), dim3(PART_TPB), 0, s, reqs, 0u, tmp,
+                       rows, dev);
     return hipGetLastError();
 }
 
@@ -1069,11 +1170,11 @@ hipError_t launch_partition_finish(const PartReqDev *reqs, uint32_t n_reqs, uint
                                    hipStream_t s) {
     if (n_chunks == 0) return hipSuccess;
     hipLaunchKernelGGL(part_scan_kernel, dim3(1), dim3(1024), 0, s, counts, n_chunks, excl, reqs,
-                       n_reqs, totals);
+                       n_reqs, totals, nullptr);
     hipLaunchKernelGGL(part_scatter_kernel, dim3(n_chunks), dim3(PART_TPB), 0, s, reqs, n_reqs,
-                       rows, flags, excl, totals, tmp);
+                       rows, flags, excl, totals, tmp, nullptr);
     hipLaunchKernelGGL(part_copy_kernel, dim3(n_chunks), dim3(PART_TPB), 0, s, reqs, n_reqs, tmp,
-                       rows);
+                       rows, nullptr);
     return hipGetLastError();
 }
 
@@ -1095,8 +1196,12 @@ __device__ __forceinline__ uint64_t rotl64(uint64_t x, int r) { return (x << r) 
 template <int IDB>
 __global__ __launch_bounds__(PART_TPB) void leaf_kernel(const LeafDev *leaves, uint32_t n,
                                                         const uint32_t *rows, float *delta,
-                                                        void *ids) {
+                                                        void *ids, const uint32_t *dev) {
     const uint32_t chunk = blockIdx.x;
+    if (dev) {  // a device-grown tree: leaf count and chunks on the device
+        if (chunk >= dev[1]) return;
+        n = dev[0];
+    }
     uint32_t lo = 0, hi = n;
     while (hi - lo > 1) {
         uint32_t mid = (lo + hi) >> 1;
@@ -1129,17 +1234,17 @@ __global__ __launch_bounds__(256) void apply_leaves_kernel(const void *ids, cons
 
 hipError_t launch_assign_leaves(const LeafDev *leaves, uint32_t n_leaves, uint32_t n_chunks,
                                 const uint32_t *rows, float *delta, void *ids, int id_bytes,
-                                hipStream_t s) {
+                                const uint32_t *dev, hipStream_t s) {
     if (n_chunks == 0) return hipSuccess;
     if (id_bytes == 1)
         hipLaunchKernelGGL(leaf_kernel<1>, dim3(n_chunks), dim3(PART_TPB), 0, s, leaves, n_leaves,
-                           rows, delta, ids);
+                           rows, delta, ids, dev);
     else if (id_bytes == 2)
         hipLaunchKernelGGL(leaf_kernel<2>, dim3(n_chunks), dim3(PART_TPB), 0, s, leaves, n_leaves,
-                           rows, delta, ids);
+                           rows, delta, ids, dev);
     else
         hipLaunchKernelGGL(leaf_kernel<0>, dim3(n_chunks), dim3(PART_TPB), 0, s, leaves, n_leaves,
-                           rows, delta, ids);
+                           rows, delta, ids, dev);
     return hipGetLastError();
 }
 
@@ -1609,6 +1714,283 @@ hipError_t launch_shap(const ShapNodeDev *nodes, const uint32_t *tree_roots, uin
     FBH_SHAP_CASE(1024)
 #undef FBH_SHAP_CASE
     return hipErrorInvalidValue;
+}
+
+// ======================================================================
+// device-grown depthwise trees
+// ======================================================================
+// The host enqueues every level of a depthwise tree without waiting: each
+// level's decision kernel reads the split packets where the split scan left
+// them and plans the partition and the children exactly as the host grower
+// would (build_tree, src/training/mod.rs:3357-4565).
+
+__global__ void grow_init_kernel(GrowParamsDev G, int64_t rg, int64_t rh, uint32_t root_slot,
+                                 LNodeDev *level, TreeNodeDev *tree, GrowState *st) {
+    if (threadIdx.x != 0) return;
+    GrowState s{};
+    s.n_level = 1;
+    s.tree_size = 1;
+    s.leaf_count = 1;
+    *st = s;
+    LNodeDev r{};
+    r.tree_id = 0;
+    r.row_off = 0;
+    r.row_len = G.n_rows;
+    r.slot = root_slot;
+    r.sum_g = rg;
+    r.sum_h = rh;
+    r.lower = -3.40282347e38f;
+    r.upper = 3.40282347e38f;
+    level[0] = r;
+    const double g = (double)rg * G.sp.inv_g, h = (double)rh * G.sp.inv_h;
+    TreeNodeDev t{};
+    t.left = t.right = -1;
+    t.flags = 1;
+    t.leaf_value = xgb_weight(g, h, G.sp) * G.learning_rate;
+    t.sum_hess = (float)h;
+    tree[0] = t;
+}
+
+hipError_t launch_grow_init(const GrowParamsDev &G, int64_t root_g, int64_t root_h,
+                            uint32_t root_slot, LNodeDev *level, TreeNodeDev *tree,
+                            GrowState *st, hipStream_t s) {
+    hipLaunchKernelGGL(grow_init_kernel, dim3(1), dim3(64), 0, s, G, root_g, root_h, root_slot,
+                       level, tree, st);
+    return hipGetLastError();
+}
+
+// One level of a device-grown tree (one workgroup, each thread a run of the
+// level's nodes in order):
+//  - the max_leaves budget: the first `remaining` nodes with a split split;
+//  - a node that does not split is a leaf (leaf table, when it has rows);
+//  - a split node s (s-th in order) gets children tree_size + 2s, + 1 with
+//    the weights, monotone bounds and Hessians of Tree::split_leaf and
+//    child_leaves (src/training/mod.rs:5069-5094), its partition request,
+//    and, when the children are evaluated, the lowest free histogram slot
+//    for the smaller child (the larger one takes over the node's slot).
+__global__ __launch_bounds__(1024) void grow_decide_kernel(
+    GrowParamsDev G, uint32_t depth, const SplitPacketDev *pk, const uint64_t *pk_cats,
+    const LNodeDev *level, TreeNodeDev *tree, uint64_t *tree_cats, const int8_t *monotone,
+    const DevColumn *cols, PartReqDev *reqs, PairDev *pairs, uint32_t *triples, LeafDev *leaves,
+    float *leaf_vals, GrowState *st) {
+    __shared__ uint32_t buf[1024];
+    __shared__ uint32_t held[MAX_GROW_SLOTS / 32];
+    __shared__ uint16_t freelist[MAX_GROW_SLOTS];
+    const uint32_t tid = threadIdx.x;
+    const GrowState S0 = *st;
+    __syncthreads();  // every thread has read the state before thread 0 rewrites it
+    const uint32_t n = S0.n_level;
+    const uint32_t per = (n + 1023) / 1024;
+    const uint32_t i0 = min(tid * per, n), i1 = min(i0 + per, n);
+
+    uint32_t nf = 0;
+    for (uint32_t i = i0; i < i1; i++) nf += pk[i].found ? 1u : 0u;
+    uint32_t tot_found;
+    const uint32_t f_before = block_scan_1024(nf, buf, tot_found);
+    uint32_t remaining = 0xFFFFFFFFu;
+    if (G.max_leaves)
+        remaining = G.max_leaves > S0.leaf_count ? G.max_leaves - S0.leaf_count : 0u;
+    const uint32_t n_split = min(tot_found, remaining);
+    const uint32_t leaf_count = S0.leaf_count + n_split;
+    bool evaluated =
+        n_split > 0 && depth + 1 < G.max_depth && !(G.max_leaves && leaf_count >= G.max_leaves);
+
+    uint32_t nl = 0, nc = 0;
+    {
+        uint32_t fr = f_before;
+        for (uint32_t i = i0; i < i1; i++) {
+            const bool found = pk[i].found != 0;
+            if (found && fr < n_split) nc += (level[i].row_len + PART_CHUNK - 1) / PART_CHUNK;
+            else if (level[i].row_len) nl++;
+            if (found) fr++;
+        }
+    }
+    uint32_t tot_leaves, tot_chunks;
+    const uint32_t l_before = block_scan_1024(nl, buf, tot_leaves);
+    const uint32_t c_before = block_scan_1024(nc, buf, tot_chunks);
+
+    bool slots_short = false;
+    if (evaluated) {
+        const uint32_t words = (G.n_slots + 31) / 32;
+        for (uint32_t w = tid; w < words; w += 1024) held[w] = 0;
+        __syncthreads();
+        uint32_t fr = f_before;
+        for (uint32_t i = i0; i < i1; i++) {
+            if (!pk[i].found) continue;
+            if (fr < n_split) atomicOr(&held[level[i].slot >> 5], 1u << (level[i].slot & 31));
+            fr++;
+        }
+        __syncthreads();
+        const uint32_t sp = (G.n_slots + 1023) / 1024;
+        const uint32_t s0 = min(tid * sp, G.n_slots), s1 = min(s0 + sp, G.n_slots);
+        uint32_t nfree = 0;
+        for (uint32_t q = s0; q < s1; q++) nfree += ((held[q >> 5] >> (q & 31)) & 1u) ? 0u : 1u;
+        uint32_t tot_free;
+        uint32_t fb = block_scan_1024(nfree, buf, tot_free);
+        for (uint32_t q = s0; q < s1; q++)
+            if (!((held[q >> 5] >> (q & 31)) & 1u)) freelist[fb++] = (uint16_t)q;
+        __syncthreads();
+        if (tot_free < n_split) {
+            slots_short = true;
+            evaluated = false;
+        }
+    }
+
+    uint32_t fr = f_before, lr = l_before, cb = c_before;
+    for (uint32_t i = i0; i < i1; i++) {
+        const SplitPacketDev P = pk[i];
+        const LNodeDev L = level[i];
+        const bool split = P.found && fr < n_split;
+        if (split) {
+            const uint32_t s = fr;
+            const uint32_t lid = S0.tree_size + 2 * s, rid = lid + 1;
+            const double gl = (double)P.left[0] * G.sp.inv_g, hl = (double)P.left[1] * G.sp.inv_h;
+            const double gr = (double)P.right[0] * G.sp.inv_g,
+                         hr = (double)P.right[1] * G.sp.inv_h;
+            const float wl = apply_bounds(xgb_weight(gl, hl, G.sp), L.lower, L.upper);
+            const float wr = apply_bounds(xgb_weight(gr, hr, G.sp), L.lower, L.upper);
+            const int mono = monotone[P.feat];
+            const float mid = (wl + wr) / 2.0f;
+            float llo = L.lower, lhi = L.upper, rlo = L.lower, rhi = L.upper;
+            if (mono < 0) {
+                llo = mid;
+                rhi = mid;
+            } else if (mono > 0) {
+                lhi = mid;
+                rlo = mid;
+            }
+            TreeNodeDev t = tree[L.tree_id];
+            t.feat = P.feat;
+            t.bin = P.bin;
+            t.left = (int32_t)lid;
+            t.right = (int32_t)rid;
+            t.leaf_value = 0.0f;
+            t.gain = P.gain;
+            t.flags = (P.missing_left ? 2u : 0u) | (P.is_cat ? 4u : 0u);
+            t.cat_off = S0.tree_cat_words + s * G.cw;
+            t.n_cat_words = P.is_cat ? P.n_cat_words : 0u;
+            for (uint32_t w = 0; w < t.n_cat_words; w++)
+                tree_cats[t.cat_off + w] = pk_cats[P.cat_offset + w];
+            tree[L.tree_id] = t;
+            TreeNodeDev a{}, b{};
+            a.left = a.right = b.left = b.right = -1;
+            a.flags = b.flags = 1;
+            a.leaf_value = wl * G.learning_rate;
+            a.sum_hess = (float)hl;
+            b.leaf_value = wr * G.learning_rate;
+            b.sum_hess = (float)hr;
+            tree[lid] = a;
+            tree[rid] = b;
+            const DevColumn col = cols[P.feat];
+            PartReqDev q{};
+            q.row_off = L.row_off;
+            q.row_len = L.row_len;
+            q.chunk_begin = cb;
+            q.count_base = cb;
+            q.n_chunks = (L.row_len + PART_CHUNK - 1) / PART_CHUNK;
+            q.data = col.data;
+            q.stride = col.width;
+            q.byte_off = 0;
+            q.width = col.width;
+            q.bin = P.bin;
+            q.missing_left = P.missing_left;
+            q.cat_off = P.cat_offset;
+            q.n_cat_words = P.is_cat ? P.n_cat_words : 0u;
+            reqs[s] = q;
+            cb += q.n_chunks;
+            PairDev d{};
+            d.req = L.row_len ? s : NO_SLOT;
+            d.row_off = L.row_off;
+            d.row_len = L.row_len;
+            d.parent_slot = L.slot;
+            d.new_slot = evaluated ? (uint32_t)freelist[s] : NO_SLOT;
+            d.eval_index = evaluated ? s : NO_SLOT;
+            d.lower[0] = llo;
+            d.lower[1] = rlo;
+            d.upper[0] = lhi;
+            d.upper[1] = rhi;
+            d.left_sum[0] = P.left[0];
+            d.left_sum[1] = P.left[1];
+            d.right_sum[0] = P.right[0];
+            d.right_sum[1] = P.right[1];
+            d.left_id = lid;
+            d.right_id = rid;
+            pairs[s] = d;
+            if (evaluated) {
+                triples[3 * s] = L.slot;
+                triples[3 * s + 1] = L.slot;
+                triples[3 * s + 2] = freelist[s];
+            }
+        } else if (L.row_len) {
+            const uint32_t k = S0.n_leaves + lr++;
+            LeafDev lf{};
+            lf.row_off = L.row_off;
+            lf.row_len = L.row_len;
+            lf.value = tree[L.tree_id].leaf_value;
+            lf.id = k;
+            leaves[k] = lf;
+            leaf_vals[k] = lf.value;
+        }
+        if (P.found) fr++;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        GrowState s = S0;
+        s.n_split = n_split;
+        s.part_chunks = tot_chunks;
+        s.n_eval = evaluated ? n_split : 0u;
+        s.tree_size = S0.tree_size + 2 * n_split;
+        s.leaf_count = leaf_count;
+        s.n_leaves = S0.n_leaves + tot_leaves;
+        s.tree_cat_words = S0.tree_cat_words + n_split * G.cw;
+        s.error = S0.error | (slots_short ? 1u : 0u);
+        *st = s;
+    }
+}
+
+hipError_t launch_grow_decide(const GrowParamsDev &G, uint32_t depth, const SplitPacketDev *pk,
+                              const uint64_t *pk_cats, const LNodeDev *level, TreeNodeDev *tree,
+                              uint64_t *tree_cats, const int8_t *monotone, const DevColumn *cols,
+                              PartReqDev *reqs, PairDev *pairs, uint32_t *triples,
+                              LeafDev *leaves, float *leaf_vals, GrowState *st, hipStream_t s) {
+    if (G.n_slots > MAX_GROW_SLOTS) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(grow_decide_kernel, dim3(1), dim3(1024), 0, s, G, depth, pk, pk_cats, level,
+                       tree, tree_cats, monotone, cols, reqs, pairs, triples, leaves, leaf_vals,
+                       st);
+    return hipGetLastError();
+}
+
+// Chunk layout of the finished leaf table and the rows it covers.
+__global__ __launch_bounds__(1024) void leaf_plan_kernel(LeafDev *leaves, GrowState *st) {
+    __shared__ uint32_t buf[1024];
+    __shared__ unsigned long long cov_sh;
+    const uint32_t n = st->n_leaves;
+    if (threadIdx.x == 0) cov_sh = 0;
+    const uint32_t per = (n + 1023) / 1024;
+    const uint32_t i0 = min(threadIdx.x * per, n), i1 = min(i0 + per, n);
+    uint32_t nc = 0;
+    unsigned long long cov = 0;
+    for (uint32_t i = i0; i < i1; i++) {
+        nc += (leaves[i].row_len + PART_CHUNK - 1) / PART_CHUNK;
+        cov += leaves[i].row_len;
+    }
+    uint32_t total;
+    uint32_t cb = block_scan_1024(nc, buf, total);
+    for (uint32_t i = i0; i < i1; i++) {
+        leaves[i].chunk_begin = cb;
+        cb += (leaves[i].row_len + PART_CHUNK - 1) / PART_CHUNK;
+    }
+    atomicAdd(&cov_sh, cov);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        st->leaf_chunks = total;
+        st->covered = cov_sh;
+    }
+}
+
+hipError_t launch_leaf_plan(LeafDev *leaves, GrowState *st, hipStream_t s) {
+    hipLaunchKernelGGL(leaf_plan_kernel, dim3(1), dim3(1024), 0, s, leaves, st);
+    return hipGetLastError();
 }
 
 }  // namespace fbh

@@ -264,6 +264,9 @@ class Grower {
                1.0 / scales[1]};
         leaves_spans_.clear();
         leaves_values_.clear();
+        if (device_trees_ && p_.grow_policy == 0 && p_.max_depth >= 1 && p_.max_depth <= 14 &&
+            p_.max_leaves != 1)
+            return grow_on_device(root_sum);
         Tree t;
         double g, h;
         lm_.to_f64(root_sum, g, h);
@@ -286,6 +289,8 @@ class Grower {
     // Leaf values of the last grown tree, by leaf position.
     const std::vector<float> &leaf_values() const { return leaves_values_; }
     uint32_t n_rows_ = 0;
+    bool device_trees_ = false;  // depthwise trees grow whole on the device
+    uint32_t device_trees = 0;   // trees grown that way
 
   private:
     struct Pending {
@@ -337,6 +342,45 @@ class Grower {
         return out;
     }
 
+    // split_threshold (tree.rs:991-1001): the cut below the split bin.
+    float cond_of(uint32_t feat, uint32_t bin) const {
+        const uint32_t nc = cuts_.n_cuts(feat);
+        if (bin == 0) return -std::numeric_limits<float>::max();
+        if (bin > nc) return std::numeric_limits<float>::max();
+        return cuts_.values[cuts_.offsets[feat] + bin - 1];
+    }
+
+    // A depthwise tree grown whole by fbh_grow_depthwise, rebuilt here with
+    // Tree::split_leaf in node-id order (the order the device numbered it).
+    Tree grow_on_device(const int64_t root_sum[2]) {
+        fbh_grow_params gp{p_.max_depth, p_.max_leaves, p_.learning_rate, 0};
+        const uint32_t cap_nodes = (2u << p_.max_depth) - 1, cap_leaves = 1u << p_.max_depth;
+        std::vector<fbh_tree_node> tn(cap_nodes);
+        std::vector<uint64_t> cats((size_t)std::max<uint32_t>(1, cat_cap_) * cap_leaves);
+        leaves_values_.assign(cap_leaves, 0.0f);
+        uint32_t nn = 0, nl = 0;
+        call(fbh_grow_depthwise(ctx_, &gp, &sp_, root_sum, tn.data(), cap_nodes, &nn, cats.data(),
+                                (uint32_t)cats.size(), leaves_values_.data(), cap_leaves, &nl));
+        leaves_values_.resize(nl);
+        Tree t;
+        t.push_leaf(tn[0].leaf_value, tn[0].sum_hess);
+        for (uint32_t id = 0; id < nn; id++) {
+            const fbh_tree_node &a = tn[id];
+            if (a.flags & 1u) continue;
+            const fbh_tree_node &l = tn[a.left], &r = tn[a.right];
+            const bool is_cat = (a.flags & 4u) != 0;
+            const auto lr = t.split_leaf(id, a.feat, is_cat ? 0.0f : cond_of(a.feat, a.bin),
+                                         (a.flags & 2u) != 0, a.gain, l.leaf_value, l.sum_hess,
+                                         r.leaf_value, r.sum_hess);
+            if (lr.first != (uint32_t)a.left || lr.second != (uint32_t)a.right)
+                throw RuntimeError("device tree nodes out of order");
+            if (is_cat) t.set_categories(id, cats.data() + a.cat_offset, a.n_cat_words);
+        }
+        if (t.nodes.size() != nn) throw RuntimeError("device tree node count mismatch");
+        device_trees++;
+        return t;
+    }
+
     // Tree::split_leaf with child_leaves (src/training/mod.rs:5069-5094).
     void apply(Tree &t, uint32_t node, const fbh_split &s, const uint64_t *cats, Bounds parent,
                uint32_t &l, uint32_t &r, Bounds &lb, Bounds &rb) {
@@ -356,13 +400,7 @@ class Grower {
             lb.hi = mid;
             rb.lo = mid;
         }
-        float cond = 0.0f;
-        if (!s.is_cat) {  // split_threshold (tree.rs:991-1001)
-            const uint32_t nc = cuts_.n_cuts(s.feat);
-            if (s.bin == 0) cond = -std::numeric_limits<float>::max();
-            else if (s.bin > nc) cond = std::numeric_limits<float>::max();
-            else cond = cuts_.values[cuts_.offsets[s.feat] + s.bin - 1];
-        }
+        const float cond = s.is_cat ? 0.0f : cond_of(s.feat, s.bin);
         auto lr = t.split_leaf(node, s.feat, cond, s.missing_left != 0, s.gain,
                                wl * p_.learning_rate, lm_.hess(s.left), wr * p_.learning_rate,
                                lm_.hess(s.right));
@@ -752,6 +790,12 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     std::vector<float> pred(n, margin);
     Grower grower(ctx.get(), p, m.cuts, mono, slots);
     grower.n_rows_ = (uint32_t)n;
+    {
+        fbh_plan plan{};
+        call(fbh_ctx_plan(ctx.get(), &plan));
+        grower.device_trees_ = !p.host_levels && plan.columns_resident &&
+                               plan.resident_tiles == plan.n_tiles && slots <= 16384;
+    }
     const uint32_t obj = p.objective;
     call(fbh_set_objective(ctx.get(), obj, y, grad_w, margin));
     SigmoidJob job{&pool, pred.data(), &grower.leaf_values()};
@@ -797,6 +841,7 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     if (p.n_rounds > 0) close_round(p.n_rounds - 1);
     g_stats.train_seconds = std::chrono::duration<double>(Clock::now() - t_train).count();
     g_stats.host_gradient_seconds = grad_s;
+    g_stats.device_trees = grower.device_trees;
     g_stats.rounds = p.n_rounds;
     g_stats.device_sigmoid = dev_sigmoid ? 1 : 0;
     {

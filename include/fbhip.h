@@ -308,6 +308,41 @@ int fbh_partition_eval(fbh_ctx *ctx, const fbh_part_req *reqs, uint32_t n_reqs,
                        fbh_span *children, uint32_t *left_slot, fbh_split *out,
                        uint64_t *cat_out, uint32_t cat_capacity);
 
+/* One node of a tree grown on the device, in the order the host grower
+ * numbers them (Tree::split_leaf, src/model/tree.rs:140-170). */
+typedef struct fbh_tree_node {
+    uint32_t feat, bin;   /* split: feature and bin as in fbh_split */
+    int32_t left, right;  /* child ids, -1 for a leaf */
+    float leaf_value;     /* learning rate applied; 0 for a split node */
+    float sum_hess;
+    float gain;
+    uint32_t flags;       /* bit 0 leaf, bit 1 missing goes left, bit 2 categorical */
+    uint32_t cat_offset;  /* right-going category set: cat_words[cat_offset..+n_cat_words] */
+    uint32_t n_cat_words;
+    uint32_t reserved[2];
+} fbh_tree_node;
+
+typedef struct fbh_grow_params {
+    uint32_t max_depth;   /* 1..=14 */
+    uint32_t max_leaves;  /* 0: unlimited */
+    float learning_rate;
+    uint32_t reserved;
+} fbh_grow_params;
+
+/* A whole depthwise tree on the device (build_tree, src/training/mod.rs:
+ * 3357-4565, driving the calls fbh_eval_nodes / fbh_partition_eval /
+ * fbh_assign_leaves stand for), enqueued level after level without waiting
+ * on the host: the max_leaves budget, node ids, leaf weights, monotone
+ * bounds, partitions, histogram slots and the leaf assignment are decided
+ * by kernels, and one copy brings the tree back. The root sum is the one
+ * the gradient call returned; every tile and column must be resident. Leaf
+ * values come back in leaf-id order (the ids fbh_gradient_exchange hands to
+ * a host sigmoid callback). */
+int fbh_grow_depthwise(fbh_ctx *ctx, const fbh_grow_params *grow, const fbh_split_params *params,
+                       const int64_t root_sum[2], fbh_tree_node *nodes, uint32_t node_capacity,
+                       uint32_t *n_nodes, uint64_t *cat_words, uint32_t cat_capacity,
+                       float *leaf_values, uint32_t leaf_capacity, uint32_t *n_leaves);
+
 /* GpuTrainCtx::assign_leaf_values (src/backend/cuda/train_ctx.rs:2128-2252):
  * delta[row] = value for every row of each span. */
 int fbh_assign_leaves(fbh_ctx *ctx, const fbh_span *spans, const float *values, uint32_t n);

@@ -59,7 +59,10 @@ typedef struct {
     uint32_t host_sigmoid;     /* 1: logistic sigmoid on the host every round
                                   (0: on the device once it matches the host
                                   libm on the probe inputs) */
-    uint32_t reserved2[2];
+    uint32_t host_levels;      /* 1: depthwise trees grow level by level from
+                                  the host (0: whole trees on the device when
+                                  every tile and column is resident) */
+    uint32_t reserved2;
 } fbt_params;
 
 /* One tree node: Node (src/model/tree.rs:52-111). */
@@ -94,6 +97,8 @@ typedef struct {
     uint64_t streamed_bytes;  /* host-to-device bytes of streamed records and columns */
     uint64_t planned_bytes;   /* peak_bytes of the plan */
     uint64_t budget_bytes;    /* the budget the plan honoured */
+    uint32_t device_trees;    /* trees grown whole on the device (fbh_grow_depthwise) */
+    uint32_t reserved;
 } fbt_stats;
 
 typedef struct fbt_model fbt_model;

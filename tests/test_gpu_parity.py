@@ -219,6 +219,57 @@ def test_sampled_weighted_rounds_match_oracle(fb, oracle, objective, depth, host
     assert np.array_equal(pm.train_margins(n).view(np.uint32), om.train_margins(n).view(np.uint32))
 
 
+@pytest.mark.parametrize("case", ["budget", "monotone", "categorical", "sampled_deep", "stump",
+                                  "squared"])
+def test_device_grown_trees_match_host_levels_and_oracle(fb, oracle, case):
+    """Whole depthwise trees grown on the device (the max_leaves budget, node
+    ids, weights, bounds, slots, partitions and leaves decided by kernels)
+    equal the trees the host grows level by level and the CPU oracle's, node
+    for node, with margins equal bit for bit."""
+    rng = np.random.default_rng(sum(map(ord, case)))
+    n, nf = 30_011, 6
+    x = rng.normal(size=(n, nf)).astype(np.float32)
+    x[rng.random((n, nf)) < 0.04] = np.nan
+    z = np.nan_to_num(x[:, 0]) - 0.8 * np.nan_to_num(x[:, 1]) + 0.5 * np.nan_to_num(x[:, 2]) ** 2
+    y = (z + 0.4 * rng.normal(size=n) > 0.3).astype(np.float32)
+    p = {"n_rounds": 5, "max_depth": 6, "eta": 0.3, "max_bin": 64,
+         "objective": "binary:logistic"}
+    w = None
+    mono = None
+    cat = None
+    if case == "budget":
+        p.update(max_leaves=11)
+    elif case == "monotone":
+        mono = [1, -1, 0, 1, 0, 0]
+    elif case == "categorical":
+        x[:, 5] = rng.integers(0, 40, n)
+        y = ((x[:, 5] % 3 == 1) | (np.nan_to_num(x[:, 0]) > 1)).astype(np.float32)
+        cat = [0, 0, 0, 0, 0, 1]
+    elif case == "sampled_deep":
+        p.update(max_depth=10, subsample=0.6, seed=3, min_child_weight=0.3)
+        w = rng.uniform(0.5, 2.0, size=n).astype(np.float32)
+    elif case == "stump":
+        p.update(max_depth=1)
+    elif case == "squared":
+        p.update(objective="reg:squarederror")
+        y = z.astype(np.float32)
+    om = oracle.train(x, y, oracle.make_params(**p), weights=w, monotone=mono, categorical=cat)
+    pp = product_params(p)
+    if mono:
+        pp["monotone_constraints"] = mono
+    if cat:
+        pp["feature_types"] = ["c" if c else "q" for c in cat]
+    dev = fb.train(pp, x, y, weight=w, num_boost_round=p["n_rounds"])
+    host = fb.train(dict(pp, hip_host_levels=True), x, y, weight=w, num_boost_round=p["n_rounds"])
+    assert dev.stats["device_trees"] == p["n_rounds"]
+    assert host.stats["device_trees"] == 0
+    assert_same_models(om, dev)
+    assert_same_models(om, host)
+    want = om.train_margins(n).view(np.uint32)
+    assert np.array_equal(dev.train_margins(n).view(np.uint32), want)
+    assert np.array_equal(host.train_margins(n).view(np.uint32), want)
+
+
 @pytest.mark.parametrize("max_bin", [255, 256])
 def test_plumbing_config_matches_oracle(fb, oracle, max_bin):
     X, y, params, _ = _synthetic("plumbing", 30_000)
