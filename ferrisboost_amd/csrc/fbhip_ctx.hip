@@ -1248,6 +1248,7 @@ struct EvalPlan {
     // are then upper bounds that size the grids).
     const uint32_t *dev_n_hn = nullptr, *dev_n_tri = nullptr, *dev_n_nodes = nullptr;
     bool download = true;  // copy the packets back (a device-grown tree reads them in place)
+    const uint32_t *rows = nullptr;  // arena of the accumulated nodes (null: the row arena)
 };
 
 void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
@@ -1279,7 +1280,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
             L.chunk_rows = E.chunk_rows;
             L.dev_chunk_rows = E.dev_chunk_rows;
             L.chunk_groups = div_up(E.grid_chunks, XCDS);
-            L.rows = c->rows;
+            L.rows = E.rows ? E.rows : c->rows;
             L.gpair = c->gpair;
             L.hist = c->hist;
             L.hist_width = c->hist_width;
@@ -1905,11 +1906,15 @@ int fbh_grow_depthwise(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_pa
                                      GB.tree_cats, d_mono, GB.cols, GB.reqs, GB.pairs,
                                      GB.triples, GB.leaves, GB.leaf_vals, GB.st, c->stream),
                   "tree level decision");
+            // Level d's rows are in arena d % 2; its children go to the other.
+            uint32_t *arena_in = (d & 1) ? c->tmp : c->rows;
+            uint32_t *arena_out = (d & 1) ? c->rows : c->tmp;
             check(launch_partition_dev(GB.reqs, &GB.st->n_split, n_rows / PART_CHUNK + nb + 1,
-                                       c->rows, c->tmp, c->flags, c->d_counts, c->d_excl,
+                                       arena_in, arena_out, c->flags, c->d_counts, c->d_excl,
                                        c->d_totals, pk_cats, c->stream),
                   "partition");
-            const GrowDevOut out{GB.st, GB.level[(d + 1) & 1], GB.tree, GB.leaves, GB.leaf_vals};
+            const GrowDevOut out{GB.st, GB.level[(d + 1) & 1], GB.tree, GB.leaves, GB.leaf_vals,
+                                 (d + 1) & 1u};
             check(launch_level_plan(GB.pairs, nb, c->d_totals, rule, c->d_lvl_hist,
                                     c->d_lvl_split, c->d_lvl_out, c->d_lvl_out + 4 * MAX_NODES,
                                     c->d_lvl_rows, out, c->stream),
@@ -1929,6 +1934,7 @@ int fbh_grow_depthwise(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_pa
             E.n_nodes = lvl_bound(d + 1);
             E.dev_n_nodes = &GB.st->n_level;
             E.download = false;
+            E.rows = arena_out;
             enqueue_eval(c, E, sp);
         }
         check(launch_leaf_plan(GB.leaves, GB.st, c->stream), "leaf plan");
@@ -1936,7 +1942,7 @@ int fbh_grow_depthwise(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_pa
         if (gp->max_leaves) leaf_bound = std::min<uint64_t>(leaf_bound, gp->max_leaves);
         const int idb = c->objective >= 0 ? (leaf_bound <= 256 ? 1 : 2) : 0;
         check(launch_assign_leaves(GB.leaves, 0, (uint32_t)(n_rows / PART_CHUNK + leaf_bound + 1),
-                                   c->rows, c->delta, c->leaf_ids, idb, &GB.st->n_leaves,
+                                   c->rows, c->tmp, c->delta, c->leaf_ids, idb, &GB.st->n_leaves,
                                    c->stream),
               "leaf assignment");
         if (idb)
@@ -2007,6 +2013,7 @@ int fbh_assign_leaves(fbh_ctx *c, const fbh_span *spans, const float *values, ui
             ld[m].chunk_begin = chunks;
             ld[m].value = values[i];
             ld[m].id = i;
+            ld[m].arena = 0;
             chunks += div_up(spans[i].len, PART_CHUNK);
             m++;
         }
@@ -2021,9 +2028,8 @@ int fbh_assign_leaves(fbh_ctx *c, const fbh_span *spans, const float *values, ui
         const float *d_vals = reinterpret_cast<const float *>(c->d_leaves + m);
         check(hipEventRecord(c->leaves_done, c->stream), "event");
         c->leaves_pending = true;
-        check(launch_assign_leaves(c->d_leaves, m, chunks, c->rows, c->delta, c->leaf_ids, idb,
-                                   nullptr,
-                                   c->stream),
+        check(launch_assign_leaves(c->d_leaves, m, chunks, c->rows, c->rows, c->delta,
+                                   c->leaf_ids, idb, nullptr, c->stream),
               "leaf assignment");
         if (idb)
             check(launch_apply_leaves(c->leaf_ids, idb, d_vals, c->n_rows, c->margin, c->stream),

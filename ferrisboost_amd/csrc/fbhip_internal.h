@@ -205,7 +205,8 @@ struct ChunkRule {
 struct LeafDev {
     uint32_t row_off, row_len, chunk_begin;
     float value;
-    uint32_t id;  // position of the leaf in the caller's list
+    uint32_t id;     // position of the leaf in the caller's list
+    uint32_t arena;  // 0: the row arena, 1: the second arena (device-grown trees)
 };
 
 // Flattened ensemble for TreeSHAP.
@@ -229,6 +230,7 @@ struct GrowDevOut {
     const TreeNodeDev *tree;
     LeafDev *leaves;
     float *leaf_vals;
+    uint32_t child_arena;      // arena holding the rows of this level's children
 };
 
 // Last-error message shared by every fbh_* entry point (thread local).
@@ -283,12 +285,14 @@ hipError_t launch_split_nodes(const FeatCandDev *cands, const SplitFeatDev *feat
 hipError_t launch_partition_count(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
                                   const uint32_t *rows, uint8_t *flags, uint32_t *chunk_counts,
                                   const uint64_t *cat_words, hipStream_t s);
-// All four passes over requests planned on the device: dev = {requests,
-// chunks}; grid_chunks is an upper bound of the chunks.
+// Count, scan and stable scatter over requests planned on the device: dev =
+// {requests, chunks}; grid_chunks is an upper bound of the chunks. The
+// children land in rows_out at their parents' positions (no copy back: the
+// arenas alternate by level).
 hipError_t launch_partition_dev(const PartReqDev *reqs, const uint32_t *dev, uint32_t grid_chunks,
-                                uint32_t *rows, uint32_t *tmp, uint8_t *flags, uint32_t *counts,
-                                uint32_t *excl, uint32_t *totals, const uint64_t *cat_words,
-                                hipStream_t s);
+                                const uint32_t *rows_in, uint32_t *rows_out, uint8_t *flags,
+                                uint32_t *counts, uint32_t *excl, uint32_t *totals,
+                                const uint64_t *cat_words, hipStream_t s);
 // Passes 2-4 (scan, stable scatter, copy back) over all requests of the call.
 hipError_t launch_partition_finish(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
                                    uint32_t *rows, uint32_t *tmp, const uint8_t *flags,
@@ -299,8 +303,8 @@ hipError_t launch_partition_finish(const PartReqDev *reqs, uint32_t n_reqs, uint
 // dev (nullable): {leaf count, chunks} read on the device; n_chunks is then
 // the grid's upper bound.
 hipError_t launch_assign_leaves(const LeafDev *leaves, uint32_t n_leaves, uint32_t n_chunks,
-                                const uint32_t *rows, float *delta, void *ids, int id_bytes,
-                                const uint32_t *dev, hipStream_t s);
+                                const uint32_t *rows, const uint32_t *rows_alt, float *delta,
+                                void *ids, int id_bytes, const uint32_t *dev, hipStream_t s);
 // margin[row] += values[ids[row]] over all rows (id_bytes 1 or 2).
 hipError_t launch_apply_leaves(const void *ids, int id_bytes, const float *values, uint64_t n,
                                float *margin, hipStream_t s);

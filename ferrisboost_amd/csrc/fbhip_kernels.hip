@@ -385,19 +385,32 @@ hipError_t launch_zero_nodes(int64_t *hist, uint64_t width, const HistNodeDev *n
 
 // Exclusive scan of v over the 1024 threads of the block (carry added by the
 // caller); returns this thread's prefix and sets total.
-__device__ uint32_t block_scan_1024(uint32_t v, uint32_t *buf, uint32_t &total) {
-    buf[threadIdx.x] = v;
-    __syncthreads();
-    for (uint32_t off = 1; off < 1024; off <<= 1) {
-        const uint32_t a = threadIdx.x >= off ? buf[threadIdx.x - off] : 0;
-        __syncthreads();
-        buf[threadIdx.x] += a;
-        __syncthreads();
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+    const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t t = __shfl_up(v, off, 64);
+        if (lane >= (uint32_t)off) v += t;
     }
-    const uint32_t incl = buf[threadIdx.x];
-    total = buf[1023];
+    return v;
+}
+
+// Wave scans by shuffles, then one wave scans the 16 wave totals (buf needs
+// 32 entries).
+__device__ uint32_t block_scan_1024(uint32_t v, uint32_t *buf, uint32_t &total) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t incl = wave_incl_scan(v);
+    if (lane == 63) buf[wave] = incl;
     __syncthreads();
-    return incl - v;
+    if (wave == 0) {
+        const uint32_t w = wave_incl_scan(lane < 16 ? buf[lane] : 0u);
+        if (lane < 16) buf[16 + lane] = w;
+    }
+    __syncthreads();
+    const uint32_t before = wave ? buf[16 + wave - 1] : 0u;
+    total = buf[31];
+    __syncthreads();
+    return before + incl - v;
 }
 
 // One workgroup plans the children of a fused partition + evaluation step
@@ -529,6 +542,7 @@ __global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, 
                         lf.row_len = lens[c];
                         lf.value = D.tree[ids[c]].leaf_value;
                         lf.id = k;
+                        lf.arena = D.child_arena;
                         D.leaves[k] = lf;
                         D.leaf_vals[k] = lf.value;
                         k++;
@@ -1049,31 +1063,23 @@ __global__ __launch_bounds__(1024) void part_scan_kernel(const uint32_t *counts,
                                                          uint32_t *excl, const PartReqDev *reqs,
                                                          uint32_t n_reqs, uint32_t *totals,
                                                          const uint32_t *dev) {
-    __shared__ uint32_t buf[1024];
-    __shared__ uint32_t carry;
+    __shared__ uint32_t buf[32];
     if (dev) {
         n_reqs = dev[0];
         n_chunks = dev[1];
     }
-    if (threadIdx.x == 0) carry = 0;
-    __syncthreads();
-    for (uint32_t base = 0; base < n_chunks; base += 1024) {
-        const uint32_t i = base + threadIdx.x;
-        const uint32_t v = i < n_chunks ? counts[i] : 0;
-        buf[threadIdx.x] = v;
-        __syncthreads();
-        for (uint32_t off = 1; off < 1024; off <<= 1) {
-            uint32_t a = threadIdx.x >= off ? buf[threadIdx.x - off] : 0;
-            __syncthreads();
-            buf[threadIdx.x] += a;
-            __syncthreads();
-        }
-        if (i < n_chunks) excl[i] = carry + buf[threadIdx.x] - v;
-        __syncthreads();
-        if (threadIdx.x == 0) carry += buf[1023];
-        __syncthreads();
+    // Each thread a run of chunks: one block scan of the run sums.
+    const uint32_t per = (n_chunks + 1023) / 1024;
+    const uint32_t c0 = min(threadIdx.x * per, n_chunks), c1 = min(c0 + per, n_chunks);
+    uint32_t sum = 0;
+    for (uint32_t i = c0; i < c1; i++) sum += counts[i];
+    uint32_t total;
+    uint32_t run = block_scan_1024(sum, buf, total);
+    for (uint32_t i = c0; i < c1; i++) {
+        excl[i] = run;
+        run += counts[i];
     }
-    if (threadIdx.x == 0) excl[n_chunks] = carry;
+    if (threadIdx.x == 0) excl[n_chunks] = total;
     __syncthreads();
     for (uint32_t r = threadIdx.x; r < n_reqs; r += 1024)
         totals[r] = excl[reqs[r].chunk_begin + reqs[r].n_chunks] - excl[reqs[r].chunk_begin];
@@ -1149,18 +1155,16 @@ hipError_t launch_partition_count(const PartReqDev *reqs, uint32_t n_reqs, uint3
 }
 
 hipError_t launch_partition_dev(const PartReqDev *reqs, const uint32_t *dev, uint32_t grid_chunks,
-                                uint32_t *rows, uint32_t *tmp, uint8_t *flags, uint32_t *counts,
-                                uint32_t *excl, uint32_t *totals, const uint64_t *cat_words,
-                                hipStream_t s) {
+                                const uint32_t *rows_in, uint32_t *rows_out, uint8_t *flags,
+                                uint32_t *counts, uint32_t *excl, uint32_t *totals,
+                                const uint64_t *cat_words, hipStream_t s) {
     if (grid_chunks == 0) return hipSuccess;
-    hipLaunchKernelGGL(part_count_kernel, dim3(grid_chunks), dim3(PART_TPB), 0, s, reqs, 0u, rows,
-                       flags, counts, cat_words, dev);
+    hipLaunchKernelGGL(part_count_kernel, dim3(grid_chunks), dim3(PART_TPB), 0, s, reqs, 0u,
+                       rows_in, flags, counts, cat_words, dev);
     hipLaunchKernelGGL(part_scan_kernel, dim3(1), dim3(1024), 0, s, counts, 0u, excl, reqs, 0u,
                        totals, dev);
     hipLaunchKernelGGL(part_scatter_kernel, dim3(grid_chunks), dim3(PART_TPB), 0, s, reqs, 0u,
-                       rows, flags, excl, totals, tmp, dev);
-    hipLaunchKernelGGL(part_copy_kernel, dim3(grid_chunks), dim3(PART_TPB), 0, s, reqs, 0u, tmp,
-                       rows, dev);
+                       rows_in, flags, excl, totals, rows_out, dev);
     return hipGetLastError();
 }
 
@@ -1195,7 +1199,8 @@ __device__ __forceinline__ uint64_t rotl64(uint64_t x, int r) { return (x << r) 
 // as u8 / u16 (the margins are then updated in row order by apply_leaves).
 template <int IDB>
 __global__ __launch_bounds__(PART_TPB) void leaf_kernel(const LeafDev *leaves, uint32_t n,
-                                                        const uint32_t *rows, float *delta,
+                                                        const uint32_t *rows,
+                                                        const uint32_t *rows_alt, float *delta,
                                                         void *ids, const uint32_t *dev) {
     const uint32_t chunk = blockIdx.x;
     if (dev) {  // a device-grown tree: leaf count and chunks on the device
@@ -1211,8 +1216,9 @@ __global__ __launch_bounds__(PART_TPB) void leaf_kernel(const LeafDev *leaves, u
     const LeafDev L = leaves[lo];
     const uint32_t c0 = (chunk - L.chunk_begin) * PART_CHUNK;
     const uint32_t c1 = min(c0 + PART_CHUNK, L.row_len);
+    const uint32_t *rr = L.arena ? rows_alt : rows;
     for (uint32_t i = c0 + threadIdx.x; i < c1; i += PART_TPB) {
-        const uint32_t r = rows[L.row_off + i];
+        const uint32_t r = rr[L.row_off + i];
         if (IDB == 0) delta[r] = L.value;
         if (IDB == 1) static_cast<uint8_t *>(ids)[r] = (uint8_t)L.id;
         if (IDB == 2) static_cast<uint16_t *>(ids)[r] = (uint16_t)L.id;
@@ -1233,18 +1239,18 @@ __global__ __launch_bounds__(256) void apply_leaves_kernel(const void *ids, cons
 }
 
 hipError_t launch_assign_leaves(const LeafDev *leaves, uint32_t n_leaves, uint32_t n_chunks,
-                                const uint32_t *rows, float *delta, void *ids, int id_bytes,
-                                const uint32_t *dev, hipStream_t s) {
+                                const uint32_t *rows, const uint32_t *rows_alt, float *delta,
+                                void *ids, int id_bytes, const uint32_t *dev, hipStream_t s) {
     if (n_chunks == 0) return hipSuccess;
     if (id_bytes == 1)
         hipLaunchKernelGGL(leaf_kernel<1>, dim3(n_chunks), dim3(PART_TPB), 0, s, leaves, n_leaves,
-                           rows, delta, ids, dev);
+                           rows, rows_alt, delta, ids, dev);
     else if (id_bytes == 2)
         hipLaunchKernelGGL(leaf_kernel<2>, dim3(n_chunks), dim3(PART_TPB), 0, s, leaves, n_leaves,
-                           rows, delta, ids, dev);
+                           rows, rows_alt, delta, ids, dev);
     else
         hipLaunchKernelGGL(leaf_kernel<0>, dim3(n_chunks), dim3(PART_TPB), 0, s, leaves, n_leaves,
-                           rows, delta, ids, dev);
+                           rows, rows_alt, delta, ids, dev);
     return hipGetLastError();
 }
 
@@ -1928,6 +1934,7 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
             lf.row_len = L.row_len;
             lf.value = tree[L.tree_id].leaf_value;
             lf.id = k;
+            lf.arena = depth & 1u;
             leaves[k] = lf;
             leaf_vals[k] = lf.value;
         }
