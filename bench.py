@@ -106,7 +106,10 @@ def train_workload(args, X, y, params, desc: str, traffic_tag: str):
     from ferrisboost_amd import _native as N
 
     rounds = args.warmup + args.steps
-    gparams = dict(params, device="cuda:0", hip_profile=True)
+    # The round loop collects each tree a round late; hip_sync_round makes it
+    # wait for the device before the first timed round, so the timed rounds
+    # are bracketed by device synchronisation on both sides.
+    gparams = dict(params, device="cuda:0", hip_profile=True, hip_sync_round=args.warmup)
     t0 = time.time()
     model = fb.train(gparams, X, y, num_boost_round=rounds)
     log(f"trained {rounds} rounds in {time.time() - t0:.1f}s "
@@ -195,7 +198,8 @@ def streaming_workload(args):
     budget = 4 << 30
     rounds = args.warmup + args.steps
     t0 = time.time()
-    model = fb.train(dict(params, device="cuda:0", gpu_memory_budget=budget, hip_profile=True),
+    model = fb.train(dict(params, device="cuda:0", gpu_memory_budget=budget, hip_profile=True,
+                          hip_sync_round=args.warmup),
                      X, y, num_boost_round=rounds)
     st = model.stats
     log(f"trained {rounds} rounds in {time.time() - t0:.1f}s (setup {st['setup_seconds']:.1f}s); "

@@ -75,6 +75,7 @@ _DEFAULTS: dict[str, Any] = {
     "hip_profile": False,
     "hip_host_sigmoid": False,
     "hip_host_levels": False,
+    "hip_sync_round": 0,
 }
 
 _ALIASES = {
@@ -192,6 +193,7 @@ def _params_struct(p: dict[str, Any], n_features: int) -> N.TrainParams:
     s.profile = 1 if p["hip_profile"] else 0
     s.host_sigmoid = 1 if p["hip_host_sigmoid"] else 0
     s.host_levels = 1 if p["hip_host_levels"] else 0
+    s.sync_round = int(p["hip_sync_round"])
     return s
 
 

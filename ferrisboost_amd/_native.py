@@ -153,7 +153,7 @@ class TrainParams(C.Structure):
         ("profile", C.c_uint32),
         ("host_sigmoid", C.c_uint32),
         ("host_levels", C.c_uint32),
-        ("reserved2", C.c_uint32),
+        ("sync_round", C.c_uint32),
     ]
 
 
@@ -203,7 +203,8 @@ HIP_SYMBOLS = [
     "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_gradient_exchange",
     "fbh_download_margin", "fbh_sigmoid_host", "fbh_sigmoid_device", "fbh_sigmoid_checksum",
     "fbh_begin_tree", "fbh_eval_nodes", "fbh_download_histogram",
-    "fbh_partition", "fbh_partition_eval", "fbh_grow_depthwise", "fbh_assign_leaves", "fbh_download_delta", "fbh_host_alloc",
+    "fbh_partition", "fbh_partition_eval", "fbh_grow_depthwise", "fbh_grow_depthwise_async",
+    "fbh_grow_collect", "fbh_assign_leaves", "fbh_download_delta", "fbh_host_alloc",
     "fbh_host_free", "fbh_download_rows",
     "fbh_hist_timing", "fbh_set_timing", "fbh_build_histogram", "fbh_partition_rows",
     "fbh_shap_model_create", "fbh_shap_model_destroy", "fbh_shap_contribs",

@@ -16,6 +16,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <deque>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -169,6 +170,7 @@ struct fbh_ctx {
 
     float *gpair_f32 = nullptr;
     int64_t *gpair = nullptr;
+    bool root_on_device = false;  // the last quantisation's root sum is on the device
     uint32_t *rows = nullptr, *tmp = nullptr;
     uint8_t *flags = nullptr;
     float *delta = nullptr;
@@ -207,7 +209,16 @@ struct fbh_ctx {
         LeafDev *leaves = nullptr;
         float *leaf_vals = nullptr;
         DevColumn *cols = nullptr;
-        PinnedBuf out;  // state, tree, category words and leaf values coming back
+        // Two result slots (state, tree, category words, leaf values), so a
+        // tree can be collected while the next one is already enqueued.
+        PinnedBuf out[2];
+        hipEvent_t done[2] = {nullptr, nullptr};
+        uint64_t next_slot = 0;
+        struct Job {
+            int slot;
+            uint32_t cat_words;  // category words per node of the tree's features
+        };
+        std::deque<Job> pending;
     } grow;
     size_t off_tilefeats = 0, off_sfeats = 0;  // offsets in the tree-table buffer
     size_t stage_bytes = 0;
@@ -222,6 +233,7 @@ struct fbh_ctx {
     bool leaves_pending = false;
 
     // per tree
+    std::vector<uint8_t> tree_tables;  // the tree tables last sent to the device
     std::vector<uint32_t> tree_feats;
     std::vector<int64_t> hist_off;  // global feature -> compact offset, -1 if not built
     uint64_t hist_width = 0;
@@ -282,8 +294,12 @@ struct fbh_ctx {
         if (pin_small.p) (void)hipHostFree(pin_small.p);
         if (pin_leaves.p) (void)hipHostFree(pin_leaves.p);
         if (pin_out.p) (void)hipHostFree(pin_out.p);
-        if (grow.out.p) (void)hipHostFree(grow.out.p);
-        grow.out.p = nullptr;
+        for (int k = 0; k < 2; k++) {
+            if (grow.out[k].p) (void)hipHostFree(grow.out[k].p);
+            grow.out[k].p = nullptr;
+            if (grow.done[k]) (void)hipEventDestroy(grow.done[k]);
+            grow.done[k] = nullptr;
+        }
         if (pin_ids.p) (void)hipHostFree(pin_ids.p);
         if (pin_src.p) (void)hipHostFree(pin_src.p);
         pin_small.p = pin_leaves.p = pin_out.p = pin_ids.p = pin_src.p = nullptr;
@@ -371,13 +387,21 @@ struct fbh_ctx {
         return (uint32_t)std::min<uint64_t>(std::max<uint64_t>(r, R.min_rows), R.max_rows);
     }
 
+    // Adds the histogram time of every completed launch; pairs still in
+    // flight (a tree enqueued behind the one collected) stay for later.
     void collect_timing() {
+        size_t keep = 0;
         for (size_t i = 0; i < ev_used; i++) {
+            if (hipEventQuery(ev_pool[i].second) != hipSuccess) {
+                std::swap(ev_pool[keep], ev_pool[i]);
+                keep++;
+                continue;
+            }
             float ms = 0.0f;
             if (hipEventElapsedTime(&ms, ev_pool[i].first, ev_pool[i].second) == hipSuccess)
                 hist_ms += ms;
         }
-        ev_used = 0;
+        ev_used = keep;
     }
 };
 
@@ -925,13 +949,15 @@ void quantize_device_pairs(fbh_ctx *c, uint64_t th, uint64_t seed, uint64_t tree
                                 c->red_i64, c->n_red_blocks, c->red_i64 + 2 * c->n_red_blocks,
                                 c->stream),
           "gradient quantisation");
+    c->root_on_device = true;
+    scales_out[0] = c->scales[0];
+    scales_out[1] = c->scales[1];
+    if (!root_out) return;  // the sum stays on the device for fbh_grow_depthwise
     check(hipMemcpyAsync(c->pin_out.p, c->red_i64 + 2 * c->n_red_blocks, 16,
                          hipMemcpyDeviceToHost, c->stream),
           "root sum download");
     c->sync();
     std::memcpy(root_out, c->pin_out.p, 16);
-    scales_out[0] = c->scales[0];
-    scales_out[1] = c->scales[1];
 }
 
 }  // namespace
@@ -987,7 +1013,7 @@ int fbh_set_objective(fbh_ctx *c, uint32_t objective, const float *labels,
 int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th, uint64_t seed,
                           uint64_t tree, double scales_out[2], int64_t root_out[2]) {
     return guard([&] {
-        if (!c || !scales_out || !root_out) throw InputError("null argument");
+        if (!c || !scales_out) throw InputError("null argument");
         if (c->objective < 0) throw InputError("fbh_set_objective has not been called");
         check(hipSetDevice(c->device), "hipSetDevice");
         if (c->leaves_pending) {
@@ -1057,6 +1083,7 @@ int fbh_upload_gpair_fixed(fbh_ctx *c, const int64_t *g2n, const double scales[2
               "gradient upload");
         c->scales[0] = scales[0];
         c->scales[1] = scales[1];
+        c->root_on_device = false;
         c->sync();
     });
 }
@@ -1180,19 +1207,26 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
             sf.push_back(s);
         }
         c->cat_words_per_node = cat_base;
-        uint8_t *st = static_cast<uint8_t *>(c->pin_small.p);
-        std::memcpy(st, td.data(), sizeof(TileDev) * td.size());
-        std::memcpy(st + c->off_tilefeats, tf.data(), sizeof(TileFeatDev) * tf.size());
-        std::memcpy(st + c->off_sfeats, sf.data(), sizeof(SplitFeatDev) * sf.size());
-        check(hipMemcpyAsync(c->d_tiles, st, c->off_sfeats + sizeof(SplitFeatDev) * sf.size(),
-                             hipMemcpyHostToDevice, c->stream),
-              "tree tables");
+        // The tables go up only when they differ from the last tree's (every
+        // tree of a run without column sampling has the same).
+        std::vector<uint8_t> tables(c->off_sfeats + sizeof(SplitFeatDev) * sf.size(), 0);
+        std::memcpy(tables.data(), td.data(), sizeof(TileDev) * td.size());
+        std::memcpy(tables.data() + c->off_tilefeats, tf.data(), sizeof(TileFeatDev) * tf.size());
+        std::memcpy(tables.data() + c->off_sfeats, sf.data(), sizeof(SplitFeatDev) * sf.size());
+        const bool upload = tables != c->tree_tables;
+        if (upload) {
+            std::memcpy(c->pin_small.p, tables.data(), tables.size());
+            check(hipMemcpyAsync(c->d_tiles, c->pin_small.p, tables.size(), hipMemcpyHostToDevice,
+                                 c->stream),
+                  "tree tables");
+            c->tree_tables = std::move(tables);
+        }
         // The delta is kept only for callers without a device objective.
         if (c->objective < 0 && !c->delta) c->delta = c->alloc<float>(c->n_rows, "prediction delta");
         check(launch_init_rows(c->rows, c->objective >= 0 ? nullptr : c->delta, c->n_rows,
                                c->stream),
               "row arena reset");
-        c->sync();
+        if (upload) c->sync();  // the staging is reused by the next call
         c->tree_begun = true;
         root->offset = 0;
         root->len = (uint32_t)c->n_rows;
@@ -1806,6 +1840,8 @@ void ensure_grow(fbh_ctx *c, uint32_t D) {
               "column table");
     }
     if (G.depth >= D) return;
+    if (!G.pending.empty())
+        throw InputError("a deeper tree cannot start while grown trees wait to be collected");
     G.depth = D;
     G.level_cap = (size_t)1 << (D - 1);
     G.tree_cap = ((size_t)2 << D) - 1;
@@ -1820,10 +1856,211 @@ void ensure_grow(fbh_ctx *c, uint32_t D) {
     G.triples = c->alloc<uint32_t>(3 * G.level_cap, "grown tree triples");
     G.leaves = c->alloc<LeafDev>(G.leaf_cap, "grown tree leaves");
     G.leaf_vals = c->alloc<float>(G.leaf_cap, "grown tree leaf values");
-    if (G.out.p) (void)hipHostFree(G.out.p);
-    G.out.p = nullptr;
-    c->pinned(G.out, al256(sizeof(GrowState)) + al256(sizeof(TreeNodeDev) * G.tree_cap) +
-                         al256(8 * G.cat_cap) + al256(4 * G.leaf_cap));
+    for (int k = 0; k < 2; k++) {
+        if (G.out[k].p) (void)hipHostFree(G.out[k].p);
+        G.out[k].p = nullptr;
+        c->pinned(G.out[k], al256(sizeof(GrowState)) + al256(sizeof(TreeNodeDev) * G.tree_cap) +
+                                al256(8 * G.cat_cap) + al256(4 * G.leaf_cap));
+        if (!G.done[k])
+            check(hipEventCreateWithFlags(&G.done[k], hipEventDisableTiming), "event");
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+}  // extern "C"
+
+namespace {
+
+// Enqueues a whole depthwise tree (see fbh_grow_depthwise) and its download
+// into the next of two pinned result slots; returns without waiting.
+void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params *sp,
+                  const int64_t *root_sum) {
+    if (!c || !gp || !sp) throw InputError("null argument");
+    ensure_tree(c);
+    const uint32_t D = gp->max_depth;
+    if (D == 0 || D > MAX_GROW_DEPTH)
+        throw InputError("a device-grown tree needs max_depth in 1..=" +
+                         std::to_string(MAX_GROW_DEPTH));
+    if (gp->max_leaves == 1) throw InputError("max_leaves 1 leaves nothing to grow");
+    if (!c->plan.columns_resident || !c->streamed.empty())
+        throw InputError("a device-grown tree needs every tile and column resident");
+    if (c->n_slots > MAX_GROW_SLOTS)
+        throw InputError("a device-grown tree supports at most " + std::to_string(MAX_GROW_SLOTS) +
+                         " histogram slots");
+    if (!root_sum && !c->root_on_device)
+        throw InputError("no root sum: pass it, or compute the gradients on the device first");
+    auto &GB = c->grow;
+    if (GB.pending.size() >= 2)
+        throw InputError("two grown trees are waiting; collect one with fbh_grow_collect");
+    check(hipSetDevice(c->device), "hipSetDevice");
+    ensure_grow(c, D);
+    const uint32_t n_rows = (uint32_t)c->n_rows;
+    const uint32_t n_slots = c->n_slots;
+    auto lvl_bound = [&](uint32_t d) { return std::min<uint32_t>(1u << d, n_slots); };
+
+    // The root: one accumulated node over every row, planned here; its split
+    // node (sums, bounds) is written by the init kernel from the root sum.
+    Stager S{c};
+    const uint32_t cr = c->chunk_rows_for(n_rows);
+    HistNodeDev h{};
+    h.row_off = 0;
+    h.row_len = n_rows;
+    h.chunk_begin = 0;
+    h.slot = 0;
+    h.n_chunks = div_up(n_rows, cr);
+    EvalPlan E0;
+    E0.hn = S.dev<HistNodeDev>(S.put(&h, sizeof(h)));
+    E0.n_hn = 1;
+    E0.grid_chunks = h.n_chunks;
+    E0.chunk_rows = cr;
+    if (h.n_chunks != 1 || c->has_global || !c->streamed.empty()) {
+        const uint32_t zero0 = 0;
+        E0.zero_slots = S.dev<uint32_t>(S.put(&zero0, 4));
+        E0.n_zero = 1;
+    }
+    E0.sn = c->d_lvl_split;
+    E0.n_nodes = 1;
+    E0.download = false;
+    const int64_t *d_root = root_sum ? S.dev<const int64_t>(S.put(root_sum, 16))
+                                     : c->red_i64 + 2 * c->n_red_blocks;
+    const int8_t *d_mono = S.dev<const int8_t>(S.put(c->monotone.data(), c->n_features));
+    S.send();
+
+    GrowParamsDev G{};
+    G.sp.inv_g = 1.0 / c->scales[0];
+    G.sp.inv_h = 1.0 / c->scales[1];
+    G.sp.lambda_ = sp->lambda_;
+    G.sp.gamma = sp->gamma;
+    G.sp.mcw = sp->min_child_weight;
+    G.sp.alpha = sp->alpha;
+    G.sp.mds = sp->max_delta_step;
+    G.sp.max_cat_to_onehot = sp->max_cat_to_onehot;
+    G.sp.max_cat_threshold = sp->max_cat_threshold;
+    G.sp.n_feats = (uint32_t)c->tree_feats.size();
+    G.sp.cat_words_per_node = c->cat_words_per_node;
+    G.learning_rate = gp->learning_rate;
+    G.max_depth = D;
+    G.max_leaves = gp->max_leaves;
+    G.n_slots = n_slots;
+    G.cw = std::max(1u, c->cat_words_per_node);
+    G.n_rows = n_rows;
+    check(launch_grow_init(G, d_root, 0, GB.level[0], c->d_lvl_split, GB.tree, GB.st, c->stream),
+          "tree init");
+    enqueue_eval(c, E0, sp);
+    account_hist(c, n_rows, 1);
+
+    const ChunkRule rule = c->chunk_rule();
+    uint8_t *pk_base = reinterpret_cast<uint8_t *>(c->d_packets);
+    for (uint32_t d = 0; d < D; d++) {
+        const uint32_t nb = lvl_bound(d);
+        const uint64_t *pk_cats =
+            reinterpret_cast<const uint64_t *>(pk_base + al256(sizeof(SplitPacketDev) * nb));
+        check(launch_grow_decide(G, d, c->d_packets, pk_cats, GB.level[d & 1], GB.tree,
+                                 GB.tree_cats, d_mono, GB.cols, GB.reqs, GB.pairs, GB.triples,
+                                 GB.leaves, GB.leaf_vals, GB.st, c->stream),
+              "tree level decision");
+        // Level d's rows are in arena d % 2; its children go to the other.
+        uint32_t *arena_in = (d & 1) ? c->tmp : c->rows;
+        uint32_t *arena_out = (d & 1) ? c->rows : c->tmp;
+        check(launch_partition_dev(GB.reqs, &GB.st->n_split, n_rows / PART_CHUNK + nb + 1, arena_in,
+                                   arena_out, c->flags, c->d_counts, c->d_excl, c->d_totals,
+                                   pk_cats, c->stream),
+              "partition");
+        const GrowDevOut out{GB.st, GB.level[(d + 1) & 1], GB.tree, GB.leaves, GB.leaf_vals,
+                             (d + 1) & 1u};
+        check(launch_level_plan(GB.pairs, nb, c->d_totals, rule, c->d_lvl_hist, c->d_lvl_split,
+                                c->d_lvl_out, c->d_lvl_out + 4 * MAX_NODES, c->d_lvl_rows, out,
+                                c->stream),
+              "level plan");
+        if (d + 1 == D) break;
+        EvalPlan E;
+        E.hn = c->d_lvl_hist;
+        E.n_hn = nb;
+        E.dev_n_hn = &GB.st->n_eval;
+        E.grid_chunks = rule.fixed ? n_rows / rule.fixed + nb + 1
+                                   : std::max<uint32_t>(rule.want_chunks, 256) + nb;
+        E.dev_chunk_rows = c->d_lvl_rows;
+        E.triples = GB.triples;
+        E.n_tri = nb;
+        E.dev_n_tri = &GB.st->n_eval;
+        E.sn = c->d_lvl_split;
+        E.n_nodes = lvl_bound(d + 1);
+        E.dev_n_nodes = &GB.st->n_level;
+        E.download = false;
+        E.rows = arena_out;
+        enqueue_eval(c, E, sp);
+    }
+    check(launch_leaf_plan(GB.leaves, GB.st, c->stream), "leaf plan");
+    uint64_t leaf_bound = (uint64_t)1 << D;
+    if (gp->max_leaves) leaf_bound = std::min<uint64_t>(leaf_bound, gp->max_leaves);
+    const int idb = c->objective >= 0 ? (leaf_bound <= 256 ? 1 : 2) : 0;
+    check(launch_assign_leaves(GB.leaves, 0, (uint32_t)(n_rows / PART_CHUNK + leaf_bound + 1),
+                               c->rows, c->tmp, c->delta, c->leaf_ids, idb, &GB.st->n_leaves,
+                               c->stream),
+          "leaf assignment");
+    if (idb)
+        check(launch_apply_leaves(c->leaf_ids, idb, GB.leaf_vals, c->n_rows, c->margin, c->stream),
+              "margin update");
+    c->leaf_id_bytes = idb;
+    c->ids_fresh = idb != 0;
+
+    // Download into the next result slot; collected in order.
+    const int k = (int)(GB.next_slot++ & 1);
+    uint8_t *po = static_cast<uint8_t *>(GB.out[k].p);
+    const size_t o_tree = al256(sizeof(GrowState));
+    const size_t o_cats = o_tree + al256(sizeof(TreeNodeDev) * GB.tree_cap);
+    const size_t o_vals = o_cats + al256(8 * GB.cat_cap);
+    check(hipMemcpyAsync(po, GB.st, sizeof(GrowState), hipMemcpyDeviceToHost, c->stream),
+          "tree download");
+    check(hipMemcpyAsync(po + o_tree, GB.tree, sizeof(TreeNodeDev) * GB.tree_cap,
+                         hipMemcpyDeviceToHost, c->stream),
+          "tree download");
+    if (c->cat_words_per_node)
+        check(hipMemcpyAsync(po + o_cats, GB.tree_cats, 8 * GB.cat_cap, hipMemcpyDeviceToHost,
+                             c->stream),
+              "tree download");
+    check(hipMemcpyAsync(po + o_vals, GB.leaf_vals, 4 * GB.leaf_cap, hipMemcpyDeviceToHost,
+                         c->stream),
+          "tree download");
+    check(hipEventRecord(GB.done[k], c->stream), "event");
+    GB.pending.push_back({k, c->cat_words_per_node});
+}
+
+// Waits for the oldest enqueued tree and copies it out.
+void grow_collect(fbh_ctx *c, fbh_tree_node *nodes, uint32_t node_capacity, uint32_t *n_nodes,
+                  uint64_t *cat_words, uint32_t cat_capacity, float *leaf_values,
+                  uint32_t leaf_capacity, uint32_t *n_leaves) {
+    if (!c || !nodes || !n_nodes || !leaf_values || !n_leaves) throw InputError("null argument");
+    auto &GB = c->grow;
+    if (GB.pending.empty()) throw InputError("no grown tree to collect");
+    const auto job = GB.pending.front();
+    GB.pending.pop_front();
+    check(hipSetDevice(c->device), "hipSetDevice");
+    check(hipEventSynchronize(GB.done[job.slot]), "tree download");
+    if (c->timing) c->collect_timing();
+    const uint8_t *po = static_cast<const uint8_t *>(GB.out[job.slot].p);
+    const size_t o_tree = al256(sizeof(GrowState));
+    const size_t o_cats = o_tree + al256(sizeof(TreeNodeDev) * GB.tree_cap);
+    const size_t o_vals = o_cats + al256(8 * GB.cat_cap);
+    GrowState st;
+    std::memcpy(&st, po, sizeof(st));
+    if (st.error) throw RuntimeError("histogram slots exhausted; raise the slot budget");
+    account_hist(c, st.hist_rows, st.hist_nodes);
+    if (st.covered != c->n_rows)
+        throw RuntimeError("leaves cover " + std::to_string(st.covered) + " of " +
+                           std::to_string(c->n_rows) + " rows");
+    if (st.tree_size > node_capacity || st.n_leaves > leaf_capacity ||
+        (job.cat_words && st.tree_cat_words > cat_capacity))
+        throw InputError("output capacity too small for the grown tree");
+    static_assert(sizeof(TreeNodeDev) == sizeof(fbh_tree_node), "tree node layout");
+    std::memcpy(nodes, po + o_tree, sizeof(fbh_tree_node) * st.tree_size);
+    if (job.cat_words && cat_words) std::memcpy(cat_words, po + o_cats, 8 * (size_t)st.tree_cat_words);
+    std::memcpy(leaf_values, po + o_vals, 4 * (size_t)st.n_leaves);
+    *n_nodes = st.tree_size;
+    *n_leaves = st.n_leaves;
 }
 
 }  // namespace
@@ -1835,159 +2072,25 @@ int fbh_grow_depthwise(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_pa
                        uint32_t *n_nodes, uint64_t *cat_words, uint32_t cat_capacity,
                        float *leaf_values, uint32_t leaf_capacity, uint32_t *n_leaves) {
     return guard([&] {
-        if (!c || !gp || !sp || !root_sum || !nodes || !n_nodes || !leaf_values || !n_leaves)
-            throw InputError("null argument");
-        ensure_tree(c);
-        const uint32_t D = gp->max_depth;
-        if (D == 0 || D > MAX_GROW_DEPTH)
-            throw InputError("a device-grown tree needs max_depth in 1..=" +
-                             std::to_string(MAX_GROW_DEPTH));
-        if (gp->max_leaves == 1) throw InputError("max_leaves 1 leaves nothing to grow");
-        if (!c->plan.columns_resident || !c->streamed.empty())
-            throw InputError("a device-grown tree needs every tile and column resident");
-        if (c->n_slots > MAX_GROW_SLOTS)
-            throw InputError("a device-grown tree supports at most " +
-                             std::to_string(MAX_GROW_SLOTS) + " histogram slots");
-        check(hipSetDevice(c->device), "hipSetDevice");
-        ensure_grow(c, D);
-        auto &GB = c->grow;
-        const uint32_t n_rows = (uint32_t)c->n_rows;
-        const uint32_t n_slots = c->n_slots;
-        auto lvl_bound = [&](uint32_t d) { return std::min<uint32_t>(1u << d, n_slots); };
+        if (c && !c->grow.pending.empty())
+            throw InputError("grown trees are waiting; collect them with fbh_grow_collect");
+        grow_enqueue(c, gp, sp, root_sum);
+        grow_collect(c, nodes, node_capacity, n_nodes, cat_words, cat_capacity, leaf_values,
+                     leaf_capacity, n_leaves);
+    });
+}
 
-        // The root is evaluated as fbh_eval_nodes plans it, without waiting.
-        Stager S{c};
-        fbh_node root{};
-        root.rows = {0, n_rows};
-        root.sum[0] = root_sum[0];
-        root.sum[1] = root_sum[1];
-        root.lower = -std::numeric_limits<float>::max();
-        root.upper = std::numeric_limits<float>::max();
-        root.slot = 0;
-        root.subtract_parent = -1;
-        root.subtract_sibling = -1;
-        EvalPlan E0;
-        const auto acc0 = stage_host_eval(c, &root, 1, nullptr, S, E0);
-        E0.download = false;
-        const int8_t *d_mono = S.dev<const int8_t>(S.put(c->monotone.data(), c->n_features));
-        S.send();
+int fbh_grow_depthwise_async(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params *sp,
+                             const int64_t root_sum[2]) {
+    return guard([&] { grow_enqueue(c, gp, sp, root_sum); });
+}
 
-        GrowParamsDev G{};
-        G.sp.inv_g = 1.0 / c->scales[0];
-        G.sp.inv_h = 1.0 / c->scales[1];
-        G.sp.lambda_ = sp->lambda_;
-        G.sp.gamma = sp->gamma;
-        G.sp.mcw = sp->min_child_weight;
-        G.sp.alpha = sp->alpha;
-        G.sp.mds = sp->max_delta_step;
-        G.sp.max_cat_to_onehot = sp->max_cat_to_onehot;
-        G.sp.max_cat_threshold = sp->max_cat_threshold;
-        G.sp.n_feats = (uint32_t)c->tree_feats.size();
-        G.sp.cat_words_per_node = c->cat_words_per_node;
-        G.learning_rate = gp->learning_rate;
-        G.max_depth = D;
-        G.max_leaves = gp->max_leaves;
-        G.n_slots = n_slots;
-        G.cw = std::max(1u, c->cat_words_per_node);
-        G.n_rows = n_rows;
-        check(launch_grow_init(G, root_sum[0], root_sum[1], 0, GB.level[0], GB.tree, GB.st,
-                               c->stream),
-              "tree init");
-        enqueue_eval(c, E0, sp);
-        account_hist(c, acc0.first, acc0.second);
-
-        const ChunkRule rule = c->chunk_rule();
-        uint8_t *pk_base = reinterpret_cast<uint8_t *>(c->d_packets);
-        for (uint32_t d = 0; d < D; d++) {
-            const uint32_t nb = lvl_bound(d);
-            const uint64_t *pk_cats =
-                reinterpret_cast<const uint64_t *>(pk_base + al256(sizeof(SplitPacketDev) * nb));
-            check(launch_grow_decide(G, d, c->d_packets, pk_cats, GB.level[d & 1], GB.tree,
-                                     GB.tree_cats, d_mono, GB.cols, GB.reqs, GB.pairs,
-                                     GB.triples, GB.leaves, GB.leaf_vals, GB.st, c->stream),
-                  "tree level decision");
-            // Level d's rows are in arena d % 2; its children go to the other.
-            uint32_t *arena_in = (d & 1) ? c->tmp : c->rows;
-            uint32_t *arena_out = (d & 1) ? c->rows : c->tmp;
-            check(launch_partition_dev(GB.reqs, &GB.st->n_split, n_rows / PART_CHUNK + nb + 1,
-                                       arena_in, arena_out, c->flags, c->d_counts, c->d_excl,
-                                       c->d_totals, pk_cats, c->stream),
-                  "partition");
-            const GrowDevOut out{GB.st, GB.level[(d + 1) & 1], GB.tree, GB.leaves, GB.leaf_vals,
-                                 (d + 1) & 1u};
-            check(launch_level_plan(GB.pairs, nb, c->d_totals, rule, c->d_lvl_hist,
-                                    c->d_lvl_split, c->d_lvl_out, c->d_lvl_out + 4 * MAX_NODES,
-                                    c->d_lvl_rows, out, c->stream),
-                  "level plan");
-            if (d + 1 == D) break;
-            EvalPlan E;
-            E.hn = c->d_lvl_hist;
-            E.n_hn = nb;
-            E.dev_n_hn = &GB.st->n_eval;
-            E.grid_chunks = rule.fixed ? n_rows / rule.fixed + nb + 1
-                                       : std::max<uint32_t>(rule.want_chunks, 256) + nb;
-            E.dev_chunk_rows = c->d_lvl_rows;
-            E.triples = GB.triples;
-            E.n_tri = nb;
-            E.dev_n_tri = &GB.st->n_eval;
-            E.sn = c->d_lvl_split;
-            E.n_nodes = lvl_bound(d + 1);
-            E.dev_n_nodes = &GB.st->n_level;
-            E.download = false;
-            E.rows = arena_out;
-            enqueue_eval(c, E, sp);
-        }
-        check(launch_leaf_plan(GB.leaves, GB.st, c->stream), "leaf plan");
-        uint64_t leaf_bound = (uint64_t)1 << D;
-        if (gp->max_leaves) leaf_bound = std::min<uint64_t>(leaf_bound, gp->max_leaves);
-        const int idb = c->objective >= 0 ? (leaf_bound <= 256 ? 1 : 2) : 0;
-        check(launch_assign_leaves(GB.leaves, 0, (uint32_t)(n_rows / PART_CHUNK + leaf_bound + 1),
-                                   c->rows, c->tmp, c->delta, c->leaf_ids, idb, &GB.st->n_leaves,
-                                   c->stream),
-              "leaf assignment");
-        if (idb)
-            check(launch_apply_leaves(c->leaf_ids, idb, GB.leaf_vals, c->n_rows, c->margin,
-                                      c->stream),
-                  "margin update");
-        c->leaf_id_bytes = idb;
-        c->ids_fresh = idb != 0;
-
-        uint8_t *po = static_cast<uint8_t *>(GB.out.p);
-        const size_t o_tree = al256(sizeof(GrowState));
-        const size_t o_cats = o_tree + al256(sizeof(TreeNodeDev) * GB.tree_cap);
-        const size_t o_vals = o_cats + al256(8 * GB.cat_cap);
-        check(hipMemcpyAsync(po, GB.st, sizeof(GrowState), hipMemcpyDeviceToHost, c->stream),
-              "tree download");
-        check(hipMemcpyAsync(po + o_tree, GB.tree, sizeof(TreeNodeDev) * GB.tree_cap,
-                             hipMemcpyDeviceToHost, c->stream),
-              "tree download");
-        if (c->cat_words_per_node)
-            check(hipMemcpyAsync(po + o_cats, GB.tree_cats, 8 * GB.cat_cap, hipMemcpyDeviceToHost,
-                                 c->stream),
-                  "tree download");
-        check(hipMemcpyAsync(po + o_vals, GB.leaf_vals, 4 * GB.leaf_cap, hipMemcpyDeviceToHost,
-                             c->stream),
-              "tree download");
-        c->sync();
-        if (c->timing) c->collect_timing();
-        GrowState st;
-        std::memcpy(&st, po, sizeof(st));
-        if (st.error)
-            throw RuntimeError("histogram slots exhausted; raise the slot budget");
-        account_hist(c, st.hist_rows, st.hist_nodes);
-        if (st.covered != c->n_rows)
-            throw RuntimeError("leaves cover " + std::to_string(st.covered) + " of " +
-                               std::to_string(c->n_rows) + " rows");
-        if (st.tree_size > node_capacity || st.n_leaves > leaf_capacity ||
-            (c->cat_words_per_node && st.tree_cat_words > cat_capacity))
-            throw InputError("output capacity too small for the grown tree");
-        static_assert(sizeof(TreeNodeDev) == sizeof(fbh_tree_node), "tree node layout");
-        std::memcpy(nodes, po + o_tree, sizeof(fbh_tree_node) * st.tree_size);
-        if (c->cat_words_per_node && cat_words)
-            std::memcpy(cat_words, po + o_cats, 8 * (size_t)st.tree_cat_words);
-        std::memcpy(leaf_values, po + o_vals, 4 * (size_t)st.n_leaves);
-        *n_nodes = st.tree_size;
-        *n_leaves = st.n_leaves;
+int fbh_grow_collect(fbh_ctx *c, fbh_tree_node *nodes, uint32_t node_capacity, uint32_t *n_nodes,
+                     uint64_t *cat_words, uint32_t cat_capacity, float *leaf_values,
+                     uint32_t leaf_capacity, uint32_t *n_leaves) {
+    return guard([&] {
+        grow_collect(c, nodes, node_capacity, n_nodes, cat_words, cat_capacity, leaf_values,
+                     leaf_capacity, n_leaves);
     });
 }
 
@@ -2087,8 +2190,7 @@ int fbh_set_timing(fbh_ctx *c, int enabled) {
 int fbh_hist_timing(fbh_ctx *c, double *ms, uint64_t *launches, uint64_t *bytes, int reset) {
     return guard([&] {
         if (!c) throw InputError("null argument");
-        c->sync();
-        c->collect_timing();
+        c->collect_timing();  // launches still running are counted by a later call
         if (ms) *ms = c->hist_ms;
         if (launches) *launches = c->hist_launches;
         if (bytes) *bytes = c->hist_bytes;

@@ -262,8 +262,8 @@ hipError_t launch_level_plan(const PairDev *pairs, uint32_t n_pairs, const uint3
                              const GrowDevOut &D, hipStream_t s);
 // Device-grown depthwise trees (one workgroup each): the root, the decision
 // of one level (see grow_decide_kernel) and the leaf table's chunks.
-hipError_t launch_grow_init(const GrowParamsDev &G, int64_t root_g, int64_t root_h,
-                            uint32_t root_slot, LNodeDev *level, TreeNodeDev *tree,
+hipError_t launch_grow_init(const GrowParamsDev &G, const int64_t *root, uint32_t root_slot,
+                            LNodeDev *level, SplitNodeDev *root_split, TreeNodeDev *tree,
                             GrowState *st, hipStream_t s);
 hipError_t launch_grow_decide(const GrowParamsDev &G, uint32_t depth, const SplitPacketDev *pk,
                               const uint64_t *pk_cats, const LNodeDev *level, TreeNodeDev *tree,

@@ -1730,9 +1730,11 @@ hipError_t launch_shap(const ShapNodeDev *nodes, const uint32_t *tree_roots, uin
 // them and plans the partition and the children exactly as the host grower
 // would (build_tree, src/training/mod.rs:3357-4565).
 
-__global__ void grow_init_kernel(GrowParamsDev G, int64_t rg, int64_t rh, uint32_t root_slot,
-                                 LNodeDev *level, TreeNodeDev *tree, GrowState *st) {
+__global__ void grow_init_kernel(GrowParamsDev G, const int64_t *root, uint32_t root_slot,
+                                 LNodeDev *level, SplitNodeDev *root_split, TreeNodeDev *tree,
+                                 GrowState *st) {
     if (threadIdx.x != 0) return;
+    const int64_t rg = root[0], rh = root[1];
     GrowState s{};
     s.n_level = 1;
     s.tree_size = 1;
@@ -1748,6 +1750,13 @@ __global__ void grow_init_kernel(GrowParamsDev G, int64_t rg, int64_t rh, uint32
     r.lower = -3.40282347e38f;
     r.upper = 3.40282347e38f;
     level[0] = r;
+    SplitNodeDev sn{};
+    sn.sum_g = rg;
+    sn.sum_h = rh;
+    sn.lower = r.lower;
+    sn.upper = r.upper;
+    sn.slot = root_slot;
+    root_split[0] = sn;
     const double g = (double)rg * G.sp.inv_g, h = (double)rh * G.sp.inv_h;
     TreeNodeDev t{};
     t.left = t.right = -1;
@@ -1757,11 +1766,11 @@ __global__ void grow_init_kernel(GrowParamsDev G, int64_t rg, int64_t rh, uint32
     tree[0] = t;
 }
 
-hipError_t launch_grow_init(const GrowParamsDev &G, int64_t root_g, int64_t root_h,
-                            uint32_t root_slot, LNodeDev *level, TreeNodeDev *tree,
+hipError_t launch_grow_init(const GrowParamsDev &G, const int64_t *root, uint32_t root_slot,
+                            LNodeDev *level, SplitNodeDev *root_split, TreeNodeDev *tree,
                             GrowState *st, hipStream_t s) {
-    hipLaunchKernelGGL(grow_init_kernel, dim3(1), dim3(64), 0, s, G, root_g, root_h, root_slot,
-                       level, tree, st);
+    hipLaunchKernelGGL(grow_init_kernel, dim3(1), dim3(64), 0, s, G, root, root_slot, level,
+                       root_split, tree, st);
     return hipGetLastError();
 }
 

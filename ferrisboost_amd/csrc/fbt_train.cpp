@@ -259,14 +259,19 @@ class Grower {
         cat_cap_ = words;
     }
 
-    Tree grow(const double scales[2], const int64_t root_sum[2]) {
+    void lm_scales(const double scales[2]) {
         lm_ = {p_.lambda_, p_.alpha, p_.max_delta_step, p_.learning_rate, 1.0 / scales[0],
                1.0 / scales[1]};
+    }
+
+    Tree grow(const double scales[2], const int64_t root_sum[2]) {
+        lm_scales(scales);
         leaves_spans_.clear();
         leaves_values_.clear();
-        if (device_trees_ && p_.grow_policy == 0 && p_.max_depth >= 1 && p_.max_depth <= 14 &&
-            p_.max_leaves != 1)
-            return grow_on_device(root_sum);
+        if (device_growth()) {
+            grow_async(root_sum);
+            return collect();
+        }
         Tree t;
         double g, h;
         lm_.to_f64(root_sum, g, h);
@@ -291,6 +296,48 @@ class Grower {
     uint32_t n_rows_ = 0;
     bool device_trees_ = false;  // depthwise trees grow whole on the device
     uint32_t device_trees = 0;   // trees grown that way
+
+    bool device_growth() const {
+        return device_trees_ && p_.grow_policy == 0 && p_.max_depth >= 1 && p_.max_depth <= 14 &&
+               p_.max_leaves != 1;
+    }
+
+    // Enqueues a depthwise tree on the device (root_sum NULL: the one the
+    // gradient call left there); collect() waits for it and rebuilds it.
+    void grow_async(const int64_t *root_sum) {
+        fbh_grow_params gp{p_.max_depth, p_.max_leaves, p_.learning_rate, 0};
+        call(fbh_grow_depthwise_async(ctx_, &gp, &sp_, root_sum));
+    }
+
+    // The oldest enqueued device tree, rebuilt with Tree::split_leaf in
+    // node-id order (the order the device numbered it).
+    Tree collect() {
+        const uint32_t cap_nodes = (2u << p_.max_depth) - 1, cap_leaves = 1u << p_.max_depth;
+        std::vector<fbh_tree_node> tn(cap_nodes);
+        std::vector<uint64_t> cats((size_t)std::max<uint32_t>(1, cat_cap_) * cap_leaves);
+        leaves_values_.assign(cap_leaves, 0.0f);
+        uint32_t nn = 0, nl = 0;
+        call(fbh_grow_collect(ctx_, tn.data(), cap_nodes, &nn, cats.data(), (uint32_t)cats.size(),
+                              leaves_values_.data(), cap_leaves, &nl));
+        leaves_values_.resize(nl);
+        Tree t;
+        t.push_leaf(tn[0].leaf_value, tn[0].sum_hess);
+        for (uint32_t id = 0; id < nn; id++) {
+            const fbh_tree_node &a = tn[id];
+            if (a.flags & 1u) continue;
+            const fbh_tree_node &l = tn[a.left], &r = tn[a.right];
+            const bool is_cat = (a.flags & 4u) != 0;
+            const auto lr = t.split_leaf(id, a.feat, is_cat ? 0.0f : cond_of(a.feat, a.bin),
+                                         (a.flags & 2u) != 0, a.gain, l.leaf_value, l.sum_hess,
+                                         r.leaf_value, r.sum_hess);
+            if (lr.first != (uint32_t)a.left || lr.second != (uint32_t)a.right)
+                throw RuntimeError("device tree nodes out of order");
+            if (is_cat) t.set_categories(id, cats.data() + a.cat_offset, a.n_cat_words);
+        }
+        if (t.nodes.size() != nn) throw RuntimeError("device tree node count mismatch");
+        device_trees++;
+        return t;
+    }
 
   private:
     struct Pending {
@@ -348,37 +395,6 @@ class Grower {
         if (bin == 0) return -std::numeric_limits<float>::max();
         if (bin > nc) return std::numeric_limits<float>::max();
         return cuts_.values[cuts_.offsets[feat] + bin - 1];
-    }
-
-    // A depthwise tree grown whole by fbh_grow_depthwise, rebuilt here with
-    // Tree::split_leaf in node-id order (the order the device numbered it).
-    Tree grow_on_device(const int64_t root_sum[2]) {
-        fbh_grow_params gp{p_.max_depth, p_.max_leaves, p_.learning_rate, 0};
-        const uint32_t cap_nodes = (2u << p_.max_depth) - 1, cap_leaves = 1u << p_.max_depth;
-        std::vector<fbh_tree_node> tn(cap_nodes);
-        std::vector<uint64_t> cats((size_t)std::max<uint32_t>(1, cat_cap_) * cap_leaves);
-        leaves_values_.assign(cap_leaves, 0.0f);
-        uint32_t nn = 0, nl = 0;
-        call(fbh_grow_depthwise(ctx_, &gp, &sp_, root_sum, tn.data(), cap_nodes, &nn, cats.data(),
-                                (uint32_t)cats.size(), leaves_values_.data(), cap_leaves, &nl));
-        leaves_values_.resize(nl);
-        Tree t;
-        t.push_leaf(tn[0].leaf_value, tn[0].sum_hess);
-        for (uint32_t id = 0; id < nn; id++) {
-            const fbh_tree_node &a = tn[id];
-            if (a.flags & 1u) continue;
-            const fbh_tree_node &l = tn[a.left], &r = tn[a.right];
-            const bool is_cat = (a.flags & 4u) != 0;
-            const auto lr = t.split_leaf(id, a.feat, is_cat ? 0.0f : cond_of(a.feat, a.bin),
-                                         (a.flags & 2u) != 0, a.gain, l.leaf_value, l.sum_hess,
-                                         r.leaf_value, r.sum_hess);
-            if (lr.first != (uint32_t)a.left || lr.second != (uint32_t)a.right)
-                throw RuntimeError("device tree nodes out of order");
-            if (is_cat) t.set_categories(id, cats.data() + a.cat_offset, a.n_cat_words);
-        }
-        if (t.nodes.size() != nn) throw RuntimeError("device tree node count mismatch");
-        device_trees++;
-        return t;
     }
 
     // Tree::split_leaf with child_leaves (src/training/mod.rs:5069-5094).
@@ -821,22 +837,48 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
             bytes_seen = bytes;
         }
     };
+    // Device-grown trees are collected one round late: the next round's
+    // gradients are enqueued first, so the host rebuilds tree r while the
+    // device works on round r + 1 (a host sigmoid needs tree r's leaf values
+    // first, so it collects before its gradients).
+    const bool overlap = grower.device_growth();
+    const bool host_sig = obj == 1 && !dev_sigmoid;
+    bool pending = false;
     for (uint32_t round = 0; round < p.n_rounds; round++) {
+        if (pending && round == p.sync_round) {  // the device is idle when this round starts
+            m.trees.push_back(grower.collect());
+            pending = false;
+        }
         if (round > 0) close_round(round - 1);
+        if (pending && host_sig) {
+            m.trees.push_back(grower.collect());
+            pending = false;
+        }
         const auto tg = Clock::now();
         double scales[2];
         int64_t root_sum[2];
-        call(fbh_gradient_exchange(ctx.get(), obj == 1 && !dev_sigmoid ? sigmoid_chunk : nullptr, &job,
+        call(fbh_gradient_exchange(ctx.get(), host_sig ? sigmoid_chunk : nullptr, &job,
                                    sample_threshold(p.subsample), p.seed, round, scales,
-                                   root_sum));
+                                   overlap ? nullptr : root_sum));
         grad_s += std::chrono::duration<double>(Clock::now() - tg).count();
+        if (pending) {
+            m.trees.push_back(grower.collect());
+            pending = false;
+        }
         std::vector<uint32_t> feats;
         if (p.colsample_bytree < 1.0f) feats = sample_columns(nf, p.colsample_bytree, p.seed, round);
         fbh_span root;
         call(fbh_begin_tree(ctx.get(), feats.empty() ? nullptr : feats.data(),
                             (uint32_t)feats.size(), mono.data(), nf, &root));
-        m.trees.push_back(grower.grow(scales, root_sum));
+        if (overlap) {
+            grower.lm_scales(scales);
+            grower.grow_async(nullptr);
+            pending = true;
+        } else {
+            m.trees.push_back(grower.grow(scales, root_sum));
+        }
     }
+    if (pending) m.trees.push_back(grower.collect());
     call(fbh_download_margin(ctx.get(), pred.data()));
     if (p.n_rounds > 0) close_round(p.n_rounds - 1);
     g_stats.train_seconds = std::chrono::duration<double>(Clock::now() - t_train).count();

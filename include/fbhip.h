@@ -220,7 +220,9 @@ typedef void (*fbh_sigmoid_fn)(void *user, uint64_t row_begin, uint64_t n, const
  * while later chunks are in flight and uploads the sigmoids. Either way the
  * device derives g = s - y, h = max(s(1 - s), 1e-16) (times the weight) with
  * the host's f32 operations, then masks, scales and quantizes as
- * fbh_upload_quantize_gpair. */
+ * fbh_upload_quantize_gpair. With root_out NULL the root sum stays on the
+ * device (for fbh_grow_depthwise) and the call returns once the scales are
+ * known, without waiting for the quantisation. */
 int fbh_gradient_exchange(fbh_ctx *ctx, fbh_sigmoid_fn fn, void *user, uint64_t sample_threshold,
                           uint64_t seed, uint64_t tree, double scales_out[2],
                           int64_t root_sum_out[2]);
@@ -335,13 +337,25 @@ typedef struct fbh_grow_params {
  * on the host: the max_leaves budget, node ids, leaf weights, monotone
  * bounds, partitions, histogram slots and the leaf assignment are decided
  * by kernels, and one copy brings the tree back. The root sum is the one
- * the gradient call returned; every tile and column must be resident. Leaf
+ * the gradient call returned (NULL: the one it left on the device); every
+ * tile and column must be resident. Leaf
  * values come back in leaf-id order (the ids fbh_gradient_exchange hands to
  * a host sigmoid callback). */
 int fbh_grow_depthwise(fbh_ctx *ctx, const fbh_grow_params *grow, const fbh_split_params *params,
                        const int64_t root_sum[2], fbh_tree_node *nodes, uint32_t node_capacity,
                        uint32_t *n_nodes, uint64_t *cat_words, uint32_t cat_capacity,
                        float *leaf_values, uint32_t leaf_capacity, uint32_t *n_leaves);
+/* The same in two halves: _async enqueues the tree and returns; collect
+ * waits for the oldest enqueued tree and copies it out (at most two wait).
+ * A caller enqueues the next round's gradients before collecting, so the
+ * host rebuilds tree r while the device computes round r + 1. root_sum may
+ * be NULL after fbh_gradient_exchange with a NULL root_out: the root sum then
+ * never leaves the device. */
+int fbh_grow_depthwise_async(fbh_ctx *ctx, const fbh_grow_params *grow,
+                             const fbh_split_params *params, const int64_t root_sum[2]);
+int fbh_grow_collect(fbh_ctx *ctx, fbh_tree_node *nodes, uint32_t node_capacity,
+                     uint32_t *n_nodes, uint64_t *cat_words, uint32_t cat_capacity,
+                     float *leaf_values, uint32_t leaf_capacity, uint32_t *n_leaves);
 
 /* GpuTrainCtx::assign_leaf_values (src/backend/cuda/train_ctx.rs:2128-2252):
  * delta[row] = value for every row of each span. */
@@ -359,7 +373,9 @@ int fbh_host_free(void *p);
 int fbh_download_rows(fbh_ctx *ctx, uint32_t *out);
 
 /* Device time of the histogram kernels since creation or the last reset, in
- * milliseconds, and their launch count (HIP events on the context stream). */
+ * milliseconds, and their launch count (HIP events on the context stream).
+ * Does not wait: launches still running are counted by a later call (after
+ * any blocking call, such as fbh_download_margin, everything is counted). */
 int fbh_hist_timing(fbh_ctx *ctx, double *ms_out, uint64_t *launches_out, uint64_t *bytes_out,
                     int reset);
 /* Enables HIP-event timing of histogram launches (off by default). */

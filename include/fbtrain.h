@@ -62,7 +62,9 @@ typedef struct {
     uint32_t host_levels;      /* 1: depthwise trees grow level by level from
                                   the host (0: whole trees on the device when
                                   every tile and column is resident) */
-    uint32_t reserved2;
+    uint32_t sync_round;       /* nonzero: the loop waits for the device before
+                                  this round starts (a clean timing boundary;
+                                  trees are otherwise collected a round late) */
 } fbt_params;
 
 /* One tree node: Node (src/model/tree.rs:52-111). */
