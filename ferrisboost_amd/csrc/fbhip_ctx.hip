@@ -258,6 +258,7 @@ struct fbh_ctx {
     uint64_t streamed_bytes = 0;     // host-to-device bytes of streamed records and columns
     bool has_global = false;  // this tree builds a feature with global atomics
     uint32_t hist_row_bytes = 0;  // active cell bytes per row over all built tiles
+    uint32_t hist_tiles = 0;      // resident tiles with features built this tree
     uint64_t bins_active = 0;     // bins of the tree's features
     uint32_t cat_words_per_node = 0;
     bool tree_begun = false;
@@ -379,12 +380,37 @@ struct fbh_ctx {
         R.want_chunks = (uint32_t)std::max<uint64_t>(1, wgs / n_tiles);
         return R;
     }
-    uint32_t chunk_rows_for(uint64_t acc_rows) const {
+    // Rows per chunk for accumulated nodes of these lengths: the smallest
+    // multiple of 1024 whose chunks (ceil(len / rows) per node) fit one wave
+    // of workgroups, so no launch runs a second, mostly idle wave; with more
+    // nodes than the wave holds, rows / want_chunks rounded up.
+    uint32_t chunk_rows_for(const uint32_t *lens, size_t n) const {
         const ChunkRule R = chunk_rule();
         if (R.fixed) return R.fixed;
-        uint64_t r = (acc_rows + R.want_chunks - 1) / R.want_chunks;
-        r = (r + 1023) & ~uint64_t(1023);
-        return (uint32_t)std::min<uint64_t>(std::max<uint64_t>(r, R.min_rows), R.max_rows);
+        uint64_t acc = 0, nz = 0;
+        for (size_t i = 0; i < n; i++) {
+            acc += lens[i];
+            nz += lens[i] ? 1 : 0;
+        }
+        uint64_t lo = (acc + (uint64_t)R.want_chunks * 1024 - 1) / ((uint64_t)R.want_chunks * 1024);
+        lo = std::max<uint64_t>(lo, 1);
+        if (R.want_chunks > nz) {
+            const uint64_t room = R.want_chunks - nz;
+            uint64_t hi = (acc + room * 1024 - 1) / (room * 1024);
+            hi = std::max(hi, lo);
+            while (lo < hi) {
+                const uint64_t mid = (lo + hi) / 2, rows = mid * 1024;
+                uint64_t k = 0;
+                for (size_t i = 0; i < n; i++) k += (lens[i] + rows - 1) / rows;
+                if (k <= R.want_chunks) hi = mid;
+                else lo = mid + 1;
+            }
+        }
+        return (uint32_t)std::min<uint64_t>(std::max<uint64_t>(lo * 1024, R.min_rows), R.max_rows);
+    }
+    uint32_t chunk_rows_for(uint64_t rows) const {
+        const uint32_t len = (uint32_t)rows;
+        return chunk_rows_for(&len, 1);
     }
 
     // Adds the histogram time of every completed launch; pairs still in
@@ -486,6 +512,16 @@ bool layout_bundles(fbh_ctx &c) {
 }
 
 uint32_t div_up(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+// Upper bound of the chunks a device-planned launch over n_nodes accumulated
+// nodes makes under the rule: at most want_chunks when they fit one wave,
+// else at most rows / chunk_rows + n_nodes with chunk_rows >= rows /
+// want_chunks, or rows / max_rows + n_nodes when the rows per chunk hit
+// their maximum.
+uint32_t rule_chunk_bound(const ChunkRule &R, uint64_t n_rows, uint32_t n_nodes) {
+    const uint64_t clamp = (n_rows + R.max_rows - 1) / R.max_rows;
+    return (uint32_t)(std::max<uint64_t>(R.want_chunks, clamp) + n_nodes);
+}
 
 // Per-row bytes of the arrays fbh_set_objective adds later: labels, margins,
 // leaf ids, row weights and host sigmoids (a context without objective keeps
@@ -1185,7 +1221,11 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
             c->streamed.push_back({(uint32_t)(&t - c->tiles.data()), k, lds, active_bytes});
         }
         c->hist_row_bytes = 0;
-        for (const auto &g : c->groups) c->hist_row_bytes += g.bytes_per_row;
+        c->hist_tiles = 0;
+        for (const auto &g : c->groups) {
+            c->hist_row_bytes += g.bytes_per_row;
+            c->hist_tiles += g.n_tiles;
+        }
         for (const auto &sd : c->streamed) c->hist_row_bytes += sd.bytes_per_row;
         c->bins_active = 0;
         for (uint32_t f : c->tree_feats) c->bins_active += c->n_bins[f];
@@ -1314,6 +1354,8 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
             L.chunk_rows = E.chunk_rows;
             L.dev_chunk_rows = E.dev_chunk_rows;
             L.chunk_groups = div_up(E.grid_chunks, XCDS);
+            // Chunk-major XCD locality needs at least one chunk per XCD.
+            L.linear = c->chunk_rule().want_chunks < XCDS ? 1u : 0u;
             L.rows = E.rows ? E.rows : c->rows;
             L.gpair = c->gpair;
             L.hist = c->hist;
@@ -1457,9 +1499,13 @@ std::pair<uint64_t, uint64_t> stage_host_eval(fbh_ctx *c, const fbh_node *nodes,
         std::vector<uint32_t> zero_slots;
         uint32_t chunks = 0;
         uint64_t acc_rows = 0;
+        std::vector<uint32_t> acc_lens;
         for (uint32_t i = 0; i < n; i++)
-            if (nodes[i].subtract_parent < 0) acc_rows += nodes[i].rows.len;
-        const uint32_t chunk_rows = c->chunk_rows_for(acc_rows);
+            if (nodes[i].subtract_parent < 0) {
+                acc_rows += nodes[i].rows.len;
+                acc_lens.push_back(nodes[i].rows.len);
+            }
+        const uint32_t chunk_rows = c->chunk_rows_for(acc_lens.data(), acc_lens.size());
         for (uint32_t i = 0; i < n; i++) {
             const fbh_node &nd = nodes[i];
             if (nd.subtract_parent >= 0) continue;
@@ -1752,7 +1798,7 @@ int fbh_partition_eval(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
         std::vector<PairDev> pd(n);
         std::vector<uint32_t> triples;
         const ChunkRule rule = c->chunk_rule();
-        uint64_t bound_rule = (uint64_t)std::max<uint32_t>(rule.want_chunks, 256) + n_eval;
+        uint64_t bound_rule = rule_chunk_bound(rule, c->n_rows, n_eval);
         uint64_t bound_min = 0;  // the smaller child holds at most half its parent's rows
         uint32_t e = 0;
         for (uint32_t i = 0; i < n; i++) {
@@ -1980,8 +2026,7 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
         E.hn = c->d_lvl_hist;
         E.n_hn = nb;
         E.dev_n_hn = &GB.st->n_eval;
-        E.grid_chunks = rule.fixed ? n_rows / rule.fixed + nb + 1
-                                   : std::max<uint32_t>(rule.want_chunks, 256) + nb;
+        E.grid_chunks = rule.fixed ? n_rows / rule.fixed + nb + 1 : rule_chunk_bound(rule, n_rows, nb);
         E.dev_chunk_rows = c->d_lvl_rows;
         E.triples = GB.triples;
         E.n_tri = nb;

@@ -61,6 +61,7 @@ struct HistLaunch {
     // are read from here (chunk_rows is then unused).
     const uint32_t *dev_chunk_rows;
     uint32_t chunk_groups;     // ceil(n_chunks / XCDS)
+    uint32_t linear;           // 1: linear workgroup mapping (many tiles), 0: XCD-local
     const uint32_t *rows;      // row arena
     const int64_t *gpair;      // [n_rows][2]
     int64_t *hist;             // [slots][hist_width][2]

@@ -54,6 +54,24 @@ __device__ __forceinline__ void load_record(const uint8_t *p, uint32_t (&r)[RD])
     }
 }
 
+// Workgroup -> (tile, chunk). XCD-local (few tiles): every tile of chunk c
+// runs on XCD c % 8, so the chunk's row ids and pairs come from HBM once
+// into that XCD's L2. Linear (many tiles, few chunks): consecutive
+// workgroups take consecutive tiles of one chunk, spreading every chunk over
+// all XCDs, so no XCD idles when there are fewer than 8 chunks.
+__device__ __forceinline__ void block_to_work(const HistLaunch &L, uint32_t b, uint32_t &tile_i,
+                                              uint32_t &chunk) {
+    if (L.linear) {
+        tile_i = b % L.n_tiles;
+        chunk = b / L.n_tiles;
+        return;
+    }
+    const uint32_t xcd = b % XCDS;
+    const uint32_t k = b / XCDS;
+    tile_i = k % L.n_tiles;
+    chunk = (k / L.n_tiles) * XCDS + xcd;
+}
+
 __device__ __forceinline__ void lds_add_u64(unsigned long long *p, unsigned long long v) {
     __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
@@ -68,10 +86,7 @@ __device__ __forceinline__ void global_add_u64(unsigned long long *p, unsigned l
 // otherwise. Fixed-point addition is exact and order independent, so the
 // result equals the host engine's bit for bit.
 //
-// Workgroup -> (chunk, tile) is XCD aware: workgroups are dispatched
-// round-robin over the 8 XCDs, and every tile of chunk c runs on XCD c % 8,
-// so the chunk's row ids and gradient pairs are fetched from HBM once into
-// that XCD's L2 and re-read from there by the other tiles.
+// Workgroup -> (chunk, tile) follows block_to_work.
 //
 // LDS layout is planar: slots [0, S) hold gradient sums, [S, 2S) Hessian
 // sums (S = tile slots + 64). The last 64 slots of each plane are one dummy
@@ -87,11 +102,8 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
     constexpr int NF = RD * FPD;
     constexpr uint32_t MASK = W == 1 ? 0xFFu : 0xFFFFu;
 
-    const uint32_t b = blockIdx.x;
-    const uint32_t xcd = b % XCDS;
-    const uint32_t k = b / XCDS;
-    const uint32_t tile_i = k % L.n_tiles;
-    const uint32_t chunk = (k / L.n_tiles) * XCDS + xcd;
+    uint32_t tile_i, chunk;
+    block_to_work(L, blockIdx.x, tile_i, chunk);
     if (chunk >= L.n_chunks) return;
     const TileDev T = L.tiles[tile_i];
     const uint32_t n_nodes = L.dev_n_nodes ? *L.dev_n_nodes : L.n_nodes;
@@ -189,10 +201,10 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
                 for (int q = 0; q < FPD; q++) {
                     const int fi = d * FPD + q;
                     if (fi >= (int)T.n_feat) continue;  // uniform
+                    if (nb[fi] == 0) continue;  // not built this tree (uniform)
                     const uint32_t bin = (rec[u][d] >> (q * 8 * W)) & MASK;
-                    // Missing (all ones) and unseen-category codes are >= n_bins,
-                    // and features not built this tree have n_bins == 0; out-of-
-                    // range rows (ok false) carry a zero pair.
+                    // Missing (all ones) and unseen-category codes are >= n_bins;
+                    // out-of-range rows (ok false) carry a zero pair.
                     const uint32_t s = bin < nb[fi] ? loff[fi] + bin : dummy;
                     lds_add_u64(gplane + s, gg);
                     lds_add_u64(hplane + s, hh);
@@ -227,11 +239,8 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
 // atomics; each tile of this kind holds one feature.
 template <int W>
 __global__ __launch_bounds__(HIST_TPB) void hist_global_kernel(const HistLaunch L) {
-    const uint32_t b = blockIdx.x;
-    const uint32_t xcd = b % XCDS;
-    const uint32_t k = b / XCDS;
-    const uint32_t tile_i = k % L.n_tiles;
-    const uint32_t chunk = (k / L.n_tiles) * XCDS + xcd;
+    uint32_t tile_i, chunk;
+    block_to_work(L, blockIdx.x, tile_i, chunk);
     if (chunk >= L.n_chunks) return;
     const TileDev T = L.tiles[tile_i];
     const TileFeatDev F = L.feats[T.feat_base];
@@ -267,7 +276,7 @@ __global__ __launch_bounds__(HIST_TPB) void hist_global_kernel(const HistLaunch 
 }
 
 hipError_t launch_hist_global(const HistLaunch &L, int width, hipStream_t s) {
-    const uint32_t blocks = L.chunk_groups * XCDS * L.n_tiles;
+    const uint32_t blocks = L.linear ? L.n_chunks * L.n_tiles : L.chunk_groups * XCDS * L.n_tiles;
     if (blocks == 0) return hipSuccess;
     if (width == 1)
         hipLaunchKernelGGL(hist_global_kernel<1>, dim3(blocks), dim3(HIST_TPB), 0, s, L);
@@ -278,7 +287,7 @@ hipError_t launch_hist_global(const HistLaunch &L, int width, hipStream_t s) {
 
 template <int W, int RD, int TPB, bool STREAM>
 static hipError_t launch_hist_t(const HistLaunch &L, size_t lds, hipStream_t s) {
-    const uint32_t blocks = L.chunk_groups * XCDS * L.n_tiles;
+    const uint32_t blocks = L.linear ? L.n_chunks * L.n_tiles : L.chunk_groups * XCDS * L.n_tiles;
     if (blocks == 0) return hipSuccess;
     // gfx950 has 160 KiB of LDS per workgroup; opt in beyond the 64 KiB
     // default (a per-function attribute, set once per device).
@@ -447,19 +456,50 @@ __global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, 
     atomicAdd(&acc_sh, acc);
     __syncthreads();
     unsigned long long acc_nodes = 0;
-    if (threadIdx.x == 0) {
-        uint64_t r;
-        if (rule.fixed) {
-            r = rule.fixed;
-        } else {
-            r = (acc_sh + rule.want_chunks - 1) / rule.want_chunks;
-            r = (r + 1023) & ~uint64_t(1023);
-            r = r < rule.min_rows ? rule.min_rows : (r > rule.max_rows ? rule.max_rows : r);
+    // Rows per chunk: the smallest multiple of 1024 whose chunks fit one wave
+    // (binary search; each step one block sum of ceil(len / rows)), as the
+    // host plans it.
+    if (rule.fixed) {
+        if (threadIdx.x == 0) cr_sh = rule.fixed;
+    } else {
+        const uint64_t acc_all = acc_sh;
+        uint32_t nz = 0;
+        for (uint32_t i = threadIdx.x; i < n; i += 1024) {
+            const PairDev P = pairs[i];
+            if (P.eval_index == NO_SLOT) continue;
+            const uint32_t nl = P.req == NO_SLOT ? 0u : totals[P.req];
+            nz += min(nl, P.row_len - nl) ? 1u : 0u;
         }
-        cr_sh = (uint32_t)r;
-        *chunk_rows_out = (uint32_t)r;
+        uint32_t n_nz;
+        (void)block_scan_1024(nz, buf, n_nz);
+        const uint64_t W = rule.want_chunks;
+        uint64_t lo = (acc_all + W * 1024 - 1) / (W * 1024);
+        lo = lo < 1 ? 1 : lo;
+        if (W > n_nz) {
+            const uint64_t room = W - n_nz;
+            uint64_t hi = (acc_all + room * 1024 - 1) / (room * 1024);
+            hi = hi < lo ? lo : hi;
+            while (lo < hi) {  // uniform: every thread holds the same bounds
+                const uint64_t mid = (lo + hi) / 2, rows = mid * 1024;
+                uint32_t k = 0;
+                for (uint32_t i = threadIdx.x; i < n; i += 1024) {
+                    const PairDev P = pairs[i];
+                    if (P.eval_index == NO_SLOT) continue;
+                    const uint32_t nl = P.req == NO_SLOT ? 0u : totals[P.req];
+                    k += (uint32_t)((min(nl, P.row_len - nl) + rows - 1) / rows);
+                }
+                uint32_t total_k;
+                (void)block_scan_1024(k, buf, total_k);
+                if (total_k <= W) hi = mid;
+                else lo = mid + 1;
+            }
+        }
+        uint64_t r = lo * 1024;
+        r = r < rule.min_rows ? rule.min_rows : (r > rule.max_rows ? rule.max_rows : r);
+        if (threadIdx.x == 0) cr_sh = (uint32_t)r;
     }
     __syncthreads();
+    if (threadIdx.x == 0) *chunk_rows_out = cr_sh;
     const uint32_t cr = cr_sh;
     uint32_t carry = 0;
     for (uint32_t base = 0; base < n; base += 1024) {
