@@ -106,27 +106,38 @@ def train_workload(args, X, y, params, desc: str, traffic_tag: str):
     from ferrisboost_amd import _native as N
 
     rounds = args.warmup + args.steps
-    # The round loop collects each tree a round late; hip_sync_round makes it
-    # wait for the device before the first timed round, so the timed rounds
-    # are bracketed by device synchronisation on both sides.
-    gparams = dict(params, device="cuda:0", hip_profile=True, hip_sync_round=args.warmup)
-    t0 = time.time()
-    model = fb.train(gparams, X, y, num_boost_round=rounds)
-    log(f"trained {rounds} rounds in {time.time() - t0:.1f}s "
-        f"(setup {model.stats['setup_seconds']:.1f}s, device sigmoid "
-        f"{model.stats['device_sigmoid']})")
-    wall = np.zeros(rounds)
-    hms = np.zeros(rounds)
-    hbytes = np.zeros(rounds, np.uint64)
-    n = N.train_lib().fbt_last_round_stats(N.ptr(wall), N.ptr(hms), N.ptr(hbytes), rounds)
-    assert n == rounds
     timed = slice(args.warmup, rounds)
+
+    def run(profile: bool):
+        # The round loop collects each tree a round late; hip_sync_round makes
+        # it wait for the device before the first timed round, so the timed
+        # rounds are bracketed by device synchronisation on both sides.
+        gparams = dict(params, device="cuda:0", hip_profile=profile, hip_sync_round=args.warmup)
+        t0 = time.time()
+        model = fb.train(gparams, X, y, num_boost_round=rounds)
+        log(f"trained {rounds} rounds in {time.time() - t0:.1f}s "
+            f"(profile {profile}, setup {model.stats['setup_seconds']:.1f}s, device sigmoid "
+            f"{model.stats['device_sigmoid']})")
+        wall = np.zeros(rounds)
+        hms = np.zeros(rounds)
+        hbytes = np.zeros(rounds, np.uint64)
+        n = N.train_lib().fbt_last_round_stats(N.ptr(wall), N.ptr(hms), N.ptr(hbytes), rounds)
+        assert n == rounds
+        return model, wall, hms, hbytes
+
+    # The throughput comes from a run without event timing; the histogram
+    # kernels are timed (HIP events on their dispatches) in a second run.
+    model, wall, _, _ = run(False)
     t_wall = float(wall[timed].sum())
+    pmodel, _, hms, hbytes = run(True)
+    # Both runs grow the same trees (the device path is deterministic).
+    same_runs = all(np.array_equal(model.tree_nodes(t), pmodel.tree_nodes(t))
+                    for t in range(rounds))
     t_hist_ms = float(hms[timed].sum())
     b_hist = float(hbytes[timed].astype(np.float64).sum())
     hist_gbps = b_hist / (t_hist_ms * 1e-3) / 1e9 if t_hist_ms > 0 else 0.0
-    launches = int(model.stats["hist_launches"])
-    bytes_per_launch = float(model.stats["hist_bytes"]) / launches if launches else 0.0
+    launches = int(pmodel.stats["hist_launches"])
+    bytes_per_launch = float(pmodel.stats["hist_bytes"]) / launches if launches else 0.0
     traffic = load_traffic(os.path.join(ROOT, "profiles", f"hist_traffic_{traffic_tag}.txt"))
     roofline = {
         "bound": "hbm",
@@ -181,6 +192,7 @@ def train_workload(args, X, y, params, desc: str, traffic_tag: str):
         "roofline": roofline,
         "cpu_baseline": cpu,
         "parity_first_rounds_vs_cpu": parity,
+        "repeat_runs_identical": same_runs,
     })
     return out
 

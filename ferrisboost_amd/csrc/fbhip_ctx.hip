@@ -1335,6 +1335,11 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
               "histogram clear");
     if (E.n_hn && E.grid_chunks) {
         const size_t ev = c->ev_used;
+        // Timing: the first resident launch takes the start event and the
+        // last one the stop event on their dispatch; streamed windows (host
+        // copies in between) are bracketed by event records instead.
+        hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+        const bool marker = c->timing && (!c->streamed.empty() || c->groups.empty());
         if (c->timing) {
             if (c->ev_pool.size() <= ev) {
                 hipEvent_t a, b;
@@ -1342,7 +1347,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
                 check(hipEventCreate(&b), "event");
                 c->ev_pool.push_back({a, b});
             }
-            check(hipEventRecord(c->ev_pool[ev].first, c->stream), "event");
+            if (marker) check(hipEventRecord(c->ev_pool[ev].first, c->stream), "event");
         }
         auto launch_base = [&]() {
             HistLaunch L{};
@@ -1362,15 +1367,21 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
             L.hist_width = c->hist_width;
             return L;
         };
-        for (const auto &g : c->groups) {
+        for (size_t gi = 0; gi < c->groups.size(); gi++) {
+            const auto &g = c->groups[gi];
             HistLaunch L = launch_base();
             L.tiles = c->d_tiles + g.tile_begin;
             L.n_tiles = g.n_tiles;
+            if (c->timing && !marker) {
+                ev_start = gi == 0 ? c->ev_pool[ev].first : nullptr;
+                ev_stop = gi + 1 == c->groups.size() ? c->ev_pool[ev].second : nullptr;
+            }
             if (g.global)
-                check(launch_hist_global(L, g.width, c->stream), "histogram launch");
+                check(launch_hist_global(L, g.width, ev_start, ev_stop, c->stream),
+                      "histogram launch");
             else
                 check(launch_hist(L, g.width, g.rd, (int)c->hist_tpb, false,
-                                  (size_t)(g.lds_max + 64) * 16, c->stream),
+                                  (size_t)(g.lds_max + 64) * 16, ev_start, ev_stop, c->stream),
                       "histogram launch");
         }
         // Streamed tiles: row windows of their pinned host records go up
@@ -1395,7 +1406,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
                 L.row_lo = (uint32_t)lo;
                 L.row_hi = (uint32_t)hi;
                 check(launch_hist(L, (int)t.width, (int)(t.rec / 4), 256, true,
-                                  (size_t)(sd.lds_slots + 64) * 16, c->stream),
+                                  (size_t)(sd.lds_slots + 64) * 16, nullptr, nullptr, c->stream),
                       "streamed histogram launch");
                 check(hipEventRecord(c->win_free[b], c->stream), "event");
             }
@@ -1403,7 +1414,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
         }
         c->hist_launches++;
         if (c->timing) {
-            check(hipEventRecord(c->ev_pool[ev].second, c->stream), "event");
+            if (marker) check(hipEventRecord(c->ev_pool[ev].second, c->stream), "event");
             c->ev_used++;
         }
     }

@@ -241,9 +241,12 @@ const char *last_error();
 // ---------------------------------------------------------------- launchers
 // threads_per_block is 256, 512 or 1024.
 // stream: L describes one streamed tile window (see HistLaunch).
+// ev_start / ev_stop (nullable) take the launch's start / end time.
 hipError_t launch_hist(const HistLaunch &L, int width, int rec_dwords, int threads_per_block,
-                       bool stream, size_t lds_bytes, hipStream_t s);
-hipError_t launch_hist_global(const HistLaunch &L, int width, hipStream_t s);
+                       bool stream, size_t lds_bytes, hipEvent_t ev_start, hipEvent_t ev_stop,
+                       hipStream_t s);
+hipError_t launch_hist_global(const HistLaunch &L, int width, hipEvent_t ev_start,
+                              hipEvent_t ev_stop, hipStream_t s);
 hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slots, uint32_t n,
                              hipStream_t s);
 // dev_n (nullable): the triple count read on the device, n its upper bound.

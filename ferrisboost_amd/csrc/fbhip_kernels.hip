@@ -20,6 +20,8 @@
 #include "fb_expf.h"
 #include "fbhip_internal.h"
 
+#include <hip/hip_ext.h>
+
 #include <math.h>
 
 #include <algorithm>
@@ -275,18 +277,22 @@ __global__ __launch_bounds__(HIST_TPB) void hist_global_kernel(const HistLaunch 
     }
 }
 
-hipError_t launch_hist_global(const HistLaunch &L, int width, hipStream_t s) {
+hipError_t launch_hist_global(const HistLaunch &L, int width, hipEvent_t ev_start,
+                              hipEvent_t ev_stop, hipStream_t s) {
     const uint32_t blocks = L.linear ? L.n_chunks * L.n_tiles : L.chunk_groups * XCDS * L.n_tiles;
     if (blocks == 0) return hipSuccess;
     if (width == 1)
-        hipLaunchKernelGGL(hist_global_kernel<1>, dim3(blocks), dim3(HIST_TPB), 0, s, L);
+        hipExtLaunchKernelGGL(hist_global_kernel<1>, dim3(blocks), dim3(HIST_TPB), 0, s, ev_start,
+                              ev_stop, 0, L);
     else
-        hipLaunchKernelGGL(hist_global_kernel<2>, dim3(blocks), dim3(HIST_TPB), 0, s, L);
+        hipExtLaunchKernelGGL(hist_global_kernel<2>, dim3(blocks), dim3(HIST_TPB), 0, s, ev_start,
+                              ev_stop, 0, L);
     return hipGetLastError();
 }
 
 template <int W, int RD, int TPB, bool STREAM>
-static hipError_t launch_hist_t(const HistLaunch &L, size_t lds, hipStream_t s) {
+static hipError_t launch_hist_t(const HistLaunch &L, size_t lds, hipEvent_t ev_start,
+                                hipEvent_t ev_stop, hipStream_t s) {
     const uint32_t blocks = L.linear ? L.n_chunks * L.n_tiles : L.chunk_groups * XCDS * L.n_tiles;
     if (blocks == 0) return hipSuccess;
     // gfx950 has 160 KiB of LDS per workgroup; opt in beyond the 64 KiB
@@ -306,24 +312,27 @@ static hipError_t launch_hist_t(const HistLaunch &L, size_t lds, hipStream_t s) 
         if (e != hipSuccess) return e;
         attr_done |= 1ull << dev;
     }
-    hipLaunchKernelGGL((hist_kernel<W, RD, 4, TPB, STREAM>), dim3(blocks), dim3(TPB), lds, s, L);
+    // Timing events ride on the dispatch itself (no separate marker packets).
+    hipExtLaunchKernelGGL((hist_kernel<W, RD, 4, TPB, STREAM>), dim3(blocks), dim3(TPB),
+                          (uint32_t)lds, s, ev_start, ev_stop, 0, L);
     return hipGetLastError();
 }
 
 template <int W, int RD>
 static hipError_t launch_hist_wr(const HistLaunch &L, int tpb, bool stream, size_t lds,
-                                 hipStream_t s) {
-    if (stream) return launch_hist_t<W, RD, 256, true>(L, lds, s);
-    if (tpb == 256) return launch_hist_t<W, RD, 256, false>(L, lds, s);
-    if (tpb == 512) return launch_hist_t<W, RD, 512, false>(L, lds, s);
-    if (tpb == 1024) return launch_hist_t<W, RD, 1024, false>(L, lds, s);
+                                 hipEvent_t e0, hipEvent_t e1, hipStream_t s) {
+    if (stream) return launch_hist_t<W, RD, 256, true>(L, lds, e0, e1, s);
+    if (tpb == 256) return launch_hist_t<W, RD, 256, false>(L, lds, e0, e1, s);
+    if (tpb == 512) return launch_hist_t<W, RD, 512, false>(L, lds, e0, e1, s);
+    if (tpb == 1024) return launch_hist_t<W, RD, 1024, false>(L, lds, e0, e1, s);
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_hist(const HistLaunch &L, int width, int rd, int tpb, bool stream, size_t lds,
-                       hipStream_t s) {
+                       hipEvent_t ev_start, hipEvent_t ev_stop, hipStream_t s) {
 #define FBH_HIST_WR(WW, R) \
-    if (width == WW && rd == R) return launch_hist_wr<WW, R>(L, tpb, stream, lds, s);
+    if (width == WW && rd == R) \
+        return launch_hist_wr<WW, R>(L, tpb, stream, lds, ev_start, ev_stop, s);
     FBH_HIST_WR(1, 1) FBH_HIST_WR(1, 2) FBH_HIST_WR(1, 3) FBH_HIST_WR(1, 4)
     FBH_HIST_WR(1, 8) FBH_HIST_WR(1, 12) FBH_HIST_WR(1, 16)
     FBH_HIST_WR(2, 1) FBH_HIST_WR(2, 2) FBH_HIST_WR(2, 3) FBH_HIST_WR(2, 4)
