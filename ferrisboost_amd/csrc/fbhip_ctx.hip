@@ -220,7 +220,9 @@ struct fbh_ctx {
         };
         std::deque<Job> pending;
     } grow;
-    size_t off_tilefeats = 0, off_sfeats = 0;  // offsets in the tree-table buffer
+    size_t off_tilefeats = 0, off_sfeats = 0, off_order = 0;  // offsets in the tree-table buffer
+    uint32_t *d_split_order = nullptr;  // tree features: numeric positions, then categorical
+    uint32_t n_split_num = 0, n_split_cat = 0;
     size_t stage_bytes = 0;
     uint64_t max_chunks = 0;    // capacity of the partition chunk arrays
     uint64_t cat_in_words = 0;  // capacity of the partition category words
@@ -549,11 +551,13 @@ void fixed_allocations(fbh_ctx &c, A &&a) {
     // buffer so that a tree's plan goes to the device in one copy.
     c.off_tilefeats = al256(sizeof(TileDev) * c.tiles.size());
     c.off_sfeats = c.off_tilefeats + al256(sizeof(TileFeatDev) * c.n_features);
+    c.off_order = c.off_sfeats + al256(sizeof(SplitFeatDev) * c.n_features);
     uint8_t *tt = static_cast<uint8_t *>(
-        a(c.off_sfeats + sizeof(SplitFeatDev) * c.n_features, "tree tables"));
+        a(c.off_order + 4 * (uint64_t)c.n_features, "tree tables"));
     c.d_tiles = reinterpret_cast<TileDev *>(tt);
     c.d_tilefeats = reinterpret_cast<TileFeatDev *>(tt ? tt + c.off_tilefeats : nullptr);
     c.d_sfeats = reinterpret_cast<SplitFeatDev *>(tt ? tt + c.off_sfeats : nullptr);
+    c.d_split_order = reinterpret_cast<uint32_t *>(tt ? tt + c.off_order : nullptr);
     const uint64_t cw = std::max(1u, c.max_cat_words);
     c.d_cands = static_cast<FeatCandDev *>(
         a(sizeof(FeatCandDev) * (uint64_t)c.n_slots * c.n_features, "split candidates"));
@@ -583,7 +587,7 @@ void fixed_allocations(fbh_ctx &c, A &&a) {
     const size_t pair_tables = sizeof(PairDev) * MAX_NODES + 256;
     c.stage_bytes = std::max<size_t>(
         {eval_tables + part_tables + pair_tables,
-         c.off_sfeats + sizeof(SplitFeatDev) * c.n_features});
+         c.off_order + 4 * (size_t)c.n_features});
     c.d_stage = static_cast<uint8_t *>(a(c.stage_bytes, "launch tables"));
 }
 
@@ -1249,10 +1253,21 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
         c->cat_words_per_node = cat_base;
         // The tables go up only when they differ from the last tree's (every
         // tree of a run without column sampling has the same).
-        std::vector<uint8_t> tables(c->off_sfeats + sizeof(SplitFeatDev) * sf.size(), 0);
+        // Split-scan order: numeric features of at most 256 bins (one wave
+        // each, four bins a lane), then the others (one workgroup each).
+        auto by_wave = [&](uint32_t j) { return !sf[j].categorical && sf[j].n_bins <= 256; };
+        std::vector<uint32_t> order;
+        for (uint32_t j = 0; j < sf.size(); j++)
+            if (by_wave(j)) order.push_back(j);
+        c->n_split_num = (uint32_t)order.size();
+        for (uint32_t j = 0; j < sf.size(); j++)
+            if (!by_wave(j)) order.push_back(j);
+        c->n_split_cat = (uint32_t)(order.size() - c->n_split_num);
+        std::vector<uint8_t> tables(c->off_order + 4 * order.size(), 0);
         std::memcpy(tables.data(), td.data(), sizeof(TileDev) * td.size());
         std::memcpy(tables.data() + c->off_tilefeats, tf.data(), sizeof(TileFeatDev) * tf.size());
         std::memcpy(tables.data() + c->off_sfeats, sf.data(), sizeof(SplitFeatDev) * sf.size());
+        std::memcpy(tables.data() + c->off_order, order.data(), 4 * order.size());
         const bool upload = tables != c->tree_tables;
         if (upload) {
             std::memcpy(c->pin_small.p, tables.data(), tables.size());
@@ -1433,7 +1448,8 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
     P.max_cat_threshold = sp->max_cat_threshold;
     P.n_feats = (uint32_t)c->tree_feats.size();
     P.cat_words_per_node = c->cat_words_per_node;
-    check(launch_split_feats(c->hist, c->hist_width, E.sn, E.n_nodes, c->d_sfeats, E.enabled, P,
+    check(launch_split_feats(c->hist, c->hist_width, E.sn, E.n_nodes, c->d_sfeats,
+                             c->d_split_order, c->n_split_num, c->n_split_cat, E.enabled, P,
                              c->d_cands, c->d_cat_scratch, E.dev_n_nodes, c->stream),
           "split scan");
     const uint32_t cw = std::max(1u, c->cat_words_per_node);

@@ -275,8 +275,12 @@ hipError_t launch_grow_decide(const GrowParamsDev &G, uint32_t depth, const Spli
                               PartReqDev *reqs, PairDev *pairs, uint32_t *triples,
                               LeafDev *leaves, float *leaf_vals, GrowState *st, hipStream_t s);
 hipError_t launch_leaf_plan(LeafDev *leaves, GrowState *st, hipStream_t s);
+// order: the tree's feature positions, n_num numeric ones of at most 256
+// bins first (one wave each), then n_cat others, categorical or wider (one
+// workgroup each).
 hipError_t launch_split_feats(const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
-                              uint32_t n_nodes, const SplitFeatDev *feats, const uint8_t *enabled,
+                              uint32_t n_nodes, const SplitFeatDev *feats, const uint32_t *order,
+                              uint32_t n_num, uint32_t n_cat, const uint8_t *enabled,
                               SplitParamsDev P, FeatCandDev *cands, uint64_t *cat_scratch,
                               const uint32_t *dev_n, hipStream_t s);
 hipError_t launch_split_nodes(const FeatCandDev *cands, const SplitFeatDev *feats,

@@ -882,19 +882,121 @@ __device__ void split_categorical(const int64_t *h, uint32_t n, const SplitNodeD
     }
 }
 
+__device__ __forceinline__ int64_t wave_scan_incl_i64(int64_t v, uint32_t lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int64_t t = __shfl_up(v, off, 64);
+        if (lane >= (uint32_t)off) v = wadd(v, t);
+    }
+    return v;
+}
+
+// The best of the wave's candidates by the total order of `better` (gain,
+// then the lower ordinal): every lane ends with the same one.
+__device__ __forceinline__ Best wave_best(Best b) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        Best o;
+        o.gain = __shfl_xor(b.gain, off, 64);
+        o.ord = __shfl_xor(b.ord, off, 64);
+        o.found = __shfl_xor(b.found, off, 64);
+        o.lg = __shfl_xor(b.lg, off, 64);
+        o.lh = __shfl_xor(b.lh, off, 64);
+        if (better(o, b)) b = o;
+    }
+    return b;
+}
+
+// One wave per (numeric feature, node), four features per workgroup: the
+// numeric scan of split_feat_kernel on 64 lanes with shuffles only (no
+// barriers). Each lane takes a run of bins; integer prefix sums are exact in
+// any order, and the argmax keeps the reference's tie rule.
+__global__ __launch_bounds__(256) void split_num_kernel(
+    const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
+    const SplitFeatDev *feats, const uint32_t *order, uint32_t n_num, const uint8_t *enabled,
+    SplitParamsDev P, FeatCandDev *cands, const uint32_t *dev_n) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t li = blockIdx.x * 4 + wave, ni = blockIdx.y;
+    if (dev_n && ni >= *dev_n) return;
+    if (li >= n_num) return;  // a whole wave
+    const uint32_t j = order[li];
+    const SplitFeatDev F = feats[j];
+    const SplitNodeDev N = nodes[ni];
+    FeatCandDev *outc = cands + (size_t)ni * P.n_feats + j;
+    if (enabled && !enabled[(size_t)ni * P.n_feats + j]) {
+        if (lane == 0) outc->found = 0;
+        return;
+    }
+    const int64_t *h = hist + ((uint64_t)N.slot * hist_width + F.hist_off) * 2u;
+    const double ng = (double)N.sum_g * P.inv_g, nh = (double)N.sum_h * P.inv_h;
+    const float parent = gain_given_weight(ng, nh, apply_bounds(xgb_weight(ng, nh, P), N.lower,
+                                                                N.upper), P);
+    const uint32_t n = F.n_bins;
+    const uint32_t per = (n + 63) / 64;
+    const uint32_t b0 = min(lane * per, n), b1 = min(b0 + per, n);
+    int64_t tg = 0, th = 0;
+    for (uint32_t bb = b0; bb < b1; bb++) {
+        tg = wadd(tg, h[2 * bb]);
+        th = wadd(th, h[2 * bb + 1]);
+    }
+    const int64_t ig = wave_scan_incl_i64(tg, lane), ih = wave_scan_incl_i64(th, lane);
+    const int64_t eg = wsub(ig, tg), eh = wsub(ih, th);
+    const int64_t totg = __shfl(ig, 63, 64), toth = __shfl(ih, 63, 64);
+
+    Best best{0.0f, 0u, 0u, 0, 0};
+    const int mono = F.monotone;
+    // Forward: missing rows go right.
+    int64_t lg = eg, lh = eh;
+    for (uint32_t bb = b0; bb < b1; bb++) {
+        lg = wadd(lg, h[2 * bb]);
+        lh = wadd(lh, h[2 * bb + 1]);
+        float gain;
+        if (candidate_gain(lg, lh, wsub(N.sum_g, lg), wsub(N.sum_h, lh), parent, mono, N.lower,
+                           N.upper, P, gain))
+            offer(best, gain, bb, lg, lh);
+    }
+    // Reverse: missing rows go left; skipped when the bins hold the whole node.
+    if (!(totg == N.sum_g && toth == N.sum_h)) {
+        int64_t rg = wsub(wsub(totg, eg), tg), rh = wsub(wsub(toth, eh), th);
+        for (uint32_t bb = b1; bb-- > b0;) {
+            rg = wadd(rg, h[2 * bb]);
+            rh = wadd(rh, h[2 * bb + 1]);
+            const int64_t l2g = wsub(N.sum_g, rg), l2h = wsub(N.sum_h, rh);
+            float gain;
+            if (candidate_gain(l2g, l2h, rg, rh, parent, mono, N.lower, N.upper, P, gain))
+                offer(best, gain, n + (n - 1 - bb), l2g, l2h);
+        }
+    }
+    best = wave_best(best);
+    if (lane == 0) {
+        outc->found = best.found;
+        outc->gain = best.gain;
+        if (best.ord < n) {
+            outc->bin = best.ord + 1;
+            outc->missing_left = 0;
+        } else {
+            outc->bin = n - 1 - (best.ord - n);
+            outc->missing_left = 1;
+        }
+        outc->left_g = best.lg;
+        outc->left_h = best.lh;
+    }
+}
+
 // One workgroup per (feature, node): prefix sums of the feature's bins, the
 // forward (missing right) and reverse (missing left, only when the node has
 // missing mass) candidates, and the first best by the reference's rules.
 __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
     const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
-    const SplitFeatDev *feats, const uint8_t *enabled, SplitParamsDev P, FeatCandDev *cands,
-    uint64_t *cat_scratch, const uint32_t *dev_n) {
+    const SplitFeatDev *feats, const uint32_t *order, uint32_t order_off, const uint8_t *enabled,
+    SplitParamsDev P, FeatCandDev *cands, uint64_t *cat_scratch, const uint32_t *dev_n) {
     __shared__ Best shb[SPLIT_TPB];
     __shared__ int64_t sg[SPLIT_TPB], shh[SPLIT_TPB];
     extern __shared__ unsigned char dyn[];
 
-    const uint32_t j = blockIdx.x, ni = blockIdx.y, tid = threadIdx.x;
+    const uint32_t ni = blockIdx.y, tid = threadIdx.x;
     if (dev_n && ni >= *dev_n) return;
+    const uint32_t j = order[order_off + blockIdx.x];
     const SplitFeatDev F = feats[j];
     const SplitNodeDev N = nodes[ni];
     FeatCandDev *outc = cands + (size_t)ni * P.n_feats + j;
@@ -970,14 +1072,22 @@ __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
 }
 
 hipError_t launch_split_feats(const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
-                              uint32_t n_nodes, const SplitFeatDev *feats, const uint8_t *enabled,
+                              uint32_t n_nodes, const SplitFeatDev *feats, const uint32_t *order,
+                              uint32_t n_num, uint32_t n_cat, const uint8_t *enabled,
                               SplitParamsDev P, FeatCandDev *cands, uint64_t *cat_scratch,
                               const uint32_t *dev_n, hipStream_t s) {
     if (n_nodes == 0 || P.n_feats == 0) return hipSuccess;
-    const size_t dyn = P.cat_words_per_node ? (sizeof(float) + sizeof(uint32_t)) * MAX_DEVICE_CATS
-                                            : 0;
-    hipLaunchKernelGGL(split_feat_kernel, dim3(P.n_feats, n_nodes), dim3(SPLIT_TPB), dyn, s, hist,
-                       hist_width, nodes, feats, enabled, P, cands, cat_scratch, dev_n);
+    if (n_num)
+        hipLaunchKernelGGL(split_num_kernel, dim3((n_num + 3) / 4, n_nodes), dim3(256), 0, s, hist,
+                           hist_width, nodes, feats, order, n_num, enabled, P, cands, dev_n);
+    if (n_cat) {
+        const size_t dyn = P.cat_words_per_node
+                               ? (sizeof(float) + sizeof(uint32_t)) * MAX_DEVICE_CATS
+                               : 0;
+        hipLaunchKernelGGL(split_feat_kernel, dim3(n_cat, n_nodes), dim3(SPLIT_TPB), dyn, s, hist,
+                           hist_width, nodes, feats, order, n_num, enabled, P, cands, cat_scratch,
+                           dev_n);
+    }
     return hipGetLastError();
 }
 
