@@ -209,6 +209,7 @@ struct fbh_ctx {
         LeafDev *leaves = nullptr;
         float *leaf_vals = nullptr;
         DevColumn *cols = nullptr;
+        uint16_t *feat_off = nullptr;  // byte offset of each feature in the row bundle (leaf walk)
         // Two result slots (state, tree, category words, leaf values), so a
         // tree can be collected while the next one is already enqueued.
         PinnedBuf out[2];
@@ -1899,6 +1900,15 @@ namespace {
 
 constexpr uint32_t MAX_GROW_DEPTH = 14;
 
+// Every tile's records in one row bundle: a row's cells for every feature
+// are in one record, so leaves can be found by walking the tree in row order.
+bool single_bundle(const fbh_ctx &c) {
+    if (c.bundles.size() != 1) return false;
+    for (const auto &t : c.tiles)
+        if (t.bundle != 0 || t.global) return false;
+    return true;
+}
+
 // Buffers of device-grown trees up to depth D (grown, never shrunk).
 void ensure_grow(fbh_ctx *c, uint32_t D) {
     auto &G = c->grow;
@@ -1911,6 +1921,17 @@ void ensure_grow(fbh_ctx *c, uint32_t D) {
         check(hipMemcpy(G.cols, cols.data(), sizeof(DevColumn) * cols.size(),
                         hipMemcpyHostToDevice),
               "column table");
+        if (single_bundle(*c)) {
+            std::vector<uint16_t> off(c->n_features);
+            for (uint32_t f = 0; f < c->n_features; f++) {
+                const auto &t = c->tiles[c->feat_tile[f]];
+                off[f] = (uint16_t)((t.bundle_off + c->feat_pos[f] * t.width) |
+                                    (t.width == 2 ? 0x8000u : 0u));
+            }
+            G.feat_off = c->alloc<uint16_t>(c->n_features, "grown tree feature offsets");
+            check(hipMemcpy(G.feat_off, off.data(), 2 * off.size(), hipMemcpyHostToDevice),
+                  "feature offsets");
+        }
     }
     if (G.depth >= D) return;
     if (!G.pending.empty())
@@ -2026,6 +2047,10 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     account_hist(c, n_rows, 1);
 
     const ChunkRule rule = c->chunk_rule();
+    // Leaves by a row-order walk of the finished tree (no last-level
+    // partition, no scattered leaf ids) when one bundle holds every cell and
+    // the tree fits the walk's LDS table.
+    const bool walk = GB.feat_off && ((2u << D) - 1) <= MAX_WALK_NODES;
     uint8_t *pk_base = reinterpret_cast<uint8_t *>(c->d_packets);
     for (uint32_t d = 0; d < D; d++) {
         const uint32_t nb = lvl_bound(d);
@@ -2035,6 +2060,7 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
                                  GB.tree_cats, d_mono, GB.cols, GB.reqs, GB.pairs, GB.triples,
                                  GB.leaves, GB.leaf_vals, GB.st, c->stream),
               "tree level decision");
+        if (walk && d + 1 == D) break;  // the last level's children are found by the walk
         // Level d's rows are in arena d % 2; its children go to the other.
         uint32_t *arena_in = (d & 1) ? c->tmp : c->rows;
         uint32_t *arena_out = (d & 1) ? c->rows : c->tmp;
@@ -2065,17 +2091,26 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
         E.rows = arena_out;
         enqueue_eval(c, E, sp);
     }
-    check(launch_leaf_plan(GB.leaves, GB.st, c->stream), "leaf plan");
     uint64_t leaf_bound = (uint64_t)1 << D;
     if (gp->max_leaves) leaf_bound = std::min<uint64_t>(leaf_bound, gp->max_leaves);
     const int idb = c->objective >= 0 ? (leaf_bound <= 256 ? 1 : 2) : 0;
-    check(launch_assign_leaves(GB.leaves, 0, (uint32_t)(n_rows / PART_CHUNK + leaf_bound + 1),
-                               c->rows, c->tmp, c->delta, c->leaf_ids, idb, &GB.st->n_leaves,
-                               c->stream),
-          "leaf assignment");
-    if (idb)
-        check(launch_apply_leaves(c->leaf_ids, idb, GB.leaf_vals, c->n_rows, c->margin, c->stream),
-              "margin update");
+    if (walk) {
+        check(launch_tree_leaves(c->bundles[0].data, c->bundles[0].pitch, c->n_rows, GB.tree,
+                                 GB.tree_cats, GB.feat_off, GB.st, c->leaf_ids, idb, c->margin,
+                                 c->delta, GB.leaf_vals, c->stream),
+              "leaf walk");
+    } else {
+        check(launch_leaf_plan(GB.leaves, GB.st, c->stream), "leaf plan");
+        check(launch_assign_leaves(GB.leaves, 0,
+                                   (uint32_t)(n_rows / PART_CHUNK + leaf_bound + 1), c->rows,
+                                   c->tmp, c->delta, c->leaf_ids, idb, &GB.st->n_leaves,
+                                   c->stream),
+              "leaf assignment");
+        if (idb)
+            check(launch_apply_leaves(c->leaf_ids, idb, GB.leaf_vals, c->n_rows, c->margin,
+                                      c->stream),
+                  "margin update");
+    }
     c->leaf_id_bytes = idb;
     c->ids_fresh = idb != 0;
 

@@ -14,6 +14,7 @@ constexpr int PART_CHUNK = 2048;   // rows of one partition chunk (8 per thread)
 constexpr int XCDS = 8;            // MI355X accelerator complex dies
 constexpr uint32_t NO_SLOT = 0xFFFFFFFFu;
 constexpr uint32_t MAX_GROW_SLOTS = 16384;  // histogram slots a device-grown tree can use
+constexpr uint32_t MAX_WALK_NODES = 1024;   // tree nodes the row-order leaf walk holds in LDS
 
 // One histogram tile: a group of features of one width stored as row
 // records, record i at data + i * stride, feature k of the tile at byte
@@ -275,6 +276,13 @@ hipError_t launch_grow_decide(const GrowParamsDev &G, uint32_t depth, const Spli
                               PartReqDev *reqs, PairDev *pairs, uint32_t *triples,
                               LeafDev *leaves, float *leaf_vals, GrowState *st, hipStream_t s);
 hipError_t launch_leaf_plan(LeafDev *leaves, GrowState *st, hipStream_t s);
+// Leaves of a device-grown tree by a row-order walk over the single row
+// bundle (feat_off[f]: byte offset of feature f in the bundle row, bit 15 set
+// for 16-bit cells); at most MAX_WALK_NODES tree nodes.
+hipError_t launch_tree_leaves(const uint8_t *bundle, uint32_t pitch, uint64_t n_rows,
+                              const TreeNodeDev *tree, const uint64_t *tree_cats,
+                              const uint16_t *feat_off, GrowState *st, void *ids, int id_bytes,
+                              float *margin, float *delta, float *leaf_vals, hipStream_t s);
 // order: the tree's feature positions, n_num numeric ones of at most 256
 // bins first (one wave each), then n_cat others, categorical or wider (one
 // workgroup each).

@@ -413,22 +413,28 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
     return v;
 }
 
-// Wave scans by shuffles, then one wave scans the 16 wave totals (buf needs
-// 32 entries).
-__device__ uint32_t block_scan_1024(uint32_t v, uint32_t *buf, uint32_t &total) {
+// Exclusive block scan: wave scans by shuffles, then one wave scans the
+// wave totals (blockDim.x a multiple of 64, at most 1024; buf needs 32
+// entries).
+__device__ uint32_t block_scan(uint32_t v, uint32_t *buf, uint32_t &total) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t nw = blockDim.x >> 6;
     const uint32_t incl = wave_incl_scan(v);
     if (lane == 63) buf[wave] = incl;
     __syncthreads();
     if (wave == 0) {
-        const uint32_t w = wave_incl_scan(lane < 16 ? buf[lane] : 0u);
-        if (lane < 16) buf[16 + lane] = w;
+        const uint32_t w = wave_incl_scan(lane < nw ? buf[lane] : 0u);
+        if (lane < nw) buf[16 + lane] = w;
     }
     __syncthreads();
     const uint32_t before = wave ? buf[16 + wave - 1] : 0u;
-    total = buf[31];
+    total = buf[16 + nw - 1];
     __syncthreads();
     return before + incl - v;
+}
+
+__device__ __forceinline__ uint32_t block_scan_1024(uint32_t v, uint32_t *buf, uint32_t &total) {
+    return block_scan(v, buf, total);
 }
 
 // One workgroup plans the children of a fused partition + evaluation step
@@ -2161,6 +2167,140 @@ __global__ __launch_bounds__(1024) void leaf_plan_kernel(LeafDev *leaves, GrowSt
         st->leaf_chunks = total;
         st->covered = cov_sh;
     }
+}
+
+// Leaves of a device-grown tree by walking it in row order, when every tree
+// feature sits in one row bundle: the row's record gives each split's cell
+// (the partition's go-left rule: missing -> default direction, categorical
+// -> not in the right-going set, else bin < split bin). ids[row] is the
+// leaf's position among the leaves in node-id order; the margin gets the
+// leaf value with the same f32 addition as apply_leaves (or delta[row] =
+// value without an objective). This replaces the last level's partition and
+// the scattered leaf-id writes. Workgroup 0 also writes the leaf values by
+// position and the leaf count.
+template <int IDB, int PB>
+__global__ __launch_bounds__(256) void tree_leaves_kernel(
+    const uint8_t *bundle, uint64_t n_rows, const TreeNodeDev *tree, const uint64_t *tree_cats,
+    const uint16_t *feat_off, GrowState *st, void *ids, float *margin, float *delta,
+    float *leaf_vals) {
+    __shared__ uint32_t buf[32];
+    // Node: meta (bits 0-5 cell offset, 6: 16-bit cell, 7: leaf, 8: missing
+    // goes left, 9: categorical), split bin, left, right.
+    __shared__ ushort4 s_node[MAX_WALK_NODES];
+    __shared__ uint16_t s_leaf[MAX_WALK_NODES];
+    __shared__ uint32_t s_cat[MAX_WALK_NODES];
+    __shared__ uint8_t s_ncw[MAX_WALK_NODES];
+    __shared__ float s_val[MAX_WALK_NODES];
+    const uint32_t n = st->tree_size;
+    __syncthreads();  // every thread has read the size before workgroup 0 updates the state
+    uint32_t carry = 0;
+    for (uint32_t base = 0; base < n; base += blockDim.x) {
+        const uint32_t k = base + threadIdx.x;
+        uint32_t lf = 0;
+        if (k < n) {
+            const TreeNodeDev t = tree[k];
+            lf = t.flags & 1u;
+            const uint32_t fo = lf ? 0u : feat_off[t.feat];
+            const uint32_t meta = (fo & 0x3Fu) | ((fo & 0x8000u) ? 0x40u : 0u) | (lf << 7) |
+                                  ((t.flags & 2u) << 7) | ((t.flags & 4u) << 7);
+            s_node[k] = make_ushort4((uint16_t)meta, (uint16_t)t.bin, (uint16_t)t.left,
+                                     (uint16_t)t.right);
+            s_cat[k] = t.cat_off;
+            s_ncw[k] = (uint8_t)t.n_cat_words;
+            s_val[k] = t.leaf_value;
+        }
+        uint32_t tot;
+        const uint32_t before = carry + block_scan(lf, buf, tot);
+        if (k < n && lf) {
+            s_leaf[k] = (uint16_t)before;
+            if (blockIdx.x == 0) leaf_vals[before] = s_val[k];
+        }
+        carry += tot;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        st->n_leaves = carry;
+        st->covered = n_rows;
+    }
+    __syncthreads();
+    for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < n_rows;
+         r += (uint64_t)gridDim.x * blockDim.x) {
+        // The row's whole record in registers, then cells by select.
+        uint32_t rec[PB];
+#pragma unroll
+        for (int q = 0; q < PB / 4; q++) {
+            const uint4 v = reinterpret_cast<const uint4 *>(bundle + r * (PB * 4))[q];
+            rec[4 * q] = v.x;
+            rec[4 * q + 1] = v.y;
+            rec[4 * q + 2] = v.z;
+            rec[4 * q + 3] = v.w;
+        }
+        uint32_t node = 0;
+        ushort4 nd = s_node[0];
+        while (!(nd.x & 0x80u)) {
+            const uint32_t off = nd.x & 0x3Fu;
+            const uint32_t qi = off >> 2;
+            uint32_t word = rec[0];
+#pragma unroll
+            for (int q = 1; q < PB; q++) word = (qi == (uint32_t)q) ? rec[q] : word;
+            const bool w2 = (nd.x & 0x40u) != 0;
+            const uint32_t bin = (word >> ((off & 3u) * 8u)) & (w2 ? 0xFFFFu : 0xFFu);
+            const uint32_t missing = w2 ? 0xFFFFu : 0xFFu;
+            bool gl;
+            if (bin == missing) {
+                gl = (nd.x & 0x100u) != 0;
+            } else if (nd.x & 0x200u) {
+                const uint32_t w = bin >> 6;
+                gl = !(w < s_ncw[node] && ((tree_cats[s_cat[node] + w] >> (bin & 63)) & 1ull));
+            } else {
+                gl = bin < nd.y;
+            }
+            node = gl ? nd.z : nd.w;
+            nd = s_node[node];
+        }
+        if (IDB == 0) {
+            delta[r] = s_val[node];
+        } else {
+            if (IDB == 1) static_cast<uint8_t *>(ids)[r] = (uint8_t)s_leaf[node];
+            else static_cast<uint16_t *>(ids)[r] = s_leaf[node];
+            margin[r] = margin[r] + s_val[node];
+        }
+    }
+}
+
+template <int IDB>
+static void launch_walk_pb(uint32_t pitch, dim3 g, hipStream_t s, const uint8_t *bundle,
+                           uint64_t n_rows, const TreeNodeDev *tree, const uint64_t *tree_cats,
+                           const uint16_t *feat_off, GrowState *st, void *ids, float *margin,
+                           float *delta, float *leaf_vals) {
+    if (pitch == 16)
+        hipLaunchKernelGGL((tree_leaves_kernel<IDB, 4>), g, dim3(256), 0, s, bundle, n_rows, tree,
+                           tree_cats, feat_off, st, ids, margin, delta, leaf_vals);
+    else if (pitch == 32)
+        hipLaunchKernelGGL((tree_leaves_kernel<IDB, 8>), g, dim3(256), 0, s, bundle, n_rows, tree,
+                           tree_cats, feat_off, st, ids, margin, delta, leaf_vals);
+    else
+        hipLaunchKernelGGL((tree_leaves_kernel<IDB, 16>), g, dim3(256), 0, s, bundle, n_rows,
+                           tree, tree_cats, feat_off, st, ids, margin, delta, leaf_vals);
+}
+
+hipError_t launch_tree_leaves(const uint8_t *bundle, uint32_t pitch, uint64_t n_rows,
+                              const TreeNodeDev *tree, const uint64_t *tree_cats,
+                              const uint16_t *feat_off, GrowState *st, void *ids, int id_bytes,
+                              float *margin, float *delta, float *leaf_vals, hipStream_t s) {
+    if (pitch != 16 && pitch != 32 && pitch != 64) return hipErrorInvalidValue;
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((n_rows + 255) / 256, 2048);
+    if (blocks == 0) return hipSuccess;
+    const dim3 g(blocks);
+    if (id_bytes == 1)
+        launch_walk_pb<1>(pitch, g, s, bundle, n_rows, tree, tree_cats, feat_off, st, ids, margin,
+                          delta, leaf_vals);
+    else if (id_bytes == 2)
+        launch_walk_pb<2>(pitch, g, s, bundle, n_rows, tree, tree_cats, feat_off, st, ids, margin,
+                          delta, leaf_vals);
+    else
+        launch_walk_pb<0>(pitch, g, s, bundle, n_rows, tree, tree_cats, feat_off, st, ids, margin,
+                          delta, leaf_vals);
+    return hipGetLastError();
 }
 
 hipError_t launch_leaf_plan(LeafDev *leaves, GrowState *st, hipStream_t s) {

@@ -220,12 +220,17 @@ def test_sampled_weighted_rounds_match_oracle(fb, oracle, objective, depth, host
 
 
 @pytest.mark.parametrize("case", ["budget", "monotone", "categorical", "sampled_deep", "stump",
-                                  "squared"])
+                                  "squared", "walk_budget", "walk_categorical", "walk_squared"])
 def test_device_grown_trees_match_host_levels_and_oracle(fb, oracle, case):
     """Whole depthwise trees grown on the device (the max_leaves budget, node
     ids, weights, bounds, slots, partitions and leaves decided by kernels)
     equal the trees the host grows level by level and the CPU oracle's, node
-    for node, with margins equal bit for bit."""
+    for node, with margins equal bit for bit. The walk_ cases use 4 KiB tiles:
+    two features a tile, three tiles in one 16-byte row bundle, so leaves and
+    margins come from the row-order walk of the finished tree instead of a
+    last-level partition."""
+    walk = case.startswith("walk_")
+    case = case[5:] if walk else case
     rng = np.random.default_rng(sum(map(ord, case)))
     n, nf = 30_011, 6
     x = rng.normal(size=(n, nf)).astype(np.float32)
@@ -255,6 +260,8 @@ def test_device_grown_trees_match_host_levels_and_oracle(fb, oracle, case):
         y = z.astype(np.float32)
     om = oracle.train(x, y, oracle.make_params(**p), weights=w, monotone=mono, categorical=cat)
     pp = product_params(p)
+    if walk:
+        pp["hip_tile_bytes"] = 4096
     if mono:
         pp["monotone_constraints"] = mono
     if cat:
