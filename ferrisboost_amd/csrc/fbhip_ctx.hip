@@ -175,9 +175,10 @@ struct fbh_ctx {
     uint8_t *flags = nullptr;
     float *delta = nullptr;
     int64_t *hist = nullptr;
+    ScalesDev *d_scales = nullptr;  // scales of the current gradients
     double *red_f64 = nullptr;
     int64_t *red_i64 = nullptr;
-    uint32_t n_red_blocks = 1024;
+    uint32_t n_red_blocks = 8192;  // blocks of the bounds and quantisation passes
 
     // launch tables (device) and their pinned staging
     TileDev *d_tiles = nullptr;
@@ -228,7 +229,13 @@ struct fbh_ctx {
     uint64_t max_chunks = 0;    // capacity of the partition chunk arrays
     uint64_t cat_in_words = 0;  // capacity of the partition category words
 
-    PinnedBuf pin_small;   // launch tables, reused by blocking calls
+    // Pinned staging of launch tables going to the device: a ring of slots,
+    // each reused only after the copy out of it has run, so a call can
+    // return while its tables are still on their way.
+    static constexpr int STAGE_SLOTS = 4;
+    PinnedBuf pin_stage[STAGE_SLOTS];
+    hipEvent_t stage_ev[STAGE_SLOTS] = {};
+    int stage_next = 0;
     PinnedBuf pin_leaves;  // leaf tables (asynchronous call)
     PinnedBuf pin_out;     // results coming back
     size_t pin_out_spans = 0;  // offset of a fused step's spans in pin_out
@@ -295,7 +302,12 @@ struct fbh_ctx {
         for (auto &a : allocs)
             if (a.p) (void)hipFree(a.p);
         allocs.clear();
-        if (pin_small.p) (void)hipHostFree(pin_small.p);
+        for (int k = 0; k < STAGE_SLOTS; k++) {
+            if (pin_stage[k].p) (void)hipHostFree(pin_stage[k].p);
+            pin_stage[k].p = nullptr;
+            if (stage_ev[k]) (void)hipEventDestroy(stage_ev[k]);
+            stage_ev[k] = nullptr;
+        }
         if (pin_leaves.p) (void)hipHostFree(pin_leaves.p);
         if (pin_out.p) (void)hipHostFree(pin_out.p);
         for (int k = 0; k < 2; k++) {
@@ -306,7 +318,7 @@ struct fbh_ctx {
         }
         if (pin_ids.p) (void)hipHostFree(pin_ids.p);
         if (pin_src.p) (void)hipHostFree(pin_src.p);
-        pin_small.p = pin_leaves.p = pin_out.p = pin_ids.p = pin_src.p = nullptr;
+        pin_leaves.p = pin_out.p = pin_ids.p = pin_src.p = nullptr;
         if (copy_stream) (void)hipStreamSynchronize(copy_stream);
         for (void *h : host_allocs) (void)hipHostFree(h);
         host_allocs.clear();
@@ -364,6 +376,20 @@ struct fbh_ctx {
     }
 
     void sync() { check(hipStreamSynchronize(stream), "stream synchronize"); }
+
+    // The next staging slot, once the copy that last read it has run.
+    uint8_t *stage_acquire(int &slot) {
+        slot = stage_next;
+        stage_next = (stage_next + 1) % STAGE_SLOTS;
+        check(hipEventSynchronize(stage_ev[slot]), "staging reuse");
+        return static_cast<uint8_t *>(pin_stage[slot].p);
+    }
+    // Copies `bytes` of the slot to dst in stream order; marks the slot busy.
+    void stage_send(int slot, void *dst, size_t bytes) {
+        check(hipMemcpyAsync(dst, pin_stage[slot].p, bytes, hipMemcpyHostToDevice, stream),
+              "launch tables");
+        check(hipEventRecord(stage_ev[slot], stream), "event");
+    }
 
     // Rows per histogram workgroup for a launch accumulating acc_rows rows:
     // enough chunks for hist_waves full waves of workgroups over all tiles
@@ -546,6 +572,7 @@ void fixed_allocations(fbh_ctx &c, A &&a) {
     c.tmp = static_cast<uint32_t *>(a(4 * n, "partition arena"));
     c.flags = static_cast<uint8_t *>(a(n, "partition flags"));
     c.hist = static_cast<int64_t *>(a(16 * (uint64_t)c.n_slots * c.width_max, "histogram slots"));
+    c.d_scales = static_cast<ScalesDev *>(a(sizeof(ScalesDev), "quantizer scales"));
     c.red_f64 = static_cast<double *>(a(8 * (2 * (uint64_t)c.n_red_blocks + 2), "reduction scratch"));
     c.red_i64 = static_cast<int64_t *>(a(8 * (2 * (uint64_t)c.n_red_blocks + 2), "reduction scratch"));
     // The per-tree tables (tiles, tile features, split features) share one
@@ -859,7 +886,10 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
         fixed_allocations(*c, [&](uint64_t b, const char *what) -> void * {
             return c->alloc<uint8_t>(b, what);
         });
-        c->pinned(c->pin_small, c->stage_bytes);
+        for (int k = 0; k < fbh_ctx::STAGE_SLOTS; k++) {
+            c->pinned(c->pin_stage[k], c->stage_bytes);
+            check(hipEventCreateWithFlags(&c->stage_ev[k], hipEventDisableTiming), "event");
+        }
         c->pinned(c->pin_leaves, (sizeof(LeafDev) + 4) * MAX_NODES);
         // Results: packets, category sets, then a fused step's spans and slots.
         c->pin_out_spans = al256(sizeof(SplitPacketDev) * MAX_NODES) +
@@ -954,45 +984,72 @@ int fbh_upload_block(fbh_ctx *c, const uint32_t *feat_ids, uint32_t n_feats, uin
 
 namespace {
 
+// GradQuantizer::try_from_bounds (src/types.rs:288-303): the power-of-two
+// scale of one component from its bound, with the host's libm.
+double host_scale(double m, uint64_t n_rows) {
+    double s = 1.0;
+    if (m > 0.0 && std::isfinite(m)) {
+        const double budget = (double)(1ull << 62) / (double)std::max<uint64_t>(n_rows, 1);
+        const double raw = budget / m;
+        if (std::isfinite(raw) && raw > 0.0) {
+            double l = std::floor(std::log2(raw));
+            int e = std::isnan(l) ? 0 : (l > 1000.0 ? 1000 : (l < -1000.0 ? -1000 : (int)l));
+            s = std::exp2((double)e);
+        }
+    }
+    return s;
+}
+
+const char *const NONFINITE_GRADIENT =
+    "non-finite gradient or Hessian (or invalid bounds); reduce extreme labels, "
+    "weights, base_score or objective parameters";
+
+// The device's scales against the host's from the same bounds: they agree
+// unless log2 of the scale budget lies within an ulp of an integer and the
+// host's libm rounds it differently; then nothing grown with them is used.
+void check_device_scales(const ScalesDev &S, uint64_t n_rows) {
+    if (S.from_host) return;
+    if (S.status) throw InputError(NONFINITE_GRADIENT);
+    for (int k = 0; k < 2; k++)
+        if (host_scale(S.max_abs[k], n_rows) != S.scale[k])
+            throw RuntimeError("device quantizer scale differs from the host's libm for bound " +
+                               std::to_string(S.max_abs[k]));
+}
+
 // Bounds, power-of-two scales and fixed-point pairs of the f32 pairs in
 // gpair_f32 (GradQuantizer::try_from_bounds, src/types.rs:288-303, 367-385;
-// device passes src/backend/cuda/histogram.cu:1079-1177).
+// device passes src/backend/cuda/histogram.cu:1079-1177). The scales are
+// computed on the device; with scales_out NULL they stay there (no host
+// round trip) and are checked when the tree is collected. bounds_done: the
+// gradient kernel already masked the subsample and wrote the block bounds.
 void quantize_device_pairs(fbh_ctx *c, uint64_t th, uint64_t seed, uint64_t tree,
-                           double scales_out[2], int64_t root_out[2]) {
-    check(launch_gpair_maxabs(c->gpair_f32, c->n_rows, th, seed, tree, c->red_f64,
-                              c->n_red_blocks, c->red_f64 + 2 * c->n_red_blocks, c->stream),
-          "gradient bounds");
-    double mx[2];
-    check(hipMemcpyAsync(c->pin_out.p, c->red_f64 + 2 * c->n_red_blocks, 16,
-                         hipMemcpyDeviceToHost, c->stream),
-          "bounds download");
-    c->sync();
-    std::memcpy(mx, c->pin_out.p, 16);
-    if (!(std::isfinite(mx[0]) && std::isfinite(mx[1]) && mx[0] >= 0.0 && mx[1] >= 0.0))
-        throw InputError(
-            "non-finite gradient or Hessian (or invalid bounds); reduce extreme labels, "
-            "weights, base_score or objective parameters");
-    for (int k = 0; k < 2; k++) {
-        double s = 1.0;
-        const double m = mx[k];
-        if (m > 0.0 && std::isfinite(m)) {
-            const double budget = (double)(1ull << 62) / (double)std::max<uint64_t>(c->n_rows, 1);
-            const double raw = budget / m;
-            if (std::isfinite(raw) && raw > 0.0) {
-                double l = std::floor(std::log2(raw));
-                int e = std::isnan(l) ? 0 : (l > 1000.0 ? 1000 : (l < -1000.0 ? -1000 : (int)l));
-                s = std::exp2((double)e);
-            }
-        }
-        c->scales[k] = s;
+                           double scales_out[2], int64_t root_out[2], bool bounds_done) {
+    if (!bounds_done)
+        check(launch_gpair_maxabs(c->gpair_f32, c->n_rows, th, seed, tree, c->red_f64,
+                                  c->n_red_blocks, c->stream),
+              "gradient bounds");
+    check(launch_reduce_bounds(c->red_f64, c->n_red_blocks, c->red_f64 + 2 * c->n_red_blocks,
+                               c->n_rows, c->d_scales, c->stream),
+          "quantizer scales");
+    if (scales_out) {
+        ScalesDev S;
+        check(hipMemcpyAsync(c->pin_out.p, c->d_scales, sizeof(S), hipMemcpyDeviceToHost,
+                             c->stream),
+              "scales download");
+        c->sync();
+        std::memcpy(&S, c->pin_out.p, sizeof(S));
+        check_device_scales(S, c->n_rows);
+        c->scales[0] = S.scale[0];
+        c->scales[1] = S.scale[1];
     }
-    check(launch_gpair_quantize(c->gpair_f32, c->n_rows, c->scales[0], c->scales[1], c->gpair,
-                                c->red_i64, c->n_red_blocks, c->red_i64 + 2 * c->n_red_blocks,
-                                c->stream),
+    check(launch_gpair_quantize(c->gpair_f32, c->n_rows, c->d_scales, c->gpair, c->red_i64,
+                                c->n_red_blocks, c->red_i64 + 2 * c->n_red_blocks, c->stream),
           "gradient quantisation");
     c->root_on_device = true;
-    scales_out[0] = c->scales[0];
-    scales_out[1] = c->scales[1];
+    if (scales_out) {
+        scales_out[0] = c->scales[0];
+        scales_out[1] = c->scales[1];
+    }
     if (!root_out) return;  // the sum stays on the device for fbh_grow_depthwise
     check(hipMemcpyAsync(c->pin_out.p, c->red_i64 + 2 * c->n_red_blocks, 16,
                          hipMemcpyDeviceToHost, c->stream),
@@ -1010,7 +1067,7 @@ int fbh_upload_quantize_gpair(fbh_ctx *c, const float *g2n, uint64_t th, uint64_
         check(hipSetDevice(c->device), "hipSetDevice");
         check(hipMemcpyAsync(c->gpair_f32, g2n, c->n_rows * 8, hipMemcpyHostToDevice, c->stream),
               "gradient upload");
-        quantize_device_pairs(c, th, seed, tree, scales_out, root_out);
+        quantize_device_pairs(c, th, seed, tree, scales_out, root_out, false);
     });
 }
 
@@ -1054,7 +1111,10 @@ int fbh_set_objective(fbh_ctx *c, uint32_t objective, const float *labels,
 int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th, uint64_t seed,
                           uint64_t tree, double scales_out[2], int64_t root_out[2]) {
     return guard([&] {
-        if (!c || !scales_out) throw InputError("null argument");
+        if (!c) throw InputError("null argument");
+        if (!scales_out && (root_out || fn))
+            throw InputError("the scales stay on the device only with neither a root sum nor "
+                             "a sigmoid callback");
         if (c->objective < 0) throw InputError("fbh_set_objective has not been called");
         check(hipSetDevice(c->device), "hipSetDevice");
         if (c->leaves_pending) {
@@ -1065,7 +1125,8 @@ int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th
         if (c->objective == 0 || !fn) {
             // Squared error, or logistic with the device sigmoid.
             check(launch_gradient(c->margin, c->labels, w, c->n_rows, c->objective == 0 ? 0 : 2,
-                                  c->gpair_f32, c->stream),
+                                  c->gpair_f32, th, seed, tree, c->red_f64, c->n_red_blocks,
+                                  c->stream),
                   "device gradient");
         } else {
             const uint64_t n = c->n_rows;
@@ -1097,11 +1158,12 @@ int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th
             }
             check(hipEventRecord(c->up_done, c->up_stream), "event");
             check(hipStreamWaitEvent(c->stream, c->up_done, 0), "stream wait");
-            check(launch_gradient(c->sig, c->labels, w, n, 1, c->gpair_f32, c->stream),
+            check(launch_gradient(c->sig, c->labels, w, n, 1, c->gpair_f32, th, seed, tree,
+                                  c->red_f64, c->n_red_blocks, c->stream),
                   "device gradient");
         }
         c->ids_fresh = false;
-        quantize_device_pairs(c, th, seed, tree, scales_out, root_out);
+        quantize_device_pairs(c, th, seed, tree, scales_out, root_out, true);
     });
 }
 
@@ -1124,6 +1186,7 @@ int fbh_upload_gpair_fixed(fbh_ctx *c, const int64_t *g2n, const double scales[2
               "gradient upload");
         c->scales[0] = scales[0];
         c->scales[1] = scales[1];
+        check(launch_set_scales(c->d_scales, scales[0], scales[1], c->stream), "scales");
         c->root_on_device = false;
         c->sync();
     });
@@ -1271,10 +1334,9 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
         std::memcpy(tables.data() + c->off_order, order.data(), 4 * order.size());
         const bool upload = tables != c->tree_tables;
         if (upload) {
-            std::memcpy(c->pin_small.p, tables.data(), tables.size());
-            check(hipMemcpyAsync(c->d_tiles, c->pin_small.p, tables.size(), hipMemcpyHostToDevice,
-                                 c->stream),
-                  "tree tables");
+            int slot;
+            std::memcpy(c->stage_acquire(slot), tables.data(), tables.size());
+            c->stage_send(slot, c->d_tiles, tables.size());
             c->tree_tables = std::move(tables);
         }
         // The delta is kept only for callers without a device objective.
@@ -1282,7 +1344,6 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
         check(launch_init_rows(c->rows, c->objective >= 0 ? nullptr : c->delta, c->n_rows,
                                c->stream),
               "row arena reset");
-        if (upload) c->sync();  // the staging is reused by the next call
         c->tree_begun = true;
         root->offset = 0;
         root->len = (uint32_t)c->n_rows;
@@ -1299,11 +1360,14 @@ namespace {
 struct Stager {
     fbh_ctx *c;
     size_t o = 0;
+    int slot = -1;
+    uint8_t *host = nullptr;
     size_t put(const void *src, size_t bytes) {
+        if (!host) host = c->stage_acquire(slot);
         const size_t at = o;
         const size_t next = at + ((bytes + 255) & ~size_t(255));
         if (next > c->stage_bytes) throw RuntimeError("launch tables exceed the staging buffer");
-        if (bytes) std::memcpy(static_cast<uint8_t *>(c->pin_small.p) + at, src, bytes);
+        if (bytes) std::memcpy(host + at, src, bytes);
         o = next;
         return at;
     }
@@ -1312,9 +1376,7 @@ struct Stager {
         return reinterpret_cast<T *>(c->d_stage + off);
     }
     void send() {
-        if (o)
-            check(hipMemcpyAsync(c->d_stage, c->pin_small.p, o, hipMemcpyHostToDevice, c->stream),
-                  "tables");
+        if (o) c->stage_send(slot, c->d_stage, o);
     }
 };
 
@@ -1438,8 +1500,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
           "sibling subtraction");
     // ---- split scan ----
     SplitParamsDev P{};
-    P.inv_g = 1.0 / c->scales[0];
-    P.inv_h = 1.0 / c->scales[1];
+    P.scales = c->d_scales;
     P.lambda_ = sp->lambda_;
     P.gamma = sp->gamma;
     P.mcw = sp->min_child_weight;
@@ -2024,8 +2085,7 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     S.send();
 
     GrowParamsDev G{};
-    G.sp.inv_g = 1.0 / c->scales[0];
-    G.sp.inv_h = 1.0 / c->scales[1];
+    G.sp.scales = c->d_scales;
     G.sp.lambda_ = sp->lambda_;
     G.sp.gamma = sp->gamma;
     G.sp.mcw = sp->min_child_weight;
@@ -2154,7 +2214,8 @@ void grow_collect(fbh_ctx *c, fbh_tree_node *nodes, uint32_t node_capacity, uint
     const size_t o_vals = o_cats + al256(8 * GB.cat_cap);
     GrowState st;
     std::memcpy(&st, po, sizeof(st));
-    if (st.error) throw RuntimeError("histogram slots exhausted; raise the slot budget");
+    check_device_scales(st.scales, c->n_rows);
+    if (st.error & 1u) throw RuntimeError("histogram slots exhausted; raise the slot budget");
     account_hist(c, st.hist_rows, st.hist_nodes);
     if (st.covered != c->n_rows)
         throw RuntimeError("leaves cover " + std::to_string(st.covered) + " of " +

@@ -92,8 +92,21 @@ struct SplitNodeDev {
     uint32_t pad;
 };
 
+// Quantizer scales of the current gradients in device memory: computed on
+// the device from the gradient bounds, or set from the host for pairs it
+// uploads already quantised. Kernels read the inverses from here, so a round
+// needs no host round trip between its gradients and its tree.
+struct ScalesDev {
+    double scale[2];    // power-of-two scales of g and h
+    double inv[2];      // their inverses
+    double max_abs[2];  // the bounds they come from (0 when set from the host)
+    uint32_t status;    // 0: valid; 1: non-finite or negative bounds
+    uint32_t from_host; // 1: set from the host (no bounds)
+};
+
 struct SplitParamsDev {
-    double inv_g, inv_h;  // inverse quantizer scales
+    const ScalesDev *scales;  // quantizer scales (device memory)
+    double inv_g, inv_h;      // their inverses, loaded from `scales` by each kernel on entry
     float lambda_, gamma, mcw, alpha, mds;
     uint32_t max_cat_to_onehot, max_cat_threshold;
     uint32_t n_feats;     // features of the tree
@@ -155,11 +168,12 @@ struct GrowState {
     uint32_t tree_size;     // tree nodes so far
     uint32_t leaf_count;    // leaves as the host grower counts them (max_leaves)
     uint32_t tree_cat_words;
-    uint32_t error;         // nonzero: histogram slots ran out
+    uint32_t error;         // bit 0: histogram slots ran out; bit 1: invalid gradient bounds
     uint32_t hist_nodes;    // accumulated nodes with rows (all levels)
     uint32_t pad;
     uint64_t hist_rows;     // accumulated rows (all levels)
     uint64_t covered;       // rows of all leaves
+    ScalesDev scales;       // the scales the tree was grown with
 };
 
 // Column of one feature for the partition of a device-grown tree.
@@ -330,7 +344,8 @@ hipError_t launch_apply_leaves(const void *ids, int id_bytes, const float *value
 // mode 2: as 1 with s computed on the device from the margin.
 // All are multiplied by the row weight when w is non-null.
 hipError_t launch_gradient(const float *src, const float *y, const float *w, uint64_t n,
-                           int mode, float *g2n, hipStream_t s);
+                           int mode, float *g2n, uint64_t threshold, uint64_t seed, uint64_t tree,
+                           double *block_max, uint32_t n_blocks, hipStream_t s);
 hipError_t launch_sigmoid(const float *in, uint64_t n, float *out, hipStream_t s);
 hipError_t launch_sigmoid_checksum(uint64_t begin, uint64_t end, unsigned long long *out,
                                    hipStream_t s);
@@ -338,8 +353,11 @@ hipError_t launch_fill_f32(float *p, float v, uint64_t n, hipStream_t s);
 hipError_t launch_init_rows(uint32_t *rows, float *delta, uint64_t n, hipStream_t s);
 hipError_t launch_gpair_maxabs(float *g2n, uint64_t n, uint64_t threshold, uint64_t seed,
                                uint64_t tree, double *block_max, uint32_t n_blocks,
-                               double *out_max, hipStream_t s);
-hipError_t launch_gpair_quantize(const float *g2n, uint64_t n, double scale_g, double scale_h,
+                               hipStream_t s);
+hipError_t launch_reduce_bounds(const double *block_max, uint32_t n_blocks, double *out_max,
+                                uint64_t n_rows, ScalesDev *scales, hipStream_t s);
+hipError_t launch_set_scales(ScalesDev *scales, double scale_g, double scale_h, hipStream_t s);
+hipError_t launch_gpair_quantize(const float *g2n, uint64_t n, const ScalesDev *scales,
                                  int64_t *out, int64_t *block_sum, uint32_t n_blocks,
                                  int64_t *out_sum, hipStream_t s);
 hipError_t launch_pack_feature(const uint8_t *col, uint64_t n_rows, uint32_t width, uint8_t *tile,

@@ -644,6 +644,12 @@ __device__ __forceinline__ double threshold_l1(double g, float alpha) {
     return 0.0;
 }
 
+// The inverse quantizer scales of the current gradients, from device memory.
+__device__ __forceinline__ void load_scales(SplitParamsDev &P) {
+    P.inv_g = P.scales->inv[0];
+    P.inv_h = P.scales->inv[1];
+}
+
 // XGBoost CalcWeight, as split.rs:182-192.
 __device__ __forceinline__ float xgb_weight(double g, double h, const SplitParamsDev &P) {
     if (h <= 0.0) return 0.0f;
@@ -925,6 +931,7 @@ __global__ __launch_bounds__(256) void split_num_kernel(
     const uint32_t li = blockIdx.x * 4 + wave, ni = blockIdx.y;
     if (dev_n && ni >= *dev_n) return;
     if (li >= n_num) return;  // a whole wave
+    load_scales(P);
     const uint32_t j = order[li];
     const SplitFeatDev F = feats[j];
     const SplitNodeDev N = nodes[ni];
@@ -999,6 +1006,7 @@ __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
     __shared__ Best shb[SPLIT_TPB];
     __shared__ int64_t sg[SPLIT_TPB], shh[SPLIT_TPB];
     extern __shared__ unsigned char dyn[];
+    load_scales(P);
 
     const uint32_t ni = blockIdx.y, tid = threadIdx.x;
     if (dev_n && ni >= *dev_n) return;
@@ -1106,6 +1114,7 @@ __global__ __launch_bounds__(SPLIT_TPB) void split_node_kernel(
     __shared__ Best shb[SPLIT_TPB];
     const uint32_t ni = blockIdx.x, tid = threadIdx.x;
     if (dev_n && ni >= *dev_n) return;
+    load_scales(P);
     const FeatCandDev *c = cands + (size_t)ni * P.n_feats;
     Best best{0.0f, 0u, 0u, 0, 0};
     for (uint32_t j = tid; j < P.n_feats; j += SPLIT_TPB) {
@@ -1437,9 +1446,18 @@ hipError_t launch_apply_leaves(const void *ids, int id_bytes, const float *value
 // pairs equal the host's bit for bit. mode 0: squared error from the margin;
 // 1: logistic from the host's sigmoid in src; 2: logistic from the margin
 // with the device sigmoid (bit-identical to the host's libm).
+__device__ __forceinline__ bool row_selected(uint64_t row, uint64_t th, uint64_t seed,
+                                             uint64_t tree);
+__device__ __forceinline__ double finite_abs(float v);
+__device__ void block_max2(double mg, double mh, double *block_max);
+
+// block_max set: rows outside the round's subsample get a zero pair, and
+// each block's max |g|, max |h| goes to block_max (the bounds pass fused in).
 __global__ __launch_bounds__(256) void gradient_kernel(const float *src, const float *y,
                                                        const float *w, uint64_t n, int mode,
-                                                       float *g2n) {
+                                                       float *g2n, uint64_t th, uint64_t seed,
+                                                       uint64_t tree, double *block_max) {
+    double mg = 0.0, mh = 0.0;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * blockDim.x) {
         const float v = mode == 2 ? fb_sigmoid(src[i]) : src[i];
@@ -1449,15 +1467,24 @@ __global__ __launch_bounds__(256) void gradient_kernel(const float *src, const f
             g = g * w[i];
             h = h * w[i];
         }
+        if (block_max) {
+            if (!row_selected(i, th, seed, tree)) g = h = 0.0f;
+            mg = fmax(mg, finite_abs(g));
+            mh = fmax(mh, finite_abs(h));
+        }
         reinterpret_cast<float2 *>(g2n)[i] = make_float2(g, h);
     }
+    if (block_max) block_max2(mg, mh, block_max);
 }
 
 hipError_t launch_gradient(const float *src, const float *y, const float *w, uint64_t n, int mode,
-                           float *g2n, hipStream_t s) {
-    const uint32_t blocks = (uint32_t)std::min<uint64_t>((n + 255) / 256, 8192);
+                           float *g2n, uint64_t th, uint64_t seed, uint64_t tree,
+                           double *block_max, uint32_t n_blocks, hipStream_t s) {
+    const uint32_t blocks =
+        block_max ? n_blocks : (uint32_t)std::min<uint64_t>((n + 255) / 256, 8192);
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(gradient_kernel, dim3(blocks), dim3(256), 0, s, src, y, w, n, mode, g2n);
+    hipLaunchKernelGGL(gradient_kernel, dim3(blocks), dim3(256), 0, s, src, y, w, n, mode, g2n,
+                       th, seed, tree, block_max);
     return hipGetLastError();
 }
 
@@ -1546,22 +1573,9 @@ __device__ __forceinline__ double finite_abs(float v) {
     return isfinite(v) ? fabs((double)v) : (double)INFINITY;
 }
 
-// Masks sampled-out rows (in place) and reduces max |g|, max |h| per block.
-__global__ __launch_bounds__(256) void gpair_maxabs_kernel(float *g2n, uint64_t n, uint64_t th,
-                                                           uint64_t seed, uint64_t tree,
-                                                           double *block_max) {
+// Block maxima of the two bounds (256 threads) into block_max[2 * block].
+__device__ void block_max2(double mg, double mh, double *block_max) {
     __shared__ double sm[2][256];
-    double mg = 0.0, mh = 0.0;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (uint64_t)gridDim.x * blockDim.x) {
-        float2 v = reinterpret_cast<float2 *>(g2n)[i];
-        if (!row_selected(i, th, seed, tree)) {
-            v = make_float2(0.0f, 0.0f);
-            reinterpret_cast<float2 *>(g2n)[i] = v;
-        }
-        mg = fmax(mg, finite_abs(v.x));
-        mh = fmax(mh, finite_abs(v.y));
-    }
     sm[0][threadIdx.x] = mg;
     sm[1][threadIdx.x] = mh;
     __syncthreads();
@@ -1578,17 +1592,68 @@ __global__ __launch_bounds__(256) void gpair_maxabs_kernel(float *g2n, uint64_t 
     }
 }
 
-__global__ void reduce_max_kernel(const double *block_max, uint32_t n, double *out) {
-    __shared__ double sm[2][256];
+// floor(log2(x)) for a positive, finite, normal x as the floor of a correctly
+// rounded log2(x) gives it (the host's `log2(raw).floor()`): the exact floor,
+// except when log2(x) lies less than half a double spacing below an integer,
+// where the rounded logarithm is that integer.
+__device__ int floor_rounded_log2(double x) {
+    int e;
+    const double f = frexp(x, &e);  // x = f * 2^e, f in [0.5, 1)
+    if (f == 0.5) return e - 1;     // a power of two
+    if (e == 0) return -1;          // log2(x) in (-1, 0), never rounded to 0
+    // log2(x) = e - eps, eps = -log2(f) in (0, 1); f - 1 is exact.
+    const double eps = -log1p(f - 1.0) / 0.69314718055994530942;
+    const int ae = e > 0 ? e : -e;
+    const int a = 31 - __clz(ae);  // |e| in [2^a, 2^(a+1))
+    // Spacing of the doubles next to e on the side of e - eps.
+    const double spacing =
+        (e > 0 && (ae & (ae - 1)) == 0) ? ldexp(1.0, a - 53) : ldexp(1.0, a - 52);
+    return eps < 0.5 * spacing ? e : e - 1;
+}
+
+// GradQuantizer::try_from_bounds (src/types.rs:288-303): a power-of-two
+// scale per component with max_abs * n_rows * scale below 2^62.
+__device__ double scale_from_bound(double m, uint64_t n_rows) {
+    if (!(m > 0.0) || !isfinite(m)) return 1.0;
+    const double budget = 4611686018427387904.0 / (double)(n_rows ? n_rows : 1);
+    const double raw = budget / m;
+    if (!isfinite(raw) || !(raw > 0.0)) return 1.0;
+    int l = floor_rounded_log2(raw);
+    l = l > 1000 ? 1000 : (l < -1000 ? -1000 : l);
+    return ldexp(1.0, l);
+}
+
+// Masks sampled-out rows (in place) and reduces max |g|, max |h| per block.
+__global__ __launch_bounds__(256) void gpair_maxabs_kernel(float *g2n, uint64_t n, uint64_t th,
+                                                           uint64_t seed, uint64_t tree,
+                                                           double *block_max) {
     double mg = 0.0, mh = 0.0;
-    for (uint32_t i = threadIdx.x; i < n; i += 256) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        float2 v = reinterpret_cast<float2 *>(g2n)[i];
+        if (!row_selected(i, th, seed, tree)) {
+            v = make_float2(0.0f, 0.0f);
+            reinterpret_cast<float2 *>(g2n)[i] = v;
+        }
+        mg = fmax(mg, finite_abs(v.x));
+        mh = fmax(mh, finite_abs(v.y));
+    }
+    block_max2(mg, mh, block_max);
+}
+
+// The bounds of the whole array, and from them the quantizer scales.
+__global__ void reduce_max_kernel(const double *block_max, uint32_t n, double *out,
+                                  uint64_t n_rows, ScalesDev *scales) {
+    __shared__ double sm[2][1024];
+    double mg = 0.0, mh = 0.0;
+    for (uint32_t i = threadIdx.x; i < n; i += 1024) {
         mg = fmax(mg, block_max[2 * i]);
         mh = fmax(mh, block_max[2 * i + 1]);
     }
     sm[0][threadIdx.x] = mg;
     sm[1][threadIdx.x] = mh;
     __syncthreads();
-    for (uint32_t s = 128; s > 0; s >>= 1) {
+    for (uint32_t s = 512; s > 0; s >>= 1) {
         if (threadIdx.x < s) {
             sm[0][threadIdx.x] = fmax(sm[0][threadIdx.x], sm[0][threadIdx.x + s]);
             sm[1][threadIdx.x] = fmax(sm[1][threadIdx.x], sm[1][threadIdx.x + s]);
@@ -1598,15 +1663,49 @@ __global__ void reduce_max_kernel(const double *block_max, uint32_t n, double *o
     if (threadIdx.x == 0) {
         out[0] = sm[0][0];
         out[1] = sm[1][0];
+        ScalesDev S{};
+        S.max_abs[0] = sm[0][0];
+        S.max_abs[1] = sm[1][0];
+        S.status = (isfinite(S.max_abs[0]) && isfinite(S.max_abs[1]) && S.max_abs[0] >= 0.0 &&
+                    S.max_abs[1] >= 0.0)
+                       ? 0u
+                       : 1u;
+        for (int k = 0; k < 2; k++) {
+            S.scale[k] = scale_from_bound(S.max_abs[k], n_rows);
+            S.inv[k] = 1.0 / S.scale[k];
+        }
+        *scales = S;
     }
 }
 
+// Scales the host chose (pairs it quantised itself).
+__global__ void set_scales_kernel(ScalesDev *scales, double sg, double sh) {
+    if (threadIdx.x != 0) return;
+    ScalesDev S{};
+    S.scale[0] = sg;
+    S.scale[1] = sh;
+    S.inv[0] = 1.0 / sg;
+    S.inv[1] = 1.0 / sh;
+    S.from_host = 1;
+    *scales = S;
+}
+
+hipError_t launch_set_scales(ScalesDev *scales, double sg, double sh, hipStream_t s) {
+    hipLaunchKernelGGL(set_scales_kernel, dim3(1), dim3(64), 0, s, scales, sg, sh);
+    return hipGetLastError();
+}
+
+hipError_t launch_reduce_bounds(const double *block_max, uint32_t n_blocks, double *out_max,
+                                uint64_t n_rows, ScalesDev *scales, hipStream_t s) {
+    hipLaunchKernelGGL(reduce_max_kernel, dim3(1), dim3(1024), 0, s, block_max, n_blocks, out_max,
+                       n_rows, scales);
+    return hipGetLastError();
+}
+
 hipError_t launch_gpair_maxabs(float *g2n, uint64_t n, uint64_t th, uint64_t seed, uint64_t tree,
-                               double *block_max, uint32_t n_blocks, double *out_max,
-                               hipStream_t s) {
+                               double *block_max, uint32_t n_blocks, hipStream_t s) {
     hipLaunchKernelGGL(gpair_maxabs_kernel, dim3(n_blocks), dim3(256), 0, s, g2n, n, th, seed,
                        tree, block_max);
-    hipLaunchKernelGGL(reduce_max_kernel, dim3(1), dim3(256), 0, s, block_max, n_blocks, out_max);
     return hipGetLastError();
 }
 
@@ -1620,9 +1719,10 @@ __device__ __forceinline__ int64_t sat_i64(double x) {
 
 // GradQuantizer::to_fixed: round half away from zero of v * 2^k.
 __global__ __launch_bounds__(256) void gpair_quantize_kernel(const float *g2n, uint64_t n,
-                                                             double sg, double sh, int64_t *out,
+                                                             const ScalesDev *scales, int64_t *out,
                                                              int64_t *block_sum) {
     __shared__ int64_t sm[2][256];
+    const double sg = scales->scale[0], sh = scales->scale[1];
     uint64_t ag = 0, ah = 0;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * blockDim.x) {
@@ -1650,16 +1750,16 @@ __global__ __launch_bounds__(256) void gpair_quantize_kernel(const float *g2n, u
 }
 
 __global__ void reduce_sum_kernel(const int64_t *block_sum, uint32_t n, int64_t *out) {
-    __shared__ int64_t sm[2][256];
+    __shared__ int64_t sm[2][1024];
     uint64_t ag = 0, ah = 0;
-    for (uint32_t i = threadIdx.x; i < n; i += 256) {
+    for (uint32_t i = threadIdx.x; i < n; i += 1024) {
         ag += (uint64_t)block_sum[2 * i];
         ah += (uint64_t)block_sum[2 * i + 1];
     }
     sm[0][threadIdx.x] = (int64_t)ag;
     sm[1][threadIdx.x] = (int64_t)ah;
     __syncthreads();
-    for (uint32_t s = 128; s > 0; s >>= 1) {
+    for (uint32_t s = 512; s > 0; s >>= 1) {
         if (threadIdx.x < s) {
             sm[0][threadIdx.x] = wadd(sm[0][threadIdx.x], sm[0][threadIdx.x + s]);
             sm[1][threadIdx.x] = wadd(sm[1][threadIdx.x], sm[1][threadIdx.x + s]);
@@ -1672,12 +1772,12 @@ __global__ void reduce_sum_kernel(const int64_t *block_sum, uint32_t n, int64_t 
     }
 }
 
-hipError_t launch_gpair_quantize(const float *g2n, uint64_t n, double sg, double sh, int64_t *out,
-                                 int64_t *block_sum, uint32_t n_blocks, int64_t *out_sum,
-                                 hipStream_t s) {
-    hipLaunchKernelGGL(gpair_quantize_kernel, dim3(n_blocks), dim3(256), 0, s, g2n, n, sg, sh, out,
+hipError_t launch_gpair_quantize(const float *g2n, uint64_t n, const ScalesDev *scales,
+                                 int64_t *out, int64_t *block_sum, uint32_t n_blocks,
+                                 int64_t *out_sum, hipStream_t s) {
+    hipLaunchKernelGGL(gpair_quantize_kernel, dim3(n_blocks), dim3(256), 0, s, g2n, n, scales, out,
                        block_sum);
-    hipLaunchKernelGGL(reduce_sum_kernel, dim3(1), dim3(256), 0, s, block_sum, n_blocks, out_sum);
+    hipLaunchKernelGGL(reduce_sum_kernel, dim3(1), dim3(1024), 0, s, block_sum, n_blocks, out_sum);
     return hipGetLastError();
 }
 
@@ -1899,11 +1999,14 @@ __global__ void grow_init_kernel(GrowParamsDev G, const int64_t *root, uint32_t 
                                  LNodeDev *level, SplitNodeDev *root_split, TreeNodeDev *tree,
                                  GrowState *st) {
     if (threadIdx.x != 0) return;
+    load_scales(G.sp);
     const int64_t rg = root[0], rh = root[1];
     GrowState s{};
     s.n_level = 1;
     s.tree_size = 1;
     s.leaf_count = 1;
+    s.scales = *G.sp.scales;
+    s.error = s.scales.status ? 2u : 0u;
     *st = s;
     LNodeDev r{};
     r.tree_id = 0;
@@ -1956,6 +2059,7 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
     __shared__ uint32_t buf[1024];
     __shared__ uint32_t held[MAX_GROW_SLOTS / 32];
     __shared__ uint16_t freelist[MAX_GROW_SLOTS];
+    load_scales(G.sp);
     const uint32_t tid = threadIdx.x;
     const GrowState S0 = *st;
     __syncthreads();  // every thread has read the state before thread 0 rewrites it

@@ -837,48 +837,49 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
             bytes_seen = bytes;
         }
     };
-    // Device-grown trees are collected one round late: the next round's
-    // gradients are enqueued first, so the host rebuilds tree r while the
-    // device works on round r + 1 (a host sigmoid needs tree r's leaf values
-    // first, so it collects before its gradients).
+    // Device-grown trees are collected one round late: round r + 1's
+    // gradients and tree are enqueued before tree r is collected, with the
+    // quantizer scales left on the device, so the host rebuilds tree r while
+    // the device works on round r + 1 and no round waits for the host. A
+    // host sigmoid needs tree r's leaf values first, so it collects before
+    // its gradients (and takes the scales back to the host).
     const bool overlap = grower.device_growth();
     const bool host_sig = obj == 1 && !dev_sigmoid;
-    bool pending = false;
+    const bool device_scales = overlap && !host_sig;
+    uint32_t pending = 0;
+    auto collect_all = [&]() {
+        for (; pending; pending--) m.trees.push_back(grower.collect());
+    };
     for (uint32_t round = 0; round < p.n_rounds; round++) {
-        if (pending && round == p.sync_round) {  // the device is idle when this round starts
-            m.trees.push_back(grower.collect());
-            pending = false;
-        }
+        if (pending && round == p.sync_round) collect_all();  // the device is idle when this round starts
         if (round > 0) close_round(round - 1);
-        if (pending && host_sig) {
-            m.trees.push_back(grower.collect());
-            pending = false;
-        }
+        if (pending && host_sig) collect_all();
         const auto tg = Clock::now();
         double scales[2];
         int64_t root_sum[2];
         call(fbh_gradient_exchange(ctx.get(), host_sig ? sigmoid_chunk : nullptr, &job,
-                                   sample_threshold(p.subsample), p.seed, round, scales,
+                                   sample_threshold(p.subsample), p.seed, round,
+                                   device_scales ? nullptr : scales,
                                    overlap ? nullptr : root_sum));
         grad_s += std::chrono::duration<double>(Clock::now() - tg).count();
-        if (pending) {
-            m.trees.push_back(grower.collect());
-            pending = false;
-        }
+        if (pending && !device_scales) collect_all();
         std::vector<uint32_t> feats;
         if (p.colsample_bytree < 1.0f) feats = sample_columns(nf, p.colsample_bytree, p.seed, round);
         fbh_span root;
         call(fbh_begin_tree(ctx.get(), feats.empty() ? nullptr : feats.data(),
                             (uint32_t)feats.size(), mono.data(), nf, &root));
         if (overlap) {
-            grower.lm_scales(scales);
+            if (!device_scales) grower.lm_scales(scales);
             grower.grow_async(nullptr);
-            pending = true;
+            if (++pending == 2) {
+                m.trees.push_back(grower.collect());
+                pending--;
+            }
         } else {
             m.trees.push_back(grower.grow(scales, root_sum));
         }
     }
-    if (pending) m.trees.push_back(grower.collect());
+    collect_all();
     call(fbh_download_margin(ctx.get(), pred.data()));
     if (p.n_rounds > 0) close_round(p.n_rounds - 1);
     g_stats.train_seconds = std::chrono::duration<double>(Clock::now() - t_train).count();

@@ -220,9 +220,16 @@ typedef void (*fbh_sigmoid_fn)(void *user, uint64_t row_begin, uint64_t n, const
  * while later chunks are in flight and uploads the sigmoids. Either way the
  * device derives g = s - y, h = max(s(1 - s), 1e-16) (times the weight) with
  * the host's f32 operations, then masks, scales and quantizes as
- * fbh_upload_quantize_gpair. With root_out NULL the root sum stays on the
- * device (for fbh_grow_depthwise) and the call returns once the scales are
- * known, without waiting for the quantisation. */
+ * fbh_upload_quantize_gpair. The scales are computed on the device from the
+ * bounds (the floor of a correctly rounded log2, as the host's libm gives
+ * it). With root_out NULL the root sum stays on the device (for
+ * fbh_grow_depthwise) and the call returns once the scales are known,
+ * without waiting for the quantisation. With scales_out NULL as well (the
+ * callback must then be NULL) nothing comes back and the call does not wait
+ * at all: the scales stay on the device for the kernels that follow, and
+ * fbh_grow_collect reports invalid bounds (non-finite gradients) of the
+ * round the tree was grown in, and checks the device's scales against the
+ * host libm's. */
 int fbh_gradient_exchange(fbh_ctx *ctx, fbh_sigmoid_fn fn, void *user, uint64_t sample_threshold,
                           uint64_t seed, uint64_t tree, double scales_out[2],
                           int64_t root_sum_out[2]);

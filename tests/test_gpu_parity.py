@@ -277,6 +277,26 @@ def test_device_grown_trees_match_host_levels_and_oracle(fb, oracle, case):
     assert np.array_equal(host.train_margins(n).view(np.uint32), want)
 
 
+@pytest.mark.parametrize("host_levels", [False, True])
+def test_nonfinite_gradients_stop_training(fb, host_levels):
+    """Gradients that overflow f32 (labels near the f32 maximum times a
+    weight of 10) stop training with the reference's error, whether the
+    quantizer scales come back to the host every round (host-grown levels)
+    or stay on the device (device-grown trees, checked when the tree is
+    collected)."""
+    from ferrisboost_amd import _native as N
+
+    rng = np.random.default_rng(5)
+    n = 4096
+    x = rng.normal(size=(n, 3)).astype(np.float32)
+    y = np.where(np.arange(n) % 2 == 0, 3e38, -3e38).astype(np.float32)
+    w = np.full(n, 10.0, np.float32)
+    params = {"objective": "reg:squarederror", "max_depth": 3, "max_bin": 16,
+              "hip_host_levels": host_levels}
+    with pytest.raises(N.InputError, match="non-finite gradient"):
+        fb.train(params, x, y, weight=w, num_boost_round=2)
+
+
 @pytest.mark.parametrize("max_bin", [255, 256])
 def test_plumbing_config_matches_oracle(fb, oracle, max_bin):
     X, y, params, _ = _synthetic("plumbing", 30_000)
