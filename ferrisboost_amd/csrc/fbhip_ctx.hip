@@ -1401,16 +1401,19 @@ struct EvalPlan {
     const uint32_t *dev_n_hn = nullptr, *dev_n_tri = nullptr, *dev_n_nodes = nullptr;
     bool download = true;  // copy the packets back (a device-grown tree reads them in place)
     const uint32_t *rows = nullptr;  // arena of the accumulated nodes (null: the row arena)
+    bool cleared = false;            // the accumulated slots were cleared by the partition
 };
 
 void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
-    if (E.dev_chunk_rows)
-        check(launch_zero_nodes(c->hist, c->hist_width, E.hn, E.n_hn, E.dev_n_hn,
-                                c->has_global || !c->streamed.empty(), c->stream),
-              "histogram clear");
-    else
-        check(launch_zero_slots(c->hist, c->hist_width, E.zero_slots, E.n_zero, c->stream),
-              "histogram clear");
+    if (!E.cleared) {
+        if (E.dev_chunk_rows)
+            check(launch_zero_nodes(c->hist, c->hist_width, E.hn, E.n_hn, E.dev_n_hn,
+                                    c->has_global || !c->streamed.empty(), c->stream),
+                  "histogram clear");
+        else
+            check(launch_zero_slots(c->hist, c->hist_width, E.zero_slots, E.n_zero, c->stream),
+                  "histogram clear");
+    }
     if (E.n_hn && E.grid_chunks) {
         const size_t ev = c->ev_used;
         // Timing: the first resident launch takes the start event and the
@@ -2124,16 +2127,19 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
         // Level d's rows are in arena d % 2; its children go to the other.
         uint32_t *arena_in = (d & 1) ? c->tmp : c->rows;
         uint32_t *arena_out = (d & 1) ? c->rows : c->tmp;
-        check(launch_partition_dev(GB.reqs, &GB.st->n_split, n_rows / PART_CHUNK + nb + 1, arena_in,
-                                   arena_out, c->flags, c->d_counts, c->d_excl, c->d_totals,
-                                   pk_cats, c->stream),
-              "partition");
         const GrowDevOut out{GB.st, GB.level[(d + 1) & 1], GB.tree, GB.leaves, GB.leaf_vals,
                              (d + 1) & 1u};
-        check(launch_level_plan(GB.pairs, nb, c->d_totals, rule, c->d_lvl_hist, c->d_lvl_split,
-                                c->d_lvl_out, c->d_lvl_out + 4 * MAX_NODES, c->d_lvl_rows, out,
-                                c->stream),
-              "level plan");
+        // The scatter clears the next level's accumulated slots (none after the last level).
+        ZeroNodesDev Z{};
+        if (d + 1 < D)
+            Z = {c->hist, c->hist_width, c->d_lvl_hist, &GB.st->n_eval,
+                 (c->has_global || !c->streamed.empty()) ? 1u : 0u, 0u};
+        check(launch_partition_level(GB.reqs, &GB.st->n_split, n_rows / PART_CHUNK + nb + 1,
+                                     arena_in, arena_out, c->flags, c->d_counts, c->d_excl,
+                                     c->d_totals, pk_cats, GB.pairs, rule, c->d_lvl_hist,
+                                     c->d_lvl_split, c->d_lvl_out, c->d_lvl_out + 4 * MAX_NODES,
+                                     c->d_lvl_rows, out, Z, c->stream),
+              "partition and level plan");
         if (d + 1 == D) break;
         EvalPlan E;
         E.hn = c->d_lvl_hist;
@@ -2149,6 +2155,7 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
         E.dev_n_nodes = &GB.st->n_level;
         E.download = false;
         E.rows = arena_out;
+        E.cleared = true;
         enqueue_eval(c, E, sp);
     }
     uint64_t leaf_bound = (uint64_t)1 << D;

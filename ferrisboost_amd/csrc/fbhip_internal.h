@@ -176,6 +176,17 @@ struct GrowState {
     ScalesDev scales;       // the scales the tree was grown with
 };
 
+// Histogram slots a partition's scatter clears for the next level's
+// accumulated nodes (hist NULL: none).
+struct ZeroNodesDev {
+    int64_t *hist;
+    uint64_t width;
+    const HistNodeDev *nodes;
+    const uint32_t *dev_n;  // node count, read on the device
+    uint32_t force;         // clear single-chunk nodes too
+    uint32_t pad;
+};
+
 // Column of one feature for the partition of a device-grown tree.
 struct DevColumn {
     const uint8_t *data;
@@ -312,6 +323,15 @@ hipError_t launch_split_nodes(const FeatCandDev *cands, const SplitFeatDev *feat
                               hipStream_t s);
 // Pass 1 (direction flags, left count per chunk) over a group of requests
 // whose chunk_begin numbers the group's own chunks; counts land at count_base.
+// A device-grown level's partition with its plan: count, scan + children
+// plan (one workgroup), scatter (clearing Z's slots).
+hipError_t launch_partition_level(const PartReqDev *reqs, const uint32_t *dev, uint32_t grid_chunks,
+                                  const uint32_t *rows_in, uint32_t *rows_out, uint8_t *flags,
+                                  uint32_t *counts, uint32_t *excl, uint32_t *totals,
+                                  const uint64_t *cat_words, const PairDev *pairs, ChunkRule rule,
+                                  HistNodeDev *hn, SplitNodeDev *sn, uint32_t *spans,
+                                  uint32_t *left_slot, uint32_t *chunk_rows, const GrowDevOut &D,
+                                  const ZeroNodesDev &Z, hipStream_t s);
 hipError_t launch_partition_count(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
                                   const uint32_t *rows, uint8_t *flags, uint32_t *chunk_counts,
                                   const uint64_t *cat_words, hipStream_t s);

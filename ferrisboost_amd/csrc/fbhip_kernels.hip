@@ -439,11 +439,10 @@ __device__ __forceinline__ uint32_t block_scan_1024(uint32_t v, uint32_t *buf, u
 
 // One workgroup plans the children of a fused partition + evaluation step
 // from the partition's left counts (see launch_level_plan).
-__global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, uint32_t n,
-                                                          const uint32_t *totals, ChunkRule rule,
-                                                          HistNodeDev *hn, SplitNodeDev *sn,
-                                                          uint32_t *spans, uint32_t *left_slot,
-                                                          uint32_t *chunk_rows_out, GrowDevOut D) {
+__device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t *totals,
+                                ChunkRule rule, HistNodeDev *hn, SplitNodeDev *sn,
+                                uint32_t *spans, uint32_t *left_slot, uint32_t *chunk_rows_out,
+                                const GrowDevOut &D) {
     __shared__ uint32_t buf[1024];
     __shared__ unsigned long long acc_sh, acc_nodes_sh;
     __shared__ uint32_t cr_sh;
@@ -456,8 +455,11 @@ __global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, 
     }
     if (threadIdx.x == 0) acc_sh = acc_nodes_sh = 0;
     __syncthreads();
-    // Spans of every pair and the rows the evaluated pairs accumulate.
+    // Spans of every pair and the rows the evaluated pairs accumulate. The
+    // thread's first pair (all of them when n <= 1024) stays in registers:
+    // left count, and the accumulated (smaller) child's rows when evaluated.
     unsigned long long acc = 0;
+    uint32_t my_nl = 0, my_small = 0;
     for (uint32_t i = threadIdx.x; i < n; i += 1024) {
         const PairDev P = pairs[i];
         const uint32_t nl = P.req == NO_SLOT ? 0u : totals[P.req];
@@ -466,8 +468,21 @@ __global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, 
         spans[4 * i + 1] = nl;
         spans[4 * i + 2] = P.row_off + nl;
         spans[4 * i + 3] = nr;
-        if (P.eval_index != NO_SLOT) acc += min(nl, nr);
+        const bool ev = P.eval_index != NO_SLOT;
+        if (ev) acc += min(nl, nr);
+        if (i == threadIdx.x) {
+            my_nl = nl;
+            my_small = ev ? min(nl, nr) : 0u;
+        }
     }
+    // Accumulated rows of pair i (0 when it is not evaluated).
+    auto small_of = [&](uint32_t i) -> uint32_t {
+        if (i == threadIdx.x) return my_small;
+        const PairDev P = pairs[i];
+        if (P.eval_index == NO_SLOT) return 0u;
+        const uint32_t nl = P.req == NO_SLOT ? 0u : totals[P.req];
+        return min(nl, P.row_len - nl);
+    };
     atomicAdd(&acc_sh, acc);
     __syncthreads();
     unsigned long long acc_nodes = 0;
@@ -479,12 +494,7 @@ __global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, 
     } else {
         const uint64_t acc_all = acc_sh;
         uint32_t nz = 0;
-        for (uint32_t i = threadIdx.x; i < n; i += 1024) {
-            const PairDev P = pairs[i];
-            if (P.eval_index == NO_SLOT) continue;
-            const uint32_t nl = P.req == NO_SLOT ? 0u : totals[P.req];
-            nz += min(nl, P.row_len - nl) ? 1u : 0u;
-        }
+        for (uint32_t i = threadIdx.x; i < n; i += 1024) nz += small_of(i) ? 1u : 0u;
         uint32_t n_nz;
         (void)block_scan_1024(nz, buf, n_nz);
         const uint64_t W = rule.want_chunks;
@@ -497,12 +507,8 @@ __global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, 
             while (lo < hi) {  // uniform: every thread holds the same bounds
                 const uint64_t mid = (lo + hi) / 2, rows = mid * 1024;
                 uint32_t k = 0;
-                for (uint32_t i = threadIdx.x; i < n; i += 1024) {
-                    const PairDev P = pairs[i];
-                    if (P.eval_index == NO_SLOT) continue;
-                    const uint32_t nl = P.req == NO_SLOT ? 0u : totals[P.req];
-                    k += (uint32_t)((min(nl, P.row_len - nl) + rows - 1) / rows);
-                }
+                for (uint32_t i = threadIdx.x; i < n; i += 1024)
+                    k += (uint32_t)((small_of(i) + rows - 1) / rows);
                 uint32_t total_k;
                 (void)block_scan_1024(k, buf, total_k);
                 if (total_k <= W) hi = mid;
@@ -521,10 +527,11 @@ __global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, 
         const uint32_t i = base + threadIdx.x;
         PairDev P{};
         uint32_t nl = 0, nr = 0, nc = 0;
-        const bool ev = i < n && pairs[i].eval_index != NO_SLOT;
+        bool ev = false;
         if (i < n) {
             P = pairs[i];
-            nl = P.req == NO_SLOT ? 0u : totals[P.req];
+            ev = P.eval_index != NO_SLOT;
+            nl = base == 0 ? my_nl : (P.req == NO_SLOT ? 0u : totals[P.req]);
             nr = P.row_len - nl;
             if (ev) nc = (min(nl, nr) + cr - 1) / cr;
         }
@@ -619,6 +626,14 @@ __global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, 
             st->hist_nodes += (uint32_t)acc_nodes_sh;
         }
     }
+}
+
+__global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, uint32_t n,
+                                                          const uint32_t *totals, ChunkRule rule,
+                                                          HistNodeDev *hn, SplitNodeDev *sn,
+                                                          uint32_t *spans, uint32_t *left_slot,
+                                                          uint32_t *chunk_rows_out, GrowDevOut D) {
+    level_plan_body(pairs, n, totals, rule, hn, sn, spans, left_slot, chunk_rows_out, D);
 }
 
 hipError_t launch_level_plan(const PairDev *pairs, uint32_t n_pairs, const uint32_t *totals,
@@ -1233,10 +1248,9 @@ __global__ __launch_bounds__(PART_TPB) void part_count_kernel(const PartReqDev *
 
 // Pass 2: exclusive scan of the chunk counts (one workgroup) and the left
 // total of every request.
-__global__ __launch_bounds__(1024) void part_scan_kernel(const uint32_t *counts, uint32_t n_chunks,
-                                                         uint32_t *excl, const PartReqDev *reqs,
-                                                         uint32_t n_reqs, uint32_t *totals,
-                                                         const uint32_t *dev) {
+__device__ void part_scan_body(const uint32_t *counts, uint32_t n_chunks, uint32_t *excl,
+                               const PartReqDev *reqs, uint32_t n_reqs, uint32_t *totals,
+                               const uint32_t *dev) {
     __shared__ uint32_t buf[32];
     if (dev) {
         n_reqs = dev[0];
@@ -1259,8 +1273,30 @@ __global__ __launch_bounds__(1024) void part_scan_kernel(const uint32_t *counts,
         totals[r] = excl[reqs[r].chunk_begin + reqs[r].n_chunks] - excl[reqs[r].chunk_begin];
 }
 
+__global__ __launch_bounds__(1024) void part_scan_kernel(const uint32_t *counts, uint32_t n_chunks,
+                                                         uint32_t *excl, const PartReqDev *reqs,
+                                                         uint32_t n_reqs, uint32_t *totals,
+                                                         const uint32_t *dev) {
+    part_scan_body(counts, n_chunks, excl, reqs, n_reqs, totals, dev);
+}
+
+// Pass 2 of a device-grown level, fused with its plan: the scan, then (one
+// workgroup, so the totals are visible after a barrier) the children plan of
+// level_plan_kernel.
+__global__ __launch_bounds__(1024) void part_scan_plan_kernel(
+    const uint32_t *counts, uint32_t *excl, const PartReqDev *reqs, uint32_t *totals,
+    const uint32_t *dev, const PairDev *pairs, ChunkRule rule, HistNodeDev *hn, SplitNodeDev *sn,
+    uint32_t *spans, uint32_t *left_slot, uint32_t *chunk_rows_out, GrowDevOut D) {
+    part_scan_body(counts, 0u, excl, reqs, 0u, totals, dev);
+    __syncthreads();
+    level_plan_body(pairs, 0u, totals, rule, hn, sn, spans, left_slot, chunk_rows_out, D);
+}
+
 // Pass 3: stable scatter into the temporary arena. Rows of a chunk are taken
 // in order, 256 at a time; a wave's lanes rank their rows with a ballot.
+// Z.hist set: the workgroups also clear the histogram slots of the next
+// level's accumulated nodes (those with several chunks, or all with force),
+// as zero_nodes_kernel would, spread over the whole grid.
 __global__ __launch_bounds__(PART_TPB) void part_scatter_kernel(const PartReqDev *reqs,
                                                                 uint32_t n_reqs,
                                                                 const uint32_t *rows,
@@ -1268,8 +1304,19 @@ __global__ __launch_bounds__(PART_TPB) void part_scatter_kernel(const PartReqDev
                                                                 const uint32_t *excl,
                                                                 const uint32_t *totals,
                                                                 uint32_t *tmp,
-                                                                const uint32_t *dev) {
+                                                                const uint32_t *dev,
+                                                                ZeroNodesDev Z) {
     __shared__ uint32_t wave_left[PART_TPB / 64];
+    if (Z.hist) {
+        const uint64_t W = Z.width * 2u;
+        const uint64_t all = (uint64_t)*Z.dev_n * W;
+        for (uint64_t k = (uint64_t)blockIdx.x * PART_TPB + threadIdx.x; k < all;
+             k += (uint64_t)gridDim.x * PART_TPB) {
+            const uint64_t e = k / W;
+            const HistNodeDev N = Z.nodes[e];
+            if (Z.force || N.n_chunks != 1) Z.hist[(uint64_t)N.slot * W + (k - e * W)] = 0;
+        }
+    }
     const uint32_t chunk = blockIdx.x;
     if (dev && chunk >= dev[1]) return;
     const uint32_t ri = find_req(reqs, dev ? dev[0] : n_reqs, chunk);
@@ -1338,7 +1385,24 @@ hipError_t launch_partition_dev(const PartReqDev *reqs, const uint32_t *dev, uin
     hipLaunchKernelGGL(part_scan_kernel, dim3(1), dim3(1024), 0, s, counts, 0u, excl, reqs, 0u,
                        totals, dev);
     hipLaunchKernelGGL(part_scatter_kernel, dim3(grid_chunks), dim3(PART_TPB), 0, s, reqs, 0u,
-                       rows_in, flags, excl, totals, rows_out, dev);
+                       rows_in, flags, excl, totals, rows_out, dev, ZeroNodesDev{});
+    return hipGetLastError();
+}
+
+hipError_t launch_partition_level(const PartReqDev *reqs, const uint32_t *dev, uint32_t grid_chunks,
+                                  const uint32_t *rows_in, uint32_t *rows_out, uint8_t *flags,
+                                  uint32_t *counts, uint32_t *excl, uint32_t *totals,
+                                  const uint64_t *cat_words, const PairDev *pairs, ChunkRule rule,
+                                  HistNodeDev *hn, SplitNodeDev *sn, uint32_t *spans,
+                                  uint32_t *left_slot, uint32_t *chunk_rows, const GrowDevOut &D,
+                                  const ZeroNodesDev &Z, hipStream_t s) {
+    if (grid_chunks == 0) return hipSuccess;
+    hipLaunchKernelGGL(part_count_kernel, dim3(grid_chunks), dim3(PART_TPB), 0, s, reqs, 0u,
+                       rows_in, flags, counts, cat_words, dev);
+    hipLaunchKernelGGL(part_scan_plan_kernel, dim3(1), dim3(1024), 0, s, counts, excl, reqs, totals,
+                       dev, pairs, rule, hn, sn, spans, left_slot, chunk_rows, D);
+    hipLaunchKernelGGL(part_scatter_kernel, dim3(grid_chunks), dim3(PART_TPB), 0, s, reqs, 0u,
+                       rows_in, flags, excl, totals, rows_out, dev, Z);
     return hipGetLastError();
 }
 
@@ -1350,7 +1414,7 @@ hipError_t launch_partition_finish(const PartReqDev *reqs, uint32_t n_reqs, uint
     hipLaunchKernelGGL(part_scan_kernel, dim3(1), dim3(1024), 0, s, counts, n_chunks, excl, reqs,
                        n_reqs, totals, nullptr);
     hipLaunchKernelGGL(part_scatter_kernel, dim3(n_chunks), dim3(PART_TPB), 0, s, reqs, n_reqs,
-                       rows, flags, excl, totals, tmp, nullptr);
+                       rows, flags, excl, totals, tmp, nullptr, ZeroNodesDev{});
     hipLaunchKernelGGL(part_copy_kernel, dim3(n_chunks), dim3(PART_TPB), 0, s, reqs, n_reqs, tmp,
                        rows, nullptr);
     return hipGetLastError();

@@ -880,8 +880,11 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
         }
     }
     collect_all();
+    // The last round ends when its tree is collected (the device is then
+    // idle); the one download of the training margins comes after it.
+    if (overlap && p.n_rounds > 0) close_round(p.n_rounds - 1);
     call(fbh_download_margin(ctx.get(), pred.data()));
-    if (p.n_rounds > 0) close_round(p.n_rounds - 1);
+    if (!overlap && p.n_rounds > 0) close_round(p.n_rounds - 1);
     g_stats.train_seconds = std::chrono::duration<double>(Clock::now() - t_train).count();
     g_stats.host_gradient_seconds = grad_s;
     g_stats.device_trees = grower.device_trees;
