@@ -211,6 +211,8 @@ struct fbh_ctx {
         float *leaf_vals = nullptr;
         DevColumn *cols = nullptr;
         uint16_t *feat_off = nullptr;  // byte offset of each feature in the row bundle (leaf walk)
+        int64_t *partials = nullptr;   // per-chunk partial histograms
+        uint64_t partial_bytes = 0;
         // Two result slots (state, tree, category words, leaf values), so a
         // tree can be collected while the next one is already enqueued.
         PinnedBuf out[2];
@@ -1402,6 +1404,11 @@ struct EvalPlan {
     bool download = true;  // copy the packets back (a device-grown tree reads them in place)
     const uint32_t *rows = nullptr;  // arena of the accumulated nodes (null: the row arena)
     bool cleared = false;            // the accumulated slots were cleared by the partition
+    // Per-chunk partial histograms (device-grown trees): multi-chunk nodes
+    // store their chunks here and reduce_chunks_kernel sums them into the
+    // slots; max_groups bounds the reduction groups of the launch.
+    int64_t *partials = nullptr;
+    uint32_t max_groups = 0;
 };
 
 void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
@@ -1445,6 +1452,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
             L.rows = E.rows ? E.rows : c->rows;
             L.gpair = c->gpair;
             L.hist = c->hist;
+            L.partials = E.partials;
             L.hist_width = c->hist_width;
             return L;
         };
@@ -1499,6 +1507,10 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
             c->ev_used++;
         }
     }
+    if (E.partials)
+        check(launch_reduce_chunks(c->hist, c->hist_width, E.partials, E.hn, E.n_hn, E.dev_n_hn,
+                                   E.max_groups, c->stream),
+              "chunk reduction");
     check(launch_subtract(c->hist, c->hist_width, E.triples, E.n_tri, E.dev_n_tri, c->stream),
           "sibling subtraction");
     // ---- split scan ----
@@ -1963,6 +1975,8 @@ int fbh_partition_eval(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
 namespace {
 
 constexpr uint32_t MAX_GROW_DEPTH = 14;
+// Largest per-chunk partial histogram buffer of a device-grown tree.
+constexpr uint64_t MAX_PARTIAL_BYTES = 256ull << 20;
 
 // Every tile's records in one row bundle: a row's cells for every feature
 // are in one record, so leaves can be found by walking the tree in row order.
@@ -2074,7 +2088,30 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     E0.n_hn = 1;
     E0.grid_chunks = h.n_chunks;
     E0.chunk_rows = cr;
-    if (h.n_chunks != 1 || c->has_global || !c->streamed.empty()) {
+    // Per-chunk partials instead of global atomics for multi-chunk nodes when
+    // every tile is an LDS tile and the buffer (grid chunks x histogram) is
+    // modest; only nodes of more than REDUCE_GROUP chunks then need cleared
+    // slots (their groups add atomically).
+    const ChunkRule rule = c->chunk_rule();
+    auto level_grid = [&](uint32_t nb) {
+        return rule.fixed ? n_rows / rule.fixed + nb + 1 : rule_chunk_bound(rule, n_rows, nb);
+    };
+    uint64_t all_bins = 0;
+    for (uint32_t b : c->n_bins) all_bins += b;
+    const uint64_t max_grid = std::max<uint64_t>(h.n_chunks, level_grid(lvl_bound(D - 1)));
+    const uint64_t partial_bytes = max_grid * all_bins * 16;
+    int64_t *partials = nullptr;
+    if (!c->has_global && partial_bytes <= MAX_PARTIAL_BYTES) {
+        if (GB.partial_bytes < partial_bytes) {
+            GB.partials = c->alloc<int64_t>(partial_bytes / 8, "partial histograms");
+            GB.partial_bytes = partial_bytes;
+        }
+        partials = GB.partials;
+    }
+    E0.partials = partials;
+    E0.max_groups = reduce_groups(h.n_chunks);
+    const bool root_atomic = partials ? h.n_chunks > REDUCE_GROUP : h.n_chunks != 1;
+    if (root_atomic || c->has_global || !c->streamed.empty()) {
         const uint32_t zero0 = 0;
         E0.zero_slots = S.dev<uint32_t>(S.put(&zero0, 4));
         E0.n_zero = 1;
@@ -2109,7 +2146,6 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     enqueue_eval(c, E0, sp);
     account_hist(c, n_rows, 1);
 
-    const ChunkRule rule = c->chunk_rule();
     // Leaves by a row-order walk of the finished tree (no last-level
     // partition, no scattered leaf ids) when one bundle holds every cell and
     // the tree fits the walk's LDS table.
@@ -2133,7 +2169,7 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
         ZeroNodesDev Z{};
         if (d + 1 < D)
             Z = {c->hist, c->hist_width, c->d_lvl_hist, &GB.st->n_eval,
-                 (c->has_global || !c->streamed.empty()) ? 1u : 0u, 0u};
+                 (c->has_global || !c->streamed.empty()) ? 1u : 0u, partials ? REDUCE_GROUP : 0u};
         check(launch_partition_level(GB.reqs, &GB.st->n_split, n_rows / PART_CHUNK + nb + 1,
                                      arena_in, arena_out, c->flags, c->d_counts, c->d_excl,
                                      c->d_totals, pk_cats, GB.pairs, rule, c->d_lvl_hist,
@@ -2145,7 +2181,9 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
         E.hn = c->d_lvl_hist;
         E.n_hn = nb;
         E.dev_n_hn = &GB.st->n_eval;
-        E.grid_chunks = rule.fixed ? n_rows / rule.fixed + nb + 1 : rule_chunk_bound(rule, n_rows, nb);
+        E.grid_chunks = level_grid(nb);
+        E.partials = partials;
+        E.max_groups = E.grid_chunks / REDUCE_GROUP + nb + 1;
         E.dev_chunk_rows = c->d_lvl_rows;
         E.triples = GB.triples;
         E.n_tri = nb;

@@ -46,8 +46,14 @@ struct HistNodeDev {
     uint32_t chunk_begin;  // first chunk of the node in the launch
     uint32_t slot;         // output histogram slot
     uint32_t n_chunks;
-    uint32_t pad[3];
+    uint32_t group_begin;  // first reduction group of the node (per-chunk partials)
+    uint32_t pad[2];
 };
+
+// Reduction groups of a node of n chunks (one for a node without rows).
+__host__ __device__ inline uint32_t reduce_groups(uint32_t n_chunks) {
+    return n_chunks <= 16u ? 1u : (n_chunks + 15u) / 16u;
+}
 
 struct HistLaunch {
     const TileDev *tiles;      // tiles of this launch (same width / record size)
@@ -66,6 +72,10 @@ struct HistLaunch {
     const uint32_t *rows;      // row arena
     const int64_t *gpair;      // [n_rows][2]
     int64_t *hist;             // [slots][hist_width][2]
+    // Non-null: a node of several chunks stores each chunk's histogram here
+    // ([chunk][hist_width][2], plain stores) for reduce_chunks_kernel,
+    // instead of adding it into its slot with global atomics.
+    int64_t *partials;
     uint64_t hist_width;
     // Streamed tile: its records of rows [row_lo, row_hi) sit at
     // stream_data + (row - row_lo) * stride; only those rows are accumulated.
@@ -184,8 +194,12 @@ struct ZeroNodesDev {
     const HistNodeDev *nodes;
     const uint32_t *dev_n;  // node count, read on the device
     uint32_t force;         // clear single-chunk nodes too
-    uint32_t pad;
+    uint32_t group;         // nonzero: per-chunk partials; clear only nodes of more chunks than this
 };
+
+// Chunks of one node that one workgroup of reduce_chunks_kernel sums
+// (reduce_groups).
+constexpr uint32_t REDUCE_GROUP = 16;
 
 // Column of one feature for the partition of a device-grown tree.
 struct DevColumn {
@@ -276,6 +290,14 @@ hipError_t launch_hist_global(const HistLaunch &L, int width, hipEvent_t ev_star
 hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slots, uint32_t n,
                              hipStream_t s);
 // dev_n (nullable): the triple count read on the device, n its upper bound.
+// Per-chunk partial histograms of the accumulated nodes into their slots:
+// plain stores for nodes of 2..REDUCE_GROUP chunks (and zeros for nodes
+// without rows), global atomics into the cleared slot per group of
+// REDUCE_GROUP chunks for larger ones. max_groups bounds the groups of all
+// nodes (HistNodeDev::group_begin numbers them).
+hipError_t launch_reduce_chunks(int64_t *hist, uint64_t width, const int64_t *partials,
+                                const HistNodeDev *nodes, uint32_t n, const uint32_t *dev_n,
+                                uint32_t max_groups, hipStream_t s);
 hipError_t launch_subtract(int64_t *hist, uint64_t width, const uint32_t *triples, uint32_t n,
                            const uint32_t *dev_n, hipStream_t s);
 // Zero the slots of accumulated nodes that need it: all when force, else

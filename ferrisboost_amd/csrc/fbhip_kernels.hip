@@ -216,8 +216,12 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
     }
     __syncthreads();
 
-    int64_t *out = L.hist + (uint64_t)N.slot * L.hist_width * 2u;
+    // One chunk: its slot. Several: the chunk's partial histogram, or
+    // atomics into the cleared slot.
     const bool single = !STREAM && N.n_chunks == 1;
+    const bool partial = !STREAM && !single && L.partials;
+    int64_t *out = partial ? L.partials + (uint64_t)chunk * L.hist_width * 2u
+                           : L.hist + (uint64_t)N.slot * L.hist_width * 2u;
     for (uint32_t fi = 0; fi < T.n_feat; fi++) {
         const TileFeatDev F = L.feats[T.feat_base + fi];
         for (uint32_t bin = tid; bin < F.n_bins; bin += TPB) {
@@ -225,7 +229,7 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
             const unsigned long long hh = hplane[F.lds_off + bin];
             unsigned long long *dst =
                 reinterpret_cast<unsigned long long *>(out + 2u * (F.hist_off + bin));
-            if (single) {
+            if (single || partial) {
                 dst[0] = gg;
                 dst[1] = hh;
             } else if ((gg | hh) != 0ull) {
@@ -355,6 +359,53 @@ hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slot
     if (n == 0) return hipSuccess;
     uint32_t bx = (uint32_t)std::min<uint64_t>((width * 2 + 255) / 256, 1024);
     hipLaunchKernelGGL(zero_slots_kernel, dim3(bx, n), dim3(256), 0, s, hist, width, slots);
+    return hipGetLastError();
+}
+
+// Grid (word blocks, groups): group y belongs to the node whose
+// group_begin range holds it. A node of at most REDUCE_GROUP chunks has one
+// group, which sums them and stores the slot (zeros for a node without rows);
+// a larger node's groups each add the sum of their REDUCE_GROUP chunks into
+// its cleared slot.
+__global__ void reduce_chunks_kernel(int64_t *hist, uint64_t width, const int64_t *partials,
+                                     const HistNodeDev *nodes, uint32_t n_nodes,
+                                     const uint32_t *dev_n) {
+    const uint32_t n = dev_n ? *dev_n : n_nodes;
+    if (n == 0) return;
+    const uint32_t y = blockIdx.y;
+    // Groups past the last node's (the grid is an upper bound) leave at once.
+    const HistNodeDev last = nodes[n - 1];
+    if (y >= last.group_begin + reduce_groups(last.n_chunks)) return;
+    uint32_t lo = 0, hi = n;
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (nodes[mid].group_begin <= y) lo = mid;
+        else hi = mid;
+    }
+    const HistNodeDev N = nodes[lo];
+    const uint32_t g = y - N.group_begin;
+    if (g >= reduce_groups(N.n_chunks) || N.n_chunks == 1) return;  // past the groups / written
+    const uint32_t c0 = g * REDUCE_GROUP, c1 = min(c0 + REDUCE_GROUP, N.n_chunks);
+    const bool store = N.n_chunks <= REDUCE_GROUP;
+    const uint64_t W = width * 2u;
+    unsigned long long *dst = reinterpret_cast<unsigned long long *>(hist + (uint64_t)N.slot * W);
+    const unsigned long long *src = reinterpret_cast<const unsigned long long *>(partials);
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < W;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        unsigned long long v = 0;
+        for (uint32_t c = c0; c < c1; c++) v += src[(uint64_t)(N.chunk_begin + c) * W + i];
+        if (store) dst[i] = v;
+        else if (v) global_add_u64(dst + i, v);
+    }
+}
+
+hipError_t launch_reduce_chunks(int64_t *hist, uint64_t width, const int64_t *partials,
+                                const HistNodeDev *nodes, uint32_t n, const uint32_t *dev_n,
+                                uint32_t max_groups, hipStream_t s) {
+    if (n == 0 || max_groups == 0) return hipSuccess;
+    const uint32_t bx = (uint32_t)std::min<uint64_t>((width * 2 + 255) / 256, 1024);
+    hipLaunchKernelGGL(reduce_chunks_kernel, dim3(bx, max_groups), dim3(256), 0, s, hist, width,
+                       partials, nodes, n, dev_n);
     return hipGetLastError();
 }
 
@@ -522,7 +573,7 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
     __syncthreads();
     if (threadIdx.x == 0) *chunk_rows_out = cr_sh;
     const uint32_t cr = cr_sh;
-    uint32_t carry = 0;
+    uint32_t carry = 0, gcarry = 0;
     for (uint32_t base = 0; base < n; base += 1024) {
         const uint32_t i = base + threadIdx.x;
         PairDev P{};
@@ -535,8 +586,10 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
             nr = P.row_len - nl;
             if (ev) nc = (min(nl, nr) + cr - 1) / cr;
         }
-        uint32_t total, leaves_total = 0, leaf_before = 0;
+        uint32_t total, leaves_total = 0, leaf_before = 0, groups_total;
         const uint32_t before = carry + block_scan_1024(nc, buf, total);
+        const uint32_t group_before = gcarry + block_scan_1024(ev ? reduce_groups(nc) : 0u, buf,
+                                                               groups_total);
         // Children of pairs that are not evaluated are leaves (those with rows).
         if (D.st) {
             const uint32_t nlv = (i < n && !ev) ? (nl > 0) + (nr > 0) : 0u;
@@ -553,6 +606,7 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
                 h.chunk_begin = before;
                 h.slot = P.new_slot;
                 h.n_chunks = nc;
+                h.group_begin = group_before;
                 hn[e] = h;
                 SplitNodeDev l{}, r{};
                 l.sum_g = P.left_sum[0];
@@ -613,6 +667,7 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
             }
         }
         carry += total;
+        gcarry += groups_total;
         leaf_base += leaves_total;
     }
     if (D.st) {
@@ -1314,7 +1369,8 @@ __global__ __launch_bounds__(PART_TPB) void part_scatter_kernel(const PartReqDev
              k += (uint64_t)gridDim.x * PART_TPB) {
             const uint64_t e = k / W;
             const HistNodeDev N = Z.nodes[e];
-            if (Z.force || N.n_chunks != 1) Z.hist[(uint64_t)N.slot * W + (k - e * W)] = 0;
+            const bool clear = Z.group ? N.n_chunks > Z.group : (Z.force || N.n_chunks != 1);
+            if (clear) Z.hist[(uint64_t)N.slot * W + (k - e * W)] = 0;
         }
     }
     const uint32_t chunk = blockIdx.x;
