@@ -1256,10 +1256,14 @@ __device__ __forceinline__ uint32_t find_req(const PartReqDev *reqs, uint32_t n,
     return lo;
 }
 
-__device__ __forceinline__ bool goes_left(const PartReqDev &R, uint32_t row,
-                                          const uint64_t *cat_words) {
+__device__ __forceinline__ uint32_t cell_of(const PartReqDev &R, uint32_t row) {
     const uint8_t *p = R.data + (size_t)row * R.stride + R.byte_off;
-    const uint32_t bin = R.width == 1 ? (uint32_t)p[0] : (uint32_t) * reinterpret_cast<const uint16_t *>(p);
+    return R.width == 1 ? (uint32_t)p[0] : (uint32_t) * reinterpret_cast<const uint16_t *>(p);
+}
+
+// The partition's go-left rule for a cell value of the request's feature.
+__device__ __forceinline__ bool bin_goes_left(const PartReqDev &R, uint32_t bin,
+                                              const uint64_t *cat_words) {
     const uint32_t missing = R.width == 1 ? 0xFFu : 0xFFFFu;
     if (bin == missing) return R.missing_left != 0;
     if (R.n_cat_words) {
@@ -1270,6 +1274,11 @@ __device__ __forceinline__ bool goes_left(const PartReqDev &R, uint32_t row,
     return bin < R.bin;
 }
 
+__device__ __forceinline__ bool goes_left(const PartReqDev &R, uint32_t row,
+                                          const uint64_t *cat_words) {
+    return bin_goes_left(R, cell_of(R, row), cat_words);
+}
+
 // Pass 1: direction flag per row and the left count of every chunk.
 __global__ __launch_bounds__(PART_TPB) void part_count_kernel(const PartReqDev *reqs,
                                                               uint32_t n_reqs,
@@ -1277,18 +1286,34 @@ __global__ __launch_bounds__(PART_TPB) void part_count_kernel(const PartReqDev *
                                                               uint8_t *flags, uint32_t *counts,
                                                               const uint64_t *cat_words,
                                                               const uint32_t *dev) {
+    constexpr int ROUNDS = PART_CHUNK / PART_TPB;
     __shared__ uint32_t wave_sum[PART_TPB / 64];
     const uint32_t chunk = blockIdx.x;
     if (dev && chunk >= dev[1]) return;
     const PartReqDev R = reqs[find_req(reqs, dev ? dev[0] : n_reqs, chunk)];
     const uint32_t c0 = (chunk - R.chunk_begin) * PART_CHUNK;
     const uint32_t c1 = min(c0 + PART_CHUNK, R.row_len);
+    // All of the thread's row ids, then all of their cells, in flight at once.
+    uint32_t row[ROUNDS], bin[ROUNDS];
+#pragma unroll
+    for (int r = 0; r < ROUNDS; r++) {
+        const uint32_t i = c0 + r * PART_TPB + threadIdx.x;
+        row[r] = i < c1 ? rows[R.row_off + i] : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < ROUNDS; r++) {
+        const uint32_t i = c0 + r * PART_TPB + threadIdx.x;
+        bin[r] = i < c1 ? cell_of(R, row[r]) : 0u;
+    }
     uint32_t cnt = 0;
-    for (uint32_t i = c0 + threadIdx.x; i < c1; i += PART_TPB) {
-        const uint32_t pos = R.row_off + i;
-        const bool gl = goes_left(R, rows[pos], cat_words);
-        flags[pos] = gl ? 1 : 0;
-        cnt += gl;
+#pragma unroll
+    for (int r = 0; r < ROUNDS; r++) {
+        const uint32_t i = c0 + r * PART_TPB + threadIdx.x;
+        if (i < c1) {
+            const bool gl = bin_goes_left(R, bin[r], cat_words);
+            flags[R.row_off + i] = gl ? 1 : 0;
+            cnt += gl;
+        }
     }
     // wave reduction
     for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
@@ -1361,7 +1386,6 @@ __global__ __launch_bounds__(PART_TPB) void part_scatter_kernel(const PartReqDev
                                                                 uint32_t *tmp,
                                                                 const uint32_t *dev,
                                                                 ZeroNodesDev Z) {
-    __shared__ uint32_t wave_left[PART_TPB / 64];
     if (Z.hist) {
         const uint64_t W = Z.width * 2u;
         const uint64_t all = (uint64_t)*Z.dev_n * W;
@@ -1382,31 +1406,45 @@ __global__ __launch_bounds__(PART_TPB) void part_scatter_kernel(const PartReqDev
     const uint32_t left_base = excl[chunk] - excl[R.chunk_begin];
     const uint32_t total_left = totals[ri];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint32_t done_left = 0;  // lefts of earlier rounds in this chunk
-    for (uint32_t base = c0; base < c1; base += PART_TPB) {
-        const uint32_t i = base + threadIdx.x;
+    // Every round's flags and row ids in flight at once, every round's
+    // ballot counts in LDS behind one barrier.
+    constexpr int ROUNDS = PART_CHUNK / PART_TPB;
+    constexpr int WAVES = PART_TPB / 64;
+    __shared__ uint32_t round_left[ROUNDS][WAVES];
+    uint32_t row[ROUNDS], below[ROUNDS];
+    uint32_t left_bits = 0;
+#pragma unroll
+    for (int r = 0; r < ROUNDS; r++) {
+        const uint32_t i = c0 + r * PART_TPB + threadIdx.x;
         const bool valid = i < c1;
-        const bool gl = valid && flags[R.row_off + i];
-        const uint64_t ball = __ballot(gl);
-        const uint32_t below = __popcll(ball & ((1ull << lane) - 1ull));
-        if (lane == 0) wave_left[wave] = __popcll(ball);
-        __syncthreads();
-        uint32_t before = 0, round_left = 0;
-        for (uint32_t w = 0; w < PART_TPB / 64; w++) {
-            if (w < wave) before += wave_left[w];
-            round_left += wave_left[w];
+        row[r] = valid ? rows[R.row_off + i] : 0u;
+        left_bits |= (valid && flags[R.row_off + i] ? 1u : 0u) << r;
+    }
+#pragma unroll
+    for (int r = 0; r < ROUNDS; r++) {
+        const uint64_t ball = __ballot((left_bits >> r) & 1u);
+        below[r] = __popcll(ball & ((1ull << lane) - 1ull));
+        if (lane == 0) round_left[r][wave] = __popcll(ball);
+    }
+    __syncthreads();
+    uint32_t done_left = 0;  // lefts of earlier rounds in this chunk
+#pragma unroll
+    for (int r = 0; r < ROUNDS; r++) {
+        uint32_t before = 0, in_round = 0;
+        for (uint32_t w = 0; w < WAVES; w++) {
+            if (w < wave) before += round_left[r][w];
+            in_round += round_left[r][w];
         }
-        if (valid) {
-            const uint32_t row = rows[R.row_off + i];
-            const uint32_t lrank = done_left + before + below;
+        const uint32_t i = c0 + r * PART_TPB + threadIdx.x;
+        if (i < c1) {
+            const uint32_t lrank = done_left + before + below[r];
             const uint32_t idx_in_chunk = i - c0;
             uint32_t dst;
-            if (gl) dst = R.row_off + left_base + lrank;
+            if ((left_bits >> r) & 1u) dst = R.row_off + left_base + lrank;
             else dst = R.row_off + total_left + (c0 - left_base) + (idx_in_chunk - lrank);
-            tmp[dst] = row;
+            tmp[dst] = row[r];
         }
-        done_left += round_left;
-        __syncthreads();
+        done_left += in_round;
     }
 }
 
