@@ -1615,22 +1615,39 @@ __global__ __launch_bounds__(256) void gradient_kernel(const float *src, const f
                                                        const float *w, uint64_t n, int mode,
                                                        float *g2n, uint64_t th, uint64_t seed,
                                                        uint64_t tree, double *block_max) {
+    // Four rows a thread per step (loads of all four first).
+    constexpr int U = 4;
     double mg = 0.0, mh = 0.0;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (uint64_t)gridDim.x * blockDim.x) {
-        const float v = mode == 2 ? fb_sigmoid(src[i]) : src[i];
-        float g = v - y[i];
-        float h = mode != 0 ? fmaxf(v * (1.0f - v), 1e-16f) : 1.0f;
-        if (w) {
-            g = g * w[i];
-            h = h * w[i];
+    const uint64_t S = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t base = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; base < n;
+         base += U * S) {
+        float sv[U], yv[U], wv[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint64_t i = base + u * S;
+            const bool ok = i < n;
+            sv[u] = ok ? src[i] : 0.0f;
+            yv[u] = ok ? y[i] : 0.0f;
+            wv[u] = (ok && w) ? w[i] : 1.0f;
         }
-        if (block_max) {
-            if (!row_selected(i, th, seed, tree)) g = h = 0.0f;
-            mg = fmax(mg, finite_abs(g));
-            mh = fmax(mh, finite_abs(h));
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint64_t i = base + u * S;
+            if (i >= n) continue;
+            const float v = mode == 2 ? fb_sigmoid(sv[u]) : sv[u];
+            float g = v - yv[u];
+            float h = mode != 0 ? fmaxf(v * (1.0f - v), 1e-16f) : 1.0f;
+            if (w) {
+                g = g * wv[u];
+                h = h * wv[u];
+            }
+            if (block_max) {
+                if (!row_selected(i, th, seed, tree)) g = h = 0.0f;
+                mg = fmax(mg, finite_abs(g));
+                mh = fmax(mh, finite_abs(h));
+            }
+            reinterpret_cast<float2 *>(g2n)[i] = make_float2(g, h);
         }
-        reinterpret_cast<float2 *>(g2n)[i] = make_float2(g, h);
     }
     if (block_max) block_max2(mg, mh, block_max);
 }
@@ -1731,22 +1748,22 @@ __device__ __forceinline__ double finite_abs(float v) {
     return isfinite(v) ? fabs((double)v) : (double)INFINITY;
 }
 
-// Block maxima of the two bounds (256 threads) into block_max[2 * block].
+// Block maxima of the two bounds (256 threads) into block_max[2 * block]:
+// shuffles within each wave, then the four wave results.
 __device__ void block_max2(double mg, double mh, double *block_max) {
-    __shared__ double sm[2][256];
-    sm[0][threadIdx.x] = mg;
-    sm[1][threadIdx.x] = mh;
-    __syncthreads();
-    for (uint32_t s = 128; s > 0; s >>= 1) {
-        if (threadIdx.x < s) {
-            sm[0][threadIdx.x] = fmax(sm[0][threadIdx.x], sm[0][threadIdx.x + s]);
-            sm[1][threadIdx.x] = fmax(sm[1][threadIdx.x], sm[1][threadIdx.x + s]);
-        }
-        __syncthreads();
+    __shared__ double sm[2][4];
+    for (int off = 32; off > 0; off >>= 1) {
+        mg = fmax(mg, __shfl_xor(mg, off, 64));
+        mh = fmax(mh, __shfl_xor(mh, off, 64));
     }
+    if ((threadIdx.x & 63) == 0) {
+        sm[0][threadIdx.x >> 6] = mg;
+        sm[1][threadIdx.x >> 6] = mh;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        block_max[2 * blockIdx.x] = sm[0][0];
-        block_max[2 * blockIdx.x + 1] = sm[1][0];
+        block_max[2 * blockIdx.x] = fmax(fmax(sm[0][0], sm[0][1]), fmax(sm[0][2], sm[0][3]));
+        block_max[2 * blockIdx.x + 1] = fmax(fmax(sm[1][0], sm[1][1]), fmax(sm[1][2], sm[1][3]));
     }
 }
 
@@ -1879,31 +1896,43 @@ __device__ __forceinline__ int64_t sat_i64(double x) {
 __global__ __launch_bounds__(256) void gpair_quantize_kernel(const float *g2n, uint64_t n,
                                                              const ScalesDev *scales, int64_t *out,
                                                              int64_t *block_sum) {
-    __shared__ int64_t sm[2][256];
+    __shared__ int64_t sm[2][4];
     const double sg = scales->scale[0], sh = scales->scale[1];
     uint64_t ag = 0, ah = 0;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (uint64_t)gridDim.x * blockDim.x) {
-        const float2 v = reinterpret_cast<const float2 *>(g2n)[i];
-        const int64_t qg = sat_i64(round((double)v.x * sg));
-        const int64_t qh = sat_i64(round((double)v.y * sh));
-        reinterpret_cast<longlong2 *>(out)[i] = make_longlong2(qg, qh);
-        ag += (uint64_t)qg;
-        ah += (uint64_t)qh;
-    }
-    sm[0][threadIdx.x] = (int64_t)ag;
-    sm[1][threadIdx.x] = (int64_t)ah;
-    __syncthreads();
-    for (uint32_t s = 128; s > 0; s >>= 1) {
-        if (threadIdx.x < s) {
-            sm[0][threadIdx.x] = wadd(sm[0][threadIdx.x], sm[0][threadIdx.x + s]);
-            sm[1][threadIdx.x] = wadd(sm[1][threadIdx.x], sm[1][threadIdx.x + s]);
+    constexpr int U = 4;
+    const uint64_t S = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t base = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; base < n;
+         base += U * S) {
+        float2 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint64_t i = base + u * S;
+            v[u] = i < n ? reinterpret_cast<const float2 *>(g2n)[i] : make_float2(0.0f, 0.0f);
         }
-        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint64_t i = base + u * S;
+            if (i >= n) continue;
+            const int64_t qg = sat_i64(round((double)v[u].x * sg));
+            const int64_t qh = sat_i64(round((double)v[u].y * sh));
+            reinterpret_cast<longlong2 *>(out)[i] = make_longlong2(qg, qh);
+            ag += (uint64_t)qg;
+            ah += (uint64_t)qh;
+        }
     }
+    // Wrapping sums: shuffles within each wave, then the four wave sums.
+    for (int off = 32; off > 0; off >>= 1) {
+        ag += (uint64_t)__shfl_xor((long long)ag, off, 64);
+        ah += (uint64_t)__shfl_xor((long long)ah, off, 64);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sm[0][threadIdx.x >> 6] = (int64_t)ag;
+        sm[1][threadIdx.x >> 6] = (int64_t)ah;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        block_sum[2 * blockIdx.x] = sm[0][0];
-        block_sum[2 * blockIdx.x + 1] = sm[1][0];
+        block_sum[2 * blockIdx.x] = wadd(wadd(sm[0][0], sm[0][1]), wadd(sm[0][2], sm[0][3]));
+        block_sum[2 * blockIdx.x + 1] = wadd(wadd(sm[1][0], sm[1][1]), wadd(sm[1][2], sm[1][3]));
     }
 }
 
