@@ -488,31 +488,78 @@ __device__ __forceinline__ uint32_t block_scan_1024(uint32_t v, uint32_t *buf, u
     return block_scan(v, buf, total);
 }
 
+// block_scan of 64-bit values (two packed 32-bit counters scan together
+// when neither total overflows); buf needs 32 entries.
+__device__ uint64_t block_scan_u64(uint64_t v, uint64_t *buf, uint64_t &total) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t nw = blockDim.x >> 6;
+    uint64_t incl = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint64_t t = __shfl_up(incl, off, 64);
+        if (lane >= (uint32_t)off) incl += t;
+    }
+    if (lane == 63) buf[wave] = incl;
+    __syncthreads();
+    if (wave == 0) {
+        uint64_t w = lane < nw ? buf[lane] : 0ull;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint64_t t = __shfl_up(w, off, 64);
+            if (lane >= (uint32_t)off) w += t;
+        }
+        if (lane < nw) buf[16 + lane] = w;
+    }
+    __syncthreads();
+    const uint64_t before = wave ? buf[16 + wave - 1] : 0ull;
+    total = buf[16 + nw - 1];
+    __syncthreads();
+    return before + incl - v;
+}
+
 // One workgroup plans the children of a fused partition + evaluation step
 // from the partition's left counts (see launch_level_plan).
+// Loads a caller issued early for level_plan_body: the state's counts and
+// the thread's first pair.
+struct PlanPrefetch {
+    bool valid;
+    uint32_t n, leaf_base;
+    PairDev first;
+};
+
 __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t *totals,
                                 ChunkRule rule, HistNodeDev *hn, SplitNodeDev *sn,
                                 uint32_t *spans, uint32_t *left_slot, uint32_t *chunk_rows_out,
-                                const GrowDevOut &D) {
+                                const GrowDevOut &D, const PlanPrefetch &pre) {
     __shared__ uint32_t buf[1024];
     __shared__ unsigned long long acc_sh, acc_nodes_sh;
-    __shared__ uint32_t cr_sh;
+    __shared__ uint64_t buf64[32];
+    __shared__ uint32_t cr_sh, nz_sh;
     // A device-grown tree: the pair count and the leaf table base come from
     // its state (read by every thread before thread 0 updates it).
     uint32_t leaf_base = 0;
-    if (D.st) {
+    if (pre.valid) {
+        n = pre.n;
+        leaf_base = pre.leaf_base;
+    } else if (D.st) {
         n = D.st->n_split;
         leaf_base = D.st->n_leaves;
     }
-    if (threadIdx.x == 0) acc_sh = acc_nodes_sh = 0;
+    auto pair_at = [&](uint32_t i) -> PairDev {
+        return (pre.valid && i == threadIdx.x) ? pre.first : pairs[i];
+    };
+    if (threadIdx.x == 0) {
+        acc_sh = acc_nodes_sh = 0;
+        nz_sh = 0;
+    }
     __syncthreads();
     // Spans of every pair and the rows the evaluated pairs accumulate. The
     // thread's first pair (all of them when n <= 1024) stays in registers:
     // left count, and the accumulated (smaller) child's rows when evaluated.
     unsigned long long acc = 0;
-    uint32_t my_nl = 0, my_small = 0;
+    uint32_t my_nl = 0, my_small = 0, nz = 0;
     for (uint32_t i = threadIdx.x; i < n; i += 1024) {
-        const PairDev P = pairs[i];
+        const PairDev P = pair_at(i);
         const uint32_t nl = P.req == NO_SLOT ? 0u : totals[P.req];
         const uint32_t nr = P.row_len - nl;
         spans[4 * i + 0] = P.row_off;
@@ -521,6 +568,7 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
         spans[4 * i + 3] = nr;
         const bool ev = P.eval_index != NO_SLOT;
         if (ev) acc += min(nl, nr);
+        if (ev && min(nl, nr)) nz++;
         if (i == threadIdx.x) {
             my_nl = nl;
             my_small = ev ? min(nl, nr) : 0u;
@@ -535,6 +583,7 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
         return min(nl, P.row_len - nl);
     };
     atomicAdd(&acc_sh, acc);
+    if (nz) atomicAdd(&nz_sh, nz);
     __syncthreads();
     unsigned long long acc_nodes = 0;
     // Rows per chunk: the smallest multiple of 1024 whose chunks fit one wave
@@ -544,10 +593,7 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
         if (threadIdx.x == 0) cr_sh = rule.fixed;
     } else {
         const uint64_t acc_all = acc_sh;
-        uint32_t nz = 0;
-        for (uint32_t i = threadIdx.x; i < n; i += 1024) nz += small_of(i) ? 1u : 0u;
-        uint32_t n_nz;
-        (void)block_scan_1024(nz, buf, n_nz);
+        const uint32_t n_nz = nz_sh;  // evaluated pairs whose accumulated child has rows
         const uint64_t W = rule.want_chunks;
         uint64_t lo = (acc_all + W * 1024 - 1) / (W * 1024);
         lo = lo < 1 ? 1 : lo;
@@ -580,16 +626,21 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
         uint32_t nl = 0, nr = 0, nc = 0;
         bool ev = false;
         if (i < n) {
-            P = pairs[i];
+            P = pair_at(i);
             ev = P.eval_index != NO_SLOT;
             nl = base == 0 ? my_nl : (P.req == NO_SLOT ? 0u : totals[P.req]);
             nr = P.row_len - nl;
             if (ev) nc = (min(nl, nr) + cr - 1) / cr;
         }
-        uint32_t total, leaves_total = 0, leaf_before = 0, groups_total;
-        const uint32_t before = carry + block_scan_1024(nc, buf, total);
-        const uint32_t group_before = gcarry + block_scan_1024(ev ? reduce_groups(nc) : 0u, buf,
-                                                               groups_total);
+        uint32_t leaves_total = 0, leaf_before = 0;
+        // Chunks (low half) and reduction groups (high half) in one scan.
+        uint64_t both_total;
+        const uint64_t both =
+            block_scan_u64((uint64_t)nc | ((uint64_t)(ev ? reduce_groups(nc) : 0u) << 32), buf64,
+                           both_total);
+        const uint32_t total = (uint32_t)both_total, groups_total = (uint32_t)(both_total >> 32);
+        const uint32_t before = carry + (uint32_t)both;
+        const uint32_t group_before = gcarry + (uint32_t)(both >> 32);
         // Children of pairs that are not evaluated are leaves (those with rows).
         if (D.st) {
             const uint32_t nlv = (i < n && !ev) ? (nl > 0) + (nr > 0) : 0u;
@@ -688,7 +739,8 @@ __global__ __launch_bounds__(1024) void level_plan_kernel(const PairDev *pairs, 
                                                           HistNodeDev *hn, SplitNodeDev *sn,
                                                           uint32_t *spans, uint32_t *left_slot,
                                                           uint32_t *chunk_rows_out, GrowDevOut D) {
-    level_plan_body(pairs, n, totals, rule, hn, sn, spans, left_slot, chunk_rows_out, D);
+    level_plan_body(pairs, n, totals, rule, hn, sn, spans, left_slot, chunk_rows_out, D,
+                    PlanPrefetch{});
 }
 
 hipError_t launch_level_plan(const PairDev *pairs, uint32_t n_pairs, const uint32_t *totals,
@@ -1367,9 +1419,77 @@ __global__ __launch_bounds__(1024) void part_scan_plan_kernel(
     const uint32_t *counts, uint32_t *excl, const PartReqDev *reqs, uint32_t *totals,
     const uint32_t *dev, const PairDev *pairs, ChunkRule rule, HistNodeDev *hn, SplitNodeDev *sn,
     uint32_t *spans, uint32_t *left_slot, uint32_t *chunk_rows_out, GrowDevOut D) {
-    part_scan_body(counts, 0u, excl, reqs, 0u, totals, dev);
+    constexpr uint32_t LDS_CHUNKS = 8192;
+    __shared__ uint32_t s_excl[LDS_CHUNKS + 1];
+    __shared__ uint32_t s_tot[1024];
+    __shared__ uint32_t buf[32];
+    // Everything the scan and plan read that does not depend on the scan is
+    // requested first: the counts, the state, the thread's request and pair.
+    const uint32_t n_reqs = dev[0], n_chunks = dev[1];
+    PlanPrefetch pre{};
+    pre.valid = D.st != nullptr;
+    if (pre.valid) {
+        pre.n = D.st->n_split;
+        pre.leaf_base = D.st->n_leaves;
+        if (threadIdx.x < pre.n) pre.first = pairs[threadIdx.x];
+    }
+    if (n_chunks > LDS_CHUNKS || n_reqs > 1024) {
+        part_scan_body(counts, 0u, excl, reqs, 0u, totals, dev);
+        __syncthreads();
+        level_plan_body(pairs, 0u, totals, rule, hn, sn, spans, left_slot, chunk_rows_out, D,
+                        pre);
+        return;
+    }
+    uint32_t cb = 0, cn = 0;
+    if (threadIdx.x < n_reqs) {
+        cb = reqs[threadIdx.x].chunk_begin;
+        cn = reqs[threadIdx.x].n_chunks;
+    }
+    // Exclusive scan of the counts (a run of chunks a thread), kept in LDS
+    // and written out for the scatter; the request totals from LDS.
+    const uint32_t per = (n_chunks + 1023) / 1024;
+    const uint32_t c0 = min(threadIdx.x * per, n_chunks), c1 = min(c0 + per, n_chunks);
+    uint32_t cnt[8];
+    uint32_t sum = 0;
+    if (per <= 8) {
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++) {
+            cnt[k] = c0 + k < c1 ? counts[c0 + k] : 0u;
+            sum += cnt[k];
+        }
+    } else {
+        for (uint32_t i = c0; i < c1; i++) sum += counts[i];
+    }
+    uint32_t total;
+    uint32_t run = block_scan_1024(sum, buf, total);
+    if (per <= 8) {
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++) {
+            if (c0 + k < c1) {
+                s_excl[c0 + k] = run;
+                excl[c0 + k] = run;
+                run += cnt[k];
+            }
+        }
+    } else {
+        for (uint32_t i = c0; i < c1; i++) {
+            s_excl[i] = run;
+            excl[i] = run;
+            run += counts[i];
+        }
+    }
+    if (threadIdx.x == 0) {
+        s_excl[n_chunks] = total;
+        excl[n_chunks] = total;
+    }
     __syncthreads();
-    level_plan_body(pairs, 0u, totals, rule, hn, sn, spans, left_slot, chunk_rows_out, D);
+    if (threadIdx.x < n_reqs) {
+        const uint32_t t = s_excl[cb + cn] - s_excl[cb];
+        s_tot[threadIdx.x] = t;
+        totals[threadIdx.x] = t;
+    }
+    __syncthreads();
+    level_plan_body(pairs, 0u, s_tot, rule, hn, sn, spans, left_slot, chunk_rows_out, D, pre);
 }
 
 // Pass 3: stable scatter into the temporary arena. Rows of a chunk are taken
