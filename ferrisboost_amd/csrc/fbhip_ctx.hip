@@ -176,6 +176,9 @@ struct fbh_ctx {
     float *delta = nullptr;
     int64_t *hist = nullptr;
     ScalesDev *d_scales = nullptr;  // scales of the current gradients
+    // The row arena of a new tree is the identity; it is written out only
+    // when something reads it (a device-grown tree walks the root without it).
+    bool rows_identity = false;
     double *red_f64 = nullptr;
     int64_t *red_i64 = nullptr;
     uint32_t n_red_blocks = 8192;  // blocks of the bounds and quantisation passes
@@ -213,6 +216,12 @@ struct fbh_ctx {
         uint16_t *feat_off = nullptr;  // byte offset of each feature in the row bundle (leaf walk)
         int64_t *partials = nullptr;   // per-chunk partial histograms
         uint64_t partial_bytes = 0;
+        // The root's accumulation table (offset 0) and the monotone
+        // constraints (offset 256) on the device, with the host copies they
+        // were last uploaded from.
+        uint8_t *root_tables = nullptr;
+        HistNodeDev h_root_hn{};
+        std::vector<int8_t> h_mono;
         // Two result slots (state, tree, category words, leaf values), so a
         // tree can be collected while the next one is already enqueued.
         PinnedBuf out[2];
@@ -379,6 +388,9 @@ struct fbh_ctx {
 
     void sync() { check(hipStreamSynchronize(stream), "stream synchronize"); }
 
+    // The row arena written out (rows in order) if the tree has not yet.
+    void ensure_rows();
+
     // The next staging slot, once the copy that last read it has run.
     uint8_t *stage_acquire(int &slot) {
         slot = stage_next;
@@ -461,6 +473,13 @@ struct fbh_ctx {
         ev_used = keep;
     }
 };
+
+void fbh_ctx::ensure_rows() {
+    if (!rows_identity) return;
+    check(launch_init_rows(rows, objective >= 0 ? nullptr : delta, n_rows, stream),
+          "row arena reset");
+    rows_identity = false;
+}
 
 namespace {
 
@@ -1044,8 +1063,11 @@ void quantize_device_pairs(fbh_ctx *c, uint64_t th, uint64_t seed, uint64_t tree
         c->scales[0] = S.scale[0];
         c->scales[1] = S.scale[1];
     }
+    // The per-block sums stay in red_i64; only a host caller needs them summed
+    // here (a device-grown tree sums them in its root kernel).
     check(launch_gpair_quantize(c->gpair_f32, c->n_rows, c->d_scales, c->gpair, c->red_i64,
-                                c->n_red_blocks, c->red_i64 + 2 * c->n_red_blocks, c->stream),
+                                c->n_red_blocks,
+                                root_out ? c->red_i64 + 2 * c->n_red_blocks : nullptr, c->stream),
           "gradient quantisation");
     c->root_on_device = true;
     if (scales_out) {
@@ -1343,9 +1365,9 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
         }
         // The delta is kept only for callers without a device objective.
         if (c->objective < 0 && !c->delta) c->delta = c->alloc<float>(c->n_rows, "prediction delta");
-        check(launch_init_rows(c->rows, c->objective >= 0 ? nullptr : c->delta, c->n_rows,
-                               c->stream),
-              "row arena reset");
+        // Callers without a device objective also clear their prediction delta.
+        c->rows_identity = true;
+        if (c->objective < 0) c->ensure_rows();
         c->tree_begun = true;
         root->offset = 0;
         root->len = (uint32_t)c->n_rows;
@@ -1404,6 +1426,7 @@ struct EvalPlan {
     bool download = true;  // copy the packets back (a device-grown tree reads them in place)
     const uint32_t *rows = nullptr;  // arena of the accumulated nodes (null: the row arena)
     bool cleared = false;            // the accumulated slots were cleared by the partition
+    bool identity = false;           // the accumulated rows are in order (no arena read)
     // Per-chunk partial histograms (device-grown trees): multi-chunk nodes
     // store their chunks here and reduce_chunks_kernel sums them into the
     // slots; max_groups bounds the reduction groups of the launch.
@@ -1449,7 +1472,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
             L.chunk_groups = div_up(E.grid_chunks, XCDS);
             // Chunk-major XCD locality needs at least one chunk per XCD.
             L.linear = c->chunk_rule().want_chunks < XCDS ? 1u : 0u;
-            L.rows = E.rows ? E.rows : c->rows;
+            L.rows = E.identity ? nullptr : (E.rows ? E.rows : c->rows);
             L.gpair = c->gpair;
             L.hist = c->hist;
             L.partials = E.partials;
@@ -1671,6 +1694,7 @@ int fbh_eval_nodes(fbh_ctx *c, const fbh_node *nodes, uint32_t n, const fbh_spli
         if (n == 0) return;
         if (n > c->n_slots) throw InputError("more nodes than histogram slots");
         check(hipSetDevice(c->device), "hipSetDevice");
+        c->ensure_rows();
         Stager S{c};
         EvalPlan E;
         const auto acc = stage_host_eval(c, nodes, n, enabled, S, E);
@@ -1848,6 +1872,7 @@ int fbh_partition(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n, const uint64
         if (n == 0) return;
         if (n > MAX_NODES) throw InputError("too many partition requests");
         check(hipSetDevice(c->device), "hipSetDevice");
+        c->ensure_rows();
         Stager S{c};
         const PartStage P = stage_partition(c, reqs, n, cat_words, n_cat_words, S);
         for (uint32_t i = 0; i < n; i++) {
@@ -1883,6 +1908,7 @@ int fbh_partition_eval(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
         if (n == 0) return;
         if (n > MAX_NODES) throw InputError("too many partition requests");
         check(hipSetDevice(c->device), "hipSetDevice");
+        c->ensure_rows();
         // Every slot of the evaluated pairs is used once: the larger child
         // takes over the parent's slot, the smaller one accumulates into its own.
         std::vector<uint8_t> used(c->n_slots, 0);
@@ -1993,6 +2019,8 @@ void ensure_grow(fbh_ctx *c, uint32_t D) {
     const uint32_t cw = std::max(1u, c->max_cat_words);
     if (!G.cols) {
         G.st = c->alloc<GrowState>(1, "grown tree state");
+        G.root_tables = c->alloc<uint8_t>(256 + c->n_features, "grown tree root tables");
+        G.h_root_hn.n_chunks = ~0u;  // never a real plan: the first tree uploads
         G.cols = c->alloc<DevColumn>(c->n_features, "grown tree columns");
         std::vector<DevColumn> cols(c->n_features);
         for (uint32_t f = 0; f < c->n_features; f++) cols[f] = {c->cols[f], c->width[f], 0};
@@ -2073,9 +2101,19 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     const uint32_t n_slots = c->n_slots;
     auto lvl_bound = [&](uint32_t d) { return std::min<uint32_t>(1u << d, n_slots); };
 
-    // The root: one accumulated node over every row, planned here; its split
-    // node (sums, bounds) is written by the init kernel from the root sum.
-    Stager S{c};
+    // Leaves by a row-order walk of the finished tree (no last-level
+    // partition, no scattered leaf ids) when one bundle holds every cell and
+    // the tree fits the walk's LDS table. Without leaf spans to assign, the
+    // root's rows need not be written out: its accumulation and partition
+    // take the identity.
+    const bool walk = GB.feat_off && ((2u << D) - 1) <= MAX_WALK_NODES;
+    if (!walk) c->ensure_rows();
+    const bool ident = c->rows_identity;
+
+    // The root: one accumulated node over every row, planned here (the
+    // table and the monotone constraints go up only when they change); its
+    // split node (sums, bounds) is written by the prep kernel from the root
+    // sum, which also clears the root's slot when it accumulates atomically.
     const uint32_t cr = c->chunk_rows_for(n_rows);
     HistNodeDev h{};
     h.row_off = 0;
@@ -2083,11 +2121,23 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     h.chunk_begin = 0;
     h.slot = 0;
     h.n_chunks = div_up(n_rows, cr);
+    const bool new_hn = std::memcmp(&h, &GB.h_root_hn, sizeof(h)) != 0;
+    const bool new_mono = c->monotone != GB.h_mono;
+    if (new_hn || new_mono) {
+        int slot;
+        uint8_t *hp = c->stage_acquire(slot);
+        std::memcpy(hp, &h, sizeof(h));
+        std::memcpy(hp + 256, c->monotone.data(), c->n_features);
+        c->stage_send(slot, GB.root_tables, 256 + c->n_features);
+        GB.h_root_hn = h;
+        GB.h_mono = c->monotone;
+    }
     EvalPlan E0;
-    E0.hn = S.dev<HistNodeDev>(S.put(&h, sizeof(h)));
+    E0.hn = reinterpret_cast<const HistNodeDev *>(GB.root_tables);
     E0.n_hn = 1;
     E0.grid_chunks = h.n_chunks;
     E0.chunk_rows = cr;
+    E0.identity = ident;
     // Per-chunk partials instead of global atomics for multi-chunk nodes when
     // every tile is an LDS tile and the buffer (grid chunks x histogram) is
     // modest; only nodes of more than REDUCE_GROUP chunks then need cleared
@@ -2111,18 +2161,20 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     E0.partials = partials;
     E0.max_groups = reduce_groups(h.n_chunks);
     const bool root_atomic = partials ? h.n_chunks > REDUCE_GROUP : h.n_chunks != 1;
-    if (root_atomic || c->has_global || !c->streamed.empty()) {
-        const uint32_t zero0 = 0;
-        E0.zero_slots = S.dev<uint32_t>(S.put(&zero0, 4));
-        E0.n_zero = 1;
-    }
+    const bool clear_root = root_atomic || c->has_global;
+    E0.cleared = true;
     E0.sn = c->d_lvl_split;
     E0.n_nodes = 1;
     E0.download = false;
-    const int64_t *d_root = root_sum ? S.dev<const int64_t>(S.put(root_sum, 16))
-                                     : c->red_i64 + 2 * c->n_red_blocks;
-    const int8_t *d_mono = S.dev<const int8_t>(S.put(c->monotone.data(), c->n_features));
-    S.send();
+    // A root sum from the host is staged; else the prep kernel sums the
+    // quantisation's block sums.
+    const int64_t *d_root = nullptr;
+    if (root_sum) {
+        Stager S{c};
+        d_root = S.dev<const int64_t>(S.put(root_sum, 16));
+        S.send();
+    }
+    const int8_t *d_mono = reinterpret_cast<const int8_t *>(GB.root_tables + 256);
 
     GrowParamsDev G{};
     G.sp.scales = c->d_scales;
@@ -2141,15 +2193,13 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     G.n_slots = n_slots;
     G.cw = std::max(1u, c->cat_words_per_node);
     G.n_rows = n_rows;
-    check(launch_grow_init(G, d_root, 0, GB.level[0], c->d_lvl_split, GB.tree, GB.st, c->stream),
-          "tree init");
+    check(launch_grow_prep(G, d_root, d_root ? nullptr : c->red_i64, c->n_red_blocks, 0,
+                           GB.level[0], c->d_lvl_split, GB.tree, GB.st,
+                           clear_root ? c->hist : nullptr, 2 * c->hist_width, c->stream),
+          "tree root");
     enqueue_eval(c, E0, sp);
     account_hist(c, n_rows, 1);
 
-    // Leaves by a row-order walk of the finished tree (no last-level
-    // partition, no scattered leaf ids) when one bundle holds every cell and
-    // the tree fits the walk's LDS table.
-    const bool walk = GB.feat_off && ((2u << D) - 1) <= MAX_WALK_NODES;
     uint8_t *pk_base = reinterpret_cast<uint8_t *>(c->d_packets);
     for (uint32_t d = 0; d < D; d++) {
         const uint32_t nb = lvl_bound(d);
@@ -2161,8 +2211,9 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
               "tree level decision");
         if (walk && d + 1 == D) break;  // the last level's children are found by the walk
         // Level d's rows are in arena d % 2; its children go to the other.
-        uint32_t *arena_in = (d & 1) ? c->tmp : c->rows;
+        uint32_t *arena_in = (d & 1) ? c->tmp : (ident && d == 0 ? nullptr : c->rows);
         uint32_t *arena_out = (d & 1) ? c->rows : c->tmp;
+        if (arena_out == c->rows) c->rows_identity = false;
         const GrowDevOut out{GB.st, GB.level[(d + 1) & 1], GB.tree, GB.leaves, GB.leaf_vals,
                              (d + 1) & 1u};
         // The scatter clears the next level's accumulated slots (none after the last level).
@@ -2314,6 +2365,7 @@ int fbh_assign_leaves(fbh_ctx *c, const fbh_span *spans, const float *values, ui
         if (n == 0) return;
         if (n > MAX_NODES) throw InputError("too many leaves");
         check(hipSetDevice(c->device), "hipSetDevice");
+        c->ensure_rows();
         if (c->leaves_pending) {
             check(hipEventSynchronize(c->leaves_done), "leaf table reuse");
             c->leaves_pending = false;
@@ -2387,6 +2439,7 @@ int fbh_download_rows(fbh_ctx *c, uint32_t *out) {
     return guard([&] {
         if (!c || !out) throw InputError("null argument");
         check(hipSetDevice(c->device), "hipSetDevice");
+        c->ensure_rows();
         check(hipMemcpyAsync(out, c->rows, c->n_rows * 4, hipMemcpyDeviceToHost, c->stream),
               "row download");
         c->sync();

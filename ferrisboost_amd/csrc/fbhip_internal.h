@@ -314,9 +314,12 @@ hipError_t launch_level_plan(const PairDev *pairs, uint32_t n_pairs, const uint3
                              const GrowDevOut &D, hipStream_t s);
 // Device-grown depthwise trees (one workgroup each): the root, the decision
 // of one level (see grow_decide_kernel) and the leaf table's chunks.
-hipError_t launch_grow_init(const GrowParamsDev &G, const int64_t *root, uint32_t root_slot,
-                            LNodeDev *level, SplitNodeDev *root_split, TreeNodeDev *tree,
-                            GrowState *st, hipStream_t s);
+// root NULL: the root sum is the wrapping sum of n_blocks (g, h) block sums.
+// clear (clear_words i64) is cleared by the same launch.
+hipError_t launch_grow_prep(const GrowParamsDev &G, const int64_t *root, const int64_t *block_sums,
+                            uint32_t n_blocks, uint32_t root_slot, LNodeDev *level,
+                            SplitNodeDev *root_split, TreeNodeDev *tree, GrowState *st,
+                            int64_t *clear, uint64_t clear_words, hipStream_t s);
 hipError_t launch_grow_decide(const GrowParamsDev &G, uint32_t depth, const SplitPacketDev *pk,
                               const uint64_t *pk_cats, const LNodeDev *level, TreeNodeDev *tree,
                               uint64_t *tree_cats, const int8_t *monotone, const DevColumn *cols,

@@ -166,7 +166,9 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
     unsigned long long *gplane = lds;
     unsigned long long *hplane = lds + S;
 
-    const uint32_t *rows = L.rows + N.row_off;
+    // A null row arena: the node's rows are row_off, row_off + 1, ... (the
+    // root before any partition).
+    const uint32_t *rows = L.rows ? L.rows + N.row_off : nullptr;
     const longlong2 *gp = reinterpret_cast<const longlong2 *>(L.gpair);
     for (uint32_t i = r0 + tid; i < r1; i += TPB * UNROLL) {
         uint32_t row[UNROLL];
@@ -175,7 +177,7 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
         for (int u = 0; u < UNROLL; u++) {
             const uint32_t idx = i + u * TPB;
             ok[u] = idx < r1;
-            row[u] = ok[u] ? rows[idx] : 0u;
+            row[u] = ok[u] ? (rows ? rows[idx] : N.row_off + idx) : 0u;
         }
         longlong2 g[UNROLL];
         uint32_t rec[UNROLL][RD];
@@ -266,10 +268,10 @@ __global__ __launch_bounds__(HIST_TPB) void hist_global_kernel(const HistLaunch 
     const uint32_t r1 = min(r0 + chunk_rows, N.row_len);
     unsigned long long *out = reinterpret_cast<unsigned long long *>(
         L.hist + ((uint64_t)N.slot * L.hist_width + F.hist_off) * 2u);
-    const uint32_t *rows = L.rows + N.row_off;
+    const uint32_t *rows = L.rows ? L.rows + N.row_off : nullptr;
     const longlong2 *gp = reinterpret_cast<const longlong2 *>(L.gpair);
     for (uint32_t i = r0 + threadIdx.x; i < r1; i += HIST_TPB) {
-        const uint32_t row = rows[i];
+        const uint32_t row = rows ? rows[i] : N.row_off + i;
         const longlong2 g = gp[row];
         if ((g.x | g.y) == 0) continue;
         const uint8_t *p = T.data + (size_t)row * T.stride;
@@ -1331,7 +1333,8 @@ __device__ __forceinline__ bool goes_left(const PartReqDev &R, uint32_t row,
     return bin_goes_left(R, cell_of(R, row), cat_words);
 }
 
-// Pass 1: direction flag per row and the left count of every chunk.
+// Pass 1: direction flag per row and the left count of every chunk. A null
+// row arena is the identity (rows in order).
 __global__ __launch_bounds__(PART_TPB) void part_count_kernel(const PartReqDev *reqs,
                                                               uint32_t n_reqs,
                                                               const uint32_t *rows,
@@ -1350,7 +1353,7 @@ __global__ __launch_bounds__(PART_TPB) void part_count_kernel(const PartReqDev *
 #pragma unroll
     for (int r = 0; r < ROUNDS; r++) {
         const uint32_t i = c0 + r * PART_TPB + threadIdx.x;
-        row[r] = i < c1 ? rows[R.row_off + i] : 0u;
+        row[r] = i < c1 ? (rows ? rows[R.row_off + i] : R.row_off + i) : 0u;
     }
 #pragma unroll
     for (int r = 0; r < ROUNDS; r++) {
@@ -1537,7 +1540,7 @@ __global__ __launch_bounds__(PART_TPB) void part_scatter_kernel(const PartReqDev
     for (int r = 0; r < ROUNDS; r++) {
         const uint32_t i = c0 + r * PART_TPB + threadIdx.x;
         const bool valid = i < c1;
-        row[r] = valid ? rows[R.row_off + i] : 0u;
+        row[r] = valid ? (rows ? rows[R.row_off + i] : R.row_off + i) : 0u;
         left_bits |= (valid && flags[R.row_off + i] ? 1u : 0u) << r;
     }
 #pragma unroll
@@ -2084,7 +2087,9 @@ hipError_t launch_gpair_quantize(const float *g2n, uint64_t n, const ScalesDev *
                                  int64_t *out_sum, hipStream_t s) {
     hipLaunchKernelGGL(gpair_quantize_kernel, dim3(n_blocks), dim3(256), 0, s, g2n, n, scales, out,
                        block_sum);
-    hipLaunchKernelGGL(reduce_sum_kernel, dim3(1), dim3(1024), 0, s, block_sum, n_blocks, out_sum);
+    if (out_sum)
+        hipLaunchKernelGGL(reduce_sum_kernel, dim3(1), dim3(1024), 0, s, block_sum, n_blocks,
+                           out_sum);
     return hipGetLastError();
 }
 
@@ -2302,12 +2307,51 @@ hipError_t launch_shap(const ShapNodeDev *nodes, const uint32_t *tree_roots, uin
 // them and plans the partition and the children exactly as the host grower
 // would (build_tree, src/training/mod.rs:3357-4565).
 
-__global__ void grow_init_kernel(GrowParamsDev G, const int64_t *root, uint32_t root_slot,
-                                 LNodeDev *level, SplitNodeDev *root_split, TreeNodeDev *tree,
-                                 GrowState *st) {
-    if (threadIdx.x != 0) return;
+// The root of a device-grown tree. Block 0 takes the root sum (staged from
+// the host, or the wrapping sum of the quantisation's per-block sums) and
+// initialises the state, the root's level node, split node and tree node;
+// every block clears its share of `clear` (the root's histogram slot when it
+// accumulates atomically).
+__global__ __launch_bounds__(1024) void grow_prep_kernel(
+    GrowParamsDev G, const int64_t *root, const int64_t *block_sums, uint32_t n_blocks,
+    uint32_t root_slot, LNodeDev *level, SplitNodeDev *root_split, TreeNodeDev *tree,
+    GrowState *st, int64_t *clear, uint64_t clear_words) {
+    __shared__ int64_t wsum[2][16];
+    if (clear)
+        for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < clear_words;
+             i += (uint64_t)gridDim.x * blockDim.x)
+            clear[i] = 0;
+    if (blockIdx.x != 0) return;
+    int64_t rg, rh;
+    if (block_sums) {
+        uint64_t ag = 0, ah = 0;
+        for (uint32_t i = threadIdx.x; i < n_blocks; i += blockDim.x) {
+            ag += (uint64_t)block_sums[2 * i];
+            ah += (uint64_t)block_sums[2 * i + 1];
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            ag += (uint64_t)__shfl_xor((long long)ag, off, 64);
+            ah += (uint64_t)__shfl_xor((long long)ah, off, 64);
+        }
+        if ((threadIdx.x & 63) == 0) {
+            wsum[0][threadIdx.x >> 6] = (int64_t)ag;
+            wsum[1][threadIdx.x >> 6] = (int64_t)ah;
+        }
+        __syncthreads();
+        if (threadIdx.x != 0) return;
+        ag = ah = 0;
+        for (uint32_t w = 0; w < blockDim.x / 64; w++) {
+            ag += (uint64_t)wsum[0][w];
+            ah += (uint64_t)wsum[1][w];
+        }
+        rg = (int64_t)ag;
+        rh = (int64_t)ah;
+    } else {
+        if (threadIdx.x != 0) return;
+        rg = root[0];
+        rh = root[1];
+    }
     load_scales(G.sp);
-    const int64_t rg = root[0], rh = root[1];
     GrowState s{};
     s.n_level = 1;
     s.tree_size = 1;
@@ -2341,11 +2385,15 @@ __global__ void grow_init_kernel(GrowParamsDev G, const int64_t *root, uint32_t 
     tree[0] = t;
 }
 
-hipError_t launch_grow_init(const GrowParamsDev &G, const int64_t *root, uint32_t root_slot,
-                            LNodeDev *level, SplitNodeDev *root_split, TreeNodeDev *tree,
-                            GrowState *st, hipStream_t s) {
-    hipLaunchKernelGGL(grow_init_kernel, dim3(1), dim3(64), 0, s, G, root, root_slot, level,
-                       root_split, tree, st);
+hipError_t launch_grow_prep(const GrowParamsDev &G, const int64_t *root, const int64_t *block_sums,
+                            uint32_t n_blocks, uint32_t root_slot, LNodeDev *level,
+                            SplitNodeDev *root_split, TreeNodeDev *tree, GrowState *st,
+                            int64_t *clear, uint64_t clear_words, hipStream_t s) {
+    const uint32_t blocks =
+        clear ? (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>((clear_words + 1023) / 1024, 256))
+              : 1u;
+    hipLaunchKernelGGL(grow_prep_kernel, dim3(blocks), dim3(1024), 0, s, G, root, block_sums,
+                       n_blocks, root_slot, level, root_split, tree, st, clear, clear_words);
     return hipGetLastError();
 }
 
