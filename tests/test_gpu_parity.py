@@ -277,6 +277,120 @@ def test_device_grown_trees_match_host_levels_and_oracle(fb, oracle, case):
     assert np.array_equal(host.train_margins(n).view(np.uint32), want)
 
 
+class _TreeNode(C.Structure):
+    _fields_ = [("feat", C.c_uint32), ("bin", C.c_uint32), ("left", C.c_int32),
+                ("right", C.c_int32), ("leaf_value", C.c_float), ("sum_hess", C.c_float),
+                ("gain", C.c_float), ("flags", C.c_uint32), ("cat_offset", C.c_uint32),
+                ("n_cat_words", C.c_uint32), ("reserved", C.c_uint32 * 2)]
+
+
+class _GrowParams(C.Structure):
+    _fields_ = [("max_depth", C.c_uint32), ("max_leaves", C.c_uint32),
+                ("learning_rate", C.c_float), ("reserved", C.c_uint32)]
+
+
+@pytest.mark.parametrize("tile_bytes", [0, 4096])
+def test_device_grown_tree_from_host_pairs_matches_oracle_splits(N, oracle, tile_bytes):
+    """A whole tree grown through the C ABI from fixed-point pairs the host
+    quantized (no device objective: leaves land in the prediction delta),
+    against a depthwise grower built from the oracle's histogram, split and
+    partition: every split (feature, bin, missing direction, gain bit for
+    bit), the children's Hessian sums, node numbering, and each row's delta
+    equal to the value of the leaf the oracle's partitions put it in. With
+    4 KiB tiles the five features share one row bundle and the leaves come
+    from the row-order walk; with the default tile they come from the leaf
+    spans."""
+    rng = np.random.default_rng(77 + tile_bytes)
+    n, nf, nb, depth = 20_011, 5, 41, 4
+    bins = rng.integers(0, nb, size=(nf, n)).astype(np.uint8)
+    bins[rng.random((nf, n)) < 0.05] = 0xFF
+    g = rng.integers(-(1 << 30), 1 << 30, size=n)
+    g += (bins[0].astype(np.int64) - nb // 2) << 26  # make feature 0 informative
+    h = rng.integers(1, 1 << 30, size=n)
+    fixed = np.stack([g, h], axis=1).reshape(-1).astype(np.int64)
+    scales = np.array([2.0 ** 24, 2.0 ** 26])
+    offsets = np.arange(nf + 1, dtype=np.uint32) * nb
+    feat_ids = np.arange(nf, dtype=np.uint32)
+    lam, mcw, eta = 1.0, 0.5, 0.3
+    op = oracle.make_params(**{"lambda": lam, "gamma": 0.0, "min_child_weight": mcw})
+
+    # The oracle's depthwise tree: levels in order, children ids tree_size + 2s.
+    want = {}  # node id -> (feat, bin, missing_left, gain bits, left id, right id)
+    leaf_rows = {}
+    level = [(0, np.arange(n, dtype=np.uint32), np.array([g.sum(), h.sum()], np.int64))]
+    size = 1
+    for d in range(depth):
+        nxt = []
+        for node, rows, ssum in level:
+            sp = None
+            if rows.size:
+                hist = oracle.hist_build(bins, offsets, fixed, rows)
+                sp = oracle.best_split(hist, feat_ids, offsets, ssum, scales, op)
+            if sp is None or not sp.found:
+                leaf_rows[node] = rows
+                continue
+            out, nl = oracle.partition(rows, bins[sp.feat], sp.bin, bool(sp.missing_left))
+            lid, rid = size, size + 1
+            size += 2
+            want[node] = (sp.feat, sp.bin, bool(sp.missing_left),
+                          np.float32(sp.gain).view(np.uint32), lid, rid,
+                          np.array(sp.left, np.int64), np.array(sp.right, np.int64))
+            nxt.append((lid, out[:nl], np.array(sp.left, np.int64)))
+            nxt.append((rid, out[nl:], np.array(sp.right, np.int64)))
+        level = nxt
+    for node, rows, _ in level:
+        leaf_rows[node] = rows
+
+    L = N.hip()
+    width = np.ones(nf, np.uint8)
+    nbins = np.full(nf, nb, np.uint32)
+    shape = N.Shape(nf, N.ptr(width), N.ptr(nbins), None)
+    cfg = N.Config()
+    cfg.tile_bytes = tile_bytes
+    ctx = C.c_void_p()
+    N.check_hip(L.fbh_ctx_create(0, n, C.byref(shape), C.byref(cfg), C.byref(ctx)))
+    try:
+        N.check_hip(L.fbh_upload_block(ctx, N.ptr(feat_ids), nf, 1, N.ptr(np.ascontiguousarray(bins))))
+        N.check_hip(L.fbh_upload_gpair_fixed(ctx, N.ptr(fixed), N.ptr(scales)))
+        root = N.Span()
+        N.check_hip(L.fbh_begin_tree(ctx, None, 0, None, 0, C.byref(root)))
+        sp = N.SplitParams()
+        sp.lambda_, sp.gamma, sp.min_child_weight = lam, 0.0, mcw
+        gp = _GrowParams(depth, 0, eta, 0)
+        cap = (2 << depth) - 1
+        nodes = (_TreeNode * cap)()
+        vals = np.zeros(1 << depth, np.float32)
+        cats = np.zeros(1, np.uint64)
+        nn, nlv = C.c_uint32(), C.c_uint32()
+        root_sum = np.array([g.sum(), h.sum()], np.int64)
+        N.check_hip(L.fbh_grow_depthwise(ctx, C.byref(gp), C.byref(sp), N.ptr(root_sum), nodes,
+                                         C.c_uint32(cap), C.byref(nn), N.ptr(cats), C.c_uint32(1),
+                                         N.ptr(vals), C.c_uint32(vals.size), C.byref(nlv)))
+        delta = np.empty(n, np.float32)
+        N.check_hip(L.fbh_download_delta(ctx, N.ptr(delta)))
+    finally:
+        L.fbh_ctx_destroy(ctx)
+
+    assert nn.value == size
+    assert want, "the oracle tree has no split"
+    inv_h = 1.0 / scales[1]
+    for node in range(size):
+        t = nodes[node]
+        if node in want:
+            f, b, ml, gain, lid, rid, ls, rs = want[node]
+            assert (t.flags & 1) == 0, node
+            assert (t.feat, t.bin, bool(t.flags & 2)) == (f, b, ml), node
+            assert np.float32(t.gain).view(np.uint32) == gain, node
+            assert (t.left, t.right) == (lid, rid), node
+            assert np.float32(nodes[lid].sum_hess) == np.float32(ls[1] * inv_h), node
+            assert np.float32(nodes[rid].sum_hess) == np.float32(rs[1] * inv_h), node
+        else:
+            assert t.flags & 1, node
+            rows = leaf_rows[node]
+            assert np.all(delta[rows].view(np.uint32) == np.float32(t.leaf_value).view(np.uint32)), node
+    assert sum(r.size for r in leaf_rows.values()) == n
+
+
 @pytest.mark.parametrize("host_levels", [False, True])
 def test_nonfinite_gradients_stop_training(fb, host_levels):
     """Gradients that overflow f32 (labels near the f32 maximum times a
