@@ -2421,9 +2421,19 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
     const uint32_t n = S0.n_level;
     const uint32_t per = (n + 1023) / 1024;
     const uint32_t i0 = min(tid * per, n), i1 = min(i0 + per, n);
+    // With at most 1024 nodes each thread's packet and node stay in
+    // registers for every pass.
+    SplitPacketDev myP{};
+    LNodeDev myL{};
+    if (per == 1 && i0 < n) {
+        myP = pk[i0];
+        myL = level[i0];
+    }
+    auto pk_at = [&](uint32_t i) -> SplitPacketDev { return per == 1 ? myP : pk[i]; };
+    auto lv_at = [&](uint32_t i) -> LNodeDev { return per == 1 ? myL : level[i]; };
 
     uint32_t nf = 0;
-    for (uint32_t i = i0; i < i1; i++) nf += pk[i].found ? 1u : 0u;
+    for (uint32_t i = i0; i < i1; i++) nf += pk_at(i).found ? 1u : 0u;
     uint32_t tot_found;
     const uint32_t f_before = block_scan_1024(nf, buf, tot_found);
     uint32_t remaining = 0xFFFFFFFFu;
@@ -2438,15 +2448,19 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
     {
         uint32_t fr = f_before;
         for (uint32_t i = i0; i < i1; i++) {
-            const bool found = pk[i].found != 0;
-            if (found && fr < n_split) nc += (level[i].row_len + PART_CHUNK - 1) / PART_CHUNK;
-            else if (level[i].row_len) nl++;
+            const bool found = pk_at(i).found != 0;
+            const uint32_t len = lv_at(i).row_len;
+            if (found && fr < n_split) nc += (len + PART_CHUNK - 1) / PART_CHUNK;
+            else if (len) nl++;
             if (found) fr++;
         }
     }
-    uint32_t tot_leaves, tot_chunks;
-    const uint32_t l_before = block_scan_1024(nl, buf, tot_leaves);
-    const uint32_t c_before = block_scan_1024(nc, buf, tot_chunks);
+    // Leaves (low half) and partition chunks (high half) in one scan.
+    __shared__ uint64_t buf64[32];
+    uint64_t both_total;
+    const uint64_t both = block_scan_u64((uint64_t)nl | ((uint64_t)nc << 32), buf64, both_total);
+    const uint32_t tot_leaves = (uint32_t)both_total, tot_chunks = (uint32_t)(both_total >> 32);
+    const uint32_t l_before = (uint32_t)both, c_before = (uint32_t)(both >> 32);
 
     bool slots_short = false;
     if (evaluated) {
@@ -2455,8 +2469,9 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
         __syncthreads();
         uint32_t fr = f_before;
         for (uint32_t i = i0; i < i1; i++) {
-            if (!pk[i].found) continue;
-            if (fr < n_split) atomicOr(&held[level[i].slot >> 5], 1u << (level[i].slot & 31));
+            if (!pk_at(i).found) continue;
+            const uint32_t slot = lv_at(i).slot;
+            if (fr < n_split) atomicOr(&held[slot >> 5], 1u << (slot & 31));
             fr++;
         }
         __syncthreads();
@@ -2477,8 +2492,8 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
 
     uint32_t fr = f_before, lr = l_before, cb = c_before;
     for (uint32_t i = i0; i < i1; i++) {
-        const SplitPacketDev P = pk[i];
-        const LNodeDev L = level[i];
+        const SplitPacketDev P = pk_at(i);
+        const LNodeDev L = lv_at(i);
         const bool split = P.found && fr < n_split;
         if (split) {
             const uint32_t s = fr;
@@ -2693,6 +2708,8 @@ __global__ __launch_bounds__(256) void tree_leaves_kernel(
             rec[4 * q + 2] = v.z;
             rec[4 * q + 3] = v.w;
         }
+        // The margin's load is issued before the walk, its use after.
+        const float m = IDB ? margin[r] : 0.0f;
         uint32_t node = 0;
         ushort4 nd = s_node[0];
         while (!(nd.x & 0x80u)) {
@@ -2721,7 +2738,7 @@ __global__ __launch_bounds__(256) void tree_leaves_kernel(
         } else {
             if (IDB == 1) static_cast<uint8_t *>(ids)[r] = (uint8_t)s_leaf[node];
             else static_cast<uint16_t *>(ids)[r] = s_leaf[node];
-            margin[r] = margin[r] + s_val[node];
+            margin[r] = m + s_val[node];
         }
     }
 }
