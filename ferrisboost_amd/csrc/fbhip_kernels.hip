@@ -1510,14 +1510,17 @@ __global__ __launch_bounds__(PART_TPB) void part_scatter_kernel(const PartReqDev
                                                                 const uint32_t *dev,
                                                                 ZeroNodesDev Z) {
     if (Z.hist) {
+        // Node by node, so the words of slots that need no clearing are never visited.
         const uint64_t W = Z.width * 2u;
-        const uint64_t all = (uint64_t)*Z.dev_n * W;
-        for (uint64_t k = (uint64_t)blockIdx.x * PART_TPB + threadIdx.x; k < all;
-             k += (uint64_t)gridDim.x * PART_TPB) {
-            const uint64_t e = k / W;
+        const uint32_t nn = *Z.dev_n;
+        for (uint32_t e = 0; e < nn; e++) {
             const HistNodeDev N = Z.nodes[e];
             const bool clear = Z.group ? N.n_chunks > Z.group : (Z.force || N.n_chunks != 1);
-            if (clear) Z.hist[(uint64_t)N.slot * W + (k - e * W)] = 0;
+            if (!clear) continue;
+            int64_t *slot = Z.hist + (uint64_t)N.slot * W;
+            for (uint64_t k = (uint64_t)blockIdx.x * PART_TPB + threadIdx.x; k < W;
+                 k += (uint64_t)gridDim.x * PART_TPB)
+                slot[k] = 0;
         }
     }
     const uint32_t chunk = blockIdx.x;
