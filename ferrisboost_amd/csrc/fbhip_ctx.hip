@@ -79,6 +79,8 @@ uint32_t round_stride(uint32_t bytes) {
 }
 
 constexpr uint32_t MAX_RECORD_BYTES = 64;
+// Largest per-chunk partial histogram buffer.
+constexpr uint64_t MAX_PARTIAL_BYTES = 256ull << 20;
 constexpr uint32_t MAX_NODES = 16384;      // nodes of one eval / partition call
 constexpr uint32_t DEFAULT_TILE_BYTES = 64 * 1024;
 // Rows per histogram workgroup: chosen per launch so that the launch makes
@@ -176,6 +178,8 @@ struct fbh_ctx {
     float *delta = nullptr;
     int64_t *hist = nullptr;
     ScalesDev *d_scales = nullptr;  // scales of the current gradients
+    int64_t *partials = nullptr;    // per-chunk partial histograms
+    uint64_t partial_bytes = 0;
     // The row arena of a new tree is the identity; it is written out only
     // when something reads it (a device-grown tree walks the root without it).
     bool rows_identity = false;
@@ -214,8 +218,6 @@ struct fbh_ctx {
         float *leaf_vals = nullptr;
         DevColumn *cols = nullptr;
         uint16_t *feat_off = nullptr;  // byte offset of each feature in the row bundle (leaf walk)
-        int64_t *partials = nullptr;   // per-chunk partial histograms
-        uint64_t partial_bytes = 0;
         // The root's accumulation table (offset 0) and the monotone
         // constraints (offset 256) on the device, with the host copies they
         // were last uploaded from.
@@ -371,6 +373,24 @@ struct fbh_ctx {
         return static_cast<T *>(p);
     }
 
+    // Frees a buffer alloc() made, once the stream has finished with it.
+    void release_alloc(void *p) {
+        if (!p) return;
+        sync();
+        for (size_t i = 0; i < allocs.size(); i++)
+            if (allocs[i].p == p) {
+                (void)hipFree(p);
+                device_bytes -= allocs[i].bytes;
+                allocs.erase(allocs.begin() + (long)i);
+                return;
+            }
+    }
+
+    // Per-chunk partial histograms (see HistLaunch::partials) of `bytes`, or
+    // NULL when a launch cannot use them (global or streamed tiles) or they
+    // would exceed MAX_PARTIAL_BYTES; grown on demand.
+    int64_t *partial_buffer(uint64_t bytes);
+
     void pinned(PinnedBuf &b, size_t bytes) {
         check(hipHostMalloc(&b.p, bytes, hipHostMallocDefault), "pinned host allocation");
         b.bytes = bytes;
@@ -473,6 +493,16 @@ struct fbh_ctx {
         ev_used = keep;
     }
 };
+
+int64_t *fbh_ctx::partial_buffer(uint64_t bytes) {
+    if (has_global || !streamed.empty() || bytes > MAX_PARTIAL_BYTES) return nullptr;
+    if (bytes > partial_bytes) {
+        release_alloc(partials);
+        partials = alloc<int64_t>(bytes / 8 + 1, "partial histograms");
+        partial_bytes = bytes;
+    }
+    return partials;
+}
 
 void fbh_ctx::ensure_rows() {
     if (!rows_identity) return;
@@ -1438,7 +1468,8 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
     if (!E.cleared) {
         if (E.dev_chunk_rows)
             check(launch_zero_nodes(c->hist, c->hist_width, E.hn, E.n_hn, E.dev_n_hn,
-                                    c->has_global || !c->streamed.empty(), c->stream),
+                                    c->has_global || !c->streamed.empty(),
+                                    E.partials ? REDUCE_GROUP : 0u, c->stream),
                   "histogram clear");
         else
             check(launch_zero_slots(c->hist, c->hist_width, E.zero_slots, E.n_zero, c->stream),
@@ -1633,13 +1664,22 @@ std::pair<uint64_t, uint64_t> stage_host_eval(fbh_ctx *c, const fbh_node *nodes,
                 acc_lens.push_back(nodes[i].rows.len);
             }
         const uint32_t chunk_rows = c->chunk_rows_for(acc_lens.data(), acc_lens.size());
+        uint64_t all_chunks = 0;
+        for (uint32_t i = 0; i < n; i++)
+            if (nodes[i].subtract_parent < 0) all_chunks += div_up(nodes[i].rows.len, chunk_rows);
+        // Multi-chunk nodes store per-chunk partials (summed by the chunk
+        // reduction) when the buffer allows; only nodes of more than
+        // REDUCE_GROUP chunks, or without rows, then need a zeroed slot.
+        E.partials = c->partial_buffer(all_chunks * c->hist_width * 16);
+        uint32_t groups = 0;
         for (uint32_t i = 0; i < n; i++) {
             const fbh_node &nd = nodes[i];
             if (nd.subtract_parent >= 0) continue;
             const uint32_t nc = div_up(nd.rows.len, chunk_rows);
             // Single-chunk nodes are written by plain stores, except that a
             // globally accumulated feature needs a zeroed slot.
-            if (nc != 1 || c->has_global || !c->streamed.empty()) zero_slots.push_back(nd.slot);
+            const bool atomic = E.partials ? (nc == 0 || nc > REDUCE_GROUP) : nc != 1;
+            if (atomic || c->has_global || !c->streamed.empty()) zero_slots.push_back(nd.slot);
             if (nc == 0) continue;
             HistNodeDev h{};
             h.row_off = nd.rows.offset;
@@ -1647,9 +1687,12 @@ std::pair<uint64_t, uint64_t> stage_host_eval(fbh_ctx *c, const fbh_node *nodes,
             h.chunk_begin = chunks;
             h.slot = nd.slot;
             h.n_chunks = nc;
+            h.group_begin = groups;
             hn.push_back(h);
             chunks += nc;
+            groups += reduce_groups(nc);
         }
+        E.max_groups = groups;
         std::vector<uint32_t> triples;
         for (uint32_t i = 0; i < n; i++) {
             const fbh_node &nd = nodes[i];
@@ -1967,6 +2010,8 @@ int fbh_partition_eval(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
             E.n_hn = n_eval;
             E.grid_chunks = (uint32_t)(rule.fixed ? bound_min : std::min(bound_rule, bound_min));
             E.dev_chunk_rows = c->d_lvl_rows;
+            E.partials = c->partial_buffer((uint64_t)E.grid_chunks * c->hist_width * 16);
+            E.max_groups = E.grid_chunks / REDUCE_GROUP + n_eval + 1;
             E.triples = S.dev<const uint32_t>(o_tri);
             E.n_tri = n_eval;
             E.sn = c->d_lvl_split;
@@ -2001,8 +2046,7 @@ int fbh_partition_eval(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
 namespace {
 
 constexpr uint32_t MAX_GROW_DEPTH = 14;
-// Largest per-chunk partial histogram buffer of a device-grown tree.
-constexpr uint64_t MAX_PARTIAL_BYTES = 256ull << 20;
+
 
 // Every tile's records in one row bundle: a row's cells for every feature
 // are in one record, so leaves can be found by walking the tree in row order.
@@ -2149,15 +2193,7 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     uint64_t all_bins = 0;
     for (uint32_t b : c->n_bins) all_bins += b;
     const uint64_t max_grid = std::max<uint64_t>(h.n_chunks, level_grid(lvl_bound(D - 1)));
-    const uint64_t partial_bytes = max_grid * all_bins * 16;
-    int64_t *partials = nullptr;
-    if (!c->has_global && partial_bytes <= MAX_PARTIAL_BYTES) {
-        if (GB.partial_bytes < partial_bytes) {
-            GB.partials = c->alloc<int64_t>(partial_bytes / 8, "partial histograms");
-            GB.partial_bytes = partial_bytes;
-        }
-        partials = GB.partials;
-    }
+    int64_t *partials = c->partial_buffer(max_grid * all_bins * 16);
     E0.partials = partials;
     E0.max_groups = reduce_groups(h.n_chunks);
     const bool root_atomic = partials ? h.n_chunks > REDUCE_GROUP : h.n_chunks != 1;

@@ -303,7 +303,7 @@ hipError_t launch_subtract(int64_t *hist, uint64_t width, const uint32_t *triple
 // Zero the slots of accumulated nodes that need it: all when force, else
 // those not written by plain stores (n_chunks != 1).
 hipError_t launch_zero_nodes(int64_t *hist, uint64_t width, const HistNodeDev *nodes, uint32_t n,
-                             const uint32_t *dev_n, bool force, hipStream_t s);
+                             const uint32_t *dev_n, bool force, uint32_t group, hipStream_t s);
 // Device plan of a fused step: children spans (2 per pair) and the left
 // child's slot per pair, the accumulated nodes (one per evaluated pair, in
 // pair order), the split-scan nodes (left, right per evaluated pair) and

@@ -433,11 +433,14 @@ hipError_t launch_subtract(int64_t *hist, uint64_t width, const uint32_t *triple
     return hipGetLastError();
 }
 
+// group nonzero: per-chunk partials; only nodes of more chunks than that
+// accumulate atomically. Otherwise every node of several (or no) chunks.
 __global__ void zero_nodes_kernel(int64_t *hist, uint64_t width, const HistNodeDev *nodes,
-                                  const uint32_t *dev_n, bool force) {
+                                  const uint32_t *dev_n, bool force, uint32_t group) {
     if (dev_n && blockIdx.y >= *dev_n) return;
     const HistNodeDev N = nodes[blockIdx.y];
-    if (!force && N.n_chunks == 1) return;  // written by plain stores
+    const bool clear = group ? N.n_chunks > group : (force || N.n_chunks != 1);
+    if (!clear) return;  // written by plain stores
     int64_t *base = hist + (uint64_t)N.slot * width * 2u;
     const uint64_t n = width * 2u;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -446,11 +449,11 @@ __global__ void zero_nodes_kernel(int64_t *hist, uint64_t width, const HistNodeD
 }
 
 hipError_t launch_zero_nodes(int64_t *hist, uint64_t width, const HistNodeDev *nodes, uint32_t n,
-                             const uint32_t *dev_n, bool force, hipStream_t s) {
+                             const uint32_t *dev_n, bool force, uint32_t group, hipStream_t s) {
     if (n == 0) return hipSuccess;
     uint32_t bx = (uint32_t)std::min<uint64_t>((width * 2 + 255) / 256, 1024);
     hipLaunchKernelGGL(zero_nodes_kernel, dim3(bx, n), dim3(256), 0, s, hist, width, nodes, dev_n,
-                       force);
+                       force, group);
     return hipGetLastError();
 }
 
