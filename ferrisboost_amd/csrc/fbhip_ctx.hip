@@ -91,6 +91,10 @@ constexpr uint32_t MIN_CHUNK_ROWS = 4096;
 // upload of different chunks overlap).
 constexpr int EXCHANGE_CHUNKS = 8;
 constexpr uint32_t HIST_WAVES = 1;
+// Host-driven evaluations (lossguide expansions, host levels) accumulate
+// fewer rows per launch; two waves of workgroups measured faster there
+// (wide-bin lossguide: 107 against 99 rounds/s).
+constexpr uint32_t HOST_HIST_WAVES = 2;
 
 struct DeviceBuf {
     void *p = nullptr;
@@ -120,6 +124,7 @@ struct fbh_ctx {
     uint32_t fixed_chunk_rows = 0;  // nonzero: rows per workgroup forced by the caller
     uint32_t hist_tpb = 256;        // histogram threads per workgroup
     uint32_t hist_waves = HIST_WAVES;
+    uint32_t host_hist_waves = HOST_HIST_WAVES;
     uint32_t n_cus = 256;
     uint32_t n_slots = 0;
     uint32_t max_cat_words = 0;
@@ -429,7 +434,7 @@ struct fbh_ctx {
     // enough chunks for hist_waves full waves of workgroups over all tiles
     // (occupancy bounded by LDS and by 2048 threads per CU), so that each
     // workgroup flushes its LDS histogram once per many rows.
-    ChunkRule chunk_rule() const {
+    ChunkRule chunk_rule(bool host = false) const {
         ChunkRule R{fixed_chunk_rows, 1, MIN_CHUNK_ROWS, 1u << 24};
         uint64_t n_tiles = 0, lds_max = 0;
         for (const auto &g : groups) {
@@ -439,7 +444,7 @@ struct fbh_ctx {
         if (n_tiles == 0) return R;
         uint64_t per_cu = lds_max ? (160u * 1024u) / lds_max : 8;
         per_cu = std::max<uint64_t>(1, std::min<uint64_t>(per_cu, 2048 / hist_tpb));
-        const uint64_t wgs = (uint64_t)n_cus * per_cu * hist_waves;
+        const uint64_t wgs = (uint64_t)n_cus * per_cu * (host ? host_hist_waves : hist_waves);
         R.want_chunks = (uint32_t)std::max<uint64_t>(1, wgs / n_tiles);
         return R;
     }
@@ -447,8 +452,8 @@ struct fbh_ctx {
     // multiple of 1024 whose chunks (ceil(len / rows) per node) fit one wave
     // of workgroups, so no launch runs a second, mostly idle wave; with more
     // nodes than the wave holds, rows / want_chunks rounded up.
-    uint32_t chunk_rows_for(const uint32_t *lens, size_t n) const {
-        const ChunkRule R = chunk_rule();
+    uint32_t chunk_rows_for(const uint32_t *lens, size_t n, bool host = false) const {
+        const ChunkRule R = chunk_rule(host);
         if (R.fixed) return R.fixed;
         uint64_t acc = 0, nz = 0;
         for (size_t i = 0; i < n; i++) {
@@ -826,6 +831,8 @@ fbh_config configure(fbh_ctx &c, uint64_t n_rows, const fbh_shape *shape, const 
     c.fixed_chunk_rows = (uint32_t)env_u64("FB_HIP_CHUNK_ROWS", conf.rows_per_block);
     c.hist_tpb = (uint32_t)env_u64("FB_HIP_HIST_TPB", 256);
     c.hist_waves = (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HIST_WAVES", HIST_WAVES));
+    c.host_hist_waves =
+        (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HOST_HIST_WAVES", HOST_HIST_WAVES));
     if (c.tile_bytes < 4096 || c.tile_bytes > 160 * 1024)
         throw InputError("tile_bytes must be in 4096..=163840");
     if (c.fixed_chunk_rows && (c.fixed_chunk_rows < 256 || c.fixed_chunk_rows % 256))
@@ -1462,6 +1469,7 @@ struct EvalPlan {
     // slots; max_groups bounds the reduction groups of the launch.
     int64_t *partials = nullptr;
     uint32_t max_groups = 0;
+    bool host_rule = false;  // planned with the host-driven chunk rule (HOST_HIST_WAVES)
 };
 
 void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
@@ -1502,7 +1510,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
             L.dev_chunk_rows = E.dev_chunk_rows;
             L.chunk_groups = div_up(E.grid_chunks, XCDS);
             // Chunk-major XCD locality needs at least one chunk per XCD.
-            L.linear = c->chunk_rule().want_chunks < XCDS ? 1u : 0u;
+            L.linear = c->chunk_rule(E.host_rule).want_chunks < XCDS ? 1u : 0u;
             L.rows = E.identity ? nullptr : (E.rows ? E.rows : c->rows);
             L.gpair = c->gpair;
             L.hist = c->hist;
@@ -1663,7 +1671,8 @@ std::pair<uint64_t, uint64_t> stage_host_eval(fbh_ctx *c, const fbh_node *nodes,
                 acc_rows += nodes[i].rows.len;
                 acc_lens.push_back(nodes[i].rows.len);
             }
-        const uint32_t chunk_rows = c->chunk_rows_for(acc_lens.data(), acc_lens.size());
+        const uint32_t chunk_rows = c->chunk_rows_for(acc_lens.data(), acc_lens.size(), true);
+        E.host_rule = true;
         uint64_t all_chunks = 0;
         for (uint32_t i = 0; i < n; i++)
             if (nodes[i].subtract_parent < 0) all_chunks += div_up(nodes[i].rows.len, chunk_rows);
@@ -1970,7 +1979,7 @@ int fbh_partition_eval(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
         const PartStage P = stage_partition(c, reqs, n, cat_words, n_cat_words, S);
         std::vector<PairDev> pd(n);
         std::vector<uint32_t> triples;
-        const ChunkRule rule = c->chunk_rule();
+        const ChunkRule rule = c->chunk_rule(true);
         uint64_t bound_rule = rule_chunk_bound(rule, c->n_rows, n_eval);
         uint64_t bound_min = 0;  // the smaller child holds at most half its parent's rows
         uint32_t e = 0;
@@ -2012,6 +2021,7 @@ int fbh_partition_eval(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
             E.dev_chunk_rows = c->d_lvl_rows;
             E.partials = c->partial_buffer((uint64_t)E.grid_chunks * c->hist_width * 16);
             E.max_groups = E.grid_chunks / REDUCE_GROUP + n_eval + 1;
+            E.host_rule = true;
             E.triples = S.dev<const uint32_t>(o_tri);
             E.n_tri = n_eval;
             E.sn = c->d_lvl_split;
