@@ -360,14 +360,6 @@ hipError_t launch_partition_level(const PartReqDev *reqs, const uint32_t *dev, u
 hipError_t launch_partition_count(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
                                   const uint32_t *rows, uint8_t *flags, uint32_t *chunk_counts,
                                   const uint64_t *cat_words, hipStream_t s);
-// Count, scan and stable scatter over requests planned on the device: dev =
-// {requests, chunks}; grid_chunks is an upper bound of the chunks. The
-// children land in rows_out at their parents' positions (no copy back: the
-// arenas alternate by level).
-hipError_t launch_partition_dev(const PartReqDev *reqs, const uint32_t *dev, uint32_t grid_chunks,
-                                const uint32_t *rows_in, uint32_t *rows_out, uint8_t *flags,
-                                uint32_t *counts, uint32_t *excl, uint32_t *totals,
-                                const uint64_t *cat_words, hipStream_t s);
 // Passes 2-4 (scan, stable scatter, copy back) over all requests of the call.
 hipError_t launch_partition_finish(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
                                    uint32_t *rows, uint32_t *tmp, const uint8_t *flags,

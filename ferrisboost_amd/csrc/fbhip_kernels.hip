@@ -1598,20 +1598,6 @@ hipError_t launch_partition_count(const PartReqDev *reqs, uint32_t n_reqs, uint3
     return hipGetLastError();
 }
 
-hipError_t launch_partition_dev(const PartReqDev *reqs, const uint32_t *dev, uint32_t grid_chunks,
-                                const uint32_t *rows_in, uint32_t *rows_out, uint8_t *flags,
-                                uint32_t *counts, uint32_t *excl, uint32_t *totals,
-                                const uint64_t *cat_words, hipStream_t s) {
-    if (grid_chunks == 0) return hipSuccess;
-    hipLaunchKernelGGL(part_count_kernel, dim3(grid_chunks), dim3(PART_TPB), 0, s, reqs, 0u,
-                       rows_in, flags, counts, cat_words, dev);
-    hipLaunchKernelGGL(part_scan_kernel, dim3(1), dim3(1024), 0, s, counts, 0u, excl, reqs, 0u,
-                       totals, dev);
-    hipLaunchKernelGGL(part_scatter_kernel, dim3(grid_chunks), dim3(PART_TPB), 0, s, reqs, 0u,
-                       rows_in, flags, excl, totals, rows_out, dev, ZeroNodesDev{});
-    return hipGetLastError();
-}
-
 hipError_t launch_partition_level(const PartReqDev *reqs, const uint32_t *dev, uint32_t grid_chunks,
                                   const uint32_t *rows_in, uint32_t *rows_out, uint8_t *flags,
                                   uint32_t *counts, uint32_t *excl, uint32_t *totals,
