@@ -392,8 +392,9 @@ struct fbh_ctx {
     }
 
     // Per-chunk partial histograms (see HistLaunch::partials) of `bytes`, or
-    // NULL when a launch cannot use them (global or streamed tiles) or they
-    // would exceed MAX_PARTIAL_BYTES; grown on demand.
+    // NULL when a launch cannot use them (global or streamed tiles), they
+    // would exceed MAX_PARTIAL_BYTES or the memory budget has no room left
+    // for them; grown on demand. Without them launches flush with atomics.
     int64_t *partial_buffer(uint64_t bytes);
 
     void pinned(PinnedBuf &b, size_t bytes) {
@@ -501,6 +502,9 @@ struct fbh_ctx {
 
 int64_t *fbh_ctx::partial_buffer(uint64_t bytes) {
     if (has_global || !streamed.empty() || bytes > MAX_PARTIAL_BYTES) return nullptr;
+    // Outside the memory plan: only within the budget's remaining room.
+    if (bytes > partial_bytes && device_bytes - partial_bytes + bytes + 256 > plan.budget)
+        return nullptr;
     if (bytes > partial_bytes) {
         release_alloc(partials);
         partials = alloc<int64_t>(bytes / 8 + 1, "partial histograms");
