@@ -1187,6 +1187,19 @@ int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th
             c->leaves_pending = false;
         }
         const float *w = c->has_weights ? c->gweights : nullptr;
+        if (!scales_out) {
+            // Everything stays on the device: the pairs are quantized in the
+            // gradient pass under the previous round's scales and redone only
+            // if this round's bounds give other scales.
+            check(launch_gradient_spec(c->margin, c->labels, w, c->n_rows,
+                                       c->objective == 0 ? 0 : 2, th, seed, tree, c->red_f64,
+                                       c->n_red_blocks, c->d_scales, c->gpair, c->red_i64,
+                                       c->stream),
+                  "device gradient");
+            c->ids_fresh = false;
+            c->root_on_device = true;
+            return;
+        }
         if (c->objective == 0 || !fn) {
             // Squared error, or logistic with the device sigmoid.
             check(launch_gradient(c->margin, c->labels, w, c->n_rows, c->objective == 0 ? 0 : 2,

@@ -112,6 +112,8 @@ struct ScalesDev {
     double max_abs[2];  // the bounds they come from (0 when set from the host)
     uint32_t status;    // 0: valid; 1: non-finite or negative bounds
     uint32_t from_host; // 1: set from the host (no bounds)
+    uint32_t spec_miss; // 1: a speculative gradient pass used other scales
+    uint32_t pad;
 };
 
 struct SplitParamsDev {
@@ -388,6 +390,14 @@ hipError_t launch_sigmoid_checksum(uint64_t begin, uint64_t end, unsigned long l
                                    hipStream_t s);
 hipError_t launch_fill_f32(float *p, float v, uint64_t n, hipStream_t s);
 hipError_t launch_init_rows(uint32_t *rows, float *delta, uint64_t n, hipStream_t s);
+// The gradients of a round quantized in the same pass under the previous
+// round's scales (still in `scales`), then the bounds and this round's
+// scales, then a pass that recomputes the pairs only if the scales changed:
+// fixed-point pairs and block sums as gpair_quantize would give.
+hipError_t launch_gradient_spec(const float *src, const float *y, const float *w, uint64_t n,
+                                int mode, uint64_t th, uint64_t seed, uint64_t tree,
+                                double *block_max, uint32_t n_blocks, ScalesDev *scales,
+                                int64_t *fixed, int64_t *block_sum, hipStream_t s);
 hipError_t launch_gpair_maxabs(float *g2n, uint64_t n, uint64_t threshold, uint64_t seed,
                                uint64_t tree, double *block_max, uint32_t n_blocks,
                                hipStream_t s);

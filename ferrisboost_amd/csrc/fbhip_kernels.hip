@@ -1724,15 +1724,31 @@ __device__ __forceinline__ bool row_selected(uint64_t row, uint64_t th, uint64_t
 __device__ __forceinline__ double finite_abs(float v);
 __device__ void block_max2(double mg, double mh, double *block_max);
 
+__device__ __forceinline__ int64_t sat_i64(double x);
+__device__ void block_sum2(uint64_t ag, uint64_t ah, int64_t *block_sum);
+
 // block_max set: rows outside the round's subsample get a zero pair, and
 // each block's max |g|, max |h| goes to block_max (the bounds pass fused in).
+// spec set: instead of the f32 pairs, the fixed-point pairs under the scales
+// in spec (the previous round's) go to fixed, with the block sums; the bounds
+// pass then tells whether those were this round's scales
+// (gradient_fixup_kernel redoes the pairs when not). The same grid and
+// operations as without spec, so each row's g and h are the same floats.
 __global__ __launch_bounds__(256) void gradient_kernel(const float *src, const float *y,
                                                        const float *w, uint64_t n, int mode,
                                                        float *g2n, uint64_t th, uint64_t seed,
-                                                       uint64_t tree, double *block_max) {
+                                                       uint64_t tree, double *block_max,
+                                                       const ScalesDev *spec, int64_t *fixed,
+                                                       int64_t *block_sum) {
     // Four rows a thread per step (loads of all four first).
     constexpr int U = 4;
     double mg = 0.0, mh = 0.0;
+    uint64_t ag = 0, ah = 0;
+    double sg = 0.0, sh = 0.0;
+    if (spec) {
+        sg = spec->scale[0];
+        sh = spec->scale[1];
+    }
     const uint64_t S = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t base = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; base < n;
          base += U * S) {
@@ -1761,10 +1777,67 @@ __global__ __launch_bounds__(256) void gradient_kernel(const float *src, const f
                 mg = fmax(mg, finite_abs(g));
                 mh = fmax(mh, finite_abs(h));
             }
-            reinterpret_cast<float2 *>(g2n)[i] = make_float2(g, h);
+            if (spec) {
+                const int64_t qg = sat_i64(round((double)g * sg));
+                const int64_t qh = sat_i64(round((double)h * sh));
+                reinterpret_cast<longlong2 *>(fixed)[i] = make_longlong2(qg, qh);
+                ag += (uint64_t)qg;
+                ah += (uint64_t)qh;
+            } else {
+                reinterpret_cast<float2 *>(g2n)[i] = make_float2(g, h);
+            }
         }
     }
     if (block_max) block_max2(mg, mh, block_max);
+    if (spec) block_sum2(ag, ah, block_sum);
+}
+
+// After a speculative gradient pass: when the bounds gave other scales than
+// the ones the pass used, the pairs and block sums are computed again (the
+// same gradient) under the right scales; otherwise every block leaves at once.
+__global__ __launch_bounds__(256) void gradient_fixup_kernel(const float *src, const float *y,
+                                                             const float *w, uint64_t n, int mode,
+                                                             uint64_t th, uint64_t seed,
+                                                             uint64_t tree,
+                                                             const ScalesDev *scales,
+                                                             int64_t *fixed, int64_t *block_sum) {
+    if (!scales->spec_miss) return;  // uniform
+    const double sg = scales->scale[0], sh = scales->scale[1];
+    uint64_t ag = 0, ah = 0;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const float v = mode == 2 ? fb_sigmoid(src[i]) : src[i];
+        float g = v - y[i];
+        float h = mode != 0 ? fmaxf(v * (1.0f - v), 1e-16f) : 1.0f;
+        if (w) {
+            g = g * w[i];
+            h = h * w[i];
+        }
+        if (!row_selected(i, th, seed, tree)) g = h = 0.0f;
+        const int64_t qg = sat_i64(round((double)g * sg));
+        const int64_t qh = sat_i64(round((double)h * sh));
+        reinterpret_cast<longlong2 *>(fixed)[i] = make_longlong2(qg, qh);
+        ag += (uint64_t)qg;
+        ah += (uint64_t)qh;
+    }
+    block_sum2(ag, ah, block_sum);
+}
+
+__global__ void reduce_max_kernel(const double *block_max, uint32_t n, double *out,
+                                  uint64_t n_rows, ScalesDev *scales);
+
+hipError_t launch_gradient_spec(const float *src, const float *y, const float *w, uint64_t n,
+                                int mode, uint64_t th, uint64_t seed, uint64_t tree,
+                                double *block_max, uint32_t n_blocks, ScalesDev *scales,
+                                int64_t *fixed, int64_t *block_sum, hipStream_t s) {
+    if (n_blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(gradient_kernel, dim3(n_blocks), dim3(256), 0, s, src, y, w, n, mode,
+                       nullptr, th, seed, tree, block_max, scales, fixed, block_sum);
+    hipLaunchKernelGGL(reduce_max_kernel, dim3(1), dim3(1024), 0, s, block_max, n_blocks,
+                       block_max + 2 * n_blocks, n, scales);
+    hipLaunchKernelGGL(gradient_fixup_kernel, dim3(n_blocks), dim3(256), 0, s, src, y, w, n, mode,
+                       th, seed, tree, scales, fixed, block_sum);
+    return hipGetLastError();
 }
 
 hipError_t launch_gradient(const float *src, const float *y, const float *w, uint64_t n, int mode,
@@ -1774,7 +1847,7 @@ hipError_t launch_gradient(const float *src, const float *y, const float *w, uin
         block_max ? n_blocks : (uint32_t)std::min<uint64_t>((n + 255) / 256, 8192);
     if (blocks == 0) return hipSuccess;
     hipLaunchKernelGGL(gradient_kernel, dim3(blocks), dim3(256), 0, s, src, y, w, n, mode, g2n,
-                       th, seed, tree, block_max);
+                       th, seed, tree, block_max, nullptr, nullptr, nullptr);
     return hipGetLastError();
 }
 
@@ -1882,6 +1955,25 @@ __device__ void block_max2(double mg, double mh, double *block_max) {
     }
 }
 
+// Wrapping block sums of the two components (256 threads) into
+// block_sum[2 * block].
+__device__ void block_sum2(uint64_t ag, uint64_t ah, int64_t *block_sum) {
+    __shared__ int64_t sm[2][4];
+    for (int off = 32; off > 0; off >>= 1) {
+        ag += (uint64_t)__shfl_xor((long long)ag, off, 64);
+        ah += (uint64_t)__shfl_xor((long long)ah, off, 64);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sm[0][threadIdx.x >> 6] = (int64_t)ag;
+        sm[1][threadIdx.x >> 6] = (int64_t)ah;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        block_sum[2 * blockIdx.x] = wadd(wadd(sm[0][0], sm[0][1]), wadd(sm[0][2], sm[0][3]));
+        block_sum[2 * blockIdx.x + 1] = wadd(wadd(sm[1][0], sm[1][1]), wadd(sm[1][2], sm[1][3]));
+    }
+}
+
 // floor(log2(x)) for a positive, finite, normal x as the floor of a correctly
 // rounded log2(x) gives it (the host's `log2(raw).floor()`): the exact floor,
 // except when log2(x) lies less than half a double spacing below an integer,
@@ -1953,6 +2045,7 @@ __global__ void reduce_max_kernel(const double *block_max, uint32_t n, double *o
     if (threadIdx.x == 0) {
         out[0] = sm[0][0];
         out[1] = sm[1][0];
+        const ScalesDev prev = *scales;  // the scales a speculative pass used
         ScalesDev S{};
         S.max_abs[0] = sm[0][0];
         S.max_abs[1] = sm[1][0];
@@ -1964,6 +2057,7 @@ __global__ void reduce_max_kernel(const double *block_max, uint32_t n, double *o
             S.scale[k] = scale_from_bound(S.max_abs[k], n_rows);
             S.inv[k] = 1.0 / S.scale[k];
         }
+        S.spec_miss = (prev.scale[0] == S.scale[0] && prev.scale[1] == S.scale[1]) ? 0u : 1u;
         *scales = S;
     }
 }
@@ -2011,7 +2105,6 @@ __device__ __forceinline__ int64_t sat_i64(double x) {
 __global__ __launch_bounds__(256) void gpair_quantize_kernel(const float *g2n, uint64_t n,
                                                              const ScalesDev *scales, int64_t *out,
                                                              int64_t *block_sum) {
-    __shared__ int64_t sm[2][4];
     const double sg = scales->scale[0], sh = scales->scale[1];
     uint64_t ag = 0, ah = 0;
     constexpr int U = 4;
@@ -2035,20 +2128,7 @@ __global__ __launch_bounds__(256) void gpair_quantize_kernel(const float *g2n, u
             ah += (uint64_t)qh;
         }
     }
-    // Wrapping sums: shuffles within each wave, then the four wave sums.
-    for (int off = 32; off > 0; off >>= 1) {
-        ag += (uint64_t)__shfl_xor((long long)ag, off, 64);
-        ah += (uint64_t)__shfl_xor((long long)ah, off, 64);
-    }
-    if ((threadIdx.x & 63) == 0) {
-        sm[0][threadIdx.x >> 6] = (int64_t)ag;
-        sm[1][threadIdx.x >> 6] = (int64_t)ah;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        block_sum[2 * blockIdx.x] = wadd(wadd(sm[0][0], sm[0][1]), wadd(sm[0][2], sm[0][3]));
-        block_sum[2 * blockIdx.x + 1] = wadd(wadd(sm[1][0], sm[1][1]), wadd(sm[1][2], sm[1][3]));
-    }
+    block_sum2(ag, ah, block_sum);
 }
 
 __global__ void reduce_sum_kernel(const int64_t *block_sum, uint32_t n, int64_t *out) {
