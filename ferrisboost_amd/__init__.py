@@ -131,7 +131,7 @@ def _normalize(params: Mapping[str, Any], num_boost_round: int) -> dict[str, Any
         out[canon] = value
     if out["objective"] not in _OBJECTIVES:
         raise ValueError(
-            f"objective {out['objective']!r} is not available on the device path of this build; "
+            f"objective {out['objective']!r} is not available on the ferrisboost_amd device path; "
             f"supported: {', '.join(_OBJECTIVES)}"
         )
     if out["grow_policy"] not in _GROW:
@@ -143,17 +143,17 @@ def _normalize(params: Mapping[str, Any], num_boost_round: int) -> dict[str, Any
     gm = out["gpu_math"]
     if gm not in (None, "exact"):
         if gm == "fast":
-            raise ValueError('gpu_math="fast" is not available in this build; use "exact"')
+            raise ValueError('gpu_math="fast" is not available in ferrisboost_amd; use "exact"')
         raise ValueError(f'gpu_math must be "exact" or "fast", got {gm!r}')
     if out["sampling_method"] != "uniform":
-        raise ValueError("sampling_method must be uniform on the device path of this build")
+        raise ValueError("sampling_method must be uniform on the ferrisboost_amd device path")
     for k in ("colsample_bylevel", "colsample_bynode"):
         if float(out[k]) != 1.0:
-            raise ValueError(f"{k} < 1 is not available on the device path of this build")
+            raise ValueError(f"{k} < 1 is not available on the ferrisboost_amd device path")
     if out["interaction_constraints"]:
-        raise ValueError("interaction_constraints are not available on the device path of this build")
+        raise ValueError("interaction_constraints are not available on the ferrisboost_amd device path")
     if out["feature_weights"] is not None:
-        raise ValueError("feature_weights are not available on the device path of this build")
+        raise ValueError("feature_weights are not available on the ferrisboost_amd device path")
     out["num_boost_round"] = int(num_boost_round)
     return out
 

@@ -651,7 +651,7 @@ void validate(const fbt_params &p, uint64_t n, uint32_t nf, const float *y) {
     if (p.objective > 1) throw InputError("objective must be reg:squarederror or binary:logistic");
     if (p.grow_policy > 1) throw InputError("grow_policy must be depthwise or lossguide");
     if (p.gpu_math != 0)
-        throw InputError("gpu_math=\"fast\" is not available in this build; use \"exact\"");
+        throw InputError("gpu_math=\"fast\" is not available in ferrisboost_amd; use \"exact\"");
     if (p.max_bin < 1 || p.max_bin > 65535)
         throw InputError("max_bin must be in 1..=65535, got " + std::to_string(p.max_bin));
     if (p.max_depth > 14)

@@ -51,7 +51,7 @@ typedef struct {
     uint32_t reserved;
     /* device-path knobs */
     int32_t device;            /* "cuda:N" */
-    uint32_t gpu_math;         /* 0 = exact (only mode of this build) */
+    uint32_t gpu_math;         /* 0 = exact (the only mode) */
     uint64_t gpu_memory_budget;/* bytes, 0 = automatic */
     uint32_t tile_bytes;       /* LDS histogram tile (0 = default) */
     uint32_t rows_per_block;   /* histogram rows per workgroup (0 = default) */

@@ -1,8 +1,8 @@
 // oracle.cpp -- CPU restatement of the FerrisBoost CPU engine.
 //
 // TEST INFRASTRUCTURE ONLY. The test suite, the smoke check and the
-// benchmark's CPU-baseline leg load this library as the checker; the shipped
-// package never links, loads or calls it.
+// benchmark's CPU-baseline leg load this library to check or time against
+// it; the shipped package never links, loads or calls it.
 //
 // Each function names the reference file:line it restates (reference crate
 // `ferrisboost` 0.1.1, Rust). The reference cannot be compiled here (no Rust

@@ -3,8 +3,8 @@
  * TEST INFRASTRUCTURE ONLY. This library is a CPU restatement of the
  * FerrisBoost CPU engine (reference crate `ferrisboost` 0.1.1). Only the
  * test suite, the smoke check and the CPU-baseline leg of the benchmark load
- * it, and only as the checker. Nothing in the shipped package links, loads or
- * calls it.
+ * it, and only to check or time against it. Nothing in the shipped package
+ * links, loads or calls it.
  *
  * Every function cites the reference file:line whose behaviour it restates.
  * Parity status of each part is listed in oracle.cpp's header.

@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (liboracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by the test suite, the smoke check and the
-CPU-baseline leg of bench.py, always as the checker. The shipped package
+CPU-baseline leg of bench.py, only to check or time against. The shipped package
 (ferrisboost_amd) never imports this module.
 """
 

@@ -1,6 +1,6 @@
 """CPU pins of the oracle (no GPU).
 
-The oracle is the checker of every GPU parity test, so it is itself checked
+The oracle is the reference of every GPU parity test, so it is itself checked
 here against what fixes its behaviour independently of its own code:
 
 * the reference's XGBoost-3.4.1 golden margins (tests/fixtures of the
