@@ -220,7 +220,8 @@ def test_sampled_weighted_rounds_match_oracle(fb, oracle, objective, depth, host
 
 
 @pytest.mark.parametrize("case", ["budget", "monotone", "categorical", "sampled_deep", "stump",
-                                  "squared", "walk_budget", "walk_categorical", "walk_squared"])
+                                  "squared", "walk_budget", "walk_categorical", "walk_squared",
+                                  "walk_u16"])
 def test_device_grown_trees_match_host_levels_and_oracle(fb, oracle, case):
     """Whole depthwise trees grown on the device (the max_leaves budget, node
     ids, weights, bounds, slots, partitions and leaves decided by kernels)
@@ -228,9 +229,11 @@ def test_device_grown_trees_match_host_levels_and_oracle(fb, oracle, case):
     for node, with margins equal bit for bit. The walk_ cases use 4 KiB tiles:
     two features a tile, three tiles in one 16-byte row bundle, so leaves and
     margins come from the row-order walk of the finished tree instead of a
-    last-level partition."""
+    last-level partition; walk_u16 has 300 bins (16-bit cells, three
+    features a 16 KiB tile, two tiles in one 16-byte bundle)."""
     walk = case.startswith("walk_")
     case = case[5:] if walk else case
+    wide_bins = case == "u16"
     rng = np.random.default_rng(sum(map(ord, case)))
     n, nf = 30_011, 6
     x = rng.normal(size=(n, nf)).astype(np.float32)
@@ -258,10 +261,12 @@ def test_device_grown_trees_match_host_levels_and_oracle(fb, oracle, case):
     elif case == "squared":
         p.update(objective="reg:squarederror")
         y = z.astype(np.float32)
+    elif case == "u16":
+        p.update(max_bin=300)
     om = oracle.train(x, y, oracle.make_params(**p), weights=w, monotone=mono, categorical=cat)
     pp = product_params(p)
     if walk:
-        pp["hip_tile_bytes"] = 4096
+        pp["hip_tile_bytes"] = 16384 if wide_bins else 4096
     if mono:
         pp["monotone_constraints"] = mono
     if cat:
