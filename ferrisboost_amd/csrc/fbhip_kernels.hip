@@ -1513,17 +1513,30 @@ __global__ __launch_bounds__(PART_TPB) void part_scatter_kernel(const PartReqDev
                                                                 const uint32_t *dev,
                                                                 ZeroNodesDev Z) {
     if (Z.hist) {
-        // Node by node, so the words of slots that need no clearing are never visited.
+        // The block's threads examine PART_TPB nodes at a time (one load
+        // each) and list those to clear; only listed slots are visited.
+        __shared__ uint32_t clr[PART_TPB];
+        __shared__ uint32_t n_clr;
         const uint64_t W = Z.width * 2u;
         const uint32_t nn = *Z.dev_n;
-        for (uint32_t e = 0; e < nn; e++) {
-            const HistNodeDev N = Z.nodes[e];
-            const bool clear = Z.group ? N.n_chunks > Z.group : (Z.force || N.n_chunks != 1);
-            if (!clear) continue;
-            int64_t *slot = Z.hist + (uint64_t)N.slot * W;
-            for (uint64_t k = (uint64_t)blockIdx.x * PART_TPB + threadIdx.x; k < W;
-                 k += (uint64_t)gridDim.x * PART_TPB)
-                slot[k] = 0;
+        for (uint32_t e0 = 0; e0 < nn; e0 += PART_TPB) {
+            if (threadIdx.x == 0) n_clr = 0;
+            __syncthreads();
+            const uint32_t e = e0 + threadIdx.x;
+            if (e < nn) {
+                const HistNodeDev N = Z.nodes[e];
+                const bool clear = Z.group ? N.n_chunks > Z.group : (Z.force || N.n_chunks != 1);
+                if (clear) clr[atomicAdd(&n_clr, 1u)] = N.slot;
+            }
+            __syncthreads();
+            const uint32_t k = n_clr;
+            for (uint32_t j = 0; j < k; j++) {
+                int64_t *slot = Z.hist + (uint64_t)clr[j] * W;
+                for (uint64_t i = (uint64_t)blockIdx.x * PART_TPB + threadIdx.x; i < W;
+                     i += (uint64_t)gridDim.x * PART_TPB)
+                    slot[i] = 0;
+            }
+            __syncthreads();
         }
     }
     const uint32_t chunk = blockIdx.x;
