@@ -1334,6 +1334,11 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
                 tf.resize(d.feat_base);
                 return false;
             }
+            if (!t.global && hist_rot_layout(t.width, t.rec)) {
+                // Interleaved layout: feature k at slot bin * 16 + k.
+                for (uint32_t k = 0; k < d.n_feat; k++) tf[d.feat_base + k].lds_off = k;
+                lds = HIST_ROT_SLOTS;
+            }
             d.lds_slots = t.global ? 0 : lds;
             td.push_back(d);
             return true;

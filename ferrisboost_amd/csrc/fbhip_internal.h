@@ -31,6 +31,13 @@ struct TileDev {
     uint32_t pad;
 };
 
+// LDS layout of 8-bit tiles with 16-byte records: slot bin * 16 + k for
+// feature k of the tile (bins below 256), whatever the tile's bin counts.
+constexpr uint32_t HIST_ROT_SLOTS = 16u * 256u;
+inline bool hist_rot_layout(uint32_t width, uint32_t rec_bytes) {
+    return width == 1 && rec_bytes == 16;
+}
+
 // Per-feature entry of a tile for one tree.
 struct TileFeatDev {
     uint32_t n_bins;    // 0 when the feature is not built this tree
