@@ -83,6 +83,9 @@ constexpr uint32_t MAX_RECORD_BYTES = 64;
 constexpr uint64_t MAX_PARTIAL_BYTES = 256ull << 20;
 constexpr uint32_t MAX_NODES = 16384;      // nodes of one eval / partition call
 constexpr uint32_t DEFAULT_TILE_BYTES = 64 * 1024;
+// Device-grown trees of at most this many features pick each node's best
+// split inside the level decision instead of a separate argmax launch.
+constexpr size_t FUSED_ARGMAX_FEATS = 64;
 // Rows per histogram workgroup: chosen per launch so that the launch makes
 // one full wave of workgroups (HIST_WAVES), never fewer than MIN_CHUNK_ROWS
 // rows: each workgroup then flushes its LDS histogram once per launch.
@@ -1483,6 +1486,9 @@ struct EvalPlan {
     // are then upper bounds that size the grids).
     const uint32_t *dev_n_hn = nullptr, *dev_n_tri = nullptr, *dev_n_nodes = nullptr;
     bool download = true;  // copy the packets back (a device-grown tree reads them in place)
+    // The level decision makes the packets from the candidates itself
+    // (device-grown trees of few features): no argmax launch.
+    bool fused_argmax = false;
     const uint32_t *rows = nullptr;  // arena of the accumulated nodes (null: the row arena)
     bool cleared = false;            // the accumulated slots were cleared by the partition
     bool identity = false;           // the accumulated rows are in order (no arena read)
@@ -1617,9 +1623,10 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
     const size_t pk_bytes = sizeof(SplitPacketDev) * E.n_nodes;
     uint8_t *d_out = reinterpret_cast<uint8_t *>(c->d_packets);
     uint64_t *d_cats = reinterpret_cast<uint64_t *>(d_out + ((pk_bytes + 255) & ~size_t(255)));
-    check(launch_split_nodes(c->d_cands, c->d_sfeats, E.n_nodes, P, E.sn, c->d_cat_scratch,
-                             c->d_packets, d_cats, cw, E.dev_n_nodes, c->stream),
-          "split argmax");
+    if (!E.fused_argmax)
+        check(launch_split_nodes(c->d_cands, c->d_sfeats, E.n_nodes, P, E.sn, c->d_cat_scratch,
+                                 c->d_packets, d_cats, cw, E.dev_n_nodes, c->stream),
+              "split argmax");
     if (!E.download) return;
     // Packets and category sets land back to back: one download.
     const size_t out_bytes = c->cat_words_per_node > 0
@@ -2234,6 +2241,9 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     E0.sn = c->d_lvl_split;
     E0.n_nodes = 1;
     E0.download = false;
+    // One thread a node scans the candidates in the level decision.
+    const bool fuse = c->tree_feats.size() <= FUSED_ARGMAX_FEATS;
+    E0.fused_argmax = fuse;
     // A root sum from the host is staged; else the prep kernel sums the
     // quantisation's block sums.
     const int64_t *d_root = nullptr;
@@ -2269,13 +2279,16 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     account_hist(c, n_rows, 1);
 
     uint8_t *pk_base = reinterpret_cast<uint8_t *>(c->d_packets);
+    const FusedArgmaxDev A =
+        fuse ? FusedArgmaxDev{c->d_cands, c->d_sfeats, c->d_lvl_split, c->d_cat_scratch}
+             : FusedArgmaxDev{};
     for (uint32_t d = 0; d < D; d++) {
         const uint32_t nb = lvl_bound(d);
-        const uint64_t *pk_cats =
-            reinterpret_cast<const uint64_t *>(pk_base + al256(sizeof(SplitPacketDev) * nb));
+        uint64_t *pk_cats =
+            reinterpret_cast<uint64_t *>(pk_base + al256(sizeof(SplitPacketDev) * nb));
         check(launch_grow_decide(G, d, c->d_packets, pk_cats, GB.level[d & 1], GB.tree,
                                  GB.tree_cats, d_mono, GB.cols, GB.reqs, GB.pairs, GB.triples,
-                                 GB.leaves, GB.leaf_vals, GB.st, c->stream),
+                                 GB.leaves, GB.leaf_vals, GB.st, A, c->stream),
               "tree level decision");
         if (walk && d + 1 == D) break;  // the last level's children are found by the walk
         // Level d's rows are in arena d % 2; its children go to the other.
@@ -2311,6 +2324,7 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
         E.n_nodes = lvl_bound(d + 1);
         E.dev_n_nodes = &GB.st->n_level;
         E.download = false;
+        E.fused_argmax = fuse;
         E.rows = arena_out;
         E.cleared = true;
         enqueue_eval(c, E, sp);

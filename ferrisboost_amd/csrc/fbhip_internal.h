@@ -329,11 +329,21 @@ hipError_t launch_grow_prep(const GrowParamsDev &G, const int64_t *root, const i
                             uint32_t n_blocks, uint32_t root_slot, LNodeDev *level,
                             SplitNodeDev *root_split, TreeNodeDev *tree, GrowState *st,
                             int64_t *clear, uint64_t clear_words, hipStream_t s);
+// cands non-null: the level decision picks each node's best feature from
+// the split scan's candidates itself (split_node_kernel not launched) and
+// writes the winners' category sets to pk_cats.
+struct FusedArgmaxDev {
+    const FeatCandDev *cands;
+    const SplitFeatDev *feats;
+    const SplitNodeDev *nodes;
+    const uint64_t *cat_scratch;
+};
 hipError_t launch_grow_decide(const GrowParamsDev &G, uint32_t depth, const SplitPacketDev *pk,
-                              const uint64_t *pk_cats, const LNodeDev *level, TreeNodeDev *tree,
+                              uint64_t *pk_cats, const LNodeDev *level, TreeNodeDev *tree,
                               uint64_t *tree_cats, const int8_t *monotone, const DevColumn *cols,
                               PartReqDev *reqs, PairDev *pairs, uint32_t *triples,
-                              LeafDev *leaves, float *leaf_vals, GrowState *st, hipStream_t s);
+                              LeafDev *leaves, float *leaf_vals, GrowState *st,
+                              const FusedArgmaxDev &A, hipStream_t s);
 hipError_t launch_leaf_plan(LeafDev *leaves, GrowState *st, hipStream_t s);
 // Leaves of a device-grown tree by a row-order walk over the single row
 // bundle (feat_off[f]: byte offset of feature f in the bundle row, bit 15 set

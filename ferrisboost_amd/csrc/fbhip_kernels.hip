@@ -1297,6 +1297,86 @@ hipError_t launch_split_feats(const int64_t *hist, uint64_t hist_width, const Sp
 
 // Per node: the best feature by gain, ties to the lowest feature id
 // (features are in ascending global order), as reduce_best / update_best.
+// The packet of node ni whose best feature (in split-scan order) is ord;
+// a categorical winner's category set is copied to cat_out.
+__device__ SplitPacketDev split_packet(const FeatCandDev *c, const SplitFeatDev *feats,
+                                       const SplitParamsDev &P, uint32_t ni, uint32_t found,
+                                       uint32_t ord, const SplitNodeDev *nodes,
+                                       const uint64_t *cat_scratch, uint64_t *cat_out,
+                                       uint32_t cat_out_words) {
+    SplitPacketDev pk;
+    pk.found = found;
+    pk.feat = 0;
+    pk.bin = 0;
+    pk.missing_left = 0;
+    pk.gain = 0.0f;
+    pk.is_cat = 0;
+    pk.cat_offset = ni * cat_out_words;
+    pk.n_cat_words = 0;
+    pk.left[0] = pk.left[1] = pk.right[0] = pk.right[1] = 0;
+    if (found) {
+        const FeatCandDev w = c[ord];
+        const SplitFeatDev F = feats[ord];
+        const SplitNodeDev N = nodes[ni];
+        pk.feat = F.feat;
+        pk.bin = w.bin;
+        pk.missing_left = w.missing_left;
+        pk.gain = w.gain;
+        pk.left[0] = w.left_g;
+        pk.left[1] = w.left_h;
+        pk.right[0] = wsub(N.sum_g, w.left_g);
+        pk.right[1] = wsub(N.sum_h, w.left_h);
+        if (F.categorical) {
+            pk.is_cat = 1;
+            pk.n_cat_words = F.cat_words;
+            const uint64_t *src = cat_scratch + (size_t)ni * P.cat_words_per_node + F.cat_base;
+            for (uint32_t k = 0; k < F.cat_words && k < cat_out_words; k++)
+                cat_out[(size_t)ni * cat_out_words + k] = src[k];
+        }
+    }
+    return pk;
+}
+
+// The packet of node ni from its candidates by one thread: the first
+// feature of the largest gain, as block_best picks it (found candidates
+// have gains above MIN_GAIN_EPS, never NaN).
+__device__ SplitPacketDev split_packet_serial(const FeatCandDev *cands, const SplitFeatDev *feats,
+                                              const SplitParamsDev &P, uint32_t ni,
+                                              const SplitNodeDev *nodes,
+                                              const uint64_t *cat_scratch, uint64_t *cat_out,
+                                              uint32_t cat_out_words) {
+    const FeatCandDev *c = cands + (size_t)ni * P.n_feats;
+    uint32_t found = 0, ord = 0;
+    float gain = 0.0f;
+    uint32_t j = 0;
+    // Eight candidates' loads in flight at a time.
+    for (; j + 8 <= P.n_feats; j += 8) {
+        float gj[8];
+        uint32_t fj[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            gj[k] = c[j + k].gain;
+            fj[k] = c[j + k].found;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (fj[k] && (!found || gj[k] > gain)) {
+                found = 1;
+                gain = gj[k];
+                ord = j + k;
+            }
+    }
+    for (; j < P.n_feats; j++) {
+        const FeatCandDev cj = c[j];
+        if (cj.found && (!found || cj.gain > gain)) {
+            found = 1;
+            gain = cj.gain;
+            ord = j;
+        }
+    }
+    return split_packet(c, feats, P, ni, found, ord, nodes, cat_scratch, cat_out, cat_out_words);
+}
+
 __global__ __launch_bounds__(SPLIT_TPB) void split_node_kernel(
     const FeatCandDev *cands, const SplitFeatDev *feats, SplitParamsDev P,
     const SplitNodeDev *nodes, const uint64_t *cat_scratch, SplitPacketDev *out,
@@ -1316,39 +1396,9 @@ __global__ __launch_bounds__(SPLIT_TPB) void split_node_kernel(
         }
     }
     best = block_best(best, shb);
-    if (tid == 0) {
-        SplitPacketDev pk;
-        pk.found = best.found;
-        pk.feat = 0;
-        pk.bin = 0;
-        pk.missing_left = 0;
-        pk.gain = 0.0f;
-        pk.is_cat = 0;
-        pk.cat_offset = ni * cat_out_words;
-        pk.n_cat_words = 0;
-        pk.left[0] = pk.left[1] = pk.right[0] = pk.right[1] = 0;
-        if (best.found) {
-            const FeatCandDev w = c[best.ord];
-            const SplitFeatDev F = feats[best.ord];
-            const SplitNodeDev N = nodes[ni];
-            pk.feat = F.feat;
-            pk.bin = w.bin;
-            pk.missing_left = w.missing_left;
-            pk.gain = w.gain;
-            pk.left[0] = w.left_g;
-            pk.left[1] = w.left_h;
-            pk.right[0] = wsub(N.sum_g, w.left_g);
-            pk.right[1] = wsub(N.sum_h, w.left_h);
-            if (F.categorical) {
-                pk.is_cat = 1;
-                pk.n_cat_words = F.cat_words;
-                const uint64_t *src = cat_scratch + (size_t)ni * P.cat_words_per_node + F.cat_base;
-                for (uint32_t k = 0; k < F.cat_words && k < cat_out_words; k++)
-                    cat_out[(size_t)ni * cat_out_words + k] = src[k];
-            }
-        }
-        out[ni] = pk;
-    }
+    if (tid == 0)
+        out[ni] = split_packet(c, feats, P, ni, best.found, best.ord, nodes, cat_scratch, cat_out,
+                               cat_out_words);
 }
 
 hipError_t launch_split_nodes(const FeatCandDev *cands, const SplitFeatDev *feats,
@@ -2555,10 +2605,10 @@ hipError_t launch_grow_prep(const GrowParamsDev &G, const int64_t *root, const i
 //    and, when the children are evaluated, the lowest free histogram slot
 //    for the smaller child (the larger one takes over the node's slot).
 __global__ __launch_bounds__(1024) void grow_decide_kernel(
-    GrowParamsDev G, uint32_t depth, const SplitPacketDev *pk, const uint64_t *pk_cats,
+    GrowParamsDev G, uint32_t depth, const SplitPacketDev *pk, uint64_t *pk_cats,
     const LNodeDev *level, TreeNodeDev *tree, uint64_t *tree_cats, const int8_t *monotone,
     const DevColumn *cols, PartReqDev *reqs, PairDev *pairs, uint32_t *triples, LeafDev *leaves,
-    float *leaf_vals, GrowState *st) {
+    float *leaf_vals, GrowState *st, FusedArgmaxDev A) {
     __shared__ uint32_t buf[1024];
     __shared__ uint32_t held[MAX_GROW_SLOTS / 32];
     __shared__ uint16_t freelist[MAX_GROW_SLOTS];
@@ -2571,13 +2621,20 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
     const uint32_t i0 = min(tid * per, n), i1 = min(i0 + per, n);
     // With at most 1024 nodes each thread's packet and node stay in
     // registers for every pass.
+    // A.cands set: the packets are made here from the split scan's
+    // candidates (split_node_kernel's work), else read.
+    auto make_pk = [&](uint32_t i) -> SplitPacketDev {
+        return A.cands ? split_packet_serial(A.cands, A.feats, G.sp, i, A.nodes, A.cat_scratch,
+                                             pk_cats, G.cw)
+                       : pk[i];
+    };
     SplitPacketDev myP{};
     LNodeDev myL{};
     if (per == 1 && i0 < n) {
-        myP = pk[i0];
+        myP = make_pk(i0);
         myL = level[i0];
     }
-    auto pk_at = [&](uint32_t i) -> SplitPacketDev { return per == 1 ? myP : pk[i]; };
+    auto pk_at = [&](uint32_t i) -> SplitPacketDev { return per == 1 ? myP : make_pk(i); };
     auto lv_at = [&](uint32_t i) -> LNodeDev { return per == 1 ? myL : level[i]; };
 
     uint32_t nf = 0;
@@ -2752,14 +2809,15 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
 }
 
 hipError_t launch_grow_decide(const GrowParamsDev &G, uint32_t depth, const SplitPacketDev *pk,
-                              const uint64_t *pk_cats, const LNodeDev *level, TreeNodeDev *tree,
+                              uint64_t *pk_cats, const LNodeDev *level, TreeNodeDev *tree,
                               uint64_t *tree_cats, const int8_t *monotone, const DevColumn *cols,
                               PartReqDev *reqs, PairDev *pairs, uint32_t *triples,
-                              LeafDev *leaves, float *leaf_vals, GrowState *st, hipStream_t s) {
+                              LeafDev *leaves, float *leaf_vals, GrowState *st,
+                              const FusedArgmaxDev &A, hipStream_t s) {
     if (G.n_slots > MAX_GROW_SLOTS) return hipErrorInvalidValue;
     hipLaunchKernelGGL(grow_decide_kernel, dim3(1), dim3(1024), 0, s, G, depth, pk, pk_cats, level,
                        tree, tree_cats, monotone, cols, reqs, pairs, triples, leaves, leaf_vals,
-                       st);
+                       st, A);
     return hipGetLastError();
 }
 
