@@ -62,6 +62,8 @@ __host__ __device__ inline uint32_t reduce_groups(uint32_t n_chunks) {
     return n_chunks <= 16u ? 1u : (n_chunks + 15u) / 16u;
 }
 
+struct ScalesDev;
+
 struct HistLaunch {
     const TileDev *tiles;      // tiles of this launch (same width / record size)
     const TileFeatDev *feats;
@@ -83,6 +85,11 @@ struct HistLaunch {
     // ([chunk][hist_width][2], plain stores) for reduce_chunks_kernel,
     // instead of adding it into its slot with global atomics.
     int64_t *partials;
+    // Non-null: the pairs are read as f32 [n_rows][2] and quantized here
+    // with the scales at `scales`, as the gradient pass quantized gpair
+    // (8 instead of 16 bytes a scattered row).
+    const float *gpair_f32;
+    const ScalesDev *scales;
     uint64_t hist_width;
     // Streamed tile: its records of rows [row_lo, row_hi) sit at
     // stream_data + (row - row_lo) * stride; only those rows are accumulated.
@@ -410,11 +417,13 @@ hipError_t launch_init_rows(uint32_t *rows, float *delta, uint64_t n, hipStream_
 // The gradients of a round quantized in the same pass under the previous
 // round's scales (still in `scales`), then the bounds and this round's
 // scales, then a pass that recomputes the pairs only if the scales changed:
-// fixed-point pairs and block sums as gpair_quantize would give.
+// fixed-point pairs and block sums as gpair_quantize would give. g2n
+// non-null: the (subsample-masked) f32 pairs are written there too; fixed
+// may then be null (block sums only, the pairs quantized where they are read).
 hipError_t launch_gradient_spec(const float *src, const float *y, const float *w, uint64_t n,
                                 int mode, uint64_t th, uint64_t seed, uint64_t tree,
                                 double *block_max, uint32_t n_blocks, ScalesDev *scales,
-                                int64_t *fixed, int64_t *block_sum, hipStream_t s);
+                                int64_t *fixed, int64_t *block_sum, float *g2n, hipStream_t s);
 hipError_t launch_gpair_maxabs(float *g2n, uint64_t n, uint64_t threshold, uint64_t seed,
                                uint64_t tree, double *block_max, uint32_t n_blocks,
                                hipStream_t s);

@@ -25,6 +25,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 namespace fbh {
 
@@ -73,6 +74,8 @@ __device__ __forceinline__ void block_to_work(const HistLaunch &L, uint32_t b, u
     tile_i = k % L.n_tiles;
     chunk = (k / L.n_tiles) * XCDS + xcd;
 }
+
+__device__ __forceinline__ int64_t sat_i64(double x);
 
 __device__ __forceinline__ void lds_add_u64(unsigned long long *p, unsigned long long v) {
     __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -187,76 +190,97 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
     // root before any partition).
     const uint32_t *rows = L.rows ? L.rows + N.row_off : nullptr;
     const longlong2 *gp = reinterpret_cast<const longlong2 *>(L.gpair);
-    for (uint32_t i = r0 + tid; i < r1; i += TPB * UNROLL) {
-        uint32_t row[UNROLL];
-        bool ok[UNROLL];
-#pragma unroll
-        for (int u = 0; u < UNROLL; u++) {
-            const uint32_t idx = i + u * TPB;
-            ok[u] = idx < r1;
-            row[u] = ok[u] ? (rows ? rows[idx] : N.row_off + idx) : 0u;
-        }
-        longlong2 g[UNROLL];
-        uint32_t rec[UNROLL][RD];
-#pragma unroll
-        for (int u = 0; u < UNROLL; u++) {
-            if (ok[u]) {
-                g[u] = gp[row[u]];
-                if (STREAM)
-                    load_record<RD>(L.stream_data + (size_t)(row[u] - L.row_lo) * T.stride, rec[u]);
-                else
-                    load_record<RD>(T.data + (size_t)row[u] * T.stride, rec[u]);
-            } else {
-                g[u] = make_longlong2(0, 0);
-#pragma unroll
-                for (int d = 0; d < RD; d++) rec[u][d] = 0u;
-            }
-        }
-        if (ROT) {
-            // Rotate each record right by rot bytes: byte k becomes the byte
-            // of feature (k + rot) mod 16.
-            const uint32_t dsh = rot >> 2, bsh = rot & 3u;
-#pragma unroll
+    const float2 *gf = reinterpret_cast<const float2 *>(L.gpair_f32);
+    double sg = 0.0, sh = 0.0;
+    if (gf) {
+        sg = L.scales->scale[0];
+        sh = L.scales->scale[1];
+    }
+    // The row loop, compiled once per pair format (no per-row branch).
+    auto accumulate = [&](auto pair_f32) {
+        constexpr bool PF = decltype(pair_f32)::value;
+        for (uint32_t i = r0 + tid; i < r1; i += TPB * UNROLL) {
+            uint32_t row[UNROLL];
+            bool ok[UNROLL];
+    #pragma unroll
             for (int u = 0; u < UNROLL; u++) {
-                uint32_t b[4], a[4];
-#pragma unroll
-                for (int j = 0; j < 4; j++) b[j] = (dsh & 1u) ? rec[u][(j + 1) & 3] : rec[u][j];
-#pragma unroll
-                for (int j = 0; j < 4; j++) a[j] = (dsh & 2u) ? b[(j + 2) & 3] : b[j];
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    rec[u][j] = __builtin_amdgcn_alignbyte(a[(j + 1) & 3], a[j], bsh);
+                const uint32_t idx = i + u * TPB;
+                ok[u] = idx < r1;
+                row[u] = ok[u] ? (rows ? rows[idx] : N.row_off + idx) : 0u;
             }
-        }
-#pragma unroll
-        for (int u = 0; u < UNROLL; u++) {
-            const unsigned long long gg = (unsigned long long)g[u].x;
-            const unsigned long long hh = (unsigned long long)g[u].y;
-#pragma unroll
-            for (int d = 0; d < RD; d++) {
-#pragma unroll
-                for (int q = 0; q < FPD; q++) {
-                    const int fi = d * FPD + q;
-                    const uint32_t bin = (rec[u][d] >> (q * 8 * W)) & MASK;
-                    uint32_t s;
-                    if (ROT) {
-                        // Features outside the tile or not built this tree
-                        // have nb 0 and add into the lane's dummy.
-                        const uint32_t feat = ((uint32_t)fi + rot) & 15u;
-                        s = (bin < nb[fi] ? bin << 4 : dummy) + feat;
-                    } else {
-                        if (fi >= (int)T.n_feat) continue;  // uniform
-                        if (nb[fi] == 0) continue;  // not built this tree (uniform)
-                        // Missing (all ones) and unseen-category codes are >= n_bins;
-                        // out-of-range rows (ok false) carry a zero pair.
-                        s = bin < nb[fi] ? loff[fi] + bin : dummy;
+            longlong2 g[UNROLL];
+            float2 f[UNROLL];
+            uint32_t rec[UNROLL][RD];
+    #pragma unroll
+            for (int u = 0; u < UNROLL; u++) {
+                if (ok[u]) {
+                    if constexpr (PF) f[u] = gf[row[u]];
+                    else g[u] = gp[row[u]];
+                    if (STREAM)
+                        load_record<RD>(L.stream_data + (size_t)(row[u] - L.row_lo) * T.stride, rec[u]);
+                    else
+                        load_record<RD>(T.data + (size_t)row[u] * T.stride, rec[u]);
+                } else {
+                    f[u] = make_float2(0.0f, 0.0f);
+                    g[u] = make_longlong2(0, 0);
+    #pragma unroll
+                    for (int d = 0; d < RD; d++) rec[u][d] = 0u;
+                }
+            }
+            if constexpr (PF) {
+    #pragma unroll
+                for (int u = 0; u < UNROLL; u++)
+                    g[u] = make_longlong2(sat_i64(round((double)f[u].x * sg)),
+                                          sat_i64(round((double)f[u].y * sh)));
+            }
+            if (ROT) {
+                // Rotate each record right by rot bytes: byte k becomes the byte
+                // of feature (k + rot) mod 16.
+                const uint32_t dsh = rot >> 2, bsh = rot & 3u;
+    #pragma unroll
+                for (int u = 0; u < UNROLL; u++) {
+                    uint32_t b[4], a[4];
+    #pragma unroll
+                    for (int j = 0; j < 4; j++) b[j] = (dsh & 1u) ? rec[u][(j + 1) & 3] : rec[u][j];
+    #pragma unroll
+                    for (int j = 0; j < 4; j++) a[j] = (dsh & 2u) ? b[(j + 2) & 3] : b[j];
+    #pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        rec[u][j] = __builtin_amdgcn_alignbyte(a[(j + 1) & 3], a[j], bsh);
+                }
+            }
+    #pragma unroll
+            for (int u = 0; u < UNROLL; u++) {
+                const unsigned long long gg = (unsigned long long)g[u].x;
+                const unsigned long long hh = (unsigned long long)g[u].y;
+    #pragma unroll
+                for (int d = 0; d < RD; d++) {
+    #pragma unroll
+                    for (int q = 0; q < FPD; q++) {
+                        const int fi = d * FPD + q;
+                        const uint32_t bin = (rec[u][d] >> (q * 8 * W)) & MASK;
+                        uint32_t s;
+                        if (ROT) {
+                            // Features outside the tile or not built this tree
+                            // have nb 0 and add into the lane's dummy.
+                            const uint32_t feat = ((uint32_t)fi + rot) & 15u;
+                            s = (bin < nb[fi] ? bin << 4 : dummy) + feat;
+                        } else {
+                            if (fi >= (int)T.n_feat) continue;  // uniform
+                            if (nb[fi] == 0) continue;  // not built this tree (uniform)
+                            // Missing (all ones) and unseen-category codes are >= n_bins;
+                            // out-of-range rows (ok false) carry a zero pair.
+                            s = bin < nb[fi] ? loff[fi] + bin : dummy;
+                        }
+                        lds_add_u64(gplane + s, gg);
+                        lds_add_u64(hplane + s, hh);
                     }
-                    lds_add_u64(gplane + s, gg);
-                    lds_add_u64(hplane + s, hh);
                 }
             }
         }
-    }
+    };
+    if (gf) accumulate(std::true_type{});
+    else accumulate(std::false_type{});
     __syncthreads();
 
     // One chunk: its slot. Several: the chunk's partial histogram, or
@@ -333,9 +357,21 @@ __global__ __launch_bounds__(HIST_TPB) void hist_global_kernel(const HistLaunch 
         L.hist + ((uint64_t)N.slot * L.hist_width + F.hist_off) * 2u);
     const uint32_t *rows = L.rows ? L.rows + N.row_off : nullptr;
     const longlong2 *gp = reinterpret_cast<const longlong2 *>(L.gpair);
+    const float2 *gf = reinterpret_cast<const float2 *>(L.gpair_f32);
+    double sg = 0.0, sh = 0.0;
+    if (gf) {
+        sg = L.scales->scale[0];
+        sh = L.scales->scale[1];
+    }
     for (uint32_t i = r0 + threadIdx.x; i < r1; i += HIST_TPB) {
         const uint32_t row = rows ? rows[i] : N.row_off + i;
-        const longlong2 g = gp[row];
+        longlong2 g;
+        if (gf) {
+            const float2 v = gf[row];
+            g = make_longlong2(sat_i64(round((double)v.x * sg)), sat_i64(round((double)v.y * sh)));
+        } else {
+            g = gp[row];
+        }
         if ((g.x | g.y) == 0) continue;
         const uint8_t *p = T.data + (size_t)row * T.stride;
         const uint32_t bin = W == 1 ? (uint32_t)p[0] : (uint32_t)*reinterpret_cast<const uint16_t *>(p);
@@ -1855,8 +1891,8 @@ __device__ void block_sum2(uint64_t ag, uint64_t ah, int64_t *block_sum);
 
 // block_max set: rows outside the round's subsample get a zero pair, and
 // each block's max |g|, max |h| goes to block_max (the bounds pass fused in).
-// spec set: instead of the f32 pairs, the fixed-point pairs under the scales
-// in spec (the previous round's) go to fixed, with the block sums; the bounds
+// g2n set: the f32 pairs go there. spec set: the fixed-point pairs under the
+// scales in spec (the previous round's) go to fixed (when set), with the block sums; the bounds
 // pass then tells whether those were this round's scales
 // (gradient_fixup_kernel redoes the pairs when not). The same grid and
 // operations as without spec, so each row's g and h are the same floats.
@@ -1906,12 +1942,11 @@ __global__ __launch_bounds__(256) void gradient_kernel(const float *src, const f
             if (spec) {
                 const int64_t qg = sat_i64(round((double)g * sg));
                 const int64_t qh = sat_i64(round((double)h * sh));
-                reinterpret_cast<longlong2 *>(fixed)[i] = make_longlong2(qg, qh);
+                if (fixed) reinterpret_cast<longlong2 *>(fixed)[i] = make_longlong2(qg, qh);
                 ag += (uint64_t)qg;
                 ah += (uint64_t)qh;
-            } else {
-                reinterpret_cast<float2 *>(g2n)[i] = make_float2(g, h);
             }
+            if (g2n) reinterpret_cast<float2 *>(g2n)[i] = make_float2(g, h);
         }
     }
     if (block_max) block_max2(mg, mh, block_max);
@@ -1942,7 +1977,7 @@ __global__ __launch_bounds__(256) void gradient_fixup_kernel(const float *src, c
         if (!row_selected(i, th, seed, tree)) g = h = 0.0f;
         const int64_t qg = sat_i64(round((double)g * sg));
         const int64_t qh = sat_i64(round((double)h * sh));
-        reinterpret_cast<longlong2 *>(fixed)[i] = make_longlong2(qg, qh);
+        if (fixed) reinterpret_cast<longlong2 *>(fixed)[i] = make_longlong2(qg, qh);
         ag += (uint64_t)qg;
         ah += (uint64_t)qh;
     }
@@ -1955,10 +1990,10 @@ __global__ void reduce_max_kernel(const double *block_max, uint32_t n, double *o
 hipError_t launch_gradient_spec(const float *src, const float *y, const float *w, uint64_t n,
                                 int mode, uint64_t th, uint64_t seed, uint64_t tree,
                                 double *block_max, uint32_t n_blocks, ScalesDev *scales,
-                                int64_t *fixed, int64_t *block_sum, hipStream_t s) {
+                                int64_t *fixed, int64_t *block_sum, float *g2n, hipStream_t s) {
     if (n_blocks == 0) return hipSuccess;
     hipLaunchKernelGGL(gradient_kernel, dim3(n_blocks), dim3(256), 0, s, src, y, w, n, mode,
-                       nullptr, th, seed, tree, block_max, scales, fixed, block_sum);
+                       g2n, th, seed, tree, block_max, scales, fixed, block_sum);
     hipLaunchKernelGGL(reduce_max_kernel, dim3(1), dim3(1024), 0, s, block_max, n_blocks,
                        block_max + 2 * n_blocks, n, scales);
     hipLaunchKernelGGL(gradient_fixup_kernel, dim3(n_blocks), dim3(256), 0, s, src, y, w, n, mode,
