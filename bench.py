@@ -19,9 +19,10 @@ device syncs. Other workloads (--workload):
 Prints one JSON line:
   value         boosting rounds per second (shap: rows per second)
   roofline      the dominant kernel: histogram algorithmic bytes (cells +
-                the gradient pair it reads (8 B f32 on layouts of <= 4 tiles,
-                else 16 B fixed point) + 4 B row id per accumulated row, + 32 B
-                per written histogram bin) over their HIP-event time, against
+                16 B gradient pair + 4 B row id per accumulated row, + 32 B
+                per written histogram bin; the pair counts 16 B also where the
+                kernel reads 8 B of f32 and quantizes it) over their HIP-event
+                time, against
                 8 TB/s HBM; traffic from the committed rocprofv3 summary
   cpu_baseline  the CPU oracle (C++ restatement of the reference CPU engine)
                 on a bounded sample of the same workload, threads stated

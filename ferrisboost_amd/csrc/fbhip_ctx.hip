@@ -1674,14 +1674,13 @@ void unpack_packets(fbh_ctx *c, uint32_t n, fbh_split *out, uint64_t *cat_words,
     }
 }
 
-// Algorithmic bytes of one histogram launch: cells + the pair it reads (16
-// fixed-point, 8 f32) + row id (4) per accumulated row, and the written
-// histogram (2 x 16 per bin) per node.
+// Algorithmic bytes of one histogram launch: cells + gpair (16) + row id (4)
+// per accumulated row, and the written histogram (2 x 16 per bin) per node.
+// The pair counts as the algorithm's 16-byte fixed-point pair also where the
+// kernel reads it as 8 bytes of f32 and quantizes it in registers.
 void account_hist(fbh_ctx *c, uint64_t acc_rows, uint64_t nodes_with_rows) {
     if (nodes_with_rows == 0) return;
-    const uint64_t pair = c->f32_pairs ? 8 : 16;
-    c->hist_bytes +=
-        acc_rows * (c->hist_row_bytes + pair + 4) + nodes_with_rows * 32 * c->bins_active;
+    c->hist_bytes += acc_rows * (c->hist_row_bytes + 20) + nodes_with_rows * 32 * c->bins_active;
 }
 
 }  // namespace
