@@ -181,9 +181,8 @@ struct fbh_ctx {
     std::vector<uint8_t> uploaded;
 
     float *gpair_f32 = nullptr;
-    // The histograms read gpair_f32 and quantize it under d_scales (half
-    // the bytes of a scattered row) instead of reading gpair; gpair may then
-    // be stale.
+    // gpair_f32 holds the f32 pairs that quantize to gpair under d_scales:
+    // histograms of scattered rows read those instead (half the bytes).
     bool f32_pairs = false;
     // Every tile's workgroup quantizes the pairs it reads again, so f32
     // pairs pay only with few tiles (measured: 2 tiles +3 %, 33 tiles -6 %).
@@ -1204,13 +1203,12 @@ int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th
             // Everything stays on the device: the pairs' quantisation under
             // the previous round's scales, with its block sums, redone only
             // if this round's bounds give other scales. With few tiles the
-            // histograms quantize f32 pairs as they read them: only those
-            // are written; else the fixed-point pairs.
+            // f32 pairs go out too, for the histograms of scattered rows.
             const bool f32 = c->f32_hist();
             check(launch_gradient_spec(c->margin, c->labels, w, c->n_rows,
                                        c->objective == 0 ? 0 : 2, th, seed, tree, c->red_f64,
-                                       c->n_red_blocks, c->d_scales, f32 ? nullptr : c->gpair,
-                                       c->red_i64, f32 ? c->gpair_f32 : nullptr, c->stream),
+                                       c->n_red_blocks, c->d_scales, c->gpair, c->red_i64,
+                                       f32 ? c->gpair_f32 : nullptr, c->stream),
                   "device gradient");
             c->ids_fresh = false;
             c->root_on_device = true;
@@ -1556,7 +1554,10 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
             L.linear = c->chunk_rule(E.host_rule).want_chunks < XCDS ? 1u : 0u;
             L.rows = E.identity ? nullptr : (E.rows ? E.rows : c->rows);
             L.gpair = c->gpair;
-            if (c->f32_pairs) {
+            // Rows in order (the root) read the fixed-point pairs: there
+            // the reads are contiguous and the LDS atomics bound the launch,
+            // which quantizing in registers slowed (210 against 162 us).
+            if (c->f32_pairs && !E.identity) {
                 L.gpair_f32 = c->gpair_f32;
                 L.scales = c->d_scales;
             }

@@ -19,6 +19,7 @@
 
 #include "fb_expf.h"
 #include "fbhip_internal.h"
+#include "fbhip_quant.h"
 
 #include <hip/hip_ext.h>
 
@@ -74,8 +75,6 @@ __device__ __forceinline__ void block_to_work(const HistLaunch &L, uint32_t b, u
     tile_i = k % L.n_tiles;
     chunk = (k / L.n_tiles) * XCDS + xcd;
 }
-
-__device__ __forceinline__ int64_t sat_i64(double x);
 
 __device__ __forceinline__ void lds_add_u64(unsigned long long *p, unsigned long long v) {
     __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -190,11 +189,12 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
     // root before any partition).
     const uint32_t *rows = L.rows ? L.rows + N.row_off : nullptr;
     const longlong2 *gp = reinterpret_cast<const longlong2 *>(L.gpair);
+    // f32 pairs: quantized by shifts (the scales are powers of two).
     const float2 *gf = reinterpret_cast<const float2 *>(L.gpair_f32);
-    double sg = 0.0, sh = 0.0;
+    int lg = 0, lh = 0;
     if (gf) {
-        sg = L.scales->scale[0];
-        sh = L.scales->scale[1];
+        lg = pow2_exponent(L.scales->scale[0]);
+        lh = pow2_exponent(L.scales->scale[1]);
     }
     // The row loop, compiled once per pair format (no per-row branch).
     auto accumulate = [&](auto pair_f32) {
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
         for (uint32_t i = r0 + tid; i < r1; i += TPB * UNROLL) {
             uint32_t row[UNROLL];
             bool ok[UNROLL];
-    #pragma unroll
+#pragma unroll
             for (int u = 0; u < UNROLL; u++) {
                 const uint32_t idx = i + u * TPB;
                 ok[u] = idx < r1;
@@ -211,7 +211,7 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
             longlong2 g[UNROLL];
             float2 f[UNROLL];
             uint32_t rec[UNROLL][RD];
-    #pragma unroll
+#pragma unroll
             for (int u = 0; u < UNROLL; u++) {
                 if (ok[u]) {
                     if constexpr (PF) f[u] = gf[row[u]];
@@ -223,39 +223,38 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
                 } else {
                     f[u] = make_float2(0.0f, 0.0f);
                     g[u] = make_longlong2(0, 0);
-    #pragma unroll
+#pragma unroll
                     for (int d = 0; d < RD; d++) rec[u][d] = 0u;
                 }
             }
             if constexpr (PF) {
-    #pragma unroll
+#pragma unroll
                 for (int u = 0; u < UNROLL; u++)
-                    g[u] = make_longlong2(sat_i64(round((double)f[u].x * sg)),
-                                          sat_i64(round((double)f[u].y * sh)));
+                    g[u] = make_longlong2(quantize_pow2(f[u].x, lg), quantize_pow2(f[u].y, lh));
             }
             if (ROT) {
                 // Rotate each record right by rot bytes: byte k becomes the byte
                 // of feature (k + rot) mod 16.
                 const uint32_t dsh = rot >> 2, bsh = rot & 3u;
-    #pragma unroll
+#pragma unroll
                 for (int u = 0; u < UNROLL; u++) {
                     uint32_t b[4], a[4];
-    #pragma unroll
+#pragma unroll
                     for (int j = 0; j < 4; j++) b[j] = (dsh & 1u) ? rec[u][(j + 1) & 3] : rec[u][j];
-    #pragma unroll
+#pragma unroll
                     for (int j = 0; j < 4; j++) a[j] = (dsh & 2u) ? b[(j + 2) & 3] : b[j];
-    #pragma unroll
+#pragma unroll
                     for (int j = 0; j < 4; j++)
                         rec[u][j] = __builtin_amdgcn_alignbyte(a[(j + 1) & 3], a[j], bsh);
                 }
             }
-    #pragma unroll
+#pragma unroll
             for (int u = 0; u < UNROLL; u++) {
                 const unsigned long long gg = (unsigned long long)g[u].x;
                 const unsigned long long hh = (unsigned long long)g[u].y;
-    #pragma unroll
+#pragma unroll
                 for (int d = 0; d < RD; d++) {
-    #pragma unroll
+#pragma unroll
                     for (int q = 0; q < FPD; q++) {
                         const int fi = d * FPD + q;
                         const uint32_t bin = (rec[u][d] >> (q * 8 * W)) & MASK;
@@ -358,17 +357,17 @@ __global__ __launch_bounds__(HIST_TPB) void hist_global_kernel(const HistLaunch 
     const uint32_t *rows = L.rows ? L.rows + N.row_off : nullptr;
     const longlong2 *gp = reinterpret_cast<const longlong2 *>(L.gpair);
     const float2 *gf = reinterpret_cast<const float2 *>(L.gpair_f32);
-    double sg = 0.0, sh = 0.0;
+    int lg = 0, lh = 0;
     if (gf) {
-        sg = L.scales->scale[0];
-        sh = L.scales->scale[1];
+        lg = pow2_exponent(L.scales->scale[0]);
+        lh = pow2_exponent(L.scales->scale[1]);
     }
     for (uint32_t i = r0 + threadIdx.x; i < r1; i += HIST_TPB) {
         const uint32_t row = rows ? rows[i] : N.row_off + i;
         longlong2 g;
         if (gf) {
             const float2 v = gf[row];
-            g = make_longlong2(sat_i64(round((double)v.x * sg)), sat_i64(round((double)v.y * sh)));
+            g = make_longlong2(quantize_pow2(v.x, lg), quantize_pow2(v.y, lh));
         } else {
             g = gp[row];
         }

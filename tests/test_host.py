@@ -7,7 +7,9 @@
   is a RuntimeError -- the package has no CPU fallback;
 * the product's quantile sketch (the setup step that feeds both engines)
   produces the oracle's cuts bit for bit;
-* bench.py refuses more than one GPU.
+* bench.py refuses more than one GPU;
+* the histograms' shift quantizer of f32 pairs equals the gradient pass's
+  double formula.
 """
 
 from __future__ import annotations
@@ -291,3 +293,67 @@ def test_plan_default_reserve():
     assert p.budget == (100 << 30) - (100 << 30) // 100 * 15
     p = _plan(100_000, 28, free=2 << 30)
     assert p.budget == (2 << 30) - (512 << 20)
+
+
+_QUANT_CHECK = r"""
+#include "fbhip_quant.h"
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+// The gradient pass's formula: round half away from zero of v * 2^l in
+// double, saturated to int64, NaN to 0.
+static int64_t by_double(float v, int l) {
+    double x = std::round(std::ldexp((double)v, l));
+    if (std::isnan(x)) return 0;
+    if (x >= 9223372036854775808.0) return INT64_MAX;
+    if (x < -9223372036854775808.0) return INT64_MIN;
+    return (int64_t)x;
+}
+int main() {
+    const int ls[] = {0, 1, 14, 23, 24, 38, 39, 40, 41, 62, 63, 64, 212, 1000,
+                      -1, -24, -25, -149, -1000};
+    long bad = 0, n = 0;
+    for (int l : ls) {
+        if (fbh::pow2_exponent(std::ldexp(1.0, l)) != l) bad++;
+        // every 251st bit pattern, plus the neighbourhood of every power of two
+        for (uint64_t u = 0; u <= 0xFFFFFFFFull; u += 251) {
+            for (uint32_t d = 0; d < 2; d++) {
+                uint32_t b = (uint32_t)u ^ (d ? 0x80000000u : 0u);
+                float v;
+                memcpy(&v, &b, 4);
+                n++;
+                if (fbh::quantize_pow2(v, l) != by_double(v, l)) bad++;
+            }
+        }
+        for (uint32_t e = 0; e < 256; e++)
+            for (int k = -3; k <= 3; k++)
+                for (uint32_t sgn = 0; sgn < 2; sgn++) {
+                    uint32_t b = ((e << 23) + (uint32_t)k) ^ (sgn << 31);
+                    float v;
+                    memcpy(&v, &b, 4);
+                    n++;
+                    if (fbh::quantize_pow2(v, l) != by_double(v, l)) bad++;
+                }
+    }
+    printf("%ld %ld\n", n, bad);
+    return bad != 0;
+}
+"""
+
+
+def test_shift_quantizer_equals_the_double_formula(tmp_path):
+    """The histograms' integer quantisation of f32 pairs (fbhip_quant.h) gives
+    sat_i64(round((double)v * 2^l)), the gradient pass's value
+    (GradQuantizer::to_fixed, src/types.rs:367-385), for the scales 2^l the
+    quantizer makes: sampled bit patterns of both signs and every exponent's
+    neighbourhood (zeros, subnormals, infinities, NaNs, the 2^63 saturation
+    edge) at shifts from -1000 to 1000. Built from the product header with
+    the host compiler."""
+    src = tmp_path / "quant_check.cpp"
+    src.write_text(_QUANT_CHECK)
+    exe = tmp_path / "quant_check"
+    inc = os.path.join(ROOT, "ferrisboost_amd", "csrc")
+    subprocess.run(["g++", "-O2", "-std=c++17", "-I", inc, str(src), "-o", str(exe)], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    n, bad = map(int, r.stdout.split())
+    assert n > 600_000_000 // 2 and bad == 0, r.stdout
