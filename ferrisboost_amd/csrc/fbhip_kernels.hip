@@ -196,6 +196,12 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
         lg = pow2_exponent(L.scales->scale[0]);
         lh = pow2_exponent(L.scales->scale[1]);
     }
+    // Interleaved layout: the gradient plane plus 8 bytes per slot of the
+    // feature the lane takes at step k, (k + rot) mod 16.
+    char *fptr[NF];
+#pragma unroll
+    for (int k = 0; k < NF; k++)
+        fptr[k] = reinterpret_cast<char *>(gplane) + ((((uint32_t)k + rot) & 15u) << 3);
     // The row loop, compiled once per pair format (no per-row branch).
     auto accumulate = [&](auto pair_f32) {
         constexpr bool PF = decltype(pair_f32)::value;
@@ -261,9 +267,14 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
                         uint32_t s;
                         if (ROT) {
                             // Features outside the tile or not built this tree
-                            // have nb 0 and add into the lane's dummy.
-                            const uint32_t feat = ((uint32_t)fi + rot) & 15u;
-                            s = (bin < nb[fi] ? bin << 4 : dummy) + feat;
+                            // have nb 0 and add into the lane's dummy. Slot
+                            // bin * 16 + feat (or the dummy's) in bytes, from
+                            // the step's feature pointer.
+                            unsigned long long *p = reinterpret_cast<unsigned long long *>(
+                                fptr[fi] + (bin < nb[fi] ? bin << 7 : dummy << 3));
+                            lds_add_u64(p, gg);
+                            lds_add_u64(p + S, hh);
+                            continue;
                         } else {
                             if (fi >= (int)T.n_feat) continue;  // uniform
                             if (nb[fi] == 0) continue;  // not built this tree (uniform)
