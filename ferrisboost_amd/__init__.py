@@ -197,13 +197,34 @@ def _params_struct(p: dict[str, Any], n_features: int) -> N.TrainParams:
     return s
 
 
-class Model:
-    """A trained model (Model, src/model/tree.rs:213-290)."""
+_F32_MAX = float(np.finfo(np.float32).max)
+_IMPORTANCE = ("weight", "gain", "cover", "total_gain", "total_cover")
 
-    def __init__(self, handle, n_features: int, objective: str):
+
+def _validate_missing(value) -> float:
+    """validate_missing (src/source/mod.rs): NaN or a finite float32 other
+    than the reserved largest float32."""
+    v = float(value)
+    if np.isnan(v):
+        return float("nan")
+    with np.errstate(over="ignore"):
+        f = np.float32(v)
+    if not np.isfinite(f):
+        raise ValueError(f"missing must be NaN or a finite float32, got {value!r}")
+    if abs(float(f)) == _F32_MAX:
+        raise ValueError("missing must not be the largest float32 (it is reserved for split boundaries)")
+    return float(f)
+
+
+class Model:
+    """A trained or loaded model (Model, src/model/tree.rs:213-290; the
+    Python class of python/ferrisboost/_core.pyi:55-265)."""
+
+    def __init__(self, handle, n_features: int, objective: str, device: int = 0):
         self._h = handle
-        self.n_features = n_features
-        self.objective = objective
+        self._n_features = n_features
+        self._objective = objective
+        self._device = device
         self.stats: dict[str, float] = {}
 
     def __del__(self):
@@ -212,9 +233,41 @@ class Model:
             N.train_lib().fbt_model_free(h)
             self._h = None
 
+    # ---- properties of python/ferrisboost/_core.pyi:55-80
+    @property
+    def n_features(self) -> int:
+        return self._n_features
+
+    @property
+    def objective(self) -> str:
+        return self._objective
+
     @property
     def num_trees(self) -> int:
         return N.train_lib().fbt_model_n_trees(self._h)
+
+    @property
+    def num_class(self) -> int:
+        return 1
+
+    @property
+    def feature_names(self) -> list[str]:
+        return []
+
+    @property
+    def quantile_alpha(self):
+        return None
+
+    @property
+    def best_iteration(self):
+        return None
+
+    @property
+    def best_score(self):
+        return None
+
+    def evals_result(self) -> dict:
+        return {}
 
     @property
     def base_score(self) -> float:
@@ -223,6 +276,10 @@ class Model:
     @property
     def base_margin(self) -> float:
         return N.train_lib().fbt_model_base_margin(self._h)
+
+    @property
+    def scale_pos_weight(self) -> float:
+        return N.train_lib().fbt_model_scale_pos_weight(self._h)
 
     def tree_nodes(self, t: int) -> np.ndarray:
         L = N.train_lib()
@@ -253,24 +310,130 @@ class Model:
         N.check_train(N.train_lib().fbt_model_train_margins(self._h, N.ptr(out), n_rows))
         return out
 
-    def predict(self, X, output_margin: bool = False, pred_contribs: bool = False,
-                device: str | None = "cuda") -> np.ndarray:
-        """Margins (output_margin=True), probabilities / values, or SHAP
-        contributions [n_rows, n_features + 1] with the bias last
-        (pred_contribs=True, computed on the device)."""
-        X = np.ascontiguousarray(X, np.float32)
+    # ---- prediction and explanation
+    def _tree_range(self, n_trees, iteration_range) -> tuple[int, int]:
+        total = self.num_trees
+        if iteration_range is not None:
+            if n_trees is not None:
+                raise ValueError("iteration_range and n_trees cannot both be given: the former "
+                                 "counts rounds, the latter counts trees")
+            begin, end = (int(v) for v in iteration_range)
+            if begin < 0 or end < 0:
+                raise ValueError("iteration_range bounds must be non-negative")
+            end = total if end == 0 else end
+            if end > total:
+                raise ValueError(f"iteration_range end = {end} exceeds the model's {total} rounds")
+            if begin > end:
+                raise ValueError(f"iteration_range begin = {begin} is greater than end = {end}")
+            return begin, end
+        if n_trees is None:
+            return 0, total
+        if int(n_trees) < 0:
+            raise ValueError("n_trees must be non-negative")
+        return 0, min(int(n_trees), total)
+
+    def predict(self, data, output_margin: bool = False, n_trees: int | None = None,
+                header: bool = True, *, predict_threads: int = 0, use_gpu: bool = True,
+                iteration_range: tuple[int, int] | None = None, pred_contribs: bool = False,
+                approx_contribs: bool = False, pred_interactions: bool = False,
+                pred_leaf: bool = False, missing: float = float("nan"), base_margin=None,
+                strict_shape: bool = False, device: str | None = None) -> np.ndarray:
+        """Model.predict (python/ferrisboost/_core.pyi:94-197).
+
+        Margins (output_margin=True) or probabilities / values, in float32,
+        over every tree or the trees n_trees / iteration_range select.
+        Explanations, at most one per call and not with output_margin:
+        pred_contribs (TreeSHAP, (n, F + 1), bias last; with approx_contribs
+        the Saabas attribution), pred_interactions ((n, F + 1, F + 1)) and
+        pred_leaf ((n, trees) leaf ids). base_margin replaces the intercept
+        per row (and the bias of explanations); missing marks values scored
+        as NaN; strict_shape adds the output-group axis.
+
+        Explanations and, with use_gpu=True (the default on this device
+        path), margins and values run on the GPU (`device`, default the
+        training device); use_gpu=False scores margins and values on the
+        host. Every result equals the reference CPU engine's bit for bit.
+        """
+        del header, predict_threads  # file inputs and CPU worker counts do not apply
+        if isinstance(data, (str, bytes)) or hasattr(data, "__fspath__") or (
+                isinstance(data, (list, tuple)) and data and isinstance(data[0], (str, bytes))):
+            raise ValueError("file inputs are not available on the ferrisboost_amd device path; "
+                             "pass an array")
+        kinds = [pred_contribs, pred_interactions, pred_leaf]
+        if sum(bool(k) for k in kinds) > 1:
+            raise ValueError("pred_contribs, pred_interactions and pred_leaf are exclusive: one "
+                             "type of prediction at a time")
+        if approx_contribs and pred_interactions:
+            raise ValueError("approx_contribs cannot be combined with pred_interactions")
+        explain = any(kinds)
+        if explain and output_margin:
+            raise ValueError("output_margin cannot be combined with pred_contribs / "
+                             "pred_interactions / pred_leaf: one type of prediction at a time")
+        X = np.asarray(data, dtype=np.float32)
         if X.ndim != 2 or X.shape[1] != self.n_features:
-            raise ValueError(f"expected a 2-D array with {self.n_features} columns")
-        if pred_contribs:
-            out = np.zeros((X.shape[0], self.n_features + 1), np.float32)
-            N.check_train(N.train_lib().fbt_shap(self._h, N.ptr(X), X.shape[0], X.shape[1],
-                                                 _parse_device(device), N.ptr(out)))
-            return out
-        out = np.zeros(X.shape[0], np.float32)
-        N.train_lib().fbt_predict_margin(self._h, N.ptr(X), X.shape[0], X.shape[1], N.ptr(out))
-        if output_margin or self.objective == "reg:squarederror":
-            return out
-        return (1.0 / (1.0 + np.exp(-out))).astype(np.float32)
+            raise ValueError(f"expected a 2-D array with {self.n_features} columns, got shape "
+                             f"{X.shape}")
+        X = np.ascontiguousarray(X)
+        miss = _validate_missing(missing)
+        if not np.isnan(miss):
+            X = np.where(X == np.float32(miss), np.float32("nan"), X).astype(np.float32)
+        n = X.shape[0]
+        bm = None
+        if base_margin is not None:
+            bm = np.ascontiguousarray(np.asarray(base_margin, dtype=np.float32).reshape(-1))
+            if bm.shape != (n,):
+                raise ValueError(f"base_margin has {bm.size} values, expected {n} rows x 1 outputs")
+        b, e = self._tree_range(n_trees, iteration_range)
+        dev = _parse_device(device) if device is not None else self._device
+        if pred_leaf:
+            kind, shape = N.OUT_LEAF, (n, e - b)
+        elif pred_interactions:
+            kind, shape = N.OUT_INTERACTIONS, (n, self.n_features + 1, self.n_features + 1)
+        elif pred_contribs:
+            kind = N.OUT_APPROX if approx_contribs else N.OUT_CONTRIBS
+            shape = (n, self.n_features + 1)
+        else:
+            kind = N.OUT_MARGIN if output_margin else N.OUT_VALUE
+            shape = (n,)
+            if not use_gpu:
+                dev = -1
+        out = np.zeros(shape, np.float32)
+        N.check_train(N.train_lib().fbt_predict(self._h, N.ptr(X), n, self.n_features, kind, b, e,
+                                                N.ptr(bm), dev, N.ptr(out)))
+        if strict_shape:
+            if pred_leaf:
+                out = out.reshape(n, e - b, 1, 1)
+            else:
+                out = out.reshape((n, 1) + out.shape[1:])
+        return out
+
+    def get_score(self, importance_type: str = "weight") -> dict[str, float]:
+        """Feature importance as XGBoost's Booster.get_score (feature_scores,
+        src/model/explain.rs:57-114): split counts, or the gain / cover of
+        the splits, averaged per split or summed."""
+        if importance_type not in _IMPORTANCE:
+            raise ValueError(f"importance_type must be one of {', '.join(_IMPORTANCE)}, got "
+                             f"{importance_type!r}")
+        count = np.zeros(self.n_features, np.float64)
+        gain = np.zeros(self.n_features, np.float64)
+        cover = np.zeros(self.n_features, np.float64)
+        for t in self.trees():
+            for nd in t[t["is_leaf"] == 0]:
+                f = int(nd["feat"])
+                count[f] += 1
+                gain[f] += float(nd["gain"])
+                cover[f] += float(nd["sum_hess"])
+        out = {}
+        for f in range(self.n_features):
+            if count[f] == 0:
+                continue
+            v = {"weight": count[f], "gain": gain[f] / count[f], "cover": cover[f] / count[f],
+                 "total_gain": gain[f], "total_cover": cover[f]}[importance_type]
+            out[f"f{f}"] = float(v)
+        return out
+
+    def get_categories(self):
+        return None
 
     def to_json(self) -> str:
         L = N.train_lib()
@@ -279,9 +442,31 @@ class Model:
         L.fbt_model_to_json(self._h, buf, n + 1)
         return buf.value.decode()
 
-    def save_model(self, path: str) -> None:
+    def save_model(self, path: str, quiet: bool | None = None,
+                   model_io_threads: int | None = None) -> None:
+        """XGBoost-compatible JSON (Model::to_xgboost_json, src/model/tree.rs:600-752)."""
+        del quiet, model_io_threads
         with open(path, "w") as f:
             f.write(self.to_json())
+
+    @staticmethod
+    def load_model(path: str, quiet: bool = False, model_io_threads: int = 0,
+                   ingest_threads: int = 0, device: str | None = None) -> "Model":
+        """XGBoost-compatible JSON (Model::from_xgboost_json,
+        src/model/tree.rs:754-990): binary:logistic and reg:squarederror
+        models load; anything the reader cannot represent is a ValueError."""
+        del quiet, model_io_threads, ingest_threads
+        with open(path, "rb") as f:
+            return Model.from_json(f.read(), device=device)
+
+    @staticmethod
+    def from_json(text, device: str | None = None) -> "Model":
+        raw = text.encode() if isinstance(text, str) else bytes(text)
+        L = N.train_lib()
+        h = C.c_void_p()
+        N.check_train(L.fbt_model_from_json(raw, len(raw), C.byref(h)))
+        obj = {0: "reg:squarederror", 1: "binary:logistic"}[L.fbt_model_objective(h)]
+        return Model(h, L.fbt_model_n_features(h), obj, _parse_device(device))
 
 
 def train(params: Mapping[str, Any], X, label, weight=None, num_boost_round: int = 10) -> Model:
@@ -317,7 +502,7 @@ def train(params: Mapping[str, Any], X, label, weight=None, num_boost_round: int
     N.check_train(N.train_lib().fbt_train(
         N.ptr(X), X.shape[0], X.shape[1], N.ptr(y), N.ptr(w), N.ptr(cat), N.ptr(mono),
         0 if mono is None else mono.size, C.byref(s), C.byref(h)))
-    m = Model(h, X.shape[1], p["objective"])
+    m = Model(h, X.shape[1], p["objective"], s.device)
     st = N.Stats()
     N.check_train(N.train_lib().fbt_last_stats(C.byref(st)))
     m.stats = {k: getattr(st, k) for k, _ in N.Stats._fields_ if k != "reserved"}

@@ -208,14 +208,17 @@ HIP_SYMBOLS = [
     "fbh_host_free", "fbh_download_rows",
     "fbh_hist_timing", "fbh_set_timing", "fbh_build_histogram", "fbh_partition_rows",
     "fbh_shap_model_create", "fbh_shap_model_destroy", "fbh_shap_contribs",
-    "fbh_shap_contribs_device", "fbh_shap_last_ms",
+    "fbh_shap_contribs_device", "fbh_shap_last_ms", "fbh_shap_interactions",
+    "fbh_saabas_contribs", "fbh_predict", "fbh_predict_device",
 ]
 TRAIN_SYMBOLS = [
     "fbt_last_error", "fbt_train", "fbt_last_stats", "fbt_last_round_stats", "fbt_model_free", "fbt_model_n_trees",
     "fbt_model_tree_len", "fbt_model_tree_nodes", "fbt_model_n_cat_words", "fbt_model_cat_words",
     "fbt_model_base_score", "fbt_model_base_margin", "fbt_model_n_features",
     "fbt_model_train_margins", "fbt_model_n_cuts", "fbt_model_cuts", "fbt_predict_margin",
-    "fbt_model_to_json", "fbt_shap", "fbt_last_shap_ms", "fbt_sketch_cuts",
+    "fbt_model_to_json", "fbt_shap", "fbt_last_shap_ms", "fbt_sketch_cuts", "fbt_predict",
+    "fbt_model_from_json", "fbt_model_objective", "fbt_model_scale_pos_weight",
+    "fbt_model_is_categorical",
 ]
 
 _hip = None
@@ -290,6 +293,10 @@ def hip() -> C.CDLL:
         L.fbh_shap_contribs_device.argtypes = [P, P, C.c_uint64, P, P, C.c_int]
         L.fbh_shap_last_ms.argtypes = [P]
         L.fbh_shap_last_ms.restype = C.c_double
+        for name in ("fbh_shap_interactions", "fbh_saabas_contribs"):
+            getattr(L, name).argtypes = [P, P, C.c_uint64, P, P]
+        L.fbh_predict.argtypes = [P, P, C.c_uint64, P, C.c_uint32, P]
+        L.fbh_predict_device.argtypes = [P, P, C.c_uint64, P, C.c_uint32, P, C.c_int]
         _hip = L
     return _hip
 
@@ -334,8 +341,21 @@ def train_lib() -> C.CDLL:
         L.fbt_sketch_cuts.argtypes = [P, C.c_uint64, C.c_uint32, C.c_uint32, P, P, P, P]
         L.fbt_last_shap_ms.argtypes = []
         L.fbt_last_shap_ms.restype = C.c_double
+        L.fbt_predict.argtypes = [P, P, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32,
+                                  C.c_uint32, P, C.c_int, P]
+        L.fbt_model_from_json.argtypes = [C.c_char_p, C.c_size_t, C.POINTER(P)]
+        L.fbt_model_objective.argtypes = [P]
+        L.fbt_model_objective.restype = C.c_uint32
+        L.fbt_model_scale_pos_weight.argtypes = [P]
+        L.fbt_model_scale_pos_weight.restype = C.c_float
+        L.fbt_model_is_categorical.argtypes = [P, C.c_uint32]
+        L.fbt_model_is_categorical.restype = C.c_uint32
         _train = L
     return _train
+
+
+# fbt_predict outputs (include/fbtrain.h).
+OUT_MARGIN, OUT_VALUE, OUT_LEAF, OUT_CONTRIBS, OUT_APPROX, OUT_INTERACTIONS = range(6)
 
 
 def ptr(a):

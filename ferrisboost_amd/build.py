@@ -35,7 +35,7 @@ HIP_FLAGS = [
 ]
 
 BACKEND_SRCS = ["fbhip_kernels.hip", "fbhip_ctx.hip", "fbhip_shap.hip"]
-DRIVER_SRCS = ["fbt_data.cpp", "fbt_train.cpp", "fbt_model.cpp", "fbt_api.cpp"]
+DRIVER_SRCS = ["fbt_data.cpp", "fbt_train.cpp", "fbt_model.cpp", "fbt_json.cpp", "fbt_api.cpp"]
 
 LIB_HIP = os.path.join(HERE, "libfbhip.so")
 LIB_TRAIN = os.path.join(HERE, "libfbtrain.so")

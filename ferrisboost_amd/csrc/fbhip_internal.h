@@ -440,11 +440,5 @@ hipError_t launch_pack_feature(const uint8_t *col, uint64_t n_rows, uint32_t wid
 constexpr uint32_t MAX_DEVICE_CATS = 4096;
 // Distinct split features of one tree the TreeSHAP kernel accepts.
 constexpr uint32_t MAX_SHAP_UNIQUE = 1024;
-hipError_t launch_shap(const ShapNodeDev *nodes, const uint32_t *tree_roots, uint32_t n_trees,
-                       const uint32_t *tree_ufeat_off, const uint32_t *ufeats,
-                       const uint32_t *cat_words, const float *rule, const float *rows,
-                       uint64_t n_rows, uint32_t n_features, const float *margin, float bias,
-                       float root_mean, float *out, uint32_t max_unique, uint32_t max_depth,
-                       hipStream_t s);
 
 }  // namespace fbh

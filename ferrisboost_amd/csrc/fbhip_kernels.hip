@@ -2358,191 +2358,6 @@ hipError_t launch_pack_feature(const uint8_t *col, uint64_t n_rows, uint32_t wid
 }
 
 // ======================================================================
-// QuadratureTreeSHAP
-// ======================================================================
-
-constexpr int QP = 8;          // quadrature points
-constexpr float UNSEEN = -999.0f;
-constexpr int SHAP_MAXD = 16;  // path frames (max_depth <= 14)
-constexpr int SHAP_TPB = 128;
-
-__device__ __forceinline__ bool shap_goes_left(const ShapNodeDev &n, float v,
-                                               const uint32_t *cat_words) {
-    if (isnan(v)) return (n.flags & 2u) != 0;
-    if (n.flags & 4u) {
-        if (v < 0.0f || v >= 16777216.0f) return true;
-        const uint32_t cat = (uint32_t)v;
-        const uint32_t word = cat / 32;
-        if (word >= n.cat_len) return true;
-        return ((cat_words[n.cat_offset + word] >> (cat % 32)) & 1u) == 0;
-    }
-    return v < n.split_cond;
-}
-
-// One thread per row: every tree's QuadratureTreeSHAP with the recursion of
-// Runner::run_node / visit_child unrolled onto an explicit path stack, in
-// the host's exact float32 operation order.
-template <int MAXU>
-__global__ __launch_bounds__(SHAP_TPB) void shap_kernel(
-    const ShapNodeDev *nodes, const uint32_t *tree_roots, uint32_t n_trees,
-    const uint32_t *tree_ufeat_off, const uint32_t *ufeats, const uint32_t *cat_words,
-    const float *rule, const float *rows, uint64_t n_rows, uint32_t n_features,
-    const float *margin, float bias, float root_mean, float *out) {
-    const uint64_t row = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (row >= n_rows) return;
-    float rn[QP], rw[QP];
-#pragma unroll
-    for (int i = 0; i < QP; i++) {
-        rn[i] = rule[i];
-        rw[i] = rule[QP + i];
-    }
-    const float *x = rows + row * n_features;
-    float *p = out + row * (uint64_t)(n_features + 1);
-    for (uint32_t f = 0; f <= n_features; f++) p[f] = 0.0f;
-
-    float tc[MAXU];
-    float c[SHAP_MAXD][QP];
-    float hl[SHAP_MAXD][QP];
-    float wprod[SHAP_MAXD];
-    float pe[SHAP_MAXD], pold[SHAP_MAXD];
-    uint32_t nid[SHAP_MAXD], pfeat[SHAP_MAXD];
-    uint8_t stage[SHAP_MAXD], gl[SHAP_MAXD];
-
-    for (uint32_t t = 0; t < n_trees; t++) {
-        const uint32_t root = tree_roots[t];
-        const uint32_t u0 = tree_ufeat_off[t], nu = tree_ufeat_off[t + 1] - u0;
-        if (nodes[root].flags & 1u) continue;  // a leaf-only tree contributes nothing
-        for (uint32_t u = 0; u < nu; u++) tc[u] = 0.0f;
-        int d = 0;
-        nid[0] = root;
-        wprod[0] = 1.0f;
-#pragma unroll
-        for (int i = 0; i < QP; i++) c[0][i] = 1.0f;
-        stage[0] = 0;
-        {
-            const ShapNodeDev &n0 = nodes[root];
-            gl[0] = shap_goes_left(n0, x[n0.feat], cat_words);
-        }
-        float ret[QP];
-        for (;;) {
-            const ShapNodeDev &n = nodes[nid[d]];
-            // Begin the visit of the next child of frame d.
-            const bool right = stage[d] != 0;
-            const uint32_t child = (uint32_t)(right ? n.right : n.left);
-            const float cw = right ? n.right_weight : n.left_weight;
-            const bool sat = right ? !gl[d] : (gl[d] != 0);
-            const uint32_t feat = n.feat;
-            float p_old = UNSEEN;
-            for (int k = d - 1; k >= 0; k--)
-                if (pfeat[k] == feat) {
-                    p_old = pe[k];
-                    break;
-                }
-            const float p_e = sat ? (p_old == UNSEEN ? 1.0f / cw : p_old / cw) : 0.0f;
-            float cc[QP];
-            const float ae = p_e - 1.0f;
-#pragma unroll
-            for (int i = 0; i < QP; i++) {
-                const float m = 1.0f + ae * rn[i];
-                cc[i] = c[d][i] * m;
-            }
-            if (p_old != UNSEEN) {
-                const float ao = p_old - 1.0f;
-                if (ao != 0.0f) {
-#pragma unroll
-                    for (int i = 0; i < QP; i++) cc[i] /= 1.0f + ao * rn[i];
-                }
-            }
-            pfeat[d] = feat;
-            pe[d] = p_e;
-            pold[d] = p_old;
-            const float wchild = wprod[d] * cw;
-            const ShapNodeDev &cn = nodes[child];
-            if (!(cn.flags & 1u)) {
-                // descend
-                d++;
-                nid[d] = child;
-                wprod[d] = wchild;
-#pragma unroll
-                for (int i = 0; i < QP; i++) c[d][i] = cc[i];
-                stage[d] = 0;
-                gl[d] = shap_goes_left(cn, x[cn.feat], cat_words);
-                continue;
-            }
-            const float ls = wchild * cn.leaf_value;
-#pragma unroll
-            for (int i = 0; i < QP; i++) {
-                const float a = cc[i] * ls;
-                ret[i] = a * rw[i];
-            }
-            // Finish visits upward while frames complete.
-            for (;;) {
-                // extract_delta (explain.rs:225-240) for the visit of frame d.
-                const float pen = pe[d];
-                const float px = pold[d] == UNSEEN ? 1.0f : pold[d];
-                float acc = 0.0f;
-                if (pen != 1.0f) {
-                    const float a = pen - 1.0f;
-#pragma unroll
-                    for (int i = 0; i < QP; i++) {
-                        const float num = a * ret[i];
-                        const float den = 1.0f + a * rn[i];
-                        acc += num / den;
-                    }
-                }
-                if (px != 1.0f) {
-                    const float a = px - 1.0f;
-#pragma unroll
-                    for (int i = 0; i < QP; i++) {
-                        const float num = a * ret[i];
-                        const float den = 1.0f + a * rn[i];
-                        acc -= num / den;
-                    }
-                }
-                const uint32_t us = nodes[nid[d]].uslot;
-                tc[us] += acc;
-                if (stage[d] == 0) {
-#pragma unroll
-                    for (int i = 0; i < QP; i++) hl[d][i] = ret[i];
-                    stage[d] = 1;
-                    break;  // begin the right visit of frame d
-                }
-#pragma unroll
-                for (int i = 0; i < QP; i++) ret[i] = hl[d][i] + ret[i];
-                if (d == 0) goto tree_done;
-                d--;
-            }
-        }
-    tree_done:
-        for (uint32_t u = 0; u < nu; u++) p[ufeats[u0 + u]] += tc[u];
-    }
-    p[n_features] += root_mean;
-    p[n_features] += margin ? margin[row] : bias;
-}
-
-hipError_t launch_shap(const ShapNodeDev *nodes, const uint32_t *tree_roots, uint32_t n_trees,
-                       const uint32_t *tree_ufeat_off, const uint32_t *ufeats,
-                       const uint32_t *cat_words, const float *rule, const float *rows,
-                       uint64_t n_rows, uint32_t n_features, const float *margin, float bias,
-                       float root_mean, float *out, uint32_t max_unique, uint32_t max_depth,
-                       hipStream_t s) {
-    if (n_rows == 0) return hipSuccess;
-    if (max_depth > SHAP_MAXD) return hipErrorInvalidValue;
-    const uint32_t blocks = (uint32_t)((n_rows + SHAP_TPB - 1) / SHAP_TPB);
-#define FBH_SHAP_CASE(U)                                                                         \
-    if (max_unique <= U) {                                                                       \
-        hipLaunchKernelGGL(shap_kernel<U>, dim3(blocks), dim3(SHAP_TPB), 0, s, nodes,           \
-                           tree_roots, n_trees, tree_ufeat_off, ufeats, cat_words, rule, rows,  \
-                           n_rows, n_features, margin, bias, root_mean, out);                    \
-        return hipGetLastError();                                                               \
-    }
-    FBH_SHAP_CASE(32) FBH_SHAP_CASE(64) FBH_SHAP_CASE(128) FBH_SHAP_CASE(256)
-    FBH_SHAP_CASE(1024)
-#undef FBH_SHAP_CASE
-    return hipErrorInvalidValue;
-}
-
-// ======================================================================
 // device-grown depthwise trees
 // ======================================================================
 // The host enqueues every level of a depthwise tree without waiting: each

@@ -1,6 +1,8 @@
 // fbt_api.cpp -- C ABI of the round driver (include/fbtrain.h).
 
+#include <cmath>
 #include <cstring>
+#include <limits>
 #include <memory>
 #include <string>
 
@@ -160,54 +162,141 @@ size_t fbt_model_to_json(const fbt_model *m, char *buf, size_t len) {
     return s.size();
 }
 
+}  // extern "C"
+
+namespace {
+
+// The device explanation model of trees [begin, end) (GpuExplainModel::new,
+// src/backend/cuda/explain.rs:186-490, over the model slice that
+// iteration_range selects, src/python/mod.rs:1993-2029).
+using ShapModel = std::unique_ptr<fbh_shap_model, int (*)(fbh_shap_model *)>;
+
+void backend_fail(int rc) {
+    char buf[1024];
+    fbh_last_error(buf, sizeof(buf));
+    if (rc == FBH_INPUT_ERROR) throw fbt::InputError(buf);
+    throw fbt::RuntimeError(buf);
+}
+
+ShapModel explain_model(const fbt::Model &m, uint32_t begin, uint32_t end, int device) {
+    std::vector<uint32_t> offs{0}, feat, cat_off, cat_len, words;
+    std::vector<float> cond, leaf, hess;
+    std::vector<int32_t> left, right;
+    std::vector<uint8_t> dl, is_leaf;
+    for (uint32_t t = begin; t < end; t++) {
+        for (const auto &n : m.trees[t].nodes) {
+            feat.push_back(n.feat);
+            cond.push_back(n.split_cond);
+            left.push_back(n.left);
+            right.push_back(n.right);
+            dl.push_back(n.default_left);
+            is_leaf.push_back(n.is_leaf);
+            leaf.push_back(n.leaf_value);
+            hess.push_back(n.sum_hess);
+            cat_off.push_back((uint32_t)words.size());
+            cat_len.push_back(n.is_leaf ? 0u : (uint32_t)n.cats.size());
+            if (!n.is_leaf) words.insert(words.end(), n.cats.begin(), n.cats.end());
+        }
+        offs.push_back((uint32_t)feat.size());
+    }
+    fbh_shap_model *sm = nullptr;
+    const int rc = fbh_shap_model_create(device, end - begin, offs.data(), feat.data(), cond.data(),
+                                         left.data(), right.data(), dl.data(), is_leaf.data(),
+                                         leaf.data(), hess.data(), cat_off.data(), cat_len.data(),
+                                         words.data(), (uint32_t)words.size(), m.n_features,
+                                         m.base_margin(), &sm);
+    if (rc) backend_fail(rc);
+    return ShapModel(sm, fbh_shap_model_destroy);
+}
+
+}  // namespace
+
+extern "C" {
+
 int fbt_shap(const fbt_model *mm, const float *x, uint64_t n_rows, uint32_t n_features,
              int device, float *out) {
+    return fbt_predict(mm, x, n_rows, n_features, FBT_OUT_CONTRIBS, 0,
+                       mm ? (uint32_t)mm->m.trees.size() : 0, nullptr, device, out);
+}
+
+int fbt_predict(const fbt_model *mm, const float *x, uint64_t n_rows, uint32_t n_features,
+                uint32_t output, uint32_t tree_begin, uint32_t tree_end, const float *base_margin,
+                int device, float *out) {
     return guard([&] {
-        if (!mm || !x || !out) throw fbt::InputError("null argument");
+        if (!mm || (!x && n_rows) || (!out && n_rows)) throw fbt::InputError("null argument");
         const fbt::Model &m = mm->m;
         if (n_features != m.n_features)
             throw fbt::InputError("expected " + std::to_string(m.n_features) + " features, got " +
                                   std::to_string(n_features));
-        std::vector<uint32_t> offs{0}, feat, cat_off, cat_len, words;
-        std::vector<float> cond, leaf, hess;
-        std::vector<int32_t> left, right;
-        std::vector<uint8_t> dl, is_leaf;
-        for (const auto &t : m.trees) {
-            for (const auto &n : t.nodes) {
-                feat.push_back(n.feat);
-                cond.push_back(n.split_cond);
-                left.push_back(n.left);
-                right.push_back(n.right);
-                dl.push_back(n.default_left);
-                is_leaf.push_back(n.is_leaf);
-                leaf.push_back(n.leaf_value);
-                hess.push_back(n.sum_hess);
-                cat_off.push_back((uint32_t)words.size());
-                cat_len.push_back((uint32_t)n.cats.size());
-                words.insert(words.end(), n.cats.begin(), n.cats.end());
+        if (output > FBT_OUT_INTERACTIONS) throw fbt::InputError("unknown prediction output");
+        if (tree_begin > tree_end || tree_end > m.trees.size())
+            throw fbt::InputError("tree range [" + std::to_string(tree_begin) + ", " +
+                                  std::to_string(tree_end) + ") is outside the model's " +
+                                  std::to_string(m.trees.size()) + " trees");
+        // Feature values equal to f32::MAX are reserved for split boundaries
+        // (src/model/tree.rs:985-990) and rejected, as in training.
+        const uint64_t cells = n_rows * (uint64_t)n_features;
+        for (uint64_t i = 0; i < cells; i++)
+            if (x[i] == std::numeric_limits<float>::max())
+                throw fbt::InputError(
+                    "feature values equal to the largest float32 (3.4028235e38) are reserved "
+                    "and cannot be scored");
+        const bool logistic = m.objective == 1;
+        if (device < 0) {
+            // Host scoring (use_gpu=False): Model::predict_margin_upto and the
+            // objective's transform with the host libm.
+            if (output != FBT_OUT_MARGIN && output != FBT_OUT_VALUE)
+                throw fbt::InputError("explanations run on the device; pass a device index");
+            const float bm = m.base_margin();
+            for (uint64_t r = 0; r < n_rows; r++) {
+                float acc = base_margin ? base_margin[r] : bm;
+                for (uint32_t t = tree_begin; t < tree_end; t++) acc += m.trees[t].leaf_value(x + r * n_features);
+                out[r] = output == FBT_OUT_VALUE && logistic ? 1.0f / (1.0f + std::exp(-acc)) : acc;
             }
-            offs.push_back((uint32_t)feat.size());
+            return;
         }
-        fbh_shap_model *sm = nullptr;
-        char buf[1024];
-        int rc = fbh_shap_model_create(device, (uint32_t)m.trees.size(), offs.data(), feat.data(),
-                                       cond.data(), left.data(), right.data(), dl.data(),
-                                       is_leaf.data(), leaf.data(), hess.data(), cat_off.data(),
-                                       cat_len.data(), words.data(), (uint32_t)words.size(),
-                                       n_features, m.base_margin(), &sm);
-        if (rc) {
-            fbh_last_error(buf, sizeof(buf));
-            if (rc == FBH_INPUT_ERROR) throw fbt::InputError(buf);
-            throw fbt::RuntimeError(buf);
+        ShapModel sm = explain_model(m, tree_begin, tree_end, device);
+        int rc = FBH_OK;
+        switch (output) {
+            case FBT_OUT_MARGIN:
+                rc = fbh_predict(sm.get(), x, n_rows, base_margin, FBH_PREDICT_MARGIN, out);
+                break;
+            case FBT_OUT_VALUE:
+                rc = fbh_predict(sm.get(), x, n_rows, base_margin,
+                                 logistic ? FBH_PREDICT_SIGMOID : FBH_PREDICT_MARGIN, out);
+                break;
+            case FBT_OUT_LEAF:
+                rc = fbh_predict(sm.get(), x, n_rows, nullptr, FBH_PREDICT_LEAF, out);
+                break;
+            case FBT_OUT_CONTRIBS:
+                rc = fbh_shap_contribs(sm.get(), x, n_rows, base_margin, out);
+                break;
+            case FBT_OUT_APPROX_CONTRIBS:
+                rc = fbh_saabas_contribs(sm.get(), x, n_rows, base_margin, out);
+                break;
+            default:
+                rc = fbh_shap_interactions(sm.get(), x, n_rows, base_margin, out);
+                break;
         }
-        std::unique_ptr<fbh_shap_model, int (*)(fbh_shap_model *)> own(sm, fbh_shap_model_destroy);
-        rc = fbh_shap_contribs(sm, x, n_rows, nullptr, out);
-        if (rc) {
-            fbh_last_error(buf, sizeof(buf));
-            throw fbt::RuntimeError(buf);
-        }
-        g_last_shap_ms = fbh_shap_last_ms(sm);
+        if (rc) backend_fail(rc);
+        g_last_shap_ms = fbh_shap_last_ms(sm.get());
     });
+}
+
+int fbt_model_from_json(const char *json, size_t len, fbt_model **out) {
+    return guard([&] {
+        if (!json || !out) throw fbt::InputError("null argument");
+        *out = nullptr;
+        auto m = std::make_unique<fbt_model>();
+        m->m = fbt::model_from_json(json, len);
+        *out = m.release();
+    });
+}
+
+uint32_t fbt_model_objective(const fbt_model *m) { return m->m.objective; }
+float fbt_model_scale_pos_weight(const fbt_model *m) { return m->m.scale_pos_weight; }
+uint32_t fbt_model_is_categorical(const fbt_model *m, uint32_t feat) {
+    return feat < m->m.cuts.categorical.size() ? m->m.cuts.categorical[feat] : 0u;
 }
 
 double fbt_last_shap_ms(void) { return g_last_shap_ms; }

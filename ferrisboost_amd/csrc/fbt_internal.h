@@ -82,5 +82,8 @@ struct Model {
 
 float base_margin_of(uint32_t objective, float base_score);
 std::string model_to_json(const Model &m);
+// Model::from_xgboost_json (src/model/tree.rs:754-990); InputError on a
+// document the reader cannot represent.
+Model model_from_json(const char *text, size_t len);
 
 }  // namespace fbt

@@ -430,9 +430,45 @@ int fbh_shap_contribs(fbh_shap_model *m, const float *rows, uint64_t n_rows,
  * sync == 0. */
 int fbh_shap_contribs_device(fbh_shap_model *m, const float *d_rows, uint64_t n_rows,
                              const float *d_margin, float *d_out, int sync);
-/* Milliseconds of the SHAP kernels of the last fbh_shap_contribs (all
- * batches) or fbh_shap_contribs_device (sync != 0) call (HIP events). */
+/* Milliseconds of the kernels of the model's last host call (all batches) or
+ * device call with sync != 0 (HIP events): fbh_shap_contribs[_device],
+ * fbh_shap_interactions, fbh_saabas_contribs, fbh_predict[_device]. */
 double fbh_shap_last_ms(const fbh_shap_model *m);
+
+/* Explainer::compute with Kind::Interactions (interaction_row,
+ * src/model/explain.rs:762-811; device shx interaction kernels,
+ * src/backend/cuda/histogram.cu:3438-3571) for pred_interactions: out
+ * [n_rows][n_features + 1][n_features + 1], symmetric, each row summing to
+ * the row's pred_contribs. */
+int fbh_shap_interactions(fbh_shap_model *m, const float *rows, uint64_t n_rows,
+                          const float *margin, float *out);
+/* Explainer::compute with Kind::Contribs { approx: true } (saabas_row,
+ * src/model/explain.rs:730-760; histogram.cu:4101-4181) for
+ * approx_contribs: out [n_rows][n_features + 1], bias last. */
+int fbh_saabas_contribs(fbh_shap_model *m, const float *rows, uint64_t n_rows,
+                        const float *margin, float *out);
+
+/* Prediction outputs of fbh_predict. */
+enum { FBH_PREDICT_MARGIN = 0, FBH_PREDICT_SIGMOID = 1, FBH_PREDICT_LEAF = 2 };
+/* GpuPredictor::predict_margins_from (src/backend/cuda/inference.rs:300-431;
+ * kernels predict_margin_soa[_cat], src/backend/cuda/histogram.cu:2459-2494,
+ * 3600-3642) and leaf_row (src/model/explain.rs:689-702) over the model's
+ * trees, on host rows [n_rows][n_features]:
+ *   FBH_PREDICT_MARGIN:  out[row] = (margin ? margin[row] : bias) plus every
+ *                        tree's leaf, added in tree order (Model::predict_margin,
+ *                        src/model/tree.rs:486-510);
+ *   FBH_PREDICT_SIGMOID: the logistic link 1 / (1 + expf(-m)) of that margin
+ *                        (objective.rs:37-39, 600-614), bit-identical to the
+ *                        host libm's;
+ *   FBH_PREDICT_LEAF:    out [n_rows][n_trees], the tree-local node id of each
+ *                        tree's leaf as a float (margin unused). */
+int fbh_predict(fbh_shap_model *m, const float *rows, uint64_t n_rows, const float *margin,
+                uint32_t output, float *out);
+/* The same on device buffers, asynchronous on the model's stream when
+ * sync == 0. */
+int fbh_predict_device(fbh_shap_model *m, const float *d_rows, uint64_t n_rows,
+                       const float *d_margin, uint32_t output, float *d_out, int sync);
+
 
 #ifdef __cplusplus
 }

@@ -144,6 +144,41 @@ size_t fbt_model_to_json(const fbt_model *m, char *buf, size_t len);
 /* pred_contribs on the device (GpuExplainModel): out [n_rows][n_features+1]. */
 int fbt_shap(const fbt_model *m, const float *x, uint64_t n_rows, uint32_t n_features,
              int device, float *out);
+
+/* Outputs of fbt_predict. */
+enum {
+    FBT_OUT_MARGIN = 0,          /* raw margins [n_rows] */
+    FBT_OUT_VALUE = 1,           /* margins through the objective's link [n_rows] */
+    FBT_OUT_LEAF = 2,            /* pred_leaf: tree-local leaf ids [n_rows][trees] */
+    FBT_OUT_CONTRIBS = 3,        /* pred_contribs: TreeSHAP [n_rows][n_features + 1] */
+    FBT_OUT_APPROX_CONTRIBS = 4, /* approx_contribs: Saabas [n_rows][n_features + 1] */
+    FBT_OUT_INTERACTIONS = 5     /* pred_interactions [n_rows][n_features + 1]^2 */
+};
+/* Model.predict (python/ferrisboost/_core.pyi:94-197, src/python/mod.rs:
+ * 2667-2800) over the trees [tree_begin, tree_end) (n_trees and
+ * iteration_range select them: a prefix, or the slice of
+ * src/python/mod.rs:1993-2029, which keeps the model's base score). x is
+ * row-major [n_rows][n_features] f32, NaN = missing; base_margin (may be
+ * NULL) is XGBoost's per-row starting margin, replacing the intercept and the
+ * bias of explanations. device >= 0 runs on that GPU (the GpuPredictor /
+ * GpuExplainModel kernels); device < 0 scores FBT_OUT_MARGIN / FBT_OUT_VALUE
+ * on the host (use_gpu=False). The logistic link is 1 / (1 + expf(-m))
+ * (objective.rs:37-39, 600-614) on either side, bit for bit. Feature values
+ * equal to the largest float32 are an input error (they are reserved for
+ * split boundaries). */
+int fbt_predict(const fbt_model *m, const float *x, uint64_t n_rows, uint32_t n_features,
+                uint32_t output, uint32_t tree_begin, uint32_t tree_end, const float *base_margin,
+                int device, float *out);
+/* Model::from_xgboost_json (src/model/tree.rs:754-990, 1259-1470): a model
+ * of binary:logistic or reg:squarederror trees from XGBoost-schema JSON
+ * text, with the reference's checks (input error on what it cannot
+ * represent). The loaded model has no cuts; it predicts and explains. */
+int fbt_model_from_json(const char *json, size_t len, fbt_model **out);
+/* The model's objective (0 = reg:squarederror, 1 = binary:logistic), its
+ * scale_pos_weight, and whether feature `feat` is categorical. */
+uint32_t fbt_model_objective(const fbt_model *m);
+float fbt_model_scale_pos_weight(const fbt_model *m);
+uint32_t fbt_model_is_categorical(const fbt_model *m, uint32_t feat);
 /* Device time of the SHAP kernels of this thread's last fbt_shap call (ms). */
 double fbt_last_shap_ms(void);
 

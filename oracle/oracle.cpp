@@ -1326,13 +1326,58 @@ float extract_delta(const Rule &r, const float *h, float pe, float px) {
     return acc;
 }
 
+// extract_interaction_delta (src/model/explain.rs:219-247).
+float extract_interaction_delta(const Rule &r, const float *h, float pe, float px, float q) {
+    if (q == 1.0f) return 0.0f;
+    const float ap = q - 1.0f, ae = pe - 1.0f;
+    float acc = 0.0f;
+    if (px == 1.0f) {
+        for (int i = 0; i < POINTS; i++) {
+            const float edge = ae / (1.0f + ae * r.nodes[i]);
+            acc += ap * h[i] * edge / (1.0f + ap * r.nodes[i]);
+        }
+    } else {
+        const float ax = px - 1.0f;
+        for (int i = 0; i < POINTS; i++) {
+            const float edge = ae / (1.0f + ae * r.nodes[i]) - ax / (1.0f + ax * r.nodes[i]);
+            acc += ap * h[i] * edge / (1.0f + ap * r.nodes[i]);
+        }
+    }
+    return acc;
+}
+
+// Runner (src/model/explain.rs:303-401) with the Additive formulation
+// (matrix == nullptr: phi[feat] += delta) or the Interaction formulation
+// (:267-301: diag[feat] += delta, partners on the live path into matrix).
 struct ShapRunner {
     const std::vector<Node> &nodes;
     const float *feats;
     const Rule &rule;
     std::vector<float> &path_prob;
-    std::vector<float> &phi;
+    std::vector<float> &phi;  // Additive: per-tree contributions; Interaction: diag
+    float *matrix = nullptr;  // Interaction: [nc][nc]
+    size_t ncols = 0;
+    std::vector<std::pair<u32, float>> path;
 
+    void on_return(u32 feat, const float *h, float pe, float px) {
+        phi[feat] += extract_delta(rule, h, pe, px);
+        if (!matrix) return;
+        const size_t len = path.size();
+        bool skipped_current = false;
+        for (size_t i = len; i-- > 0;) {
+            const u32 split = path[i].first;
+            bool shadowed = false;
+            for (size_t j = i + 1; j < len; j++)
+                if (path[j].first == split) shadowed = true;
+            if (shadowed) continue;
+            if (!skipped_current && split == feat) {
+                skipped_current = true;
+                continue;
+            }
+            matrix[feat * ncols + split] +=
+                extract_interaction_delta(rule, h, pe, px, path[i].second);
+        }
+    }
     void visit(size_t split, size_t child, float cw, bool sat, const float *c, float wprod,
                float *out_h) {
         u32 feat = nodes[split].feat;
@@ -1348,9 +1393,11 @@ struct ShapRunner {
                 for (int i = 0; i < POINTS; i++) cc[i] /= 1.0f + ao * rule.nodes[i];
         }
         path_prob[feat] = pe;
+        path.emplace_back(feat, pe);
         run(child, cc, wprod * cw, out_h);
         float px = p_old == UNSEEN ? 1.0f : p_old;
-        phi[feat] += extract_delta(rule, out_h, pe, px);
+        on_return(feat, out_h, pe, px);
+        path.pop_back();
         path_prob[feat] = p_old;
     }
     void run(size_t idx, const float *c, float wprod, float *out_h) {
@@ -1370,6 +1417,22 @@ struct ShapRunner {
         for (int i = 0; i < POINTS; i++) out_h[i] += rh[i];
     }
 };
+
+// fill_node_means (src/model/explain.rs:409-422): f32 cover-weighted means.
+float fill_node_means(const std::vector<Node> &nodes, size_t idx, std::vector<float> &means) {
+    const Node &n = nodes[idx];
+    float value;
+    if (n.is_leaf) {
+        value = n.leaf_value;
+    } else {
+        const size_t l = (size_t)n.left, r = (size_t)n.right;
+        float result = fill_node_means(nodes, l, means) * nodes[l].sum_hess;
+        result += fill_node_means(nodes, r, means) * nodes[r].sum_hess;
+        value = result / n.sum_hess;
+    }
+    means[idx] = value;
+    return value;
+}
 
 double root_mean(const std::vector<Node> &nodes, size_t idx) {
     const Node &n = nodes[idx];
@@ -1718,32 +1781,107 @@ int orc_model_from_nodes(const orc_node *nodes, const uint32_t *offs, uint32_t n
 }
 
 int orc_shap(const orc_model *m, const float *x, uint64_t n, uint32_t nf, float *out) {
+    return orc_explain(m, 0, x, n, nf, nullptr, out);
+}
+
+// Explainer::compute_with_margin (src/model/explain.rs:612-811) for one
+// output group: kind 0 shap_row, 1 saabas_row, 2 interaction_row, 3 leaf_row.
+int orc_explain(const orc_model *m, uint32_t kind, const float *x, uint64_t n, uint32_t nf,
+                const float *margin, float *out) {
     Rule rule = make_rule();
     double sum = 0.0;
+    std::vector<std::vector<float>> means;
     for (const Tree &t : m->trees) {
         if (t.nodes.empty()) {
             g_error = "tree has no nodes";
             return 1;
         }
+        if (kind == 1) {
+            means.emplace_back(t.nodes.size(), 0.0f);
+            fill_node_means(t.nodes, 0, means.back());
+        }
         sum += root_mean(t.nodes, 0);
     }
-    float root_mean_f = (float)sum;
-    float bias = base_margin_of(m->objective, m->base_score);
-    std::vector<float> path_prob(nf, UNSEEN), contribs(nf + 1);
+    const float root_mean_f = (float)sum;
+    const float base = base_margin_of(m->objective, m->base_score);
+    const size_t nc = (size_t)nf + 1;
+    std::vector<float> path_prob(nf, UNSEEN), contribs(nc), diag(nc);
     for (u64 r = 0; r < n; r++) {
-        float *p = out + r * (nf + 1);
-        std::fill(p, p + nf + 1, 0.0f);
-        for (const Tree &t : m->trees) {
+        const float *feats = x + r * nf;
+        const float bias = margin ? margin[r] : base;
+        if (kind == 3) {  // leaf_row
+            float *o = out + r * m->trees.size();
+            for (size_t t = 0; t < m->trees.size(); t++) {
+                const auto &nodes = m->trees[t].nodes;
+                size_t i = 0;
+                while (!nodes[i].is_leaf)
+                    i = (size_t)(Tree::goes_left(nodes[i], feats[nodes[i].feat]) ? nodes[i].left
+                                                                                 : nodes[i].right);
+                o[t] = (float)i;
+            }
+            continue;
+        }
+        if (kind == 2) {  // interaction_row
+            float *mat = out + r * nc * nc;
+            std::fill(mat, mat + nc * nc, 0.0f);
+            std::fill(diag.begin(), diag.end(), 0.0f);
+            for (const Tree &t : m->trees) {
+                if (t.nodes[0].is_leaf) continue;
+                ShapRunner runner{t.nodes, feats, rule, path_prob, diag, mat, nc, {}};
+                float ones[POINTS], h[POINTS] = {0};
+                for (int i = 0; i < POINTS; i++) ones[i] = 1.0f;
+                runner.run(0, ones, 1.0f, h);
+            }
+            diag[nc - 1] += root_mean_f;
+            diag[nc - 1] += bias;
+            for (size_t a = 0; a < nc; a++)
+                for (size_t b = a + 1; b < nc; b++) {
+                    const float sym = 0.5f * (mat[a * nc + b] + mat[b * nc + a]);
+                    mat[a * nc + b] = sym;
+                    mat[b * nc + a] = sym;
+                }
+            for (size_t a = 0; a < nc; a++) {
+                float value = diag[a];
+                for (size_t b = 0; b < nc; b++)
+                    if (b != a) value -= mat[a * nc + b];
+                mat[a * nc + a] = value;
+            }
+            continue;
+        }
+        float *p = out + r * nc;
+        std::fill(p, p + nc, 0.0f);
+        for (size_t ti = 0; ti < m->trees.size(); ti++) {
+            const Tree &t = m->trees[ti];
             std::fill(contribs.begin(), contribs.end(), 0.0f);
+            if (kind == 1) {  // saabas_row
+                const auto &nodes = t.nodes;
+                const auto &mn = means[ti];
+                float node_value = mn[0];
+                contribs[nc - 1] += node_value;
+                if (!nodes[0].is_leaf) {
+                    size_t idx = 0, split = 0;
+                    while (!nodes[idx].is_leaf) {
+                        split = nodes[idx].feat;
+                        idx = (size_t)(Tree::goes_left(nodes[idx], feats[split]) ? nodes[idx].left
+                                                                                 : nodes[idx].right);
+                        const float nv = mn[idx];
+                        contribs[split] += nv - node_value;
+                        node_value = nv;
+                    }
+                    contribs[split] += nodes[idx].leaf_value - node_value;
+                }
+                for (size_t c = 0; c < nc; c++) p[c] += contribs[c];
+                continue;
+            }
             if (!t.nodes[0].is_leaf) {
-                ShapRunner runner{t.nodes, x + r * nf, rule, path_prob, contribs};
+                ShapRunner runner{t.nodes, feats, rule, path_prob, contribs, nullptr, 0, {}};
                 float ones[POINTS], h[POINTS] = {0};
                 for (int i = 0; i < POINTS; i++) ones[i] = 1.0f;
                 runner.run(0, ones, 1.0f, h);
             }
             for (u32 c = 0; c < nf; c++) p[c] += contribs[c];
         }
-        p[nf] += root_mean_f;
+        if (kind == 0) p[nf] += root_mean_f;
         p[nf] += bias;
     }
     return 0;

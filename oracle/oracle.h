@@ -153,6 +153,12 @@ void orc_model_train_margins(const orc_model *m, float *out);
  * out: [n_rows][n_features + 1]. */
 int orc_shap(const orc_model *m, const float *x, uint64_t n_rows, uint32_t n_features,
              float *out);
+/* Explainer::compute_with_margin (src/model/explain.rs:612-811): kind 0
+ * TreeSHAP contributions [n][nf + 1], 1 Saabas contributions [n][nf + 1],
+ * 2 interaction values [n][nf + 1][nf + 1], 3 leaf ids [n][n_trees];
+ * margin (may be NULL) replaces the bias per row. */
+int orc_explain(const orc_model *m, uint32_t kind, const float *x, uint64_t n_rows,
+                uint32_t n_features, const float *margin, float *out);
 void orc_quadrature_rule(float nodes[8], float weights[8]);
 
 /* ---- colsample (src/data/colsample.rs:57-117) ---- */

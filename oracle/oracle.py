@@ -170,6 +170,7 @@ def lib() -> C.CDLL:
         L.orc_model_train_margins.argtypes = [P, P]
         L.orc_model_train_margins.restype = None
         L.orc_shap.argtypes = [P, P, C.c_uint64, C.c_uint32, P]
+        L.orc_explain.argtypes = [P, C.c_uint32, P, C.c_uint64, C.c_uint32, P, P]
         L.orc_quadrature_rule.argtypes = [P, P]
         L.orc_quadrature_rule.restype = None
         L.orc_sample_features.argtypes = [C.c_uint32, C.c_float, C.c_uint64, C.c_uint64, P]
@@ -283,6 +284,21 @@ class Model:
         x = np.ascontiguousarray(x, np.float32)
         out = np.zeros((x.shape[0], x.shape[1] + 1), np.float32)
         rc = lib().orc_shap(self.h, _p(x), x.shape[0], x.shape[1], _p(out))
+        if rc:
+            raise RuntimeError(lib().orc_last_error().decode())
+        return out
+
+    _EXPLAIN = {"contribs": 0, "approx": 1, "interactions": 2, "leaf": 3}
+
+    def explain(self, x: np.ndarray, kind: str, margin=None) -> np.ndarray:
+        """Explainer::compute_with_margin: kind contribs / approx / interactions / leaf."""
+        x = np.ascontiguousarray(x, np.float32)
+        n, nf = x.shape
+        shape = {"contribs": (n, nf + 1), "approx": (n, nf + 1),
+                 "interactions": (n, nf + 1, nf + 1), "leaf": (n, self.n_trees)}[kind]
+        out = np.zeros(shape, np.float32)
+        m = None if margin is None else np.ascontiguousarray(margin, np.float32)
+        rc = lib().orc_explain(self.h, self._EXPLAIN[kind], _p(x), n, nf, _p(m), _p(out))
         if rc:
             raise RuntimeError(lib().orc_last_error().decode())
         return out

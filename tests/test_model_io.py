@@ -1,0 +1,428 @@
+"""Model interchange on the host: the XGBoost-schema JSON writer and reader
+(Model::to_xgboost_json / from_xgboost_json, src/model/tree.rs:600-990,
+1091-1470). No GPU: a loaded model is written back and scored on the host.
+
+Pins, none of them the code under test restated:
+* the reference's own JSON test vectors and expectations
+  (src/model/tree.rs:1887-2090): the "real-looking" XGBoost dump, the
+  shape assertions of the writer, the rejection cases, the base_score
+  spellings, the scale_pos_weight texts;
+* the field order of the reference's serde structs (tree.rs:1097-1197);
+* numpy's shortest round-trip digits for every float the writer prints,
+  rendered with the layout rules of the ryu crate's format_finite, which
+  serde_json uses for f32.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+
+import numpy as np
+import pytest
+
+import ferrisboost_amd as fb
+from ferrisboost_amd import _native as N
+
+NO_PARENT = 2147483647
+
+# src/model/tree.rs:1951-1975 (the reference's hand-written XGBoost 2.0.3 dump).
+XGB_DUMP = r"""{
+  "version": [2, 0, 3],
+  "learner": {
+    "attributes": {"best_iteration": "3"},
+    "feature_names": [],
+    "feature_types": [],
+    "gradient_booster": {
+      "model": {
+        "gbtree_model_param": {"num_parallel_tree": "1", "num_trees": "1"},
+        "iteration_indptr": [0, 1],
+        "tree_info": [0],
+        "trees": [{
+          "base_weights": [0E0, -1E0, 5E-1],
+          "categories": [], "categories_nodes": [], "categories_segments": [],
+          "categories_sizes": [],
+          "default_left": [1, 0, 0],
+          "id": 0,
+          "left_children": [1, -1, -1],
+          "loss_changes": [1.25E1, 0E0, 0E0],
+          "parents": [2147483647, 0, 0],
+          "right_children": [2, -1, -1],
+          "split_conditions": [2.5E0, -3E-1, 1.5E-1],
+          "split_indices": [1, 0, 0],
+          "split_type": [0, 0, 0],
+          "sum_hessian": [8E0, 5E0, 3E0],
+          "tree_param": {"num_deleted": "0", "num_feature": "3",
+                         "num_nodes": "3", "size_leaf_vector": "1"}
+        }]
+      },
+      "name": "gbtree"
+    },
+    "learner_model_param": {"base_score": "5E-1", "boost_from_average": "1",
+                            "num_class": "0", "num_feature": "3", "num_target": "1"},
+    "objective": {"name": "binary:logistic", "reg_loss_param": {"scale_pos_weight": "1"}}
+  }
+}"""
+
+
+def _fixture_json(objective="reg:squarederror", base_score="0.5", spw="1", cats=None):
+    """The fixture tree of src/model/tree.rs:1474-1480 as an XGBoost document:
+    x0 < 1.5 (missing left) -> [x1 < 0.5 -> leaves 1.0 / 2.0], leaf 3.0;
+    covers 10, 6, 4, 3, 3; gains 4 and 2."""
+    tree = {
+        "base_weights": [0.0, 0.0, 3.0, 1.0, 2.0],
+        "categories": [], "categories_nodes": [], "categories_segments": [],
+        "categories_sizes": [],
+        "default_left": [1, 0, 0, 0, 0], "id": 0,
+        "left_children": [1, 3, -1, -1, -1], "loss_changes": [4.0, 2.0, 0.0, 0.0, 0.0],
+        "parents": [NO_PARENT, 0, 0, 1, 1], "right_children": [2, 4, -1, -1, -1],
+        "split_conditions": [1.5, 0.5, 3.0, 1.0, 2.0], "split_indices": [0, 1, 0, 0, 0],
+        "split_type": [0, 0, 0, 0, 0], "sum_hessian": [10.0, 6.0, 4.0, 3.0, 3.0],
+        "tree_param": {"num_deleted": "0", "num_feature": "2", "num_nodes": "5",
+                       "size_leaf_vector": "1"},
+    }
+    feature_types = []
+    if cats is not None:
+        tree["split_type"] = [0, 1, 0, 0, 0]
+        tree["categories"] = list(cats)
+        tree["categories_nodes"] = [1]
+        tree["categories_segments"] = [0]
+        tree["categories_sizes"] = [len(cats)]
+        feature_types = ["q", "c"]
+    doc = {
+        "version": [2, 0, 0],
+        "learner": {
+            "attributes": {}, "feature_names": [], "feature_types": feature_types,
+            "gradient_booster": {"name": "gbtree", "model": {
+                "gbtree_model_param": {"num_trees": "1", "num_parallel_tree": "1"},
+                "iteration_indptr": [0, 1], "tree_info": [0], "trees": [tree]}},
+            "learner_model_param": {"base_score": base_score, "boost_from_average": "1",
+                                    "num_class": "0", "num_feature": "2", "num_target": "1"},
+            "objective": {"name": objective, "reg_loss_param": {"scale_pos_weight": spw}},
+        },
+    }
+    return json.dumps(doc)
+
+
+def _host_margin(m, rows):
+    return m.predict(np.asarray(rows, np.float32), output_margin=True, use_gpu=False)
+
+
+def test_reads_a_real_looking_xgboost_dump():
+    """src/model/tree.rs:1977-2004."""
+    m = fb.Model.from_json(XGB_DUMP)
+    assert m.objective == "binary:logistic"
+    assert m.n_features == 3 and m.num_trees == 1
+    assert m.base_score == 0.5  # "5E-1"
+    t = m.tree_nodes(0)
+    assert not t[0]["is_leaf"] and t[0]["feat"] == 1
+    assert t[0]["split_cond"] == 2.5 and t[0]["default_left"] == 1
+    assert t[0]["sum_hess"] == 8.0 and t[0]["gain"] == 12.5
+    assert t[1]["is_leaf"] and t[1]["leaf_value"] == np.float32(-0.3)
+    got = _host_margin(m, [[0.0, 2.0, 0.0], [0.0, np.nan, 0.0], [0.0, 9.0, 0.0]])
+    assert got.tolist() == [np.float32(-0.3), np.float32(-0.3), np.float32(0.15)]
+
+
+@pytest.mark.parametrize("frm, to, what", [
+    ('"num_class": "0"', '"num_class": "3"', "multiclass"),
+    ('"binary:logistic"', '"survival:bogus"', "objective"),
+    ('"num_parallel_tree": "1"', '"num_parallel_tree": "4"', "forest"),
+    ('"split_type": [0, 0, 0]', '"split_type": [1, 0, 0]', "categorical split"),
+    ('"left_children": [1, -1, -1]', '"left_children": [0, -1, -1]', "cycle"),
+    ('"right_children": [2, -1, -1]', '"right_children": [-1, -1, -1]', "one-sided child"),
+    ('"split_indices": [1, 0, 0]', '"split_indices": [3, 0, 0]', "out-of-range feature"),
+])
+def test_rejects_what_it_cannot_represent(frm, to, what):
+    """src/model/tree.rs:2006-2045: every case is a ValueError with a message."""
+    broken = XGB_DUMP.replace(frm, to)
+    assert broken != XGB_DUMP
+    with pytest.raises(ValueError) as e:
+        fb.Model.from_json(broken)
+    assert str(e.value), what
+
+
+@pytest.mark.parametrize("frm, to, what", [
+    ('"num_target": "1"', '"num_target": "2"', "num_target"),
+    ('"tree_info": [0]', '"tree_info": [1]', "tree_info"),
+    ('"size_leaf_vector": "1"', '"size_leaf_vector": "2"', "size_leaf_vector"),
+])
+def test_multi_output_models_are_rejected(frm, to, what):
+    """src/model/tree.rs:2047-2076: the message names the offending field."""
+    with pytest.raises(ValueError, match=what):
+        fb.Model.from_json(XGB_DUMP.replace(frm, to))
+
+
+def test_old_models_load():
+    """src/model/tree.rs:2069-2075: size_leaf_vector "0" and no num_target."""
+    old = XGB_DUMP.replace('"size_leaf_vector": "1"', '"size_leaf_vector": "0"').replace(
+        ', "num_target": "1"', "")
+    assert old != XGB_DUMP
+    assert fb.Model.from_json(old).num_trees == 1
+
+
+@pytest.mark.parametrize("raw, want", [("[5E-1]", 0.5), ("5E-1", 0.5), (" [ -1.5 ] ", -1.5)])
+def test_base_score_parses_both_spellings(raw, want):
+    """src/model/tree.rs:2078-2088."""
+    m = fb.Model.from_json(XGB_DUMP.replace('"base_score": "5E-1"', f'"base_score": "{raw}"'))
+    assert m.base_score == want
+
+
+@pytest.mark.parametrize("raw", ["[0.1, 0.2]", "[]", "abc"])
+def test_base_score_rejects_vectors_and_garbage(raw):
+    with pytest.raises(ValueError):
+        fb.Model.from_json(XGB_DUMP.replace('"base_score": "5E-1"', f'"base_score": "{raw}"'))
+
+
+def test_dump_has_the_shape_xgboost_expects():
+    """src/model/tree.rs:1887-1948: strings for every parameter, the parent
+    sentinel, leaf values in split_conditions, numeric split types."""
+    v = json.loads(fb.Model.from_json(_fixture_json()).to_json())
+    assert v["version"][0] == 2
+    lr = v["learner"]
+    assert lr["gradient_booster"]["name"] == "gbtree"
+    assert lr["objective"]["name"] == "reg:squarederror"
+    assert lr["objective"]["reg_loss_param"]["scale_pos_weight"] == "1"
+    assert lr["learner_model_param"]["num_feature"] == "2"
+    assert lr["learner_model_param"]["num_class"] == "0"
+    assert lr["learner_model_param"]["base_score"] == "0.5"
+    model = lr["gradient_booster"]["model"]
+    assert model["gbtree_model_param"]["num_trees"] == "1"
+    assert model["tree_info"] == [0] and model["iteration_indptr"] == [0, 1]
+    t = model["trees"][0]
+    assert t["tree_param"]["num_nodes"] == "5"
+    assert t["left_children"] == [1, 3, -1, -1, -1]
+    assert t["right_children"] == [2, 4, -1, -1, -1]
+    assert t["parents"] == [NO_PARENT, 0, 0, 1, 1]
+    assert t["default_left"] == [1, 0, 0, 0, 0]
+    assert t["split_indices"] == [0, 1, 0, 0, 0]
+    assert t["split_conditions"] == [1.5, 0.5, 3.0, 1.0, 2.0]
+    assert t["sum_hessian"] == [10.0, 6.0, 4.0, 3.0, 3.0]
+    assert t["loss_changes"] == [4.0, 2.0, 0.0, 0.0, 0.0]
+    assert t["split_type"] == [0, 0, 0, 0, 0] and t["categories"] == []
+    assert lr["feature_types"] == []
+
+
+def _keys_in_order(text: str, path: list[str]) -> list[str]:
+    obj = json.loads(text, object_pairs_hook=lambda kv: kv)
+
+    def find(o, p):
+        if not p:
+            return o
+        return find(dict(o)[p[0]] if p[0] != "#0" else o[0], p[1:])
+
+    return [k for k, _ in find(obj, path)]
+
+
+def test_key_order_follows_the_reference_structs():
+    """serde writes struct fields in declaration order (src/model/tree.rs:
+    1097-1197); reg_loss_param is the flattened BTreeMap of the objective."""
+    text = fb.Model.from_json(_fixture_json()).to_json()
+    assert _keys_in_order(text, []) == ["version", "learner"]
+    assert _keys_in_order(text, ["learner"]) == [
+        "attributes", "feature_names", "feature_types", "gradient_booster",
+        "learner_model_param", "objective"]
+    assert _keys_in_order(text, ["learner", "gradient_booster"]) == ["name", "model"]
+    assert _keys_in_order(text, ["learner", "gradient_booster", "model"]) == [
+        "gbtree_model_param", "iteration_indptr", "tree_info", "trees"]
+    assert _keys_in_order(text, ["learner", "gradient_booster", "model",
+                                 "gbtree_model_param"]) == ["num_trees", "num_parallel_tree"]
+    assert _keys_in_order(text, ["learner", "learner_model_param"]) == [
+        "base_score", "boost_from_average", "num_class", "num_feature", "num_target"]
+    assert _keys_in_order(text, ["learner", "objective"]) == ["name", "reg_loss_param"]
+    assert _keys_in_order(text, ["learner", "gradient_booster", "model", "trees", "#0"]) == [
+        "base_weights", "categories", "categories_nodes", "categories_segments",
+        "categories_sizes", "default_left", "id", "left_children", "loss_changes", "parents",
+        "right_children", "split_conditions", "split_indices", "split_type", "sum_hessian",
+        "tree_param"]
+    assert _keys_in_order(text, ["learner", "gradient_booster", "model", "trees", "#0",
+                                 "tree_param"]) == [
+        "num_deleted", "num_feature", "num_nodes", "size_leaf_vector"]
+
+
+@pytest.mark.parametrize("spw, text", [(3.0, "3"), (0.3, "0.3"), (2.5, "2.5")])
+def test_scale_pos_weight_is_saved_and_loaded(spw, text):
+    """src/model/tree.rs:1758-1790: Display of f32 and a byte-identical
+    second save."""
+    m = fb.Model.from_json(_fixture_json(objective="binary:logistic", spw=repr(spw)))
+    js = m.to_json()
+    assert json.loads(js)["learner"]["objective"]["reg_loss_param"]["scale_pos_weight"] == text
+    back = fb.Model.from_json(js)
+    assert back.scale_pos_weight == np.float32(spw)
+    assert back.to_json() == js
+
+
+def test_missing_scale_pos_weight_reads_as_one():
+    doc = json.loads(_fixture_json())
+    del doc["learner"]["objective"]["reg_loss_param"]
+    assert fb.Model.from_json(json.dumps(doc)).scale_pos_weight == 1.0
+
+
+def test_logistic_base_score_stays_a_probability():
+    """src/model/tree.rs:1871-1885: saved in probability space, not logit."""
+    m = fb.Model.from_json(_fixture_json(objective="binary:logistic", base_score="0.25"))
+    back = fb.Model.from_json(m.to_json())
+    assert back.base_score == np.float32(0.25)
+    assert json.loads(m.to_json())["learner"]["learner_model_param"]["base_score"] == "0.25"
+    row = np.array([[9.0, 0.0]], np.float32)
+    assert _host_margin(back, row)[0] == _host_margin(m, row)[0]
+
+
+def _ryu_layout(x: np.float32) -> str:
+    """serde_json's f32 text: numpy's shortest round-trip digits laid out by
+    the rules of the ryu crate's format_finite (decimal point positions
+    0..=16, scientific notation otherwise, always a fraction or exponent)."""
+    if x == 0:
+        return "-0.0" if math.copysign(1.0, float(x)) < 0 else "0.0"
+    sci = np.format_float_scientific(x, unique=True, trim="-")
+    sign = "-" if sci.startswith("-") else ""
+    sci = sci.lstrip("-")
+    mant, exp = sci.split("e")
+    digits = mant.replace(".", "").rstrip("0") or "0"
+    kk = int(exp) + 1
+    n = len(digits)
+    k = kk - n
+    if 0 <= k and kk <= 16:
+        body = digits + "0" * k + ".0"
+    elif 0 < kk <= 16:
+        body = digits[:kk] + "." + digits[kk:]
+    elif -5 < kk <= 0:
+        body = "0." + "0" * (-kk) + digits
+    elif n == 1:
+        body = f"{digits}e{kk - 1}"
+    else:
+        body = f"{digits[0]}.{digits[1:]}e{kk - 1}"
+    return sign + body
+
+
+def test_float_text_is_the_shortest_round_trip_layout():
+    """Every float of a saved tree prints as serde_json/ryu would: numpy's
+    shortest digits, ryu's layout; and reads back to the same bits."""
+    rng = np.random.default_rng(7)
+    vals = np.concatenate([
+        rng.normal(size=200).astype(np.float32),
+        (rng.normal(size=100) * 10.0 ** rng.integers(-30, 30, size=100)).astype(np.float32),
+        np.array([1.0, 0.1, 1e-7, 1.5e20, 123456789.0, 1e16, 1e17, 3.4028235e38, 1e-45,
+                  -0.0, 0.0001, 0.00001, 65504.0], np.float32),
+    ])
+    vals = vals[np.isfinite(vals)]
+    # one tree per value: a stump whose right leaf holds the value
+    doc = json.loads(_fixture_json())
+    base = doc["learner"]["gradient_booster"]["model"]["trees"][0]
+    trees = []
+    for i, v in enumerate(vals):
+        t = json.loads(json.dumps(base))
+        t["id"] = i
+        t["split_conditions"][2] = float(v)
+        t["base_weights"][2] = float(v)
+        trees.append(t)
+    m_ = doc["learner"]["gradient_booster"]["model"]
+    m_["trees"] = trees
+    m_["tree_info"] = [0] * len(trees)
+    m_["iteration_indptr"] = list(range(len(trees) + 1))
+    m_["gbtree_model_param"]["num_trees"] = str(len(trees))
+    text = fb.Model.from_json(json.dumps(doc)).to_json()
+    saved = json.loads(text)["learner"]["gradient_booster"]["model"]["trees"]
+    raw = text.split('"split_conditions":[')[1:]
+    for i, v in enumerate(vals):
+        printed = raw[i].split("]")[0].split(",")[2]
+        assert printed == _ryu_layout(v), (float(v), printed)
+        assert np.float32(saved[i]["split_conditions"][2]).view(np.uint32) == v.view(np.uint32)
+
+
+def test_categorical_split_round_trips():
+    """src/model/tree.rs:2199-2219: category lists, split types and feature
+    types survive a save and load; members go right."""
+    m = fb.Model.from_json(_fixture_json(cats=[1, 4, 33]))
+    t = m.tree_nodes(0)
+    assert t[1]["cat_len"] == 2  # words for categories up to 33
+    js = m.to_json()
+    v = json.loads(js)
+    tr = v["learner"]["gradient_booster"]["model"]["trees"][0]
+    assert tr["categories"] == [1, 4, 33] and tr["categories_nodes"] == [1]
+    assert tr["categories_sizes"] == [3] and tr["split_type"] == [0, 1, 0, 0, 0]
+    assert v["learner"]["feature_types"] == ["q", "c"]
+    assert fb.Model.from_json(js).to_json() == js
+    got = _host_margin(m, [[0.0, 4.0], [0.0, 5.0], [0.0, 33.0], [0.0, -1.0], [0.0, np.nan]])
+    # base margin 0.5; node 1 sends members right (leaf 2.0), others left
+    # (1.0); NaN follows the default direction, right
+    assert got.tolist() == [2.5, 1.5, 2.5, 1.5, 2.5]
+
+
+@pytest.mark.parametrize("bad", [
+    '{"version": [2,0,0]}', "[1, 2", '{"learner": ', "not json",
+])
+def test_malformed_documents_are_value_errors(bad):
+    with pytest.raises(ValueError):
+        fb.Model.from_json(bad)
+
+
+def test_host_prediction_link_is_the_host_libm_sigmoid(oracle):
+    """predict() on the host applies 1 / (1 + expf(-m)) with the host libm
+    (objective.rs:37-39, 600-614), bit for bit with the oracle's sigmoid."""
+    m = fb.Model.from_json(_fixture_json(objective="binary:logistic"))
+    rows = np.random.default_rng(3).normal(size=(5000, 2)).astype(np.float32) * 3
+    margin = m.predict(rows, output_margin=True, use_gpu=False)
+    prob = m.predict(rows, use_gpu=False)
+    want = np.zeros_like(margin)
+    oracle.lib().orc_sigmoid(oracle._p(margin), margin.size, oracle._p(want))
+    assert np.array_equal(prob.view(np.uint32), want.view(np.uint32))
+
+
+def test_predict_argument_errors():
+    m = fb.Model.from_json(XGB_DUMP)
+    x = np.zeros((2, 3), np.float32)
+    with pytest.raises(ValueError, match="cannot both"):
+        m.predict(x, n_trees=1, iteration_range=(0, 1), use_gpu=False)
+    with pytest.raises(ValueError, match="exceeds"):
+        m.predict(x, iteration_range=(0, 2), use_gpu=False)
+    with pytest.raises(ValueError, match="greater"):
+        m.predict(x, iteration_range=(2, 1), use_gpu=False)
+    with pytest.raises(ValueError, match="output_margin"):
+        m.predict(x, output_margin=True, pred_contribs=True)
+    with pytest.raises(ValueError, match="exclusive"):
+        m.predict(x, pred_contribs=True, pred_leaf=True)
+    with pytest.raises(ValueError, match="approx_contribs"):
+        m.predict(x, pred_interactions=True, approx_contribs=True)
+    with pytest.raises(ValueError, match="columns"):
+        m.predict(np.zeros((2, 4), np.float32), use_gpu=False)
+    with pytest.raises(ValueError, match="reserved"):
+        m.predict(np.full((1, 3), np.finfo(np.float32).max, np.float32), use_gpu=False)
+    with pytest.raises(ValueError, match="missing"):
+        m.predict(x, missing=float("inf"), use_gpu=False)
+    with pytest.raises(ValueError, match="file inputs"):
+        m.predict("data.csv")
+    with pytest.raises(ValueError, match="base_margin"):
+        m.predict(x, base_margin=np.zeros(3), use_gpu=False)
+
+
+def test_iteration_range_and_base_margin_on_the_host():
+    """begin == end leaves the intercept (src/python/mod.rs:1993-2029); a
+    base margin replaces it; missing maps a sentinel to NaN."""
+    m = fb.Model.from_json(XGB_DUMP)
+    x = np.array([[0.0, 2.0, 0.0], [0.0, 9.0, 0.0]], np.float32)
+    assert m.predict(x, output_margin=True, iteration_range=(1, 1), use_gpu=False).tolist() == [0, 0]
+    bm = np.array([1.0, -1.0], np.float32)
+    got = m.predict(x, output_margin=True, base_margin=bm, use_gpu=False)
+    assert got.tolist() == [np.float32(1.0) + np.float32(-0.3), np.float32(-1.0) + np.float32(0.15)]
+    xs = x.copy()
+    xs[1, 1] = -999.0
+    got = m.predict(xs, output_margin=True, missing=-999.0, use_gpu=False)
+    assert got[1] == np.float32(-0.3)  # missing goes left
+    assert m.predict(x, output_margin=True, strict_shape=True, use_gpu=False).shape == (2, 1)
+
+
+def test_feature_importance_types():
+    """get_score (src/model/explain.rs:57-114, :1180-1196)."""
+    m = fb.Model.from_json(_fixture_json())
+    assert m.get_score("weight") == {"f0": 1.0, "f1": 1.0}
+    assert m.get_score("total_gain") == {"f0": 4.0, "f1": 2.0}
+    assert m.get_score("cover") == {"f0": 10.0, "f1": 6.0}
+    with pytest.raises(ValueError):
+        m.get_score("bogus")
+
+
+def test_loaded_model_has_no_device_requirement_for_host_scoring():
+    """Loading and host scoring touch no device (no HIP call)."""
+    assert N.train_lib() is not None
+    m = fb.Model.from_json(XGB_DUMP)
+    assert m.predict(np.zeros((3, 3), np.float32), use_gpu=False).shape == (3,)

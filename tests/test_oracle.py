@@ -634,6 +634,142 @@ def test_shap_categorical_matches_brute_force(oracle):
     assert np.max(np.abs(got.sum(axis=1) - m.predict_margin(rows))) < 1e-4
 
 
+def _brute_interaction(model, row, nf, i, j):
+    """Shapley interaction value of (i, j), split evenly between (i, j) and
+    (j, i), by subset enumeration (src/model/explain.rs:964-980)."""
+    trees = model.trees()
+    cats = model.cat_words()
+
+    def val(mask):
+        return sum(_tree_value(t, 0, row, mask, cats) for t in trees)
+
+    acc = 0.0
+    for s in range(1 << nf):
+        if s >> i & 1 or s >> j & 1:
+            continue
+        k = bin(s).count("1")
+        w = math.factorial(k) * math.factorial(nf - k - 2) / (2.0 * math.factorial(nf - 1))
+        acc += w * (val(s | 1 << i | 1 << j) - val(s | 1 << i) - val(s | 1 << j) + val(s))
+    return acc
+
+
+def _small_model(oracle, seed, nf=4, depth=3, rounds=5, categorical=False):
+    rng = np.random.default_rng(seed)
+    n = 700
+    x = rng.normal(size=(n, nf)).astype(np.float32)
+    x[rng.random((n, nf)) < 0.1] = np.nan
+    cat = None
+    if categorical:
+        x[:, 1] = rng.integers(0, 9, size=n)
+        cat = np.zeros(nf, np.uint8)
+        cat[1] = 1
+    y = ((np.nan_to_num(x[:, 0]) * np.nan_to_num(x[:, 2]) > 0) ^ (np.nan_to_num(x[:, 1]) > 3))
+    p = oracle.make_params(n_rounds=rounds, max_depth=depth, eta=0.4, max_bin=32)
+    return oracle.train(x, y.astype(np.float32), p, categorical=cat), x
+
+
+@pytest.mark.parametrize("categorical", [False, True])
+def test_interactions_match_brute_force_and_row_sums(oracle, categorical):
+    """src/model/explain.rs:1112-1139: off-diagonal entries equal the
+    brute-force Shapley interaction values, the matrix is symmetric, and
+    each row sums to the row's SHAP value."""
+    m, x = _small_model(oracle, 41, categorical=categorical)
+    nf = x.shape[1]
+    rows = x[:8]
+    inter = m.explain(rows, "interactions")
+    shap = m.explain(rows, "contribs")
+    for r in range(rows.shape[0]):
+        mat = inter[r]
+        for i in range(nf):
+            for j in range(nf):
+                if i != j:
+                    want = _brute_interaction(m, rows[r], nf, i, j)
+                    assert abs(float(mat[i, j]) - want) < 5e-5, (r, i, j)
+                    assert mat[i, j] == mat[j, i]
+        assert np.max(np.abs(mat.sum(axis=1) - shap[r])) < 1e-4, r
+
+
+def test_saabas_equals_treeshap_on_stumps_and_sums_to_margin(oracle):
+    """On depth-1 trees the path attribution of Saabas is the exact Shapley
+    value (one split: the only feature gets leaf - root mean); on deeper
+    trees the contributions still telescope to the margin."""
+    m1, x = _small_model(oracle, 43, depth=1, rounds=6)
+    rows = x[:50]
+    sa, sh = m1.explain(rows, "approx"), m1.explain(rows, "contribs")
+    assert np.max(np.abs(sa - sh)) < 1e-6
+    m3, x3 = _small_model(oracle, 44, depth=4, rounds=6)
+    rows = x3[:200]
+    sa = m3.explain(rows, "approx")
+    assert np.max(np.abs(sa.sum(axis=1) - m3.predict_margin(rows))) < 1e-5
+
+
+def test_saabas_closed_form_on_a_hand_tree(oracle):
+    """The tree of src/model/tree.rs:1474-1480 (x0 < 1.5, missing left; its
+    left child x1 < 0.5), worked by hand: node means are cover-weighted leaf
+    means, and each path step adds the change of the mean to its split
+    feature (src/model/explain.rs:730-760)."""
+    nodes = np.zeros(5, oracle.NODE_DTYPE)
+    # root: feat 0 < 1.5, default left; children 1 (cover 6), 2 (leaf 3.0, cover 4)
+    nodes[0] = (0, 1.5, 1, 2, 1, 0, 0, 0.0, 4.0, 10.0, 0, 0)
+    nodes[1] = (1, 0.5, 3, 4, 0, 0, 0, 0.0, 2.0, 6.0, 0, 0)
+    nodes[2] = (0, 3.0, -1, -1, 0, 1, 0, 3.0, 0.0, 4.0, 0, 0)
+    nodes[3] = (0, 1.0, -1, -1, 0, 1, 0, 1.0, 0.0, 3.0, 0, 0)
+    nodes[4] = (0, 2.0, -1, -1, 0, 1, 0, 2.0, 0.0, 3.0, 0, 0)
+    m = oracle.model_from_nodes([nodes], [], "reg:squarederror", 0.5)
+    rows = np.array([[0.0, 0.0], [0.0, 1.0], [2.0, 0.0], [np.nan, 0.5]], np.float32)
+    got = m.explain(rows, "approx")
+    m1 = (1.0 * 3 + 2.0 * 3) / 6.0           # mean of node 1: 1.5
+    m0 = (m1 * 6 + 3.0 * 4) / 10.0           # root mean: 2.1
+    want = np.array([
+        [m1 - m0, 1.0 - m1, m0 + 0.5],
+        [m1 - m0, 2.0 - m1, m0 + 0.5],
+        [3.0 - m0, 0.0, m0 + 0.5],
+        [m1 - m0, 2.0 - m1, m0 + 0.5],
+    ], np.float32)
+    assert np.max(np.abs(got - want)) < 1e-6
+    leaf = m.explain(rows, "leaf")
+    assert leaf[:, 0].tolist() == [3.0, 4.0, 2.0, 4.0]
+
+
+def test_leaf_indices_follow_the_tree(oracle):
+    """src/model/explain.rs:1159-1178: one split at 0.5 (missing left) and a
+    root-only tree; rows 0.2, 0.9, NaN reach leaves l, r, l and 0."""
+    t0 = np.zeros(3, oracle.NODE_DTYPE)
+    t0[0] = (0, 0.5, 1, 2, 1, 0, 0, 0.0, 1.0, 10.0, 0, 0)
+    t0[1] = (0, 1.0, -1, -1, 0, 1, 0, 1.0, 0.0, 4.0, 0, 0)
+    t0[2] = (0, 2.0, -1, -1, 0, 1, 0, 2.0, 0.0, 6.0, 0, 0)
+    t1 = np.zeros(1, oracle.NODE_DTYPE)
+    t1[0] = (0, 3.0, -1, -1, 0, 1, 0, 3.0, 0.0, 1.0, 0, 0)
+    m = oracle.model_from_nodes([t0, t1], [], "reg:squarederror", 0.5)
+    rows = np.array([[0.2], [0.9], [np.nan]], np.float32)
+    assert m.explain(rows, "leaf").tolist() == [[1.0, 0.0], [2.0, 0.0], [1.0, 0.0]]
+
+
+def test_leaf_ids_reproduce_the_margin(oracle):
+    """Summing each tree's leaf value at the returned id, in tree order from
+    the base margin, gives predict_margin bit for bit."""
+    m, x = _small_model(oracle, 45, depth=5, rounds=7, categorical=True)
+    rows = x[:300]
+    leaf = m.explain(rows, "leaf").astype(np.int64)
+    trees = m.trees()
+    acc = np.full(rows.shape[0], np.float32(m.base_margin), np.float32)
+    for t, tr in enumerate(trees):
+        acc = (acc + tr["leaf_value"][leaf[:, t]]).astype(np.float32)
+    assert np.array_equal(acc.view(np.uint32), m.predict_margin(rows).view(np.uint32))
+
+
+def test_explain_base_margin_replaces_the_bias(oracle):
+    """src/model/explain.rs:1216-1285: a per-row base margin replaces the
+    intercept in the bias column and nothing else."""
+    m, x = _small_model(oracle, 46)
+    rows = x[:20]
+    bm = np.linspace(-1, 1, 20).astype(np.float32)
+    for kind in ("contribs", "approx"):
+        a, b = m.explain(rows, kind), m.explain(rows, kind, margin=bm)
+        assert np.array_equal(a[:, :-1], b[:, :-1])
+        assert np.allclose(b[:, -1] - a[:, -1], bm - np.float32(m.base_margin), atol=1e-6)
+
+
 # ---------------------------------------------------------------- row subsample
 
 def _selected(oracle, n, rate, seed, tree):
