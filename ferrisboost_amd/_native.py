@@ -209,7 +209,7 @@ HIP_SYMBOLS = [
     "fbh_hist_timing", "fbh_set_timing", "fbh_build_histogram", "fbh_partition_rows",
     "fbh_shap_model_create", "fbh_shap_model_destroy", "fbh_shap_contribs",
     "fbh_shap_contribs_device", "fbh_shap_last_ms", "fbh_shap_interactions",
-    "fbh_saabas_contribs", "fbh_predict", "fbh_predict_device",
+    "fbh_saabas_contribs", "fbh_predict", "fbh_predict_device", "fbh_shap_contribs_noalloc",
 ]
 TRAIN_SYMBOLS = [
     "fbt_last_error", "fbt_train", "fbt_last_stats", "fbt_last_round_stats", "fbt_model_free", "fbt_model_n_trees",
@@ -293,7 +293,7 @@ def hip() -> C.CDLL:
         L.fbh_shap_contribs_device.argtypes = [P, P, C.c_uint64, P, P, C.c_int]
         L.fbh_shap_last_ms.argtypes = [P]
         L.fbh_shap_last_ms.restype = C.c_double
-        for name in ("fbh_shap_interactions", "fbh_saabas_contribs"):
+        for name in ("fbh_shap_interactions", "fbh_saabas_contribs", "fbh_shap_contribs_noalloc"):
             getattr(L, name).argtypes = [P, P, C.c_uint64, P, P]
         L.fbh_predict.argtypes = [P, P, C.c_uint64, P, C.c_uint32, P]
         L.fbh_predict_device.argtypes = [P, P, C.c_uint64, P, C.c_uint32, P, C.c_int]

@@ -26,11 +26,19 @@
 #include <cmath>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
 using namespace fbh;
+
+// File-scope device array for fbh_shap_contribs_noalloc: every device holds
+// its own copy at its own address, found once per device with
+// hipGetSymbolAddress (scratch_of below); host code uses that address, never
+// the array's name, which on the host is only a stand-in. Calls on one device
+// share it.
+static __device__ __align__(256) unsigned char scratch[FBH_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -677,6 +685,27 @@ void run_host_alloc(fbh_shap_model *m, Kind k, const float *rows, uint64_t n_row
     run_host(m, k, st, rows, n_rows, margin, out);
 }
 
+// ------------------------------------------------ the no-allocation scratch
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)FBH_NOALLOC_SCRATCH_BYTES;
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[MAX_DEVICES] = {};
+
+// The device's scratch address; the device must be current.
+void *scratch_of(int device) {
+    if (device < 0 || device >= MAX_DEVICES) throw ShapError(FBH_INPUT_ERROR, "device index out of range");
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void *p = nullptr;
+        chk(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (!p) throw ShapError(FBH_RUNTIME_ERROR, "hipGetSymbolAddress(scratch) returned null");
+        g_scratch_ptr[device] = p;
+    }
+    return g_scratch_ptr[device];
+}
+
+uint64_t round256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
+
 }  // namespace
 
 extern "C" {
@@ -868,6 +897,40 @@ int fbh_predict_device(fbh_shap_model *m, const float *d_rows, uint64_t n_rows,
             chk(hipEventElapsedTime(&ms, m->e0, m->e1), "event");
             m->last_ms = ms;
         }
+    });
+}
+
+int fbh_shap_contribs_noalloc(fbh_shap_model *m, const float *rows, uint64_t n_rows,
+                              const float *margin, float *out) {
+    return shap_guard([&] {
+        if (!m || (!rows && n_rows) || (!out && n_rows))
+            throw ShapError(FBH_INPUT_ERROR, "null argument");
+        check_kind(m, Kind::Contribs);
+        const uint64_t nf = m->n_features, w = nf + 1;
+        // Layout of one batch in the scratch: rows [b][nf], margins [b],
+        // contributions [b][nf + 1], each region 256-byte aligned.
+        const uint64_t per_row = 4 * (nf + 1 + w);
+        const uint64_t room = NOALLOC_SCRATCH_BYTES - 3 * 256;
+        const uint64_t cap = room / per_row;
+        if (cap == 0)
+            throw ShapError(FBH_INPUT_ERROR,
+                            "fbh_shap_contribs_noalloc: one row of " + std::to_string(nf) +
+                                " features needs " + std::to_string(per_row) +
+                                " bytes of device scratch, above its " +
+                                std::to_string(NOALLOC_SCRATCH_BYTES) + " bytes");
+        if (n_rows == 0) return;
+        chk(hipSetDevice(m->device), "hipSetDevice");
+        unsigned char *base = static_cast<unsigned char *>(scratch_of(m->device));
+        Staging st;
+        st.cap_rows = std::min<uint64_t>(cap, n_rows);
+        st.rows = reinterpret_cast<float *>(base);
+        st.margin = reinterpret_cast<float *>(base + round256(4 * st.cap_rows * nf));
+        st.out = reinterpret_cast<float *>(reinterpret_cast<unsigned char *>(st.margin) +
+                                           round256(4 * st.cap_rows));
+        if ((reinterpret_cast<unsigned char *>(st.out) - base) + 4 * st.cap_rows * w >
+            NOALLOC_SCRATCH_BYTES)
+            throw ShapError(FBH_RUNTIME_ERROR, "fbh_shap_contribs_noalloc: scratch layout overflow");
+        run_host(m, Kind::Contribs, st, rows, n_rows, margin, out);
     });
 }
 

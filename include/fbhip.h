@@ -431,7 +431,7 @@ int fbh_shap_contribs(fbh_shap_model *m, const float *rows, uint64_t n_rows,
 int fbh_shap_contribs_device(fbh_shap_model *m, const float *d_rows, uint64_t n_rows,
                              const float *d_margin, float *d_out, int sync);
 /* Milliseconds of the kernels of the model's last host call (all batches) or
- * device call with sync != 0 (HIP events): fbh_shap_contribs[_device],
+ * device call with sync != 0 (HIP events): fbh_shap_contribs[_device|_noalloc],
  * fbh_shap_interactions, fbh_saabas_contribs, fbh_predict[_device]. */
 double fbh_shap_last_ms(const fbh_shap_model *m);
 
@@ -469,6 +469,20 @@ int fbh_predict(fbh_shap_model *m, const float *rows, uint64_t n_rows, const flo
 int fbh_predict_device(fbh_shap_model *m, const float *d_rows, uint64_t n_rows,
                        const float *d_margin, uint32_t output, float *d_out, int sync);
 
+/* Bytes of device scratch fbh_shap_contribs_noalloc stages through. */
+#define FBH_NOALLOC_SCRATCH_BYTES (32u << 20)
+/* fbh_shap_contribs without any device allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Rows, margins and contributions are staged batch by batch
+ * through a fixed FBH_NOALLOC_SCRATCH_BYTES array that each device holds for
+ * the life of the process (found once per device on the first call); a row
+ * of more than (FBH_NOALLOC_SCRATCH_BYTES - 768) / (8 * n_features + 8)
+ * features' worth of data is an input error. Results equal
+ * fbh_shap_contribs bit for bit. Calls that overlap on one device share the
+ * array and race: serialise them. */
+int fbh_shap_contribs_noalloc(fbh_shap_model *m, const float *rows, uint64_t n_rows,
+                              const float *margin, float *out);
 
 #ifdef __cplusplus
 }
