@@ -141,10 +141,34 @@ def _normalize(params: Mapping[str, Any], num_boost_round: int) -> dict[str, Any
     if num_boost_round < 1:
         raise ValueError(f"num_boost_round must be >= 1, got {num_boost_round}")
     gm = out["gpu_math"]
-    if gm not in (None, "exact"):
-        if gm == "fast":
-            raise ValueError('gpu_math="fast" is not available in ferrisboost_amd; use "exact"')
-        raise ValueError(f'gpu_math must be "exact" or "fast", got {gm!r}')
+    if gm is not None:
+        gm = str(gm)
+        if gm not in ("exact", "fast"):
+            raise ValueError(f'gpu_math must be "exact" or "fast", got {gm!r}; fast does not '
+                             "guarantee byte-identical CPU/GPU models")
+        out["gpu_math"] = gm
+    # GPU knobs of python/ferrisboost/__init__.py:224-280, validated as there.
+    if out["hist_streams"] is not None:
+        out["hist_streams"] = int(out["hist_streams"])
+        if out["hist_streams"] not in (1, 2):
+            raise ValueError(f"hist_streams must be 1 or 2, got {out['hist_streams']}; omit it "
+                             "to let it be chosen automatically")
+    if out["resident_blocks"] is not None:
+        out["resident_blocks"] = int(out["resident_blocks"])
+        if out["resident_blocks"] < 0:
+            raise ValueError(f"resident_blocks must not be negative, got {out['resident_blocks']};"
+                             " omit it to let it be chosen automatically; 0 means pure streaming")
+    if out["hist_nodes_per_batch"] is not None:
+        v = int(out["hist_nodes_per_batch"])
+        if not 1 <= v <= 32:
+            raise ValueError(f"hist_nodes_per_batch must be in 1..=32, got {v}; 1 disables "
+                             "multi-node batching")
+        raise ValueError("hist_nodes_per_batch is not available on the ferrisboost_amd device "
+                         "path: each level's histograms are planned and built in one launch on "
+                         "the device; omit it")
+    if out["device_quantize"] is not None and not bool(out["device_quantize"]):
+        raise ValueError("device_quantize=False is not available on the ferrisboost_amd device "
+                         "path: gradient pairs are always quantized on the device; omit it")
     if out["sampling_method"] != "uniform":
         raise ValueError("sampling_method must be uniform on the ferrisboost_amd device path")
     for k in ("colsample_bylevel", "colsample_bynode"):
@@ -185,7 +209,7 @@ def _params_struct(p: dict[str, Any], n_features: int) -> N.TrainParams:
         s.has_base_score = 1
     s.nthread = int(p["nthread"])
     s.device = _parse_device(p["device"])
-    s.gpu_math = 0
+    s.gpu_math = 1 if p["gpu_math"] == "fast" else 0
     budget = p["gpu_memory_budget"]
     s.gpu_memory_budget = int(budget) if budget else 0
     s.tile_bytes = int(p["hip_tile_bytes"])
@@ -194,6 +218,8 @@ def _params_struct(p: dict[str, Any], n_features: int) -> N.TrainParams:
     s.host_sigmoid = 1 if p["hip_host_sigmoid"] else 0
     s.host_levels = 1 if p["hip_host_levels"] else 0
     s.sync_round = int(p["hip_sync_round"])
+    s.hist_streams = int(p["hist_streams"] or 0)
+    s.resident_limit = 0 if p["resident_blocks"] is None else int(p["resident_blocks"]) + 1
     return s
 
 

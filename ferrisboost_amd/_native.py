@@ -50,7 +50,9 @@ class Config(C.Structure):
         ("tile_bytes", C.c_uint32),
         ("rows_per_block", C.c_uint32),
         ("max_cat_words", C.c_uint32),
-        ("reserved", C.c_uint32 * 6),
+        ("stream_windows", C.c_uint32),
+        ("resident_limit", C.c_uint32),
+        ("reserved", C.c_uint32 * 4),
     ]
 
 
@@ -154,6 +156,8 @@ class TrainParams(C.Structure):
         ("host_sigmoid", C.c_uint32),
         ("host_levels", C.c_uint32),
         ("sync_round", C.c_uint32),
+        ("hist_streams", C.c_uint32),
+        ("resident_limit", C.c_uint32),
     ]
 
 
@@ -201,7 +205,7 @@ HIP_SYMBOLS = [
     "fbh_plan_memory", "fbh_ctx_plan", "fbh_ctx_streamed_bytes",
     "fbh_ctx_device_bytes", "fbh_upload_block", "fbh_upload_quantize_gpair",
     "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_gradient_exchange",
-    "fbh_download_margin", "fbh_sigmoid_host", "fbh_sigmoid_device", "fbh_sigmoid_checksum",
+    "fbh_download_margin", "fbh_set_gpu_math", "fbh_gradient_pairs", "fbh_sigmoid_host", "fbh_sigmoid_device", "fbh_sigmoid_checksum",
     "fbh_begin_tree", "fbh_eval_nodes", "fbh_download_histogram",
     "fbh_partition", "fbh_partition_eval", "fbh_grow_depthwise", "fbh_grow_depthwise_async",
     "fbh_grow_collect", "fbh_assign_leaves", "fbh_download_delta", "fbh_host_alloc",
@@ -265,6 +269,8 @@ def hip() -> C.CDLL:
         L.fbh_set_objective.argtypes = [P, C.c_uint32, P, P, C.c_float]
         L.fbh_gradient_exchange.argtypes = [P, P, P, C.c_uint64, C.c_uint64, C.c_uint64, P, P]
         L.fbh_download_margin.argtypes = [P, P]
+        L.fbh_set_gpu_math.argtypes = [P, C.c_uint32]
+        L.fbh_gradient_pairs.argtypes = [C.c_int, C.c_uint32, C.c_uint32, P, P, P, C.c_uint64, P]
         L.fbh_sigmoid_host.argtypes = [P, C.c_uint64, P]
         L.fbh_sigmoid_device.argtypes = [C.c_int, P, C.c_uint64, P]
         L.fbh_sigmoid_checksum.argtypes = [C.c_int, C.c_uint64, C.c_uint64, P]

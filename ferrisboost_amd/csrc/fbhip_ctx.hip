@@ -187,6 +187,8 @@ struct fbh_ctx {
     // Every tile's workgroup quantizes the pairs it reads again, so f32
     // pairs pay only with few tiles (measured: 2 tiles +3 %, 33 tiles -6 %).
     bool f32_hist() const { return tiles.size() <= F32_PAIR_MAX_TILES; }
+    // launch_gradient mode of the device objective.
+    int gradient_mode() const { return objective == 0 ? 0 : (fast_math ? 3 : 2); }
     int64_t *gpair = nullptr;
     bool root_on_device = false;  // the last quantisation's root sum is on the device
     uint32_t *rows = nullptr, *tmp = nullptr;
@@ -292,8 +294,10 @@ struct fbh_ctx {
         uint32_t bytes_per_row;
     };
     std::vector<Streamed> streamed;  // streamed tiles with active features this tree
-    uint64_t win_flip = 0;           // alternates the two record windows
-    uint64_t col_flip = 0;           // alternates the two column windows
+    uint64_t win_flip = 0;           // alternates the record windows
+    uint64_t col_flip = 0;           // alternates the column windows
+    uint32_t n_windows = 2;          // streaming windows of each kind (hist_streams)
+    uint32_t resident_cap = UINT32_MAX;  // tiles the plan may keep resident (resident_blocks)
     uint64_t streamed_bytes = 0;     // host-to-device bytes of streamed records and columns
     bool has_global = false;  // this tree builds a feature with global atomics
     uint32_t hist_row_bytes = 0;  // active cell bytes per row over all built tiles
@@ -305,6 +309,7 @@ struct fbh_ctx {
 
     // objective state on the device (fbh_set_objective)
     int objective = -1;                 // -1 none, 0 squared error, 1 logistic
+    bool fast_math = false;             // gpu_math="fast": hardware exp in the logistic gradient
     float *labels = nullptr, *gweights = nullptr, *margin = nullptr;
     void *leaf_ids = nullptr;           // per-row leaf position of the last tree
     int leaf_id_bytes = 0;              // 1 or 2 for the last assigned tree
@@ -739,7 +744,12 @@ fbh_plan plan_memory(fbh_ctx &c, uint64_t budget) {
         if (t.bundle < 0) rec_all += n * t.rec;
     for (uint32_t f = 0; f < c.n_features; f++) col_all += n * c.width[f];
     for (auto &t : c.tiles) t.resident = true;
-    if (rec_all + col_all <= avail) {
+    // resident_blocks: at most this many tiles stay resident (tiles of a
+    // feature too wide for LDS always do and are not counted).
+    uint32_t lds_tiles = 0;
+    for (const auto &t : c.tiles) lds_tiles += t.global ? 0 : 1;
+    const bool capped = c.resident_cap < lds_tiles;
+    if (rec_all + col_all <= avail && !capped) {
         P.resident_record_bytes = rec_all;
         P.column_bytes = col_all;
         P.columns_resident = 1;
@@ -750,12 +760,14 @@ fbh_plan plan_memory(fbh_ctx &c, uint64_t budget) {
         uint32_t max_stride = 4, max_w = 1;
         for (const auto &t : c.tiles) max_stride = std::max(max_stride, t.stride);
         for (uint32_t f = 0; f < c.n_features; f++) max_w = std::max<uint32_t>(max_w, c.width[f]);
-        // Two column windows (uploads, partitions of streamed features) and
-        // two record windows (histograms of streamed tiles).
-        const uint64_t col_win = 2 * n * max_w;
+        // Column windows (uploads, partitions of streamed features) and
+        // record windows (histograms of streamed tiles): two of each, so
+        // uploads overlap the kernels, or one (hist_streams = 1).
+        const uint64_t nw = c.n_windows;
+        const uint64_t col_win = nw * n * max_w;
         uint64_t w = std::min<uint64_t>(MAX_WINDOW_BYTES, avail / 8) / (2 * max_stride);
         w = std::min<uint64_t>(n, std::max<uint64_t>(w, MIN_WINDOW_ROWS));
-        const uint64_t rec_win = 2 * w * max_stride;
+        const uint64_t rec_win = nw * w * max_stride;
         if (col_win + rec_win > avail)
             throw InputError("gpu_memory_budget of " + std::to_string(budget) +
                              " bytes leaves " + std::to_string(avail) +
@@ -772,9 +784,11 @@ fbh_plan plan_memory(fbh_ctx &c, uint64_t budget) {
             P.resident_tiles++;
         }
         bool any_streamed = false;
+        uint32_t kept = 0;
         for (auto &t : c.tiles) {
             if (t.global) continue;
-            if (n * t.stride <= left) {
+            if (n * t.stride <= left && kept < c.resident_cap) {
+                kept++;
                 left -= n * t.stride;
                 P.resident_record_bytes += n * t.stride;
                 P.resident_tiles++;
@@ -854,6 +868,11 @@ fbh_config configure(fbh_ctx &c, uint64_t n_rows, const fbh_shape *shape, const 
         throw InputError("rows_per_block must be a positive multiple of 256");
     if (c.hist_tpb != 256 && c.hist_tpb != 512 && c.hist_tpb != 1024)
         throw InputError("histogram threads per workgroup must be 256, 512 or 1024");
+    if (conf.stream_windows > 2)
+        throw InputError("stream_windows (hist_streams) must be 1 or 2, got " +
+                         std::to_string(conf.stream_windows));
+    c.n_windows = conf.stream_windows ? conf.stream_windows : 2;
+    c.resident_cap = conf.resident_limit ? conf.resident_limit - 1 : UINT32_MAX;
     c.n_slots = conf.hist_slots ? conf.hist_slots : 64;
     if (c.n_slots > MAX_NODES)
         throw InputError("hist_slots must be at most " + std::to_string(MAX_NODES));
@@ -938,10 +957,10 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
             for (const auto &t : c->tiles) max_stride = std::max(max_stride, t.stride);
             for (uint32_t f = 0; f < c->n_features; f++)
                 max_w = std::max<uint32_t>(max_w, c->width[f]);
-            for (int k = 0; k < 2; k++)
+            for (uint32_t k = 0; k < c->n_windows; k++)
                 c->win_col[k] = c->alloc<uint8_t>(n_rows * max_w, "column window");
             if (P.window_rows)
-                for (int k = 0; k < 2; k++)
+                for (uint32_t k = 0; k < c->n_windows; k++)
                     c->win_rec[k] =
                         c->alloc<uint8_t>((uint64_t)P.window_rows * max_stride, "record window");
             for (const auto &t : c->tiles)
@@ -1185,6 +1204,37 @@ int fbh_set_objective(fbh_ctx *c, uint32_t objective, const float *labels,
     });
 }
 
+int fbh_set_gpu_math(fbh_ctx *c, uint32_t gpu_math) {
+    return guard([&] {
+        if (!c) throw InputError("null argument");
+        if (gpu_math > 1) throw InputError("gpu_math must be 0 (exact) or 1 (fast)");
+        c->fast_math = gpu_math == 1;
+    });
+}
+
+int fbh_gradient_pairs(int device, uint32_t objective, uint32_t gpu_math, const float *margin,
+                       const float *labels, const float *weights, uint64_t n, float *out) {
+    return guard([&] {
+        if ((!margin || !labels || !out) && n) throw InputError("null argument");
+        if (objective > 1) throw InputError("objective must be 0 (squared error) or 1 (logistic)");
+        if (gpu_math > 1) throw InputError("gpu_math must be 0 (exact) or 1 (fast)");
+        if (n == 0) return;
+        check(hipSetDevice(device), "hipSetDevice");
+        float *d = nullptr;
+        const uint64_t words = n * (weights ? 5 : 4);
+        check(hipMalloc(&d, 4 * words), "gradient buffers");
+        std::unique_ptr<float, decltype(&hipFree)> own(d, hipFree);
+        float *dm = d, *dy = d + n, *dg = d + 2 * n, *dw = weights ? d + 4 * n : nullptr;
+        check(hipMemcpy(dm, margin, 4 * n, hipMemcpyHostToDevice), "margin upload");
+        check(hipMemcpy(dy, labels, 4 * n, hipMemcpyHostToDevice), "label upload");
+        if (weights) check(hipMemcpy(dw, weights, 4 * n, hipMemcpyHostToDevice), "weight upload");
+        const int mode = objective == 0 ? 0 : (gpu_math ? 3 : 2);
+        check(launch_gradient(dm, dy, dw, n, mode, dg, UINT64_MAX, 0, 0, nullptr, 0, nullptr),
+              "gradient");
+        check(hipMemcpy(out, dg, 8 * n, hipMemcpyDeviceToHost), "gradient download");
+    });
+}
+
 int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th, uint64_t seed,
                           uint64_t tree, double scales_out[2], int64_t root_out[2]) {
     return guard([&] {
@@ -1193,6 +1243,9 @@ int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th
             throw InputError("the scales stay on the device only with neither a root sum nor "
                              "a sigmoid callback");
         if (c->objective < 0) throw InputError("fbh_set_objective has not been called");
+        if (fn && c->fast_math && c->objective == 1)
+            throw InputError("gpu_math=\"fast\" computes the logistic sigmoid on the device; "
+                             "a host sigmoid callback is not used with it");
         check(hipSetDevice(c->device), "hipSetDevice");
         if (c->leaves_pending) {
             check(hipEventSynchronize(c->leaves_done), "leaf table reuse");
@@ -1206,7 +1259,7 @@ int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th
             // f32 pairs go out too, for the histograms of scattered rows.
             const bool f32 = c->f32_hist();
             check(launch_gradient_spec(c->margin, c->labels, w, c->n_rows,
-                                       c->objective == 0 ? 0 : 2, th, seed, tree, c->red_f64,
+                                       c->gradient_mode(), th, seed, tree, c->red_f64,
                                        c->n_red_blocks, c->d_scales, c->gpair, c->red_i64,
                                        f32 ? c->gpair_f32 : nullptr, c->stream),
                   "device gradient");
@@ -1217,7 +1270,7 @@ int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th
         }
         if (c->objective == 0 || !fn) {
             // Squared error, or logistic with the device sigmoid.
-            check(launch_gradient(c->margin, c->labels, w, c->n_rows, c->objective == 0 ? 0 : 2,
+            check(launch_gradient(c->margin, c->labels, w, c->n_rows, c->gradient_mode(),
                                   c->gpair_f32, th, seed, tree, c->red_f64, c->n_red_blocks,
                                   c->stream),
                   "device gradient");
@@ -1591,7 +1644,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
             const uint64_t W = c->plan.window_rows;
             for (uint64_t lo = 0; lo < c->n_rows; lo += W) {
                 const uint64_t hi = std::min<uint64_t>(c->n_rows, lo + W);
-                const int b = (int)(c->win_flip++ & 1);
+                const int b = (int)(c->win_flip++ % c->n_windows);
                 check(hipStreamWaitEvent(c->copy_stream, c->win_free[b], 0), "stream wait");
                 check(hipMemcpyAsync(c->win_rec[b], t.host + lo * t.stride, (hi - lo) * t.stride,
                                      hipMemcpyHostToDevice, c->copy_stream),
@@ -1912,11 +1965,11 @@ PartStage stage_partition(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
         P.grp.push_back(g);
         P.groups.back().second++;
     }
-    // Streamed groups alternate between the two column windows.
+    // Streamed groups alternate between the column windows.
     P.group_win.assign(P.groups.size(), -1);
     for (size_t gi = 0; gi < P.groups.size(); gi++) {
         if (P.group_feat[gi] == UINT32_MAX) continue;
-        P.group_win[gi] = (int)(c->col_flip++ & 1);
+        P.group_win[gi] = (int)(c->col_flip++ % c->n_windows);
         for (uint32_t k = P.groups[gi].first; k < P.groups[gi].first + P.groups[gi].second; k++)
             P.grp[k].data = c->win_col[P.group_win[gi]];
     }

@@ -404,7 +404,8 @@ hipError_t launch_apply_leaves(const void *ids, int id_bytes, const float *value
 // Objective gradient pairs (f32, interleaved) from a per-row source value:
 // mode 0: squared error from the margin (g = p - y, h = 1);
 // mode 1: from the host's sigmoid s (g = s - y, h = max(s(1 - s), 1e-16));
-// mode 2: as 1 with s computed on the device from the margin.
+// mode 2: as 1 with s computed on the device from the margin;
+// mode 3: as 2 with the hardware exponential (gpu_math="fast").
 // All are multiplied by the row weight when w is non-null.
 hipError_t launch_gradient(const float *src, const float *y, const float *w, uint64_t n,
                            int mode, float *g2n, uint64_t threshold, uint64_t seed, uint64_t tree,

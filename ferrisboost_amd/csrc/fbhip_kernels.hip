@@ -1890,7 +1890,15 @@ hipError_t launch_apply_leaves(const void *ids, int id_bytes, const float *value
 // with the host's operation order; compiled without FMA contraction, so the
 // pairs equal the host's bit for bit. mode 0: squared error from the margin;
 // 1: logistic from the host's sigmoid in src; 2: logistic from the margin
-// with the device sigmoid (bit-identical to the host's libm).
+// with the device sigmoid (bit-identical to the host's libm); 3: logistic
+// from the margin with the hardware exponential (gpu_math="fast", the
+// reference's apply_delta_and_gradient, src/backend/cuda/histogram.cu:
+// 673-783: deterministic, not bit-equal to the host).
+__device__ __forceinline__ float fast_sigmoid(float m) { return 1.0f / (1.0f + __expf(-m)); }
+
+__device__ __forceinline__ float objective_source(int mode, float v) {
+    return mode == 2 ? fb_sigmoid(v) : mode == 3 ? fast_sigmoid(v) : v;
+}
 __device__ __forceinline__ bool row_selected(uint64_t row, uint64_t th, uint64_t seed,
                                              uint64_t tree);
 __device__ __forceinline__ double finite_abs(float v);
@@ -1937,7 +1945,7 @@ __global__ __launch_bounds__(256) void gradient_kernel(const float *src, const f
         for (int u = 0; u < U; u++) {
             const uint64_t i = base + u * S;
             if (i >= n) continue;
-            const float v = mode == 2 ? fb_sigmoid(sv[u]) : sv[u];
+            const float v = objective_source(mode, sv[u]);
             float g = v - yv[u];
             float h = mode != 0 ? fmaxf(v * (1.0f - v), 1e-16f) : 1.0f;
             if (w) {
@@ -1977,7 +1985,7 @@ __global__ __launch_bounds__(256) void gradient_fixup_kernel(const float *src, c
     uint64_t ag = 0, ah = 0;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * blockDim.x) {
-        const float v = mode == 2 ? fb_sigmoid(src[i]) : src[i];
+        const float v = objective_source(mode, src[i]);
         float g = v - y[i];
         float h = mode != 0 ? fmaxf(v * (1.0f - v), 1e-16f) : 1.0f;
         if (w) {

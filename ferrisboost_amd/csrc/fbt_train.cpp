@@ -1,7 +1,8 @@
 // fbt_train.cpp -- the round driver of the device path.
 //
 // Restates train_with_backend (src/training/mod.rs:1299-2376) for the
-// single-output logistic and squared-error objectives with gpu_math="exact".
+// single-output logistic and squared-error objectives, gpu_math "exact" or
+// "fast".
 // The device keeps labels, weights and margins; squared-error gradients are
 // computed there. For logistic, every round downloads the previous tree's
 // per-row leaf id (one byte at depth <= 8), the host applies the leaf value
@@ -650,8 +651,10 @@ void validate(const fbt_params &p, uint64_t n, uint32_t nf, const float *y) {
     if (nf == 0) throw InputError("training data must have at least one feature");
     if (p.objective > 1) throw InputError("objective must be reg:squarederror or binary:logistic");
     if (p.grow_policy > 1) throw InputError("grow_policy must be depthwise or lossguide");
-    if (p.gpu_math != 0)
-        throw InputError("gpu_math=\"fast\" is not available in ferrisboost_amd; use \"exact\"");
+    if (p.gpu_math > 1) throw InputError("gpu_math must be 0 (exact) or 1 (fast)");
+    if (p.gpu_math == 1 && p.host_sigmoid)
+        throw InputError("gpu_math=\"fast\" computes the sigmoid on the device; it cannot be "
+                         "combined with a host sigmoid");
     if (p.max_bin < 1 || p.max_bin > 65535)
         throw InputError("max_bin must be in 1..=65535, got " + std::to_string(p.max_bin));
     if (p.max_depth > 14)
@@ -775,6 +778,8 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     cfg.memory_budget = p.gpu_memory_budget;
     cfg.tile_bytes = p.tile_bytes;
     cfg.rows_per_block = p.rows_per_block;
+    cfg.stream_windows = p.hist_streams;
+    cfg.resident_limit = p.resident_limit;
     uint32_t slots;
     if (p.grow_policy == 1) {
         const uint64_t leaves = p.max_leaves ? p.max_leaves : (1ull << std::min(p.max_depth, 14u));
@@ -814,8 +819,12 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     }
     const uint32_t obj = p.objective;
     call(fbh_set_objective(ctx.get(), obj, y, grad_w, margin));
+    // gpu_math="fast" (fast_gradient_and_quantize, src/backend/cuda/train_ctx.rs:2404-2512):
+    // the logistic gradient takes the hardware exponential on the device.
+    call(fbh_set_gpu_math(ctx.get(), p.gpu_math));
     SigmoidJob job{&pool, pred.data(), &grower.leaf_values()};
-    const bool dev_sigmoid = obj == 1 && !p.host_sigmoid && device_sigmoid_matches_host(p.device);
+    const bool dev_sigmoid =
+        obj == 1 && !p.host_sigmoid && (p.gpu_math == 1 || device_sigmoid_matches_host(p.device));
     double grad_s = 0.0;
     g_round_wall.assign(p.n_rounds, 0.0);
     g_round_hist_ms.assign(p.n_rounds, 0.0);

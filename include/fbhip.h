@@ -58,7 +58,13 @@ typedef struct {
     uint32_t tile_bytes;     /* LDS bytes of one histogram tile (<= 160 KiB) */
     uint32_t rows_per_block; /* rows one histogram workgroup accumulates */
     uint32_t max_cat_words;  /* 64-bit words of the widest category set */
-    uint32_t reserved[6];
+    uint32_t stream_windows; /* hist_streams: 1 or 2 device windows of each kind
+                                for streamed records and columns (2: uploads
+                                overlap the kernels) */
+    uint32_t resident_limit; /* resident_blocks + 1: keep at most that many LDS
+                                tiles resident, streaming the rest even when
+                                they would fit (0: as the budget allows) */
+    uint32_t reserved[4];
 } fbh_config;
 
 /* Split-scan parameters: the TrainParams fields split.rs reads
@@ -233,6 +239,20 @@ typedef void (*fbh_sigmoid_fn)(void *user, uint64_t row_begin, uint64_t n, const
 int fbh_gradient_exchange(fbh_ctx *ctx, fbh_sigmoid_fn fn, void *user, uint64_t sample_threshold,
                           uint64_t seed, uint64_t tree, double scales_out[2],
                           int64_t root_sum_out[2]);
+
+/* gpu_math (src/python/mod.rs, TrainParams::gpu_math): 0 = "exact" (the
+ * default: the device sigmoid is bit-identical to the host libm's), 1 =
+ * "fast": the logistic gradient uses the hardware exponential, as the
+ * reference's fast path does on its device (apply_delta_and_gradient,
+ * src/backend/cuda/histogram.cu:673-783; fast_gradient_and_quantize,
+ * src/backend/cuda/train_ctx.rs:2404-2512): deterministic, not bit-equal to
+ * the CPU engine. A host sigmoid callback is an input error in fast mode. */
+int fbh_set_gpu_math(fbh_ctx *ctx, uint32_t gpu_math);
+/* The f32 gradient pairs [n][2] of `margin` under objective 0 / 1 with
+ * gpu_math 0 (exact) or 1 (fast), on host buffers (weights may be NULL):
+ * the per-row arithmetic of fbh_gradient_exchange, for characterisation. */
+int fbh_gradient_pairs(int device, uint32_t objective, uint32_t gpu_math, const float *margin,
+                       const float *labels, const float *weights, uint64_t n, float *gpair2n_out);
 
 /* The device margins (the training margins after the assigned trees). */
 int fbh_download_margin(fbh_ctx *ctx, float *out);

@@ -51,7 +51,9 @@ typedef struct {
     uint32_t reserved;
     /* device-path knobs */
     int32_t device;            /* "cuda:N" */
-    uint32_t gpu_math;         /* 0 = exact (the only mode) */
+    uint32_t gpu_math;         /* 0 = "exact" (bit-identical to the CPU engine),
+                                  1 = "fast" (hardware exp in the logistic
+                                  gradient: deterministic, not bit-equal) */
     uint64_t gpu_memory_budget;/* bytes, 0 = automatic */
     uint32_t tile_bytes;       /* LDS histogram tile (0 = default) */
     uint32_t rows_per_block;   /* histogram rows per workgroup (0 = default) */
@@ -65,6 +67,9 @@ typedef struct {
     uint32_t sync_round;       /* nonzero: the loop waits for the device before
                                   this round starts (a clean timing boundary;
                                   trees are otherwise collected a round late) */
+    uint32_t hist_streams;     /* hist_streams: 1 or 2 streaming windows (0 = 2) */
+    uint32_t resident_limit;   /* resident_blocks + 1: at most that many LDS
+                                  tiles stay resident (0 = as the budget allows) */
 } fbt_params;
 
 /* One tree node: Node (src/model/tree.rs:52-111). */

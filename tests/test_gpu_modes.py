@@ -1,0 +1,118 @@
+"""GPU: gpu_math="fast" and the reference's GPU knobs that this backend
+honours (hist_streams, resident_blocks)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import assert_same_models, product_params
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def fb():
+    import ferrisboost_amd as fb
+    from ferrisboost_amd import _native as N
+
+    if not N.device_available(0):
+        pytest.fail("no gfx950 device: the GPU suite needs an MI355X")
+    return fb
+
+
+def _pairs(N, objective, gpu_math, margin, labels, weights=None):
+    out = np.zeros(2 * margin.size, np.float32)
+    N.check_hip(N.hip().fbh_gradient_pairs(0, objective, gpu_math, N.ptr(margin), N.ptr(labels),
+                                           N.ptr(weights), margin.size, N.ptr(out)))
+    return out
+
+
+def _binned(oracle, x, max_bin=255):
+    """Column-major u8 bins under the oracle's sketch: #{cuts <= v}, NaN the
+    sentinel (find_bin, src/data/columns.rs:335-341)."""
+    vals, offs = oracle.sketch_cuts(x, max_bin)
+    nf = x.shape[1]
+    bins = np.empty((nf, x.shape[0]), np.uint8)
+    hoffs = np.zeros(nf + 1, np.uint32)
+    for f in range(nf):
+        c = vals[offs[f]:offs[f + 1]]
+        b = np.searchsorted(c, x[:, f], side="right").astype(np.int64)
+        b[np.isnan(x[:, f])] = 0xFF
+        bins[f] = b
+        hoffs[f + 1] = hoffs[f] + c.size + 1
+    return bins, hoffs
+
+
+def test_fast_pairs_keep_per_bin_sums_within_1e6(fb, oracle):
+    """gpu_math="fast" (apply_delta_and_gradient, src/backend/cuda/
+    histogram.cu:673-783): deterministic, and every per-bin histogram sum of
+    the narrow 10.5M x 28 workload's shape (here 1M rows, margins spread as
+    after training) within 1e-6 of the exact sum, relative to the bin's
+    magnitude. The exact pairs equal the oracle's host gradients bit for bit."""
+    from ferrisboost_amd import _native as N
+    from ferrisboost_amd import datasets
+
+    x, y, _, _ = datasets.narrow_binary(1_000_000, seed=12)
+    rng = np.random.default_rng(5)
+    margin = (rng.normal(0.0, 2.5, size=y.size)).astype(np.float32)
+    exact = _pairs(N, 1, 0, margin, y)
+    fast = _pairs(N, 1, 1, margin, y)
+    assert np.array_equal(fast.view(np.uint32), _pairs(N, 1, 1, margin, y).view(np.uint32))
+    want = np.zeros_like(exact)
+    oracle.lib().orc_gradients(oracle._p(margin), oracle._p(y), None, y.size, 1, oracle._p(want))
+    assert np.array_equal(exact.view(np.uint32), want.view(np.uint32))
+    assert not np.array_equal(exact.view(np.uint32), fast.view(np.uint32))  # a different exp
+    bins, offs = _binned(oracle, x)
+    scales = oracle.quantizer_scales(float(np.abs(exact[0::2]).max()),
+                                     float(np.abs(exact[1::2]).max()), y.size)
+    qe, _ = oracle.quantize(exact, scales)
+    qf, _ = oracle.quantize(fast, scales)
+    he = oracle.hist_build(bins, offs, qe).reshape(-1, 2).astype(np.float64)
+    hf = oracle.hist_build(bins, offs, qf).reshape(-1, 2).astype(np.float64)
+    mag = oracle.hist_build(bins, offs, np.abs(qe)).reshape(-1, 2).astype(np.float64)
+    rel = np.abs(hf - he) / np.maximum(mag, 1.0)
+    assert rel.max() <= 1e-6, rel.max()
+
+
+def test_fast_training_is_deterministic(fb):
+    from ferrisboost_amd import datasets
+
+    x, y, params, _ = datasets.narrow_binary(300_000, seed=13, max_bin=255)
+    p = dict(params, gpu_math="fast")
+    a = fb.train(p, x, y, num_boost_round=12)
+    b = fb.train(p, x, y, num_boost_round=12)
+    assert_same_models(a, b)
+    n = y.size
+    assert np.array_equal(a.train_margins(n).view(np.uint32), b.train_margins(n).view(np.uint32))
+    assert a.stats["device_sigmoid"] == 1
+    # squared error has no exponential: fast equals exact
+    sq = dict(params, objective="reg:squarederror")
+    assert_same_models(fb.train(sq, x, y, num_boost_round=3),
+                       fb.train(dict(sq, gpu_math="fast"), x, y, num_boost_round=3))
+
+
+@pytest.mark.parametrize("knobs", [{"resident_blocks": 0}, {"resident_blocks": 1},
+                                   {"resident_blocks": 0, "hist_streams": 1},
+                                   {"hist_streams": 1, "gpu_memory_budget": None}])
+def test_resident_blocks_and_hist_streams_keep_the_model(fb, oracle, knobs):
+    """resident_blocks caps the resident tiles (0: everything streams) and
+    hist_streams picks one or two streaming windows; trees and margins stay
+    those of the all-resident run and the oracle."""
+    rng = np.random.default_rng(101)
+    n, nf = 60_013, 36
+    x = rng.normal(size=(n, nf)).astype(np.float32)
+    x[rng.random((n, nf)) < 0.03] = np.nan
+    y = (np.nan_to_num(x[:, 1]) + np.nan_to_num(x[:, 20]) * np.nan_to_num(x[:, 33])
+         + 0.4 * rng.normal(size=n) > 0).astype(np.float32)
+    p = {"n_rounds": 3, "max_depth": 5, "eta": 0.3, "max_bin": 255}
+    pp = product_params(p)
+    ref = fb.train(pp, x, y, num_boost_round=3)
+    kn = {k: v for k, v in knobs.items() if v is not None}
+    got = fb.train(dict(pp, **kn), x, y, num_boost_round=3)
+    if "resident_blocks" in kn:
+        assert got.stats["resident_tiles"] == kn["resident_blocks"]
+        assert got.stats["streamed_bytes"] > 0
+    assert_same_models(ref, got)
+    assert np.array_equal(got.train_margins(n).view(np.uint32), ref.train_margins(n).view(np.uint32))
+    assert_same_models(oracle.train(x, y, oracle.make_params(**p)), got)

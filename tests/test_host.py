@@ -102,8 +102,12 @@ def _tiny():
     ({"grow_policy": "levelwise"}, "grow_policy"),
     ({"max_bin": 0}, "max_bin"),
     ({"max_bin": 70000}, "max_bin"),
-    ({"gpu_math": "fast"}, "gpu_math"),
     ({"gpu_math": "sloppy"}, "gpu_math"),
+    ({"hist_streams": 3}, "hist_streams"),
+    ({"resident_blocks": -1}, "resident_blocks"),
+    ({"hist_nodes_per_batch": 40}, "hist_nodes_per_batch"),
+    ({"hist_nodes_per_batch": 8}, "hist_nodes_per_batch is not available"),
+    ({"device_quantize": False}, "device_quantize"),
     ({"colsample_bylevel": 0.5}, "colsample_bylevel"),
     ({"colsample_bynode": 0.5}, "colsample_bynode"),
     ({"tree_method": "exact"}, "tree_method"),
@@ -137,6 +141,7 @@ def test_bad_shapes_are_value_errors():
     ({"eta": -1.0}, "learning_rate"),
     ({"subsample": 0.0}, "subsample"),
     ({"colsample_bytree": 1.5}, "colsample_bytree"),
+    ({"gpu_math": "fast", "hip_host_sigmoid": True}, "gpu_math"),
 ])
 def test_driver_validation_is_input_error(params, msg):
     """The C++ driver validates before any device call (src/types.rs:432-660,
@@ -231,7 +236,7 @@ def test_host_sigmoid_restatement_equals_libm(oracle):
 # ---------------------------------------------------------------- memory plan
 
 def _plan(n_rows, n_features, n_bins=256, width=1, budget=0, free=0, slots=128,
-          categorical=None):
+          categorical=None, windows=0, resident_limit=0):
     from ferrisboost_amd import _native as N
 
     w = np.full(n_features, width, np.uint8)
@@ -241,6 +246,8 @@ def _plan(n_rows, n_features, n_bins=256, width=1, budget=0, free=0, slots=128,
     cfg = N.Config()
     cfg.memory_budget = budget
     cfg.hist_slots = slots
+    cfg.stream_windows = windows
+    cfg.resident_limit = resident_limit
     out = N.Plan()
     N.check_hip(N.hip().fbh_plan_memory(n_rows, C.byref(shape), C.byref(cfg), free, C.byref(out)))
     return out
@@ -277,6 +284,30 @@ def test_plan_residency_grows_with_the_budget():
         assert p.resident_tiles >= prev
         prev = p.resident_tiles
     assert prev == _plan(50_000_000, 200, budget=24 << 30).n_tiles
+
+
+def test_plan_resident_blocks_caps_resident_tiles():
+    """resident_blocks (python/ferrisboost/__init__.py:233-239): at most that
+    many tiles stay resident even when all would fit; 0 is pure streaming."""
+    full = _plan(2_000_000, 120, free=280 << 30)
+    assert full.resident_tiles == full.n_tiles >= 4
+    for k in (0, 1, 3):
+        p = _plan(2_000_000, 120, free=280 << 30, resident_limit=k + 1)
+        assert p.resident_tiles == k and p.columns_resident == 0
+        assert p.staging_bytes > 0 and p.streamed_record_bytes > 0
+    big = _plan(2_000_000, 120, free=280 << 30, resident_limit=full.n_tiles + 5)
+    assert big.resident_tiles == big.n_tiles and big.columns_resident == 1
+
+
+def test_plan_hist_streams_sets_the_streaming_windows():
+    """hist_streams 1 keeps one window of each kind instead of two: half the
+    staging bytes (src/python/mod.rs:224-231 validates 1 or 2)."""
+    two = _plan(50_000_000, 200, budget=6 << 30)
+    one = _plan(50_000_000, 200, budget=6 << 30, windows=1)
+    assert two.staging_bytes == 2 * one.staging_bytes
+    assert one.window_rows == two.window_rows and one.peak_bytes <= one.budget
+    with pytest.raises(ValueError, match="stream_windows"):
+        _plan(50_000_000, 200, budget=6 << 30, windows=3)
 
 
 def test_plan_rejects_a_budget_below_the_per_row_arrays():
