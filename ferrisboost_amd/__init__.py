@@ -27,7 +27,7 @@ import numpy as np
 
 from . import _native as N
 
-__all__ = ["train", "Model", "device_available", "__version__"]
+__all__ = ["train", "sketch", "Cuts", "Model", "device_available", "__version__"]
 __version__ = "0.1.0"
 
 # Canonical name -> default, as python/ferrisboost/__init__.py:_DEFAULTS.
@@ -495,28 +495,70 @@ class Model:
         return Model(h, L.fbt_model_n_features(h), obj, _parse_device(device))
 
 
-def train(params: Mapping[str, Any], X, label, weight=None, num_boost_round: int = 10) -> Model:
-    """fb.train on the device path (python/ferrisboost/__init__.py:train)."""
-    p = _normalize(params, num_boost_round)
+class Cuts:
+    """Quantile cuts of a matrix (BinCuts, src/data/columns.rs:50-360): the
+    sketch of one training matrix, reusable by several train() calls on the
+    same data (no reference counterpart: the reference sketches per source)."""
+
+    def __init__(self, values: np.ndarray, offsets: np.ndarray, max_bin: int,
+                 categorical: np.ndarray | None):
+        self.values = np.ascontiguousarray(values, np.float32)
+        self.offsets = np.ascontiguousarray(offsets, np.uint32)
+        self.max_bin = int(max_bin)
+        self.categorical = None if categorical is None else np.ascontiguousarray(categorical, np.uint8)
+
+
+def _categorical_flags(feature_types, n_features):
+    if feature_types is None:
+        return None
+    if len(feature_types) != n_features:
+        raise ValueError("feature_types must have one entry per feature")
+    return np.array([1 if t == "c" else 0 for t in feature_types], np.uint8)
+
+
+def _matrix(X, missing):
     X = np.asarray(X, dtype=np.float32)
     if X.ndim != 2:
         raise ValueError("X must be a 2-D array")
     X = np.ascontiguousarray(X)
-    miss = p["missing"]
-    if miss is not None and not (isinstance(miss, float) and np.isnan(miss)):
-        X = np.where(X == np.float32(miss), np.float32("nan"), X).astype(np.float32)
+    if missing is not None and not (isinstance(missing, float) and np.isnan(missing)):
+        X = np.where(X == np.float32(missing), np.float32("nan"), X).astype(np.float32)
+    return X
+
+
+def sketch(X, max_bin: int = 255, weight=None, feature_types=None,
+           missing: float = float("nan")) -> Cuts:
+    """The cuts train() would sketch for this matrix (FeatureSketch::cuts,
+    src/data/sketch.rs:236-275, one sketch per feature): pass them to
+    train(..., cuts=) to train several models without sketching again."""
+    X = _matrix(X, missing)
+    if not 0 < int(max_bin) <= 65535:
+        raise ValueError(f"max_bin must be in 1..=65535, got {max_bin}")
+    n, nf = X.shape
+    w = None if weight is None else np.ascontiguousarray(np.asarray(weight, dtype=np.float32))
+    cat = _categorical_flags(feature_types, nf)
+    cap = sum(65534 if (cat is not None and cat[f]) else max(int(max_bin), 2) for f in range(nf))
+    vals = np.zeros(cap + 1, np.float32)
+    offs = np.zeros(nf + 1, np.uint32)
+    N.check_train(N.train_lib().fbt_sketch_cuts(N.ptr(X), n, nf, int(max_bin), N.ptr(w), N.ptr(cat),
+                                                N.ptr(vals), N.ptr(offs)))
+    return Cuts(vals[: offs[-1]].copy(), offs, max_bin, cat)
+
+
+def train(params: Mapping[str, Any], X, label, weight=None, num_boost_round: int = 10,
+          cuts: Cuts | None = None) -> Model:
+    """fb.train on the device path (python/ferrisboost/__init__.py:train).
+    cuts (from sketch() on the same matrix, max_bin and feature_types)
+    replaces the sketch."""
+    p = _normalize(params, num_boost_round)
+    X = _matrix(X, p["missing"])
     y = np.ascontiguousarray(np.asarray(label, dtype=np.float32))
     if y.shape != (X.shape[0],):
         raise ValueError(f"label has {y.size} rows, but the training data has {X.shape[0]} rows")
     w = None if weight is None else np.ascontiguousarray(np.asarray(weight, dtype=np.float32))
     if w is not None and w.shape != (X.shape[0],):
         raise ValueError("weight must have one value per row")
-    cat = None
-    ft = p["feature_types"]
-    if ft is not None:
-        if len(ft) != X.shape[1]:
-            raise ValueError("feature_types must have one entry per feature")
-        cat = np.array([1 if t == "c" else 0 for t in ft], np.uint8)
+    cat = _categorical_flags(p["feature_types"], X.shape[1])
     mono = None
     mc = p["monotone_constraints"]
     if mc:
@@ -525,11 +567,20 @@ def train(params: Mapping[str, Any], X, label, weight=None, num_boost_round: int
         mono = np.ascontiguousarray([int(np.sign(v)) for v in mc], np.int8)
     s = _params_struct(p, X.shape[1])
     h = C.c_void_p()
-    N.check_train(N.train_lib().fbt_train(
-        N.ptr(X), X.shape[0], X.shape[1], N.ptr(y), N.ptr(w), N.ptr(cat), N.ptr(mono),
-        0 if mono is None else mono.size, C.byref(s), C.byref(h)))
+    L = N.train_lib()
+    if cuts is None:
+        N.check_train(L.fbt_train(
+            N.ptr(X), X.shape[0], X.shape[1], N.ptr(y), N.ptr(w), N.ptr(cat), N.ptr(mono),
+            0 if mono is None else mono.size, C.byref(s), C.byref(h)))
+    else:
+        if cuts.max_bin != int(p["max_bin"]) or cuts.offsets.size != X.shape[1] + 1:
+            raise ValueError("cuts were sketched for another max_bin or feature count")
+        N.check_train(L.fbt_train_cuts(
+            N.ptr(X), X.shape[0], X.shape[1], N.ptr(y), N.ptr(w), N.ptr(cat), N.ptr(mono),
+            0 if mono is None else mono.size, C.byref(s), N.ptr(cuts.values), N.ptr(cuts.offsets),
+            C.byref(h)))
     m = Model(h, X.shape[1], p["objective"], s.device)
     st = N.Stats()
-    N.check_train(N.train_lib().fbt_last_stats(C.byref(st)))
+    N.check_train(L.fbt_last_stats(C.byref(st)))
     m.stats = {k: getattr(st, k) for k, _ in N.Stats._fields_ if k != "reserved"}
     return m

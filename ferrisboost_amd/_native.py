@@ -216,7 +216,7 @@ HIP_SYMBOLS = [
     "fbh_saabas_contribs", "fbh_predict", "fbh_predict_device", "fbh_shap_contribs_noalloc",
 ]
 TRAIN_SYMBOLS = [
-    "fbt_last_error", "fbt_train", "fbt_last_stats", "fbt_last_round_stats", "fbt_model_free", "fbt_model_n_trees",
+    "fbt_last_error", "fbt_train", "fbt_train_cuts", "fbt_last_stats", "fbt_last_round_stats", "fbt_model_free", "fbt_model_n_trees",
     "fbt_model_tree_len", "fbt_model_tree_nodes", "fbt_model_n_cat_words", "fbt_model_cat_words",
     "fbt_model_base_score", "fbt_model_base_margin", "fbt_model_n_features",
     "fbt_model_train_margins", "fbt_model_n_cuts", "fbt_model_cuts", "fbt_predict_margin",
@@ -317,6 +317,8 @@ def train_lib() -> C.CDLL:
         L.fbt_last_error.restype = C.c_size_t
         L.fbt_train.argtypes = [P, C.c_uint64, C.c_uint32, P, P, P, P, C.c_uint32,
                                 C.POINTER(TrainParams), C.POINTER(P)]
+        L.fbt_train_cuts.argtypes = [P, C.c_uint64, C.c_uint32, P, P, P, P, C.c_uint32,
+                                     C.POINTER(TrainParams), P, P, C.POINTER(P)]
         L.fbt_last_stats.argtypes = [C.POINTER(Stats)]
         L.fbt_last_round_stats.argtypes = [P, P, P, C.c_uint32]
         L.fbt_last_round_stats.restype = C.c_uint32

@@ -11,7 +11,8 @@
 
 namespace fbt {
 Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float *w,
-            const uint8_t *cat, const int8_t *mono, uint32_t n_mono, const fbt_params &p);
+            const uint8_t *cat, const int8_t *mono, uint32_t n_mono, const fbt_params &p,
+            const Cuts *given);
 fbt_stats last_stats();
 uint32_t last_round_stats(double *wall, double *ms, uint64_t *bytes, uint32_t cap);
 }  // namespace fbt
@@ -63,7 +64,28 @@ int fbt_train(const float *x, uint64_t n_rows, uint32_t n_features, const float 
         *out = nullptr;
         auto m = std::make_unique<fbt_model>();
         m->m = fbt::train(x, n_rows, n_features, labels, weights, categorical, monotone, n_monotone,
-                          *params);
+                          *params, nullptr);
+        *out = m.release();
+    });
+}
+
+int fbt_train_cuts(const float *x, uint64_t n_rows, uint32_t n_features, const float *labels,
+                   const float *weights, const uint8_t *categorical, const int8_t *monotone,
+                   uint32_t n_monotone, const fbt_params *params, const float *cut_values,
+                   const uint32_t *cut_offsets, fbt_model **out) {
+    return guard([&] {
+        if (!x || !labels || !params || !out || !cut_values || !cut_offsets)
+            throw fbt::InputError("null argument");
+        *out = nullptr;
+        fbt::Cuts c;
+        c.offsets.assign(cut_offsets, cut_offsets + n_features + 1);
+        c.values.assign(cut_values, cut_values + c.offsets.back());
+        c.categorical.assign(n_features, 0);
+        for (uint32_t f = 0; f < n_features; f++)
+            c.categorical[f] = categorical && categorical[f] ? 1 : 0;
+        auto m = std::make_unique<fbt_model>();
+        m->m = fbt::train(x, n_rows, n_features, labels, weights, categorical, monotone, n_monotone,
+                          *params, &c);
         *out = m.release();
     });
 }

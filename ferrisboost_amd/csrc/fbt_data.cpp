@@ -248,6 +248,33 @@ Cuts sketch_matrix(const float *x, uint64_t n, uint32_t nf, uint32_t max_bin, co
     return c;
 }
 
+void check_cuts(const Cuts &c, uint32_t nf, uint32_t max_bin, const uint8_t *cat) {
+    if (c.offsets.size() != (size_t)nf + 1 || c.offsets[0] != 0 ||
+        c.offsets.back() != c.values.size())
+        throw InputError("cuts: offsets must hold n_features + 1 entries from 0 to the value count");
+    for (uint32_t f = 0; f < nf; f++) {
+        if (c.offsets[f + 1] < c.offsets[f]) throw InputError("cuts: offsets must not decrease");
+        const bool is_cat = cat && cat[f];
+        if ((c.categorical[f] != 0) != is_cat)
+            throw InputError("cuts: feature " + std::to_string(f) +
+                             " is categorical in one place and numeric in the other");
+        const uint32_t nc = c.n_cuts(f);
+        if (!is_cat && nc + 1 > std::max(max_bin, 1u))
+            throw InputError("cuts: feature " + std::to_string(f) + " has " + std::to_string(nc) +
+                             " cuts, more than max_bin - 1 = " + std::to_string(max_bin - 1));
+        if (c.n_bins(f) > (is_cat ? 65534u : 65535u))
+            throw InputError("cuts: feature " + std::to_string(f) + " has too many bins");
+        const float *v = c.values.data() + c.offsets[f];
+        for (uint32_t i = 0; i < nc; i++) {
+            if (!std::isfinite(v[i]))
+                throw InputError("cuts: feature " + std::to_string(f) + " has a non-finite cut");
+            if (i && !(v[i] > v[i - 1]))
+                throw InputError("cuts: feature " + std::to_string(f) +
+                                 " cuts must be strictly increasing");
+        }
+    }
+}
+
 void bin_columns(const float *x, uint64_t n, uint32_t nf, const Cuts &cuts,
                  const std::vector<uint32_t> &feats, uint32_t width, void *out, unsigned threads) {
     parallel_for((uint32_t)feats.size(), threads, [&](uint32_t l) {

@@ -38,6 +38,11 @@ struct Cuts {
 Cuts sketch_matrix(const float *x, uint64_t n_rows, uint32_t n_features, uint32_t max_bin,
                    const float *weights, const uint8_t *categorical, unsigned threads);
 
+// Cuts handed in by a caller (fbt_train_cuts): per feature strictly
+// increasing finite values, at most max_bin - 1 for a numeric feature and
+// categorical flags matching `categorical`; InputError otherwise.
+void check_cuts(const Cuts &c, uint32_t n_features, uint32_t max_bin, const uint8_t *categorical);
+
 // Column-major bins of `feats` (one width) for upload.
 void bin_columns(const float *x, uint64_t n_rows, uint32_t n_features, const Cuts &cuts,
                  const std::vector<uint32_t> &feats, uint32_t width, void *out, unsigned threads);

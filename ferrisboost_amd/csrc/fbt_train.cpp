@@ -702,7 +702,8 @@ uint32_t last_round_stats(double *wall, double *ms, uint64_t *bytes, uint32_t ca
 }
 
 Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float *w,
-            const uint8_t *cat, const int8_t *mono_in, uint32_t n_mono, const fbt_params &p) {
+            const uint8_t *cat, const int8_t *mono_in, uint32_t n_mono, const fbt_params &p,
+            const Cuts *given) {
     const auto t_setup = Clock::now();
     validate(p, n, nf, y);
     if (n_mono > nf) throw InputError("monotone_constraints has more entries than features");
@@ -726,7 +727,12 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     m.objective = p.objective;
     m.n_features = nf;
     m.scale_pos_weight = p.scale_pos_weight;
-    m.cuts = sketch_matrix(x, n, nf, p.max_bin, w, cat, threads);
+    if (given) {
+        check_cuts(*given, nf, p.max_bin, cat);
+        m.cuts = *given;
+    } else {
+        m.cuts = sketch_matrix(x, n, nf, p.max_bin, w, cat, threads);
+    }
     // Base score: explicit, else the label mean weighted by the sample weights
     // only (Objective::estimate_base_score, src/training/objective.rs:42-60,
     // 452-470; scale_pos_weight enters the gradient weights alone,

@@ -118,6 +118,16 @@ size_t fbt_last_error(char *buf, size_t len);
 int fbt_train(const float *x, uint64_t n_rows, uint32_t n_features, const float *labels,
               const float *weights, const uint8_t *categorical, const int8_t *monotone,
               uint32_t n_monotone, const fbt_params *params, fbt_model **out);
+/* fbt_train with the cuts given instead of sketched (the cut_values /
+ * cut_offsets fbt_sketch_cuts returns for the same data, max_bin, weights
+ * and categorical flags), so several models over one matrix share one
+ * sketch. The cuts are checked (strictly increasing finite values, at most
+ * max_bin - 1 per numeric feature, offsets n_features + 1 long); no
+ * reference counterpart (the reference re-sketches per DenseSource). */
+int fbt_train_cuts(const float *x, uint64_t n_rows, uint32_t n_features, const float *labels,
+                   const float *weights, const uint8_t *categorical, const int8_t *monotone,
+                   uint32_t n_monotone, const fbt_params *params, const float *cut_values,
+                   const uint32_t *cut_offsets, fbt_model **out);
 int fbt_last_stats(fbt_stats *out);
 /* Per-round timing of the last training call: wall seconds of round r (from
  * its start to the start of round r+1, delta download and gradient pass
