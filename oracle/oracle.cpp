@@ -1923,6 +1923,17 @@ uint64_t orc_sigmoid_checksum(uint64_t begin, uint64_t end, uint32_t threads) {
     return acc;
 }
 
+void orc_splitmix64(uint64_t seed, uint64_t n, uint64_t *out) {
+    SplitMix64 r{seed};
+    for (uint64_t i = 0; i < n; i++) out[i] = r.next();
+}
+
+uint64_t orc_mix64(uint64_t z) { return mix64(z); }
+
+uint64_t orc_row_hash(uint64_t row, uint64_t seed, uint64_t tree) {
+    return mix64(seed ^ rotl(tree * 0x9E3779B97F4A7C15ull, 23) ^ (row * 0xD6E8FEB86659FD93ull));
+}
+
 uint64_t orc_threshold_for(float rate) { return threshold_for(rate); }
 
 int orc_row_selected(uint64_t row, uint64_t th, uint64_t seed, uint64_t tree) {

@@ -165,6 +165,13 @@ void orc_quadrature_rule(float nodes[8], float weights[8]);
 uint32_t orc_sample_features(uint32_t n_features, float rate, uint64_t seed, uint64_t round,
                              uint32_t *out);
 
+/* ---- the generators behind sampling ----
+ * SplitMix64::next_u64 (src/data/colsample.rs:34-45) from `seed`, n outputs;
+ * its finaliser mix (src/data/subsample.rs:44-47); row_hash (:50-55). */
+void orc_splitmix64(uint64_t seed, uint64_t n, uint64_t *out);
+uint64_t orc_mix64(uint64_t z);
+uint64_t orc_row_hash(uint64_t row, uint64_t seed, uint64_t tree);
+
 /* ---- row subsample (src/data/subsample.rs:1-104) ---- */
 uint64_t orc_threshold_for(float rate);
 int orc_row_selected(uint64_t row, uint64_t threshold, uint64_t seed, uint64_t tree);

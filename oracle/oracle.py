@@ -179,6 +179,12 @@ def lib() -> C.CDLL:
         L.orc_sigmoid.restype = None
         L.orc_sigmoid_checksum.argtypes = [C.c_uint64, C.c_uint64, C.c_uint32]
         L.orc_sigmoid_checksum.restype = C.c_uint64
+        L.orc_splitmix64.argtypes = [C.c_uint64, C.c_uint64, P]
+        L.orc_splitmix64.restype = None
+        L.orc_mix64.argtypes = [C.c_uint64]
+        L.orc_mix64.restype = C.c_uint64
+        L.orc_row_hash.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64]
+        L.orc_row_hash.restype = C.c_uint64
         L.orc_threshold_for.argtypes = [C.c_float]
         L.orc_threshold_for.restype = C.c_uint64
         L.orc_row_selected.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64]

@@ -42,6 +42,27 @@ def test_headers_declare_the_boundary():
     assert {"fbt_train", "fbt_shap", "fbt_model_to_json"} <= set(train)
 
 
+def test_integration_ffi_block_matches_the_header():
+    """INTEGRATION.md's Rust FFI block declares every function of
+    include/fbhip.h with the same parameter and return types, in order, and
+    every #[repr(C)] struct with the header's fields (names and types)."""
+    import ffi_check as F
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    hdr = open(os.path.join(root, "include", "fbhip.h")).read()
+    block = F.rust_block(open(os.path.join(root, "INTEGRATION.md")).read())
+    hf, rf = F.header_functions(hdr), F.rust_functions(block)
+    assert set(hf) == set(rf), (sorted(set(hf) - set(rf)), sorted(set(rf) - set(hf)))
+    for name, (ret, args) in hf.items():
+        rret, rargs = rf[name]
+        assert (rret if rret != "()" else "c_void") == ret, name
+        assert [t for _, t in rargs] == [t for _, t in args], name
+    hs, rs = F.header_structs(hdr), F.rust_structs(block)
+    assert len(hs) >= 10
+    for name, fields in hs.items():
+        assert rs.get(name) == fields, name
+
+
 def test_libraries_export_every_declared_symbol():
     from ferrisboost_amd import _native as N
 
