@@ -148,8 +148,17 @@ struct fbh_ctx {
         uint8_t *host = nullptr;   // pinned host records of a streamed tile
         int32_t bundle = -1;       // row bundle holding the records, or -1
         uint32_t bundle_off = 0;   // offset of the record in the bundle row
+        bool rot = false;          // interleaved LDS layout (16 cells a record)
     };
     std::vector<Tile> tiles;
+    // Packed tiles of the current tree: with column sampling, the tree's
+    // features of interleaved tiles are packed 16 to a record (from the bin
+    // columns, into `pack`) when that takes at most 3/4 of the tiles that
+    // hold them, so the histograms read and add no unsampled cells.
+    std::vector<Tile> pack_tiles;
+    uint8_t *pack = nullptr;
+    uint64_t pack_bytes = 0;
+    std::vector<uint32_t> pack_sig;  // features (and width marks) the pack holds now
     // Row bundles: consecutive tiles of one width and record size whose
     // records fit in 64 bytes share one allocation, row r's records together
     // at data + r * pitch. A histogram over a scattered node then fetches one
@@ -253,7 +262,9 @@ struct fbh_ctx {
         };
         std::deque<Job> pending;
     } grow;
-    size_t off_tilefeats = 0, off_sfeats = 0, off_order = 0;  // offsets in the tree-table buffer
+    // offsets in the tree-table buffer
+    size_t off_tilefeats = 0, off_sfeats = 0, off_order = 0, off_pack = 0, tables_bytes = 0;
+    PackTileDev *d_pack = nullptr;  // the packed tiles' sources (tree tables)
     uint32_t *d_split_order = nullptr;  // tree features: numeric positions, then categorical
     uint32_t n_split_num = 0, n_split_cat = 0;
     size_t stage_bytes = 0;
@@ -285,6 +296,7 @@ struct fbh_ctx {
         uint32_t lds_max;
         uint32_t bytes_per_row;  // active feature bytes of the group's tiles
         bool global;
+        bool rot;
     };
     std::vector<Group> groups;
     struct Streamed {
@@ -538,28 +550,66 @@ void fbh_ctx::ensure_rows() {
 
 namespace {
 
+// Features of `width` bytes that go to interleaved tiles: at least 9 of
+// them (fewer fill a compact planar record better), 8-bit ones or 16-bit
+// ones of at most HIST_ROT_BINS bins; none when the tile budget is below the
+// interleaved layout's.
+std::vector<uint32_t> rot_features(const fbh_ctx &c, uint32_t w,
+                                   const std::vector<uint32_t> &feats) {
+    std::vector<uint32_t> out;
+    if (c.tile_bytes < DEFAULT_TILE_BYTES) return out;
+    for (uint32_t f : feats)
+        if (c.width[f] == w && c.n_bins[f] <= HIST_ROT_BINS) out.push_back(f);
+    if (out.size() < 9) out.clear();
+    return out;
+}
+
+// Interleaved tiles holding `feats` (16-cell records), the features spread
+// evenly over ceil(n / 16) tiles so that no tile is left nearly empty.
+template <class F>
+void rot_tiles(uint32_t w, const std::vector<uint32_t> &feats, F &&emit) {
+    const size_t n = feats.size(), nt = (n + 15) / 16;
+    for (size_t i = 0; i < nt; i++) {
+        fbh_ctx::Tile t{w, 16 * w, 16 * w, {}, nullptr, false};
+        t.rot = true;
+        for (size_t k = n * i / nt; k < n * (i + 1) / nt; k++) t.feats.push_back(feats[k]);
+        emit(std::move(t));
+    }
+}
+
 void plan_tiles(fbh_ctx &c) {
     c.feat_tile.assign(c.n_features, -1);
     c.feat_pos.assign(c.n_features, -1);
+    auto push = [&](fbh_ctx::Tile t) {
+        const uint32_t id = (uint32_t)c.tiles.size();
+        for (size_t k = 0; k < t.feats.size(); k++) {
+            c.feat_tile[t.feats[k]] = (int32_t)id;
+            c.feat_pos[t.feats[k]] = (int32_t)k;
+        }
+        c.tiles.push_back(std::move(t));
+    };
+    std::vector<uint32_t> all(c.n_features);
+    for (uint32_t f = 0; f < c.n_features; f++) all[f] = f;
     for (uint32_t w : {1u, 2u}) {
+        const std::vector<uint32_t> rot = rot_features(c, w, all);
+        std::vector<uint8_t> in_rot(c.n_features, 0);
+        for (uint32_t f : rot) in_rot[f] = 1;
+        rot_tiles(w, rot, push);
         fbh_ctx::Tile cur{w, 0, 0, {}, nullptr, false};
         uint64_t lds = 0;
         auto flush = [&]() {
             if (cur.feats.empty()) return;
             cur.rec = round_stride((uint32_t)cur.feats.size() * w);
             cur.stride = cur.rec;
-            const uint32_t t = (uint32_t)c.tiles.size();
-            for (size_t k = 0; k < cur.feats.size(); k++) {
-                c.feat_tile[cur.feats[k]] = (int32_t)t;
-                c.feat_pos[cur.feats[k]] = (int32_t)k;
-            }
-            c.tiles.push_back(cur);
+            // an 8-bit 16-byte record is always interleaved
+            cur.rot = w == 1 && cur.rec == 16 && !cur.global;
+            push(cur);
             cur.feats.clear();
             cur.global = false;
             lds = 0;
         };
         for (uint32_t f = 0; f < c.n_features; f++) {
-            if (c.width[f] != w) continue;
+            if (c.width[f] != w || in_rot[f]) continue;
             // The tile's LDS also holds 64 per-lane dummy slots (1 KiB).
             const uint64_t budget = c.tile_bytes - 1024u;
             const uint64_t fb = (uint64_t)c.n_bins[f] * 16u;
@@ -656,12 +706,15 @@ void fixed_allocations(fbh_ctx &c, A &&a) {
     c.off_tilefeats = al256(sizeof(TileDev) * c.tiles.size());
     c.off_sfeats = c.off_tilefeats + al256(sizeof(TileFeatDev) * c.n_features);
     c.off_order = c.off_sfeats + al256(sizeof(SplitFeatDev) * c.n_features);
-    uint8_t *tt = static_cast<uint8_t *>(
-        a(c.off_order + 4 * (uint64_t)c.n_features, "tree tables"));
+    c.off_pack = c.off_order + al256(4 * (uint64_t)c.n_features);
+    // at most ceil(features / 16) packed tiles of each width
+    c.tables_bytes = c.off_pack + sizeof(PackTileDev) * ((uint64_t)c.n_features / 16 + 2);
+    uint8_t *tt = static_cast<uint8_t *>(a(c.tables_bytes, "tree tables"));
     c.d_tiles = reinterpret_cast<TileDev *>(tt);
     c.d_tilefeats = reinterpret_cast<TileFeatDev *>(tt ? tt + c.off_tilefeats : nullptr);
     c.d_sfeats = reinterpret_cast<SplitFeatDev *>(tt ? tt + c.off_sfeats : nullptr);
     c.d_split_order = reinterpret_cast<uint32_t *>(tt ? tt + c.off_order : nullptr);
+    c.d_pack = reinterpret_cast<PackTileDev *>(tt ? tt + c.off_pack : nullptr);
     const uint64_t cw = std::max(1u, c.max_cat_words);
     c.d_cands = static_cast<FeatCandDev *>(
         a(sizeof(FeatCandDev) * (uint64_t)c.n_slots * c.n_features, "split candidates"));
@@ -689,9 +742,7 @@ void fixed_allocations(fbh_ctx &c, A &&a) {
                                (size_t)c.n_slots * c.n_features + 8 * 256;
     const size_t part_tables = 2 * sizeof(PartReqDev) * MAX_NODES + 8 * c.cat_in_words + 4 * 256;
     const size_t pair_tables = sizeof(PairDev) * MAX_NODES + 256;
-    c.stage_bytes = std::max<size_t>(
-        {eval_tables + part_tables + pair_tables,
-         c.off_order + 4 * (size_t)c.n_features});
+    c.stage_bytes = std::max<size_t>({eval_tables + part_tables + pair_tables, c.tables_bytes});
     c.d_stage = static_cast<uint8_t *>(a(c.stage_bytes, "launch tables"));
 }
 
@@ -1070,11 +1121,91 @@ int fbh_upload_block(fbh_ctx *c, const uint32_t *feat_ids, uint32_t n_feats, uin
             }
             c->uploaded[f] = 1;
         }
+        c->pack_sig.clear();  // packed records of these features are stale
         c->sync();
     });
 }
 
 namespace {
+
+// This tree's packed tiles (fbh_ctx::pack_tiles) from its compact histogram
+// layout (hist_off). Per width, the tree's features of interleaved tiles are
+// packed when every such tile is resident, the bin columns are on the
+// device, ceil(features / 16) tiles are at most 3/4 of the tiles holding
+// them, and the pack fits the budget's remaining room (it is outside the
+// memory plan). Packed tiles of one width share 64-byte row bundles.
+// Returns the widths packed: bit 1 for 8-bit, bit 2 for 16-bit tiles.
+uint32_t plan_pack(fbh_ctx &c) {
+    c.pack_tiles.clear();
+    if (!c.plan.columns_resident) return 0;
+    struct Want {
+        uint32_t w;
+        std::vector<uint32_t> feats;
+    };
+    std::vector<Want> want;
+    for (uint32_t w : {1u, 2u}) {
+        uint32_t holding = 0;
+        bool resident = true;
+        std::vector<uint32_t> feats;
+        for (const auto &t : c.tiles) {
+            if (!t.rot || t.width != w) continue;
+            resident = resident && t.resident;
+            bool any = false;
+            for (uint32_t f : t.feats)
+                if (c.hist_off[f] >= 0) {
+                    feats.push_back(f);
+                    any = true;
+                }
+            holding += any ? 1 : 0;
+        }
+        const uint32_t nt = (uint32_t)(feats.size() + 15) / 16;
+        if (!resident || feats.empty() || 4 * nt > 3 * holding) continue;
+        std::sort(feats.begin(), feats.end());
+        want.push_back({w, std::move(feats)});
+    }
+    if (want.empty()) return 0;
+    // Bundle b of width w: tiles [b * per, (b + 1) * per), per = 64 / (16 w).
+    auto pitch_of = [](uint32_t w, uint32_t k) {
+        uint32_t p = 16;
+        while (p < 16 * w * k) p *= 2;
+        return p;
+    };
+    uint64_t need = 0;
+    for (const auto &x : want) {
+        const uint32_t nt = (uint32_t)(x.feats.size() + 15) / 16, per = 4 / x.w;
+        for (uint32_t b = 0; b * per < nt; b++)
+            need += c.n_rows * pitch_of(x.w, std::min(per, nt - b * per));
+    }
+    if (need > c.pack_bytes) {
+        if (c.device_bytes - c.pack_bytes + need + 256 > c.plan.budget) return 0;
+        c.release_alloc(c.pack);
+        c.pack = nullptr;
+        c.pack_bytes = 0;
+        c.pack_sig.clear();
+        c.pack = c.alloc<uint8_t>(need, "packed tiles");
+        c.pack_bytes = need;
+    }
+    uint32_t mask = 0;
+    uint8_t *base = c.pack;
+    for (const auto &x : want) {
+        const uint32_t per = 4 / x.w;
+        const uint32_t first = (uint32_t)c.pack_tiles.size();
+        rot_tiles(x.w, x.feats, [&](fbh_ctx::Tile t) { c.pack_tiles.push_back(std::move(t)); });
+        const uint32_t nt = (uint32_t)c.pack_tiles.size() - first;
+        for (uint32_t b = 0; b * per < nt; b++) {
+            const uint32_t k = std::min(per, nt - b * per);
+            const uint32_t pitch = pitch_of(x.w, k);
+            for (uint32_t j = 0; j < k; j++) {
+                fbh_ctx::Tile &t = c.pack_tiles[first + b * per + j];
+                t.data = base + 16u * x.w * j;
+                t.stride = pitch;
+            }
+            base += c.n_rows * pitch;
+        }
+        mask |= 1u << x.w;
+    }
+    return mask;
+}
 
 // GradQuantizer::try_from_bounds (src/types.rs:288-303): the power-of-two
 // scale of one component from its bound, with the host's libm.
@@ -1403,7 +1534,7 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
                 tf.resize(d.feat_base);
                 return false;
             }
-            if (!t.global && hist_rot_layout(t.width, t.rec)) {
+            if (t.rot) {
                 // Interleaved layout: feature k at slot bin * 16 + k.
                 for (uint32_t k = 0; k < d.n_feat; k++) tf[d.feat_base + k].lds_off = k;
                 lds = HIST_ROT_SLOTS;
@@ -1412,17 +1543,25 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
             td.push_back(d);
             return true;
         };
+        const uint32_t packed = plan_pack(*c);
+        std::vector<const fbh_ctx::Tile *> built;  // resident tiles of this tree's histograms
+        for (const auto &t : c->tiles)
+            if (t.resident && !(t.rot && (packed >> t.width & 1u))) built.push_back(&t);
+        for (const auto &t : c->pack_tiles) built.push_back(&t);
         for (int glob = 0; glob < 2; glob++)
         for (uint32_t w : {1u, 2u}) {
-            for (uint32_t rec : {4u, 8u, 12u, 16u, 32u, 48u, 64u}) {
-                fbh_ctx::Group g{(int)w, (int)rec / 4, (uint32_t)td.size(), 0, 0, 0, glob == 1};
-                for (const auto &t : c->tiles) {
-                    if (t.width != w || t.rec != rec || (int)t.global != glob) continue;
-                    if (!t.resident) continue;
+            for (uint32_t rec : {4u, 8u, 12u, 16u, 32u, 48u, 64u})
+            for (int rot = 0; rot < 2; rot++) {
+                fbh_ctx::Group g{(int)w, (int)rec / 4, (uint32_t)td.size(), 0, 0, 0, glob == 1,
+                                 rot == 1};
+                for (const fbh_ctx::Tile *t : built) {
+                    if (t->width != w || t->rec != rec || (int)t->global != glob ||
+                        (int)t->rot != rot)
+                        continue;
                     uint32_t lds, active_bytes;
-                    if (!add_tile(t, lds, active_bytes)) continue;
+                    if (!add_tile(*t, lds, active_bytes)) continue;
                     g.n_tiles++;
-                    if (!t.global) g.lds_max = std::max(g.lds_max, lds);
+                    if (!t->global) g.lds_max = std::max(g.lds_max, lds);
                     g.bytes_per_row += active_bytes;
                 }
                 if (g.n_tiles) {
@@ -1479,17 +1618,53 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
         for (uint32_t j = 0; j < sf.size(); j++)
             if (!by_wave(j)) order.push_back(j);
         c->n_split_cat = (uint32_t)(order.size() - c->n_split_num);
-        std::vector<uint8_t> tables(c->off_order + 4 * order.size(), 0);
+        // Packed tiles' sources: 16 columns each (null for an empty cell).
+        std::vector<PackTileDev> pk;
+        for (const auto &t : c->pack_tiles) {
+            PackTileDev d{};
+            d.out = t.data;
+            d.stride = t.stride;
+            for (size_t k = 0; k < 16; k++) {
+                const bool live = k < t.feats.size();
+                d.col[k] = c->cols[t.feats[live ? k : 0]];
+                d.live |= live ? 1u << k : 0u;
+            }
+            pk.push_back(d);
+        }
+        std::vector<uint8_t> tables(pk.empty() ? c->off_order + 4 * order.size()
+                                               : c->off_pack + sizeof(PackTileDev) * pk.size(),
+                                    0);
         std::memcpy(tables.data(), td.data(), sizeof(TileDev) * td.size());
         std::memcpy(tables.data() + c->off_tilefeats, tf.data(), sizeof(TileFeatDev) * tf.size());
         std::memcpy(tables.data() + c->off_sfeats, sf.data(), sizeof(SplitFeatDev) * sf.size());
         std::memcpy(tables.data() + c->off_order, order.data(), 4 * order.size());
+        if (!pk.empty())
+            std::memcpy(tables.data() + c->off_pack, pk.data(), sizeof(PackTileDev) * pk.size());
         const bool upload = tables != c->tree_tables;
         if (upload) {
             int slot;
             std::memcpy(c->stage_acquire(slot), tables.data(), tables.size());
             c->stage_send(slot, c->d_tiles, tables.size());
             c->tree_tables = std::move(tables);
+        }
+        // The packed records, unless the pack already holds these features.
+        std::vector<uint32_t> sig;
+        for (const auto &t : c->pack_tiles) {
+            sig.push_back(0x80000000u | (t.width << 8) | (uint32_t)t.feats.size());
+            sig.insert(sig.end(), t.feats.begin(), t.feats.end());
+        }
+        if (!sig.empty() && sig != c->pack_sig) {
+            for (uint32_t w : {1u, 2u}) {
+                uint32_t first = 0, n = 0;
+                for (uint32_t i = 0; i < c->pack_tiles.size(); i++)
+                    if (c->pack_tiles[i].width == w) {
+                        if (n == 0) first = i;
+                        n++;
+                    }
+                check(launch_pack_tiles(c->d_pack + first, n, w, c->n_rows, c->stream),
+                      "tile packing");
+            }
+            c->pack_sig = std::move(sig);
         }
         // The delta is kept only for callers without a device objective.
         if (c->objective < 0 && !c->delta) c->delta = c->alloc<float>(c->n_rows, "prediction delta");
@@ -1632,7 +1807,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
                 check(launch_hist_global(L, g.width, ev_start, ev_stop, c->stream),
                       "histogram launch");
             else
-                check(launch_hist(L, g.width, g.rd, (int)c->hist_tpb, false,
+                check(launch_hist(L, g.width, g.rd, g.rot, (int)c->hist_tpb, false,
                                   (size_t)(g.lds_max + 64) * 16, ev_start, ev_stop, c->stream),
                       "histogram launch");
         }
@@ -1657,7 +1832,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
                 L.stream_data = c->win_rec[b];
                 L.row_lo = (uint32_t)lo;
                 L.row_hi = (uint32_t)hi;
-                check(launch_hist(L, (int)t.width, (int)(t.rec / 4), 256, true,
+                check(launch_hist(L, (int)t.width, (int)(t.rec / 4), t.rot, 256, true,
                                   (size_t)(sd.lds_slots + 64) * 16, nullptr, nullptr, c->stream),
                       "streamed histogram launch");
                 check(hipEventRecord(c->win_free[b], c->stream), "event");

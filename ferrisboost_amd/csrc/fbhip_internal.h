@@ -31,12 +31,12 @@ struct TileDev {
     uint32_t pad;
 };
 
-// LDS layout of 8-bit tiles with 16-byte records: slot bin * 16 + k for
-// feature k of the tile (bins below 256), whatever the tile's bin counts.
-constexpr uint32_t HIST_ROT_SLOTS = 16u * 256u;
-inline bool hist_rot_layout(uint32_t width, uint32_t rec_bytes) {
-    return width == 1 && rec_bytes == 16;
-}
+// Interleaved tiles: 16 cells a record (8-bit cells in 16 bytes, or 16-bit
+// cells of features with at most HIST_ROT_BINS bins in 32 bytes). Their LDS
+// layout is slot bin * 16 + k for feature k of the tile, whatever the tile's
+// bin counts. Every 16-byte 8-bit tile is interleaved.
+constexpr uint32_t HIST_ROT_BINS = 256u;
+constexpr uint32_t HIST_ROT_SLOTS = 16u * HIST_ROT_BINS;
 
 // Per-feature entry of a tile for one tree.
 struct TileFeatDev {
@@ -298,9 +298,11 @@ const char *last_error();
 // threads_per_block is 256, 512 or 1024.
 // stream: L describes one streamed tile window (see HistLaunch).
 // ev_start / ev_stop (nullable) take the launch's start / end time.
-hipError_t launch_hist(const HistLaunch &L, int width, int rec_dwords, int threads_per_block,
-                       bool stream, size_t lds_bytes, hipEvent_t ev_start, hipEvent_t ev_stop,
-                       hipStream_t s);
+// rot: the tile uses the interleaved layout (required for 8-bit 16-byte
+// records, allowed for 16-bit 32-byte ones).
+hipError_t launch_hist(const HistLaunch &L, int width, int rec_dwords, bool rot,
+                       int threads_per_block, bool stream, size_t lds_bytes, hipEvent_t ev_start,
+                       hipEvent_t ev_stop, hipStream_t s);
 hipError_t launch_hist_global(const HistLaunch &L, int width, hipEvent_t ev_start,
                               hipEvent_t ev_stop, hipStream_t s);
 hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slots, uint32_t n,
@@ -436,6 +438,20 @@ hipError_t launch_gpair_quantize(const float *g2n, uint64_t n, const ScalesDev *
                                  int64_t *out_sum, hipStream_t s);
 hipError_t launch_pack_feature(const uint8_t *col, uint64_t n_rows, uint32_t width, uint8_t *tile,
                                uint32_t stride, uint32_t byte_off, hipStream_t s);
+
+// One interleaved tile of a tree's own features, packed from the bin
+// columns: row r's record at out + r * stride, cell k copied from col[k]
+// when bit k of `live` is set, else zero (col[k] is then any valid column).
+struct PackTileDev {
+    uint8_t *out;
+    uint32_t stride;
+    uint32_t live;
+    const uint8_t *col[16];
+};
+// Records of n_tiles packed tiles of `width`-byte cells (device table, in
+// row-bundle order: tiles b * 4 / width ... of bundle b share its rows).
+hipError_t launch_pack_tiles(const PackTileDev *tiles, uint32_t n_tiles, uint32_t width,
+                             uint64_t n_rows, hipStream_t s);
 
 // Categories the device split scan sorts in LDS (weights + order, 32 KiB).
 constexpr uint32_t MAX_DEVICE_CATS = 4096;

@@ -96,10 +96,11 @@ __device__ __forceinline__ void global_add_u64(unsigned long long *p, unsigned l
 // sums (S = tile slots + 64). The last 64 slots of each plane are one dummy
 // slot per lane: a missing / unseen / unselected cell adds zero there instead
 // of branching, so the atomic stream has no divergent control flow.
-// 8-bit tiles with 16-byte records (hist_rot_layout) use the interleaved
-// layout instead: slot bin * 16 + k for feature k of the tile, the plane
-// HIST_ROT_SLOTS + 64 slots long, and lane l takes the record's features in
-// the order l, l + 1, ... (mod 16). The 64 lanes of one LDS atomic then hit
+// Interleaved tiles (ROT: 16 features of 8 bits in a 16-byte record, or of
+// 16 bits with at most 256 bins each in a 32-byte record) use the
+// interleaved layout instead: slot bin * 16 + k for feature k of the tile,
+// the plane HIST_ROT_SLOTS + 64 slots long, and lane l takes the record's
+// features in the order l, l + 1, ... (mod 16). The 64 lanes of one LDS atomic then hit
 // 16 features, four lanes each, and slot bin * 16 + k sits in bank pair k
 // whatever the bin: every bank pair takes exactly four lanes, where the
 // planar layout's random bins pile up to twice that on one pair. The dummy
@@ -108,13 +109,12 @@ __device__ __forceinline__ void global_add_u64(unsigned long long *p, unsigned l
 // STREAM: the tile is streamed; the launch covers the rows of one window
 // [L.row_lo, L.row_hi), whose records are at L.stream_data, and every node's
 // histogram accumulates over several launches (global atomics only).
-template <int W, int RD, int UNROLL, int TPB, bool STREAM>
+template <int W, int RD, int UNROLL, int TPB, bool STREAM, bool ROT>
 __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
     extern __shared__ unsigned long long lds[];
     constexpr int FPD = 4 / W;
     constexpr int NF = RD * FPD;
     constexpr uint32_t MASK = W == 1 ? 0xFFu : 0xFFFFu;
-    constexpr bool ROT = W == 1 && RD == 4;
     static_assert(!ROT || NF == 16, "interleaved layout: 16 features a record");
     static_assert(TPB % 64 == 0, "whole waves");
 
@@ -238,20 +238,28 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
                 for (int u = 0; u < UNROLL; u++)
                     g[u] = make_longlong2(quantize_pow2(f[u].x, lg), quantize_pow2(f[u].y, lh));
             }
-            if (ROT) {
-                // Rotate each record right by rot bytes: byte k becomes the byte
-                // of feature (k + rot) mod 16.
-                const uint32_t dsh = rot >> 2, bsh = rot & 3u;
+            if constexpr (ROT) {
+                // Rotate each record right by rot features: cell k becomes the
+                // cell of feature (k + rot) mod 16. Whole dwords first (a
+                // barrel shifter over the record's RD dwords), then the
+                // remaining cells within a dword (bytes).
+                const uint32_t dsh = rot / FPD, bsh = (rot % FPD) * W;
 #pragma unroll
                 for (int u = 0; u < UNROLL; u++) {
-                    uint32_t b[4], a[4];
+                    uint32_t a[RD];
 #pragma unroll
-                    for (int j = 0; j < 4; j++) b[j] = (dsh & 1u) ? rec[u][(j + 1) & 3] : rec[u][j];
+                    for (int j = 0; j < RD; j++) a[j] = rec[u][j];
 #pragma unroll
-                    for (int j = 0; j < 4; j++) a[j] = (dsh & 2u) ? b[(j + 2) & 3] : b[j];
+                    for (int st = 1; st < RD; st <<= 1) {
+                        uint32_t b[RD];
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        rec[u][j] = __builtin_amdgcn_alignbyte(a[(j + 1) & 3], a[j], bsh);
+                        for (int j = 0; j < RD; j++) b[j] = (dsh & (uint32_t)st) ? a[(j + st) % RD] : a[j];
+#pragma unroll
+                        for (int j = 0; j < RD; j++) a[j] = b[j];
+                    }
+#pragma unroll
+                    for (int j = 0; j < RD; j++)
+                        rec[u][j] = __builtin_amdgcn_alignbyte(a[(j + 1) % RD], a[j], bsh);
                 }
             }
 #pragma unroll
@@ -405,7 +413,7 @@ hipError_t launch_hist_global(const HistLaunch &L, int width, hipEvent_t ev_star
     return hipGetLastError();
 }
 
-template <int W, int RD, int TPB, bool STREAM>
+template <int W, int RD, int TPB, bool STREAM, bool ROT>
 static hipError_t launch_hist_t(const HistLaunch &L, size_t lds, hipEvent_t ev_start,
                                 hipEvent_t ev_stop, hipStream_t s) {
     const uint32_t blocks = L.linear ? L.n_chunks * L.n_tiles : L.chunk_groups * XCDS * L.n_tiles;
@@ -418,7 +426,7 @@ static hipError_t launch_hist_t(const HistLaunch &L, size_t lds, hipEvent_t ev_s
     if (e != hipSuccess) return e;
     if (dev < 64 && !(attr_done >> dev & 1)) {
         // The dynamic share is what the kernel's static LDS leaves of 160 KiB.
-        const void *fn = reinterpret_cast<const void *>(&hist_kernel<W, RD, 4, TPB, STREAM>);
+        const void *fn = reinterpret_cast<const void *>(&hist_kernel<W, RD, 4, TPB, STREAM, ROT>);
         hipFuncAttributes fa{};
         e = hipFuncGetAttributes(&fa, fn);
         if (e != hipSuccess) return e;
@@ -428,30 +436,32 @@ static hipError_t launch_hist_t(const HistLaunch &L, size_t lds, hipEvent_t ev_s
         attr_done |= 1ull << dev;
     }
     // Timing events ride on the dispatch itself (no separate marker packets).
-    hipExtLaunchKernelGGL((hist_kernel<W, RD, 4, TPB, STREAM>), dim3(blocks), dim3(TPB),
+    hipExtLaunchKernelGGL((hist_kernel<W, RD, 4, TPB, STREAM, ROT>), dim3(blocks), dim3(TPB),
                           (uint32_t)lds, s, ev_start, ev_stop, 0, L);
     return hipGetLastError();
 }
 
-template <int W, int RD>
+template <int W, int RD, bool ROT>
 static hipError_t launch_hist_wr(const HistLaunch &L, int tpb, bool stream, size_t lds,
                                  hipEvent_t e0, hipEvent_t e1, hipStream_t s) {
-    if (stream) return launch_hist_t<W, RD, 256, true>(L, lds, e0, e1, s);
-    if (tpb == 256) return launch_hist_t<W, RD, 256, false>(L, lds, e0, e1, s);
-    if (tpb == 512) return launch_hist_t<W, RD, 512, false>(L, lds, e0, e1, s);
-    if (tpb == 1024) return launch_hist_t<W, RD, 1024, false>(L, lds, e0, e1, s);
+    if (stream) return launch_hist_t<W, RD, 256, true, ROT>(L, lds, e0, e1, s);
+    if (tpb == 256) return launch_hist_t<W, RD, 256, false, ROT>(L, lds, e0, e1, s);
+    if (tpb == 512) return launch_hist_t<W, RD, 512, false, ROT>(L, lds, e0, e1, s);
+    if (tpb == 1024) return launch_hist_t<W, RD, 1024, false, ROT>(L, lds, e0, e1, s);
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_hist(const HistLaunch &L, int width, int rd, int tpb, bool stream, size_t lds,
-                       hipEvent_t ev_start, hipEvent_t ev_stop, hipStream_t s) {
-#define FBH_HIST_WR(WW, R) \
-    if (width == WW && rd == R) \
-        return launch_hist_wr<WW, R>(L, tpb, stream, lds, ev_start, ev_stop, s);
-    FBH_HIST_WR(1, 1) FBH_HIST_WR(1, 2) FBH_HIST_WR(1, 3) FBH_HIST_WR(1, 4)
-    FBH_HIST_WR(1, 8) FBH_HIST_WR(1, 12) FBH_HIST_WR(1, 16)
-    FBH_HIST_WR(2, 1) FBH_HIST_WR(2, 2) FBH_HIST_WR(2, 3) FBH_HIST_WR(2, 4)
-    FBH_HIST_WR(2, 8) FBH_HIST_WR(2, 12) FBH_HIST_WR(2, 16)
+hipError_t launch_hist(const HistLaunch &L, int width, int rd, bool rot, int tpb, bool stream,
+                       size_t lds, hipEvent_t ev_start, hipEvent_t ev_stop, hipStream_t s) {
+#define FBH_HIST_WR(WW, R, RT) \
+    if (width == WW && rd == R && rot == RT) \
+        return launch_hist_wr<WW, R, RT>(L, tpb, stream, lds, ev_start, ev_stop, s);
+    FBH_HIST_WR(1, 1, false) FBH_HIST_WR(1, 2, false) FBH_HIST_WR(1, 3, false)
+    FBH_HIST_WR(1, 4, true) FBH_HIST_WR(1, 8, false) FBH_HIST_WR(1, 12, false)
+    FBH_HIST_WR(1, 16, false)
+    FBH_HIST_WR(2, 1, false) FBH_HIST_WR(2, 2, false) FBH_HIST_WR(2, 3, false)
+    FBH_HIST_WR(2, 4, false) FBH_HIST_WR(2, 8, false) FBH_HIST_WR(2, 8, true)
+    FBH_HIST_WR(2, 12, false) FBH_HIST_WR(2, 16, false)
 #undef FBH_HIST_WR
     return hipErrorInvalidValue;
 }
@@ -2362,6 +2372,61 @@ hipError_t launch_pack_feature(const uint8_t *col, uint64_t n_rows, uint32_t wid
     if (blocks == 0) return hipSuccess;
     hipLaunchKernelGGL(pack_feature_kernel, dim3(blocks), dim3(256), 0, s, col, n_rows, width,
                        tile, stride, byte_off);
+    return hipGetLastError();
+}
+
+// Packed tiles: thread = row, blockIdx.y = one 64-byte row bundle (the
+// 64 / (16 W) consecutive tiles sharing it). The cells of one column are
+// read by consecutive lanes (coalesced); each thread writes its row's whole
+// bundle, so no partly written line leaves the cache.
+template <int W>
+__global__ __launch_bounds__(256) void pack_tiles_kernel(const PackTileDev *__restrict__ tiles,
+                                                         uint32_t n_tiles, uint64_t n_rows) {
+    constexpr int CPD = 4 / W;       // cells a dword
+    constexpr uint32_t PER = 4 / W;  // tiles a bundle
+    const uint64_t r = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (r >= n_rows) return;
+    const uint32_t t0 = blockIdx.y * PER;
+    const uint32_t nt = min(PER, n_tiles - t0);
+    // Every cell of the bundle loads first (an empty cell, or a tile past
+    // the last, from the first tile's first column), so all the loads issue
+    // back to back; empty cells are masked to zero.
+    uint32_t v[PER][16];
+#pragma unroll
+    for (uint32_t j = 0; j < PER; j++) {
+        const PackTileDev &T = tiles[t0 + (j < nt ? j : 0u)];
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            v[j][k] = W == 1 ? (uint32_t)T.col[k][r]
+                             : (uint32_t)reinterpret_cast<const uint16_t *>(T.col[k])[r];
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < PER; j++) {
+        if (j >= nt) break;
+        const PackTileDev &T = tiles[t0 + j];
+        uint32_t d[4 * W];
+#pragma unroll
+        for (int q = 0; q < 4 * W; q++) d[q] = 0u;
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            if (T.live >> k & 1u) d[k / CPD] |= v[j][k] << ((k % CPD) * 8 * W);
+        uint4 *dst = reinterpret_cast<uint4 *>(T.out + r * T.stride);
+#pragma unroll
+        for (int q = 0; q < W; q++)
+            dst[q] = make_uint4(d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]);
+    }
+}
+
+hipError_t launch_pack_tiles(const PackTileDev *tiles, uint32_t n_tiles, uint32_t width,
+                             uint64_t n_rows, hipStream_t s) {
+    if (n_tiles == 0 || n_rows == 0) return hipSuccess;
+    if (width != 1 && width != 2) return hipErrorInvalidValue;
+    const uint32_t per = 4 / width;
+    const dim3 grid((uint32_t)((n_rows + 255) / 256), (n_tiles + per - 1) / per);
+    if (width == 1)
+        hipLaunchKernelGGL(pack_tiles_kernel<1>, grid, dim3(256), 0, s, tiles, n_tiles, n_rows);
+    else
+        hipLaunchKernelGGL(pack_tiles_kernel<2>, grid, dim3(256), 0, s, tiles, n_tiles, n_rows);
     return hipGetLastError();
 }
 

@@ -72,6 +72,27 @@ def test_histogram_matches_oracle(N, oracle, width, n_feats):
         assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("n_feats", [9, 17, 40])
+def test_histogram_interleaved_16bit_matches_oracle(N, oracle, n_feats):
+    """16-bit features of at most 256 bins share interleaved tiles of 16
+    cells (32-byte records): bins 0..255, the all-ones missing code, bin
+    counts from 1 to 256."""
+    rng = np.random.default_rng(700 + n_feats)
+    n = 5001
+    n_bins = rng.integers(1, 257, size=n_feats)
+    n_bins[0] = 256
+    offsets = np.concatenate([[0], np.cumsum(n_bins)]).astype(np.uint32)
+    bins = np.empty((n_feats, n), np.uint16)
+    for f in range(n_feats):
+        b = rng.integers(0, n_bins[f], size=n)
+        b[rng.random(n) < 0.08] = 0xFFFF
+        bins[f] = b
+    gpair = rng.integers(-(1 << 41), 1 << 41, size=2 * n).astype(np.int64)
+    for rows in (None, np.sort(rng.choice(n, size=n // 5, replace=False)).astype(np.uint32)):
+        got = _device_hist(N, bins, offsets, gpair, rows)
+        assert np.array_equal(got, oracle.hist_build(bins, offsets, gpair, rows))
+
+
 def test_histogram_wide_features_use_global_path(N, oracle):
     # 16-bit features whose histogram exceeds an LDS tile, mixed with small ones.
     rng = np.random.default_rng(55)
@@ -427,12 +448,16 @@ def test_plumbing_config_matches_oracle(fb, oracle, max_bin):
     assert np.array_equal(pm.train_margins(X.shape[0]), om.train_margins(X.shape[0]))
 
 
-def test_wide_colsample_matches_oracle(fb, oracle):
+@pytest.mark.parametrize("max_bin, rate", [(256, 0.5), (64, 0.5), (256, 0.3), (64, 0.8)])
+def test_wide_colsample_matches_oracle(fb, oracle, max_bin, rate):
+    """Column sampling over interleaved tiles of 16-bit (max_bin 256) and
+    8-bit (64) cells: at rates 0.5 and 0.3 each tree's features are packed
+    into fresh tiles, at 0.8 the tiles are used as they are."""
     from ferrisboost_amd import datasets
 
     X, y, params, _ = datasets.wide_binary(6_000, n_features=300)
     rounds = 6
-    params = dict(params, max_depth=6)
+    params = dict(params, max_depth=6, max_bin=max_bin, colsample_bytree=rate)
     om = oracle.train(X, y, oracle.make_params(n_rounds=rounds, **params))
     pm = fb.train(params, X, y, num_boost_round=rounds)
     assert_same_models(om, pm)
