@@ -298,20 +298,31 @@ class Grower {
     bool device_trees_ = false;  // depthwise trees grow whole on the device
     uint32_t device_trees = 0;   // trees grown that way
 
+    // Lossguide whose leaf cap cannot bind (max_leaves 0, or at least
+    // 2^max_depth): best-first expansion then splits every node with a split
+    // above depth max_depth, the same set of splits as depthwise growth
+    // without a cap; only the node numbering (expansion order) differs.
+    bool lossguide_uncapped() const {
+        return p_.grow_policy == 1 && p_.max_depth <= 14 &&
+               (p_.max_leaves == 0 || p_.max_leaves >= (1u << p_.max_depth));
+    }
+
     bool device_growth() const {
-        return device_trees_ && p_.grow_policy == 0 && p_.max_depth >= 1 && p_.max_depth <= 14 &&
-               p_.max_leaves != 1;
+        return device_trees_ && (p_.grow_policy == 0 || lossguide_uncapped()) &&
+               p_.max_depth >= 1 && p_.max_depth <= 14 && p_.max_leaves != 1;
     }
 
     // Enqueues a depthwise tree on the device (root_sum NULL: the one the
     // gradient call left there); collect() waits for it and rebuilds it.
     void grow_async(const int64_t *root_sum) {
-        fbh_grow_params gp{p_.max_depth, p_.max_leaves, p_.learning_rate, 0};
+        fbh_grow_params gp{p_.max_depth, p_.grow_policy == 1 ? 0u : p_.max_leaves,
+                           p_.learning_rate, 0};
         call(fbh_grow_depthwise_async(ctx_, &gp, &sp_, root_sum));
     }
 
     // The oldest enqueued device tree, rebuilt with Tree::split_leaf in
-    // node-id order (the order the device numbered it).
+    // node-id order (the order the device numbered it), or, for lossguide,
+    // in best-first order.
     Tree collect() {
         const uint32_t cap_nodes = (2u << p_.max_depth) - 1, cap_leaves = 1u << p_.max_depth;
         std::vector<fbh_tree_node> tn(cap_nodes);
@@ -321,6 +332,8 @@ class Grower {
         call(fbh_grow_collect(ctx_, tn.data(), cap_nodes, &nn, cats.data(), (uint32_t)cats.size(),
                               leaves_values_.data(), cap_leaves, &nl));
         leaves_values_.resize(nl);
+        device_trees++;
+        if (p_.grow_policy == 1) return best_first(tn.data(), nn, cats.data());
         Tree t;
         t.push_leaf(tn[0].leaf_value, tn[0].sum_hess);
         for (uint32_t id = 0; id < nn; id++) {
@@ -336,7 +349,47 @@ class Grower {
             if (is_cat) t.set_categories(id, cats.data() + a.cat_offset, a.n_cat_words);
         }
         if (t.nodes.size() != nn) throw RuntimeError("device tree node count mismatch");
-        device_trees++;
+        return t;
+    }
+
+    // The lossguide tree of a device-grown one (lossguide_uncapped): the
+    // expansion loop of src/training/lossguide.rs:571-690 replayed over the
+    // device's splits, popping the highest gain first and, on equal gains,
+    // the lower node id (PendingSplit's order, lossguide.rs:46-52); each
+    // expansion numbers the two children next, as Tree::split_leaf does.
+    Tree best_first(const fbh_tree_node *tn, uint32_t nn, const uint64_t *cats) {
+        struct Open {
+            float gain;
+            uint32_t id;   // node id in the lossguide tree
+            uint32_t dev;  // node id in the device tree
+        };
+        auto less = [](const Open &a, const Open &b) {
+            if (a.gain != b.gain) return a.gain < b.gain;
+            return a.id > b.id;
+        };
+        std::priority_queue<Open, std::vector<Open>, decltype(less)> heap(less);
+        Tree t;
+        t.push_leaf(tn[0].leaf_value, tn[0].sum_hess);
+        if (!(tn[0].flags & 1u)) heap.push({tn[0].gain, 0, 0});
+        uint32_t expanded = 0;
+        while (!heap.empty()) {
+            const Open o = heap.top();
+            heap.pop();
+            const fbh_tree_node &a = tn[o.dev];
+            if ((uint32_t)a.left >= nn || (uint32_t)a.right >= nn)
+                throw RuntimeError("device tree child out of range");
+            const fbh_tree_node &l = tn[a.left], &r = tn[a.right];
+            const bool is_cat = (a.flags & 4u) != 0;
+            const auto lr = t.split_leaf(o.id, a.feat, is_cat ? 0.0f : cond_of(a.feat, a.bin),
+                                         (a.flags & 2u) != 0, a.gain, l.leaf_value, l.sum_hess,
+                                         r.leaf_value, r.sum_hess);
+            if (is_cat) t.set_categories(o.id, cats + a.cat_offset, a.n_cat_words);
+            if (!(l.flags & 1u)) heap.push({l.gain, lr.first, (uint32_t)a.left});
+            if (!(r.flags & 1u)) heap.push({r.gain, lr.second, (uint32_t)a.right});
+            expanded++;
+        }
+        if (t.nodes.size() != nn || 2 * expanded + 1 != nn)
+            throw RuntimeError("device tree node count mismatch");
         return t;
     }
 

@@ -242,7 +242,8 @@ def test_sampled_weighted_rounds_match_oracle(fb, oracle, objective, depth, host
 
 @pytest.mark.parametrize("case", ["budget", "monotone", "categorical", "sampled_deep", "stump",
                                   "squared", "walk_budget", "walk_categorical", "walk_squared",
-                                  "walk_u16"])
+                                  "walk_u16", "lg_plain", "lg_monotone", "lg_categorical",
+                                  "lg_sampled_deep", "lg_cap64"])
 def test_device_grown_trees_match_host_levels_and_oracle(fb, oracle, case):
     """Whole depthwise trees grown on the device (the max_leaves budget, node
     ids, weights, bounds, slots, partitions and leaves decided by kernels)
@@ -251,9 +252,14 @@ def test_device_grown_trees_match_host_levels_and_oracle(fb, oracle, case):
     two features a tile, three tiles in one 16-byte row bundle, so leaves and
     margins come from the row-order walk of the finished tree instead of a
     last-level partition; walk_u16 has 300 bins (16-bit cells, three
-    features a 16 KiB tile, two tiles in one 16-byte bundle)."""
+    features a 16 KiB tile, two tiles in one 16-byte bundle). The lg_ cases
+    grow lossguide trees whose leaf cap cannot bind (max_leaves 0, or 64 at
+    depth 6): the device grows every split and the host numbers the nodes
+    in best-first order, against the host's expansion-by-expansion growth."""
     walk = case.startswith("walk_")
     case = case[5:] if walk else case
+    lossguide = case.startswith("lg_")
+    case = case[3:] if lossguide else case
     wide_bins = case == "u16"
     rng = np.random.default_rng(sum(map(ord, case)))
     n, nf = 30_011, 6
@@ -284,6 +290,10 @@ def test_device_grown_trees_match_host_levels_and_oracle(fb, oracle, case):
         y = z.astype(np.float32)
     elif case == "u16":
         p.update(max_bin=300)
+    elif case == "cap64":
+        p.update(max_leaves=64)
+    if lossguide:
+        p.update(grow_policy="lossguide")
     om = oracle.train(x, y, oracle.make_params(**p), weights=w, monotone=mono, categorical=cat)
     pp = product_params(p)
     if walk:
