@@ -1517,6 +1517,7 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
             d.width = t.width;
             d.n_feat = (uint32_t)t.feats.size();
             d.feat_base = (uint32_t)tf.size();
+            d.rec_dwords = t.rec / 4;
             lds = 0;
             active_bytes = 0;
             for (uint32_t f : t.feats) {
@@ -1548,26 +1549,27 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
         for (const auto &t : c->tiles)
             if (t.resident && !(t.rot && (packed >> t.width & 1u))) built.push_back(&t);
         for (const auto &t : c->pack_tiles) built.push_back(&t);
+        // One launch per (global, width, interleaved): interleaved tiles all
+        // have 16-cell records; planar tiles of one width share a launch at
+        // the largest record size among them (a smaller record loads only
+        // its own dwords), so a few odd tiles never run as a launch of
+        // their own with too few workgroups to fill the device.
         for (int glob = 0; glob < 2; glob++)
-        for (uint32_t w : {1u, 2u}) {
-            for (uint32_t rec : {4u, 8u, 12u, 16u, 32u, 48u, 64u})
-            for (int rot = 0; rot < 2; rot++) {
-                fbh_ctx::Group g{(int)w, (int)rec / 4, (uint32_t)td.size(), 0, 0, 0, glob == 1,
-                                 rot == 1};
-                for (const fbh_ctx::Tile *t : built) {
-                    if (t->width != w || t->rec != rec || (int)t->global != glob ||
-                        (int)t->rot != rot)
-                        continue;
-                    uint32_t lds, active_bytes;
-                    if (!add_tile(*t, lds, active_bytes)) continue;
-                    g.n_tiles++;
-                    if (!t->global) g.lds_max = std::max(g.lds_max, lds);
-                    g.bytes_per_row += active_bytes;
-                }
-                if (g.n_tiles) {
-                    c->groups.push_back(g);
-                    c->has_global = c->has_global || g.global;
-                }
+        for (uint32_t w : {1u, 2u})
+        for (int rot = 0; rot < 2; rot++) {
+            fbh_ctx::Group g{(int)w, 0, (uint32_t)td.size(), 0, 0, 0, glob == 1, rot == 1};
+            for (const fbh_ctx::Tile *t : built) {
+                if (t->width != w || (int)t->global != glob || (int)t->rot != rot) continue;
+                uint32_t lds, active_bytes;
+                if (!add_tile(*t, lds, active_bytes)) continue;
+                g.n_tiles++;
+                g.rd = std::max(g.rd, (int)t->rec / 4);
+                if (!t->global) g.lds_max = std::max(g.lds_max, lds);
+                g.bytes_per_row += active_bytes;
+            }
+            if (g.n_tiles) {
+                c->groups.push_back(g);
+                c->has_global = c->has_global || g.global;
             }
         }
         // Streamed tiles: entries after the resident groups, launched one

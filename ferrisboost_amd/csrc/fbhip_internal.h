@@ -28,7 +28,7 @@ struct TileDev {
     uint32_t n_feat;     // features in the record
     uint32_t feat_base;  // first entry of this tile in the TileFeatDev table
     uint32_t lds_slots;  // LDS histogram slots of the tile's active features
-    uint32_t pad;
+    uint32_t rec_dwords; // record size in dwords (a launch's tiles may be smaller than its own)
 };
 
 // Interleaved tiles: 16 cells a record (8-bit cells in 16 bytes, or 16-bit
@@ -65,7 +65,7 @@ __host__ __device__ inline uint32_t reduce_groups(uint32_t n_chunks) {
 struct ScalesDev;
 
 struct HistLaunch {
-    const TileDev *tiles;      // tiles of this launch (same width / record size)
+    const TileDev *tiles;      // tiles of this launch (one width; records up to the launch's size)
     const TileFeatDev *feats;
     uint32_t n_tiles;
     const HistNodeDev *nodes;

@@ -222,10 +222,19 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
                 if (ok[u]) {
                     if constexpr (PF) f[u] = gf[row[u]];
                     else g[u] = gp[row[u]];
-                    if (STREAM)
-                        load_record<RD>(L.stream_data + (size_t)(row[u] - L.row_lo) * T.stride, rec[u]);
-                    else
-                        load_record<RD>(T.data + (size_t)row[u] * T.stride, rec[u]);
+                    const uint8_t *src = STREAM ? L.stream_data + (size_t)(row[u] - L.row_lo) * T.stride
+                                                : T.data + (size_t)row[u] * T.stride;
+                    if (ROT || T.rec_dwords == RD) {
+                        load_record<RD>(src, rec[u]);
+                    } else {
+                        // A smaller record than the launch's (planar tiles of
+                        // one width share a launch): its dwords only.
+#pragma unroll
+                        for (int d = 0; d < RD; d++)
+                            rec[u][d] = d < (int)T.rec_dwords
+                                            ? reinterpret_cast<const uint32_t *>(src)[d]
+                                            : 0u;
+                    }
                 } else {
                     f[u] = make_float2(0.0f, 0.0f);
                     g[u] = make_longlong2(0, 0);
