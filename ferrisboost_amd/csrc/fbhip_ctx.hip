@@ -83,6 +83,11 @@ constexpr uint32_t MAX_RECORD_BYTES = 64;
 constexpr uint64_t MAX_PARTIAL_BYTES = 256ull << 20;
 constexpr uint32_t MAX_NODES = 16384;      // nodes of one eval / partition call
 constexpr uint32_t DEFAULT_TILE_BYTES = 64 * 1024;
+// LDS of a planar tile (its bins plus the 1 KiB of lane dummies) when the
+// caller sets no tile size: three workgroups then share a CU's 160 KiB,
+// which the loads of tiles with few wide-bin features need (2M rows x 80
+// features of 1024 bins: 254 against 340 us a histogram).
+constexpr uint32_t PLANAR_TILE_BYTES = 53 * 1024;
 // Device-grown trees of at most this many features pick each node's best
 // split inside the level decision instead of a separate argmax launch.
 constexpr size_t FUSED_ARGMAX_FEATS = 64;
@@ -126,8 +131,9 @@ struct fbh_ctx {
     std::vector<uint8_t> width, cat;
     std::vector<uint32_t> n_bins;
     uint32_t tile_bytes = DEFAULT_TILE_BYTES;
+    uint32_t planar_tile_bytes = PLANAR_TILE_BYTES;
     uint32_t fixed_chunk_rows = 0;  // nonzero: rows per workgroup forced by the caller
-    uint32_t hist_tpb = 256;        // histogram threads per workgroup
+    uint32_t hist_tpb = 0;          // histogram threads per workgroup (0: per launch)
     uint32_t hist_waves = HIST_WAVES;
     uint32_t host_hist_waves = HOST_HIST_WAVES;
     uint32_t n_cus = 256;
@@ -459,6 +465,17 @@ struct fbh_ctx {
         check(hipEventRecord(stage_ev[slot], stream), "event");
     }
 
+    // Threads of a histogram workgroup of group g: 512 when the LDS lets
+    // three or more workgroups share a CU (planar tiles of few wide-bin
+    // features: the rows' loads then need more waves in flight; measured
+    // on 2M rows x 80 features of 1024 bins, 254 against 340 us), else 256
+    // (interleaved tiles: two workgroups a CU, LDS-atomic bound).
+    int hist_threads(const Group &g) const {
+        if (hist_tpb) return (int)hist_tpb;
+        const uint64_t lds = (uint64_t)(g.lds_max + 64) * 16;
+        return !g.rot && 3 * lds <= 160u * 1024u ? 512 : 256;
+    }
+
     // Rows per histogram workgroup for a launch accumulating acc_rows rows:
     // enough chunks for hist_waves full waves of workgroups over all tiles
     // (occupancy bounded by LDS and by 2048 threads per CU), so that each
@@ -472,7 +489,7 @@ struct fbh_ctx {
         }
         if (n_tiles == 0) return R;
         uint64_t per_cu = lds_max ? (160u * 1024u) / lds_max : 8;
-        per_cu = std::max<uint64_t>(1, std::min<uint64_t>(per_cu, 2048 / hist_tpb));
+        per_cu = std::max<uint64_t>(1, std::min<uint64_t>(per_cu, 2048 / (hist_tpb ? hist_tpb : 256)));
         const uint64_t wgs = (uint64_t)n_cus * per_cu * (host ? host_hist_waves : hist_waves);
         R.want_chunks = (uint32_t)std::max<uint64_t>(1, wgs / n_tiles);
         return R;
@@ -611,13 +628,17 @@ void plan_tiles(fbh_ctx &c) {
         for (uint32_t f = 0; f < c.n_features; f++) {
             if (c.width[f] != w || in_rot[f]) continue;
             // The tile's LDS also holds 64 per-lane dummy slots (1 KiB).
-            const uint64_t budget = c.tile_bytes - 1024u;
+            // Tiles share planar_tile_bytes; a feature wider than that but
+            // within tile_bytes takes a tile of its own.
+            const uint64_t budget = c.planar_tile_bytes - 1024u;
             const uint64_t fb = (uint64_t)c.n_bins[f] * 16u;
             if (fb > budget) {
-                // Too wide for LDS: a tile of its own, accumulated in global memory.
+                // A tile of its own: in LDS up to tile_bytes, else too wide
+                // for LDS and accumulated in global memory.
                 flush();
                 cur.feats.push_back(f);
-                cur.global = true;
+                cur.global = fb > (uint64_t)c.tile_bytes - 1024u;
+                lds = fb;
                 flush();
                 continue;
             }
@@ -908,8 +929,11 @@ fbh_config configure(fbh_ctx &c, uint64_t n_rows, const fbh_shape *shape, const 
     if (cfg) conf = *cfg;
     c.tile_bytes = (uint32_t)env_u64("FB_HIP_TILE_BYTES",
                                       conf.tile_bytes ? conf.tile_bytes : DEFAULT_TILE_BYTES);
+    c.planar_tile_bytes = conf.tile_bytes || std::getenv("FB_HIP_TILE_BYTES")
+                              ? c.tile_bytes
+                              : PLANAR_TILE_BYTES;
     c.fixed_chunk_rows = (uint32_t)env_u64("FB_HIP_CHUNK_ROWS", conf.rows_per_block);
-    c.hist_tpb = (uint32_t)env_u64("FB_HIP_HIST_TPB", 256);
+    c.hist_tpb = (uint32_t)env_u64("FB_HIP_HIST_TPB", 0);
     c.hist_waves = (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HIST_WAVES", HIST_WAVES));
     c.host_hist_waves =
         (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HOST_HIST_WAVES", HOST_HIST_WAVES));
@@ -917,7 +941,7 @@ fbh_config configure(fbh_ctx &c, uint64_t n_rows, const fbh_shape *shape, const 
         throw InputError("tile_bytes must be in 4096..=163840");
     if (c.fixed_chunk_rows && (c.fixed_chunk_rows < 256 || c.fixed_chunk_rows % 256))
         throw InputError("rows_per_block must be a positive multiple of 256");
-    if (c.hist_tpb != 256 && c.hist_tpb != 512 && c.hist_tpb != 1024)
+    if (c.hist_tpb != 0 && c.hist_tpb != 256 && c.hist_tpb != 512 && c.hist_tpb != 1024)
         throw InputError("histogram threads per workgroup must be 256, 512 or 1024");
     if (conf.stream_windows > 2)
         throw InputError("stream_windows (hist_streams) must be 1 or 2, got " +
@@ -1809,7 +1833,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
                 check(launch_hist_global(L, g.width, ev_start, ev_stop, c->stream),
                       "histogram launch");
             else
-                check(launch_hist(L, g.width, g.rd, g.rot, (int)c->hist_tpb, false,
+                check(launch_hist(L, g.width, g.rd, g.rot, c->hist_threads(g), false,
                                   (size_t)(g.lds_max + 64) * 16, ev_start, ev_stop, c->stream),
                       "histogram launch");
         }
