@@ -165,13 +165,15 @@ struct fbh_ctx {
     uint8_t *pack = nullptr;
     uint64_t pack_bytes = 0;
     std::vector<uint32_t> pack_sig;  // features (and width marks) the pack holds now
-    // Row bundles: consecutive tiles of one width and record size whose
-    // records fit in 64 bytes share one allocation, row r's records together
-    // at data + r * pitch. A histogram over a scattered node then fetches one
-    // cache line per row for the whole bundle instead of one per tile (the
-    // tiles of a bundle run side by side on one XCD). Used when every tile is
-    // resident. The gradient pairs stay a separate array: they are rewritten
-    // every round, and a partial-line write costs a full line.
+    // Row bundles: consecutive LDS tiles whose records fit in one 128-byte
+    // cache line share one allocation, row r's records together at data +
+    // r * pitch (a power of two, so no row straddles two lines). A histogram
+    // over a scattered node then fetches one line per row for the whole
+    // bundle instead of one per tile, and a line holds no other row when the
+    // pitch is 128 (the tiles of a bundle run side by side on one XCD). Used
+    // when every tile is resident. The gradient pairs stay a separate array:
+    // they are rewritten every round, and a partial-line write costs a full
+    // line.
     struct Bundle {
         uint32_t pitch;
         uint8_t *data;
@@ -651,10 +653,14 @@ void plan_tiles(fbh_ctx &c) {
     }
 }
 
-// Row-bundle layout (see fbh_ctx::bundles): runs of consecutive tiles of one
-// width and record size, up to 64 bytes of records each; a record's offset
-// is a multiple of its size, so every load keeps its alignment. A run of one
-// tile stays on its own. Returns whether any bundle was formed.
+// Row-bundle layout (see fbh_ctx::bundles): runs of consecutive LDS tiles
+// (any width and record size) up to BUNDLE_BYTES of records each; a
+// record's offset is a multiple of its load size (16 bytes for records of
+// 16 or more, 8 for 8, else 4), so every load keeps its alignment. A run of
+// one tile stays on its own. Returns whether any bundle was formed.
+constexpr uint32_t BUNDLE_BYTES = 128;
+uint32_t record_align(uint32_t rec) { return rec >= 16 ? 16u : (rec == 8 ? 8u : 4u); }
+
 bool layout_bundles(fbh_ctx &c) {
     c.bundles.clear();
     for (auto &t : c.tiles) {
@@ -663,13 +669,16 @@ bool layout_bundles(fbh_ctx &c) {
     }
     size_t i = 0;
     while (i < c.tiles.size()) {
-        const fbh_ctx::Tile &a = c.tiles[i];
+        std::vector<uint32_t> offs{0};
+        uint32_t used = c.tiles[i].rec;
         size_t j = i + 1;
-        uint32_t used = a.rec;
-        if (!a.global)
-            while (j < c.tiles.size() && !c.tiles[j].global && c.tiles[j].width == a.width &&
-                   c.tiles[j].rec == a.rec && used + a.rec <= 64) {
-                used += a.rec;
+        if (!c.tiles[i].global)
+            while (j < c.tiles.size() && !c.tiles[j].global) {
+                const uint32_t a = record_align(c.tiles[j].rec);
+                const uint32_t at = (used + a - 1) / a * a;
+                if (at + c.tiles[j].rec > BUNDLE_BYTES) break;
+                offs.push_back(at);
+                used = at + c.tiles[j].rec;
                 j++;
             }
         if (j - i >= 2) {
@@ -679,7 +688,7 @@ bool layout_bundles(fbh_ctx &c) {
             c.bundles.push_back({pitch, nullptr});
             for (size_t k = i; k < j; k++) {
                 c.tiles[k].bundle = b;
-                c.tiles[k].bundle_off = (uint32_t)(k - i) * a.rec;
+                c.tiles[k].bundle_off = offs[k - i];
             }
         }
         i = j;
@@ -1157,7 +1166,7 @@ namespace {
 // packed when every such tile is resident, the bin columns are on the
 // device, ceil(features / 16) tiles are at most 3/4 of the tiles holding
 // them, and the pack fits the budget's remaining room (it is outside the
-// memory plan). Packed tiles of one width share 64-byte row bundles.
+// memory plan). Packed tiles of one width share 128-byte row bundles.
 // Returns the widths packed: bit 1 for 8-bit, bit 2 for 16-bit tiles.
 uint32_t plan_pack(fbh_ctx &c) {
     c.pack_tiles.clear();
@@ -1188,7 +1197,7 @@ uint32_t plan_pack(fbh_ctx &c) {
         want.push_back({w, std::move(feats)});
     }
     if (want.empty()) return 0;
-    // Bundle b of width w: tiles [b * per, (b + 1) * per), per = 64 / (16 w).
+    // Bundle b of width w: tiles [b * per, (b + 1) * per), per = 128 / (16 w).
     auto pitch_of = [](uint32_t w, uint32_t k) {
         uint32_t p = 16;
         while (p < 16 * w * k) p *= 2;
@@ -1196,7 +1205,7 @@ uint32_t plan_pack(fbh_ctx &c) {
     };
     uint64_t need = 0;
     for (const auto &x : want) {
-        const uint32_t nt = (uint32_t)(x.feats.size() + 15) / 16, per = 4 / x.w;
+        const uint32_t nt = (uint32_t)(x.feats.size() + 15) / 16, per = 8 / x.w;
         for (uint32_t b = 0; b * per < nt; b++)
             need += c.n_rows * pitch_of(x.w, std::min(per, nt - b * per));
     }
@@ -1212,7 +1221,7 @@ uint32_t plan_pack(fbh_ctx &c) {
     uint32_t mask = 0;
     uint8_t *base = c.pack;
     for (const auto &x : want) {
-        const uint32_t per = 4 / x.w;
+        const uint32_t per = 8 / x.w;
         const uint32_t first = (uint32_t)c.pack_tiles.size();
         rot_tiles(x.w, x.feats, [&](fbh_ctx::Tile t) { c.pack_tiles.push_back(std::move(t)); });
         const uint32_t nt = (uint32_t)c.pack_tiles.size() - first;
@@ -2363,10 +2372,11 @@ namespace {
 constexpr uint32_t MAX_GROW_DEPTH = 14;
 
 
-// Every tile's records in one row bundle: a row's cells for every feature
-// are in one record, so leaves can be found by walking the tree in row order.
+// Every tile's records in one row bundle of at most 64 bytes (the leaf
+// walk holds a row in 16 registers): a row's cells for every feature are in
+// one record, so leaves can be found by walking the tree in row order.
 bool single_bundle(const fbh_ctx &c) {
-    if (c.bundles.size() != 1) return false;
+    if (c.bundles.size() != 1 || c.bundles[0].pitch > 64) return false;
     for (const auto &t : c.tiles)
         if (t.bundle != 0 || t.global) return false;
     return true;

@@ -449,7 +449,7 @@ struct PackTileDev {
     const uint8_t *col[16];
 };
 // Records of n_tiles packed tiles of `width`-byte cells (device table, in
-// row-bundle order: tiles b * 4 / width ... of bundle b share its rows).
+// row-bundle order: tiles b * 8 / width ... of bundle b share its rows).
 hipError_t launch_pack_tiles(const PackTileDev *tiles, uint32_t n_tiles, uint32_t width,
                              uint64_t n_rows, hipStream_t s);
 

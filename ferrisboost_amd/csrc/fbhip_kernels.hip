@@ -2384,45 +2384,50 @@ hipError_t launch_pack_feature(const uint8_t *col, uint64_t n_rows, uint32_t wid
     return hipGetLastError();
 }
 
-// Packed tiles: thread = row, blockIdx.y = one 64-byte row bundle (the
-// 64 / (16 W) consecutive tiles sharing it). The cells of one column are
+// Packed tiles: thread = row, blockIdx.y = one 128-byte row bundle (the
+// 128 / (16 W) consecutive tiles sharing it). The cells of one column are
 // read by consecutive lanes (coalesced); each thread writes its row's whole
 // bundle, so no partly written line leaves the cache.
 template <int W>
 __global__ __launch_bounds__(256) void pack_tiles_kernel(const PackTileDev *__restrict__ tiles,
                                                          uint32_t n_tiles, uint64_t n_rows) {
-    constexpr int CPD = 4 / W;       // cells a dword
-    constexpr uint32_t PER = 4 / W;  // tiles a bundle
+    constexpr int CPD = 4 / W;        // cells a dword
+    constexpr uint32_t PER = 8 / W;   // tiles a bundle
+    constexpr uint32_t HALF = PER / 2;  // tiles loaded together (64 bytes of records)
     const uint64_t r = (uint64_t)blockIdx.x * 256u + threadIdx.x;
     if (r >= n_rows) return;
     const uint32_t t0 = blockIdx.y * PER;
     const uint32_t nt = min(PER, n_tiles - t0);
-    // Every cell of the bundle loads first (an empty cell, or a tile past
-    // the last, from the first tile's first column), so all the loads issue
-    // back to back; empty cells are masked to zero.
-    uint32_t v[PER][16];
 #pragma unroll
-    for (uint32_t j = 0; j < PER; j++) {
-        const PackTileDev &T = tiles[t0 + (j < nt ? j : 0u)];
+    for (uint32_t h = 0; h < PER; h += HALF) {
+        if (h >= nt) break;
+        // Every cell of the half loads first (an empty cell, or a tile past
+        // the last, from the first tile's first column), so the loads issue
+        // back to back; empty cells are masked to zero.
+        uint32_t v[HALF][16];
 #pragma unroll
-        for (int k = 0; k < 16; k++)
-            v[j][k] = W == 1 ? (uint32_t)T.col[k][r]
-                             : (uint32_t)reinterpret_cast<const uint16_t *>(T.col[k])[r];
-    }
+        for (uint32_t j = 0; j < HALF; j++) {
+            const PackTileDev &T = tiles[t0 + (h + j < nt ? h + j : 0u)];
 #pragma unroll
-    for (uint32_t j = 0; j < PER; j++) {
-        if (j >= nt) break;
-        const PackTileDev &T = tiles[t0 + j];
-        uint32_t d[4 * W];
+            for (int k = 0; k < 16; k++)
+                v[j][k] = W == 1 ? (uint32_t)T.col[k][r]
+                                 : (uint32_t)reinterpret_cast<const uint16_t *>(T.col[k])[r];
+        }
 #pragma unroll
-        for (int q = 0; q < 4 * W; q++) d[q] = 0u;
+        for (uint32_t j = 0; j < HALF; j++) {
+            if (h + j >= nt) break;
+            const PackTileDev &T = tiles[t0 + h + j];
+            uint32_t d[4 * W];
 #pragma unroll
-        for (int k = 0; k < 16; k++)
-            if (T.live >> k & 1u) d[k / CPD] |= v[j][k] << ((k % CPD) * 8 * W);
-        uint4 *dst = reinterpret_cast<uint4 *>(T.out + r * T.stride);
+            for (int q = 0; q < 4 * W; q++) d[q] = 0u;
 #pragma unroll
-        for (int q = 0; q < W; q++)
-            dst[q] = make_uint4(d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]);
+            for (int k = 0; k < 16; k++)
+                if (T.live >> k & 1u) d[k / CPD] |= v[j][k] << ((k % CPD) * 8 * W);
+            uint4 *dst = reinterpret_cast<uint4 *>(T.out + r * T.stride);
+#pragma unroll
+            for (int q = 0; q < W; q++)
+                dst[q] = make_uint4(d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]);
+        }
     }
 }
 
@@ -2430,7 +2435,7 @@ hipError_t launch_pack_tiles(const PackTileDev *tiles, uint32_t n_tiles, uint32_
                              uint64_t n_rows, hipStream_t s) {
     if (n_tiles == 0 || n_rows == 0) return hipSuccess;
     if (width != 1 && width != 2) return hipErrorInvalidValue;
-    const uint32_t per = 4 / width;
+    const uint32_t per = 8 / width;
     const dim3 grid((uint32_t)((n_rows + 255) / 256), (n_tiles + per - 1) / per);
     if (width == 1)
         hipLaunchKernelGGL(pack_tiles_kernel<1>, grid, dim3(256), 0, s, tiles, n_tiles, n_rows);
