@@ -85,6 +85,18 @@ def cpu_threads() -> int:
     return max(1, min(16, os.cpu_count() or 1))
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the baseline's record."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def base_line(args, value, unit, ms_per_step, config, dtype="int64"):
     return {
         "metric": METRIC,
@@ -158,7 +170,7 @@ def train_workload(args, X, y, params, desc: str, traffic_tag: str):
 
         threads = cpu_threads()
         cols = max(1, -(-X.shape[1] // threads))
-        op = {k: v for k, v in params.items() if k not in ("device", "feature_types")}
+        op = {k: v for k, v in params.items() if k not in ("device", "feature_types", "gpu_math")}
         op.update(n_rounds=args.cpu_rounds, cols_per_block=cols, nthread=threads)
         cat = None
         if "feature_types" in params:
@@ -175,15 +187,22 @@ def train_workload(args, X, y, params, desc: str, traffic_tag: str):
             "kind": "port",
             "sample": f"first {args.cpu_rounds} rounds of the same {X.shape[0]}x{X.shape[1]} "
                       f"workload (histograms threaded over {blocks} column blocks; "
-                      "gradient, split and partition single-threaded)",
+                      "gradient, split and partition single-threaded, so this understates "
+                      "a fully threaded CPU engine)",
+            "cpu_model": cpu_model(),
+            "host_cpus": os.cpu_count(),
         }
-        parity = all(
-            np.array_equal(om.tree(t)[f], model.tree_nodes(t)[f])
-            for t in range(args.cpu_rounds) for f in om.tree(t).dtype.names if f != "pad")
+        # gpu_math="fast" is deterministic but not byte-equal to the CPU
+        # engine (the device exponential), so no tree comparison is made.
+        if params.get("gpu_math") != "fast":
+            parity = all(
+                np.array_equal(om.tree(t)[f], model.tree_nodes(t)[f])
+                for t in range(args.cpu_rounds) for f in om.tree(t).dtype.names if f != "pad")
 
     config = {"workload": desc, "rows": int(X.shape[0]), "features": int(X.shape[1])}
     config.update({k: params[k] for k in ("max_bin", "max_depth", "max_leaves", "grow_policy",
-                                          "colsample_bytree", "objective") if k in params})
+                                          "colsample_bytree", "objective", "gpu_math")
+                   if k in params})
     out = base_line(args, round(args.steps / t_wall, 3), "rounds/s",
                     round(1e3 * t_wall / args.steps, 3), config)
     out.update({
@@ -314,6 +333,9 @@ def main() -> int:
                     choices=["narrow", "wide", "widebin", "streaming", "shap"])
     ap.add_argument("--rows", type=int, default=0, help="rows (0: the workload's own size)")
     ap.add_argument("--max-bin", type=int, default=255, help="narrow workload: 255 (u8) or 256 (u16)")
+    ap.add_argument("--gpu-math", default="exact", choices=["exact", "fast"],
+                    help="narrow workload: exact (host-libm gradients, byte-identical trees) or "
+                         "fast (hardware exp on the device)")
     ap.add_argument("--cpu-rounds", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -342,10 +364,11 @@ def main() -> int:
         X, y, params, _ = datasets.narrow_binary(args.rows or 10_500_000, max_bin=args.max_bin)
         log(f"data {X.shape} generated in {time.time() - t0:.1f}s")
         u = "u8" if args.max_bin <= 255 else "u16"
+        params = dict(params, gpu_math=args.gpu_math)
         out = train_workload(
             args, X, y, params,
             f"narrow {X.shape[0]}x{X.shape[1]} HIGGS-like binary, max_bin={args.max_bin} "
-            f"({u} bins), depth 8, eta 0.1, gpu_math=exact, depthwise", f"narrow_{u}")
+            f"({u} bins), depth 8, eta 0.1, gpu_math={args.gpu_math}, depthwise", f"narrow_{u}")
     elif args.workload == "wide":
         X, y, params, _ = datasets.wide_binary(args.rows or 400_000, n_features=2000)
         log(f"data {X.shape} generated in {time.time() - t0:.1f}s")
