@@ -5,11 +5,15 @@
  * build_tree (src/training/mod.rs:3357-4565) and lossguide::grow
  * (src/training/lossguide.rs:494-700). It prepares the data exactly like
  * DenseSource (sketch -> cuts -> u8/u16 column blocks,
- * src/source/dense.rs:99-290), computes exact-mode gradients on the host
- * (gpu_math="exact", src/training/mod.rs:2033-2087) and runs every
- * histogram, split scan, partition and leaf scatter through the fbh_*
- * backend (fbhip.h). It never falls back to a CPU histogram or split path:
- * without a usable device, fbt_train fails with FBH_RUNTIME_ERROR.
+ * src/source/dense.rs:99-290) and runs gradients, histograms, split scans,
+ * partitions, leaves and margins through the fbh_* backend (fbhip.h): the
+ * exact-mode gradient (gpu_math="exact", src/training/mod.rs:2033-2087) on
+ * the device with the host libm's sigmoid restated, or through the host
+ * libm when the device's does not match it or the caller asks; the fast
+ * mode (gpu_math="fast") with the hardware exponential. Depthwise trees,
+ * and lossguide trees whose leaf cap cannot bind, grow whole on the device.
+ * It never falls back to a CPU histogram or split path: without a usable
+ * device, fbt_train fails with FBH_RUNTIME_ERROR.
  *
  * Status codes as fbhip.h (0 ok, 1 input error, 2 runtime error).
  */
