@@ -15,6 +15,7 @@ device syncs. Other workloads (--workload):
             stream from pinned host memory
   shap      GPU TreeSHAP of 1M rows x 200 features against a 100-tree,
             depth-8 ensemble (trained first, untimed); one step = one pass
+  predict   GPU margins of the same rows and ensemble; one step = one pass
 
 Prints one JSON line:
   value         boosting rounds per second (shap: rows per second)
@@ -267,9 +268,10 @@ def streaming_workload(args):
     return out
 
 
-def shap_workload(args):
+def explained_model(args):
+    """The 100-tree depth-8 ensemble of the streaming data's first rows (1M x
+    200 by default), trained untimed, and those rows."""
     import ferrisboost_amd as fb
-    from ferrisboost_amd import _native as N
     from ferrisboost_amd import datasets
 
     n_rows = args.rows or 1_000_000
@@ -277,6 +279,63 @@ def shap_workload(args):
     t0 = time.time()
     model = fb.train(dict(params, device="cuda:0"), X, y, num_boost_round=100)
     log(f"trained 100 trees on {X.shape} in {time.time() - t0:.1f}s")
+    return model, X
+
+
+def predict_workload(args):
+    from ferrisboost_amd import _native as N
+
+    model, X = explained_model(args)
+    n_rows = X.shape[0]
+    L = N.train_lib()
+    model.predict(X[:4096], output_margin=True)  # load the kernels
+    for _ in range(args.warmup):
+        model.predict(X, output_margin=True)
+    kernel_ms = 0.0
+    t0 = time.time()
+    for _ in range(args.steps):
+        margin = model.predict(X, output_margin=True)
+        kernel_ms += L.fbt_last_shap_ms()
+    wall = time.time() - t0
+    rows_per_s = args.steps * n_rows / (kernel_ms * 1e-3)
+    # bytes the kernel must move: the row in, its margin out
+    per_row = 4 * X.shape[1] + 4
+    gbps = args.steps * n_rows * per_row / (kernel_ms * 1e-3) / 1e9
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+
+        k = 20_000
+        om = O.model_from_nodes(model.trees(), model.cat_words(), model.objective,
+                                model.base_score)
+        t0 = time.time()
+        ref = om.predict_margin(X[:k])
+        cpu_s = time.time() - t0
+        parity = bool(np.array_equal(ref.view(np.uint32), margin[:k].view(np.uint32)))
+        cpu = {"value": round(k / cpu_s, 1), "unit": "rows/s", "cores": 1, "kind": "port",
+               "sample": f"margins of the first {k} rows (same trees), one thread",
+               "cpu_model": cpu_model(), "host_cpus": os.cpu_count()}
+    config = {"workload": f"GPU prediction (margins), {n_rows} rows x {X.shape[1]} features, "
+                          "100 trees depth 8", "rows": n_rows, "features": int(X.shape[1]),
+              "trees": 100, "max_depth": 8}
+    out = base_line(args, round(rows_per_s, 1), "rows/s", round(kernel_ms / args.steps, 3),
+                    config, dtype="f32")
+    out.update({
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+        "pcie_inclusive_rows_per_s": round(args.steps * n_rows / wall, 1),
+        "cpu_baseline": cpu,
+        "margins_bit_identical_to_cpu": parity,
+    })
+    return out
+
+
+def shap_workload(args):
+    from ferrisboost_amd import _native as N
+
+    model, X = explained_model(args)
+    n_rows = X.shape[0]
     L = N.train_lib()
     model.predict(X[:4096], pred_contribs=True)  # load the kernels
     for _ in range(args.warmup):
@@ -330,7 +389,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="narrow",
-                    choices=["narrow", "wide", "widebin", "streaming", "shap"])
+                    choices=["narrow", "wide", "widebin", "streaming", "shap", "predict"])
     ap.add_argument("--rows", type=int, default=0, help="rows (0: the workload's own size)")
     ap.add_argument("--max-bin", type=int, default=255, help="narrow workload: 255 (u8) or 256 (u16)")
     ap.add_argument("--gpu-math", default="exact", choices=["exact", "fast"],
@@ -358,6 +417,8 @@ def main() -> int:
     t0 = time.time()
     if args.workload == "shap":
         out = shap_workload(args)
+    elif args.workload == "predict":
+        out = predict_workload(args)
     elif args.workload == "streaming":
         out = streaming_workload(args)
     elif args.workload == "narrow":

@@ -2384,50 +2384,70 @@ hipError_t launch_pack_feature(const uint8_t *col, uint64_t n_rows, uint32_t wid
     return hipGetLastError();
 }
 
-// Packed tiles: thread = row, blockIdx.y = one 128-byte row bundle (the
-// 128 / (16 W) consecutive tiles sharing it). The cells of one column are
-// read by consecutive lanes (coalesced); each thread writes its row's whole
-// bundle, so no partly written line leaves the cache.
+// Packed tiles: a workgroup packs 256 consecutive rows of one row bundle
+// (blockIdx.y; the 128 / (16 W) consecutive tiles sharing it, every tile's
+// stride the bundle's pitch). Phase 1 reads each of the bundle's columns for
+// the 256 rows (consecutive lanes, consecutive cells) into the rows'
+// records in LDS; phase 2 writes the 256 records, consecutive lanes writing
+// consecutive 16-byte pieces of the bundle's contiguous rows. Empty cells
+// are zero.
+constexpr uint32_t PACK_ROWS = 256;
+constexpr uint32_t PACK_LDS_STRIDE = 33;  // dwords a row in LDS (32 + 1: no bank conflicts)
+
 template <int W>
 __global__ __launch_bounds__(256) void pack_tiles_kernel(const PackTileDev *__restrict__ tiles,
                                                          uint32_t n_tiles, uint64_t n_rows) {
-    constexpr int CPD = 4 / W;        // cells a dword
-    constexpr uint32_t PER = 8 / W;   // tiles a bundle
-    constexpr uint32_t HALF = PER / 2;  // tiles loaded together (64 bytes of records)
-    const uint64_t r = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-    if (r >= n_rows) return;
+    constexpr uint32_t PER = 8 / W;       // tiles a bundle
+    constexpr uint32_t CELLS = 16 * PER;  // cells a bundle row (128 bytes)
+    constexpr uint32_t CPD = 4 / W;       // cells a dword
+    __shared__ uint32_t rec[PACK_ROWS * PACK_LDS_STRIDE];
     const uint32_t t0 = blockIdx.y * PER;
     const uint32_t nt = min(PER, n_tiles - t0);
+    const uint64_t r0 = (uint64_t)blockIdx.x * PACK_ROWS;
+    const uint32_t tid = threadIdx.x;
+    const bool in = r0 + tid < n_rows;
+    const uint64_t r = in ? r0 + tid : r0;  // a valid row for every lane's loads
+    // Phase 1: thread tid builds row r0 + tid's record, 64 cells at a time:
+    // every cell loads first (an empty cell, or a tile past the last, from a
+    // valid column), so the loads issue back to back; then the dwords are
+    // assembled, empty cells and rows past the end masked to zero.
+    constexpr uint32_t GT = 64 / 16;  // tiles loaded together
 #pragma unroll
-    for (uint32_t h = 0; h < PER; h += HALF) {
-        if (h >= nt) break;
-        // Every cell of the half loads first (an empty cell, or a tile past
-        // the last, from the first tile's first column), so the loads issue
-        // back to back; empty cells are masked to zero.
-        uint32_t v[HALF][16];
+    for (uint32_t g = 0; g < PER; g += GT) {
+        uint32_t v[GT][16];
 #pragma unroll
-        for (uint32_t j = 0; j < HALF; j++) {
-            const PackTileDev &T = tiles[t0 + (h + j < nt ? h + j : 0u)];
+        for (uint32_t j = 0; j < GT; j++) {
+            const PackTileDev &T = tiles[t0 + (g + j < nt ? g + j : 0u)];
 #pragma unroll
             for (int k = 0; k < 16; k++)
                 v[j][k] = W == 1 ? (uint32_t)T.col[k][r]
                                  : (uint32_t)reinterpret_cast<const uint16_t *>(T.col[k])[r];
         }
 #pragma unroll
-        for (uint32_t j = 0; j < HALF; j++) {
-            if (h + j >= nt) break;
-            const PackTileDev &T = tiles[t0 + h + j];
-            uint32_t d[4 * W];
+        for (uint32_t j = 0; j < GT; j++) {
+            const uint32_t live = g + j < nt && in ? tiles[t0 + g + j].live : 0u;
 #pragma unroll
-            for (int q = 0; q < 4 * W; q++) d[q] = 0u;
+            for (uint32_t q = 0; q < 16 / CPD; q++) {
+                uint32_t d = 0;
 #pragma unroll
-            for (int k = 0; k < 16; k++)
-                if (T.live >> k & 1u) d[k / CPD] |= v[j][k] << ((k % CPD) * 8 * W);
-            uint4 *dst = reinterpret_cast<uint4 *>(T.out + r * T.stride);
-#pragma unroll
-            for (int q = 0; q < W; q++)
-                dst[q] = make_uint4(d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]);
+                for (uint32_t c = 0; c < CPD; c++) {
+                    const uint32_t k = q * CPD + c;
+                    if (live >> k & 1u) d |= v[j][k] << (c * 8 * W);
+                }
+                rec[tid * PACK_LDS_STRIDE + (g + j) * (16 / CPD) + q] = d;
+            }
         }
+    }
+    __syncthreads();
+    // Phase 2: the bundle's rows r0.. are contiguous at pitch bytes each.
+    const uint32_t pitch = tiles[t0].stride;  // 16 W nt rounded up to a power of two
+    const uint32_t quads = pitch / 16;        // 16-byte pieces a row
+    const uint64_t rows = min<uint64_t>(PACK_ROWS, n_rows - r0);
+    uint8_t *base = tiles[t0].out + r0 * pitch;
+    for (uint32_t i = tid; i < rows * quads; i += 256) {
+        const uint32_t row = i / quads, qd = i % quads;
+        const uint32_t *src = rec + row * PACK_LDS_STRIDE + 4 * qd;
+        reinterpret_cast<uint4 *>(base)[i] = make_uint4(src[0], src[1], src[2], src[3]);
     }
 }
 
@@ -2436,7 +2456,7 @@ hipError_t launch_pack_tiles(const PackTileDev *tiles, uint32_t n_tiles, uint32_
     if (n_tiles == 0 || n_rows == 0) return hipSuccess;
     if (width != 1 && width != 2) return hipErrorInvalidValue;
     const uint32_t per = 8 / width;
-    const dim3 grid((uint32_t)((n_rows + 255) / 256), (n_tiles + per - 1) / per);
+    const dim3 grid((uint32_t)((n_rows + PACK_ROWS - 1) / PACK_ROWS), (n_tiles + per - 1) / per);
     if (width == 1)
         hipLaunchKernelGGL(pack_tiles_kernel<1>, grid, dim3(256), 0, s, tiles, n_tiles, n_rows);
     else

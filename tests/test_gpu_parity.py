@@ -458,14 +458,17 @@ def test_plumbing_config_matches_oracle(fb, oracle, max_bin):
     assert np.array_equal(pm.train_margins(X.shape[0]), om.train_margins(X.shape[0]))
 
 
-@pytest.mark.parametrize("max_bin, rate", [(256, 0.5), (64, 0.5), (256, 0.3), (64, 0.8)])
-def test_wide_colsample_matches_oracle(fb, oracle, max_bin, rate):
+@pytest.mark.parametrize("max_bin, rate, n_rows", [(256, 0.5, 6_000), (64, 0.5, 6_000),
+                                                    (256, 0.3, 6_001), (64, 0.3, 6_002),
+                                                    (64, 0.8, 6_000)])
+def test_wide_colsample_matches_oracle(fb, oracle, max_bin, rate, n_rows):
     """Column sampling over interleaved tiles of 16-bit (max_bin 256) and
     8-bit (64) cells: at rates 0.5 and 0.3 each tree's features are packed
-    into fresh tiles, at 0.8 the tiles are used as they are."""
+    into fresh tiles (four rows a thread when the row count is a multiple of
+    8, else one), at 0.8 the tiles are used as they are."""
     from ferrisboost_amd import datasets
 
-    X, y, params, _ = datasets.wide_binary(6_000, n_features=300)
+    X, y, params, _ = datasets.wide_binary(n_rows, n_features=300)
     rounds = 6
     params = dict(params, max_depth=6, max_bin=max_bin, colsample_bytree=rate)
     om = oracle.train(X, y, oracle.make_params(n_rounds=rounds, **params))
