@@ -76,6 +76,7 @@ _DEFAULTS: dict[str, Any] = {
     "hip_host_sigmoid": False,
     "hip_host_levels": False,
     "hip_sync_round": 0,
+    "hip_host_binning": False,
 }
 
 _ALIASES = {
@@ -220,6 +221,7 @@ def _params_struct(p: dict[str, Any], n_features: int) -> N.TrainParams:
     s.sync_round = int(p["hip_sync_round"])
     s.hist_streams = int(p["hist_streams"] or 0)
     s.resident_limit = 0 if p["resident_blocks"] is None else int(p["resident_blocks"]) + 1
+    s.host_binning = 1 if p["hip_host_binning"] else 0
     return s
 
 
@@ -582,5 +584,5 @@ def train(params: Mapping[str, Any], X, label, weight=None, num_boost_round: int
     m = Model(h, X.shape[1], p["objective"], s.device)
     st = N.Stats()
     N.check_train(L.fbt_last_stats(C.byref(st)))
-    m.stats = {k: getattr(st, k) for k, _ in N.Stats._fields_ if k != "reserved"}
+    m.stats = {k: getattr(st, k) for k, _ in N.Stats._fields_}
     return m

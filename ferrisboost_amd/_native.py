@@ -158,6 +158,7 @@ class TrainParams(C.Structure):
         ("sync_round", C.c_uint32),
         ("hist_streams", C.c_uint32),
         ("resident_limit", C.c_uint32),
+        ("host_binning", C.c_uint32),
     ]
 
 
@@ -178,7 +179,9 @@ class Stats(C.Structure):
         ("planned_bytes", C.c_uint64),
         ("budget_bytes", C.c_uint64),
         ("device_trees", C.c_uint32),
-        ("reserved", C.c_uint32),
+        ("device_binning", C.c_uint32),
+        ("sketch_seconds", C.c_double),
+        ("bin_seconds", C.c_double),
     ]
 
 
@@ -203,7 +206,8 @@ NODE_DTYPE = np.dtype(
 HIP_SYMBOLS = [
     "fbh_last_error", "fbh_device_available", "fbh_ctx_create", "fbh_ctx_destroy",
     "fbh_plan_memory", "fbh_ctx_plan", "fbh_ctx_streamed_bytes",
-    "fbh_ctx_device_bytes", "fbh_upload_block", "fbh_upload_quantize_gpair",
+    "fbh_ctx_device_bytes", "fbh_upload_block", "fbh_set_cuts", "fbh_rows_staging_bytes",
+    "fbh_upload_rows", "fbh_finish_rows", "fbh_upload_quantize_gpair",
     "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_gradient_exchange",
     "fbh_download_margin", "fbh_set_gpu_math", "fbh_gradient_pairs", "fbh_sigmoid_host", "fbh_sigmoid_device", "fbh_sigmoid_checksum",
     "fbh_begin_tree", "fbh_eval_nodes", "fbh_download_histogram",
@@ -264,6 +268,11 @@ def hip() -> C.CDLL:
         L.fbh_ctx_device_bytes.argtypes = [P]
         L.fbh_ctx_device_bytes.restype = C.c_uint64
         L.fbh_upload_block.argtypes = [P, P, C.c_uint32, C.c_uint32, P]
+        L.fbh_set_cuts.argtypes = [P, P, P, P]
+        L.fbh_rows_staging_bytes.argtypes = [P]
+        L.fbh_rows_staging_bytes.restype = C.c_uint64
+        L.fbh_upload_rows.argtypes = [P, P, C.c_uint64, C.c_uint64]
+        L.fbh_finish_rows.argtypes = [P]
         L.fbh_upload_quantize_gpair.argtypes = [P, P, C.c_uint64, C.c_uint64, C.c_uint64, P, P]
         L.fbh_upload_gpair_fixed.argtypes = [P, P, P]
         L.fbh_set_objective.argtypes = [P, C.c_uint32, P, P, C.c_float]

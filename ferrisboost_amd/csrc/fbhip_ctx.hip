@@ -168,6 +168,17 @@ struct fbh_ctx {
     uint8_t *pack = nullptr;
     uint64_t pack_bytes = 0;
     std::vector<uint32_t> pack_sig;  // features (and width marks) the pack holds now
+    // Device binning (fbh_set_cuts / fbh_upload_rows): the cuts and feature
+    // table, and the row staging, all outside the memory plan.
+    BinFeatDev *d_binfeats = nullptr;
+    float *d_cut_values = nullptr;
+    float *rows_stage = nullptr;
+    bool cuts_set = false;
+    // Rows the staging holds: 64 MiB of rows, at least 64 rows.
+    uint64_t stage_rows() const {
+        const uint64_t per = 4ull * std::max<uint32_t>(n_features, 1);
+        return std::max<uint64_t>(64, std::min<uint64_t>(n_rows, (64ull << 20) / per));
+    }
     // Row bundles: consecutive LDS tiles whose records fit in one 128-byte
     // cache line share one allocation, row r's records together at data +
     // r * pitch (a power of two, so no row straddles two lines). A histogram
@@ -1165,6 +1176,121 @@ int fbh_upload_block(fbh_ctx *c, const uint32_t *feat_ids, uint32_t n_feats, uin
             c->uploaded[f] = 1;
         }
         c->pack_sig.clear();  // packed records of these features are stale
+        c->sync();
+    });
+}
+
+int fbh_set_cuts(fbh_ctx *c, const float *cut_values, const uint32_t *cut_offsets,
+                 const uint8_t *categorical) {
+    return guard([&] {
+        if (!c || !cut_offsets || (!cut_values && cut_offsets[c->n_features] != 0))
+            throw InputError("null argument");
+        if (!c->plan.columns_resident)
+            throw InputError("device binning needs the bin columns resident; the plan streams "
+                             "them (bin on the host and upload column blocks)");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        const uint32_t nf = c->n_features;
+        if (cut_offsets[0] != 0) throw InputError("cut offsets must start at 0");
+        for (uint32_t f = 0; f < nf; f++) {
+            if (cut_offsets[f + 1] < cut_offsets[f])
+                throw InputError("cut offsets must not decrease");
+            const uint32_t nc = cut_offsets[f + 1] - cut_offsets[f];
+            if ((uint64_t)nc + 1 != c->n_bins[f])
+                throw InputError("feature " + std::to_string(f) + " has " + std::to_string(nc) +
+                                 " cuts for " + std::to_string(c->n_bins[f]) + " bins");
+            if ((categorical && categorical[f]) != (c->cat[f] != 0))
+                throw InputError("feature " + std::to_string(f) +
+                                 " is categorical in the cuts and not in the shape, or back");
+            for (uint32_t i = cut_offsets[f] + 1; i < cut_offsets[f + 1]; i++)
+                if (!(cut_values[i] > cut_values[i - 1]))
+                    throw InputError("feature " + std::to_string(f) +
+                                     " cuts must be strictly increasing");
+        }
+        const uint64_t n_vals = cut_offsets[nf];
+        const uint64_t bytes = 4 * std::max<uint64_t>(n_vals, 1) + sizeof(BinFeatDev) * nf + 512;
+        if (c->device_bytes + bytes > c->plan.budget)
+            throw InputError("the device cuts do not fit the budget's remaining room");
+        if (!c->d_cut_values) {
+            c->d_cut_values = c->alloc<float>(std::max<uint64_t>(n_vals, 1), "device cuts");
+            c->d_binfeats = c->alloc<BinFeatDev>(nf, "device binning table");
+        } else {
+            throw InputError("the cuts of this context are already set");
+        }
+        std::vector<BinFeatDev> tab(nf);
+        for (uint32_t f = 0; f < nf; f++) {
+            tab[f].cuts = c->d_cut_values + cut_offsets[f];
+            tab[f].col = c->cols[f];
+            tab[f].n_cuts = cut_offsets[f + 1] - cut_offsets[f];
+            tab[f].n_bins = c->n_bins[f];
+            tab[f].width = c->width[f];
+            tab[f].categorical = c->cat[f];
+        }
+        if (n_vals)
+            check(hipMemcpyAsync(c->d_cut_values, cut_values, 4 * n_vals, hipMemcpyHostToDevice,
+                                 c->stream),
+                  "cuts upload");
+        check(hipMemcpyAsync(c->d_binfeats, tab.data(), sizeof(BinFeatDev) * nf,
+                             hipMemcpyHostToDevice, c->stream),
+              "binning table upload");
+        c->sync();
+        c->cuts_set = true;
+    });
+}
+
+uint64_t fbh_rows_staging_bytes(const fbh_ctx *c) {
+    return c ? c->stage_rows() * 4ull * c->n_features : 0;
+}
+
+int fbh_upload_rows(fbh_ctx *c, const float *x, uint64_t row0, uint64_t n_rows) {
+    return guard([&] {
+        if (!c || (!x && n_rows)) throw InputError("null argument");
+        if (!c->cuts_set) throw InputError("fbh_set_cuts must come before fbh_upload_rows");
+        if (row0 > c->n_rows || n_rows > c->n_rows - row0)
+            throw InputError("rows out of range");
+        if (n_rows == 0) return;
+        check(hipSetDevice(c->device), "hipSetDevice");
+        const uint64_t cap = c->stage_rows(), nf = c->n_features;
+        if (!c->rows_stage) {
+            const uint64_t bytes = cap * 4 * nf;
+            if (c->device_bytes + bytes + 256 > c->plan.budget)
+                throw InputError("the row staging of device binning (" + std::to_string(bytes) +
+                                 " bytes) does not fit the budget's remaining room");
+            c->rows_stage = c->alloc<float>(cap * nf, "row staging");
+        }
+        for (uint64_t r = 0; r < n_rows; r += cap) {
+            const uint64_t b = std::min(cap, n_rows - r);
+            // Stream order: this copy waits for the previous chunk's binning.
+            check(hipMemcpyAsync(c->rows_stage, x + r * nf, 4 * b * nf, hipMemcpyHostToDevice,
+                                 c->stream),
+                  "row upload");
+            check(launch_bin_rows(c->rows_stage, b, (uint32_t)nf, row0 + r, c->d_binfeats,
+                                  c->stream),
+                  "row binning");
+        }
+        c->sync();  // the caller may reuse x
+    });
+}
+
+int fbh_finish_rows(fbh_ctx *c) {
+    return guard([&] {
+        if (!c) throw InputError("null argument");
+        if (!c->cuts_set) throw InputError("fbh_set_cuts must come before fbh_finish_rows");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        for (uint32_t f = 0; f < c->n_features; f++) {
+            const fbh_ctx::Tile &t = c->tiles[c->feat_tile[f]];
+            if (t.resident) {
+                const uint32_t off = (uint32_t)c->feat_pos[f] * c->width[f];
+                check(launch_pack_feature(c->cols[f], c->n_rows, c->width[f], t.data, t.stride,
+                                          off, c->stream),
+                      "tile packing");
+            } else {
+                // A streamed tile's records live in pinned host memory: bring
+                // the column back and lay it into them as fbh_upload_block does.
+                throw InputError("device binning needs every tile resident");
+            }
+            c->uploaded[f] = 1;
+        }
+        c->pack_sig.clear();
         c->sync();
     });
 }

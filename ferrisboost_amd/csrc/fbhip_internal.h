@@ -439,6 +439,21 @@ hipError_t launch_gpair_quantize(const float *g2n, uint64_t n, const ScalesDev *
 hipError_t launch_pack_feature(const uint8_t *col, uint64_t n_rows, uint32_t width, uint8_t *tile,
                                uint32_t stride, uint32_t byte_off, hipStream_t s);
 
+// One feature of the device binning: its cuts, bin count and width, and
+// its resident bin column.
+struct BinFeatDev {
+    const float *cuts;
+    uint8_t *col;
+    uint32_t n_cuts;
+    uint32_t n_bins;
+    uint32_t width;        // 1 or 2
+    uint32_t categorical;  // 1: code_to_bin instead of the cut search
+};
+// Bins rows [row0, row0 + n_rows) of the row-major f32 matrix x (device
+// memory, the chunk's first row at x) into the features' columns.
+hipError_t launch_bin_rows(const float *x, uint64_t n_rows, uint32_t n_features, uint64_t row0,
+                           const BinFeatDev *feats, hipStream_t s);
+
 // One interleaved tile of a tree's own features, packed from the bin
 // columns: row r's record at out + r * stride, cell k copied from col[k]
 // when bit k of `live` is set, else zero (col[k] is then any valid column).

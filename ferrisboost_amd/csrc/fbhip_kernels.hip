@@ -2384,6 +2384,64 @@ hipError_t launch_pack_feature(const uint8_t *col, uint64_t n_rows, uint32_t wid
     return hipGetLastError();
 }
 
+// Device binning (find_bin / quantize_value, src/data/columns.rs:335-356;
+// categorical::code_to_bin): a workgroup bins a block of 64 rows x 64
+// features. The block is read row by row (consecutive lanes, consecutive
+// features of a row) into LDS, then binned column by column (consecutive
+// lanes, consecutive rows of a feature), so both the matrix reads and the
+// column writes are coalesced. A numeric value's bin is the number of cuts
+// <= it (std::upper_bound), NaN the missing code, a categorical code v its
+// own bin when 0 <= v < n_bins and else the unseen-category code.
+constexpr uint32_t BIN_ROWS = 64, BIN_FEATS = 64;
+
+__global__ __launch_bounds__(256) void bin_rows_kernel(const float *__restrict__ x,
+                                                       uint64_t n_rows, uint32_t nf, uint64_t row0,
+                                                       const BinFeatDev *__restrict__ feats) {
+    __shared__ float blk[BIN_ROWS][BIN_FEATS + 1];
+    const uint64_t rb = (uint64_t)blockIdx.x * BIN_ROWS;
+    const uint32_t fb = blockIdx.y * BIN_FEATS;
+    const uint32_t nr = (uint32_t)min<uint64_t>(BIN_ROWS, n_rows - rb);
+    const uint32_t nfb = min(BIN_FEATS, nf - fb);
+    for (uint32_t i = threadIdx.x; i < BIN_ROWS * BIN_FEATS; i += 256) {
+        const uint32_t r = i / BIN_FEATS, f = i % BIN_FEATS;
+        if (r < nr && f < nfb) blk[r][f] = x[(rb + r) * nf + fb + f];
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < BIN_ROWS * BIN_FEATS; i += 256) {
+        const uint32_t f = i / BIN_ROWS, r = i % BIN_ROWS;
+        if (r >= nr || f >= nfb) continue;
+        const BinFeatDev F = feats[fb + f];
+        const float v = blk[r][f];
+        const uint32_t missing = F.width == 1 ? 0xFFu : 0xFFFFu;
+        uint32_t bin;
+        if (v != v) {
+            bin = missing;
+        } else if (F.categorical) {
+            bin = (v >= 0.0f && v < (float)F.n_bins) ? (uint32_t)v : missing - 1u;
+        } else {
+            uint32_t lo = 0, hi = F.n_cuts;  // first cut > v
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (F.cuts[mid] <= v) lo = mid + 1;
+                else hi = mid;
+            }
+            bin = lo;
+        }
+        const uint64_t row = row0 + rb + r;
+        if (F.width == 1) F.col[row] = (uint8_t)bin;
+        else reinterpret_cast<uint16_t *>(F.col)[row] = (uint16_t)bin;
+    }
+}
+
+hipError_t launch_bin_rows(const float *x, uint64_t n_rows, uint32_t n_features, uint64_t row0,
+                           const BinFeatDev *feats, hipStream_t s) {
+    if (n_rows == 0 || n_features == 0) return hipSuccess;
+    const dim3 grid((uint32_t)((n_rows + BIN_ROWS - 1) / BIN_ROWS),
+                    (n_features + BIN_FEATS - 1) / BIN_FEATS);
+    hipLaunchKernelGGL(bin_rows_kernel, grid, dim3(256), 0, s, x, n_rows, n_features, row0, feats);
+    return hipGetLastError();
+}
+
 // Packed tiles: a workgroup packs 256 consecutive rows of one row bundle
 // (blockIdx.y; the 128 / (16 W) consecutive tiles sharing it, every tile's
 // stride the bundle's pitch). Phase 1 reads each of the bundle's columns for

@@ -780,12 +780,14 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     m.objective = p.objective;
     m.n_features = nf;
     m.scale_pos_weight = p.scale_pos_weight;
+    const auto t_sketch = Clock::now();
     if (given) {
         check_cuts(*given, nf, p.max_bin, cat);
         m.cuts = *given;
     } else {
         m.cuts = sketch_matrix(x, n, nf, p.max_bin, w, cat, threads);
     }
+    const double sketch_s = std::chrono::duration<double>(Clock::now() - t_sketch).count();
     // Base score: explicit, else the label mean weighted by the sample weights
     // only (Objective::estimate_base_score, src/training/objective.rs:42-60,
     // 452-470; scale_pos_weight enters the gradient weights alone,
@@ -853,13 +855,39 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     call(fbh_ctx_create(p.device, n, &shape, &cfg, &raw));
     std::unique_ptr<fbh_ctx, int (*)(fbh_ctx *)> ctx(raw, fbh_ctx_destroy);
     call(fbh_set_timing(ctx.get(), p.profile ? 1 : 0));
-    for (const auto &feats : blocks_by_width(m.cuts, p.cols_per_block)) {
-        const uint32_t wdt = m.cuts.width(feats[0]);
-        std::vector<uint8_t> buf((size_t)feats.size() * n * wdt);
-        bin_columns(x, n, nf, m.cuts, feats, wdt, buf.data(), threads);
-        call(fbh_upload_block(ctx.get(), feats.data(), (uint32_t)feats.size(), wdt, buf.data()));
+    // Binning: on the device when the plan keeps the bin columns resident and
+    // the budget's room holds the row staging, else column blocks binned on
+    // the host (the same bins either way).
+    const auto t_bin = Clock::now();
+    bool device_binning = false;
+    {
+        fbh_plan plan{};
+        call(fbh_ctx_plan(ctx.get(), &plan));
+        const uint64_t held = fbh_ctx_device_bytes(ctx.get());
+        const uint64_t need = fbh_rows_staging_bytes(ctx.get()) +
+                              4 * (uint64_t)m.cuts.values.size() + 64 * (uint64_t)nf + (1u << 16);
+        device_binning = !p.host_binning && plan.columns_resident && held + need <= plan.budget;
     }
+    if (device_binning) {
+        call(fbh_set_cuts(ctx.get(), m.cuts.values.data(), m.cuts.offsets.data(),
+                          m.cuts.categorical.data()));
+        const uint64_t step = 1u << 20;
+        for (uint64_t r0 = 0; r0 < n; r0 += step)
+            call(fbh_upload_rows(ctx.get(), x + r0 * nf, r0, std::min(step, n - r0)));
+        call(fbh_finish_rows(ctx.get()));
+    } else {
+        for (const auto &feats : blocks_by_width(m.cuts, p.cols_per_block)) {
+            const uint32_t wdt = m.cuts.width(feats[0]);
+            std::vector<uint8_t> buf((size_t)feats.size() * n * wdt);
+            bin_columns(x, n, nf, m.cuts, feats, wdt, buf.data(), threads);
+            call(fbh_upload_block(ctx.get(), feats.data(), (uint32_t)feats.size(), wdt, buf.data()));
+        }
+    }
+    const double bin_s = std::chrono::duration<double>(Clock::now() - t_bin).count();
     g_stats = fbt_stats{};
+    g_stats.device_binning = device_binning ? 1 : 0;
+    g_stats.sketch_seconds = sketch_s;
+    g_stats.bin_seconds = bin_s;
     g_stats.device_bytes = (double)fbh_ctx_device_bytes(ctx.get());
     g_stats.setup_seconds = std::chrono::duration<double>(Clock::now() - t_setup).count();
 

@@ -186,6 +186,34 @@ uint64_t fbh_ctx_device_bytes(const fbh_ctx *ctx);
 int fbh_upload_block(fbh_ctx *ctx, const uint32_t *feat_ids, uint32_t n_feats, uint32_t width,
                      const void *bins);
 
+/* Binning on the device (the quantisation half of DenseSource's ingest,
+ * src/source/dense.rs:99-290, with find_bin / quantize_value,
+ * src/data/columns.rs:335-356, and categorical::code_to_bin): the cuts of
+ * every feature (a FeatureSketch's cuts, src/data/sketch.rs:236-275) once,
+ * then row-major f32 rows in chunks. Each chunk is binned on the device
+ * straight into the context's resident bin columns: NaN to the missing code
+ * (all ones of the feature's width); a numeric value to the number of cuts
+ * <= it; a categorical value v to v when 0 <= v < n_bins, else to the
+ * unseen-category code (missing - 1). fbh_finish_rows then lays the columns
+ * into the tile records, as fbh_upload_block does. The chunk's rows are
+ * staged in device memory outside the memory plan: fbh_rows_staging_bytes
+ * gives how much, and the calls are an input error when the budget's
+ * remaining room cannot hold it or when the plan streams the columns (bin
+ * on the host and use fbh_upload_block then).
+ * cut_values[cut_offsets[f] .. cut_offsets[f + 1]) are feature f's cuts,
+ * strictly increasing; categorical[f] (nullable) marks categorical
+ * features, whose cut count is then n_bins - 1 (the codes 1..n_bins-1). */
+int fbh_set_cuts(fbh_ctx *ctx, const float *cut_values, const uint32_t *cut_offsets,
+                 const uint8_t *categorical);
+/* Device bytes the row staging of fbh_upload_rows takes. */
+uint64_t fbh_rows_staging_bytes(const fbh_ctx *ctx);
+/* Rows [row0, row0 + n_rows) of the matrix, row-major with the context's
+ * n_features columns (x points at row row0). */
+int fbh_upload_rows(fbh_ctx *ctx, const float *x, uint64_t row0, uint64_t n_rows);
+/* Every feature's tile records from its binned column; the features count
+ * as uploaded from then on. */
+int fbh_finish_rows(fbh_ctx *ctx);
+
 /* ------------------------------------------------------------ gradients */
 /* GpuTrainCtx::upload_and_quantize_gpair_sampled
  * (src/backend/cuda/train_ctx.rs:2345-2391, 3182-3343): uploads interleaved

@@ -74,6 +74,10 @@ typedef struct {
     uint32_t hist_streams;     /* hist_streams: 1 or 2 streaming windows (0 = 2) */
     uint32_t resident_limit;   /* resident_blocks + 1: at most that many LDS
                                   tiles stay resident (0 = as the budget allows) */
+    uint32_t host_binning;     /* 1: bin the rows on the host and upload column
+                                  blocks (0: bin on the device when the plan
+                                  keeps the columns resident and the budget has
+                                  room for the row staging) */
 } fbt_params;
 
 /* One tree node: Node (src/model/tree.rs:52-111). */
@@ -109,7 +113,9 @@ typedef struct {
     uint64_t planned_bytes;   /* peak_bytes of the plan */
     uint64_t budget_bytes;    /* the budget the plan honoured */
     uint32_t device_trees;    /* trees grown whole on the device (fbh_grow_depthwise) */
-    uint32_t reserved;
+    uint32_t device_binning;  /* 1: the rows were binned on the device (fbh_upload_rows) */
+    double sketch_seconds;    /* the quantile sketch (host), part of setup_seconds */
+    double bin_seconds;       /* binning and upload of the bins, part of setup_seconds */
 } fbt_stats;
 
 typedef struct fbt_model fbt_model;
