@@ -207,6 +207,7 @@ HIP_SYMBOLS = [
     "fbh_last_error", "fbh_device_available", "fbh_ctx_create", "fbh_ctx_destroy",
     "fbh_plan_memory", "fbh_ctx_plan", "fbh_ctx_streamed_bytes",
     "fbh_ctx_device_bytes", "fbh_upload_block", "fbh_set_cuts", "fbh_rows_staging_bytes",
+    "fbh_apply_leaf_values",
     "fbh_upload_rows", "fbh_finish_rows", "fbh_upload_quantize_gpair",
     "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_gradient_exchange",
     "fbh_download_margin", "fbh_set_gpu_math", "fbh_gradient_pairs", "fbh_sigmoid_host", "fbh_sigmoid_device", "fbh_sigmoid_checksum",
@@ -273,6 +274,7 @@ def hip() -> C.CDLL:
         L.fbh_rows_staging_bytes.restype = C.c_uint64
         L.fbh_upload_rows.argtypes = [P, P, C.c_uint64, C.c_uint64]
         L.fbh_finish_rows.argtypes = [P]
+        L.fbh_apply_leaf_values.argtypes = [P, P, C.c_uint32]
         L.fbh_upload_quantize_gpair.argtypes = [P, P, C.c_uint64, C.c_uint64, C.c_uint64, P, P]
         L.fbh_upload_gpair_fixed.argtypes = [P, P, P]
         L.fbh_set_objective.argtypes = [P, C.c_uint32, P, P, C.c_float]

@@ -349,6 +349,7 @@ struct fbh_ctx {
     void *leaf_ids = nullptr;           // per-row leaf position of the last tree
     int leaf_id_bytes = 0;              // 1 or 2 for the last assigned tree
     bool ids_fresh = false;             // leaf ids not yet handed to the host
+    bool leaves_deferred = false;       // the last grown tree's values are not in the margins yet
     bool has_weights = false;
     float *sig = nullptr;               // the host's per-row sigmoids (logistic)
     PinnedBuf pin_ids, pin_src;         // leaf-id download / sigmoid upload staging
@@ -1543,6 +1544,9 @@ int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th
                           uint64_t tree, double scales_out[2], int64_t root_out[2]) {
     return guard([&] {
         if (!c) throw InputError("null argument");
+        if (c->leaves_deferred)
+            throw InputError("the last grown tree's leaf values were deferred and not applied "
+                             "(fbh_apply_leaf_values): the margins are not up to date");
         if (!scales_out && (root_out || fn))
             throw InputError("the scales stay on the device only with neither a root sum nor "
                              "a sigmoid callback");
@@ -1621,6 +1625,9 @@ int fbh_download_margin(fbh_ctx *c, float *out) {
     return guard([&] {
         if (!c || !out) throw InputError("null argument");
         if (c->objective < 0) throw InputError("fbh_set_objective has not been called");
+        if (c->leaves_deferred)
+            throw InputError("the last grown tree's leaf values were deferred and not applied "
+                             "(fbh_apply_leaf_values): the margins are not up to date");
         check(hipSetDevice(c->device), "hipSetDevice");
         check(hipMemcpyAsync(out, c->margin, c->n_rows * 4, hipMemcpyDeviceToHost, c->stream),
               "margin download");
@@ -2602,6 +2609,12 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
         throw InputError("a device-grown tree needs max_depth in 1..=" +
                          std::to_string(MAX_GROW_DEPTH));
     if (gp->max_leaves == 1) throw InputError("max_leaves 1 leaves nothing to grow");
+    if (gp->flags & ~(uint32_t)FBH_GROW_DEFER_LEAVES) throw InputError("unknown grow flags");
+    if ((gp->flags & FBH_GROW_DEFER_LEAVES) && c->objective < 0)
+        throw InputError("deferred leaf values need a device objective (fbh_set_objective)");
+    if (c->leaves_deferred)
+        throw InputError("the last grown tree's leaf values were deferred and not applied "
+                         "(fbh_apply_leaf_values)");
     if (!c->plan.columns_resident || !c->streamed.empty())
         throw InputError("a device-grown tree needs every tile and column resident");
     if (c->n_slots > MAX_GROW_SLOTS)
@@ -2766,10 +2779,12 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     uint64_t leaf_bound = (uint64_t)1 << D;
     if (gp->max_leaves) leaf_bound = std::min<uint64_t>(leaf_bound, gp->max_leaves);
     const int idb = c->objective >= 0 ? (leaf_bound <= 256 ? 1 : 2) : 0;
+    // Deferred leaves: ids only; fbh_apply_leaf_values adds the values.
+    const bool defer = (gp->flags & FBH_GROW_DEFER_LEAVES) != 0;
     if (walk) {
         check(launch_tree_leaves(c->bundles[0].data, c->bundles[0].pitch, c->n_rows, GB.tree,
-                                 GB.tree_cats, GB.feat_off, GB.st, c->leaf_ids, idb, c->margin,
-                                 c->delta, GB.leaf_vals, c->stream),
+                                 GB.tree_cats, GB.feat_off, GB.st, c->leaf_ids, idb,
+                                 defer ? nullptr : c->margin, c->delta, GB.leaf_vals, c->stream),
               "leaf walk");
     } else {
         check(launch_leaf_plan(GB.leaves, GB.st, c->stream), "leaf plan");
@@ -2778,13 +2793,14 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
                                    c->tmp, c->delta, c->leaf_ids, idb, &GB.st->n_leaves,
                                    c->stream),
               "leaf assignment");
-        if (idb)
+        if (idb && !defer)
             check(launch_apply_leaves(c->leaf_ids, idb, GB.leaf_vals, c->n_rows, c->margin,
                                       c->stream),
                   "margin update");
     }
     c->leaf_id_bytes = idb;
     c->ids_fresh = idb != 0;
+    c->leaves_deferred = defer;
 
     // Download into the next result slot; collected in order.
     const int k = (int)(GB.next_slot++ & 1);
@@ -2837,6 +2853,12 @@ void grow_collect(fbh_ctx *c, fbh_tree_node *nodes, uint32_t node_capacity, uint
         throw InputError("output capacity too small for the grown tree");
     static_assert(sizeof(TreeNodeDev) == sizeof(fbh_tree_node), "tree node layout");
     std::memcpy(nodes, po + o_tree, sizeof(fbh_tree_node) * st.tree_size);
+    // Split nodes carry their value as a leaf from the decision kernel; a
+    // leaf's is its value.
+    for (uint32_t i = 0; i < st.tree_size; i++) {
+        if (nodes[i].flags & 1u) nodes[i].value_as_leaf = nodes[i].leaf_value;
+        else nodes[i].leaf_pos = 0xFFFFFFFFu;
+    }
     if (job.cat_words && cat_words) std::memcpy(cat_words, po + o_cats, 8 * (size_t)st.tree_cat_words);
     std::memcpy(leaf_values, po + o_vals, 4 * (size_t)st.n_leaves);
     *n_nodes = st.tree_size;
@@ -2871,6 +2893,37 @@ int fbh_grow_collect(fbh_ctx *c, fbh_tree_node *nodes, uint32_t node_capacity, u
     return guard([&] {
         grow_collect(c, nodes, node_capacity, n_nodes, cat_words, cat_capacity, leaf_values,
                      leaf_capacity, n_leaves);
+    });
+}
+
+int fbh_apply_leaf_values(fbh_ctx *c, const float *values, uint32_t n) {
+    return guard([&] {
+        if (!c || (n && !values)) throw InputError("null argument");
+        if (!c->leaves_deferred)
+            throw InputError("the last grown tree's leaf values are already applied "
+                             "(grow it with FBH_GROW_DEFER_LEAVES)");
+        if (!c->grow.pending.empty())
+            throw InputError("collect the grown tree (fbh_grow_collect) before applying its leaves");
+        const uint32_t cap = c->leaf_id_bytes == 1 ? 256u : MAX_NODES;
+        if (n == 0 || n > cap) throw InputError("leaf value count out of range");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        if (c->leaves_pending) {
+            check(hipEventSynchronize(c->leaves_done), "leaf table reuse");
+            c->leaves_pending = false;
+        }
+        // Every id of the tree indexes the table: pad it to the id range.
+        float *pv = static_cast<float *>(c->pin_leaves.p);
+        std::memcpy(pv, values, 4 * (size_t)n);
+        for (uint32_t i = n; i < cap; i++) pv[i] = 0.0f;
+        const size_t bytes = 4 * (size_t)cap;
+        float *d_vals = reinterpret_cast<float *>(c->d_leaves);
+        check(hipMemcpyAsync(d_vals, pv, bytes, hipMemcpyHostToDevice, c->stream), "leaf values");
+        check(hipEventRecord(c->leaves_done, c->stream), "event");
+        c->leaves_pending = true;
+        check(launch_apply_leaves(c->leaf_ids, c->leaf_id_bytes, d_vals, c->n_rows, c->margin,
+                                  c->stream),
+              "margin update");
+        c->leaves_deferred = false;
     });
 }
 

@@ -284,7 +284,7 @@ struct ShapNodeDev {
 struct GrowDevOut {
     GrowState *st;
     LNodeDev *next;            // the next level's evaluated nodes
-    const TreeNodeDev *tree;
+    TreeNodeDev *tree;         // read; leaves registered here get their position
     LeafDev *leaves;
     float *leaf_vals;
     uint32_t child_arena;      // arena holding the rows of this level's children
@@ -356,9 +356,10 @@ hipError_t launch_grow_decide(const GrowParamsDev &G, uint32_t depth, const Spli
 hipError_t launch_leaf_plan(LeafDev *leaves, GrowState *st, hipStream_t s);
 // Leaves of a device-grown tree by a row-order walk over the single row
 // bundle (feat_off[f]: byte offset of feature f in the bundle row, bit 15 set
-// for 16-bit cells); at most MAX_WALK_NODES tree nodes.
+// for 16-bit cells); at most MAX_WALK_NODES tree nodes. Workgroup 0 writes
+// each leaf's position into its node (pad[1]). margin NULL: leaf ids only.
 hipError_t launch_tree_leaves(const uint8_t *bundle, uint32_t pitch, uint64_t n_rows,
-                              const TreeNodeDev *tree, const uint64_t *tree_cats,
+                              TreeNodeDev *tree, const uint64_t *tree_cats,
                               const uint16_t *feat_off, GrowState *st, void *ids, int id_bytes,
                               float *margin, float *delta, float *leaf_vals, hipStream_t s);
 // order: the tree's feature positions, n_num numeric ones of at most 256

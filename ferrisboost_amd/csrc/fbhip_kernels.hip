@@ -845,6 +845,7 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
                         lf.arena = D.child_arena;
                         D.leaves[k] = lf;
                         D.leaf_vals[k] = lf.value;
+                        D.tree[ids[c]].pad[1] = k;  // the leaf's position
                         k++;
                     }
                 }
@@ -2605,6 +2606,7 @@ __global__ __launch_bounds__(1024) void grow_prep_kernel(
     t.flags = 1;
     t.leaf_value = xgb_weight(g, h, G.sp) * G.learning_rate;
     t.sum_hess = (float)h;
+    t.pad[1] = NO_SLOT;  // no leaf position yet
     tree[0] = t;
 }
 
@@ -2748,6 +2750,7 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
             t.bin = P.bin;
             t.left = (int32_t)lid;
             t.right = (int32_t)rid;
+            t.pad[0] = __float_as_uint(t.leaf_value);  // its value had it stayed a leaf
             t.leaf_value = 0.0f;
             t.gain = P.gain;
             t.flags = (P.missing_left ? 2u : 0u) | (P.is_cat ? 4u : 0u);
@@ -2759,6 +2762,7 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
             TreeNodeDev a{}, b{};
             a.left = a.right = b.left = b.right = -1;
             a.flags = b.flags = 1;
+            a.pad[1] = b.pad[1] = NO_SLOT;  // no leaf position yet
             a.leaf_value = wl * G.learning_rate;
             a.sum_hess = (float)hl;
             b.leaf_value = wr * G.learning_rate;
@@ -2815,6 +2819,7 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
             lf.arena = depth & 1u;
             leaves[k] = lf;
             leaf_vals[k] = lf.value;
+            tree[L.tree_id].pad[1] = k;  // the leaf's position
         }
         if (P.found) fr++;
     }
@@ -2885,7 +2890,7 @@ __global__ __launch_bounds__(1024) void leaf_plan_kernel(LeafDev *leaves, GrowSt
 // position and the leaf count.
 template <int IDB, int PB>
 __global__ __launch_bounds__(256) void tree_leaves_kernel(
-    const uint8_t *bundle, uint64_t n_rows, const TreeNodeDev *tree, const uint64_t *tree_cats,
+    const uint8_t *bundle, uint64_t n_rows, TreeNodeDev *tree, const uint64_t *tree_cats,
     const uint16_t *feat_off, GrowState *st, void *ids, float *margin, float *delta,
     float *leaf_vals) {
     __shared__ uint32_t buf[32];
@@ -2903,11 +2908,14 @@ __global__ __launch_bounds__(256) void tree_leaves_kernel(
         const uint32_t k = base + threadIdx.x;
         uint32_t lf = 0;
         if (k < n) {
-            const TreeNodeDev t = tree[k];
-            lf = t.flags & 1u;
+            // The fields the walk uses, one by one: workgroup 0 writes each
+            // leaf's position (pad[1]) below, which no workgroup reads.
+            const TreeNodeDev &t = tree[k];
+            const uint32_t flags = t.flags;
+            lf = flags & 1u;
             const uint32_t fo = lf ? 0u : feat_off[t.feat];
             const uint32_t meta = (fo & 0x3Fu) | ((fo & 0x8000u) ? 0x40u : 0u) | (lf << 7) |
-                                  ((t.flags & 2u) << 7) | ((t.flags & 4u) << 7);
+                                  ((flags & 2u) << 7) | ((flags & 4u) << 7);
             s_node[k] = make_ushort4((uint16_t)meta, (uint16_t)t.bin, (uint16_t)t.left,
                                      (uint16_t)t.right);
             s_cat[k] = t.cat_off;
@@ -2918,7 +2926,10 @@ __global__ __launch_bounds__(256) void tree_leaves_kernel(
         const uint32_t before = carry + block_scan(lf, buf, tot);
         if (k < n && lf) {
             s_leaf[k] = (uint16_t)before;
-            if (blockIdx.x == 0) leaf_vals[before] = s_val[k];
+            if (blockIdx.x == 0) {
+                leaf_vals[before] = s_val[k];
+                tree[k].pad[1] = before;  // the leaf's position
+            }
         }
         carry += tot;
     }
@@ -2939,8 +2950,9 @@ __global__ __launch_bounds__(256) void tree_leaves_kernel(
             rec[4 * q + 2] = v.z;
             rec[4 * q + 3] = v.w;
         }
-        // The margin's load is issued before the walk, its use after.
-        const float m = IDB ? margin[r] : 0.0f;
+        // The margin's load is issued before the walk, its use after (no
+        // margin: leaf ids only, the values are added later).
+        const float m = IDB && margin ? margin[r] : 0.0f;
         uint32_t node = 0;
         ushort4 nd = s_node[0];
         while (!(nd.x & 0x80u)) {
@@ -2969,14 +2981,14 @@ __global__ __launch_bounds__(256) void tree_leaves_kernel(
         } else {
             if (IDB == 1) static_cast<uint8_t *>(ids)[r] = (uint8_t)s_leaf[node];
             else static_cast<uint16_t *>(ids)[r] = s_leaf[node];
-            margin[r] = m + s_val[node];
+            if (margin) margin[r] = m + s_val[node];
         }
     }
 }
 
 template <int IDB>
 static void launch_walk_pb(uint32_t pitch, dim3 g, hipStream_t s, const uint8_t *bundle,
-                           uint64_t n_rows, const TreeNodeDev *tree, const uint64_t *tree_cats,
+                           uint64_t n_rows, TreeNodeDev *tree, const uint64_t *tree_cats,
                            const uint16_t *feat_off, GrowState *st, void *ids, float *margin,
                            float *delta, float *leaf_vals) {
     if (pitch == 16)
@@ -2991,7 +3003,7 @@ static void launch_walk_pb(uint32_t pitch, dim3 g, hipStream_t s, const uint8_t 
 }
 
 hipError_t launch_tree_leaves(const uint8_t *bundle, uint32_t pitch, uint64_t n_rows,
-                              const TreeNodeDev *tree, const uint64_t *tree_cats,
+                              TreeNodeDev *tree, const uint64_t *tree_cats,
                               const uint16_t *feat_off, GrowState *st, void *ids, int id_bytes,
                               float *margin, float *delta, float *leaf_vals, hipStream_t s) {
     if (pitch != 16 && pitch != 32 && pitch != 64) return hipErrorInvalidValue;

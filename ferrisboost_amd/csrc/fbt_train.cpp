@@ -307,16 +307,31 @@ class Grower {
                (p_.max_leaves == 0 || p_.max_leaves >= (1u << p_.max_depth));
     }
 
+    // Lossguide under a binding leaf cap, grown speculatively on the device:
+    // every split down to max_depth, of which the host keeps the ones the
+    // best-first expansion takes before the cap (the rows' leaf values wait
+    // for that choice). Used while the whole tree is at most 8 times the
+    // cap's leaves; a deeper tree is grown expansion by expansion instead.
+    bool lossguide_capped() const {
+        return p_.grow_policy == 1 && !lossguide_uncapped() && p_.max_leaves >= 2 &&
+               p_.max_depth >= 1 && p_.max_depth <= 14 &&
+               (1ull << p_.max_depth) <= 8ull * p_.max_leaves;
+    }
+
     bool device_growth() const {
-        return device_trees_ && (p_.grow_policy == 0 || lossguide_uncapped()) &&
+        return device_trees_ &&
+               (p_.grow_policy == 0 || lossguide_uncapped() || lossguide_capped()) &&
                p_.max_depth >= 1 && p_.max_depth <= 14 && p_.max_leaves != 1;
     }
+    // The device leaves the leaf values to collect() (FBH_GROW_DEFER_LEAVES):
+    // such a tree is collected before the next round's gradients.
+    bool deferred_leaves() const { return device_growth() && lossguide_capped(); }
 
     // Enqueues a depthwise tree on the device (root_sum NULL: the one the
     // gradient call left there); collect() waits for it and rebuilds it.
     void grow_async(const int64_t *root_sum) {
         fbh_grow_params gp{p_.max_depth, p_.grow_policy == 1 ? 0u : p_.max_leaves,
-                           p_.learning_rate, 0};
+                           p_.learning_rate, deferred_leaves() ? (uint32_t)FBH_GROW_DEFER_LEAVES : 0u};
         call(fbh_grow_depthwise_async(ctx_, &gp, &sp_, root_sum));
     }
 
@@ -352,11 +367,15 @@ class Grower {
         return t;
     }
 
-    // The lossguide tree of a device-grown one (lossguide_uncapped): the
-    // expansion loop of src/training/lossguide.rs:571-690 replayed over the
-    // device's splits, popping the highest gain first and, on equal gains,
-    // the lower node id (PendingSplit's order, lossguide.rs:46-52); each
-    // expansion numbers the two children next, as Tree::split_leaf does.
+    // The lossguide tree of a device-grown one: the expansion loop of
+    // src/training/lossguide.rs:571-690 replayed over the device's splits,
+    // popping the highest gain first and, on equal gains, the lower node id
+    // (PendingSplit's order, lossguide.rs:46-52); each expansion numbers the
+    // two children next, as Tree::split_leaf does, and the loop stops at the
+    // leaf cap. Uncapped (lossguide_uncapped) every split is taken; under a
+    // cap the device's deeper splits are dropped, and each of its leaves
+    // takes the value of the kept leaf above it, which collect() adds to the
+    // margins (fbh_apply_leaf_values).
     Tree best_first(const fbh_tree_node *tn, uint32_t nn, const uint64_t *cats) {
         struct Open {
             float gain;
@@ -368,11 +387,15 @@ class Grower {
             return a.id > b.id;
         };
         std::priority_queue<Open, std::vector<Open>, decltype(less)> heap(less);
+        const bool capped = deferred_leaves();
+        std::vector<uint32_t> kept(nn, UINT32_MAX);  // device node -> lossguide node
+        std::vector<uint32_t> parent(nn, UINT32_MAX);
         Tree t;
-        t.push_leaf(tn[0].leaf_value, tn[0].sum_hess);
+        t.push_leaf(tn[0].value_as_leaf, tn[0].sum_hess);
+        kept[0] = 0;
         if (!(tn[0].flags & 1u)) heap.push({tn[0].gain, 0, 0});
-        uint32_t expanded = 0;
-        while (!heap.empty()) {
+        uint32_t expanded = 0, leaf_count = 1;
+        while (!heap.empty() && (p_.max_leaves == 0 || leaf_count < p_.max_leaves)) {
             const Open o = heap.top();
             heap.pop();
             const fbh_tree_node &a = tn[o.dev];
@@ -381,15 +404,52 @@ class Grower {
             const fbh_tree_node &l = tn[a.left], &r = tn[a.right];
             const bool is_cat = (a.flags & 4u) != 0;
             const auto lr = t.split_leaf(o.id, a.feat, is_cat ? 0.0f : cond_of(a.feat, a.bin),
-                                         (a.flags & 2u) != 0, a.gain, l.leaf_value, l.sum_hess,
-                                         r.leaf_value, r.sum_hess);
+                                         (a.flags & 2u) != 0, a.gain, l.value_as_leaf,
+                                         l.sum_hess, r.value_as_leaf, r.sum_hess);
             if (is_cat) t.set_categories(o.id, cats + a.cat_offset, a.n_cat_words);
+            kept[a.left] = lr.first;
+            kept[a.right] = lr.second;
+            leaf_count++;
+            expanded++;
+            // lossguide.rs:677-690: at the cap the children stay leaves
+            if (p_.max_leaves != 0 && leaf_count == p_.max_leaves) break;
             if (!(l.flags & 1u)) heap.push({l.gain, lr.first, (uint32_t)a.left});
             if (!(r.flags & 1u)) heap.push({r.gain, lr.second, (uint32_t)a.right});
-            expanded++;
         }
-        if (t.nodes.size() != nn || 2 * expanded + 1 != nn)
-            throw RuntimeError("device tree node count mismatch");
+        if (!capped) {
+            if (t.nodes.size() != nn || 2 * expanded + 1 != nn)
+                throw RuntimeError("device tree node count mismatch");
+            return t;
+        }
+        // Leaf values by the device's leaf positions: each device leaf takes
+        // the value of its nearest kept ancestor (itself when kept).
+        for (uint32_t i = 0; i < nn; i++)
+            if (!(tn[i].flags & 1u)) {
+                parent[(uint32_t)tn[i].left] = i;
+                parent[(uint32_t)tn[i].right] = i;
+            }
+        std::vector<float> table(leaves_values_.size(), 0.0f);
+        std::vector<uint8_t> seen(table.size(), 0);
+        for (uint32_t i = 0; i < nn; i++) {
+            if (!(tn[i].flags & 1u) || tn[i].leaf_pos == UINT32_MAX) continue;
+            if (tn[i].leaf_pos >= table.size()) throw RuntimeError("device leaf position out of range");
+            if (leaves_values_[tn[i].leaf_pos] != tn[i].leaf_value)
+                throw RuntimeError("device leaf positions disagree with the leaf values");
+            uint32_t k = i;
+            while (kept[k] == UINT32_MAX) {
+                k = parent[k];
+                if (k == UINT32_MAX) throw RuntimeError("device tree node without a kept ancestor");
+            }
+            const auto &node = t.nodes[kept[k]];
+            if (!node.is_leaf) throw RuntimeError("kept ancestor of a device leaf is not a leaf");
+            table[tn[i].leaf_pos] = node.leaf_value;
+            seen[tn[i].leaf_pos] = 1;
+        }
+        for (uint8_t v : seen)
+            if (!v) throw RuntimeError("a device leaf position has no leaf");
+        if (!table.empty())
+            call(fbh_apply_leaf_values(ctx_, table.data(), (uint32_t)table.size()));
+        leaves_values_ = std::move(table);
         return t;
     }
 
@@ -845,6 +905,11 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     if (p.grow_policy == 1) {
         const uint64_t leaves = p.max_leaves ? p.max_leaves : (1ull << std::min(p.max_depth, 14u));
         slots = (uint32_t)std::min<uint64_t>(leaves + 2, 16384);
+        // A capped tree grown speculatively on the device (Grower::
+        // lossguide_capped) needs a depthwise level's slots.
+        if (p.max_leaves >= 2 && p.max_depth >= 1 && p.max_depth <= 14 &&
+            (1ull << p.max_depth) <= 8ull * p.max_leaves)
+            slots = std::max<uint32_t>(slots, 1u << (p.max_depth - 1));
     } else {
         slots = 1u << (p.max_depth > 0 ? p.max_depth - 1 : 0);
         if (p.max_leaves) slots = std::min(slots, p.max_leaves + 1);
@@ -939,7 +1004,7 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     // the device works on round r + 1 and no round waits for the host. A
     // host sigmoid needs tree r's leaf values first, so it collects before
     // its gradients (and takes the scales back to the host).
-    const bool overlap = grower.device_growth();
+    const bool overlap = grower.device_growth() && !grower.deferred_leaves();
     const bool host_sig = obj == 1 && !dev_sigmoid;
     const bool device_scales = overlap && !host_sig;
     uint32_t pending = 0;

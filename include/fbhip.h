@@ -376,14 +376,27 @@ typedef struct fbh_tree_node {
     uint32_t flags;       /* bit 0 leaf, bit 1 missing goes left, bit 2 categorical */
     uint32_t cat_offset;  /* right-going category set: cat_words[cat_offset..+n_cat_words] */
     uint32_t n_cat_words;
-    uint32_t reserved[2];
+    float value_as_leaf;  /* the node's leaf value (learning rate applied) had it
+                             stayed a leaf; equal to leaf_value for a leaf */
+    uint32_t leaf_pos;    /* a leaf's position among the leaf values (its rows'
+                             leaf id); 0xFFFFFFFF for a split node or a leaf
+                             without rows */
 } fbh_tree_node;
+
+/* fbh_grow_params.flags */
+enum {
+    /* The rows' leaf ids are computed but no leaf value is added to the
+     * margins: the caller adds them with fbh_apply_leaf_values once it has
+     * decided them (lossguide under a binding leaf cap, which keeps only
+     * some of the grown splits). Needs a device objective. */
+    FBH_GROW_DEFER_LEAVES = 1
+};
 
 typedef struct fbh_grow_params {
     uint32_t max_depth;   /* 1..=14 */
     uint32_t max_leaves;  /* 0: unlimited */
     float learning_rate;
-    uint32_t reserved;
+    uint32_t flags;       /* FBH_GROW_* */
 } fbh_grow_params;
 
 /* A whole depthwise tree on the device (build_tree, src/training/mod.rs:
@@ -411,6 +424,13 @@ int fbh_grow_depthwise_async(fbh_ctx *ctx, const fbh_grow_params *grow,
 int fbh_grow_collect(fbh_ctx *ctx, fbh_tree_node *nodes, uint32_t node_capacity,
                      uint32_t *n_nodes, uint64_t *cat_words, uint32_t cat_capacity,
                      float *leaf_values, uint32_t leaf_capacity, uint32_t *n_leaves);
+
+/* GpuTrainCtx::assign_leaf_values for a tree grown with
+ * FBH_GROW_DEFER_LEAVES (src/backend/cuda/train_ctx.rs:2128-2252, the
+ * device_leaves of lossguide::grow, src/training/lossguide.rs:693-695):
+ * margin[row] += values[leaf id of row] for the last grown tree, values by
+ * the leaf positions fbh_grow_collect reported (n_values of them). */
+int fbh_apply_leaf_values(fbh_ctx *ctx, const float *values, uint32_t n_values);
 
 /* GpuTrainCtx::assign_leaf_values (src/backend/cuda/train_ctx.rs:2128-2252):
  * delta[row] = value for every row of each span. */

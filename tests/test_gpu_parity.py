@@ -243,7 +243,8 @@ def test_sampled_weighted_rounds_match_oracle(fb, oracle, objective, depth, host
 @pytest.mark.parametrize("case", ["budget", "monotone", "categorical", "sampled_deep", "stump",
                                   "squared", "walk_budget", "walk_categorical", "walk_squared",
                                   "walk_u16", "lg_plain", "lg_monotone", "lg_categorical",
-                                  "lg_sampled_deep", "lg_cap64"])
+                                  "lg_sampled_deep", "lg_cap64", "lg_cap11", "lg_cap9_categorical",
+                                  "walk_lg_cap11", "lg_cap20_monotone"])
 def test_device_grown_trees_match_host_levels_and_oracle(fb, oracle, case):
     """Whole depthwise trees grown on the device (the max_leaves budget, node
     ids, weights, bounds, slots, partitions and leaves decided by kernels)
@@ -253,9 +254,12 @@ def test_device_grown_trees_match_host_levels_and_oracle(fb, oracle, case):
     margins come from the row-order walk of the finished tree instead of a
     last-level partition; walk_u16 has 300 bins (16-bit cells, three
     features a 16 KiB tile, two tiles in one 16-byte bundle). The lg_ cases
-    grow lossguide trees whose leaf cap cannot bind (max_leaves 0, or 64 at
-    depth 6): the device grows every split and the host numbers the nodes
-    in best-first order, against the host's expansion-by-expansion growth."""
+    grow lossguide trees: whose leaf cap cannot bind (max_leaves 0, or 64 at
+    depth 6), where the device grows every split and the host numbers the
+    nodes in best-first order; and under a binding cap (9, 11, 20 leaves at
+    depth 6), where the host keeps the splits best-first expansion takes
+    before the cap and the device adds the kept leaves' values to the rows
+    afterwards; against the host's expansion-by-expansion growth."""
     walk = case.startswith("walk_")
     case = case[5:] if walk else case
     lossguide = case.startswith("lg_")
@@ -292,6 +296,16 @@ def test_device_grown_trees_match_host_levels_and_oracle(fb, oracle, case):
         p.update(max_bin=300)
     elif case == "cap64":
         p.update(max_leaves=64)
+    elif case == "cap11":
+        p.update(max_leaves=11)
+    elif case == "cap9_categorical":
+        x[:, 5] = rng.integers(0, 40, n)
+        y = ((x[:, 5] % 3 == 1) | (np.nan_to_num(x[:, 0]) > 1)).astype(np.float32)
+        cat = [0, 0, 0, 0, 0, 1]
+        p.update(max_leaves=9)
+    elif case == "cap20_monotone":
+        mono = [1, -1, 0, 1, 0, 0]
+        p.update(max_leaves=20)
     if lossguide:
         p.update(grow_policy="lossguide")
     om = oracle.train(x, y, oracle.make_params(**p), weights=w, monotone=mono, categorical=cat)
@@ -317,12 +331,13 @@ class _TreeNode(C.Structure):
     _fields_ = [("feat", C.c_uint32), ("bin", C.c_uint32), ("left", C.c_int32),
                 ("right", C.c_int32), ("leaf_value", C.c_float), ("sum_hess", C.c_float),
                 ("gain", C.c_float), ("flags", C.c_uint32), ("cat_offset", C.c_uint32),
-                ("n_cat_words", C.c_uint32), ("reserved", C.c_uint32 * 2)]
+                ("n_cat_words", C.c_uint32), ("value_as_leaf", C.c_float),
+                ("leaf_pos", C.c_uint32)]
 
 
 class _GrowParams(C.Structure):
     _fields_ = [("max_depth", C.c_uint32), ("max_leaves", C.c_uint32),
-                ("learning_rate", C.c_float), ("reserved", C.c_uint32)]
+                ("learning_rate", C.c_float), ("flags", C.c_uint32)]
 
 
 @pytest.mark.parametrize("tile_bytes", [0, 4096])
