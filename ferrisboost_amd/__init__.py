@@ -77,6 +77,7 @@ _DEFAULTS: dict[str, Any] = {
     "hip_host_levels": False,
     "hip_sync_round": 0,
     "hip_host_binning": False,
+    "hip_host_sketch": False,
 }
 
 _ALIASES = {
@@ -222,6 +223,7 @@ def _params_struct(p: dict[str, Any], n_features: int) -> N.TrainParams:
     s.hist_streams = int(p["hist_streams"] or 0)
     s.resident_limit = 0 if p["resident_blocks"] is None else int(p["resident_blocks"]) + 1
     s.host_binning = 1 if p["hip_host_binning"] else 0
+    s.host_sketch = 1 if p["hip_host_sketch"] else 0
     return s
 
 

@@ -159,6 +159,7 @@ class TrainParams(C.Structure):
         ("hist_streams", C.c_uint32),
         ("resident_limit", C.c_uint32),
         ("host_binning", C.c_uint32),
+        ("host_sketch", C.c_uint32),
     ]
 
 
@@ -182,6 +183,7 @@ class Stats(C.Structure):
         ("device_binning", C.c_uint32),
         ("sketch_seconds", C.c_double),
         ("bin_seconds", C.c_double),
+        ("device_sketch", C.c_uint32),
     ]
 
 
@@ -208,7 +210,9 @@ HIP_SYMBOLS = [
     "fbh_plan_memory", "fbh_ctx_plan", "fbh_ctx_streamed_bytes",
     "fbh_ctx_device_bytes", "fbh_upload_block", "fbh_set_cuts", "fbh_rows_staging_bytes",
     "fbh_apply_leaf_values",
-    "fbh_upload_rows", "fbh_finish_rows", "fbh_upload_quantize_gpair",
+    "fbh_upload_rows", "fbh_finish_rows", "fbh_sketch_device_bytes", "fbh_sketch_fits",
+    "fbh_sketch_create", "fbh_sketch_push_rows", "fbh_sketch_cuts", "fbh_sketch_destroy",
+    "fbh_upload_quantize_gpair",
     "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_gradient_exchange",
     "fbh_download_margin", "fbh_set_gpu_math", "fbh_gradient_pairs", "fbh_sigmoid_host", "fbh_sigmoid_device", "fbh_sigmoid_checksum",
     "fbh_begin_tree", "fbh_eval_nodes", "fbh_download_histogram",
@@ -274,6 +278,14 @@ def hip() -> C.CDLL:
         L.fbh_rows_staging_bytes.restype = C.c_uint64
         L.fbh_upload_rows.argtypes = [P, P, C.c_uint64, C.c_uint64]
         L.fbh_finish_rows.argtypes = [P]
+        L.fbh_sketch_device_bytes.argtypes = [C.c_uint64, C.c_uint32, C.c_uint32, P]
+        L.fbh_sketch_device_bytes.restype = C.c_uint64
+        L.fbh_sketch_fits.argtypes = [C.c_int, C.c_uint64, C.c_uint32, C.c_uint32, P, C.c_uint64]
+        L.fbh_sketch_create.argtypes = [C.c_int, C.c_uint64, C.c_uint32, C.c_uint32, P,
+                                        C.c_uint64, C.POINTER(P)]
+        L.fbh_sketch_push_rows.argtypes = [P, P, C.c_uint64]
+        L.fbh_sketch_cuts.argtypes = [P, P, C.c_uint64, P, P]
+        L.fbh_sketch_destroy.argtypes = [P]
         L.fbh_apply_leaf_values.argtypes = [P, P, C.c_uint32]
         L.fbh_upload_quantize_gpair.argtypes = [P, P, C.c_uint64, C.c_uint64, C.c_uint64, P, P]
         L.fbh_upload_gpair_fixed.argtypes = [P, P, P]

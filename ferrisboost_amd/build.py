@@ -34,7 +34,7 @@ HIP_FLAGS = [
     "-Wno-unused-result",
 ]
 
-BACKEND_SRCS = ["fbhip_kernels.hip", "fbhip_ctx.hip", "fbhip_shap.hip"]
+BACKEND_SRCS = ["fbhip_kernels.hip", "fbhip_ctx.hip", "fbhip_shap.hip", "fbhip_sketch.hip"]
 DRIVER_SRCS = ["fbt_data.cpp", "fbt_train.cpp", "fbt_model.cpp", "fbt_json.cpp", "fbt_api.cpp"]
 
 LIB_HIP = os.path.join(HERE, "libfbhip.so")

@@ -8,7 +8,10 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <memory>
 #include <thread>
+
+#include "../../include/fbhip.h"
 
 #include "fbt_internal.h"
 
@@ -208,6 +211,27 @@ uint32_t Cuts::bin_of(uint32_t f, float v) const {
     return (uint32_t)(std::upper_bound(c, c + n_cuts(f), v) - c);
 }
 
+static std::vector<float> sketch_numeric(const float *x, uint64_t n, uint32_t nf, uint32_t f,
+                                  uint32_t max_bin, const float *w) {
+    FeatureQuantiles q(max_bin);
+    for (uint64_t r = 0; r < n; r++) q.add(x[r * nf + f], w ? w[r] : 1.0f);
+    return q.cuts(max_bin);
+}
+
+static Cuts assemble_cuts(std::vector<std::vector<float>> &per, uint32_t nf, const uint8_t *cat) {
+    Cuts c;
+    c.offsets.push_back(0);
+    for (uint32_t f = 0; f < nf; f++) {
+        c.values.insert(c.values.end(), per[f].begin(), per[f].end());
+        c.offsets.push_back((uint32_t)c.values.size());
+        c.categorical.push_back(cat && cat[f] ? 1 : 0);
+    }
+    for (uint32_t f = 0; f < nf; f++)
+        if (c.n_bins(f) > (c.is_cat(f) ? 65534u : 65535u))
+            throw InputError("feature " + std::to_string(f) + " has too many bins");
+    return c;
+}
+
 Cuts sketch_matrix(const float *x, uint64_t n, uint32_t nf, uint32_t max_bin, const float *w,
                    const uint8_t *cat, unsigned threads) {
     std::vector<std::vector<float>> per(nf);
@@ -227,25 +251,47 @@ Cuts sketch_matrix(const float *x, uint64_t n, uint32_t nf, uint32_t max_bin, co
             for (int c = 1; c <= std::max(max_code, 0); c++) per[f].push_back((float)c);
             return;
         }
-        FeatureQuantiles q(max_bin);
-        for (uint64_t r = 0; r < n; r++) q.add(x[r * nf + f], w ? w[r] : 1.0f);
-        per[f] = q.cuts(max_bin);
+        per[f] = sketch_numeric(x, n, nf, f, max_bin, w);
     });
     for (uint32_t f = 0; f < nf; f++)
         if (bad[f])
             throw InputError("categorical feature #" + std::to_string(f) +
                              " contains a value that is not an integer code in 0..=65533");
-    Cuts c;
-    c.offsets.push_back(0);
+    return assemble_cuts(per, nf, cat);
+}
+
+Cuts sketch_matrix_device(int device, const float *x, uint64_t n, uint32_t nf, uint32_t max_bin,
+                          const uint8_t *cat, uint64_t memory_budget, unsigned threads) {
+    fbh_sketch *raw = nullptr;
+    auto call = [](int rc) {
+        if (rc == FBH_OK) return;
+        char buf[1024];
+        fbh_last_error(buf, sizeof buf);
+        if (rc == FBH_INPUT_ERROR) throw InputError(buf);
+        throw RuntimeError(buf);
+    };
+    call(fbh_sketch_create(device, n, nf, max_bin, cat, memory_budget, &raw));
+    std::unique_ptr<fbh_sketch, int (*)(fbh_sketch *)> s(raw, fbh_sketch_destroy);
+    call(fbh_sketch_push_rows(s.get(), x, n));
+    uint64_t cap = 0;
+    for (uint32_t f = 0; f < nf; f++) cap += (cat && cat[f]) ? 65533u : (max_bin ? max_bin - 1 : 0);
+    std::vector<float> values(std::max<uint64_t>(cap, 1));
+    std::vector<uint32_t> offsets(nf + 1);
+    std::vector<uint8_t> host(nf);
+    call(fbh_sketch_cuts(s.get(), values.data(), cap, offsets.data(), host.data()));
+    s.reset();
+    std::vector<std::vector<float>> per(nf);
+    std::vector<uint32_t> on_host;
     for (uint32_t f = 0; f < nf; f++) {
-        c.values.insert(c.values.end(), per[f].begin(), per[f].end());
-        c.offsets.push_back((uint32_t)c.values.size());
-        c.categorical.push_back(cat && cat[f] ? 1 : 0);
+        if (host[f]) on_host.push_back(f);
+        else per[f].assign(values.begin() + offsets[f], values.begin() + offsets[f + 1]);
     }
-    for (uint32_t f = 0; f < nf; f++)
-        if (c.n_bins(f) > (c.is_cat(f) ? 65534u : 65535u))
-            throw InputError("feature " + std::to_string(f) + " has too many bins");
-    return c;
+    // Features holding both zero signs with a zero among their cuts: the
+    // host sketch decides the zero's sign.
+    parallel_for((uint32_t)on_host.size(), threads, [&](uint32_t i) {
+        per[on_host[i]] = sketch_numeric(x, n, nf, on_host[i], max_bin, nullptr);
+    });
+    return assemble_cuts(per, nf, cat);
 }
 
 void check_cuts(const Cuts &c, uint32_t nf, uint32_t max_bin, const uint8_t *cat) {

@@ -38,6 +38,13 @@ struct Cuts {
 Cuts sketch_matrix(const float *x, uint64_t n_rows, uint32_t n_features, uint32_t max_bin,
                    const float *weights, const uint8_t *categorical, unsigned threads);
 
+// The same cuts from the device sketch (fbh_sketch_*), for unit row
+// weights; a feature the device leaves to the host (both zero signs) is
+// sketched here.
+Cuts sketch_matrix_device(int device, const float *x, uint64_t n_rows, uint32_t n_features,
+                          uint32_t max_bin, const uint8_t *categorical, uint64_t memory_budget,
+                          unsigned threads);
+
 // Cuts handed in by a caller (fbt_train_cuts): per feature strictly
 // increasing finite values, at most max_bin - 1 for a numeric feature and
 // categorical flags matching `categorical`; InputError otherwise.

@@ -841,9 +841,16 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     m.n_features = nf;
     m.scale_pos_weight = p.scale_pos_weight;
     const auto t_sketch = Clock::now();
+    // The device sketch gives the host sketch's cuts for unit row weights.
+    const bool device_sketch =
+        !given && !w && !p.host_sketch &&
+        fbh_sketch_fits(p.device, n, nf, p.max_bin, cat, p.gpu_memory_budget);
     if (given) {
         check_cuts(*given, nf, p.max_bin, cat);
         m.cuts = *given;
+    } else if (device_sketch) {
+        m.cuts = sketch_matrix_device(p.device, x, n, nf, p.max_bin, cat, p.gpu_memory_budget,
+                                      threads);
     } else {
         m.cuts = sketch_matrix(x, n, nf, p.max_bin, w, cat, threads);
     }
@@ -951,6 +958,7 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     const double bin_s = std::chrono::duration<double>(Clock::now() - t_bin).count();
     g_stats = fbt_stats{};
     g_stats.device_binning = device_binning ? 1 : 0;
+    g_stats.device_sketch = device_sketch ? 1 : 0;
     g_stats.sketch_seconds = sketch_s;
     g_stats.bin_seconds = bin_s;
     g_stats.device_bytes = (double)fbh_ctx_device_bytes(ctx.get());

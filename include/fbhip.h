@@ -214,6 +214,51 @@ int fbh_upload_rows(fbh_ctx *ctx, const float *x, uint64_t row0, uint64_t n_rows
  * as uploaded from then on. */
 int fbh_finish_rows(fbh_ctx *ctx);
 
+/* The quantile sketch on the device (the sketch half of DenseSource's
+ * ingest, src/source/dense.rs:99-290): SketchSet::with_categorical,
+ * push_row over every row with weight 1, finalize_checked
+ * (src/data/sketch.rs:440-560). The cuts equal the host sketch's bit for
+ * bit: each feature's non-missing values are batched in row order, sorted
+ * and merged through the same binary counter of summaries, with the same
+ * f32 operations. Row weights other than 1 are not taken (sketch those on
+ * the host). The one value the host leaves to its unstable sort is the sign
+ * of a zero entry whose batch holds both -0.0 and +0.0 (they compare
+ * equal): a numeric feature holding both signs whose cuts include a zero is
+ * reported in host_features and left to the caller's host sketch.
+ * The sketch is independent of any context: it allocates its own device
+ * memory (fbh_sketch_device_bytes at most) and frees it at destroy. */
+typedef struct fbh_sketch fbh_sketch;
+/* Device bytes a sketch of these sizes takes at most; 0 when the device
+ * sketch does not take them (max_bin above 1024, 2^32 rows or more). */
+uint64_t fbh_sketch_device_bytes(uint64_t n_rows, uint32_t n_features, uint32_t max_bin,
+                                 const uint8_t *categorical);
+/* 1 when fbh_sketch_create would accept these sizes on this device
+ * (fbh_sketch_device_bytes within memory_budget, or within free HBM minus
+ * max(15 %, 512 MiB) when memory_budget is 0), else 0. Never errors. */
+int fbh_sketch_fits(int device, uint64_t n_rows, uint32_t n_features, uint32_t max_bin,
+                    const uint8_t *categorical, uint64_t memory_budget);
+/* SketchSet::with_categorical (src/data/sketch.rs:452-466) for n_rows rows
+ * of n_features features; categorical[f] (nullable) marks categorical
+ * features. Input error when the sizes do not fit (fbh_sketch_fits). */
+int fbh_sketch_create(int device, uint64_t n_rows, uint32_t n_features, uint32_t max_bin,
+                      const uint8_t *categorical, uint64_t memory_budget, fbh_sketch **out);
+/* SketchSet::push_row (src/data/sketch.rs:474-483) over the next n_rows
+ * rows, row-major f32 (NaN is missing). At most the created row count in
+ * all; x may be reused when the call returns. */
+int fbh_sketch_push_rows(fbh_sketch *s, const float *x, uint64_t n_rows);
+/* SketchSet::finalize_checked (src/data/sketch.rs:517-560), once: feature
+ * f's cuts into cut_values[cut_offsets[f] .. cut_offsets[f + 1])
+ * (n_features + 1 offsets). A categorical feature's cuts are its codes
+ * 1..max_code; an invalid code (negative, fractional or above 65533) is
+ * the reference's input error. host_features[f] (n_features entries) is 1
+ * for a numeric feature holding both zero signs whose cuts include a zero;
+ * its cuts are then left empty for the caller to sketch on the host; else
+ * 0. Input error when the
+ * cuts need more than values_capacity values (the offsets are set). */
+int fbh_sketch_cuts(fbh_sketch *s, float *cut_values, uint64_t values_capacity,
+                    uint32_t *cut_offsets, uint8_t *host_features);
+int fbh_sketch_destroy(fbh_sketch *s);
+
 /* ------------------------------------------------------------ gradients */
 /* GpuTrainCtx::upload_and_quantize_gpair_sampled
  * (src/backend/cuda/train_ctx.rs:2345-2391, 3182-3343): uploads interleaved

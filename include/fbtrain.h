@@ -78,6 +78,9 @@ typedef struct {
                                   blocks (0: bin on the device when the plan
                                   keeps the columns resident and the budget has
                                   room for the row staging) */
+    uint32_t host_sketch;      /* 1: sketch the cuts on the host (0: on the
+                                  device for unit row weights when the budget
+                                  has room, the same cuts either way) */
 } fbt_params;
 
 /* One tree node: Node (src/model/tree.rs:52-111). */
@@ -114,8 +117,9 @@ typedef struct {
     uint64_t budget_bytes;    /* the budget the plan honoured */
     uint32_t device_trees;    /* trees grown whole on the device (fbh_grow_depthwise) */
     uint32_t device_binning;  /* 1: the rows were binned on the device (fbh_upload_rows) */
-    double sketch_seconds;    /* the quantile sketch (host), part of setup_seconds */
+    double sketch_seconds;    /* the quantile sketch, part of setup_seconds */
     double bin_seconds;       /* binning and upload of the bins, part of setup_seconds */
+    uint32_t device_sketch;   /* 1: the cuts came from the device sketch (fbh_sketch_*) */
 } fbt_stats;
 
 typedef struct fbt_model fbt_model;
