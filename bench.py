@@ -211,11 +211,12 @@ def train_workload(args, X, y, params, desc: str, traffic_tag: str):
         "hist_ms_per_round": round(t_hist_ms / args.steps, 3),
         "hist_launches_per_round": round(launches / rounds, 2),
         "gradient_ms_per_round": round(1e3 * model.stats["host_gradient_seconds"] / rounds, 3),
-        # setup (outside the timed rounds): the host quantile sketch, then
-        # binning (on the device when the plan keeps the columns resident)
+        # setup (outside the timed rounds): the quantile sketch, then binning
+        # (each on the device when it fits, the host's cuts and bins either way)
         "setup": {"seconds": round(model.stats["setup_seconds"], 3),
                   "sketch_seconds": round(model.stats["sketch_seconds"], 3),
                   "binning_seconds": round(model.stats["bin_seconds"], 3),
+                  "device_sketch": bool(model.stats["device_sketch"]),
                   "device_binning": bool(model.stats["device_binning"])},
         "roofline": roofline,
         "cpu_baseline": cpu,

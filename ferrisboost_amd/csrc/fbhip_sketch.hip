@@ -361,42 +361,53 @@ struct SkMergeTask {
     uint32_t *nd;
 };
 
+// compress's targets: target_k = total * k / slots (f32, two roundings).
+__device__ __forceinline__ float sk_target(float total, uint32_t k, uint32_t slots) {
+    return total * (float)k / (float)slots;
+}
+
+// The largest k in [0, slots - 1] with target_k <= m (0: none). The targets
+// never decrease in k, so an estimate from the exact quotient is moved to
+// the boundary by evaluating the targets themselves.
+__device__ uint32_t sk_targets_upto(float m, float total, uint32_t slots) {
+    const double e = (double)m * (double)slots / (double)total;
+    uint32_t k = e <= 0.0 ? 0u : (e >= (double)(slots - 1) ? slots - 1 : (uint32_t)e);
+    while (k + 1 <= slots - 1 && sk_target(total, k + 1, slots) <= m) k++;
+    while (k >= 1 && sk_target(total, k, slots) > m) k--;
+    return k;
+}
+
 // compress as a prefix maximum. The host walk keeps entry 0, then for
-// k = 1 .. slots - 1 the first j >= taken + 1 whose rmid reaches
-// target_k = total * k / slots (stopping at n - 1), capped at
-// n - 1 - (slots - 1 - k), and finally entry n - 1 if not taken. rmid never
-// decreases along a summary (every entry's rmin is at least its
-// predecessor's rmax, and f32 rounding is monotone), so the walk's j is
-// max(taken + 1, lb_k), lb_k = the first index >= 1 whose rmid reaches
-// target_k (n - 1 if none). With u_k = taken_k - k the recurrence becomes
+// k = 1 .. slots - 1 the first j >= taken + 1 whose rmid reaches target_k
+// (stopping at n - 1), capped at n - 1 - (slots - 1 - k), and finally entry
+// n - 1 if not taken. rmid never decreases along a summary (every entry's
+// rmin is at least its predecessor's rmax, and f32 rounding is monotone), so
+// the walk's j is max(taken + 1, lb_k), lb_k = the first index in
+// [1, n - 2] whose rmid reaches target_k (n - 1 if none). With
+// u_k = taken_k - k the recurrence becomes
 // u_k = min(max(lb_k - k, u_{k-1}), n - slots), u_0 = 0, that is
 // taken_k = k + min(n - slots, max(0, max_{i <= k} (lb_i - i))).
-// Writes taken_k into sel[k] for k = 1 .. slots - 1. `all` threads call it.
+// lb comes from the entries' side: with c_i the number of targets entry i's
+// rmid reaches (nondecreasing in i), lb_k = i for c_{i-1} < k <= c_i
+// (c_0 = 0), so each entry scatters its own k and the reads are coalesced.
+// Writes taken_k into sel[k] for k = 1 .. slots - 1; every thread calls it.
 template <class IDX>
 __device__ void sk_compress_plan(const SkEntry *s, uint32_t n, uint32_t slots, IDX *sel,
                                  int *ibuf) {
     const float total = s[n - 1].rmax;
+    for (uint32_t k = 1 + threadIdx.x; k < slots; k += SK_TPB) sel[k] = (IDX)(n - 1);
+    __syncthreads();
+    for (uint32_t i = 1 + threadIdx.x; i + 1 < n; i += SK_TPB) {
+        const uint32_t ci = sk_targets_upto(sk_mid(s + i), total, slots);
+        const uint32_t cp = i == 1 ? 0u : sk_targets_upto(sk_mid(s + i - 1), total, slots);
+        for (uint32_t k = cp + 1; k <= ci; k++) sel[k] = (IDX)i;
+    }
+    __syncthreads();
     const uint32_t nk = slots - 1;
     const uint32_t per = (nk + SK_TPB - 1) / SK_TPB;
     const uint32_t ka = 1 + min(nk, threadIdx.x * per), kb = 1 + min(nk, threadIdx.x * per + per);
     int run = INT_MIN;
-    uint32_t idx = 1;
-    for (uint32_t k = ka; k < kb; k++) {
-        const float target = total * (float)k / (float)slots;
-        if (k == ka) {
-            uint32_t lo = 1, hi = n - 1;
-            while (lo < hi) {
-                const uint32_t mid = (lo + hi) >> 1;
-                if (sk_mid(s + mid) < target) lo = mid + 1;
-                else hi = mid;
-            }
-            idx = lo;
-        } else {
-            while (idx < n - 1 && sk_mid(s + idx) < target) idx++;
-        }
-        sel[k] = (IDX)idx;
-        run = max(run, (int)idx - (int)k);
-    }
+    for (uint32_t k = ka; k < kb; k++) run = max(run, (int)sel[k] - (int)k);
     int r = sk_scan_max(run, ibuf);
     const int C = (int)(n - slots);
     for (uint32_t k = ka; k < kb; k++) {
@@ -406,90 +417,136 @@ __device__ void sk_compress_plan(const SkEntry *s, uint32_t n, uint32_t slots, I
     __syncthreads();
 }
 
+// Merge path: the a-entries among the first k outputs of merge(a, b) (on
+// equal values a's entry goes first).
+__device__ uint32_t sk_merge_path(const SkEntry *a, uint32_t na, const SkEntry *b, uint32_t nb,
+                                  uint32_t k) {
+    uint32_t lo = k > nb ? k - nb : 0u, hi = min(k, na);
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (a[mid].v <= b[k - mid - 1].v) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// The merged output runs in chunks of SK_MCH: each chunk's entries of a and
+// b (plus one on each side) are staged in LDS with coalesced loads, each
+// thread merges SK_MPT outputs from there, and the runs of equal values are
+// counted by a block scan. Chunk boundaries come from one merge-path search
+// each, all at once.
+constexpr uint32_t SK_MCH = 1024;
+constexpr uint32_t SK_MPT = SK_MCH / SK_TPB;
+constexpr uint32_t SK_MAX_CHUNKS = 64;  // 2 * 16 * 1024 outputs at most under `prune`
+
 __global__ __launch_bounds__(SK_TPB) void sk_merge_kernel(const SkMergeTask *__restrict__ tasks,
                                                           uint32_t limit, uint32_t prune) {
     extern __shared__ uint16_t sel[];
+    __shared__ SkEntry sa[SK_MCH + 2], sb[SK_MCH + 2];
+    __shared__ uint32_t bound[SK_MAX_CHUNKS + 1];
     __shared__ uint32_t buf[8];
     __shared__ int ibuf[8];
     const SkMergeTask T = tasks[blockIdx.x];
     const SkEntry *a = T.a, *b = T.b;
     const uint32_t na = *T.na, nb = *T.nb, M = na + nb;
-    const uint32_t per = (M + SK_TPB - 1) / SK_TPB;
-    const uint32_t k0 = min(M, threadIdx.x * per), k1 = min(M, k0 + per);
-    // Merge path: i0 = the a-entries among the first k0 outputs (on equal
-    // values a's entry goes first).
-    uint32_t lo = k0 > nb ? k0 - nb : 0u, hi = min(k0, na);
-    while (lo < hi) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if (a[mid].v <= b[k0 - mid - 1].v) lo = mid + 1;
-        else hi = mid;
-    }
-    const uint32_t i0 = lo, j0 = k0 - lo;
-    const bool has_prev0 = k0 > 0 && k0 < M;
-    float prev0 = 0.0f;
-    if (has_prev0) {
-        if (i0 == 0) prev0 = b[j0 - 1].v;
-        else if (j0 == 0) prev0 = a[i0 - 1].v;
-        else prev0 = fmaxf(a[i0 - 1].v, b[j0 - 1].v);
-    }
-    // Pass 1: outputs of [k0, k1) that start a run of equal values.
-    uint32_t starts = 0;
-    {
-        uint32_t i = i0, j = j0;
-        bool has_prev = has_prev0;
-        float prev = prev0;
-        for (uint32_t k = k0; k < k1; k++) {
-            const bool ta = i < na && (j >= nb || a[i].v <= b[j].v);
-            const float v = ta ? a[i].v : b[j].v;
-            if (!has_prev || v != prev) starts++;
-            prev = v;
-            has_prev = true;
-            if (ta) i++;
-            else j++;
-        }
-    }
-    uint32_t n_out;
-    uint32_t o = sk_scan_sum(starts, buf, n_out);
-    // Pass 2: emit each run's entry; its partner (the other summary's entry
-    // of the same value, always the next output) is combined into it.
-    {
-        uint32_t i = i0, j = j0;
-        float pa = i0 > 0 ? a[i0 - 1].rmax : 0.0f;  // pass_a: rmax of a's last entry taken
-        float pb = j0 > 0 ? b[j0 - 1].rmax : 0.0f;
-        bool has_prev = has_prev0;
-        float prev = prev0;
-        for (uint32_t k = k0; k < k1; k++) {
-            const bool ta = i < na && (j >= nb || a[i].v <= b[j].v);
-            SkEntry x = ta ? sk_ld(a + i) : sk_ld(b + j);
-            const float sh = ta ? pb : pa;
-            const float xr = x.rmax;
-            x.rmin = x.rmin + sh;
-            x.rmax = x.rmax + sh;
-            if (ta) {
-                pa = xr;
-                i++;
-            } else {
-                pb = xr;
-                j++;
+    const uint32_t n_ch = (M + SK_MCH - 1) / SK_MCH;
+    uint32_t out = 0;  // entries written so far
+    for (uint32_t g0 = 0; g0 < n_ch; g0 += SK_MAX_CHUNKS) {
+        // Boundaries of chunks g0 .. g0 + SK_MAX_CHUNKS (a-entries before each).
+        const uint32_t gn = min(SK_MAX_CHUNKS, n_ch - g0);
+        for (uint32_t t = threadIdx.x; t <= gn; t += SK_TPB)
+            bound[t] = sk_merge_path(a, na, b, nb, min(M, (g0 + t) * SK_MCH));
+        __syncthreads();
+        for (uint32_t g = 0; g < gn; g++) {
+            const uint32_t c0 = (g0 + g) * SK_MCH, c1 = min(M, c0 + SK_MCH);
+            const uint32_t ia = bound[g], jb = c0 - ia, ia1 = bound[g + 1], jb1 = c1 - ia1;
+            // sa[x] = a[ia - 1 + x] for x in [0, ia1 - ia + 2), where present.
+            for (uint32_t x = threadIdx.x; x < ia1 - ia + 2; x += SK_TPB) {
+                const uint32_t i = ia + x;  // a[i - 1]
+                if (i >= 1 && i - 1 < na) sa[x] = sk_ld(a + i - 1);
             }
-            const bool start = !has_prev || x.v != prev;
-            prev = x.v;
-            has_prev = true;
-            if (!start) continue;
-            if (k + 1 < M) {
-                const bool ta2 = i < na && (j >= nb || a[i].v <= b[j].v);
-                const SkEntry y = ta2 ? sk_ld(a + i) : sk_ld(b + j);
-                if (y.v == x.v) {
-                    const float sh2 = ta2 ? pb : pa;
-                    x.w = x.w + y.w;
-                    x.rmin = fminf(x.rmin, y.rmin + sh2);
-                    x.rmax = fmaxf(x.rmax, y.rmax + sh2);
+            for (uint32_t x = threadIdx.x; x < jb1 - jb + 2; x += SK_TPB) {
+                const uint32_t j = jb + x;
+                if (j >= 1 && j - 1 < nb) sb[x] = sk_ld(b + j - 1);
+            }
+            __syncthreads();
+            // This thread's outputs [k0, k1) of the chunk.
+            const uint32_t len = c1 - c0, la = ia1 - ia, lb = jb1 - jb;
+            const uint32_t k0 = min(len, threadIdx.x * SK_MPT), k1 = min(len, k0 + SK_MPT);
+            uint32_t il;
+            {
+                uint32_t lo = k0 > lb ? k0 - lb : 0u, hi = min(k0, la);
+                while (lo < hi) {
+                    const uint32_t mid = (lo + hi) >> 1;
+                    if (sa[mid + 1].v <= sb[k0 - mid].v) lo = mid + 1;
+                    else hi = mid;
+                }
+                il = lo;
+            }
+            uint32_t i = ia + il, j = jb + (k0 - il);  // global positions
+#define SA(q) sa[(q) - ia + 1]
+#define SB(q) sb[(q) - jb + 1]
+            const uint32_t kk = c0 + k0;  // global output index
+            bool has_prev = kk > 0;
+            float prev = 0.0f;
+            if (has_prev) {
+                if (i == 0) prev = SB(j - 1).v;
+                else if (j == 0) prev = SA(i - 1).v;
+                else prev = fmaxf(SA(i - 1).v, SB(j - 1).v);
+            }
+            float pa = i > 0 ? SA(i - 1).rmax : 0.0f;  // pass_a: rmax of a's last entry taken
+            float pb = j > 0 ? SB(j - 1).rmax : 0.0f;
+            SkEntry e[SK_MPT];
+            uint32_t flags = 0;  // bit q: output k0 + q starts a run
+#pragma unroll
+            for (uint32_t q = 0; q < SK_MPT; q++) {
+                e[q] = SkEntry{};
+                if (k0 + q < k1) {
+                    const bool ta = i < na && (j >= nb || SA(i).v <= SB(j).v);
+                    SkEntry x = ta ? SA(i) : SB(j);
+                    const float sh = ta ? pb : pa;
+                    const float xr = x.rmax;
+                    x.rmin = x.rmin + sh;
+                    x.rmax = x.rmax + sh;
+                    if (ta) {
+                        pa = xr;
+                        i++;
+                    } else {
+                        pb = xr;
+                        j++;
+                    }
+                    const bool start = !has_prev || x.v != prev;
+                    prev = x.v;
+                    has_prev = true;
+                    // A run's partner (the other summary's entry of the same
+                    // value) is always the next output; staged, since
+                    // outputs up to c1 are.
+                    if (start && kk + q + 1 < M) {
+                        const bool ta2 = i < na && (j >= nb || SA(i).v <= SB(j).v);
+                        const SkEntry y = ta2 ? SA(i) : SB(j);
+                        if (y.v == x.v) {
+                            const float sh2 = ta2 ? pb : pa;
+                            x.w = x.w + y.w;
+                            x.rmin = fminf(x.rmin, y.rmin + sh2);
+                            x.rmax = fmaxf(x.rmax, y.rmax + sh2);
+                        }
+                    }
+                    e[q] = x;
+                    flags |= start ? 1u << q : 0u;
                 }
             }
-            sk_st(T.d + o, x);
-            o++;
+#undef SA
+#undef SB
+            uint32_t n_chunk;
+            const uint32_t o = out + sk_scan_sum((uint32_t)__popc(flags), buf, n_chunk);
+#pragma unroll
+            for (uint32_t q = 0; q < SK_MPT; q++)
+                if (flags >> q & 1u) sk_st(T.d + o + __popc(flags & ((1u << q) - 1u)), e[q]);
+            out += n_chunk;
+            __syncthreads();  // the staged entries are rewritten next
         }
     }
+    const uint32_t n_out = out;
     if (!prune || n_out <= limit) {
         if (threadIdx.x == 0) *T.nd = n_out;
         return;
@@ -503,10 +560,10 @@ __global__ __launch_bounds__(SK_TPB) void sk_merge_kernel(const SkMergeTask *__r
     sk_compress_plan<uint16_t>(T.d, n, slots, sel, ibuf);
     for (uint32_t base = 1; base < slots; base += SK_TPB) {
         const uint32_t k = base + threadIdx.x;
-        SkEntry e{};
-        if (k < slots) e = sk_ld(T.d + sel[k]);
+        SkEntry v{};
+        if (k < slots) v = sk_ld(T.d + sel[k]);
         __syncthreads();
-        if (k < slots) sk_st(T.d + k, e);
+        if (k < slots) sk_st(T.d + k, v);
         __syncthreads();
     }
     if (threadIdx.x == 0) {
@@ -970,6 +1027,7 @@ int fbh_sketch_cuts(fbh_sketch *s, float *cut_values, uint64_t values_capacity,
             sk_check(allow_lds(sk_sort_kernel), "LDS attribute");
             const uint32_t cut_lds = 4 * (uint32_t)L + 4 * max_bin;
             sk_check(allow_lds(sk_cuts_kernel), "LDS attribute");
+            sk_check(allow_lds(sk_merge_kernel), "LDS attribute");
             hipLaunchKernelGGL(sk_sort_kernel, dim3((uint32_t)sorts.size()), dim3(SK_TPB),
                                4 * Pk, s->stream, reinterpret_cast<const SkSortTask *>(tab + o_sort),
                                Pk);

@@ -8,7 +8,8 @@ The device reorganises FeatureSketch (src/data/sketch.rs:72-302) in two ways:
   first, and compresses once;
 * compress()'s greedy walk (:404-440) runs as a prefix maximum:
   taken_k = k + min(n - slots, max(0, max_{i<=k} (lb_i - i))), lb_k the first
-  index >= 1 whose rmid reaches target_k.
+  index >= 1 whose rmid reaches target_k, found from the entries' side (entry
+  i takes the k with c_{i-1} < k <= c_i, c_i the targets its rmid reaches).
 
 This file models both in f32 numpy arithmetic and checks, on small inputs
 with many batches, that they give the host sketch's cuts bit for bit (the
@@ -124,13 +125,51 @@ def _compress_prefix(s, cap):
     return out
 
 
+def _compress_scatter(s, cap):
+    """The device's compress: lb from the entries' side (entry i takes the
+    targets k in (c_{i-1}, c_i], c_i = the targets its rmid reaches), then
+    the prefix maximum."""
+    n = len(s)
+    if n <= cap:
+        return s
+    total = s[-1][3]
+    slots = cap - 1
+
+    def target(k):
+        return f32(f32(total * f32(k)) / f32(slots))
+
+    def upto(m):
+        k = min(max(int(float(m) * slots / float(total)), 0), slots - 1)
+        while k + 1 <= slots - 1 and target(k + 1) <= m:
+            k += 1
+        while k >= 1 and target(k) > m:
+            k -= 1
+        return k
+
+    lb = [n - 1] * slots
+    for i in range(1, n - 1):
+        lo = 0 if i == 1 else upto(_mid(s[i - 1]))
+        for k in range(lo + 1, upto(_mid(s[i])) + 1):
+            lb[k] = i
+    out = [s[0]]
+    run = -(1 << 30)
+    taken = 0
+    for k in range(1, slots):
+        run = max(run, lb[k] - k)
+        taken = k + min(n - slots, max(0, run))
+        out.append(s[taken])
+    if taken < n - 1:
+        out.append(s[-1])
+    return out
+
+
 def _midpoint(a, b):
     d = f32(b - a)
     m = f32(a + f32(d * f32(0.5))) if np.isfinite(d) else f32(f32(a * f32(0.5)) + f32(b * f32(0.5)))
     return b if m <= a else m
 
 
-def _device_cuts(col, max_bin, compress=_compress_prefix):
+def _device_cuts(col, max_bin, compress=_compress_scatter):
     """The device's schedule for one numeric feature (unit weights)."""
     n_cuts = max_bin - 1
     if n_cuts <= 0:
@@ -222,6 +261,8 @@ def test_prefix_compress_equals_the_walk_on_sketch_summaries():
                 checked += 1
             w = _compress_walk(m, cap)
             p = _compress_prefix(m, cap)
+            q = _compress_scatter(m, cap)
             assert [list(map(float, e)) for e in w] == [list(map(float, e)) for e in p], trial
+            assert [list(map(float, e)) for e in w] == [list(map(float, e)) for e in q], trial
             a, b = w, _summary((np.round(rng.standard_normal(cap) * 9) + 0.0).astype(np.float32))
     assert checked > 20
