@@ -411,6 +411,162 @@ __global__ __launch_bounds__(SHAP_TPB) void shap_kernel(
     }
 }
 
+// The same QuadratureTreeSHAP contributions for trees of at most SHAP_REC_D
+// split levels, with the path stack in registers. Every row of a wave visits
+// the same nodes in the same order (both children of every split, in
+// order), so the recursion below unrolls into straight code over the frames
+// (frame D's coefficients, left-subtree return and path entry are locals of
+// shap_visit<D>), node loads are uniform across the wave, and only the
+// tree's per-feature sums (tc, indexed by the node's unique slot) stay in
+// memory. The float operations and their order are shap_kernel's, so the
+// results are identical.
+constexpr int SHAP_REC_D = 8;
+
+struct ShapPath {
+    uint32_t feat[SHAP_REC_D];
+    float pe[SHAP_REC_D];
+};
+
+struct ShapRowCtx {
+    const float *x;
+    float rn[QP], rw[QP];
+};
+
+// A wave-uniform value in a scalar register (every active lane holds it).
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float uni(float v) {
+    return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(v)));
+}
+
+// Visits internal node `nid` at frame D whose incoming coefficients are c
+// and path weight wprod; adds the frame's return (left + right subtree) to
+// ret, which the caller zeroed.
+template <int D>
+__device__ __forceinline__ void shap_visit(const ShapNodeDev *__restrict__ nodes,
+                                           const uint32_t *__restrict__ cat_words,
+                                           const ShapRowCtx &R, uint32_t nid,
+                                           const float (&c)[QP], float wprod, ShapPath &P,
+                                           float *tc, float (&ret)[QP]) {
+    const ShapNodeDev &n = nodes[nid];
+    const uint32_t feat = uni(n.feat);
+    const bool gl = shap_goes_left(n, R.x[feat], cat_words);
+    float p_old = UNSEEN;  // the newest occurrence of feat on the path above
+#pragma unroll
+    for (int k = 0; k < D; k++)
+        if (P.feat[k] == feat) p_old = P.pe[k];
+    const uint32_t uslot = uni(n.uslot);
+    for (int side = 0; side < 2; side++) {
+        const bool right = side != 0;
+        const uint32_t child = uni((uint32_t)(right ? n.right : n.left));
+        const float cw = uni(right ? n.right_weight : n.left_weight);
+        const bool sat = right ? !gl : gl;
+        const float p_e = sat ? (p_old == UNSEEN ? 1.0f / cw : p_old / cw) : 0.0f;
+        float cc[QP];
+        const float ae = p_e - 1.0f;
+#pragma unroll
+        for (int i = 0; i < QP; i++) {
+            const float m = 1.0f + ae * R.rn[i];
+            cc[i] = c[i] * m;
+        }
+        if (p_old != UNSEEN) {
+            const float ao = p_old - 1.0f;
+            if (ao != 0.0f) {
+#pragma unroll
+                for (int i = 0; i < QP; i++) cc[i] /= 1.0f + ao * R.rn[i];
+            }
+        }
+        P.feat[D] = feat;
+        P.pe[D] = p_e;
+        const float wchild = wprod * cw;
+        const uint32_t cflags = uni(nodes[child].flags);
+        float r[QP];
+        if (!(cflags & 1u)) {
+#pragma unroll
+            for (int i = 0; i < QP; i++) r[i] = 0.0f;
+            if constexpr (D + 1 < SHAP_REC_D)
+                shap_visit<D + 1>(nodes, cat_words, R, child, cc, wchild, P, tc, r);
+        } else {
+            const float ls = wchild * uni(nodes[child].leaf_value);
+#pragma unroll
+            for (int i = 0; i < QP; i++) {
+                const float a = cc[i] * ls;
+                r[i] = a * R.rw[i];
+            }
+        }
+        // extract_delta (explain.rs:202-217) for this visit of frame D. The
+        // empty asm keeps the denominators (functions of p_e and p_old alone)
+        // from being computed before the subtree and held across it.
+        float pe_x = p_e, po_x = p_old;
+        asm volatile("" : "+v"(pe_x), "+v"(po_x));
+        const float px = po_x == UNSEEN ? 1.0f : po_x;
+        float acc = 0.0f;
+        if (pe_x != 1.0f) {
+            const float a = pe_x - 1.0f;
+#pragma unroll
+            for (int i = 0; i < QP; i++) {
+                const float num = a * r[i];
+                const float den = 1.0f + a * R.rn[i];
+                acc += num / den;
+            }
+        }
+        if (px != 1.0f) {
+            const float a = px - 1.0f;
+#pragma unroll
+            for (int i = 0; i < QP; i++) {
+                const float num = a * r[i];
+                const float den = 1.0f + a * R.rn[i];
+                acc -= num / den;
+            }
+        }
+        tc[uslot] += acc;
+        // The frame's return: the left subtree's, then + the right subtree's
+        // (0 + x == x for every x but -0, and a subtree return is never the
+        // left operand of anything else).
+#pragma unroll
+        for (int i = 0; i < QP; i++) ret[i] = right ? ret[i] + r[i] : r[i];
+    }
+}
+
+template <int MAXU>
+__global__ __launch_bounds__(SHAP_TPB) void shap_rec_kernel(
+    const ShapNodeDev *__restrict__ nodes, const uint32_t *__restrict__ tree_roots,
+    uint32_t n_trees, const uint32_t *__restrict__ tree_ufeat_off,
+    const uint32_t *__restrict__ ufeats, const uint32_t *__restrict__ cat_words,
+    const float *__restrict__ rule, const float *__restrict__ rows, uint64_t n_rows,
+    uint32_t n_features, const float *__restrict__ margin, float bias, float root_mean,
+    float *__restrict__ out) {
+    const uint64_t row = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= n_rows) return;
+    ShapRowCtx R;
+    R.x = rows + row * n_features;
+#pragma unroll
+    for (int i = 0; i < QP; i++) {
+        R.rn[i] = rule[i];
+        R.rw[i] = rule[QP + i];
+    }
+    const uint32_t nc = n_features + 1;
+    float *p = out + row * (uint64_t)nc;
+    for (uint32_t f = 0; f <= n_features; f++) p[f] = 0.0f;
+    float tc[MAXU];
+    ShapPath P;
+    for (uint32_t t = 0; t < n_trees; t++) {
+        const uint32_t root = tree_roots[t];
+        const uint32_t u0 = tree_ufeat_off[t], nu = tree_ufeat_off[t + 1] - u0;
+        if (nodes[root].flags & 1u) continue;  // a leaf-only tree contributes nothing
+        for (uint32_t u = 0; u < nu; u++) tc[u] = 0.0f;
+        float c0[QP], ret[QP];
+#pragma unroll
+        for (int i = 0; i < QP; i++) {
+            c0[i] = 1.0f;
+            ret[i] = 0.0f;
+        }
+        shap_visit<0>(nodes, cat_words, R, uni(root), c0, 1.0f, P, tc, ret);
+        for (uint32_t u = 0; u < nu; u++) p[ufeats[u0 + u]] += tc[u];
+    }
+    p[n_features] += root_mean;
+    p[n_features] += margin ? margin[row] : bias;
+}
+
 // ====================================================================== host
 
 struct ShapError : std::runtime_error {
@@ -560,6 +716,19 @@ hipError_t launch_shap(const fbh_shap_model *m, bool inter, const float *rows, u
                            out);
         return hipGetLastError();
     }
+#define FBH_SHAP_REC_CASE(U)                                                                     \
+    if (m->max_unique <= U) {                                                                    \
+        hipLaunchKernelGGL((shap_rec_kernel<U>), dim3(blocks), dim3(SHAP_TPB), 0, m->stream,      \
+                           m->d_nodes, m->d_roots, m->n_trees, m->d_uoff, m->d_ufeats,          \
+                           m->d_cats, m->d_rule, rows, n_rows, m->n_features, margin, m->bias,  \
+                           m->root_mean, out);                                                   \
+        return hipGetLastError();                                                               \
+    }
+    if (m->max_depth <= SHAP_REC_D) {
+        FBH_SHAP_REC_CASE(32) FBH_SHAP_REC_CASE(64) FBH_SHAP_REC_CASE(128) FBH_SHAP_REC_CASE(256)
+        FBH_SHAP_REC_CASE(1024)
+    }
+#undef FBH_SHAP_REC_CASE
 #define FBH_SHAP_CASE(U)                                                                         \
     if (m->max_unique <= U) {                                                                    \
         hipLaunchKernelGGL((shap_kernel<U, false>), dim3(blocks), dim3(SHAP_TPB), 0, m->stream,   \
