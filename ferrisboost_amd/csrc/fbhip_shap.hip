@@ -427,9 +427,26 @@ struct ShapPath {
     float pe[SHAP_REC_D];
 };
 
+// A tree of at most SHAP_REC_D split levels has at most 2^(SHAP_REC_D + 1) - 1
+// nodes: one go-left bit each, in words of 32 per lane.
+constexpr int SHAP_REC_NODES = 1 << (SHAP_REC_D + 1);
+constexpr int SHAP_GL_WORDS = SHAP_REC_NODES / 32;
+
+// What the recursion reads of a node, 16 bytes, staged in LDS per tree:
+// meta = left (9 bits) | right << 9 (9 bits) | unique slot << 18 (10 bits) |
+// leaf << 31, children as tree-local ids; w0 the left branch weight (a
+// leaf: its value), w1 the right branch weight.
+struct RecNodeDev {
+    uint32_t feat;
+    uint32_t meta;
+    float w0, w1;
+};
+constexpr uint32_t REC_LEAF = 1u << 31;
+
 struct ShapRowCtx {
-    const float *x;
     float rn[QP], rw[QP];
+    const RecNodeDev *tn;            // LDS: the tree's nodes, tree-local ids
+    const uint32_t (*gl)[SHAP_TPB];  // LDS: go-left bit of node i in word i / 32
 };
 
 // A wave-uniform value in a scalar register (every active lane holds it).
@@ -438,27 +455,25 @@ __device__ __forceinline__ float uni(float v) {
     return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(v)));
 }
 
-// Visits internal node `nid` at frame D whose incoming coefficients are c
-// and path weight wprod; adds the frame's return (left + right subtree) to
-// ret, which the caller zeroed.
+// Visits internal node `li` (tree-local) at frame D whose incoming
+// coefficients are c and path weight wprod; writes the frame's return (left
+// + right subtree) to ret.
 template <int D>
-__device__ __forceinline__ void shap_visit(const ShapNodeDev *__restrict__ nodes,
-                                           const uint32_t *__restrict__ cat_words,
-                                           const ShapRowCtx &R, uint32_t nid,
+__device__ __forceinline__ void shap_visit(const ShapRowCtx &R, uint32_t li,
                                            const float (&c)[QP], float wprod, ShapPath &P,
                                            float *tc, float (&ret)[QP]) {
-    const ShapNodeDev &n = nodes[nid];
-    const uint32_t feat = uni(n.feat);
-    const bool gl = shap_goes_left(n, R.x[feat], cat_words);
+    const RecNodeDev n = R.tn[li];
+    const uint32_t feat = uni(n.feat), meta = uni(n.meta);
+    const bool gl = (R.gl[li >> 5][threadIdx.x] >> (li & 31)) & 1u;
     float p_old = UNSEEN;  // the newest occurrence of feat on the path above
 #pragma unroll
     for (int k = 0; k < D; k++)
         if (P.feat[k] == feat) p_old = P.pe[k];
-    const uint32_t uslot = uni(n.uslot);
+    const uint32_t uslot = (meta >> 18) & 1023u;
     for (int side = 0; side < 2; side++) {
         const bool right = side != 0;
-        const uint32_t child = uni((uint32_t)(right ? n.right : n.left));
-        const float cw = uni(right ? n.right_weight : n.left_weight);
+        const uint32_t child = right ? (meta >> 9) & 511u : meta & 511u;
+        const float cw = uni(right ? n.w1 : n.w0);
         const bool sat = right ? !gl : gl;
         const float p_e = sat ? (p_old == UNSEEN ? 1.0f / cw : p_old / cw) : 0.0f;
         float cc[QP];
@@ -478,15 +493,15 @@ __device__ __forceinline__ void shap_visit(const ShapNodeDev *__restrict__ nodes
         P.feat[D] = feat;
         P.pe[D] = p_e;
         const float wchild = wprod * cw;
-        const uint32_t cflags = uni(nodes[child].flags);
+        const RecNodeDev cn = R.tn[child];
         float r[QP];
-        if (!(cflags & 1u)) {
+        if (!(uni(cn.meta) & REC_LEAF)) {
 #pragma unroll
             for (int i = 0; i < QP; i++) r[i] = 0.0f;
             if constexpr (D + 1 < SHAP_REC_D)
-                shap_visit<D + 1>(nodes, cat_words, R, child, cc, wchild, P, tc, r);
+                shap_visit<D + 1>(R, child, cc, wchild, P, tc, r);
         } else {
-            const float ls = wchild * uni(nodes[child].leaf_value);
+            const float ls = wchild * uni(cn.w0);
 #pragma unroll
             for (int i = 0; i < QP; i++) {
                 const float a = cc[i] * ls;
@@ -527,18 +542,55 @@ __device__ __forceinline__ void shap_visit(const ShapNodeDev *__restrict__ nodes
     }
 }
 
+// The row's go-left bits of every node of the tree in [root, end) (leaves
+// 0), 32 nodes at a time with their loads issued together, so the recursion
+// reads no row data. Node fields are wave-uniform.
+__device__ __forceinline__ void shap_gl_bits(const ShapNodeDev *__restrict__ nodes,
+                                             const uint32_t *__restrict__ cat_words,
+                                             const float *x, uint32_t root, uint32_t end,
+                                             uint32_t (*gl)[SHAP_TPB]) {
+    for (uint32_t w = 0; root + 32 * w < end; w++) {
+        const uint32_t b = root + 32 * w;
+        float v[32];
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            const uint32_t id = min(b + j, end - 1);
+            const uint32_t fl = uni(nodes[id].flags);
+            const uint32_t f = (fl & 1u) ? 0u : uni(nodes[id].feat);
+            v[j] = x[f];
+        }
+        uint32_t bits = 0;
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            const uint32_t id = min(b + j, end - 1);
+            const ShapNodeDev &n = nodes[id];
+            if (b + j < end && !(uni(n.flags) & 1u) && shap_goes_left(n, v[j], cat_words))
+                bits |= 1u << j;
+        }
+        gl[w][threadIdx.x] = bits;
+    }
+}
+
 template <int MAXU>
 __global__ __launch_bounds__(SHAP_TPB) void shap_rec_kernel(
-    const ShapNodeDev *__restrict__ nodes, const uint32_t *__restrict__ tree_roots,
-    uint32_t n_trees, const uint32_t *__restrict__ tree_ufeat_off,
+    const ShapNodeDev *__restrict__ nodes, const RecNodeDev *__restrict__ rec,
+    const uint32_t *__restrict__ tree_roots,
+    uint32_t n_trees, uint32_t n_nodes, const uint32_t *__restrict__ tree_ufeat_off,
     const uint32_t *__restrict__ ufeats, const uint32_t *__restrict__ cat_words,
     const float *__restrict__ rule, const float *__restrict__ rows, uint64_t n_rows,
     uint32_t n_features, const float *__restrict__ margin, float bias, float root_mean,
     float *__restrict__ out) {
-    const uint64_t row = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (row >= n_rows) return;
+    __shared__ uint32_t glw[SHAP_GL_WORDS][SHAP_TPB];
+    __shared__ RecNodeDev tn[SHAP_REC_NODES];
+    // Every thread takes part in the per-tree staging (barriers); a thread
+    // past the last row computes on the last row and writes nothing.
+    const uint64_t row0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool active = row0 < n_rows;
+    const uint64_t row = active ? row0 : n_rows - 1;
+    const float *x = rows + row * n_features;
     ShapRowCtx R;
-    R.x = rows + row * n_features;
+    R.tn = tn;
+    R.gl = glw;
 #pragma unroll
     for (int i = 0; i < QP; i++) {
         R.rn[i] = rule[i];
@@ -546,23 +598,28 @@ __global__ __launch_bounds__(SHAP_TPB) void shap_rec_kernel(
     }
     const uint32_t nc = n_features + 1;
     float *p = out + row * (uint64_t)nc;
-    for (uint32_t f = 0; f <= n_features; f++) p[f] = 0.0f;
+    if (active)
+        for (uint32_t f = 0; f <= n_features; f++) p[f] = 0.0f;
     float tc[MAXU];
     ShapPath P;
     for (uint32_t t = 0; t < n_trees; t++) {
-        const uint32_t root = tree_roots[t];
-        const uint32_t u0 = tree_ufeat_off[t], nu = tree_ufeat_off[t + 1] - u0;
+        const uint32_t root = uni(tree_roots[t]);
+        const uint32_t end = t + 1 < n_trees ? tree_roots[t + 1] : n_nodes;
         if (nodes[root].flags & 1u) continue;  // a leaf-only tree contributes nothing
+        const uint32_t u0 = tree_ufeat_off[t], nu = tree_ufeat_off[t + 1] - u0;
+        __syncthreads();  // every wave is done with the previous tree's nodes
+        for (uint32_t i = threadIdx.x; i < end - root; i += SHAP_TPB) tn[i] = rec[root + i];
         for (uint32_t u = 0; u < nu; u++) tc[u] = 0.0f;
+        shap_gl_bits(nodes, cat_words, x, root, end, glw);
+        __syncthreads();
         float c0[QP], ret[QP];
 #pragma unroll
-        for (int i = 0; i < QP; i++) {
-            c0[i] = 1.0f;
-            ret[i] = 0.0f;
-        }
-        shap_visit<0>(nodes, cat_words, R, uni(root), c0, 1.0f, P, tc, ret);
-        for (uint32_t u = 0; u < nu; u++) p[ufeats[u0 + u]] += tc[u];
+        for (int i = 0; i < QP; i++) c0[i] = 1.0f;
+        shap_visit<0>(R, 0u, c0, 1.0f, P, tc, ret);
+        if (active)
+            for (uint32_t u = 0; u < nu; u++) p[ufeats[u0 + u]] += tc[u];
     }
+    if (!active) return;
     p[n_features] += root_mean;
     p[n_features] += margin ? margin[row] : bias;
 }
@@ -624,10 +681,12 @@ float branch_weight(float cover, float parent) {
 struct fbh_shap_model {
     int device = 0;
     hipStream_t stream = nullptr;
-    uint32_t n_trees = 0, n_features = 0, max_unique = 1, max_depth = 1;
+    uint32_t n_trees = 0, n_features = 0, max_unique = 1, max_depth = 1, n_nodes = 0;
+    uint32_t max_tree_nodes = 0;
     float bias = 0.0f, root_mean = 0.0f;
     std::string cover_error;  // non-empty: TreeSHAP is undefined for this model
     ShapNodeDev *d_nodes = nullptr;
+    RecNodeDev *d_rec = nullptr;
     PredNodeDev *d_pred = nullptr;
     float *d_means = nullptr;
     uint32_t *d_roots = nullptr, *d_uoff = nullptr, *d_ufeats = nullptr, *d_cats = nullptr;
@@ -719,12 +778,13 @@ hipError_t launch_shap(const fbh_shap_model *m, bool inter, const float *rows, u
 #define FBH_SHAP_REC_CASE(U)                                                                     \
     if (m->max_unique <= U) {                                                                    \
         hipLaunchKernelGGL((shap_rec_kernel<U>), dim3(blocks), dim3(SHAP_TPB), 0, m->stream,      \
-                           m->d_nodes, m->d_roots, m->n_trees, m->d_uoff, m->d_ufeats,          \
+                           m->d_nodes, m->d_rec, m->d_roots, m->n_trees, m->n_nodes, m->d_uoff, \
+                           m->d_ufeats,                                                          \
                            m->d_cats, m->d_rule, rows, n_rows, m->n_features, margin, m->bias,  \
                            m->root_mean, out);                                                   \
         return hipGetLastError();                                                               \
     }
-    if (m->max_depth <= SHAP_REC_D) {
+    if (m->max_depth <= SHAP_REC_D && m->max_tree_nodes <= (uint32_t)SHAP_REC_NODES) {
         FBH_SHAP_REC_CASE(32) FBH_SHAP_REC_CASE(64) FBH_SHAP_REC_CASE(128) FBH_SHAP_REC_CASE(256)
         FBH_SHAP_REC_CASE(1024)
     }
@@ -906,6 +966,7 @@ int fbh_shap_model_create(int device, uint32_t n_trees, const uint32_t *tree_off
         std::vector<float> lv(leaf_value, leaf_value + total), hs(sum_hess, sum_hess + total);
         std::vector<uint8_t> lf(is_leaf, is_leaf + total);
         std::vector<ShapNodeDev> nodes(total);
+        std::vector<RecNodeDev> rec(total);
         std::vector<PredNodeDev> pred(total);
         std::vector<float> means(total, 0.0f);
         std::vector<uint32_t> roots(n_trees), uoff(n_trees + 1, 0), ufeats;
@@ -913,6 +974,7 @@ int fbh_shap_model_create(int device, uint32_t n_trees, const uint32_t *tree_off
         for (uint32_t t = 0; t < n_trees; t++) {
             const uint32_t b = tree_offsets[t], e = tree_offsets[t + 1];
             if (e <= b) throw ShapError(FBH_INPUT_ERROR, "tree " + std::to_string(t) + " has no nodes");
+            m->max_tree_nodes = std::max(m->max_tree_nodes, e - b);
             roots[t] = b;
             std::vector<int32_t> slot_of(n_features, -1);
             uoff[t] = (uint32_t)ufeats.size();
@@ -967,6 +1029,18 @@ int fbh_shap_model_create(int device, uint32_t n_trees, const uint32_t *tree_off
                     m->max_depth = std::max(m->max_depth, depth[i - b] + 1);
                 }
                 nodes[i] = d;
+                RecNodeDev &q = rec[i];
+                q.feat = d.feat;
+                if (is_leaf[i]) {
+                    q.meta = REC_LEAF;
+                    q.w0 = d.leaf_value;
+                } else {  // packed only where the tree fits (max_tree_nodes)
+                    q.meta = ((uint32_t)(d.left - (int32_t)b) & 511u) |
+                             (((uint32_t)(d.right - (int32_t)b) & 511u) << 9) |
+                             ((d.uslot & 1023u) << 18);
+                    q.w0 = d.left_weight;
+                    q.w1 = d.right_weight;
+                }
             }
             m->max_unique = std::max<uint32_t>(m->max_unique, (uint32_t)ufeats.size() - uoff[t]);
             if (m->max_unique > MAX_SHAP_UNIQUE)
@@ -984,9 +1058,11 @@ int fbh_shap_model_create(int device, uint32_t n_trees, const uint32_t *tree_off
                                  cat_words ? cat_words + n_cat_words : nullptr);
         m->n_trees = n_trees;
         m->n_features = n_features;
+        m->n_nodes = total;
         m->bias = bias;
         m->root_mean = (float)rm_sum;
         m->d_nodes = m->upload(nodes, "shap nodes");
+        m->d_rec = m->upload(rec, "shap node records");
         m->d_pred = m->upload(pred, "walk nodes");
         m->d_means = m->upload(means, "node means");
         m->d_roots = m->upload(roots, "shap roots");
