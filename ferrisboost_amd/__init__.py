@@ -33,6 +33,7 @@ __version__ = "0.1.0"
 # Canonical name -> default, as python/ferrisboost/__init__.py:_DEFAULTS.
 _DEFAULTS: dict[str, Any] = {
     "objective": "binary:logistic",
+    "num_class": None,
     "max_depth": 6,
     "max_leaves": 0,
     "grow_policy": "depthwise",
@@ -88,7 +89,9 @@ _ALIASES = {
     "random_state": "seed",
 }
 
-_OBJECTIVES = {"reg:squarederror": 0, "binary:logistic": 1}
+_OBJECTIVES = {"reg:squarederror": 0, "binary:logistic": 1, "multi:softprob": 2,
+               "multi:softmax": 3}
+_OBJECTIVE_NAMES = {v: k for k, v in _OBJECTIVES.items()}
 _GROW = {"depthwise": 0, "lossguide": 1}
 
 _UNIMPLEMENTED = {
@@ -136,6 +139,16 @@ def _normalize(params: Mapping[str, Any], num_boost_round: int) -> dict[str, Any
             f"objective {out['objective']!r} is not available on the ferrisboost_amd device path; "
             f"supported: {', '.join(_OBJECTIVES)}"
         )
+    # num_class (python/ferrisboost/__init__.py:281-286): an integer, not negative;
+    # the multiclass objectives need at least 2.
+    if out["num_class"] is not None:
+        if isinstance(out["num_class"], bool) or int(out["num_class"]) != out["num_class"]:
+            raise ValueError(f"num_class must be an integer, got {out['num_class']!r}")
+        out["num_class"] = int(out["num_class"])
+        if out["num_class"] < 0:
+            raise ValueError("num_class must not be negative")
+    if str(out["objective"]).startswith("multi:") and (out["num_class"] or 0) < 2:
+        raise ValueError(f"{out['objective']} requires num_class >= 2, got {out['num_class']}")
     if out["grow_policy"] not in _GROW:
         raise ValueError(f"grow_policy must be depthwise or lossguide, got {out['grow_policy']!r}")
     if not 0 < int(out["max_bin"]) <= 65535:
@@ -203,6 +216,7 @@ def _params_struct(p: dict[str, Any], n_features: int) -> N.TrainParams:
     s.cols_per_block = int(cpb) if cpb else max(n_features, 1)
     s.seed = int(p["seed"]) & 0xFFFFFFFFFFFFFFFF
     s.objective = _OBJECTIVES[p["objective"]]
+    s.num_class = int(p["num_class"] or 0) if p["objective"].startswith("multi:") else 0
     s.grow_policy = _GROW[p["grow_policy"]]
     s.max_cat_to_onehot = int(p["max_cat_to_onehot"])
     s.max_cat_threshold = int(p["max_cat_threshold"])
@@ -278,7 +292,16 @@ class Model:
 
     @property
     def num_class(self) -> int:
-        return 1
+        """Outputs per row: num_class of a multiclass model, else 1."""
+        return N.train_lib().fbt_model_num_outputs(self._h)
+
+    def class_margins(self) -> np.ndarray:
+        """A multiclass model's per-class intercepts (empty otherwise)."""
+        k = self.num_class
+        out = np.zeros(k if k > 1 else 0, np.float32)
+        if k > 1:
+            N.train_lib().fbt_model_class_margins(self._h, N.ptr(out))
+        return out
 
     @property
     def feature_names(self) -> list[str]:
@@ -336,7 +359,10 @@ class Model:
         return vals, offs
 
     def train_margins(self, n_rows: int) -> np.ndarray:
-        out = np.zeros(n_rows, np.float32)
+        """Training margins: (n,), or class-major (num_class, n) for a
+        multiclass model."""
+        k = self.num_class
+        out = np.zeros((k, n_rows) if k > 1 else n_rows, np.float32)
         N.check_train(N.train_lib().fbt_model_train_margins(self._h, N.ptr(out), n_rows))
         return out
 
@@ -347,15 +373,18 @@ class Model:
             if n_trees is not None:
                 raise ValueError("iteration_range and n_trees cannot both be given: the former "
                                  "counts rounds, the latter counts trees")
+            # Rounds: num_class trees each (Model::slice_rounds, src/model/tree.rs:428-455).
+            k = self.num_class
+            rounds = total // k
             begin, end = (int(v) for v in iteration_range)
             if begin < 0 or end < 0:
                 raise ValueError("iteration_range bounds must be non-negative")
-            end = total if end == 0 else end
-            if end > total:
-                raise ValueError(f"iteration_range end = {end} exceeds the model's {total} rounds")
+            end = rounds if end == 0 else end
+            if end > rounds:
+                raise ValueError(f"iteration_range end = {end} exceeds the model's {rounds} rounds")
             if begin > end:
                 raise ValueError(f"iteration_range begin = {begin} is greater than end = {end}")
-            return begin, end
+            return begin * k, end * k
         if n_trees is None:
             return 0, total
         if int(n_trees) < 0:
@@ -408,23 +437,36 @@ class Model:
         if not np.isnan(miss):
             X = np.where(X == np.float32(miss), np.float32("nan"), X).astype(np.float32)
         n = X.shape[0]
+        k = self.num_class
         bm = None
         if base_margin is not None:
-            bm = np.ascontiguousarray(np.asarray(base_margin, dtype=np.float32).reshape(-1))
-            if bm.shape != (n,):
-                raise ValueError(f"base_margin has {bm.size} values, expected {n} rows x 1 outputs")
+            bm = np.asarray(base_margin, dtype=np.float32)
+            if k > 1:
+                # (n, num_class) rows; the backend takes it class-major.
+                if bm.shape != (n, k):
+                    raise ValueError(f"base_margin must have shape ({n}, {k}), got {bm.shape}")
+                bm = np.ascontiguousarray(bm.T)
+            else:
+                bm = np.ascontiguousarray(bm.reshape(-1))
+                if bm.shape != (n,):
+                    raise ValueError(f"base_margin has {bm.size} values, expected {n} rows x 1 "
+                                     "outputs")
         b, e = self._tree_range(n_trees, iteration_range)
         dev = _parse_device(device) if device is not None else self._device
+        groups = (k,) if k > 1 else ()
         if pred_leaf:
             kind, shape = N.OUT_LEAF, (n, e - b)
         elif pred_interactions:
-            kind, shape = N.OUT_INTERACTIONS, (n, self.n_features + 1, self.n_features + 1)
+            kind = N.OUT_INTERACTIONS
+            shape = (n,) + groups + (self.n_features + 1, self.n_features + 1)
         elif pred_contribs:
             kind = N.OUT_APPROX if approx_contribs else N.OUT_CONTRIBS
-            shape = (n, self.n_features + 1)
+            shape = (n,) + groups + (self.n_features + 1,)
         else:
             kind = N.OUT_MARGIN if output_margin else N.OUT_VALUE
-            shape = (n,)
+            # multi:softmax's values are class indices, one per row
+            shape = (n,) if (not output_margin and self.objective == "multi:softmax") else (
+                (n,) + groups)
             if not use_gpu:
                 dev = -1
         out = np.zeros(shape, np.float32)
@@ -432,8 +474,8 @@ class Model:
                                                 N.ptr(bm), dev, N.ptr(out)))
         if strict_shape:
             if pred_leaf:
-                out = out.reshape(n, e - b, 1, 1)
-            else:
+                out = out.reshape(n, (e - b) // k, k, 1)
+            elif k == 1 or out.ndim == 1:
                 out = out.reshape((n, 1) + out.shape[1:])
         return out
 
@@ -495,7 +537,7 @@ class Model:
         L = N.train_lib()
         h = C.c_void_p()
         N.check_train(L.fbt_model_from_json(raw, len(raw), C.byref(h)))
-        obj = {0: "reg:squarederror", 1: "binary:logistic"}[L.fbt_model_objective(h)]
+        obj = _OBJECTIVE_NAMES[L.fbt_model_objective(h)]
         return Model(h, L.fbt_model_n_features(h), obj, _parse_device(device))
 
 

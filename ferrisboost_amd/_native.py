@@ -52,7 +52,8 @@ class Config(C.Structure):
         ("max_cat_words", C.c_uint32),
         ("stream_windows", C.c_uint32),
         ("resident_limit", C.c_uint32),
-        ("reserved", C.c_uint32 * 4),
+        ("n_outputs", C.c_uint32),
+        ("reserved", C.c_uint32 * 3),
     ]
 
 
@@ -146,7 +147,7 @@ class TrainParams(C.Structure):
         ("base_score", C.c_float),
         ("has_base_score", C.c_uint32),
         ("nthread", C.c_uint32),
-        ("reserved", C.c_uint32),
+        ("num_class", C.c_uint32),
         ("device", C.c_int32),
         ("gpu_math", C.c_uint32),
         ("gpu_memory_budget", C.c_uint64),
@@ -213,7 +214,8 @@ HIP_SYMBOLS = [
     "fbh_upload_rows", "fbh_finish_rows", "fbh_sketch_device_bytes", "fbh_sketch_fits",
     "fbh_sketch_create", "fbh_sketch_push_rows", "fbh_sketch_cuts", "fbh_sketch_destroy",
     "fbh_upload_quantize_gpair",
-    "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_gradient_exchange",
+    "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_set_multiclass",
+    "fbh_multiclass_begin_round", "fbh_set_output", "fbh_gradient_exchange",
     "fbh_download_margin", "fbh_set_gpu_math", "fbh_gradient_pairs", "fbh_sigmoid_host", "fbh_sigmoid_device", "fbh_sigmoid_checksum",
     "fbh_begin_tree", "fbh_eval_nodes", "fbh_download_histogram",
     "fbh_partition", "fbh_partition_eval", "fbh_grow_depthwise", "fbh_grow_depthwise_async",
@@ -231,6 +233,7 @@ TRAIN_SYMBOLS = [
     "fbt_model_train_margins", "fbt_model_n_cuts", "fbt_model_cuts", "fbt_predict_margin",
     "fbt_model_to_json", "fbt_shap", "fbt_last_shap_ms", "fbt_sketch_cuts", "fbt_predict",
     "fbt_model_from_json", "fbt_model_objective", "fbt_model_scale_pos_weight",
+    "fbt_model_num_outputs", "fbt_model_class_margins",
     "fbt_model_is_categorical",
 ]
 
@@ -290,6 +293,9 @@ def hip() -> C.CDLL:
         L.fbh_upload_quantize_gpair.argtypes = [P, P, C.c_uint64, C.c_uint64, C.c_uint64, P, P]
         L.fbh_upload_gpair_fixed.argtypes = [P, P, P]
         L.fbh_set_objective.argtypes = [P, C.c_uint32, P, P, C.c_float]
+        L.fbh_set_multiclass.argtypes = [P, C.c_uint32, P, P, P]
+        L.fbh_multiclass_begin_round.argtypes = [P]
+        L.fbh_set_output.argtypes = [P, C.c_uint32]
         L.fbh_gradient_exchange.argtypes = [P, P, P, C.c_uint64, C.c_uint64, C.c_uint64, P, P]
         L.fbh_download_margin.argtypes = [P, P]
         L.fbh_set_gpu_math.argtypes = [P, C.c_uint32]
@@ -377,6 +383,10 @@ def train_lib() -> C.CDLL:
         L.fbt_model_from_json.argtypes = [C.c_char_p, C.c_size_t, C.POINTER(P)]
         L.fbt_model_objective.argtypes = [P]
         L.fbt_model_objective.restype = C.c_uint32
+        L.fbt_model_num_outputs.argtypes = [P]
+        L.fbt_model_num_outputs.restype = C.c_uint32
+        L.fbt_model_class_margins.argtypes = [P, P]
+        L.fbt_model_class_margins.restype = None
         L.fbt_model_scale_pos_weight.argtypes = [P]
         L.fbt_model_scale_pos_weight.restype = C.c_float
         L.fbt_model_is_categorical.argtypes = [P, C.c_uint32]

@@ -219,7 +219,10 @@ struct fbh_ctx {
     // pairs pay only with few tiles (measured: 2 tiles +3 %, 33 tiles -6 %).
     bool f32_hist() const { return tiles.size() <= F32_PAIR_MAX_TILES; }
     // launch_gradient mode of the device objective.
-    int gradient_mode() const { return objective == 0 ? 0 : (fast_math ? 3 : 2); }
+    int gradient_mode() const {
+        if (objective == 2) return fast_math ? 5 : 4;
+        return objective == 0 ? 0 : (fast_math ? 3 : 2);
+    }
     int64_t *gpair = nullptr;
     bool root_on_device = false;  // the last quantisation's root sum is on the device
     uint32_t *rows = nullptr, *tmp = nullptr;
@@ -342,8 +345,12 @@ struct fbh_ctx {
     bool tree_begun = false;
     double scales[2] = {1.0, 1.0};
 
-    // objective state on the device (fbh_set_objective)
-    int objective = -1;                 // -1 none, 0 squared error, 1 logistic
+    // objective state on the device (fbh_set_objective, fbh_set_multiclass)
+    int objective = -1;                 // -1 none, 0 squared error, 1 logistic, 2 softmax
+    uint32_t n_outputs = 1;             // margin columns (class-major), as planned
+    uint32_t out_k = 0;                 // the column gradients read and leaves update
+    float2 *softmax_stats = nullptr;    // per-row (wmax, wsum) of the round (softmax)
+    float *cur_margin() const { return margin + (uint64_t)out_k * n_rows; }
     bool fast_math = false;             // gpu_math="fast": hardware exp in the logistic gradient
     float *labels = nullptr, *gweights = nullptr, *margin = nullptr;
     void *leaf_ids = nullptr;           // per-row leaf position of the last tree
@@ -835,6 +842,8 @@ fbh_plan plan_memory(fbh_ctx &c, uint64_t budget) {
     });
     const uint64_t n = c.n_rows;
     fixed += OBJECTIVE_ROW_BYTES * n;
+    // More margin columns and the softmax row statistics (multiclass).
+    if (c.n_outputs > 1) fixed += (4ull * (c.n_outputs - 1) + 8) * n;
     P.fixed_bytes = fixed;
     if (fixed > budget)
         throw InputError("gpu_memory_budget of " + std::to_string(budget) +
@@ -978,6 +987,7 @@ fbh_config configure(fbh_ctx &c, uint64_t n_rows, const fbh_shape *shape, const 
         throw InputError("stream_windows (hist_streams) must be 1 or 2, got " +
                          std::to_string(conf.stream_windows));
     c.n_windows = conf.stream_windows ? conf.stream_windows : 2;
+    c.n_outputs = conf.n_outputs ? conf.n_outputs : 1;
     c.resident_cap = conf.resident_limit ? conf.resident_limit - 1 : UINT32_MAX;
     c.n_slots = conf.hist_slots ? conf.hist_slots : 64;
     if (c.n_slots > MAX_NODES)
@@ -1477,6 +1487,8 @@ int fbh_set_objective(fbh_ctx *c, uint32_t objective, const float *labels,
     return guard([&] {
         if (!c || !labels) throw InputError("null argument");
         if (objective > 1) throw InputError("objective must be 0 (squared error) or 1 (logistic)");
+        if (c->n_outputs != 1)
+            throw InputError("a context planned for several outputs takes fbh_set_multiclass");
         check(hipSetDevice(c->device), "hipSetDevice");
         if (c->objective < 0) {
             c->labels = c->alloc<float>(c->n_rows, "labels");
@@ -1505,6 +1517,69 @@ int fbh_set_objective(fbh_ctx *c, uint32_t objective, const float *labels,
         check(launch_fill_f32(c->margin, base_margin, c->n_rows, c->stream), "margin init");
         c->sync();
         c->objective = (int)objective;
+        c->ids_fresh = false;
+    });
+}
+
+int fbh_set_multiclass(fbh_ctx *c, uint32_t n_classes, const float *labels,
+                       const float *weights, const float *class_margins) {
+    return guard([&] {
+        if (!c || !labels || !class_margins) throw InputError("null argument");
+        if (n_classes < 2) throw InputError("multiclass objectives require num_class >= 2");
+        if (n_classes != c->n_outputs)
+            throw InputError("the context was planned for " + std::to_string(c->n_outputs) +
+                             " outputs, not " + std::to_string(n_classes) + " classes");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        if (c->objective < 0) {
+            c->labels = c->alloc<float>(c->n_rows, "labels");
+            c->margin = c->alloc<float>((uint64_t)n_classes * c->n_rows, "class margins");
+            c->leaf_ids = c->alloc<uint16_t>(c->n_rows, "leaf ids");
+            c->softmax_stats = c->alloc<float2>(c->n_rows, "softmax row statistics");
+        } else if (c->objective != 2) {
+            throw InputError("the context already holds a single-output objective");
+        }
+        if (weights && !c->gweights) c->gweights = c->alloc<float>(c->n_rows, "row weights");
+        c->sync();
+        check(hipMemcpy(c->labels, labels, 4 * c->n_rows, hipMemcpyHostToDevice), "label upload");
+        c->has_weights = weights != nullptr;
+        if (weights)
+            check(hipMemcpy(c->gweights, weights, 4 * c->n_rows, hipMemcpyHostToDevice),
+                  "weight upload");
+        for (uint32_t k = 0; k < n_classes; k++)
+            check(launch_fill_f32(c->margin + (uint64_t)k * c->n_rows, class_margins[k],
+                                  c->n_rows, c->stream),
+                  "margin init");
+        c->sync();
+        c->objective = 2;
+        c->out_k = 0;
+        c->ids_fresh = false;
+    });
+}
+
+int fbh_multiclass_begin_round(fbh_ctx *c) {
+    return guard([&] {
+        if (!c) throw InputError("null argument");
+        if (c->objective != 2) throw InputError("fbh_set_multiclass has not been called");
+        if (c->leaves_deferred)
+            throw InputError("the last grown tree's leaf values were deferred and not applied "
+                             "(fbh_apply_leaf_values): the margins are not up to date");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        check(launch_softmax_stats(c->margin, c->n_outputs, c->n_rows, c->fast_math ? 1 : 0,
+                                   c->softmax_stats, c->stream),
+              "softmax row statistics");
+    });
+}
+
+int fbh_set_output(fbh_ctx *c, uint32_t k) {
+    return guard([&] {
+        if (!c) throw InputError("null argument");
+        if (k >= c->n_outputs)
+            throw InputError("output " + std::to_string(k) + " of " +
+                             std::to_string(c->n_outputs));
+        if (c->leaves_deferred)
+            throw InputError("the last grown tree's leaf values were deferred and not applied "
+                             "(fbh_apply_leaf_values): the margins are not up to date");
+        c->out_k = k;
         c->ids_fresh = false;
     });
 }
@@ -1566,21 +1641,22 @@ int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th
             // if this round's bounds give other scales. With few tiles the
             // f32 pairs go out too, for the histograms of scattered rows.
             const bool f32 = c->f32_hist();
-            check(launch_gradient_spec(c->margin, c->labels, w, c->n_rows,
+            check(launch_gradient_spec(c->cur_margin(), c->labels, w, c->n_rows,
                                        c->gradient_mode(), th, seed, tree, c->red_f64,
                                        c->n_red_blocks, c->d_scales, c->gpair, c->red_i64,
-                                       f32 ? c->gpair_f32 : nullptr, c->stream),
+                                       f32 ? c->gpair_f32 : nullptr, c->stream,
+                                       c->softmax_stats, c->out_k),
                   "device gradient");
             c->ids_fresh = false;
             c->root_on_device = true;
             c->f32_pairs = f32;
             return;
         }
-        if (c->objective == 0 || !fn) {
-            // Squared error, or logistic with the device sigmoid.
-            check(launch_gradient(c->margin, c->labels, w, c->n_rows, c->gradient_mode(),
+        if (c->objective != 1 || !fn) {
+            // Squared error, softmax, or logistic with the device sigmoid.
+            check(launch_gradient(c->cur_margin(), c->labels, w, c->n_rows, c->gradient_mode(),
                                   c->gpair_f32, th, seed, tree, c->red_f64, c->n_red_blocks,
-                                  c->stream),
+                                  c->stream, c->softmax_stats, c->out_k),
                   "device gradient");
         } else {
             const uint64_t n = c->n_rows;
@@ -1629,7 +1705,8 @@ int fbh_download_margin(fbh_ctx *c, float *out) {
             throw InputError("the last grown tree's leaf values were deferred and not applied "
                              "(fbh_apply_leaf_values): the margins are not up to date");
         check(hipSetDevice(c->device), "hipSetDevice");
-        check(hipMemcpyAsync(out, c->margin, c->n_rows * 4, hipMemcpyDeviceToHost, c->stream),
+        check(hipMemcpyAsync(out, c->margin, (uint64_t)c->n_outputs * c->n_rows * 4,
+                             hipMemcpyDeviceToHost, c->stream),
               "margin download");
         c->sync();
     });
@@ -2784,7 +2861,7 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     if (walk) {
         check(launch_tree_leaves(c->bundles[0].data, c->bundles[0].pitch, c->n_rows, GB.tree,
                                  GB.tree_cats, GB.feat_off, GB.st, c->leaf_ids, idb,
-                                 defer ? nullptr : c->margin, c->delta, GB.leaf_vals, c->stream),
+                                 defer ? nullptr : c->cur_margin(), c->delta, GB.leaf_vals, c->stream),
               "leaf walk");
     } else {
         check(launch_leaf_plan(GB.leaves, GB.st, c->stream), "leaf plan");
@@ -2794,7 +2871,7 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
                                    c->stream),
               "leaf assignment");
         if (idb && !defer)
-            check(launch_apply_leaves(c->leaf_ids, idb, GB.leaf_vals, c->n_rows, c->margin,
+            check(launch_apply_leaves(c->leaf_ids, idb, GB.leaf_vals, c->n_rows, c->cur_margin(),
                                       c->stream),
                   "margin update");
     }
@@ -2920,7 +2997,7 @@ int fbh_apply_leaf_values(fbh_ctx *c, const float *values, uint32_t n) {
         check(hipMemcpyAsync(d_vals, pv, bytes, hipMemcpyHostToDevice, c->stream), "leaf values");
         check(hipEventRecord(c->leaves_done, c->stream), "event");
         c->leaves_pending = true;
-        check(launch_apply_leaves(c->leaf_ids, c->leaf_id_bytes, d_vals, c->n_rows, c->margin,
+        check(launch_apply_leaves(c->leaf_ids, c->leaf_id_bytes, d_vals, c->n_rows, c->cur_margin(),
                                   c->stream),
               "margin update");
         c->leaves_deferred = false;
@@ -2969,7 +3046,7 @@ int fbh_assign_leaves(fbh_ctx *c, const fbh_span *spans, const float *values, ui
                                    c->leaf_ids, idb, nullptr, c->stream),
               "leaf assignment");
         if (idb)
-            check(launch_apply_leaves(c->leaf_ids, idb, d_vals, c->n_rows, c->margin, c->stream),
+            check(launch_apply_leaves(c->leaf_ids, idb, d_vals, c->n_rows, c->cur_margin(), c->stream),
                   "margin update");
         c->leaf_id_bytes = idb;
         c->ids_fresh = idb != 0;

@@ -408,11 +408,19 @@ hipError_t launch_apply_leaves(const void *ids, int id_bytes, const float *value
 // mode 0: squared error from the margin (g = p - y, h = 1);
 // mode 1: from the host's sigmoid s (g = s - y, h = max(s(1 - s), 1e-16));
 // mode 2: as 1 with s computed on the device from the margin;
-// mode 3: as 2 with the hardware exponential (gpu_math="fast").
+// mode 3: as 2 with the hardware exponential (gpu_math="fast");
+// modes 4/5: softmax class cls of the margins src, from the round's per-row
+// statistics (launch_softmax_stats), with glibc's expf restated (4) or the
+// hardware exponential (5).
 // All are multiplied by the row weight when w is non-null.
 hipError_t launch_gradient(const float *src, const float *y, const float *w, uint64_t n,
                            int mode, float *g2n, uint64_t threshold, uint64_t seed, uint64_t tree,
-                           double *block_max, uint32_t n_blocks, hipStream_t s);
+                           double *block_max, uint32_t n_blocks, hipStream_t s,
+                           const float2 *stats = nullptr, uint32_t cls = 0);
+// Per row of K class-major margin columns: (largest margin from the smallest
+// normal float up, float of the double sum of exp(m - that)).
+hipError_t launch_softmax_stats(const float *margin, uint32_t K, uint64_t n, int fast,
+                                float2 *stats, hipStream_t s);
 hipError_t launch_sigmoid(const float *in, uint64_t n, float *out, hipStream_t s);
 hipError_t launch_sigmoid_checksum(uint64_t begin, uint64_t end, unsigned long long *out,
                                    hipStream_t s);
@@ -427,7 +435,8 @@ hipError_t launch_init_rows(uint32_t *rows, float *delta, uint64_t n, hipStream_
 hipError_t launch_gradient_spec(const float *src, const float *y, const float *w, uint64_t n,
                                 int mode, uint64_t th, uint64_t seed, uint64_t tree,
                                 double *block_max, uint32_t n_blocks, ScalesDev *scales,
-                                int64_t *fixed, int64_t *block_sum, float *g2n, hipStream_t s);
+                                int64_t *fixed, int64_t *block_sum, float *g2n, hipStream_t s,
+                                const float2 *stats = nullptr, uint32_t cls = 0);
 hipError_t launch_gpair_maxabs(float *g2n, uint64_t n, uint64_t threshold, uint64_t seed,
                                uint64_t tree, double *block_max, uint32_t n_blocks,
                                hipStream_t s);

@@ -1919,6 +1919,65 @@ __device__ __forceinline__ float fast_sigmoid(float m) { return 1.0f / (1.0f + _
 __device__ __forceinline__ float objective_source(int mode, float v) {
     return mode == 2 ? fb_sigmoid(v) : mode == 3 ? fast_sigmoid(v) : v;
 }
+
+// One row's weighted pair. Modes 0-3: squared error (0) or logistic from the
+// source value (1: host sigmoids, 2: the exact device sigmoid, 3: the fast
+// one); g = v - y, h = max(v (1 - v), 1e-16) (1 for squared error), both
+// times the weight. Modes 4/5: softmax class cls from the round's row
+// statistics st = (wmax, wsum) (Objective::softmax_gradients,
+// src/training/objective.rs:1175-1219; 4: glibc's expf restated, 5: the
+// hardware exp): p = exp(m - wmax) / wsum, h = max(2 p (1 - p) w, 1e-16),
+// g = (p - [y == cls]) w.
+__device__ __forceinline__ void row_pair(int mode, float s, float y, bool has_w, float w,
+                                         const float2 *stats, uint32_t cls, uint64_t i, float &g,
+                                         float &h) {
+    if (mode >= 4) {
+        const float2 st = stats[i];
+        const float e = mode == 4 ? fb_expf(s - st.x) : __expf(s - st.x);
+        float p = e / st.y;
+        const float wt = has_w ? w : 1.0f;
+        h = fmaxf(2.0f * p * (1.0f - p) * wt, 1e-16f);
+        if (y == (float)cls) p = p - 1.0f;
+        g = p * wt;
+        return;
+    }
+    const float v = objective_source(mode, s);
+    g = v - y;
+    h = mode != 0 ? fmaxf(v * (1.0f - v), 1e-16f) : 1.0f;
+    if (has_w) {
+        g = g * w;
+        h = h * w;
+    }
+}
+
+// softmax_row_stats (src/backend/cuda/histogram.cu:786-835; the row loop of
+// Objective::softmax_gradients): per row, the largest of the K class margins
+// (from the smallest normal float up) and the sum over classes, in class
+// order and in double, of exp(m - wmax); the sum is kept as a float, the
+// divisor every class uses.
+__global__ __launch_bounds__(256) void softmax_stats_kernel(const float *margin, uint32_t K,
+                                                            uint64_t n, int fast, float2 *stats) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        float wmax = 1.17549435e-38f;
+        for (uint32_t k = 0; k < K; k++) wmax = fmaxf(margin[(uint64_t)k * n + i], wmax);
+        double wsum = 0.0;
+        for (uint32_t k = 0; k < K; k++) {
+            const float d = margin[(uint64_t)k * n + i] - wmax;
+            wsum += (double)(fast ? __expf(d) : fb_expf(d));
+        }
+        stats[i] = make_float2(wmax, (float)wsum);
+    }
+}
+
+hipError_t launch_softmax_stats(const float *margin, uint32_t K, uint64_t n, int fast,
+                                float2 *stats, hipStream_t s) {
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((n + 255) / 256, 8192);
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(softmax_stats_kernel, dim3(blocks), dim3(256), 0, s, margin, K, n, fast,
+                       stats);
+    return hipGetLastError();
+}
 __device__ __forceinline__ bool row_selected(uint64_t row, uint64_t th, uint64_t seed,
                                              uint64_t tree);
 __device__ __forceinline__ double finite_abs(float v);
@@ -1939,7 +1998,8 @@ __global__ __launch_bounds__(256) void gradient_kernel(const float *src, const f
                                                        float *g2n, uint64_t th, uint64_t seed,
                                                        uint64_t tree, double *block_max,
                                                        const ScalesDev *spec, int64_t *fixed,
-                                                       int64_t *block_sum) {
+                                                       int64_t *block_sum, const float2 *stats,
+                                                       uint32_t cls) {
     // Four rows a thread per step (loads of all four first).
     constexpr int U = 4;
     double mg = 0.0, mh = 0.0;
@@ -1965,13 +2025,8 @@ __global__ __launch_bounds__(256) void gradient_kernel(const float *src, const f
         for (int u = 0; u < U; u++) {
             const uint64_t i = base + u * S;
             if (i >= n) continue;
-            const float v = objective_source(mode, sv[u]);
-            float g = v - yv[u];
-            float h = mode != 0 ? fmaxf(v * (1.0f - v), 1e-16f) : 1.0f;
-            if (w) {
-                g = g * wv[u];
-                h = h * wv[u];
-            }
+            float g, h;
+            row_pair(mode, sv[u], yv[u], w != nullptr, wv[u], stats, cls, i, g, h);
             if (block_max) {
                 if (!row_selected(i, th, seed, tree)) g = h = 0.0f;
                 mg = fmax(mg, finite_abs(g));
@@ -1999,19 +2054,15 @@ __global__ __launch_bounds__(256) void gradient_fixup_kernel(const float *src, c
                                                              uint64_t th, uint64_t seed,
                                                              uint64_t tree,
                                                              const ScalesDev *scales,
-                                                             int64_t *fixed, int64_t *block_sum) {
+                                                             int64_t *fixed, int64_t *block_sum,
+                                                             const float2 *stats, uint32_t cls) {
     if (!scales->spec_miss) return;  // uniform
     const double sg = scales->scale[0], sh = scales->scale[1];
     uint64_t ag = 0, ah = 0;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * blockDim.x) {
-        const float v = objective_source(mode, src[i]);
-        float g = v - y[i];
-        float h = mode != 0 ? fmaxf(v * (1.0f - v), 1e-16f) : 1.0f;
-        if (w) {
-            g = g * w[i];
-            h = h * w[i];
-        }
+        float g, h;
+        row_pair(mode, src[i], y[i], w != nullptr, w ? w[i] : 1.0f, stats, cls, i, g, h);
         if (!row_selected(i, th, seed, tree)) g = h = 0.0f;
         const int64_t qg = sat_i64(round((double)g * sg));
         const int64_t qh = sat_i64(round((double)h * sh));
@@ -2028,25 +2079,27 @@ __global__ void reduce_max_kernel(const double *block_max, uint32_t n, double *o
 hipError_t launch_gradient_spec(const float *src, const float *y, const float *w, uint64_t n,
                                 int mode, uint64_t th, uint64_t seed, uint64_t tree,
                                 double *block_max, uint32_t n_blocks, ScalesDev *scales,
-                                int64_t *fixed, int64_t *block_sum, float *g2n, hipStream_t s) {
+                                int64_t *fixed, int64_t *block_sum, float *g2n, hipStream_t s,
+                                const float2 *stats, uint32_t cls) {
     if (n_blocks == 0) return hipSuccess;
     hipLaunchKernelGGL(gradient_kernel, dim3(n_blocks), dim3(256), 0, s, src, y, w, n, mode,
-                       g2n, th, seed, tree, block_max, scales, fixed, block_sum);
+                       g2n, th, seed, tree, block_max, scales, fixed, block_sum, stats, cls);
     hipLaunchKernelGGL(reduce_max_kernel, dim3(1), dim3(1024), 0, s, block_max, n_blocks,
                        block_max + 2 * n_blocks, n, scales);
     hipLaunchKernelGGL(gradient_fixup_kernel, dim3(n_blocks), dim3(256), 0, s, src, y, w, n, mode,
-                       th, seed, tree, scales, fixed, block_sum);
+                       th, seed, tree, scales, fixed, block_sum, stats, cls);
     return hipGetLastError();
 }
 
 hipError_t launch_gradient(const float *src, const float *y, const float *w, uint64_t n, int mode,
                            float *g2n, uint64_t th, uint64_t seed, uint64_t tree,
-                           double *block_max, uint32_t n_blocks, hipStream_t s) {
+                           double *block_max, uint32_t n_blocks, hipStream_t s,
+                           const float2 *stats, uint32_t cls) {
     const uint32_t blocks =
         block_max ? n_blocks : (uint32_t)std::min<uint64_t>((n + 255) / 256, 8192);
     if (blocks == 0) return hipSuccess;
     hipLaunchKernelGGL(gradient_kernel, dim3(blocks), dim3(256), 0, s, src, y, w, n, mode, g2n,
-                       th, seed, tree, block_max, nullptr, nullptr, nullptr);
+                       th, seed, tree, block_max, nullptr, nullptr, nullptr, stats, cls);
     return hipGetLastError();
 }
 

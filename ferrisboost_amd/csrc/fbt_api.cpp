@@ -1,5 +1,6 @@
 // fbt_api.cpp -- C ABI of the round driver (include/fbtrain.h).
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <limits>
@@ -153,9 +154,16 @@ uint32_t fbt_model_n_features(const fbt_model *m) { return m->m.n_features; }
 int fbt_model_train_margins(const fbt_model *m, float *out, uint64_t n) {
     return guard([&] {
         if (!m || !out) throw fbt::InputError("null argument");
-        if (n != m->m.train_margins.size()) throw fbt::InputError("row count mismatch");
-        std::memcpy(out, m->m.train_margins.data(), 4 * n);
+        const uint64_t k = m->m.n_outputs();
+        if (n * k != m->m.train_margins.size()) throw fbt::InputError("row count mismatch");
+        std::memcpy(out, m->m.train_margins.data(), 4 * n * k);
     });
+}
+
+uint32_t fbt_model_num_outputs(const fbt_model *m) { return m->m.n_outputs(); }
+
+void fbt_model_class_margins(const fbt_model *m, float *out) {
+    std::copy(m->m.class_margins.begin(), m->m.class_margins.end(), out);
 }
 
 uint32_t fbt_model_n_cuts(const fbt_model *m) { return (uint32_t)m->m.cuts.values.size(); }
@@ -166,6 +174,15 @@ void fbt_model_cuts(const fbt_model *m, float *values, uint32_t *offsets) {
 }
 
 void fbt_predict_margin(const fbt_model *m, const float *x, uint64_t n, uint32_t nf, float *out) {
+    if (m->m.n_outputs() > 1) {  // Model::predict_margins_upto (src/model/tree.rs:470-480)
+        const uint32_t K = m->m.n_outputs();
+        for (uint64_t r = 0; r < n; r++) {
+            float *o = out + r * K;
+            for (uint32_t k = 0; k < K; k++) o[k] = m->m.class_margins[k];
+            for (size_t t = 0; t < m->m.trees.size(); t++) o[t % K] += m->m.trees[t].leaf_value(x + r * nf);
+        }
+        return;
+    }
     const float bm = m->m.base_margin();
     for (uint64_t r = 0; r < n; r++) {
         float acc = bm;
@@ -200,12 +217,15 @@ void backend_fail(int rc) {
     throw fbt::RuntimeError(buf);
 }
 
-ShapModel explain_model(const fbt::Model &m, uint32_t begin, uint32_t end, int device) {
+// The device model of the given trees with `bias` as the intercept of
+// predictions and explanations.
+ShapModel explain_model(const fbt::Model &m, const std::vector<uint32_t> &ids, float bias,
+                        int device) {
     std::vector<uint32_t> offs{0}, feat, cat_off, cat_len, words;
     std::vector<float> cond, leaf, hess;
     std::vector<int32_t> left, right;
     std::vector<uint8_t> dl, is_leaf;
-    for (uint32_t t = begin; t < end; t++) {
+    for (uint32_t t : ids) {
         for (const auto &n : m.trees[t].nodes) {
             feat.push_back(n.feat);
             cond.push_back(n.split_cond);
@@ -222,13 +242,106 @@ ShapModel explain_model(const fbt::Model &m, uint32_t begin, uint32_t end, int d
         offs.push_back((uint32_t)feat.size());
     }
     fbh_shap_model *sm = nullptr;
-    const int rc = fbh_shap_model_create(device, end - begin, offs.data(), feat.data(), cond.data(),
-                                         left.data(), right.data(), dl.data(), is_leaf.data(),
-                                         leaf.data(), hess.data(), cat_off.data(), cat_len.data(),
-                                         words.data(), (uint32_t)words.size(), m.n_features,
-                                         m.base_margin(), &sm);
+    const int rc = fbh_shap_model_create(device, (uint32_t)ids.size(), offs.data(), feat.data(),
+                                         cond.data(), left.data(), right.data(), dl.data(),
+                                         is_leaf.data(), leaf.data(), hess.data(), cat_off.data(),
+                                         cat_len.data(), words.data(), (uint32_t)words.size(),
+                                         m.n_features, bias, &sm);
     if (rc) backend_fail(rc);
     return ShapModel(sm, fbh_shap_model_destroy);
+}
+
+ShapModel explain_model(const fbt::Model &m, uint32_t begin, uint32_t end, int device) {
+    std::vector<uint32_t> ids;
+    for (uint32_t t = begin; t < end; t++) ids.push_back(t);
+    return explain_model(m, ids, m.base_margin(), device);
+}
+
+// softmax_in_place (src/training/objective.rs:1308-1322): the row's largest
+// margin, the double sum of expf(v - max) in order, each value divided by
+// the float of that sum.
+void softmax_row(float *row, uint32_t k) {
+    float wmax = row[0];
+    for (uint32_t i = 1; i < k; i++) wmax = std::fmax(row[i], wmax);
+    double wsum = 0.0;
+    for (uint32_t i = 0; i < k; i++) {
+        row[i] = std::exp(row[i] - wmax);
+        wsum += (double)row[i];
+    }
+    const float d = (float)wsum;
+    for (uint32_t i = 0; i < k; i++) row[i] /= d;
+}
+
+// argmax (src/training/objective.rs:1324-1333): the first largest.
+uint32_t argmax_row(const float *row, uint32_t k) {
+    uint32_t best = 0;
+    for (uint32_t i = 1; i < k; i++)
+        if (row[i] > row[best]) best = i;
+    return best;
+}
+
+// A multiclass model's outputs: each class scored or explained by its own
+// trees with its own intercept (Model::class_view, src/model/tree.rs:
+// 395-425), the per-class results laid out [row][class][...].
+void predict_multiclass(const fbt::Model &m, const float *x, uint64_t n_rows, uint32_t nf,
+                        uint32_t output, uint32_t begin, uint32_t end, const float *base_margin,
+                        int device, float *out) {
+    const uint32_t K = m.n_outputs();
+    if (output == FBT_OUT_LEAF) {
+        if (device < 0) throw fbt::InputError("explanations run on the device; pass a device index");
+        ShapModel sm = explain_model(m, begin, end, device);
+        if (int rc = fbh_predict(sm.get(), x, n_rows, nullptr, FBH_PREDICT_LEAF, out)) backend_fail(rc);
+        g_last_shap_ms = fbh_shap_last_ms(sm.get());
+        return;
+    }
+    const bool scores = output == FBT_OUT_MARGIN || output == FBT_OUT_VALUE;
+    if (!scores && device < 0)
+        throw fbt::InputError("explanations run on the device; pass a device index");
+    const uint64_t width = scores ? 1 : output == FBT_OUT_INTERACTIONS
+                                            ? (uint64_t)(nf + 1) * (nf + 1)
+                                            : (uint64_t)nf + 1;
+    std::vector<float> margins(scores ? n_rows * K : 0), col(n_rows * width);
+    double ms = 0.0;
+    for (uint32_t k = 0; k < K; k++) {
+        std::vector<uint32_t> ids;
+        for (uint32_t t = begin; t < end; t++)
+            if (t % K == k) ids.push_back(t);
+        const float *bm = base_margin ? base_margin + (uint64_t)k * n_rows : nullptr;
+        const float bias = m.class_margins[k];
+        if (device < 0) {
+            for (uint64_t r = 0; r < n_rows; r++) {
+                float acc = bm ? bm[r] : bias;
+                for (uint32_t t : ids) acc += m.trees[t].leaf_value(x + r * nf);
+                col[r] = acc;
+            }
+        } else {
+            ShapModel sm = explain_model(m, ids, bias, device);
+            int rc = FBH_OK;
+            if (scores) rc = fbh_predict(sm.get(), x, n_rows, bm, FBH_PREDICT_MARGIN, col.data());
+            else if (output == FBT_OUT_CONTRIBS) rc = fbh_shap_contribs(sm.get(), x, n_rows, bm, col.data());
+            else if (output == FBT_OUT_APPROX_CONTRIBS)
+                rc = fbh_saabas_contribs(sm.get(), x, n_rows, bm, col.data());
+            else rc = fbh_shap_interactions(sm.get(), x, n_rows, bm, col.data());
+            if (rc) backend_fail(rc);
+            ms += fbh_shap_last_ms(sm.get());
+        }
+        if (scores) {
+            for (uint64_t r = 0; r < n_rows; r++) margins[r * K + k] = col[r];
+        } else {
+            for (uint64_t r = 0; r < n_rows; r++)
+                std::memcpy(out + (r * K + k) * width, col.data() + r * width, 4 * width);
+        }
+    }
+    g_last_shap_ms = ms;
+    if (!scores) return;
+    if (output == FBT_OUT_MARGIN) {
+        std::memcpy(out, margins.data(), 4 * margins.size());
+    } else if (m.objective == 3) {  // multi:softmax: the class index
+        for (uint64_t r = 0; r < n_rows; r++) out[r] = (float)argmax_row(&margins[r * K], K);
+    } else {  // multi:softprob: the probabilities
+        for (uint64_t r = 0; r < n_rows; r++) softmax_row(&margins[r * K], K);
+        std::memcpy(out, margins.data(), 4 * margins.size());
+    }
 }
 
 }  // namespace
@@ -263,6 +376,11 @@ int fbt_predict(const fbt_model *mm, const float *x, uint64_t n_rows, uint32_t n
                 throw fbt::InputError(
                     "feature values equal to the largest float32 (3.4028235e38) are reserved "
                     "and cannot be scored");
+        if (m.n_outputs() > 1) {
+            predict_multiclass(m, x, n_rows, n_features, output, tree_begin, tree_end, base_margin,
+                               device, out);
+            return;
+        }
         const bool logistic = m.objective == 1;
         if (device < 0) {
             // Host scoring (use_gpu=False): Model::predict_margin_upto and the

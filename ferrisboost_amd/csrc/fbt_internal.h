@@ -84,7 +84,12 @@ struct Tree {
 struct Model {
     std::vector<Tree> trees;
     float base_score = 0.5f;
-    uint32_t objective = 1;
+    uint32_t objective = 1;  // 0 squared error, 1 logistic, 2 multi:softprob, 3 multi:softmax
+    // A multiclass model's per-class intercepts (class_base_margins,
+    // src/model/tree.rs:256-260); tree t belongs to class t % K. Empty for a
+    // single-output model.
+    std::vector<float> class_margins;
+    uint32_t n_outputs() const { return class_margins.empty() ? 1u : (uint32_t)class_margins.size(); }
     uint32_t n_features = 0;
     float scale_pos_weight = 1.0f;
     Cuts cuts;

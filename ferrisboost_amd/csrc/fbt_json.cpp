@@ -250,8 +250,8 @@ float param_f32(const std::string &name, const std::string &raw) {
     return x;
 }
 
-// parse_base_score (src/model/tree.rs:1060-1079): "5E-1" or "[5E-1]".
-float parse_base_score(const std::string &raw) {
+// The comma-separated parts of "a", "[a]" or "[a,b,c]".
+std::vector<std::string> base_score_parts(const std::string &raw) {
     std::string t = trim(raw);
     if (t.size() >= 2 && t.front() == '[' && t.back() == ']') t = t.substr(1, t.size() - 2);
     std::vector<std::string> parts;
@@ -264,9 +264,23 @@ float parse_base_score(const std::string &raw) {
         s = c + 1;
     }
     if (parts.empty()) throw bad("base_score is empty: \"" + raw + "\"");
+    return parts;
+}
+
+// parse_base_score (src/model/tree.rs:1060-1079): "5E-1" or "[5E-1]".
+float parse_base_score(const std::string &raw) {
+    const std::vector<std::string> parts = base_score_parts(raw);
     if (parts.size() > 1)
         throw bad("base_score is a vector (\"" + raw + "\"); multi-target models are not supported");
     return param_f32("base_score", parts[0]);
+}
+
+// parse_base_score_vector (src/model/tree.rs:1033-1050): a multiclass
+// model's intercepts "[a,b,c]" (or a scalar).
+std::vector<float> parse_base_score_vector(const std::string &raw) {
+    std::vector<float> v;
+    for (const std::string &p : base_score_parts(raw)) v.push_back(param_f32("base_score", p));
+    return v;
 }
 
 constexpr int32_t NO_CHILD = -1;
@@ -413,9 +427,12 @@ Model model_from_json(const char *text, size_t len) {
     Model m;
     if (oname == "binary:logistic") m.objective = 1;
     else if (oname == "reg:squarederror") m.objective = 0;
+    else if (oname == "multi:softprob") m.objective = 2;
+    else if (oname == "multi:softmax") m.objective = 3;
     else
         throw bad("objective " + oname +
-                  " is not supported; supported: binary:logistic, reg:squarederror");
+                  " is not supported; supported: binary:logistic, reg:squarederror, "
+                  "multi:softprob, multi:softmax");
     const long long ncp = param_int("num_class", str(req(mp, "num_class", "learner_model_param"), "num_class"));
     const size_t num_class_param = (size_t)std::max(ncp, 1ll);
     size_t num_target = 1;
@@ -452,12 +469,27 @@ Model model_from_json(const char *text, size_t len) {
     const std::string &npt = str(req(gp, "num_parallel_tree", "gbtree_model_param"), "num_parallel_tree");
     if (param_int("num_parallel_tree", npt) != 1)
         throw bad("num_parallel_tree = " + npt + " (random forest mode) is not supported");
-    if (num_class != 1)
+    // num_class must match the objective's outputs (src/model/tree.rs:838-845).
+    const bool multi = m.objective >= 2;
+    if (multi ? num_class < 2 : num_class != 1)
         throw bad("num_class = " + std::to_string(num_class) + " is inconsistent with objective " + oname);
     const long long nf = param_int("num_feature", str(req(mp, "num_feature", "learner_model_param"), "num_feature"));
     if (nf < 0 || nf > 0xFFFFFFFFll) throw bad("num_feature out of range");
     m.n_features = (uint32_t)nf;
-    m.base_score = parse_base_score(str(req(mp, "base_score", "learner_model_param"), "base_score"));
+    const std::string &bs_raw = str(req(mp, "base_score", "learner_model_param"), "base_score");
+    if (multi) {
+        // The intercepts: a vector of num_class values, or a scalar copied
+        // to every class (parse_base_score_vector, src/model/tree.rs:846-862).
+        std::vector<float> v = parse_base_score_vector(bs_raw);
+        if (v.size() == 1) v.assign(num_class, v[0]);
+        if (v.size() != num_class)
+            throw bad("base_score has " + std::to_string(v.size()) + " values, but num_class = " +
+                      std::to_string(num_class));
+        m.class_margins = v;
+        m.base_score = v[0];
+    } else {
+        m.base_score = parse_base_score(bs_raw);
+    }
     for (const JVal &t : trees.a) m.trees.push_back(read_tree(t));
     // feature_types: "c" marks a categorical feature.
     m.cuts.categorical.assign(m.n_features, 0);

@@ -176,16 +176,21 @@ std::string model_to_json(const Model &m) {
         }
     o += "],\"gradient_booster\":{\"name\":\"gbtree\",\"model\":{";
     const size_t nt = m.trees.size();
+    // K trees a round (multiclass): indptr steps by K, the last round may be
+    // short; tree i belongs to output i % K (src/model/tree.rs:689-699).
+    const size_t K = m.n_outputs();
     o += "\"gbtree_model_param\":{\"num_trees\":\"" + std::to_string(nt) +
          "\",\"num_parallel_tree\":\"1\"},\"iteration_indptr\":[";
-    for (size_t i = 0; i <= nt; i++) {
+    for (size_t i = 0; i < nt; i += K) {
         if (i) o += ',';
         o += std::to_string(i);
     }
+    if (nt) o += ',';
+    o += std::to_string(nt);
     o += "],\"tree_info\":[";
     for (size_t i = 0; i < nt; i++) {
         if (i) o += ',';
-        o += '0';
+        o += std::to_string(i % K);
     }
     o += "],\"trees\":[";
     auto i32s = [](int32_t v) { return std::to_string(v); };
@@ -261,13 +266,34 @@ std::string model_to_json(const Model &m) {
              std::to_string(m.n_features) + "\",\"num_nodes\":\"" + std::to_string(n) +
              "\",\"size_leaf_vector\":\"1\"}}";
     }
-    o += "]}},\"learner_model_param\":{\"base_score\":\"" + display_f32(m.base_score) +
-         "\",\"boost_from_average\":\"1\",\"num_class\":\"0\",\"num_feature\":\"" +
+    // base_score: the scalar before the link, or a multiclass model's
+    // intercepts as XGBoost's vector "[a,b,c]" (src/model/tree.rs:700-733).
+    std::string bs;
+    if (m.class_margins.empty()) {
+        bs = display_f32(m.base_score);
+    } else {
+        bs = "[";
+        for (size_t k = 0; k < m.class_margins.size(); k++) {
+            if (k) bs += ',';
+            bs += display_f32(m.class_margins[k]);
+        }
+        bs += "]";
+    }
+    const bool multi = m.objective >= 2;
+    o += "]}},\"learner_model_param\":{\"base_score\":\"" + bs +
+         "\",\"boost_from_average\":\"1\",\"num_class\":\"" +
+         (multi ? std::to_string(K) : std::string("0")) + "\",\"num_feature\":\"" +
          std::to_string(m.n_features) + "\",\"num_target\":\"1\"},";
     o += "\"objective\":{\"name\":\"";
-    o += m.objective == 1 ? "binary:logistic" : "reg:squarederror";
-    o += "\",\"reg_loss_param\":{\"scale_pos_weight\":\"" + display_f32(m.scale_pos_weight) +
-         "\"}}}}";
+    static const char *const names[] = {"reg:squarederror", "binary:logistic", "multi:softprob",
+                                        "multi:softmax"};
+    o += names[m.objective <= 3 ? m.objective : 0];
+    // Objective::json_params (src/training/objective.rs:772-822).
+    if (multi)
+        o += "\",\"softmax_multiclass_param\":{\"num_class\":\"" + std::to_string(K) + "\"}}}}";
+    else
+        o += "\",\"reg_loss_param\":{\"scale_pos_weight\":\"" +
+             display_f32(m.scale_pos_weight) + "\"}}}}";
     return o;
 }
 

@@ -762,7 +762,13 @@ void validate(const fbt_params &p, uint64_t n, uint32_t nf, const float *y) {
         throw InputError("training data has " + std::to_string(n) +
                          " rows, above the supported limit 4294967295");
     if (nf == 0) throw InputError("training data must have at least one feature");
-    if (p.objective > 1) throw InputError("objective must be reg:squarederror or binary:logistic");
+    if (p.objective > 3)
+        throw InputError("objective must be reg:squarederror, binary:logistic, multi:softprob or "
+                         "multi:softmax");
+    const bool multi = p.objective >= 2;
+    if (multi && p.num_class < 2)
+        throw InputError(std::string(p.objective == 2 ? "multi:softprob" : "multi:softmax") +
+                         " requires num_class >= 2, got " + std::to_string(p.num_class));
     if (p.grow_policy > 1) throw InputError("grow_policy must be depthwise or lossguide");
     if (p.gpu_math > 1) throw InputError("gpu_math must be 0 (exact) or 1 (fast)");
     if (p.gpu_math == 1 && p.host_sigmoid)
@@ -793,7 +799,37 @@ void validate(const fbt_params &p, uint64_t n, uint32_t nf, const float *y) {
         if (!std::isfinite(y[i])) throw InputError("labels must all be finite");
         if (p.objective == 1 && !(y[i] >= 0.0f && y[i] <= 1.0f))
             throw InputError("training set: binary:logistic labels must be in [0, 1]");
+        // Objective::validate_labels (src/training/objective.rs:681-687).
+        if (multi && !(y[i] >= 0.0f && y[i] < (float)p.num_class && y[i] == std::trunc(y[i])))
+            throw InputError(std::string("training set: ") +
+                             (p.objective == 2 ? "multi:softprob" : "multi:softmax") +
+                             " labels must be integers in [0, num_class=" +
+                             std::to_string(p.num_class) + ")");
     }
+}
+
+// Objective::initial_class_margins (src/training/objective.rs:1225-1248):
+// the centred logs of the class frequencies, in the reference's f32/f64
+// steps with the host libm.
+std::vector<float> initial_class_margins(const float *y, const float *w, uint64_t n, uint32_t k) {
+    std::vector<float> bins(k, 0.0f);
+    for (uint64_t i = 0; i < n; i++) bins[(uint32_t)y[i]] += w ? w[i] : 1.0f;
+    double sum_w = 0.0;
+    if (!w) {
+        sum_w = (double)n;
+    } else {
+        for (uint64_t i = 0; i < n; i++) sum_w += (double)w[i];
+    }
+    const float eps = 1e-6f;
+    if (sum_w < (double)eps) return std::vector<float>(k, 0.0f);
+    const double inv = 1.0 / sum_w;
+    std::vector<float> logs(k);
+    for (uint32_t c = 0; c < k; c++) logs[c] = std::log((float)((double)bins[c] * inv) + eps);
+    const float nk = (float)k;
+    float mean = 0.0f;
+    for (float v : logs) mean = mean + v / nk;
+    for (float &v : logs) v = v - mean;
+    return logs;
 }
 
 fbt_stats g_stats{};
@@ -858,8 +894,16 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     // Base score: explicit, else the label mean weighted by the sample weights
     // only (Objective::estimate_base_score, src/training/objective.rs:42-60,
     // 452-470; scale_pos_weight enters the gradient weights alone,
-    // src/training/mod.rs:1450-1468).
-    if (p.has_base_score) {
+    // src/training/mod.rs:1450-1468). A multiclass model keeps one intercept
+    // per class: base_score copied, else initial_class_margins
+    // (src/training/mod.rs:1430-1449).
+    const bool multi = p.objective >= 2;
+    const uint32_t K = multi ? p.num_class : 1;
+    if (multi) {
+        m.class_margins = p.has_base_score ? std::vector<float>(K, p.base_score)
+                                           : initial_class_margins(y, w, n, K);
+        m.base_score = m.class_margins[0];
+    } else if (p.has_base_score) {
         m.base_score = p.base_score;
     } else {
         double acc = 0.0;
@@ -908,6 +952,7 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     cfg.rows_per_block = p.rows_per_block;
     cfg.stream_windows = p.hist_streams;
     cfg.resident_limit = p.resident_limit;
+    cfg.n_outputs = K;
     uint32_t slots;
     if (p.grow_policy == 1) {
         const uint64_t leaves = p.max_leaves ? p.max_leaves : (1ull << std::min(p.max_depth, 14u));
@@ -968,7 +1013,7 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     const auto t_train = Clock::now();
     // Host margins feed the logistic sigmoid; the device keeps its own copy
     // (the same f32 additions), which squared error uses directly.
-    std::vector<float> pred(n, margin);
+    std::vector<float> pred((uint64_t)K * n, margin);
     Grower grower(ctx.get(), p, m.cuts, mono, slots);
     grower.n_rows_ = (uint32_t)n;
     {
@@ -978,7 +1023,10 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
                                plan.resident_tiles == plan.n_tiles && slots <= 16384;
     }
     const uint32_t obj = p.objective;
-    call(fbh_set_objective(ctx.get(), obj, y, grad_w, margin));
+    // train_multiclass_rounds takes the sample weights (scale_pos_weight is
+    // a binary objective's).
+    if (multi) call(fbh_set_multiclass(ctx.get(), K, y, w, m.class_margins.data()));
+    else call(fbh_set_objective(ctx.get(), obj, y, grad_w, margin));
     // gpu_math="fast" (fast_gradient_and_quantize, src/backend/cuda/train_ctx.rs:2404-2512):
     // the logistic gradient takes the hardware exponential on the device.
     call(fbh_set_gpu_math(ctx.get(), p.gpu_math));
@@ -1019,33 +1067,44 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     auto collect_all = [&]() {
         for (; pending; pending--) m.trees.push_back(grower.collect());
     };
+    // A multiclass round (train_multiclass_rounds, src/training/mod.rs:
+    // 2578-2850) takes every class's statistics from the round's starting
+    // margins, then grows one tree per class in class order: row and column
+    // sampling key on the tree index round * K + class, and each tree's
+    // leaves go to its own class's margins.
     for (uint32_t round = 0; round < p.n_rounds; round++) {
         if (pending && round == p.sync_round) collect_all();  // the device is idle when this round starts
         if (round > 0) close_round(round - 1);
         if (pending && host_sig) collect_all();
-        const auto tg = Clock::now();
-        double scales[2];
-        int64_t root_sum[2];
-        call(fbh_gradient_exchange(ctx.get(), host_sig ? sigmoid_chunk : nullptr, &job,
-                                   sample_threshold(p.subsample), p.seed, round,
-                                   device_scales ? nullptr : scales,
-                                   overlap ? nullptr : root_sum));
-        grad_s += std::chrono::duration<double>(Clock::now() - tg).count();
-        if (pending && !device_scales) collect_all();
-        std::vector<uint32_t> feats;
-        if (p.colsample_bytree < 1.0f) feats = sample_columns(nf, p.colsample_bytree, p.seed, round);
-        fbh_span root;
-        call(fbh_begin_tree(ctx.get(), feats.empty() ? nullptr : feats.data(),
-                            (uint32_t)feats.size(), mono.data(), nf, &root));
-        if (overlap) {
-            if (!device_scales) grower.lm_scales(scales);
-            grower.grow_async(nullptr);
-            if (++pending == 2) {
-                m.trees.push_back(grower.collect());
-                pending--;
+        if (multi) call(fbh_multiclass_begin_round(ctx.get()));
+        for (uint32_t cls = 0; cls < K; cls++) {
+            const uint64_t tree = (uint64_t)round * K + cls;
+            if (multi) call(fbh_set_output(ctx.get(), cls));
+            const auto tg = Clock::now();
+            double scales[2];
+            int64_t root_sum[2];
+            call(fbh_gradient_exchange(ctx.get(), host_sig ? sigmoid_chunk : nullptr, &job,
+                                       sample_threshold(p.subsample), p.seed, tree,
+                                       device_scales ? nullptr : scales,
+                                       overlap ? nullptr : root_sum));
+            grad_s += std::chrono::duration<double>(Clock::now() - tg).count();
+            if (pending && !device_scales) collect_all();
+            std::vector<uint32_t> feats;
+            if (p.colsample_bytree < 1.0f)
+                feats = sample_columns(nf, p.colsample_bytree, p.seed, tree);
+            fbh_span root;
+            call(fbh_begin_tree(ctx.get(), feats.empty() ? nullptr : feats.data(),
+                                (uint32_t)feats.size(), mono.data(), nf, &root));
+            if (overlap) {
+                if (!device_scales) grower.lm_scales(scales);
+                grower.grow_async(nullptr);
+                if (++pending == 2) {
+                    m.trees.push_back(grower.collect());
+                    pending--;
+                }
+            } else {
+                m.trees.push_back(grower.grow(scales, root_sum));
             }
-        } else {
-            m.trees.push_back(grower.grow(scales, root_sum));
         }
     }
     collect_all();

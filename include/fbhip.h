@@ -64,7 +64,9 @@ typedef struct {
     uint32_t resident_limit; /* resident_blocks + 1: keep at most that many LDS
                                 tiles resident, streaming the rest even when
                                 they would fit (0: as the budget allows) */
-    uint32_t reserved[4];
+    uint32_t n_outputs;      /* margin columns the objective keeps: num_class
+                                of a multiclass objective (0 or 1: one) */
+    uint32_t reserved[3];
 } fbh_config;
 
 /* Split-scan parameters: the TrainParams fields split.rs reads
@@ -327,8 +329,31 @@ int fbh_set_gpu_math(fbh_ctx *ctx, uint32_t gpu_math);
 int fbh_gradient_pairs(int device, uint32_t objective, uint32_t gpu_math, const float *margin,
                        const float *labels, const float *weights, uint64_t n, float *gpair2n_out);
 
-/* The device margins (the training margins after the assigned trees). */
+/* The device margins (the training margins after the assigned trees);
+ * n_outputs x n_rows class-major values for a multiclass objective. */
 int fbh_download_margin(fbh_ctx *ctx, float *out);
+
+/* Multiclass objectives (multi:softprob / multi:softmax): the resident state
+ * of train_multiclass_rounds (src/training/mod.rs:2578-2850) and its device
+ * gradient (softmax_row_stats / softmax_class_gradient,
+ * src/backend/cuda/histogram.cu:786-890; Objective::softmax_gradients,
+ * src/training/objective.rs:1175-1219). The context keeps n_classes margin
+ * columns (class-major, n_classes x n_rows), each starting at its class
+ * intercept; labels are class indices; weights (may be NULL) are the sample
+ * weights. The context must have been created with cfg->n_outputs equal to
+ * n_classes. */
+int fbh_set_multiclass(fbh_ctx *ctx, uint32_t n_classes, const float *labels,
+                       const float *weights, const float *class_margins);
+/* At the start of a round: every row's largest class margin (from the
+ * smallest normal float up) and the sum over classes, in double, of
+ * exp(margin - largest), which the round's class gradients share: each class
+ * of a round takes its pairs from the margins the round started with. exp is
+ * glibc's expf restated (gpu_math exact, the host's values bit for bit) or
+ * the hardware exponential (fast). */
+int fbh_multiclass_begin_round(fbh_ctx *ctx);
+/* The output (class) the next gradient call computes the pairs of and whose
+ * margin column the next tree's leaves update. */
+int fbh_set_output(fbh_ctx *ctx, uint32_t output);
 
 /* The logistic sigmoid 1 / (1 + expf(-x)) of Objective::gradient
  * (src/training/objective.rs:37-39) with expf restated from glibc's

@@ -45,14 +45,15 @@ typedef struct {
     float colsample_bytree;
     uint32_t cols_per_block;
     uint64_t seed;
-    uint32_t objective;        /* 0 = reg:squarederror, 1 = binary:logistic */
+    uint32_t objective;        /* 0 = reg:squarederror, 1 = binary:logistic,
+                                  2 = multi:softprob, 3 = multi:softmax */
     uint32_t grow_policy;      /* 0 = depthwise, 1 = lossguide */
     uint32_t max_cat_to_onehot;
     uint32_t max_cat_threshold;
     float base_score;          /* used when has_base_score != 0 */
     uint32_t has_base_score;
     uint32_t nthread;          /* host threads (0 = up to 16) */
-    uint32_t reserved;
+    uint32_t num_class;        /* classes of multi:softprob / multi:softmax */
     /* device-path knobs */
     int32_t device;            /* "cuda:N" */
     uint32_t gpu_math;         /* 0 = "exact" (bit-identical to the CPU engine),
@@ -159,12 +160,21 @@ void fbt_model_cat_words(const fbt_model *m, uint32_t *out);
 float fbt_model_base_score(const fbt_model *m);
 float fbt_model_base_margin(const fbt_model *m);
 uint32_t fbt_model_n_features(const fbt_model *m);
-/* Training-set margins the round loop accumulated (n_rows floats). */
+/* Training-set margins the round loop accumulated: n_rows floats, or
+ * num_class x n_rows class-major for a multiclass model (n_rows is the
+ * training row count either way). */
 int fbt_model_train_margins(const fbt_model *m, float *out, uint64_t n_rows);
+/* Outputs per row (num_class of a multiclass model, else 1) and a multiclass
+ * model's per-class intercepts (class_base_margins, src/model/tree.rs:
+ * 256-260; tree t belongs to class t % num_class). */
+uint32_t fbt_model_num_outputs(const fbt_model *m);
+void fbt_model_class_margins(const fbt_model *m, float *out);
 /* Cuts the model was trained with (values, offsets n_features + 1). */
 uint32_t fbt_model_n_cuts(const fbt_model *m);
 void fbt_model_cuts(const fbt_model *m, float *values, uint32_t *offsets);
-/* Model::predict_margin (src/model/tree.rs:486-510) on row-major rows. */
+/* Model::predict_margin (src/model/tree.rs:486-510) on row-major rows; a
+ * multiclass model writes [n_rows][num_class] (predict_margins_upto,
+ * src/model/tree.rs:470-480). */
 void fbt_predict_margin(const fbt_model *m, const float *x, uint64_t n_rows, uint32_t n_features,
                         float *out);
 /* XGBoost-schema JSON (Model::to_xgboost_json, src/model/tree.rs:600-760).
@@ -176,12 +186,17 @@ int fbt_shap(const fbt_model *m, const float *x, uint64_t n_rows, uint32_t n_fea
 
 /* Outputs of fbt_predict. */
 enum {
-    FBT_OUT_MARGIN = 0,          /* raw margins [n_rows] */
-    FBT_OUT_VALUE = 1,           /* margins through the objective's link [n_rows] */
+    FBT_OUT_MARGIN = 0,          /* raw margins [n_rows] ([n_rows][K] multiclass) */
+    FBT_OUT_VALUE = 1,           /* margins through the objective's link [n_rows]
+                                    (multi:softprob: probabilities [n_rows][K];
+                                    multi:softmax: the class index [n_rows]) */
     FBT_OUT_LEAF = 2,            /* pred_leaf: tree-local leaf ids [n_rows][trees] */
     FBT_OUT_CONTRIBS = 3,        /* pred_contribs: TreeSHAP [n_rows][n_features + 1] */
     FBT_OUT_APPROX_CONTRIBS = 4, /* approx_contribs: Saabas [n_rows][n_features + 1] */
     FBT_OUT_INTERACTIONS = 5     /* pred_interactions [n_rows][n_features + 1]^2 */
+    /* A multiclass model explains each class with its own trees and
+     * intercept (Model::class_view, src/model/tree.rs:395-425): contributions
+     * [n_rows][K][n_features + 1], interactions [n_rows][K][...]^2. */
 };
 /* Model.predict (python/ferrisboost/_core.pyi:94-197, src/python/mod.rs:
  * 2667-2800) over the trees [tree_begin, tree_end) (n_trees and
@@ -192,7 +207,9 @@ enum {
  * bias of explanations. device >= 0 runs on that GPU (the GpuPredictor /
  * GpuExplainModel kernels); device < 0 scores FBT_OUT_MARGIN / FBT_OUT_VALUE
  * on the host (use_gpu=False). The logistic link is 1 / (1 + expf(-m))
- * (objective.rs:37-39, 600-614) on either side, bit for bit. Feature values
+ * (objective.rs:37-39, 600-614) on either side, bit for bit; softprob's is
+ * the row softmax of softmax_in_place (objective.rs:1308-1322) with the host
+ * libm. A multiclass model's base_margin is class-major (K x n_rows). Feature values
  * equal to the largest float32 are an input error (they are reserved for
  * split boundaries). */
 int fbt_predict(const fbt_model *m, const float *x, uint64_t n_rows, uint32_t n_features,

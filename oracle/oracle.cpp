@@ -829,6 +829,45 @@ void gradient(u32 obj, float pred, float label, float &g, float &h) {
     }
 }
 
+// Objective::softmax_gradients (src/training/objective.rs:1175-1219): from
+// every class's margin of row i, the pair of class k. wmax starts at the
+// smallest normal float (as XGBoost's gradient does), the sum of expf runs
+// in double in class order, and the Hessian takes the sample weight before
+// its floor.
+void softmax_pair(const std::vector<std::vector<float>> &preds, u64 i, float label, float wt,
+                  u32 k, float &g, float &h) {
+    float wmax = std::numeric_limits<float>::min();
+    for (const auto &col : preds) wmax = std::fmax(col[i], wmax);
+    double wsum = 0.0;
+    for (const auto &col : preds) wsum += (double)std::exp(col[i] - wmax);
+    float p = std::exp(preds[k][i] - wmax) / (float)wsum;
+    h = std::fmax(2.0f * p * (1.0f - p) * wt, 1e-16f);
+    if (label == (float)k) p -= 1.0f;
+    g = p * wt;
+}
+
+// Objective::initial_class_margins (src/training/objective.rs:1225-1248):
+// centred logs of the class frequencies.
+std::vector<float> initial_class_margins(const float *y, const float *w, u64 n, u32 k_count) {
+    std::vector<float> bins(k_count, 0.0f);
+    for (u64 i = 0; i < n; i++) bins[(u32)y[i]] += w ? w[i] : 1.0f;
+    double sum_w = 0.0;
+    if (!w) {
+        sum_w = (double)n;
+    } else {
+        for (u64 i = 0; i < n; i++) sum_w += (double)w[i];
+    }
+    if (sum_w < (double)K_RT_EPS) return std::vector<float>(k_count, 0.0f);
+    const double inv = 1.0 / sum_w;
+    std::vector<float> logs(k_count);
+    for (u32 c = 0; c < k_count; c++) logs[c] = std::log((float)((double)bins[c] * inv) + K_RT_EPS);
+    const float nk = (float)k_count;
+    float mean = 0.0f;
+    for (float v : logs) mean = mean + v / nk;
+    for (float &v : logs) v = v - mean;
+    return logs;
+}
+
 float base_margin_of(u32 obj, float bs) {  // objective.rs:363-398
     if (obj == 1) {
         float x = std::min(std::max(bs, K_RT_EPS), 1.0f - K_RT_EPS);
@@ -936,6 +975,7 @@ struct orc_model {
     std::vector<Tree> trees;
     float base_score = 0.5f;
     u32 objective = 1;
+    std::vector<float> class_margins;  // a multiclass model's intercepts (K)
     std::vector<float> train_margins;
     double train_seconds = 0.0;
 };
@@ -1604,6 +1644,74 @@ uint64_t orc_partition(const uint32_t *rows, uint64_t n, const void *col, uint32
     return nl;
 }
 
+}  // extern "C"
+
+namespace {
+
+// train_multiclass_rounds (src/training/mod.rs:2578-2850): K margin columns
+// from the class intercepts (base_score copied K times when given); each
+// round takes every class's pairs from the round's starting margins
+// (softmax_gradients), then grows one tree per class in class order, with
+// row and column sampling keyed on the tree index round * K + class, each
+// tree's leaves added to its own class's margins.
+void train_multiclass(const float *x, u64 n, u32 nf, const float *labels, const float *weights,
+                      const Params &P, const Cuts &cuts, const std::vector<Block> &blocks,
+                      orc_model &m) {
+    (void)x;
+    const orc_params &p = P.p;
+    const u32 K = p.num_class;
+    if (K < 2) throw std::runtime_error("multiclass objectives require num_class >= 2");
+    for (u64 i = 0; i < n; i++) {
+        const float v = labels[i];
+        if (!(v >= 0.0f && v < (float)K && v == std::trunc(v)))
+            throw std::runtime_error("labels must be integers in [0, num_class)");
+    }
+    m.class_margins = p.has_base_score ? std::vector<float>(K, p.base_score)
+                                       : initial_class_margins(labels, weights, n, K);
+    m.base_score = m.class_margins[0];
+    std::vector<std::vector<float>> preds(K);
+    for (u32 k = 0; k < K; k++) preds[k].assign(n, m.class_margins[k]);
+    std::vector<std::vector<float>> gf(K, std::vector<float>(2 * n));
+    std::vector<Fixed> gpair(n);
+    auto t0 = std::chrono::steady_clock::now();
+    const u64 th = threshold_for(p.subsample);
+    for (u32 round = 0; round < p.n_rounds; round++) {
+        for (u64 i = 0; i < n; i++) {
+            const float wt = weights ? weights[i] : 1.0f;
+            for (u32 k = 0; k < K; k++)
+                softmax_pair(preds, i, labels[i], wt, k, gf[k][2 * i], gf[k][2 * i + 1]);
+        }
+        for (u32 k = 0; k < K; k++) {
+            const u64 tree = (u64)round * K + k;
+            double mg = 0, mh = 0;
+            for (u64 i = 0; i < n; i++) {
+                float &g = gf[k][2 * i], &h = gf[k][2 * i + 1];
+                if (!row_selected(i, th, p.seed, tree)) g = h = 0.0f;
+                mg = std::fmax(mg, finite_abs(g));
+                mh = std::fmax(mh, finite_abs(h));
+            }
+            Quantizer q = Quantizer::from_bounds(mg, mh, n);
+            Fixed root;
+            for (u64 i = 0; i < n; i++) {
+                gpair[i] = q.to_fixed(gf[k][2 * i], gf[k][2 * i + 1]);
+                root = add(root, gpair[i]);
+            }
+            std::vector<u32> smp;
+            const bool use_smp = p.colsample_bytree < 1.0f;
+            if (use_smp) smp = sample_features(nf, p.colsample_bytree, p.seed, tree);
+            Trainer tr(cuts, blocks, P, q, gpair, preds[k], use_smp ? &smp : nullptr);
+            m.trees.push_back(p.grow_policy == 1 ? tr.lossguide(root) : tr.depthwise(root));
+        }
+    }
+    m.train_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    m.train_margins.clear();
+    for (u32 k = 0; k < K; k++) m.train_margins.insert(m.train_margins.end(), preds[k].begin(), preds[k].end());
+}
+
+}  // namespace
+
+extern "C" {
+
 int orc_train(const float *x, uint64_t n, uint32_t nf, const float *labels, const float *weights,
               const uint8_t *categorical, const int8_t *monotone, uint32_t n_monotone,
               const orc_params *pp, orc_model **out) {
@@ -1618,6 +1726,11 @@ int orc_train(const float *x, uint64_t n, uint32_t nf, const float *labels, cons
         std::vector<Block> blocks = bin_blocks(x, n, nf, cuts, p.cols_per_block);
         auto m = std::make_unique<orc_model>();
         m->objective = p.objective;
+        if (p.objective == 2 || p.objective == 3) {
+            train_multiclass(x, n, nf, labels, weights, P, cuts, blocks, *m);
+            *out = m.release();
+            return 0;
+        }
         m->base_score = p.has_base_score ? p.base_score : estimate_base_score(labels, weights, n);
         float margin = base_margin_of(p.objective, m->base_score);
         std::vector<float> pred(n, margin);
@@ -1721,7 +1834,24 @@ float orc_model_base_score(const orc_model *m) { return m->base_score; }
 float orc_model_base_margin(const orc_model *m) { return base_margin_of(m->objective, m->base_score); }
 double orc_model_train_seconds(const orc_model *m) { return m->train_seconds; }
 
+uint32_t orc_model_num_outputs(const orc_model *m) {
+    return m->class_margins.empty() ? 1u : (u32)m->class_margins.size();
+}
+
+void orc_model_class_margins(const orc_model *m, float *out) {
+    std::copy(m->class_margins.begin(), m->class_margins.end(), out);
+}
+
 void orc_predict_margin(const orc_model *m, const float *x, uint64_t n, uint32_t nf, float *out) {
+    if (!m->class_margins.empty()) {  // Model::predict_margins_upto (src/model/tree.rs:470-480)
+        const u32 K = (u32)m->class_margins.size();
+        for (u64 r = 0; r < n; r++) {
+            float *o = out + r * K;
+            for (u32 k = 0; k < K; k++) o[k] = m->class_margins[k];
+            for (size_t t = 0; t < m->trees.size(); t++) o[t % K] += m->trees[t].leaf_value(x + r * nf);
+        }
+        return;
+    }
     float bm = base_margin_of(m->objective, m->base_score);
     for (u64 r = 0; r < n; r++) {
         float acc = bm;

@@ -37,14 +37,15 @@ typedef struct {
     float colsample_bytree;
     uint32_t cols_per_block;
     uint64_t seed;
-    uint32_t objective;       /* 0 = reg:squarederror, 1 = binary:logistic */
+    uint32_t objective;       /* 0 = reg:squarederror, 1 = binary:logistic,
+                                 2 = multi:softprob, 3 = multi:softmax */
     uint32_t grow_policy;     /* 0 = depthwise, 1 = lossguide */
     uint32_t max_cat_to_onehot;
     uint32_t max_cat_threshold;
     float base_score;         /* used when has_base_score != 0 */
     uint32_t has_base_score;
     uint32_t nthread;         /* histogram worker threads (0 = 1) */
-    uint32_t reserved;
+    uint32_t num_class;       /* classes of multi:softprob / multi:softmax */
 } orc_params;
 
 /* One tree node; same field meaning as Node (src/model/tree.rs:52-111). */
@@ -135,6 +136,13 @@ int orc_model_from_nodes(const orc_node *nodes, const uint32_t *tree_offsets, ui
                          const uint32_t *cat_words, uint32_t n_cat_words, uint32_t objective,
                          float base_score, orc_model **out);
 uint32_t orc_model_n_trees(const orc_model *m);
+/* Outputs per row (num_class of a multiclass model, else 1) and the class
+ * intercepts (class_base_margins, src/model/tree.rs:256-260) of a
+ * multiclass model. Training margins of a multiclass model are class-major
+ * (K x n), and orc_predict_margin writes n x K for it (predict_margins_upto,
+ * src/model/tree.rs:470-480). */
+uint32_t orc_model_num_outputs(const orc_model *m);
+void orc_model_class_margins(const orc_model *m, float *out);
 uint32_t orc_model_tree_len(const orc_model *m, uint32_t tree);
 void orc_model_tree_nodes(const orc_model *m, uint32_t tree, orc_node *out);
 uint32_t orc_model_n_cat_words(const orc_model *m);

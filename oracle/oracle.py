@@ -56,7 +56,7 @@ class Params(C.Structure):
         ("base_score", C.c_float),
         ("has_base_score", C.c_uint32),
         ("nthread", C.c_uint32),
-        ("reserved", C.c_uint32),
+        ("num_class", C.c_uint32),
     ]
 
 
@@ -110,7 +110,8 @@ class Split(C.Structure):
     ]
 
 
-OBJECTIVES = {"reg:squarederror": 0, "binary:logistic": 1}
+OBJECTIVES = {"reg:squarederror": 0, "binary:logistic": 1, "multi:softprob": 2,
+              "multi:softmax": 3}
 GROW = {"depthwise": 0, "lossguide": 1}
 
 _lib = None
@@ -151,6 +152,10 @@ def lib() -> C.CDLL:
         L.orc_model_free.restype = None
         L.orc_model_n_trees.argtypes = [P]
         L.orc_model_n_trees.restype = C.c_uint32
+        L.orc_model_num_outputs.argtypes = [P]
+        L.orc_model_num_outputs.restype = C.c_uint32
+        L.orc_model_class_margins.argtypes = [P, P]
+        L.orc_model_class_margins.restype = None
         L.orc_model_tree_len.argtypes = [P, C.c_uint32]
         L.orc_model_tree_len.restype = C.c_uint32
         L.orc_model_tree_nodes.argtypes = [P, C.c_uint32, P]
@@ -231,6 +236,7 @@ def make_params(**kw) -> Params:
         p.base_score = kw["base_score"]
         p.has_base_score = 1
     p.nthread = kw.get("nthread", 1)
+    p.num_class = kw.get("num_class", 0)
     return p
 
 
@@ -264,6 +270,16 @@ class Model:
         return out
 
     @property
+    def num_outputs(self) -> int:
+        return lib().orc_model_num_outputs(self.h)
+
+    def class_margins(self) -> np.ndarray:
+        out = np.zeros(self.num_outputs, np.float32)
+        if self.num_outputs > 1:
+            lib().orc_model_class_margins(self.h, _p(out))
+        return out
+
+    @property
     def base_score(self) -> float:
         return lib().orc_model_base_score(self.h)
 
@@ -276,13 +292,17 @@ class Model:
         return lib().orc_model_train_seconds(self.h)
 
     def predict_margin(self, x: np.ndarray) -> np.ndarray:
+        """Margins, [n] (or [n, K] for a multiclass model)."""
         x = np.ascontiguousarray(x, np.float32)
-        out = np.zeros(x.shape[0], np.float32)
+        k = self.num_outputs
+        out = np.zeros((x.shape[0], k) if k > 1 else x.shape[0], np.float32)
         lib().orc_predict_margin(self.h, _p(x), x.shape[0], x.shape[1], _p(out))
         return out
 
     def train_margins(self, n: int) -> np.ndarray:
-        out = np.zeros(n, np.float32)
+        """Training margins, [n] (or class-major [K, n] for a multiclass model)."""
+        k = self.num_outputs
+        out = np.zeros((k, n) if k > 1 else n, np.float32)
         lib().orc_model_train_margins(self.h, _p(out))
         return out
 

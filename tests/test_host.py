@@ -119,7 +119,11 @@ def _tiny():
 @pytest.mark.parametrize("params, msg", [
     ({"device": "cpu"}, "device"),
     ({"device": "tpu"}, "device"),
-    ({"objective": "multi:softprob"}, "objective"),
+    ({"objective": "reg:quantileerror"}, "objective"),
+    ({"objective": "multi:softprob"}, "num_class >= 2"),
+    ({"objective": "multi:softmax", "num_class": 1}, "num_class >= 2"),
+    ({"objective": "multi:softprob", "num_class": 2.5}, "num_class must be an integer"),
+    ({"objective": "multi:softprob", "num_class": -3}, "num_class must not be negative"),
     ({"grow_policy": "levelwise"}, "grow_policy"),
     ({"max_bin": 0}, "max_bin"),
     ({"max_bin": 70000}, "max_bin"),
