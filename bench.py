@@ -43,6 +43,12 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
+# VALU issue peak: 256 CUs x 64 lanes x 2.4 GHz, one fp32 operation a lane a cycle (the
+# kernels are built without FMA contraction and without packed fp32).
+VALU_PEAK_TOPS = 39.3
+# TreeSHAP of the 100-tree depth-8 ensemble: VALU lane-operations a row, counted by
+# SQ_INSTS_VALU x 64 / rows for shap_rec_kernel on the shap workload.
+SHAP_VALU_OPS_PER_ROW = 11.23e6
 METRIC = "histogram build GB/s (% HBM peak) + boosting rounds/sec, 10.5M×28 u8 bins depth 8"
 
 
@@ -357,6 +363,7 @@ def shap_workload(args):
     # bytes the kernel must move: the row in, its contributions out
     per_row = 4 * X.shape[1] + 4 * (X.shape[1] + 1)
     gbps = args.steps * n_rows * per_row / (kernel_ms * 1e-3) / 1e9
+    tops = rows_per_s * SHAP_VALU_OPS_PER_ROW / 1e12
     margin = model.predict(X[:20000], output_margin=True)
     additivity = float(np.max(np.abs(phi[:20000].sum(axis=1) - margin)))
 
@@ -380,8 +387,10 @@ def shap_workload(args):
     out = base_line(args, round(rows_per_s, 1), "rows/s", round(kernel_ms / args.steps, 3),
                     config, dtype="f32")
     out.update({
-        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 5), "traffic": None},
+        "roofline": {"bound": "valu", "achieved": round(tops, 2), "peak": VALU_PEAK_TOPS,
+                     "unit": "T lane-ops/s", "frac": round(tops / VALU_PEAK_TOPS, 4),
+                     "traffic": None, "ops_per_row": SHAP_VALU_OPS_PER_ROW,
+                     "hbm_gbps": round(gbps, 2)},
         "pcie_inclusive_rows_per_s": round(args.steps * n_rows / wall, 1),
         "additivity_max_abs": additivity,
         "cpu_baseline": cpu,
