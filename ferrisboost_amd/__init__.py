@@ -34,6 +34,7 @@ __version__ = "0.1.0"
 _DEFAULTS: dict[str, Any] = {
     "objective": "binary:logistic",
     "num_class": None,
+    "quantile_alpha": None,
     "max_depth": 6,
     "max_leaves": 0,
     "grow_policy": "depthwise",
@@ -90,7 +91,7 @@ _ALIASES = {
 }
 
 _OBJECTIVES = {"reg:squarederror": 0, "binary:logistic": 1, "multi:softprob": 2,
-               "multi:softmax": 3}
+               "multi:softmax": 3, "reg:quantileerror": 4}
 _OBJECTIVE_NAMES = {v: k for k, v in _OBJECTIVES.items()}
 _GROW = {"depthwise": 0, "lossguide": 1}
 
@@ -149,6 +150,7 @@ def _normalize(params: Mapping[str, Any], num_boost_round: int) -> dict[str, Any
             raise ValueError("num_class must not be negative")
     if str(out["objective"]).startswith("multi:") and (out["num_class"] or 0) < 2:
         raise ValueError(f"{out['objective']} requires num_class >= 2, got {out['num_class']}")
+    out["quantile_alpha"] = _normalize_quantile_alpha(out["quantile_alpha"], out["objective"])
     if out["grow_policy"] not in _GROW:
         raise ValueError(f"grow_policy must be depthwise or lossguide, got {out['grow_policy']!r}")
     if not 0 < int(out["max_bin"]) <= 65535:
@@ -197,6 +199,35 @@ def _normalize(params: Mapping[str, Any], num_boost_round: int) -> dict[str, Any
     return out
 
 
+def _normalize_quantile_alpha(value: Any, objective: str) -> list[float] | None:
+    """quantile_alpha (python/ferrisboost/__init__.py:362-383): required by
+    reg:quantileerror (XGBoost has no default); a scalar is a one-element
+    list; several values train one output (one tree a round) per quantile;
+    each in [0, 1], ascending, at most 64."""
+    if value is None:
+        if objective == "reg:quantileerror":
+            raise ValueError(
+                "reg:quantileerror needs quantile_alpha (one or more ascending quantiles in [0, 1], "
+                "e.g. 0.9 or [0.1, 0.5, 0.9])"
+            )
+        return None
+    if isinstance(value, (list, tuple, np.ndarray)):
+        flat = np.asarray(value, dtype=np.float64).ravel().tolist()
+    else:
+        flat = [float(value)]
+    if not flat:
+        raise ValueError("quantile_alpha must not be an empty list")
+    for alpha in flat:
+        if not 0.0 <= alpha <= 1.0:
+            raise ValueError(f"quantile_alpha must be in [0, 1], got {alpha}")
+    if any(a > b for a, b in zip(flat, flat[1:])):
+        raise ValueError(
+            f"quantile_alpha must be in ascending order (as XGBoost requires), got {flat}")
+    if len(flat) > 64:
+        raise ValueError(f"quantile_alpha accepts at most 64 quantiles, got {len(flat)}")
+    return flat
+
+
 def _params_struct(p: dict[str, Any], n_features: int) -> N.TrainParams:
     s = N.TrainParams()
     s.n_rounds = p["num_boost_round"]
@@ -217,6 +248,11 @@ def _params_struct(p: dict[str, Any], n_features: int) -> N.TrainParams:
     s.seed = int(p["seed"]) & 0xFFFFFFFFFFFFFFFF
     s.objective = _OBJECTIVES[p["objective"]]
     s.num_class = int(p["num_class"] or 0) if p["objective"].startswith("multi:") else 0
+    if p["objective"] == "reg:quantileerror":
+        alphas = np.ascontiguousarray(p["quantile_alpha"], np.float32)
+        s._alphas = alphas  # the struct points into it
+        s.n_quantile_alpha = alphas.size
+        s.quantile_alpha = alphas.ctypes.data_as(C.POINTER(C.c_float))
     s.grow_policy = _GROW[p["grow_policy"]]
     s.max_cat_to_onehot = int(p["max_cat_to_onehot"])
     s.max_cat_threshold = int(p["max_cat_threshold"])
@@ -292,11 +328,24 @@ class Model:
 
     @property
     def num_class(self) -> int:
-        """Outputs per row: num_class of a multiclass model, else 1."""
+        """Outputs per row: num_class of a multiclass model, the number of
+        quantile_alpha of a reg:quantileerror model, else 1."""
         return N.train_lib().fbt_model_num_outputs(self._h)
 
+    @property
+    def quantile_alpha(self) -> list[float] | None:
+        """reg:quantileerror's quantiles; None for other models
+        (src/python/mod.rs:3159-3166)."""
+        L = N.train_lib()
+        k = L.fbt_model_quantile_alpha(self._h, None, 0)
+        if k == 0:
+            return None
+        out = np.zeros(k, np.float32)
+        L.fbt_model_quantile_alpha(self._h, N.ptr(out), k)
+        return [float(v) for v in out]
+
     def class_margins(self) -> np.ndarray:
-        """A multiclass model's per-class intercepts (empty otherwise)."""
+        """A multi-output model's per-output intercepts (empty otherwise)."""
         k = self.num_class
         out = np.zeros(k if k > 1 else 0, np.float32)
         if k > 1:
@@ -306,10 +355,6 @@ class Model:
     @property
     def feature_names(self) -> list[str]:
         return []
-
-    @property
-    def quantile_alpha(self):
-        return None
 
     @property
     def best_iteration(self):

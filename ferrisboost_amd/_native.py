@@ -161,6 +161,8 @@ class TrainParams(C.Structure):
         ("resident_limit", C.c_uint32),
         ("host_binning", C.c_uint32),
         ("host_sketch", C.c_uint32),
+        ("n_quantile_alpha", C.c_uint32),
+        ("quantile_alpha", C.POINTER(C.c_float)),
     ]
 
 
@@ -215,7 +217,8 @@ HIP_SYMBOLS = [
     "fbh_sketch_create", "fbh_sketch_push_rows", "fbh_sketch_cuts", "fbh_sketch_destroy",
     "fbh_upload_quantize_gpair",
     "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_set_multiclass",
-    "fbh_multiclass_begin_round", "fbh_set_output", "fbh_gradient_exchange",
+    "fbh_multiclass_begin_round", "fbh_set_output", "fbh_set_quantile",
+    "fbh_quantile_last_scale", "fbh_tanh_checksum", "fbh_gradient_exchange",
     "fbh_download_margin", "fbh_set_gpu_math", "fbh_gradient_pairs", "fbh_sigmoid_host", "fbh_sigmoid_device", "fbh_sigmoid_checksum",
     "fbh_begin_tree", "fbh_eval_nodes", "fbh_download_histogram",
     "fbh_partition", "fbh_partition_eval", "fbh_grow_depthwise", "fbh_grow_depthwise_async",
@@ -233,7 +236,7 @@ TRAIN_SYMBOLS = [
     "fbt_model_train_margins", "fbt_model_n_cuts", "fbt_model_cuts", "fbt_predict_margin",
     "fbt_model_to_json", "fbt_shap", "fbt_last_shap_ms", "fbt_sketch_cuts", "fbt_predict",
     "fbt_model_from_json", "fbt_model_objective", "fbt_model_scale_pos_weight",
-    "fbt_model_num_outputs", "fbt_model_class_margins",
+    "fbt_model_num_outputs", "fbt_model_class_margins", "fbt_model_quantile_alpha",
     "fbt_model_is_categorical",
 ]
 
@@ -296,6 +299,9 @@ def hip() -> C.CDLL:
         L.fbh_set_multiclass.argtypes = [P, C.c_uint32, P, P, P]
         L.fbh_multiclass_begin_round.argtypes = [P]
         L.fbh_set_output.argtypes = [P, C.c_uint32]
+        L.fbh_set_quantile.argtypes = [P, C.c_uint32, P, P, P, P]
+        L.fbh_quantile_last_scale.argtypes = [P, P]
+        L.fbh_tanh_checksum.argtypes = [C.c_int, C.c_uint64, C.c_uint64, P]
         L.fbh_gradient_exchange.argtypes = [P, P, P, C.c_uint64, C.c_uint64, C.c_uint64, P, P]
         L.fbh_download_margin.argtypes = [P, P]
         L.fbh_set_gpu_math.argtypes = [P, C.c_uint32]
@@ -387,6 +393,8 @@ def train_lib() -> C.CDLL:
         L.fbt_model_num_outputs.restype = C.c_uint32
         L.fbt_model_class_margins.argtypes = [P, P]
         L.fbt_model_class_margins.restype = None
+        L.fbt_model_quantile_alpha.argtypes = [P, P, C.c_uint32]
+        L.fbt_model_quantile_alpha.restype = C.c_uint32
         L.fbt_model_scale_pos_weight.argtypes = [P]
         L.fbt_model_scale_pos_weight.restype = C.c_float
         L.fbt_model_is_categorical.argtypes = [P, C.c_uint32]

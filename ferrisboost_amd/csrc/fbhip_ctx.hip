@@ -220,6 +220,7 @@ struct fbh_ctx {
     bool f32_hist() const { return tiles.size() <= F32_PAIR_MAX_TILES; }
     // launch_gradient mode of the device objective.
     int gradient_mode() const {
+        if (objective == 3) return 6;
         if (objective == 2) return fast_math ? 5 : 4;
         return objective == 0 ? 0 : (fast_math ? 3 : 2);
     }
@@ -346,10 +347,15 @@ struct fbh_ctx {
     double scales[2] = {1.0, 1.0};
 
     // objective state on the device (fbh_set_objective, fbh_set_multiclass)
-    int objective = -1;                 // -1 none, 0 squared error, 1 logistic, 2 softmax
+    int objective = -1;                 // -1 none, 0 squared error, 1 logistic, 2 softmax,
+                                        // 3 quantile
     uint32_t n_outputs = 1;             // margin columns (class-major), as planned
     uint32_t out_k = 0;                 // the column gradients read and leaves update
     float2 *softmax_stats = nullptr;    // per-row (wmax, wsum) of the round (softmax)
+    float2 *quantile_slot = nullptr;    // (scale, alpha) of the current output (quantile)
+    std::vector<float> alphas;          // quantile_alpha of each output
+    double quantile_sum_w = 0.0;        // the serial double sum of the weights (or n)
+    float quantile_scale = 0.0f;        // the last scale taken (exact mode)
     float *cur_margin() const { return margin + (uint64_t)out_k * n_rows; }
     bool fast_math = false;             // gpu_math="fast": hardware exp in the logistic gradient
     float *labels = nullptr, *gweights = nullptr, *margin = nullptr;
@@ -1488,7 +1494,9 @@ int fbh_set_objective(fbh_ctx *c, uint32_t objective, const float *labels,
         if (!c || !labels) throw InputError("null argument");
         if (objective > 1) throw InputError("objective must be 0 (squared error) or 1 (logistic)");
         if (c->n_outputs != 1)
-            throw InputError("a context planned for several outputs takes fbh_set_multiclass");
+            throw InputError("a context planned for several outputs takes fbh_set_multiclass "
+                             "or fbh_set_quantile");
+        if (c->objective > 1) throw InputError("the context already holds another objective");
         check(hipSetDevice(c->device), "hipSetDevice");
         if (c->objective < 0) {
             c->labels = c->alloc<float>(c->n_rows, "labels");
@@ -1554,6 +1562,103 @@ int fbh_set_multiclass(fbh_ctx *c, uint32_t n_classes, const float *labels,
         c->out_k = 0;
         c->ids_fresh = false;
     });
+}
+
+int fbh_set_quantile(fbh_ctx *c, uint32_t n_alphas, const float *alphas, const float *labels,
+                     const float *weights, const float *intercepts) {
+    return guard([&] {
+        if (!c || !alphas || !labels || !intercepts) throw InputError("null argument");
+        if (n_alphas == 0) throw InputError("reg:quantileerror needs at least one quantile_alpha");
+        if (n_alphas != c->n_outputs)
+            throw InputError("the context was planned for " + std::to_string(c->n_outputs) +
+                             " outputs, not " + std::to_string(n_alphas) + " quantiles");
+        for (uint32_t k = 0; k < n_alphas; k++) {
+            if (!(alphas[k] >= 0.0f && alphas[k] <= 1.0f))
+                throw InputError("quantile_alpha must be in [0, 1]");
+            if (k && alphas[k - 1] > alphas[k])
+                throw InputError("quantile_alpha must be in ascending order");
+        }
+        check(hipSetDevice(c->device), "hipSetDevice");
+        if (c->objective < 0) {
+            c->labels = c->alloc<float>(c->n_rows, "labels");
+            c->margin = c->alloc<float>((uint64_t)n_alphas * c->n_rows, "quantile margins");
+            c->leaf_ids = c->alloc<uint16_t>(c->n_rows, "leaf ids");
+            c->quantile_slot = c->alloc<float2>(1, "quantile scale");
+            c->pinned(c->pin_src, std::max<uint64_t>(4 * c->n_rows, 64));
+        } else if (c->objective != 3) {
+            throw InputError("the context already holds another objective");
+        }
+        if (weights && !c->gweights) c->gweights = c->alloc<float>(c->n_rows, "row weights");
+        c->sync();
+        check(hipMemcpy(c->labels, labels, 4 * c->n_rows, hipMemcpyHostToDevice), "label upload");
+        c->has_weights = weights != nullptr;
+        // Objective::quantile_scale's denominator: n, or the weights summed
+        // in row order in double.
+        double sw = 0.0;
+        if (weights) {
+            check(hipMemcpy(c->gweights, weights, 4 * c->n_rows, hipMemcpyHostToDevice),
+                  "weight upload");
+            for (uint64_t i = 0; i < c->n_rows; i++) sw += (double)weights[i];
+        } else {
+            sw = (double)c->n_rows;
+        }
+        c->quantile_sum_w = sw;
+        for (uint32_t k = 0; k < n_alphas; k++)
+            check(launch_fill_f32(c->margin + (uint64_t)k * c->n_rows, intercepts[k], c->n_rows,
+                                  c->stream),
+                  "margin init");
+        c->sync();
+        c->alphas.assign(alphas, alphas + n_alphas);
+        c->objective = 3;
+        c->out_k = 0;
+        c->ids_fresh = false;
+    });
+}
+
+int fbh_quantile_last_scale(fbh_ctx *c, float *scale) {
+    return guard([&] {
+        if (!c || !scale) throw InputError("null argument");
+        if (c->objective != 3) throw InputError("fbh_set_quantile has not been called");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        float2 v;
+        check(hipMemcpyAsync(&v, c->quantile_slot, sizeof(v), hipMemcpyDeviceToHost, c->stream),
+              "scale download");
+        c->sync();
+        *scale = v.x;
+    });
+}
+
+// The round's scale of the current output (Objective::quantile_scale,
+// src/training/objective.rs:1115-1137) into the (scale, alpha) slot the
+// gradient reads. Exact: each row's f32 term on the device, summed on the
+// host in row order in double (the reference's serial sum, which no parallel
+// order reproduces). Fast: a fixed-order reduction on the device.
+static void quantile_take_scale(fbh_ctx *c) {
+    const float *w = c->has_weights ? c->gweights : nullptr;
+    const float alpha = c->alphas[c->out_k];
+    const uint64_t n = c->n_rows;
+    if (c->fast_math) {
+        check(launch_quantile_scale_fast(c->cur_margin(), c->labels, w, n, alpha, c->red_f64,
+                                         c->quantile_slot, c->stream),
+              "quantile scale");
+        return;
+    }
+    float *terms = c->gpair_f32;  // rewritten by the gradient pass that follows
+    check(launch_quantile_terms(c->cur_margin(), c->labels, w, n, terms, c->stream),
+          "quantile terms");
+    float *host = static_cast<float *>(c->pin_src.p);
+    check(hipMemcpyAsync(host, terms, 4 * n, hipMemcpyDeviceToHost, c->stream),
+          "quantile terms download");
+    c->sync();
+    double stat = 0.0;
+    for (uint64_t i = 0; i < n; i++) stat += (double)host[i];
+    float scale = 0.0f;
+    if (!(std::fabs(c->quantile_sum_w) < 1e-6)) {
+        const double root_mean = stat / c->quantile_sum_w;
+        scale = (float)(root_mean * root_mean);
+    }
+    c->quantile_scale = scale;
+    check(launch_quantile_set(c->quantile_slot, scale, alpha, c->stream), "quantile scale");
 }
 
 int fbh_multiclass_begin_round(fbh_ctx *c) {
@@ -1635,6 +1740,9 @@ int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th
             c->leaves_pending = false;
         }
         const float *w = c->has_weights ? c->gweights : nullptr;
+        if (c->objective == 3) quantile_take_scale(c);
+        // Mode 6 reads (scale, alpha) from the slot; softmax reads row statistics.
+        const float2 *stats = c->objective == 3 ? c->quantile_slot : c->softmax_stats;
         if (!scales_out) {
             // Everything stays on the device: the pairs' quantisation under
             // the previous round's scales, with its block sums, redone only
@@ -1644,8 +1752,8 @@ int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th
             check(launch_gradient_spec(c->cur_margin(), c->labels, w, c->n_rows,
                                        c->gradient_mode(), th, seed, tree, c->red_f64,
                                        c->n_red_blocks, c->d_scales, c->gpair, c->red_i64,
-                                       f32 ? c->gpair_f32 : nullptr, c->stream,
-                                       c->softmax_stats, c->out_k),
+                                       f32 ? c->gpair_f32 : nullptr, c->stream, stats,
+                                       c->out_k),
                   "device gradient");
             c->ids_fresh = false;
             c->root_on_device = true;
@@ -1656,7 +1764,7 @@ int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th
             // Squared error, softmax, or logistic with the device sigmoid.
             check(launch_gradient(c->cur_margin(), c->labels, w, c->n_rows, c->gradient_mode(),
                                   c->gpair_f32, th, seed, tree, c->red_f64, c->n_red_blocks,
-                                  c->stream, c->softmax_stats, c->out_k),
+                                  c->stream, stats, c->out_k),
                   "device gradient");
         } else {
             const uint64_t n = c->n_rows;
@@ -3136,21 +3244,28 @@ int fbh_sigmoid_device(int device, const float *in, uint64_t n, float *out) {
     });
 }
 
+static void function_checksum(int device, uint64_t begin, uint64_t end, uint64_t *out,
+                              bool tanh) {
+    if (!out) throw InputError("null argument");
+    if (end > (1ull << 32) || begin > end) throw InputError("range must lie in [0, 2^32]");
+    check(hipSetDevice(device), "hipSetDevice");
+    unsigned long long *d = nullptr;
+    check(hipMalloc(&d, 8), "device allocation");
+    std::unique_ptr<unsigned long long, hipError_t (*)(void *)> own(d, hipFree);
+    const unsigned long long zero = 0;
+    check(hipMemcpy(d, &zero, 8, hipMemcpyHostToDevice), "clear");
+    check(launch_sigmoid_checksum(begin, end, d, nullptr, tanh), "checksum");
+    unsigned long long v = 0;
+    check(hipMemcpy(&v, d, 8, hipMemcpyDeviceToHost), "checksum download");
+    *out = v;
+}
+
+int fbh_tanh_checksum(int device, uint64_t begin, uint64_t end, uint64_t *out) {
+    return guard([&] { function_checksum(device, begin, end, out, true); });
+}
+
 int fbh_sigmoid_checksum(int device, uint64_t begin, uint64_t end, uint64_t *out) {
-    return guard([&] {
-        if (!out) throw InputError("null argument");
-        if (end > (1ull << 32) || begin > end) throw InputError("range must lie in [0, 2^32]");
-        check(hipSetDevice(device), "hipSetDevice");
-        unsigned long long *d = nullptr;
-        check(hipMalloc(&d, 8), "device allocation");
-        std::unique_ptr<unsigned long long, hipError_t (*)(void *)> own(d, hipFree);
-        const unsigned long long zero = 0;
-        check(hipMemcpy(d, &zero, 8, hipMemcpyHostToDevice), "clear");
-        check(launch_sigmoid_checksum(begin, end, d, nullptr), "sigmoid checksum");
-        unsigned long long v = 0;
-        check(hipMemcpy(&v, d, 8, hipMemcpyDeviceToHost), "checksum download");
-        *out = v;
-    });
+    return guard([&] { function_checksum(device, begin, end, out, false); });
 }
 
 int fbh_build_histogram(int device, const void *bins, uint32_t width, uint64_t n_rows,

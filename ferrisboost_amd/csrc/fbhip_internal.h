@@ -423,7 +423,16 @@ hipError_t launch_softmax_stats(const float *margin, uint32_t K, uint64_t n, int
                                 float2 *stats, hipStream_t s);
 hipError_t launch_sigmoid(const float *in, uint64_t n, float *out, hipStream_t s);
 hipError_t launch_sigmoid_checksum(uint64_t begin, uint64_t end, unsigned long long *out,
-                                   hipStream_t s);
+                                   hipStream_t s, bool tanh = false);
+// reg:quantileerror: the scale's per-row terms (exact: summed on the host),
+// the (scale, alpha) slot the gradient's mode 6 reads, and the fast mode's
+// fixed-order device reduction into that slot (partials: 512 doubles).
+hipError_t launch_quantile_terms(const float *margin, const float *y, const float *w, uint64_t n,
+                                 float *out, hipStream_t s);
+hipError_t launch_quantile_set(float2 *slot, float scale, float alpha, hipStream_t s);
+hipError_t launch_quantile_scale_fast(const float *margin, const float *y, const float *w,
+                                      uint64_t n, float alpha, double *partials, float2 *slot,
+                                      hipStream_t s);
 hipError_t launch_fill_f32(float *p, float v, uint64_t n, hipStream_t s);
 hipError_t launch_init_rows(uint32_t *rows, float *delta, uint64_t n, hipStream_t s);
 // The gradients of a round quantized in the same pass under the previous

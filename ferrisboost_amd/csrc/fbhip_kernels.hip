@@ -18,6 +18,7 @@
 //   shap_kernel          QuadratureTreeSHAP (explain.rs:303-401, 704-728)
 
 #include "fb_expf.h"
+#include "fb_tanhf.h"
 #include "fbhip_internal.h"
 #include "fbhip_quant.h"
 
@@ -1927,10 +1928,34 @@ __device__ __forceinline__ float objective_source(int mode, float v) {
 // statistics st = (wmax, wsum) (Objective::softmax_gradients,
 // src/training/objective.rs:1175-1219; 4: glibc's expf restated, 5: the
 // hardware exp): p = exp(m - wmax) / wsum, h = max(2 p (1 - p) w, 1e-16),
-// g = (p - [y == cls]) w.
+// g = (p - [y == cls]) w. Mode 6: reg:quantileerror under the round's
+// (scale S, alpha) in stats[0] (Objective::quantile_gradient,
+// objective.rs:1142-1160): x = (m - y) / (0.04 S),
+// g = S/2 (tanh x + 1 - 2 alpha), h = 12.5 max(tanh x / x, 3e-4) (1 at
+// x = 0), both times the weight, (0, 0) unless S > 0; tanh is glibc's tanhf
+// restated, the host's values bit for bit.
 __device__ __forceinline__ void row_pair(int mode, float s, float y, bool has_w, float w,
                                          const float2 *stats, uint32_t cls, uint64_t i, float &g,
                                          float &h) {
+    if (mode == 6) {
+        const float2 q = stats[0];
+        const float scale = q.x, alpha = q.y;
+        if (!(scale > 0.0f)) {
+            g = h = 0.0f;
+            return;
+        }
+        const float x = (s - y) / (0.04f * scale);
+        const float t = fb_tanhf(x);
+        float ratio = x == 0.0f ? 1.0f : t / x;
+        ratio = fmaxf(ratio, 3.0e-4f);
+        g = 0.5f * scale * (t + 1.0f - 2.0f * alpha);
+        h = 0.5f / 0.04f * ratio;
+        if (has_w) {
+            g = g * w;
+            h = h * w;
+        }
+        return;
+    }
     if (mode >= 4) {
         const float2 st = stats[i];
         const float e = mode == 4 ? fb_expf(s - st.x) : __expf(s - st.x);
@@ -1968,6 +1993,110 @@ __global__ __launch_bounds__(256) void softmax_stats_kernel(const float *margin,
         }
         stats[i] = make_float2(wmax, (float)wsum);
     }
+}
+
+// The terms of the quantile scale (Objective::quantile_scale,
+// objective.rs:1115-1137): per row the f32 value w * sqrtf|m - y| (sqrtf|m - y|
+// without weights), which the host sums in row order in double.
+__global__ __launch_bounds__(256) void quantile_terms_kernel(const float *margin, const float *y,
+                                                             const float *w, uint64_t n,
+                                                             float *out) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const float r = sqrtf(fabsf(margin[i] - y[i]));
+        out[i] = w ? w[i] * r : r;
+    }
+}
+
+hipError_t launch_quantile_terms(const float *margin, const float *y, const float *w, uint64_t n,
+                                 float *out, hipStream_t s) {
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((n + 255) / 256, 8192);
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(quantile_terms_kernel, dim3(blocks), dim3(256), 0, s, margin, y, w, n, out);
+    return hipGetLastError();
+}
+
+__global__ void quantile_set_kernel(float2 *slot, float scale, float alpha) {
+    if (threadIdx.x == 0) slot[0] = make_float2(scale, alpha);
+}
+
+hipError_t launch_quantile_set(float2 *slot, float scale, float alpha, hipStream_t s) {
+    hipLaunchKernelGGL(quantile_set_kernel, dim3(1), dim3(64), 0, s, slot, scale, alpha);
+    return hipGetLastError();
+}
+
+// gpu_math="fast": the scale on the device in a fixed order (the reference's
+// quantile_apply_delta_partials / quantile_reduce_scale,
+// src/backend/cuda/histogram.cu:907-1010): each of QUANTILE_BLOCKS x 256
+// threads sums its grid-stride rows in double, a fixed tree sums each
+// block, and one workgroup sums the block partials the same way, so every
+// run gives the same scale (not the host's serial sum).
+constexpr uint32_t QUANTILE_BLOCKS = 256;
+
+__global__ __launch_bounds__(256) void quantile_partials_kernel(const float *margin,
+                                                                const float *y, const float *w,
+                                                                uint64_t n, double *partials) {
+    __shared__ double rs[256], rw[256];
+    double stat = 0.0, sum_w = 0.0;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const float r = sqrtf(fabsf(margin[i] - y[i]));
+        if (w) {
+            stat += (double)(w[i] * r);
+            sum_w += (double)w[i];
+        } else {
+            stat += (double)r;
+        }
+    }
+    rs[threadIdx.x] = stat;
+    rw[threadIdx.x] = sum_w;
+    __syncthreads();
+    for (uint32_t k = 128; k > 0; k >>= 1) {
+        if (threadIdx.x < k) {
+            rs[threadIdx.x] += rs[threadIdx.x + k];
+            rw[threadIdx.x] += rw[threadIdx.x + k];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        partials[2 * blockIdx.x] = rs[0];
+        partials[2 * blockIdx.x + 1] = rw[0];
+    }
+}
+
+__global__ __launch_bounds__(256) void quantile_reduce_kernel(const double *partials,
+                                                              uint64_t n, int weighted,
+                                                              float alpha, float2 *slot) {
+    __shared__ double rs[256], rw[256];
+    rs[threadIdx.x] = partials[2 * threadIdx.x];
+    rw[threadIdx.x] = partials[2 * threadIdx.x + 1];
+    __syncthreads();
+    for (uint32_t k = 128; k > 0; k >>= 1) {
+        if (threadIdx.x < k) {
+            rs[threadIdx.x] += rs[threadIdx.x + k];
+            rw[threadIdx.x] += rw[threadIdx.x + k];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const double total_w = weighted ? rw[0] : (double)n;
+        float scale = 0.0f;
+        if (!(fabs(total_w) < 1e-6)) {
+            const double root_mean = rs[0] / total_w;
+            scale = (float)(root_mean * root_mean);
+        }
+        slot[0] = make_float2(scale, alpha);
+    }
+}
+
+hipError_t launch_quantile_scale_fast(const float *margin, const float *y, const float *w,
+                                      uint64_t n, float alpha, double *partials, float2 *slot,
+                                      hipStream_t s) {
+    hipLaunchKernelGGL(quantile_partials_kernel, dim3(QUANTILE_BLOCKS), dim3(256), 0, s, margin,
+                       y, w, n, partials);
+    hipLaunchKernelGGL(quantile_reduce_kernel, dim3(1), dim3(QUANTILE_BLOCKS), 0, s, partials, n,
+                       w ? 1 : 0, alpha, slot);
+    return hipGetLastError();
 }
 
 hipError_t launch_softmax_stats(const float *margin, uint32_t K, uint64_t n, int fast,
@@ -2116,15 +2245,18 @@ hipError_t launch_sigmoid(const float *in, uint64_t n, float *out, hipStream_t s
     return hipGetLastError();
 }
 
-// Sum over bit patterns u in [begin, end) of mix64(u ^ bits(sigmoid(u)) << 32)
-// (NaN outputs canonicalised), wrapping: a fingerprint of the sigmoid over
-// every float input, compared with the host libm's.
+// Sum over bit patterns u in [begin, end) of mix64(u ^ bits(f(u)) << 32)
+// (NaN outputs canonicalised), wrapping: a fingerprint of the device sigmoid
+// (TANH false) or tanhf (TANH true) over every float input, compared with
+// the host libm's.
+template <bool TANH>
 __global__ __launch_bounds__(256) void sigmoid_checksum_kernel(uint64_t begin, uint64_t end,
                                                                unsigned long long *out) {
     uint64_t acc = 0;
     for (uint64_t u = begin + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; u < end;
          u += (uint64_t)gridDim.x * blockDim.x) {
-        const float s = fb_sigmoid(__builtin_bit_cast(float, (uint32_t)u));
+        const float x = __builtin_bit_cast(float, (uint32_t)u);
+        const float s = TANH ? fb_tanhf(x) : fb_sigmoid(x);
         const uint32_t b = s != s ? 0x7fc00000u : __builtin_bit_cast(uint32_t, s);
         acc += mix64(u ^ ((uint64_t)b << 32));
     }
@@ -2139,10 +2271,15 @@ __global__ __launch_bounds__(256) void sigmoid_checksum_kernel(uint64_t begin, u
 }
 
 hipError_t launch_sigmoid_checksum(uint64_t begin, uint64_t end, unsigned long long *out,
-                                   hipStream_t s) {
+                                   hipStream_t s, bool tanh) {
     if (end <= begin) return hipSuccess;
     const uint32_t blocks = (uint32_t)std::min<uint64_t>((end - begin + 255) / 256, 65536);
-    hipLaunchKernelGGL(sigmoid_checksum_kernel, dim3(blocks), dim3(256), 0, s, begin, end, out);
+    if (tanh)
+        hipLaunchKernelGGL(sigmoid_checksum_kernel<true>, dim3(blocks), dim3(256), 0, s, begin,
+                           end, out);
+    else
+        hipLaunchKernelGGL(sigmoid_checksum_kernel<false>, dim3(blocks), dim3(256), 0, s, begin,
+                           end, out);
     return hipGetLastError();
 }
 

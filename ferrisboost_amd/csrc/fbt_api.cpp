@@ -162,6 +162,12 @@ int fbt_model_train_margins(const fbt_model *m, float *out, uint64_t n) {
 
 uint32_t fbt_model_num_outputs(const fbt_model *m) { return m->m.n_outputs(); }
 
+uint32_t fbt_model_quantile_alpha(const fbt_model *m, float *out, uint32_t cap) {
+    const auto &a = m->m.quantile_alpha;
+    if (out) std::copy(a.begin(), a.begin() + std::min<size_t>(cap, a.size()), out);
+    return (uint32_t)a.size();
+}
+
 void fbt_model_class_margins(const fbt_model *m, float *out) {
     std::copy(m->m.class_margins.begin(), m->m.class_margins.end(), out);
 }
@@ -280,6 +286,20 @@ uint32_t argmax_row(const float *row, uint32_t k) {
     return best;
 }
 
+// sort_row_ascending (src/training/objective.rs:1294-1306): XGBoost's
+// insertion sort with a > comparison, which keeps NaN where it compares.
+void sort_row_ascending(float *row, uint32_t k) {
+    for (uint32_t i = 1; i < k; i++) {
+        const float v = row[i];
+        uint32_t pos = i;
+        while (pos > 0 && row[pos - 1] > v) {
+            row[pos] = row[pos - 1];
+            pos--;
+        }
+        row[pos] = v;
+    }
+}
+
 // A multiclass model's outputs: each class scored or explained by its own
 // trees with its own intercept (Model::class_view, src/model/tree.rs:
 // 395-425), the per-class results laid out [row][class][...].
@@ -335,6 +355,9 @@ void predict_multiclass(const fbt::Model &m, const float *x, uint64_t n_rows, ui
     g_last_shap_ms = ms;
     if (!scores) return;
     if (output == FBT_OUT_MARGIN) {
+        std::memcpy(out, margins.data(), 4 * margins.size());
+    } else if (m.objective == 4) {  // several quantiles: each row ascending (non-crossing)
+        for (uint64_t r = 0; r < n_rows; r++) sort_row_ascending(&margins[r * K], K);
         std::memcpy(out, margins.data(), 4 * margins.size());
     } else if (m.objective == 3) {  // multi:softmax: the class index
         for (uint64_t r = 0; r < n_rows; r++) out[r] = (float)argmax_row(&margins[r * K], K);

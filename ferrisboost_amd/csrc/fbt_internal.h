@@ -84,11 +84,14 @@ struct Tree {
 struct Model {
     std::vector<Tree> trees;
     float base_score = 0.5f;
-    uint32_t objective = 1;  // 0 squared error, 1 logistic, 2 multi:softprob, 3 multi:softmax
-    // A multiclass model's per-class intercepts (class_base_margins,
-    // src/model/tree.rs:256-260); tree t belongs to class t % K. Empty for a
-    // single-output model.
+    uint32_t objective = 1;  // 0 squared error, 1 logistic, 2 multi:softprob, 3 multi:softmax,
+                             // 4 reg:quantileerror
+    // A multiclass (or multi-quantile) model's per-output intercepts
+    // (class_base_margins, src/model/tree.rs:256-260); tree t belongs to
+    // output t % K. Empty for a single-output model.
     std::vector<float> class_margins;
+    // reg:quantileerror's quantile_alpha, one per output (ascending).
+    std::vector<float> quantile_alpha;
     uint32_t n_outputs() const { return class_margins.empty() ? 1u : (uint32_t)class_margins.size(); }
     uint32_t n_features = 0;
     float scale_pos_weight = 1.0f;

@@ -283,6 +283,53 @@ std::vector<float> parse_base_score_vector(const std::string &raw) {
     return v;
 }
 
+// quantile_alphas_from_json (src/training/objective.rs:1015-1036):
+// quantile_loss_param.quantile_alpha as XGBoost's string "[0.1,0.5]" (also
+// "0.9", "(0.9)", "[1E-1,5E-1]"), a number, or an array of numbers; 1 to 64
+// values (QuantileAlphas::new, src/types.rs:700-712). Empty when absent or
+// unreadable.
+std::vector<float> quantile_alphas_from_json(const JVal &obj) {
+    const JVal *blk = obj.get("quantile_loss_param");
+    const JVal *raw = blk ? blk->get("quantile_alpha") : nullptr;
+    if (!raw) return {};
+    std::vector<float> v;
+    auto number = [](const std::string &text, float &out) {
+        const std::string t = trim(text);
+        char *end = nullptr;
+        out = std::strtof(t.c_str(), &end);
+        const bool hex = t.find('x') != std::string::npos || t.find('X') != std::string::npos;
+        return !t.empty() && *end == 0 && !hex;
+    };
+    if (raw->t == JVal::Str) {
+        std::string t = trim(raw->s);
+        size_t b = 0, e = t.size();
+        while (b < e && (t[b] == '[' || t[b] == '(')) b++;
+        while (e > b && (t[e - 1] == ']' || t[e - 1] == ')')) e--;
+        t = t.substr(b, e - b);
+        size_t s0 = 0;
+        while (true) {
+            const size_t c = t.find(',', s0);
+            float x;
+            if (!number(t.substr(s0, c == std::string::npos ? std::string::npos : c - s0), x))
+                return {};
+            v.push_back(x);
+            if (c == std::string::npos) break;
+            s0 = c + 1;
+        }
+    } else if (raw->t == JVal::Num) {
+        v.push_back((float)std::strtod(raw->s.c_str(), nullptr));
+    } else if (raw->t == JVal::Arr) {
+        for (const JVal &x : raw->a) {
+            if (x.t != JVal::Num) return {};
+            v.push_back((float)std::strtod(x.s.c_str(), nullptr));
+        }
+    } else {
+        return {};
+    }
+    if (v.size() > 64) return {};
+    return v;
+}
+
 constexpr int32_t NO_CHILD = -1;
 
 // xgb::Tree::to_tree (src/model/tree.rs:1259-1470).
@@ -429,10 +476,17 @@ Model model_from_json(const char *text, size_t len) {
     else if (oname == "reg:squarederror") m.objective = 0;
     else if (oname == "multi:softprob") m.objective = 2;
     else if (oname == "multi:softmax") m.objective = 3;
+    else if (oname == "reg:quantileerror") m.objective = 4;
     else
         throw bad("objective " + oname +
                   " is not supported; supported: binary:logistic, reg:squarederror, "
-                  "multi:softprob, multi:softmax");
+                  "multi:softprob, multi:softmax, reg:quantileerror");
+    if (m.objective == 4) {
+        m.quantile_alpha = quantile_alphas_from_json(obj);
+        if (m.quantile_alpha.empty())
+            throw bad("objective reg:quantileerror has no readable "
+                      "quantile_loss_param.quantile_alpha");
+    }
     const long long ncp = param_int("num_class", str(req(mp, "num_class", "learner_model_param"), "num_class"));
     const size_t num_class_param = (size_t)std::max(ncp, 1ll);
     size_t num_target = 1;
@@ -440,7 +494,10 @@ Model model_from_json(const char *text, size_t len) {
         const std::string &s = str(*nt, "num_target");
         if (!trim(s).empty()) num_target = (size_t)std::max(param_int("num_target", s), 1ll);
     }
-    if (num_target > 1)
+    // Several targets only as a multi-quantile model, one target per alpha
+    // (src/model/tree.rs:793-802).
+    if (num_target > 1 && !(m.objective == 4 && m.quantile_alpha.size() > 1 &&
+                            num_target == m.quantile_alpha.size()))
         throw bad("multi-target models are not supported (num_target = " +
                   std::to_string(num_target) +
                   "); only reg:quantileerror with multiple quantile_alpha is supported");
@@ -470,8 +527,9 @@ Model model_from_json(const char *text, size_t len) {
     if (param_int("num_parallel_tree", npt) != 1)
         throw bad("num_parallel_tree = " + npt + " (random forest mode) is not supported");
     // num_class must match the objective's outputs (src/model/tree.rs:838-845).
-    const bool multi = m.objective >= 2;
-    if (multi ? num_class < 2 : num_class != 1)
+    const size_t outputs = m.objective == 4 ? m.quantile_alpha.size() : 0;
+    const bool multi = m.objective == 2 || m.objective == 3 || outputs > 1;
+    if (m.objective == 4 ? num_class != outputs : multi ? num_class < 2 : num_class != 1)
         throw bad("num_class = " + std::to_string(num_class) + " is inconsistent with objective " + oname);
     const long long nf = param_int("num_feature", str(req(mp, "num_feature", "learner_model_param"), "num_feature"));
     if (nf < 0 || nf > 0xFFFFFFFFll) throw bad("num_feature out of range");

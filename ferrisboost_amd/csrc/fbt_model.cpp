@@ -279,17 +279,29 @@ std::string model_to_json(const Model &m) {
         }
         bs += "]";
     }
-    const bool multi = m.objective >= 2;
+    // A multiclass model writes num_class; several quantiles are targets:
+    // num_class 0, num_target K (src/model/tree.rs:720-732).
+    const bool multi = m.objective == 2 || m.objective == 3;
+    const bool quantile = m.objective == 4;
     o += "]}},\"learner_model_param\":{\"base_score\":\"" + bs +
          "\",\"boost_from_average\":\"1\",\"num_class\":\"" +
          (multi ? std::to_string(K) : std::string("0")) + "\",\"num_feature\":\"" +
-         std::to_string(m.n_features) + "\",\"num_target\":\"1\"},";
+         std::to_string(m.n_features) + "\",\"num_target\":\"" +
+         (quantile ? std::to_string(K) : std::string("1")) + "\"},";
     o += "\"objective\":{\"name\":\"";
     static const char *const names[] = {"reg:squarederror", "binary:logistic", "multi:softprob",
-                                        "multi:softmax"};
-    o += names[m.objective <= 3 ? m.objective : 0];
-    // Objective::json_params (src/training/objective.rs:772-822).
-    if (multi)
+                                        "multi:softmax", "reg:quantileerror"};
+    o += names[m.objective <= 4 ? m.objective : 0];
+    // Objective::json_params (src/training/objective.rs:772-822): the
+    // quantiles as XGBoost's ParamArray string "[a,b,c]".
+    if (quantile) {
+        std::string qa = "[";
+        for (size_t k = 0; k < m.quantile_alpha.size(); k++) {
+            if (k) qa += ',';
+            qa += display_f32(m.quantile_alpha[k]);
+        }
+        o += "\",\"quantile_loss_param\":{\"quantile_alpha\":\"" + qa + "]\"}}}}";
+    } else if (multi)
         o += "\",\"softmax_multiclass_param\":{\"num_class\":\"" + std::to_string(K) + "\"}}}}";
     else
         o += "\",\"reg_loss_param\":{\"scale_pos_weight\":\"" +

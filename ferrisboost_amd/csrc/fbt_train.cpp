@@ -762,10 +762,27 @@ void validate(const fbt_params &p, uint64_t n, uint32_t nf, const float *y) {
         throw InputError("training data has " + std::to_string(n) +
                          " rows, above the supported limit 4294967295");
     if (nf == 0) throw InputError("training data must have at least one feature");
-    if (p.objective > 3)
-        throw InputError("objective must be reg:squarederror, binary:logistic, multi:softprob or "
-                         "multi:softmax");
-    const bool multi = p.objective >= 2;
+    if (p.objective > 4)
+        throw InputError("objective must be reg:squarederror, binary:logistic, multi:softprob, "
+                         "multi:softmax or reg:quantileerror");
+    const bool multi = p.objective == 2 || p.objective == 3;
+    if (p.objective == 4) {
+        // QuantileAlphas::new and Objective::validate_params
+        // (src/types.rs:700-712, src/training/objective.rs:317-330).
+        if (p.n_quantile_alpha == 0 || !p.quantile_alpha)
+            throw InputError("reg:quantileerror requires quantile_alpha (one or more ascending "
+                             "quantiles in [0, 1])");
+        if (p.n_quantile_alpha > 64)
+            throw InputError("quantile_alpha accepts at most 64 quantiles, got " +
+                             std::to_string(p.n_quantile_alpha));
+        for (uint32_t k = 0; k < p.n_quantile_alpha; k++) {
+            const float a = p.quantile_alpha[k];
+            if (!(a >= 0.0f && a <= 1.0f))
+                throw InputError("quantile_alpha must be in [0, 1], got " + std::to_string(a));
+            if (k && p.quantile_alpha[k - 1] > a)
+                throw InputError("quantile_alpha must be in ascending order (as XGBoost requires)");
+        }
+    }
     if (multi && p.num_class < 2)
         throw InputError(std::string(p.objective == 2 ? "multi:softprob" : "multi:softmax") +
                          " requires num_class >= 2, got " + std::to_string(p.num_class));
@@ -806,6 +823,56 @@ void validate(const fbt_params &p, uint64_t n, uint32_t nf, const float *y) {
                              " labels must be integers in [0, num_class=" +
                              std::to_string(p.num_class) + ")");
     }
+}
+
+// quantile_intercepts (src/training/objective.rs:1039-1087), XGBoost's
+// common::Quantile / WeightedQuantile: the labels stably sorted once in
+// f32::total_cmp order; without weights the order statistic at
+// alpha (n + 1), linearly interpolated in double from the f32 difference;
+// with weights the first label whose f32 running weight reaches
+// alpha * total.
+std::vector<float> quantile_intercepts(const float *alphas, uint32_t k, const float *y,
+                                       const float *w, uint64_t n) {
+    if (n == 0) return std::vector<float>(k, 0.5f);
+    auto key = [](float v) {
+        int32_t b;
+        std::memcpy(&b, &v, 4);
+        return b ^ (int32_t)((uint32_t)(b >> 31) >> 1);
+    };
+    std::vector<uint32_t> idx(n);
+    for (uint64_t i = 0; i < n; i++) idx[i] = (uint32_t)i;
+    std::stable_sort(idx.begin(), idx.end(),
+                     [&](uint32_t a, uint32_t b) { return key(y[a]) < key(y[b]); });
+    std::vector<float> cdf;
+    if (w) {
+        cdf.resize(n);
+        cdf[0] = w[idx[0]];
+        for (uint64_t i = 1; i < n; i++) cdf[i] = cdf[i - 1] + w[idx[i]];
+    }
+    std::vector<float> out(k);
+    for (uint32_t j = 0; j < k; j++) {
+        const double alpha = (double)alphas[j];
+        if (!w) {
+            const double nf = (double)n;
+            if (alpha <= 1.0 / (nf + 1.0)) {
+                out[j] = y[idx[0]];
+            } else if (alpha >= nf / (nf + 1.0)) {
+                out[j] = y[idx[n - 1]];
+            } else {
+                const double x = alpha * (nf + 1.0);
+                const double lo = std::floor(x) - 1.0;
+                const double d = (x - 1.0) - lo;
+                const float v0 = y[idx[(uint64_t)lo]], v1 = y[idx[(uint64_t)lo + 1]];
+                out[j] = (float)((double)v0 + d * (double)(v1 - v0));
+            }
+        } else {
+            const float thresh = (float)((double)cdf[n - 1] * alpha);
+            const uint64_t at = (uint64_t)(std::lower_bound(cdf.begin(), cdf.end(), thresh) -
+                                           cdf.begin());
+            out[j] = y[idx[std::min<uint64_t>(at, n - 1)]];
+        }
+    }
+    return out;
 }
 
 // Objective::initial_class_margins (src/training/objective.rs:1225-1248):
@@ -897,9 +964,19 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     // src/training/mod.rs:1450-1468). A multiclass model keeps one intercept
     // per class: base_score copied, else initial_class_margins
     // (src/training/mod.rs:1430-1449).
-    const bool multi = p.objective >= 2;
-    const uint32_t K = multi ? p.num_class : 1;
-    if (multi) {
+    // reg:quantileerror takes the labels' alpha quantiles (one intercept per
+    // alpha, src/training/objective.rs:452-456, src/training/mod.rs:1442-1444).
+    const bool multi = p.objective == 2 || p.objective == 3;
+    const bool quantile = p.objective == 4;
+    const uint32_t K = multi ? p.num_class : quantile ? p.n_quantile_alpha : 1;
+    std::vector<float> intercepts;
+    if (quantile) {
+        m.quantile_alpha.assign(p.quantile_alpha, p.quantile_alpha + K);
+        intercepts = p.has_base_score ? std::vector<float>(K, p.base_score)
+                                      : quantile_intercepts(p.quantile_alpha, K, y, w, n);
+        if (K > 1) m.class_margins = intercepts;
+        m.base_score = intercepts[0];
+    } else if (multi) {
         m.class_margins = p.has_base_score ? std::vector<float>(K, p.base_score)
                                            : initial_class_margins(y, w, n, K);
         m.base_score = m.class_margins[0];
@@ -929,7 +1006,7 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     // scale_pos_weight folded into the gradient weights (mod.rs:5470-5496).
     std::vector<float> gw;
     const float *grad_w = w;
-    if (p.scale_pos_weight != 1.0f) {
+    if (p.scale_pos_weight != 1.0f && (p.objective == 0 || p.objective == 1)) {
         gw.resize(n);
         for (uint64_t i = 0; i < n; i++) {
             const float wi = w ? w[i] : 1.0f;
@@ -1026,6 +1103,8 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     // train_multiclass_rounds takes the sample weights (scale_pos_weight is
     // a binary objective's).
     if (multi) call(fbh_set_multiclass(ctx.get(), K, y, w, m.class_margins.data()));
+    else if (quantile)
+        call(fbh_set_quantile(ctx.get(), K, p.quantile_alpha, y, w, intercepts.data()));
     else call(fbh_set_objective(ctx.get(), obj, y, grad_w, margin));
     // gpu_math="fast" (fast_gradient_and_quantize, src/backend/cuda/train_ctx.rs:2404-2512):
     // the logistic gradient takes the hardware exponential on the device.
@@ -1079,7 +1158,7 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
         if (multi) call(fbh_multiclass_begin_round(ctx.get()));
         for (uint32_t cls = 0; cls < K; cls++) {
             const uint64_t tree = (uint64_t)round * K + cls;
-            if (multi) call(fbh_set_output(ctx.get(), cls));
+            if (K > 1) call(fbh_set_output(ctx.get(), cls));
             const auto tg = Clock::now();
             double scales[2];
             int64_t root_sum[2];

@@ -351,9 +351,28 @@ int fbh_set_multiclass(fbh_ctx *ctx, uint32_t n_classes, const float *labels,
  * glibc's expf restated (gpu_math exact, the host's values bit for bit) or
  * the hardware exponential (fast). */
 int fbh_multiclass_begin_round(fbh_ctx *ctx);
-/* The output (class) the next gradient call computes the pairs of and whose
- * margin column the next tree's leaves update. */
+/* The output (class or quantile) the next gradient call computes the pairs
+ * of and whose margin column the next tree's leaves update. */
 int fbh_set_output(fbh_ctx *ctx, uint32_t output);
+
+/* reg:quantileerror (Objective::quantile_gradient / quantile_scale,
+ * src/training/objective.rs:1002-1160; train_multiclass_rounds with several
+ * quantile_alpha, src/training/mod.rs:2578-2890; the fast path's
+ * quantile_apply_delta_partials / quantile_reduce_scale /
+ * quantile_gradient_rows, src/backend/cuda/histogram.cu:907-1077): one margin
+ * column per alpha (ascending, in [0, 1]), each starting at its intercept;
+ * weights (may be NULL) are the sample weights. The context must have been
+ * created with cfg->n_outputs equal to n_alphas. Every fbh_gradient_exchange
+ * first takes the round's scale S = (sum w sqrtf|m - y| / sum w)^2 of the
+ * current output's column: gpu_math exact sums the f32 terms on the host in
+ * row order in double (the reference's serial sum, bit for bit; one
+ * device-to-host copy of 4 bytes a row), fast sums them on the device in a
+ * fixed order (deterministic). The pairs use glibc's tanhf restated, so
+ * exact-mode pairs equal the host's bit for bit.
+ * fbh_quantile_last_scale reads back the scale the last gradient call used. */
+int fbh_set_quantile(fbh_ctx *ctx, uint32_t n_alphas, const float *alphas, const float *labels,
+                     const float *weights, const float *intercepts);
+int fbh_quantile_last_scale(fbh_ctx *ctx, float *scale);
 
 /* The logistic sigmoid 1 / (1 + expf(-x)) of Objective::gradient
  * (src/training/objective.rs:37-39) with expf restated from glibc's
@@ -366,6 +385,9 @@ int fbh_set_output(fbh_ctx *ctx, uint32_t output);
 int fbh_sigmoid_host(const float *in, uint64_t n, float *out);
 int fbh_sigmoid_device(int device, const float *in, uint64_t n, float *out);
 int fbh_sigmoid_checksum(int device, uint64_t begin, uint64_t end, uint64_t *out);
+/* The same fingerprint of the device tanhf (glibc's fdlibm-derived tanhf
+ * restated; Objective::quantile_gradient, src/training/objective.rs:1151). */
+int fbh_tanh_checksum(int device, uint64_t begin, uint64_t end, uint64_t *out);
 
 /* ------------------------------------------------------------------ tree */
 /* GpuTrainCtx::begin_tree_rows (src/backend/cuda/train_ctx.rs:1971-1993) plus

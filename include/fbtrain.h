@@ -46,7 +46,8 @@ typedef struct {
     uint32_t cols_per_block;
     uint64_t seed;
     uint32_t objective;        /* 0 = reg:squarederror, 1 = binary:logistic,
-                                  2 = multi:softprob, 3 = multi:softmax */
+                                  2 = multi:softprob, 3 = multi:softmax,
+                                  4 = reg:quantileerror */
     uint32_t grow_policy;      /* 0 = depthwise, 1 = lossguide */
     uint32_t max_cat_to_onehot;
     uint32_t max_cat_threshold;
@@ -82,6 +83,9 @@ typedef struct {
     uint32_t host_sketch;      /* 1: sketch the cuts on the host (0: on the
                                   device for unit row weights when the budget
                                   has room, the same cuts either way) */
+    uint32_t n_quantile_alpha; /* reg:quantileerror: quantiles (1..=64), one
+                                  output and one tree a round each */
+    const float *quantile_alpha; /* ascending, in [0, 1] */
 } fbt_params;
 
 /* One tree node: Node (src/model/tree.rs:52-111). */
@@ -164,11 +168,16 @@ uint32_t fbt_model_n_features(const fbt_model *m);
  * num_class x n_rows class-major for a multiclass model (n_rows is the
  * training row count either way). */
 int fbt_model_train_margins(const fbt_model *m, float *out, uint64_t n_rows);
-/* Outputs per row (num_class of a multiclass model, else 1) and a multiclass
- * model's per-class intercepts (class_base_margins, src/model/tree.rs:
- * 256-260; tree t belongs to class t % num_class). */
+/* Outputs per row (num_class of a multiclass model, the number of
+ * quantile_alpha of a reg:quantileerror model, else 1) and a multi-output
+ * model's per-output intercepts (class_base_margins, src/model/tree.rs:
+ * 256-260; tree t belongs to output t % outputs). */
 uint32_t fbt_model_num_outputs(const fbt_model *m);
 void fbt_model_class_margins(const fbt_model *m, float *out);
+/* A reg:quantileerror model's quantile_alpha (the Python model's
+ * quantile_alpha, src/python/mod.rs:3159-3166): the count, with up to cap
+ * values copied to out (may be NULL); 0 for other objectives. */
+uint32_t fbt_model_quantile_alpha(const fbt_model *m, float *out, uint32_t cap);
 /* Cuts the model was trained with (values, offsets n_features + 1). */
 uint32_t fbt_model_n_cuts(const fbt_model *m);
 void fbt_model_cuts(const fbt_model *m, float *values, uint32_t *offsets);

@@ -868,6 +868,103 @@ std::vector<float> initial_class_margins(const float *y, const float *w, u64 n, 
     return logs;
 }
 
+// reg:quantileerror (src/training/objective.rs:1002-1160, XGBoost 3.4.1's
+// QuantileRegression): a smoothed pinball loss with a majorise-minimise
+// curvature. Each round takes one scale from every row's margin,
+//   S = (sum w sqrtf|p - y| / sum w)^2
+// (f32 terms, a serial double sum), then per row
+//   x = (p - y) / (0.04 S), g = S/2 (tanh x + 1 - 2 alpha),
+//   h = 0.5 / 0.04 max(tanh x / x, 3e-4) (1 at x = 0),
+// both times the sample weight; S <= 0 gives (0, 0). tanh is the host libm's.
+constexpr float QUANTILE_SMOOTHING_SCALE = 0.04f;     // objective.rs:31
+constexpr float QUANTILE_MIN_SURROGATE_RATIO = 3.0e-4f;  // objective.rs:32
+
+// Objective::quantile_scale (objective.rs:1115-1137).
+float quantile_scale(const float *pred, const float *y, const float *w, u64 n) {
+    double stat = 0.0, sum_w = 0.0;
+    if (!w) {
+        for (u64 i = 0; i < n; i++) stat += (double)std::sqrt(std::fabs(pred[i] - y[i]));
+        sum_w = (double)n;
+    } else {
+        for (u64 i = 0; i < n; i++) {
+            stat += (double)(w[i] * std::sqrt(std::fabs(pred[i] - y[i])));
+            sum_w += (double)w[i];
+        }
+    }
+    if (std::fabs(sum_w) < 1e-6) return 0.0f;
+    const double root_mean = stat / sum_w;
+    return (float)(root_mean * root_mean);
+}
+
+// Objective::quantile_gradient (objective.rs:1142-1160), unweighted.
+void quantile_pair(float alpha, float scale, float pred, float label, float &g, float &h) {
+    if (!(scale > 0.0f)) {
+        g = h = 0.0f;
+        return;
+    }
+    const float r = pred - label;
+    const float x = r / (QUANTILE_SMOOTHING_SCALE * scale);
+    const float t = std::tanh(x);
+    float ratio = x == 0.0f ? 1.0f : t / x;
+    ratio = std::fmax(ratio, QUANTILE_MIN_SURROGATE_RATIO);
+    g = 0.5f * scale * (t + 1.0f - 2.0f * alpha);
+    h = 0.5f / QUANTILE_SMOOTHING_SCALE * ratio;
+}
+
+// f32::total_cmp's order as an integer key.
+int32_t total_key(float v) {
+    int32_t b;
+    std::memcpy(&b, &v, 4);
+    return b ^ (int32_t)((uint32_t)(b >> 31) >> 1);
+}
+
+// quantile_intercepts (objective.rs:1039-1087), XGBoost's common::Quantile /
+// WeightedQuantile: labels stably sorted once; unweighted, linear
+// interpolation between order statistics at alpha (n + 1); weighted, the
+// first label whose f32 running weight reaches alpha times the total.
+std::vector<float> quantile_intercepts(const float *alphas, u32 k, const float *y, const float *w,
+                                       u64 n) {
+    if (n == 0) return std::vector<float>(k, 0.5f);
+    std::vector<u64> idx(n);
+    for (u64 i = 0; i < n; i++) idx[i] = i;
+    std::stable_sort(idx.begin(), idx.end(),
+                     [&](u64 a, u64 b) { return total_key(y[a]) < total_key(y[b]); });
+    auto val = [&](u64 i) { return y[idx[i]]; };
+    std::vector<float> cdf;
+    if (w) {
+        cdf.resize(n);
+        cdf[0] = w[idx[0]];
+        for (u64 i = 1; i < n; i++) cdf[i] = cdf[i - 1] + w[idx[i]];
+    }
+    std::vector<float> out(k);
+    for (u32 j = 0; j < k; j++) {
+        const double alpha = (double)alphas[j];
+        if (!w) {
+            const double nf = (double)n;
+            if (alpha <= 1.0 / (nf + 1.0)) {
+                out[j] = val(0);
+                continue;
+            }
+            if (alpha >= nf / (nf + 1.0)) {
+                out[j] = val(n - 1);
+                continue;
+            }
+            const double x = alpha * (nf + 1.0);
+            const double kk = std::floor(x) - 1.0;
+            const double d = (x - 1.0) - kk;
+            const float v0 = val((u64)kk), v1 = val((u64)kk + 1);
+            out[j] = (float)((double)v0 + d * (double)(v1 - v0));
+        } else {
+            const float thresh = (float)((double)cdf[n - 1] * alpha);
+            u64 at = (u64)(std::lower_bound(cdf.begin(), cdf.end(), thresh,
+                                            [](float c, float t) { return c < t; }) -
+                           cdf.begin());
+            out[j] = val(std::min<u64>(at, n - 1));
+        }
+    }
+    return out;
+}
+
 float base_margin_of(u32 obj, float bs) {  // objective.rs:363-398
     if (obj == 1) {
         float x = std::min(std::max(bs, K_RT_EPS), 1.0f - K_RT_EPS);
@@ -976,6 +1073,7 @@ struct orc_model {
     float base_score = 0.5f;
     u32 objective = 1;
     std::vector<float> class_margins;  // a multiclass model's intercepts (K)
+    std::vector<float> quantile_alpha;  // reg:quantileerror's quantiles
     std::vector<float> train_margins;
     double train_seconds = 0.0;
 };
@@ -1654,20 +1752,28 @@ namespace {
 // (softmax_gradients), then grows one tree per class in class order, with
 // row and column sampling keyed on the tree index round * K + class, each
 // tree's leaves added to its own class's margins.
+// Several quantile_alpha values (multi-target reg:quantileerror) run the same
+// loop with one output per alpha: intercepts the labels' alpha quantiles
+// (mod.rs:1442-1444), each target's pairs from its own column's scale
+// (quantile_multi_gradients, mod.rs:2871-2890).
 void train_multiclass(const float *x, u64 n, u32 nf, const float *labels, const float *weights,
                       const Params &P, const Cuts &cuts, const std::vector<Block> &blocks,
                       orc_model &m) {
     (void)x;
     const orc_params &p = P.p;
-    const u32 K = p.num_class;
-    if (K < 2) throw std::runtime_error("multiclass objectives require num_class >= 2");
-    for (u64 i = 0; i < n; i++) {
-        const float v = labels[i];
-        if (!(v >= 0.0f && v < (float)K && v == std::trunc(v)))
-            throw std::runtime_error("labels must be integers in [0, num_class)");
+    const bool quantile = p.objective == 4;
+    const u32 K = quantile ? p.n_quantile_alpha : p.num_class;
+    if (!quantile) {
+        if (K < 2) throw std::runtime_error("multiclass objectives require num_class >= 2");
+        for (u64 i = 0; i < n; i++) {
+            const float v = labels[i];
+            if (!(v >= 0.0f && v < (float)K && v == std::trunc(v)))
+                throw std::runtime_error("labels must be integers in [0, num_class)");
+        }
     }
     m.class_margins = p.has_base_score ? std::vector<float>(K, p.base_score)
-                                       : initial_class_margins(labels, weights, n, K);
+                      : quantile ? quantile_intercepts(p.quantile_alpha, K, labels, weights, n)
+                                 : initial_class_margins(labels, weights, n, K);
     m.base_score = m.class_margins[0];
     std::vector<std::vector<float>> preds(K);
     for (u32 k = 0; k < K; k++) preds[k].assign(n, m.class_margins[k]);
@@ -1676,10 +1782,24 @@ void train_multiclass(const float *x, u64 n, u32 nf, const float *labels, const 
     auto t0 = std::chrono::steady_clock::now();
     const u64 th = threshold_for(p.subsample);
     for (u32 round = 0; round < p.n_rounds; round++) {
-        for (u64 i = 0; i < n; i++) {
-            const float wt = weights ? weights[i] : 1.0f;
-            for (u32 k = 0; k < K; k++)
-                softmax_pair(preds, i, labels[i], wt, k, gf[k][2 * i], gf[k][2 * i + 1]);
+        if (quantile) {
+            for (u32 k = 0; k < K; k++) {
+                const float qs = quantile_scale(preds[k].data(), labels, weights, n);
+                for (u64 i = 0; i < n; i++) {
+                    float &g = gf[k][2 * i], &h = gf[k][2 * i + 1];
+                    quantile_pair(p.quantile_alpha[k], qs, preds[k][i], labels[i], g, h);
+                    if (weights) {
+                        g = g * weights[i];
+                        h = h * weights[i];
+                    }
+                }
+            }
+        } else {
+            for (u64 i = 0; i < n; i++) {
+                const float wt = weights ? weights[i] : 1.0f;
+                for (u32 k = 0; k < K; k++)
+                    softmax_pair(preds, i, labels[i], wt, k, gf[k][2 * i], gf[k][2 * i + 1]);
+            }
         }
         for (u32 k = 0; k < K; k++) {
             const u64 tree = (u64)round * K + k;
@@ -1726,12 +1846,28 @@ int orc_train(const float *x, uint64_t n, uint32_t nf, const float *labels, cons
         std::vector<Block> blocks = bin_blocks(x, n, nf, cuts, p.cols_per_block);
         auto m = std::make_unique<orc_model>();
         m->objective = p.objective;
-        if (p.objective == 2 || p.objective == 3) {
+        const bool quantile = p.objective == 4;
+        if (quantile) {
+            // Objective::validate_params (objective.rs:317-330).
+            if (p.n_quantile_alpha == 0 || !p.quantile_alpha)
+                throw std::runtime_error("reg:quantileerror requires quantile_alpha");
+            for (u32 k = 0; k < p.n_quantile_alpha; k++) {
+                const float a = p.quantile_alpha[k];
+                if (!(a >= 0.0f && a <= 1.0f))
+                    throw std::runtime_error("quantile_alpha must be in [0, 1]");
+                if (k && p.quantile_alpha[k - 1] > a)
+                    throw std::runtime_error("quantile_alpha must be in ascending order");
+            }
+            m->quantile_alpha.assign(p.quantile_alpha, p.quantile_alpha + p.n_quantile_alpha);
+        }
+        if (p.objective == 2 || p.objective == 3 || (quantile && p.n_quantile_alpha > 1)) {
             train_multiclass(x, n, nf, labels, weights, P, cuts, blocks, *m);
             *out = m.release();
             return 0;
         }
-        m->base_score = p.has_base_score ? p.base_score : estimate_base_score(labels, weights, n);
+        m->base_score = p.has_base_score ? p.base_score
+                        : quantile ? quantile_intercepts(p.quantile_alpha, 1, labels, weights, n)[0]
+                                   : estimate_base_score(labels, weights, n);
         float margin = base_margin_of(p.objective, m->base_score);
         std::vector<float> pred(n, margin);
         std::vector<Fixed> gpair(n);
@@ -1741,7 +1877,7 @@ int orc_train(const float *x, uint64_t n, uint32_t nf, const float *labels, cons
         // logistic and squared error both use it (objective.rs:346-356).
         std::vector<float> spw_w;
         const float *gw = weights;
-        if (p.scale_pos_weight != 1.0f) {
+        if (p.scale_pos_weight != 1.0f && !quantile) {
             spw_w.resize(n);
             for (u64 i = 0; i < n; i++) {
                 const float w = weights ? weights[i] : 1.0f;
@@ -1753,9 +1889,13 @@ int orc_train(const float *x, uint64_t n, uint32_t nf, const float *labels, cons
         for (u32 round = 0; round < p.n_rounds; round++) {
             double mg = 0, mh = 0;
             u64 th = threshold_for(p.subsample);
+            const float qs = quantile ? quantile_scale(pred.data(), labels, weights, n) : 0.0f;
             for (u64 i = 0; i < n; i++) {
                 float g, h;
-                gradient(p.objective, pred[i], labels[i], g, h);
+                if (quantile)
+                    quantile_pair(p.quantile_alpha[0], qs, pred[i], labels[i], g, h);
+                else
+                    gradient(p.objective, pred[i], labels[i], g, h);
                 if (gw) {
                     g = g * gw[i];
                     h = h * gw[i];
@@ -2028,6 +2168,44 @@ void orc_sigmoid(const float *in, uint64_t n, float *out) {
     for (uint64_t i = 0; i < n; i++) out[i] = sigmoidf(in[i]);
 }
 
+}  // extern "C"
+
+namespace {
+
+template <class F>
+uint64_t function_checksum(uint64_t begin, uint64_t end, uint32_t threads, F fn) {
+    if (threads == 0) threads = 1;
+    std::vector<u64> part(threads, 0);
+    std::vector<std::thread> pool;
+    for (u32 t = 0; t < threads; t++)
+        pool.emplace_back([&, t] {
+            u64 acc = 0;
+            for (u64 u = begin + t; u < end; u += threads) {
+                const u32 b = (u32)u;
+                float x;
+                std::memcpy(&x, &b, 4);
+                const float s = fn(x);
+                u32 sb;
+                std::memcpy(&sb, &s, 4);
+                if (s != s) sb = 0x7fc00000u;
+                acc += mix64(u ^ ((u64)sb << 32));
+            }
+            part[t] = acc;
+        });
+    for (auto &th : pool) th.join();
+    u64 acc = 0;
+    for (u64 v : part) acc += v;
+    return acc;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint64_t orc_tanh_checksum(uint64_t begin, uint64_t end, uint32_t threads) {
+    return function_checksum(begin, end, threads, [](float x) { return std::tanh(x); });
+}
+
 uint64_t orc_sigmoid_checksum(uint64_t begin, uint64_t end, uint32_t threads) {
     if (threads == 0) threads = 1;
     std::vector<u64> part(threads, 0);
@@ -2085,6 +2263,30 @@ void orc_gradients(const float *pred, const float *labels, const float *w, uint6
 }
 
 float orc_base_margin(uint32_t obj, float bs) { return base_margin_of(obj, bs); }
+
+float orc_quantile_scale(const float *pred, const float *labels, const float *w, uint64_t n) {
+    return quantile_scale(pred, labels, w, n);
+}
+
+void orc_quantile_pairs(const float *pred, const float *labels, const float *w, uint64_t n,
+                        float alpha, float scale, float *out) {
+    for (u64 i = 0; i < n; i++) {
+        float g, h;
+        quantile_pair(alpha, scale, pred[i], labels[i], g, h);
+        if (w) {
+            g *= w[i];
+            h *= w[i];
+        }
+        out[2 * i] = g;
+        out[2 * i + 1] = h;
+    }
+}
+
+void orc_quantile_intercepts(const float *labels, const float *w, uint64_t n, const float *alphas,
+                             uint32_t k, float *out) {
+    const std::vector<float> v = quantile_intercepts(alphas, k, labels, w, n);
+    std::copy(v.begin(), v.end(), out);
+}
 float orc_estimate_base_score(const float *y, const float *w, uint64_t n) {
     return estimate_base_score(y, w, n);
 }

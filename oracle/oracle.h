@@ -38,7 +38,8 @@ typedef struct {
     uint32_t cols_per_block;
     uint64_t seed;
     uint32_t objective;       /* 0 = reg:squarederror, 1 = binary:logistic,
-                                 2 = multi:softprob, 3 = multi:softmax */
+                                 2 = multi:softprob, 3 = multi:softmax,
+                                 4 = reg:quantileerror */
     uint32_t grow_policy;     /* 0 = depthwise, 1 = lossguide */
     uint32_t max_cat_to_onehot;
     uint32_t max_cat_threshold;
@@ -46,6 +47,8 @@ typedef struct {
     uint32_t has_base_score;
     uint32_t nthread;         /* histogram worker threads (0 = 1) */
     uint32_t num_class;       /* classes of multi:softprob / multi:softmax */
+    uint32_t n_quantile_alpha; /* quantiles of reg:quantileerror (one output each) */
+    const float *quantile_alpha;
 } orc_params;
 
 /* One tree node; same field meaning as Node (src/model/tree.rs:52-111). */
@@ -189,12 +192,22 @@ void orc_gradients(const float *pred, const float *labels, const float *weights,
                    uint32_t objective, float *out2n);
 float orc_base_margin(uint32_t objective, float base_score);
 float orc_estimate_base_score(const float *labels, const float *weights, uint64_t n);
+/* reg:quantileerror (objective.rs:1002-1160): the round's scale
+ * (sum w sqrtf|p - y| / sum w)^2, the weighted pairs of one alpha under a
+ * scale, and the labels' alpha quantiles (the intercepts). */
+float orc_quantile_scale(const float *pred, const float *labels, const float *weights, uint64_t n);
+void orc_quantile_pairs(const float *pred, const float *labels, const float *weights, uint64_t n,
+                        float alpha, float scale, float *out2n);
+void orc_quantile_intercepts(const float *labels, const float *weights, uint64_t n,
+                             const float *alphas, uint32_t k, float *out);
 
 /* Logistic sigmoid 1 / (1 + expf(-x)) with the host libm (objective.rs:37-39),
  * elementwise, and its fingerprint over float bit patterns [begin, end):
  * wrapping sum of splitmix64(u ^ bits(s(u)) << 32), NaN outputs as 0x7fc00000. */
 void orc_sigmoid(const float *in, uint64_t n, float *out);
 uint64_t orc_sigmoid_checksum(uint64_t begin, uint64_t end, uint32_t threads);
+/* The same fingerprint of the host libm's tanhf (objective.rs:1151). */
+uint64_t orc_tanh_checksum(uint64_t begin, uint64_t end, uint32_t threads);
 
 /* Message of the last failing call on this thread. */
 const char *orc_last_error(void);

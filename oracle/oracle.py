@@ -57,6 +57,8 @@ class Params(C.Structure):
         ("has_base_score", C.c_uint32),
         ("nthread", C.c_uint32),
         ("num_class", C.c_uint32),
+        ("n_quantile_alpha", C.c_uint32),
+        ("quantile_alpha", C.POINTER(C.c_float)),
     ]
 
 
@@ -111,7 +113,7 @@ class Split(C.Structure):
 
 
 OBJECTIVES = {"reg:squarederror": 0, "binary:logistic": 1, "multi:softprob": 2,
-              "multi:softmax": 3}
+              "multi:softmax": 3, "reg:quantileerror": 4}
 GROW = {"depthwise": 0, "lossguide": 1}
 
 _lib = None
@@ -184,6 +186,8 @@ def lib() -> C.CDLL:
         L.orc_sigmoid.restype = None
         L.orc_sigmoid_checksum.argtypes = [C.c_uint64, C.c_uint64, C.c_uint32]
         L.orc_sigmoid_checksum.restype = C.c_uint64
+        L.orc_tanh_checksum.argtypes = [C.c_uint64, C.c_uint64, C.c_uint32]
+        L.orc_tanh_checksum.restype = C.c_uint64
         L.orc_splitmix64.argtypes = [C.c_uint64, C.c_uint64, P]
         L.orc_splitmix64.restype = None
         L.orc_mix64.argtypes = [C.c_uint64]
@@ -200,6 +204,12 @@ def lib() -> C.CDLL:
         L.orc_base_margin.restype = C.c_float
         L.orc_estimate_base_score.argtypes = [P, P, C.c_uint64]
         L.orc_estimate_base_score.restype = C.c_float
+        L.orc_quantile_scale.argtypes = [P, P, P, C.c_uint64]
+        L.orc_quantile_scale.restype = C.c_float
+        L.orc_quantile_pairs.argtypes = [P, P, P, C.c_uint64, C.c_float, C.c_float, P]
+        L.orc_quantile_pairs.restype = None
+        L.orc_quantile_intercepts.argtypes = [P, P, C.c_uint64, P, C.c_uint32, P]
+        L.orc_quantile_intercepts.restype = None
         L.orc_last_error.restype = C.c_char_p
         _lib = L
     return _lib
@@ -237,6 +247,12 @@ def make_params(**kw) -> Params:
         p.has_base_score = 1
     p.nthread = kw.get("nthread", 1)
     p.num_class = kw.get("num_class", 0)
+    qa = kw.get("quantile_alpha")
+    if qa is not None:
+        arr = np.ascontiguousarray(np.atleast_1d(np.asarray(qa, np.float32)))
+        p._alphas = arr  # keeps the array alive with the struct
+        p.n_quantile_alpha = arr.size
+        p.quantile_alpha = arr.ctypes.data_as(C.POINTER(C.c_float))
     return p
 
 
@@ -355,6 +371,32 @@ def model_from_nodes(trees, cat_words, objective: str, base_score: float) -> Mod
     if rc:
         raise RuntimeError(lib().orc_last_error().decode())
     return Model(h)
+
+
+def quantile_scale(pred, labels, weights=None) -> float:
+    pred = np.ascontiguousarray(pred, np.float32)
+    y = np.ascontiguousarray(labels, np.float32)
+    w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+    return float(lib().orc_quantile_scale(_p(pred), _p(y), _p(w), y.size))
+
+
+def quantile_pairs(pred, labels, alpha, scale, weights=None) -> np.ndarray:
+    """[n, 2] weighted pairs of one quantile under a given scale."""
+    pred = np.ascontiguousarray(pred, np.float32)
+    y = np.ascontiguousarray(labels, np.float32)
+    w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+    out = np.empty((y.size, 2), np.float32)
+    lib().orc_quantile_pairs(_p(pred), _p(y), _p(w), y.size, alpha, scale, _p(out))
+    return out
+
+
+def quantile_intercepts(labels, alphas, weights=None) -> np.ndarray:
+    y = np.ascontiguousarray(labels, np.float32)
+    w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+    a = np.ascontiguousarray(np.atleast_1d(alphas), np.float32)
+    out = np.empty(a.size, np.float32)
+    lib().orc_quantile_intercepts(_p(y), _p(w), y.size, _p(a), a.size, _p(out))
+    return out
 
 
 def sketch_cuts(x, max_bin, weights=None, categorical=None):

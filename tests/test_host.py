@@ -119,7 +119,12 @@ def _tiny():
 @pytest.mark.parametrize("params, msg", [
     ({"device": "cpu"}, "device"),
     ({"device": "tpu"}, "device"),
-    ({"objective": "reg:quantileerror"}, "objective"),
+    ({"objective": "reg:pseudohubererror"}, "objective"),
+    ({"objective": "reg:quantileerror"}, "needs quantile_alpha"),
+    ({"objective": "reg:quantileerror", "quantile_alpha": 1.5}, r"must be in \[0, 1\]"),
+    ({"objective": "reg:quantileerror", "quantile_alpha": [0.9, 0.1]}, "ascending"),
+    ({"objective": "reg:quantileerror", "quantile_alpha": []}, "must not be an empty list"),
+    ({"objective": "reg:quantileerror", "quantile_alpha": [0.5] * 65}, "at most 64"),
     ({"objective": "multi:softprob"}, "num_class >= 2"),
     ({"objective": "multi:softmax", "num_class": 1}, "num_class >= 2"),
     ({"objective": "multi:softprob", "num_class": 2.5}, "num_class must be an integer"),
