@@ -13,6 +13,9 @@ device syncs. Other workloads (--workload):
   streaming 50M x 200 N(0,1) binary, max_bin 255 (u8, about 10 GB of bins),
             depth 8, with the device budget forced to 4 GiB: most tiles
             stream from pinned host memory
+  multiclass  the narrow rows with 4 classes, multi:softprob (4 trees a round)
+  quantile  the narrow rows with a continuous target, reg:quantileerror at
+            quantile_alpha 0.1 / 0.5 / 0.9 (3 trees a round)
   shap      GPU TreeSHAP of 1M rows x 200 features against a 100-tree,
             depth-8 ensemble (trained first, untimed); one step = one pass
   predict   GPU margins of the same rows and ensemble; one step = one pass
@@ -159,7 +162,8 @@ def train_workload(args, X, y, params, desc: str, traffic_tag: str):
     hist_gbps = b_hist / (t_hist_ms * 1e-3) / 1e9 if t_hist_ms > 0 else 0.0
     launches = int(pmodel.stats["hist_launches"])
     bytes_per_launch = float(pmodel.stats["hist_bytes"]) / launches if launches else 0.0
-    traffic = load_traffic(os.path.join(ROOT, "profiles", f"hist_traffic_{traffic_tag}.txt"))
+    traffic = (load_traffic(os.path.join(ROOT, "profiles", f"hist_traffic_{traffic_tag}.txt"))
+               if traffic_tag else None)
     roofline = {
         "bound": "hbm",
         "achieved": round(hist_gbps, 1),
@@ -204,11 +208,12 @@ def train_workload(args, X, y, params, desc: str, traffic_tag: str):
         if params.get("gpu_math") != "fast":
             parity = all(
                 np.array_equal(om.tree(t)[f], model.tree_nodes(t)[f])
-                for t in range(args.cpu_rounds) for f in om.tree(t).dtype.names if f != "pad")
+                for t in range(om.n_trees) for f in om.tree(t).dtype.names if f != "pad")
 
     config = {"workload": desc, "rows": int(X.shape[0]), "features": int(X.shape[1])}
     config.update({k: params[k] for k in ("max_bin", "max_depth", "max_leaves", "grow_policy",
-                                          "colsample_bytree", "objective", "gpu_math")
+                                          "colsample_bytree", "objective", "num_class",
+                                          "quantile_alpha", "gpu_math")
                    if k in params})
     out = base_line(args, round(args.steps / t_wall, 3), "rounds/s",
                     round(1e3 * t_wall / args.steps, 3), config)
@@ -405,7 +410,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="narrow",
-                    choices=["narrow", "wide", "widebin", "streaming", "shap", "predict"])
+                    choices=["narrow", "multiclass", "quantile", "wide", "widebin", "streaming",
+                             "shap", "predict"])
     ap.add_argument("--rows", type=int, default=0, help="rows (0: the workload's own size)")
     ap.add_argument("--max-bin", type=int, default=255, help="narrow workload: 255 (u8) or 256 (u16)")
     ap.add_argument("--gpu-math", default="exact", choices=["exact", "fast"],
@@ -446,6 +452,19 @@ def main() -> int:
             args, X, y, params,
             f"narrow {X.shape[0]}x{X.shape[1]} HIGGS-like binary, max_bin={args.max_bin} "
             f"({u} bins), depth 8, eta 0.1, gpu_math={args.gpu_math}, depthwise", f"narrow_{u}")
+    elif args.workload in ("multiclass", "quantile"):
+        if args.workload == "multiclass":
+            X, y, params, _ = datasets.narrow_multiclass(args.rows or 10_500_000)
+            what = "4 classes, multi:softprob (4 trees a round)"
+        else:
+            X, y, params, _ = datasets.narrow_quantile(args.rows or 10_500_000)
+            what = "reg:quantileerror at quantile_alpha 0.1/0.5/0.9 (3 trees a round)"
+        log(f"data {X.shape} generated in {time.time() - t0:.1f}s")
+        params = dict(params, gpu_math=args.gpu_math)
+        out = train_workload(
+            args, X, y, params,
+            f"narrow {X.shape[0]}x{X.shape[1]} rows, {what}, max_bin=255 (u8 bins), depth 8, "
+            f"eta 0.1, gpu_math={args.gpu_math}, depthwise", None)
     elif args.workload == "wide":
         X, y, params, _ = datasets.wide_binary(args.rows or 400_000, n_features=2000)
         log(f"data {X.shape} generated in {time.time() - t0:.1f}s")

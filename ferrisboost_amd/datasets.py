@@ -114,6 +114,44 @@ def narrow_binary(n_rows: int = 10_500_000, seed: int = 2, max_bin: int = 256):
     return X, y, params, {"rounds": 500}
 
 
+def narrow_multiclass(n_rows: int = 10_500_000, n_classes: int = 4, seed: int = 2,
+                      max_bin: int = 255):
+    """The narrow 28-feature rows with K balanced classes: the quantile bins of a
+    nonlinear score plus logistic noise (multi:softprob, depth 8, eta 0.1)."""
+    X, _, _, _ = narrow_binary(n_rows, seed=seed, max_bin=max_bin)
+    s = np.empty(n_rows, np.float64)
+
+    def score(g, a, b):
+        Xs = X[a:b].astype(np.float64)
+        s[a:b] = (Xs[:, 0] + 0.8 * Xs[:, 3] * Xs[:, 1] - 0.5 * Xs[:, 11] + 0.3 * Xs[:, 22]
+                  + g.logistic(size=b - a) * 0.5)
+
+    _chunked(n_rows, seed + 3000, score, 1 << 18)
+    edges = np.quantile(s[:: max(1, n_rows // 200_000)], np.linspace(0, 1, n_classes + 1)[1:-1])
+    y = np.searchsorted(edges, s).astype(np.float32)
+    params = {"objective": "multi:softprob", "num_class": n_classes, "max_depth": 8, "eta": 0.1,
+              "max_bin": max_bin, "grow_policy": "depthwise"}
+    return X, y, params, {"rounds": 500}
+
+
+def narrow_quantile(n_rows: int = 10_500_000, alphas=(0.1, 0.5, 0.9), seed: int = 2,
+                    max_bin: int = 255):
+    """The narrow 28-feature rows with a heteroscedastic continuous target
+    (reg:quantileerror at the given quantiles, depth 8, eta 0.1)."""
+    X, _, _, _ = narrow_binary(n_rows, seed=seed, max_bin=max_bin)
+    y = np.empty(n_rows, np.float32)
+
+    def target(g, a, b):
+        Xs = X[a:b].astype(np.float64)
+        y[a:b] = (1.5 * Xs[:, 0] - 0.7 * Xs[:, 11] * Xs[:, 2] + 0.4 * np.log1p(Xs[:, 21])
+                  + g.standard_exponential(b - a) * (1.0 + np.abs(Xs[:, 4])))
+
+    _chunked(n_rows, seed + 4000, target, 1 << 18)
+    params = {"objective": "reg:quantileerror", "quantile_alpha": list(alphas), "max_depth": 8,
+              "eta": 0.1, "max_bin": max_bin, "grow_policy": "depthwise"}
+    return X, y, params, {"rounds": 500}
+
+
 def wide_binary(n_rows: int = 400_000, n_features: int = 2000, seed: int = 3, max_bin: int = 256):
     rng = np.random.default_rng(seed)
     w = np.zeros(n_features)
