@@ -354,7 +354,9 @@ class Model:
 
     @property
     def feature_names(self) -> list[str]:
-        return []
+        """The feature column names of a Parquet or Arrow training input
+        (empty for arrays)."""
+        return list(getattr(self, "_feature_names", []))
 
     @property
     def best_iteration(self):
@@ -636,12 +638,70 @@ def sketch(X, max_bin: int = 255, weight=None, feature_types=None,
     return Cuts(vals[: offs[-1]].copy(), offs, max_bin, cat)
 
 
+def _arrow_input(data) -> bool:
+    from . import arrow_rows
+
+    if arrow_rows.is_path(data):
+        return True
+    mod = type(data).__module__ or ""
+    return mod.startswith("pyarrow")
+
+
+def _train_arrow(p: dict[str, Any], data, label, weight, cuts) -> Model:
+    """train() on a .parquet path or a pyarrow Table / RecordBatchReader: the
+    label (and weight) are column names; the feature rows stream through
+    fbt_train_rows (python/ferrisboost/__init__.py:1090-1230)."""
+    from . import arrow_rows
+
+    if cuts is not None:
+        raise ValueError("cuts= takes a numpy matrix; Parquet and Arrow inputs sketch their own")
+    if arrow_rows.is_path(data):
+        path = str(data).lower()
+        if not (path.endswith(".parquet") or path.endswith(".pq")):
+            raise ValueError(f"cannot tell the format of {str(data)!r} from its extension; "
+                             "supported: .parquet / .pq")
+    if weight is not None and not isinstance(weight, str):
+        raise ValueError("for Parquet and Arrow inputs, weight names the weight column")
+    src = arrow_rows.ArrowRows(data, label, weight, p["enable_categorical"], p["missing"])
+    types = arrow_rows.feature_types_of(src, p["feature_types"])
+    cat = _categorical_flags(types, src.n_features)
+    mono = None
+    mc = p["monotone_constraints"]
+    if mc:
+        if isinstance(mc, str):
+            mc = [int(v) for v in mc.strip("()").split(",") if v.strip()]
+        mono = np.ascontiguousarray([int(np.sign(v)) for v in mc], np.int8)
+    s = _params_struct(p, src.n_features)
+    h = C.c_void_p()
+    L = N.train_lib()
+    errors: list = []
+    fn = src.as_callback(errors)
+    rc = L.fbt_train_rows(fn, None, src.n_rows, src.n_features, N.ptr(src.labels),
+                          N.ptr(src.weights), N.ptr(cat), N.ptr(mono),
+                          0 if mono is None else mono.size, C.byref(s), C.byref(h))
+    if errors:
+        raise errors[0]
+    N.check_train(rc)
+    m = Model(h, src.n_features, p["objective"], s.device)
+    m._feature_names = list(src.features)
+    st = N.Stats()
+    N.check_train(L.fbt_last_stats(C.byref(st)))
+    m.stats = {k: getattr(st, k) for k, _ in N.Stats._fields_}
+    return m
+
+
 def train(params: Mapping[str, Any], X, label, weight=None, num_boost_round: int = 10,
           cuts: Cuts | None = None) -> Model:
     """fb.train on the device path (python/ferrisboost/__init__.py:train).
-    cuts (from sketch() on the same matrix, max_bin and feature_types)
-    replaces the sketch."""
+
+    X is a 2-D array (label and weight arrays), or a .parquet path or a
+    pyarrow Table / RecordBatchReader with label (and weight) naming
+    columns: the other columns are the features, streamed to the device in
+    chunks for the sketch and the binning. cuts (from sketch() on the same
+    matrix, max_bin and feature_types) replaces the sketch."""
     p = _normalize(params, num_boost_round)
+    if _arrow_input(X):
+        return _train_arrow(p, X, label, weight, cuts)
     X = _matrix(X, p["missing"])
     y = np.ascontiguousarray(np.asarray(label, dtype=np.float32))
     if y.shape != (X.shape[0],):

@@ -166,6 +166,10 @@ class TrainParams(C.Structure):
     ]
 
 
+# fbt_rows_fn: int (*)(void *user, uint64_t begin, uint64_t n, float *out)
+ROWS_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint64, C.c_uint64, C.POINTER(C.c_float))
+
+
 class Stats(C.Structure):
     _fields_ = [
         ("train_seconds", C.c_double),
@@ -230,7 +234,7 @@ HIP_SYMBOLS = [
     "fbh_saabas_contribs", "fbh_predict", "fbh_predict_device", "fbh_shap_contribs_noalloc",
 ]
 TRAIN_SYMBOLS = [
-    "fbt_last_error", "fbt_train", "fbt_train_cuts", "fbt_last_stats", "fbt_last_round_stats", "fbt_model_free", "fbt_model_n_trees",
+    "fbt_last_error", "fbt_train", "fbt_train_cuts", "fbt_train_rows", "fbt_last_stats", "fbt_last_round_stats", "fbt_model_free", "fbt_model_n_trees",
     "fbt_model_tree_len", "fbt_model_tree_nodes", "fbt_model_n_cat_words", "fbt_model_cat_words",
     "fbt_model_base_score", "fbt_model_base_margin", "fbt_model_n_features",
     "fbt_model_train_margins", "fbt_model_n_cuts", "fbt_model_cuts", "fbt_predict_margin",
@@ -354,6 +358,8 @@ def train_lib() -> C.CDLL:
                                 C.POINTER(TrainParams), C.POINTER(P)]
         L.fbt_train_cuts.argtypes = [P, C.c_uint64, C.c_uint32, P, P, P, P, C.c_uint32,
                                      C.POINTER(TrainParams), P, P, C.POINTER(P)]
+        L.fbt_train_rows.argtypes = [ROWS_FN, P, C.c_uint64, C.c_uint32, P, P, P, P, C.c_uint32,
+                                     C.POINTER(TrainParams), C.POINTER(P)]
         L.fbt_last_stats.argtypes = [C.POINTER(Stats)]
         L.fbt_last_round_stats.argtypes = [P, P, P, C.c_uint32]
         L.fbt_last_round_stats.restype = C.c_uint32

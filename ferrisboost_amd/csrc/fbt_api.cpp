@@ -11,7 +11,7 @@
 #include "fbt_internal.h"
 
 namespace fbt {
-Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float *w,
+Model train(const RowSource &src, uint64_t n, uint32_t nf, const float *y, const float *w,
             const uint8_t *cat, const int8_t *mono, uint32_t n_mono, const fbt_params &p,
             const Cuts *given);
 fbt_stats last_stats();
@@ -64,8 +64,31 @@ int fbt_train(const float *x, uint64_t n_rows, uint32_t n_features, const float 
         if (!x || !labels || !params || !out) throw fbt::InputError("null argument");
         *out = nullptr;
         auto m = std::make_unique<fbt_model>();
-        m->m = fbt::train(x, n_rows, n_features, labels, weights, categorical, monotone, n_monotone,
-                          *params, nullptr);
+        fbt::RowSource src;
+        src.x = x;
+        m->m = fbt::train(src, n_rows, n_features, labels, weights, categorical, monotone,
+                          n_monotone, *params, nullptr);
+        *out = m.release();
+    });
+}
+
+int fbt_train_rows(fbt_rows_fn fn, void *user, uint64_t n_rows, uint32_t n_features,
+                   const float *labels, const float *weights, const uint8_t *categorical,
+                   const int8_t *monotone, uint32_t n_monotone, const fbt_params *params,
+                   fbt_model **out) {
+    return guard([&] {
+        if (!fn || !labels || !params || !out) throw fbt::InputError("null argument");
+        *out = nullptr;
+        fbt::RowSource src;
+        src.read = [&](uint64_t begin, uint64_t count, float *rows) {
+            if (int rc = fn(user, begin, count, rows))
+                throw fbt::InputError("the row reader failed at rows " + std::to_string(begin) +
+                                      ".." + std::to_string(begin + count) + " (code " +
+                                      std::to_string(rc) + ")");
+        };
+        auto m = std::make_unique<fbt_model>();
+        m->m = fbt::train(src, n_rows, n_features, labels, weights, categorical, monotone,
+                          n_monotone, *params, nullptr);
         *out = m.release();
     });
 }
@@ -85,8 +108,10 @@ int fbt_train_cuts(const float *x, uint64_t n_rows, uint32_t n_features, const f
         for (uint32_t f = 0; f < n_features; f++)
             c.categorical[f] = categorical && categorical[f] ? 1 : 0;
         auto m = std::make_unique<fbt_model>();
-        m->m = fbt::train(x, n_rows, n_features, labels, weights, categorical, monotone, n_monotone,
-                          *params, &c);
+        fbt::RowSource src;
+        src.x = x;
+        m->m = fbt::train(src, n_rows, n_features, labels, weights, categorical, monotone,
+                          n_monotone, *params, &c);
         *out = m.release();
     });
 }

@@ -260,8 +260,9 @@ Cuts sketch_matrix(const float *x, uint64_t n, uint32_t nf, uint32_t max_bin, co
     return assemble_cuts(per, nf, cat);
 }
 
-Cuts sketch_matrix_device(int device, const float *x, uint64_t n, uint32_t nf, uint32_t max_bin,
-                          const uint8_t *cat, uint64_t memory_budget, unsigned threads) {
+Cuts sketch_matrix_device(int device, const RowSource &src, uint64_t n, uint32_t nf,
+                          uint32_t max_bin, const uint8_t *cat, uint64_t memory_budget,
+                          unsigned threads) {
     fbh_sketch *raw = nullptr;
     auto call = [](int rc) {
         if (rc == FBH_OK) return;
@@ -272,7 +273,9 @@ Cuts sketch_matrix_device(int device, const float *x, uint64_t n, uint32_t nf, u
     };
     call(fbh_sketch_create(device, n, nf, max_bin, cat, memory_budget, &raw));
     std::unique_ptr<fbh_sketch, int (*)(fbh_sketch *)> s(raw, fbh_sketch_destroy);
-    call(fbh_sketch_push_rows(s.get(), x, n));
+    src.each_chunk(n, nf, [&](uint64_t, uint64_t k, const float *rows) {
+        call(fbh_sketch_push_rows(s.get(), rows, k));
+    });
     uint64_t cap = 0;
     for (uint32_t f = 0; f < nf; f++) cap += (cat && cat[f]) ? 65533u : (max_bin ? max_bin - 1 : 0);
     std::vector<float> values(std::max<uint64_t>(cap, 1));
@@ -287,10 +290,26 @@ Cuts sketch_matrix_device(int device, const float *x, uint64_t n, uint32_t nf, u
         else per[f].assign(values.begin() + offsets[f], values.begin() + offsets[f + 1]);
     }
     // Features holding both zero signs with a zero among their cuts: the
-    // host sketch decides the zero's sign.
-    parallel_for((uint32_t)on_host.size(), threads, [&](uint32_t i) {
-        per[on_host[i]] = sketch_numeric(x, n, nf, on_host[i], max_bin, nullptr);
-    });
+    // host sketch decides the zero's sign (a reader's rows are read again for
+    // just those columns).
+    if (!on_host.empty()) {
+        const uint32_t k = (uint32_t)on_host.size();
+        std::vector<float> cols;
+        const float *mat = src.x;
+        uint32_t stride = nf;
+        if (!mat) {
+            cols.resize(n * k);
+            src.each_chunk(n, nf, [&](uint64_t r0, uint64_t c, const float *rows) {
+                for (uint64_t r = 0; r < c; r++)
+                    for (uint32_t j = 0; j < k; j++) cols[(r0 + r) * k + j] = rows[r * nf + on_host[j]];
+            });
+            mat = cols.data();
+            stride = k;
+        }
+        parallel_for(k, threads, [&](uint32_t i) {
+            per[on_host[i]] = sketch_numeric(mat, n, stride, src.x ? on_host[i] : i, max_bin, nullptr);
+        });
+    }
     return assemble_cuts(per, nf, cat);
 }
 

@@ -1,7 +1,10 @@
 // fbt_internal.h -- host-side types of the round driver (libfbtrain.so).
 #pragma once
 
+#include <algorithm>
 #include <cstdint>
+#include <cstdlib>
+#include <functional>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -34,6 +37,37 @@ struct Cuts {
     uint32_t bin_of(uint32_t f, float v) const;
 };
 
+// Row-major f32 rows: the whole matrix in memory (x), or a reader that fills
+// `count` rows from `begin` (rows are read front to back, once per pass).
+struct RowSource {
+    const float *x = nullptr;
+    std::function<void(uint64_t begin, uint64_t count, float *out)> read;
+    // Rows a pass reads at a time: about 64 MB of f32 (FB_READ_ROWS sets
+    // the row count).
+    static uint64_t chunk_rows(uint32_t n_features) {
+        if (const char *e = std::getenv("FB_READ_ROWS")) {
+            const long long v = std::atoll(e);
+            if (v > 0) return (uint64_t)v;
+        }
+        return std::max<uint64_t>(1, (64ull << 20) / (4ull * std::max(n_features, 1u)));
+    }
+    // Every row, front to back, in chunks: fn(begin, count, rows).
+    template <class F>
+    void each_chunk(uint64_t n, uint32_t nf, F &&fn) const {
+        if (x) {
+            fn(0, n, x);
+            return;
+        }
+        const uint64_t step = chunk_rows(nf);
+        std::vector<float> buf(std::min(step, n) * nf);
+        for (uint64_t r0 = 0; r0 < n; r0 += step) {
+            const uint64_t k = std::min(step, n - r0);
+            read(r0, k, buf.data());
+            fn(r0, k, buf.data());
+        }
+    }
+};
+
 // Sketch every feature of a row-major matrix (DenseSource binning pass).
 Cuts sketch_matrix(const float *x, uint64_t n_rows, uint32_t n_features, uint32_t max_bin,
                    const float *weights, const uint8_t *categorical, unsigned threads);
@@ -41,9 +75,9 @@ Cuts sketch_matrix(const float *x, uint64_t n_rows, uint32_t n_features, uint32_
 // The same cuts from the device sketch (fbh_sketch_*), for unit row
 // weights; a feature the device leaves to the host (both zero signs) is
 // sketched here.
-Cuts sketch_matrix_device(int device, const float *x, uint64_t n_rows, uint32_t n_features,
-                          uint32_t max_bin, const uint8_t *categorical, uint64_t memory_budget,
-                          unsigned threads);
+Cuts sketch_matrix_device(int device, const RowSource &src, uint64_t n_rows,
+                          uint32_t n_features, uint32_t max_bin, const uint8_t *categorical,
+                          uint64_t memory_budget, unsigned threads);
 
 // Cuts handed in by a caller (fbt_train_cuts): per feature strictly
 // increasing finite values, at most max_bin - 1 for a numeric feature and

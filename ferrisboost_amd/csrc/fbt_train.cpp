@@ -917,10 +917,22 @@ uint32_t last_round_stats(double *wall, double *ms, uint64_t *bytes, uint32_t ca
     return n;
 }
 
-Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float *w,
+Model train(const RowSource &src, uint64_t n, uint32_t nf, const float *y, const float *w,
             const uint8_t *cat, const int8_t *mono_in, uint32_t n_mono, const fbt_params &p,
             const Cuts *given) {
     const auto t_setup = Clock::now();
+    // A reader's rows are held in host memory only where a host pass needs
+    // the whole matrix (the host sketch of weighted rows, host binning).
+    const float *x = src.x;
+    std::vector<float> held;
+    auto materialise = [&]() {
+        if (x) return;
+        held.resize(n * nf);
+        src.each_chunk(n, nf, [&](uint64_t r0, uint64_t k, const float *rows) {
+            std::memcpy(held.data() + r0 * nf, rows, 4 * k * nf);
+        });
+        x = held.data();
+    };
     validate(p, n, nf, y);
     if (n_mono > nf) throw InputError("monotone_constraints has more entries than features");
     std::vector<int8_t> mono(nf, 0);
@@ -952,9 +964,10 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
         check_cuts(*given, nf, p.max_bin, cat);
         m.cuts = *given;
     } else if (device_sketch) {
-        m.cuts = sketch_matrix_device(p.device, x, n, nf, p.max_bin, cat, p.gpu_memory_budget,
+        m.cuts = sketch_matrix_device(p.device, src, n, nf, p.max_bin, cat, p.gpu_memory_budget,
                                       threads);
     } else {
+        materialise();
         m.cuts = sketch_matrix(x, n, nf, p.max_bin, w, cat, threads);
     }
     const double sketch_s = std::chrono::duration<double>(Clock::now() - t_sketch).count();
@@ -1065,11 +1078,16 @@ Model train(const float *x, uint64_t n, uint32_t nf, const float *y, const float
     if (device_binning) {
         call(fbh_set_cuts(ctx.get(), m.cuts.values.data(), m.cuts.offsets.data(),
                           m.cuts.categorical.data()));
-        const uint64_t step = 1u << 20;
-        for (uint64_t r0 = 0; r0 < n; r0 += step)
-            call(fbh_upload_rows(ctx.get(), x + r0 * nf, r0, std::min(step, n - r0)));
+        RowSource rows = src;
+        rows.x = x;
+        rows.each_chunk(n, nf, [&](uint64_t r0, uint64_t k, const float *chunk) {
+            const uint64_t step = 1u << 20;
+            for (uint64_t b = 0; b < k; b += step)
+                call(fbh_upload_rows(ctx.get(), chunk + b * nf, r0 + b, std::min(step, k - b)));
+        });
         call(fbh_finish_rows(ctx.get()));
     } else {
+        materialise();
         for (const auto &feats : blocks_by_width(m.cuts, p.cols_per_block)) {
             const uint32_t wdt = m.cuts.width(feats[0]);
             std::vector<uint8_t> buf((size_t)feats.size() * n * wdt);

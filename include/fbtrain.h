@@ -137,6 +137,21 @@ size_t fbt_last_error(char *buf, size_t len);
 int fbt_train(const float *x, uint64_t n_rows, uint32_t n_features, const float *labels,
               const float *weights, const uint8_t *categorical, const int8_t *monotone,
               uint32_t n_monotone, const fbt_params *params, fbt_model **out);
+/* Training from a row reader (the Parquet / Arrow sources of the Python
+ * entry, DenseSource's two passes, src/source/dense.rs:99-290): fn(user,
+ * begin, count, out) fills `count` row-major f32 rows from row `begin` (NaN
+ * is missing) and returns 0, or nonzero to stop with an input error. The
+ * reader is called front to back in chunks of about 64 MB, once to sketch
+ * the cuts and once to bin the rows, both on the device when the plan allows;
+ * the matrix is gathered into host memory only where a host pass needs it
+ * whole (weighted rows, whose sketch runs on the host, or host binning).
+ * Labels and weights are whole arrays. The result equals fbt_train on the
+ * same rows. */
+typedef int (*fbt_rows_fn)(void *user, uint64_t row_begin, uint64_t n_rows, float *out);
+int fbt_train_rows(fbt_rows_fn fn, void *user, uint64_t n_rows, uint32_t n_features,
+                   const float *labels, const float *weights, const uint8_t *categorical,
+                   const int8_t *monotone, uint32_t n_monotone, const fbt_params *params,
+                   fbt_model **out);
 /* fbt_train with the cuts given instead of sketched (the cut_values /
  * cut_offsets fbt_sketch_cuts returns for the same data, max_bin, weights
  * and categorical flags), so several models over one matrix share one

@@ -1,0 +1,109 @@
+"""GPU: training from a Parquet file or an Arrow table (the rows streamed to
+the device sketch and binning in chunks through fbt_train_rows) gives the
+model that training from the same rows as a numpy matrix gives, byte for
+byte: unit weights (streamed), weighted rows (gathered for the host sketch),
+dictionary columns as categorical features, a feature the device sketch
+leaves to the host (zeros of both signs among its cuts), and a reader error
+raised back to the caller."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pa = pytest.importorskip("pyarrow")
+pq = pytest.importorskip("pyarrow.parquet")
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def fb():
+    import ferrisboost_amd as fb
+    from ferrisboost_amd import _native as N
+
+    if not N.device_available(0):
+        pytest.fail("no gfx950 device: the GPU suite needs an MI355X")
+    return fb
+
+
+@pytest.fixture
+def small_reads(monkeypatch):
+    # several read chunks per pass
+    monkeypatch.setenv("FB_READ_ROWS", "3001")
+
+
+def _data(n=20_000, seed=0):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n, 6)).astype(np.float32)
+    x[rng.random((n, 6)) < 0.05] = np.nan
+    # zeros of both signs, with zero among the cuts (left to the host sketch)
+    x[:, 5] = np.where(rng.random(n) < 0.3, np.round(rng.standard_normal(n)) * 0.0,
+                       rng.standard_normal(n)).astype(np.float32)
+    codes = rng.integers(0, 7, n)
+    y = (np.nan_to_num(x[:, 0]) + (codes % 3) * 0.7 + rng.standard_normal(n) * 0.3 > 0.5)
+    return x, codes, y.astype(np.float32), rng.uniform(0.2, 2.0, n).astype(np.float32)
+
+
+def _table(x, codes, y, w, categorical, weight_column=True):
+    cols = {f"f{j}": pa.array(x[:, j], mask=np.isnan(x[:, j])) for j in range(x.shape[1])}
+    if categorical:
+        cols["c"] = pa.DictionaryArray.from_arrays(pa.array(codes.astype(np.int32)),
+                                                   pa.array([f"k{i}" for i in range(7)]))
+    cols["label"] = pa.array(y)
+    if weight_column:
+        cols["weight"] = pa.array(w)
+    return pa.table(cols)
+
+
+PARAMS = {"objective": "binary:logistic", "max_depth": 6, "eta": 0.3, "max_bin": 64}
+
+
+@pytest.mark.parametrize("weighted", [False, True])
+def test_parquet_trains_the_array_model(fb, tmp_path, small_reads, weighted):
+    x, codes, y, w = _data()
+    path = tmp_path / "train.parquet"
+    pq.write_table(_table(x, codes, y, w, False, weight_column=weighted), path,
+                   row_group_size=4096)
+    m_file = fb.train(PARAMS, str(path), "label", weight="weight" if weighted else None,
+                      num_boost_round=5)
+    arr = np.ascontiguousarray(x)
+    # feature 5 holds both zero signs and a zero cut: the device sketch leaves it to the host
+    cuts = fb.sketch(arr, 64)
+    z = x[:, 5][x[:, 5] == 0]
+    assert (cuts.values[cuts.offsets[5]:cuts.offsets[6]] == 0).any()
+    assert np.signbit(z).any() and not np.signbit(z).all()
+    m_arr = fb.train(PARAMS, arr, y, weight=w if weighted else None, num_boost_round=5)
+    assert m_file.to_json() == m_arr.to_json()
+    assert np.array_equal(m_file.train_margins(y.size).view(np.uint32),
+                          m_arr.train_margins(y.size).view(np.uint32))
+    assert m_file.feature_names == [f"f{j}" for j in range(6)]
+    assert bool(m_file.stats["device_sketch"]) == (not weighted)
+    assert m_file.stats["device_binning"]
+
+
+def test_dictionary_columns_are_categorical(fb, small_reads):
+    x, codes, y, w = _data(seed=1)
+    t = _table(x, codes, y, w, True)
+    p = dict(PARAMS, enable_categorical=True)
+    m_tab = fb.train(p, t, "label", num_boost_round=5)
+    arr = np.ascontiguousarray(np.column_stack([x, codes.astype(np.float32), w]))
+    m_arr = fb.train(dict(PARAMS, feature_types=["q"] * 6 + ["c", "q"]), arr, y,
+                     num_boost_round=5)
+    assert m_tab.to_json() == m_arr.to_json()
+    with pytest.raises(ValueError, match="enable_categorical"):
+        fb.train(PARAMS, t, "label", num_boost_round=1)
+
+
+def test_reader_errors_reach_the_caller(fb, monkeypatch):
+    from ferrisboost_amd import arrow_rows
+
+    x, codes, y, w = _data(n=2000, seed=2)
+    t = _table(x, codes, y, w, False)
+
+    def broken(self, batch):
+        raise OSError("the source went away")
+
+    monkeypatch.setattr(arrow_rows.ArrowRows, "_rows_of", broken)
+    with pytest.raises(OSError, match="went away"):
+        fb.train(PARAMS, t, "label", num_boost_round=1)
