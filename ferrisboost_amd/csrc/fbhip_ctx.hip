@@ -1585,6 +1585,11 @@ int fbh_set_quantile(fbh_ctx *c, uint32_t n_alphas, const float *alphas, const f
             c->leaf_ids = c->alloc<uint16_t>(c->n_rows, "leaf ids");
             c->quantile_slot = c->alloc<float2>(1, "quantile scale");
             c->pinned(c->pin_src, std::max<uint64_t>(4 * c->n_rows, 64));
+            for (int k = 0; k < EXCHANGE_CHUNKS; k++) {
+                hipEvent_t e;
+                check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "event");
+                c->chunk_ev.push_back(e);
+            }
         } else if (c->objective != 3) {
             throw InputError("the context already holds another objective");
         }
@@ -1646,12 +1651,24 @@ static void quantile_take_scale(fbh_ctx *c) {
     float *terms = c->gpair_f32;  // rewritten by the gradient pass that follows
     check(launch_quantile_terms(c->cur_margin(), c->labels, w, n, terms, c->stream),
           "quantile terms");
+    // The terms come down in chunks, each signalling its own event, and the
+    // host sums chunk k while later chunks are still in flight.
     float *host = static_cast<float *>(c->pin_src.p);
-    check(hipMemcpyAsync(host, terms, 4 * n, hipMemcpyDeviceToHost, c->stream),
-          "quantile terms download");
-    c->sync();
+    const uint64_t step = ((n + EXCHANGE_CHUNKS - 1) / EXCHANGE_CHUNKS + 255) & ~uint64_t(255);
+    for (int k = 0; k < EXCHANGE_CHUNKS; k++) {
+        const uint64_t b = std::min<uint64_t>(n, k * step), e = std::min<uint64_t>(n, b + step);
+        if (e > b)
+            check(hipMemcpyAsync(host + b, terms + b, 4 * (e - b), hipMemcpyDeviceToHost,
+                                 c->stream),
+                  "quantile terms download");
+        check(hipEventRecord(c->chunk_ev[k], c->stream), "event");
+    }
     double stat = 0.0;
-    for (uint64_t i = 0; i < n; i++) stat += (double)host[i];
+    for (int k = 0; k < EXCHANGE_CHUNKS; k++) {
+        const uint64_t b = std::min<uint64_t>(n, k * step), e = std::min<uint64_t>(n, b + step);
+        check(hipEventSynchronize(c->chunk_ev[k]), "quantile terms download");
+        for (uint64_t i = b; i < e; i++) stat += (double)host[i];
+    }
     float scale = 0.0f;
     if (!(std::fabs(c->quantile_sum_w) < 1e-6)) {
         const double root_mean = stat / c->quantile_sum_w;

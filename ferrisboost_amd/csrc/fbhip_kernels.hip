@@ -2122,8 +2122,26 @@ __device__ void block_sum2(uint64_t ag, uint64_t ah, int64_t *block_sum);
 // pass then tells whether those were this round's scales
 // (gradient_fixup_kernel redoes the pairs when not). The same grid and
 // operations as without spec, so each row's g and h are the same floats.
+// Calls f with std::integral_constant<int, mode> for the gradient modes 0-6.
+template <class F>
+hipError_t with_mode(int mode, F &&f) {
+    switch (mode) {
+        case 0: return f(std::integral_constant<int, 0>{});
+        case 1: return f(std::integral_constant<int, 1>{});
+        case 2: return f(std::integral_constant<int, 2>{});
+        case 3: return f(std::integral_constant<int, 3>{});
+        case 4: return f(std::integral_constant<int, 4>{});
+        case 5: return f(std::integral_constant<int, 5>{});
+        case 6: return f(std::integral_constant<int, 6>{});
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// The objective mode is a template argument, so each objective's kernel
+// holds only its own arithmetic (and registers).
+template <int MODE>
 __global__ __launch_bounds__(256) void gradient_kernel(const float *src, const float *y,
-                                                       const float *w, uint64_t n, int mode,
+                                                       const float *w, uint64_t n,
                                                        float *g2n, uint64_t th, uint64_t seed,
                                                        uint64_t tree, double *block_max,
                                                        const ScalesDev *spec, int64_t *fixed,
@@ -2155,7 +2173,7 @@ __global__ __launch_bounds__(256) void gradient_kernel(const float *src, const f
             const uint64_t i = base + u * S;
             if (i >= n) continue;
             float g, h;
-            row_pair(mode, sv[u], yv[u], w != nullptr, wv[u], stats, cls, i, g, h);
+            row_pair(MODE, sv[u], yv[u], w != nullptr, wv[u], stats, cls, i, g, h);
             if (block_max) {
                 if (!row_selected(i, th, seed, tree)) g = h = 0.0f;
                 mg = fmax(mg, finite_abs(g));
@@ -2178,8 +2196,9 @@ __global__ __launch_bounds__(256) void gradient_kernel(const float *src, const f
 // After a speculative gradient pass: when the bounds gave other scales than
 // the ones the pass used, the pairs and block sums are computed again (the
 // same gradient) under the right scales; otherwise every block leaves at once.
+template <int MODE>
 __global__ __launch_bounds__(256) void gradient_fixup_kernel(const float *src, const float *y,
-                                                             const float *w, uint64_t n, int mode,
+                                                             const float *w, uint64_t n,
                                                              uint64_t th, uint64_t seed,
                                                              uint64_t tree,
                                                              const ScalesDev *scales,
@@ -2191,7 +2210,7 @@ __global__ __launch_bounds__(256) void gradient_fixup_kernel(const float *src, c
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * blockDim.x) {
         float g, h;
-        row_pair(mode, src[i], y[i], w != nullptr, w ? w[i] : 1.0f, stats, cls, i, g, h);
+        row_pair(MODE, src[i], y[i], w != nullptr, w ? w[i] : 1.0f, stats, cls, i, g, h);
         if (!row_selected(i, th, seed, tree)) g = h = 0.0f;
         const int64_t qg = sat_i64(round((double)g * sg));
         const int64_t qh = sat_i64(round((double)h * sh));
@@ -2211,13 +2230,16 @@ hipError_t launch_gradient_spec(const float *src, const float *y, const float *w
                                 int64_t *fixed, int64_t *block_sum, float *g2n, hipStream_t s,
                                 const float2 *stats, uint32_t cls) {
     if (n_blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(gradient_kernel, dim3(n_blocks), dim3(256), 0, s, src, y, w, n, mode,
-                       g2n, th, seed, tree, block_max, scales, fixed, block_sum, stats, cls);
-    hipLaunchKernelGGL(reduce_max_kernel, dim3(1), dim3(1024), 0, s, block_max, n_blocks,
-                       block_max + 2 * n_blocks, n, scales);
-    hipLaunchKernelGGL(gradient_fixup_kernel, dim3(n_blocks), dim3(256), 0, s, src, y, w, n, mode,
-                       th, seed, tree, scales, fixed, block_sum, stats, cls);
-    return hipGetLastError();
+    return with_mode(mode, [&](auto M) {
+        constexpr int MODE = decltype(M)::value;
+        hipLaunchKernelGGL(gradient_kernel<MODE>, dim3(n_blocks), dim3(256), 0, s, src, y, w, n,
+                           g2n, th, seed, tree, block_max, scales, fixed, block_sum, stats, cls);
+        hipLaunchKernelGGL(reduce_max_kernel, dim3(1), dim3(1024), 0, s, block_max, n_blocks,
+                           block_max + 2 * n_blocks, n, scales);
+        hipLaunchKernelGGL(gradient_fixup_kernel<MODE>, dim3(n_blocks), dim3(256), 0, s, src, y,
+                           w, n, th, seed, tree, scales, fixed, block_sum, stats, cls);
+        return hipGetLastError();
+    });
 }
 
 hipError_t launch_gradient(const float *src, const float *y, const float *w, uint64_t n, int mode,
@@ -2227,9 +2249,12 @@ hipError_t launch_gradient(const float *src, const float *y, const float *w, uin
     const uint32_t blocks =
         block_max ? n_blocks : (uint32_t)std::min<uint64_t>((n + 255) / 256, 8192);
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(gradient_kernel, dim3(blocks), dim3(256), 0, s, src, y, w, n, mode, g2n,
-                       th, seed, tree, block_max, nullptr, nullptr, nullptr, stats, cls);
-    return hipGetLastError();
+    return with_mode(mode, [&](auto M) {
+        constexpr int MODE = decltype(M)::value;
+        hipLaunchKernelGGL(gradient_kernel<MODE>, dim3(blocks), dim3(256), 0, s, src, y, w, n,
+                           g2n, th, seed, tree, block_max, nullptr, nullptr, nullptr, stats, cls);
+        return hipGetLastError();
+    });
 }
 
 __global__ __launch_bounds__(256) void sigmoid_kernel(const float *in, uint64_t n, float *out) {

@@ -839,38 +839,43 @@ std::vector<float> quantile_intercepts(const float *alphas, uint32_t k, const fl
         std::memcpy(&b, &v, 4);
         return b ^ (int32_t)((uint32_t)(b >> 31) >> 1);
     };
-    std::vector<uint32_t> idx(n);
-    for (uint64_t i = 0; i < n; i++) idx[i] = (uint32_t)i;
-    std::stable_sort(idx.begin(), idx.end(),
-                     [&](uint32_t a, uint32_t b) { return key(y[a]) < key(y[b]); });
-    std::vector<float> cdf;
-    if (w) {
-        cdf.resize(n);
-        cdf[0] = w[idx[0]];
-        for (uint64_t i = 1; i < n; i++) cdf[i] = cdf[i - 1] + w[idx[i]];
-    }
+    auto lt = [&](float a, float b) { return key(a) < key(b); };
     std::vector<float> out(k);
-    for (uint32_t j = 0; j < k; j++) {
-        const double alpha = (double)alphas[j];
-        if (!w) {
-            const double nf = (double)n;
+    if (!w) {
+        // Only order statistics are read, and labels of equal keys are equal
+        // bits, so selection gives the stable sort's values in O(n).
+        std::vector<float> v(y, y + n);
+        const double nf = (double)n;
+        for (uint32_t j = 0; j < k; j++) {
+            const double alpha = (double)alphas[j];
             if (alpha <= 1.0 / (nf + 1.0)) {
-                out[j] = y[idx[0]];
+                out[j] = *std::min_element(v.begin(), v.end(), lt);
             } else if (alpha >= nf / (nf + 1.0)) {
-                out[j] = y[idx[n - 1]];
+                out[j] = *std::max_element(v.begin(), v.end(), lt);
             } else {
                 const double x = alpha * (nf + 1.0);
                 const double lo = std::floor(x) - 1.0;
                 const double d = (x - 1.0) - lo;
-                const float v0 = y[idx[(uint64_t)lo]], v1 = y[idx[(uint64_t)lo + 1]];
+                const uint64_t i = (uint64_t)lo;
+                std::nth_element(v.begin(), v.begin() + i, v.end(), lt);
+                const float v0 = v[i];
+                const float v1 = *std::min_element(v.begin() + i + 1, v.end(), lt);
                 out[j] = (float)((double)v0 + d * (double)(v1 - v0));
             }
-        } else {
-            const float thresh = (float)((double)cdf[n - 1] * alpha);
-            const uint64_t at = (uint64_t)(std::lower_bound(cdf.begin(), cdf.end(), thresh) -
-                                           cdf.begin());
-            out[j] = y[idx[std::min<uint64_t>(at, n - 1)]];
         }
+        return out;
+    }
+    std::vector<uint32_t> idx(n);
+    for (uint64_t i = 0; i < n; i++) idx[i] = (uint32_t)i;
+    std::stable_sort(idx.begin(), idx.end(), [&](uint32_t a, uint32_t b) { return lt(y[a], y[b]); });
+    std::vector<float> cdf(n);
+    cdf[0] = w[idx[0]];
+    for (uint64_t i = 1; i < n; i++) cdf[i] = cdf[i - 1] + w[idx[i]];
+    for (uint32_t j = 0; j < k; j++) {
+        const float thresh = (float)((double)cdf[n - 1] * (double)alphas[j]);
+        const uint64_t at =
+            (uint64_t)(std::lower_bound(cdf.begin(), cdf.end(), thresh) - cdf.begin());
+        out[j] = y[idx[std::min<uint64_t>(at, n - 1)]];
     }
     return out;
 }
