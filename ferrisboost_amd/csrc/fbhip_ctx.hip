@@ -280,6 +280,7 @@ struct fbh_ctx {
         // Two result slots (state, tree, category words, leaf values), so a
         // tree can be collected while the next one is already enqueued.
         PinnedBuf out[2];
+        uint8_t *out_dev[2] = {nullptr, nullptr};  // device views of out
         hipEvent_t done[2] = {nullptr, nullptr};
         uint64_t next_slot = 0;
         struct Job {
@@ -2785,8 +2786,14 @@ void ensure_grow(fbh_ctx *c, uint32_t D) {
     for (int k = 0; k < 2; k++) {
         if (G.out[k].p) (void)hipHostFree(G.out[k].p);
         G.out[k].p = nullptr;
-        c->pinned(G.out[k], al256(sizeof(GrowState)) + al256(sizeof(TreeNodeDev) * G.tree_cap) +
-                                al256(8 * G.cat_cap) + al256(4 * G.leaf_cap));
+        // Coherent: the kernel's writes go to host memory, not the device caches.
+        const size_t bytes = al256(sizeof(GrowState)) + al256(sizeof(TreeNodeDev) * G.tree_cap) +
+                             al256(8 * G.cat_cap) + al256(4 * G.leaf_cap);
+        check(hipHostMalloc(&G.out[k].p, bytes, hipHostMallocCoherent), "pinned host allocation");
+        G.out[k].bytes = bytes;
+        void *dv = nullptr;
+        check(hipHostGetDevicePointer(&dv, G.out[k].p, 0), "device view of the tree buffer");
+        G.out_dev[k] = static_cast<uint8_t *>(dv);
         if (!G.done[k])
             check(hipEventCreateWithFlags(&G.done[k], hipEventDisableTiming), "event");
     }
@@ -3004,23 +3011,16 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     c->ids_fresh = idb != 0;
     c->leaves_deferred = defer;
 
-    // Download into the next result slot; collected in order.
+    // Written into the next result slot by a kernel in the stream (no copy
+    // engine); collected in order.
     const int k = (int)(GB.next_slot++ & 1);
-    uint8_t *po = static_cast<uint8_t *>(GB.out[k].p);
     const size_t o_tree = al256(sizeof(GrowState));
     const size_t o_cats = o_tree + al256(sizeof(TreeNodeDev) * GB.tree_cap);
     const size_t o_vals = o_cats + al256(8 * GB.cat_cap);
-    check(hipMemcpyAsync(po, GB.st, sizeof(GrowState), hipMemcpyDeviceToHost, c->stream),
-          "tree download");
-    check(hipMemcpyAsync(po + o_tree, GB.tree, sizeof(TreeNodeDev) * GB.tree_cap,
-                         hipMemcpyDeviceToHost, c->stream),
-          "tree download");
-    if (c->cat_words_per_node)
-        check(hipMemcpyAsync(po + o_cats, GB.tree_cats, 8 * GB.cat_cap, hipMemcpyDeviceToHost,
-                             c->stream),
-              "tree download");
-    check(hipMemcpyAsync(po + o_vals, GB.leaf_vals, 4 * GB.leaf_cap, hipMemcpyDeviceToHost,
-                         c->stream),
+    check(launch_tree_out(GB.st, GB.tree, (uint32_t)GB.tree_cap,
+                          c->cat_words_per_node ? GB.tree_cats : nullptr, (uint32_t)GB.cat_cap,
+                          GB.leaf_vals, (uint32_t)GB.leaf_cap, GB.out_dev[k], o_tree, o_cats,
+                          o_vals, c->stream),
           "tree download");
     check(hipEventRecord(GB.done[k], c->stream), "event");
     GB.pending.push_back({k, c->cat_words_per_node});

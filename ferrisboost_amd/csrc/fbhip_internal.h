@@ -358,6 +358,12 @@ hipError_t launch_leaf_plan(LeafDev *leaves, GrowState *st, hipStream_t s);
 // bundle (feat_off[f]: byte offset of feature f in the bundle row, bit 15 set
 // for 16-bit cells); at most MAX_WALK_NODES tree nodes. Workgroup 0 writes
 // each leaf's position into its node (pad[1]). margin NULL: leaf ids only.
+// A grown tree's state, used nodes, category words and leaf values into a
+// device view of pinned host memory, in stream order.
+hipError_t launch_tree_out(const GrowState *st, const TreeNodeDev *tree, uint32_t tree_cap,
+                           const uint64_t *cats, uint32_t cat_cap, const float *vals,
+                           uint32_t leaf_cap, uint8_t *out, uint64_t o_tree, uint64_t o_cats,
+                           uint64_t o_vals, hipStream_t s);
 hipError_t launch_tree_leaves(const uint8_t *bundle, uint32_t pitch, uint64_t n_rows,
                               TreeNodeDev *tree, const uint64_t *tree_cats,
                               const uint16_t *feat_off, GrowState *st, void *ids, int id_bytes,

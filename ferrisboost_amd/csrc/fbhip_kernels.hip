@@ -2099,6 +2099,46 @@ hipError_t launch_quantile_scale_fast(const float *margin, const float *y, const
     return hipGetLastError();
 }
 
+// A grown tree's result into pinned host memory from the stream's own queue
+// (a copy-engine transfer makes the compute queue wait for a handoff between
+// engines, measured at 50-75 us a tree): the state, then the used nodes,
+// category words and leaf values at their offsets in `out` (a device view of
+// the host buffer). Counts come from the state and are clamped to the
+// capacities.
+__device__ __forceinline__ void copy_words(const void *src, void *dst, uint64_t bytes,
+                                           uint64_t t, uint64_t T) {
+    const uint32_t *s = static_cast<const uint32_t *>(src);
+    uint32_t *d = static_cast<uint32_t *>(dst);
+    for (uint64_t i = t; i < bytes / 4; i += T) d[i] = s[i];
+}
+
+__global__ __launch_bounds__(256) void tree_out_kernel(const GrowState *st, const TreeNodeDev *tree,
+                                                       uint32_t tree_cap, const uint64_t *cats,
+                                                       uint32_t cat_cap, const float *vals,
+                                                       uint32_t leaf_cap, uint8_t *out,
+                                                       uint64_t o_tree, uint64_t o_cats,
+                                                       uint64_t o_vals) {
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t T = (uint64_t)gridDim.x * blockDim.x;
+    const uint32_t nt = min(st->tree_size, tree_cap);
+    const uint32_t nl = min(st->n_leaves, leaf_cap);
+    const uint32_t nc = cats ? min(st->tree_cat_words, cat_cap) : 0u;
+    copy_words(st, out, sizeof(GrowState), t, T);
+    copy_words(tree, out + o_tree, (uint64_t)nt * sizeof(TreeNodeDev), t, T);
+    if (nc) copy_words(cats, out + o_cats, (uint64_t)nc * 8, t, T);
+    copy_words(vals, out + o_vals, (uint64_t)nl * 4, t, T);
+    __threadfence_system();
+}
+
+hipError_t launch_tree_out(const GrowState *st, const TreeNodeDev *tree, uint32_t tree_cap,
+                           const uint64_t *cats, uint32_t cat_cap, const float *vals,
+                           uint32_t leaf_cap, uint8_t *out, uint64_t o_tree, uint64_t o_cats,
+                           uint64_t o_vals, hipStream_t s) {
+    hipLaunchKernelGGL(tree_out_kernel, dim3(8), dim3(256), 0, s, st, tree, tree_cap, cats,
+                       cat_cap, vals, leaf_cap, out, o_tree, o_cats, o_vals);
+    return hipGetLastError();
+}
+
 hipError_t launch_softmax_stats(const float *margin, uint32_t K, uint64_t n, int fast,
                                 float2 *stats, hipStream_t s) {
     const uint32_t blocks = (uint32_t)std::min<uint64_t>((n + 255) / 256, 8192);
