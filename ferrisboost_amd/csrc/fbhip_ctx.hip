@@ -117,6 +117,7 @@ struct DeviceBuf {
 struct PinnedBuf {
     void *p = nullptr;
     size_t bytes = 0;
+    void *dev = nullptr;  // device view of a mapped (coherent) buffer
 };
 
 }  // namespace
@@ -467,6 +468,18 @@ struct fbh_ctx {
         check(hipHostMalloc(&b.p, bytes, hipHostMallocDefault), "pinned host allocation");
         b.bytes = bytes;
     }
+    // Coherent pinned memory that kernels read through its device view:
+    // host-to-device sends then run as a kernel in the compute stream
+    // (send_mapped) instead of a copy-engine transfer, whose handoff between
+    // engines stalls the queue for tens of microseconds.
+    void pinned_mapped(PinnedBuf &b, size_t bytes) {
+        check(hipHostMalloc(&b.p, bytes, hipHostMallocCoherent), "pinned host allocation");
+        b.bytes = bytes;
+        check(hipHostGetDevicePointer(&b.dev, b.p, 0), "device view of pinned memory");
+    }
+    void send_mapped(void *dst, const PinnedBuf &b, size_t bytes) {
+        check(launch_copy_bytes(dst, b.dev, bytes, stream), "launch tables");
+    }
 
     uint8_t *host_alloc(size_t bytes, const char *what) {
         void *p = nullptr;
@@ -492,8 +505,7 @@ struct fbh_ctx {
     }
     // Copies `bytes` of the slot to dst in stream order; marks the slot busy.
     void stage_send(int slot, void *dst, size_t bytes) {
-        check(hipMemcpyAsync(dst, pin_stage[slot].p, bytes, hipMemcpyHostToDevice, stream),
-              "launch tables");
+        send_mapped(dst, pin_stage[slot], bytes);
         check(hipEventRecord(stage_ev[slot], stream), "event");
     }
 
@@ -1102,7 +1114,7 @@ int fbh_ctx_create(int device, uint64_t n_rows, const fbh_shape *shape, const fb
             return c->alloc<uint8_t>(b, what);
         });
         for (int k = 0; k < fbh_ctx::STAGE_SLOTS; k++) {
-            c->pinned(c->pin_stage[k], c->stage_bytes);
+            c->pinned_mapped(c->pin_stage[k], c->stage_bytes);
             check(hipEventCreateWithFlags(&c->stage_ev[k], hipEventDisableTiming), "event");
         }
         c->pinned(c->pin_leaves, (sizeof(LeafDev) + 4) * MAX_NODES);

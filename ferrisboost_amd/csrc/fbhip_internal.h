@@ -358,6 +358,9 @@ hipError_t launch_leaf_plan(LeafDev *leaves, GrowState *st, hipStream_t s);
 // bundle (feat_off[f]: byte offset of feature f in the bundle row, bit 15 set
 // for 16-bit cells); at most MAX_WALK_NODES tree nodes. Workgroup 0 writes
 // each leaf's position into its node (pad[1]). margin NULL: leaf ids only.
+// bytes from a device view of coherent pinned host memory to device memory,
+// as a kernel in the stream.
+hipError_t launch_copy_bytes(void *dst, const void *src, uint64_t bytes, hipStream_t s);
 // A grown tree's state, used nodes, category words and leaf values into a
 // device view of pinned host memory, in stream order.
 hipError_t launch_tree_out(const GrowState *st, const TreeNodeDev *tree, uint32_t tree_cap,

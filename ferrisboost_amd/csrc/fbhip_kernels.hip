@@ -2139,6 +2139,31 @@ hipError_t launch_tree_out(const GrowState *st, const TreeNodeDev *tree, uint32_
     return hipGetLastError();
 }
 
+// bytes from src (a device view of coherent pinned host memory) to dst, in
+// the stream (no copy engine): four-byte words, then the tail.
+__global__ __launch_bounds__(256) void copy_bytes_kernel(uint8_t *dst, const uint8_t *src,
+                                                         uint64_t bytes) {
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t T = (uint64_t)gridDim.x * blockDim.x;
+    const uint64_t words = bytes / 4;
+    if ((((uintptr_t)dst | (uintptr_t)src) & 3u) == 0) {
+        const uint32_t *s = reinterpret_cast<const uint32_t *>(src);
+        uint32_t *d = reinterpret_cast<uint32_t *>(dst);
+        for (uint64_t i = t; i < words; i += T) d[i] = s[i];
+        for (uint64_t i = 4 * words + t; i < bytes; i += T) dst[i] = src[i];
+    } else {
+        for (uint64_t i = t; i < bytes; i += T) dst[i] = src[i];
+    }
+}
+
+hipError_t launch_copy_bytes(void *dst, const void *src, uint64_t bytes, hipStream_t s) {
+    if (bytes == 0) return hipSuccess;
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((bytes / 4 + 255) / 256 + 1, 64);
+    hipLaunchKernelGGL(copy_bytes_kernel, dim3(blocks), dim3(256), 0, s,
+                       static_cast<uint8_t *>(dst), static_cast<const uint8_t *>(src), bytes);
+    return hipGetLastError();
+}
+
 hipError_t launch_softmax_stats(const float *margin, uint32_t K, uint64_t n, int fast,
                                 float2 *stats, hipStream_t s) {
     const uint32_t blocks = (uint32_t)std::min<uint64_t>((n + 255) / 256, 8192);
