@@ -2736,8 +2736,7 @@ constexpr uint32_t PACK_LDS_STRIDE = 33;  // dwords a row in LDS (32 + 1: no ban
 template <int W>
 __global__ __launch_bounds__(256) void pack_tiles_kernel(const PackTileDev *__restrict__ tiles,
                                                          uint32_t n_tiles, uint64_t n_rows) {
-    constexpr uint32_t PER = 8 / W;       // tiles a bundle
-    constexpr uint32_t CELLS = 16 * PER;  // cells a bundle row (128 bytes)
+    constexpr uint32_t PER = 8 / W;       // tiles a bundle (16 cells each: 128 bytes a row)
     constexpr uint32_t CPD = 4 / W;       // cells a dword
     __shared__ uint32_t rec[PACK_ROWS * PACK_LDS_STRIDE];
     const uint32_t t0 = blockIdx.y * PER;
