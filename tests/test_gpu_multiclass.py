@@ -194,3 +194,16 @@ def test_labels_outside_the_classes_are_value_errors(fb):
         yy[10] = bad
         with pytest.raises(ValueError, match="integers in"):
             fb.train({"objective": "multi:softprob", "num_class": 3}, x, yy, num_boost_round=1)
+
+
+def test_large_first_rounds_equal_oracle(fb, oracle):
+    """2M rows x 12 features, 4 classes, depth 8: the softmax statistics and
+    class pairs at size, against the oracle's first rounds."""
+    x, y, _ = _data(2_000_000, 4, seed=41, n_feat=12)
+    params = {"objective": "multi:softprob", "num_class": 4, "max_depth": 8, "eta": 0.1,
+              "max_bin": 255}
+    pm = fb.train(params, x, y, num_boost_round=2)
+    om = oracle.train(x, y, oracle.make_params(n_rounds=2, nthread=8, **params))
+    assert_same_models(om, pm)
+    assert np.array_equal(pm.train_margins(y.size).view(np.uint32),
+                          om.train_margins(y.size).view(np.uint32))
