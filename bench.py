@@ -210,7 +210,8 @@ def train_workload(args, X, y, params, desc: str, traffic_tag: str):
                 np.array_equal(om.tree(t)[f], model.tree_nodes(t)[f])
                 for t in range(om.n_trees) for f in om.tree(t).dtype.names if f != "pad")
 
-    config = {"workload": desc, "rows": int(X.shape[0]), "features": int(X.shape[1])}
+    config = {"workload": desc, "rows": int(X.shape[0]), "features": int(X.shape[1]),
+              "rounds": rounds}
     config.update({k: params[k] for k in ("max_bin", "max_depth", "max_leaves", "grow_policy",
                                           "colsample_bytree", "objective", "num_class",
                                           "quantile_alpha", "gpu_math")
@@ -221,6 +222,8 @@ def train_workload(args, X, y, params, desc: str, traffic_tag: str):
         "hist_gbps": round(hist_gbps, 1),
         "hist_ms_per_round": round(t_hist_ms / args.steps, 3),
         "hist_launches_per_round": round(launches / rounds, 2),
+        # the whole job: setup (sketch and binning) plus every round, warmup included
+        "job_seconds": round(model.stats["setup_seconds"] + float(wall.sum()), 3),
         "gradient_ms_per_round": round(1e3 * model.stats["host_gradient_seconds"] / rounds, 3),
         # setup (outside the timed rounds): the quantile sketch, then binning
         # (each on the device when it fits, the host's cuts and bins either way)
@@ -404,10 +407,16 @@ def shap_workload(args):
     return out
 
 
+# Boosting rounds of the full training jobs the bench workloads stand for.
+FULL_ROUNDS = {"narrow": 500, "wide": 200, "widebin": 300}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default: the rest of the workload's full round count "
+                         "for narrow, wide and widebin, else 20)")
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="narrow",
                     choices=["narrow", "multiclass", "quantile", "wide", "widebin", "streaming",
@@ -422,6 +431,11 @@ def main() -> int:
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a device copy of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
+    if args.steps is None:
+        # A training workload's default run is the whole job: warmup plus
+        # timed rounds add up to its round count (500, 200 and 300 rounds).
+        full = FULL_ROUNDS.get(args.workload)
+        args.steps = max(1, full - args.warmup) if full else 20
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported "
               "(the training path is single-device)", file=sys.stderr)
