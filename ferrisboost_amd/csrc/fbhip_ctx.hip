@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <cmath>
 #include <deque>
+#include <future>
 #include <cstdio>
 #include <cstdlib>
 #include <map>
@@ -358,6 +359,21 @@ struct fbh_ctx {
     std::vector<float> alphas;          // quantile_alpha of each output
     double quantile_sum_w = 0.0;        // the serial double sum of the weights (or n)
     float quantile_scale = 0.0f;        // the last scale taken (exact mode)
+    // Exact scales of several outputs, summed on host threads side by side:
+    // output j's margins change only with output j's own trees, so every
+    // output's sum can start when the first of them is needed.
+    std::vector<std::future<double>> q_sums;  // output j's pending or finished sum
+    std::vector<uint8_t> q_have;        // q_sums[j] is for output j's current margins
+    float *q_terms = nullptr;           // n_outputs x n_rows terms (device)
+    PinnedBuf pin_q;                    // the same terms on the host
+    void q_forget(int k) {              // k < 0: every output
+        for (size_t j = 0; j < q_sums.size(); j++) {
+            if (k >= 0 && j != (size_t)k) continue;
+            if (q_sums[j].valid()) q_sums[j].wait();
+            q_sums[j] = std::future<double>();
+            q_have[j] = 0;
+        }
+    }
     float *cur_margin() const { return margin + (uint64_t)out_k * n_rows; }
     bool fast_math = false;             // gpu_math="fast": hardware exp in the logistic gradient
     float *labels = nullptr, *gweights = nullptr, *margin = nullptr;
@@ -382,6 +398,7 @@ struct fbh_ctx {
     ~fbh_ctx() { release(); }
 
     void release() {
+        q_forget(-1);  // the sums read pin_q and wait on chunk_ev
         if (device >= 0) (void)hipSetDevice(device);
         if (stream) (void)hipStreamSynchronize(stream);
         for (auto &a : allocs)
@@ -403,7 +420,9 @@ struct fbh_ctx {
         }
         if (pin_ids.p) (void)hipHostFree(pin_ids.p);
         if (pin_src.p) (void)hipHostFree(pin_src.p);
-        pin_leaves.p = pin_out.p = pin_ids.p = pin_src.p = nullptr;
+        if (pin_q.p) (void)hipHostFree(pin_q.p);
+        pin_leaves.p = pin_out.p = pin_ids.p = pin_src.p = pin_q.p = nullptr;
+        q_terms = nullptr;
         if (copy_stream) (void)hipStreamSynchronize(copy_stream);
         for (void *h : host_allocs) (void)hipHostFree(h);
         host_allocs.clear();
@@ -1597,6 +1616,8 @@ int fbh_set_quantile(fbh_ctx *c, uint32_t n_alphas, const float *alphas, const f
             c->margin = c->alloc<float>((uint64_t)n_alphas * c->n_rows, "quantile margins");
             c->leaf_ids = c->alloc<uint16_t>(c->n_rows, "leaf ids");
             c->quantile_slot = c->alloc<float2>(1, "quantile scale");
+            c->q_sums.resize(n_alphas);
+            c->q_have.assign(n_alphas, 0);
             c->pinned(c->pin_src, std::max<uint64_t>(4 * c->n_rows, 64));
             for (int k = 0; k < EXCHANGE_CHUNKS; k++) {
                 hipEvent_t e;
@@ -1621,6 +1642,7 @@ int fbh_set_quantile(fbh_ctx *c, uint32_t n_alphas, const float *alphas, const f
             sw = (double)c->n_rows;
         }
         c->quantile_sum_w = sw;
+        c->q_forget(-1);
         for (uint32_t k = 0; k < n_alphas; k++)
             check(launch_fill_f32(c->margin + (uint64_t)k * c->n_rows, intercepts[k], c->n_rows,
                                   c->stream),
@@ -1651,6 +1673,49 @@ int fbh_quantile_last_scale(fbh_ctx *c, float *scale) {
 // gradient reads. Exact: each row's f32 term on the device, summed on the
 // host in row order in double (the reference's serial sum, which no parallel
 // order reproduces). Fast: a fixed-order reduction on the device.
+static void quantile_finish(fbh_ctx *c, double stat, float alpha);
+
+// Every output's terms at once, downloaded in chunks, each output summed in
+// row order on a host thread of its own (the same serial double sum as a
+// single output's).
+static void quantile_sum_all(fbh_ctx *c, const float *w) {
+    c->q_forget(-1);  // their buffers and events are reused below
+    const uint32_t K = c->n_outputs;
+    const uint64_t n = c->n_rows;
+    if (!c->q_terms) {
+        c->q_terms = c->alloc<float>((uint64_t)K * n, "quantile terms");
+        c->pinned(c->pin_q, 4ull * K * n);
+    }
+    for (uint32_t j = 0; j < K; j++)
+        check(launch_quantile_terms(c->margin + (uint64_t)j * n, c->labels, w, n,
+                                    c->q_terms + (uint64_t)j * n, c->stream),
+              "quantile terms");
+    float *host = static_cast<float *>(c->pin_q.p);
+    const uint64_t step = ((n + EXCHANGE_CHUNKS - 1) / EXCHANGE_CHUNKS + 255) & ~uint64_t(255);
+    for (int k = 0; k < EXCHANGE_CHUNKS; k++) {
+        const uint64_t b = std::min<uint64_t>(n, k * step), e = std::min<uint64_t>(n, b + step);
+        for (uint32_t j = 0; e > b && j < K; j++)
+            check(hipMemcpyAsync(host + (uint64_t)j * n + b, c->q_terms + (uint64_t)j * n + b,
+                                 4 * (e - b), hipMemcpyDeviceToHost, c->stream),
+                  "quantile terms download");
+        check(hipEventRecord(c->chunk_ev[k], c->stream), "event");
+    }
+    for (uint32_t j = 0; j < K; j++) {
+        const float *t = host + (uint64_t)j * n;
+        c->q_sums[j] = std::async(std::launch::async, [c, t, n, step] {
+            double stat = 0.0;
+            for (int k = 0; k < EXCHANGE_CHUNKS; k++) {
+                const uint64_t b = std::min<uint64_t>(n, k * step);
+                const uint64_t e = std::min<uint64_t>(n, b + step);
+                check(hipEventSynchronize(c->chunk_ev[k]), "quantile terms download");
+                for (uint64_t i = b; i < e; i++) stat += (double)t[i];
+            }
+            return stat;
+        });
+        c->q_have[j] = 1;
+    }
+}
+
 static void quantile_take_scale(fbh_ctx *c) {
     const float *w = c->has_weights ? c->gweights : nullptr;
     const float alpha = c->alphas[c->out_k];
@@ -1659,6 +1724,17 @@ static void quantile_take_scale(fbh_ctx *c) {
         check(launch_quantile_scale_fast(c->cur_margin(), c->labels, w, n, alpha, c->red_f64,
                                          c->quantile_slot, c->stream),
               "quantile scale");
+        return;
+    }
+    const uint32_t K = c->n_outputs, out = c->out_k;
+    const uint64_t batch_bytes = 4ull * K * n;
+    if (K > 1 && (c->q_terms || (batch_bytes <= (1ull << 30) &&
+                                 c->device_bytes + batch_bytes + 256 <= c->plan.budget))) {
+        if (!c->q_have[out]) quantile_sum_all(c, w);
+        const double stat = c->q_sums[out].get();  // a worker's error is raised here
+        c->q_sums[out] = std::future<double>();
+        c->q_have[out] = 0;  // this output's tree follows
+        quantile_finish(c, stat, alpha);
         return;
     }
     float *terms = c->gpair_f32;  // rewritten by the gradient pass that follows
@@ -1682,6 +1758,11 @@ static void quantile_take_scale(fbh_ctx *c) {
         check(hipEventSynchronize(c->chunk_ev[k]), "quantile terms download");
         for (uint64_t i = b; i < e; i++) stat += (double)host[i];
     }
+    quantile_finish(c, stat, alpha);
+}
+
+// The scale from a term sum into the slot the gradient reads.
+static void quantile_finish(fbh_ctx *c, double stat, float alpha) {
     float scale = 0.0f;
     if (!(std::fabs(c->quantile_sum_w) < 1e-6)) {
         const double root_mean = stat / c->quantile_sum_w;
@@ -3002,6 +3083,7 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     const int idb = c->objective >= 0 ? (leaf_bound <= 256 ? 1 : 2) : 0;
     // Deferred leaves: ids only; fbh_apply_leaf_values adds the values.
     const bool defer = (gp->flags & FBH_GROW_DEFER_LEAVES) != 0;
+    c->q_forget((int)c->out_k);  // this output's margins change
     if (walk) {
         check(launch_tree_leaves(c->bundles[0].data, c->bundles[0].pitch, c->n_rows, GB.tree,
                                  GB.tree_cats, GB.feat_off, GB.st, c->leaf_ids, idb,
@@ -3134,6 +3216,7 @@ int fbh_apply_leaf_values(fbh_ctx *c, const float *values, uint32_t n) {
         check(hipMemcpyAsync(d_vals, pv, bytes, hipMemcpyHostToDevice, c->stream), "leaf values");
         check(hipEventRecord(c->leaves_done, c->stream), "event");
         c->leaves_pending = true;
+        c->q_forget((int)c->out_k);
         check(launch_apply_leaves(c->leaf_ids, c->leaf_id_bytes, d_vals, c->n_rows, c->cur_margin(),
                                   c->stream),
               "margin update");
@@ -3182,6 +3265,7 @@ int fbh_assign_leaves(fbh_ctx *c, const fbh_span *spans, const float *values, ui
         check(launch_assign_leaves(c->d_leaves, m, chunks, c->rows, c->rows, c->delta,
                                    c->leaf_ids, idb, nullptr, c->stream),
               "leaf assignment");
+        c->q_forget((int)c->out_k);
         if (idb)
             check(launch_apply_leaves(c->leaf_ids, idb, d_vals, c->n_rows, c->cur_margin(), c->stream),
                   "margin update");
