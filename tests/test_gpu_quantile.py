@@ -59,6 +59,13 @@ CASES = {
     "three_alphas": dict(n=6000, alpha=[0.1, 0.5, 0.9], params={"max_depth": 5}),
     "alphas_weighted_sampled": dict(n=5000, alpha=[0.05, 0.5, 0.5, 0.95], weights=True,
                                     params={"max_depth": 4, "subsample": 0.8, "seed": 3}),
+    # every output's scale sum is started by the first output's call: these take the
+    # deferred leaf values (capped lossguide) and the host-driven levels with several alphas
+    "alphas_lossguide_capped": dict(n=5000, alpha=[0.2, 0.5, 0.8],
+                                    params={"grow_policy": "lossguide", "max_leaves": 11,
+                                            "max_depth": 6}),
+    "alphas_host_levels": dict(n=4000, alpha=[0.3, 0.7],
+                               params={"max_depth": 4, "hip_host_levels": True}),
 }
 
 
@@ -109,10 +116,12 @@ def test_quantile_equals_oracle(fb, oracle, case):
     assert np.array_equal(pred.view(np.uint32), om.predict_margin(x).view(np.uint32))
 
 
-def test_full_size_first_rounds_equal_oracle(fb, oracle):
-    """400k rows: the host's serial scale sum and the device pairs at size."""
+@pytest.mark.parametrize("alpha", [0.75, [0.2, 0.5, 0.8]])
+def test_full_size_first_rounds_equal_oracle(fb, oracle, alpha):
+    """400k rows: the host's serial scale sums (one output, or several summed side by
+    side on host threads over chunked downloads) and the device pairs at size."""
     x, y, _ = _data(400_000, seed=21, n_feat=12)
-    params = {"objective": "reg:quantileerror", "quantile_alpha": 0.75, "max_depth": 8,
+    params = {"objective": "reg:quantileerror", "quantile_alpha": alpha, "max_depth": 8,
               "eta": 0.1, "max_bin": 255}
     pm = fb.train(params, x, y, num_boost_round=3)
     om = oracle.train(x, y, oracle.make_params(n_rounds=3, nthread=8, **params))
