@@ -366,7 +366,11 @@ int fbh_set_output(fbh_ctx *ctx, uint32_t output);
  * first takes the round's scale S = (sum w sqrtf|m - y| / sum w)^2 of the
  * current output's column: gpu_math exact sums the f32 terms on the host in
  * row order in double (the reference's serial sum, bit for bit; one
- * device-to-host copy of 4 bytes a row), fast sums them on the device in a
+ * device-to-host copy of 4 bytes a row; with several alphas, every
+ * column's sum starts at the first column's call, one host thread each,
+ * when n_alphas x 4 bytes a row fit the memory budget's remaining room and
+ * 1 GiB, and a later column's call takes its finished sum), fast sums them
+ * on the device in a
  * fixed order (deterministic). The pairs use glibc's tanhf restated, so
  * exact-mode pairs equal the host's bit for bit.
  * fbh_quantile_last_scale reads back the scale the last gradient call used. */
