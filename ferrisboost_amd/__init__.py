@@ -188,15 +188,104 @@ def _normalize(params: Mapping[str, Any], num_boost_round: int) -> dict[str, Any
                          "path: gradient pairs are always quantized on the device; omit it")
     if out["sampling_method"] != "uniform":
         raise ValueError("sampling_method must be uniform on the ferrisboost_amd device path")
-    for k in ("colsample_bylevel", "colsample_bynode"):
-        if float(out[k]) != 1.0:
-            raise ValueError(f"{k} < 1 is not available on the ferrisboost_amd device path")
+    # src/training/mod.rs:1550-1565 (the reference's message names the key).
+    for k in ("subsample", "colsample_bytree", "colsample_bylevel", "colsample_bynode"):
+        out[k] = float(out[k])
+        if not 0.0 < out[k] <= 1.0:
+            raise ValueError(f"{k} must be in (0, 1], got {out[k]}")
     if out["interaction_constraints"]:
         raise ValueError("interaction_constraints are not available on the ferrisboost_amd device path")
     if out["feature_weights"] is not None:
-        raise ValueError("feature_weights are not available on the ferrisboost_amd device path")
+        out["feature_weights"] = _feature_weights_spec(out["feature_weights"])
     out["num_boost_round"] = int(num_boost_round)
     return out
+
+
+def _feature_weights_spec(raw):
+    """feature_weights (src/python/feature_weights.rs:14-70): a mapping of
+    feature names to weights, or a one-dimensional list / tuple / numpy array
+    of weights by position."""
+    if isinstance(raw, Mapping):
+        named = {}
+        for k, v in raw.items():
+            if not isinstance(k, str):
+                raise ValueError("feature_weights dictionary keys must be feature-name strings")
+            named[k] = _one_weight(v, f"feature_weights[{k!r}]")
+        return named
+    if isinstance(raw, (str, bytes)) or not isinstance(raw, (list, tuple, np.ndarray)):
+        raise ValueError("feature_weights must be a mapping, list, tuple, or one-dimensional "
+                         "NumPy array")
+    if isinstance(raw, np.ndarray) and raw.ndim != 1:
+        raise ValueError("feature_weights NumPy array must be one-dimensional")
+    out = [_one_weight(v, f"feature_weights[{i}]") for i, v in enumerate(raw)]
+    if not out:
+        raise ValueError("feature_weights positional vector must not be empty")
+    return out
+
+
+def _one_weight(v, where: str) -> float:
+    if isinstance(v, (bool, np.bool_)):
+        raise ValueError(f"{where} must be a number, not a boolean")
+    try:
+        f = float(v)
+    except (TypeError, ValueError):
+        raise ValueError(f"{where} must be a number") from None
+    if not (np.isfinite(f) and f >= 0.0):
+        raise ValueError("feature_weights must be finite and nonnegative")
+    return f
+
+
+def _resolve_feature_weights(spec, n_features: int, names: list[str] | None):
+    """The weights by feature position (FeatureWeightsSpec::resolve,
+    src/python/feature_weights.rs:72-): positional lists must match the
+    feature count; names need the data's feature names."""
+    if spec is None:
+        return None
+    if isinstance(spec, dict):
+        if not names:
+            raise ValueError("feature_weights given by name needs data with feature names "
+                             "(a pyarrow Table or a Parquet file)")
+        unknown = [k for k in spec if k not in names]
+        if unknown:
+            raise ValueError(f"feature_weights names unknown features {unknown}")
+        w = np.ones(n_features, np.float32)
+        for k, v in spec.items():
+            w[names.index(k)] = v
+    else:
+        if len(spec) != n_features:
+            raise ValueError(f"feature_weights has {len(spec)} entries, expected {n_features}")
+        w = np.asarray(spec, np.float32)
+    if not (w > 0).any():
+        raise ValueError("feature_weights must contain at least one positive weight")
+    return np.ascontiguousarray(w)
+
+
+def _as_base_margin(margin, n: int, k: int) -> np.ndarray:
+    """base_margin (python/ferrisboost/__init__.py:966-989): (n,) or (n, 1)
+    for one output, (n, k) for several; finite. Returned class-major, as
+    the driver takes it ([k][n] flattened)."""
+    if hasattr(margin, "to_numpy") and not isinstance(margin, np.ndarray):
+        margin = margin.to_numpy()
+    arr = np.asarray(margin, dtype=np.float32)
+    if arr.ndim == 1 and k == 1:
+        arr = arr.reshape(-1, 1)
+    if arr.ndim != 2 or arr.shape[1] != k:
+        want = "(n,) or (n, 1)" if k == 1 else f"(n, {k})"
+        raise ValueError(f"base_margin must have shape {want}, got {tuple(arr.shape)}")
+    if arr.shape[0] != n:
+        raise ValueError(f"training set: base_margin has {arr.size} values, expected {n} rows "
+                         f"x {k} outputs = {n * k}")
+    if not np.isfinite(arr).all():
+        raise ValueError("base_margin contains NaN or inf; every starting margin must be finite")
+    return np.ascontiguousarray(arr.T).reshape(-1)
+
+
+def _n_outputs(p: dict[str, Any]) -> int:
+    if p["objective"].startswith("multi:"):
+        return int(p["num_class"])
+    if p["objective"] == "reg:quantileerror":
+        return len(p["quantile_alpha"])
+    return 1
 
 
 def _normalize_quantile_alpha(value: Any, objective: str) -> list[float] | None:
@@ -228,8 +317,18 @@ def _normalize_quantile_alpha(value: Any, objective: str) -> list[float] | None:
     return flat
 
 
-def _params_struct(p: dict[str, Any], n_features: int) -> N.TrainParams:
+def _params_struct(p: dict[str, Any], n_features: int, names: list[str] | None = None,
+                   base_margin: np.ndarray | None = None) -> N.TrainParams:
     s = N.TrainParams()
+    s.colsample_bylevel = float(p["colsample_bylevel"])
+    s.colsample_bynode = float(p["colsample_bynode"])
+    fw = _resolve_feature_weights(p["feature_weights"], n_features, names)
+    if fw is not None:
+        s._fw = fw  # the struct points into it
+        s.feature_weights = fw.ctypes.data_as(C.POINTER(C.c_float))
+    if base_margin is not None:
+        s._bm = base_margin
+        s.base_margin = base_margin.ctypes.data_as(C.POINTER(C.c_float))
     s.n_rounds = p["num_boost_round"]
     s.max_depth = int(p["max_depth"])
     s.max_leaves = int(p["max_leaves"])
@@ -475,7 +574,14 @@ class Model:
         if explain and output_margin:
             raise ValueError("output_margin cannot be combined with pred_contribs / "
                              "pred_interactions / pred_leaf: one type of prediction at a time")
-        X = np.asarray(data, dtype=np.float32)
+        if _arrow_input(data):
+            from . import arrow_rows
+
+            X = arrow_rows.table_matrix(data, getattr(self, "_feature_names", None),
+                                        getattr(self, "_categories", None), self.n_features,
+                                        float("nan"))
+        else:
+            X = np.asarray(data, dtype=np.float32)
         if X.ndim != 2 or X.shape[1] != self.n_features:
             raise ValueError(f"expected a 2-D array with {self.n_features} columns, got shape "
                              f"{X.shape}")
@@ -552,7 +658,14 @@ class Model:
         return out
 
     def get_categories(self):
-        return None
+        """Category names by feature (python/ferrisboost/_core.pyi; Model::
+        categories, src/data/category_names.rs): a list of the categories in
+        code order for a categorical feature trained from named categories
+        (an Arrow string dictionary or string column), None for any other
+        feature; None instead of a list when no feature has names. Kept on
+        this object only: the model JSON does not carry them."""
+        cats = getattr(self, "_categories", None)
+        return None if cats is None else [None if c is None else list(c) for c in cats]
 
     def to_json(self) -> str:
         L = N.train_lib()
@@ -647,10 +760,11 @@ def _arrow_input(data) -> bool:
     return mod.startswith("pyarrow")
 
 
-def _train_arrow(p: dict[str, Any], data, label, weight, cuts) -> Model:
+def _train_arrow(p: dict[str, Any], data, label, weight, cuts, base_margin) -> Model:
     """train() on a .parquet path or a pyarrow Table / RecordBatchReader: the
-    label (and weight) are column names; the feature rows stream through
-    fbt_train_rows (python/ferrisboost/__init__.py:1090-1230)."""
+    label (and weight) are column names (or arrays for a table); the feature
+    rows stream through fbt_train_rows (python/ferrisboost/__init__.py:
+    1090-1230)."""
     from . import arrow_rows
 
     if cuts is not None:
@@ -660,8 +774,6 @@ def _train_arrow(p: dict[str, Any], data, label, weight, cuts) -> Model:
         if not (path.endswith(".parquet") or path.endswith(".pq")):
             raise ValueError(f"cannot tell the format of {str(data)!r} from its extension; "
                              "supported: .parquet / .pq")
-    if weight is not None and not isinstance(weight, str):
-        raise ValueError("for Parquet and Arrow inputs, weight names the weight column")
     src = arrow_rows.ArrowRows(data, label, weight, p["enable_categorical"], p["missing"])
     types = arrow_rows.feature_types_of(src, p["feature_types"])
     cat = _categorical_flags(types, src.n_features)
@@ -671,7 +783,8 @@ def _train_arrow(p: dict[str, Any], data, label, weight, cuts) -> Model:
         if isinstance(mc, str):
             mc = [int(v) for v in mc.strip("()").split(",") if v.strip()]
         mono = np.ascontiguousarray([int(np.sign(v)) for v in mc], np.int8)
-    s = _params_struct(p, src.n_features)
+    bm = None if base_margin is None else _as_base_margin(base_margin, src.n_rows, _n_outputs(p))
+    s = _params_struct(p, src.n_features, list(src.features), bm)
     h = C.c_void_p()
     L = N.train_lib()
     errors: list = []
@@ -684,25 +797,79 @@ def _train_arrow(p: dict[str, Any], data, label, weight, cuts) -> Model:
     N.check_train(rc)
     m = Model(h, src.n_features, p["objective"], s.device)
     m._feature_names = list(src.features)
+    m._categories = arrow_rows.categories_of(src, types)
     st = N.Stats()
     N.check_train(L.fbt_last_stats(C.byref(st)))
     m.stats = {k: getattr(st, k) for k, _ in N.Stats._fields_}
     return m
 
 
-def train(params: Mapping[str, Any], X, label, weight=None, num_boost_round: int = 10,
-          cuts: Cuts | None = None) -> Model:
-    """fb.train on the device path (python/ferrisboost/__init__.py:train).
+# train() arguments of the reference that this device path leaves out:
+# validation sets and what hangs off them, training continuation, ranking
+# groups and survival bounds (outside the histogram / split / partition path).
+_UNSUPPORTED_ARGS = {
+    "evals": "validation sets (evals) are not available on the ferrisboost_amd device path",
+    "early_stopping_rounds": "early stopping needs validation sets, which the ferrisboost_amd "
+                             "device path does not take",
+    "callbacks": "callbacks are not available on the ferrisboost_amd device path",
+    "base_margin_eval_set": "validation sets (and their margins) are not available on the "
+                            "ferrisboost_amd device path",
+    "init_model": "training continuation (init_model) is not available on the ferrisboost_amd "
+                  "device path",
+    "xgb_model": "training continuation (xgb_model) is not available on the ferrisboost_amd "
+                 "device path",
+    "qid": "ranking objectives (qid) are not available on the ferrisboost_amd device path",
+    "group": "ranking objectives (group) are not available on the ferrisboost_amd device path",
+    "eval_qid": "ranking objectives are not available on the ferrisboost_amd device path",
+    "eval_group": "ranking objectives are not available on the ferrisboost_amd device path",
+    "label_lower_bound": "survival:aft is not available on the ferrisboost_amd device path",
+    "label_upper_bound": "survival:aft is not available on the ferrisboost_amd device path",
+}
 
-    X is a 2-D array (label and weight arrays), or a .parquet path or a
-    pyarrow Table / RecordBatchReader with label (and weight) naming
-    columns: the other columns are the features, streamed to the device in
-    chunks for the sketch and the binning. cuts (from sketch() on the same
-    matrix, max_bin and feature_types) replaces the sketch."""
+
+def train(params: Mapping[str, Any], data, label=None, num_boost_round: int = 10,
+          evals=(), early_stopping_rounds=None, evals_result: dict | None = None,
+          verbose_eval=False, callbacks=None, header: bool = True, quiet: bool = False,
+          weight=None, feature_types=None, base_margin=None, base_margin_eval_set=None,
+          init_model=None, xgb_model=None, qid=None, group=None, eval_qid=None,
+          eval_group=None, label_lower_bound=None, label_upper_bound=None, *,
+          cuts: Cuts | None = None) -> Model:
+    """fb.train on the device path, with the reference's signature
+    (python/ferrisboost/__init__.py:1090-1114): train(params, data, label,
+    num_boost_round, evals, ...).
+
+    data is a 2-D array (label, weight and base_margin arrays), a .parquet
+    path (label and weight name columns) or a pyarrow Table /
+    RecordBatchReader (label and weight name columns or are arrays; the
+    other columns are the features, streamed to the device in chunks for the
+    sketch and the binning). base_margin gives every row's starting raw
+    margin, (n,) or (n, num_outputs); the intercept is still estimated from
+    the labels and stored. feature_types ("q" / "c" per feature) overrides
+    params["feature_types"]. cuts (from sketch() on the same matrix, max_bin
+    and feature_types) replaces the sketch. Validation sets, early stopping,
+    callbacks, training continuation, ranking groups and survival bounds are
+    not part of this path: passing them is a ValueError."""
+    given = {"evals": evals, "early_stopping_rounds": early_stopping_rounds,
+             "callbacks": callbacks, "base_margin_eval_set": base_margin_eval_set,
+             "init_model": init_model, "xgb_model": xgb_model, "qid": qid, "group": group,
+             "eval_qid": eval_qid, "eval_group": eval_group,
+             "label_lower_bound": label_lower_bound, "label_upper_bound": label_upper_bound}
+    for k, v in given.items():
+        if v is not None and not (k == "evals" and len(v) == 0):
+            raise ValueError(_UNSUPPORTED_ARGS[k])
+    if isinstance(num_boost_round, bool) or not isinstance(num_boost_round, (int, np.integer)):
+        raise ValueError(f"num_boost_round must be an integer, got {num_boost_round!r}")
+    del verbose_eval, header, quiet  # no evaluation log; files are Parquet only
+    if evals_result is not None:
+        evals_result.clear()  # no validation sets, so no metric history
+    if feature_types is not None:
+        params = dict(params, feature_types=list(feature_types))
     p = _normalize(params, num_boost_round)
-    if _arrow_input(X):
-        return _train_arrow(p, X, label, weight, cuts)
-    X = _matrix(X, p["missing"])
+    if _arrow_input(data):
+        return _train_arrow(p, data, label, weight, cuts, base_margin)
+    if label is None:
+        raise ValueError("label is required for array inputs")
+    X = _matrix(data, p["missing"])
     y = np.ascontiguousarray(np.asarray(label, dtype=np.float32))
     if y.shape != (X.shape[0],):
         raise ValueError(f"label has {y.size} rows, but the training data has {X.shape[0]} rows")
@@ -716,7 +883,8 @@ def train(params: Mapping[str, Any], X, label, weight=None, num_boost_round: int
         if isinstance(mc, str):
             mc = [int(v) for v in mc.strip("()").split(",") if v.strip()]
         mono = np.ascontiguousarray([int(np.sign(v)) for v in mc], np.int8)
-    s = _params_struct(p, X.shape[1])
+    bm = None if base_margin is None else _as_base_margin(base_margin, X.shape[0], _n_outputs(p))
+    s = _params_struct(p, X.shape[1], None, bm)
     h = C.c_void_p()
     L = N.train_lib()
     if cuts is None:

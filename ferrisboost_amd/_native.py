@@ -163,6 +163,10 @@ class TrainParams(C.Structure):
         ("host_sketch", C.c_uint32),
         ("n_quantile_alpha", C.c_uint32),
         ("quantile_alpha", C.POINTER(C.c_float)),
+        ("base_margin", C.POINTER(C.c_float)),
+        ("colsample_bylevel", C.c_float),
+        ("colsample_bynode", C.c_float),
+        ("feature_weights", C.POINTER(C.c_float)),
     ]
 
 
@@ -223,9 +227,9 @@ HIP_SYMBOLS = [
     "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_set_multiclass",
     "fbh_multiclass_begin_round", "fbh_set_output", "fbh_set_quantile",
     "fbh_quantile_last_scale", "fbh_tanh_checksum", "fbh_gradient_exchange",
-    "fbh_download_margin", "fbh_set_gpu_math", "fbh_gradient_pairs", "fbh_sigmoid_host", "fbh_sigmoid_device", "fbh_sigmoid_checksum",
+    "fbh_download_margin", "fbh_set_margins", "fbh_set_gpu_math", "fbh_gradient_pairs", "fbh_sigmoid_host", "fbh_sigmoid_device", "fbh_sigmoid_checksum",
     "fbh_begin_tree", "fbh_eval_nodes", "fbh_download_histogram",
-    "fbh_partition", "fbh_partition_eval", "fbh_grow_depthwise", "fbh_grow_depthwise_async",
+    "fbh_partition", "fbh_partition_eval", "fbh_partition_eval_masked", "fbh_grow_depthwise", "fbh_grow_depthwise_async",
     "fbh_grow_collect", "fbh_assign_leaves", "fbh_download_delta", "fbh_host_alloc",
     "fbh_host_free", "fbh_download_rows",
     "fbh_hist_timing", "fbh_set_timing", "fbh_build_histogram", "fbh_partition_rows",
@@ -308,6 +312,7 @@ def hip() -> C.CDLL:
         L.fbh_tanh_checksum.argtypes = [C.c_int, C.c_uint64, C.c_uint64, P]
         L.fbh_gradient_exchange.argtypes = [P, P, P, C.c_uint64, C.c_uint64, C.c_uint64, P, P]
         L.fbh_download_margin.argtypes = [P, P]
+        L.fbh_set_margins.argtypes = [P, P]
         L.fbh_set_gpu_math.argtypes = [P, C.c_uint32]
         L.fbh_gradient_pairs.argtypes = [C.c_int, C.c_uint32, C.c_uint32, P, P, P, C.c_uint64, P]
         L.fbh_sigmoid_host.argtypes = [P, C.c_uint64, P]
@@ -320,6 +325,8 @@ def hip() -> C.CDLL:
         L.fbh_partition.argtypes = [P, P, C.c_uint32, P, C.c_uint32, P]
         L.fbh_partition_eval.argtypes = [P, P, C.c_uint32, P, C.c_uint32, P, P, P, P, P, P,
                                          C.c_uint32]
+        L.fbh_partition_eval_masked.argtypes = [P, P, C.c_uint32, P, C.c_uint32, P, P, P, P, P,
+                                                P, P, C.c_uint32]
         L.fbh_assign_leaves.argtypes = [P, P, P, C.c_uint32]
         L.fbh_download_delta.argtypes = [P, P]
         L.fbh_download_rows.argtypes = [P, P]

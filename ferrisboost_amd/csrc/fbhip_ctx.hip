@@ -366,13 +366,28 @@ struct fbh_ctx {
     std::vector<uint8_t> q_have;        // q_sums[j] is for output j's current margins
     float *q_terms = nullptr;           // n_outputs x n_rows terms (device)
     PinnedBuf pin_q;                    // the same terms on the host
+    // A worker's error of a sum dropped before anyone took it (the first
+    // one), raised by the next quantile scale instead of being lost.
+    std::exception_ptr q_error;
     void q_forget(int k) {              // k < 0: every output
         for (size_t j = 0; j < q_sums.size(); j++) {
             if (k >= 0 && j != (size_t)k) continue;
-            if (q_sums[j].valid()) q_sums[j].wait();
+            if (q_sums[j].valid()) {
+                try {
+                    q_sums[j].get();
+                } catch (...) {
+                    if (!q_error) q_error = std::current_exception();
+                }
+            }
             q_sums[j] = std::future<double>();
             q_have[j] = 0;
         }
+    }
+    void q_raise() {
+        if (!q_error) return;
+        std::exception_ptr e = q_error;
+        q_error = nullptr;
+        std::rethrow_exception(e);
     }
     float *cur_margin() const { return margin + (uint64_t)out_k * n_rows; }
     bool fast_math = false;             // gpu_math="fast": hardware exp in the logistic gradient
@@ -1717,6 +1732,7 @@ static void quantile_sum_all(fbh_ctx *c, const float *w) {
 }
 
 static void quantile_take_scale(fbh_ctx *c) {
+    c->q_raise();
     const float *w = c->has_weights ? c->gweights : nullptr;
     const float alpha = c->alphas[c->out_k];
     const uint64_t n = c->n_rows;
@@ -1913,6 +1929,19 @@ int fbh_gradient_exchange(fbh_ctx *c, fbh_sigmoid_fn fn, void *user, uint64_t th
         }
         c->ids_fresh = false;
         quantize_device_pairs(c, th, seed, tree, scales_out, root_out, true);
+    });
+}
+
+int fbh_set_margins(fbh_ctx *c, const float *margins) {
+    return guard([&] {
+        if (!c || !margins) throw InputError("null argument");
+        if (c->objective < 0) throw InputError("fbh_set_objective has not been called");
+        check(hipSetDevice(c->device), "hipSetDevice");
+        c->sync();
+        check(hipMemcpy(c->margin, margins, (uint64_t)c->n_outputs * c->n_rows * 4,
+                        hipMemcpyHostToDevice),
+              "margin upload");
+        if (c->objective == 3) c->q_forget(-1);  // every output's scale sum is stale
     });
 }
 
@@ -2718,6 +2747,15 @@ int fbh_partition_eval(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
                        const fbh_child_pair *pairs, const fbh_split_params *sp,
                        fbh_span *children, uint32_t *left_slot, fbh_split *out,
                        uint64_t *cat_out, uint32_t cat_capacity) {
+    return fbh_partition_eval_masked(c, reqs, n, cat_words, n_cat_words, pairs, sp, nullptr,
+                                     children, left_slot, out, cat_out, cat_capacity);
+}
+
+int fbh_partition_eval_masked(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
+                              const uint64_t *cat_words, uint32_t n_cat_words,
+                              const fbh_child_pair *pairs, const fbh_split_params *sp,
+                              const uint8_t *enabled, fbh_span *children, uint32_t *left_slot,
+                              fbh_split *out, uint64_t *cat_out, uint32_t cat_capacity) {
     return guard([&] {
         if (!c || (n && (!reqs || !pairs || !children || !left_slot)) || !sp)
             throw InputError("null argument");
@@ -2771,6 +2809,10 @@ int fbh_partition_eval(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
         }
         const size_t o_pairs = S.put(pd.data(), sizeof(PairDev) * n);
         const size_t o_tri = S.put(triples.data(), 4 * triples.size());
+        // children's masks, (left, right) per evaluated pair: the split
+        // nodes' order of the level plan
+        const size_t o_en =
+            enabled && n_eval ? S.put(enabled, (size_t)2 * n_eval * c->tree_feats.size()) : 0;
         S.send();
         if (!P.pr.empty()) enqueue_partition(c, P, S);
         check(launch_level_plan(S.dev<const PairDev>(o_pairs), n, c->d_totals, rule,
@@ -2791,6 +2833,7 @@ int fbh_partition_eval(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
             E.n_tri = n_eval;
             E.sn = c->d_lvl_split;
             E.n_nodes = 2 * n_eval;
+            if (enabled) E.enabled = S.dev<const uint8_t>(o_en);
             enqueue_eval(c, E, sp);
         }
         uint8_t *po = static_cast<uint8_t *>(c->pin_out.p);

@@ -549,6 +549,14 @@ Model model_from_json(const char *text, size_t len) {
         m.base_score = parse_base_score(bs_raw);
     }
     for (const JVal &t : trees.a) m.trees.push_back(read_tree(t));
+    // A split feature past the model's feature count would read past a row
+    // (CpuInferenceTree::new, src/model/inference.rs:50-62, refuses it).
+    for (size_t t = 0; t < m.trees.size(); t++)
+        for (const Node &nd : m.trees[t].nodes)
+            if (!nd.is_leaf && nd.feat >= m.n_features)
+                throw bad("tree " + std::to_string(t) + " contains out-of-range feature " +
+                          std::to_string(nd.feat) + " (the model has " +
+                          std::to_string(m.n_features) + " features)");
     // feature_types: "c" marks a categorical feature.
     m.cuts.categorical.assign(m.n_features, 0);
     m.cuts.offsets.assign((size_t)m.n_features + 1, 0);

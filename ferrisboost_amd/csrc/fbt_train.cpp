@@ -22,6 +22,7 @@
 #include <cstring>
 #include <functional>
 #include <limits>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <queue>
@@ -203,36 +204,125 @@ struct Bounds {  // NodeBounds (split.rs:120-160)
     float apply(float w) const { return w < lo ? lo : (w > hi ? hi : w); }
 };
 
-// colsample::sample_features (src/data/colsample.rs:57-73): SplitMix64
-// Fisher-Yates keyed by (seed, round), first `count` ids, sorted.
-std::vector<uint32_t> sample_columns(uint32_t nf, float rate, uint64_t seed, uint64_t round) {
-    std::vector<uint32_t> ids(nf);
-    for (uint32_t i = 0; i < nf; i++) ids[i] = i;
-    const double c = std::floor((double)rate * (double)nf);
-    size_t take = (std::isfinite(c) && c >= 1.0) ? (size_t)c : 1;
-    take = std::max<size_t>(std::min<size_t>(take, nf), 1);
-    if (take >= nf) return ids;
-    const uint64_t r = round * 0x9E3779B97F4A7C15ull;
-    uint64_t state = seed ^ ((r << 17) | (r >> 47));
-    auto next = [&state] {
+// The column samplers (src/data/colsample.rs). SplitMix64 with unbiased
+// bounded draws (rejection above the last whole multiple of n).
+struct Mix64 {
+    uint64_t state;
+    uint64_t next() {
         state += 0x9E3779B97F4A7C15ull;
         uint64_t z = state;
         z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
         z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
         return z ^ (z >> 31);
-    };
-    for (size_t i = nf - 1; i >= 1; i--) {
-        const uint64_t n = i + 1;
+    }
+    uint64_t below(uint64_t n) {
         const uint64_t zone = UINT64_MAX - (UINT64_MAX % n) - 1;
         uint64_t v;
         do v = next();
         while (v > zone);
-        std::swap(ids[i], ids[v % n]);
+        return v % n;
     }
+};
+
+// sampled_count: max(1, floor(rate * n)), at most n (colsample.rs:57-68).
+size_t sample_size(size_t n, float rate) {
+    if (n == 0) return 0;
+    const double c = std::floor((double)rate * (double)n);
+    const size_t take = (std::isfinite(c) && c >= 1.0) ? (size_t)c : 1;
+    return std::max<size_t>(std::min(take, n), 1);
+}
+
+// The first `take` ids after a backward Fisher-Yates shuffle under `key`,
+// ascending (sample_features / sample_subset, colsample.rs:74-116).
+std::vector<uint32_t> shuffle_take(std::vector<uint32_t> ids, size_t take, uint64_t key) {
+    if (take >= ids.size()) return ids;
+    Mix64 rng{key};
+    for (size_t i = ids.size() - 1; i >= 1; i--) std::swap(ids[i], ids[rng.below(i + 1)]);
     ids.resize(take);
     std::sort(ids.begin(), ids.end());
     return ids;
 }
+
+uint64_t tree_key(uint64_t seed, uint64_t round) {
+    const uint64_t r = round * 0x9E3779B97F4A7C15ull;
+    return seed ^ ((r << 17) | (r >> 47));
+}
+
+// Weighted draws without replacement (sample_weighted, colsample.rs:
+// 146-172): every positive-weight id of `base` gets the exponential clock
+// -ln(U) / w with U = (52 random bits + 1) / (2^52 + 1); the `take` earliest
+// clocks win, ties to the lower id. rate >= 1 keeps the whole base.
+std::vector<uint32_t> weighted_take(const std::vector<uint32_t> &base, size_t n, float rate,
+                                    uint64_t key, const float *w) {
+    if (rate >= 1.0f) return base;
+    std::vector<uint32_t> pos;
+    for (uint32_t id : base)
+        if (w[id] > 0.0f) pos.push_back(id);
+    const size_t take = std::min(sample_size(n, rate), pos.size());
+    if (take == pos.size()) return pos;
+    Mix64 rng{key};
+    std::vector<std::pair<double, uint32_t>> clock(pos.size());
+    for (size_t i = 0; i < pos.size(); i++) {
+        const double u = (double)((rng.next() >> 12) + 1) / 4503599627370497.0;
+        clock[i] = {-std::log(u) / (double)w[pos[i]], pos[i]};
+    }
+    std::nth_element(clock.begin(), clock.begin() + take, clock.end());
+    std::vector<uint32_t> out(take);
+    for (size_t i = 0; i < take; i++) out[i] = clock[i].second;
+    std::sort(out.begin(), out.end());
+    return out;
+}
+
+// colsample_bytree's set of a tree (sample_features_weighted, colsample.rs:
+// 174-195); w is NULL for the uniform sampler.
+std::vector<uint32_t> sample_columns(uint32_t nf, float rate, uint64_t seed, uint64_t round,
+                                     const float *w = nullptr) {
+    std::vector<uint32_t> ids(nf);
+    for (uint32_t i = 0; i < nf; i++) ids[i] = i;
+    if (w) return weighted_take(ids, nf, rate, tree_key(seed, round), w);
+    return shuffle_take(std::move(ids), sample_size(nf, rate), tree_key(seed, round));
+}
+
+// validated_weights (colsample.rs:119-141): NULL when absent or all equal.
+const float *checked_weights(const float *w, uint32_t nf) {
+    if (!w) return nullptr;
+    bool positive = false;
+    for (uint32_t f = 0; f < nf; f++) {
+        if (!(std::isfinite(w[f]) && w[f] >= 0.0f))
+            throw InputError("feature_weights must be finite and nonnegative");
+        positive = positive || w[f] > 0.0f;
+    }
+    if (!positive) throw InputError("feature_weights must contain at least one positive weight");
+    for (uint32_t f = 1; f < nf; f++)
+        if (w[f] != w[0]) return w;
+    return nullptr;
+}
+
+float rate_or_one(float r) { return r == 0.0f ? 1.0f : r; }
+
+// NestedSampler (colsample.rs:203-286): the level set of a depth from the
+// tree's set, the node set of a tree node id from its level's set, keyed
+// by (seed, tree, tag, depth or node) through three SplitMix64 steps.
+struct NestedSets {
+    float bylevel = 1.0f, bynode = 1.0f;
+    const float *w = nullptr;
+    uint64_t seed = 0, tree = 0;
+    bool active() const { return bylevel < 1.0f || bynode < 1.0f; }
+    uint64_t key(uint64_t tag, uint64_t idx) const {
+        auto step = [](uint64_t x) { return Mix64{x}.next(); };
+        return step(step(step(seed ^ (tag * 0xD6E8FEB86659FD93ull)) ^ tree) ^ idx);
+    }
+    std::vector<uint32_t> pick(const std::vector<uint32_t> &base, float rate, uint64_t k) const {
+        if (w) return weighted_take(base, base.size(), rate, k, w);
+        return shuffle_take(base, sample_size(base.size(), rate), k);
+    }
+    std::vector<uint32_t> level(const std::vector<uint32_t> &tree_set, uint32_t depth) const {
+        return pick(tree_set, bylevel, key(1, depth));
+    }
+    std::vector<uint32_t> node(const std::vector<uint32_t> &level_set, uint64_t id) const {
+        return bynode < 1.0f ? pick(level_set, bynode, key(2, id)) : level_set;
+    }
+};
 
 uint64_t sample_threshold(float rate) {  // subsample::threshold_for
     if (rate >= 1.0f || !(rate > 0.0f)) return UINT64_MAX;
@@ -243,8 +333,8 @@ uint64_t sample_threshold(float rate) {  // subsample::threshold_for
 class Grower {
   public:
     Grower(fbh_ctx *ctx, const fbt_params &p, const Cuts &cuts, const std::vector<int8_t> &mono,
-           uint32_t n_slots)
-        : ctx_(ctx), p_(p), cuts_(cuts), mono_(mono) {
+           uint32_t n_slots, const NestedSets &nested)
+        : ctx_(ctx), p_(p), cuts_(cuts), mono_(mono), nested_(nested) {
         sp_.lambda_ = p.lambda_;
         sp_.gamma = p.gamma;
         sp_.min_child_weight = p.min_child_weight;
@@ -259,6 +349,18 @@ class Grower {
             if (cuts.is_cat(f)) words += (cuts.n_bins(f) + 63) / 64;
         cat_cap_ = words;
     }
+
+    // The next tree's features (ascending: its bytree set, or every
+    // feature) and the key of its nested sets (the tree index).
+    void begin_tree(std::vector<uint32_t> features, uint64_t tree) {
+        tree_feats_ = std::move(features);
+        nested_.tree = tree;
+        levels_.clear();
+    }
+    // colsample_bylevel / bynode restrict each node's split scan to its own
+    // feature set (mod.rs:3575-3638): such trees grow level by level from
+    // the host, which draws the sets of the nodes it numbers.
+    bool masked() const { return nested_.active(); }
 
     void lm_scales(const double scales[2]) {
         lm_ = {p_.lambda_, p_.alpha, p_.max_delta_step, p_.learning_rate, 1.0 / scales[0],
@@ -319,7 +421,7 @@ class Grower {
     }
 
     bool device_growth() const {
-        return device_trees_ &&
+        return device_trees_ && !masked() &&
                (p_.grow_policy == 0 || lossguide_uncapped() || lossguide_capped()) &&
                p_.max_depth >= 1 && p_.max_depth <= 14 && p_.max_leaves != 1;
     }
@@ -480,8 +582,37 @@ class Grower {
         leaves_values_.push_back(t.nodes[node].leaf_value);
     }
 
+    // The level set of a depth, drawn once per tree.
+    const std::vector<uint32_t> &level_set(uint32_t depth) {
+        auto it = levels_.find(depth);
+        if (it == levels_.end()) it = levels_.emplace(depth, nested_.level(tree_feats_, depth)).first;
+        return it->second;
+    }
+
+    // enabled bytes of the given nodes (tree node ids at one depth) over the
+    // tree's features, node after node; empty when nothing is masked.
+    std::vector<uint8_t> masks(uint32_t depth, const std::vector<uint32_t> &ids) {
+        std::vector<uint8_t> out;
+        if (!masked()) return out;
+        const size_t F = tree_feats_.size();
+        out.assign(ids.size() * F, 0);
+        const std::vector<uint32_t> &level = level_set(depth);
+        for (size_t i = 0; i < ids.size(); i++) {
+            const std::vector<uint32_t> set = nested_.node(level, ids[i]);
+            size_t k = 0;
+            for (size_t j = 0; j < F && k < set.size(); j++)
+                if (tree_feats_[j] == set[k]) {
+                    out[i * F + j] = 1;
+                    k++;
+                }
+            if (k != set.size()) throw RuntimeError("a node's feature set is not in the tree's");
+        }
+        return out;
+    }
+
     // Split scans of a batch of nodes; returns packets.
-    std::vector<fbh_split> eval(const std::vector<Pending> &batch) {
+    std::vector<fbh_split> eval(const std::vector<Pending> &batch,
+                                const std::vector<uint8_t> &enabled = {}) {
         std::vector<fbh_node> nodes(batch.size());
         for (size_t i = 0; i < batch.size(); i++) {
             const Pending &b = batch[i];
@@ -498,7 +629,8 @@ class Grower {
         }
         std::vector<fbh_split> out(batch.size());
         cat_words_.assign((size_t)std::max<uint32_t>(1, cat_cap_) * batch.size(), 0);
-        call(fbh_eval_nodes(ctx_, nodes.data(), (uint32_t)nodes.size(), &sp_, nullptr, out.data(),
+        call(fbh_eval_nodes(ctx_, nodes.data(), (uint32_t)nodes.size(), &sp_,
+                            enabled.empty() ? nullptr : enabled.data(), out.data(),
                             cat_words_.data(), (uint32_t)cat_words_.size()));
         return out;
     }
@@ -563,9 +695,16 @@ class Grower {
         std::vector<uint32_t> left_slot(n);
         std::vector<fbh_split> packets(2 * n);
         cat_words_.assign((size_t)std::max<uint32_t>(1, cat_cap_) * 2 * n, 0);
-        call(fbh_partition_eval(ctx_, reqs.data(), (uint32_t)n, cats.data(), (uint32_t)cats.size(),
-                                pairs.data(), &sp_, children.data(), left_slot.data(),
-                                packets.data(), cat_words_.data(), (uint32_t)cat_words_.size()));
+        // the children's sets, (left, right) per pair (every pair of a step
+        // is evaluated, and its children share one depth)
+        std::vector<uint32_t> ids;
+        for (const Pending &c : next) ids.push_back(c.node);
+        const std::vector<uint8_t> en = masks(next.empty() ? 0 : next[0].depth, ids);
+        call(fbh_partition_eval_masked(ctx_, reqs.data(), (uint32_t)n, cats.data(),
+                                       (uint32_t)cats.size(), pairs.data(), &sp_,
+                                       en.empty() ? nullptr : en.data(), children.data(),
+                                       left_slot.data(), packets.data(), cat_words_.data(),
+                                       (uint32_t)cat_words_.size()));
         for (size_t k = 0; k < n; k++) {
             next[2 * k].rows = children[2 * k];
             next[2 * k + 1].rows = children[2 * k + 1];
@@ -605,7 +744,7 @@ class Grower {
             give_slot(level[0].slot);
             return;
         }
-        std::vector<fbh_split> chosen = eval(level);
+        std::vector<fbh_split> chosen = eval(level, masks(0, {0}));
         std::vector<uint64_t> cats = cat_words_;
         for (uint32_t depth = 0;; depth++) {
             if (p_.max_leaves != 0) {
@@ -702,7 +841,7 @@ class Grower {
         } else {
             root.slot = take_slot();
             const std::vector<Pending> batch{root};
-            take(batch, eval(batch), cat_words_);
+            take(batch, eval(batch, masks(0, {0})), cat_words_);
         }
         uint32_t leaf_count = 1;
         while (p_.max_leaves == 0 || leaf_count < p_.max_leaves) {
@@ -747,6 +886,9 @@ class Grower {
     const fbt_params &p_;
     const Cuts &cuts_;
     const std::vector<int8_t> &mono_;
+    NestedSets nested_;
+    std::vector<uint32_t> tree_feats_;
+    std::map<uint32_t, std::vector<uint32_t>> levels_;
     fbh_split_params sp_{};
     LeafMath lm_{};
     std::vector<uint32_t> free_;
@@ -811,6 +953,19 @@ void validate(const fbt_params &p, uint64_t n, uint32_t nf, const float *y) {
         throw InputError("subsample must be in (0, 1]");
     if (!(p.colsample_bytree > 0.0f && p.colsample_bytree <= 1.0f))
         throw InputError("colsample_bytree must be in (0, 1]");
+    // src/training/mod.rs:1550-1565 (0 in the struct reads as 1).
+    if (!(rate_or_one(p.colsample_bylevel) > 0.0f && rate_or_one(p.colsample_bylevel) <= 1.0f))
+        throw InputError("colsample_bylevel must be in (0, 1]");
+    if (!(rate_or_one(p.colsample_bynode) > 0.0f && rate_or_one(p.colsample_bynode) <= 1.0f))
+        throw InputError("colsample_bynode must be in (0, 1]");
+    checked_weights(p.feature_weights, nf);
+    // validate_start_margins (src/training/mod.rs:1109-1130).
+    if (p.base_margin) {
+        const uint64_t k = multi ? p.num_class : p.objective == 4 ? p.n_quantile_alpha : 1;
+        for (uint64_t i = 0; i < k * n; i++)
+            if (!std::isfinite(p.base_margin[i]))
+                throw InputError("training set: base_margin values must all be finite");
+    }
     if (p.cols_per_block == 0) throw InputError("cols_per_block must be > 0");
     for (uint64_t i = 0; i < n; i++) {
         if (!std::isfinite(y[i])) throw InputError("labels must all be finite");
@@ -1114,7 +1269,16 @@ Model train(const RowSource &src, uint64_t n, uint32_t nf, const float *y, const
     // Host margins feed the logistic sigmoid; the device keeps its own copy
     // (the same f32 additions), which squared error uses directly.
     std::vector<float> pred((uint64_t)K * n, margin);
-    Grower grower(ctx.get(), p, m.cuts, mono, slots);
+    // base_margin: every row starts at its own margin (class-major), the
+    // intercepts stay as estimated (src/training/mod.rs:1831-1852, 2605-2616).
+    if (p.base_margin) std::copy(p.base_margin, p.base_margin + (uint64_t)K * n, pred.begin());
+    const float *fw = checked_weights(p.feature_weights, nf);
+    NestedSets nested;
+    nested.bylevel = rate_or_one(p.colsample_bylevel);
+    nested.bynode = rate_or_one(p.colsample_bynode);
+    nested.w = fw;
+    nested.seed = p.seed;
+    Grower grower(ctx.get(), p, m.cuts, mono, slots, nested);
     grower.n_rows_ = (uint32_t)n;
     {
         fbh_plan plan{};
@@ -1129,6 +1293,7 @@ Model train(const RowSource &src, uint64_t n, uint32_t nf, const float *y, const
     else if (quantile)
         call(fbh_set_quantile(ctx.get(), K, p.quantile_alpha, y, w, intercepts.data()));
     else call(fbh_set_objective(ctx.get(), obj, y, grad_w, margin));
+    if (p.base_margin) call(fbh_set_margins(ctx.get(), pred.data()));
     // gpu_math="fast" (fast_gradient_and_quantize, src/backend/cuda/train_ctx.rs:2404-2512):
     // the logistic gradient takes the hardware exponential on the device.
     call(fbh_set_gpu_math(ctx.get(), p.gpu_math));
@@ -1193,7 +1358,13 @@ Model train(const RowSource &src, uint64_t n, uint32_t nf, const float *y, const
             if (pending && !device_scales) collect_all();
             std::vector<uint32_t> feats;
             if (p.colsample_bytree < 1.0f)
-                feats = sample_columns(nf, p.colsample_bytree, p.seed, tree);
+                feats = sample_columns(nf, p.colsample_bytree, p.seed, tree, fw);
+            if (grower.masked()) {
+                std::vector<uint32_t> all;
+                if (feats.empty())
+                    for (uint32_t f = 0; f < nf; f++) all.push_back(f);
+                grower.begin_tree(feats.empty() ? std::move(all) : feats, tree);
+            }
             fbh_span root;
             call(fbh_begin_tree(ctx.get(), feats.empty() ? nullptr : feats.data(),
                                 (uint32_t)feats.size(), mono.data(), nf, &root));

@@ -332,6 +332,13 @@ int fbh_gradient_pairs(int device, uint32_t objective, uint32_t gpu_math, const 
 /* The device margins (the training margins after the assigned trees);
  * n_outputs x n_rows class-major values for a multiclass objective. */
 int fbh_download_margin(fbh_ctx *ctx, float *out);
+/* GpuTrainCtx::init_fast_math_rows (src/backend/cuda/train_ctx.rs:2985-3010)
+ * for every objective: replaces the margins the objective call set with
+ * per-row starting margins, class-major [n_outputs][n_rows] (XGBoost's
+ * base_margin; TrainConfig::base_margin, src/training/mod.rs:646-652).
+ * Call after fbh_set_objective / fbh_set_multiclass / fbh_set_quantile and
+ * before the first gradients. */
+int fbh_set_margins(fbh_ctx *ctx, const float *margins);
 
 /* Multiclass objectives (multi:softprob / multi:softmax): the resident state
  * of train_multiclass_rounds (src/training/mod.rs:2578-2850) and its device
@@ -460,6 +467,19 @@ int fbh_partition_eval(fbh_ctx *ctx, const fbh_part_req *reqs, uint32_t n_reqs,
                        const fbh_child_pair *pairs, const fbh_split_params *params,
                        fbh_span *children, uint32_t *left_slot, fbh_split *out,
                        uint64_t *cat_out, uint32_t cat_capacity);
+
+/* fbh_partition_eval whose children scan only some of the tree's features:
+ * enabled[(2 * e + k) * n_tree_features + j] != 0 lets child k (0 left, 1
+ * right) of the e-th evaluated pair split on tree feature j (the order
+ * fbh_begin_tree selected). The reference's masked split scan
+ * (split_cached_features_masked, src/backend/cuda/histogram.cu:482-494; the
+ * per-(node, feature) byte masks of split_ctx.rs:66) for colsample_bylevel /
+ * colsample_bynode (src/training/mod.rs:3575-3638). NULL = every feature. */
+int fbh_partition_eval_masked(fbh_ctx *ctx, const fbh_part_req *reqs, uint32_t n_reqs,
+                              const uint64_t *cat_words, uint32_t n_cat_words,
+                              const fbh_child_pair *pairs, const fbh_split_params *params,
+                              const uint8_t *enabled, fbh_span *children, uint32_t *left_slot,
+                              fbh_split *out, uint64_t *cat_out, uint32_t cat_capacity);
 
 /* One node of a tree grown on the device, in the order the host grower
  * numbers them (Tree::split_leaf, src/model/tree.rs:140-170). */
@@ -640,7 +660,12 @@ int fbh_predict_device(fbh_shap_model *m, const float *d_rows, uint64_t n_rows,
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). Rows, margins and contributions are staged batch by batch
  * through a fixed FBH_NOALLOC_SCRATCH_BYTES array that each device holds for
- * the life of the process (found once per device on the first call); a row
+ * the life of the process (found once per device on the first call). The
+ * copies in and out are ordinary (pageable) copies followed by a stream
+ * synchronisation, so the call is not capturable as it stands; and the
+ * kernel's private per-lane segment (its register spills) is backed by the
+ * HIP runtime, which may size that backing at the kernel's first launch,
+ * as for any kernel. A row
  * of more than (FBH_NOALLOC_SCRATCH_BYTES - 768) / (8 * n_features + 8)
  * features' worth of data is an input error. Results equal
  * fbh_shap_contribs bit for bit. Calls that overlap on one device share the

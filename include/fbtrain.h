@@ -86,6 +86,21 @@ typedef struct {
     uint32_t n_quantile_alpha; /* reg:quantileerror: quantiles (1..=64), one
                                   output and one tree a round each */
     const float *quantile_alpha; /* ascending, in [0, 1] */
+    const float *base_margin;  /* per-row starting margins, class-major
+                                  [outputs][n_rows], finite (XGBoost's
+                                  base_margin; TrainConfig::base_margin,
+                                  src/training/mod.rs:646-652); NULL: every
+                                  row starts at the intercept. The intercepts
+                                  are estimated and stored either way. */
+    float colsample_bylevel;   /* (0, 1]: each depth's features drawn from the
+                                  tree's (src/data/colsample.rs:203-286);
+                                  0 reads as 1 */
+    float colsample_bynode;    /* (0, 1]: each node's features drawn from its
+                                  depth's; 0 reads as 1 */
+    const float *feature_weights; /* n_features nonnegative weights of the
+                                  column samplers (feature_weights,
+                                  src/data/colsample.rs:119-195); NULL or all
+                                  equal: uniform */
 } fbt_params;
 
 /* One tree node: Node (src/model/tree.rs:52-111). */

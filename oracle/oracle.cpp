@@ -798,6 +798,101 @@ std::vector<u32> sample_features(u32 nf, float rate, u64 seed, u64 round) {
     return ids;
 }
 
+// validated_weights (src/data/colsample.rs:119-141): NULL when absent or
+// when every weight is equal (the uniform sampler then runs unchanged).
+const float *validated_weights(const float *w, u32 nf) {
+    if (!w) return nullptr;
+    bool positive = false;
+    for (u32 f = 0; f < nf; f++) {
+        if (!std::isfinite(w[f]) || w[f] < 0.0f)
+            throw std::runtime_error("feature_weights must be finite and nonnegative");
+        positive = positive || w[f] > 0.0f;
+    }
+    if (!positive)
+        throw std::runtime_error("feature_weights must contain at least one positive weight");
+    for (u32 f = 1; f < nf; f++)
+        if (w[f] != w[0]) return w;
+    return nullptr;
+}
+
+// sample_subset (src/data/colsample.rs:101-116): max(1, floor(rate * |base|))
+// of an ascending set by Fisher-Yates under `key`, ascending.
+std::vector<u32> sample_subset(const std::vector<u32> &base, float rate, u64 key) {
+    const size_t take = sampled_count(base.size(), rate);
+    if (take >= base.size()) return base;
+    std::vector<u32> ids = base;
+    SplitMix64 rng{key};
+    for (size_t i = ids.size() - 1; i >= 1; i--) {
+        const size_t j = (size_t)rng.below(i + 1);
+        std::swap(ids[i], ids[j]);
+    }
+    ids.resize(take);
+    std::sort(ids.begin(), ids.end());
+    return ids;
+}
+
+// sample_weighted (src/data/colsample.rs:146-172): weighted draws without
+// replacement by exponential clocks, key -ln(U) / w with U from 52 random
+// bits, the `take` smallest keys (ties to the lower id); zero weights are
+// never drawn, except that rate >= 1 keeps the whole base.
+std::vector<u32> sample_weighted(const std::vector<u32> &base, size_t n, float rate, u64 key,
+                                 const float *w) {
+    if (rate >= 1.0f) return base;
+    std::vector<u32> positive;
+    for (u32 id : base)
+        if (w[id] > 0.0f) positive.push_back(id);
+    const size_t take = std::min(sampled_count(n, rate), positive.size());
+    if (take == positive.size()) return positive;
+    SplitMix64 rng{key};
+    std::vector<std::pair<double, u32>> keys;
+    keys.reserve(positive.size());
+    for (u32 id : positive) {
+        const double u = (double)((rng.next() >> 12) + 1) / 4503599627370497.0;
+        keys.push_back({-std::log(u) / (double)w[id], id});
+    }
+    std::sort(keys.begin(), keys.end());
+    std::vector<u32> out;
+    for (size_t i = 0; i < take; i++) out.push_back(keys[i].second);
+    std::sort(out.begin(), out.end());
+    return out;
+}
+
+// sample_features_weighted (src/data/colsample.rs:174-195).
+std::vector<u32> sample_features_weighted(u32 nf, float rate, u64 seed, u64 round,
+                                          const float *w) {
+    if (!w) return sample_features(nf, rate, seed, round);
+    std::vector<u32> all(nf);
+    for (u32 i = 0; i < nf; i++) all[i] = i;
+    return sample_weighted(all, nf, rate, seed ^ rotl(round * 0x9E3779B97F4A7C15ull, 17), w);
+}
+
+// subset_key (src/data/colsample.rs:197-201): (seed, tree, tag, idx) through
+// one SplitMix64 step each.
+u64 subset_key(u64 seed, u64 tree, u64 tag, u64 idx) {
+    auto mix = [](u64 x) { return SplitMix64{x}.next(); };
+    return mix(mix(mix(seed ^ (tag * 0xD6E8FEB86659FD93ull)) ^ tree) ^ idx);
+}
+
+// NestedSampler (src/data/colsample.rs:203-286): bytree -> bylevel ->
+// bynode; the level set once per depth, the node set per tree node id; they
+// restrict the split enumeration only.
+struct Nested {
+    const float *weights = nullptr;
+    float bylevel = 1.0f, bynode = 1.0f;
+    u64 seed = 0, tree = 0;
+    std::vector<u32> level_set(const std::vector<u32> &tree_set, u32 depth) const {
+        const u64 key = subset_key(seed, tree, 1, depth);
+        return weights ? sample_weighted(tree_set, tree_set.size(), bylevel, key, weights)
+                       : sample_subset(tree_set, bylevel, key);
+    }
+    bool samples_nodes() const { return bynode < 1.0f; }
+    std::vector<u32> node_set(const std::vector<u32> &level, u64 node) const {
+        const u64 key = subset_key(seed, tree, 2, node);
+        return weights ? sample_weighted(level, level.size(), bynode, key, weights)
+                       : sample_subset(level, bynode, key);
+    }
+};
+
 // subsample (src/data/subsample.rs).
 inline u64 mix64(u64 z) {
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -1100,11 +1195,22 @@ struct Trainer {
     std::vector<u32> rows_cur, rows_next;
     const std::vector<u32> *sampled;
     unsigned nthread;
+    // bylevel / bynode (mod.rs:3524-3528, 3582-3638): the sets start from
+    // the tree's bytree set (every feature when it is not sampled).
+    const Nested *nested = nullptr;
+    std::vector<u32> tree_features;
 
     Trainer(const Cuts &c, const std::vector<Block> &b, const Params &P_, const Quantizer &q_,
-            const std::vector<Fixed> &g, std::vector<float> &pr, const std::vector<u32> *smp)
-        : cuts(c), blocks(b), P(P_), p(P_.p), q(q_), gpair(g), pred(pr), sampled(smp) {
+            const std::vector<Fixed> &g, std::vector<float> &pr, const std::vector<u32> *smp,
+            const Nested *nst = nullptr)
+        : cuts(c), blocks(b), P(P_), p(P_.p), q(q_), gpair(g), pred(pr), sampled(smp),
+          nested(nst) {
         nthread = std::max(1u, p.nthread);
+        if (nested) {
+            if (sampled) tree_features = *sampled;
+            else
+                for (u32 f = 0; f < cuts.n_feats(); f++) tree_features.push_back(f);
+        }
         for (u32 bi = 0; bi < blocks.size(); bi++) {
             Plan pl;
             pl.block = bi;
@@ -1152,12 +1258,25 @@ struct Trainer {
         }
     }
 
-    Cand best_of(const std::vector<std::vector<Fixed>> &h, Fixed sum, Bounds b) {
+    // The enumeration sets of a batch of nodes at one depth (node ids as in
+    // the tree): the node set, else the level set, else the bytree set
+    // (enum_features, mod.rs:3626-3638; lossguide.rs:85-101).
+    std::vector<std::vector<u32>> enum_sets(u32 depth, const std::vector<size_t> &ids) const {
+        std::vector<std::vector<u32>> out;
+        if (!nested) return out;
+        const std::vector<u32> level = nested->level_set(tree_features, depth);
+        for (size_t id : ids)
+            out.push_back(nested->samples_nodes() ? nested->node_set(level, id) : level);
+        return out;
+    }
+
+    Cand best_of(const std::vector<std::vector<Fixed>> &h, Fixed sum, Bounds b,
+                 const std::vector<u32> *enum_set = nullptr) {
         SplitCtx sc = ctx(b);
         Cand best;
         for (size_t pi = 0; pi < plans.size(); pi++) {
             Cand c = best_split_in_block(h[pi].data(), plans[pi].feats, plans[pi].offsets, sum, sc,
-                                         sampled, &cuts.cat);
+                                         enum_set ? enum_set : sampled, &cuts.cat);
             reduce_into(best, c);
         }
         return best;
@@ -1257,9 +1376,13 @@ struct Trainer {
                     for (size_t k = 0; k < hists[i][pi].size(); k++)
                         hists[i][pi][k] = sub(ph[pi][k], hists[level[i].sibling][pi][k]);
             }
+            std::vector<size_t> ids;
+            for (const LN &ln : level) ids.push_back(ln.node);
+            const std::vector<std::vector<u32>> sets = enum_sets(depth, ids);
             std::vector<Cand> chosen(level.size());
             for (size_t i = 0; i < level.size(); i++)
-                chosen[i] = best_of(hists[i], level[i].sum, level[i].bounds);
+                chosen[i] = best_of(hists[i], level[i].sum, level[i].bounds,
+                                    sets.empty() ? nullptr : &sets[i]);
             if (p.max_leaves != 0) {
                 u32 remaining = p.max_leaves > leaf_count ? p.max_leaves - leaf_count : 0;
                 for (Cand &c : chosen)
@@ -1361,8 +1484,12 @@ struct Trainer {
                     build_hists(rows_cur.data() + leaves[i].start, leaves[i].len, *hs[i]);
                 }
             }
+            std::vector<size_t> ids;
+            for (const Leaf &l : leaves) ids.push_back(l.id);
+            const std::vector<std::vector<u32>> sets = enum_sets(leaves[0].depth, ids);
             for (size_t i = 0; i < leaves.size(); i++) {
-                Cand c = best_of(*hs[i], leaves[i].sum, leaves[i].bounds);
+                Cand c = best_of(*hs[i], leaves[i].sum, leaves[i].bounds,
+                                 sets.empty() ? nullptr : &sets[i]);
                 if (c.found) heap.push(Pending{leaves[i], c, hs[i]});
                 else finish_leaf(leaves[i]);
             }
@@ -1756,6 +1883,34 @@ namespace {
 // loop with one output per alpha: intercepts the labels' alpha quantiles
 // (mod.rs:1442-1444), each target's pairs from its own column's scale
 // (quantile_multi_gradients, mod.rs:2871-2890).
+float rate_or_one(float r) { return r == 0.0f ? 1.0f : r; }
+bool nested_active(const orc_params &p) {
+    return rate_or_one(p.colsample_bylevel) < 1.0f || rate_or_one(p.colsample_bynode) < 1.0f;
+}
+Nested nested_of(const orc_params &p, u64 tree, const float *fw) {
+    Nested n;
+    n.weights = fw;
+    n.bylevel = rate_or_one(p.colsample_bylevel);
+    n.bynode = rate_or_one(p.colsample_bynode);
+    n.seed = p.seed;
+    n.tree = tree;
+    return n;
+}
+
+// The checks of validate_params and validate_start_margins
+// (src/training/mod.rs:1109-1130, 1550-1565) that the oracle meets.
+void validate_inputs(const orc_params &p, u64 n, u32 k) {
+    for (float r : {p.colsample_bylevel, p.colsample_bynode}) {
+        const float v = rate_or_one(r);
+        if (!(v > 0.0f && v <= 1.0f))
+            throw std::runtime_error("colsample_bylevel / colsample_bynode must be in (0, 1]");
+    }
+    if (p.base_margin)
+        for (u64 i = 0; i < n * k; i++)
+            if (!std::isfinite(p.base_margin[i]))
+                throw std::runtime_error("base_margin values must all be finite");
+}
+
 void train_multiclass(const float *x, u64 n, u32 nf, const float *labels, const float *weights,
                       const Params &P, const Cuts &cuts, const std::vector<Block> &blocks,
                       orc_model &m) {
@@ -1776,7 +1931,12 @@ void train_multiclass(const float *x, u64 n, u32 nf, const float *labels, const 
                                  : initial_class_margins(labels, weights, n, K);
     m.base_score = m.class_margins[0];
     std::vector<std::vector<float>> preds(K);
-    for (u32 k = 0; k < K; k++) preds[k].assign(n, m.class_margins[k]);
+    for (u32 k = 0; k < K; k++) {
+        // base_margin: class-major starting margins (mod.rs:2605-2616)
+        if (p.base_margin) preds[k].assign(p.base_margin + (u64)k * n, p.base_margin + (u64)(k + 1) * n);
+        else preds[k].assign(n, m.class_margins[k]);
+    }
+    const float *fw = validated_weights(p.feature_weights, nf);
     std::vector<std::vector<float>> gf(K, std::vector<float>(2 * n));
     std::vector<Fixed> gpair(n);
     auto t0 = std::chrono::steady_clock::now();
@@ -1818,8 +1978,10 @@ void train_multiclass(const float *x, u64 n, u32 nf, const float *labels, const 
             }
             std::vector<u32> smp;
             const bool use_smp = p.colsample_bytree < 1.0f;
-            if (use_smp) smp = sample_features(nf, p.colsample_bytree, p.seed, tree);
-            Trainer tr(cuts, blocks, P, q, gpair, preds[k], use_smp ? &smp : nullptr);
+            if (use_smp) smp = sample_features_weighted(nf, p.colsample_bytree, p.seed, tree, fw);
+            const Nested nst = nested_of(p, tree, fw);
+            Trainer tr(cuts, blocks, P, q, gpair, preds[k], use_smp ? &smp : nullptr,
+                       nested_active(p) ? &nst : nullptr);
             m.trees.push_back(p.grow_policy == 1 ? tr.lossguide(root) : tr.depthwise(root));
         }
     }
@@ -1860,6 +2022,11 @@ int orc_train(const float *x, uint64_t n, uint32_t nf, const float *labels, cons
             }
             m->quantile_alpha.assign(p.quantile_alpha, p.quantile_alpha + p.n_quantile_alpha);
         }
+        validate_inputs(p, n,
+                        p.objective == 2 || p.objective == 3 ? p.num_class
+                        : quantile                           ? std::max(1u, p.n_quantile_alpha)
+                                                             : 1u);
+        validated_weights(p.feature_weights, nf);
         if (p.objective == 2 || p.objective == 3 || (quantile && p.n_quantile_alpha > 1)) {
             train_multiclass(x, n, nf, labels, weights, P, cuts, blocks, *m);
             *out = m.release();
@@ -1870,6 +2037,8 @@ int orc_train(const float *x, uint64_t n, uint32_t nf, const float *labels, cons
                                    : estimate_base_score(labels, weights, n);
         float margin = base_margin_of(p.objective, m->base_score);
         std::vector<float> pred(n, margin);
+        if (p.base_margin) pred.assign(p.base_margin, p.base_margin + n);  // mod.rs:1831-1834
+        const float *fw = validated_weights(p.feature_weights, nf);
         std::vector<Fixed> gpair(n);
         std::vector<float> gf(2 * n);
         // gradient_weights (src/training/mod.rs:5466-5490): scale_pos_weight
@@ -1914,8 +2083,10 @@ int orc_train(const float *x, uint64_t n, uint32_t nf, const float *labels, cons
             }
             std::vector<u32> smp;
             bool use_smp = p.colsample_bytree < 1.0f;
-            if (use_smp) smp = sample_features(nf, p.colsample_bytree, p.seed, round);
-            Trainer tr(cuts, blocks, P, q, gpair, pred, use_smp ? &smp : nullptr);
+            if (use_smp) smp = sample_features_weighted(nf, p.colsample_bytree, p.seed, round, fw);
+            const Nested nst = nested_of(p, round, fw);
+            Trainer tr(cuts, blocks, P, q, gpair, pred, use_smp ? &smp : nullptr,
+                       nested_active(p) ? &nst : nullptr);
             m->trees.push_back(p.grow_policy == 1 ? tr.lossguide(root) : tr.depthwise(root));
         }
         m->train_seconds =
@@ -2162,6 +2333,41 @@ uint32_t orc_sample_features(uint32_t nf, float rate, uint64_t seed, uint64_t ro
     std::vector<u32> s = sample_features(nf, rate, seed, round);
     std::copy(s.begin(), s.end(), out);
     return (u32)s.size();
+}
+
+int orc_validated_weights(const float *w, uint32_t nf) {
+    try {
+        return validated_weights(w, nf) ? 1 : 0;
+    } catch (std::exception &e) {
+        g_error = e.what();
+        return -1;
+    }
+}
+
+uint32_t orc_sample_features_weighted(uint32_t nf, float rate, uint64_t seed, uint64_t round,
+                                      const float *w, uint32_t *out) {
+    std::vector<u32> s = sample_features_weighted(nf, rate, seed, round, w);
+    std::copy(s.begin(), s.end(), out);
+    return (u32)s.size();
+}
+
+uint32_t orc_nested_set(const uint32_t *base, uint32_t n, float bylevel, float bynode,
+                        uint64_t seed, uint64_t tree, uint32_t tag, uint64_t idx,
+                        const float *w, uint32_t *out) {
+    Nested ns;
+    ns.weights = w;
+    ns.bylevel = bylevel;
+    ns.bynode = bynode;
+    ns.seed = seed;
+    ns.tree = tree;
+    const std::vector<u32> b(base, base + n);
+    const std::vector<u32> s = tag == 1 ? ns.level_set(b, (u32)idx) : ns.node_set(b, idx);
+    std::copy(s.begin(), s.end(), out);
+    return (u32)s.size();
+}
+
+uint64_t orc_subset_key(uint64_t seed, uint64_t tree, uint64_t tag, uint64_t idx) {
+    return subset_key(seed, tree, tag, idx);
 }
 
 void orc_sigmoid(const float *in, uint64_t n, float *out) {

@@ -49,6 +49,11 @@ typedef struct {
     uint32_t num_class;       /* classes of multi:softprob / multi:softmax */
     uint32_t n_quantile_alpha; /* quantiles of reg:quantileerror (one output each) */
     const float *quantile_alpha;
+    const float *base_margin;  /* starting margins, class-major [outputs][n_rows]
+                                  (TrainConfig::base_margin; NULL: the intercepts) */
+    float colsample_bylevel;   /* (0, 1]; 0 reads as 1 */
+    float colsample_bynode;    /* (0, 1]; 0 reads as 1 */
+    const float *feature_weights; /* n_features column-sampling weights (NULL: uniform) */
 } orc_params;
 
 /* One tree node; same field meaning as Node (src/model/tree.rs:52-111). */
@@ -175,6 +180,21 @@ void orc_quadrature_rule(float nodes[8], float weights[8]);
 /* ---- colsample (src/data/colsample.rs:57-117) ---- */
 uint32_t orc_sample_features(uint32_t n_features, float rate, uint64_t seed, uint64_t round,
                              uint32_t *out);
+
+/* validated_weights (src/data/colsample.rs:119-141): 0 = uniform sampling
+ * (absent or all equal), 1 = weighted, -1 = invalid (orc_last_error). */
+int orc_validated_weights(const float *weights, uint32_t n_features);
+/* sample_features_weighted (src/data/colsample.rs:174-195); weights NULL =
+ * the uniform sampler. */
+uint32_t orc_sample_features_weighted(uint32_t n_features, float rate, uint64_t seed,
+                                      uint64_t round, const float *weights, uint32_t *out);
+/* NestedSampler (src/data/colsample.rs:203-286): tag 1 = level_set(base,
+ * depth = idx), tag 2 = node_set(base, node = idx). */
+uint32_t orc_nested_set(const uint32_t *base, uint32_t n, float bylevel, float bynode,
+                        uint64_t seed, uint64_t tree, uint32_t tag, uint64_t idx,
+                        const float *weights, uint32_t *out);
+/* subset_key (src/data/colsample.rs:197-201). */
+uint64_t orc_subset_key(uint64_t seed, uint64_t tree, uint64_t tag, uint64_t idx);
 
 /* ---- the generators behind sampling ----
  * SplitMix64::next_u64 (src/data/colsample.rs:34-45) from `seed`, n outputs;

@@ -59,6 +59,10 @@ class Params(C.Structure):
         ("num_class", C.c_uint32),
         ("n_quantile_alpha", C.c_uint32),
         ("quantile_alpha", C.POINTER(C.c_float)),
+        ("base_margin", C.POINTER(C.c_float)),
+        ("colsample_bylevel", C.c_float),
+        ("colsample_bynode", C.c_float),
+        ("feature_weights", C.POINTER(C.c_float)),
     ]
 
 
@@ -182,6 +186,16 @@ def lib() -> C.CDLL:
         L.orc_quadrature_rule.restype = None
         L.orc_sample_features.argtypes = [C.c_uint32, C.c_float, C.c_uint64, C.c_uint64, P]
         L.orc_sample_features.restype = C.c_uint32
+        L.orc_validated_weights.argtypes = [P, C.c_uint32]
+        L.orc_validated_weights.restype = C.c_int
+        L.orc_sample_features_weighted.argtypes = [C.c_uint32, C.c_float, C.c_uint64,
+                                                   C.c_uint64, P, P]
+        L.orc_sample_features_weighted.restype = C.c_uint32
+        L.orc_nested_set.argtypes = [P, C.c_uint32, C.c_float, C.c_float, C.c_uint64,
+                                     C.c_uint64, C.c_uint32, C.c_uint64, P, P]
+        L.orc_nested_set.restype = C.c_uint32
+        L.orc_subset_key.argtypes = [C.c_uint64] * 4
+        L.orc_subset_key.restype = C.c_uint64
         L.orc_sigmoid.argtypes = [P, C.c_uint64, P]
         L.orc_sigmoid.restype = None
         L.orc_sigmoid_checksum.argtypes = [C.c_uint64, C.c_uint64, C.c_uint32]
@@ -253,6 +267,19 @@ def make_params(**kw) -> Params:
         p._alphas = arr  # keeps the array alive with the struct
         p.n_quantile_alpha = arr.size
         p.quantile_alpha = arr.ctypes.data_as(C.POINTER(C.c_float))
+    # base_margin: class-major starting margins ([outputs][n] flattened)
+    bm = kw.get("base_margin")
+    if bm is not None:
+        arr = np.ascontiguousarray(np.asarray(bm, np.float32).ravel())
+        p._base_margin = arr
+        p.base_margin = arr.ctypes.data_as(C.POINTER(C.c_float))
+    p.colsample_bylevel = kw.get("colsample_bylevel", 1.0)
+    p.colsample_bynode = kw.get("colsample_bynode", 1.0)
+    fw = kw.get("feature_weights")
+    if fw is not None:
+        arr = np.ascontiguousarray(np.asarray(fw, np.float32).ravel())
+        p._feature_weights = arr
+        p.feature_weights = arr.ctypes.data_as(C.POINTER(C.c_float))
     return p
 
 
@@ -485,3 +512,36 @@ def sample_features(n_features, rate, seed, round_):
     out = np.zeros(max(n_features, 1), np.uint32)
     k = lib().orc_sample_features(n_features, rate, seed, round_, _p(out))
     return out[:k].copy()
+
+
+def _f32_or_none(w):
+    return None if w is None else np.ascontiguousarray(w, np.float32)
+
+
+def validated_weights(weights, n_features) -> int:
+    """0 = uniform sampling, 1 = weighted; invalid weights raise ValueError."""
+    w = _f32_or_none(weights)
+    rc = lib().orc_validated_weights(_p(w), n_features)
+    if rc < 0:
+        raise ValueError(lib().orc_last_error().decode())
+    return rc
+
+
+def sample_features_weighted(n_features, rate, seed, round_, weights=None):
+    w = _f32_or_none(weights)
+    out = np.zeros(max(n_features, 1), np.uint32)
+    k = lib().orc_sample_features_weighted(n_features, rate, seed, round_, _p(w), _p(out))
+    return out[:k].copy()
+
+
+def nested_set(base, bylevel, bynode, seed, tree, tag, idx, weights=None):
+    """NestedSampler level_set (tag 1, idx = depth) / node_set (tag 2, idx = node)."""
+    b = np.ascontiguousarray(base, np.uint32)
+    w = _f32_or_none(weights)
+    out = np.zeros(max(b.size, 1), np.uint32)
+    k = lib().orc_nested_set(_p(b), b.size, bylevel, bynode, seed, tree, tag, idx, _p(w), _p(out))
+    return out[:k].copy()
+
+
+def subset_key(seed, tree, tag, idx) -> int:
+    return int(lib().orc_subset_key(seed, tree, tag, idx))

@@ -84,3 +84,36 @@ def assert_same_models(oracle_model, product_model):
                     f"tree {t} field {f} differs at nodes {diff[:8].tolist()}: "
                     f"{av[diff[:4]].tolist()} vs {bv[diff[:4]].tolist()} {bad[:0]}")
     assert np.array_equal(oracle_model.cat_words(), product_model.cat_words())
+
+
+def wiggly(n, seed, nf=5):
+    """wiggly_data (src/training/mod.rs:7431-7451): an LCG in u64, features in
+    [-2, 2), every 13th cell (by i + f) missing, a smooth signal plus noise."""
+    mask = (1 << 64) - 1
+    state = (seed * 0x9E3779B97F4A7C15 + 1) & mask
+
+    def nxt():
+        nonlocal state
+        state = (state * 6364136223846793005 + 1442695040888963407) & mask
+        return np.float32(np.float32(state >> 40) / np.float32(1 << 24))
+
+    x = np.empty((n, nf), np.float32)
+    y = np.empty(n, np.float32)
+    for i in range(n):
+        row = [np.float32(nxt() * np.float32(4.0) - np.float32(2.0)) for _ in range(nf)]
+        sig = (np.sin(row[0] * np.float32(1.7)) + np.float32(0.8) * np.cos(row[1] * np.float32(3.0))
+               - np.float32(0.5) * row[2] + np.float32(0.3) * nxt())
+        for f in range(nf):
+            x[i, f] = np.nan if (i + f) % 13 == 0 else row[f]
+        y[i] = sig
+    return x, y
+
+
+def node_depths(tree) -> np.ndarray:
+    """Depth of every node of a tree (structured node array)."""
+    depth = np.zeros(tree.size, np.int64)
+    for i in range(tree.size):
+        if not tree["is_leaf"][i]:
+            depth[tree["left"][i]] = depth[i] + 1
+            depth[tree["right"][i]] = depth[i] + 1
+    return depth

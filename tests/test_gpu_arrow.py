@@ -2,7 +2,8 @@
 the device sketch and binning in chunks through fbt_train_rows) gives the
 model that training from the same rows as a numpy matrix gives, byte for
 byte: unit weights (streamed), weighted rows (gathered for the host sketch),
-dictionary columns as categorical features, a feature the device sketch
+string dictionary columns as categorical features coded by category
+whatever each chunk's dictionary, a feature the device sketch
 leaves to the host (zeros of both signs among its cuts), and a reader error
 raised back to the caller."""
 
@@ -82,15 +83,47 @@ def test_parquet_trains_the_array_model(fb, tmp_path, small_reads, weighted):
     assert m_file.stats["device_binning"]
 
 
+def _first_appearance(codes):
+    u, first = np.unique(codes, return_index=True)
+    remap = np.empty(u.max() + 1, np.int64)
+    remap[u[np.argsort(first)]] = np.arange(u.size)
+    return remap[codes]
+
+
+def _chunked_dictionaries(codes, names, seed):
+    """The category column as chunks whose dictionaries list the categories
+    in their own orders (as Arrow chunks and Parquet row groups may)."""
+    rng = np.random.default_rng(seed)
+    chunks = []
+    for part in np.array_split(np.arange(codes.size), 3):
+        perm = rng.permutation(len(names))  # chunk dictionary position -> category
+        pos = np.argsort(perm)              # category -> chunk dictionary position
+        chunks.append(pa.DictionaryArray.from_arrays(
+            pa.array(pos[codes[part]].astype(np.int32)), pa.array([names[i] for i in perm])))
+    return pa.chunked_array(chunks)
+
+
 def test_dictionary_columns_are_categorical(fb, small_reads):
+    # String dictionaries are coded by category in the order rows first use
+    # them (src/source/cat_recode.rs:1-30), whatever each chunk's dictionary.
     x, codes, y, w = _data(seed=1)
     t = _table(x, codes, y, w, True)
     p = dict(PARAMS, enable_categorical=True)
     m_tab = fb.train(p, t, "label", num_boost_round=5)
-    arr = np.ascontiguousarray(np.column_stack([x, codes.astype(np.float32), w]))
+    arr = np.ascontiguousarray(np.column_stack([x, _first_appearance(codes).astype(np.float32),
+                                                w]))
     m_arr = fb.train(dict(PARAMS, feature_types=["q"] * 6 + ["c", "q"]), arr, y,
                      num_boost_round=5)
     assert m_tab.to_json() == m_arr.to_json()
+    names = [f"k{i}" for i in range(7)]
+    assert m_tab.get_categories()[6] == [names[c] for c in
+                                         codes[np.sort(np.unique(codes, return_index=True)[1])]]
+    t2 = t.set_column(t.column_names.index("c"), "c", _chunked_dictionaries(codes, names, 5))
+    m_chunks = fb.train(p, t2, "label", num_boost_round=5)
+    assert m_chunks.to_json() == m_tab.to_json()
+    # prediction re-codes a table's categories by value
+    want = m_arr.predict(arr, output_margin=True)
+    assert np.array_equal(m_tab.predict(t2, output_margin=True), want)
     with pytest.raises(ValueError, match="enable_categorical"):
         fb.train(PARAMS, t, "label", num_boost_round=1)
 

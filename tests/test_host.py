@@ -138,8 +138,16 @@ def _tiny():
     ({"hist_nodes_per_batch": 40}, "hist_nodes_per_batch"),
     ({"hist_nodes_per_batch": 8}, "hist_nodes_per_batch is not available"),
     ({"device_quantize": False}, "device_quantize"),
-    ({"colsample_bylevel": 0.5}, "colsample_bylevel"),
-    ({"colsample_bynode": 0.5}, "colsample_bynode"),
+    ({"colsample_bylevel": 0.0}, r"colsample_bylevel must be in \(0, 1\]"),
+    ({"colsample_bynode": 1.5}, r"colsample_bynode must be in \(0, 1\]"),
+    ({"colsample_bynode": float("nan")}, "colsample_bynode"),
+    ({"feature_weights": [1.0, -1.0, 1.0]}, "nonnegative"),
+    ({"feature_weights": [0.0, 0.0, 0.0]}, "at least one positive"),
+    ({"feature_weights": [1.0, 2.0]}, "has 2 entries, expected 3"),
+    ({"feature_weights": "abc"}, "must be a mapping"),
+    ({"feature_weights": np.ones((2, 2))}, "one-dimensional"),
+    ({"feature_weights": [True, 1.0, 1.0]}, "boolean"),
+    ({"feature_weights": {"f0": 1.0}}, "needs data with feature names"),
     ({"tree_method": "exact"}, "tree_method"),
     ({"no_such_param": 1}, "unknown parameter"),
     ({"interaction_constraints": [[0, 1]]}, "interaction"),
@@ -150,6 +158,50 @@ def test_bad_params_are_value_errors(params, msg):
     x, y = _tiny()
     with pytest.raises(ValueError, match=msg):
         fb.train(params, x, label=y, num_boost_round=2)
+
+
+def test_train_takes_the_reference_argument_order():
+    """python/ferrisboost/__init__.py:1090-1114: train(params, data, label,
+    num_boost_round, evals, ...); what this path leaves out is refused by
+    name before any device work."""
+    import ferrisboost_amd as fb
+
+    x, y = _tiny()
+    with pytest.raises(ValueError, match="num_boost_round must be >= 1"):
+        fb.train({}, x, y, 0)  # the fourth positional argument is num_boost_round
+    with pytest.raises(ValueError, match="num_boost_round must be an integer"):
+        fb.train({}, x, y, np.ones(x.shape[0], np.float32))
+    with pytest.raises(ValueError, match="validation sets"):
+        fb.train({}, x, y, 2, [(x, y, "valid")])
+    for kw, what in (({"early_stopping_rounds": 3}, "early stopping"),
+                     ({"init_model": "m.json"}, "continuation"),
+                     ({"xgb_model": "m.json"}, "continuation"),
+                     ({"qid": np.zeros(x.shape[0])}, "ranking"),
+                     ({"label_lower_bound": y}, "survival")):
+        with pytest.raises(ValueError, match=what):
+            fb.train({}, x, y, 2, **kw)
+    with pytest.raises(ValueError, match="label is required"):
+        fb.train({}, x)
+    results = {"stale": 1}
+    with pytest.raises((RuntimeError, ValueError)):
+        fb.train({"max_depth": 15}, x, y, 2, evals_result=results)
+    assert results == {}
+
+
+@pytest.mark.parametrize("params, margin, msg", [
+    ({}, np.zeros(7, np.float32), "base_margin has 7 values, expected"),
+    ({}, np.zeros((64, 2), np.float32), r"must have shape \(n,\) or \(n, 1\)"),
+    ({"objective": "multi:softprob", "num_class": 3}, np.zeros(64, np.float32),
+     r"must have shape \(n, 3\)"),
+    ({}, np.full(64, np.inf, np.float32), "finite"),
+])
+def test_base_margin_shapes_are_checked(params, margin, msg):
+    import ferrisboost_amd as fb
+
+    x, y = _tiny()
+    y = np.floor(y * 2.999).astype(np.float32) if params else y
+    with pytest.raises(ValueError, match=msg):
+        fb.train(params, x, y, 2, base_margin=margin)
 
 
 def test_bad_shapes_are_value_errors():

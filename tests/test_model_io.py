@@ -141,6 +141,18 @@ def test_rejects_what_it_cannot_represent(frm, to, what):
     assert str(e.value), what
 
 
+def test_split_feature_past_the_model_feature_count_is_rejected():
+    """A tree whose num_feature is large enough but whose split feature is
+    past the learner's num_feature would read past a row on the host; the
+    reference refuses such a model (src/model/inference.rs:50-62)."""
+    wide = XGB_DUMP.replace('"split_indices": [1, 0, 0]', '"split_indices": [50000000, 0, 0]')
+    wide = wide.replace('"num_feature": "3",\n                         "num_nodes"',
+                        '"num_feature": "60000000",\n                         "num_nodes"')
+    assert wide.count("60000000") == 1 and "50000000" in wide
+    with pytest.raises(ValueError, match="out-of-range feature 50000000"):
+        fb.Model.from_json(wide)
+
+
 @pytest.mark.parametrize("frm, to, what", [
     ('"num_target": "1"', '"num_target": "2"', "num_target"),
     ('"tree_info": [0]', '"tree_info": [1]', "tree_info"),
