@@ -21,15 +21,27 @@
 //   * TreeSHAP: additivity (sum of contributions = margin), exact Shapley
 //     values by subset enumeration on small trees, the quadrature rule
 //     integrating polynomials of degree <= 15 exactly;
-//   * colsample: the reference's count and sortedness unit tests;
-//   * sketch: low-cardinality midpoint cuts (the fixtures) and the
-//     reference's sketch unit-test properties. High-cardinality cut values
-//     beyond those are parity unpinned.
-// Lossguide growth and categorical splits have no golden fixture in the
-// reference; they are pinned by brute-force split enumeration and by
-// invariants (leaf hessians sum to the root, max_leaves respected), so their
-// end-to-end tree shape is partially pinned only.
-//
+//   * colsample: the reference's count, sortedness, nested and weighted
+//     sampler tests (src/data/colsample.rs:313-465), the laws of the
+//     weighted draws (first draw in proportion to weight, pairs by
+//     successive draws) and of uniform subsets (tests/test_oracle_colsample.py);
+//   * growth policies and categorical splits: the reference's lossguide and
+//     max_leaves tests (tests/lossguide.rs, tests/max_leaves.rs) and its
+//     categorical split tests (src/training/split.rs:1371-1590), restated in
+//     tests/test_oracle_growth.py;
+//   * sketch (tests/test_sketch_pins.py): in the exact-summary regime
+//     (max_bin < distinct values <= 16 * max_bin) the cuts equal the cuts of
+//     numpy's exact unique counts in any batch order; in the lossy regime
+//     (C2's and C4's columns) estimated ranks never exceed true ranks and
+//     every cut's true midrank lies in [target, target + B(N, limit)).
+//     Planted in a copy of this file, a swapped pass_a / pass_b in
+//     merge_entries, a dedup that keeps the last rmin, a cut walk with <=,
+//     and ranks kept in f64 each fail those tests. Three choices are left
+//     open because either way gives a valid summary: the operand order of
+//     the level merge, the tie rule of merge_entries (<= vs <) and the tie
+//     rule of compress's target walk; they move lossy-regime cuts by less
+//     than the bound, and only the reference's own cut values on
+//     high-cardinality data could pin them (parity unpinned there).
 // Floating point: compiled with -ffp-contract=off and without fast-math so
 // every f32 / f64 operation rounds like the reference's (Rust does not
 // contract a*b+c). expf / logf come from the same glibc the reference links.
@@ -37,6 +49,7 @@
 #include "oracle.h"
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstdint>
@@ -198,6 +211,10 @@ std::vector<Entry> merge_entries(const std::vector<Entry> &a, const std::vector<
     return dedup_same_value(out);
 }
 
+// Test instrumentation: how often compress's ceiling moved a pick below the
+// entry its target walk reached (read by the sketch-bound tests).
+std::atomic<uint64_t> g_compress_clamps{0};
+
 std::vector<Entry> compress(const std::vector<Entry> &entries, size_t max_size) {
     size_t n = entries.size();
     if (n <= max_size) return entries;
@@ -212,6 +229,7 @@ std::vector<Entry> compress(const std::vector<Entry> &entries, size_t max_size) 
         size_t j = taken + 1;
         while (j < n - 1 && entries[j].rmid() < target) j++;
         size_t ceiling = n - 1 - (slots - 1 - k);
+        if (std::max(j, taken + 1) > ceiling) g_compress_clamps++;
         j = std::min(std::max(j, taken + 1), ceiling);
         if (j > taken) {
             out.push_back(entries[j]);
@@ -2333,6 +2351,22 @@ uint32_t orc_sample_features(uint32_t nf, float rate, uint64_t seed, uint64_t ro
     std::vector<u32> s = sample_features(nf, rate, seed, round);
     std::copy(s.begin(), s.end(), out);
     return (u32)s.size();
+}
+
+uint64_t orc_compress_clamps() { return g_compress_clamps.load(); }
+
+uint64_t orc_sketch_summary(const float *col, uint64_t n, const float *w, uint32_t max_bin,
+                            float *out, uint64_t capacity) {
+    FeatureSketch sk(max_bin, false);
+    for (uint64_t i = 0; i < n; i++) sk.push(col[i], w ? w[i] : 1.0f);
+    const std::vector<Entry> e = sk.collapse();
+    for (uint64_t i = 0; i < std::min<uint64_t>(e.size(), capacity); i++) {
+        out[4 * i] = e[i].value;
+        out[4 * i + 1] = e[i].weight;
+        out[4 * i + 2] = e[i].rmin;
+        out[4 * i + 3] = e[i].rmax;
+    }
+    return e.size();
 }
 
 int orc_validated_weights(const float *w, uint32_t nf) {

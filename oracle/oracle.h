@@ -181,6 +181,16 @@ void orc_quadrature_rule(float nodes[8], float weights[8]);
 uint32_t orc_sample_features(uint32_t n_features, float rate, uint64_t seed, uint64_t round,
                              uint32_t *out);
 
+/* The collapsed summary of one numeric feature's sketch (FeatureSketch::
+ * collapse, src/data/sketch.rs:183-203) after pushing col[0..n) with weights
+ * (NULL: 1): (value, weight, rmin, rmax) per entry into out (4 floats each,
+ * at most capacity entries). Returns the entry count. */
+uint64_t orc_sketch_summary(const float *col, uint64_t n, const float *weights,
+                            uint32_t max_bin, float *out, uint64_t capacity);
+/* Times compress's ceiling (src/data/sketch.rs:422-424) has moved a pick
+ * below the entry its target walk reached, since the library loaded. */
+uint64_t orc_compress_clamps(void);
+
 /* validated_weights (src/data/colsample.rs:119-141): 0 = uniform sampling
  * (absent or all equal), 1 = weighted, -1 = invalid (orc_last_error). */
 int orc_validated_weights(const float *weights, uint32_t n_features);

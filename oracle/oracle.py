@@ -186,6 +186,10 @@ def lib() -> C.CDLL:
         L.orc_quadrature_rule.restype = None
         L.orc_sample_features.argtypes = [C.c_uint32, C.c_float, C.c_uint64, C.c_uint64, P]
         L.orc_sample_features.restype = C.c_uint32
+        L.orc_sketch_summary.argtypes = [P, C.c_uint64, P, C.c_uint32, P, C.c_uint64]
+        L.orc_sketch_summary.restype = C.c_uint64
+        L.orc_compress_clamps.argtypes = []
+        L.orc_compress_clamps.restype = C.c_uint64
         L.orc_validated_weights.argtypes = [P, C.c_uint32]
         L.orc_validated_weights.restype = C.c_int
         L.orc_sample_features_weighted.argtypes = [C.c_uint32, C.c_float, C.c_uint64,
@@ -545,3 +549,26 @@ def nested_set(base, bylevel, bynode, seed, tree, tag, idx, weights=None):
 
 def subset_key(seed, tree, tag, idx) -> int:
     return int(lib().orc_subset_key(seed, tree, tag, idx))
+
+
+def sketch_summary(col, max_bin, weights=None):
+    """The collapsed sketch summary of one numeric column: a structured array
+    of (value, weight, rmin, rmax)."""
+    c = np.ascontiguousarray(col, np.float32)
+    w = _f32_or_none(weights)
+    cap = 16 * max(max_bin, 2) + 64
+    out = np.zeros((cap, 4), np.float32)
+    k = lib().orc_sketch_summary(_p(c), c.size, _p(w), max_bin, _p(out), cap)
+    if k > cap:
+        out = np.zeros((k, 4), np.float32)
+        lib().orc_sketch_summary(_p(c), c.size, _p(w), max_bin, _p(out), k)
+    out = out[:k]
+    rec = np.zeros(k, [("value", np.float32), ("weight", np.float32), ("rmin", np.float32),
+                       ("rmax", np.float32)])
+    for i, f in enumerate(rec.dtype.names):
+        rec[f] = out[:, i]
+    return rec
+
+
+def compress_clamps() -> int:
+    return int(lib().orc_compress_clamps())

@@ -222,3 +222,20 @@ def test_full_size_device_sketch_equals_host(N, workload):
         X, _, params, _ = datasets.widebin_cat()
         cat = np.array([t == "c" for t in params["feature_types"]], np.uint8)
     _same(N, X, params["max_bin"], cat)
+
+
+def test_device_sketch_in_the_exact_regime_equals_exact_rank_cuts(N):
+    """The exact-summary regime of tests/test_sketch_pins.py on the device:
+    D distinct values with max_bin < D <= 16 * max_bin, so the cuts are fixed
+    by the exact ranks (numpy's unique counts), in several batch orders."""
+    from test_sketch_pins import EXACT, _exact_case, expected_cuts
+
+    for case in EXACT:
+        max_bin, d, n, order, weighted = case
+        if weighted:
+            continue  # weighted rows are sketched on the host
+        col, _ = _exact_case(*case, seed=d)
+        want = expected_cuts(col, None, max_bin)
+        dv, do, flags = _device(N, col.reshape(-1, 1), max_bin)
+        assert not flags[0]
+        assert np.array_equal(dv.view(np.uint32), want.view(np.uint32)), case
