@@ -81,8 +81,10 @@ uint32_t round_stride(uint32_t bytes) {
 }
 
 constexpr uint32_t MAX_RECORD_BYTES = 64;
-// Largest per-chunk partial histogram buffer.
-constexpr uint64_t MAX_PARTIAL_BYTES = 256ull << 20;
+// Largest per-chunk partial histogram buffer (also bounded by the budget's
+// remaining room). Wide-bin 2M x 100 needs about 360 MB at its root; with
+// 256 MB its 7,440 root workgroups flushed with global atomics instead.
+constexpr uint64_t MAX_PARTIAL_BYTES = 2048ull << 20;
 constexpr uint32_t MAX_NODES = 16384;      // nodes of one eval / partition call
 constexpr uint32_t DEFAULT_TILE_BYTES = 64 * 1024;
 // LDS of a planar tile (its bins plus the 1 KiB of lane dummies) when the
@@ -138,6 +140,9 @@ struct fbh_ctx {
     uint32_t tile_bytes = DEFAULT_TILE_BYTES;
     uint32_t planar_tile_bytes = PLANAR_TILE_BYTES;
     uint32_t fixed_chunk_rows = 0;  // nonzero: rows per workgroup forced by the caller
+    uint32_t shared_line_rows = SHARED_LINE_CHUNK_ROWS;
+    uint32_t planar_max_feats = 0;  // nonzero: at most this many features a planar tile
+    uint64_t max_partial_bytes = MAX_PARTIAL_BYTES;
     uint32_t hist_tpb = 0;          // histogram threads per workgroup (0: per launch)
     uint32_t hist_waves = HIST_WAVES;
     uint32_t host_hist_waves = HOST_HIST_WAVES;
@@ -160,8 +165,17 @@ struct fbh_ctx {
         int32_t bundle = -1;       // row bundle holding the records, or -1
         uint32_t bundle_off = 0;   // offset of the record in the bundle row
         bool rot = false;          // interleaved LDS layout (16 cells a record)
+        // The tile's records again, tile-major (row r at tm + r * rec): the
+        // root of a tree whose tiles share bundle lines reads these, where
+        // its rows are in order, so its chunks need no shared lines in L2.
+        uint8_t *tm = nullptr;
     };
     std::vector<Tile> tiles;
+    bool tm_stale = false;  // some tile's records changed after its tile-major copy was made
+    // Hot bins of categorical features (TileFeatDev::hot), found once from
+    // the resident bin columns after the last upload.
+    std::vector<uint32_t> hot_a, hot_b;
+    bool hot_ready = false;
     // Packed tiles of the current tree: with column sampling, the tree's
     // features of interleaved tiles are packed 16 to a record (from the bin
     // columns, into `pack`) when that takes at most 3/4 of the tiles that
@@ -292,7 +306,8 @@ struct fbh_ctx {
         std::deque<Job> pending;
     } grow;
     // offsets in the tree-table buffer
-    size_t off_tilefeats = 0, off_sfeats = 0, off_order = 0, off_pack = 0, tables_bytes = 0;
+    size_t off_tilefeats = 0, off_sfeats = 0, off_order = 0, off_pack = 0, off_root = 0,
+           tables_bytes = 0;
     PackTileDev *d_pack = nullptr;  // the packed tiles' sources (tree tables)
     uint32_t *d_split_order = nullptr;  // tree features: numeric positions, then categorical
     uint32_t n_split_num = 0, n_split_cat = 0;
@@ -344,6 +359,10 @@ struct fbh_ctx {
     uint32_t hist_row_bytes = 0;  // active cell bytes per row over all built tiles
     uint32_t hist_tiles = 0;      // resident tiles with features built this tree
     uint32_t line_share = 1;      // most built tiles sharing one row bundle this tree
+    // The tree's root reads tile-major copies (d_root_tiles): every built
+    // tile is planar, resident and has one, and its tiles share bundle lines.
+    bool root_tm = false;
+    TileDev *d_root_tiles = nullptr;
     uint64_t bins_active = 0;     // bins of the tree's features
     uint32_t cat_words_per_node = 0;
     bool tree_begun = false;
@@ -558,7 +577,7 @@ struct fbh_ctx {
     // enough chunks for hist_waves full waves of workgroups over all tiles
     // (occupancy bounded by LDS and by 2048 threads per CU), so that each
     // workgroup flushes its LDS histogram once per many rows.
-    ChunkRule chunk_rule(bool host = false) const {
+    ChunkRule chunk_rule(bool host = false, bool own_lines = false) const {
         ChunkRule R{fixed_chunk_rows, 1, MIN_CHUNK_ROWS, 1u << 24};
         uint64_t n_tiles = 0, lds_max = 0;
         for (const auto &g : groups) {
@@ -575,15 +594,16 @@ struct fbh_ctx {
         // to be read once into L2 (wide-bin 2M x 100, 16 tiles a line:
         // 394 against 343 rounds/s; with 2 or 4 tiles a line the longer
         // default chunks are faster).
-        if (line_share > 4) R.max_rows = SHARED_LINE_CHUNK_ROWS;
+        if (line_share > 4 && !own_lines) R.max_rows = shared_line_rows;
         return R;
     }
     // Rows per chunk for accumulated nodes of these lengths: the smallest
     // multiple of 1024 whose chunks (ceil(len / rows) per node) fit one wave
     // of workgroups, so no launch runs a second, mostly idle wave; with more
     // nodes than the wave holds, rows / want_chunks rounded up.
-    uint32_t chunk_rows_for(const uint32_t *lens, size_t n, bool host = false) const {
-        const ChunkRule R = chunk_rule(host);
+    uint32_t chunk_rows_for(const uint32_t *lens, size_t n, bool host = false,
+                            bool own_lines = false) const {
+        const ChunkRule R = chunk_rule(host, own_lines);
         if (R.fixed) return R.fixed;
         uint64_t acc = 0, nz = 0;
         for (size_t i = 0; i < n; i++) {
@@ -606,9 +626,9 @@ struct fbh_ctx {
         }
         return (uint32_t)std::min<uint64_t>(std::max<uint64_t>(lo * 1024, R.min_rows), R.max_rows);
     }
-    uint32_t chunk_rows_for(uint64_t rows) const {
+    uint32_t chunk_rows_for(uint64_t rows, bool own_lines = false) const {
         const uint32_t len = (uint32_t)rows;
-        return chunk_rows_for(&len, 1);
+        return chunk_rows_for(&len, 1, false, own_lines);
     }
 
     // Adds the histogram time of every completed launch; pairs still in
@@ -630,7 +650,7 @@ struct fbh_ctx {
 };
 
 int64_t *fbh_ctx::partial_buffer(uint64_t bytes) {
-    if (has_global || !streamed.empty() || bytes > MAX_PARTIAL_BYTES) return nullptr;
+    if (has_global || !streamed.empty() || bytes > max_partial_bytes) return nullptr;
     // Outside the memory plan: only within the budget's remaining room.
     if (bytes > partial_bytes && device_bytes - partial_bytes + bytes + 256 > plan.budget)
         return nullptr;
@@ -678,6 +698,14 @@ void rot_tiles(uint32_t w, const std::vector<uint32_t> &feats, F &&emit) {
     }
 }
 
+// LDS bytes of a planar feature: its bins, plus the lane slots of its hot
+// bins for a categorical feature that may have them.
+uint64_t feature_lds_bytes(const fbh_ctx &c, uint32_t f) {
+    uint64_t b = (uint64_t)c.n_bins[f] * 16u;
+    if (c.cat[f] && c.n_bins[f] >= 2 && c.n_bins[f] <= HOT_MAX_BINS) b += HOT_SLOTS * 16u;
+    return b;
+}
+
 void plan_tiles(fbh_ctx &c) {
     c.feat_tile.assign(c.n_features, -1);
     c.feat_pos.assign(c.n_features, -1);
@@ -698,6 +726,21 @@ void plan_tiles(fbh_ctx &c) {
         rot_tiles(w, rot, push);
         fbh_ctx::Tile cur{w, 0, 0, {}, nullptr, false};
         uint64_t lds = 0;
+        // Planar tiles of one width hold at most as many features as a tile
+        // holds of the width's widest LDS feature, so that every workgroup of
+        // a launch adds about as many cells a row (wide-bin 2M x 100: tiles of
+        // 3 x 1024-bin numeric and 6 x 500-code categorical features against
+        // 3 and 3, 424 against 455 rounds/s).
+        uint32_t max_feats = c.planar_max_feats;
+        if (!max_feats) {
+            uint64_t widest = 0;
+            for (uint32_t f = 0; f < c.n_features; f++) {
+                const uint64_t fb = feature_lds_bytes(c, f);
+                if (c.width[f] == w && !in_rot[f] && fb <= c.planar_tile_bytes - 1024u)
+                    widest = std::max(widest, fb);
+            }
+            max_feats = widest ? (uint32_t)((c.planar_tile_bytes - 1024u) / widest) : 0u;
+        }
         auto flush = [&]() {
             if (cur.feats.empty()) return;
             cur.rec = round_stride((uint32_t)cur.feats.size() * w);
@@ -715,7 +758,7 @@ void plan_tiles(fbh_ctx &c) {
             // Tiles share planar_tile_bytes; a feature wider than that but
             // within tile_bytes takes a tile of its own.
             const uint64_t budget = c.planar_tile_bytes - 1024u;
-            const uint64_t fb = (uint64_t)c.n_bins[f] * 16u;
+            const uint64_t fb = feature_lds_bytes(c, f);
             if (fb > budget) {
                 // A tile of its own: in LDS up to tile_bytes, else too wide
                 // for LDS and accumulated in global memory.
@@ -727,7 +770,9 @@ void plan_tiles(fbh_ctx &c) {
                 continue;
             }
             const uint32_t rec = (uint32_t)(cur.feats.size() + 1) * w;
-            if (!cur.feats.empty() && (lds + fb > budget || rec > MAX_RECORD_BYTES)) flush();
+            if (!cur.feats.empty() && (lds + fb > budget || rec > MAX_RECORD_BYTES ||
+                                       (max_feats && cur.feats.size() >= max_feats)))
+                flush();
             cur.feats.push_back(f);
             lds += fb;
         }
@@ -820,13 +865,15 @@ void fixed_allocations(fbh_ctx &c, A &&a) {
     c.off_order = c.off_sfeats + al256(sizeof(SplitFeatDev) * c.n_features);
     c.off_pack = c.off_order + al256(4 * (uint64_t)c.n_features);
     // at most ceil(features / 16) packed tiles of each width
-    c.tables_bytes = c.off_pack + sizeof(PackTileDev) * ((uint64_t)c.n_features / 16 + 2);
+    c.off_root = c.off_pack + al256(sizeof(PackTileDev) * ((uint64_t)c.n_features / 16 + 2));
+    c.tables_bytes = c.off_root + sizeof(TileDev) * c.tiles.size();
     uint8_t *tt = static_cast<uint8_t *>(a(c.tables_bytes, "tree tables"));
     c.d_tiles = reinterpret_cast<TileDev *>(tt);
     c.d_tilefeats = reinterpret_cast<TileFeatDev *>(tt ? tt + c.off_tilefeats : nullptr);
     c.d_sfeats = reinterpret_cast<SplitFeatDev *>(tt ? tt + c.off_sfeats : nullptr);
     c.d_split_order = reinterpret_cast<uint32_t *>(tt ? tt + c.off_order : nullptr);
     c.d_pack = reinterpret_cast<PackTileDev *>(tt ? tt + c.off_pack : nullptr);
+    c.d_root_tiles = reinterpret_cast<TileDev *>(tt ? tt + c.off_root : nullptr);
     const uint64_t cw = std::max(1u, c.max_cat_words);
     c.d_cands = static_cast<FeatCandDev *>(
         a(sizeof(FeatCandDev) * (uint64_t)c.n_slots * c.n_features, "split candidates"));
@@ -1027,6 +1074,9 @@ fbh_config configure(fbh_ctx &c, uint64_t n_rows, const fbh_shape *shape, const 
                               : PLANAR_TILE_BYTES;
     c.fixed_chunk_rows = (uint32_t)env_u64("FB_HIP_CHUNK_ROWS", conf.rows_per_block);
     c.hist_tpb = (uint32_t)env_u64("FB_HIP_HIST_TPB", 0);
+    c.shared_line_rows = (uint32_t)env_u64("FB_HIP_LINE_ROWS", SHARED_LINE_CHUNK_ROWS);
+    c.planar_max_feats = (uint32_t)env_u64("FB_HIP_PLANAR_MAXF", 0);
+    c.max_partial_bytes = env_u64("FB_HIP_PARTIAL_MB", MAX_PARTIAL_BYTES >> 20) << 20;
     c.hist_waves = (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HIST_WAVES", HIST_WAVES));
     c.host_hist_waves =
         (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HOST_HIST_WAVES", HOST_HIST_WAVES));
@@ -1199,6 +1249,8 @@ int fbh_upload_block(fbh_ctx *c, const uint32_t *feat_ids, uint32_t n_feats, uin
     return guard([&] {
         if (!c || !feat_ids || !bins) throw InputError("null argument");
         check(hipSetDevice(c->device), "hipSetDevice");
+        c->tm_stale = true;
+        c->hot_ready = false;
         for (uint32_t l = 0; l < n_feats; l++) {
             const uint32_t f = feat_ids[l];
             if (f >= c->n_features) throw InputError("feature id out of range");
@@ -1340,6 +1392,8 @@ int fbh_finish_rows(fbh_ctx *c) {
         if (!c) throw InputError("null argument");
         if (!c->cuts_set) throw InputError("fbh_set_cuts must come before fbh_finish_rows");
         check(hipSetDevice(c->device), "hipSetDevice");
+        c->tm_stale = true;
+        c->hot_ready = false;
         for (uint32_t f = 0; f < c->n_features; f++) {
             const fbh_ctx::Tile &t = c->tiles[c->feat_tile[f]];
             if (t.resident) {
@@ -1360,6 +1414,77 @@ int fbh_finish_rows(fbh_ctx *c) {
 }
 
 namespace {
+
+// Tile-major copies (Tile::tm) of the given tiles, packed from the resident
+// bin columns; made once (again after an upload changed the records), and
+// only while they fit the budget's remaining room (they are outside the
+// memory plan). Returns whether every tile has one.
+bool ensure_tile_major(fbh_ctx &c, const std::vector<const fbh_ctx::Tile *> &tiles) {
+    if (c.tm_stale) {
+        for (auto &t : c.tiles)
+            if (t.tm) {
+                c.release_alloc(t.tm);
+                t.tm = nullptr;
+            }
+        c.tm_stale = false;
+    }
+    uint64_t need = 0;
+    for (const fbh_ctx::Tile *t : tiles)
+        if (!t->tm) need += std::max<uint64_t>((uint64_t)t->rec * c.n_rows, 256);
+    if (need && c.device_bytes + need + 256 > c.plan.budget) return false;
+    for (const fbh_ctx::Tile *tp : tiles) {
+        fbh_ctx::Tile &t = c.tiles[tp - c.tiles.data()];
+        if (t.tm) continue;
+        t.tm = c.alloc<uint8_t>((uint64_t)t.rec * c.n_rows, "tile-major records");
+        for (uint32_t f : t.feats)
+            check(launch_pack_feature(c.cols[f], c.n_rows, t.width, t.tm, t.rec,
+                                      (uint32_t)c.feat_pos[f] * t.width, c.stream),
+                  "tile-major packing");
+    }
+    return true;
+}
+
+// The hot bins of every categorical feature of at most HOT_MAX_BINS codes:
+// its one or two codes that each hold at least 1/16 of the rows (sampled),
+// from which a wave of 64 random rows takes four or more lanes on one
+// address. Needs the bin columns on the device; none otherwise.
+void ensure_hot_bins(fbh_ctx &c) {
+    if (c.hot_ready) return;
+    c.hot_a.assign(c.n_features, HOT_NONE);
+    c.hot_b.assign(c.n_features, HOT_NONE);
+    c.hot_ready = true;
+    if (!c.plan.columns_resident || env_u64("FB_HIP_NO_HOT", 0)) return;
+    std::vector<CatColDev> cols;
+    std::vector<uint32_t> feats;
+    for (uint32_t f = 0; f < c.n_features; f++)
+        if (c.cat[f] && c.n_bins[f] <= HOT_MAX_BINS && c.n_bins[f] >= 2 && c.cols[f]) {
+            cols.push_back({c.cols[f], c.width[f], c.n_bins[f]});
+            feats.push_back(f);
+        }
+    if (cols.empty()) return;
+    const uint32_t sample = 1u << 20;
+    const uint64_t tb = sizeof(CatColDev) * cols.size(), ob = 16 * cols.size();
+    if (c.device_bytes + tb + ob + 1024 > c.plan.budget) return;
+    uint8_t *buf = c.alloc<uint8_t>(((tb + 255) & ~uint64_t(255)) + ob, "hot-bin search");
+    uint32_t *d_out = reinterpret_cast<uint32_t *>(buf + ((tb + 255) & ~uint64_t(255)));
+    check(hipMemcpyAsync(buf, cols.data(), tb, hipMemcpyHostToDevice, c.stream), "hot-bin table");
+    check(launch_cat_hot(reinterpret_cast<const CatColDev *>(buf), (uint32_t)cols.size(), c.n_rows,
+                         sample, d_out, c.stream),
+          "hot-bin search");
+    std::vector<uint32_t> out(4 * cols.size());
+    check(hipMemcpyAsync(out.data(), d_out, ob, hipMemcpyDeviceToHost, c.stream),
+          "hot-bin download");
+    c.sync();
+    c.release_alloc(buf);
+    const uint64_t m = std::min<uint64_t>(c.n_rows, sample);
+    const uint32_t need = (uint32_t)std::max<uint64_t>(4, m / 16);
+    for (size_t i = 0; i < feats.size(); i++) {
+        const uint32_t f = feats[i];
+        if (out[4 * i] != HOT_NONE && out[4 * i + 2] >= need) c.hot_a[f] = out[4 * i];
+        if (c.hot_a[f] != HOT_NONE && out[4 * i + 1] != HOT_NONE && out[4 * i + 3] >= need)
+            c.hot_b[f] = out[4 * i + 1];
+    }
+}
 
 // This tree's packed tiles (fbh_ctx::pack_tiles) from its compact histogram
 // layout (hist_off). Per width, the tree's features of interleaved tiles are
@@ -2008,7 +2133,9 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
         }
         c->hist_width = off;
         // tiles with active features, grouped by (width, record dwords)
+        ensure_hot_bins(*c);
         std::vector<TileDev> td;
+        std::vector<const fbh_ctx::Tile *> td_src;  // the tile of each entry
         std::vector<TileFeatDev> tf;
         c->groups.clear();
         c->streamed.clear();
@@ -2025,14 +2152,22 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
             d.rec_dwords = t.rec / 4;
             lds = 0;
             active_bytes = 0;
+            const bool hot_ok = !t.rot && !t.global && t.resident;
             for (uint32_t f : t.feats) {
                 TileFeatDev e{};
+                e.hot[0] = e.hot[1] = HOT_NONE;
                 if (c->hist_off[f] >= 0) {
                     e.n_bins = c->n_bins[f];
                     e.lds_off = lds;
                     e.hist_off = (uint32_t)c->hist_off[f];
                     lds += c->n_bins[f];
                     active_bytes += t.width;
+                    if (hot_ok && c->hot_a[f] != HOT_NONE) {
+                        e.hot[0] = c->hot_a[f];
+                        e.hot[1] = c->hot_b[f];
+                        e.hot_off = lds;
+                        lds += HOT_SLOTS;
+                    }
                 }
                 tf.push_back(e);
             }
@@ -2047,6 +2182,7 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
             }
             d.lds_slots = t.global ? 0 : lds;
             td.push_back(d);
+            td_src.push_back(&t);
             return true;
         };
         const uint32_t packed = plan_pack(*c);
@@ -2093,6 +2229,29 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
             for (const fbh_ctx::Tile *t : built)
                 if (t->bundle >= 0)
                     c->line_share = std::max(c->line_share, ++per_bundle[t->bundle]);
+        }
+        // Tile-major copies for the root when the built tiles share bundle
+        // lines: the root's rows are in order, so each workgroup then reads
+        // its own tile's records contiguously and its chunks can be as long
+        // as one wave of workgroups allows (fewer flushes of the LDS
+        // histograms); deeper levels gather rows and keep the bundles.
+        std::vector<TileDev> td_root;
+        c->root_tm = false;
+        if (c->line_share > 4 && c->streamed.empty() && !c->has_global &&
+            c->plan.columns_resident && !c->groups.empty()) {
+            bool ok = true;
+            for (const auto &g : c->groups) ok = ok && !g.rot && !g.global;
+            for (size_t i = 0; ok && i < td_src.size(); i++)
+                ok = td_src[i] >= c->tiles.data() && td_src[i] < c->tiles.data() + c->tiles.size();
+            if (ok) ok = ensure_tile_major(*c, td_src);
+            if (ok) {
+                td_root = td;
+                for (size_t i = 0; i < td_root.size(); i++) {
+                    td_root[i].data = td_src[i]->tm;
+                    td_root[i].stride = td_src[i]->rec;
+                }
+                c->root_tm = true;
+            }
         }
         c->hist_row_bytes = 0;
         c->hist_tiles = 0;
@@ -2146,15 +2305,20 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
             }
             pk.push_back(d);
         }
-        std::vector<uint8_t> tables(pk.empty() ? c->off_order + 4 * order.size()
-                                               : c->off_pack + sizeof(PackTileDev) * pk.size(),
-                                    0);
+        std::vector<uint8_t> tables(
+            !td_root.empty() ? c->off_root + sizeof(TileDev) * td_root.size()
+            : pk.empty()     ? c->off_order + 4 * order.size()
+                             : c->off_pack + sizeof(PackTileDev) * pk.size(),
+            0);
         std::memcpy(tables.data(), td.data(), sizeof(TileDev) * td.size());
         std::memcpy(tables.data() + c->off_tilefeats, tf.data(), sizeof(TileFeatDev) * tf.size());
         std::memcpy(tables.data() + c->off_sfeats, sf.data(), sizeof(SplitFeatDev) * sf.size());
         std::memcpy(tables.data() + c->off_order, order.data(), 4 * order.size());
         if (!pk.empty())
             std::memcpy(tables.data() + c->off_pack, pk.data(), sizeof(PackTileDev) * pk.size());
+        if (!td_root.empty())
+            std::memcpy(tables.data() + c->off_root, td_root.data(),
+                        sizeof(TileDev) * td_root.size());
         const bool upload = tables != c->tree_tables;
         if (upload) {
             int slot;
@@ -2254,6 +2418,7 @@ struct EvalPlan {
     int64_t *partials = nullptr;
     uint32_t max_groups = 0;
     bool host_rule = false;  // planned with the host-driven chunk rule (HOST_HIST_WAVES)
+    const TileDev *tiles = nullptr;  // the tile table (null: the tree's, d_tiles)
 };
 
 void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
@@ -2312,7 +2477,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
         for (size_t gi = 0; gi < c->groups.size(); gi++) {
             const auto &g = c->groups[gi];
             HistLaunch L = launch_base();
-            L.tiles = c->d_tiles + g.tile_begin;
+            L.tiles = (E.tiles ? E.tiles : c->d_tiles) + g.tile_begin;
             L.n_tiles = g.n_tiles;
             if (c->timing && !marker) {
                 ev_start = gi == 0 ? c->ev_pool[ev].first : nullptr;
@@ -2989,7 +3154,11 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     // table and the monotone constraints go up only when they change); its
     // split node (sums, bounds) is written by the prep kernel from the root
     // sum, which also clears the root's slot when it accumulates atomically.
-    const uint32_t cr = c->chunk_rows_for(n_rows);
+    // With tile-major root records (the root's rows are 0..n in order,
+    // through the arena or not) no chunk shares bundle lines with another
+    // tile's workgroups: chunks as long as one wave allows.
+    const bool root_tm = c->root_tm;
+    const uint32_t cr = c->chunk_rows_for(n_rows, root_tm);
     HistNodeDev h{};
     h.row_off = 0;
     h.row_len = n_rows;
@@ -3013,6 +3182,7 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     E0.grid_chunks = h.n_chunks;
     E0.chunk_rows = cr;
     E0.identity = ident;
+    if (root_tm) E0.tiles = c->d_root_tiles;
     // Per-chunk partials instead of global atomics for multi-chunk nodes when
     // every tile is an LDS tile and the buffer (grid chunks x histogram) is
     // modest; only nodes of more than REDUCE_GROUP chunks then need cleared

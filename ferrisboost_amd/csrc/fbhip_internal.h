@@ -43,8 +43,17 @@ struct TileFeatDev {
     uint32_t n_bins;    // 0 when the feature is not built this tree
     uint32_t lds_off;   // first LDS slot of the feature
     uint32_t hist_off;  // first slot of the feature in a node histogram
+    // Planar tiles: the feature's two most frequent bins (HOT_NONE: none)
+    // are added into 64 lane-private LDS slots each, from hot_off (first
+    // bin) and hot_off + 64 (second), so the many lanes of one wave that
+    // hold a frequent category do not serialise on one address; the flush
+    // folds the lane slots back into their bin.
+    uint32_t hot[2];
+    uint32_t hot_off;
     uint32_t pad;
 };
+constexpr uint32_t HOT_NONE = 0xFFFFFFFFu;
+constexpr uint32_t HOT_SLOTS = 128u;  // lane-private slots of a feature with hot bins
 
 // One node of a histogram batch.
 struct HistNodeDev {
@@ -464,6 +473,17 @@ hipError_t launch_set_scales(ScalesDev *scales, double scale_g, double scale_h, 
 hipError_t launch_gpair_quantize(const float *g2n, uint64_t n, const ScalesDev *scales,
                                  int64_t *out, int64_t *block_sum, uint32_t n_blocks,
                                  int64_t *out_sum, hipStream_t s);
+// The two most frequent codes of categorical bin columns (HOT_MAX_BINS codes
+// at most), counted over up to `sample` rows spread evenly: out[4 f ..] =
+// (first code, second code, first count, second count), ties to the lower
+// code; HOT_NONE when a column has no second code.
+constexpr uint32_t HOT_MAX_BINS = 4096;
+struct CatColDev {
+    const uint8_t *col;
+    uint32_t width, n_bins;
+};
+hipError_t launch_cat_hot(const CatColDev *cols, uint32_t n_cols, uint64_t n_rows, uint32_t sample,
+                          uint32_t *out, hipStream_t s);
 hipError_t launch_pack_feature(const uint8_t *col, uint64_t n_rows, uint32_t width, uint8_t *tile,
                                uint32_t stride, uint32_t byte_off, hipStream_t s);
 

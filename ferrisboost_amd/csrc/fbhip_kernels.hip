@@ -165,6 +165,7 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
     // of its feature (k + rot) mod 16. Planar: per feature.
     const uint32_t rot = tid & 15u;
     uint32_t nb[NF], loff[NF];
+    uint32_t hot0[ROT ? 1 : NF], hot1[ROT ? 1 : NF], hoff[ROT ? 1 : NF];
 #pragma unroll
     for (int k = 0; k < NF; k++) {
         const uint32_t fi = ROT ? ((uint32_t)k + rot) & 15u : (uint32_t)k;
@@ -172,9 +173,18 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
             const TileFeatDev F = L.feats[T.feat_base + fi];
             nb[k] = F.n_bins;
             loff[k] = F.lds_off;
+            if constexpr (!ROT) {
+                hot0[k] = F.hot[0];
+                hot1[k] = F.hot[1];
+                hoff[k] = F.hot_off + (tid & 63u);
+            }
         } else {
             nb[k] = 0;
             loff[k] = 0;
+            if constexpr (!ROT) {
+                hot0[k] = hot1[k] = HOT_NONE;
+                hoff[k] = 0;
+            }
         }
     }
 
@@ -297,8 +307,13 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
                             if (fi >= (int)T.n_feat) continue;  // uniform
                             if (nb[fi] == 0) continue;  // not built this tree (uniform)
                             // Missing (all ones) and unseen-category codes are >= n_bins;
-                            // out-of-range rows (ok false) carry a zero pair.
+                            // out-of-range rows (ok false) carry a zero pair. A hot
+                            // bin goes to the lane's own slot of that bin.
                             s = bin < nb[fi] ? loff[fi] + bin : dummy;
+                            if constexpr (!ROT) {
+                                s = bin == hot0[fi] ? hoff[fi] : s;
+                                s = bin == hot1[fi] ? hoff[fi] + 64u : s;
+                            }
                         }
                         lds_add_u64(gplane + s, gg);
                         lds_add_u64(hplane + s, hh);
@@ -342,8 +357,17 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
     for (uint32_t fi = 0; fi < T.n_feat; fi++) {
         const TileFeatDev F = L.feats[T.feat_base + fi];
         for (uint32_t bin = tid; bin < F.n_bins; bin += TPB) {
-            const unsigned long long gg = gplane[F.lds_off + bin];
-            const unsigned long long hh = hplane[F.lds_off + bin];
+            unsigned long long gg = gplane[F.lds_off + bin];
+            unsigned long long hh = hplane[F.lds_off + bin];
+            // a hot bin: its 64 lane slots (integer sums, any order)
+            const int hk = bin == F.hot[0] ? 0 : bin == F.hot[1] ? 1 : -1;
+            if (hk >= 0) {
+                const uint32_t b = F.hot_off + 64u * (uint32_t)hk;
+                for (uint32_t l = 0; l < 64; l++) {
+                    gg += gplane[b + l];
+                    hh += hplane[b + l];
+                }
+            }
             unsigned long long *dst =
                 reinterpret_cast<unsigned long long *>(out + 2u * (F.hist_off + bin));
             if (single || partial) {
@@ -2654,6 +2678,56 @@ __global__ void pack_feature_kernel(const uint8_t *col, uint64_t n_rows, uint32_
         if (width == 1) dst[0] = col[r];
         else *reinterpret_cast<uint16_t *>(dst) = reinterpret_cast<const uint16_t *>(col)[r];
     }
+}
+
+// One workgroup a column: counts in LDS over the sampled rows, then the
+// largest count twice (lower code first on ties).
+__global__ __launch_bounds__(256) void cat_hot_kernel(const CatColDev *cols, uint64_t n_rows,
+                                                      uint32_t sample, uint32_t *out) {
+    __shared__ uint32_t cnt[HOT_MAX_BINS];
+    __shared__ uint32_t best_c[256], best_b[256];
+    const CatColDev F = cols[blockIdx.x];
+    const uint32_t nb = min(F.n_bins, HOT_MAX_BINS);
+    for (uint32_t i = threadIdx.x; i < nb; i += 256) cnt[i] = 0;
+    __syncthreads();
+    const uint64_t m = min<uint64_t>(n_rows, sample);
+    for (uint64_t i = threadIdx.x; i < m; i += 256) {
+        const uint64_t r = m == n_rows ? i : i * n_rows / m;
+        const uint32_t code = F.width == 1 ? (uint32_t)F.col[r]
+                                           : (uint32_t) reinterpret_cast<const uint16_t *>(F.col)[r];
+        if (code < nb) atomicAdd(&cnt[code], 1u);
+    }
+    __syncthreads();
+    for (int pick = 0; pick < 2; pick++) {
+        uint32_t bc = 0, bb = HOT_NONE;
+        for (uint32_t i = threadIdx.x; i < nb; i += 256)
+            if (cnt[i] > bc) {
+                bc = cnt[i];
+                bb = i;
+            }
+        best_c[threadIdx.x] = bc;
+        best_b[threadIdx.x] = bb;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t c = 0, b = HOT_NONE;
+            for (int t = 0; t < 256; t++)
+                if (best_c[t] > c || (best_c[t] == c && c > 0 && best_b[t] < b)) {
+                    c = best_c[t];
+                    b = best_b[t];
+                }
+            out[4 * blockIdx.x + pick] = b;
+            out[4 * blockIdx.x + 2 + pick] = c;
+            if (b != HOT_NONE) cnt[b] = 0;
+        }
+        __syncthreads();
+    }
+}
+
+hipError_t launch_cat_hot(const CatColDev *cols, uint32_t n_cols, uint64_t n_rows, uint32_t sample,
+                          uint32_t *out, hipStream_t s) {
+    if (n_cols == 0) return hipSuccess;
+    hipLaunchKernelGGL(cat_hot_kernel, dim3(n_cols), dim3(256), 0, s, cols, n_rows, sample, out);
+    return hipGetLastError();
 }
 
 hipError_t launch_pack_feature(const uint8_t *col, uint64_t n_rows, uint32_t width, uint8_t *tile,

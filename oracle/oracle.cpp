@@ -2502,6 +2502,14 @@ void orc_gradients(const float *pred, const float *labels, const float *w, uint6
     }
 }
 
+void orc_softmax_pairs(const float *margins, const float *labels, const float *w, uint64_t n,
+                       uint32_t k_count, uint32_t k, float *out) {
+    std::vector<std::vector<float>> preds(k_count);
+    for (u32 c = 0; c < k_count; c++) preds[c].assign(margins + (u64)c * n, margins + (u64)(c + 1) * n);
+    for (u64 i = 0; i < n; i++)
+        softmax_pair(preds, i, labels[i], w ? w[i] : 1.0f, k, out[2 * i], out[2 * i + 1]);
+}
+
 float orc_base_margin(uint32_t obj, float bs) { return base_margin_of(obj, bs); }
 
 float orc_quantile_scale(const float *pred, const float *labels, const float *w, uint64_t n) {

@@ -191,6 +191,12 @@ uint64_t orc_sketch_summary(const float *col, uint64_t n, const float *weights,
  * below the entry its target walk reached, since the library loaded. */
 uint64_t orc_compress_clamps(void);
 
+/* Objective::softmax_gradients (src/training/objective.rs:1175-1219) of class
+ * k from class-major margins [k_count][n]: f32 pairs [n][2], weights may be
+ * NULL. */
+void orc_softmax_pairs(const float *margins, const float *labels, const float *weights,
+                       uint64_t n, uint32_t k_count, uint32_t k, float *out2n);
+
 /* validated_weights (src/data/colsample.rs:119-141): 0 = uniform sampling
  * (absent or all equal), 1 = weighted, -1 = invalid (orc_last_error). */
 int orc_validated_weights(const float *weights, uint32_t n_features);

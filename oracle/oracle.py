@@ -190,6 +190,8 @@ def lib() -> C.CDLL:
         L.orc_sketch_summary.restype = C.c_uint64
         L.orc_compress_clamps.argtypes = []
         L.orc_compress_clamps.restype = C.c_uint64
+        L.orc_softmax_pairs.argtypes = [P, P, P, C.c_uint64, C.c_uint32, C.c_uint32, P]
+        L.orc_softmax_pairs.restype = None
         L.orc_validated_weights.argtypes = [P, C.c_uint32]
         L.orc_validated_weights.restype = C.c_int
         L.orc_sample_features_weighted.argtypes = [C.c_uint32, C.c_float, C.c_uint64,
@@ -572,3 +574,13 @@ def sketch_summary(col, max_bin, weights=None):
 
 def compress_clamps() -> int:
     return int(lib().orc_compress_clamps())
+
+
+def softmax_pairs(margins_kn, labels, weights, k):
+    """Softmax pairs of class k, [n][2] f32, from class-major margins [K][n]."""
+    m = np.ascontiguousarray(margins_kn, np.float32)
+    y = np.ascontiguousarray(labels, np.float32)
+    w = _f32_or_none(weights)
+    out = np.zeros(2 * y.size, np.float32)
+    lib().orc_softmax_pairs(_p(m), _p(y), _p(w), y.size, m.shape[0], k, _p(out))
+    return out

@@ -507,6 +507,25 @@ def test_lossguide_categorical_matches_oracle(fb, oracle):
     assert np.array_equal(pm.train_margins(X.shape[0]), om.train_margins(X.shape[0]))
 
 
+@pytest.mark.parametrize("policy", ["lossguide", "depthwise"])
+def test_tile_major_root_matches_oracle(fb, oracle, policy):
+    """Many planar tiles sharing each row bundle (wide-bin numeric and
+    categorical features, as C4): the root reads tile-major copies of the
+    records in long chunks, the deeper levels the bundles."""
+    from ferrisboost_amd import datasets
+
+    X, y, params, _ = datasets.widebin_cat(150_000, n_num=40, n_cat=8, n_codes=300)
+    params = dict(params, grow_policy=policy, max_depth=5, max_leaves=0 if policy ==
+                  "depthwise" else 255)
+    cat = [1 if t == "c" else 0 for t in params["feature_types"]]
+    op = {k: v for k, v in params.items() if k != "feature_types"}
+    om = oracle.train(X, y, oracle.make_params(n_rounds=3, **op), categorical=cat)
+    pm = fb.train(params, X, y, num_boost_round=3)
+    assert_same_models(om, pm)
+    assert np.array_equal(pm.train_margins(X.shape[0]).view(np.uint32),
+                          om.train_margins(X.shape[0]).view(np.uint32))
+
+
 def test_depthwise_categorical_partition_path(fb, oracle):
     from ferrisboost_amd import datasets
 
