@@ -548,6 +548,10 @@ struct fbh_ctx {
 
     // The row arena written out (rows in order) if the tree has not yet.
     void ensure_rows();
+    // The cell value that means missing for feature f (see PartReqDev::missing).
+    uint32_t missing_code(uint32_t f) const {
+        return width[f] == 2 ? 0xFFFFu : (n_bins[f] > 255 ? 0x100u : 0xFFu);
+    }
 
     // The next staging slot, once the copy that last read it has run.
     uint8_t *stage_acquire(int &slot) {
@@ -1052,7 +1056,9 @@ fbh_config configure(fbh_ctx &c, uint64_t n_rows, const fbh_shape *shape, const 
         if (c.width[f] != 1 && c.width[f] != 2)
             throw InputError("feature " + std::to_string(f) + " has bin width " +
                              std::to_string(c.width[f]) + "; only 1 and 2 are supported");
-        const uint32_t lim = c.width[f] == 1 ? 255u : 65535u;
+        // An 8-bit numeric feature may hold 256 bins when it has no missing
+        // row (the caller's promise): every byte is then a bin.
+        const uint32_t lim = c.width[f] == 1 ? (c.cat[f] ? 255u : 256u) : 65535u;
         if (c.n_bins[f] == 0 || c.n_bins[f] > lim)
             throw InputError("feature " + std::to_string(f) + " has " +
                              std::to_string(c.n_bins[f]) + " bins, not storable at width " +
@@ -2784,6 +2790,7 @@ PartStage stage_partition(fbh_ctx *c, const fbh_part_req *reqs, uint32_t n,
             d.byte_off = 0;
         }
         d.width = t.width;
+        d.missing = c->missing_code(r.feat);
         d.bin = r.bin;
         d.missing_left = r.missing_left;
         d.cat_off = r.cat_offset;
@@ -3051,7 +3058,8 @@ void ensure_grow(fbh_ctx *c, uint32_t D) {
         G.h_root_hn.n_chunks = ~0u;  // never a real plan: the first tree uploads
         G.cols = c->alloc<DevColumn>(c->n_features, "grown tree columns");
         std::vector<DevColumn> cols(c->n_features);
-        for (uint32_t f = 0; f < c->n_features; f++) cols[f] = {c->cols[f], c->width[f], 0};
+        for (uint32_t f = 0; f < c->n_features; f++)
+            cols[f] = {c->cols[f], c->width[f], c->missing_code(f)};
         check(hipMemcpy(G.cols, cols.data(), sizeof(DevColumn) * cols.size(),
                         hipMemcpyHostToDevice),
               "column table");
@@ -3060,7 +3068,8 @@ void ensure_grow(fbh_ctx *c, uint32_t D) {
             for (uint32_t f = 0; f < c->n_features; f++) {
                 const auto &t = c->tiles[c->feat_tile[f]];
                 off[f] = (uint16_t)((t.bundle_off + c->feat_pos[f] * t.width) |
-                                    (t.width == 2 ? 0x8000u : 0u));
+                                    (t.width == 2 ? 0x8000u : 0u) |
+                                    (c->missing_code(f) == 0x100u ? 0x4000u : 0u));
             }
             G.feat_off = c->alloc<uint16_t>(c->n_features, "grown tree feature offsets");
             check(hipMemcpy(G.feat_off, off.data(), 2 * off.size(), hipMemcpyHostToDevice),

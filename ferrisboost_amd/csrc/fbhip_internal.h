@@ -175,6 +175,9 @@ struct PartReqDev {
     uint32_t bin, missing_left;
     uint32_t cat_off, n_cat_words;
     uint32_t count_base;   // index of the request's first chunk in the chunk arrays
+    // The cell value that means missing: all ones of the width, except for an
+    // 8-bit feature of 256 bins (no missing row, every byte a bin): 256.
+    uint32_t missing;
 };
 
 // One split node of a fused partition + evaluation step: its children's
@@ -229,7 +232,8 @@ constexpr uint32_t REDUCE_GROUP = 16;
 // Column of one feature for the partition of a device-grown tree.
 struct DevColumn {
     const uint8_t *data;
-    uint32_t width, pad;
+    uint32_t width;
+    uint32_t missing;  // the cell value that means missing (256 for a full 8-bit column: none)
 };
 
 

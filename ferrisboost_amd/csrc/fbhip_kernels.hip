@@ -1525,8 +1525,7 @@ __device__ __forceinline__ uint32_t cell_of(const PartReqDev &R, uint32_t row) {
 // The partition's go-left rule for a cell value of the request's feature.
 __device__ __forceinline__ bool bin_goes_left(const PartReqDev &R, uint32_t bin,
                                               const uint64_t *cat_words) {
-    const uint32_t missing = R.width == 1 ? 0xFFu : 0xFFFFu;
-    if (bin == missing) return R.missing_left != 0;
+    if (bin == R.missing) return R.missing_left != 0;
     if (R.n_cat_words) {
         const uint32_t w = bin >> 6;
         const bool in = w < R.n_cat_words && ((cat_words[R.cat_off + w] >> (bin & 63)) & 1ull);
@@ -3133,6 +3132,7 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
             q.stride = col.width;
             q.byte_off = 0;
             q.width = col.width;
+            q.missing = col.missing;
             q.bin = P.bin;
             q.missing_left = P.missing_left;
             q.cat_off = P.cat_offset;
@@ -3248,7 +3248,8 @@ __global__ __launch_bounds__(256) void tree_leaves_kernel(
     float *leaf_vals) {
     __shared__ uint32_t buf[32];
     // Node: meta (bits 0-5 cell offset, 6: 16-bit cell, 7: leaf, 8: missing
-    // goes left, 9: categorical), split bin, left, right.
+    // goes left, 9: categorical, 10: an 8-bit cell without a missing code),
+    // split bin, left, right.
     __shared__ ushort4 s_node[MAX_WALK_NODES];
     __shared__ uint16_t s_leaf[MAX_WALK_NODES];
     __shared__ uint32_t s_cat[MAX_WALK_NODES];
@@ -3268,7 +3269,8 @@ __global__ __launch_bounds__(256) void tree_leaves_kernel(
             lf = flags & 1u;
             const uint32_t fo = lf ? 0u : feat_off[t.feat];
             const uint32_t meta = (fo & 0x3Fu) | ((fo & 0x8000u) ? 0x40u : 0u) | (lf << 7) |
-                                  ((flags & 2u) << 7) | ((flags & 4u) << 7);
+                                  ((flags & 2u) << 7) | ((flags & 4u) << 7) |
+                                  ((fo & 0x4000u) ? 0x400u : 0u);
             s_node[k] = make_ushort4((uint16_t)meta, (uint16_t)t.bin, (uint16_t)t.left,
                                      (uint16_t)t.right);
             s_cat[k] = t.cat_off;
@@ -3316,7 +3318,8 @@ __global__ __launch_bounds__(256) void tree_leaves_kernel(
             for (int q = 1; q < PB; q++) word = (qi == (uint32_t)q) ? rec[q] : word;
             const bool w2 = (nd.x & 0x40u) != 0;
             const uint32_t bin = (word >> ((off & 3u) * 8u)) & (w2 ? 0xFFFFu : 0xFFu);
-            const uint32_t missing = w2 ? 0xFFFFu : 0xFFu;
+            // an 8-bit column of 256 bins has no missing code (bit 10)
+            const uint32_t missing = w2 ? 0xFFFFu : ((nd.x & 0x400u) ? 0x100u : 0xFFu);
             bool gl;
             if (bin == missing) {
                 gl = (nd.x & 0x100u) != 0;

@@ -25,13 +25,21 @@ struct Cuts {
     std::vector<float> values;
     std::vector<uint32_t> offsets;  // n_features + 1
     std::vector<uint8_t> categorical;
+    // Numeric features of 256 bins with no missing value in the training
+    // rows (empty: none known): stored in 8-bit cells, every byte a bin.
+    std::vector<uint8_t> full;
 
     uint32_t n_features() const { return (uint32_t)offsets.size() - 1; }
     uint32_t n_cuts(uint32_t f) const { return offsets[f + 1] - offsets[f]; }
     uint32_t n_bins(uint32_t f) const { return n_cuts(f) + 1; }
     bool is_cat(uint32_t f) const { return categorical[f] != 0; }
-    // BinWidth::for_feature (src/data/bins.rs:55-66).
+    // BinWidth::for_feature (src/data/bins.rs:55-66): 8-bit cells up to 255
+    // bins (the all-ones byte is the missing code), 16-bit beyond. Storage
+    // only: a 256-bin numeric feature without missing values needs no
+    // missing code, so its bins fit 8-bit cells too (same bins, half the
+    // bytes the histograms read).
     uint32_t width(uint32_t f) const {
+        if (n_bins(f) == 256 && !is_cat(f) && f < full.size() && full[f]) return 1;
         return n_bins(f) <= (is_cat(f) ? 254u : 255u) ? 1u : 2u;
     }
     uint32_t bin_of(uint32_t f, float v) const;

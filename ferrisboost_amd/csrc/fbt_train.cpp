@@ -1077,6 +1077,34 @@ uint32_t last_round_stats(double *wall, double *ms, uint64_t *bytes, uint32_t ca
     return n;
 }
 
+// Cuts::full from the rows: which 256-bin numeric features hold no NaN.
+// One pass over the row-major matrix, rows split among threads.
+void mark_full_features(Cuts &c, const float *x, uint64_t n, uint32_t nf, unsigned threads) {
+    std::vector<uint32_t> cand;
+    for (uint32_t f = 0; f < nf; f++)
+        if (!c.is_cat(f) && c.n_bins(f) == 256) cand.push_back(f);
+    c.full.assign(nf, 0);
+    if (cand.empty() || n == 0) return;
+    const unsigned nt = std::max(1u, std::min<unsigned>(threads, (unsigned)std::min<uint64_t>(n, 64)));
+    std::vector<std::vector<uint8_t>> nan_seen(nt, std::vector<uint8_t>(cand.size(), 0));
+    std::vector<std::thread> pool;
+    for (unsigned t = 0; t < nt; t++)
+        pool.emplace_back([&, t] {
+            std::vector<uint8_t> &seen = nan_seen[t];
+            const uint64_t lo = n * t / nt, hi = n * (t + 1) / nt;
+            for (uint64_t r = lo; r < hi; r++) {
+                const float *row = x + r * nf;
+                for (size_t k = 0; k < cand.size(); k++) seen[k] |= row[cand[k]] != row[cand[k]];
+            }
+        });
+    for (auto &th : pool) th.join();
+    for (size_t k = 0; k < cand.size(); k++) {
+        uint8_t any = 0;
+        for (unsigned t = 0; t < nt; t++) any |= nan_seen[t][k];
+        c.full[cand[k]] = any ? 0 : 1;
+    }
+}
+
 Model train(const RowSource &src, uint64_t n, uint32_t nf, const float *y, const float *w,
             const uint8_t *cat, const int8_t *mono_in, uint32_t n_mono, const fbt_params &p,
             const Cuts *given) {
@@ -1131,6 +1159,9 @@ Model train(const RowSource &src, uint64_t n, uint32_t nf, const float *y, const
         m.cuts = sketch_matrix(x, n, nf, p.max_bin, w, cat, threads);
     }
     const double sketch_s = std::chrono::duration<double>(Clock::now() - t_sketch).count();
+    // 256-bin numeric features without a missing row take 8-bit cells
+    // (Cuts::full), when the rows are in host memory for the check.
+    if (x) mark_full_features(m.cuts, x, n, nf, threads);
     // Base score: explicit, else the label mean weighted by the sample weights
     // only (Objective::estimate_base_score, src/training/objective.rs:42-60,
     // 452-470; scale_pos_weight enters the gradient weights alone,

@@ -507,6 +507,37 @@ def test_lossguide_categorical_matches_oracle(fb, oracle):
     assert np.array_equal(pm.train_margins(X.shape[0]), om.train_margins(X.shape[0]))
 
 
+@pytest.mark.parametrize("knobs", [
+    {},                                             # device-grown, row walk (one bundle)
+    {"hip_host_levels": True},                      # host-driven levels
+    {"grow_policy": "lossguide", "max_leaves": 20},  # capped lossguide
+    {"resident_blocks": 0},                         # everything streamed
+    {"colsample_bytree": 0.6},                      # packed interleaved tiles
+])
+def test_full_byte_cells_match_oracle(fb, oracle, knobs):
+    """max_bin 256 on continuous features without missing values: 256 bins a
+    feature, stored as 8-bit cells in which every byte is a bin (no missing
+    code); one feature with a NaN keeps 16-bit cells. Trees and margins equal
+    the oracle's, whose bins are 16-bit as the reference's."""
+    rng = np.random.default_rng(77)
+    n, nf = 40_000, 20
+    x = rng.normal(size=(n, nf)).astype(np.float32)
+    x[5, 3] = np.nan  # feature 3 has a missing value: 16-bit cells
+    y = (x[:, 0] + np.nan_to_num(x[:, 3]) * x[:, 7] - 0.5 * x[:, 12] + 0.3 * rng.normal(size=n)
+         > 0).astype(np.float32)
+    p = {"max_depth": 6, "eta": 0.3, "max_bin": 256}
+    kw = dict(knobs)
+    op = {k: v for k, v in dict(p, **kw).items() if not k.startswith("hip_") and
+          k != "resident_blocks"}
+    om = oracle.train(x, y, oracle.make_params(n_rounds=4, **op))
+    pm = fb.train(dict(p, **kw), x, y, 4)
+    assert_same_models(om, pm)
+    assert np.array_equal(pm.train_margins(n).view(np.uint32), om.train_margins(n).view(np.uint32))
+    # the bins reach 255: the last bin is a real one
+    t = pm.trees()
+    assert any((tr["is_leaf"] == 0).any() for tr in t)
+
+
 @pytest.mark.parametrize("policy", ["lossguide", "depthwise"])
 def test_tile_major_root_matches_oracle(fb, oracle, policy):
     """Many planar tiles sharing each row bundle (wide-bin numeric and
