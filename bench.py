@@ -26,8 +26,9 @@ Prints one JSON line:
                 16 B gradient pair + 4 B row id per accumulated row, + 32 B
                 per written histogram bin; the pair counts 16 B also where the
                 kernel reads 8 B of f32 and quantizes it) over their HIP-event
-                time, against
-                8 TB/s HBM; traffic from the committed rocprofv3 summary
+                time, against 8 TB/s HBM; traffic: HBM bytes per launch in the
+                same rounds, from the committed rocprofv3 counter summary
+                (`--traffic-summary` writes it from the counter runs)
   cpu_baseline  the CPU oracle (C++ restatement of the reference CPU engine)
                 on a bounded sample of the same workload, threads stated
 """
@@ -60,20 +61,47 @@ def log(msg: str) -> None:
 
 
 def load_traffic(path: str):
-    """`key = value` lines of a committed rocprofv3 counter summary."""
-    out = {}
+    """A committed counter summary of the histogram kernel: `key = value`
+    lines, and one `round R LAUNCHES FETCH_KIB WRITE_KIB` line per round of
+    the profiled job's first training run (FETCH_SIZE and WRITE_SIZE summed
+    over that round's histogram dispatches)."""
+    meta, rounds = {}, {}
     try:
         with open(path) as f:
             for line in f:
-                if "=" in line and not line.lstrip().startswith("#"):
-                    k, v = line.split("=", 1)
-                    try:
-                        out[k.strip()] = float(v.split()[0])
-                    except (ValueError, IndexError):
-                        pass
+                s = line.strip()
+                if not s or s.startswith("#"):
+                    continue
+                if s.startswith("round "):
+                    _, r, n, fk, wk = s.split()
+                    rounds[int(r)] = (int(n), float(fk), float(wk))
+                elif "=" in s:
+                    k, v = s.split("=", 1)
+                    meta[k.strip()] = v.strip()
     except OSError:
-        return None
-    return out or None
+        return None, None
+    return meta, rounds
+
+
+def window_traffic(path: str, workload: str, lo: int, hi: int):
+    """HBM bytes per histogram launch over rounds [lo, hi) of `workload`, from
+    the committed summary (None and the reason where it does not cover them:
+    another workload, or rounds it did not profile)."""
+    meta, rounds = load_traffic(path)
+    if meta is None:
+        return None, f"no counter summary {os.path.relpath(path, ROOT)}"
+    if meta.get("workload") != workload:
+        return None, f"{os.path.relpath(path, ROOT)} profiles another workload"
+    if any(r not in rounds for r in range(lo, hi)):
+        return None, f"{os.path.relpath(path, ROOT)} does not cover rounds {lo}..{hi - 1}"
+    ff, wf = float(meta["fetch_factor"]), float(meta["write_factor"])
+    n = sum(rounds[r][0] for r in range(lo, hi))
+    fetch = sum(rounds[r][1] for r in range(lo, hi)) * 1024.0 * ff
+    write = sum(rounds[r][2] for r in range(lo, hi)) * 1024.0 * wf
+    if n == 0:
+        return None, f"no histogram launch in rounds {lo}..{hi - 1}"
+    return {"bytes": (fetch + write) / n, "fetch": fetch / n, "write": write / n,
+            "launches": n}, None
 
 
 def copy_probe(mib: int) -> int:
@@ -145,34 +173,48 @@ def train_workload(args, X, y, params, desc: str, traffic_tag: str):
         wall = np.zeros(rounds)
         hms = np.zeros(rounds)
         hbytes = np.zeros(rounds, np.uint64)
+        hlaunch = np.zeros(rounds, np.uint64)
         n = N.train_lib().fbt_last_round_stats(N.ptr(wall), N.ptr(hms), N.ptr(hbytes), rounds)
         assert n == rounds
-        return model, wall, hms, hbytes
+        assert N.train_lib().fbt_last_round_launches(N.ptr(hlaunch), rounds) == rounds
+        return model, wall, hms, hbytes, hlaunch
 
     # The throughput comes from a run without event timing; the histogram
     # kernels are timed (HIP events on their dispatches) in a second run.
-    model, wall, _, _ = run(False)
+    model, wall, _, _, _ = run(False)
     t_wall = float(wall[timed].sum())
-    pmodel, _, hms, hbytes = run(True)
+    pmodel, _, hms, hbytes, hlaunch = run(True)
     # Both runs grow the same trees (the device path is deterministic).
     same_runs = all(np.array_equal(model.tree_nodes(t), pmodel.tree_nodes(t))
                     for t in range(rounds))
     t_hist_ms = float(hms[timed].sum())
     b_hist = float(hbytes[timed].astype(np.float64).sum())
     hist_gbps = b_hist / (t_hist_ms * 1e-3) / 1e9 if t_hist_ms > 0 else 0.0
-    launches = int(pmodel.stats["hist_launches"])
-    bytes_per_launch = float(pmodel.stats["hist_bytes"]) / launches if launches else 0.0
-    traffic = (load_traffic(os.path.join(ROOT, "profiles", f"hist_traffic_{traffic_tag}.txt"))
-               if traffic_tag else None)
+    launches = int(hlaunch[timed].sum())
+    bytes_per_launch = b_hist / launches if launches else 0.0
     roofline = {
         "bound": "hbm",
         "achieved": round(hist_gbps, 1),
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
         "frac": round(hist_gbps / HBM_PEAK_GBPS, 4),
-        "traffic": traffic.get("hbm_bytes_per_launch") if traffic else None,
+        "traffic": None,
         "algorithmic_bytes_per_launch": round(bytes_per_launch),
     }
+    # HBM traffic of the same rounds' histogram launches (the trees are the
+    # same in every run of this workload), from the committed counter summary.
+    if traffic_tag:
+        tr, why = window_traffic(os.path.join(ROOT, "profiles", f"hist_traffic_{traffic_tag}.txt"),
+                                 desc, args.warmup, rounds)
+        if tr and tr["launches"] != launches:
+            tr, why = None, (f"the summary counts {tr['launches']} launches in rounds "
+                             f"{args.warmup}..{rounds - 1}, this run {launches}")
+        if tr:
+            roofline["traffic"] = round(tr["bytes"])
+            roofline["traffic_rounds"] = [args.warmup, rounds - 1]
+            roofline["traffic_over_algorithmic"] = round(tr["bytes"] / bytes_per_launch, 3)
+        else:
+            roofline["traffic_note"] = why
 
     cpu = None
     parity = None
@@ -221,7 +263,7 @@ def train_workload(args, X, y, params, desc: str, traffic_tag: str):
     out.update({
         "hist_gbps": round(hist_gbps, 1),
         "hist_ms_per_round": round(t_hist_ms / args.steps, 3),
-        "hist_launches_per_round": round(launches / rounds, 2),
+        "hist_launches_per_round": round(launches / args.steps, 2),
         # the whole job: setup (sketch and binning) plus every round, warmup included
         "job_seconds": round(model.stats["setup_seconds"] + float(wall.sum()), 3),
         "gradient_ms_per_round": round(1e3 * model.stats["host_gradient_seconds"] / rounds, 3),
@@ -411,6 +453,160 @@ def shap_workload(args):
 FULL_ROUNDS = {"narrow": 500, "wide": 200, "widebin": 300}
 
 
+def workload_desc(args):
+    """The training workload's description (the line's config.workload) and
+    the tag of its histogram counter summary (None: no summary kept)."""
+    w = args.workload
+    if w == "narrow":
+        rows = args.rows or 10_500_000
+        cells = ("u8 bins" if args.max_bin <= 255 else
+                 "256 bins a feature in 8-bit cells: no missing values" if args.max_bin == 256
+                 else "u16 bins")
+        return (f"narrow {rows}x28 HIGGS-like binary, max_bin={args.max_bin} ({cells}), depth 8, "
+                f"eta 0.1, gpu_math={args.gpu_math}, depthwise",
+                f"narrow_{args.max_bin}" if args.gpu_math == "exact" else None)
+    if w in ("multiclass", "quantile"):
+        rows = args.rows or 10_500_000
+        what = ("4 classes, multi:softprob (4 trees a round)" if w == "multiclass" else
+                "reg:quantileerror at quantile_alpha 0.1/0.5/0.9 (3 trees a round)")
+        return (f"narrow {rows}x28 rows, {what}, max_bin=255 (u8 bins), depth 8, "
+                f"eta 0.1, gpu_math={args.gpu_math}, depthwise", None)
+    if w == "wide":
+        rows = args.rows or 400_000
+        return (f"wide {rows}x2000 L2-normalised binary, max_bin=256, depth 8, "
+                f"colsample_bytree 0.5, gpu_math={args.gpu_math}",
+                "wide" if args.gpu_math == "exact" else None)
+    rows = args.rows or 2_000_000
+    return (f"wide-bin {rows}x100 (80 numeric 10% NaN + 20 categorical x 500 "
+            "Zipf codes), max_bin=1024 (u16), reg:squarederror, lossguide 255 leaves", "widebin")
+
+
+def workload_data(args):
+    from ferrisboost_amd import datasets
+
+    w = args.workload
+    if w == "narrow":
+        X, y, params, _ = datasets.narrow_binary(args.rows or 10_500_000, max_bin=args.max_bin)
+    elif w == "multiclass":
+        X, y, params, _ = datasets.narrow_multiclass(args.rows or 10_500_000)
+    elif w == "quantile":
+        X, y, params, _ = datasets.narrow_quantile(args.rows or 10_500_000)
+    elif w == "wide":
+        X, y, params, _ = datasets.wide_binary(args.rows or 400_000, n_features=2000)
+    else:
+        X, y, params, _ = datasets.widebin_cat(args.rows or 2_000_000)
+    return X, y, params
+
+
+def _counter_rows(d: str, counter: str):
+    """(dispatch id, kernel name, value) of every dispatch in a rocprofv3
+    --pmc CSV under directory d, in dispatch order."""
+    import csv
+    import glob
+
+    files = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {d}")
+    out = []
+    for fn in files:
+        with open(fn, newline="") as f:
+            for row in csv.DictReader(f):
+                if row["Counter_Name"] == counter:
+                    out.append((int(row["Dispatch_Id"]), row["Kernel_Name"],
+                                float(row["Counter_Value"])))
+    out.sort()
+    return out
+
+
+def traffic_summary(args, d: str) -> int:
+    """Write profiles/hist_traffic_<tag>.txt from the counter runs under d:
+    <tag>_FETCH_SIZE/ and <tag>_WRITE_SIZE/ (the bench command with
+    hist_kernel and gradient_kernel dispatches counted), copy_FETCH_SIZE/ and
+    copy_WRITE_SIZE/ (--copy-probe 1024). The histogram dispatches of round r
+    are those between the r-th and the (r+1)-th gradient dispatch of the
+    first training run."""
+    desc, tag = workload_desc(args)
+    if tag is None:
+        raise SystemExit(f"no counter summary is kept for {desc}")
+    rounds = args.warmup + args.steps
+    copy_bytes = 1024 << 20
+    factor = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        v = [x for _, k, x in _counter_rows(os.path.join(d, f"copy_{c}"), c) if "copy" in k.lower()]
+        factor[c] = copy_bytes / (1024.0 * sum(v) / len(v))
+    per = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        rows = _counter_rows(os.path.join(d, f"{tag}_{c}"), c)
+        grads = [i for i, k, _ in rows if "gradient_kernel<" in k]
+        if len(grads) != 2 * rounds:
+            raise SystemExit(f"{c}: {len(grads)} gradient dispatches, expected 2 x {rounds}")
+        table = [[] for _ in range(rounds)]
+        r = -1
+        for i, k, x in rows:
+            if "gradient_kernel<" in k:
+                r += 1
+            elif "hist_kernel" in k and 0 <= r < rounds:
+                table[r].append(x)
+        per[c] = table
+    if [len(t) for t in per["FETCH_SIZE"]] != [len(t) for t in per["WRITE_SIZE"]]:
+        raise SystemExit("the FETCH_SIZE and WRITE_SIZE runs launched different histograms")
+    extra = "" if args.workload != "narrow" else (
+        f" --max-bin {args.max_bin}" if args.max_bin != 255 else "")
+    cmd = f"python3 bench.py --workload {args.workload}{extra} --steps {args.steps} " \
+          f"--warmup {args.warmup} --no-cpu"
+    ff, wf = factor["FETCH_SIZE"], factor["WRITE_SIZE"]
+    lines = [
+        f"# HBM traffic of the histogram kernel: {desc}, {rounds} rounds",
+        "# Commands (repository root on the MI355X box; one counter a pass):",
+    ]
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        lines.append(f'#   rocprofv3 --pmc {c} -f csv --kernel-include-regex "hist_kernel|gradient_kernel" '
+                     f"-d gpurun_out/pmct/{tag}_{c} -o c -- {cmd}")
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        lines.append(f"#   rocprofv3 --pmc {c} -f csv -d gpurun_out/pmct/copy_{c} -o c -- "
+                     "python3 bench.py --copy-probe 1024")
+    lines += [
+        f"#   python3 bench.py --workload {args.workload}{extra} --steps {args.steps} "
+        f"--warmup {args.warmup} --traffic-summary gpurun_out/pmct",
+        "# Calibration: a 1 GiB device copy reads FETCH_SIZE "
+        f"{copy_bytes / 1024 / ff:.0f} KiB and WRITE_SIZE {copy_bytes / 1024 / wf:.0f} KiB a "
+        "dispatch, so bytes = KiB x 1024 x factor. FETCH_SIZE counts L2 misses to the fabric,",
+        "# some of which the 256 MB Infinity Cache serves, so it bounds HBM reads from above.",
+        "# The bench line of a run of this workload averages the rounds it times; the rows",
+        "# below are the first training run of the command (the second grows the same trees).",
+        f"workload = {desc}",
+        f"fetch_factor = {ff:.4f}",
+        f"write_factor = {wf:.4f}",
+        f"rounds = {rounds}",
+    ]
+    # per launch position within a round (the tree level for depthwise
+    # trees), over the rounds a default bench window times and over all
+    def by_pos(lo, hi):
+        acc = {}
+        for r in range(lo, min(hi, rounds)):
+            for j, (fk, wk) in enumerate(zip(per["FETCH_SIZE"][r], per["WRITE_SIZE"][r])):
+                a = acc.setdefault(j, [0, 0.0, 0.0])
+                a[0] += 1
+                a[1] += fk
+                a[2] += wk
+        return acc
+    for lo, hi in ((5, 25), (0, rounds)):
+        lines.append(f"# launch j of a round, rounds {lo}..{min(hi, rounds) - 1}: launches, "
+                     "fetch MB, write MB a launch")
+        for j, (n, fk, wk) in sorted(by_pos(lo, hi).items()):
+            lines.append(f"#   {j:3d} {n:6d} {fk * 1024 * ff / n / 1e6:10.1f} "
+                         f"{wk * 1024 * wf / n / 1e6:8.1f}")
+    lines.append("# round, histogram launches, FETCH_SIZE KiB, WRITE_SIZE KiB (sums over the round)")
+    for r in range(rounds):
+        lines.append(f"round {r} {len(per['FETCH_SIZE'][r])} {sum(per['FETCH_SIZE'][r]):.0f} "
+                     f"{sum(per['WRITE_SIZE'][r]):.0f}")
+    path = os.path.join(ROOT, "profiles", f"hist_traffic_{tag}.txt")
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print(path)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -422,14 +618,18 @@ def main() -> int:
                     choices=["narrow", "multiclass", "quantile", "wide", "widebin", "streaming",
                              "shap", "predict"])
     ap.add_argument("--rows", type=int, default=0, help="rows (0: the workload's own size)")
-    ap.add_argument("--max-bin", type=int, default=255, help="narrow workload: 255 (u8) or 256 (u16)")
+    ap.add_argument("--max-bin", type=int, default=255, help="narrow workload: 255 or 256 (8-bit cells; 256 bins fill a byte where "
+                         "no value is missing) or more (u16)")
     ap.add_argument("--gpu-math", default="exact", choices=["exact", "fast"],
-                    help="narrow workload: exact (host-libm gradients, byte-identical trees) or "
-                         "fast (hardware exp on the device)")
+                    help="narrow, multiclass, quantile and wide workloads: exact (byte-identical "
+                         "trees) or fast (hardware exp on the device)")
     ap.add_argument("--cpu-rounds", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a device copy of MIB MiB (counter calibration) and exit")
+    ap.add_argument("--traffic-summary", metavar="DIR", default=None,
+                    help="write the workload's histogram counter summary under profiles/ from "
+                         "the rocprofv3 --pmc runs under DIR (no GPU needed) and exit")
     args = ap.parse_args()
     if args.steps is None:
         # A training workload's default run is the whole job: warmup plus
@@ -442,9 +642,10 @@ def main() -> int:
         return 2
     if args.copy_probe:
         return copy_probe(args.copy_probe)
+    if args.traffic_summary:
+        return traffic_summary(args, args.traffic_summary)
 
     import ferrisboost_amd as fb
-    from ferrisboost_amd import datasets
 
     if not fb.device_available(0):
         print("no gfx950 device at cuda:0", file=sys.stderr)
@@ -457,42 +658,13 @@ def main() -> int:
         out = predict_workload(args)
     elif args.workload == "streaming":
         out = streaming_workload(args)
-    elif args.workload == "narrow":
-        X, y, params, _ = datasets.narrow_binary(args.rows or 10_500_000, max_bin=args.max_bin)
-        log(f"data {X.shape} generated in {time.time() - t0:.1f}s")
-        u = "u8" if args.max_bin <= 255 else "u16"
-        params = dict(params, gpu_math=args.gpu_math)
-        out = train_workload(
-            args, X, y, params,
-            f"narrow {X.shape[0]}x{X.shape[1]} HIGGS-like binary, max_bin={args.max_bin} "
-            f"({u} bins), depth 8, eta 0.1, gpu_math={args.gpu_math}, depthwise", f"narrow_{u}")
-    elif args.workload in ("multiclass", "quantile"):
-        if args.workload == "multiclass":
-            X, y, params, _ = datasets.narrow_multiclass(args.rows or 10_500_000)
-            what = "4 classes, multi:softprob (4 trees a round)"
-        else:
-            X, y, params, _ = datasets.narrow_quantile(args.rows or 10_500_000)
-            what = "reg:quantileerror at quantile_alpha 0.1/0.5/0.9 (3 trees a round)"
-        log(f"data {X.shape} generated in {time.time() - t0:.1f}s")
-        params = dict(params, gpu_math=args.gpu_math)
-        out = train_workload(
-            args, X, y, params,
-            f"narrow {X.shape[0]}x{X.shape[1]} rows, {what}, max_bin=255 (u8 bins), depth 8, "
-            f"eta 0.1, gpu_math={args.gpu_math}, depthwise", None)
-    elif args.workload == "wide":
-        X, y, params, _ = datasets.wide_binary(args.rows or 400_000, n_features=2000)
-        log(f"data {X.shape} generated in {time.time() - t0:.1f}s")
-        out = train_workload(
-            args, X, y, params,
-            f"wide {X.shape[0]}x{X.shape[1]} L2-normalised binary, max_bin=256, depth 8, "
-            "colsample_bytree 0.5, gpu_math=exact", "wide")
     else:
-        X, y, params, _ = datasets.widebin_cat(args.rows or 2_000_000)
+        X, y, params = workload_data(args)
         log(f"data {X.shape} generated in {time.time() - t0:.1f}s")
-        out = train_workload(
-            args, X, y, params,
-            f"wide-bin {X.shape[0]}x{X.shape[1]} (80 numeric 10% NaN + 20 categorical x 500 "
-            "Zipf codes), max_bin=1024 (u16), reg:squarederror, lossguide 255 leaves", "widebin")
+        desc, tag = workload_desc(args)
+        if args.workload != "widebin":
+            params = dict(params, gpu_math=args.gpu_math)
+        out = train_workload(args, X, y, params, desc, tag)
     print(json.dumps(out), flush=True)
     return 0
 

@@ -238,7 +238,8 @@ HIP_SYMBOLS = [
     "fbh_saabas_contribs", "fbh_predict", "fbh_predict_device", "fbh_shap_contribs_noalloc",
 ]
 TRAIN_SYMBOLS = [
-    "fbt_last_error", "fbt_train", "fbt_train_cuts", "fbt_train_rows", "fbt_last_stats", "fbt_last_round_stats", "fbt_model_free", "fbt_model_n_trees",
+    "fbt_last_error", "fbt_train", "fbt_train_cuts", "fbt_train_rows", "fbt_last_stats",
+    "fbt_last_round_stats", "fbt_last_round_launches", "fbt_model_free", "fbt_model_n_trees",
     "fbt_model_tree_len", "fbt_model_tree_nodes", "fbt_model_n_cat_words", "fbt_model_cat_words",
     "fbt_model_base_score", "fbt_model_base_margin", "fbt_model_n_features",
     "fbt_model_train_margins", "fbt_model_n_cuts", "fbt_model_cuts", "fbt_predict_margin",
@@ -370,6 +371,8 @@ def train_lib() -> C.CDLL:
         L.fbt_last_stats.argtypes = [C.POINTER(Stats)]
         L.fbt_last_round_stats.argtypes = [P, P, P, C.c_uint32]
         L.fbt_last_round_stats.restype = C.c_uint32
+        L.fbt_last_round_launches.argtypes = [P, C.c_uint32]
+        L.fbt_last_round_launches.restype = C.c_uint32
         L.fbt_model_free.argtypes = [P]
         L.fbt_model_free.restype = None
         for name in ("fbt_model_n_trees", "fbt_model_n_cat_words", "fbt_model_n_features",

@@ -16,6 +16,7 @@ Model train(const RowSource &src, uint64_t n, uint32_t nf, const float *y, const
             const Cuts *given);
 fbt_stats last_stats();
 uint32_t last_round_stats(double *wall, double *ms, uint64_t *bytes, uint32_t cap);
+uint32_t last_round_launches(uint64_t *launches, uint32_t cap);
 }  // namespace fbt
 
 struct fbt_model {
@@ -126,6 +127,10 @@ int fbt_last_stats(fbt_stats *out) {
 uint32_t fbt_last_round_stats(double *wall_s, double *hist_ms, uint64_t *hist_bytes,
                               uint32_t capacity) {
     return fbt::last_round_stats(wall_s, hist_ms, hist_bytes, capacity);
+}
+
+uint32_t fbt_last_round_launches(uint64_t *hist_launches, uint32_t capacity) {
+    return fbt::last_round_launches(hist_launches, capacity);
 }
 
 void fbt_model_free(fbt_model *m) { delete m; }

@@ -1061,7 +1061,7 @@ std::vector<float> initial_class_margins(const float *y, const float *w, uint64_
 
 fbt_stats g_stats{};
 std::vector<double> g_round_wall, g_round_hist_ms;
-std::vector<uint64_t> g_round_hist_bytes;
+std::vector<uint64_t> g_round_hist_bytes, g_round_hist_launches;
 
 }  // namespace
 
@@ -1074,6 +1074,13 @@ uint32_t last_round_stats(double *wall, double *ms, uint64_t *bytes, uint32_t ca
         if (ms) ms[i] = g_round_hist_ms[i];
         if (bytes) bytes[i] = g_round_hist_bytes[i];
     }
+    return n;
+}
+
+uint32_t last_round_launches(uint64_t *launches, uint32_t cap) {
+    const uint32_t n = (uint32_t)g_round_hist_launches.size();
+    for (uint32_t i = 0; i < std::min(n, cap); i++)
+        if (launches) launches[i] = g_round_hist_launches[i];
     return n;
 }
 
@@ -1335,9 +1342,10 @@ Model train(const RowSource &src, uint64_t n, uint32_t nf, const float *y, const
     g_round_wall.assign(p.n_rounds, 0.0);
     g_round_hist_ms.assign(p.n_rounds, 0.0);
     g_round_hist_bytes.assign(p.n_rounds, 0);
+    g_round_hist_launches.assign(p.n_rounds, 0);
     auto t_round = Clock::now();
     double ms_seen = 0.0;
-    uint64_t bytes_seen = 0;
+    uint64_t bytes_seen = 0, launches_seen = 0;
     auto close_round = [&](uint32_t r) {
         const auto now = Clock::now();
         g_round_wall[r] = std::chrono::duration<double>(now - t_round).count();
@@ -1348,8 +1356,10 @@ Model train(const RowSource &src, uint64_t n, uint32_t nf, const float *y, const
             call(fbh_hist_timing(ctx.get(), &ms, &launches, &bytes, 0));
             g_round_hist_ms[r] = ms - ms_seen;
             g_round_hist_bytes[r] = bytes - bytes_seen;
+            g_round_hist_launches[r] = launches - launches_seen;
             ms_seen = ms;
             bytes_seen = bytes;
+            launches_seen = launches;
         }
     };
     // Device-grown trees are collected one round late: round r + 1's

@@ -184,6 +184,10 @@ int fbt_last_stats(fbt_stats *out);
  * latter two need params.profile = 1). Returns the number of rounds. */
 uint32_t fbt_last_round_stats(double *wall_s, double *hist_ms, uint64_t *hist_bytes,
                               uint32_t capacity);
+/* Histogram launches of each round of the last training call (needs
+ * params.profile = 1), counted as fbt_last_round_stats counts the bytes.
+ * Returns the number of rounds. */
+uint32_t fbt_last_round_launches(uint64_t *hist_launches, uint32_t capacity);
 
 void fbt_model_free(fbt_model *m);
 uint32_t fbt_model_n_trees(const fbt_model *m);
