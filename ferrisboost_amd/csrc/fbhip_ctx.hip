@@ -86,6 +86,13 @@ constexpr uint32_t MAX_RECORD_BYTES = 64;
 // 256 MB its 7,440 root workgroups flushed with global atomics instead.
 constexpr uint64_t MAX_PARTIAL_BYTES = 2048ull << 20;
 constexpr uint32_t MAX_NODES = 16384;      // nodes of one eval / partition call
+// A level of a device-grown tree partitions in one pass (part_split_kernel)
+// when its partition chunks, divided by the level's node bound (2^depth),
+// number at most this many. Each workgroup reserves its places with one
+// atomic on its node's cursor pair, and the atomics on one cursor serialize
+// (about 14 ns each measured: 74 us for 5128 chunks of one node, against
+// 56 us for the count, scan and scatter passes).
+constexpr uint32_t ONE_PASS_CHUNKS_PER_NODE = 512;
 constexpr uint32_t DEFAULT_TILE_BYTES = 64 * 1024;
 // LDS of a planar tile (its bins plus the 1 KiB of lane dummies) when the
 // caller sets no tile size: three workgroups then share a CU's 160 KiB,
@@ -143,6 +150,7 @@ struct fbh_ctx {
     uint32_t shared_line_rows = SHARED_LINE_CHUNK_ROWS;
     uint32_t planar_max_feats = 0;  // nonzero: at most this many features a planar tile
     uint64_t max_partial_bytes = MAX_PARTIAL_BYTES;
+    uint32_t one_pass_chunks = ONE_PASS_CHUNKS_PER_NODE;  // 0: never one pass
     uint32_t hist_tpb = 0;          // histogram threads per workgroup (0: per launch)
     uint32_t hist_waves = HIST_WAVES;
     uint32_t host_hist_waves = HOST_HIST_WAVES;
@@ -249,6 +257,7 @@ struct fbh_ctx {
     ScalesDev *d_scales = nullptr;  // scales of the current gradients
     int64_t *partials = nullptr;    // per-chunk partial histograms
     uint64_t partial_bytes = 0;
+    unsigned long long *d_cursors = nullptr;  // cursor pairs of the one-pass partition
     // The row arena of a new tree is the identity; it is written out only
     // when something reads it (a device-grown tree walks the root without it).
     bool rows_identity = false;
@@ -890,6 +899,8 @@ void fixed_allocations(fbh_ctx &c, A &&a) {
     c.d_counts = static_cast<uint32_t *>(a(4 * c.max_chunks, "partition counts"));
     c.d_excl = static_cast<uint32_t *>(a(4 * (c.max_chunks + 1), "partition offsets"));
     c.d_totals = static_cast<uint32_t *>(a(4 * (uint64_t)MAX_NODES, "partition totals"));
+    c.d_cursors = static_cast<unsigned long long *>(
+        a(8 * (uint64_t)PART_CURSOR_STRIDE * MAX_NODES, "partition cursors"));
     // Leaf table followed by the leaf values of one call.
     c.d_leaves = static_cast<LeafDev *>(a((sizeof(LeafDev) + 4) * MAX_NODES, "leaf table"));
     // Device plan of a fused partition + evaluation step.
@@ -1083,6 +1094,7 @@ fbh_config configure(fbh_ctx &c, uint64_t n_rows, const fbh_shape *shape, const 
     c.shared_line_rows = (uint32_t)env_u64("FB_HIP_LINE_ROWS", SHARED_LINE_CHUNK_ROWS);
     c.planar_max_feats = (uint32_t)env_u64("FB_HIP_PLANAR_MAXF", 0);
     c.max_partial_bytes = env_u64("FB_HIP_PARTIAL_MB", MAX_PARTIAL_BYTES >> 20) << 20;
+    c.one_pass_chunks = (uint32_t)env_u64("FB_HIP_ONE_PASS_CHUNKS", ONE_PASS_CHUNKS_PER_NODE);
     c.hist_waves = (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HIST_WAVES", HIST_WAVES));
     c.host_hist_waves =
         (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HOST_HIST_WAVES", HOST_HIST_WAVES));
@@ -3206,7 +3218,9 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     int64_t *partials = c->partial_buffer(max_grid * all_bins * 16);
     E0.partials = partials;
     E0.max_groups = reduce_groups(h.n_chunks);
-    const bool root_atomic = partials ? h.n_chunks > REDUCE_GROUP : h.n_chunks != 1;
+    // With partials a node of several reduction groups has its slot cleared
+    // by the histogram launch itself (its first chunk's workgroups).
+    const bool root_atomic = partials ? false : h.n_chunks != 1;
     const bool clear_root = root_atomic || c->has_global;
     E0.cleared = true;
     E0.sn = c->d_lvl_split;
@@ -3242,6 +3256,13 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     G.n_slots = n_slots;
     G.cw = std::max(1u, c->cat_words_per_node);
     G.n_rows = n_rows;
+    // One-pass partitions need partials (no slot is cleared before the next
+    // level's histograms) and few chunks a node (one_pass_chunks); the level
+    // decision then zeroes each split node's cursors.
+    auto one_pass_at = [&](uint32_t d) {
+        return partials != nullptr && c->one_pass_chunks &&
+               n_rows / PART_CHUNK <= ((uint64_t)c->one_pass_chunks << std::min(d, 40u));
+    };
     check(launch_grow_prep(G, d_root, d_root ? nullptr : c->red_i64, c->n_red_blocks, 0,
                            GB.level[0], c->d_lvl_split, GB.tree, GB.st,
                            clear_root ? c->hist : nullptr, 2 * c->hist_width, c->stream),
@@ -3257,6 +3278,8 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
         const uint32_t nb = lvl_bound(d);
         uint64_t *pk_cats =
             reinterpret_cast<uint64_t *>(pk_base + al256(sizeof(SplitPacketDev) * nb));
+        const bool one_pass = one_pass_at(d) && !(walk && d + 1 == D);
+        G.part_cur = one_pass ? c->d_cursors : nullptr;
         check(launch_grow_decide(G, d, c->d_packets, pk_cats, GB.level[d & 1], GB.tree,
                                  GB.tree_cats, d_mono, GB.cols, GB.reqs, GB.pairs, GB.triples,
                                  GB.leaves, GB.leaf_vals, GB.st, A, c->stream),
@@ -3268,17 +3291,28 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
         if (arena_out == c->rows) c->rows_identity = false;
         const GrowDevOut out{GB.st, GB.level[(d + 1) & 1], GB.tree, GB.leaves, GB.leaf_vals,
                              (d + 1) & 1u};
-        // The scatter clears the next level's accumulated slots (none after the last level).
-        ZeroNodesDev Z{};
-        if (d + 1 < D)
-            Z = {c->hist, c->hist_width, c->d_lvl_hist, &GB.st->n_eval,
-                 (c->has_global || !c->streamed.empty()) ? 1u : 0u, partials ? REDUCE_GROUP : 0u};
-        check(launch_partition_level(GB.reqs, &GB.st->n_split, n_rows / PART_CHUNK + nb + 1,
-                                     arena_in, arena_out, c->flags, c->d_counts, c->d_excl,
-                                     c->d_totals, pk_cats, GB.pairs, rule, c->d_lvl_hist,
-                                     c->d_lvl_split, c->d_lvl_out, c->d_lvl_out + 4 * MAX_NODES,
-                                     c->d_lvl_rows, out, Z, c->stream),
-              "partition and level plan");
+        if (one_pass) {
+            check(launch_partition_split(GB.reqs, &GB.st->n_split, n_rows / PART_CHUNK + nb + 1,
+                                         arena_in, arena_out, c->d_cursors, c->d_totals, pk_cats,
+                                         GB.pairs, rule, c->d_lvl_hist, c->d_lvl_split,
+                                         c->d_lvl_out, c->d_lvl_out + 4 * MAX_NODES,
+                                         c->d_lvl_rows, out, c->stream),
+                  "partition and level plan");
+        } else {
+            // Without partials the scatter clears the next level's
+            // accumulated slots of several chunks (none after the last
+            // level); with them the histogram launch clears what it needs.
+            ZeroNodesDev Z{};
+            if (d + 1 < D && !partials)
+                Z = {c->hist, c->hist_width, c->d_lvl_hist, &GB.st->n_eval,
+                     (c->has_global || !c->streamed.empty()) ? 1u : 0u, 0u};
+            check(launch_partition_level(GB.reqs, &GB.st->n_split, n_rows / PART_CHUNK + nb + 1,
+                                         arena_in, arena_out, c->flags, c->d_counts, c->d_excl,
+                                         c->d_totals, pk_cats, GB.pairs, rule, c->d_lvl_hist,
+                                         c->d_lvl_split, c->d_lvl_out, c->d_lvl_out + 4 * MAX_NODES,
+                                         c->d_lvl_rows, out, Z, c->stream),
+                  "partition and level plan");
+        }
         if (d + 1 == D) break;
         EvalPlan E;
         E.hn = c->d_lvl_hist;
@@ -3362,6 +3396,7 @@ void grow_collect(fbh_ctx *c, fbh_tree_node *nodes, uint32_t node_capacity, uint
     std::memcpy(&st, po, sizeof(st));
     check_device_scales(st.scales, c->n_rows);
     if (st.error & 1u) throw RuntimeError("histogram slots exhausted; raise the slot budget");
+    if (st.error & 4u) throw RuntimeError("partition cursors out of range");
     account_hist(c, st.hist_rows, st.hist_nodes);
     if (st.covered != c->n_rows)
         throw RuntimeError("leaves cover " + std::to_string(st.covered) + " of " +

@@ -11,6 +11,9 @@ constexpr int HIST_TPB = 256;      // threads of one histogram workgroup
 constexpr int SPLIT_TPB = 256;     // threads of one split-scan workgroup
 constexpr int PART_TPB = 256;      // threads of one partition workgroup
 constexpr int PART_CHUNK = 2048;   // rows of one partition chunk (8 per thread)
+// 64-bit words between the cursors of two requests of the one-pass
+// partition (one 128-byte line each).
+constexpr uint32_t PART_CURSOR_STRIDE = 16;
 constexpr int XCDS = 8;            // MI355X accelerator complex dies
 constexpr uint32_t NO_SLOT = 0xFFFFFFFFu;
 constexpr uint32_t MAX_GROW_SLOTS = 16384;  // histogram slots a device-grown tree can use
@@ -263,6 +266,10 @@ struct GrowParamsDev {
     uint32_t cw;           // category words per node of the split outputs
     uint32_t n_rows;
     uint32_t pad[2];
+    // One-pass partition (part_split_kernel): the level decision zeroes each
+    // request's cursor pair here (PART_CURSOR_STRIDE apart); null: the
+    // three-pass partition.
+    unsigned long long *part_cur;
 };
 
 // Rows per chunk of a device-planned histogram launch: fixed when nonzero,
@@ -408,6 +415,17 @@ hipError_t launch_partition_level(const PartReqDev *reqs, const uint32_t *dev, u
                                   HistNodeDev *hn, SplitNodeDev *sn, uint32_t *spans,
                                   uint32_t *left_slot, uint32_t *chunk_rows, const GrowDevOut &D,
                                   const ZeroNodesDev &Z, hipStream_t s);
+// The same in one pass (part_split_kernel, cursors zeroed by the level
+// decision), then the children plan (left totals from the cursors into
+// totals). No slot is cleared: only for levels whose histograms need none.
+hipError_t launch_partition_split(const PartReqDev *reqs, const uint32_t *dev,
+                                  uint32_t grid_chunks, const uint32_t *rows_in,
+                                  uint32_t *rows_out, unsigned long long *cursors,
+                                  uint32_t *totals,
+                                  const uint64_t *cat_words, const PairDev *pairs, ChunkRule rule,
+                                  HistNodeDev *hn, SplitNodeDev *sn, uint32_t *spans,
+                                  uint32_t *left_slot, uint32_t *chunk_rows, const GrowDevOut &D,
+                                  hipStream_t s);
 hipError_t launch_partition_count(const PartReqDev *reqs, uint32_t n_reqs, uint32_t n_chunks,
                                   const uint32_t *rows, uint8_t *flags, uint32_t *chunk_counts,
                                   const uint64_t *cat_words, hipStream_t s);

@@ -332,6 +332,13 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
     const bool partial = !STREAM && !single && L.partials;
     int64_t *out = partial ? L.partials + (uint64_t)chunk * L.hist_width * 2u
                            : L.hist + (uint64_t)N.slot * L.hist_width * 2u;
+    // A node of more than REDUCE_GROUP chunks is summed into its slot by
+    // atomics (reduce_chunks_kernel): its first chunk's workgroups clear the
+    // slot's bins of their tile here, so nothing clears it before.
+    unsigned long long *clr =
+        (partial && chunk == N.chunk_begin && N.n_chunks > REDUCE_GROUP)
+            ? reinterpret_cast<unsigned long long *>(L.hist + (uint64_t)N.slot * L.hist_width * 2u)
+            : nullptr;
     if (ROT) {
         // Slots in order (conflict-free LDS reads): each thread keeps one
         // feature, tid mod 16, and a wave writes 4 bins of 16 features.
@@ -350,6 +357,10 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
             } else if ((gg | hh) != 0ull) {
                 global_add_u64(dst, gg);
                 global_add_u64(dst + 1, hh);
+            }
+            if (clr) {
+                clr[2u * (F.hist_off + bin)] = 0ull;
+                clr[2u * (F.hist_off + bin) + 1u] = 0ull;
             }
         }
         return;
@@ -376,6 +387,10 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
             } else if ((gg | hh) != 0ull) {
                 global_add_u64(dst, gg);
                 global_add_u64(dst + 1, hh);
+            }
+            if (clr) {
+                clr[2u * (F.hist_off + bin)] = 0ull;
+                clr[2u * (F.hist_off + bin) + 1u] = 0ull;
             }
         }
     }
@@ -521,7 +536,8 @@ hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slot
 // group_begin range holds it. A node of at most REDUCE_GROUP chunks has one
 // group, which sums them and stores the slot (zeros for a node without rows);
 // a larger node's groups each add the sum of their REDUCE_GROUP chunks into
-// its cleared slot.
+// its slot, which the histogram launch cleared (its first chunk's
+// workgroups).
 __global__ void reduce_chunks_kernel(int64_t *hist, uint64_t width, const int64_t *partials,
                                      const HistNodeDev *nodes, uint32_t n_nodes,
                                      const uint32_t *dev_n) {
@@ -1791,6 +1807,131 @@ __global__ __launch_bounds__(PART_TPB) void part_scatter_kernel(const PartReqDev
         }
         done_left += in_round;
     }
+}
+
+// A device-grown level's partition in one pass. Each workgroup takes one
+// chunk of a split node's rows, finds every row's direction from the split
+// feature's cell, and reserves places for its left rows at the front of the
+// node's span and for its right rows at the back with one 64-bit atomic add
+// on the node's cursor pair (left count in the low half, right count in the
+// high half; zeroed by the level decision). Within a chunk the rows keep
+// their order on each side; the chunks of a node take their places in the
+// order their atomics land, so a child's rows are runs of ascending row ids
+// in no fixed order. Everything computed from a node's rows is an integer sum
+// (histograms, child sums) or per row (leaf assignment), so trees and margins
+// do not depend on that order. The cursor's low half ends at the node's left
+// count. A reservation past the node's span (cursors not zeroed) writes
+// nothing and sets error bit 2.
+__global__ __launch_bounds__(PART_TPB) void part_split_kernel(const PartReqDev *reqs,
+                                                              const uint32_t *dev,
+                                                              const uint32_t *rows_in,
+                                                              uint32_t *rows_out,
+                                                              unsigned long long *cursors,
+                                                              const uint64_t *cat_words,
+                                                              GrowState *st) {
+    constexpr int ROUNDS = PART_CHUNK / PART_TPB;
+    constexpr int WAVES = PART_TPB / 64;
+    __shared__ uint32_t round_left[ROUNDS][WAVES];
+    __shared__ uint32_t base_sh[2];
+    const uint32_t chunk = blockIdx.x;
+    if (chunk >= dev[1]) return;
+    const uint32_t ri = find_req(reqs, dev[0], chunk);
+    const PartReqDev R = reqs[ri];
+    const uint32_t c0 = (chunk - R.chunk_begin) * PART_CHUNK;
+    const uint32_t c1 = min(c0 + PART_CHUNK, R.row_len);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // All of the thread's row ids, then all of their cells, in flight at once.
+    uint32_t row[ROUNDS], bin[ROUNDS];
+#pragma unroll
+    for (int r = 0; r < ROUNDS; r++) {
+        const uint32_t i = c0 + r * PART_TPB + threadIdx.x;
+        row[r] = i < c1 ? (rows_in ? rows_in[R.row_off + i] : R.row_off + i) : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < ROUNDS; r++) {
+        const uint32_t i = c0 + r * PART_TPB + threadIdx.x;
+        bin[r] = i < c1 ? cell_of(R, row[r]) : 0u;
+    }
+    uint32_t left_bits = 0, below[ROUNDS];
+#pragma unroll
+    for (int r = 0; r < ROUNDS; r++) {
+        const uint32_t i = c0 + r * PART_TPB + threadIdx.x;
+        const bool gl = i < c1 && bin_goes_left(R, bin[r], cat_words);
+        left_bits |= (gl ? 1u : 0u) << r;
+        const uint64_t ball = __ballot(gl);
+        below[r] = __popcll(ball & ((1ull << lane) - 1ull));
+        if (lane == 0) round_left[r][wave] = __popcll(ball);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t nl = 0;
+        for (int r = 0; r < ROUNDS; r++)
+            for (int w = 0; w < WAVES; w++) nl += round_left[r][w];
+        const uint32_t nr = (c1 - c0) - nl;
+        const unsigned long long old =
+            atomicAdd(cursors + (uint64_t)ri * PART_CURSOR_STRIDE,
+                      ((unsigned long long)nr << 32) | nl);
+        const uint32_t lb = (uint32_t)old, rb = (uint32_t)(old >> 32);
+        // Whatever order the chunks reserve in, the lefts and rights reserved
+        // so far (this chunk's included) add up to at most the node's rows.
+        const bool ok = (uint64_t)lb + nl + rb + nr <= R.row_len;
+        base_sh[0] = lb;
+        base_sh[1] = ok ? R.row_len - rb - nr : NO_SLOT;  // where this chunk's right rows start
+        if (!ok) atomicOr(&st->error, 4u);
+    }
+    __syncthreads();
+    const uint32_t lbase = base_sh[0], rstart = base_sh[1];
+    if (rstart == NO_SLOT) return;
+    uint32_t done_left = 0;  // lefts of earlier rounds in this chunk
+#pragma unroll
+    for (int r = 0; r < ROUNDS; r++) {
+        uint32_t before = 0, in_round = 0;
+        for (uint32_t w = 0; w < WAVES; w++) {
+            if (w < wave) before += round_left[r][w];
+            in_round += round_left[r][w];
+        }
+        const uint32_t i = c0 + r * PART_TPB + threadIdx.x;
+        if (i < c1) {
+            const uint32_t lrank = done_left + before + below[r];
+            const uint32_t dst = ((left_bits >> r) & 1u)
+                                     ? R.row_off + lbase + lrank
+                                     : R.row_off + rstart + (i - c0 - lrank);
+            rows_out[dst] = row[r];
+        }
+        done_left += in_round;
+    }
+}
+
+// The children plan of a level partitioned by part_split_kernel: the left
+// counts are the cursors' low halves.
+__global__ __launch_bounds__(1024) void part_plan_kernel(
+    const unsigned long long *cursors, uint32_t *totals, const PairDev *pairs, ChunkRule rule,
+    HistNodeDev *hn, SplitNodeDev *sn, uint32_t *spans, uint32_t *left_slot,
+    uint32_t *chunk_rows_out, GrowDevOut D) {
+    PlanPrefetch pre{};
+    pre.valid = true;
+    pre.n = D.st->n_split;
+    pre.leaf_base = D.st->n_leaves;
+    if (threadIdx.x < pre.n) pre.first = pairs[threadIdx.x];
+    for (uint32_t r = threadIdx.x; r < pre.n; r += 1024)
+        totals[r] = (uint32_t)cursors[(uint64_t)r * PART_CURSOR_STRIDE];
+    __syncthreads();
+    level_plan_body(pairs, 0u, totals, rule, hn, sn, spans, left_slot, chunk_rows_out, D, pre);
+}
+
+hipError_t launch_partition_split(const PartReqDev *reqs, const uint32_t *dev,
+                                  uint32_t grid_chunks, const uint32_t *rows_in,
+                                  uint32_t *rows_out, unsigned long long *cursors,
+                                  uint32_t *totals, const uint64_t *cat_words,
+                                  const PairDev *pairs, ChunkRule rule, HistNodeDev *hn,
+                                  SplitNodeDev *sn, uint32_t *spans, uint32_t *left_slot,
+                                  uint32_t *chunk_rows, const GrowDevOut &D, hipStream_t s) {
+    if (grid_chunks == 0 || !D.st) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(part_split_kernel, dim3(grid_chunks), dim3(PART_TPB), 0, s, reqs, dev,
+                       rows_in, rows_out, cursors, cat_words, D.st);
+    hipLaunchKernelGGL(part_plan_kernel, dim3(1), dim3(1024), 0, s, cursors, totals, pairs, rule,
+                       hn, sn, spans, left_slot, chunk_rows, D);
+    return hipGetLastError();
 }
 
 __global__ __launch_bounds__(PART_TPB) void part_copy_kernel(const PartReqDev *reqs,
@@ -3138,6 +3279,7 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
             q.cat_off = P.cat_offset;
             q.n_cat_words = P.is_cat ? P.n_cat_words : 0u;
             reqs[s] = q;
+            if (G.part_cur) G.part_cur[(uint64_t)s * PART_CURSOR_STRIDE] = 0ull;
             cb += q.n_chunks;
             PairDev d{};
             d.req = L.row_len ? s : NO_SLOT;
