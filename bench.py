@@ -10,7 +10,8 @@ device syncs. Other workloads (--workload):
   wide      400k x 2000 L2-normalised rows, colsample_bytree 0.5, depth 8
   widebin   2M x (80 numeric with 10% NaN + 20 categorical x 500 codes),
             max_bin 1024 (u16), reg:squarederror, lossguide, 255 leaves
-  streaming 50M x 200 N(0,1) binary, max_bin 255 (u8, about 10 GB of bins),
+  streaming 50M x 200 N(0,1) binary, max_bin 256 (8-bit cells: no missing
+            value; about 10 GB of bins),
             depth 8, with the device budget forced to 4 GiB: most tiles
             stream from pinned host memory
   multiclass  the narrow rows with 4 classes, multi:softprob (4 trees a round)
@@ -290,7 +291,9 @@ def streaming_workload(args):
     n_rows = args.rows or 50_000_000
     t0 = time.time()
     X, y, params, _ = datasets.streaming(n_rows=n_rows, n_features=200)
-    params = dict(params, max_bin=255)  # u8 bins: 50M x 200 is about 10 GB
+    # The configured max_bin 256 (no missing value: 8-bit cells), or 255
+    max_bin = args.max_bin or params["max_bin"]
+    params = dict(params, max_bin=max_bin)
     log(f"data {X.shape} generated in {time.time() - t0:.1f}s")
     budget = 4 << 30
     rounds = args.warmup + args.steps
@@ -307,9 +310,9 @@ def streaming_workload(args):
     hbytes = np.zeros(rounds, np.uint64)
     N.train_lib().fbt_last_round_stats(N.ptr(wall), N.ptr(hms), N.ptr(hbytes), rounds)
     t_wall = float(wall[args.warmup:].sum())
-    config = {"workload": f"streaming {n_rows}x200 N(0,1) binary, max_bin=255 (u8), depth 8, "
-                          "gpu_memory_budget=4 GiB", "rows": n_rows, "features": 200,
-              "max_bin": 255, "max_depth": 8, "gpu_memory_budget": budget}
+    config = {"workload": f"streaming {n_rows}x200 N(0,1) binary, max_bin={max_bin} (8-bit "
+                          "cells), depth 8, gpu_memory_budget=4 GiB", "rows": n_rows,
+              "features": 200, "max_bin": max_bin, "max_depth": 8, "gpu_memory_budget": budget}
     out = base_line(args, round(args.steps / t_wall, 4), "rounds/s",
                     round(1e3 * t_wall / args.steps, 1), config)
     streamed = float(st["streamed_bytes"])
@@ -618,8 +621,10 @@ def main() -> int:
                     choices=["narrow", "multiclass", "quantile", "wide", "widebin", "streaming",
                              "shap", "predict"])
     ap.add_argument("--rows", type=int, default=0, help="rows (0: the workload's own size)")
-    ap.add_argument("--max-bin", type=int, default=255, help="narrow workload: 255 or 256 (8-bit cells; 256 bins fill a byte where "
-                         "no value is missing) or more (u16)")
+    ap.add_argument("--max-bin", type=int, default=0,
+                    help="narrow and streaming workloads: 255 or 256 (8-bit cells; 256 bins fill "
+                         "a byte where no value is missing) or more (u16); default 255 for "
+                         "narrow, the configured 256 for streaming")
     ap.add_argument("--gpu-math", default="exact", choices=["exact", "fast"],
                     help="narrow, multiclass, quantile and wide workloads: exact (byte-identical "
                          "trees) or fast (hardware exp on the device)")
@@ -636,6 +641,8 @@ def main() -> int:
         # timed rounds add up to its round count (500, 200 and 300 rounds).
         full = FULL_ROUNDS.get(args.workload)
         args.steps = max(1, full - args.warmup) if full else 20
+    if args.max_bin == 0 and args.workload != "streaming":
+        args.max_bin = 255
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported "
               "(the training path is single-device)", file=sys.stderr)

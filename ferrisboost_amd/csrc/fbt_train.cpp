@@ -19,6 +19,8 @@
 #include <chrono>
 #include <cmath>
 #include <condition_variable>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <limits>
@@ -1344,12 +1346,21 @@ Model train(const RowSource &src, uint64_t n, uint32_t nf, const float *y, const
     g_round_hist_bytes.assign(p.n_rounds, 0);
     g_round_hist_launches.assign(p.n_rounds, 0);
     auto t_round = Clock::now();
+    const auto t_first = t_round;
     double ms_seen = 0.0;
     uint64_t bytes_seen = 0, launches_seen = 0;
+    // FB_LOG_ROUNDS=k: a progress line on stderr every k rounds.
+    const char *log_env = std::getenv("FB_LOG_ROUNDS");
+    const unsigned long log_every = log_env ? std::strtoul(log_env, nullptr, 10) : 0ul;
     auto close_round = [&](uint32_t r) {
         const auto now = Clock::now();
         g_round_wall[r] = std::chrono::duration<double>(now - t_round).count();
         t_round = now;
+        if (log_every && ((r + 1) % log_every == 0 || r + 1 == p.n_rounds)) {
+            std::fprintf(stderr, "[ferrisboost_amd] round %u of %u done, %.1f s\n", r + 1,
+                         p.n_rounds, std::chrono::duration<double>(now - t_first).count());
+            std::fflush(stderr);
+        }
         if (p.profile) {
             double ms = 0.0;
             uint64_t launches = 0, bytes = 0;

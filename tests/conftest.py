@@ -10,6 +10,9 @@ if ROOT not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a gfx950 GPU (MI355X)")
+    import helpers
+
+    helpers.PYTEST_CONFIG = config
 
 
 @pytest.fixture(scope="session")

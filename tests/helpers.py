@@ -2,10 +2,27 @@
 
 from __future__ import annotations
 
+import contextlib
 import json
 import os
 
 import numpy as np
+
+# The running pytest's config (set by conftest.py), for uncaptured().
+PYTEST_CONFIG = None
+
+
+@contextlib.contextmanager
+def uncaptured():
+    """Output written inside the block (by Python or by the native library)
+    reaches the terminal at once instead of pytest's capture: long GPU steps
+    print their progress as they go."""
+    cm = PYTEST_CONFIG.pluginmanager.getplugin("capturemanager") if PYTEST_CONFIG else None
+    if cm is None:
+        yield
+        return
+    with cm.global_and_fixture_disabled():
+        yield
 
 FIXTURES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "fixtures")
 INDEXES = ("index.json", "weighted_index.json", "monotone_index.json")

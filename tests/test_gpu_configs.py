@@ -24,7 +24,7 @@ from concurrent.futures import ThreadPoolExecutor
 import numpy as np
 import pytest
 
-from helpers import assert_same_models
+from helpers import assert_same_models, uncaptured
 
 pytestmark = pytest.mark.gpu
 
@@ -43,9 +43,10 @@ _T0 = time.time()
 
 
 def _say(msg: str) -> None:
-    """A progress line (the long steps here run for minutes)."""
-    sys.stdout.write(f"[configs {time.time() - _T0:7.1f}s] {msg}\n")
-    sys.stdout.flush()
+    """A progress line, shown at once (the long steps here run for minutes)."""
+    with uncaptured():
+        sys.stdout.write(f"[configs {time.time() - _T0:7.1f}s] {msg}\n")
+        sys.stdout.flush()
 
 
 def _oracle_params(oracle, params, rounds):
@@ -153,6 +154,7 @@ def test_c4_widebin_lossguide_first_rounds_match_oracle(fb, oracle):
 def c5():
     from ferrisboost_amd import datasets
 
+    _say("generating 50M x 200")
     X, y, params, _ = datasets.streaming(50_000_000, 200)
     _say("50M x 200 generated")
     yield X, y, params, {}
@@ -186,12 +188,42 @@ def test_c5_streamed_under_4gib_equals_resident(fb, c5, max_bin):
     _same_margins(res, st, y.size)
 
 
-def test_c5_shap_of_the_100_tree_ensemble(fb, oracle, c5):
+@pytest.fixture(scope="module")
+def c5_resident(fb, c5):
+    """The configured C5 job, resident: 100 rounds at max_bin 256."""
+    X, y, params, _ = c5
+    assert params["max_bin"] == 256
+    pm = fb.train(params, X, y, num_boost_round=100, cuts=_c5_cuts(fb, c5, params["max_bin"]))
+    _say(f"resident: 100 trees in {pm.stats['train_seconds']:.2f}s")
+    assert pm.stats["resident_tiles"] == pm.stats["n_tiles"]
+    return pm
+
+
+def test_c5_streamed_100_rounds_equal_resident(fb, c5, c5_resident, monkeypatch):
+    """The whole C5 job as configured (100 rounds, max_bin 256: no value is
+    missing, so 8-bit cells) under a 4 GiB budget: most tiles stream from
+    pinned host memory at every level of every tree, and all 100 trees and
+    the training margins equal the resident run's byte for byte."""
+    X, y, params, _ = c5
+    monkeypatch.setenv("FB_LOG_ROUNDS", "10")  # the library's progress line every 10 rounds
+    _say("streamed: 100 rounds")
+    with uncaptured():
+        st = fb.train(dict(params, gpu_memory_budget=4 << 30), X, y, num_boost_round=100,
+                      cuts=_c5_cuts(fb, c5, params["max_bin"]))
+    _say(f"streamed: 100 rounds in {st.stats['train_seconds']:.1f}s, "
+         f"{st.stats['resident_tiles']}/{st.stats['n_tiles']} tiles resident, "
+         f"{st.stats['streamed_bytes'] / 1e9:.0f} GB streamed")
+    assert st.stats["device_bytes"] <= 4 << 30
+    assert st.stats["resident_tiles"] < st.stats["n_tiles"] and st.stats["streamed_bytes"] > 0
+    assert_same_models(c5_resident, st)
+    _same_margins(c5_resident, st, y.size)
+
+
+def test_c5_shap_of_the_100_tree_ensemble(fb, oracle, c5, c5_resident):
     """TreeSHAP of the 100-tree depth-8 ensemble on 1M rows: the first 20k
     against the oracle (<= 1e-5), every row additive against the margin."""
     X, y, params, _ = c5
-    pm = fb.train(params, X, y, num_boost_round=100, cuts=_c5_cuts(fb, c5, params["max_bin"]))
-    _say(f"100 trees in {pm.stats['train_seconds']:.2f}s")
+    pm = c5_resident
     assert pm.num_trees == 100
     rows = X[:1_000_000]
     phi = pm.predict(rows, pred_contribs=True)
