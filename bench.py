@@ -54,6 +54,44 @@ VALU_PEAK_TOPS = 39.3
 # TreeSHAP of the 100-tree depth-8 ensemble: VALU lane-operations a row, counted by
 # SQ_INSTS_VALU x 64 / rows for shap_rec_kernel on the shap workload.
 SHAP_VALU_OPS_PER_ROW = 11.23e6
+# Prediction of the same ensemble: VALU lane-operations a row (SQ_INSTS_VALU x 64 / rows
+# for predict_kernel on the predict workload).
+PREDICT_VALU_OPS_PER_ROW = 11010
+# MI355X fp32 vector peak (FMA counted as two operations).
+FP32_PEAK_TFLOPS = 157.3
+# QuadratureTreeSHAP's arithmetic (8 quadrature points): for each child edge of an
+# internal node the extend (3 operations a point) and the unwind of that edge's
+# contribution (5 a point), plus the sum of the two subtrees' returns (1 a point); for a
+# leaf the scaled return (2 a point, and the path weight). The unwinds of a feature met
+# twice on a path are data-dependent and not counted: a lower bound.
+SHAP_QP = 8
+SHAP_FLOPS_INTERNAL = 2 * (3 + 5) * SHAP_QP + SHAP_QP
+SHAP_FLOPS_LEAF = 2 * SHAP_QP + 1
+
+
+def shap_flops_per_row(model) -> int:
+    """Algorithmic floating-point operations of one row's TreeSHAP over the
+    model (the same for every row: every row visits every node)."""
+    total = 0
+    for t in model.trees():
+        leaves = int((t["is_leaf"] == 1).sum())
+        total += SHAP_FLOPS_INTERNAL * (t.size - leaves) + SHAP_FLOPS_LEAF * leaves
+    return total
+
+
+def node_visits_per_row(model, X) -> float:
+    """Nodes a prediction walk visits per row (root to leaf, every tree),
+    averaged over the first 100k rows from their leaf ids."""
+    leaf = model.predict(X[:100_000], pred_leaf=True).astype(np.int64)
+    visits = 0.0
+    for k, t in enumerate(model.trees()):
+        depth = np.zeros(t.size, np.int64)
+        for i in range(t.size):  # parents come before children in node-id order
+            if t["is_leaf"][i] != 1:
+                depth[t["left"][i]] = depth[i] + 1
+                depth[t["right"][i]] = depth[i] + 1
+        visits += float((depth[leaf[:, k]] + 1).mean())
+    return visits
 METRIC = "histogram build GB/s (% HBM peak) + boosting rounds/sec, 10.5M×28 u8 bins depth 8"
 
 
@@ -367,6 +405,7 @@ def predict_workload(args):
     # bytes the kernel must move: the row in, its margin out
     per_row = 4 * X.shape[1] + 4
     gbps = args.steps * n_rows * per_row / (kernel_ms * 1e-3) / 1e9
+    visits = node_visits_per_row(model, X)
     cpu = None
     parity = None
     if not args.no_cpu:
@@ -387,9 +426,16 @@ def predict_workload(args):
               "trees": 100, "max_depth": 8}
     out = base_line(args, round(rows_per_s, 1), "rows/s", round(kernel_ms / args.steps, 3),
                     config, dtype="f32")
+    # The walk is a chain of dependent loads (node, then the row's cell, then
+    # the child), so its bound is memory latency, not bandwidth or VALU
+    # issue: the VALU and HBM figures beside it are far from their peaks.
+    valu = rows_per_s * PREDICT_VALU_OPS_PER_ROW / 1e12
     out.update({
-        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+        "roofline": {"bound": "latency", "achieved": round(rows_per_s * visits / 1e9, 2),
+                     "peak": None, "unit": "G node visits/s", "frac": None, "traffic": None,
+                     "node_visits_per_row": round(visits, 1),
+                     "valu_tops": round(valu, 3), "valu_frac": round(valu / VALU_PEAK_TOPS, 4),
+                     "hbm_gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)},
         "pcie_inclusive_rows_per_s": round(args.steps * n_rows / wall, 1),
         "cpu_baseline": cpu,
         "margins_bit_identical_to_cpu": parity,
@@ -417,6 +463,7 @@ def shap_workload(args):
     per_row = 4 * X.shape[1] + 4 * (X.shape[1] + 1)
     gbps = args.steps * n_rows * per_row / (kernel_ms * 1e-3) / 1e9
     tops = rows_per_s * SHAP_VALU_OPS_PER_ROW / 1e12
+    alg = shap_flops_per_row(model)
     margin = model.predict(X[:20000], output_margin=True)
     additivity = float(np.max(np.abs(phi[:20000].sum(axis=1) - margin)))
 
@@ -443,6 +490,9 @@ def shap_workload(args):
         "roofline": {"bound": "valu", "achieved": round(tops, 2), "peak": VALU_PEAK_TOPS,
                      "unit": "T lane-ops/s", "frac": round(tops / VALU_PEAK_TOPS, 4),
                      "traffic": None, "ops_per_row": SHAP_VALU_OPS_PER_ROW,
+                     "algorithmic_flops_per_row": alg,
+                     "algorithmic_tflops": round(rows_per_s * alg / 1e12, 2),
+                     "algorithmic_frac_fp32_peak": round(rows_per_s * alg / 1e12 / FP32_PEAK_TFLOPS, 4),
                      "hbm_gbps": round(gbps, 2)},
         "pcie_inclusive_rows_per_s": round(args.steps * n_rows / wall, 1),
         "additivity_max_abs": additivity,

@@ -3258,7 +3258,9 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     G.n_rows = n_rows;
     // One-pass partitions need partials (no slot is cleared before the next
     // level's histograms) and few chunks a node (one_pass_chunks); the level
-    // decision then zeroes each split node's cursors.
+    // decision then zeroes each split node's cursors. Partials never exist
+    // with streamed tiles, whose windows find a node's rows by binary search
+    // and so need the ascending row ids of the three-pass partition.
     auto one_pass_at = [&](uint32_t d) {
         return partials != nullptr && c->one_pass_chunks &&
                n_rows / PART_CHUNK <= ((uint64_t)c->one_pass_chunks << std::min(d, 40u));
