@@ -93,6 +93,12 @@ constexpr uint32_t MAX_NODES = 16384;      // nodes of one eval / partition call
 // (about 14 ns each measured: 74 us for 5128 chunks of one node, against
 // 56 us for the count, scan and scatter passes).
 constexpr uint32_t ONE_PASS_CHUNKS_PER_NODE = 512;
+// Histogram slots of at least this many bytes take the one-pass chunk
+// reduction, subtraction and split scan of evaluated pairs (split_pair_kernel)
+// when every tree feature allows it. Measured on one box over the first 25
+// rounds: 400k x 2000 (4 MB slots) 351 -> 361 rounds/s, 10.5M x 28 (114 KB
+// slots) 490 -> 480.
+constexpr uint64_t PAIR_PASS_MIN_SLOT_BYTES = 1u << 20;
 constexpr uint32_t DEFAULT_TILE_BYTES = 64 * 1024;
 // LDS of a planar tile (its bins plus the 1 KiB of lane dummies) when the
 // caller sets no tile size: three workgroups then share a CU's 160 KiB,
@@ -151,6 +157,7 @@ struct fbh_ctx {
     uint32_t planar_max_feats = 0;  // nonzero: at most this many features a planar tile
     uint64_t max_partial_bytes = MAX_PARTIAL_BYTES;
     uint32_t one_pass_chunks = ONE_PASS_CHUNKS_PER_NODE;  // 0: never one pass
+    bool pair_pass = true;          // split_pair_kernel where EvalPlan::pairs allows it
     uint32_t hist_tpb = 0;          // histogram threads per workgroup (0: per launch)
     uint32_t hist_waves = HIST_WAVES;
     uint32_t host_hist_waves = HOST_HIST_WAVES;
@@ -1095,6 +1102,7 @@ fbh_config configure(fbh_ctx &c, uint64_t n_rows, const fbh_shape *shape, const 
     c.planar_max_feats = (uint32_t)env_u64("FB_HIP_PLANAR_MAXF", 0);
     c.max_partial_bytes = env_u64("FB_HIP_PARTIAL_MB", MAX_PARTIAL_BYTES >> 20) << 20;
     c.one_pass_chunks = (uint32_t)env_u64("FB_HIP_ONE_PASS_CHUNKS", ONE_PASS_CHUNKS_PER_NODE);
+    c.pair_pass = env_u64("FB_HIP_NO_PAIR_PASS", 0) == 0;
     c.hist_waves = (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HIST_WAVES", HIST_WAVES));
     c.host_hist_waves =
         (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HOST_HIST_WAVES", HOST_HIST_WAVES));
@@ -2427,6 +2435,14 @@ struct EvalPlan {
     // The level decision makes the packets from the candidates itself
     // (device-grown trees of few features): no argmax launch.
     bool fused_argmax = false;
+    // hn[e], triples[3e..3e+2] and split nodes 2e, 2e + 1 describe evaluated
+    // pair e (the accumulated child, the subtraction, the left and right
+    // child): with every tree feature numeric of at most 256 bins, the chunk
+    // reduction, subtraction and split scan then run as one pass
+    // (split_pair_kernel). write_children: the children's histograms are
+    // stored (they are parents of a later evaluation).
+    bool pairs = false;
+    bool write_children = true;
     const uint32_t *rows = nullptr;  // arena of the accumulated nodes (null: the row arena)
     bool cleared = false;            // the accumulated slots were cleared by the partition
     bool identity = false;           // the accumulated rows are in order (no arena read)
@@ -2439,7 +2455,18 @@ struct EvalPlan {
     const TileDev *tiles = nullptr;  // the tile table (null: the tree's, d_tiles)
 };
 
+// Whether evaluated pairs of the current tree take split_pair_kernel: every
+// tree feature numeric of at most 256 bins, and large slots. The one pass
+// pays where slots are large (their reduction, subtraction and scan each move
+// them); with small slots its few waves a pair (four features a workgroup)
+// leave the device idler than three launches.
+bool pair_pass_ok(const fbh_ctx *c) {
+    return c->pair_pass && c->n_split_cat == 0 && c->n_split_num > 0 &&
+           c->hist_width * 16 >= PAIR_PASS_MIN_SLOT_BYTES;
+}
+
 void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
+    const bool fuse_pairs = E.pairs && pair_pass_ok(c);
     if (!E.cleared) {
         if (E.dev_chunk_rows)
             check(launch_zero_nodes(c->hist, c->hist_width, E.hn, E.n_hn, E.dev_n_hn,
@@ -2489,6 +2516,7 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
             }
             L.hist = c->hist;
             L.partials = E.partials;
+            L.clear_above = fuse_pairs ? PAIR_MAX_CHUNKS : REDUCE_GROUP;
             L.hist_width = c->hist_width;
             return L;
         };
@@ -2545,10 +2573,12 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
     }
     if (E.partials)
         check(launch_reduce_chunks(c->hist, c->hist_width, E.partials, E.hn, E.n_hn, E.dev_n_hn,
-                                   E.max_groups, c->stream),
+                                   E.max_groups, fuse_pairs ? PAIR_MAX_CHUNKS + 1 : 0u,
+                                   c->stream),
               "chunk reduction");
-    check(launch_subtract(c->hist, c->hist_width, E.triples, E.n_tri, E.dev_n_tri, c->stream),
-          "sibling subtraction");
+    if (!fuse_pairs)
+        check(launch_subtract(c->hist, c->hist_width, E.triples, E.n_tri, E.dev_n_tri, c->stream),
+              "sibling subtraction");
     // ---- split scan ----
     SplitParamsDev P{};
     P.scales = c->d_scales;
@@ -2561,10 +2591,16 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
     P.max_cat_threshold = sp->max_cat_threshold;
     P.n_feats = (uint32_t)c->tree_feats.size();
     P.cat_words_per_node = c->cat_words_per_node;
-    check(launch_split_feats(c->hist, c->hist_width, E.sn, E.n_nodes, c->d_sfeats,
-                             c->d_split_order, c->n_split_num, c->n_split_cat, E.enabled, P,
-                             c->d_cands, c->d_cat_scratch, E.dev_n_nodes, c->stream),
-          "split scan");
+    if (fuse_pairs)
+        check(launch_split_pairs(c->hist, c->hist_width, E.partials, E.hn, E.triples, E.n_hn,
+                                 E.sn, c->d_sfeats, c->d_split_order, c->n_split_num, E.enabled,
+                                 P, c->d_cands, E.dev_n_hn, E.write_children, c->stream),
+              "pair reduction, subtraction and split scan");
+    else
+        check(launch_split_feats(c->hist, c->hist_width, E.sn, E.n_nodes, c->d_sfeats,
+                                 c->d_split_order, c->n_split_num, c->n_split_cat, E.enabled, P,
+                                 c->d_cands, c->d_cat_scratch, E.dev_n_nodes, c->stream),
+              "split scan");
     const uint32_t cw = std::max(1u, c->cat_words_per_node);
     const size_t pk_bytes = sizeof(SplitPacketDev) * E.n_nodes;
     uint8_t *d_out = reinterpret_cast<uint8_t *>(c->d_packets);
@@ -3208,7 +3244,11 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     // every tile is an LDS tile and the buffer (grid chunks x histogram) is
     // modest; only nodes of more than REDUCE_GROUP chunks then need cleared
     // slots (their groups add atomically).
-    const ChunkRule rule = c->chunk_rule();
+    ChunkRule rule = c->chunk_rule();
+    // Levels below the root take the one-pass pair step where it applies
+    // (their evaluations set EvalPlan::pairs): only nodes of more than
+    // PAIR_MAX_CHUNKS chunks then need reduction groups.
+    if (pair_pass_ok(c)) rule.group_min_chunks = PAIR_MAX_CHUNKS + 1;
     auto level_grid = [&](uint32_t nb) {
         return rule.fixed ? n_rows / rule.fixed + nb + 1 : rule_chunk_bound(rule, n_rows, nb);
     };
@@ -3334,6 +3374,9 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
         E.fused_argmax = fuse;
         E.rows = arena_out;
         E.cleared = true;
+        E.pairs = true;
+        // These children are parents of the next evaluation only if there is one.
+        E.write_children = d + 2 < D;
         enqueue_eval(c, E, sp);
     }
     uint64_t leaf_bound = (uint64_t)1 << D;

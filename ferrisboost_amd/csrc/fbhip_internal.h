@@ -107,6 +107,10 @@ struct HistLaunch {
     // stream_data + (row - row_lo) * stride; only those rows are accumulated.
     const uint8_t *stream_data;
     uint32_t row_lo, row_hi;
+    // With partials: a node of more chunks than this is summed into its slot
+    // with atomics, so the launch clears the slot (REDUCE_GROUP, or
+    // PAIR_MAX_CHUNKS where split_pair_kernel sums smaller nodes itself).
+    uint32_t clear_above;
 };
 
 // Per-tree feature table of the split scan (compact histogram order).
@@ -231,6 +235,9 @@ struct ZeroNodesDev {
 // Chunks of one node that one workgroup of reduce_chunks_kernel sums
 // (reduce_groups).
 constexpr uint32_t REDUCE_GROUP = 16;
+// Chunks of an accumulated node that split_pair_kernel sums from the
+// partials itself (more: reduce_chunks_kernel, atomically into the slot).
+constexpr uint32_t PAIR_MAX_CHUNKS = 64;
 
 // Column of one feature for the partition of a device-grown tree.
 struct DevColumn {
@@ -277,6 +284,10 @@ struct GrowParamsDev {
 // [min_rows, max_rows].
 struct ChunkRule {
     uint32_t fixed, want_chunks, min_rows, max_rows;
+    // Nodes of fewer chunks get no chunk-reduction group (split_pair_kernel
+    // sums them); 0: every evaluated node gets its groups.
+    uint32_t group_min_chunks;
+    uint32_t pad;
 };
 
 struct LeafDev {
@@ -333,9 +344,11 @@ hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slot
 // without rows), global atomics into the cleared slot per group of
 // REDUCE_GROUP chunks for larger ones. max_groups bounds the groups of all
 // nodes (HistNodeDev::group_begin numbers them).
+// Nodes of fewer than min_chunks chunks are left alone (split_pair_kernel
+// sums them).
 hipError_t launch_reduce_chunks(int64_t *hist, uint64_t width, const int64_t *partials,
                                 const HistNodeDev *nodes, uint32_t n, const uint32_t *dev_n,
-                                uint32_t max_groups, hipStream_t s);
+                                uint32_t max_groups, uint32_t min_chunks, hipStream_t s);
 hipError_t launch_subtract(int64_t *hist, uint64_t width, const uint32_t *triples, uint32_t n,
                            const uint32_t *dev_n, hipStream_t s);
 // Zero the slots of accumulated nodes that need it: all when force, else
@@ -399,6 +412,15 @@ hipError_t launch_split_feats(const int64_t *hist, uint64_t hist_width, const Sp
                               uint32_t n_num, uint32_t n_cat, const uint8_t *enabled,
                               SplitParamsDev P, FeatCandDev *cands, uint64_t *cat_scratch,
                               const uint32_t *dev_n, hipStream_t s);
+// Chunk reduction (nodes of at most REDUCE_GROUP chunks), sibling
+// subtraction and split scan of evaluated pairs in one pass, for trees whose
+// features are all numeric of at most 256 bins (split_pair_kernel).
+hipError_t launch_split_pairs(int64_t *hist, uint64_t hist_width, const int64_t *partials,
+                              const HistNodeDev *hn, const uint32_t *triples, uint32_t n_pairs,
+                              const SplitNodeDev *nodes, const SplitFeatDev *feats,
+                              const uint32_t *order, uint32_t n_num, const uint8_t *enabled,
+                              SplitParamsDev P, FeatCandDev *cands, const uint32_t *dev_n,
+                              bool write, hipStream_t s);
 hipError_t launch_split_nodes(const FeatCandDev *cands, const SplitFeatDev *feats,
                               uint32_t n_nodes, SplitParamsDev P, const SplitNodeDev *nodes,
                               const uint64_t *cat_scratch, SplitPacketDev *out,

@@ -336,7 +336,7 @@ __global__ __launch_bounds__(TPB) void hist_kernel(const HistLaunch L) {
     // atomics (reduce_chunks_kernel): its first chunk's workgroups clear the
     // slot's bins of their tile here, so nothing clears it before.
     unsigned long long *clr =
-        (partial && chunk == N.chunk_begin && N.n_chunks > REDUCE_GROUP)
+        (partial && chunk == N.chunk_begin && N.n_chunks > L.clear_above)
             ? reinterpret_cast<unsigned long long *>(L.hist + (uint64_t)N.slot * L.hist_width * 2u)
             : nullptr;
     if (ROT) {
@@ -532,51 +532,71 @@ hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slot
     return hipGetLastError();
 }
 
-// Grid (word blocks, groups): group y belongs to the node whose
-// group_begin range holds it. A node of at most REDUCE_GROUP chunks has one
+// Grid (word blocks, groups; a workgroup takes groups blockIdx.y + k *
+// gridDim.y): group y belongs to the node whose group_begin range holds it.
+// A node of at most REDUCE_GROUP chunks has one
 // group, which sums them and stores the slot (zeros for a node without rows);
 // a larger node's groups each add the sum of their REDUCE_GROUP chunks into
 // its slot, which the histogram launch cleared (its first chunk's
 // workgroups).
 __global__ void reduce_chunks_kernel(int64_t *hist, uint64_t width, const int64_t *partials,
                                      const HistNodeDev *nodes, uint32_t n_nodes,
-                                     const uint32_t *dev_n) {
+                                     const uint32_t *dev_n, uint32_t max_groups,
+                                     uint32_t min_chunks) {
     const uint32_t n = dev_n ? *dev_n : n_nodes;
     if (n == 0) return;
-    const uint32_t y = blockIdx.y;
-    // Groups past the last node's (the grid is an upper bound) leave at once.
+    // Groups past the last node's (max_groups is an upper bound) are skipped.
     const HistNodeDev last = nodes[n - 1];
-    if (y >= last.group_begin + reduce_groups(last.n_chunks)) return;
-    uint32_t lo = 0, hi = n;
-    while (hi - lo > 1) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if (nodes[mid].group_begin <= y) lo = mid;
-        else hi = mid;
-    }
-    const HistNodeDev N = nodes[lo];
-    const uint32_t g = y - N.group_begin;
-    if (g >= reduce_groups(N.n_chunks) || N.n_chunks == 1) return;  // past the groups / written
-    const uint32_t c0 = g * REDUCE_GROUP, c1 = min(c0 + REDUCE_GROUP, N.n_chunks);
-    const bool store = N.n_chunks <= REDUCE_GROUP;
+    const uint32_t n_groups = min(max_groups, last.group_begin + reduce_groups(last.n_chunks));
+    if (blockIdx.y >= n_groups) return;
     const uint64_t W = width * 2u;
-    unsigned long long *dst = reinterpret_cast<unsigned long long *>(hist + (uint64_t)N.slot * W);
     const unsigned long long *src = reinterpret_cast<const unsigned long long *>(partials);
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < W;
-         i += (uint64_t)gridDim.x * blockDim.x) {
-        unsigned long long v = 0;
-        for (uint32_t c = c0; c < c1; c++) v += src[(uint64_t)(N.chunk_begin + c) * W + i];
-        if (store) dst[i] = v;
-        else if (v) global_add_u64(dst + i, v);
+    // The nodes' first groups in LDS when they fit (the searches below then
+    // wait on no global load).
+    constexpr uint32_t LDS_NODES = 256;
+    __shared__ uint32_t gb[LDS_NODES];
+    const bool in_lds = n <= LDS_NODES;
+    if (in_lds) {
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) gb[i] = nodes[i].group_begin;
+        __syncthreads();
+    }
+    for (uint32_t y = blockIdx.y; y < n_groups; y += gridDim.y) {
+        uint32_t lo = 0, hi = n;
+        while (hi - lo > 1) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if ((in_lds ? gb[mid] : nodes[mid].group_begin) <= y) lo = mid;
+            else hi = mid;
+        }
+        const HistNodeDev N = nodes[lo];
+        const uint32_t g = y - N.group_begin;
+        // past the groups / written / left to split_pair_kernel
+        if (g >= reduce_groups(N.n_chunks) || N.n_chunks == 1 || N.n_chunks < min_chunks)
+            continue;
+        const uint32_t c0 = g * REDUCE_GROUP, c1 = min(c0 + REDUCE_GROUP, N.n_chunks);
+        const bool store = N.n_chunks <= REDUCE_GROUP;
+        unsigned long long *dst =
+            reinterpret_cast<unsigned long long *>(hist + (uint64_t)N.slot * W);
+        for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < W;
+             i += (uint64_t)gridDim.x * blockDim.x) {
+            unsigned long long v = 0;
+            for (uint32_t c = c0; c < c1; c++) v += src[(uint64_t)(N.chunk_begin + c) * W + i];
+            if (store) dst[i] = v;
+            else if (v) global_add_u64(dst + i, v);
+        }
     }
 }
 
 hipError_t launch_reduce_chunks(int64_t *hist, uint64_t width, const int64_t *partials,
                                 const HistNodeDev *nodes, uint32_t n, const uint32_t *dev_n,
-                                uint32_t max_groups, hipStream_t s) {
+                                uint32_t max_groups, uint32_t min_chunks, hipStream_t s) {
     if (n == 0 || max_groups == 0) return hipSuccess;
     const uint32_t bx = (uint32_t)std::min<uint64_t>((width * 2 + 255) / 256, 1024);
-    hipLaunchKernelGGL(reduce_chunks_kernel, dim3(bx, max_groups), dim3(256), 0, s, hist, width,
-                       partials, nodes, n, dev_n);
+    // About 16384 workgroups: a launch whose groups are mostly empty (their
+    // nodes are summed elsewhere, or the bound is loose) costs little to
+    // dispatch; the workgroups of a wide histogram loop over the groups.
+    const uint32_t gy = std::min<uint32_t>(max_groups, std::max<uint32_t>(1, 16384 / bx));
+    hipLaunchKernelGGL(reduce_chunks_kernel, dim3(bx, gy), dim3(256), 0, s, hist, width,
+                       partials, nodes, n, dev_n, max_groups, min_chunks);
     return hipGetLastError();
 }
 
@@ -810,8 +830,11 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
         // Chunks (low half) and reduction groups (high half) in one scan.
         uint64_t both_total;
         const uint64_t both =
-            block_scan_u64((uint64_t)nc | ((uint64_t)(ev ? reduce_groups(nc) : 0u) << 32), buf64,
-                           both_total);
+            block_scan_u64((uint64_t)nc |
+                               ((uint64_t)(ev && nc >= rule.group_min_chunks ? reduce_groups(nc)
+                                                                             : 0u)
+                                << 32),
+                           buf64, both_total);
         const uint32_t total = (uint32_t)both_total, groups_total = (uint32_t)(both_total >> 32);
         const uint32_t before = carry + (uint32_t)both;
         const uint32_t group_before = gcarry + (uint32_t)(both >> 32);
@@ -1220,6 +1243,80 @@ __device__ __forceinline__ Best wave_best(Best b) {
 // numeric scan of split_feat_kernel on 64 lanes with shuffles only (no
 // barriers). Each lane takes a run of bins; integer prefix sums are exact in
 // any order, and the argmax keeps the reference's tie rule.
+// Bins of a numeric feature of at most 256 bins held by one wave: lane l
+// holds bins [l * per, l * per + per) in registers.
+constexpr uint32_t NUM_PER_LANE = 4;
+
+// The split scan of one (node, feature) over bins in the wave's registers
+// (g[k], h[k] of bin b0 + k): prefix sums, the forward candidates (missing
+// rows right), the reverse ones (missing rows left; skipped when the bins
+// hold the whole node) and the first best by the reference's rules, written
+// to outc by lane 0.
+__device__ __forceinline__ void scan_numeric(const int64_t (&g)[NUM_PER_LANE],
+                                             const int64_t (&h)[NUM_PER_LANE], uint32_t b0,
+                                             uint32_t b1, uint32_t n, uint32_t lane,
+                                             const SplitNodeDev &N, const SplitFeatDev &F,
+                                             const SplitParamsDev &P, FeatCandDev *outc) {
+    const double ng = (double)N.sum_g * P.inv_g, nh = (double)N.sum_h * P.inv_h;
+    const float parent = gain_given_weight(ng, nh, apply_bounds(xgb_weight(ng, nh, P), N.lower,
+                                                                N.upper), P);
+    int64_t tg = 0, th = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < NUM_PER_LANE; k++)
+        if (b0 + k < b1) {
+            tg = wadd(tg, g[k]);
+            th = wadd(th, h[k]);
+        }
+    const int64_t ig = wave_scan_incl_i64(tg, lane), ih = wave_scan_incl_i64(th, lane);
+    const int64_t eg = wsub(ig, tg), eh = wsub(ih, th);
+    const int64_t totg = __shfl(ig, 63, 64), toth = __shfl(ih, 63, 64);
+
+    Best best{0.0f, 0u, 0u, 0, 0};
+    const int mono = F.monotone;
+    // Forward: missing rows go right.
+    int64_t lg = eg, lh = eh;
+#pragma unroll
+    for (uint32_t k = 0; k < NUM_PER_LANE; k++) {
+        if (b0 + k >= b1) break;
+        lg = wadd(lg, g[k]);
+        lh = wadd(lh, h[k]);
+        float gain;
+        if (candidate_gain(lg, lh, wsub(N.sum_g, lg), wsub(N.sum_h, lh), parent, mono, N.lower,
+                           N.upper, P, gain))
+            offer(best, gain, b0 + k, lg, lh);
+    }
+    // Reverse: missing rows go left; skipped when the bins hold the whole node.
+    if (!(totg == N.sum_g && toth == N.sum_h)) {
+        int64_t rg = wsub(wsub(totg, eg), tg), rh = wsub(wsub(toth, eh), th);
+#pragma unroll
+        for (int k = NUM_PER_LANE - 1; k >= 0; k--) {
+            if (b0 + k >= b1) continue;
+            rg = wadd(rg, g[k]);
+            rh = wadd(rh, h[k]);
+            const int64_t l2g = wsub(N.sum_g, rg), l2h = wsub(N.sum_h, rh);
+            float gain;
+            if (candidate_gain(l2g, l2h, rg, rh, parent, mono, N.lower, N.upper, P, gain))
+                offer(best, gain, n + (n - 1 - (b0 + k)), l2g, l2h);
+        }
+    }
+    best = wave_best(best);
+    if (lane == 0) {
+        outc->found = best.found;
+        outc->gain = best.gain;
+        if (best.ord < n) {
+            outc->bin = best.ord + 1;
+            outc->missing_left = 0;
+        } else {
+            outc->bin = n - 1 - (best.ord - n);
+            outc->missing_left = 1;
+        }
+        outc->left_g = best.lg;
+        outc->left_h = best.lh;
+    }
+}
+
+// One wave per (node, numeric feature of at most 256 bins), four features a
+// workgroup: the feature's bins into registers, then scan_numeric.
 __global__ __launch_bounds__(256) void split_num_kernel(
     const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
     const SplitFeatDev *feats, const uint32_t *order, uint32_t n_num, const uint8_t *enabled,
@@ -1237,60 +1334,135 @@ __global__ __launch_bounds__(256) void split_num_kernel(
         if (lane == 0) outc->found = 0;
         return;
     }
-    const int64_t *h = hist + ((uint64_t)N.slot * hist_width + F.hist_off) * 2u;
-    const double ng = (double)N.sum_g * P.inv_g, nh = (double)N.sum_h * P.inv_h;
-    const float parent = gain_given_weight(ng, nh, apply_bounds(xgb_weight(ng, nh, P), N.lower,
-                                                                N.upper), P);
+    const int64_t *hp = hist + ((uint64_t)N.slot * hist_width + F.hist_off) * 2u;
     const uint32_t n = F.n_bins;
-    const uint32_t per = (n + 63) / 64;
+    const uint32_t per = (n + 63) / 64;  // at most NUM_PER_LANE
     const uint32_t b0 = min(lane * per, n), b1 = min(b0 + per, n);
-    int64_t tg = 0, th = 0;
-    for (uint32_t bb = b0; bb < b1; bb++) {
-        tg = wadd(tg, h[2 * bb]);
-        th = wadd(th, h[2 * bb + 1]);
+    int64_t g[NUM_PER_LANE], h[NUM_PER_LANE];
+#pragma unroll
+    for (uint32_t k = 0; k < NUM_PER_LANE; k++) {
+        g[k] = b0 + k < b1 ? hp[2 * (b0 + k)] : 0;
+        h[k] = b0 + k < b1 ? hp[2 * (b0 + k) + 1] : 0;
     }
-    const int64_t ig = wave_scan_incl_i64(tg, lane), ih = wave_scan_incl_i64(th, lane);
-    const int64_t eg = wsub(ig, tg), eh = wsub(ih, th);
-    const int64_t totg = __shfl(ig, 63, 64), toth = __shfl(ih, 63, 64);
+    scan_numeric(g, h, b0, b1, n, lane, N, F, P, outc);
+}
 
-    Best best{0.0f, 0u, 0u, 0, 0};
-    const int mono = F.monotone;
-    // Forward: missing rows go right.
-    int64_t lg = eg, lh = eh;
-    for (uint32_t bb = b0; bb < b1; bb++) {
-        lg = wadd(lg, h[2 * bb]);
-        lh = wadd(lh, h[2 * bb + 1]);
-        float gain;
-        if (candidate_gain(lg, lh, wsub(N.sum_g, lg), wsub(N.sum_h, lh), parent, mono, N.lower,
-                           N.upper, P, gain))
-            offer(best, gain, bb, lg, lh);
-    }
-    // Reverse: missing rows go left; skipped when the bins hold the whole node.
-    if (!(totg == N.sum_g && toth == N.sum_h)) {
-        int64_t rg = wsub(wsub(totg, eg), tg), rh = wsub(wsub(toth, eh), th);
-        for (uint32_t bb = b1; bb-- > b0;) {
-            rg = wadd(rg, h[2 * bb]);
-            rh = wadd(rh, h[2 * bb + 1]);
-            const int64_t l2g = wsub(N.sum_g, rg), l2h = wsub(N.sum_h, rh);
-            float gain;
-            if (candidate_gain(l2g, l2h, rg, rh, parent, mono, N.lower, N.upper, P, gain))
-                offer(best, gain, n + (n - 1 - bb), l2g, l2h);
+// Reduction, subtraction and split scan of one evaluated pair in one pass,
+// one wave per (pair, numeric feature of at most 256 bins): the accumulated
+// (smaller) child's bins come from its chunks' partials when it has 2 to
+// PAIR_MAX_CHUNKS chunks, else from its slot (one chunk: stored by the
+// histogram launch; more: summed there by reduce_chunks_kernel; none: zeros);
+// the larger child's are the parent's minus those. Both children's bins are
+// stored to their slots (the larger in place of the parent's) when `write`
+// (they are parents at the next level), and both are scanned. Pair e holds
+// hn[e] (the accumulated child), triples[3e..3e+2] (larger child's slot,
+// parent slot, accumulated slot) and nodes 2e, 2e + 1 (left, right).
+__global__ __launch_bounds__(256) void split_pair_kernel(
+    int64_t *hist, uint64_t hist_width, const int64_t *partials, const HistNodeDev *hn,
+    const uint32_t *triples, const SplitNodeDev *nodes, const SplitFeatDev *feats,
+    const uint32_t *order, uint32_t n_num, const uint8_t *enabled, SplitParamsDev P,
+    FeatCandDev *cands, const uint32_t *dev_n, uint32_t write) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t li = blockIdx.x * 4 + wave, e = blockIdx.y;
+    if (dev_n && e >= *dev_n) return;
+    if (li >= n_num) return;  // a whole wave
+    load_scales(P);
+    const uint32_t j = order[li];
+    const SplitFeatDev F = feats[j];
+    const HistNodeDev H = hn[e];
+    const uint32_t big_slot = triples[3 * e], par_slot = triples[3 * e + 1];
+    const uint64_t W = hist_width * 2u;
+    const uint32_t n = F.n_bins;
+    const uint32_t per = (n + 63) / 64;  // at most NUM_PER_LANE
+    const uint32_t b0 = min(lane * per, n), b1 = min(b0 + per, n);
+    const uint64_t off = 2u * (uint64_t)F.hist_off;
+    int64_t sg[NUM_PER_LANE], sh[NUM_PER_LANE];
+    const bool from_partials = partials && H.n_chunks > 1 && H.n_chunks <= PAIR_MAX_CHUNKS;
+    if (from_partials) {
+#pragma unroll
+        for (uint32_t k = 0; k < NUM_PER_LANE; k++) sg[k] = sh[k] = 0;
+        // Four chunks' loads in flight at a time (a chunk past the node's
+        // reads its first chunk again and adds nothing).
+        for (uint32_t c = 0; c < H.n_chunks; c += 4) {
+            int64_t vg[4][NUM_PER_LANE], vh[4][NUM_PER_LANE];
+#pragma unroll
+            for (uint32_t q = 0; q < 4; q++) {
+                const uint32_t cc = c + q < H.n_chunks ? c + q : 0u;
+                const int64_t *pp = partials + (uint64_t)(H.chunk_begin + cc) * W + off;
+#pragma unroll
+                for (uint32_t k = 0; k < NUM_PER_LANE; k++) {
+                    vg[q][k] = b0 + k < b1 ? pp[2 * (b0 + k)] : 0;
+                    vh[q][k] = b0 + k < b1 ? pp[2 * (b0 + k) + 1] : 0;
+                }
+            }
+#pragma unroll
+            for (uint32_t q = 0; q < 4; q++)
+                if (c + q < H.n_chunks) {
+#pragma unroll
+                    for (uint32_t k = 0; k < NUM_PER_LANE; k++) {
+                        sg[k] = wadd(sg[k], vg[q][k]);
+                        sh[k] = wadd(sh[k], vh[q][k]);
+                    }
+                }
+        }
+    } else {
+        const int64_t *sp = hist + (uint64_t)H.slot * W + off;
+#pragma unroll
+        for (uint32_t k = 0; k < NUM_PER_LANE; k++) {
+            const bool in = H.n_chunks && b0 + k < b1;
+            sg[k] = in ? sp[2 * (b0 + k)] : 0;
+            sh[k] = in ? sp[2 * (b0 + k) + 1] : 0;
         }
     }
-    best = wave_best(best);
-    if (lane == 0) {
-        outc->found = best.found;
-        outc->gain = best.gain;
-        if (best.ord < n) {
-            outc->bin = best.ord + 1;
-            outc->missing_left = 0;
-        } else {
-            outc->bin = n - 1 - (best.ord - n);
-            outc->missing_left = 1;
+    int64_t bg[NUM_PER_LANE], bh[NUM_PER_LANE];
+    {
+        const int64_t *pp = hist + (uint64_t)par_slot * W + off;
+#pragma unroll
+        for (uint32_t k = 0; k < NUM_PER_LANE; k++) {
+            bg[k] = b0 + k < b1 ? wsub(pp[2 * (b0 + k)], sg[k]) : 0;
+            bh[k] = b0 + k < b1 ? wsub(pp[2 * (b0 + k) + 1], sh[k]) : 0;
         }
-        outc->left_g = best.lg;
-        outc->left_h = best.lh;
     }
+    if (write) {
+        int64_t *bp = hist + (uint64_t)big_slot * W + off;
+        int64_t *sp = hist + (uint64_t)H.slot * W + off;
+        const bool store_small = from_partials || H.n_chunks == 0;
+#pragma unroll
+        for (uint32_t k = 0; k < NUM_PER_LANE; k++)
+            if (b0 + k < b1) {
+                bp[2 * (b0 + k)] = bg[k];
+                bp[2 * (b0 + k) + 1] = bh[k];
+                if (store_small) {
+                    sp[2 * (b0 + k)] = sg[k];
+                    sp[2 * (b0 + k) + 1] = sh[k];
+                }
+            }
+    }
+#pragma unroll
+    for (uint32_t side = 0; side < 2; side++) {
+        const uint32_t ni = 2 * e + side;
+        const SplitNodeDev N = nodes[ni];
+        FeatCandDev *outc = cands + (size_t)ni * P.n_feats + j;
+        if (enabled && !enabled[(size_t)ni * P.n_feats + j]) {
+            if (lane == 0) outc->found = 0;
+            continue;
+        }
+        if (N.slot == H.slot) scan_numeric(sg, sh, b0, b1, n, lane, N, F, P, outc);
+        else scan_numeric(bg, bh, b0, b1, n, lane, N, F, P, outc);
+    }
+}
+
+hipError_t launch_split_pairs(int64_t *hist, uint64_t hist_width, const int64_t *partials,
+                              const HistNodeDev *hn, const uint32_t *triples, uint32_t n_pairs,
+                              const SplitNodeDev *nodes, const SplitFeatDev *feats,
+                              const uint32_t *order, uint32_t n_num, const uint8_t *enabled,
+                              SplitParamsDev P, FeatCandDev *cands, const uint32_t *dev_n,
+                              bool write, hipStream_t s) {
+    if (n_pairs == 0 || n_num == 0) return hipSuccess;
+    hipLaunchKernelGGL(split_pair_kernel, dim3((n_num + 3) / 4, n_pairs), dim3(256), 0, s, hist,
+                       hist_width, partials, hn, triples, nodes, feats, order, n_num, enabled, P,
+                       cands, dev_n, write ? 1u : 0u);
+    return hipGetLastError();
 }
 
 // One workgroup per (feature, node): prefix sums of the feature's bins, the
