@@ -362,6 +362,11 @@ def streaming_workload(args):
         "device_bytes": int(st["device_bytes"]),
         "streamed_gb_per_round": round(streamed / rounds / 1e9, 2),
         "h2d_gbps": round(streamed / train_s / 1e9, 1),
+        "setup": {"seconds": round(st["setup_seconds"], 3),
+                  "sketch_seconds": round(st["sketch_seconds"], 3),
+                  "binning_seconds": round(st["bin_seconds"], 3),
+                  "device_sketch": bool(st["device_sketch"]),
+                  "device_binning": bool(st["device_binning"])},
         "roofline": {"bound": "hbm", "achieved": round(float(hbytes[args.warmup:].sum()) /
                                                          (float(hms[args.warmup:].sum()) * 1e-3) / 1e9, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": None, "traffic": None,

@@ -205,10 +205,27 @@ struct fbh_ctx {
     float *d_cut_values = nullptr;
     float *rows_stage = nullptr;
     bool cuts_set = false;
+    // Device binning under a plan that does not keep the bin columns: a
+    // chunk's bins land in bin_stage (feature f's column of stage_rows()
+    // cells at byte bin_off[f], 256-aligned), resident tiles are packed from
+    // there and streamed tiles' records are packed in rec_stage and copied
+    // to their pinned host memory.
+    uint8_t *bin_stage = nullptr, *rec_stage = nullptr;
+    std::vector<uint64_t> bin_off;
+    uint64_t bin_stage_bytes() const {
+        uint64_t cols = 0, stride = 0;
+        for (uint32_t f = 0; f < n_features; f++)
+            cols += (stage_rows() * width[f] + 255) & ~uint64_t(255);
+        for (const auto &t : tiles)
+            if (!t.resident) stride = std::max<uint64_t>(stride, t.stride);
+        return cols + stage_rows() * stride + 512;
+    }
     // Rows the staging holds: 64 MiB of rows, at least 64 rows.
+    uint64_t stage_rows_cap = 0;  // nonzero: rows of the row staging (FB_HIP_STAGE_ROWS)
     uint64_t stage_rows() const {
         const uint64_t per = 4ull * std::max<uint32_t>(n_features, 1);
-        return std::max<uint64_t>(64, std::min<uint64_t>(n_rows, (64ull << 20) / per));
+        const uint64_t cap = stage_rows_cap ? stage_rows_cap : (64ull << 20) / per;
+        return std::max<uint64_t>(64, std::min<uint64_t>(n_rows, cap));
     }
     // Row bundles: consecutive LDS tiles whose records fit in one 128-byte
     // cache line share one allocation, row r's records together at data +
@@ -1103,6 +1120,7 @@ fbh_config configure(fbh_ctx &c, uint64_t n_rows, const fbh_shape *shape, const 
     c.max_partial_bytes = env_u64("FB_HIP_PARTIAL_MB", MAX_PARTIAL_BYTES >> 20) << 20;
     c.one_pass_chunks = (uint32_t)env_u64("FB_HIP_ONE_PASS_CHUNKS", ONE_PASS_CHUNKS_PER_NODE);
     c.pair_pass = env_u64("FB_HIP_NO_PAIR_PASS", 0) == 0;
+    c.stage_rows_cap = env_u64("FB_HIP_STAGE_ROWS", 0);
     c.hist_waves = (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HIST_WAVES", HIST_WAVES));
     c.host_hist_waves =
         (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HOST_HIST_WAVES", HOST_HIST_WAVES));
@@ -1327,11 +1345,9 @@ int fbh_set_cuts(fbh_ctx *c, const float *cut_values, const uint32_t *cut_offset
     return guard([&] {
         if (!c || !cut_offsets || (!cut_values && cut_offsets[c->n_features] != 0))
             throw InputError("null argument");
-        if (!c->plan.columns_resident)
-            throw InputError("device binning needs the bin columns resident; the plan streams "
-                             "them (bin on the host and upload column blocks)");
         check(hipSetDevice(c->device), "hipSetDevice");
         const uint32_t nf = c->n_features;
+        const bool staged = !c->plan.columns_resident;
         if (cut_offsets[0] != 0) throw InputError("cut offsets must start at 0");
         for (uint32_t f = 0; f < nf; f++) {
             if (cut_offsets[f + 1] < cut_offsets[f])
@@ -1349,7 +1365,8 @@ int fbh_set_cuts(fbh_ctx *c, const float *cut_values, const uint32_t *cut_offset
                                      " cuts must be strictly increasing");
         }
         const uint64_t n_vals = cut_offsets[nf];
-        const uint64_t bytes = 4 * std::max<uint64_t>(n_vals, 1) + sizeof(BinFeatDev) * nf + 512;
+        const uint64_t bytes = 4 * std::max<uint64_t>(n_vals, 1) + sizeof(BinFeatDev) * nf + 512 +
+                               (staged ? c->bin_stage_bytes() : 0);
         if (c->device_bytes + bytes > c->plan.budget)
             throw InputError("the device cuts do not fit the budget's remaining room");
         if (!c->d_cut_values) {
@@ -1358,10 +1375,23 @@ int fbh_set_cuts(fbh_ctx *c, const float *cut_values, const uint32_t *cut_offset
         } else {
             throw InputError("the cuts of this context are already set");
         }
+        if (staged) {
+            uint64_t stride = 0, off = 0;
+            for (const auto &t : c->tiles)
+                if (!t.resident) stride = std::max<uint64_t>(stride, t.stride);
+            c->bin_off.assign(nf, 0);
+            for (uint32_t f = 0; f < nf; f++) {
+                c->bin_off[f] = off;
+                off += al256(c->stage_rows() * c->width[f]);
+            }
+            c->bin_stage = c->alloc<uint8_t>(off, "binning stage");
+            if (stride)
+                c->rec_stage = c->alloc<uint8_t>(c->stage_rows() * stride, "record stage");
+        }
         std::vector<BinFeatDev> tab(nf);
         for (uint32_t f = 0; f < nf; f++) {
             tab[f].cuts = c->d_cut_values + cut_offsets[f];
-            tab[f].col = c->cols[f];
+            tab[f].col = staged ? c->bin_stage + c->bin_off[f] : c->cols[f];
             tab[f].n_cuts = cut_offsets[f + 1] - cut_offsets[f];
             tab[f].n_bins = c->n_bins[f];
             tab[f].width = c->width[f];
@@ -1380,7 +1410,41 @@ int fbh_set_cuts(fbh_ctx *c, const float *cut_values, const uint32_t *cut_offset
 }
 
 uint64_t fbh_rows_staging_bytes(const fbh_ctx *c) {
-    return c ? c->stage_rows() * 4ull * c->n_features : 0;
+    if (!c) return 0;
+    return c->stage_rows() * 4ull * c->n_features +
+           (c->plan.columns_resident ? 0 : c->bin_stage_bytes());
+}
+
+// Rows [row0, row0 + k) binned into the binning stage: resident tiles'
+// records packed in place, streamed tiles' records packed in the record
+// stage and copied to their pinned host memory, with the streamed features'
+// columns (for their partitions). All in stream order, so the next chunk's
+// binning waits for these copies.
+static void pack_staged_rows(fbh_ctx *c, uint64_t row0, uint64_t k) {
+    for (const auto &t : c->tiles) {
+        if (t.resident) {
+            for (uint32_t f : t.feats)
+                check(launch_pack_feature(c->bin_stage + c->bin_off[f], k, c->width[f],
+                                          t.data + row0 * t.stride, t.stride,
+                                          (uint32_t)c->feat_pos[f] * c->width[f], c->stream),
+                      "tile packing");
+            continue;
+        }
+        check(hipMemsetAsync(c->rec_stage, 0, k * t.stride, c->stream), "record stage clear");
+        for (uint32_t f : t.feats)
+            check(launch_pack_feature(c->bin_stage + c->bin_off[f], k, c->width[f],
+                                      c->rec_stage, t.stride,
+                                      (uint32_t)c->feat_pos[f] * c->width[f], c->stream),
+                  "record packing");
+        check(hipMemcpyAsync(t.host + row0 * t.stride, c->rec_stage, k * t.stride,
+                             hipMemcpyDeviceToHost, c->stream),
+              "record download");
+        for (uint32_t f : t.feats)
+            check(hipMemcpyAsync(c->host_cols[f] + row0 * c->width[f],
+                                 c->bin_stage + c->bin_off[f], k * c->width[f],
+                                 hipMemcpyDeviceToHost, c->stream),
+                  "column download");
+    }
 }
 
 int fbh_upload_rows(fbh_ctx *c, const float *x, uint64_t row0, uint64_t n_rows) {
@@ -1399,15 +1463,17 @@ int fbh_upload_rows(fbh_ctx *c, const float *x, uint64_t row0, uint64_t n_rows) 
                                  " bytes) does not fit the budget's remaining room");
             c->rows_stage = c->alloc<float>(cap * nf, "row staging");
         }
+        const bool staged = !c->plan.columns_resident;
         for (uint64_t r = 0; r < n_rows; r += cap) {
             const uint64_t b = std::min(cap, n_rows - r);
             // Stream order: this copy waits for the previous chunk's binning.
             check(hipMemcpyAsync(c->rows_stage, x + r * nf, 4 * b * nf, hipMemcpyHostToDevice,
                                  c->stream),
                   "row upload");
-            check(launch_bin_rows(c->rows_stage, b, (uint32_t)nf, row0 + r, c->d_binfeats,
-                                  c->stream),
+            check(launch_bin_rows(c->rows_stage, b, (uint32_t)nf, staged ? 0 : row0 + r,
+                                  c->d_binfeats, c->stream),
                   "row binning");
+            if (staged) pack_staged_rows(c, row0 + r, b);
         }
         c->sync();  // the caller may reuse x
     });
@@ -1422,7 +1488,9 @@ int fbh_finish_rows(fbh_ctx *c) {
         c->hot_ready = false;
         for (uint32_t f = 0; f < c->n_features; f++) {
             const fbh_ctx::Tile &t = c->tiles[c->feat_tile[f]];
-            if (t.resident) {
+            if (!c->plan.columns_resident) {
+                // packed chunk by chunk as the rows came (pack_staged_rows)
+            } else if (t.resident) {
                 const uint32_t off = (uint32_t)c->feat_pos[f] * c->width[f];
                 check(launch_pack_feature(c->cols[f], c->n_rows, c->width[f], t.data, t.stride,
                                           off, c->stream),

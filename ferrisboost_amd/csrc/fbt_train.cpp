@@ -1262,9 +1262,9 @@ Model train(const RowSource &src, uint64_t n, uint32_t nf, const float *y, const
     call(fbh_ctx_create(p.device, n, &shape, &cfg, &raw));
     std::unique_ptr<fbh_ctx, int (*)(fbh_ctx *)> ctx(raw, fbh_ctx_destroy);
     call(fbh_set_timing(ctx.get(), p.profile ? 1 : 0));
-    // Binning: on the device when the plan keeps the bin columns resident and
-    // the budget's room holds the row staging, else column blocks binned on
-    // the host (the same bins either way).
+    // Binning: on the device when the budget's room holds the row staging
+    // (and, when the plan streams, the binning stages), else column blocks
+    // binned on the host (the same bins either way).
     const auto t_bin = Clock::now();
     bool device_binning = false;
     {
@@ -1273,7 +1273,7 @@ Model train(const RowSource &src, uint64_t n, uint32_t nf, const float *y, const
         const uint64_t held = fbh_ctx_device_bytes(ctx.get());
         const uint64_t need = fbh_rows_staging_bytes(ctx.get()) +
                               4 * (uint64_t)m.cuts.values.size() + 64 * (uint64_t)nf + (1u << 16);
-        device_binning = !p.host_binning && plan.columns_resident && held + need <= plan.budget;
+        device_binning = !p.host_binning && held + need <= plan.budget;
     }
     if (device_binning) {
         call(fbh_set_cuts(ctx.get(), m.cuts.values.data(), m.cuts.offsets.data(),

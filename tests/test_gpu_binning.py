@@ -18,6 +18,13 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.fixture(scope="module")
+def fb_mod():
+    import ferrisboost_amd as fb
+
+    return fb
+
+
+@pytest.fixture(scope="module")
 def N():
     from ferrisboost_amd import _native as N
 
@@ -169,3 +176,43 @@ def test_device_binned_training_equals_host_binned(case):
     assert_same_models(host, dev)
     n = y.size
     assert np.array_equal(dev.train_margins(n).view(np.uint32), host.train_margins(n).view(np.uint32))
+
+
+def test_streamed_plan_bins_on_the_device(fb_mod, N, monkeypatch):
+    """A plan that streams tiles from pinned host memory bins on the device
+    too: each chunk of rows is binned into a stage, resident tiles are packed
+    in place and streamed tiles' records and columns are copied back to their
+    pinned memory. The model equals the host-binned one at the same budget
+    and the all-resident one, byte for byte."""
+    from test_gpu_parity import _streaming_budgets
+
+    fb = fb_mod
+    rng = np.random.default_rng(71)
+    n, nf = 120_007, 40
+    x = rng.normal(size=(n, nf)).astype(np.float32)
+    x[rng.random((n, nf)) < 0.04] = np.nan
+    y = (np.nan_to_num(x[:, 0]) - np.nan_to_num(x[:, 7]) * np.nan_to_num(x[:, 31])
+         + 0.3 * rng.normal(size=n) > 0).astype(np.float32)
+    p = {"objective": "binary:logistic", "max_depth": 6, "eta": 0.3, "max_bin": 255}
+    ref = fb.train(p, x, y, num_boost_round=4)
+    assert ref.stats["resident_tiles"] == ref.stats["n_tiles"] and ref.stats["device_binning"]
+    some, _ = _streaming_budgets(N, ref, n, 32)
+    # small row stages, so the budget's room left by the plan holds them
+    monkeypatch.setenv("FB_HIP_STAGE_ROWS", "2048")
+    for k in range(64):
+        budget = some + k * (1 << 18)
+        dev = fb.train(dict(p, gpu_memory_budget=budget), x, y, num_boost_round=4)
+        if dev.stats["resident_tiles"] == dev.stats["n_tiles"]:
+            break
+        if dev.stats["device_binning"]:
+            assert dev.stats["streamed_bytes"] > 0 and dev.stats["device_bytes"] <= budget
+            host = fb.train(dict(p, gpu_memory_budget=budget, hip_host_binning=True), x, y,
+                            num_boost_round=4)
+            assert host.stats["device_binning"] == 0
+            assert host.stats["resident_tiles"] == dev.stats["resident_tiles"]
+            assert_same_models(host, dev)
+            assert_same_models(ref, dev)
+            assert np.array_equal(dev.train_margins(n).view(np.uint32),
+                                  ref.train_margins(n).view(np.uint32))
+            return
+    pytest.fail("no budget between streaming and full residency left room for device binning")
