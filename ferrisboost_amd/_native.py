@@ -222,7 +222,8 @@ HIP_SYMBOLS = [
     "fbh_ctx_device_bytes", "fbh_upload_block", "fbh_set_cuts", "fbh_rows_staging_bytes",
     "fbh_apply_leaf_values",
     "fbh_upload_rows", "fbh_finish_rows", "fbh_sketch_device_bytes", "fbh_sketch_fits",
-    "fbh_sketch_create", "fbh_sketch_push_rows", "fbh_sketch_cuts", "fbh_sketch_destroy",
+    "fbh_sketch_create", "fbh_sketch_push_rows", "fbh_sketch_cuts", "fbh_sketch_missing",
+    "fbh_sketch_destroy",
     "fbh_upload_quantize_gpair",
     "fbh_upload_gpair_fixed", "fbh_set_objective", "fbh_set_multiclass",
     "fbh_multiclass_begin_round", "fbh_set_output", "fbh_set_quantile",
@@ -300,6 +301,7 @@ def hip() -> C.CDLL:
                                         C.c_uint64, C.POINTER(P)]
         L.fbh_sketch_push_rows.argtypes = [P, P, C.c_uint64]
         L.fbh_sketch_cuts.argtypes = [P, P, C.c_uint64, P, P]
+        L.fbh_sketch_missing.argtypes = [P, P]
         L.fbh_sketch_destroy.argtypes = [P]
         L.fbh_apply_leaf_values.argtypes = [P, P, C.c_uint32]
         L.fbh_upload_quantize_gpair.argtypes = [P, P, C.c_uint64, C.c_uint64, C.c_uint64, P, P]

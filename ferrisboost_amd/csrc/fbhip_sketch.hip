@@ -856,6 +856,22 @@ int fbh_sketch_push_rows(fbh_sketch *s, const float *x, uint64_t n_rows) {
     });
 }
 
+int fbh_sketch_missing(const fbh_sketch *s, uint64_t *missing) {
+    return sk_guard([&] {
+        if (!s || !missing) throw SkError(FBH_INPUT_ERROR, "null argument");
+        sk_check(hipSetDevice(s->device), "hipSetDevice");
+        std::vector<uint64_t> n_valid(s->n_num);
+        if (s->n_num) {
+            sk_check(hipMemcpyAsync(n_valid.data(), s->n_valid, 8ull * s->n_num,
+                                    hipMemcpyDeviceToHost, s->stream),
+                     "download");
+            sk_check(hipStreamSynchronize(s->stream), "sync");
+        }
+        for (uint32_t f = 0; f < s->nf; f++)
+            missing[f] = s->num_of[f] < 0 ? 0 : s->pushed - n_valid[(uint32_t)s->num_of[f]];
+    });
+}
+
 int fbh_sketch_cuts(fbh_sketch *s, float *cut_values, uint64_t values_capacity,
                     uint32_t *cut_offsets, uint8_t *host_features) {
     return sk_guard([&] {

@@ -282,6 +282,8 @@ Cuts sketch_matrix_device(int device, const RowSource &src, uint64_t n, uint32_t
     std::vector<uint32_t> offsets(nf + 1);
     std::vector<uint8_t> host(nf);
     call(fbh_sketch_cuts(s.get(), values.data(), cap, offsets.data(), host.data()));
+    std::vector<uint64_t> missing(nf);
+    call(fbh_sketch_missing(s.get(), missing.data()));
     s.reset();
     std::vector<std::vector<float>> per(nf);
     std::vector<uint32_t> on_host;
@@ -310,7 +312,12 @@ Cuts sketch_matrix_device(int device, const RowSource &src, uint64_t n, uint32_t
             per[on_host[i]] = sketch_numeric(mat, n, stride, src.x ? on_host[i] : i, max_bin, nullptr);
         });
     }
-    return assemble_cuts(per, nf, cat);
+    Cuts c = assemble_cuts(per, nf, cat);
+    // 256-bin numeric features without a missing row take 8-bit cells.
+    c.full.assign(nf, 0);
+    for (uint32_t f = 0; f < nf; f++)
+        if (!c.is_cat(f) && c.n_bins(f) == 256 && missing[f] == 0) c.full[f] = 1;
+    return c;
 }
 
 void check_cuts(const Cuts &c, uint32_t nf, uint32_t max_bin, const uint8_t *cat) {

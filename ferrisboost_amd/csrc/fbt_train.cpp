@@ -1169,8 +1169,9 @@ Model train(const RowSource &src, uint64_t n, uint32_t nf, const float *y, const
     }
     const double sketch_s = std::chrono::duration<double>(Clock::now() - t_sketch).count();
     // 256-bin numeric features without a missing row take 8-bit cells
-    // (Cuts::full), when the rows are in host memory for the check.
-    if (x) mark_full_features(m.cuts, x, n, nf, threads);
+    // (Cuts::full): known from the device sketch, else checked over the rows
+    // when they are in host memory.
+    if (m.cuts.full.empty() && x) mark_full_features(m.cuts, x, n, nf, threads);
     // Base score: explicit, else the label mean weighted by the sample weights
     // only (Objective::estimate_base_score, src/training/objective.rs:42-60,
     // 452-470; scale_pos_weight enters the gradient weights alone,

@@ -259,6 +259,11 @@ int fbh_sketch_push_rows(fbh_sketch *s, const float *x, uint64_t n_rows);
  * cuts need more than values_capacity values (the offsets are set). */
 int fbh_sketch_cuts(fbh_sketch *s, float *cut_values, uint64_t values_capacity,
                     uint32_t *cut_offsets, uint8_t *host_features);
+/* Missing (NaN) values of every numeric feature among the rows pushed so far
+ * into missing[f] (n_features entries; 0 for categorical features). The
+ * trainer stores a 256-bin numeric feature with none in 8-bit cells. Has no
+ * counterpart in the reference (whose bins are 32-bit). */
+int fbh_sketch_missing(const fbh_sketch *s, uint64_t *missing);
 int fbh_sketch_destroy(fbh_sketch *s);
 
 /* ------------------------------------------------------------ gradients */

@@ -140,3 +140,27 @@ def test_reader_errors_reach_the_caller(fb, monkeypatch):
     monkeypatch.setattr(arrow_rows.ArrowRows, "_rows_of", broken)
     with pytest.raises(OSError, match="went away"):
         fb.train(PARAMS, t, "label", num_boost_round=1)
+
+
+def test_reader_rows_take_8bit_cells_as_arrays_do(fb):
+    """At max_bin 256 a numeric feature without a missing row fills its 256
+    bins into 8-bit cells. From an Arrow table the device sketch counts the
+    missing values, so the table-trained context plans the same cell widths
+    (the same planned bytes) as the array-trained one, and the models are
+    equal byte for byte."""
+    rng = np.random.default_rng(4)
+    n = 30_000
+    x = rng.standard_normal((n, 6)).astype(np.float32)
+    x[:, 5][rng.random(n) < 0.02] = np.nan  # one feature keeps 16-bit cells
+    y = (x[:, 0] + x[:, 1] * x[:, 2] > 0).astype(np.float32)
+    cols = {f"f{j}": pa.array(x[:, j], mask=np.isnan(x[:, j])) for j in range(6)}
+    cols["label"] = pa.array(y)
+    p = dict(PARAMS, max_bin=256)
+    m_tab = fb.train(p, pa.table(cols), "label", num_boost_round=4)
+    m_arr = fb.train(p, np.ascontiguousarray(x), y, num_boost_round=4)
+    assert m_tab.stats["device_sketch"] and m_arr.stats["device_sketch"]
+    assert m_tab.stats["planned_bytes"] == m_arr.stats["planned_bytes"]
+    assert m_tab.to_json() == m_arr.to_json()
+    m_wide = fb.train(dict(p, hip_host_sketch=True), np.ascontiguousarray(x), y,
+                      num_boost_round=4)
+    assert m_wide.stats["planned_bytes"] == m_arr.stats["planned_bytes"]
