@@ -24,6 +24,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -102,14 +103,15 @@ __device__ __forceinline__ uint32_t walk_step(const PredNodeDev &n, uint32_t id,
 // logistic link is the sigmoid of objective.rs:37-39 with glibc's expf
 // method, bit-identical to the host's. PRED_LEAF writes each tree's
 // tree-local leaf id as a float.
-__global__ __launch_bounds__(PRED_TPB) void predict_kernel(
-    const PredNodeDev *__restrict__ nodes, const ShapNodeDev *__restrict__ full,
-    const uint32_t *__restrict__ cats, const uint32_t *__restrict__ roots, uint32_t n_trees,
-    const float *__restrict__ rows, uint64_t n_rows, uint32_t nf, const float *__restrict__ init,
-    float base, uint32_t mode, float *__restrict__ out) {
-    const uint64_t row = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (row >= n_rows) return;
-    const float *x = rows + row * nf;
+// One row's walk over every tree (x: the row's cells, in global memory or
+// LDS): margins and values write out[row], leaf ids out[row * n_trees + t].
+__device__ __forceinline__ void predict_row(const PredNodeDev *__restrict__ nodes,
+                                            const ShapNodeDev *__restrict__ full,
+                                            const uint32_t *__restrict__ cats,
+                                            const uint32_t *__restrict__ roots, uint32_t n_trees,
+                                            const float *x, uint64_t row,
+                                            const float *__restrict__ init, float base,
+                                            uint32_t mode, float *__restrict__ out) {
     if (mode == PRED_LEAF) {
         float *o = out + row * n_trees;
         for (uint32_t t = 0; t < n_trees; t++) {
@@ -135,6 +137,94 @@ __global__ __launch_bounds__(PRED_TPB) void predict_kernel(
         m += n.value;
     }
     out[row] = mode == PRED_SIGMOID ? fb_sigmoid(m) : m;
+}
+
+__global__ __launch_bounds__(PRED_TPB) void predict_kernel(
+    const PredNodeDev *__restrict__ nodes, const ShapNodeDev *__restrict__ full,
+    const uint32_t *__restrict__ cats, const uint32_t *__restrict__ roots, uint32_t n_trees,
+    const float *__restrict__ rows, uint64_t n_rows, uint32_t nf, const float *__restrict__ init,
+    float base, uint32_t mode, float *__restrict__ out) {
+    const uint64_t row = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= n_rows) return;
+    predict_row(nodes, full, cats, roots, n_trees, rows + row * nf, row, init, base, mode, out);
+}
+
+// The same walk with a wave's 64 rows first copied into LDS (coalesced
+// loads; row stride nf | 1, odd, so the 64 lanes' cells of one feature fall
+// in distinct banks): a node's cell is then an LDS read instead of a
+// gather of one cache line a lane from the row-major matrix.
+constexpr uint32_t PRED_LDS_ROWS = 64;
+constexpr uint32_t PRED_LDS_MAX_F = 255;  // 64 rows x 256 floats: 64 KiB of LDS
+
+__global__ __launch_bounds__(PRED_LDS_ROWS) void predict_lds_kernel(
+    const PredNodeDev *__restrict__ nodes, const ShapNodeDev *__restrict__ full,
+    const uint32_t *__restrict__ cats, const uint32_t *__restrict__ roots, uint32_t n_trees,
+    const float *__restrict__ rows, uint64_t n_rows, uint32_t nf, const float *__restrict__ init,
+    float base, uint32_t mode, float *__restrict__ out) {
+    extern __shared__ float xs[];
+    const uint32_t S = nf | 1u;
+    const uint64_t r0 = (uint64_t)blockIdx.x * PRED_LDS_ROWS;
+    const uint32_t nr = (uint32_t)min<uint64_t>(PRED_LDS_ROWS, n_rows - r0);
+    const float *src = rows + r0 * nf;
+    for (uint32_t r = 0; r < nr; r++)
+        for (uint32_t f = threadIdx.x; f < nf; f += PRED_LDS_ROWS) xs[r * S + f] = src[r * nf + f];
+    __syncthreads();
+    if (threadIdx.x >= nr) return;
+    predict_row(nodes, full, cats, roots, n_trees, xs + threadIdx.x * S, r0 + threadIdx.x, init,
+                base, mode, out);
+}
+
+// The LDS rows shared by four waves, which take every fourth tree of a run
+// of PRED_RUN trees and put each row's leaf value in LDS; wave 0 then adds
+// the run's values to the row's margin in tree order (the host's f32
+// additions, so the margins stay bit-identical), and the waves go on to the
+// next run. Four times the waves of predict_lds_kernel on the same rows.
+constexpr uint32_t PRED_WAVES = 4;
+constexpr uint32_t PRED_RUN = 32;
+constexpr uint32_t PRED_LDS4_MAX_F = 223;  // 64 x 224 + 64 x 32 floats: 64 KiB of LDS
+
+__global__ __launch_bounds__(PRED_LDS_ROWS * PRED_WAVES) void predict_lds4_kernel(
+    const PredNodeDev *__restrict__ nodes, const ShapNodeDev *__restrict__ full,
+    const uint32_t *__restrict__ cats, const uint32_t *__restrict__ roots, uint32_t n_trees,
+    const float *__restrict__ rows, uint64_t n_rows, uint32_t nf, const float *__restrict__ init,
+    float base, uint32_t mode, float *__restrict__ out) {
+    extern __shared__ float xs[];
+    const uint32_t S = nf | 1u;
+    float *leafv = xs + PRED_LDS_ROWS * S;  // [PRED_RUN][64]
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint64_t r0 = (uint64_t)blockIdx.x * PRED_LDS_ROWS;
+    const uint32_t nr = (uint32_t)min<uint64_t>(PRED_LDS_ROWS, n_rows - r0);
+    const float *src = rows + r0 * nf;
+    for (uint32_t r = wave; r < nr; r += PRED_WAVES)
+        for (uint32_t f = lane; f < nf; f += 64) xs[r * S + f] = src[r * nf + f];
+    __syncthreads();
+    const bool live = lane < nr;
+    const uint64_t row = r0 + lane;
+    const float *x = xs + lane * S;
+    float m = 0.0f;
+    if (wave == 0 && live) m = init ? init[row] : base;
+    for (uint32_t t0 = 0; t0 < n_trees; t0 += PRED_RUN) {
+        const uint32_t t1 = min(t0 + PRED_RUN, n_trees);
+        if (live)
+            for (uint32_t t = t0 + wave; t < t1; t += PRED_WAVES) {
+                const uint32_t root = roots[t];
+                uint32_t id = root;
+                PredNodeDev n = nodes[id];
+                while (!(n.ff & PN_LEAF)) {
+                    id = walk_step(n, id, x, full, cats);
+                    n = nodes[id];
+                }
+                if (mode == PRED_LEAF) out[row * n_trees + t] = (float)(id - root);
+                else leafv[(t - t0) * 64 + lane] = n.value;
+            }
+        if (mode == PRED_LEAF) continue;
+        __syncthreads();
+        if (wave == 0 && live)
+            for (uint32_t t = t0; t < t1; t++) m += leafv[(t - t0) * 64 + lane];
+        __syncthreads();
+    }
+    if (mode != PRED_LEAF && wave == 0 && live)
+        out[row] = mode == PRED_SIGMOID ? fb_sigmoid(m) : m;
 }
 
 // saabas_row (src/model/explain.rs:730-760): along the row's path, each split
@@ -850,9 +940,26 @@ void enqueue(fbh_shap_model *m, Kind k, const float *d_rows, uint64_t n, const f
         default: {
             const uint32_t mode = k == Kind::Leaf ? PRED_LEAF
                                   : k == Kind::Value ? PRED_SIGMOID : PRED_MARGIN;
-            hipLaunchKernelGGL(predict_kernel, dim3(blocks), dim3(PRED_TPB), 0, m->stream,
-                               m->d_pred, m->d_nodes, m->d_cats, m->d_roots, m->n_trees, d_rows, n,
-                               m->n_features, d_margin, m->bias, mode, d_out);
+            const uint32_t nf = m->n_features;
+            const char *kind_env = std::getenv("FB_HIP_PREDICT_KERNEL");
+            const int pk = kind_env ? std::atoi(kind_env) : 4;
+            if (pk == 4 && nf >= 1 && nf <= PRED_LDS4_MAX_F) {
+                const uint32_t lb = (uint32_t)((n + PRED_LDS_ROWS - 1) / PRED_LDS_ROWS);
+                hipLaunchKernelGGL(predict_lds4_kernel, dim3(lb), dim3(PRED_LDS_ROWS * PRED_WAVES),
+                                   (size_t)PRED_LDS_ROWS * ((nf | 1u) + PRED_RUN) * 4, m->stream,
+                                   m->d_pred, m->d_nodes, m->d_cats, m->d_roots, m->n_trees,
+                                   d_rows, n, nf, d_margin, m->bias, mode, d_out);
+            } else if (pk >= 1 && nf >= 1 && nf <= PRED_LDS_MAX_F) {
+                const uint32_t lb = (uint32_t)((n + PRED_LDS_ROWS - 1) / PRED_LDS_ROWS);
+                hipLaunchKernelGGL(predict_lds_kernel, dim3(lb), dim3(PRED_LDS_ROWS),
+                                   (size_t)PRED_LDS_ROWS * (nf | 1u) * 4, m->stream, m->d_pred,
+                                   m->d_nodes, m->d_cats, m->d_roots, m->n_trees, d_rows, n, nf,
+                                   d_margin, m->bias, mode, d_out);
+            } else {
+                hipLaunchKernelGGL(predict_kernel, dim3(blocks), dim3(PRED_TPB), 0, m->stream,
+                                   m->d_pred, m->d_nodes, m->d_cats, m->d_roots, m->n_trees, d_rows,
+                                   n, nf, d_margin, m->bias, mode, d_out);
+            }
             chk(hipGetLastError(), "predict launch");
             return;
         }

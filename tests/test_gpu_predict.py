@@ -167,3 +167,24 @@ def test_squared_error_values_are_margins(fb, oracle):
     om, pm, x = _trained(fb, oracle, 81, objective="reg:squarederror")
     rows = x[:1000]
     assert np.array_equal(_bits(pm.predict(rows)), _bits(om.predict_margin(rows)))
+
+
+@pytest.mark.parametrize("nf", [7, 222, 240, 300])
+def test_prediction_kernels_by_row_width(fb, oracle, nf):
+    """The row width picks the walk: up to 223 features four waves share the
+    rows staged in LDS (and add each run of trees' leaf values in tree
+    order), up to 255 one wave stages them, wider rows are read in place.
+    Every one gives the oracle's margins and leaf ids, bit for bit, also for
+    a row count that leaves a partial last block and more trees than one run
+    of 32."""
+    om, pm, x = _trained(fb, oracle, 90 + nf, n=3001, nf=nf, rounds=37, depth=4)
+    margin = pm.predict(x, output_margin=True)
+    assert np.array_equal(_bits(margin), _bits(om.predict_margin(x)))
+    leaf = om.explain(x, "leaf").astype(np.int64)
+    assert np.array_equal(pm.predict(x, pred_leaf=True), leaf)
+    # a per-row base margin, then every tree's leaf in tree order (f32 adds)
+    acc = np.linspace(-1, 1, x.shape[0]).astype(np.float32)
+    got = pm.predict(x, output_margin=True, base_margin=acc.copy())
+    for t, tr in enumerate(om.trees()):
+        acc = (acc + tr["leaf_value"][leaf[:, t]]).astype(np.float32)
+    assert np.array_equal(_bits(got), _bits(acc))
