@@ -343,7 +343,7 @@ struct fbh_ctx {
            tables_bytes = 0;
     PackTileDev *d_pack = nullptr;  // the packed tiles' sources (tree tables)
     uint32_t *d_split_order = nullptr;  // tree features: numeric positions, then categorical
-    uint32_t n_split_num = 0, n_split_cat = 0;
+    uint32_t n_split_num = 0, n_split_wide = 0, n_split_cat = 0;
     size_t stage_bytes = 0;
     uint64_t max_chunks = 0;    // capacity of the partition chunk arrays
     uint64_t cat_in_words = 0;  // capacity of the partition category words
@@ -2377,15 +2377,23 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
         // The tables go up only when they differ from the last tree's (every
         // tree of a run without column sampling has the same).
         // Split-scan order: numeric features of at most 256 bins (one wave
-        // each, four bins a lane), then the others (one workgroup each).
-        auto by_wave = [&](uint32_t j) { return !sf[j].categorical && sf[j].n_bins <= 256; };
+        // each, four bins a lane), numeric ones of at most 1024 (one wave
+        // each, sixteen bins a lane), then the others (one workgroup each).
+        auto group = [&](uint32_t j) {
+            if (sf[j].categorical || sf[j].n_bins > 1024) return 2;
+            return sf[j].n_bins <= 256 ? 0 : 1;
+        };
         std::vector<uint32_t> order;
-        for (uint32_t j = 0; j < sf.size(); j++)
-            if (by_wave(j)) order.push_back(j);
-        c->n_split_num = (uint32_t)order.size();
-        for (uint32_t j = 0; j < sf.size(); j++)
-            if (!by_wave(j)) order.push_back(j);
-        c->n_split_cat = (uint32_t)(order.size() - c->n_split_num);
+        uint32_t counts[3] = {0, 0, 0};
+        for (int k = 0; k < 3; k++)
+            for (uint32_t j = 0; j < sf.size(); j++)
+                if (group(j) == k) {
+                    order.push_back(j);
+                    counts[k]++;
+                }
+        c->n_split_num = counts[0];
+        c->n_split_wide = counts[1];
+        c->n_split_cat = counts[2];
         // Packed tiles' sources: 16 columns each (null for an empty cell).
         std::vector<PackTileDev> pk;
         for (const auto &t : c->pack_tiles) {
@@ -2529,7 +2537,7 @@ struct EvalPlan {
 // them); with small slots its few waves a pair (four features a workgroup)
 // leave the device idler than three launches.
 bool pair_pass_ok(const fbh_ctx *c) {
-    return c->pair_pass && c->n_split_cat == 0 && c->n_split_num > 0 &&
+    return c->pair_pass && c->n_split_cat == 0 && c->n_split_wide == 0 && c->n_split_num > 0 &&
            c->hist_width * 16 >= PAIR_PASS_MIN_SLOT_BYTES;
 }
 
@@ -2666,7 +2674,8 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
               "pair reduction, subtraction and split scan");
     else
         check(launch_split_feats(c->hist, c->hist_width, E.sn, E.n_nodes, c->d_sfeats,
-                                 c->d_split_order, c->n_split_num, c->n_split_cat, E.enabled, P,
+                                 c->d_split_order, c->n_split_num, c->n_split_wide,
+                                 c->n_split_cat, E.enabled, P,
                                  c->d_cands, c->d_cat_scratch, E.dev_n_nodes, c->stream),
               "split scan");
     const uint32_t cw = std::max(1u, c->cat_words_per_node);

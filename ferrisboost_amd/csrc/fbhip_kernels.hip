@@ -1243,18 +1243,20 @@ __device__ __forceinline__ Best wave_best(Best b) {
 // numeric scan of split_feat_kernel on 64 lanes with shuffles only (no
 // barriers). Each lane takes a run of bins; integer prefix sums are exact in
 // any order, and the argmax keeps the reference's tie rule.
-// Bins of a numeric feature of at most 256 bins held by one wave: lane l
-// holds bins [l * per, l * per + per) in registers.
+// Bins of a numeric feature held by one wave: lane l holds bins
+// [l * per, l * per + per) in registers, per = ceil(bins / 64) at most
+// NUM_PER_LANE (features of at most 256 bins) or WIDE_PER_LANE (at most 1024).
 constexpr uint32_t NUM_PER_LANE = 4;
+constexpr uint32_t WIDE_PER_LANE = 16;
 
 // The split scan of one (node, feature) over bins in the wave's registers
 // (g[k], h[k] of bin b0 + k): prefix sums, the forward candidates (missing
 // rows right), the reverse ones (missing rows left; skipped when the bins
 // hold the whole node) and the first best by the reference's rules, written
 // to outc by lane 0.
-__device__ __forceinline__ void scan_numeric(const int64_t (&g)[NUM_PER_LANE],
-                                             const int64_t (&h)[NUM_PER_LANE], uint32_t b0,
-                                             uint32_t b1, uint32_t n, uint32_t lane,
+template <uint32_t PER>
+__device__ __forceinline__ void scan_numeric(const int64_t (&g)[PER], const int64_t (&h)[PER],
+                                             uint32_t b0, uint32_t b1, uint32_t n, uint32_t lane,
                                              const SplitNodeDev &N, const SplitFeatDev &F,
                                              const SplitParamsDev &P, FeatCandDev *outc) {
     const double ng = (double)N.sum_g * P.inv_g, nh = (double)N.sum_h * P.inv_h;
@@ -1262,7 +1264,7 @@ __device__ __forceinline__ void scan_numeric(const int64_t (&g)[NUM_PER_LANE],
                                                                 N.upper), P);
     int64_t tg = 0, th = 0;
 #pragma unroll
-    for (uint32_t k = 0; k < NUM_PER_LANE; k++)
+    for (uint32_t k = 0; k < PER; k++)
         if (b0 + k < b1) {
             tg = wadd(tg, g[k]);
             th = wadd(th, h[k]);
@@ -1276,7 +1278,7 @@ __device__ __forceinline__ void scan_numeric(const int64_t (&g)[NUM_PER_LANE],
     // Forward: missing rows go right.
     int64_t lg = eg, lh = eh;
 #pragma unroll
-    for (uint32_t k = 0; k < NUM_PER_LANE; k++) {
+    for (uint32_t k = 0; k < PER; k++) {
         if (b0 + k >= b1) break;
         lg = wadd(lg, g[k]);
         lh = wadd(lh, h[k]);
@@ -1289,7 +1291,7 @@ __device__ __forceinline__ void scan_numeric(const int64_t (&g)[NUM_PER_LANE],
     if (!(totg == N.sum_g && toth == N.sum_h)) {
         int64_t rg = wsub(wsub(totg, eg), tg), rh = wsub(wsub(toth, eh), th);
 #pragma unroll
-        for (int k = NUM_PER_LANE - 1; k >= 0; k--) {
+        for (int k = PER - 1; k >= 0; k--) {
             if (b0 + k >= b1) continue;
             rg = wadd(rg, g[k]);
             rh = wadd(rh, h[k]);
@@ -1315,16 +1317,15 @@ __device__ __forceinline__ void scan_numeric(const int64_t (&g)[NUM_PER_LANE],
     }
 }
 
-// One wave per (node, numeric feature of at most 256 bins), four features a
-// workgroup: the feature's bins into registers, then scan_numeric.
-__global__ __launch_bounds__(256) void split_num_kernel(
-    const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
-    const SplitFeatDev *feats, const uint32_t *order, uint32_t n_num, const uint8_t *enabled,
-    SplitParamsDev P, FeatCandDev *cands, const uint32_t *dev_n) {
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t li = blockIdx.x * 4 + wave, ni = blockIdx.y;
-    if (dev_n && ni >= *dev_n) return;
-    if (li >= n_num) return;  // a whole wave
+// One wave's (node, numeric feature of at most 64 * PER bins): the
+// feature's bins into registers, then scan_numeric. li indexes order.
+template <uint32_t PER>
+__device__ __forceinline__ void split_num_wave(const int64_t *hist, uint64_t hist_width,
+                                               const SplitNodeDev *nodes,
+                                               const SplitFeatDev *feats, const uint32_t *order,
+                                               uint32_t li, uint32_t ni, const uint8_t *enabled,
+                                               SplitParamsDev P, FeatCandDev *cands) {
+    const uint32_t lane = threadIdx.x & 63u;
     load_scales(P);
     const uint32_t j = order[li];
     const SplitFeatDev F = feats[j];
@@ -1336,15 +1337,27 @@ __global__ __launch_bounds__(256) void split_num_kernel(
     }
     const int64_t *hp = hist + ((uint64_t)N.slot * hist_width + F.hist_off) * 2u;
     const uint32_t n = F.n_bins;
-    const uint32_t per = (n + 63) / 64;  // at most NUM_PER_LANE
+    const uint32_t per = (n + 63) / 64;  // at most PER
     const uint32_t b0 = min(lane * per, n), b1 = min(b0 + per, n);
-    int64_t g[NUM_PER_LANE], h[NUM_PER_LANE];
+    int64_t g[PER], h[PER];
 #pragma unroll
-    for (uint32_t k = 0; k < NUM_PER_LANE; k++) {
+    for (uint32_t k = 0; k < PER; k++) {
         g[k] = b0 + k < b1 ? hp[2 * (b0 + k)] : 0;
         h[k] = b0 + k < b1 ? hp[2 * (b0 + k) + 1] : 0;
     }
-    scan_numeric(g, h, b0, b1, n, lane, N, F, P, outc);
+    scan_numeric<PER>(g, h, b0, b1, n, lane, N, F, P, outc);
+}
+
+// One wave per (node, numeric feature of at most 256 bins), four features a
+// workgroup.
+__global__ __launch_bounds__(256) void split_num_kernel(
+    const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
+    const SplitFeatDev *feats, const uint32_t *order, uint32_t n_num, const uint8_t *enabled,
+    SplitParamsDev P, FeatCandDev *cands, const uint32_t *dev_n) {
+    const uint32_t li = blockIdx.x * 4 + (threadIdx.x >> 6), ni = blockIdx.y;
+    if (dev_n && ni >= *dev_n) return;
+    if (li >= n_num) return;  // a whole wave
+    split_num_wave<NUM_PER_LANE>(hist, hist_width, nodes, feats, order, li, ni, enabled, P, cands);
 }
 
 // Reduction, subtraction and split scan of one evaluated pair in one pass,
@@ -1447,8 +1460,8 @@ __global__ __launch_bounds__(256) void split_pair_kernel(
             if (lane == 0) outc->found = 0;
             continue;
         }
-        if (N.slot == H.slot) scan_numeric(sg, sh, b0, b1, n, lane, N, F, P, outc);
-        else scan_numeric(bg, bh, b0, b1, n, lane, N, F, P, outc);
+        if (N.slot == H.slot) scan_numeric<NUM_PER_LANE>(sg, sh, b0, b1, n, lane, N, F, P, outc);
+        else scan_numeric<NUM_PER_LANE>(bg, bh, b0, b1, n, lane, N, F, P, outc);
     }
 }
 
@@ -1468,17 +1481,29 @@ hipError_t launch_split_pairs(int64_t *hist, uint64_t hist_width, const int64_t 
 // One workgroup per (feature, node): prefix sums of the feature's bins, the
 // forward (missing right) and reverse (missing left, only when the node has
 // missing mass) candidates, and the first best by the reference's rules.
+// Workgroups past the n_block one-workgroup features take the n_wide
+// numeric features of at most 1024 bins that follow order[wide_off], one
+// wave each (split_num_wave with sixteen bins a lane), in the same launch:
+// the two kinds then overlap instead of running one after the other.
 __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
     const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
-    const SplitFeatDev *feats, const uint32_t *order, uint32_t order_off, const uint8_t *enabled,
-    SplitParamsDev P, FeatCandDev *cands, uint64_t *cat_scratch, const uint32_t *dev_n) {
+    const SplitFeatDev *feats, const uint32_t *order, uint32_t order_off, uint32_t n_block,
+    uint32_t wide_off, uint32_t n_wide, const uint8_t *enabled, SplitParamsDev P,
+    FeatCandDev *cands, uint64_t *cat_scratch, const uint32_t *dev_n) {
     __shared__ Best shb[SPLIT_TPB];
     __shared__ int64_t sg[SPLIT_TPB], shh[SPLIT_TPB];
     extern __shared__ unsigned char dyn[];
-    load_scales(P);
 
     const uint32_t ni = blockIdx.y, tid = threadIdx.x;
     if (dev_n && ni >= *dev_n) return;
+    if (blockIdx.x >= n_block) {
+        const uint32_t li = (blockIdx.x - n_block) * 4 + (tid >> 6);
+        if (li < n_wide)
+            split_num_wave<WIDE_PER_LANE>(hist, hist_width, nodes, feats, order + wide_off, li, ni,
+                                          enabled, P, cands);
+        return;
+    }
+    load_scales(P);
     const uint32_t j = order[order_off + blockIdx.x];
     const SplitFeatDev F = feats[j];
     const SplitNodeDev N = nodes[ni];
@@ -1556,19 +1581,20 @@ __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
 
 hipError_t launch_split_feats(const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
                               uint32_t n_nodes, const SplitFeatDev *feats, const uint32_t *order,
-                              uint32_t n_num, uint32_t n_cat, const uint8_t *enabled,
-                              SplitParamsDev P, FeatCandDev *cands, uint64_t *cat_scratch,
-                              const uint32_t *dev_n, hipStream_t s) {
+                              uint32_t n_num, uint32_t n_wide, uint32_t n_cat,
+                              const uint8_t *enabled, SplitParamsDev P, FeatCandDev *cands,
+                              uint64_t *cat_scratch, const uint32_t *dev_n, hipStream_t s) {
     if (n_nodes == 0 || P.n_feats == 0) return hipSuccess;
     if (n_num)
         hipLaunchKernelGGL(split_num_kernel, dim3((n_num + 3) / 4, n_nodes), dim3(256), 0, s, hist,
                            hist_width, nodes, feats, order, n_num, enabled, P, cands, dev_n);
-    if (n_cat) {
+    if (n_wide || n_cat) {
         const size_t dyn = P.cat_words_per_node
                                ? (sizeof(float) + sizeof(uint32_t)) * MAX_DEVICE_CATS
                                : 0;
-        hipLaunchKernelGGL(split_feat_kernel, dim3(n_cat, n_nodes), dim3(SPLIT_TPB), dyn, s, hist,
-                           hist_width, nodes, feats, order, n_num, enabled, P, cands, cat_scratch,
+        hipLaunchKernelGGL(split_feat_kernel, dim3(n_cat + (n_wide + 3) / 4, n_nodes),
+                           dim3(SPLIT_TPB), dyn, s, hist, hist_width, nodes, feats, order,
+                           n_num + n_wide, n_cat, n_num, n_wide, enabled, P, cands, cat_scratch,
                            dev_n);
     }
     return hipGetLastError();
