@@ -55,8 +55,8 @@ VALU_PEAK_TOPS = 39.3
 # SQ_INSTS_VALU x 64 / rows for shap_rec_kernel on the shap workload.
 SHAP_VALU_OPS_PER_ROW = 11.23e6
 # Prediction of the same ensemble: VALU lane-operations a row (SQ_INSTS_VALU x 64 / rows
-# for predict_kernel on the predict workload).
-PREDICT_VALU_OPS_PER_ROW = 11010
+# for predict_lds4_kernel on the predict workload).
+PREDICT_VALU_OPS_PER_ROW = 11934
 # MI355X fp32 vector peak (FMA counted as two operations).
 FP32_PEAK_TFLOPS = 157.3
 # QuadratureTreeSHAP's arithmetic (8 quadrature points): for each child edge of an
