@@ -26,6 +26,7 @@ from typing import Any, Mapping
 import numpy as np
 
 from . import _native as N
+from . import frame_rows
 
 __all__ = ["train", "sketch", "Cuts", "Model", "device_available", "__version__"]
 __version__ = "0.1.0"
@@ -580,6 +581,12 @@ class Model:
             X = arrow_rows.table_matrix(data, getattr(self, "_feature_names", None),
                                         getattr(self, "_categories", None), self.n_features,
                                         float("nan"))
+        elif frame_rows.is_frame(data):
+            df = frame_rows.select_columns(data, getattr(self, "_feature_names", None))
+            is_cat = N.train_lib().fbt_model_is_categorical
+            flags = [bool(is_cat(self._h, f)) for f in range(self.n_features)]
+            X = frame_rows.frame_matrix(df, True, getattr(self, "_categories", None),
+                                        what="predict data", scoring=True, categorical=flags)[0]
         else:
             X = np.asarray(data, dtype=np.float32)
         if X.ndim != 2 or X.shape[1] != self.n_features:
@@ -751,6 +758,27 @@ def sketch(X, max_bin: int = 255, weight=None, feature_types=None,
     return Cuts(vals[: offs[-1]].copy(), offs, max_bin, cat)
 
 
+def _monotone(mc, names: list[str] | None) -> np.ndarray | None:
+    """monotone_constraints -> one int8 sign per feature (None for none): a
+    "(1,0,-1)" string, a sequence, or a {column name: sign} mapping for
+    inputs with column names (python/ferrisboost/__init__.py:422-426)."""
+    if not mc:
+        return None
+    if isinstance(mc, Mapping):
+        if names is None:
+            raise ValueError("monotone_constraints given by column name needs column names: a "
+                             "numpy array has none; use a positional tuple, or a DataFrame, a "
+                             "pyarrow Table or a Parquet file")
+        unknown = [k for k in mc if k not in names]
+        if unknown:
+            raise ValueError(f"monotone_constraints columns {unknown} are not feature columns; "
+                             f"feature columns: {names}")
+        mc = [mc.get(n, 0) for n in names]
+    elif isinstance(mc, str):
+        mc = [int(v) for v in mc.strip("()").split(",") if v.strip()]
+    return np.ascontiguousarray([int(np.sign(v)) for v in mc], np.int8)
+
+
 def _arrow_input(data) -> bool:
     from . import arrow_rows
 
@@ -777,12 +805,7 @@ def _train_arrow(p: dict[str, Any], data, label, weight, cuts, base_margin) -> M
     src = arrow_rows.ArrowRows(data, label, weight, p["enable_categorical"], p["missing"])
     types = arrow_rows.feature_types_of(src, p["feature_types"])
     cat = _categorical_flags(types, src.n_features)
-    mono = None
-    mc = p["monotone_constraints"]
-    if mc:
-        if isinstance(mc, str):
-            mc = [int(v) for v in mc.strip("()").split(",") if v.strip()]
-        mono = np.ascontiguousarray([int(np.sign(v)) for v in mc], np.int8)
+    mono = _monotone(p["monotone_constraints"], list(src.features))
     bm = None if base_margin is None else _as_base_margin(base_margin, src.n_rows, _n_outputs(p))
     s = _params_struct(p, src.n_features, list(src.features), bm)
     h = C.c_void_p()
@@ -838,8 +861,10 @@ def train(params: Mapping[str, Any], data, label=None, num_boost_round: int = 10
     (python/ferrisboost/__init__.py:1090-1114): train(params, data, label,
     num_boost_round, evals, ...).
 
-    data is a 2-D array (label, weight and base_margin arrays), a .parquet
-    path (label and weight name columns) or a pyarrow Table /
+    data is a 2-D array (label, weight and base_margin arrays), a pandas
+    DataFrame (category columns need params["enable_categorical"]; the
+    column names become the feature names, which predict() binds by), a
+    .parquet path (label and weight name columns) or a pyarrow Table /
     RecordBatchReader (label and weight name columns or are arrays; the
     other columns are the features, streamed to the device in chunks for the
     sketch and the binning). base_margin gives every row's starting raw
@@ -869,6 +894,11 @@ def train(params: Mapping[str, Any], data, label=None, num_boost_round: int = 10
         return _train_arrow(p, data, label, weight, cuts, base_margin)
     if label is None:
         raise ValueError("label is required for array inputs")
+    names = lists = None
+    if frame_rows.is_frame(data):
+        data, names, auto, lists = frame_rows.frame_matrix(data, p["enable_categorical"])
+        if p["feature_types"] is None and any(auto):
+            p["feature_types"] = ["c" if f else "q" for f in auto]
     X = _matrix(data, p["missing"])
     y = np.ascontiguousarray(np.asarray(label, dtype=np.float32))
     if y.shape != (X.shape[0],):
@@ -877,14 +907,9 @@ def train(params: Mapping[str, Any], data, label=None, num_boost_round: int = 10
     if w is not None and w.shape != (X.shape[0],):
         raise ValueError("weight must have one value per row")
     cat = _categorical_flags(p["feature_types"], X.shape[1])
-    mono = None
-    mc = p["monotone_constraints"]
-    if mc:
-        if isinstance(mc, str):
-            mc = [int(v) for v in mc.strip("()").split(",") if v.strip()]
-        mono = np.ascontiguousarray([int(np.sign(v)) for v in mc], np.int8)
+    mono = _monotone(p["monotone_constraints"], names)
     bm = None if base_margin is None else _as_base_margin(base_margin, X.shape[0], _n_outputs(p))
-    s = _params_struct(p, X.shape[1], None, bm)
+    s = _params_struct(p, X.shape[1], names, bm)
     h = C.c_void_p()
     L = N.train_lib()
     if cuts is None:
@@ -899,6 +924,10 @@ def train(params: Mapping[str, Any], data, label=None, num_boost_round: int = 10
             0 if mono is None else mono.size, C.byref(s), N.ptr(cuts.values), N.ptr(cuts.offsets),
             C.byref(h)))
     m = Model(h, X.shape[1], p["objective"], s.device)
+    if names is not None:
+        m._feature_names = names
+        kept = [c if (cat is not None and cat[j]) else None for j, c in enumerate(lists)]
+        m._categories = kept if any(c is not None for c in kept) else None
     st = N.Stats()
     N.check_train(L.fbt_last_stats(C.byref(st)))
     m.stats = {k: getattr(st, k) for k, _ in N.Stats._fields_}

@@ -4,8 +4,8 @@ model that training from the same rows as a numpy matrix gives, byte for
 byte: unit weights (streamed), weighted rows (gathered for the host sketch),
 string dictionary columns as categorical features coded by category
 whatever each chunk's dictionary, a feature the device sketch
-leaves to the host (zeros of both signs among its cuts), and a reader error
-raised back to the caller."""
+leaves to the host (zeros of both signs among its cuts), a reader error
+raised back to the caller, and a pandas DataFrame with a category column."""
 
 from __future__ import annotations
 
@@ -164,3 +164,37 @@ def test_reader_rows_take_8bit_cells_as_arrays_do(fb):
     m_wide = fb.train(dict(p, hip_host_sketch=True), np.ascontiguousarray(x), y,
                       num_boost_round=4)
     assert m_wide.stats["planned_bytes"] == m_arr.stats["planned_bytes"]
+
+
+def test_dataframe_trains_the_array_model(fb):
+    """A pandas DataFrame trains the model its float32 matrix trains (category
+    columns as their positions in `categories`, feature names from the
+    columns), and prediction binds columns by name and re-codes categories
+    by value."""
+    pd = pytest.importorskip("pandas")
+    x, codes, y, w = _data(n=20_000, seed=5)
+    names = ["rome", "oslo", "lima", "kyiv", "doha", "baku", "riga"]
+    df = pd.DataFrame({f"f{j}": x[:, j] for j in range(6)})
+    df["c"] = pd.Categorical.from_codes(codes, names)
+    p = dict(PARAMS, enable_categorical=True)
+    m_df = fb.train(p, df, y, num_boost_round=5, weight=w)
+    arr = np.ascontiguousarray(np.column_stack([x, codes.astype(np.float32)]))
+    m_arr = fb.train(dict(PARAMS, feature_types=["q"] * 6 + ["c"]), arr, y, num_boost_round=5,
+                     weight=w)
+    assert m_df.feature_names == list(df.columns)
+    assert m_df.get_categories()[6] == names
+    assert m_df.to_json() == m_arr.to_json()
+    assert np.array_equal(m_df.predict(df, output_margin=True),
+                          m_arr.predict(arr, output_margin=True))
+    shuffled = df.assign(c=df["c"].cat.reorder_categories(names[::-1]), extra=0.0)
+    shuffled = shuffled[["extra", "c"] + [f"f{j}" for j in range(5, -1, -1)]]
+    assert np.array_equal(m_df.predict(shuffled, output_margin=True),
+                          m_arr.predict(arr, output_margin=True))
+    # monotone constraints by column name
+    m_mono = fb.train(dict(p, monotone_constraints={"f0": 1}), df, y, num_boost_round=3)
+    m_mono_arr = fb.train(dict(PARAMS, feature_types=["q"] * 6 + ["c"],
+                               monotone_constraints=(1, 0, 0, 0, 0, 0, 0)), arr, y,
+                          num_boost_round=3)
+    assert m_mono.to_json() == m_mono_arr.to_json()
+    with pytest.raises(ValueError, match="enable_categorical"):
+        fb.train(PARAMS, df, y, num_boost_round=1)
