@@ -682,6 +682,36 @@ __device__ __forceinline__ uint32_t block_scan_1024(uint32_t v, uint32_t *buf, u
     return block_scan(v, buf, total);
 }
 
+// N exclusive block scans behind the same three barriers: v[k] becomes its
+// prefix, total[k] the sum (buf[k] needs 32 entries).
+template <int N>
+__device__ void block_scan_n(uint32_t (&v)[N], uint32_t (*buf)[32], uint32_t (&total)[N]) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t nw = blockDim.x >> 6;
+    uint32_t incl[N];
+#pragma unroll
+    for (int k = 0; k < N; k++) {
+        incl[k] = wave_incl_scan(v[k]);
+        if (lane == 63) buf[k][wave] = incl[k];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int k = 0; k < N; k++) {
+            const uint32_t w = wave_incl_scan(lane < nw ? buf[k][lane] : 0u);
+            if (lane < nw) buf[k][16 + lane] = w;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < N; k++) {
+        const uint32_t before = wave ? buf[k][16 + wave - 1] : 0u;
+        total[k] = buf[k][16 + nw - 1];
+        v[k] = before + incl[k] - v[k];
+    }
+    __syncthreads();
+}
+
 // block_scan of 64-bit values (two packed 32-bit counters scan together
 // when neither total overflows); buf needs 32 entries.
 __device__ uint64_t block_scan_u64(uint64_t v, uint64_t *buf, uint64_t &total) {
@@ -713,40 +743,61 @@ __device__ uint64_t block_scan_u64(uint64_t v, uint64_t *buf, uint64_t &total) {
 
 // One workgroup plans the children of a fused partition + evaluation step
 // from the partition's left counts (see launch_level_plan).
-// Loads a caller issued early for level_plan_body: the state's counts and
-// the thread's first pair.
+// Loads a caller issued early for level_plan_body: the state's counts, the
+// totals its last step adds to, and the thread's first pair.
 struct PlanPrefetch {
     bool valid;
-    uint32_t n, leaf_base;
+    uint32_t n, leaf_base, n_eval, hist_nodes;
+    uint64_t hist_rows;
     PairDev first;
 };
+
+__device__ __forceinline__ void prefetch_state(PlanPrefetch &pre, const GrowState *st) {
+    pre.n = st->n_split;
+    pre.leaf_base = st->n_leaves;
+    pre.n_eval = st->n_eval;
+    pre.hist_nodes = st->hist_nodes;
+    pre.hist_rows = st->hist_rows;
+}
+
+// Sum of v over the block with one barrier: wave sums by shuffles, then
+// every thread adds the wave sums. buf holds 16 entries; a caller summing
+// again before another barrier passes a different buf.
+template <typename T>
+__device__ __forceinline__ T block_sum(T v, T *buf) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63u) == 0) buf[threadIdx.x >> 6] = v;
+    __syncthreads();
+    T t = 0;
+    for (uint32_t w = 0; w < (blockDim.x >> 6); w++) t += buf[w];
+    return t;
+}
 
 __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t *totals,
                                 ChunkRule rule, HistNodeDev *hn, SplitNodeDev *sn,
                                 uint32_t *spans, uint32_t *left_slot, uint32_t *chunk_rows_out,
                                 const GrowDevOut &D, const PlanPrefetch &pre) {
-    __shared__ uint32_t buf[1024];
-    __shared__ unsigned long long acc_sh, acc_nodes_sh;
-    __shared__ uint64_t buf64[32];
-    __shared__ uint32_t cr_sh, nz_sh;
+    __shared__ uint32_t buf3[3][32];
+    __shared__ uint64_t sum64[2][16];
+    __shared__ uint32_t sum32[2][16];
+    __shared__ uint32_t cr_sh;
     // A device-grown tree: the pair count and the leaf table base come from
     // its state (read by every thread before thread 0 updates it).
     uint32_t leaf_base = 0;
+    PlanPrefetch late{};
     if (pre.valid) {
         n = pre.n;
         leaf_base = pre.leaf_base;
     } else if (D.st) {
-        n = D.st->n_split;
-        leaf_base = D.st->n_leaves;
+        prefetch_state(late, D.st);
+        n = late.n;
+        leaf_base = late.leaf_base;
     }
+    const PlanPrefetch &S = pre.valid ? pre : late;
     auto pair_at = [&](uint32_t i) -> PairDev {
         return (pre.valid && i == threadIdx.x) ? pre.first : pairs[i];
     };
-    if (threadIdx.x == 0) {
-        acc_sh = acc_nodes_sh = 0;
-        nz_sh = 0;
-    }
-    __syncthreads();
     // Spans of every pair and the rows the evaluated pairs accumulate. The
     // thread's first pair (all of them when n <= 1024) stays in registers:
     // left count, and the accumulated (smaller) child's rows when evaluated.
@@ -776,9 +827,9 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
         const uint32_t nl = P.req == NO_SLOT ? 0u : totals[P.req];
         return min(nl, P.row_len - nl);
     };
-    atomicAdd(&acc_sh, acc);
-    if (nz) atomicAdd(&nz_sh, nz);
-    __syncthreads();
+    const uint64_t acc_all = block_sum<uint64_t>(acc, sum64[0]);
+    const uint32_t n_nz = block_sum<uint32_t>(nz, sum32[0]);  // evaluated pairs whose
+                                                                // accumulated child has rows
     unsigned long long acc_nodes = 0;
     // Rows per chunk: the smallest multiple of 1024 whose chunks fit one wave
     // (binary search; each step one block sum of ceil(len / rows)), as the
@@ -786,8 +837,6 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
     if (rule.fixed) {
         if (threadIdx.x == 0) cr_sh = rule.fixed;
     } else {
-        const uint64_t acc_all = acc_sh;
-        const uint32_t n_nz = nz_sh;  // evaluated pairs whose accumulated child has rows
         const uint64_t W = rule.want_chunks;
         uint64_t lo = (acc_all + W * 1024 - 1) / (W * 1024);
         lo = lo < 1 ? 1 : lo;
@@ -795,13 +844,20 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
             const uint64_t room = W - n_nz;
             uint64_t hi = (acc_all + room * 1024 - 1) / (room * 1024);
             hi = hi < lo ? lo : hi;
+            uint32_t it = 1;  // sum32[0] was used above
             while (lo < hi) {  // uniform: every thread holds the same bounds
                 const uint64_t mid = (lo + hi) / 2, rows = mid * 1024;
                 uint32_t k = 0;
-                for (uint32_t i = threadIdx.x; i < n; i += 1024)
-                    k += (uint32_t)((small_of(i) + rows - 1) / rows);
-                uint32_t total_k;
-                (void)block_scan_1024(k, buf, total_k);
+                if (rows >> 32) {  // every node with rows takes one chunk
+                    for (uint32_t i = threadIdx.x; i < n; i += 1024) k += small_of(i) ? 1u : 0u;
+                } else {  // 32-bit divisions: a 64-bit one costs several times more
+                    const uint32_t r32 = (uint32_t)rows;
+                    for (uint32_t i = threadIdx.x; i < n; i += 1024) {
+                        const uint32_t sm = small_of(i);
+                        k += sm / r32 + (sm % r32 ? 1u : 0u);
+                    }
+                }
+                const uint32_t total_k = block_sum<uint32_t>(k, sum32[it++ & 1u]);
                 if (total_k <= W) hi = mid;
                 else lo = mid + 1;
             }
@@ -826,23 +882,16 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
             nr = P.row_len - nl;
             if (ev) nc = (min(nl, nr) + cr - 1) / cr;
         }
-        uint32_t leaves_total = 0, leaf_before = 0;
-        // Chunks (low half) and reduction groups (high half) in one scan.
-        uint64_t both_total;
-        const uint64_t both =
-            block_scan_u64((uint64_t)nc |
-                               ((uint64_t)(ev && nc >= rule.group_min_chunks ? reduce_groups(nc)
-                                                                             : 0u)
-                                << 32),
-                           buf64, both_total);
-        const uint32_t total = (uint32_t)both_total, groups_total = (uint32_t)(both_total >> 32);
-        const uint32_t before = carry + (uint32_t)both;
-        const uint32_t group_before = gcarry + (uint32_t)(both >> 32);
-        // Children of pairs that are not evaluated are leaves (those with rows).
-        if (D.st) {
-            const uint32_t nlv = (i < n && !ev) ? (nl > 0) + (nr > 0) : 0u;
-            leaf_before = leaf_base + block_scan_1024(nlv, buf, leaves_total);
-        }
+        // Chunks, reduction groups and (children of pairs that are not
+        // evaluated are leaves, those with rows) leaves in one scan.
+        uint32_t v[3] = {nc, ev && nc >= rule.group_min_chunks ? reduce_groups(nc) : 0u,
+                         (D.st && i < n && !ev) ? (nl > 0) + (nr > 0) : 0u};
+        uint32_t t[3];
+        block_scan_n<3>(v, buf3, t);
+        const uint32_t total = t[0], groups_total = t[1], leaves_total = t[2];
+        const uint32_t before = carry + v[0];
+        const uint32_t group_before = gcarry + v[1];
+        const uint32_t leaf_before = leaf_base + v[2];
         if (i < n) {
             // The smaller child (the left one on ties) is accumulated.
             const bool left_small = nl <= nr;
@@ -920,14 +969,15 @@ __device__ void level_plan_body(const PairDev *pairs, uint32_t n, const uint32_t
         leaf_base += leaves_total;
     }
     if (D.st) {
-        atomicAdd(&acc_nodes_sh, acc_nodes);
-        __syncthreads();
+        // sum64[1]: sum64[0]'s last readers may still be before the scans'
+        // barriers above.
+        const uint64_t nodes_all = block_sum<uint64_t>(acc_nodes, sum64[1]);
         if (threadIdx.x == 0) {
             GrowState *st = D.st;
-            st->n_level = 2 * st->n_eval;
+            st->n_level = 2 * S.n_eval;
             st->n_leaves = leaf_base;
-            st->hist_rows += acc_sh;
-            st->hist_nodes += (uint32_t)acc_nodes_sh;
+            st->hist_rows = S.hist_rows + acc_all;
+            st->hist_nodes = S.hist_nodes + (uint32_t)nodes_all;
         }
     }
 }
@@ -1852,8 +1902,7 @@ __global__ __launch_bounds__(1024) void part_scan_plan_kernel(
     PlanPrefetch pre{};
     pre.valid = D.st != nullptr;
     if (pre.valid) {
-        pre.n = D.st->n_split;
-        pre.leaf_base = D.st->n_leaves;
+        prefetch_state(pre, D.st);
         if (threadIdx.x < pre.n) pre.first = pairs[threadIdx.x];
     }
     if (n_chunks > LDS_CHUNKS || n_reqs > 1024) {
@@ -2106,15 +2155,22 @@ __global__ __launch_bounds__(1024) void part_plan_kernel(
     const unsigned long long *cursors, uint32_t *totals, const PairDev *pairs, ChunkRule rule,
     HistNodeDev *hn, SplitNodeDev *sn, uint32_t *spans, uint32_t *left_slot,
     uint32_t *chunk_rows_out, GrowDevOut D) {
+    __shared__ uint32_t s_tot[1024];
     PlanPrefetch pre{};
     pre.valid = true;
-    pre.n = D.st->n_split;
-    pre.leaf_base = D.st->n_leaves;
+    prefetch_state(pre, D.st);
     if (threadIdx.x < pre.n) pre.first = pairs[threadIdx.x];
-    for (uint32_t r = threadIdx.x; r < pre.n; r += 1024)
-        totals[r] = (uint32_t)cursors[(uint64_t)r * PART_CURSOR_STRIDE];
+    // The left counts (low halves of the cursors) to the totals, read back
+    // from LDS when they fit.
+    const bool lds = pre.n <= 1024;
+    for (uint32_t r = threadIdx.x; r < pre.n; r += 1024) {
+        const uint32_t t = (uint32_t)cursors[(uint64_t)r * PART_CURSOR_STRIDE];
+        totals[r] = t;
+        if (lds) s_tot[r] = t;
+    }
     __syncthreads();
-    level_plan_body(pairs, 0u, totals, rule, hn, sn, spans, left_slot, chunk_rows_out, D, pre);
+    level_plan_body(pairs, 0u, lds ? s_tot : totals, rule, hn, sn, spans, left_slot,
+                    chunk_rows_out, D, pre);
 }
 
 hipError_t launch_partition_split(const PartReqDev *reqs, const uint32_t *dev,
@@ -3332,7 +3388,17 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
     __shared__ uint16_t freelist[MAX_GROW_SLOTS];
     load_scales(G.sp);
     const uint32_t tid = threadIdx.x;
-    const GrowState S0 = *st;
+    // The fields this launch reads, one by one: a copy of the whole state
+    // would live in scratch memory.
+    struct {
+        uint32_t n_level, leaf_count, tree_size, tree_cat_words, n_leaves, error;
+    } S0;
+    S0.n_level = st->n_level;
+    S0.leaf_count = st->leaf_count;
+    S0.tree_size = st->tree_size;
+    S0.tree_cat_words = st->tree_cat_words;
+    S0.n_leaves = st->n_leaves;
+    S0.error = st->error;
     __syncthreads();  // every thread has read the state before thread 0 rewrites it
     const uint32_t n = S0.n_level;
     const uint32_t per = (n + 1023) / 1024;
@@ -3341,49 +3407,112 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
     // registers for every pass.
     // A.cands set: the packets are made here from the split scan's
     // candidates (split_node_kernel's work), else read.
+    // With few enough candidates, the workgroup first stages every
+    // (node, feature) candidate's gain in LDS (-1 when none: found
+    // candidates' gains are above MIN_GAIN_EPS), all loads in flight at
+    // once; each node's argmax then reads LDS.
+    constexpr uint32_t CAND_LDS = 4096;
+    __shared__ float cand_gain[CAND_LDS];
+    const uint32_t nfe = G.sp.n_feats;
+    const bool staged = A.cands && per == 1 && (uint64_t)n * nfe <= CAND_LDS;
+    if (staged) {
+#pragma unroll
+        for (uint32_t k = 0; k < CAND_LDS / 1024; k++) {
+            const uint32_t q = tid + k * 1024;
+            if (q < n * nfe) {
+                const float g = A.cands[q].gain;
+                const uint32_t f = A.cands[q].found;
+                cand_gain[q] = f ? g : -1.0f;
+            }
+        }
+        __syncthreads();
+    }
     auto make_pk = [&](uint32_t i) -> SplitPacketDev {
+        if (staged) {
+            // The first feature of the largest gain, as split_packet_serial.
+            uint32_t found = 0, ord = 0;
+            float best = 0.0f;
+            for (uint32_t j = 0; j < nfe; j++) {
+                const float g = cand_gain[i * nfe + j];
+                if (g > best) {
+                    best = g;
+                    ord = j;
+                    found = 1;
+                }
+            }
+            return split_packet(A.cands + (size_t)i * nfe, A.feats, G.sp, i, found, ord, A.nodes,
+                                A.cat_scratch, pk_cats, G.cw);
+        }
         return A.cands ? split_packet_serial(A.cands, A.feats, G.sp, i, A.nodes, A.cat_scratch,
                                              pk_cats, G.cw)
                        : pk[i];
     };
     SplitPacketDev myP{};
     LNodeDev myL{};
+    TreeNodeDev myT{};
+    int myMono = 0;
+    DevColumn myCol{};
     if (per == 1 && i0 < n) {
-        myP = make_pk(i0);
         myL = level[i0];
+        myP = make_pk(i0);
+        // What the node's pass below reads, requested while the scans run.
+        myT = tree[myL.tree_id];
+        if (myP.found) {
+            myMono = monotone[myP.feat];
+            myCol = cols[myP.feat];
+        }
     }
     auto pk_at = [&](uint32_t i) -> SplitPacketDev { return per == 1 ? myP : make_pk(i); };
     auto lv_at = [&](uint32_t i) -> LNodeDev { return per == 1 ? myL : level[i]; };
 
-    uint32_t nf = 0;
-    for (uint32_t i = i0; i < i1; i++) nf += pk_at(i).found ? 1u : 0u;
-    uint32_t tot_found;
-    const uint32_t f_before = block_scan_1024(nf, buf, tot_found);
-    uint32_t remaining = 0xFFFFFFFFu;
-    if (G.max_leaves)
-        remaining = G.max_leaves > S0.leaf_count ? G.max_leaves - S0.leaf_count : 0u;
-    const uint32_t n_split = min(tot_found, remaining);
-    const uint32_t leaf_count = S0.leaf_count + n_split;
-    bool evaluated =
-        n_split > 0 && depth + 1 < G.max_depth && !(G.max_leaves && leaf_count >= G.max_leaves);
-
-    uint32_t nl = 0, nc = 0;
-    {
+    uint32_t f_before, tot_found, l_before, tot_leaves, c_before, tot_chunks, n_split;
+    __shared__ uint32_t buf3[3][32];
+    if (!G.max_leaves) {
+        // No leaf cap: every node with a split splits, so the split nodes,
+        // leaves and partition chunks take one scan.
+        uint32_t v[3] = {0u, 0u, 0u}, t[3];
+        for (uint32_t i = i0; i < i1; i++) {
+            const uint32_t len = lv_at(i).row_len;
+            if (pk_at(i).found) {
+                v[0]++;
+                v[2] += (len + PART_CHUNK - 1) / PART_CHUNK;
+            } else if (len) {
+                v[1]++;
+            }
+        }
+        block_scan_n<3>(v, buf3, t);
+        f_before = v[0];
+        tot_found = t[0];
+        l_before = v[1];
+        tot_leaves = t[1];
+        c_before = v[2];
+        tot_chunks = t[2];
+        n_split = tot_found;
+    } else {
+        uint32_t nf = 0;
+        for (uint32_t i = i0; i < i1; i++) nf += pk_at(i).found ? 1u : 0u;
+        f_before = block_scan_1024(nf, buf, tot_found);
+        const uint32_t remaining =
+            G.max_leaves > S0.leaf_count ? G.max_leaves - S0.leaf_count : 0u;
+        n_split = min(tot_found, remaining);
+        uint32_t v[2] = {0u, 0u}, t[2];
         uint32_t fr = f_before;
         for (uint32_t i = i0; i < i1; i++) {
             const bool found = pk_at(i).found != 0;
             const uint32_t len = lv_at(i).row_len;
-            if (found && fr < n_split) nc += (len + PART_CHUNK - 1) / PART_CHUNK;
-            else if (len) nl++;
+            if (found && fr < n_split) v[1] += (len + PART_CHUNK - 1) / PART_CHUNK;
+            else if (len) v[0]++;
             if (found) fr++;
         }
+        block_scan_n<2>(v, buf3, t);
+        l_before = v[0];
+        tot_leaves = t[0];
+        c_before = v[1];
+        tot_chunks = t[1];
     }
-    // Leaves (low half) and partition chunks (high half) in one scan.
-    __shared__ uint64_t buf64[32];
-    uint64_t both_total;
-    const uint64_t both = block_scan_u64((uint64_t)nl | ((uint64_t)nc << 32), buf64, both_total);
-    const uint32_t tot_leaves = (uint32_t)both_total, tot_chunks = (uint32_t)(both_total >> 32);
-    const uint32_t l_before = (uint32_t)both, c_before = (uint32_t)(both >> 32);
+    const uint32_t leaf_count = S0.leaf_count + n_split;
+    bool evaluated =
+        n_split > 0 && depth + 1 < G.max_depth && !(G.max_leaves && leaf_count >= G.max_leaves);
 
     bool slots_short = false;
     if (evaluated) {
@@ -3426,7 +3555,7 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
                          hr = (double)P.right[1] * G.sp.inv_h;
             const float wl = apply_bounds(xgb_weight(gl, hl, G.sp), L.lower, L.upper);
             const float wr = apply_bounds(xgb_weight(gr, hr, G.sp), L.lower, L.upper);
-            const int mono = monotone[P.feat];
+            const int mono = per == 1 ? myMono : monotone[P.feat];
             const float mid = (wl + wr) / 2.0f;
             float llo = L.lower, lhi = L.upper, rlo = L.lower, rhi = L.upper;
             if (mono < 0) {
@@ -3436,7 +3565,7 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
                 lhi = mid;
                 rlo = mid;
             }
-            TreeNodeDev t = tree[L.tree_id];
+            TreeNodeDev t = per == 1 ? myT : tree[L.tree_id];
             t.feat = P.feat;
             t.bin = P.bin;
             t.left = (int32_t)lid;
@@ -3460,7 +3589,7 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
             b.sum_hess = (float)hr;
             tree[lid] = a;
             tree[rid] = b;
-            const DevColumn col = cols[P.feat];
+            const DevColumn col = per == 1 ? myCol : cols[P.feat];
             PartReqDev q{};
             q.row_off = L.row_off;
             q.row_len = L.row_len;
@@ -3507,7 +3636,7 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
             LeafDev lf{};
             lf.row_off = L.row_off;
             lf.row_len = L.row_len;
-            lf.value = tree[L.tree_id].leaf_value;
+            lf.value = per == 1 ? myT.leaf_value : tree[L.tree_id].leaf_value;
             lf.id = k;
             lf.arena = depth & 1u;
             leaves[k] = lf;
@@ -3518,16 +3647,14 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
     }
     __syncthreads();
     if (tid == 0) {
-        GrowState s = S0;
-        s.n_split = n_split;
-        s.part_chunks = tot_chunks;
-        s.n_eval = evaluated ? n_split : 0u;
-        s.tree_size = S0.tree_size + 2 * n_split;
-        s.leaf_count = leaf_count;
-        s.n_leaves = S0.n_leaves + tot_leaves;
-        s.tree_cat_words = S0.tree_cat_words + n_split * G.cw;
-        s.error = S0.error | (slots_short ? 1u : 0u);
-        *st = s;
+        st->n_split = n_split;
+        st->part_chunks = tot_chunks;
+        st->n_eval = evaluated ? n_split : 0u;
+        st->tree_size = S0.tree_size + 2 * n_split;
+        st->leaf_count = leaf_count;
+        st->n_leaves = S0.n_leaves + tot_leaves;
+        st->tree_cat_words = S0.tree_cat_words + n_split * G.cw;
+        st->error = S0.error | (slots_short ? 1u : 0u);
     }
 }
 
