@@ -539,49 +539,69 @@ hipError_t launch_zero_slots(int64_t *hist, uint64_t width, const uint32_t *slot
 // a larger node's groups each add the sum of their REDUCE_GROUP chunks into
 // its slot, which the histogram launch cleared (its first chunk's
 // workgroups).
-__global__ void reduce_chunks_kernel(int64_t *hist, uint64_t width, const int64_t *partials,
+__global__ __launch_bounds__(256) void reduce_chunks_kernel(int64_t *hist, uint64_t width,
+                                                           const int64_t *partials,
                                      const HistNodeDev *nodes, uint32_t n_nodes,
                                      const uint32_t *dev_n, uint32_t max_groups,
                                      uint32_t min_chunks) {
+    // The node count and, speculatively (up to the host's bound, which the
+    // node table holds), the nodes are requested together; the nodes then
+    // come from LDS when they fit.
+    constexpr uint32_t LDS_NODES = 256;  // the block size
+    __shared__ uint4 s_nodes[LDS_NODES];  // chunk_begin, slot, n_chunks, group_begin
+    const uint32_t bound = min(n_nodes, LDS_NODES);
+    uint4 mine = make_uint4(0u, 0u, 0u, 0u);
+    if (threadIdx.x < bound)
+        mine = make_uint4(nodes[threadIdx.x].chunk_begin, nodes[threadIdx.x].slot,
+                          nodes[threadIdx.x].n_chunks, nodes[threadIdx.x].group_begin);
     const uint32_t n = dev_n ? *dev_n : n_nodes;
     if (n == 0) return;
+    const bool in_lds = n <= LDS_NODES;
+    if (in_lds) {
+        if (threadIdx.x < n) s_nodes[threadIdx.x] = mine;
+        __syncthreads();
+    }
+    auto node_at = [&](uint32_t i) -> uint4 {
+        return in_lds ? s_nodes[i]
+                      : make_uint4(nodes[i].chunk_begin, nodes[i].slot, nodes[i].n_chunks,
+                                   nodes[i].group_begin);
+    };
     // Groups past the last node's (max_groups is an upper bound) are skipped.
-    const HistNodeDev last = nodes[n - 1];
-    const uint32_t n_groups = min(max_groups, last.group_begin + reduce_groups(last.n_chunks));
+    const uint4 last = node_at(n - 1);
+    const uint32_t n_groups = min(max_groups, last.w + reduce_groups(last.z));
     if (blockIdx.y >= n_groups) return;
     const uint64_t W = width * 2u;
     const unsigned long long *src = reinterpret_cast<const unsigned long long *>(partials);
-    // The nodes' first groups in LDS when they fit (the searches below then
-    // wait on no global load).
-    constexpr uint32_t LDS_NODES = 256;
-    __shared__ uint32_t gb[LDS_NODES];
-    const bool in_lds = n <= LDS_NODES;
-    if (in_lds) {
-        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) gb[i] = nodes[i].group_begin;
-        __syncthreads();
-    }
     for (uint32_t y = blockIdx.y; y < n_groups; y += gridDim.y) {
         uint32_t lo = 0, hi = n;
         while (hi - lo > 1) {
             const uint32_t mid = (lo + hi) >> 1;
-            if ((in_lds ? gb[mid] : nodes[mid].group_begin) <= y) lo = mid;
+            if ((in_lds ? s_nodes[mid].w : nodes[mid].group_begin) <= y) lo = mid;
             else hi = mid;
         }
-        const HistNodeDev N = nodes[lo];
-        const uint32_t g = y - N.group_begin;
+        const uint4 N = node_at(lo);  // chunk_begin, slot, n_chunks, group_begin
+        const uint32_t g = y - N.w;
         // past the groups / written / left to split_pair_kernel
-        if (g >= reduce_groups(N.n_chunks) || N.n_chunks == 1 || N.n_chunks < min_chunks)
-            continue;
-        const uint32_t c0 = g * REDUCE_GROUP, c1 = min(c0 + REDUCE_GROUP, N.n_chunks);
-        const bool store = N.n_chunks <= REDUCE_GROUP;
-        unsigned long long *dst =
-            reinterpret_cast<unsigned long long *>(hist + (uint64_t)N.slot * W);
+        if (g >= reduce_groups(N.z) || N.z == 1 || N.z < min_chunks) continue;
+        const uint32_t c0 = g * REDUCE_GROUP, c1 = min(c0 + REDUCE_GROUP, N.z);
+        const bool store = N.z <= REDUCE_GROUP;
+        unsigned long long *dst = reinterpret_cast<unsigned long long *>(hist + (uint64_t)N.y * W);
+        const unsigned long long *base = src + (uint64_t)(N.x + c0) * W;
         for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < W;
              i += (uint64_t)gridDim.x * blockDim.x) {
-            unsigned long long v = 0;
-            for (uint32_t c = c0; c < c1; c++) v += src[(uint64_t)(N.chunk_begin + c) * W + i];
-            if (store) dst[i] = v;
-            else if (v) global_add_u64(dst + i, v);
+            // Four chunks' loads in flight at a time (a chunk past the
+            // group's reads its first chunk again and adds nothing).
+            unsigned long long sum = 0;
+            for (uint32_t k = 0; k < c1 - c0; k += 4) {
+                unsigned long long v[4];
+#pragma unroll
+                for (uint32_t q = 0; q < 4; q++)
+                    v[q] = base[(uint64_t)(k + q < c1 - c0 ? k + q : 0u) * W + i];
+#pragma unroll
+                for (uint32_t q = 0; q < 4; q++) sum += k + q < c1 - c0 ? v[q] : 0ull;
+            }
+            if (store) dst[i] = sum;
+            else if (sum) global_add_u64(dst + i, sum);
         }
     }
 }
