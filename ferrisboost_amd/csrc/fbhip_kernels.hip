@@ -1162,7 +1162,7 @@ __device__ __forceinline__ int64_t wsub(int64_t a, int64_t b) {
 // max_cat_threshold - 1 categories per direction.
 __device__ void split_categorical(const int64_t *h, uint32_t n, const SplitNodeDev &N,
                                   float parent, int mono, const SplitParamsDev &P, Best *shb,
-                                  int64_t *sg, int64_t *shh, float *wts, uint32_t *order,
+                                  int64_t *sg, int64_t *shh, uint64_t *keys, uint32_t *order,
                                   unsigned long long *set_lds, uint64_t *set_out,
                                   uint32_t set_words, FeatCandDev *outc) {
     const uint32_t tid = threadIdx.x;
@@ -1201,22 +1201,53 @@ __device__ void split_categorical(const int64_t *h, uint32_t n, const SplitNodeD
         __syncthreads();
         if (tid == 0 && best.found) set_out[at >> 6] |= 1ull << (at & 63);
     } else {
-        for (uint32_t i = tid; i < n; i += SPLIT_TPB) {
-            const double g = (double)h[2 * i] * P.inv_g, hh = (double)h[2 * i + 1] * P.inv_h;
-            wts[i] = xgb_weight(g, hh, P);
+        // Stable ascending order by `<` (std::stable_sort / sort_by
+        // partial_cmp): a bitonic sort of (weight, category) keys, the
+        // weight's bits mapped so that unsigned order is float order (its
+        // zeros made one, as `<` sees them; weights are never NaN) and
+        // equal weights ordered by category.
+        uint32_t n2 = 1;
+        while (n2 < n) n2 <<= 1;
+        for (uint32_t i = tid; i < n2; i += SPLIT_TPB) {
+            uint64_t key = ~0ull;  // padding sorts last
+            if (i < n) {
+                const double g = (double)h[2 * i] * P.inv_g, hh = (double)h[2 * i + 1] * P.inv_h;
+                float w = xgb_weight(g, hh, P);
+                if (w == 0.0f) w = 0.0f;
+                const uint32_t u = __float_as_uint(w);
+                key = ((uint64_t)((u & 0x80000000u) ? ~u : (u | 0x80000000u)) << 32) | i;
+            }
+            keys[i] = key;
         }
         __syncthreads();
-        for (uint32_t i = tid; i < n; i += SPLIT_TPB) order[i] = i;
-        __syncthreads();
-        // Stable ascending rank by `<` (std::stable_sort / sort_by partial_cmp).
-        for (uint32_t i = tid; i < n; i += SPLIT_TPB) {
-            const float wi = wts[i];
-            uint32_t r = 0;
-            for (uint32_t j = 0; j < n; j++) {
-                const float wj = wts[j];
-                r += (wj < wi) || (j < i && !(wi < wj) && !(wj < wi));
+        for (uint32_t k = 2; k <= n2; k <<= 1)
+            for (uint32_t jj = k >> 1; jj > 0; jj >>= 1) {
+                for (uint32_t i = tid; i < n2; i += SPLIT_TPB) {
+                    const uint32_t ixj = i ^ jj;
+                    if (ixj > i) {
+                        const uint64_t a = keys[i], b = keys[ixj];
+                        if ((a > b) == ((i & k) == 0)) {
+                            keys[i] = b;
+                            keys[ixj] = a;
+                        }
+                    }
+                }
+                __syncthreads();
             }
-            if (r < n) order[r] = i;
+        // The categories in sorted order; order[] shares the keys' memory,
+        // so every key is read before any is overwritten.
+        constexpr uint32_t KPT = MAX_DEVICE_CATS / SPLIT_TPB;
+        uint32_t cat[KPT];
+#pragma unroll
+        for (uint32_t q = 0; q < KPT; q++) {
+            const uint32_t r = tid + q * SPLIT_TPB;
+            cat[q] = r < n ? (uint32_t)keys[r] : 0u;
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t q = 0; q < KPT; q++) {
+            const uint32_t r = tid + q * SPLIT_TPB;
+            if (r < n) order[r] = cat[q];
         }
         __syncthreads();
         const uint32_t n_scan = min(P.max_cat_threshold, n);
@@ -1313,38 +1344,31 @@ __device__ __forceinline__ Best wave_best(Best b) {
 // numeric scan of split_feat_kernel on 64 lanes with shuffles only (no
 // barriers). Each lane takes a run of bins; integer prefix sums are exact in
 // any order, and the argmax keeps the reference's tie rule.
-// Bins of a numeric feature held by one wave: lane l holds bins
-// [l * per, l * per + per) in registers, per = ceil(bins / 64) at most
-// NUM_PER_LANE (features of at most 256 bins) or WIDE_PER_LANE (at most 1024).
+// Bins of a numeric feature held in registers: lane l of a wave (thread t
+// of a workgroup) holds bins [l * per, l * per + per), per = ceil(bins / 64)
+// (ceil(bins / 256)) at most NUM_PER_LANE: one wave for features of at most
+// 256 bins, four for those of at most 1024.
 constexpr uint32_t NUM_PER_LANE = 4;
-constexpr uint32_t WIDE_PER_LANE = 16;
 
-// The split scan of one (node, feature) over bins in the wave's registers
-// (g[k], h[k] of bin b0 + k): prefix sums, the forward candidates (missing
-// rows right), the reverse ones (missing rows left; skipped when the bins
-// hold the whole node) and the first best by the reference's rules, written
-// to outc by lane 0.
-template <uint32_t PER>
-__device__ __forceinline__ void scan_numeric(const int64_t (&g)[PER], const int64_t (&h)[PER],
-                                             uint32_t b0, uint32_t b1, uint32_t n, uint32_t lane,
-                                             const SplitNodeDev &N, const SplitFeatDev &F,
-                                             const SplitParamsDev &P, FeatCandDev *outc) {
+// The node's gain before the split (the parent term of every candidate).
+__device__ __forceinline__ float parent_gain(const SplitNodeDev &N, const SplitParamsDev &P) {
     const double ng = (double)N.sum_g * P.inv_g, nh = (double)N.sum_h * P.inv_h;
-    const float parent = gain_given_weight(ng, nh, apply_bounds(xgb_weight(ng, nh, P), N.lower,
-                                                                N.upper), P);
-    int64_t tg = 0, th = 0;
-#pragma unroll
-    for (uint32_t k = 0; k < PER; k++)
-        if (b0 + k < b1) {
-            tg = wadd(tg, g[k]);
-            th = wadd(th, h[k]);
-        }
-    const int64_t ig = wave_scan_incl_i64(tg, lane), ih = wave_scan_incl_i64(th, lane);
-    const int64_t eg = wsub(ig, tg), eh = wsub(ih, th);
-    const int64_t totg = __shfl(ig, 63, 64), toth = __shfl(ih, 63, 64);
+    return gain_given_weight(ng, nh, apply_bounds(xgb_weight(ng, nh, P), N.lower, N.upper), P);
+}
 
+// The lane's candidates of a numeric scan over its bins (g[k], h[k] of bin
+// b0 + k, summing to tg, th): the forward ones (missing rows right) from
+// eg, eh, the sums of the feature's bins before b0, and the reverse ones
+// (missing rows left; skipped when the feature's bins, totg / toth, hold the
+// whole node). Returns the lane's first best by the reference's rules.
+template <uint32_t PER>
+__device__ __forceinline__ Best scan_candidates(const int64_t (&g)[PER], const int64_t (&h)[PER],
+                                                uint32_t b0, uint32_t b1, uint32_t n,
+                                                const SplitNodeDev &N, int mono,
+                                                const SplitParamsDev &P, float parent, int64_t tg,
+                                                int64_t th, int64_t eg, int64_t eh, int64_t totg,
+                                                int64_t toth) {
     Best best{0.0f, 0u, 0u, 0, 0};
-    const int mono = F.monotone;
     // Forward: missing rows go right.
     int64_t lg = eg, lh = eh;
 #pragma unroll
@@ -1371,20 +1395,48 @@ __device__ __forceinline__ void scan_numeric(const int64_t (&g)[PER], const int6
                 offer(best, gain, n + (n - 1 - (b0 + k)), l2g, l2h);
         }
     }
-    best = wave_best(best);
-    if (lane == 0) {
-        outc->found = best.found;
-        outc->gain = best.gain;
-        if (best.ord < n) {
-            outc->bin = best.ord + 1;
-            outc->missing_left = 0;
-        } else {
-            outc->bin = n - 1 - (best.ord - n);
-            outc->missing_left = 1;
-        }
-        outc->left_g = best.lg;
-        outc->left_h = best.lh;
+    return best;
+}
+
+// A numeric scan's best into its candidate slot (ordinals below n: bin + 1
+// with missing rows right; above: the reverse scan's, missing rows left).
+__device__ __forceinline__ void write_numeric_cand(const Best &best, uint32_t n,
+                                                   FeatCandDev *outc) {
+    outc->found = best.found;
+    outc->gain = best.gain;
+    if (best.ord < n) {
+        outc->bin = best.ord + 1;
+        outc->missing_left = 0;
+    } else {
+        outc->bin = n - 1 - (best.ord - n);
+        outc->missing_left = 1;
     }
+    outc->left_g = best.lg;
+    outc->left_h = best.lh;
+}
+
+// The split scan of one (node, feature) over bins in the wave's registers:
+// prefix sums by shuffles, the lanes' candidates, the wave's first best,
+// written to outc by lane 0.
+template <uint32_t PER>
+__device__ __forceinline__ void scan_numeric(const int64_t (&g)[PER], const int64_t (&h)[PER],
+                                             uint32_t b0, uint32_t b1, uint32_t n, uint32_t lane,
+                                             const SplitNodeDev &N, const SplitFeatDev &F,
+                                             const SplitParamsDev &P, FeatCandDev *outc) {
+    const float parent = parent_gain(N, P);
+    int64_t tg = 0, th = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < PER; k++)
+        if (b0 + k < b1) {
+            tg = wadd(tg, g[k]);
+            th = wadd(th, h[k]);
+        }
+    const int64_t ig = wave_scan_incl_i64(tg, lane), ih = wave_scan_incl_i64(th, lane);
+    const int64_t totg = __shfl(ig, 63, 64), toth = __shfl(ih, 63, 64);
+    Best best = scan_candidates<PER>(g, h, b0, b1, n, N, F.monotone, P, parent, tg, th,
+                                     wsub(ig, tg), wsub(ih, th), totg, toth);
+    best = wave_best(best);
+    if (lane == 0) write_numeric_cand(best, n, outc);
 }
 
 // One wave's (node, numeric feature of at most 64 * PER bins): the
@@ -1416,6 +1468,71 @@ __device__ __forceinline__ void split_num_wave(const int64_t *hist, uint64_t his
         h[k] = b0 + k < b1 ? hp[2 * (b0 + k) + 1] : 0;
     }
     scan_numeric<PER>(g, h, b0, b1, n, lane, N, F, P, outc);
+}
+
+// One workgroup's (node, numeric feature of 257 to 1024 bins): each of its
+// four waves holds a quarter of the bins in registers (at most four a
+// lane), the waves' sums are exchanged through LDS for the prefix and the
+// total, every lane scans its candidates, and the waves' bests are combined
+// by the same total order. Four waves a feature keep the chain of f64
+// candidate arithmetic a lane runs four times shorter than one wave would.
+// wt holds 8 and wb 4 entries of LDS. li indexes order.
+__device__ __forceinline__ void split_wide_block(const int64_t *hist, uint64_t hist_width,
+                                                 const SplitNodeDev *nodes,
+                                                 const SplitFeatDev *feats, const uint32_t *order,
+                                                 uint32_t li, uint32_t ni, const uint8_t *enabled,
+                                                 SplitParamsDev P, FeatCandDev *cands,
+                                                 int64_t *wt, Best *wb) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    load_scales(P);
+    const uint32_t j = order[li];
+    const SplitFeatDev F = feats[j];
+    const SplitNodeDev N = nodes[ni];
+    FeatCandDev *outc = cands + (size_t)ni * P.n_feats + j;
+    if (enabled && !enabled[(size_t)ni * P.n_feats + j]) {
+        if (tid == 0) outc->found = 0;
+        return;
+    }
+    const int64_t *hp = hist + ((uint64_t)N.slot * hist_width + F.hist_off) * 2u;
+    const uint32_t n = F.n_bins;
+    const uint32_t per = (n + SPLIT_TPB - 1) / SPLIT_TPB;  // at most NUM_PER_LANE
+    const uint32_t b0 = min(tid * per, n), b1 = min(b0 + per, n);
+    int64_t g[NUM_PER_LANE], h[NUM_PER_LANE];
+    int64_t tg = 0, th = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < NUM_PER_LANE; k++) {
+        g[k] = b0 + k < b1 ? hp[2 * (b0 + k)] : 0;
+        h[k] = b0 + k < b1 ? hp[2 * (b0 + k) + 1] : 0;
+        tg = wadd(tg, g[k]);
+        th = wadd(th, h[k]);
+    }
+    const int64_t ig = wave_scan_incl_i64(tg, lane), ih = wave_scan_incl_i64(th, lane);
+    if (lane == 63) {
+        wt[2 * wave] = ig;
+        wt[2 * wave + 1] = ih;
+    }
+    __syncthreads();
+    int64_t og = 0, oh = 0, totg = 0, toth = 0;
+    for (uint32_t w = 0; w < SPLIT_TPB / 64; w++) {
+        if (w < wave) {
+            og = wadd(og, wt[2 * w]);
+            oh = wadd(oh, wt[2 * w + 1]);
+        }
+        totg = wadd(totg, wt[2 * w]);
+        toth = wadd(toth, wt[2 * w + 1]);
+    }
+    Best best = scan_candidates<NUM_PER_LANE>(g, h, b0, b1, n, N, F.monotone, P, parent_gain(N, P),
+                                              tg, th, wadd(og, wsub(ig, tg)),
+                                              wadd(oh, wsub(ih, th)), totg, toth);
+    best = wave_best(best);
+    if (lane == 0) wb[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+        Best b = wb[0];
+        for (uint32_t w = 1; w < SPLIT_TPB / 64; w++)
+            if (better(wb[w], b)) b = wb[w];
+        write_numeric_cand(b, n, outc);
+    }
 }
 
 // One wave per (node, numeric feature of at most 256 bins), four features a
@@ -1553,8 +1670,8 @@ hipError_t launch_split_pairs(int64_t *hist, uint64_t hist_width, const int64_t 
 // missing mass) candidates, and the first best by the reference's rules.
 // Workgroups past the n_block one-workgroup features take the n_wide
 // numeric features of at most 1024 bins that follow order[wide_off], one
-// wave each (split_num_wave with sixteen bins a lane), in the same launch:
-// the two kinds then overlap instead of running one after the other.
+// workgroup each (split_wide_block), in the same launch: the two kinds then
+// overlap instead of running one after the other.
 __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
     const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
     const SplitFeatDev *feats, const uint32_t *order, uint32_t order_off, uint32_t n_block,
@@ -1567,10 +1684,10 @@ __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
     const uint32_t ni = blockIdx.y, tid = threadIdx.x;
     if (dev_n && ni >= *dev_n) return;
     if (blockIdx.x >= n_block) {
-        const uint32_t li = (blockIdx.x - n_block) * 4 + (tid >> 6);
+        const uint32_t li = blockIdx.x - n_block;
         if (li < n_wide)
-            split_num_wave<WIDE_PER_LANE>(hist, hist_width, nodes, feats, order + wide_off, li, ni,
-                                          enabled, P, cands);
+            split_wide_block(hist, hist_width, nodes, feats, order + wide_off, li, ni, enabled, P,
+                             cands, sg, shb);
         return;
     }
     load_scales(P);
@@ -1589,11 +1706,13 @@ __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
     const uint32_t n = F.n_bins;
 
     if (F.categorical) {
-        float *wts = reinterpret_cast<float *>(dyn);
-        uint32_t *order = reinterpret_cast<uint32_t *>(dyn + sizeof(float) * MAX_DEVICE_CATS);
+        // Sort keys (8 bytes a category), then the sorted categories in the
+        // same memory.
+        uint64_t *keys = reinterpret_cast<uint64_t *>(dyn);
+        uint32_t *order = reinterpret_cast<uint32_t *>(dyn);
         uint64_t *set = cat_scratch + (size_t)ni * P.cat_words_per_node + F.cat_base;
         __shared__ unsigned long long set_lds[MAX_DEVICE_CATS / 64];
-        split_categorical(h, n, N, parent, F.monotone, P, shb, sg, shh, wts, order, set_lds, set,
+        split_categorical(h, n, N, parent, F.monotone, P, shb, sg, shh, keys, order, set_lds, set,
                           F.cat_words, outc);
         return;
     }
@@ -1660,9 +1779,9 @@ hipError_t launch_split_feats(const int64_t *hist, uint64_t hist_width, const Sp
                            hist_width, nodes, feats, order, n_num, enabled, P, cands, dev_n);
     if (n_wide || n_cat) {
         const size_t dyn = P.cat_words_per_node
-                               ? (sizeof(float) + sizeof(uint32_t)) * MAX_DEVICE_CATS
+                               ? sizeof(uint64_t) * MAX_DEVICE_CATS
                                : 0;
-        hipLaunchKernelGGL(split_feat_kernel, dim3(n_cat + (n_wide + 3) / 4, n_nodes),
+        hipLaunchKernelGGL(split_feat_kernel, dim3(n_cat + n_wide, n_nodes),
                            dim3(SPLIT_TPB), dyn, s, hist, hist_width, nodes, feats, order,
                            n_num + n_wide, n_cat, n_num, n_wide, enabled, P, cands, cat_scratch,
                            dev_n);
