@@ -1160,6 +1160,62 @@ __device__ __forceinline__ int64_t wsub(int64_t a, int64_t b) {
 // (split.rs:484-617). One-hot below max_cat_to_onehot, otherwise a stable
 // sort of the categories by weight and prefix scans of at most
 // max_cat_threshold - 1 categories per direction.
+// Ascending bitonic sort of the 256 * E distinct keys at keys[] (LDS) by
+// the workgroup, key q * 256 + t held by thread t in registers: partners
+// in the same wave are exchanged by shuffles, those in the same thread
+// directly, and only the partners in another wave go through LDS (two
+// barriers a step).
+template <int E>
+__device__ void bitonic_sort_keys(uint64_t *keys) {
+    const uint32_t tid = threadIdx.x;
+    constexpr uint32_t N2 = E * SPLIT_TPB;
+    uint64_t v[E];
+#pragma unroll
+    for (int q = 0; q < E; q++) v[q] = keys[q * SPLIT_TPB + tid];
+    for (uint32_t k = 2; k <= N2; k <<= 1) {
+        for (uint32_t jj = k >> 1; jj > 0; jj >>= 1) {
+            if (jj >= SPLIT_TPB) {
+                const uint32_t d = jj / SPLIT_TPB;
+#pragma unroll
+                for (int q = 0; q < E; q++) {
+                    const uint32_t p = (uint32_t)q ^ d;
+                    if (p > (uint32_t)q && p < (uint32_t)E) {
+                        const bool up = ((q * SPLIT_TPB + tid) & k) == 0;
+                        const uint64_t a = v[q], b = v[p];
+                        if ((a > b) == up) {
+                            v[q] = b;
+                            v[p] = a;
+                        }
+                    }
+                }
+            } else if (jj >= 64) {
+#pragma unroll
+                for (int q = 0; q < E; q++) keys[q * SPLIT_TPB + tid] = v[q];
+                __syncthreads();
+#pragma unroll
+                for (int q = 0; q < E; q++) {
+                    const uint32_t i = q * SPLIT_TPB + tid;
+                    const uint64_t o = keys[i ^ jj];
+                    const bool keep_min = ((i & jj) == 0) == ((i & k) == 0);
+                    v[q] = keep_min ? (o < v[q] ? o : v[q]) : (o > v[q] ? o : v[q]);
+                }
+                __syncthreads();
+            } else {
+#pragma unroll
+                for (int q = 0; q < E; q++) {
+                    const uint32_t i = q * SPLIT_TPB + tid;
+                    const uint64_t o = __shfl_xor(v[q], (int)jj, 64);
+                    const bool keep_min = ((i & jj) == 0) == ((i & k) == 0);
+                    v[q] = keep_min ? (o < v[q] ? o : v[q]) : (o > v[q] ? o : v[q]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < E; q++) keys[q * SPLIT_TPB + tid] = v[q];
+    __syncthreads();
+}
+
 __device__ void split_categorical(const int64_t *h, uint32_t n, const SplitNodeDev &N,
                                   float parent, int mono, const SplitParamsDev &P, Best *shb,
                                   int64_t *sg, int64_t *shh, uint64_t *keys, uint32_t *order,
@@ -1206,7 +1262,7 @@ __device__ void split_categorical(const int64_t *h, uint32_t n, const SplitNodeD
         // weight's bits mapped so that unsigned order is float order (its
         // zeros made one, as `<` sees them; weights are never NaN) and
         // equal weights ordered by category.
-        uint32_t n2 = 1;
+        uint32_t n2 = SPLIT_TPB;
         while (n2 < n) n2 <<= 1;
         for (uint32_t i = tid; i < n2; i += SPLIT_TPB) {
             uint64_t key = ~0ull;  // padding sorts last
@@ -1220,20 +1276,28 @@ __device__ void split_categorical(const int64_t *h, uint32_t n, const SplitNodeD
             keys[i] = key;
         }
         __syncthreads();
-        for (uint32_t k = 2; k <= n2; k <<= 1)
-            for (uint32_t jj = k >> 1; jj > 0; jj >>= 1) {
-                for (uint32_t i = tid; i < n2; i += SPLIT_TPB) {
-                    const uint32_t ixj = i ^ jj;
-                    if (ixj > i) {
-                        const uint64_t a = keys[i], b = keys[ixj];
-                        if ((a > b) == ((i & k) == 0)) {
-                            keys[i] = b;
-                            keys[ixj] = a;
+        if (n2 == SPLIT_TPB) {
+            bitonic_sort_keys<1>(keys);
+        } else if (n2 == 2 * SPLIT_TPB) {
+            bitonic_sort_keys<2>(keys);
+        } else if (n2 == 4 * SPLIT_TPB) {
+            bitonic_sort_keys<4>(keys);
+        } else {
+            for (uint32_t k = 2; k <= n2; k <<= 1)
+                for (uint32_t jj = k >> 1; jj > 0; jj >>= 1) {
+                    for (uint32_t i = tid; i < n2; i += SPLIT_TPB) {
+                        const uint32_t ixj = i ^ jj;
+                        if (ixj > i) {
+                            const uint64_t a = keys[i], b = keys[ixj];
+                            if ((a > b) == ((i & k) == 0)) {
+                                keys[i] = b;
+                                keys[ixj] = a;
+                            }
                         }
                     }
+                    __syncthreads();
                 }
-                __syncthreads();
-            }
+        }
         // The categories in sorted order; order[] shares the keys' memory,
         // so every key is read before any is overwritten.
         constexpr uint32_t KPT = MAX_DEVICE_CATS / SPLIT_TPB;
