@@ -106,8 +106,11 @@ constexpr uint32_t DEFAULT_TILE_BYTES = 64 * 1024;
 // features of 1024 bins: 254 against 340 us a histogram).
 constexpr uint32_t PLANAR_TILE_BYTES = 53 * 1024;
 // Device-grown trees of at most this many features pick each node's best
-// split inside the level decision instead of a separate argmax launch.
+// split inside the level decision instead of a separate argmax launch; trees
+// of at most FUSED_STAGED_FEATS do so at the levels whose candidates the
+// decision stages in LDS (DECIDE_CAND_LDS).
 constexpr size_t FUSED_ARGMAX_FEATS = 64;
+constexpr size_t FUSED_STAGED_FEATS = 256;
 // Row layouts of at most this many tiles histogram f32 pairs (fbh_ctx::f32_hist).
 constexpr size_t F32_PAIR_MAX_TILES = 4;
 // Rows per histogram workgroup: chosen per launch so that the launch makes
@@ -3343,9 +3346,18 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     E0.sn = c->d_lvl_split;
     E0.n_nodes = 1;
     E0.download = false;
-    // One thread a node scans the candidates in the level decision.
-    const bool fuse = c->tree_feats.size() <= FUSED_ARGMAX_FEATS;
-    E0.fused_argmax = fuse;
+    // The level decision picks each node's split itself (from candidates it
+    // stages in LDS, or one thread a node scanning them) when the tree has
+    // few features, or up to FUSED_STAGED_FEATS when the level's candidates
+    // fit the staging (one thread a node scanning more features from LDS is
+    // slower than split_node_kernel's workgroup a node: 400k x 2000 at 1000
+    // features a tree lost 2 %).
+    const size_t n_tf = c->tree_feats.size();
+    auto fuse_at = [&](uint32_t d) {
+        return n_tf <= FUSED_ARGMAX_FEATS ||
+               (n_tf <= FUSED_STAGED_FEATS && (uint64_t)lvl_bound(d) * n_tf <= DECIDE_CAND_LDS);
+    };
+    E0.fused_argmax = fuse_at(0);
     // A root sum from the host is staged; else the prep kernel sums the
     // quantisation's block sums.
     const int64_t *d_root = nullptr;
@@ -3390,10 +3402,9 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
     account_hist(c, n_rows, 1);
 
     uint8_t *pk_base = reinterpret_cast<uint8_t *>(c->d_packets);
-    const FusedArgmaxDev A =
-        fuse ? FusedArgmaxDev{c->d_cands, c->d_sfeats, c->d_lvl_split, c->d_cat_scratch}
-             : FusedArgmaxDev{};
+    const FusedArgmaxDev A_fused{c->d_cands, c->d_sfeats, c->d_lvl_split, c->d_cat_scratch};
     for (uint32_t d = 0; d < D; d++) {
+        const FusedArgmaxDev A = fuse_at(d) ? A_fused : FusedArgmaxDev{};
         const uint32_t nb = lvl_bound(d);
         uint64_t *pk_cats =
             reinterpret_cast<uint64_t *>(pk_base + al256(sizeof(SplitPacketDev) * nb));
@@ -3448,7 +3459,7 @@ void grow_enqueue(fbh_ctx *c, const fbh_grow_params *gp, const fbh_split_params 
         E.n_nodes = lvl_bound(d + 1);
         E.dev_n_nodes = &GB.st->n_level;
         E.download = false;
-        E.fused_argmax = fuse;
+        E.fused_argmax = fuse_at(d + 1);
         E.rows = arena_out;
         E.cleared = true;
         E.pairs = true;

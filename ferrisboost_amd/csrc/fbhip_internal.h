@@ -18,6 +18,8 @@ constexpr int XCDS = 8;            // MI355X accelerator complex dies
 constexpr uint32_t NO_SLOT = 0xFFFFFFFFu;
 constexpr uint32_t MAX_GROW_SLOTS = 16384;  // histogram slots a device-grown tree can use
 constexpr uint32_t MAX_WALK_NODES = 1024;   // tree nodes the row-order leaf walk holds in LDS
+// (node, feature) candidates a level decision stages in LDS for its argmax.
+constexpr uint32_t DECIDE_CAND_LDS = 4096;
 
 // One histogram tile: a group of features of one width stored as row
 // records, record i at data + i * stride, feature k of the tile at byte

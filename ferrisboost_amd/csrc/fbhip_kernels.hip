@@ -3623,13 +3623,12 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
     // (node, feature) candidate's gain in LDS (-1 when none: found
     // candidates' gains are above MIN_GAIN_EPS), all loads in flight at
     // once; each node's argmax then reads LDS.
-    constexpr uint32_t CAND_LDS = 4096;
-    __shared__ float cand_gain[CAND_LDS];
+    __shared__ float cand_gain[DECIDE_CAND_LDS];
     const uint32_t nfe = G.sp.n_feats;
-    const bool staged = A.cands && per == 1 && (uint64_t)n * nfe <= CAND_LDS;
+    const bool staged = A.cands && per == 1 && (uint64_t)n * nfe <= DECIDE_CAND_LDS;
     if (staged) {
 #pragma unroll
-        for (uint32_t k = 0; k < CAND_LDS / 1024; k++) {
+        for (uint32_t k = 0; k < DECIDE_CAND_LDS / 1024; k++) {
             const uint32_t q = tid + k * 1024;
             if (q < n * nfe) {
                 const float g = A.cands[q].gain;
