@@ -1110,15 +1110,32 @@ __device__ __forceinline__ void offer(Best &best, float gain, uint32_t ord, int6
     }
 }
 
-__device__ Best block_best(Best mine, Best *sh) {
-    const uint32_t tid = threadIdx.x;
-    sh[tid] = mine;
-    __syncthreads();
-    for (uint32_t s = SPLIT_TPB / 2; s > 0; s >>= 1) {
-        if (tid < s && better(sh[tid + s], sh[tid])) sh[tid] = sh[tid + s];
-        __syncthreads();
+// The best of the wave's candidates by the total order of `better` (gain,
+// then the lower ordinal): every lane ends with the same one.
+__device__ __forceinline__ Best wave_best(Best b) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        Best o;
+        o.gain = __shfl_xor(b.gain, off, 64);
+        o.ord = __shfl_xor(b.ord, off, 64);
+        o.found = __shfl_xor(b.found, off, 64);
+        o.lg = __shfl_xor(b.lg, off, 64);
+        o.lh = __shfl_xor(b.lh, off, 64);
+        if (better(o, b)) b = o;
     }
+    return b;
+}
+
+// The block's best by the same order, in every thread: the waves' bests by
+// shuffles, then through LDS (sh: one entry a wave).
+__device__ Best block_best(Best mine, Best *sh) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const Best w = wave_best(mine);
+    if (lane == 0) sh[wave] = w;
+    __syncthreads();
     Best r = sh[0];
+    for (uint32_t k = 1; k < (blockDim.x >> 6); k++)
+        if (better(sh[k], r)) r = sh[k];
     __syncthreads();
     return r;
 }
@@ -1388,21 +1405,6 @@ __device__ __forceinline__ int64_t wave_scan_incl_i64(int64_t v, uint32_t lane) 
     return v;
 }
 
-// The best of the wave's candidates by the total order of `better` (gain,
-// then the lower ordinal): every lane ends with the same one.
-__device__ __forceinline__ Best wave_best(Best b) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        Best o;
-        o.gain = __shfl_xor(b.gain, off, 64);
-        o.ord = __shfl_xor(b.ord, off, 64);
-        o.found = __shfl_xor(b.found, off, 64);
-        o.lg = __shfl_xor(b.lg, off, 64);
-        o.lh = __shfl_xor(b.lh, off, 64);
-        if (better(o, b)) b = o;
-    }
-    return b;
-}
 
 // One wave per (numeric feature, node), four features per workgroup: the
 // numeric scan of split_feat_kernel on 64 lanes with shuffles only (no
