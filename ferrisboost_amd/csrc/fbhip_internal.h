@@ -382,7 +382,7 @@ struct FusedArgmaxDev {
     const SplitNodeDev *nodes;
     const uint64_t *cat_scratch;
 };
-hipError_t launch_grow_decide(const GrowParamsDev &G, uint32_t depth, const SplitPacketDev *pk,
+hipError_t launch_grow_decide(const GrowParamsDev &G, uint32_t depth, SplitPacketDev *pk,
                               uint64_t *pk_cats, const LNodeDev *level, TreeNodeDev *tree,
                               uint64_t *tree_cats, const int8_t *monotone, const DevColumn *cols,
                               PartReqDev *reqs, PairDev *pairs, uint32_t *triples,

@@ -2099,33 +2099,14 @@ __global__ __launch_bounds__(1024) void part_scan_kernel(const uint32_t *counts,
     part_scan_body(counts, n_chunks, excl, reqs, n_reqs, totals, dev);
 }
 
-// Pass 2 of a device-grown level, fused with its plan: the scan, then (one
-// workgroup, so the totals are visible after a barrier) the children plan of
-// level_plan_kernel.
-__global__ __launch_bounds__(1024) void part_scan_plan_kernel(
-    const uint32_t *counts, uint32_t *excl, const PartReqDev *reqs, uint32_t *totals,
-    const uint32_t *dev, const PairDev *pairs, ChunkRule rule, HistNodeDev *hn, SplitNodeDev *sn,
-    uint32_t *spans, uint32_t *left_slot, uint32_t *chunk_rows_out, GrowDevOut D) {
-    constexpr uint32_t LDS_CHUNKS = 8192;
-    __shared__ uint32_t s_excl[LDS_CHUNKS + 1];
-    __shared__ uint32_t s_tot[1024];
-    __shared__ uint32_t buf[32];
-    // Everything the scan and plan read that does not depend on the scan is
-    // requested first: the counts, the state, the thread's request and pair.
-    const uint32_t n_reqs = dev[0], n_chunks = dev[1];
-    PlanPrefetch pre{};
-    pre.valid = D.st != nullptr;
-    if (pre.valid) {
-        prefetch_state(pre, D.st);
-        if (threadIdx.x < pre.n) pre.first = pairs[threadIdx.x];
-    }
-    if (n_chunks > LDS_CHUNKS || n_reqs > 1024) {
-        part_scan_body(counts, 0u, excl, reqs, 0u, totals, dev);
-        __syncthreads();
-        level_plan_body(pairs, 0u, totals, rule, hn, sn, spans, left_slot, chunk_rows_out, D,
-                        pre);
-        return;
-    }
+// part_scan_plan_kernel's scan when the chunks and requests fit LDS: the
+// exclusive scan of the counts (a run of chunks a thread) kept in s_excl and
+// written out for the scatter; the request totals from LDS into s_tot and
+// totals.
+__device__ __forceinline__ void part_scan_lds(const uint32_t *counts, uint32_t *excl,
+                                              const PartReqDev *reqs, uint32_t *totals,
+                                              uint32_t n_reqs, uint32_t n_chunks,
+                                              uint32_t *s_excl, uint32_t *s_tot, uint32_t *buf) {
     uint32_t cb = 0, cn = 0;
     if (threadIdx.x < n_reqs) {
         cb = reqs[threadIdx.x].chunk_begin;
@@ -2175,8 +2156,41 @@ __global__ __launch_bounds__(1024) void part_scan_plan_kernel(
         totals[threadIdx.x] = t;
     }
     __syncthreads();
-    level_plan_body(pairs, 0u, s_tot, rule, hn, sn, spans, left_slot, chunk_rows_out, D, pre);
 }
+
+// Pass 2 of a device-grown level, fused with its plan: the scan, then (one
+// workgroup, so the totals are visible after a barrier) the children plan of
+// level_plan_kernel.
+__global__ __launch_bounds__(1024) void part_scan_plan_kernel(
+    const uint32_t *counts, uint32_t *excl, const PartReqDev *reqs, uint32_t *totals,
+    const uint32_t *dev, const PairDev *pairs, ChunkRule rule, HistNodeDev *hn, SplitNodeDev *sn,
+    uint32_t *spans, uint32_t *left_slot, uint32_t *chunk_rows_out, GrowDevOut D) {
+    constexpr uint32_t LDS_CHUNKS = 8192;
+    __shared__ uint32_t s_excl[LDS_CHUNKS + 1];
+    __shared__ uint32_t s_tot[1024];
+    __shared__ uint32_t buf[32];
+    // Everything the scan and plan read that does not depend on the scan is
+    // requested first: the counts, the state, the thread's request and pair.
+    const uint32_t n_reqs = dev[0], n_chunks = dev[1];
+    PlanPrefetch pre{};
+    pre.valid = D.st != nullptr;
+    if (pre.valid) {
+        prefetch_state(pre, D.st);
+        if (threadIdx.x < pre.n) pre.first = pairs[threadIdx.x];
+    }
+    // One inlined plan for both ways of scanning (the kernel's code is
+    // fetched once a level: its size is latency).
+    const bool big = n_chunks > LDS_CHUNKS || n_reqs > 1024;
+    if (big) {
+        part_scan_body(counts, 0u, excl, reqs, 0u, totals, dev);
+        __syncthreads();
+    } else {
+        part_scan_lds(counts, excl, reqs, totals, n_reqs, n_chunks, s_excl, s_tot, buf);
+    }
+    level_plan_body(pairs, 0u, big ? totals : s_tot, rule, hn, sn, spans, left_slot,
+                    chunk_rows_out, D, pre);
+}
+
 
 // Pass 3: stable scatter into the temporary arena. Rows of a chunk are taken
 // in order, 256 at a time; a wave's lanes rank their rows with a ballot.
@@ -3593,7 +3607,7 @@ hipError_t launch_grow_prep(const GrowParamsDev &G, const int64_t *root, const i
 //    and, when the children are evaluated, the lowest free histogram slot
 //    for the smaller child (the larger one takes over the node's slot).
 __global__ __launch_bounds__(1024) void grow_decide_kernel(
-    GrowParamsDev G, uint32_t depth, const SplitPacketDev *pk, uint64_t *pk_cats,
+    GrowParamsDev G, uint32_t depth, SplitPacketDev *pk, uint64_t *pk_cats,
     const LNodeDev *level, TreeNodeDev *tree, uint64_t *tree_cats, const int8_t *monotone,
     const DevColumn *cols, PartReqDev *reqs, PairDev *pairs, uint32_t *triples, LeafDev *leaves,
     float *leaf_vals, GrowState *st, FusedArgmaxDev A) {
@@ -3665,9 +3679,17 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
     TreeNodeDev myT{};
     int myMono = 0;
     DevColumn myCol{};
+    if (per == 1 && i0 < n) myL = level[i0];
+    // The packets, one inlined builder (the kernel's code is fetched once a
+    // level: its size is latency): held in registers with one node a
+    // thread, else stored to pk for the passes below.
+    if (A.cands || per == 1)
+        for (uint32_t i = i0; i < i1; i++) {
+            const SplitPacketDev P = make_pk(i);
+            if (per == 1) myP = P;
+            else pk[i] = P;
+        }
     if (per == 1 && i0 < n) {
-        myL = level[i0];
-        myP = make_pk(i0);
         // What the node's pass below reads, requested while the scans run.
         myT = tree[myL.tree_id];
         if (myP.found) {
@@ -3675,7 +3697,7 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
             myCol = cols[myP.feat];
         }
     }
-    auto pk_at = [&](uint32_t i) -> SplitPacketDev { return per == 1 ? myP : make_pk(i); };
+    auto pk_at = [&](uint32_t i) -> SplitPacketDev { return per == 1 ? myP : pk[i]; };
     auto lv_at = [&](uint32_t i) -> LNodeDev { return per == 1 ? myL : level[i]; };
 
     uint32_t f_before, tot_found, l_before, tot_leaves, c_before, tot_chunks, n_split;
@@ -3871,7 +3893,7 @@ __global__ __launch_bounds__(1024) void grow_decide_kernel(
     }
 }
 
-hipError_t launch_grow_decide(const GrowParamsDev &G, uint32_t depth, const SplitPacketDev *pk,
+hipError_t launch_grow_decide(const GrowParamsDev &G, uint32_t depth, SplitPacketDev *pk,
                               uint64_t *pk_cats, const LNodeDev *level, TreeNodeDev *tree,
                               uint64_t *tree_cats, const int8_t *monotone, const DevColumn *cols,
                               PartReqDev *reqs, PairDev *pairs, uint32_t *triples,
