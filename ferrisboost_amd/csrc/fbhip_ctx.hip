@@ -161,6 +161,7 @@ struct fbh_ctx {
     uint64_t max_partial_bytes = MAX_PARTIAL_BYTES;
     uint32_t one_pass_chunks = ONE_PASS_CHUNKS_PER_NODE;  // 0: never one pass
     bool pair_pass = true;          // split_pair_kernel where EvalPlan::pairs allows it
+    bool sub_in_scan = true;        // sibling subtraction inside split_num_kernel, likewise
     uint32_t hist_tpb = 0;          // histogram threads per workgroup (0: per launch)
     uint32_t hist_waves = HIST_WAVES;
     uint32_t host_hist_waves = HOST_HIST_WAVES;
@@ -1123,6 +1124,7 @@ fbh_config configure(fbh_ctx &c, uint64_t n_rows, const fbh_shape *shape, const 
     c.max_partial_bytes = env_u64("FB_HIP_PARTIAL_MB", MAX_PARTIAL_BYTES >> 20) << 20;
     c.one_pass_chunks = (uint32_t)env_u64("FB_HIP_ONE_PASS_CHUNKS", ONE_PASS_CHUNKS_PER_NODE);
     c.pair_pass = env_u64("FB_HIP_NO_PAIR_PASS", 0) == 0;
+    c.sub_in_scan = env_u64("FB_HIP_NO_SUB_IN_SCAN", 0) == 0;
     c.stage_rows_cap = env_u64("FB_HIP_STAGE_ROWS", 0);
     c.hist_waves = (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HIST_WAVES", HIST_WAVES));
     c.host_hist_waves =
@@ -2655,7 +2657,11 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
                                    E.max_groups, fuse_pairs ? PAIR_MAX_CHUNKS + 1 : 0u,
                                    c->stream),
               "chunk reduction");
-    if (!fuse_pairs)
+    // Device-grown pairs whose features all take split_num_kernel: the scan
+    // subtracts (one launch less a level).
+    const bool sub_in_scan = E.pairs && !fuse_pairs && c->sub_in_scan && c->n_split_cat == 0 &&
+                             c->n_split_wide == 0 && c->n_split_num > 0;
+    if (!fuse_pairs && !sub_in_scan)
         check(launch_subtract(c->hist, c->hist_width, E.triples, E.n_tri, E.dev_n_tri, c->stream),
               "sibling subtraction");
     // ---- split scan ----
@@ -2679,7 +2685,8 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
         check(launch_split_feats(c->hist, c->hist_width, E.sn, E.n_nodes, c->d_sfeats,
                                  c->d_split_order, c->n_split_num, c->n_split_wide,
                                  c->n_split_cat, E.enabled, P,
-                                 c->d_cands, c->d_cat_scratch, E.dev_n_nodes, c->stream),
+                                 c->d_cands, c->d_cat_scratch, E.dev_n_nodes,
+                                 sub_in_scan ? E.triples : nullptr, E.write_children, c->stream),
               "split scan");
     const uint32_t cw = std::max(1u, c->cat_words_per_node);
     const size_t pk_bytes = sizeof(SplitPacketDev) * E.n_nodes;

@@ -408,13 +408,17 @@ hipError_t launch_tree_leaves(const uint8_t *bundle, uint32_t pitch, uint64_t n_
                               float *margin, float *delta, float *leaf_vals, hipStream_t s);
 // order: the tree's feature positions, n_num numeric ones of at most 256
 // bins first (one wave each, 4 bins a lane), then n_wide numeric ones of at
-// most 1024 (one wave each, 16 bins a lane), then n_cat others, categorical
-// or wider (one workgroup each).
-hipError_t launch_split_feats(const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
+// most 1024 (one workgroup each, 4 bins a lane), then n_cat others,
+// categorical or wider (one workgroup each). sub_triples set (only with
+// n_wide = n_cat = 0): the sibling subtraction of evaluated pairs (nodes
+// 2e, 2e + 1; triples as launch_subtract's) is done by the scan, which
+// stores the larger children's bins when write_big.
+hipError_t launch_split_feats(int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
                               uint32_t n_nodes, const SplitFeatDev *feats, const uint32_t *order,
                               uint32_t n_num, uint32_t n_wide, uint32_t n_cat,
                               const uint8_t *enabled, SplitParamsDev P, FeatCandDev *cands,
-                              uint64_t *cat_scratch, const uint32_t *dev_n, hipStream_t s);
+                              uint64_t *cat_scratch, const uint32_t *dev_n,
+                              const uint32_t *sub_triples, bool write_big, hipStream_t s);
 // Chunk reduction (nodes of at most REDUCE_GROUP chunks), sibling
 // subtraction and split scan of evaluated pairs in one pass, for trees whose
 // features are all numeric of at most 256 bins (split_pair_kernel).

@@ -1507,23 +1507,32 @@ __device__ __forceinline__ void scan_numeric(const int64_t (&g)[PER], const int6
 
 // One wave's (node, numeric feature of at most 64 * PER bins): the
 // feature's bins into registers, then scan_numeric. li indexes order.
+// triples set (sibling subtraction fused, nodes 2e and 2e + 1 the children
+// of evaluated pair e): the larger child took its parent's slot, which
+// still holds the parent's histogram, so its bins are those minus the
+// smaller child's (slot triples[3e + 2]), stored back when write_big (the
+// next level's parents), whether or not the feature is enabled here.
 template <uint32_t PER>
-__device__ __forceinline__ void split_num_wave(const int64_t *hist, uint64_t hist_width,
+__device__ __forceinline__ void split_num_wave(int64_t *hist, uint64_t hist_width,
                                                const SplitNodeDev *nodes,
                                                const SplitFeatDev *feats, const uint32_t *order,
                                                uint32_t li, uint32_t ni, const uint8_t *enabled,
-                                               SplitParamsDev P, FeatCandDev *cands) {
+                                               SplitParamsDev P, FeatCandDev *cands,
+                                               const uint32_t *triples, uint32_t write_big) {
     const uint32_t lane = threadIdx.x & 63u;
     load_scales(P);
     const uint32_t j = order[li];
     const SplitFeatDev F = feats[j];
     const SplitNodeDev N = nodes[ni];
+    const uint32_t small_slot = triples ? triples[3 * (ni >> 1) + 2] : NO_SLOT;
+    const bool big = triples && N.slot != small_slot;
     FeatCandDev *outc = cands + (size_t)ni * P.n_feats + j;
-    if (enabled && !enabled[(size_t)ni * P.n_feats + j]) {
+    const bool off = enabled && !enabled[(size_t)ni * P.n_feats + j];
+    if (off && !big) {
         if (lane == 0) outc->found = 0;
         return;
     }
-    const int64_t *hp = hist + ((uint64_t)N.slot * hist_width + F.hist_off) * 2u;
+    int64_t *hp = hist + ((uint64_t)N.slot * hist_width + F.hist_off) * 2u;
     const uint32_t n = F.n_bins;
     const uint32_t per = (n + 63) / 64;  // at most PER
     const uint32_t b0 = min(lane * per, n), b1 = min(b0 + per, n);
@@ -1532,6 +1541,23 @@ __device__ __forceinline__ void split_num_wave(const int64_t *hist, uint64_t his
     for (uint32_t k = 0; k < PER; k++) {
         g[k] = b0 + k < b1 ? hp[2 * (b0 + k)] : 0;
         h[k] = b0 + k < b1 ? hp[2 * (b0 + k) + 1] : 0;
+    }
+    if (big) {
+        const int64_t *sp = hist + ((uint64_t)small_slot * hist_width + F.hist_off) * 2u;
+#pragma unroll
+        for (uint32_t k = 0; k < PER; k++)
+            if (b0 + k < b1) {
+                g[k] = wsub(g[k], sp[2 * (b0 + k)]);
+                h[k] = wsub(h[k], sp[2 * (b0 + k) + 1]);
+                if (write_big) {
+                    hp[2 * (b0 + k)] = g[k];
+                    hp[2 * (b0 + k) + 1] = h[k];
+                }
+            }
+        if (off) {
+            if (lane == 0) outc->found = 0;
+            return;
+        }
     }
     scan_numeric<PER>(g, h, b0, b1, n, lane, N, F, P, outc);
 }
@@ -1604,13 +1630,14 @@ __device__ __forceinline__ void split_wide_block(const int64_t *hist, uint64_t h
 // One wave per (node, numeric feature of at most 256 bins), four features a
 // workgroup.
 __global__ __launch_bounds__(256) void split_num_kernel(
-    const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
-    const SplitFeatDev *feats, const uint32_t *order, uint32_t n_num, const uint8_t *enabled,
-    SplitParamsDev P, FeatCandDev *cands, const uint32_t *dev_n) {
+    int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes, const SplitFeatDev *feats,
+    const uint32_t *order, uint32_t n_num, const uint8_t *enabled, SplitParamsDev P,
+    FeatCandDev *cands, const uint32_t *dev_n, const uint32_t *triples, uint32_t write_big) {
     const uint32_t li = blockIdx.x * 4 + (threadIdx.x >> 6), ni = blockIdx.y;
     if (dev_n && ni >= *dev_n) return;
     if (li >= n_num) return;  // a whole wave
-    split_num_wave<NUM_PER_LANE>(hist, hist_width, nodes, feats, order, li, ni, enabled, P, cands);
+    split_num_wave<NUM_PER_LANE>(hist, hist_width, nodes, feats, order, li, ni, enabled, P, cands,
+                                 triples, write_big);
 }
 
 // Reduction, subtraction and split scan of one evaluated pair in one pass,
@@ -1843,15 +1870,18 @@ __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
     }
 }
 
-hipError_t launch_split_feats(const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
+hipError_t launch_split_feats(int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
                               uint32_t n_nodes, const SplitFeatDev *feats, const uint32_t *order,
                               uint32_t n_num, uint32_t n_wide, uint32_t n_cat,
                               const uint8_t *enabled, SplitParamsDev P, FeatCandDev *cands,
-                              uint64_t *cat_scratch, const uint32_t *dev_n, hipStream_t s) {
+                              uint64_t *cat_scratch, const uint32_t *dev_n,
+                              const uint32_t *sub_triples, bool write_big, hipStream_t s) {
     if (n_nodes == 0 || P.n_feats == 0) return hipSuccess;
+    if (sub_triples && (n_wide || n_cat)) return hipErrorInvalidValue;
     if (n_num)
         hipLaunchKernelGGL(split_num_kernel, dim3((n_num + 3) / 4, n_nodes), dim3(256), 0, s, hist,
-                           hist_width, nodes, feats, order, n_num, enabled, P, cands, dev_n);
+                           hist_width, nodes, feats, order, n_num, enabled, P, cands, dev_n,
+                           sub_triples, write_big ? 1u : 0u);
     if (n_wide || n_cat) {
         const size_t dyn = P.cat_words_per_node
                                ? sizeof(uint64_t) * MAX_DEVICE_CATS
