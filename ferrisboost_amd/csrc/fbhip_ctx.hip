@@ -2657,10 +2657,8 @@ void enqueue_eval(fbh_ctx *c, const EvalPlan &E, const fbh_split_params *sp) {
                                    E.max_groups, fuse_pairs ? PAIR_MAX_CHUNKS + 1 : 0u,
                                    c->stream),
               "chunk reduction");
-    // Device-grown pairs whose features all take split_num_kernel: the scan
-    // subtracts (one launch less a level).
-    const bool sub_in_scan = E.pairs && !fuse_pairs && c->sub_in_scan && c->n_split_cat == 0 &&
-                             c->n_split_wide == 0 && c->n_split_num > 0;
+    // Device-grown pairs: the split scan subtracts (one launch less a level).
+    const bool sub_in_scan = E.pairs && !fuse_pairs && c->sub_in_scan;
     if (!fuse_pairs && !sub_in_scan)
         check(launch_subtract(c->hist, c->hist_width, E.triples, E.n_tri, E.dev_n_tri, c->stream),
               "sibling subtraction");

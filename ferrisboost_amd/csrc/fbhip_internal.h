@@ -409,10 +409,10 @@ hipError_t launch_tree_leaves(const uint8_t *bundle, uint32_t pitch, uint64_t n_
 // order: the tree's feature positions, n_num numeric ones of at most 256
 // bins first (one wave each, 4 bins a lane), then n_wide numeric ones of at
 // most 1024 (one workgroup each, 4 bins a lane), then n_cat others,
-// categorical or wider (one workgroup each). sub_triples set (only with
-// n_wide = n_cat = 0): the sibling subtraction of evaluated pairs (nodes
-// 2e, 2e + 1; triples as launch_subtract's) is done by the scan, which
-// stores the larger children's bins when write_big.
+// categorical or wider (one workgroup each). sub_triples set: the sibling
+// subtraction of evaluated pairs (nodes 2e, 2e + 1; triples as
+// launch_subtract's) is done by the scan, which stores the larger children's
+// bins when write_big (the one-workgroup features always store them).
 hipError_t launch_split_feats(int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
                               uint32_t n_nodes, const SplitFeatDev *feats, const uint32_t *order,
                               uint32_t n_num, uint32_t n_wide, uint32_t n_cat,

@@ -1569,32 +1569,57 @@ __device__ __forceinline__ void split_num_wave(int64_t *hist, uint64_t hist_widt
 // by the same total order. Four waves a feature keep the chain of f64
 // candidate arithmetic a lane runs four times shorter than one wave would.
 // wt holds 8 and wb 4 entries of LDS. li indexes order.
-__device__ __forceinline__ void split_wide_block(const int64_t *hist, uint64_t hist_width,
+__device__ __forceinline__ void split_wide_block(int64_t *hist, uint64_t hist_width,
                                                  const SplitNodeDev *nodes,
                                                  const SplitFeatDev *feats, const uint32_t *order,
                                                  uint32_t li, uint32_t ni, const uint8_t *enabled,
                                                  SplitParamsDev P, FeatCandDev *cands,
-                                                 int64_t *wt, Best *wb) {
+                                                 int64_t *wt, Best *wb, const uint32_t *triples,
+                                                 uint32_t write_big) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     load_scales(P);
     const uint32_t j = order[li];
     const SplitFeatDev F = feats[j];
     const SplitNodeDev N = nodes[ni];
     FeatCandDev *outc = cands + (size_t)ni * P.n_feats + j;
-    if (enabled && !enabled[(size_t)ni * P.n_feats + j]) {
+    // Sibling subtraction in registers (triples set), as split_num_wave.
+    const uint32_t small_slot = triples ? triples[3 * (ni >> 1) + 2] : NO_SLOT;
+    const bool big = triples && N.slot != small_slot;
+    const bool off = enabled && !enabled[(size_t)ni * P.n_feats + j];
+    if (off && !big) {
         if (tid == 0) outc->found = 0;
         return;
     }
-    const int64_t *hp = hist + ((uint64_t)N.slot * hist_width + F.hist_off) * 2u;
+    int64_t *hp = hist + ((uint64_t)N.slot * hist_width + F.hist_off) * 2u;
     const uint32_t n = F.n_bins;
     const uint32_t per = (n + SPLIT_TPB - 1) / SPLIT_TPB;  // at most NUM_PER_LANE
     const uint32_t b0 = min(tid * per, n), b1 = min(b0 + per, n);
     int64_t g[NUM_PER_LANE], h[NUM_PER_LANE];
-    int64_t tg = 0, th = 0;
 #pragma unroll
     for (uint32_t k = 0; k < NUM_PER_LANE; k++) {
         g[k] = b0 + k < b1 ? hp[2 * (b0 + k)] : 0;
         h[k] = b0 + k < b1 ? hp[2 * (b0 + k) + 1] : 0;
+    }
+    if (big) {
+        const int64_t *sp = hist + ((uint64_t)small_slot * hist_width + F.hist_off) * 2u;
+#pragma unroll
+        for (uint32_t k = 0; k < NUM_PER_LANE; k++)
+            if (b0 + k < b1) {
+                g[k] = wsub(g[k], sp[2 * (b0 + k)]);
+                h[k] = wsub(h[k], sp[2 * (b0 + k) + 1]);
+                if (write_big) {
+                    hp[2 * (b0 + k)] = g[k];
+                    hp[2 * (b0 + k) + 1] = h[k];
+                }
+            }
+        if (off) {
+            if (tid == 0) outc->found = 0;
+            return;
+        }
+    }
+    int64_t tg = 0, th = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < NUM_PER_LANE; k++) {
         tg = wadd(tg, g[k]);
         th = wadd(th, h[k]);
     }
@@ -1775,10 +1800,10 @@ hipError_t launch_split_pairs(int64_t *hist, uint64_t hist_width, const int64_t 
 // workgroup each (split_wide_block), in the same launch: the two kinds then
 // overlap instead of running one after the other.
 __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
-    const int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes,
-    const SplitFeatDev *feats, const uint32_t *order, uint32_t order_off, uint32_t n_block,
-    uint32_t wide_off, uint32_t n_wide, const uint8_t *enabled, SplitParamsDev P,
-    FeatCandDev *cands, uint64_t *cat_scratch, const uint32_t *dev_n) {
+    int64_t *hist, uint64_t hist_width, const SplitNodeDev *nodes, const SplitFeatDev *feats,
+    const uint32_t *order, uint32_t order_off, uint32_t n_block, uint32_t wide_off,
+    uint32_t n_wide, const uint8_t *enabled, SplitParamsDev P, FeatCandDev *cands,
+    uint64_t *cat_scratch, const uint32_t *dev_n, const uint32_t *triples, uint32_t write_big) {
     __shared__ Best shb[SPLIT_TPB];
     __shared__ int64_t sg[SPLIT_TPB], shh[SPLIT_TPB];
     extern __shared__ unsigned char dyn[];
@@ -1789,7 +1814,7 @@ __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
         const uint32_t li = blockIdx.x - n_block;
         if (li < n_wide)
             split_wide_block(hist, hist_width, nodes, feats, order + wide_off, li, ni, enabled, P,
-                             cands, sg, shb);
+                             cands, sg, shb, triples, write_big);
         return;
     }
     load_scales(P);
@@ -1797,11 +1822,28 @@ __global__ __launch_bounds__(SPLIT_TPB) void split_feat_kernel(
     const SplitFeatDev F = feats[j];
     const SplitNodeDev N = nodes[ni];
     FeatCandDev *outc = cands + (size_t)ni * P.n_feats + j;
-    if (enabled && !enabled[(size_t)ni * P.n_feats + j]) {
+    // Sibling subtraction (triples set), as split_num_wave: the larger child's
+    // bins, its parent's minus the smaller child's, are stored into its slot
+    // first (the scans below read them from there), enabled or not.
+    const uint32_t small_slot = triples ? triples[3 * (ni >> 1) + 2] : NO_SLOT;
+    const bool big = triples && N.slot != small_slot;
+    const bool off = enabled && !enabled[(size_t)ni * P.n_feats + j];
+    if (off && !big) {
         if (tid == 0) outc->found = 0;
         return;
     }
-    const int64_t *h = hist + ((uint64_t)N.slot * hist_width + F.hist_off) * 2u;
+    int64_t *hm = hist + ((uint64_t)N.slot * hist_width + F.hist_off) * 2u;
+    if (big) {
+        const int64_t *sp = hist + ((uint64_t)small_slot * hist_width + F.hist_off) * 2u;
+        for (uint32_t i = tid; i < 2 * F.n_bins; i += SPLIT_TPB) hm[i] = wsub(hm[i], sp[i]);
+        __threadfence_block();
+        __syncthreads();
+        if (off) {
+            if (tid == 0) outc->found = 0;
+            return;
+        }
+    }
+    const int64_t *h = hm;
     const double ng = (double)N.sum_g * P.inv_g, nh = (double)N.sum_h * P.inv_h;
     const float parent = gain_given_weight(ng, nh, apply_bounds(xgb_weight(ng, nh, P), N.lower,
                                                                 N.upper), P);
@@ -1877,7 +1919,6 @@ hipError_t launch_split_feats(int64_t *hist, uint64_t hist_width, const SplitNod
                               uint64_t *cat_scratch, const uint32_t *dev_n,
                               const uint32_t *sub_triples, bool write_big, hipStream_t s) {
     if (n_nodes == 0 || P.n_feats == 0) return hipSuccess;
-    if (sub_triples && (n_wide || n_cat)) return hipErrorInvalidValue;
     if (n_num)
         hipLaunchKernelGGL(split_num_kernel, dim3((n_num + 3) / 4, n_nodes), dim3(256), 0, s, hist,
                            hist_width, nodes, feats, order, n_num, enabled, P, cands, dev_n,
@@ -1889,7 +1930,7 @@ hipError_t launch_split_feats(int64_t *hist, uint64_t hist_width, const SplitNod
         hipLaunchKernelGGL(split_feat_kernel, dim3(n_cat + n_wide, n_nodes),
                            dim3(SPLIT_TPB), dyn, s, hist, hist_width, nodes, feats, order,
                            n_num + n_wide, n_cat, n_num, n_wide, enabled, P, cands, cat_scratch,
-                           dev_n);
+                           dev_n, sub_triples, write_big ? 1u : 0u);
     }
     return hipGetLastError();
 }
