@@ -606,12 +606,17 @@ struct fbh_ctx {
     // Threads of a histogram workgroup of group g: 512 when the LDS lets
     // three or more workgroups share a CU (planar tiles of few wide-bin
     // features: the rows' loads then need more waves in flight; measured
-    // on 2M rows x 80 features of 1024 bins, 254 against 340 us), else 256
-    // (interleaved tiles: two workgroups a CU, LDS-atomic bound).
+    // on 2M rows x 80 features of 1024 bins, 254 against 340 us), and for
+    // interleaved tiles in groups of more than F32_PAIR_MAX_TILES tiles
+    // (their rows gather 16-byte pairs once a tile, and two workgroups a CU
+    // leave those loads short of waves: 400k x 2000 at 1000 features a tree
+    // 391 -> 408 rounds/s), else 256 (C2's two interleaved tiles: LDS-atomic
+    // bound at the root, 512 threads lost 2 %).
     int hist_threads(const Group &g) const {
         if (hist_tpb) return (int)hist_tpb;
+        if (g.rot) return g.n_tiles > F32_PAIR_MAX_TILES ? 512 : 256;
         const uint64_t lds = (uint64_t)(g.lds_max + 64) * 16;
-        return !g.rot && 3 * lds <= 160u * 1024u ? 512 : 256;
+        return 3 * lds <= 160u * 1024u ? 512 : 256;
     }
 
     // Rows per histogram workgroup for a launch accumulating acc_rows rows:
