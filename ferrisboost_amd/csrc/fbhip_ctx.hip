@@ -2387,8 +2387,9 @@ int fbh_begin_tree(fbh_ctx *c, const uint32_t *features, uint32_t n_sel, const i
         // The tables go up only when they differ from the last tree's (every
         // tree of a run without column sampling has the same).
         // Split-scan order: numeric features of at most 256 bins (one wave
-        // each, four bins a lane), numeric ones of at most 1024 (one wave
-        // each, sixteen bins a lane), then the others (one workgroup each).
+        // each, four bins a lane), numeric ones of at most 1024 (one
+        // workgroup each, four bins a thread), then the others (one
+        // workgroup each).
         auto group = [&](uint32_t j) {
             if (sf[j].categorical || sf[j].n_bins > 1024) return 2;
             return sf[j].n_bins <= 256 ? 0 : 1;
