@@ -123,6 +123,12 @@ constexpr uint32_t SHARED_LINE_CHUNK_ROWS = 8192;
 // upload of different chunks overlap).
 constexpr int EXCHANGE_CHUNKS = 8;
 constexpr uint32_t HIST_WAVES = 1;
+// Device-planned launches of layouts with planar tiles plan two waves: their
+// workgroups hold fewer rows each and the second wave overlaps the first's
+// flushes (wide-bin 2M x 100 rounds 5-24: 545 against 571 rounds/s; the
+// interleaved layouts of 10.5M x 28 and 400k x 2000 lost 7 % and 6 % with
+// two).
+constexpr uint32_t PLANAR_HIST_WAVES = 2;
 // Host-driven evaluations (lossguide expansions, host levels) accumulate
 // fewer rows per launch; two waves of workgroups measured faster there
 // (wide-bin lossguide: 107 against 99 rounds/s).
@@ -163,7 +169,7 @@ struct fbh_ctx {
     bool pair_pass = true;          // split_pair_kernel where EvalPlan::pairs allows it
     bool sub_in_scan = true;        // sibling subtraction inside split_num_kernel, likewise
     uint32_t hist_tpb = 0;          // histogram threads per workgroup (0: per launch)
-    uint32_t hist_waves = HIST_WAVES;
+    uint32_t hist_waves = 0;  // 0: HIST_WAVES, PLANAR_HIST_WAVES with planar tiles
     uint32_t host_hist_waves = HOST_HIST_WAVES;
     uint32_t n_cus = 256;
     uint32_t n_slots = 0;
@@ -626,14 +632,19 @@ struct fbh_ctx {
     ChunkRule chunk_rule(bool host = false, bool own_lines = false) const {
         ChunkRule R{fixed_chunk_rows, 1, MIN_CHUNK_ROWS, 1u << 24};
         uint64_t n_tiles = 0, lds_max = 0;
+        bool planar = false;
         for (const auto &g : groups) {
             n_tiles += g.n_tiles;
             if (!g.global) lds_max = std::max<uint64_t>(lds_max, (uint64_t)(g.lds_max + 64) * 16);
+            planar = planar || (!g.global && !g.rot);
         }
         if (n_tiles == 0) return R;
         uint64_t per_cu = lds_max ? (160u * 1024u) / lds_max : 8;
         per_cu = std::max<uint64_t>(1, std::min<uint64_t>(per_cu, 2048 / (hist_tpb ? hist_tpb : 256)));
-        const uint64_t wgs = (uint64_t)n_cus * per_cu * (host ? host_hist_waves : hist_waves);
+        const uint32_t waves =
+            host ? host_hist_waves
+                 : (hist_waves ? hist_waves : (planar ? PLANAR_HIST_WAVES : HIST_WAVES));
+        const uint64_t wgs = (uint64_t)n_cus * per_cu * waves;
         R.want_chunks = (uint32_t)std::max<uint64_t>(1, wgs / n_tiles);
         // Many tiles reading one bundle line: short chunks, so the tiles'
         // workgroups of a chunk stay close enough in the rows for the line
@@ -1131,7 +1142,7 @@ fbh_config configure(fbh_ctx &c, uint64_t n_rows, const fbh_shape *shape, const 
     c.pair_pass = env_u64("FB_HIP_NO_PAIR_PASS", 0) == 0;
     c.sub_in_scan = env_u64("FB_HIP_NO_SUB_IN_SCAN", 0) == 0;
     c.stage_rows_cap = env_u64("FB_HIP_STAGE_ROWS", 0);
-    c.hist_waves = (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HIST_WAVES", HIST_WAVES));
+    c.hist_waves = (uint32_t)env_u64("FB_HIP_HIST_WAVES", 0);
     c.host_hist_waves =
         (uint32_t)std::max<uint64_t>(1, env_u64("FB_HIP_HOST_HIST_WAVES", HOST_HIST_WAVES));
     if (c.tile_bytes < 4096 || c.tile_bytes > 160 * 1024)
