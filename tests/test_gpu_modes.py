@@ -207,3 +207,40 @@ def test_resident_blocks_and_hist_streams_keep_the_model(fb, oracle, knobs):
     assert_same_models(ref, got)
     assert np.array_equal(got.train_margins(n).view(np.uint32), ref.train_margins(n).view(np.uint32))
     assert_same_models(oracle.train(x, y, oracle.make_params(**p)), got)
+
+
+@pytest.mark.parametrize("kind", ["numeric", "categorical_wide"])
+def test_subtraction_inside_the_scan_keeps_the_model(fb, oracle, monkeypatch, kind):
+    """Device-grown levels subtract siblings inside the split scan (the larger
+    child's bins from its parent's slot, stored back for the next level);
+    FB_HIP_NO_SUB_IN_SCAN=1 runs the subtraction as its own launch. Both give
+    the same trees and margins, with a per-node feature mask too (a feature
+    masked out of the larger child still has its bins subtracted and stored,
+    since the next level scans them), for numeric features of at most 256
+    bins and for categorical and 257-1024-bin ones."""
+    rng = np.random.default_rng(202)
+    n = 40_000
+    if kind == "numeric":
+        nf = 24
+        x = rng.normal(size=(n, nf)).astype(np.float32)
+        types = None
+        p = {"max_depth": 6, "eta": 0.3, "max_bin": 255, "colsample_bynode": 0.6}
+    else:
+        nf = 12
+        x = rng.normal(size=(n, nf)).astype(np.float32)
+        x[:, 8:] = rng.integers(0, 300, size=(n, 4)).astype(np.float32)
+        types = ["q"] * 8 + ["c"] * 4
+        p = {"max_depth": 6, "eta": 0.3, "max_bin": 1000, "colsample_bynode": 0.6,
+             "max_cat_to_onehot": 4}
+    x[rng.random((n, nf)) < 0.03] = np.nan
+    y = (np.nan_to_num(x[:, 1]) + np.nan_to_num(x[:, 5]) * 0.5
+         + 0.3 * rng.normal(size=n) > 0).astype(np.float32)
+    pp = dict(product_params(p), seed=7)
+    if types:
+        pp["feature_types"] = types
+    fused = fb.train(pp, x, y, num_boost_round=4)
+    monkeypatch.setenv("FB_HIP_NO_SUB_IN_SCAN", "1")
+    apart = fb.train(pp, x, y, num_boost_round=4)
+    assert_same_models(fused, apart)
+    assert np.array_equal(fused.train_margins(n).view(np.uint32),
+                          apart.train_margins(n).view(np.uint32))
